@@ -1,0 +1,568 @@
+// capi.hip -- C ABI of the gfx950 runner (include/hp_hip.h): device setup,
+// resident weight handles, shape checks and kernel sequencing.
+//
+// Shape and type checks follow packages/engine/wasm-kernels/src/lib.rs
+// (224-298, 300-426: saturating products, ERR_SHAPE before ERR_TYPE for the
+// activation/output lengths) and the resident wrappers in
+// packages/engine/src/runner/wasm/wasm-kernels.ts (520-749: handle shape must
+// match the call).
+#include "../../include/hp_hip.h"
+#include "hp_common.h"
+
+#include <mutex>
+#include <string>
+#include <vector>
+
+namespace {
+
+using namespace hp;
+
+struct Handle {
+  int type = 0;
+  size_t input_size = 0, row_count = 0, byte_length = 0;
+  TileGeom g{};
+  int tiles = 0;
+  uint8_t *data = nullptr;     // tiles (+ Q6_K d plane at the end)
+  uint16_t *dplane = nullptr;  // Q6_K only
+  uint32_t generation = 0;
+  bool live = false;
+};
+
+struct ProfileSlot {
+  std::vector<std::pair<hipEvent_t, hipEvent_t>> pending;
+  double total_ms = 0;
+  uint64_t launches = 0;
+};
+
+struct State {
+  std::recursive_mutex mu;
+  bool ready = false;
+  int device = -1;
+  int num_cus = 0;
+  size_t max_lds = 0;
+  hipStream_t stream = nullptr;
+  std::vector<Handle> handles;
+  uint8_t *q8 = nullptr;
+  float *q8d = nullptr;
+  size_t q8_cap_blocks = 0;
+  float *io_in = nullptr, *io_out[kMaxWeights] = {nullptr, nullptr, nullptr, nullptr};
+  size_t io_in_cap = 0, io_out_cap[kMaxWeights] = {0, 0, 0, 0};
+  uint64_t matmul_calls = 0, launches = 0;
+  bool profiling = false;
+  ProfileSlot prof[HP_KERNEL_COUNT];
+  std::vector<hipEvent_t> event_pool;
+};
+
+State &st() {
+  static State s;
+  return s;
+}
+
+thread_local std::string g_last_error;
+
+int32_t fail(int32_t code, const std::string &msg) {
+  g_last_error = msg;
+  return code;
+}
+
+int32_t hip_fail(hipError_t e, const char *what) {
+  return fail(HP_ERR_HIP, std::string(what) + ": " + hipGetErrorString(e));
+}
+
+#define HP_HIP_TRY(expr)                         \
+  do {                                           \
+    hipError_t _e = (expr);                      \
+    if (_e != hipSuccess) return hip_fail(_e, #expr); \
+  } while (0)
+
+size_t sat_mul(size_t a, size_t b) {
+  size_t r;
+  if (__builtin_mul_overflow(a, b, &r)) return (size_t)-1;
+  return r;
+}
+
+size_t row_bytes_for(int type, size_t input_size) {
+  if (input_size % kQK != 0) return 0;
+  if (type == kTypeQ4K) return input_size / kQK * 144;
+  if (type == kTypeQ6K) return input_size / kQK * 210;
+  return 0;
+}
+
+int32_t ensure_init(int device) {
+  State &s = st();
+  if (s.ready) return HP_OK;
+  int n = 0;
+  if (hipGetDeviceCount(&n) != hipSuccess || n <= 0) return fail(HP_ERR_NODEV, "no HIP device available");
+  if (device < 0 || device >= n) return fail(HP_ERR_ARG, "device index out of range");
+  HP_HIP_TRY(hipSetDevice(device));
+  HP_HIP_TRY(hipDeviceGetAttribute(&s.num_cus, hipDeviceAttributeMultiprocessorCount, device));
+  int lds = 0;
+  HP_HIP_TRY(hipDeviceGetAttribute(&lds, hipDeviceAttributeMaxSharedMemoryPerBlock, device));
+  s.max_lds = (size_t)lds;
+  HP_HIP_TRY(hipStreamCreateWithFlags(&s.stream, hipStreamNonBlocking));
+  s.device = device;
+  s.ready = true;
+  return HP_OK;
+}
+
+Handle *lookup(uint64_t id) {
+  State &s = st();
+  const uint64_t idx = (id & 0xffffffffu);
+  const uint32_t gen = (uint32_t)(id >> 32);
+  if (idx == 0 || idx > s.handles.size()) return nullptr;
+  Handle &h = s.handles[idx - 1];
+  if (!h.live || h.generation != gen) return nullptr;
+  return &h;
+}
+
+int32_t grow(void **p, size_t *cap, size_t bytes) {
+  if (*cap >= bytes && *p) return HP_OK;
+  State &s = st();
+  if (*p) {
+    HP_HIP_TRY(hipStreamSynchronize(s.stream));
+    HP_HIP_TRY(hipFree(*p));
+    *p = nullptr;
+    *cap = 0;
+  }
+  size_t want = bytes < 4096 ? 4096 : bytes;
+  if (hipMalloc(p, want) != hipSuccess) {
+    *p = nullptr;
+    return fail(HP_ERR_OOM, "device allocation failed");
+  }
+  *cap = want;
+  return HP_OK;
+}
+
+int32_t ensure_q8(size_t cols, size_t nb) {
+  State &s = st();
+  const size_t blocks = cols * nb;
+  if (s.q8_cap_blocks >= blocks && s.q8) return HP_OK;
+  if (s.q8) {
+    HP_HIP_TRY(hipStreamSynchronize(s.stream));
+    HP_HIP_TRY(hipFree(s.q8));
+    HP_HIP_TRY(hipFree(s.q8d));
+    s.q8 = nullptr;
+    s.q8d = nullptr;
+    s.q8_cap_blocks = 0;
+  }
+  if (hipMalloc((void **)&s.q8, blocks * kQ8BlockBytes) != hipSuccess) return fail(HP_ERR_OOM, "q8 scratch");
+  if (hipMalloc((void **)&s.q8d, blocks * sizeof(float)) != hipSuccess) return fail(HP_ERR_OOM, "q8 scratch");
+  s.q8_cap_blocks = blocks;
+  return HP_OK;
+}
+
+hipEvent_t take_event() {
+  State &s = st();
+  if (!s.event_pool.empty()) {
+    hipEvent_t e = s.event_pool.back();
+    s.event_pool.pop_back();
+    return e;
+  }
+  hipEvent_t e = nullptr;
+  if (hipEventCreate(&e) != hipSuccess) return nullptr;
+  return e;
+}
+
+// Records a start event when profiling; returns it (or null).
+hipEvent_t prof_begin(hipStream_t stream) {
+  State &s = st();
+  if (!s.profiling) return nullptr;
+  hipEvent_t e = take_event();
+  if (e) (void)hipEventRecord(e, stream);
+  return e;
+}
+
+void prof_end(int kernel, hipEvent_t start, hipStream_t stream) {
+  State &s = st();
+  if (!start) return;
+  hipEvent_t e = take_event();
+  if (!e) return;
+  (void)hipEventRecord(e, stream);
+  s.prof[kernel].pending.emplace_back(start, e);
+}
+
+void prof_collect() {
+  State &s = st();
+  for (int k = 0; k < HP_KERNEL_COUNT; k++) {
+    for (auto &pr : s.prof[k].pending) {
+      float ms = 0.0f;
+      if (hipEventSynchronize(pr.second) == hipSuccess && hipEventElapsedTime(&ms, pr.first, pr.second) == hipSuccess) {
+        s.prof[k].total_ms += ms;
+        s.prof[k].launches += 1;
+      }
+      s.event_pool.push_back(pr.first);
+      s.event_pool.push_back(pr.second);
+    }
+    s.prof[k].pending.clear();
+  }
+}
+
+// Column chunk such that the matvec launch's LDS fits the device limit.
+int cols_per_launch(const TileGeom &g, size_t max_lds) {
+  for (int c = kMaxCols; c >= 1; c--) {
+    size_t x = (size_t)c * g.nb * kQ8BlockBytes + (size_t)((c * g.nb + 3) & ~3) * 4;
+    size_t per_wave = (size_t)(g.R * 9 * g.S + c * g.R * 9) * 4;
+    if (x + 4 * per_wave <= max_lds) return c;
+  }
+  return 0;
+}
+
+// Core sequence: Q8_K quantise every column once, then one matvec launch per
+// column chunk covering every weight (multi == one launch, lib.rs:300-426).
+int32_t run_matvec(size_t count, Handle *const *hs, const float *d_input, size_t input_size, size_t cols,
+                   float *const *d_outs, hipStream_t stream) {
+  State &s = st();
+  if (cols == 0) return HP_OK;
+  const TileGeom g = hs[0]->g;
+  const size_t nb = input_size / kQK;
+  int32_t rc = ensure_q8(cols, nb);
+  if (rc != HP_OK) return rc;
+  hipEvent_t e0 = prof_begin(stream);
+  HP_HIP_TRY(launch_q8k_quantize(d_input, (int)input_size, (int)cols, s.q8, s.q8d, stream));
+  prof_end(HP_KERNEL_Q8K, e0, stream);
+  s.launches++;
+
+  MatvecArgs a{};
+  a.count = (int)count;
+  a.g = g;
+  int tiles = 0;
+  for (size_t i = 0; i < count; i++) {
+    a.w[i].data = hs[i]->data;
+    a.w[i].dplane = hs[i]->dplane;
+    a.w[i].out = d_outs[i];
+    a.w[i].type = hs[i]->type;
+    a.w[i].rows = (int)hs[i]->row_count;
+    a.w[i].tiles = hs[i]->tiles;
+    a.w[i].tile_begin = tiles;
+    tiles += hs[i]->tiles;
+  }
+  a.total_tiles = tiles;
+  const int chunk = cols_per_launch(g, s.max_lds);
+  if (chunk <= 0) return fail(HP_ERR_SHAPE, "input_size too large for the matvec LDS budget");
+  for (size_t m0 = 0; m0 < cols; m0 += (size_t)chunk) {
+    const int c = (int)((cols - m0) < (size_t)chunk ? (cols - m0) : (size_t)chunk);
+    a.q8 = s.q8 + m0 * nb * kQ8BlockBytes;
+    a.q8d = s.q8d + m0 * nb;
+    a.cols = c;
+    a.out_col0 = (int)m0;
+    hipEvent_t e1 = prof_begin(stream);
+    HP_HIP_TRY(launch_matvec(a, s.num_cus, stream));
+    prof_end(HP_KERNEL_MATVEC, e1, stream);
+    s.launches++;
+  }
+  s.matmul_calls++;
+  return HP_OK;
+}
+
+int32_t upload_common(int32_t type_id, const void *src, bool src_device, size_t weight_len, size_t input_size,
+                      size_t row_count, uint64_t *out_handle) {
+  State &s = st();
+  if (!out_handle || !src) return fail(HP_ERR_ARG, "null pointer");
+  int32_t rc = ensure_init(s.ready ? s.device : 0);
+  if (rc != HP_OK) return rc;
+  if (input_size == 0 || row_count == 0) return fail(HP_ERR_SHAPE, "resident weight shape mismatch");
+  if (type_id != kTypeQ4K && type_id != kTypeQ6K) return fail(HP_ERR_TYPE, "unsupported quantized type");
+  const size_t rb = row_bytes_for(type_id, input_size);
+  if (rb == 0) return fail(HP_ERR_TYPE, "input_size is not a multiple of 256");
+  if (weight_len != sat_mul(rb, row_count)) return fail(HP_ERR_SHAPE, "weight byte length mismatch");
+  if (row_count > (size_t)0x7fffffff / 64 || input_size / kQK > 4096) return fail(HP_ERR_SHAPE, "weight too large");
+
+  Handle h;
+  h.type = type_id;
+  h.input_size = input_size;
+  h.row_count = row_count;
+  h.byte_length = weight_len;
+  h.g = choose_geometry((int)(input_size / kQK));
+  h.tiles = (int)((row_count + h.g.R - 1) / h.g.R);
+  if (hipMalloc((void **)&h.data, weight_len) != hipSuccess) return fail(HP_ERR_OOM, "weight allocation failed");
+  if (type_id == kTypeQ6K) h.dplane = reinterpret_cast<uint16_t *>(h.data + row_count * (input_size / kQK) * 208);
+
+  const uint8_t *raw = static_cast<const uint8_t *>(src);
+  uint8_t *staging = nullptr;
+  if (!src_device) {
+    if (hipMalloc((void **)&staging, weight_len) != hipSuccess) {
+      (void)hipFree(h.data);
+      return fail(HP_ERR_OOM, "staging allocation failed");
+    }
+    hipError_t e = hipMemcpyAsync(staging, src, weight_len, hipMemcpyHostToDevice, s.stream);
+    if (e != hipSuccess) {
+      (void)hipFree(staging);
+      (void)hipFree(h.data);
+      return hip_fail(e, "hipMemcpyAsync(weights)");
+    }
+    raw = staging;
+  }
+  hipError_t e = launch_repack(type_id, raw, (int)row_count, h.g, h.data, h.dplane, s.stream);
+  if (e == hipSuccess) e = hipStreamSynchronize(s.stream);
+  if (staging) (void)hipFree(staging);
+  if (e != hipSuccess) {
+    (void)hipFree(h.data);
+    return hip_fail(e, "repack");
+  }
+  // reuse a free slot
+  size_t slot = s.handles.size();
+  for (size_t i = 0; i < s.handles.size(); i++)
+    if (!s.handles[i].live) {
+      slot = i;
+      break;
+    }
+  if (slot == s.handles.size()) s.handles.emplace_back();
+  h.generation = s.handles[slot].generation + 1;
+  h.live = true;
+  s.handles[slot] = h;
+  *out_handle = ((uint64_t)h.generation << 32) | (uint64_t)(slot + 1);
+  return HP_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+const char *hp_hip_status_string(int32_t status) {
+  switch (status) {
+    case HP_OK: return "ok";
+    case HP_ERR_SHAPE: return "shape mismatch";
+    case HP_ERR_HEADS: return "head count mismatch";
+    case HP_ERR_TYPE: return "unsupported type";
+    case HP_ERR_HIP: return "HIP runtime error";
+    case HP_ERR_HANDLE: return "unknown weight handle";
+    case HP_ERR_ARG: return "invalid argument";
+    case HP_ERR_NODEV: return "no GPU available";
+    case HP_ERR_OOM: return "device out of memory";
+    default: return "unknown status";
+  }
+}
+
+const char *hp_hip_last_error(void) { return g_last_error.c_str(); }
+
+int32_t hp_hip_init(int32_t device) {
+  State &s = st();
+  std::lock_guard<std::recursive_mutex> lock(s.mu);
+  if (s.ready && s.device != device) return fail(HP_ERR_ARG, "already initialised on another device");
+  return ensure_init(device);
+}
+
+int32_t hp_hip_device_count(int32_t *count) {
+  if (!count) return fail(HP_ERR_ARG, "null pointer");
+  int n = 0;
+  if (hipGetDeviceCount(&n) != hipSuccess) n = 0;
+  *count = n;
+  return HP_OK;
+}
+
+int32_t hp_hip_shutdown(void) {
+  State &s = st();
+  std::lock_guard<std::recursive_mutex> lock(s.mu);
+  if (!s.ready) return HP_OK;
+  (void)hipStreamSynchronize(s.stream);
+  for (auto &h : s.handles)
+    if (h.live) {
+      (void)hipFree(h.data);
+      h.live = false;
+    }
+  if (s.q8) (void)hipFree(s.q8);
+  if (s.q8d) (void)hipFree(s.q8d);
+  s.q8 = nullptr;
+  s.q8d = nullptr;
+  s.q8_cap_blocks = 0;
+  if (s.io_in) (void)hipFree(s.io_in);
+  s.io_in = nullptr;
+  s.io_in_cap = 0;
+  for (int i = 0; i < kMaxWeights; i++) {
+    if (s.io_out[i]) (void)hipFree(s.io_out[i]);
+    s.io_out[i] = nullptr;
+    s.io_out_cap[i] = 0;
+  }
+  prof_collect();
+  for (hipEvent_t e : s.event_pool) (void)hipEventDestroy(e);
+  s.event_pool.clear();
+  (void)hipStreamDestroy(s.stream);
+  s.stream = nullptr;
+  s.ready = false;
+  return HP_OK;
+}
+
+int32_t hp_hip_weight_upload(int32_t type_id, const uint8_t *weight, size_t weight_len, size_t input_size,
+                             size_t row_count, uint64_t *out_handle) {
+  std::lock_guard<std::recursive_mutex> lock(st().mu);
+  return upload_common(type_id, weight, false, weight_len, input_size, row_count, out_handle);
+}
+
+int32_t hp_hip_weight_upload_device(int32_t type_id, const void *d_weight, size_t weight_len, size_t input_size,
+                                    size_t row_count, uint64_t *out_handle) {
+  std::lock_guard<std::recursive_mutex> lock(st().mu);
+  return upload_common(type_id, d_weight, true, weight_len, input_size, row_count, out_handle);
+}
+
+int32_t hp_hip_weight_release(uint64_t handle) {
+  State &s = st();
+  std::lock_guard<std::recursive_mutex> lock(s.mu);
+  Handle *h = lookup(handle);
+  if (!h) return fail(HP_ERR_HANDLE, "unknown weight handle");
+  (void)hipStreamSynchronize(s.stream);
+  (void)hipFree(h->data);
+  h->data = nullptr;
+  h->dplane = nullptr;
+  h->live = false;
+  return HP_OK;
+}
+
+int32_t hp_hip_weight_info(uint64_t handle, int32_t *type_id, size_t *input_size, size_t *row_count,
+                           size_t *byte_length) {
+  std::lock_guard<std::recursive_mutex> lock(st().mu);
+  Handle *h = lookup(handle);
+  if (!h) return fail(HP_ERR_HANDLE, "unknown weight handle");
+  if (type_id) *type_id = h->type;
+  if (input_size) *input_size = h->input_size;
+  if (row_count) *row_count = h->row_count;
+  if (byte_length) *byte_length = h->byte_length;
+  return HP_OK;
+}
+
+int32_t hp_hip_matmul_multi_device(size_t count, const uint64_t *handles, const float *d_input, size_t input_len,
+                                   size_t input_size, size_t column_count, float *const *d_outputs,
+                                   const size_t *output_lens, void *stream) {
+  State &s = st();
+  std::lock_guard<std::recursive_mutex> lock(s.mu);
+  int32_t rc = ensure_init(s.ready ? s.device : 0);
+  if (rc != HP_OK) return rc;
+  if (count == 0 || count > (size_t)kMaxWeights || input_len != sat_mul(input_size, column_count))
+    return fail(HP_ERR_SHAPE, "multi matmul shape mismatch");
+  if (!handles || !output_lens || !d_outputs || (column_count && !d_input)) return fail(HP_ERR_ARG, "null pointer");
+  Handle *hs[kMaxWeights];
+  for (size_t i = 0; i < count; i++) {
+    hs[i] = lookup(handles[i]);
+    if (!hs[i]) return fail(HP_ERR_HANDLE, "unknown weight handle");
+    if (hs[i]->input_size != input_size) return fail(HP_ERR_SHAPE, "handle input size mismatch");
+    if (output_lens[i] != sat_mul(hs[i]->row_count, column_count))
+      return fail(HP_ERR_SHAPE, "output length mismatch");
+    if (column_count && !d_outputs[i]) return fail(HP_ERR_ARG, "null output");
+  }
+  hipStream_t strm = stream ? static_cast<hipStream_t>(stream) : s.stream;
+  return run_matvec(count, hs, d_input, input_size, column_count, d_outputs, strm);
+}
+
+int32_t hp_hip_matmul_multi(size_t count, const uint64_t *handles, const float *input, size_t input_len,
+                            size_t input_size, size_t column_count, float *const *outputs,
+                            const size_t *output_lens) {
+  State &s = st();
+  std::lock_guard<std::recursive_mutex> lock(s.mu);
+  int32_t rc = ensure_init(s.ready ? s.device : 0);
+  if (rc != HP_OK) return rc;
+  if (count == 0 || count > (size_t)kMaxWeights || input_len != sat_mul(input_size, column_count))
+    return fail(HP_ERR_SHAPE, "multi matmul shape mismatch");
+  if (!handles || !output_lens || !outputs || (column_count && !input)) return fail(HP_ERR_ARG, "null pointer");
+  Handle *hs[kMaxWeights];
+  for (size_t i = 0; i < count; i++) {
+    hs[i] = lookup(handles[i]);
+    if (!hs[i]) return fail(HP_ERR_HANDLE, "unknown weight handle");
+    if (hs[i]->input_size != input_size) return fail(HP_ERR_SHAPE, "handle input size mismatch");
+    if (output_lens[i] != sat_mul(hs[i]->row_count, column_count))
+      return fail(HP_ERR_SHAPE, "output length mismatch");
+    if (column_count && !outputs[i]) return fail(HP_ERR_ARG, "null output");
+  }
+  if (column_count == 0) return HP_OK;
+  rc = grow((void **)&s.io_in, &s.io_in_cap, input_len * sizeof(float));
+  if (rc != HP_OK) return rc;
+  float *douts[kMaxWeights];
+  for (size_t i = 0; i < count; i++) {
+    rc = grow((void **)&s.io_out[i], &s.io_out_cap[i], output_lens[i] * sizeof(float));
+    if (rc != HP_OK) return rc;
+    douts[i] = s.io_out[i];
+  }
+  HP_HIP_TRY(hipMemcpyAsync(s.io_in, input, input_len * sizeof(float), hipMemcpyHostToDevice, s.stream));
+  rc = run_matvec(count, hs, s.io_in, input_size, column_count, douts, s.stream);
+  if (rc != HP_OK) return rc;
+  for (size_t i = 0; i < count; i++)
+    HP_HIP_TRY(hipMemcpyAsync(outputs[i], douts[i], output_lens[i] * sizeof(float), hipMemcpyDeviceToHost, s.stream));
+  HP_HIP_TRY(hipStreamSynchronize(s.stream));
+  return HP_OK;
+}
+
+int32_t hp_hip_matmul(uint64_t handle, const float *input, size_t input_len, size_t input_size, size_t row_count,
+                      size_t column_count, float *output, size_t output_len) {
+  State &s = st();
+  std::lock_guard<std::recursive_mutex> lock(s.mu);
+  Handle *h = lookup(handle);
+  if (!h) return fail(HP_ERR_HANDLE, "unknown weight handle");
+  if (h->input_size != input_size || h->row_count != row_count)
+    return fail(HP_ERR_SHAPE, "resident handle shape mismatch");
+  if (input_len != sat_mul(input_size, column_count) || output_len != sat_mul(row_count, column_count))
+    return fail(HP_ERR_SHAPE, "matmul shape mismatch");
+  float *outs[1] = {output};
+  size_t lens[1] = {output_len};
+  return hp_hip_matmul_multi(1, &handle, input, input_len, input_size, column_count, outs, lens);
+}
+
+int32_t hp_hip_dequantize(uint64_t handle, size_t row_start, size_t row_count, float *output, size_t output_len) {
+  State &s = st();
+  std::lock_guard<std::recursive_mutex> lock(s.mu);
+  Handle *h = lookup(handle);
+  if (!h) return fail(HP_ERR_HANDLE, "unknown weight handle");
+  if (!output && row_count) return fail(HP_ERR_ARG, "null pointer");
+  if (row_start > h->row_count || row_count > h->row_count - row_start ||
+      output_len != sat_mul(row_count, h->input_size))
+    return fail(HP_ERR_SHAPE, "dequantize range mismatch");
+  if (row_count == 0) return HP_OK;
+  float *d = nullptr;
+  if (hipMalloc((void **)&d, output_len * sizeof(float)) != hipSuccess) return fail(HP_ERR_OOM, "dequant buffer");
+  hipError_t e = launch_dequantize(h->type, h->data, h->dplane, (int)h->row_count, h->g, (int)row_start,
+                                   (int)row_count, d, s.stream);
+  if (e == hipSuccess) e = hipMemcpyAsync(output, d, output_len * sizeof(float), hipMemcpyDeviceToHost, s.stream);
+  if (e == hipSuccess) e = hipStreamSynchronize(s.stream);
+  (void)hipFree(d);
+  if (e != hipSuccess) return hip_fail(e, "dequantize");
+  return HP_OK;
+}
+
+int32_t hp_hip_stats(hp_hip_stats_t *out) {
+  State &s = st();
+  std::lock_guard<std::recursive_mutex> lock(s.mu);
+  if (!out) return fail(HP_ERR_ARG, "null pointer");
+  hp_hip_stats_t r{};
+  for (auto &h : s.handles)
+    if (h.live) {
+      r.handle_count++;
+      r.resident_bytes += h.byte_length;
+    }
+  r.scratch_bytes = s.q8_cap_blocks * (kQ8BlockBytes + sizeof(float)) + s.io_in_cap;
+  for (int i = 0; i < kMaxWeights; i++) r.scratch_bytes += s.io_out_cap[i];
+  r.matmul_calls = s.matmul_calls;
+  r.kernel_launches = s.launches;
+  r.device = s.device;
+  r.compute_units = s.num_cus;
+  *out = r;
+  return HP_OK;
+}
+
+int32_t hp_hip_synchronize(void) {
+  State &s = st();
+  std::lock_guard<std::recursive_mutex> lock(s.mu);
+  if (!s.ready) return HP_OK;
+  HP_HIP_TRY(hipStreamSynchronize(s.stream));
+  return HP_OK;
+}
+
+int32_t hp_hip_profile(int32_t enable) {
+  State &s = st();
+  std::lock_guard<std::recursive_mutex> lock(s.mu);
+  prof_collect();
+  for (auto &p : s.prof) {
+    p.total_ms = 0;
+    p.launches = 0;
+  }
+  s.profiling = enable != 0;
+  return HP_OK;
+}
+
+int32_t hp_hip_profile_read(int32_t kernel, double *total_ms, uint64_t *launches) {
+  State &s = st();
+  std::lock_guard<std::recursive_mutex> lock(s.mu);
+  if (kernel < 0 || kernel >= HP_KERNEL_COUNT) return fail(HP_ERR_ARG, "kernel id out of range");
+  prof_collect();
+  if (total_ms) *total_ms = s.prof[kernel].total_ms;
+  if (launches) *launches = s.prof[kernel].launches;
+  return HP_OK;
+}
+
+}  // extern "C"

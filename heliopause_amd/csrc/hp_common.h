@@ -1,0 +1,86 @@
+// hp_common.h -- shared definitions of the gfx950 quantized-projection runner.
+//
+// Device layouts (all byte counts equal the GGUF tensor's byte count):
+//
+// Weight tile layout.  A weight of N rows x nb super-blocks is cut into
+// tiles of R rows.  Lane k of a wave handles row r = k / S and block slot
+// s = k % S; iteration i covers blocks i*S .. i*S+S-1 (S divides nb).  A
+// tile stores, per iteration, CH chunks of 16 bytes for each of its Rt*S
+// lanes, chunk-major, so one 16-byte load per lane reads Rt*S*16
+// contiguous bytes:
+//     tile_base(t)      = t * R * nb * CH * 16
+//     chunk(t, i, c, k) = tile_base(t) + ((i * CH + c) * Rt * S + k) * 16
+// Q4_K (CH = 9): chunk 0 = bytes 0..15 of the GGUF block (d, dmin, 12
+//   scale/min bytes).  Chunks 1..8 hold 32 dwords D[p][l] (p = 0..3, l =
+//   0..7, dword 8p+l) with byte c of D[p][l] = qs[32p + 8c + l]: the four
+//   elements 32j+8c+l (c = 0..3) that share accumulator lane l sit in one
+//   dword (low nibbles: sub-block j = 2p, high nibbles: j = 2p+1).
+// Q6_K (CH = 13): chunks 0..7 hold Dql[p][l] with byte c = nibble of
+//   element (2p, c, l) | nibble of element (2p+1, c, l) << 4; chunks 8..11
+//   hold Dqh[q][l] with byte c = qh[32q + 8c + l] ^ 0xAA (each 2-bit field
+//   stores hi ^ 2, so (nibble | field << 4) is the 6-bit two's complement of
+//   q - 32); chunk 12 = the 16 int8 scales.  The f16 d of every row-block
+//   sits in a plane after all tiles, in tile order.
+//
+// Q8_K activation layout (per column m, per block b, 272 bytes): 64 dwords
+// X[j][l] (j = 0..7, l = 0..7, dword 8j+l) with byte c = q8[32j + 8c + l],
+// then the 8 int16 sums of 32 (bsums32).  The f32 d of each block is kept
+// in a separate [M][nb] array.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+namespace hp {
+
+constexpr int kQK = 256;
+constexpr int kTypeQ4K = 1;
+constexpr int kTypeQ6K = 3;
+constexpr int kQ8BlockBytes = 272;
+constexpr int kMaxWeights = 4;
+constexpr int kMaxCols = 8;  // columns per matvec launch
+
+__host__ __device__ constexpr int chunks_for(int type) { return type == kTypeQ4K ? 9 : 13; }
+__host__ __device__ constexpr int block_bytes(int type) { return type == kTypeQ4K ? 144 : 210; }
+
+// Tile geometry shared by every weight of one launch (depends on nb only).
+struct TileGeom {
+  int nb;     // blocks per row
+  int S;      // block slots per wave iteration
+  int R;      // rows per tile (R * S <= 64)
+  int iters;  // nb / S
+};
+
+TileGeom choose_geometry(int nb);
+
+struct WeightDesc {
+  const uint8_t *data;    // tiles
+  const uint16_t *dplane; // Q6_K: f16 d per row-block in tile order; else null
+  float *out;             // [M][N] output (device)
+  int type;
+  int rows;               // N
+  int tiles;              // ceil(N / R)
+  int tile_begin;         // first global tile index of this weight
+};
+
+struct MatvecArgs {
+  WeightDesc w[kMaxWeights];
+  int count;
+  int total_tiles;
+  TileGeom g;
+  const uint8_t *q8;  // [cols][nb][272]
+  const float *q8d;   // [cols][nb]
+  int cols;           // columns in this launch (<= kMaxCols)
+  int out_col0;       // first output column written by this launch
+};
+
+// Launchers (return hipError_t of the launch).
+hipError_t launch_q8k_quantize(const float *x, int k, int cols, uint8_t *q8, float *q8d, hipStream_t s);
+hipError_t launch_matvec(const MatvecArgs &a, int num_cus, hipStream_t s);
+hipError_t launch_repack(int type, const uint8_t *raw, int rows, const TileGeom &g, uint8_t *tiles,
+                         uint16_t *dplane, hipStream_t s);
+hipError_t launch_dequantize(int type, const uint8_t *tiles, const uint16_t *dplane, int rows,
+                             const TileGeom &g, int row_start, int row_count, float *out, hipStream_t s);
+
+}  // namespace hp

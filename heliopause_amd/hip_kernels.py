@@ -1,0 +1,319 @@
+"""Host mirror of heliopause's resident quantized-weight runner API, on HIP.
+
+Mirrors ``packages/engine/src/runner/wasm/wasm-kernels.ts`` function by
+function (same names with ``Wasm`` -> ``Hip``, same argument meaning, same
+error behaviour), calling the C ABI in ``include/hp_hip.h`` through ctypes:
+
+==========================================  =========================================
+reference (wasm-kernels.ts)                 this module
+==========================================  =========================================
+``checkWasmSupport`` 1657-1675              ``checkHipSupport``
+``createWasmQuantizedWeightHandle`` 520     ``createHipQuantizedWeightHandle``
+``releaseWasmQuantizedWeightHandle`` 576    ``releaseHipQuantizedWeightHandle``
+``wasmResidentWeightStats`` 586             ``hipResidentWeightStats``
+``matMulQuantizedWasmResident`` 593         ``matMulQuantizedHipResident``
+``matMulQuantizedWasmResidentMulti`` 648    ``matMulQuantizedHipResidentMulti``
+``assertWasmOk`` 1882-1896                  ``assertHipOk``
+``quantizedTypeId`` 1908-1923               ``quantizedTypeId``
+==========================================  =========================================
+
+Unsupported types return ``None`` (the reference's ``undefined``) so a caller
+can fall back; shape errors raise.  There is no CPU fallback in this module:
+if ``libhp_hip.so`` is missing or no GPU is present, calls raise.
+"""
+from __future__ import annotations
+
+import ctypes
+from dataclasses import dataclass
+from pathlib import Path
+from typing import Optional, Sequence
+
+import numpy as np
+
+PKG = Path(__file__).resolve().parent
+LIB_PATH = PKG / "libhp_hip.so"
+
+HP_OK, HP_ERR_SHAPE, HP_ERR_HEADS, HP_ERR_TYPE = 0, 1, 2, 3
+HP_ERR_HIP, HP_ERR_HANDLE, HP_ERR_ARG, HP_ERR_NODEV, HP_ERR_OOM = 16, 17, 18, 19, 20
+HP_KERNEL_Q8K, HP_KERNEL_MATVEC, HP_KERNEL_TOPK, HP_KERNEL_GEGLU = 0, 1, 2, 3
+
+TYPE_IDS = {"Q4_K": 1, "Q5_K": 2, "Q6_K": 3, "IQ4_XS": 4, "Q8_0": 5, "Q4_0": 6}
+SUPPORTED = ("Q4_K", "Q6_K")
+BLOCK = {"Q4_K": (256, 144), "Q6_K": (256, 210)}
+
+
+class HipUnavailable(RuntimeError):
+    """The HIP extension is not built or cannot be loaded."""
+
+
+class HipStats(ctypes.Structure):
+    _fields_ = [
+        ("handle_count", ctypes.c_uint64),
+        ("resident_bytes", ctypes.c_uint64),
+        ("scratch_bytes", ctypes.c_uint64),
+        ("matmul_calls", ctypes.c_uint64),
+        ("kernel_launches", ctypes.c_uint64),
+        ("device", ctypes.c_int32),
+        ("compute_units", ctypes.c_int32),
+    ]
+
+
+_lib: Optional[ctypes.CDLL] = None
+_u64 = ctypes.c_uint64
+_sz = ctypes.c_size_t
+_f32p = ctypes.POINTER(ctypes.c_float)
+_u8p = ctypes.POINTER(ctypes.c_uint8)
+_u32p = ctypes.POINTER(ctypes.c_uint32)
+
+
+def _declare(L: ctypes.CDLL) -> None:
+    i32 = ctypes.c_int32
+    L.hp_hip_status_string.argtypes = [i32]
+    L.hp_hip_status_string.restype = ctypes.c_char_p
+    L.hp_hip_last_error.argtypes = []
+    L.hp_hip_last_error.restype = ctypes.c_char_p
+    L.hp_hip_init.argtypes = [i32]
+    L.hp_hip_shutdown.argtypes = []
+    L.hp_hip_device_count.argtypes = [ctypes.POINTER(i32)]
+    L.hp_hip_weight_upload.argtypes = [i32, ctypes.c_void_p, _sz, _sz, _sz, ctypes.POINTER(_u64)]
+    L.hp_hip_weight_upload_device.argtypes = [i32, ctypes.c_void_p, _sz, _sz, _sz, ctypes.POINTER(_u64)]
+    L.hp_hip_weight_release.argtypes = [_u64]
+    L.hp_hip_weight_info.argtypes = [_u64, ctypes.POINTER(i32), ctypes.POINTER(_sz), ctypes.POINTER(_sz),
+                                     ctypes.POINTER(_sz)]
+    L.hp_hip_matmul.argtypes = [_u64, ctypes.c_void_p, _sz, _sz, _sz, _sz, ctypes.c_void_p, _sz]
+    L.hp_hip_matmul_multi.argtypes = [_sz, ctypes.POINTER(_u64), ctypes.c_void_p, _sz, _sz, _sz,
+                                      ctypes.POINTER(ctypes.c_void_p), ctypes.POINTER(_sz)]
+    L.hp_hip_matmul_multi_device.argtypes = [_sz, ctypes.POINTER(_u64), ctypes.c_void_p, _sz, _sz, _sz,
+                                             ctypes.POINTER(ctypes.c_void_p), ctypes.POINTER(_sz), ctypes.c_void_p]
+    L.hp_hip_dequantize.argtypes = [_u64, _sz, _sz, ctypes.c_void_p, _sz]
+    L.hp_hip_stats.argtypes = [ctypes.POINTER(HipStats)]
+    L.hp_hip_synchronize.argtypes = []
+    L.hp_hip_profile.argtypes = [i32]
+    L.hp_hip_profile_read.argtypes = [i32, ctypes.POINTER(ctypes.c_double), ctypes.POINTER(_u64)]
+    for name in ("hp_hip_init", "hp_hip_shutdown", "hp_hip_device_count", "hp_hip_weight_upload",
+                 "hp_hip_weight_upload_device", "hp_hip_weight_release", "hp_hip_weight_info", "hp_hip_matmul",
+                 "hp_hip_matmul_multi", "hp_hip_matmul_multi_device", "hp_hip_dequantize", "hp_hip_stats",
+                 "hp_hip_synchronize", "hp_hip_profile", "hp_hip_profile_read"):
+        getattr(L, name).restype = i32
+    _declare_optional(L)
+
+
+def _declare_optional(L: ctypes.CDLL) -> None:
+    """Entry points added alongside the matmul ones (top-k, GeGLU)."""
+    i32 = ctypes.c_int32
+    if hasattr(L, "hp_hip_matmul_topk"):
+        L.hp_hip_matmul_topk.argtypes = [_u64, ctypes.c_void_p, _sz, _sz, _sz, _sz, ctypes.c_void_p,
+                                         ctypes.c_void_p, _sz]
+        L.hp_hip_matmul_topk.restype = i32
+    if hasattr(L, "hp_hip_topk_device"):
+        L.hp_hip_topk_device.argtypes = [ctypes.c_void_p, _sz, _sz, _sz, ctypes.c_void_p, ctypes.c_void_p,
+                                         ctypes.c_void_p]
+        L.hp_hip_topk_device.restype = i32
+    if hasattr(L, "hp_hip_topk"):
+        L.hp_hip_topk.argtypes = [ctypes.c_void_p, _sz, _sz, _sz, ctypes.c_void_p, ctypes.c_void_p, _sz]
+        L.hp_hip_topk.restype = i32
+    if hasattr(L, "hp_hip_geglu"):
+        L.hp_hip_geglu.argtypes = [ctypes.c_void_p, ctypes.c_void_p, _sz, ctypes.c_void_p]
+        L.hp_hip_geglu.restype = i32
+    if hasattr(L, "hp_hip_geglu_device"):
+        L.hp_hip_geglu_device.argtypes = [ctypes.c_void_p, ctypes.c_void_p, _sz, ctypes.c_void_p, ctypes.c_void_p]
+        L.hp_hip_geglu_device.restype = i32
+
+
+def lib() -> ctypes.CDLL:
+    """Load libhp_hip.so (raises HipUnavailable; never falls back)."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not LIB_PATH.exists():
+        raise HipUnavailable(f"{LIB_PATH} is not built (run __graft_entry__.build())")
+    try:
+        L = ctypes.CDLL(str(LIB_PATH))
+    except OSError as exc:  # pragma: no cover - depends on the host
+        raise HipUnavailable(f"cannot load {LIB_PATH}: {exc}") from exc
+    _declare(L)
+    _lib = L
+    return L
+
+
+def status_string(code: int) -> str:
+    return lib().hp_hip_status_string(code).decode()
+
+
+def last_error() -> str:
+    return lib().hp_hip_last_error().decode()
+
+
+def assertHipOk(code: int, kernel_name: str) -> None:
+    """assertWasmOk (wasm-kernels.ts:1882-1896) with the HIP status codes."""
+    if code == HP_OK:
+        return
+    if code == HP_ERR_SHAPE:
+        raise ValueError(f"{kernel_name} hip shape mismatch")
+    if code == HP_ERR_HEADS:
+        raise ValueError(f"{kernel_name} hip head count mismatch")
+    if code == HP_ERR_TYPE:
+        raise TypeError(f"{kernel_name} hip unsupported type")
+    detail = ""
+    try:
+        detail = last_error()
+    except HipUnavailable:
+        pass
+    raise RuntimeError(f"{kernel_name} hip failed with code {code} ({detail})")
+
+
+def quantizedTypeId(type_name: str) -> Optional[int]:
+    """quantizedTypeId (wasm-kernels.ts:1908-1923)."""
+    return TYPE_IDS.get(type_name)
+
+
+def checkHipSupport() -> dict:
+    """checkWasmSupport analog: {'available': bool, 'reason'?: str, 'error'?: str}."""
+    try:
+        L = lib()
+    except HipUnavailable as exc:
+        return {"available": False, "reason": "module-missing", "error": str(exc)}
+    n = ctypes.c_int32(0)
+    L.hp_hip_device_count(ctypes.byref(n))
+    if n.value <= 0:
+        return {"available": False, "reason": "device-missing"}
+    return {"available": True}
+
+
+@dataclass
+class HipQuantizedWeightHandle:
+    """WasmQuantizedWeightHandle (wasm-kernels.ts:387-397) on HBM."""
+
+    handle: int
+    type: str
+    byteLength: int
+    rowCount: int
+    inputSize: int
+    released: bool = False
+
+
+def _f32(a) -> np.ndarray:
+    return np.ascontiguousarray(a, dtype=np.float32).reshape(-1)
+
+
+def createHipQuantizedWeightHandle(type_name: str, weight_bytes, input_size: int,
+                                   row_count: int) -> Optional[HipQuantizedWeightHandle]:
+    """Upload GGUF super-blocks once into HBM (createWasmQuantizedWeightHandle, 520-574)."""
+    if type_name not in TYPE_IDS or type_name not in SUPPORTED:
+        return None
+    if input_size <= 0 or row_count <= 0:
+        raise ValueError(f"Resident quantized weight shape mismatch: inputSize={input_size} rowCount={row_count}")
+    if isinstance(weight_bytes, np.ndarray):
+        data = np.ascontiguousarray(weight_bytes, dtype=np.uint8).reshape(-1)
+    else:
+        data = np.frombuffer(bytes(weight_bytes), dtype=np.uint8)
+    out = _u64(0)
+    code = lib().hp_hip_weight_upload(TYPE_IDS[type_name], data.ctypes.data, data.size, input_size, row_count,
+                                      ctypes.byref(out))
+    if code == HP_ERR_TYPE:
+        return None
+    assertHipOk(code, "createQuantizedWeightHandle")
+    return HipQuantizedWeightHandle(out.value, type_name, int(data.size), row_count, input_size)
+
+
+def releaseHipQuantizedWeightHandle(handle: HipQuantizedWeightHandle) -> None:
+    """releaseWasmQuantizedWeightHandle (576-584): unknown handles are ignored."""
+    if handle.released:
+        return
+    lib().hp_hip_weight_release(handle.handle)
+    handle.released = True
+
+
+def hipResidentWeightStats() -> dict:
+    """wasmResidentWeightStats (586-591) plus runner counters."""
+    s = HipStats()
+    assertHipOk(lib().hp_hip_stats(ctypes.byref(s)), "residentWeightStats")
+    return {
+        "instanceCount": 1 if s.device >= 0 else 0,
+        "residentBytes": int(s.resident_bytes),
+        "handleCount": int(s.handle_count),
+        "scratchBytes": int(s.scratch_bytes),
+        "matmulCalls": int(s.matmul_calls),
+        "kernelLaunches": int(s.kernel_launches),
+        "device": int(s.device),
+        "computeUnits": int(s.compute_units),
+    }
+
+
+def matMulQuantizedHipResident(handle: HipQuantizedWeightHandle, input_columns, input_size: int, row_count: int,
+                               column_count: int) -> np.ndarray:
+    """matMulQuantizedWasmResident (593-646): returns [columnCount * rowCount] f32."""
+    if handle.released:
+        raise RuntimeError(f"Resident quantized matmul handle {handle.handle} is not available")
+    if handle.inputSize != input_size or handle.rowCount != row_count:
+        raise ValueError(f"Resident quantized matmul handle shape mismatch: {handle.inputSize}x{handle.rowCount}")
+    x = _f32(input_columns)
+    if x.size != input_size * column_count:
+        raise ValueError(f"Resident quantized matmul input shape mismatch: {x.size}")
+    out = np.empty(row_count * column_count, dtype=np.float32)
+    code = lib().hp_hip_matmul(handle.handle, x.ctypes.data, x.size, input_size, row_count, column_count,
+                               out.ctypes.data, out.size)
+    assertHipOk(code, "matMulQuantizedResident")
+    return out
+
+
+def matMulQuantizedHipResidentMulti(handles: Sequence[HipQuantizedWeightHandle], input_columns, input_size: int,
+                                    column_count: int) -> Optional[list]:
+    """matMulQuantizedWasmResidentMulti (648-749): 2..4 handles, one shared Q8_K."""
+    if len(handles) < 2 or len(handles) > 4:
+        return None
+    x = _f32(input_columns)
+    if x.size != input_size * column_count:
+        raise ValueError(f"Resident quantized multi matmul input shape mismatch: {x.size}")
+    for h in handles:
+        if h.inputSize != input_size:
+            raise ValueError(f"Resident quantized multi matmul handle shape mismatch: {h.inputSize}")
+        if h.released:
+            raise RuntimeError(f"Resident quantized multi matmul handle {h.handle} is not available")
+    n = len(handles)
+    outs = [np.empty(h.rowCount * column_count, dtype=np.float32) for h in handles]
+    hs = (_u64 * n)(*[h.handle for h in handles])
+    optr = (ctypes.c_void_p * n)(*[o.ctypes.data for o in outs])
+    olen = (_sz * n)(*[o.size for o in outs])
+    code = lib().hp_hip_matmul_multi(n, hs, x.ctypes.data, x.size, input_size, column_count, optr, olen)
+    assertHipOk(code, "MatMulQuantizedResidentMulti")
+    return outs
+
+
+def dequantizeHipResident(handle: HipQuantizedWeightHandle, row_start: int, row_count: int) -> np.ndarray:
+    """Dequantised rows [row_start, row_start+row_count) as [row_count][inputSize] f32."""
+    out = np.empty((row_count, handle.inputSize), dtype=np.float32)
+    code = lib().hp_hip_dequantize(handle.handle, row_start, row_count, out.ctypes.data, out.size)
+    assertHipOk(code, "dequantize")
+    return out
+
+
+# ---- device-pointer entry points (inputs/outputs already in HBM) -----------------
+def matmul_multi_device(handles: Sequence[int], d_input: int, input_size: int, column_count: int,
+                        d_outputs: Sequence[int], output_lens: Sequence[int], stream: int = 0) -> None:
+    n = len(handles)
+    hs = (_u64 * n)(*handles)
+    optr = (ctypes.c_void_p * n)(*d_outputs)
+    olen = (_sz * n)(*output_lens)
+    code = lib().hp_hip_matmul_multi_device(n, hs, d_input, input_size * column_count, input_size, column_count,
+                                            optr, olen, stream or None)
+    assertHipOk(code, "matmulMultiDevice")
+
+
+def profile(enable: bool) -> None:
+    assertHipOk(lib().hp_hip_profile(1 if enable else 0), "profile")
+
+
+def profile_read(kernel: int) -> tuple[float, int]:
+    ms = ctypes.c_double(0)
+    n = _u64(0)
+    assertHipOk(lib().hp_hip_profile_read(kernel, ctypes.byref(ms), ctypes.byref(n)), "profileRead")
+    return ms.value, n.value
+
+
+def synchronize() -> None:
+    assertHipOk(lib().hp_hip_synchronize(), "synchronize")
+
+
+def shutdown() -> None:
+    assertHipOk(lib().hp_hip_shutdown(), "shutdown")

@@ -1,0 +1,139 @@
+/*
+ * hp_hip.h -- C ABI of the MI355X (gfx950) quantized-projection runner.
+ *
+ * Drop-in boundary for heliopause's resident-weight matmul path.  The
+ * reference exposes the same operations as WASM exports
+ * (packages/engine/wasm-kernels/src/lib.rs:23-536) wrapped by the TS runner
+ * API in packages/engine/src/runner/wasm/wasm-kernels.ts.  This ABI keeps
+ * the reference's type ids, status codes, argument order and layouts:
+ *   input  [column_count][input_size] f32   (column m at m * input_size)
+ *   output [column_count][row_count]  f32   (out[m * row_count + row])
+ *   weight [row_count][row_bytes]     GGUF super-blocks as stored
+ * Plain pointers and sizes only.  Host-pointer entry points copy through
+ * the library's HIP stream and return when results are in host memory;
+ * *_device entry points take device pointers and are asynchronous on the
+ * given stream.  Calls are serialised by an internal lock; results written
+ * by concurrent calls on one device must not overlap.
+ */
+#ifndef HP_HIP_H
+#define HP_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Status codes.  0..3 are lib.rs:7-10 (OK, ERR_SHAPE, ERR_HEADS, ERR_TYPE);
+ * the TS wrapper maps them like assertWasmOk (wasm-kernels.ts:1882-1896).
+ * Codes >= 16 are this runtime's own. */
+#define HP_OK 0
+#define HP_ERR_SHAPE 1
+#define HP_ERR_HEADS 2
+#define HP_ERR_TYPE 3
+#define HP_ERR_HIP 16     /* a HIP runtime call failed (see hp_hip_last_error) */
+#define HP_ERR_HANDLE 17  /* unknown or released weight handle */
+#define HP_ERR_ARG 18     /* null pointer or out-of-range argument */
+#define HP_ERR_NODEV 19   /* no usable GPU */
+#define HP_ERR_OOM 20     /* device allocation failed */
+
+/* Type ids: lib.rs:12-17 (wasm-kernels.ts:1908-1923).  This runner
+ * implements Q4_K and Q6_K; the others return HP_ERR_TYPE so the caller
+ * falls back to the WASM runner, as wasm-kernels.ts:424-431 does. */
+#define HP_TYPE_Q4_K 1
+#define HP_TYPE_Q5_K 2
+#define HP_TYPE_Q6_K 3
+#define HP_TYPE_IQ4_XS 4
+#define HP_TYPE_Q8_0 5
+#define HP_TYPE_Q4_0 6
+
+/* Kernel ids for hp_hip_profile_read. */
+#define HP_KERNEL_Q8K 0
+#define HP_KERNEL_MATVEC 1
+#define HP_KERNEL_TOPK 2
+#define HP_KERNEL_GEGLU 3
+#define HP_KERNEL_COUNT 4
+
+typedef struct hp_hip_stats {
+  uint64_t handle_count;   /* live weight handles */
+  uint64_t resident_bytes; /* device bytes held by weight handles */
+  uint64_t scratch_bytes;  /* device bytes held by activation scratch */
+  uint64_t matmul_calls;
+  uint64_t kernel_launches;
+  int32_t device;
+  int32_t compute_units;
+} hp_hip_stats_t;
+
+/* Human-readable name of a status code (never NULL). */
+const char *hp_hip_status_string(int32_t status);
+/* Message describing the last failure on the calling thread ("" if none). */
+const char *hp_hip_last_error(void);
+
+/* Select the GPU and create the library stream (idempotent; other entry
+ * points call it with device 0 on first use).  Analog of the module
+ * instantiation behind prefillWasmExports (wasm-kernels.ts:1678-1741) and
+ * of checkWasmSupport (1657-1675): HP_ERR_NODEV when no GPU is usable. */
+int32_t hp_hip_init(int32_t device);
+/* Release every handle and the scratch buffers (shutdownWasmExecutionProvider,
+ * acceleration.ts:93-112). */
+int32_t hp_hip_shutdown(void);
+int32_t hp_hip_device_count(int32_t *count);
+
+/* Upload GGUF super-blocks once into an HBM-resident handle.  Replaces
+ * createWasmQuantizedWeightHandle (wasm-kernels.ts:520-574) and the scale
+ * preparation hp_prepare_quantized_scales_f32 (lib.rs:156-222): the GPU keeps
+ * no f32 side table.  weight_len must equal row_count * row_bytes. */
+int32_t hp_hip_weight_upload(int32_t type_id, const uint8_t *weight, size_t weight_len, size_t input_size,
+                             size_t row_count, uint64_t *out_handle);
+/* Same from a device buffer already holding the GGUF bytes. */
+int32_t hp_hip_weight_upload_device(int32_t type_id, const void *d_weight, size_t weight_len, size_t input_size,
+                                    size_t row_count, uint64_t *out_handle);
+/* releaseWasmQuantizedWeightHandle (wasm-kernels.ts:576-584). */
+int32_t hp_hip_weight_release(uint64_t handle);
+int32_t hp_hip_weight_info(uint64_t handle, int32_t *type_id, size_t *input_size, size_t *row_count,
+                           size_t *byte_length);
+
+/* matMulQuantizedWasmResident (wasm-kernels.ts:593-646) ->
+ * hp_matmul_quantized_prepared_f32 (lib.rs:224-298).  Q8_K-quantises each
+ * input column, then out[m*N+n] = vec_dot(row n, q8_m), bit-exact with the
+ * reference.  HP_ERR_SHAPE when the handle's shape differs from
+ * (input_size, row_count) or the lengths do not match. */
+int32_t hp_hip_matmul(uint64_t handle, const float *input, size_t input_len, size_t input_size, size_t row_count,
+                      size_t column_count, float *output, size_t output_len);
+
+/* matMulQuantizedWasmResidentMulti (wasm-kernels.ts:648-749) ->
+ * hp_matmul_quantized_prepared_multi_f32 (lib.rs:300-426): 1..4 handles of
+ * any supported type share one Q8_K quantisation per column and one launch.
+ * outputs[i] receives [column_count][rows_i]. */
+int32_t hp_hip_matmul_multi(size_t count, const uint64_t *handles, const float *input, size_t input_len,
+                            size_t input_size, size_t column_count, float *const *outputs,
+                            const size_t *output_lens);
+
+/* Device-pointer form of hp_hip_matmul_multi for chained on-device work
+ * (inputs and outputs stay in HBM).  stream: a hipStream_t, or NULL for the
+ * library stream.  Asynchronous. */
+int32_t hp_hip_matmul_multi_device(size_t count, const uint64_t *handles, const float *d_input, size_t input_len,
+                                   size_t input_size, size_t column_count, float *const *d_outputs,
+                                   const size_t *output_lens, void *stream);
+
+/* Dequantise rows [row_start, row_start + row_count) of a handle into f32
+ * [row_count][input_size] (lib.rs:1630-1664, 1709-1744; bit-exact).  Test
+ * hook proving the resident layout is lossless. */
+int32_t hp_hip_dequantize(uint64_t handle, size_t row_start, size_t row_count, float *output, size_t output_len);
+
+/* wasmResidentWeightStats (wasm-kernels.ts:586-591) plus call counters. */
+int32_t hp_hip_stats(hp_hip_stats_t *out);
+/* Wait for all work queued on the library stream. */
+int32_t hp_hip_synchronize(void);
+
+/* Kernel timing with HIP events on the stream each kernel is launched on.
+ * enable != 0 starts recording (and clears totals); read returns the total
+ * device milliseconds and launch count of one kernel id since enabling. */
+int32_t hp_hip_profile(int32_t enable);
+int32_t hp_hip_profile_read(int32_t kernel, double *total_ms, uint64_t *launches);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

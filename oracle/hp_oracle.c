@@ -1,0 +1,582 @@
+/*
+ * hp_oracle.c -- CPU restatement of heliopause's Q4_K/Q6_K projection path.
+ *
+ * TEST INFRASTRUCTURE ONLY (the checker, never the product).  See hp_oracle.h.
+ *
+ * Reference files followed (paths relative to the heliopause repository):
+ *   packages/engine/wasm-kernels/src/lib.rs     -- kernels and numerics
+ *   packages/engine/src/quant.ts                -- TS f16 conversions (gelu)
+ *   packages/engine/src/runner/wasm/layers.ts   -- gelu / GeGLU / softcap
+ *   packages/engine/src/runtime.ts              -- topK
+ *   packages/engine/src/runner/wasm/thread-pool.ts -- splitRows sharding
+ *
+ * Parity status of each function is listed in oracle/README.md.
+ */
+#include "hp_oracle.h"
+
+#include <math.h>
+#include <pthread.h>
+#include <stdlib.h>
+#include <string.h>
+
+#define QK_K 256
+
+static size_t sat_mul(size_t a, size_t b) {
+  size_t r;
+  if (__builtin_mul_overflow(a, b, &r)) return (size_t)-1;
+  return r;
+}
+
+static uint16_t rd16(const uint8_t *p) { return (uint16_t)(p[0] | (p[1] << 8)); }
+
+/* ---------------------------------------------------------------------- */
+/* lib.rs:2507-2532 float16_to_float32 (exact, keeps NaN payload bits).    */
+float hpo_f16_to_f32(uint16_t value) {
+  uint32_t sign = ((uint32_t)(value & 0x8000u)) << 16;
+  int32_t exponent = (value >> 10) & 0x1f;
+  uint32_t fraction = value & 0x03ffu;
+  uint32_t bits;
+  if (exponent == 0) {
+    if (fraction == 0) {
+      bits = sign;
+    } else {
+      uint32_t mantissa = fraction;
+      int32_t e = -14;
+      while ((mantissa & 0x0400u) == 0) {
+        mantissa <<= 1;
+        e -= 1;
+      }
+      mantissa &= 0x03ffu;
+      bits = sign | ((uint32_t)(e + 127) << 23) | (mantissa << 13);
+    }
+  } else if (exponent == 31) {
+    bits = sign | 0x7f800000u | (fraction << 13);
+  } else {
+    bits = sign | ((uint32_t)(exponent + 112) << 23) | (fraction << 13);
+  }
+  float f;
+  memcpy(&f, &bits, 4);
+  return f;
+}
+
+/* lib.rs:2534-2569 float32_to_float16 (round half up on the mantissa). */
+uint16_t hpo_f32_to_f16_rust(float value) {
+  uint32_t bits;
+  memcpy(&bits, &value, 4);
+  uint16_t sign = (uint16_t)((bits >> 16) & 0x8000u);
+  int32_t exponent = (int32_t)((bits >> 23) & 0xffu);
+  uint32_t mantissa = bits & 0x007fffffu;
+  if (exponent == 0xff) return mantissa == 0 ? (uint16_t)(sign | 0x7c00u) : (uint16_t)0x7e00u;
+  int32_t half_exponent = exponent - 127 + 15;
+  if (half_exponent >= 31) return (uint16_t)(sign | 0x7bffu);
+  if (half_exponent <= 0) {
+    if (half_exponent < -10) return sign;
+    uint32_t with_hidden = mantissa | 0x00800000u;
+    uint32_t shift = (uint32_t)(14 - half_exponent);
+    uint32_t rounded = (with_hidden + (1u << (shift - 1))) >> shift;
+    return (uint16_t)(sign | rounded);
+  }
+  uint32_t rounded_mantissa = mantissa + 0x00001000u;
+  if (rounded_mantissa & 0x00800000u) {
+    int32_t rounded_exponent = half_exponent + 1;
+    if (rounded_exponent >= 31) return (uint16_t)(sign | 0x7bffu);
+    return (uint16_t)(sign | (rounded_exponent << 10));
+  }
+  return (uint16_t)(sign | (half_exponent << 10) | (rounded_mantissa >> 13));
+}
+
+/* quant.ts:618-630 float16ToFloat32 (f64 result; exact for every input). */
+double hpo_f16_to_f64_ts(uint16_t value) {
+  double sign = (value & 0x8000u) ? -1.0 : 1.0;
+  int exponent = (value >> 10) & 0x1f;
+  int fraction = value & 0x03ff;
+  if (exponent == 0) return sign * ldexp(1.0, -14) * (fraction / 1024.0);
+  if (exponent == 31) return fraction == 0 ? sign * INFINITY : NAN;
+  return sign * ldexp(1.0, exponent - 15) * (1.0 + fraction / 1024.0);
+}
+
+/* quant.ts:671-681 roundTiesToEven */
+static double ts_round_ties_to_even(double value) {
+  double fl = floor(value);
+  double fraction = value - fl;
+  if (fraction < 0.5) return fl;
+  if (fraction > 0.5) return fl + 1.0;
+  return fmod(fl, 2.0) == 0.0 ? fl : fl + 1.0;
+}
+
+/* quant.ts:632-669 float32ToFloat16: saturates at 65504 and flushes
+ * |v| < 2^-24 to signed zero; otherwise rounds to nearest, ties to even. */
+uint16_t hpo_f64_to_f16_ts(double value) {
+  if (isnan(value)) return 0x7e00u;
+  if (value == INFINITY) return 0x7c00u;
+  if (value == -INFINITY) return 0xfc00u;
+  uint16_t sign = (value < 0 || (value == 0 && signbit(value))) ? 0x8000u : 0;
+  double a = fabs(value);
+  if (a == 0) return sign;
+  if (a >= 65504.0) return (uint16_t)(sign | 0x7bffu);
+  if (a < ldexp(1.0, -24)) return sign;
+  /* Math.floor(Math.log2(abs)) is exact for the f32 inputs this is used on;
+   * ilogb gives the same integer without a transcendental. */
+  int exponent = ilogb(a);
+  double mantissa = a / ldexp(1.0, exponent) - 1.0;
+  if (exponent < -14) {
+    double sub = ts_round_ties_to_even(a / ldexp(1.0, -24));
+    return (uint16_t)(sign | (uint16_t)sub);
+  }
+  double half_mantissa = ts_round_ties_to_even(mantissa * 1024.0);
+  if (half_mantissa == 1024.0) {
+    exponent += 1;
+    half_mantissa = 0.0;
+  }
+  return (uint16_t)(sign | ((exponent + 15) << 10) | (uint16_t)half_mantissa);
+}
+
+/* ---------------------------------------------------------------------- */
+/* lib.rs:1551-1561 quantized_row_bytes (only the two restated types). */
+size_t hpo_row_bytes(int32_t type_id, size_t elements) {
+  if (elements % QK_K != 0) return 0;
+  if (type_id == HPO_Q4_K) return elements / QK_K * 144;
+  if (type_id == HPO_Q6_K) return elements / QK_K * 210;
+  return 0;
+}
+
+/* lib.rs:2249-2259 get_scale_min_k4 */
+void hpo_get_scale_min_k4(int j, const uint8_t *q, uint8_t *sc, uint8_t *mn) {
+  if (j < 4) {
+    *sc = q[j] & 63;
+    *mn = q[j + 4] & 63;
+  } else {
+    *sc = (uint8_t)((q[j + 4] & 0x0f) | ((q[j - 4] >> 6) << 4));
+    *mn = (uint8_t)((q[j + 4] >> 4) | ((q[j] >> 6) << 4));
+  }
+}
+
+/* lib.rs:1630-1664 dequantize_q4_k: y = (d*sc)*q - (dmin*m), f32, no FMA. */
+int hpo_dequantize_q4_k(const uint8_t *bytes, size_t elements, float *out) {
+  if (elements % QK_K != 0) return 0;
+  for (size_t b = 0; b < elements / QK_K; b++) {
+    const uint8_t *blk = bytes + 144 * b;
+    float d = hpo_f16_to_f32(rd16(blk));
+    float dmin = hpo_f16_to_f32(rd16(blk + 2));
+    const uint8_t *scales = blk + 4;
+    const uint8_t *qs = blk + 16;
+    float *o = out + QK_K * b;
+    for (int g = 0; g < 4; g++) {
+      uint8_t sc1, m1, sc2, m2;
+      hpo_get_scale_min_k4(2 * g, scales, &sc1, &m1);
+      hpo_get_scale_min_k4(2 * g + 1, scales, &sc2, &m2);
+      float d1 = d * (float)sc1, d2 = d * (float)sc2;
+      float mm1 = dmin * (float)m1, mm2 = dmin * (float)m2;
+      for (int l = 0; l < 32; l++) o[64 * g + l] = d1 * (float)(qs[32 * g + l] & 0x0f) - mm1;
+      for (int l = 0; l < 32; l++) o[64 * g + 32 + l] = d2 * (float)(qs[32 * g + l] >> 4) - mm2;
+    }
+  }
+  return 1;
+}
+
+/* lib.rs:1709-1744 dequantize_q6_k: y = (d*sc)*(q-32), exact in f32. */
+int hpo_dequantize_q6_k(const uint8_t *bytes, size_t elements, float *out) {
+  if (elements % QK_K != 0) return 0;
+  for (size_t b = 0; b < elements / QK_K; b++) {
+    const uint8_t *blk = bytes + 210 * b;
+    const uint8_t *ql = blk, *qh = blk + 128, *scales = blk + 192;
+    float d = hpo_f16_to_f32(rd16(blk + 208));
+    float *o = out + QK_K * b;
+    for (int h = 0; h < 2; h++) {
+      for (int lane = 0; lane < 32; lane++) {
+        int is = lane / 16;
+        uint8_t qhb = qh[32 * h + lane];
+        int q1 = (int)((ql[64 * h + lane] & 0x0f) | (((qhb >> 0) & 3) << 4)) - 32;
+        int q2 = (int)((ql[64 * h + lane + 32] & 0x0f) | (((qhb >> 2) & 3) << 4)) - 32;
+        int q3 = (int)((ql[64 * h + lane] >> 4) | (((qhb >> 4) & 3) << 4)) - 32;
+        int q4 = (int)((ql[64 * h + lane + 32] >> 4) | (((qhb >> 6) & 3) << 4)) - 32;
+        o[128 * h + lane] = d * (float)(int8_t)scales[8 * h + is] * (float)q1;
+        o[128 * h + lane + 32] = d * (float)(int8_t)scales[8 * h + is + 2] * (float)q2;
+        o[128 * h + lane + 64] = d * (float)(int8_t)scales[8 * h + is + 4] * (float)q3;
+        o[128 * h + lane + 96] = d * (float)(int8_t)scales[8 * h + is + 6] * (float)q4;
+      }
+    }
+  }
+  return 1;
+}
+
+/* ---------------------------------------------------------------------- */
+/* Rust `f32 as i8`: saturating, NaN -> 0. */
+static int8_t sat_i8(float r) {
+  if (r != r) return 0;
+  if (r >= 127.0f) return 127;
+  if (r <= -128.0f) return -128;
+  return (int8_t)r;
+}
+
+/* lib.rs:1774-1811 quantize_q8_k.  First index of the largest |x| gives
+ * `max`; is = -127/max (correctly rounded f32 divide); q = min(127,
+ * round(is*x)) with ties away from zero; d = 1/is; bsums32 = sums of 32. */
+void hpo_quantize_q8_k(const float *x, size_t n, int8_t *qs, float *d, int16_t *bsums32) {
+  size_t nb = n / QK_K;
+  for (size_t b = 0; b < nb; b++) {
+    const float *xb = x + QK_K * b;
+    int8_t *qb = qs + QK_K * b;
+    float max = 0.0f, amax = 0.0f;
+    for (int i = 0; i < QK_K; i++) {
+      float v = xb[i];
+      float a = fabsf(v);
+      if (a > amax) {
+        amax = a;
+        max = v;
+      }
+    }
+    if (amax == 0.0f) {
+      memset(qb, 0, QK_K);
+      for (int g = 0; g < 8; g++) bsums32[8 * b + g] = 0;
+      d[b] = 0.0f;
+      continue;
+    }
+    float inverse_scale = -127.0f / max;
+    for (int i = 0; i < QK_K; i++) {
+      float p = inverse_scale * xb[i];
+      qb[i] = sat_i8(fminf(roundf(p), 127.0f));
+    }
+    for (int g = 0; g < 8; g++) {
+      int16_t sum = 0;
+      for (int i = 0; i < 32; i++) sum = (int16_t)(sum + qb[32 * g + i]);
+      bsums32[8 * b + g] = sum;
+    }
+    d[b] = 1.0f / inverse_scale;
+  }
+}
+
+/* ---------------------------------------------------------------------- */
+/* Integer part of one Q4_K block, lib.rs:2121-2160: nibbles unpacked to
+ * aux8 (2136-2146), sumi = sum_j bsums32[j]*min[j] (2148-2152),
+ * aux32[l] += sc[j] * sum_{c<4} q8[32j+8c+l]*aux8[32j+8c+l] (2154-2160 with
+ * accumulate_scaled_i8_i8_32_lanes 2443-2501). */
+void hpo_block_ints_q4_k(const uint8_t *blk, const int8_t *q8, const int16_t *bs,
+                         int32_t aux32[8], int32_t *sumi) {
+  uint8_t sc[8], mn[8];
+  for (int j = 0; j < 8; j++) hpo_get_scale_min_k4(j, blk + 4, &sc[j], &mn[j]);
+  int8_t aux8[QK_K];
+  const uint8_t *qs = blk + 16;
+  for (int g = 0; g < 4; g++) {
+    for (int l = 0; l < 32; l++) {
+      aux8[64 * g + l] = (int8_t)(qs[32 * g + l] & 0x0f);
+      aux8[64 * g + 32 + l] = (int8_t)(qs[32 * g + l] >> 4);
+    }
+  }
+  int32_t si = 0;
+  for (int j = 0; j < 8; j++) si += (int32_t)bs[j] * (int32_t)mn[j];
+  *sumi = si;
+  for (int l = 0; l < 8; l++) aux32[l] = 0;
+  for (int j = 0; j < 8; j++) {
+    int32_t s = sc[j];
+    for (int c = 0; c < 4; c++)
+      for (int l = 0; l < 8; l++)
+        aux32[l] += s * (int32_t)q8[32 * j + 8 * c + l] * (int32_t)aux8[32 * j + 8 * c + l];
+  }
+}
+
+/* Integer part of one Q6_K block, lib.rs:1928-1959: 6-bit unpack minus 32
+ * (1938-1949), then aux32[l] += sc[g] * sum_{c<2} q8[16g+8c+l]*aux8[16g+8c+l]
+ * (1951-1959 with accumulate_scaled_i8_i8_16_lanes 2265-2313). */
+void hpo_block_ints_q6_k(const uint8_t *blk, const int8_t *q8, int32_t aux32[8]) {
+  const uint8_t *ql = blk, *qh = blk + 128, *scales = blk + 192;
+  int8_t aux8[QK_K];
+  for (int h = 0; h < 2; h++) {
+    for (int lane = 0; lane < 32; lane++) {
+      uint8_t qhb = qh[32 * h + lane];
+      aux8[128 * h + lane] = (int8_t)((int16_t)((ql[64 * h + lane] & 0x0f) | (((qhb >> 0) & 3) << 4)) - 32);
+      aux8[128 * h + lane + 32] = (int8_t)((int16_t)((ql[64 * h + lane + 32] & 0x0f) | (((qhb >> 2) & 3) << 4)) - 32);
+      aux8[128 * h + lane + 64] = (int8_t)((int16_t)((ql[64 * h + lane] >> 4) | (((qhb >> 4) & 3) << 4)) - 32);
+      aux8[128 * h + lane + 96] = (int8_t)((int16_t)((ql[64 * h + lane + 32] >> 4) | (((qhb >> 6) & 3) << 4)) - 32);
+    }
+  }
+  for (int l = 0; l < 8; l++) aux32[l] = 0;
+  for (int g = 0; g < 16; g++) {
+    int32_t s = (int8_t)scales[g];
+    for (int c = 0; c < 2; c++)
+      for (int l = 0; l < 8; l++)
+        aux32[l] += s * (int32_t)q8[16 * g + 8 * c + l] * (int32_t)aux8[16 * g + 8 * c + l];
+  }
+}
+
+/* lib.rs:2116-2172 vec_dot_q4_k_q8_k_prepared.  The prepared f32 scales
+ * (lib.rs:156-222) are float16_to_float32 of the block's d/dmin, so they are
+ * read straight from the block here.  Float tail in Rust order, no FMA:
+ *   d = dW*dX; sums[l] += d*f32(aux32[l]); dm = dminW*dX; sumf -= dm*f32(sumi)
+ *   return sumf + sums.iter().sum()   (f32 Sum folds from -0.0). */
+float hpo_vec_dot_q4_k_q8_k(const uint8_t *row, size_t nblocks, const int8_t *qs,
+                            const float *d, const int16_t *bsums32) {
+  float sums[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+  float sumf = 0.0f;
+  for (size_t b = 0; b < nblocks; b++) {
+    const uint8_t *blk = row + 144 * b;
+    int32_t aux32[8], sumi;
+    hpo_block_ints_q4_k(blk, qs + QK_K * b, bsums32 + 8 * b, aux32, &sumi);
+    float dd = hpo_f16_to_f32(rd16(blk)) * d[b];
+    for (int l = 0; l < 8; l++) sums[l] += dd * (float)aux32[l];
+    float dm = hpo_f16_to_f32(rd16(blk + 2)) * d[b];
+    sumf -= dm * (float)sumi;
+  }
+  float t = -0.0f;
+  for (int l = 0; l < 8; l++) t += sums[l];
+  return sumf + t;
+}
+
+/* lib.rs:1923-1968 vec_dot_q6_k_q8_k_prepared. */
+float hpo_vec_dot_q6_k_q8_k(const uint8_t *row, size_t nblocks, const int8_t *qs, const float *d) {
+  float sums[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+  for (size_t b = 0; b < nblocks; b++) {
+    const uint8_t *blk = row + 210 * b;
+    int32_t aux32[8];
+    hpo_block_ints_q6_k(blk, qs + QK_K * b, aux32);
+    float dd = hpo_f16_to_f32(rd16(blk + 208)) * d[b];
+    for (int l = 0; l < 8; l++) sums[l] += dd * (float)aux32[l];
+  }
+  float t = -0.0f;
+  for (int l = 0; l < 8; l++) t += sums[l];
+  return t;
+}
+
+/* ---------------------------------------------------------------------- */
+typedef struct {
+  int8_t *qs;
+  float *d;
+  int16_t *bsums;
+} q8k_buf;
+
+static int q8k_alloc(q8k_buf *q, size_t k) {
+  q->qs = (int8_t *)malloc(k);
+  q->d = (float *)malloc(sizeof(float) * (k / QK_K + 1));
+  q->bsums = (int16_t *)malloc(sizeof(int16_t) * (k / 32 + 1));
+  return q->qs && q->d && q->bsums;
+}
+
+static void q8k_free(q8k_buf *q) {
+  free(q->qs);
+  free(q->d);
+  free(q->bsums);
+}
+
+static void dot_rows(int32_t type_id, const uint8_t *weight, size_t row_bytes, size_t nb,
+                     const q8k_buf *q, size_t row_begin, size_t row_end, float *out) {
+  for (size_t row = row_begin; row < row_end; row++) {
+    const uint8_t *r = weight + row * row_bytes;
+    out[row] = type_id == HPO_Q4_K ? hpo_vec_dot_q4_k_q8_k(r, nb, q->qs, q->d, q->bsums)
+                                   : hpo_vec_dot_q6_k_q8_k(r, nb, q->qs, q->d);
+  }
+}
+
+/* lib.rs:224-298 hp_matmul_quantized_prepared_f32 (checks in the same order). */
+int32_t hpo_matmul_quantized(int32_t type_id, const uint8_t *weight, size_t weight_len,
+                             const float *input, size_t input_len, size_t input_size,
+                             size_t row_count, size_t column_count, float *output,
+                             size_t output_len) {
+  if (input_len != sat_mul(input_size, column_count) || output_len != sat_mul(row_count, column_count))
+    return HPO_ERR_SHAPE;
+  size_t row_bytes = hpo_row_bytes(type_id, input_size);
+  if (row_bytes == 0) return HPO_ERR_TYPE;
+  if (weight_len != sat_mul(row_bytes, row_count)) return HPO_ERR_SHAPE;
+  q8k_buf q;
+  if (!q8k_alloc(&q, input_size)) {
+    q8k_free(&q);
+    return HPO_ERR_SHAPE;
+  }
+  size_t nb = input_size / QK_K;
+  for (size_t col = 0; col < column_count; col++) {
+    hpo_quantize_q8_k(input + col * input_size, input_size, q.qs, q.d, q.bsums);
+    dot_rows(type_id, weight, row_bytes, nb, &q, 0, row_count, output + col * row_count);
+  }
+  q8k_free(&q);
+  return HPO_OK;
+}
+
+/* lib.rs:300-426 hp_matmul_quantized_prepared_multi_f32: one Q8_K
+ * quantisation per column shared by every weight. */
+int32_t hpo_matmul_quantized_multi(size_t count, const float *input, size_t input_len,
+                                   size_t input_size, size_t column_count,
+                                   const int32_t *type_ids, const uint8_t *const *weights,
+                                   const size_t *weight_lens, const size_t *row_counts,
+                                   float *const *outputs, const size_t *output_lens) {
+  if (count == 0 || count > 4 || input_len != sat_mul(input_size, column_count)) return HPO_ERR_SHAPE;
+  for (size_t i = 0; i < count; i++) {
+    size_t row_bytes = hpo_row_bytes(type_ids[i], input_size);
+    if (row_bytes == 0) return HPO_ERR_TYPE;
+    if (weight_lens[i] != sat_mul(row_bytes, row_counts[i]) ||
+        output_lens[i] != sat_mul(row_counts[i], column_count))
+      return HPO_ERR_SHAPE;
+  }
+  q8k_buf q;
+  if (!q8k_alloc(&q, input_size)) {
+    q8k_free(&q);
+    return HPO_ERR_SHAPE;
+  }
+  size_t nb = input_size / QK_K;
+  for (size_t col = 0; col < column_count; col++) {
+    hpo_quantize_q8_k(input + col * input_size, input_size, q.qs, q.d, q.bsums);
+    for (size_t i = 0; i < count; i++) {
+      size_t row_bytes = hpo_row_bytes(type_ids[i], input_size);
+      dot_rows(type_ids[i], weights[i], row_bytes, nb, &q, 0, row_counts[i],
+               outputs[i] + col * row_counts[i]);
+    }
+  }
+  q8k_free(&q);
+  return HPO_OK;
+}
+
+/* ---------------------------------------------------------------------- */
+/* Threaded variants: thread-pool.ts:410-424 splitRows gives each worker a
+ * contiguous row shard (the first N mod T shards carry one extra row); each
+ * worker quantises every column itself and fills its rows of [M][N]
+ * (copyShardOutput, thread-pool.ts:426-443). */
+typedef struct {
+  size_t count;
+  const int32_t *type_ids;
+  const uint8_t *const *weights;
+  const size_t *row_counts;
+  float *const *outputs;
+  const float *input;
+  size_t input_size, column_count;
+  size_t shard[4][2]; /* [weight][begin,end) */
+} shard_job;
+
+static void *shard_worker(void *arg) {
+  shard_job *job = (shard_job *)arg;
+  q8k_buf q;
+  if (!q8k_alloc(&q, job->input_size)) {
+    q8k_free(&q);
+    return NULL;
+  }
+  size_t nb = job->input_size / QK_K;
+  for (size_t col = 0; col < job->column_count; col++) {
+    hpo_quantize_q8_k(job->input + col * job->input_size, job->input_size, q.qs, q.d, q.bsums);
+    for (size_t i = 0; i < job->count; i++) {
+      size_t row_bytes = hpo_row_bytes(job->type_ids[i], job->input_size);
+      dot_rows(job->type_ids[i], job->weights[i], row_bytes, nb, &q, job->shard[i][0],
+               job->shard[i][1], job->outputs[i] + col * job->row_counts[i]);
+    }
+  }
+  q8k_free(&q);
+  return NULL;
+}
+
+static void split_rows(size_t rows, size_t shards, size_t index, size_t *begin, size_t *end) {
+  size_t base = rows / shards, extra = rows % shards;
+  size_t start = index * base + (index < extra ? index : extra);
+  *begin = start;
+  *end = start + base + (index < extra ? 1 : 0);
+}
+
+int32_t hpo_matmul_quantized_multi_threaded(size_t count, const float *input, size_t input_len,
+                                            size_t input_size, size_t column_count,
+                                            const int32_t *type_ids, const uint8_t *const *weights,
+                                            const size_t *weight_lens, const size_t *row_counts,
+                                            float *const *outputs, const size_t *output_lens,
+                                            int threads) {
+  if (count == 0 || count > 4 || input_len != sat_mul(input_size, column_count)) return HPO_ERR_SHAPE;
+  for (size_t i = 0; i < count; i++) {
+    size_t row_bytes = hpo_row_bytes(type_ids[i], input_size);
+    if (row_bytes == 0) return HPO_ERR_TYPE;
+    if (weight_lens[i] != sat_mul(row_bytes, row_counts[i]) ||
+        output_lens[i] != sat_mul(row_counts[i], column_count))
+      return HPO_ERR_SHAPE;
+  }
+  if (threads < 1) threads = 1;
+  if (threads > 256) threads = 256;
+  shard_job *jobs = (shard_job *)calloc((size_t)threads, sizeof(shard_job));
+  pthread_t *tids = (pthread_t *)calloc((size_t)threads, sizeof(pthread_t));
+  if (!jobs || !tids) {
+    free(jobs);
+    free(tids);
+    return HPO_ERR_SHAPE;
+  }
+  for (int t = 0; t < threads; t++) {
+    shard_job *job = &jobs[t];
+    job->count = count;
+    job->type_ids = type_ids;
+    job->weights = weights;
+    job->row_counts = row_counts;
+    job->outputs = outputs;
+    job->input = input;
+    job->input_size = input_size;
+    job->column_count = column_count;
+    for (size_t i = 0; i < count; i++)
+      split_rows(row_counts[i], (size_t)threads, (size_t)t, &job->shard[i][0], &job->shard[i][1]);
+  }
+  for (int t = 1; t < threads; t++) pthread_create(&tids[t], NULL, shard_worker, &jobs[t]);
+  shard_worker(&jobs[0]);
+  for (int t = 1; t < threads; t++) pthread_join(tids[t], NULL);
+  free(jobs);
+  free(tids);
+  return HPO_OK;
+}
+
+int32_t hpo_matmul_quantized_threaded(int32_t type_id, const uint8_t *weight, size_t weight_len,
+                                      const float *input, size_t input_len, size_t input_size,
+                                      size_t row_count, size_t column_count, float *output,
+                                      size_t output_len, int threads) {
+  if (input_len != sat_mul(input_size, column_count) || output_len != sat_mul(row_count, column_count))
+    return HPO_ERR_SHAPE;
+  if (hpo_row_bytes(type_id, input_size) == 0) return HPO_ERR_TYPE;
+  return hpo_matmul_quantized_multi_threaded(1, input, input_len, input_size, column_count, &type_id,
+                                             &weight, &weight_len, &row_count, &output, &output_len,
+                                             threads);
+}
+
+/* ---------------------------------------------------------------------- */
+/* layers.ts:1062-1076 gelu.  JS numbers are f64: every Math.fround is a
+ * cast to float, every other operation is an f64 operation.  Math.tanh is
+ * the host libm tanh here (V8 uses an fdlibm port; both are within 1 ulp). */
+float hpo_gelu(float vf) {
+  double value = vf;
+  if (value <= -10.0) return 0.0f;
+  if (value >= 10.0) return vf;
+  double x = hpo_f16_to_f64_ts(hpo_f64_to_f16_ts(value));
+  double c = sqrt(2.0 / M_PI);
+  double t1 = (float)(c * x);
+  double x2 = (float)(x * x);
+  double t2 = (float)(0.044715 * x2);
+  double t3 = (float)(1.0 + t2);
+  double inner = (float)(t1 * t3);
+  double half = (float)(0.5 * x);
+  double t4 = (float)(1.0 + tanh(inner));
+  double activated = (float)(half * t4);
+  return (float)hpo_f16_to_f64_ts(hpo_f64_to_f16_ts(activated));
+}
+
+/* layers.ts:450-456: output[i] = Math.fround(gelu(gate[i]) * up[i]). */
+void hpo_geglu(const float *gate, const float *up, size_t n, float *out) {
+  for (size_t i = 0; i < n; i++) out[i] = (float)((double)hpo_gelu(gate[i]) * (double)up[i]);
+}
+
+/* layers.ts:407-412 softcap: Math.fround(Math.tanh(v / c) * c). */
+float hpo_softcap(float v, double cap) { return (float)(tanh((double)v / cap) * cap); }
+
+/* runtime.ts:514-527 topK: a candidate enters while fewer than k are kept
+ * or when it is strictly greater than the current k-th value; the stable
+ * descending sort keeps equal values in id order, so ties go to the lower
+ * id (-0 and +0 tie).  NaN (never greater) is placed last when it enters. */
+size_t hpo_topk(const float *values, size_t n, size_t k, uint32_t *ids, float *out_values) {
+  size_t len = 0;
+  if (k == 0) return 0;
+  for (size_t id = 0; id < n; id++) {
+    float v = values[id];
+    if (len < k || v > out_values[len - 1]) {
+      size_t pos = len;
+      if (v == v) {
+        pos = 0;
+        while (pos < len && out_values[pos] == out_values[pos] && out_values[pos] >= v) pos++;
+      }
+      size_t last = len < k ? len : k - 1;
+      for (size_t i = last; i > pos; i--) {
+        ids[i] = ids[i - 1];
+        out_values[i] = out_values[i - 1];
+      }
+      if (pos < k) {
+        ids[pos] = (uint32_t)id;
+        out_values[pos] = v;
+      }
+      if (len < k) len++;
+    }
+  }
+  return len;
+}

@@ -1,0 +1,121 @@
+"""GPU parity: Q4_K/Q6_K dequantisation and Q8_K matvec vs the oracle.
+
+Bar: bit-exact (the runner replays the reference's integer sums and its f32
+tail order, lib.rs:2116-2172 / 1923-1968), compared as raw f32 bit patterns.
+"""
+import numpy as np
+import pytest
+
+from heliopause_amd import synthetic as S
+
+pytestmark = pytest.mark.gpu
+
+TYPES = {"Q4_K": 1, "Q6_K": 3}
+
+
+def _bits(a):
+    return np.ascontiguousarray(a, dtype=np.float32).view(np.uint32)
+
+
+def _weights(type_name, seed, rows, k):
+    return S.weight_blocks(type_name, seed, rows, k)
+
+
+@pytest.mark.parametrize("type_name", ["Q4_K", "Q6_K"])
+@pytest.mark.parametrize("rows,k", [(1, 256), (7, 2560), (100, 512), (13, 10240), (64, 2048)])
+def test_dequantize_bit_exact(hip, oracle, type_name, rows, k):
+    print(f"dequant {type_name} rows={rows} k={k}", flush=True)
+    w = _weights(type_name, S.derive(S.BASE_SEED, "deq", rows, k), rows, k)
+    h = hip.createHipQuantizedWeightHandle(type_name, w, k, rows)
+    try:
+        got = hip.dequantizeHipResident(h, 0, rows)
+        ref = np.stack([oracle.dequantize(TYPES[type_name], w[r], k) for r in range(rows)])
+        assert np.array_equal(_bits(got), _bits(ref))
+        if rows > 3:
+            part = hip.dequantizeHipResident(h, 2, rows - 3)
+            assert np.array_equal(_bits(part), _bits(ref[2:rows - 1]))
+    finally:
+        hip.releaseHipQuantizedWeightHandle(h)
+
+
+@pytest.mark.parametrize("type_name", ["Q4_K", "Q6_K"])
+@pytest.mark.parametrize("rows,k,m", [(1, 256, 1), (7, 2560, 1), (61, 2560, 3), (100, 512, 8), (13, 10240, 2),
+                                      (64, 2048, 4), (5, 768, 11), (130, 2560, 5), (3, 4096, 1)])
+def test_matmul_bit_exact(hip, oracle, type_name, rows, k, m):
+    print(f"matmul {type_name} rows={rows} k={k} m={m}", flush=True)
+    seed = S.derive(S.BASE_SEED, "mm", type_name, rows, k, m)
+    w = _weights(type_name, seed, rows, k)
+    x = S.activations(seed, m, k)
+    h = hip.createHipQuantizedWeightHandle(type_name, w, k, rows)
+    try:
+        got = hip.matMulQuantizedHipResident(h, x, k, rows, m).reshape(m, rows)
+        ref = oracle.matmul(TYPES[type_name], w, x, rows)
+        assert np.array_equal(_bits(got), _bits(ref)), np.abs(got - ref).max()
+    finally:
+        hip.releaseHipQuantizedWeightHandle(h)
+
+
+def test_multi_mixed_types_bit_exact(hip, oracle):
+    """Q (Q4_K) + K (Q4_K) + V (Q6_K) in one launch sharing one Q8_K (lib.rs:300-426)."""
+    k = 2560
+    specs = [("Q4_K", 96), ("Q4_K", 40), ("Q6_K", 40)]
+    for m in (1, 4):
+        print(f"multi m={m}", flush=True)
+        seed = S.derive(S.BASE_SEED, "multi", m)
+        ws = [_weights(t, S.derive(seed, i), r, k) for i, (t, r) in enumerate(specs)]
+        x = S.activations(seed, m, k)
+        hs = [hip.createHipQuantizedWeightHandle(t, w, k, r) for (t, r), w in zip(specs, ws)]
+        try:
+            outs = hip.matMulQuantizedHipResidentMulti(hs, x, k, m)
+            refs = oracle.matmul_multi([TYPES[t] for t, _ in specs], ws, x, [r for _, r in specs])
+            for got, ref, (t, r) in zip(outs, refs, specs):
+                assert np.array_equal(_bits(got.reshape(m, r)), _bits(ref)), t
+            singles = [hip.matMulQuantizedHipResident(h, x, k, r, m) for h, (t, r) in zip(hs, specs)]
+            for got, single in zip(outs, singles):
+                assert np.array_equal(_bits(got), _bits(single))
+        finally:
+            for h in hs:
+                hip.releaseHipQuantizedWeightHandle(h)
+
+
+def test_special_inputs(hip, oracle):
+    """All-zero columns, first-index |x| ties, a huge spike and denormal-scale inputs."""
+    k, rows = 2560, 37
+    for type_name in ("Q4_K", "Q6_K"):
+        w = _weights(type_name, S.derive(S.BASE_SEED, "special", type_name), rows, k)
+        x = np.zeros((5, k), dtype=np.float32)
+        x[1, 5], x[1, 9] = 2.0, -2.0
+        x[1, 300], x[1, 301] = -3.5, 3.5
+        x[2] = S.activations(7, 1, k)[0]
+        x[2, 1000] = 1e30
+        x[3] = S.activations(8, 1, k)[0] * 1e-39
+        x[4, ::7] = 2.5
+        h = hip.createHipQuantizedWeightHandle(type_name, w, k, rows)
+        try:
+            got = hip.matMulQuantizedHipResident(h, x, k, rows, 5).reshape(5, rows)
+            ref = oracle.matmul(TYPES[type_name], w, x, rows)
+            assert np.array_equal(_bits(got), _bits(ref)), type_name
+        finally:
+            hip.releaseHipQuantizedWeightHandle(h)
+
+
+def test_shape_errors(hip):
+    k, rows = 512, 8
+    w = _weights("Q4_K", 1, rows, k)
+    assert hip.createHipQuantizedWeightHandle("Q5_K", w, k, rows) is None
+    with pytest.raises(TypeError):
+        hip.createHipQuantizedWeightHandle("Q4_K", w[:, :144], 300, rows)
+    with pytest.raises(ValueError):
+        hip.createHipQuantizedWeightHandle("Q4_K", w.reshape(-1)[:-1], k, rows)
+    h = hip.createHipQuantizedWeightHandle("Q4_K", w, k, rows)
+    try:
+        with pytest.raises(ValueError):
+            hip.matMulQuantizedHipResident(h, np.zeros(k + 1, np.float32), k, rows, 1)
+        with pytest.raises(ValueError):
+            hip.matMulQuantizedHipResident(h, np.zeros(k, np.float32), k, rows + 1, 1)
+        assert hip.matMulQuantizedHipResident(h, np.zeros(0, np.float32), k, rows, 0).size == 0
+        assert hip.matMulQuantizedHipResidentMulti([h], np.zeros(k, np.float32), k, 1) is None
+    finally:
+        hip.releaseHipQuantizedWeightHandle(h)
+    code = hip.lib().hp_hip_weight_release(h.handle)
+    assert code == hip.HP_ERR_HANDLE
