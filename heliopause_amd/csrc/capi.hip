@@ -42,9 +42,6 @@ struct State {
   size_t max_lds = 0;
   hipStream_t stream = nullptr;
   std::vector<Handle> handles;
-  uint8_t *q8 = nullptr;
-  float *q8d = nullptr;
-  size_t q8_cap_blocks = 0;
   float *io_in = nullptr, *io_out[kMaxWeights] = {nullptr, nullptr, nullptr, nullptr};
   size_t io_in_cap = 0, io_out_cap[kMaxWeights] = {0, 0, 0, 0};
   uint64_t matmul_calls = 0, launches = 0;
@@ -133,24 +130,6 @@ int32_t grow(void **p, size_t *cap, size_t bytes) {
   return HP_OK;
 }
 
-int32_t ensure_q8(size_t cols, size_t nb) {
-  State &s = st();
-  const size_t blocks = cols * nb;
-  if (s.q8_cap_blocks >= blocks && s.q8) return HP_OK;
-  if (s.q8) {
-    HP_HIP_TRY(hipStreamSynchronize(s.stream));
-    HP_HIP_TRY(hipFree(s.q8));
-    HP_HIP_TRY(hipFree(s.q8d));
-    s.q8 = nullptr;
-    s.q8d = nullptr;
-    s.q8_cap_blocks = 0;
-  }
-  if (hipMalloc((void **)&s.q8, blocks * kQ8BlockBytes) != hipSuccess) return fail(HP_ERR_OOM, "q8 scratch");
-  if (hipMalloc((void **)&s.q8d, blocks * sizeof(float)) != hipSuccess) return fail(HP_ERR_OOM, "q8 scratch");
-  s.q8_cap_blocks = blocks;
-  return HP_OK;
-}
-
 hipEvent_t take_event() {
   State &s = st();
   if (!s.event_pool.empty()) {
@@ -201,30 +180,22 @@ void prof_collect() {
 int cols_per_launch(const TileGeom &g, size_t max_lds) {
   for (int c = kMaxCols; c >= 1; c--) {
     size_t x = (size_t)c * g.nb * kQ8BlockBytes + (size_t)((c * g.nb + 3) & ~3) * 4;
-    size_t per_wave = (size_t)(g.R * 9 * g.S + c * g.R * 9) * 4;
-    if (x + 4 * per_wave <= max_lds) return c;
+    if (x <= max_lds) return c;
   }
   return 0;
 }
 
-// Core sequence: Q8_K quantise every column once, then one matvec launch per
-// column chunk covering every weight (multi == one launch, lib.rs:300-426).
+// One matvec launch per column chunk covering every weight (multi == one
+// launch, lib.rs:300-426); each launch quantises its columns in its prologue.
 int32_t run_matvec(size_t count, Handle *const *hs, const float *d_input, size_t input_size, size_t cols,
                    float *const *d_outs, hipStream_t stream) {
   State &s = st();
   if (cols == 0) return HP_OK;
   const TileGeom g = hs[0]->g;
-  const size_t nb = input_size / kQK;
-  int32_t rc = ensure_q8(cols, nb);
-  if (rc != HP_OK) return rc;
-  hipEvent_t e0 = prof_begin(stream);
-  HP_HIP_TRY(launch_q8k_quantize(d_input, (int)input_size, (int)cols, s.q8, s.q8d, stream));
-  prof_end(HP_KERNEL_Q8K, e0, stream);
-  s.launches++;
-
   MatvecArgs a{};
   a.count = (int)count;
   a.g = g;
+  a.k = (int)input_size;
   int tiles = 0;
   for (size_t i = 0; i < count; i++) {
     a.w[i].data = hs[i]->data;
@@ -241,8 +212,7 @@ int32_t run_matvec(size_t count, Handle *const *hs, const float *d_input, size_t
   if (chunk <= 0) return fail(HP_ERR_SHAPE, "input_size too large for the matvec LDS budget");
   for (size_t m0 = 0; m0 < cols; m0 += (size_t)chunk) {
     const int c = (int)((cols - m0) < (size_t)chunk ? (cols - m0) : (size_t)chunk);
-    a.q8 = s.q8 + m0 * nb * kQ8BlockBytes;
-    a.q8d = s.q8d + m0 * nb;
+    a.x = d_input + m0 * input_size;
     a.cols = c;
     a.out_col0 = (int)m0;
     hipEvent_t e1 = prof_begin(stream);
@@ -277,6 +247,8 @@ int32_t upload_common(int32_t type_id, const void *src, bool src_device, size_t 
   if (hipMalloc((void **)&h.data, weight_len) != hipSuccess) return fail(HP_ERR_OOM, "weight allocation failed");
   if (type_id == kTypeQ6K) h.dplane = reinterpret_cast<uint16_t *>(h.data + row_count * (input_size / kQK) * 208);
 
+  if (src_device && reinterpret_cast<uintptr_t>(src) % 16 != 0)
+    return fail(HP_ERR_ARG, "device weight buffer must be 16-byte aligned");
   const uint8_t *raw = static_cast<const uint8_t *>(src);
   uint8_t *staging = nullptr;
   if (!src_device) {
@@ -360,11 +332,6 @@ int32_t hp_hip_shutdown(void) {
       (void)hipFree(h.data);
       h.live = false;
     }
-  if (s.q8) (void)hipFree(s.q8);
-  if (s.q8d) (void)hipFree(s.q8d);
-  s.q8 = nullptr;
-  s.q8d = nullptr;
-  s.q8_cap_blocks = 0;
   if (s.io_in) (void)hipFree(s.io_in);
   s.io_in = nullptr;
   s.io_in_cap = 0;
@@ -438,6 +405,7 @@ int32_t hp_hip_matmul_multi_device(size_t count, const uint64_t *handles, const 
       return fail(HP_ERR_SHAPE, "output length mismatch");
     if (column_count && !d_outputs[i]) return fail(HP_ERR_ARG, "null output");
   }
+  if (reinterpret_cast<uintptr_t>(d_input) % 16 != 0) return fail(HP_ERR_ARG, "input must be 16-byte aligned");
   hipStream_t strm = stream ? static_cast<hipStream_t>(stream) : s.stream;
   return run_matvec(count, hs, d_input, input_size, column_count, d_outputs, strm);
 }
@@ -515,6 +483,35 @@ int32_t hp_hip_dequantize(uint64_t handle, size_t row_start, size_t row_count, f
   return HP_OK;
 }
 
+int32_t hp_hip_quantize_q8_k(const float *input, size_t input_len, size_t input_size, size_t column_count,
+                             int8_t *qs, float *d, int16_t *bsums32) {
+  State &s = st();
+  std::lock_guard<std::recursive_mutex> lock(s.mu);
+  int32_t rc = ensure_init(s.ready ? s.device : 0);
+  if (rc != HP_OK) return rc;
+  if (input_size == 0 || input_size % kQK != 0) return fail(HP_ERR_TYPE, "input_size is not a multiple of 256");
+  if (input_len != sat_mul(input_size, column_count)) return fail(HP_ERR_SHAPE, "q8_k input length mismatch");
+  if (column_count == 0) return HP_OK;
+  if (!input || !qs || !d || !bsums32) return fail(HP_ERR_ARG, "null pointer");
+  const size_t nb = input_size / kQK;
+  uint8_t *buf = nullptr;
+  const size_t bytes = input_len * 4 + input_len + column_count * nb * 4 + input_len / 32 * 2;
+  if (hipMalloc((void **)&buf, bytes) != hipSuccess) return fail(HP_ERR_OOM, "q8_k buffer");
+  float *dx = reinterpret_cast<float *>(buf);
+  int8_t *dq = reinterpret_cast<int8_t *>(buf + input_len * 4);
+  float *dd = reinterpret_cast<float *>(buf + input_len * 5);
+  int16_t *db = reinterpret_cast<int16_t *>(buf + input_len * 5 + column_count * nb * 4);
+  hipError_t e = hipMemcpyAsync(dx, input, input_len * 4, hipMemcpyHostToDevice, s.stream);
+  if (e == hipSuccess) e = launch_q8k_natural(dx, (int)input_size, (int)column_count, dq, dd, db, s.stream);
+  if (e == hipSuccess) e = hipMemcpyAsync(qs, dq, input_len, hipMemcpyDeviceToHost, s.stream);
+  if (e == hipSuccess) e = hipMemcpyAsync(d, dd, column_count * nb * 4, hipMemcpyDeviceToHost, s.stream);
+  if (e == hipSuccess) e = hipMemcpyAsync(bsums32, db, input_len / 32 * 2, hipMemcpyDeviceToHost, s.stream);
+  if (e == hipSuccess) e = hipStreamSynchronize(s.stream);
+  (void)hipFree(buf);
+  if (e != hipSuccess) return hip_fail(e, "quantize_q8_k");
+  return HP_OK;
+}
+
 int32_t hp_hip_stats(hp_hip_stats_t *out) {
   State &s = st();
   std::lock_guard<std::recursive_mutex> lock(s.mu);
@@ -525,7 +522,7 @@ int32_t hp_hip_stats(hp_hip_stats_t *out) {
       r.handle_count++;
       r.resident_bytes += h.byte_length;
     }
-  r.scratch_bytes = s.q8_cap_blocks * (kQ8BlockBytes + sizeof(float)) + s.io_in_cap;
+  r.scratch_bytes = s.io_in_cap;
   for (int i = 0; i < kMaxWeights; i++) r.scratch_bytes += s.io_out_cap[i];
   r.matmul_calls = s.matmul_calls;
   r.kernel_launches = s.launches;

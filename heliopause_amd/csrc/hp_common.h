@@ -22,10 +22,11 @@
 //   q - 32); chunk 12 = the 16 int8 scales.  The f16 d of every row-block
 //   sits in a plane after all tiles, in tile order.
 //
-// Q8_K activation layout (per column m, per block b, 272 bytes): 64 dwords
-// X[j][l] (j = 0..7, l = 0..7, dword 8j+l) with byte c = q8[32j + 8c + l],
-// then the 8 int16 sums of 32 (bsums32).  The f32 d of each block is kept
-// in a separate [M][nb] array.
+// Q8_K activation layout in LDS (per column m, per block b, 272 bytes): 64
+// dwords X[j][l] (j = 0..7, l = 0..7, dword 8j+l) with byte c =
+// q8[32j + 8c + l], then the 8 int16 sums of 32 (bsums32).  The f32 d of
+// each block is kept in a separate [M][nb] array.  Every matvec workgroup
+// quantises the f32 input into this layout itself (its prologue).
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -69,14 +70,15 @@ struct MatvecArgs {
   int count;
   int total_tiles;
   TileGeom g;
-  const uint8_t *q8;  // [cols][nb][272]
-  const float *q8d;   // [cols][nb]
+  const float *x;     // f32 activations of this launch's first column, [cols][k]
+  int k;              // input size (nb * 256)
   int cols;           // columns in this launch (<= kMaxCols)
   int out_col0;       // first output column written by this launch
 };
 
 // Launchers (return hipError_t of the launch).
-hipError_t launch_q8k_quantize(const float *x, int k, int cols, uint8_t *q8, float *q8d, hipStream_t s);
+hipError_t launch_q8k_natural(const float *x, int k, int cols, int8_t *qs, float *d, int16_t *bsums,
+                              hipStream_t s);
 hipError_t launch_matvec(const MatvecArgs &a, int num_cus, hipStream_t s);
 hipError_t launch_repack(int type, const uint8_t *raw, int rows, const TileGeom &g, uint8_t *tiles,
                          uint16_t *dplane, hipStream_t s);

@@ -14,11 +14,17 @@
 //
 // Work split: a wave owns one tile (R rows x S block slots per iteration,
 // layout in hp_common.h).  Every lane computes the exact integers of one
-// (row, block) with v_dot4_i32_i8 on four elements that share lane l, then
-// forms the f32 products d*f32(aux32[l]).  The order-dependent additions
-// run in LDS: lane (row, chain) adds the S products of its chain in block
-// order.  The activation (Q8_K) is staged once per workgroup in LDS.
+// (row, block) with v_dot4_i32_i8 on four elements that share lane l.  The
+// scale sum sum_j sc_j * dot_j is formed by Abel summation: one running
+// dot T_j = dot_0 + .. + dot_j per lane l and aux += T_j * (sc_j - sc_{j+1}),
+// so each (j, l) costs one dot4 and one 24-bit multiply-add.  The lane then
+// forms the f32 products d*f32(aux32[l]); the order-dependent additions run
+// across the S lanes of a row with DPP wave_shr:1: at step k lane k adds its
+// product to lane k-1's running value, which is the reference's sequential
+// block order.  Each workgroup first quantises the f32 input to Q8_K into
+// LDS (16 lanes per 256-element block), so a projection is one launch.
 #include "hp_common.h"
+#include "hp_q8k.h"
 
 namespace hp {
 
@@ -26,29 +32,83 @@ __device__ __forceinline__ float h2f(uint32_t bits16) {
   return (float)__builtin_bit_cast(_Float16, (uint16_t)bits16);
 }
 
-__device__ __forceinline__ int dot4(uint32_t a, uint32_t b) {
-  return __builtin_amdgcn_sdot4((int)a, (int)b, 0, false);
+// a * b + c with 24-bit multiplicands; here |T| < 2^23 and |sc_j - sc_j+1|
+// < 2^8, so the product is exact.  Left to the compiler (no inline asm): its
+// hazard recognizer must see the v_dot4c result being read.
+__device__ __forceinline__ int mad24(int a, int b, int c) { return __mul24(a, b) + c; }
+
+template <int CTRL>
+__device__ __forceinline__ float dppf(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xf, 0xf, false));
 }
 
-__device__ __forceinline__ void wave_lds_sync() {
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-  __builtin_amdgcn_wave_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+template <int CTRL>
+__device__ __forceinline__ int dppi(int v) {
+  return __builtin_amdgcn_update_dpp(0, v, CTRL, 0xf, 0xf, false);
 }
+
+constexpr int kDppQuadXor1 = 0xB1;   // quad_perm [1,0,3,2]
+constexpr int kDppQuadXor2 = 0x4E;   // quad_perm [2,3,0,1]
+constexpr int kDppHalfMirror = 0x141;  // row_half_mirror
+constexpr int kDppMirror = 0x140;      // row_mirror
+constexpr int kDppWaveShr1 = 0x138;    // wave_shr:1
 
 __device__ __forceinline__ uint32_t u4get(const uint4 &v, int i) {
   return i == 0 ? v.x : i == 1 ? v.y : i == 2 ? v.z : v.w;
 }
 
-// Integer part of one Q4_K row-block for M columns.
-template <int M>
-__device__ __forceinline__ void q4k_ints(const uint4 *__restrict__ ch, int stride, const uint8_t *xq,
-                                         int nb, int b, int (&aux)[M][8], int (&sumi)[M], uint32_t &dbits) {
-  const uint4 c0 = ch[0];
-  uint4 cw[8];
+// Raw 16-byte chunks of one (row, block) lane: Q4_K uses c[0..8], Q6_K
+// c[0..12] plus its f16 d from the side plane.
+struct Regs {
+  uint4 c[13];
+  uint32_t d6;
+};
+
+// Wave-uniform context of one tile.
+struct TileCtx {
+  const uint8_t *tile;
+  const uint16_t *dpl;
+  float *out;
+  int rows, row0, Rt, lanes, CH;
+  bool q4;
+};
+
+__device__ __forceinline__ TileCtx make_ctx(const MatvecArgs &a, int t, int nb, int R, int S) {
+  WeightDesc W = a.w[0];
+  if (a.count > 1 && t >= a.w[1].tile_begin) W = a.w[1];
+  if (a.count > 2 && t >= a.w[2].tile_begin) W = a.w[2];
+  if (a.count > 3 && t >= a.w[3].tile_begin) W = a.w[3];
+  TileCtx cx;
+  cx.q4 = W.type == kTypeQ4K;
+  cx.CH = cx.q4 ? 9 : 13;
+  cx.rows = W.rows;
+  cx.row0 = (t - W.tile_begin) * R;
+  cx.Rt = min(R, W.rows - cx.row0);
+  cx.lanes = cx.Rt * S;
+  cx.tile = W.data + (size_t)cx.row0 * nb * cx.CH * 16;
+  cx.dpl = W.dplane;
+  cx.out = W.out;
+  return cx;
+}
+
+__device__ __forceinline__ void load_regs(Regs &rg, const TileCtx &cx, int it, int lane, int nb) {
+  if (lane < cx.lanes) {
+    const uint4 *ch = reinterpret_cast<const uint4 *>(cx.tile + ((size_t)it * cx.CH * cx.lanes + lane) * 16);
 #pragma unroll
-  for (int c = 0; c < 8; c++) cw[c] = ch[(1 + c) * stride];
-  dbits = c0.x;
+    for (int c = 0; c < 9; c++) rg.c[c] = ch[(size_t)c * cx.lanes];
+    if (!cx.q4) {
+#pragma unroll
+      for (int c = 9; c < 13; c++) rg.c[c] = ch[(size_t)c * cx.lanes];
+      rg.d6 = cx.dpl[(size_t)cx.row0 * nb + (size_t)it * cx.lanes + lane];
+    }
+  }
+}
+
+// Integer part of one Q4_K row-block for M columns (exact aux32, sumi).
+template <int M>
+__device__ __forceinline__ void q4k_ints(const Regs &rg, const uint8_t *xq, int nb, int b, int (&aux)[M][8],
+                                         int (&sumi)[M]) {
+  const uint4 c0 = rg.c[0];
   const uint32_t s0 = c0.y, s1 = c0.z, s2 = c0.w;
   int sc[8], mn[8];
 #pragma unroll
@@ -58,10 +118,17 @@ __device__ __forceinline__ void q4k_ints(const uint4 *__restrict__ ch, int strid
     sc[j + 4] = ((s2 >> (8 * j)) & 15) | (((s0 >> (8 * j + 6)) & 3) << 4);
     mn[j + 4] = ((s2 >> (8 * j + 4)) & 15) | (((s1 >> (8 * j + 6)) & 3) << 4);
   }
+  int dsc[8];  // Abel weights: sum_j sc_j d_j = sum_j T_j (sc_j - sc_{j+1})
+#pragma unroll
+  for (int j = 0; j < 8; j++) dsc[j] = j < 7 ? sc[j] - sc[j + 1] : sc[7];
+  int T[M][8];
 #pragma unroll
   for (int m = 0; m < M; m++) {
 #pragma unroll
-    for (int l = 0; l < 8; l++) aux[m][l] = 0;
+    for (int l = 0; l < 8; l++) {
+      aux[m][l] = 0;
+      T[m][l] = 0;
+    }
     const uint4 bs = *reinterpret_cast<const uint4 *>(xq + ((size_t)m * nb + b) * kQ8BlockBytes + 256);
     int si = 0;
 #pragma unroll
@@ -72,53 +139,57 @@ __device__ __forceinline__ void q4k_ints(const uint4 *__restrict__ ch, int strid
     sumi[m] = si;
   }
 #pragma unroll
-  for (int p = 0; p < 4; p++) {
+  for (int j = 0; j < 8; j++) {
+    const int p = j >> 1;
 #pragma unroll
     for (int lq = 0; lq < 2; lq++) {
-      const uint4 D = cw[2 * p + lq];
+      const uint4 D = rg.c[1 + 2 * p + lq];
+      uint32_t w[4];
+#pragma unroll
+      for (int li = 0; li < 4; li++) {
+        const uint32_t d = u4get(D, li);
+        w[li] = (j & 1) ? ((d >> 4) & 0x0F0F0F0Fu) : (d & 0x0F0F0F0Fu);
+      }
 #pragma unroll
       for (int m = 0; m < M; m++) {
-        const uint4 *xb = reinterpret_cast<const uint4 *>(xq + ((size_t)m * nb + b) * kQ8BlockBytes);
-        const uint4 xlo = xb[4 * p + lq];      // X[2p][4lq..4lq+3]
-        const uint4 xhi = xb[4 * p + 2 + lq];  // X[2p+1][4lq..4lq+3]
+        const uint4 xv = reinterpret_cast<const uint4 *>(xq + ((size_t)m * nb + b) * kQ8BlockBytes)[2 * j + lq];
 #pragma unroll
         for (int li = 0; li < 4; li++) {
-          const uint32_t d = u4get(D, li);
-          const uint32_t lo = d & 0x0F0F0F0Fu;
-          const uint32_t hi = (d >> 4) & 0x0F0F0F0Fu;
-          int a = aux[m][4 * lq + li];
-          a += __mul24(sc[2 * p], dot4(lo, u4get(xlo, li)));
-          a += __mul24(sc[2 * p + 1], dot4(hi, u4get(xhi, li)));
-          aux[m][4 * lq + li] = a;
+          const int l = 4 * lq + li;
+          T[m][l] = __builtin_amdgcn_sdot4((int)w[li], (int)u4get(xv, li), T[m][l], false);
+          aux[m][l] = mad24(T[m][l], dsc[j], aux[m][l]);
         }
       }
     }
   }
 }
 
-// Integer part of one Q6_K row-block for M columns (aux32 exact).
+// Integer part of one Q6_K row-block for M columns (exact aux32).  Bytes of
+// the unpacked weight carry 4 * (q6 - 32); each dword covers groups 2j (c =
+// 0,1) and 2j+1 (c = 2,3), split by masking.
 template <int M>
-__device__ __forceinline__ void q6k_ints(const uint4 *__restrict__ ch, int stride, const uint8_t *xq, int nb,
-                                         int b, int (&aux)[M][8]) {
-  uint4 cq[8], ch4[4];
-#pragma unroll
-  for (int c = 0; c < 8; c++) cq[c] = ch[c * stride];
-#pragma unroll
-  for (int c = 0; c < 4; c++) ch4[c] = ch[(8 + c) * stride];
-  const uint4 csc = ch[12 * stride];
+__device__ __forceinline__ void q6k_ints(const Regs &rg, const uint8_t *xq, int nb, int b, int (&aux)[M][8]) {
+  const uint4 csc = rg.c[12];
   int sc[16];
 #pragma unroll
   for (int g = 0; g < 16; g++) sc[g] = (int)(int8_t)(u4get(csc, g >> 2) >> (8 * (g & 3)));
+  int dsc[16];
+#pragma unroll
+  for (int g = 0; g < 16; g++) dsc[g] = g < 15 ? sc[g] - sc[g + 1] : sc[15];
+  int T[M][8];
 #pragma unroll
   for (int m = 0; m < M; m++)
 #pragma unroll
-    for (int l = 0; l < 8; l++) aux[m][l] = 0;
+    for (int l = 0; l < 8; l++) {
+      aux[m][l] = 0;
+      T[m][l] = 0;
+    }
 #pragma unroll
   for (int j = 0; j < 8; j++) {
 #pragma unroll
     for (int lq = 0; lq < 2; lq++) {
-      const uint4 Dl = cq[2 * (j >> 1) + lq];
-      const uint4 Dh = ch4[2 * (j >> 2) + lq];
+      const uint4 Dl = rg.c[2 * (j >> 1) + lq];
+      const uint4 Dh = rg.c[8 + 2 * (j >> 2) + lq];
       uint32_t wlo[4], whi[4];
 #pragma unroll
       for (int li = 0; li < 4; li++) {
@@ -134,10 +205,11 @@ __device__ __forceinline__ void q6k_ints(const uint4 *__restrict__ ch, int strid
         const uint4 xv = reinterpret_cast<const uint4 *>(xq + ((size_t)m * nb + b) * kQ8BlockBytes)[2 * j + lq];
 #pragma unroll
         for (int li = 0; li < 4; li++) {
-          int a = aux[m][4 * lq + li];
-          a += __mul24(sc[2 * j], dot4(wlo[li], u4get(xv, li)));
-          a += __mul24(sc[2 * j + 1], dot4(whi[li], u4get(xv, li)));
-          aux[m][4 * lq + li] = a;
+          const int l = 4 * lq + li;
+          T[m][l] = __builtin_amdgcn_sdot4((int)wlo[li], (int)u4get(xv, li), T[m][l], false);
+          aux[m][l] = mad24(T[m][l], dsc[2 * j], aux[m][l]);
+          T[m][l] = __builtin_amdgcn_sdot4((int)whi[li], (int)u4get(xv, li), T[m][l], false);
+          aux[m][l] = mad24(T[m][l], dsc[2 * j + 1], aux[m][l]);
         }
       }
     }
@@ -148,124 +220,222 @@ __device__ __forceinline__ void q6k_ints(const uint4 *__restrict__ ch, int strid
     for (int l = 0; l < 8; l++) aux[m][l] >>= 2;  // weights carried 4 * (q6 - 32)
 }
 
-template <int M>
+// Q8_K of block (m, b) by one 16-lane DPP row (lib.rs:1774-1811).  Lane
+// i16 = 2j + u owns the 16 elements 32j + 8c + 4u + i (c, i = 0..3), i.e.
+// bytes 32j + 16u .. +15 of the transposed layout, so its quants are one
+// 16-byte LDS store; its elements are scanned in increasing index order.
+__device__ __forceinline__ void load_x16(float (&v)[16], const float *__restrict__ xb, int i16) {
+  const int j = i16 >> 1, u = i16 & 1;
+#pragma unroll
+  for (int c = 0; c < 4; c++) {
+    const float4 f = *reinterpret_cast<const float4 *>(xb + 32 * j + 8 * c + 4 * u);
+    v[4 * c] = f.x;
+    v[4 * c + 1] = f.y;
+    v[4 * c + 2] = f.z;
+    v[4 * c + 3] = f.w;
+  }
+}
+
+// One butterfly step of the (|x| desc, index asc) maximum with the partner
+// lane selected by the DPP control.
+template <int CTRL>
+__device__ __forceinline__ void lexmax_step(float &amax, float &vmax, int &idx) {
+  const float oa = dppf<CTRL>(amax);
+  const float ov = dppf<CTRL>(vmax);
+  const int oi = dppi<CTRL>(idx);
+  const bool take = oa > amax || (oa == amax && oi < idx);
+  amax = take ? oa : amax;
+  vmax = take ? ov : vmax;
+  idx = take ? oi : idx;
+}
+
+__device__ __forceinline__ void q8k_block16(const float (&v)[16], int i16, uint8_t *blk, float *dptr) {
+  const int j = i16 >> 1, u = i16 & 1;
+  float amax = 0.0f, vmax = 0.0f;
+  int idx = 0x7fffffff;
+#pragma unroll
+  for (int c = 0; c < 4; c++)
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      const float x = v[4 * c + i];
+      const float av = fabsf(x);
+      const bool gt = av > amax;  // strictly greater: the first maximum wins
+      amax = gt ? av : amax;
+      vmax = gt ? x : vmax;
+      idx = gt ? 32 * j + 8 * c + 4 * u + i : idx;
+    }
+  // (amax desc, idx asc) across the 16 lanes of the row
+  lexmax_step<kDppQuadXor1>(amax, vmax, idx);
+  lexmax_step<kDppQuadXor2>(amax, vmax, idx);
+  lexmax_step<kDppHalfMirror>(amax, vmax, idx);
+  lexmax_step<kDppMirror>(amax, vmax, idx);
+  const bool nz = amax != 0.0f;
+  const float inv = __fdiv_rn(-127.0f, vmax);
+  uint32_t word[4];
+  int sum = 0;
+#pragma unroll
+  for (int l4 = 0; l4 < 4; l4++) {
+    uint32_t wv = 0;
+#pragma unroll
+    for (int c = 0; c < 4; c++) {
+      // Rust: (is * x).round().min(127.0) as i8; min() never yields NaN, so
+      // only the low clamp of the saturating cast can act
+      const float r = fmaxf(fminf(roundf(__fmul_rn(inv, v[4 * c + l4])), 127.0f), -128.0f);
+      const int q = nz ? (int)r : 0;
+      sum += q;
+      wv |= (uint32_t)(q & 0xff) << (8 * c);
+    }
+    word[l4] = wv;  // dword l = 4u + l4 of sub-block j
+  }
+  sum += dppi<kDppQuadXor1>(sum);
+  *reinterpret_cast<uint4 *>(blk + 32 * j + 16 * u) = make_uint4(word[0], word[1], word[2], word[3]);
+  if (u == 0) reinterpret_cast<int16_t *>(blk + 256)[j] = (int16_t)sum;
+  if (i16 == 0) *dptr = nz ? __fdiv_rn(1.0f, inv) : 0.0f;
+}
+
+// lane L receives lane L-1's value (DPP wave_shr:1).
+__device__ __forceinline__ float shr1(float v) {
+  return dppf<kDppWaveShr1>(v);
+}
+
+template <int M, bool PREFETCH>
 __global__ __launch_bounds__(256) void kquant_matvec_kernel(const MatvecArgs a) {
   extern __shared__ __align__(16) uint8_t smem[];
   const TileGeom g = a.g;
   const int nb = g.nb, S = g.S, R = g.R;
   uint8_t *xq = smem;
   float *xd = reinterpret_cast<float *>(smem + (size_t)M * nb * kQ8BlockBytes);
-  const int xd_floats = (M * nb + 3) & ~3;
-  const int per_wave = R * 9 * S + M * R * 9;
 
-  // stage the Q8_K activations of this launch's columns
-  {
-    const int n16 = M * nb * kQ8BlockBytes / 16;
-    const uint4 *src = reinterpret_cast<const uint4 *>(a.q8);
-    uint4 *dst = reinterpret_cast<uint4 *>(xq);
-    for (int i = threadIdx.x; i < n16; i += blockDim.x) dst[i] = src[i];
-    for (int i = threadIdx.x; i < M * nb; i += blockDim.x) xd[i] = a.q8d[i];
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform
+  const int wpg = blockDim.x >> 6;
+  const int stride = gridDim.x * wpg;
+  const int r = lane / S;
+  const int s = lane - r * S;
+
+  // prologue inputs first (vector loads return in order), then the first
+  // weight unit, so the weights stream in while the prologue computes
+  const int grp = wave * 4 + (lane >> 4);
+  const int i16 = lane & 15;
+  const int nq = M * nb;
+  float xv[16];
+  if (grp < nq) load_x16(xv, a.x + (size_t)(grp / nb) * a.k + (size_t)(grp % nb) * kQK, i16);
+
+  int t = blockIdx.x * wpg + wave;
+  TileCtx cx{};
+  Regs cur;
+  if (t < a.total_tiles) {
+    cx = make_ctx(a, t, nb, R, S);
+    load_regs(cur, cx, 0, lane, nb);
+  }
+
+  // prologue: Q8_K of this launch's columns into LDS, 16 lanes per block
+  for (int q = grp; q < nq; q += wpg * 4) {
+    if (q != grp) load_x16(xv, a.x + (size_t)(q / nb) * a.k + (size_t)(q % nb) * kQK, i16);
+    q8k_block16(xv, i16, xq + (size_t)q * kQ8BlockBytes, xd + q);
   }
   __syncthreads();
 
-  const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
-  const int wpg = blockDim.x >> 6;
-  float *prod = xd + xd_floats + wave * per_wave;  // [R][9][S]
-  float *acc = prod + R * 9 * S;                    // [M][R][9]
-
-  for (int t = blockIdx.x * wpg + wave; t < a.total_tiles; t += gridDim.x * wpg) {
-    WeightDesc W = a.w[0];
-    if (a.count > 1 && t >= a.w[1].tile_begin) W = a.w[1];
-    if (a.count > 2 && t >= a.w[2].tile_begin) W = a.w[2];
-    if (a.count > 3 && t >= a.w[3].tile_begin) W = a.w[3];
-    const int row0 = (t - W.tile_begin) * R;
-    const int Rt = min(R, W.rows - row0);
-    const int lanes = Rt * S;
-    const bool q4 = W.type == kTypeQ4K;
-    const int CH = q4 ? 9 : 13;
-    const int NCH = q4 ? 9 : 8;
-    const uint8_t *tile = W.data + (size_t)row0 * nb * CH * 16;
-    const int r = lane / S;
-    const int s = lane - r * S;
-
+  float carry[M][9];
+  while (t < a.total_tiles) {
     for (int it = 0; it < g.iters; it++) {
+      Regs nxt;
+      if (PREFETCH) {
+        int nt = t, nit = it + 1;
+        TileCtx ncx = cx;
+        if (nit == g.iters) {
+          nt = t + stride;
+          nit = 0;
+          if (nt < a.total_tiles) ncx = make_ctx(a, nt, nb, R, S);
+        }
+        if (nt < a.total_tiles) load_regs(nxt, ncx, nit, lane, nb);
+      }
       const int b = it * S + s;
+      const bool active = lane < cx.lanes;
       int aux[M][8];
       int sumi[M];
       float dw = 0.0f, dminw = 0.0f;
-      if (lane < lanes) {
-        const uint4 *ch = reinterpret_cast<const uint4 *>(tile + ((size_t)it * CH * lanes + lane) * 16);
-        if (q4) {
-          uint32_t dbits;
-          q4k_ints<M>(ch, lanes, xq, nb, b, aux, sumi, dbits);
-          dw = h2f(dbits & 0xFFFFu);
-          dminw = h2f(dbits >> 16);
+      if (active) {
+        if (cx.q4) {
+          q4k_ints<M>(cur, xq, nb, b, aux, sumi);
+          dw = h2f(cur.c[0].x & 0xFFFFu);
+          dminw = h2f(cur.c[0].x >> 16);
         } else {
-          q6k_ints<M>(ch, lanes, xq, nb, b, aux);
-          dw = h2f(W.dplane[(size_t)row0 * nb + (size_t)it * lanes + lane]);
+          q6k_ints<M>(cur, xq, nb, b, aux);
+          dw = h2f(cur.d6);
 #pragma unroll
           for (int m = 0; m < M; m++) sumi[m] = 0;
         }
+      } else {
+#pragma unroll
+        for (int m = 0; m < M; m++) {
+          sumi[m] = 0;
+#pragma unroll
+          for (int l = 0; l < 8; l++) aux[m][l] = 0;
+        }
       }
+      const bool last = it + 1 == g.iters;
 #pragma unroll
       for (int m = 0; m < M; m++) {
-        if (lane < lanes) {
-          const float dx = xd[m * nb + b];
-          const float dd = __fmul_rn(dw, dx);
-          float *pr = prod + (r * 9) * S + s;
+        const float dx = xd[m * nb + (b < nb ? b : 0)];
+        const float dd = __fmul_rn(dw, dx);
+        float p[9];
 #pragma unroll
-          for (int l = 0; l < 8; l++) pr[l * S] = __fmul_rn(dd, (float)aux[m][l]);
-          if (q4) pr[8 * S] = __fmul_rn(__fmul_rn(dminw, dx), (float)sumi[m]);
+        for (int l = 0; l < 8; l++) p[l] = __fmul_rn(dd, (float)aux[m][l]);
+        p[8] = __fmul_rn(__fmul_rn(dminw, dx), (float)sumi[m]);
+        // step 0 (slot 0): chain start = previous iteration's value, or 0
+        float v[9];
+#pragma unroll
+        for (int c = 0; c < 8; c++) v[c] = __fadd_rn(it == 0 ? 0.0f : carry[m][c], p[c]);
+        v[8] = __fsub_rn(it == 0 ? 0.0f : carry[m][8], p[8]);
+        // steps 1..S-1: lane k adds its product to lane k-1's value
+        for (int k = 1; k < S; k++) {
+#pragma unroll
+          for (int c = 0; c < 8; c++) v[c] = __fadd_rn(shr1(v[c]), p[c]);
+          v[8] = __fsub_rn(shr1(v[8]), p[8]);
         }
-        wave_lds_sync();
-        for (int cid = lane; cid < Rt * NCH; cid += 64) {
-          const int rr = cid / NCH;
-          const int chn = cid - rr * NCH;
-          const float *pp = prod + (rr * 9 + chn) * S;
-          float *ap = acc + (m * R + rr) * 9 + chn;
-          float v = it == 0 ? 0.0f : *ap;
-          if (chn == 8) {
-            for (int q = 0; q < S; q++) v = __fsub_rn(v, pp[q]);
-          } else {
-            for (int q = 0; q < S; q++) v = __fadd_rn(v, pp[q]);
-          }
-          *ap = v;
+        if (!last) {
+          // lane (r, 0) continues from lane (r, S-1)
+          const int src = (r * S + S - 1) << 2;
+#pragma unroll
+          for (int c = 0; c < 9; c++)
+            carry[m][c] = __builtin_bit_cast(float, __builtin_amdgcn_ds_bpermute(src, __builtin_bit_cast(int, v[c])));
+        } else if (active && s == S - 1) {
+          // result = [sumf +] ((((-0 + s0) + s1) + ...) + s7)
+          float tsum = -0.0f;
+#pragma unroll
+          for (int l = 0; l < 8; l++) tsum = __fadd_rn(tsum, v[l]);
+          const float res = cx.q4 ? __fadd_rn(v[8], tsum) : tsum;
+          cx.out[(size_t)(a.out_col0 + m) * cx.rows + cx.row0 + r] = res;
         }
-        wave_lds_sync();
+      }
+      if (PREFETCH) {
+        cur = nxt;
+      } else if (!last) {
+        load_regs(cur, cx, it + 1, lane, nb);
       }
     }
-
-    // final combine: [sumf +] ((((-0 + s0) + s1) + ...) + s7)
-    for (int cid = lane; cid < M * Rt; cid += 64) {
-      const int m = cid / Rt;
-      const int rr = cid - m * Rt;
-      const float *ap = acc + (m * R + rr) * 9;
-      float tsum = -0.0f;
-#pragma unroll
-      for (int l = 0; l < 8; l++) tsum = __fadd_rn(tsum, ap[l]);
-      const float res = q4 ? __fadd_rn(ap[8], tsum) : tsum;
-      W.out[(size_t)(a.out_col0 + m) * W.rows + row0 + rr] = res;
+    t += stride;
+    if (t < a.total_tiles) {
+      cx = make_ctx(a, t, nb, R, S);
+      if (!PREFETCH) load_regs(cur, cx, 0, lane, nb);
     }
-    wave_lds_sync();
   }
 }
 
 static size_t matvec_lds_bytes(int cols, const TileGeom &g, int wpg) {
-  size_t x = (size_t)cols * g.nb * kQ8BlockBytes + (size_t)((cols * g.nb + 3) & ~3) * 4;
-  size_t per_wave = (size_t)(g.R * 9 * g.S + cols * g.R * 9) * 4;
-  return x + per_wave * wpg;
+  (void)wpg;
+  return (size_t)cols * g.nb * kQ8BlockBytes + (size_t)((cols * g.nb + 3) & ~3) * 4;
 }
 
 template <int M>
 static hipError_t launch_m(const MatvecArgs &a, int num_cus, hipStream_t s) {
-  int wpg = a.total_tiles / (2 * num_cus);
-  wpg = wpg < 1 ? 1 : wpg > 4 ? 4 : wpg;
+  const int wpg = 4;
   int grid = (a.total_tiles + wpg - 1) / wpg;
   const int cap = num_cus * 8;
   if (grid > cap) grid = cap;
   size_t lds = matvec_lds_bytes(M, a.g, wpg);
-  hipLaunchKernelGGL(kquant_matvec_kernel<M>, dim3(grid), dim3(64 * wpg), lds, s, a);
+  hipLaunchKernelGGL((kquant_matvec_kernel<M, (M <= 4)>), dim3(grid), dim3(64 * wpg), lds, s, a);
   return hipGetLastError();
 }
 

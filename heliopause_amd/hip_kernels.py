@@ -86,13 +86,16 @@ def _declare(L: ctypes.CDLL) -> None:
     L.hp_hip_matmul_multi_device.argtypes = [_sz, ctypes.POINTER(_u64), ctypes.c_void_p, _sz, _sz, _sz,
                                              ctypes.POINTER(ctypes.c_void_p), ctypes.POINTER(_sz), ctypes.c_void_p]
     L.hp_hip_dequantize.argtypes = [_u64, _sz, _sz, ctypes.c_void_p, _sz]
+    L.hp_hip_quantize_q8_k.argtypes = [ctypes.c_void_p, _sz, _sz, _sz, ctypes.c_void_p, ctypes.c_void_p,
+                                       ctypes.c_void_p]
     L.hp_hip_stats.argtypes = [ctypes.POINTER(HipStats)]
     L.hp_hip_synchronize.argtypes = []
     L.hp_hip_profile.argtypes = [i32]
     L.hp_hip_profile_read.argtypes = [i32, ctypes.POINTER(ctypes.c_double), ctypes.POINTER(_u64)]
     for name in ("hp_hip_init", "hp_hip_shutdown", "hp_hip_device_count", "hp_hip_weight_upload",
                  "hp_hip_weight_upload_device", "hp_hip_weight_release", "hp_hip_weight_info", "hp_hip_matmul",
-                 "hp_hip_matmul_multi", "hp_hip_matmul_multi_device", "hp_hip_dequantize", "hp_hip_stats",
+                 "hp_hip_matmul_multi", "hp_hip_matmul_multi_device", "hp_hip_dequantize", "hp_hip_quantize_q8_k",
+                 "hp_hip_stats",
                  "hp_hip_synchronize", "hp_hip_profile", "hp_hip_profile_read"):
         getattr(L, name).restype = i32
     _declare_optional(L)
@@ -203,6 +206,8 @@ def createHipQuantizedWeightHandle(type_name: str, weight_bytes, input_size: int
         return None
     if input_size <= 0 or row_count <= 0:
         raise ValueError(f"Resident quantized weight shape mismatch: inputSize={input_size} rowCount={row_count}")
+    if input_size % 256 != 0:  # quantizedScaleValueCount, wasm-kernels.ts:1925-1941
+        raise ValueError(f"{type_name} scale shape mismatch: {input_size}")
     if isinstance(weight_bytes, np.ndarray):
         data = np.ascontiguousarray(weight_bytes, dtype=np.uint8).reshape(-1)
     else:
@@ -286,6 +291,18 @@ def dequantizeHipResident(handle: HipQuantizedWeightHandle, row_start: int, row_
     code = lib().hp_hip_dequantize(handle.handle, row_start, row_count, out.ctypes.data, out.size)
     assertHipOk(code, "dequantize")
     return out
+
+
+def quantizeQ8KHip(input_columns, input_size: int, column_count: int):
+    """Q8_K of each column as the matvec prologue computes it: (qs, d, bsums32)."""
+    x = _f32(input_columns)
+    qs = np.empty((column_count, input_size), dtype=np.int8)
+    d = np.empty((column_count, input_size // 256), dtype=np.float32)
+    bs = np.empty((column_count, input_size // 32), dtype=np.int16)
+    code = lib().hp_hip_quantize_q8_k(x.ctypes.data, x.size, input_size, column_count, qs.ctypes.data,
+                                      d.ctypes.data, bs.ctypes.data)
+    assertHipOk(code, "quantizeQ8K")
+    return qs, d, bs
 
 
 # ---- device-pointer entry points (inputs/outputs already in HBM) -----------------

@@ -122,6 +122,14 @@ int32_t hp_hip_matmul_multi_device(size_t count, const uint64_t *handles, const 
  * hook proving the resident layout is lossless. */
 int32_t hp_hip_dequantize(uint64_t handle, size_t row_start, size_t row_count, float *output, size_t output_len);
 
+/* Q8_K activation quantisation exactly as the matvec prologue performs it
+ * (quantize_q8_k, lib.rs:1774-1811), exposed as a test hook in the
+ * reference's QuantizedQ8K layout (lib.rs:1540-1544): qs [column_count]
+ * [input_size] int8, d [column_count][input_size/256] f32, bsums32
+ * [column_count][input_size/32] int16.  Host pointers. */
+int32_t hp_hip_quantize_q8_k(const float *input, size_t input_len, size_t input_size, size_t column_count,
+                             int8_t *qs, float *d, int16_t *bsums32);
+
 /* wasmResidentWeightStats (wasm-kernels.ts:586-591) plus call counters. */
 int32_t hp_hip_stats(hp_hip_stats_t *out);
 /* Wait for all work queued on the library stream. */

@@ -103,7 +103,7 @@ def test_shape_errors(hip):
     k, rows = 512, 8
     w = _weights("Q4_K", 1, rows, k)
     assert hip.createHipQuantizedWeightHandle("Q5_K", w, k, rows) is None
-    with pytest.raises(TypeError):
+    with pytest.raises(ValueError):
         hip.createHipQuantizedWeightHandle("Q4_K", w[:, :144], 300, rows)
     with pytest.raises(ValueError):
         hip.createHipQuantizedWeightHandle("Q4_K", w.reshape(-1)[:-1], k, rows)
@@ -119,3 +119,22 @@ def test_shape_errors(hip):
         hip.releaseHipQuantizedWeightHandle(h)
     code = hip.lib().hp_hip_weight_release(h.handle)
     assert code == hip.HP_ERR_HANDLE
+
+
+@pytest.mark.parametrize("m,k", [(1, 256), (3, 2560), (2, 10240)])
+def test_q8k_bit_exact(hip, oracle, m, k):
+    """The in-kernel Q8_K quantisation (lib.rs:1774-1811) vs the oracle, all outputs."""
+    print(f"q8k m={m} k={k}", flush=True)
+    x = S.activations(S.derive(S.BASE_SEED, "q8k", m, k), m, k)
+    base = 0
+    if k >= 512:
+        x[0, :256] = 0.0                  # all-zero block
+        base = 256
+    x[0, base + 3], x[0, base + 7] = 9.0, -9.0  # |x| tie -> first index wins
+    x[-1, -1] = np.nan                    # NaN never selected as max; quantises to 127
+    x[-1, 5] = 2.5 * 127 / 127            # exercise ties away from zero at is*x = .5
+    qs, d, bs = hip.quantizeQ8KHip(x, k, m)
+    rq, rd, rb = oracle.quantize_q8_k(x)
+    assert np.array_equal(qs, rq)
+    assert np.array_equal(d.view(np.uint32), rd.view(np.uint32))
+    assert np.array_equal(bs, rb)
