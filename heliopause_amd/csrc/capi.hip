@@ -9,6 +9,7 @@
 #include "../../include/hp_hip.h"
 #include "hp_common.h"
 
+#include <cmath>
 #include <mutex>
 #include <string>
 #include <vector>
@@ -44,6 +45,8 @@ struct State {
   std::vector<Handle> handles;
   float *io_in = nullptr, *io_out[kMaxWeights] = {nullptr, nullptr, nullptr, nullptr};
   size_t io_in_cap = 0, io_out_cap[kMaxWeights] = {0, 0, 0, 0};
+  void *topk_cand = nullptr, *topk_out = nullptr;  // candidates; ids + values
+  size_t topk_cand_cap = 0, topk_out_cap = 0;
   uint64_t matmul_calls = 0, launches = 0;
   bool profiling = false;
   ProfileSlot prof[HP_KERNEL_COUNT];
@@ -286,6 +289,41 @@ int32_t upload_common(int32_t type_id, const void *src, bool src_device, size_t 
   return HP_OK;
 }
 
+// sqrt(2/pi) as Math.sqrt(2 / Math.PI) evaluates it (IEEE f64 divide and sqrt).
+double gelu_constant() { return std::sqrt(2.0 / 3.141592653589793); }
+
+int32_t topk_check(size_t rows, size_t n, size_t k) {
+  if (k == 0 || k > 64) return fail(HP_ERR_ARG, "k must be in 1..64");
+  if (n == 0 || n > 524288 || rows > 65535) return fail(HP_ERR_SHAPE, "topk supports 1..524288 values per row");
+  return HP_OK;
+}
+
+// Enqueue top-k of device logits into device ids/values (scratch owned here).
+int32_t run_topk(const float *d_logits, size_t rows, size_t n, size_t k, double cap, uint32_t *d_ids, float *d_vals,
+                 hipStream_t stream) {
+  State &s = st();
+  const size_t cb = topk_candidate_bytes((int)rows, (int)n, (int)k);
+  int32_t rc = grow(&s.topk_cand, &s.topk_cand_cap, cb);
+  if (rc != HP_OK) return rc;
+  hipEvent_t e = prof_begin(stream);
+  HP_HIP_TRY(launch_topk(d_logits, (int)rows, (int)n, (int)k, cap, static_cast<uint64_t *>(s.topk_cand), d_ids,
+                         d_vals, stream));
+  prof_end(HP_KERNEL_TOPK, e, stream);
+  s.launches += 2;
+  return HP_OK;
+}
+
+// Scratch for [rows][k] ids + values; returns device pointers.
+int32_t topk_outputs(size_t rows, size_t k, uint32_t **ids, float **vals) {
+  State &s = st();
+  const size_t bytes = rows * k * 8;
+  int32_t rc = grow(&s.topk_out, &s.topk_out_cap, bytes);
+  if (rc != HP_OK) return rc;
+  *ids = static_cast<uint32_t *>(s.topk_out);
+  *vals = reinterpret_cast<float *>(static_cast<uint8_t *>(s.topk_out) + rows * k * 4);
+  return HP_OK;
+}
+
 }  // namespace
 
 extern "C" {
@@ -340,6 +378,10 @@ int32_t hp_hip_shutdown(void) {
     s.io_out[i] = nullptr;
     s.io_out_cap[i] = 0;
   }
+  if (s.topk_cand) (void)hipFree(s.topk_cand);
+  if (s.topk_out) (void)hipFree(s.topk_out);
+  s.topk_cand = s.topk_out = nullptr;
+  s.topk_cand_cap = s.topk_out_cap = 0;
   prof_collect();
   for (hipEvent_t e : s.event_pool) (void)hipEventDestroy(e);
   s.event_pool.clear();
@@ -483,6 +525,115 @@ int32_t hp_hip_dequantize(uint64_t handle, size_t row_start, size_t row_count, f
   return HP_OK;
 }
 
+int32_t hp_hip_topk_device(const float *d_logits, size_t rows, size_t n, size_t k, double softcap,
+                           uint32_t *d_ids, float *d_values, void *stream) {
+  State &s = st();
+  std::lock_guard<std::recursive_mutex> lock(s.mu);
+  int32_t rc = ensure_init(s.ready ? s.device : 0);
+  if (rc != HP_OK) return rc;
+  rc = topk_check(rows, n, k);
+  if (rc != HP_OK) return rc;
+  if (rows == 0) return HP_OK;
+  if (!d_logits || !d_ids || !d_values) return fail(HP_ERR_ARG, "null pointer");
+  hipStream_t strm = stream ? static_cast<hipStream_t>(stream) : s.stream;
+  return run_topk(d_logits, rows, n, k, softcap, d_ids, d_values, strm);
+}
+
+int32_t hp_hip_topk(const float *logits, size_t rows, size_t n, size_t k, double softcap, uint32_t *ids,
+                    float *values, size_t out_len) {
+  State &s = st();
+  std::lock_guard<std::recursive_mutex> lock(s.mu);
+  int32_t rc = ensure_init(s.ready ? s.device : 0);
+  if (rc != HP_OK) return rc;
+  rc = topk_check(rows, n, k);
+  if (rc != HP_OK) return rc;
+  if (out_len != sat_mul(rows, k)) return fail(HP_ERR_SHAPE, "topk output length mismatch");
+  if (rows == 0) return HP_OK;
+  if (!logits || !ids || !values) return fail(HP_ERR_ARG, "null pointer");
+  rc = grow((void **)&s.io_in, &s.io_in_cap, rows * n * sizeof(float));
+  if (rc != HP_OK) return rc;
+  uint32_t *d_ids;
+  float *d_vals;
+  rc = topk_outputs(rows, k, &d_ids, &d_vals);
+  if (rc != HP_OK) return rc;
+  HP_HIP_TRY(hipMemcpyAsync(s.io_in, logits, rows * n * sizeof(float), hipMemcpyHostToDevice, s.stream));
+  rc = run_topk(s.io_in, rows, n, k, softcap, d_ids, d_vals, s.stream);
+  if (rc != HP_OK) return rc;
+  HP_HIP_TRY(hipMemcpyAsync(ids, d_ids, rows * k * 4, hipMemcpyDeviceToHost, s.stream));
+  HP_HIP_TRY(hipMemcpyAsync(values, d_vals, rows * k * 4, hipMemcpyDeviceToHost, s.stream));
+  HP_HIP_TRY(hipStreamSynchronize(s.stream));
+  return HP_OK;
+}
+
+int32_t hp_hip_matmul_topk(uint64_t handle, const float *input, size_t input_len, size_t input_size,
+                           size_t column_count, size_t k, double softcap, uint32_t *ids, float *values,
+                           size_t out_len) {
+  State &s = st();
+  std::lock_guard<std::recursive_mutex> lock(s.mu);
+  Handle *h = lookup(handle);
+  if (!h) return fail(HP_ERR_HANDLE, "unknown weight handle");
+  if (h->input_size != input_size || input_len != sat_mul(input_size, column_count))
+    return fail(HP_ERR_SHAPE, "matmul shape mismatch");
+  int32_t rc = topk_check(column_count, h->row_count, k);
+  if (rc != HP_OK) return rc;
+  if (out_len != sat_mul(column_count, k)) return fail(HP_ERR_SHAPE, "topk output length mismatch");
+  if (column_count == 0) return HP_OK;
+  if (!input || !ids || !values) return fail(HP_ERR_ARG, "null pointer");
+  rc = grow((void **)&s.io_in, &s.io_in_cap, input_len * sizeof(float));
+  if (rc != HP_OK) return rc;
+  rc = grow((void **)&s.io_out[0], &s.io_out_cap[0], column_count * h->row_count * sizeof(float));
+  if (rc != HP_OK) return rc;
+  uint32_t *d_ids;
+  float *d_vals;
+  rc = topk_outputs(column_count, k, &d_ids, &d_vals);
+  if (rc != HP_OK) return rc;
+  HP_HIP_TRY(hipMemcpyAsync(s.io_in, input, input_len * sizeof(float), hipMemcpyHostToDevice, s.stream));
+  float *logits = s.io_out[0];
+  rc = run_matvec(1, &h, s.io_in, input_size, column_count, &logits, s.stream);
+  if (rc != HP_OK) return rc;
+  rc = run_topk(logits, column_count, h->row_count, k, softcap, d_ids, d_vals, s.stream);
+  if (rc != HP_OK) return rc;
+  HP_HIP_TRY(hipMemcpyAsync(ids, d_ids, column_count * k * 4, hipMemcpyDeviceToHost, s.stream));
+  HP_HIP_TRY(hipMemcpyAsync(values, d_vals, column_count * k * 4, hipMemcpyDeviceToHost, s.stream));
+  HP_HIP_TRY(hipStreamSynchronize(s.stream));
+  return HP_OK;
+}
+
+int32_t hp_hip_geglu_device(const float *d_gate, const float *d_up, size_t n, float *d_output, void *stream) {
+  State &s = st();
+  std::lock_guard<std::recursive_mutex> lock(s.mu);
+  int32_t rc = ensure_init(s.ready ? s.device : 0);
+  if (rc != HP_OK) return rc;
+  if (n == 0) return HP_OK;
+  if (!d_gate || !d_up || !d_output) return fail(HP_ERR_ARG, "null pointer");
+  hipStream_t strm = stream ? static_cast<hipStream_t>(stream) : s.stream;
+  hipEvent_t e = prof_begin(strm);
+  HP_HIP_TRY(launch_geglu(d_gate, d_up, n, gelu_constant(), d_output, s.num_cus, strm));
+  prof_end(HP_KERNEL_GEGLU, e, strm);
+  s.launches++;
+  return HP_OK;
+}
+
+int32_t hp_hip_geglu(const float *gate, const float *up, size_t n, float *output) {
+  State &s = st();
+  std::lock_guard<std::recursive_mutex> lock(s.mu);
+  int32_t rc = ensure_init(s.ready ? s.device : 0);
+  if (rc != HP_OK) return rc;
+  if (n == 0) return HP_OK;
+  if (!gate || !up || !output) return fail(HP_ERR_ARG, "null pointer");
+  rc = grow((void **)&s.io_in, &s.io_in_cap, 2 * n * sizeof(float));
+  if (rc != HP_OK) return rc;
+  rc = grow((void **)&s.io_out[0], &s.io_out_cap[0], n * sizeof(float));
+  if (rc != HP_OK) return rc;
+  HP_HIP_TRY(hipMemcpyAsync(s.io_in, gate, n * 4, hipMemcpyHostToDevice, s.stream));
+  HP_HIP_TRY(hipMemcpyAsync(s.io_in + n, up, n * 4, hipMemcpyHostToDevice, s.stream));
+  HP_HIP_TRY(launch_geglu(s.io_in, s.io_in + n, n, gelu_constant(), s.io_out[0], s.num_cus, s.stream));
+  s.launches++;
+  HP_HIP_TRY(hipMemcpyAsync(output, s.io_out[0], n * 4, hipMemcpyDeviceToHost, s.stream));
+  HP_HIP_TRY(hipStreamSynchronize(s.stream));
+  return HP_OK;
+}
+
 int32_t hp_hip_quantize_q8_k(const float *input, size_t input_len, size_t input_size, size_t column_count,
                              int8_t *qs, float *d, int16_t *bsums32) {
   State &s = st();
@@ -522,7 +673,7 @@ int32_t hp_hip_stats(hp_hip_stats_t *out) {
       r.handle_count++;
       r.resident_bytes += h.byte_length;
     }
-  r.scratch_bytes = s.io_in_cap;
+  r.scratch_bytes = s.io_in_cap + s.topk_cand_cap + s.topk_out_cap;
   for (int i = 0; i < kMaxWeights; i++) r.scratch_bytes += s.io_out_cap[i];
   r.matmul_calls = s.matmul_calls;
   r.kernel_launches = s.launches;

@@ -82,6 +82,14 @@ hipError_t launch_q8k_natural(const float *x, int k, int cols, int8_t *qs, float
 hipError_t launch_matvec(const MatvecArgs &a, int num_cus, hipStream_t s);
 hipError_t launch_repack(int type, const uint8_t *raw, int rows, const TileGeom &g, uint8_t *tiles,
                          uint16_t *dplane, hipStream_t s);
+// Top-k (k <= 64) of each of `rows` rows of n logits (n <= 524288), optional
+// softcap (cap > 0); cand is scratch of topk_candidate_bytes(rows, n, k).
+hipError_t launch_topk(const float *logits, int rows, int n, int k, double cap, uint64_t *cand, uint32_t *ids,
+                       float *vals, hipStream_t s);
+size_t topk_candidate_bytes(int rows, int n, int k);
+int topk_elements_per_lane(int n);
+hipError_t launch_geglu(const float *gate, const float *up, size_t n, double c, float *out, int num_cus,
+                        hipStream_t s);
 hipError_t launch_dequantize(int type, const uint8_t *tiles, const uint16_t *dplane, int rows,
                              const TileGeom &g, int row_start, int row_count, float *out, hipStream_t s);
 

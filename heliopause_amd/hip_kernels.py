@@ -36,6 +36,7 @@ LIB_PATH = PKG / "libhp_hip.so"
 HP_OK, HP_ERR_SHAPE, HP_ERR_HEADS, HP_ERR_TYPE = 0, 1, 2, 3
 HP_ERR_HIP, HP_ERR_HANDLE, HP_ERR_ARG, HP_ERR_NODEV, HP_ERR_OOM = 16, 17, 18, 19, 20
 HP_KERNEL_Q8K, HP_KERNEL_MATVEC, HP_KERNEL_TOPK, HP_KERNEL_GEGLU = 0, 1, 2, 3
+GELU_C = float(np.sqrt(2.0 / np.pi))
 
 TYPE_IDS = {"Q4_K": 1, "Q5_K": 2, "Q6_K": 3, "IQ4_XS": 4, "Q8_0": 5, "Q4_0": 6}
 SUPPORTED = ("Q4_K", "Q6_K")
@@ -102,25 +103,17 @@ def _declare(L: ctypes.CDLL) -> None:
 
 
 def _declare_optional(L: ctypes.CDLL) -> None:
-    """Entry points added alongside the matmul ones (top-k, GeGLU)."""
+    """Top-k and GeGLU entry points."""
     i32 = ctypes.c_int32
-    if hasattr(L, "hp_hip_matmul_topk"):
-        L.hp_hip_matmul_topk.argtypes = [_u64, ctypes.c_void_p, _sz, _sz, _sz, _sz, ctypes.c_void_p,
-                                         ctypes.c_void_p, _sz]
-        L.hp_hip_matmul_topk.restype = i32
-    if hasattr(L, "hp_hip_topk_device"):
-        L.hp_hip_topk_device.argtypes = [ctypes.c_void_p, _sz, _sz, _sz, ctypes.c_void_p, ctypes.c_void_p,
-                                         ctypes.c_void_p]
-        L.hp_hip_topk_device.restype = i32
-    if hasattr(L, "hp_hip_topk"):
-        L.hp_hip_topk.argtypes = [ctypes.c_void_p, _sz, _sz, _sz, ctypes.c_void_p, ctypes.c_void_p, _sz]
-        L.hp_hip_topk.restype = i32
-    if hasattr(L, "hp_hip_geglu"):
-        L.hp_hip_geglu.argtypes = [ctypes.c_void_p, ctypes.c_void_p, _sz, ctypes.c_void_p]
-        L.hp_hip_geglu.restype = i32
-    if hasattr(L, "hp_hip_geglu_device"):
-        L.hp_hip_geglu_device.argtypes = [ctypes.c_void_p, ctypes.c_void_p, _sz, ctypes.c_void_p, ctypes.c_void_p]
-        L.hp_hip_geglu_device.restype = i32
+    vp = ctypes.c_void_p
+    L.hp_hip_matmul_topk.argtypes = [_u64, vp, _sz, _sz, _sz, _sz, ctypes.c_double, vp, vp, _sz]
+    L.hp_hip_topk.argtypes = [vp, _sz, _sz, _sz, ctypes.c_double, vp, vp, _sz]
+    L.hp_hip_topk_device.argtypes = [vp, _sz, _sz, _sz, ctypes.c_double, vp, vp, vp]
+    L.hp_hip_geglu.argtypes = [vp, vp, _sz, vp]
+    L.hp_hip_geglu_device.argtypes = [vp, vp, _sz, vp, vp]
+    for name in ("hp_hip_matmul_topk", "hp_hip_topk", "hp_hip_topk_device", "hp_hip_geglu",
+                 "hp_hip_geglu_device"):
+        getattr(L, name).restype = i32
 
 
 def lib() -> ctypes.CDLL:
@@ -303,6 +296,53 @@ def quantizeQ8KHip(input_columns, input_size: int, column_count: int):
                                       d.ctypes.data, bs.ctypes.data)
     assertHipOk(code, "quantizeQ8K")
     return qs, d, bs
+
+
+def _topk_result(ids: np.ndarray, vals: np.ndarray, n: int, k: int) -> list:
+    count = min(n, k)
+    return [[{"id": int(i), "value": float(v)} for i, v in zip(ids[r, :count], vals[r, :count])]
+            for r in range(ids.shape[0])]
+
+
+def topKHip(values, k: int, softcap: float = 0.0) -> list:
+    """topK (runtime.ts:514-527) of each row of ``values`` ([rows][n] or [n]) on
+    the GPU: per row a list of {id, value}, best first, ties to the lower id."""
+    v = np.ascontiguousarray(np.atleast_2d(values), dtype=np.float32)
+    rows, n = v.shape
+    ids = np.empty((rows, k), dtype=np.uint32)
+    vals = np.empty((rows, k), dtype=np.float32)
+    code = lib().hp_hip_topk(v.ctypes.data, rows, n, k, float(softcap), ids.ctypes.data, vals.ctypes.data,
+                             ids.size)
+    assertHipOk(code, "topK")
+    return _topk_result(ids, vals, n, k)
+
+
+def matMulQuantizedHipResidentTopK(handle: HipQuantizedWeightHandle, input_columns, input_size: int,
+                                   column_count: int, top_k: int, softcap: float = 0.0) -> list:
+    """forwardOutput (layers.ts:381-416) for a resident head: logits stay in HBM,
+    optional softcap, topK per column; only the candidates come back."""
+    if handle.released:
+        raise RuntimeError(f"Resident quantized matmul handle {handle.handle} is not available")
+    x = _f32(input_columns)
+    if handle.inputSize != input_size or x.size != input_size * column_count:
+        raise ValueError(f"Resident quantized matmul input shape mismatch: {x.size}")
+    ids = np.empty((column_count, top_k), dtype=np.uint32)
+    vals = np.empty((column_count, top_k), dtype=np.float32)
+    code = lib().hp_hip_matmul_topk(handle.handle, x.ctypes.data, x.size, input_size, column_count, top_k,
+                                    float(softcap), ids.ctypes.data, vals.ctypes.data, ids.size)
+    assertHipOk(code, "matMulQuantizedResidentTopK")
+    return _topk_result(ids, vals, handle.rowCount, top_k)
+
+
+def gegluHip(gate, up) -> np.ndarray:
+    """GeGLU (layers.ts:450-456): fround(gelu(gate) * up), elementwise."""
+    g = _f32(gate)
+    u = _f32(up)
+    if g.size != u.size:
+        raise ValueError(f"GeGLU shape mismatch: {g.size} vs {u.size}")
+    out = np.empty_like(g)
+    assertHipOk(lib().hp_hip_geglu(g.ctypes.data, u.ctypes.data, g.size, out.ctypes.data), "geglu")
+    return out.reshape(np.shape(gate))
 
 
 # ---- device-pointer entry points (inputs/outputs already in HBM) -----------------

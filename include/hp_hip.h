@@ -117,6 +117,28 @@ int32_t hp_hip_matmul_multi_device(size_t count, const uint64_t *handles, const 
                                    size_t input_size, size_t column_count, float *const *d_outputs,
                                    const size_t *output_lens, void *stream);
 
+/* Output head + sampling candidates: forwardOutput (layers.ts:381-416) ->
+ * logits = matmul(handle, input) kept in HBM, optional softcap
+ * fround(tanh(v / softcap) * softcap) when softcap > 0 (layers.ts:407-412),
+ * then topK (runtime.ts:514-527) per column: k (<= 64) ids and values in
+ * descending value order, ties to the lower id.  Only the candidates are
+ * copied back: ids / values are [column_count][k] (out_len = column_count*k).
+ * Replaces the WebGPU dispatchOutputTopK (segment-runner.ts:3208-3248). */
+int32_t hp_hip_matmul_topk(uint64_t handle, const float *input, size_t input_len, size_t input_size,
+                           size_t column_count, size_t k, double softcap, uint32_t *ids, float *values,
+                           size_t out_len);
+/* topK over host logits [rows][n] (n <= 524288, k <= 64); same semantics. */
+int32_t hp_hip_topk(const float *logits, size_t rows, size_t n, size_t k, double softcap, uint32_t *ids,
+                    float *values, size_t out_len);
+/* Device-pointer topK; asynchronous on stream (NULL = library stream). */
+int32_t hp_hip_topk_device(const float *d_logits, size_t rows, size_t n, size_t k, double softcap,
+                           uint32_t *d_ids, float *d_values, void *stream);
+
+/* GeGLU epilogue (layers.ts:450-456 with gelu 1062-1076):
+ * out[i] = fround(gelu(gate[i]) * up[i]), bit-exact with the JS engine. */
+int32_t hp_hip_geglu(const float *gate, const float *up, size_t n, float *output);
+int32_t hp_hip_geglu_device(const float *d_gate, const float *d_up, size_t n, float *d_output, void *stream);
+
 /* Dequantise rows [row_start, row_start + row_count) of a handle into f32
  * [row_count][input_size] (lib.rs:1630-1664, 1709-1744; bit-exact).  Test
  * hook proving the resident layout is lossless. */

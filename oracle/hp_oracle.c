@@ -523,9 +523,109 @@ int32_t hpo_matmul_quantized_threaded(int32_t type_id, const uint8_t *weight, si
 }
 
 /* ---------------------------------------------------------------------- */
+/* Math.tanh as V8 evaluates it: fdlibm's s_tanh.c over s_expm1.c (Sun
+ * Microsystems 1993; the published algorithm V8 ships as ieee754::tanh).
+ * Pinned against Math.tanh outputs in tests/golden/v8_tanh.json. */
+static uint32_t hiw(double x) { uint64_t b; memcpy(&b, &x, 8); return (uint32_t)(b >> 32); }
+static uint32_t low(double x) { uint64_t b; memcpy(&b, &x, 8); return (uint32_t)b; }
+static double words(uint32_t hi, uint32_t lo) { uint64_t b = ((uint64_t)hi << 32) | lo; double d; memcpy(&d, &b, 8); return d; }
+
+double hpo_expm1(double x) {
+  const double o_threshold = 7.09782712893383973096e+02, ln2_hi = 6.93147180369123816490e-01,
+               ln2_lo = 1.90821492927058770002e-10, invln2 = 1.44269504088896338700e+00,
+               Q1 = -3.33333333333331316428e-02, Q2 = 1.58730158725481460165e-03,
+               Q3 = -7.93650757867487942473e-05, Q4 = 4.00821782732936239552e-06,
+               Q5 = -2.01099218183624371326e-07, huge = 1.0e+300, tiny = 1.0e-300;
+  double y, hi, lo, c = 0.0, t, e, hxs, hfx, r1;
+  int32_t k;
+  uint32_t hx = hiw(x);
+  uint32_t xsb = hx & 0x80000000u;
+  hx &= 0x7fffffffu;
+  if (hx >= 0x4043687Au) {
+    if (hx >= 0x40862E42u) {
+      if (hx >= 0x7ff00000u) {
+        if (((hx & 0xfffffu) | low(x)) != 0) return x + x;
+        return xsb == 0 ? x : -1.0;
+      }
+      if (x > o_threshold) return huge * huge;
+    }
+    if (xsb != 0 && x + tiny < 0.0) return tiny - 1.0;
+  }
+  if (hx > 0x3fd62e42u) {
+    if (hx < 0x3FF0A2B2u) {
+      if (xsb == 0) { hi = x - ln2_hi; lo = ln2_lo; k = 1; }
+      else { hi = x + ln2_hi; lo = -ln2_lo; k = -1; }
+    } else {
+      k = (int32_t)(invln2 * x + (xsb == 0 ? 0.5 : -0.5));
+      t = k;
+      hi = x - t * ln2_hi;
+      lo = t * ln2_lo;
+    }
+    x = hi - lo;
+    c = (hi - x) - lo;
+  } else if (hx < 0x3c900000u) {
+    t = huge + x;
+    return x - (t - (huge + x));
+  } else {
+    k = 0;
+  }
+  hfx = 0.5 * x;
+  hxs = x * hfx;
+  r1 = 1.0 + hxs * (Q1 + hxs * (Q2 + hxs * (Q3 + hxs * (Q4 + hxs * Q5))));
+  t = 3.0 - r1 * hfx;
+  e = hxs * ((r1 - t) / (6.0 - x * t));
+  if (k == 0) return x - (x * e - hxs);
+  double twopk = words(0x3ff00000u + ((uint32_t)k << 20), 0);
+  e = (x * (e - c) - c);
+  e -= hxs;
+  if (k == -1) return 0.5 * (x - e) - 0.5;
+  if (k == 1) {
+    if (x < -0.25) return -2.0 * (e - (x + 0.5));
+    return 1.0 + 2.0 * (x - e);
+  }
+  if (k <= -2 || k > 56) {
+    y = 1.0 - (e - x);
+    y = (k == 1024) ? y * 2.0 * 8.98846567431158e+307 : y * twopk;
+    return y - 1.0;
+  }
+  if (k < 20) {
+    t = words(0x3ff00000u - (0x200000u >> k), 0);
+    y = t - (e - x);
+    y = y * twopk;
+  } else {
+    t = words((uint32_t)(0x3ff - k) << 20, 0);
+    y = x - (e + t);
+    y += 1.0;
+    y = y * twopk;
+  }
+  return y;
+}
+
+double hpo_tanh(double x) {
+  const double tiny = 1.0e-300, huge = 1.0e300;
+  double t, z;
+  uint32_t jx = hiw(x), ix = jx & 0x7fffffffu;
+  int neg = (jx & 0x80000000u) != 0;
+  if (ix >= 0x7ff00000u) return neg ? 1.0 / x - 1.0 : 1.0 / x + 1.0;
+  if (ix < 0x40360000u) {
+    if (ix < 0x3e300000u && huge + x > 1.0) return x;
+    if (ix >= 0x3ff00000u) {
+      t = hpo_expm1(2.0 * fabs(x));
+      z = 1.0 - 2.0 / (t + 2.0);
+    } else {
+      t = hpo_expm1(-2.0 * fabs(x));
+      z = -t / (t + 2.0);
+    }
+  } else {
+    z = 1.0 - tiny;
+  }
+  return neg ? -z : z;
+}
+
+/* ---------------------------------------------------------------------- */
 /* layers.ts:1062-1076 gelu.  JS numbers are f64: every Math.fround is a
- * cast to float, every other operation is an f64 operation.  Math.tanh is
- * the host libm tanh here (V8 uses an fdlibm port; both are within 1 ulp). */
+ * cast to float, every other operation is an f64 operation; Math.tanh is
+ * hpo_tanh (V8's algorithm). */
 float hpo_gelu(float vf) {
   double value = vf;
   if (value <= -10.0) return 0.0f;
@@ -538,7 +638,7 @@ float hpo_gelu(float vf) {
   double t3 = (float)(1.0 + t2);
   double inner = (float)(t1 * t3);
   double half = (float)(0.5 * x);
-  double t4 = (float)(1.0 + tanh(inner));
+  double t4 = (float)(1.0 + hpo_tanh(inner));
   double activated = (float)(half * t4);
   return (float)hpo_f16_to_f64_ts(hpo_f64_to_f16_ts(activated));
 }
@@ -549,23 +649,27 @@ void hpo_geglu(const float *gate, const float *up, size_t n, float *out) {
 }
 
 /* layers.ts:407-412 softcap: Math.fround(Math.tanh(v / c) * c). */
-float hpo_softcap(float v, double cap) { return (float)(tanh((double)v / cap) * cap); }
+float hpo_softcap(float v, double cap) { return (float)(hpo_tanh((double)v / cap) * cap); }
 
 /* runtime.ts:514-527 topK: a candidate enters while fewer than k are kept
- * or when it is strictly greater than the current k-th value; the stable
- * descending sort keeps equal values in id order, so ties go to the lower
- * id (-0 and +0 tie).  NaN (never greater) is placed last when it enters. */
+ * or when it ranks above the current k-th value; the stable descending sort
+ * keeps equal values in id order, so ties go to the lower id (-0 and +0
+ * tie).  NaN ranks below every number (JS leaves NaN's place to the sort
+ * implementation; logits carry no NaN), so NaNs fill the tail in id order. */
+static int ranks_above(float a, float b) {
+  if (b != b) return a == a;
+  if (a != a) return 0;
+  return a > b;
+}
+
 size_t hpo_topk(const float *values, size_t n, size_t k, uint32_t *ids, float *out_values) {
   size_t len = 0;
   if (k == 0) return 0;
   for (size_t id = 0; id < n; id++) {
     float v = values[id];
-    if (len < k || v > out_values[len - 1]) {
-      size_t pos = len;
-      if (v == v) {
-        pos = 0;
-        while (pos < len && out_values[pos] == out_values[pos] && out_values[pos] >= v) pos++;
-      }
+    if (len < k || ranks_above(v, out_values[len - 1])) {
+      size_t pos = 0;
+      while (pos < len && !ranks_above(v, out_values[pos])) pos++;
       size_t last = len < k ? len : k - 1;
       for (size_t i = last; i > pos; i--) {
         ids[i] = ids[i - 1];

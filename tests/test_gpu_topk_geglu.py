@@ -1,0 +1,89 @@
+"""GPU parity: top-k over logits, the output head + top-k, and GeGLU.
+
+Top-k bar: ids identical and values bit-identical to the oracle's restatement
+of runtime.ts:514-527 (descending value, ties to the lower id, -0 == +0).
+GeGLU bar: bit-identical to the oracle's restatement of layers.ts:450-456 and
+1062-1076 (whose tanh is pinned to V8's Math.tanh).
+"""
+import numpy as np
+import pytest
+
+from heliopause_amd import synthetic as S
+
+pytestmark = pytest.mark.gpu
+
+
+def _check_rows(got, logits, k, oracle, softcap=0.0):
+    for r, row in enumerate(np.atleast_2d(logits)):
+        vals = row if softcap == 0.0 else np.array([oracle.softcap(float(v), softcap) for v in row], np.float32)
+        ids, ref_vals = oracle.topk(vals, k)
+        g_ids = np.array([c["id"] for c in got[r]], dtype=np.uint32)
+        g_vals = np.array([c["value"] for c in got[r]], dtype=np.float32)
+        assert np.array_equal(g_ids, ids), (r, g_ids[:8], ids[:8])
+        assert np.array_equal(g_vals.view(np.uint32), ref_vals.view(np.uint32)), r
+
+
+@pytest.mark.parametrize("rows,n,k", [(1, 262144, 40), (4, 262144, 40), (2, 100000, 64), (3, 4096, 1),
+                                      (1, 10, 40), (2, 300000, 17), (1, 524288, 40)])
+def test_topk_random(hip, oracle, rows, n, k):
+    print(f"topk rows={rows} n={n} k={k}", flush=True)
+    logits = S.activations(S.derive(S.BASE_SEED, "topk", rows, n), rows, n) * 4.0
+    got = hip.topKHip(logits, k)
+    _check_rows(got, logits, k, oracle)
+
+
+def test_topk_ties_and_zero_signs(hip, oracle):
+    n, k = 262144, 40
+    rng = np.random.default_rng(5)
+    logits = np.zeros((3, n), dtype=np.float32)
+    logits[0] = rng.integers(-3, 4, size=n).astype(np.float32)      # massive ties
+    logits[1, ::2] = -0.0                                              # -0 / +0 ties
+    logits[1, 1000:1100] = 1.5
+    logits[2] = rng.standard_normal(n).astype(np.float32)
+    logits[2, 7] = np.nan                                              # NaN ranks last
+    logits[2, 9] = np.inf
+    logits[2, 11] = -np.inf
+    logits[2, 262143] = logits[2].max()                                # tie at the top, high id
+    got = hip.topKHip(logits, k)
+    _check_rows(got, logits, k, oracle)
+    nan_row = np.full((1, 50), np.nan, dtype=np.float32)
+    nan_row[0, 3] = 1.0
+    _check_rows(hip.topKHip(nan_row, 40), nan_row, 40, oracle)
+
+
+def test_topk_softcap(hip, oracle):
+    logits = S.activations(S.derive(S.BASE_SEED, "softcap"), 2, 65536) * 20.0
+    _check_rows(hip.topKHip(logits, 40, softcap=30.0), logits, 40, oracle, softcap=30.0)
+
+
+@pytest.mark.parametrize("rows,m", [(20000, 1), (20000, 4)])
+def test_head_matmul_topk(hip, oracle, rows, m):
+    """Q6_K output head + top-40 per column, candidates only (config 4 at reduced rows)."""
+    print(f"head rows={rows} m={m}", flush=True)
+    k_in = 2560
+    seed = S.derive(S.config_seed(4), "head", rows, m)
+    w = S.q6_k_blocks(seed, rows, k_in)
+    x = S.activations(seed, m, k_in)
+    h = hip.createHipQuantizedWeightHandle("Q6_K", w, k_in, rows)
+    try:
+        got = hip.matMulQuantizedHipResidentTopK(h, x, k_in, m, 40)
+    finally:
+        hip.releaseHipQuantizedWeightHandle(h)
+    logits = oracle.matmul(3, w, x, rows, threads=8)
+    _check_rows(got, logits, 40, oracle)
+
+
+def test_geglu_bit_exact(hip, oracle):
+    n = 1 << 20
+    seed = S.derive(S.BASE_SEED, "geglu")
+    gate = (S.activations(seed, 1, n)[0] * 3.0).astype(np.float32)
+    up = S.activations(S.derive(seed, 1), 1, n)[0]
+    special = np.array([0.0, -0.0, 1.0, -1.0, 10.0, -10.0, 9.999999, -9.999999, 10.000001, -10.000001,
+                        5.960464477539063e-08, -5.960464477539063e-08, 2.9802322387695312e-08, 1e-30, -1e-40,
+                        3.0, -3.0, 0.5, 7.25, 65504.0, -65504.0, 1e6], dtype=np.float32)
+    gate[: special.size] = special
+    up[: special.size] = np.linspace(-2, 2, special.size).astype(np.float32)
+    got = hip.gegluHip(gate, up)
+    ref = oracle.geglu(gate, up)
+    diff = np.flatnonzero(got.view(np.uint32) != ref.view(np.uint32))
+    assert diff.size == 0, (diff[:5], gate[diff[:5]], got[diff[:5]], ref[diff[:5]])
