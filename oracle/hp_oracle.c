@@ -59,6 +59,14 @@ float hpo_f16_to_f32(uint16_t value) {
   return f;
 }
 
+/* Bit pattern of hpo_f16_to_f32 (keeps signalling NaNs intact for tests). */
+uint32_t hpo_f16_to_f32_bits(uint16_t value) {
+  float f = hpo_f16_to_f32(value);
+  uint32_t b;
+  memcpy(&b, &f, 4);
+  return b;
+}
+
 /* lib.rs:2534-2569 float32_to_float16 (round half up on the mantissa). */
 uint16_t hpo_f32_to_f16_rust(float value) {
   uint32_t bits;

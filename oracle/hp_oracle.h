@@ -27,6 +27,7 @@ enum { HPO_Q4_K = 1, HPO_Q5_K = 2, HPO_Q6_K = 3, HPO_IQ4_XS = 4, HPO_Q8_0 = 5, H
 
 /* ---- scalar conversions ---------------------------------------------- */
 float hpo_f16_to_f32(uint16_t h);            /* lib.rs:2507-2532 */
+uint32_t hpo_f16_to_f32_bits(uint16_t h);    /* the same, as bits */
 uint16_t hpo_f32_to_f16_rust(float v);       /* lib.rs:2534-2569 (round half up) */
 double hpo_f16_to_f64_ts(uint16_t h);        /* quant.ts:618-630 */
 uint16_t hpo_f64_to_f16_ts(double v);        /* quant.ts:632-669 (ties to even) */

@@ -50,6 +50,8 @@ def lib() -> ctypes.CDLL:
     L = ctypes.CDLL(str(LIB_PATH))
     L.hpo_f16_to_f32.argtypes = [ctypes.c_uint16]
     L.hpo_f16_to_f32.restype = ctypes.c_float
+    L.hpo_f16_to_f32_bits.argtypes = [ctypes.c_uint16]
+    L.hpo_f16_to_f32_bits.restype = ctypes.c_uint32
     L.hpo_f32_to_f16_rust.argtypes = [ctypes.c_float]
     L.hpo_f32_to_f16_rust.restype = ctypes.c_uint16
     L.hpo_f16_to_f64_ts.argtypes = [ctypes.c_uint16]
@@ -104,7 +106,7 @@ def f16_to_f32(h: int) -> float:
 
 
 def f16_bits_to_f32_bits(h: int) -> int:
-    return int(np.float32(lib().hpo_f16_to_f32(h)).view(np.uint32))
+    return int(lib().hpo_f16_to_f32_bits(h))
 
 
 def f32_to_f16_rust(v: float) -> int:

@@ -1,4 +1,4 @@
-// Writes Math.tanh(x) for a fixed set of inputs, as IEEE-754 bit patterns,
+// Writes Math.tanh(x) for a fixed set of inputs, as little-endian f64 bytes,
 // to pin the oracle's tanh (fdlibm algorithm) to the JS engine's results.
 // Usage: node tests/golden/make_v8_tanh.js > tests/golden/v8_tanh.json
 'use strict';
@@ -10,7 +10,7 @@ let s = 0x2545F491;
 function rnd() { s = (Math.imul(s, 1664525) + 1013904223) >>> 0; return s; }
 const inputs = [];
 // the gelu/softcap domain: f32 values in [-48, 48], uniform in bits within ranges
-for (let i = 0; i < 60000; i++) {
+for (let i = 0; i < 40000; i++) {
   const e = (rnd() % 40) - 34;              // magnitude 2^-34 .. 2^5
   const m = rnd() / 4294967296;
   let x = Math.fround((1 + m) * Math.pow(2, e));
@@ -25,5 +25,11 @@ for (const t of edges) for (const d of [-2, -1, 0, 1, 2]) {
   inputs.push(y, -y);
 }
 inputs.push(0, -0, 1e-300, -1e-300, 30, -30, 100);
-const out = inputs.map((x) => [bits(x), bits(Math.tanh(x))]);
-process.stdout.write(JSON.stringify({ engine: 'node ' + process.version, pairs: out }) + '\n');
+const xs = Float64Array.from(inputs);
+const ys = xs.map((x) => Math.tanh(x));
+process.stdout.write(JSON.stringify({
+  engine: 'node ' + process.version,
+  count: xs.length,
+  x_f64le_base64: Buffer.from(xs.buffer).toString('base64'),
+  tanh_f64le_base64: Buffer.from(ys.buffer).toString('base64'),
+}) + '\n');
