@@ -1,15 +1,23 @@
 """Benchmark of the gfx950 quantized-projection path.
 
-Workload (the metric's configuration): the batched attention projections of
-one decoder layer sharing one input -- Q = Q4_K 2048x2560, K = Q4_K 512x2560,
-V = Q6_K 512x2560 -- as ONE multi-weight launch (shared Q8_K), M = 1 column.
-A step is one such projection pass.  Weights are GGUF super-blocks generated
-from a fixed seed and uploaded once; the step rotates over enough distinct
-weight copies (>= 512 MiB) that every step streams its weights from HBM, not
-from the 256 MB Infinity Cache.  Inputs and outputs stay in HBM.
+Default workload (the metric's configuration): the batched attention
+projections of one decoder layer sharing one input -- Q = Q4_K 2048x2560,
+K = Q4_K 512x2560, V = Q6_K 512x2560 -- as ONE multi-weight launch (shared
+in-kernel Q8_K), M = 1 column.  A step is one such projection pass.
 
-Prints one JSON line (rank 0).  ``value`` = algorithmic bytes per step
-(weights as stored + f32 input + f32 outputs) / wall time per step, GB/s.
+Other workloads (``--workload``): ``cfg1`` (one Q4_K 10240x2560 matvec),
+``gate_up`` (two Q4_K 10240x2560 in one launch), ``down`` (Q6_K 2560x10240),
+``ffn`` (gate/up launch -> GeGLU -> down), ``head`` (Q6_K 262144x2560 output
+head + top-40 per column, candidates only).
+
+Weights are GGUF super-blocks generated from a fixed seed and uploaded once;
+steps rotate over enough distinct weight copies (>= 640 MiB) that every step
+streams its weights from HBM rather than from the 256 MB Infinity Cache.
+Inputs and outputs stay in HBM.  The timed steps are captured once in a HIP
+graph and replayed back to back.
+
+Prints one JSON line.  ``value`` = algorithmic bytes per step (weights as
+stored + f32 activations read and written) / wall time per step, in GB/s.
 """
 from __future__ import annotations
 
@@ -27,18 +35,47 @@ sys.path.insert(0, str(ROOT))
 
 METRIC = "Q4_K/Q6_K matvec GB/s (% HBM peak); decode step ms at M=1 (1 GPU)"
 HBM_PEAK_GBPS = 8000.0
-K_IN = 2560
-SPECS = [("Q4_K", 2048), ("Q4_K", 512), ("Q6_K", 512)]
 TYPE_IDS = {"Q4_K": 1, "Q6_K": 3}
-ROW_BYTES = {"Q4_K": K_IN // 256 * 144, "Q6_K": K_IN // 256 * 210}
+BLOCK = {"Q4_K": 144, "Q6_K": 210}
+
+# name -> (config id, input size, weights of one launch, description)
+WORKLOADS = {
+    "qkv": (2, 2560, [("Q4_K", 2048), ("Q4_K", 512), ("Q6_K", 512)],
+            "attention Q/K/V projections sharing one input: Q Q4_K 2048x2560, K Q4_K 512x2560, "
+            "V Q6_K 512x2560, one multi-weight launch with in-kernel Q8_K"),
+    "cfg1": (1, 2560, [("Q4_K", 10240)], "single Q4_K 10240x2560 matvec"),
+    "gate_up": (3, 2560, [("Q4_K", 10240), ("Q4_K", 10240)], "FFN gate+up: two Q4_K 10240x2560 in one launch"),
+    "down": (3, 10240, [("Q6_K", 2560)], "FFN down: Q6_K 2560x10240"),
+    "ffn": (3, 2560, [("Q4_K", 10240), ("Q4_K", 10240)],
+            "decoder FFN: gate+up Q4_K 10240x2560 launch -> GeGLU -> down Q6_K 2560x10240"),
+    "head": (4, 2560, [("Q6_K", 262144)], "output head Q6_K 262144x2560 + top-40 per column (candidates only)"),
+}
+FFN_DOWN = ("Q6_K", 2560, 10240)
+TOPK = 40
 
 
-def weight_bytes() -> int:
-    return sum(ROW_BYTES[t] * r for t, r in SPECS)
+def row_bytes(t: str, k: int) -> int:
+    return k // 256 * BLOCK[t]
 
 
-def algorithmic_bytes(m: int) -> int:
-    return weight_bytes() + m * K_IN * 4 + m * sum(r for _, r in SPECS) * 4
+def weight_bytes(workload: str) -> int:
+    _, k, specs, _ = WORKLOADS[workload]
+    b = sum(row_bytes(t, k) * r for t, r in specs)
+    if workload == "ffn":
+        b += row_bytes(FFN_DOWN[0], FFN_DOWN[2]) * FFN_DOWN[1]
+    return b
+
+
+def algorithmic_bytes(workload: str, m: int) -> int:
+    """Weights as stored plus every f32 activation the step reads or writes."""
+    _, k, specs, _ = WORKLOADS[workload]
+    rows = sum(r for _, r in specs)
+    b = weight_bytes(workload) + m * k * 4 + m * rows * 4
+    if workload == "ffn":  # GeGLU reads gate+up, writes h; down reads h, writes y
+        b += m * (2 * 10240 + 10240 + 10240 + 2560) * 4
+    if workload == "head":  # logits read back by top-k, candidates written
+        b += m * 262144 * 4 + m * TOPK * 8
+    return b
 
 
 def parse() -> argparse.Namespace:
@@ -47,6 +84,7 @@ def parse() -> argparse.Namespace:
     p.add_argument("--steps", type=int, default=400)
     p.add_argument("--warmup", type=int, default=40)
     p.add_argument("--m", type=int, default=1)
+    p.add_argument("--workload", choices=sorted(WORKLOADS), default="qkv")
     p.add_argument("--rotate-mib", type=int, default=640, help="distinct weight bytes cycled through")
     p.add_argument("--cpu-seconds", type=float, default=12.0)
     p.add_argument("--no-cpu", action="store_true")
@@ -70,14 +108,15 @@ def copy_probe() -> int:
     return 0
 
 
-def cpu_baseline(ws, x, seconds: float) -> dict:
+def cpu_baseline(workload: str, ws, x, seconds: float) -> dict:
     """The oracle's threaded restatement of the reference's resident WASM path on
-    the same workload (bounded sample); threads = the reference's default pool."""
+    the same launch (bounded sample); threads = the reference's default pool."""
     from oracle import oracle as O
 
+    _, k, specs, _ = WORKLOADS[workload]
     threads = O.default_threads()
-    tids = [TYPE_IDS[t] for t, _ in SPECS]
-    rows = [r for _, r in SPECS]
+    tids = [TYPE_IDS[t] for t, _ in specs]
+    rows = [r for _, r in specs]
     O.matmul_multi(tids, ws, x, rows, threads=threads)  # warm
     n, t0 = 0, time.perf_counter()
     while True:
@@ -87,13 +126,13 @@ def cpu_baseline(ws, x, seconds: float) -> dict:
         if el >= seconds:
             break
     m = x.shape[0]
-    gbps = algorithmic_bytes(m) * n / el / 1e9
+    launch_bytes = sum(row_bytes(t, k) * r for t, r in specs) + m * k * 4 + m * sum(rows) * 4
     return {
-        "value": round(gbps, 3),
+        "value": round(launch_bytes * n / el / 1e9, 3),
         "unit": "GB/s",
         "cores": threads,
         "kind": "port",
-        "sample": f"{n} calls of the Q/K/V multi projection at M={m} in {el:.1f} s "
+        "sample": f"{n} calls of the {workload} projection launch at M={m} in {el:.1f} s "
                   f"({el / n * 1e3:.3f} ms/call); C restatement of lib.rs resident kernels, "
                   f"splitRows sharding over {threads} threads; host {platform.processor() or platform.machine()}, "
                   f"{os.cpu_count()} logical CPUs",
@@ -105,8 +144,7 @@ def main() -> int:
     if args.copy_probe:
         return copy_probe()
     if args.gpus != 1:
-        print(json.dumps({"error": "this build runs on one GPU only; --gpus must be 1",
-                          "n_gpus": args.gpus}))
+        print(json.dumps({"error": "this build runs on one GPU only; --gpus must be 1", "n_gpus": args.gpus}))
         return 2
     import numpy as np
     import torch
@@ -119,41 +157,53 @@ def main() -> int:
         raise SystemExit(f"HIP runner unavailable: {support}")
     torch.cuda.init()
     dev = torch.device("cuda:0")
-    m = args.m
-    seed = S.config_seed(2)
-    ws = [S.weight_blocks(t, S.derive(seed, i), r, K_IN) for i, (t, r) in enumerate(SPECS)]
-    x_host = S.activations(seed, m, K_IN)
+    wl, m = args.workload, args.m
+    cfg, k, specs, desc = WORKLOADS[wl]
+    seed = S.config_seed(cfg)
+    ws = [S.weight_blocks(t, S.derive(seed, wl, i), r, k) for i, (t, r) in enumerate(specs)]
+    w_down = S.weight_blocks(FFN_DOWN[0], S.derive(seed, wl, "down"), FFN_DOWN[1], FFN_DOWN[2]) if wl == "ffn" else None
+    x_host = S.activations(S.derive(seed, wl), m, k)
 
-    copies = max(1, math.ceil(args.rotate_mib * 2**20 / weight_bytes()))
-    handles = []
+    copies = max(1, math.ceil(args.rotate_mib * 2**20 / weight_bytes(wl)))
+    handles, down_handles = [], []
     for _ in range(copies):
-        hs = [H.createHipQuantizedWeightHandle(t, w, K_IN, r) for (t, r), w in zip(SPECS, ws)]
-        handles.append([h.handle for h in hs])
+        handles.append([H.createHipQuantizedWeightHandle(t, w, k, r).handle for (t, r), w in zip(specs, ws)])
+        if wl == "ffn":
+            down_handles.append(H.createHipQuantizedWeightHandle(FFN_DOWN[0], w_down, FFN_DOWN[2],
+                                                                 FFN_DOWN[1]).handle)
     x = torch.from_numpy(x_host).to(dev)
-    outs = [torch.empty(m * r, dtype=torch.float32, device=dev) for _, r in SPECS]
+    outs = [torch.empty(m * r, dtype=torch.float32, device=dev) for _, r in specs]
     out_ptrs = [o.data_ptr() for o in outs]
     out_lens = [o.numel() for o in outs]
+    h_ffn = torch.empty(m * 10240, dtype=torch.float32, device=dev)
+    y_ffn = torch.empty(m * 2560, dtype=torch.float32, device=dev)
+    ids = torch.empty(m * TOPK, dtype=torch.int32, device=dev)
+    vals = torch.empty(m * TOPK, dtype=torch.float32, device=dev)
     stream = torch.cuda.current_stream().cuda_stream
+    L = H.lib()
 
     def step(i: int) -> None:
-        nonlocal stream
-        H.matmul_multi_device(handles[i % copies], x.data_ptr(), K_IN, m, out_ptrs, out_lens, stream)
+        H.matmul_multi_device(handles[i % copies], x.data_ptr(), k, m, out_ptrs, out_lens, stream)
+        if wl == "ffn":
+            H.assertHipOk(L.hp_hip_geglu_device(out_ptrs[0], out_ptrs[1], m * 10240, h_ffn.data_ptr(), stream),
+                          "geglu")
+            H.matmul_multi_device([down_handles[i % copies]], h_ffn.data_ptr(), 10240, m, [y_ffn.data_ptr()],
+                                  [m * 2560], stream)
+        elif wl == "head":
+            H.assertHipOk(L.hp_hip_topk_device(out_ptrs[0], m, 262144, TOPK, 0.0, ids.data_ptr(), vals.data_ptr(),
+                                               stream), "topk")
 
     # correctness guard on the benchmarked path (first copy vs the host API)
     step(0)
     torch.cuda.synchronize()
-    ref = [o.cpu().numpy() for o in outs]
-    host = H.matMulQuantizedHipResidentMulti(
-        [H.HipQuantizedWeightHandle(h, t, 0, r, K_IN) for h, (t, r) in zip(handles[0], SPECS)], x_host, K_IN, m)
-    for a, b in zip(ref, host):
-        if not np.array_equal(a.view(np.uint32), b.view(np.uint32)):
+    host = [H.matMulQuantizedHipResident(H.HipQuantizedWeightHandle(h, t, 0, r, k), x_host, k, r, m)
+            for h, (t, r) in zip(handles[0], specs)]
+    for a, b in zip(outs, host):
+        if not np.array_equal(a.cpu().numpy().view(np.uint32), b.view(np.uint32)):
             raise SystemExit("device-pointer path disagrees with the host path")
 
-    start = torch.cuda.Event(enable_timing=True)
-    end = torch.cuda.Event(enable_timing=True)
-    step_bytes = algorithmic_bytes(m)
-
-    # eager: one host-submitted launch per step (host submission rate bound)
+    step_bytes = algorithmic_bytes(wl, m)
+    # eager: host-submitted launches (bounded by the host submission rate)
     for i in range(args.warmup):
         step(i)
     torch.cuda.synchronize()
@@ -163,9 +213,9 @@ def main() -> int:
     torch.cuda.synchronize()
     eager_ms = (time.perf_counter() - t0) / args.steps * 1e3
 
-    # timed: the steps captured once in a HIP graph (one pass over every weight
-    # copy) and replayed, so the GPU runs them back to back
+    # timed: one pass over every weight copy captured in a HIP graph, replayed
     side = torch.cuda.Stream()
+    per_graph = copies if copies >= 8 else 8 * copies
     graph = torch.cuda.CUDAGraph()
     with torch.cuda.stream(side):
         stream = side.cuda_stream
@@ -173,11 +223,13 @@ def main() -> int:
         torch.cuda.synchronize()
         with torch.cuda.graph(graph, stream=side):
             stream = torch.cuda.current_stream().cuda_stream
-            for i in range(copies):
+            for i in range(per_graph):
                 step(i)
-    replays = max(1, math.ceil(args.steps / copies))
-    steps = replays * copies
-    for _ in range(max(1, math.ceil(args.warmup / copies))):
+    replays = max(1, math.ceil(args.steps / per_graph))
+    steps = replays * per_graph
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    for _ in range(max(1, math.ceil(args.warmup / per_graph))):
         graph.replay()
     torch.cuda.synchronize()
     t0 = time.perf_counter()
@@ -189,17 +241,17 @@ def main() -> int:
     wall = time.perf_counter() - t0
     ms_per_step = wall / steps * 1e3
     value = step_bytes / (ms_per_step * 1e-3) / 1e9
-    # one kernel per step: HIP events bracketing the timed region on the launch
-    # stream give the average launch duration (back-to-back dispatches)
+    # HIP events bracketing the timed region on the launch stream: average
+    # device time per step (for one-kernel steps, the launch duration)
     kern_us = start.elapsed_time(end) / steps * 1e3
     achieved = step_bytes / (kern_us * 1e-6) / 1e9
 
-    # the same launch on one resident copy (Infinity-Cache hot), for reference
+    # Infinity-Cache-hot reference: the same step on one resident copy
     hot = torch.cuda.CUDAGraph()
     with torch.cuda.stream(side):
         with torch.cuda.graph(hot, stream=side):
             stream = torch.cuda.current_stream().cuda_stream
-            for i in range(copies):
+            for i in range(per_graph):
                 step(0)
     hot.replay()
     torch.cuda.synchronize()
@@ -211,7 +263,7 @@ def main() -> int:
     hot_us = start.elapsed_time(end) / steps * 1e3
 
     traffic = None
-    tfile = ROOT / "profiles" / "qkv_m1_traffic.json"
+    tfile = ROOT / "profiles" / f"{wl}_m{m}_traffic.json"
     if tfile.exists():
         try:
             traffic = json.loads(tfile.read_text()).get("hbm_bytes_per_launch")
@@ -220,8 +272,9 @@ def main() -> int:
 
     cpu = None
     if not args.no_cpu:
-        cpu = cpu_baseline(ws, x_host, args.cpu_seconds)
+        cpu = cpu_baseline(wl, ws, x_host, args.cpu_seconds)
 
+    kernels = {"ffn": "matvec + geglu + matvec", "head": "matvec + top-k"}
     line = {
         "metric": METRIC,
         "value": round(value, 2),
@@ -236,10 +289,9 @@ def main() -> int:
         "dtype": "int8",
         "data": "synthetic",
         "config": {
-            "workload": "attention Q/K/V projections sharing one input: Q Q4_K 2048x2560, K Q4_K 512x2560, "
-                        "V Q6_K 512x2560, one multi-weight launch with in-kernel Q8_K",
+            "workload": desc,
             "M": m,
-            "weight_bytes": weight_bytes(),
+            "weight_bytes": weight_bytes(wl),
             "algorithmic_bytes_per_step": step_bytes,
             "weight_copies_rotated": copies,
             "parallelism": "single GPU",
@@ -253,7 +305,7 @@ def main() -> int:
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBPS, 4),
             "traffic": traffic,
-            "kernel": "kquant_matvec_kernel<1, true>",
+            "kernel": kernels.get(wl, f"kquant_matvec_kernel<{min(m, 8)}>"),
             "kernel_avg_us": round(kern_us, 3),
             "kernel_avg_us_mall_hot": round(hot_us, 3),
         },
