@@ -10,7 +10,12 @@
  *   packages/engine/src/runtime.ts              -- topK
  *   packages/engine/src/runner/wasm/thread-pool.ts -- splitRows sharding
  *
- * Parity status of each function is listed in oracle/README.md.
+ * Pinning: every function is checked by tests/test_oracle_*.py against the
+ * reference's known answers, closed forms, brute force or V8's own outputs.
+ * Open item, parity unpinned: bit-level agreement of the vec-dot f32 tail
+ * (hpo_vec_dot_*) with the compiled WASM module, which cannot run here; its
+ * operation order follows lib.rs:1961-1967 and 2163-2171, and its values are
+ * checked against an f64 dot to 2e-6.
  */
 #include "hp_oracle.h"
 

@@ -7,6 +7,8 @@ saturation ranges, the 6-bit scale packing as a bijection, and dequantisation
 of blocks assembled from logical fields by a packer written here from the
 format description, with the closed-form f32 result.
 """
+import math
+
 import numpy as np
 import pytest
 
@@ -65,11 +67,46 @@ def test_f32_to_f16_ts(oracle):
     assert oracle.f64_to_f16_ts(70000.0) == 0x7BFF
 
 
+def _f16_half_away(x: float) -> int:
+    """f16 bits of x rounded to nearest, ties away from zero, saturating at
+    65504, flushing below 2^-25 to zero: computed exactly in f64."""
+    if math.isnan(x):
+        return 0x7E00
+    sign = 0x8000 if math.copysign(1.0, x) < 0 else 0
+    a = abs(x)
+    if math.isinf(a):
+        return sign | 0x7C00
+    if a < 2.0 ** -25:
+        return sign
+    if a < 2.0 ** -14:
+        return sign | int(math.floor(a / 2.0 ** -24 + 0.5))
+    mant, e = math.frexp(a)  # a = mant * 2^e, mant in [0.5, 1)
+    e -= 1
+    m = int(math.floor(a / 2.0 ** (e - 10) + 0.5))
+    if m == 2048:
+        e, m = e + 1, 1024
+    if e > 15:
+        return sign | 0x7BFF
+    return sign | ((e + 15) << 10) | (m - 1024)
+
+
 def test_f32_to_f16_rust_rounds_half_up(oracle):
     # lib.rs:2534-2569 adds half an ulp before truncating (ties away)
     assert oracle.f32_to_f16_rust(1 + 0.5 / 1024) == 0x3C01
     assert oracle.f32_to_f16_rust(1.0) == 0x3C00
     assert oracle.f32_to_f16_rust(65520.0) == 0x7BFF
+    rng = np.random.default_rng(3)
+    e = rng.integers(-27, 17, 40000).astype(np.float64)
+    v = ((rng.random(40000) + 1.0) * np.exp2(e)).astype(np.float32)
+    v = np.where(rng.random(40000) < 0.5, -v, v)
+    # exact ties and their neighbours, normal and subnormal
+    ties = np.concatenate([(np.arange(1, 2000) + 0.5) * 2.0 ** -10, (np.arange(0, 1024) + 0.5) * 2.0 ** -24])
+    ties = ties.astype(np.float32)
+    extra = np.concatenate([ties, np.nextafter(ties, np.float32(0)), np.nextafter(ties, np.float32(np.inf)),
+                            np.float32([65504, 65519.99, 65520, 65536, 1e9, 2.0 ** -25, 2.0 ** -26, 0.0, -0.0,
+                                        np.inf, -np.inf, np.nan])])
+    for x in np.concatenate([v, extra, -extra]):
+        assert oracle.f32_to_f16_rust(float(x)) == _f16_half_away(float(x)), x
 
 
 def test_row_bytes(oracle):
