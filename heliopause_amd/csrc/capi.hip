@@ -45,8 +45,8 @@ struct State {
   std::vector<Handle> handles;
   float *io_in = nullptr, *io_out[kMaxWeights] = {nullptr, nullptr, nullptr, nullptr};
   size_t io_in_cap = 0, io_out_cap[kMaxWeights] = {0, 0, 0, 0};
-  void *topk_cand = nullptr, *topk_out = nullptr;  // candidates; ids + values
-  size_t topk_cand_cap = 0, topk_out_cap = 0;
+  void *topk_scratch = nullptr, *topk_out = nullptr;  // selection scratch; ids + values
+  size_t topk_scratch_cap = 0, topk_out_cap = 0;
   uint64_t matmul_calls = 0, launches = 0;
   bool profiling = false;
   ProfileSlot prof[HP_KERNEL_COUNT];
@@ -298,18 +298,29 @@ int32_t topk_check(size_t rows, size_t n, size_t k) {
   return HP_OK;
 }
 
-// Enqueue top-k of device logits into device ids/values (scratch owned here).
+// Enqueue top-k of device logits into device ids/values, in batches of
+// kTopkMaxRows rows.  The selection scratch is zeroed when allocated; the
+// kernels return their counters to zero, so later calls need no clearing
+// (and a captured call records no memset).
 int32_t run_topk(const float *d_logits, size_t rows, size_t n, size_t k, double cap, uint32_t *d_ids, float *d_vals,
                  hipStream_t stream) {
   State &s = st();
-  const size_t cb = topk_candidate_bytes((int)rows, (int)n, (int)k);
-  int32_t rc = grow(&s.topk_cand, &s.topk_cand_cap, cb);
-  if (rc != HP_OK) return rc;
+  const size_t batch = rows < (size_t)kTopkMaxRows ? rows : (size_t)kTopkMaxRows;
+  const size_t bytes = topk_scratch_bytes((int)batch, (int)n, (int)k);
+  if (s.topk_scratch_cap < bytes || !s.topk_scratch) {
+    int32_t rc = grow(&s.topk_scratch, &s.topk_scratch_cap, bytes);
+    if (rc != HP_OK) return rc;
+    HP_HIP_TRY(hipMemsetAsync(s.topk_scratch, 0, s.topk_scratch_cap, s.stream));
+    HP_HIP_TRY(hipStreamSynchronize(s.stream));
+  }
   hipEvent_t e = prof_begin(stream);
-  HP_HIP_TRY(launch_topk(d_logits, (int)rows, (int)n, (int)k, cap, static_cast<uint64_t *>(s.topk_cand), d_ids,
-                         d_vals, stream));
+  for (size_t r0 = 0; r0 < rows; r0 += batch) {
+    const size_t nr = rows - r0 < batch ? rows - r0 : batch;
+    HP_HIP_TRY(launch_topk(d_logits + r0 * n, (int)nr, (int)n, (int)k, cap,
+                           static_cast<uint8_t *>(s.topk_scratch), d_ids + r0 * k, d_vals + r0 * k, stream));
+    s.launches += 3;
+  }
   prof_end(HP_KERNEL_TOPK, e, stream);
-  s.launches += 2;
   return HP_OK;
 }
 
@@ -378,10 +389,10 @@ int32_t hp_hip_shutdown(void) {
     s.io_out[i] = nullptr;
     s.io_out_cap[i] = 0;
   }
-  if (s.topk_cand) (void)hipFree(s.topk_cand);
+  if (s.topk_scratch) (void)hipFree(s.topk_scratch);
   if (s.topk_out) (void)hipFree(s.topk_out);
-  s.topk_cand = s.topk_out = nullptr;
-  s.topk_cand_cap = s.topk_out_cap = 0;
+  s.topk_scratch = s.topk_out = nullptr;
+  s.topk_scratch_cap = s.topk_out_cap = 0;
   prof_collect();
   for (hipEvent_t e : s.event_pool) (void)hipEventDestroy(e);
   s.event_pool.clear();
@@ -673,7 +684,7 @@ int32_t hp_hip_stats(hp_hip_stats_t *out) {
       r.handle_count++;
       r.resident_bytes += h.byte_length;
     }
-  r.scratch_bytes = s.io_in_cap + s.topk_cand_cap + s.topk_out_cap;
+  r.scratch_bytes = s.io_in_cap + s.topk_scratch_cap + s.topk_out_cap;
   for (int i = 0; i < kMaxWeights; i++) r.scratch_bytes += s.io_out_cap[i];
   r.matmul_calls = s.matmul_calls;
   r.kernel_launches = s.launches;

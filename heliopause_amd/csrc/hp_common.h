@@ -82,12 +82,17 @@ hipError_t launch_q8k_natural(const float *x, int k, int cols, int8_t *qs, float
 hipError_t launch_matvec(const MatvecArgs &a, int num_cus, hipStream_t s);
 hipError_t launch_repack(int type, const uint8_t *raw, int rows, const TileGeom &g, uint8_t *tiles,
                          uint16_t *dplane, hipStream_t s);
-// Top-k (k <= 64) of each of `rows` rows of n logits (n <= 524288), optional
-// softcap (cap > 0); cand is scratch of topk_candidate_bytes(rows, n, k).
-hipError_t launch_topk(const float *logits, int rows, int n, int k, double cap, uint64_t *cand, uint32_t *ids,
+// Top-k (k <= kTopkMaxK) of each of `rows` (<= kTopkMaxRows) rows of n
+// (<= kTopkMaxN) logits, optional softcap (cap > 0).  scratch holds
+// topk_scratch_bytes(rows, n, k) bytes, zero when first used; the kernels
+// leave their counters at zero again.  Calls sharing one scratch buffer must
+// be ordered (one stream).
+constexpr int kTopkMaxK = 64;
+constexpr int kTopkMaxN = 524288;
+constexpr int kTopkMaxRows = 16;
+hipError_t launch_topk(const float *logits, int rows, int n, int k, double cap, uint8_t *scratch, uint32_t *ids,
                        float *vals, hipStream_t s);
-size_t topk_candidate_bytes(int rows, int n, int k);
-int topk_elements_per_lane(int n);
+size_t topk_scratch_bytes(int rows, int n, int k);
 hipError_t launch_geglu(const float *gate, const float *up, size_t n, double c, float *out, int num_cus,
                         hipStream_t s);
 hipError_t launch_dequantize(int type, const uint8_t *tiles, const uint16_t *dplane, int rows,

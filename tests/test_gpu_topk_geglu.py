@@ -51,6 +51,32 @@ def test_topk_ties_and_zero_signs(hip, oracle):
     _check_rows(hip.topKHip(nan_row, 40), nan_row, 40, oracle)
 
 
+@pytest.mark.parametrize("k", [40, 64])
+def test_topk_adversarial_orders(hip, oracle, k):
+    """Inputs that defeat the chunk-maximum filter (thousands of candidates):
+    ascending and descending logits, all equal, almost all -inf, one hot
+    cluster.  Exercises the radix-select path of the final step."""
+    n = 262144
+    rng = np.random.default_rng(k)
+    base = rng.standard_normal(n).astype(np.float32)
+    rows = np.stack([np.sort(base), np.sort(base)[::-1], np.full(n, 30.0, np.float32),
+                     np.where(rng.random(n) < 1e-4, base, -np.inf).astype(np.float32), base.copy()])
+    rows[4, 5000:5100] += 10.0
+    print(f"topk adversarial k={k}", flush=True)
+    _check_rows(hip.topKHip(rows, k), rows, k, oracle)
+
+
+def test_topk_row_batches_and_reuse(hip, oracle):
+    """More rows than one launch holds (batches of 16), then calls of other
+    shapes reusing the same scratch: its counters must return to zero."""
+    logits = S.activations(S.derive(S.BASE_SEED, "topk-batches"), 37, 5000) * 3.0
+    print("topk rows=37 n=5000", flush=True)
+    _check_rows(hip.topKHip(logits, 40), logits, 40, oracle)
+    small = logits[:3, :1500].copy()
+    _check_rows(hip.topKHip(small, 7), small, 7, oracle)
+    _check_rows(hip.topKHip(logits, 40), logits, 40, oracle)
+
+
 def test_topk_softcap(hip, oracle):
     logits = S.activations(S.derive(S.BASE_SEED, "softcap"), 2, 65536) * 20.0
     _check_rows(hip.topKHip(logits, 40, softcap=30.0), logits, 40, oracle, softcap=30.0)
