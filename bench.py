@@ -88,6 +88,8 @@ def parse() -> argparse.Namespace:
     p.add_argument("--rotate-mib", type=int, default=640, help="distinct weight bytes cycled through")
     p.add_argument("--cpu-seconds", type=float, default=12.0)
     p.add_argument("--no-cpu", action="store_true")
+    p.add_argument("--kernel", choices=["auto", "valu", "mfma"], default="auto",
+                   help="matvec kernel: automatic choice, vector ALU, or matrix cores")
     p.add_argument("--copy-probe", action="store_true",
                    help="only run a plain 256 MiB device copy (HBM counter calibration) and exit")
     return p.parse_args()
@@ -155,6 +157,7 @@ def main() -> int:
     support = H.checkHipSupport()
     if not support["available"]:
         raise SystemExit(f"HIP runner unavailable: {support}")
+    H.setMatvecKernel({"auto": H.MATVEC_AUTO, "valu": H.MATVEC_VALU, "mfma": H.MATVEC_MFMA}[args.kernel])
     torch.cuda.init()
     dev = torch.device("cuda:0")
     wl, m = args.workload, args.m
@@ -275,6 +278,8 @@ def main() -> int:
         cpu = cpu_baseline(wl, ws, x_host, args.cpu_seconds)
 
     kernels = {"ffn": "matvec + geglu + matvec", "head": "matvec + top-k"}
+    tiles16 = sum((r + 15) // 16 for _, r in specs)
+    uses_mfma = args.kernel == "mfma" or (args.kernel == "auto" and k <= 2560 and (m >= 5 or (m >= 2 and tiles16 >= 1024)))
     line = {
         "metric": METRIC,
         "value": round(value, 2),
@@ -305,7 +310,7 @@ def main() -> int:
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBPS, 4),
             "traffic": traffic,
-            "kernel": kernels.get(wl, f"kquant_matvec_kernel<{min(m, 8)}>"),
+            "kernel": kernels.get(wl, "kquant_mfma_kernel" if uses_mfma else f"kquant_matvec_kernel<{min(m, 8)}>"),
             "kernel_avg_us": round(kern_us, 3),
             "kernel_avg_us_mall_hot": round(hot_us, 3),
         },

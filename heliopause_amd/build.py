@@ -17,7 +17,7 @@ PKG = Path(__file__).resolve().parent
 CSRC = PKG / "csrc"
 BUILD = PKG / "_build"
 LIB = PKG / "libhp_hip.so"
-SOURCES = ["q8k.hip", "kquant_matvec.hip", "repack.hip", "topk.hip", "geglu.hip", "capi.hip"]
+SOURCES = ["q8k.hip", "kquant_matvec.hip", "kquant_mfma.hip", "repack.hip", "topk.hip", "geglu.hip", "capi.hip"]
 
 HIPCC = os.environ.get("HIPCC", shutil.which("hipcc") or "/opt/rocm/bin/hipcc")
 ARCH = "gfx950"

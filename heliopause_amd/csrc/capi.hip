@@ -25,6 +25,8 @@ struct Handle {
   int tiles = 0;
   uint8_t *data = nullptr;     // tiles (+ Q6_K d plane at the end)
   uint16_t *dplane = nullptr;  // Q6_K only
+  uint8_t *segs = nullptr;     // matrix-core layout (16-row tile segments)
+  size_t seg_bytes = 0;
   uint32_t generation = 0;
   bool live = false;
 };
@@ -48,6 +50,7 @@ struct State {
   void *topk_scratch = nullptr, *topk_out = nullptr;  // selection scratch; ids + values
   size_t topk_scratch_cap = 0, topk_out_cap = 0;
   uint64_t matmul_calls = 0, launches = 0;
+  int matvec_kernel = 0;  // 0 auto, 1 vector ALU, 2 matrix cores
   bool profiling = false;
   ProfileSlot prof[HP_KERNEL_COUNT];
   std::vector<hipEvent_t> event_pool;
@@ -188,6 +191,23 @@ int cols_per_launch(const TileGeom &g, size_t max_lds) {
   return 0;
 }
 
+// Kernel choice.  The matrix-core kernel's cost barely grows with the column
+// count but each wave walks its 16-row tile block by block, so it needs many
+// tiles to hide memory latency; the vector-ALU kernel's cost grows with the
+// columns (and it spills registers beyond four).  Measured on MI355X: the
+// matrix cores win from five columns on, and from two columns on when the
+// launch has >= 1024 tiles (16 rows each); one column stays on the vector
+// ALU.  Both need their LDS (the columns' Q8_K for every block) to fit.
+bool use_mfma(size_t cols, int nb, int tiles16) {
+  const State &s = st();
+  const int forced = s.matvec_kernel;
+  const size_t lds = mfma_lds_bytes(cols < 8 ? (int)cols : 8, nb);
+  if (forced == 1 || lds > s.max_lds) return false;
+  if (forced == 2) return true;
+  if (cols < 2 || lds > 64 * 1024) return false;
+  return cols >= 5 || tiles16 >= 1024;
+}
+
 // One matvec launch per column chunk covering every weight (multi == one
 // launch, lib.rs:300-426); each launch quantises its columns in its prologue.
 int32_t run_matvec(size_t count, Handle *const *hs, const float *d_input, size_t input_size, size_t cols,
@@ -211,6 +231,31 @@ int32_t run_matvec(size_t count, Handle *const *hs, const float *d_input, size_t
     tiles += hs[i]->tiles;
   }
   a.total_tiles = tiles;
+  int tiles16 = 0;
+  for (size_t i = 0; i < count; i++) tiles16 += (int)((hs[i]->row_count + 15) / 16);
+  if (use_mfma(cols, g.nb, tiles16)) {
+    MfmaLaunch l{};
+    l.count = (int)count;
+    l.k = (int)input_size;
+    for (size_t i = 0; i < count; i++) {
+      l.seg[i] = hs[i]->segs;
+      l.type[i] = hs[i]->type;
+      l.rows[i] = (int)hs[i]->row_count;
+    }
+    for (size_t m0 = 0; m0 < cols; m0 += 8) {
+      const int c = (int)((cols - m0) < 8 ? (cols - m0) : 8);
+      l.x = d_input + m0 * input_size;
+      l.cols = c;
+      l.out_col0 = (int)m0;
+      for (size_t i = 0; i < count; i++) l.out[i] = d_outs[i];
+      hipEvent_t e1 = prof_begin(stream);
+      HP_HIP_TRY(launch_matvec_mfma(l, s.num_cus, stream));
+      prof_end(HP_KERNEL_MATVEC, e1, stream);
+      s.launches++;
+    }
+    s.matmul_calls++;
+    return HP_OK;
+  }
   const int chunk = cols_per_launch(g, s.max_lds);
   if (chunk <= 0) return fail(HP_ERR_SHAPE, "input_size too large for the matvec LDS budget");
   for (size_t m0 = 0; m0 < cols; m0 += (size_t)chunk) {
@@ -267,11 +312,22 @@ int32_t upload_common(int32_t type_id, const void *src, bool src_device, size_t 
     }
     raw = staging;
   }
-  hipError_t e = launch_repack(type_id, raw, (int)row_count, h.g, h.data, h.dplane, s.stream);
+  const int nb = (int)(input_size / kQK);
+  h.seg_bytes = mfma_segment_bytes(type_id, (int)row_count, nb);
+  hipError_t e = hipMalloc((void **)&h.segs, h.seg_bytes);
+  if (e != hipSuccess) {
+    h.segs = nullptr;
+    if (staging) (void)hipFree(staging);
+    (void)hipFree(h.data);
+    return fail(HP_ERR_OOM, "weight allocation failed");
+  }
+  e = launch_repack(type_id, raw, (int)row_count, h.g, h.data, h.dplane, s.stream);
+  if (e == hipSuccess) e = launch_repack_mfma(type_id, raw, (int)row_count, nb, h.segs, s.stream);
   if (e == hipSuccess) e = hipStreamSynchronize(s.stream);
   if (staging) (void)hipFree(staging);
   if (e != hipSuccess) {
     (void)hipFree(h.data);
+    (void)hipFree(h.segs);
     return hip_fail(e, "repack");
   }
   // reuse a free slot
@@ -379,6 +435,7 @@ int32_t hp_hip_shutdown(void) {
   for (auto &h : s.handles)
     if (h.live) {
       (void)hipFree(h.data);
+      (void)hipFree(h.segs);
       h.live = false;
     }
   if (s.io_in) (void)hipFree(s.io_in);
@@ -421,7 +478,9 @@ int32_t hp_hip_weight_release(uint64_t handle) {
   if (!h) return fail(HP_ERR_HANDLE, "unknown weight handle");
   (void)hipStreamSynchronize(s.stream);
   (void)hipFree(h->data);
+  (void)hipFree(h->segs);
   h->data = nullptr;
+  h->segs = nullptr;
   h->dplane = nullptr;
   h->live = false;
   return HP_OK;
@@ -674,6 +733,14 @@ int32_t hp_hip_quantize_q8_k(const float *input, size_t input_len, size_t input_
   return HP_OK;
 }
 
+int32_t hp_hip_set_matvec_kernel(int32_t which) {
+  State &s = st();
+  std::lock_guard<std::recursive_mutex> lock(s.mu);
+  if (which < 0 || which > 2) return fail(HP_ERR_ARG, "kernel selector must be 0, 1 or 2");
+  s.matvec_kernel = which;
+  return HP_OK;
+}
+
 int32_t hp_hip_stats(hp_hip_stats_t *out) {
   State &s = st();
   std::lock_guard<std::recursive_mutex> lock(s.mu);
@@ -682,7 +749,7 @@ int32_t hp_hip_stats(hp_hip_stats_t *out) {
   for (auto &h : s.handles)
     if (h.live) {
       r.handle_count++;
-      r.resident_bytes += h.byte_length;
+      r.resident_bytes += h.byte_length + h.seg_bytes;
     }
   r.scratch_bytes = s.io_in_cap + s.topk_scratch_cap + s.topk_out_cap;
   for (int i = 0; i < kMaxWeights; i++) r.scratch_bytes += s.io_out_cap[i];

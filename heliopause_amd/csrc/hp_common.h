@@ -93,6 +93,22 @@ constexpr int kTopkMaxRows = 16;
 hipError_t launch_topk(const float *logits, int rows, int n, int k, double cap, uint8_t *scratch, uint32_t *ids,
                        float *vals, hipStream_t s);
 size_t topk_scratch_bytes(int rows, int n, int k);
+// Matrix-core matvec (kquant_mfma.hip): weights in 16-row tile segments.
+struct MfmaLaunch {
+  const uint8_t *seg[kMaxWeights];
+  float *out[kMaxWeights];
+  int type[kMaxWeights];
+  int rows[kMaxWeights];
+  int count;
+  const float *x;  // f32 input of the launch's first column
+  int k;
+  int cols;        // 1..8 columns in this launch
+  int out_col0;
+};
+size_t mfma_segment_bytes(int type, int rows, int nb);
+size_t mfma_lds_bytes(int cols, int nb);
+hipError_t launch_repack_mfma(int type, const uint8_t *raw, int rows, int nb, uint8_t *segs, hipStream_t s);
+hipError_t launch_matvec_mfma(const MfmaLaunch &l, int num_cus, hipStream_t s);
 hipError_t launch_geglu(const float *gate, const float *up, size_t n, double c, float *out, int num_cus,
                         hipStream_t s);
 hipError_t launch_dequantize(int type, const uint8_t *tiles, const uint16_t *dplane, int rows,

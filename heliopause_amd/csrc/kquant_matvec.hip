@@ -329,10 +329,15 @@ __global__ __launch_bounds__(256) void kquant_matvec_kernel(const MatvecArgs a) 
     load_regs(cur, cx, 0, lane, nb);
   }
 
-  // prologue: Q8_K of this launch's columns into LDS, 16 lanes per block
   for (int q = grp; q < nq; q += wpg * 4) {
-    if (q != grp) load_x16(xv, a.x + (size_t)(q / nb) * a.k + (size_t)(q % nb) * kQK, i16);
+    const int qn = q + wpg * 4;
+    float xn[16];
+    if (qn < nq) load_x16(xn, a.x + (size_t)(qn / nb) * a.k + (size_t)(qn % nb) * kQK, i16);
     q8k_block16(xv, i16, xq + (size_t)q * kQ8BlockBytes, xd + q);
+    if (qn < nq) {
+#pragma unroll
+      for (int i = 0; i < 16; i++) xv[i] = xn[i];
+    }
   }
   __syncthreads();
 
@@ -435,7 +440,7 @@ static hipError_t launch_m(const MatvecArgs &a, int num_cus, hipStream_t s) {
   const int cap = num_cus * 8;
   if (grid > cap) grid = cap;
   size_t lds = matvec_lds_bytes(M, a.g, wpg);
-  hipLaunchKernelGGL((kquant_matvec_kernel<M, (M <= 4)>), dim3(grid), dim3(64 * wpg), lds, s, a);
+  hipLaunchKernelGGL((kquant_matvec_kernel<M, (M <= 3)>), dim3(grid), dim3(64 * wpg), lds, s, a);
   return hipGetLastError();
 }
 

@@ -1,0 +1,586 @@
+// kquant_mfma.hip -- Q4_K / Q6_K x Q8_K matvec on the gfx950 matrix cores,
+// bit-exact with the reference's WASM path (the numerics are those of
+// kquant_matvec.hip: packages/engine/wasm-kernels/src/lib.rs:2116-2172,
+// 1923-1968, 300-426).
+//
+// Why matrix cores for a bandwidth-bound matvec: exact parity needs, per
+// (row, block, column), the eight integers aux32[l] = sum_g sc_g *
+// sum_{e in g, e = l mod 8} q_e * q8_e.  On the vector ALU that is a dot4 and
+// a multiply-add per four weights per column, so columns multiply the ALU
+// work.  Here the scales are folded into the weights: A = sc_g * q_e (Q4_K
+// <= 945, Q6_K |.| <= 1024) and B = q8 (|.| <= 128) are exact in f16, every
+// product and partial sum is an integer below 2^24 (|aux32| <= 4,194,304),
+// so v_mfma_f32_16x16x32_f16 accumulates them exactly in f32 and f32(aux32)
+// is the reference's value.  The vector ALU only unpacks the weights, once
+// for all columns.
+//
+// Lanes (v_mfma_f32_16x16x32_f16): A lane i = (row i%16, quarter q = i/16)
+// holds k = 8q..8q+7; B lane i = (column n = i%16, quarter q) the same k;
+// D lane i holds rows 4(i/16)+j (j = 0..3) of column n.
+// Columns n = m + 4s: m = input column of the set (4 per set), s = class
+// slot.  MFMA (g, u), g in {0,1}, u in {0..3}: quarter q carries lane class
+// l = 2q + g, elements (j = 2u, c = 0..3) then (j = 2u+1, c = 0..3) with
+// e = 32j + 8c + l; B is x_m of the same elements when q == s, else zero.
+// So D(g) of lane (rows, n) accumulates aux32 of class 2s + g: every
+// (row, column, class) chain lives in one lane, and the f32 tail runs in
+// registers in block order:
+//   d = dW_b * dX_b; sums[l] += d * f32(aux32[l]);
+//   Q4_K: sumf -= (dminW_b * dX_b) * f32(sumi)   (sumi by one more MFMA:
+//         mins x half-block sums of q8)
+//   result = [sumf +] ((((-0 + s0) + s1) + ...) + s7)
+//
+// Weight layout (repacked at upload, same byte count per 16-row tile; rows
+// past the weight in the last tile are zero): segment (tile T, block b) at
+// (b * tiles + T) * SEG, block-major, so the waves that stream block b of
+// neighbouring tiles at the same time read one contiguous range.
+//   Q4_K, SEG = 2304: [0,256) the 16 rows' first 16 GGUF bytes (d, dmin,
+//     packed scales/mins); [256,2304) chunk c in {0,1} x lane i: dword u of
+//     class 2q + c holds in byte cc: q(2u, cc) | q(2u+1, cc) << 4.
+//   Q6_K, SEG = 3360: [0,256) 16 rows x 16 int8 scales; [256,288) 16 f16 d;
+//     [288,3360) chunks 0,1 as Q4_K with the low 4 bits of q6; chunk 2
+//     dword 2*cls + h holds in byte cc the high 2 bits of q6 at
+//     (j = 4h + jj, cc, class 2q + cls) in bits 2jj.
+#include "hp_common.h"
+
+namespace hp {
+
+typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+typedef _Float16 half2v __attribute__((ext_vector_type(2)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+namespace {
+
+__device__ __forceinline__ float h2f_bits(uint32_t bits16) {
+  return (float)__builtin_bit_cast(_Float16, (uint16_t)bits16);
+}
+
+__device__ __forceinline__ uint32_t u4at(const uint4 &v, int i) {
+  return i == 0 ? v.x : i == 1 ? v.y : i == 2 ? v.z : v.w;
+}
+
+__device__ __forceinline__ half2v as_h2(uint32_t v) { return __builtin_bit_cast(half2v, v); }
+__device__ __forceinline__ uint32_t as_u32(half2v v) { return __builtin_bit_cast(uint32_t, v); }
+
+// Halves (1024 + byte a, 1024 + byte b) of dword v: the f16 with exponent
+// bits 0x64 and mantissa = the byte is exactly 1024 + byte (byte < 1024).
+template <uint32_t SEL>
+__device__ __forceinline__ half2v magic_pair(uint32_t v) {
+  return as_h2(__builtin_amdgcn_perm(0x64646464u, v, SEL));
+}
+constexpr uint32_t kSel01 = 0x04010400u;  // bytes 0, 1
+constexpr uint32_t kSel23 = 0x04030402u;  // bytes 2, 3
+
+// (s, s) for scale byte `idx` of dword v (unsigned bytes) and the matching
+// addend -off * s, both exact in f16: fma((1024 + q), s, -off * s) = s * (q + 1024 - off).
+__device__ __forceinline__ half2v dup_byte(uint32_t v, int idx, float bias) {
+  const uint32_t sel = (uint32_t)idx | 0x04000400u | ((uint32_t)idx << 16);
+  const half2v h = as_h2(__builtin_amdgcn_perm(0x64646464u, v, sel));
+  return h - (half2v){(_Float16)bias, (_Float16)bias};
+}
+
+__device__ __forceinline__ half2v fma2(half2v a, half2v b, half2v c) { return __builtin_elementwise_fma(a, b, c); }
+
+struct MfmaWeight {
+  const uint8_t *seg;  // segments of this weight
+  float *out;
+  int type, rows, tiles, tile_begin;
+};
+
+struct MfmaArgs {
+  MfmaWeight w[kMaxWeights];
+  int count;
+  int total_tiles;
+  int nb;
+  const float *x;  // f32 input of the launch's first column, [cols][k]
+  int k;
+  int cols;        // columns of this launch (<= 8)
+  int out_col0;
+};
+
+// LDS layout (bytes): xh [M4][nb][8 classes][32] f16; bs16 [M4][nb][16] f16;
+// dx [M4][nb] f32; 16 zero bytes; per wave fin [16 rows][16 n][2] f32 and
+// finf [16 rows][4] f32.
+struct Lds {
+  _Float16 *xh, *bs;
+  float *dx;
+  uint8_t *zero;
+  float *fin, *finf;
+};
+
+constexpr int kFinFloats = 16 * 16 * 2 + 16 * 4;
+
+__device__ __forceinline__ Lds lds_layout(uint8_t *smem, int m4, int nb, int wave) {
+  Lds L;
+  L.xh = reinterpret_cast<_Float16 *>(smem);
+  L.bs = L.xh + (size_t)m4 * nb * 256;
+  L.dx = reinterpret_cast<float *>(L.bs + (size_t)m4 * nb * 16);
+  L.zero = reinterpret_cast<uint8_t *>(L.dx + (size_t)m4 * nb);
+  L.fin = reinterpret_cast<float *>(L.zero + 16) + (size_t)wave * kFinFloats;
+  L.finf = L.fin + 16 * 16 * 2;
+  return L;
+}
+
+// Q8_K of block (m, b) by one 16-lane DPP row (lib.rs:1774-1811), written as
+// f16 for the B operand.  Lane i16 = 2j + u owns elements 32j + 8c + 4u + i
+// (c, i = 0..3): class l = 4u + i, t = 4j + c, stored at xh[m][b][l][t].
+template <int CTRL>
+__device__ __forceinline__ float dppf_(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xf, 0xf, false));
+}
+template <int CTRL>
+__device__ __forceinline__ int dppi_(int v) {
+  return __builtin_amdgcn_update_dpp(0, v, CTRL, 0xf, 0xf, false);
+}
+template <int CTRL>
+__device__ __forceinline__ void lexmax_(float &amax, float &vmax, int &idx) {
+  const float oa = dppf_<CTRL>(amax);
+  const float ov = dppf_<CTRL>(vmax);
+  const int oi = dppi_<CTRL>(idx);
+  const bool take = oa > amax || (oa == amax && oi < idx);
+  amax = take ? oa : amax;
+  vmax = take ? ov : vmax;
+  idx = take ? oi : idx;
+}
+
+__device__ __forceinline__ void load_x16_(float (&v)[16], const float *__restrict__ xb, int i16) {
+  const int j = i16 >> 1, u = i16 & 1;
+#pragma unroll
+  for (int c = 0; c < 4; c++) {
+    const float4 f = *reinterpret_cast<const float4 *>(xb + 32 * j + 8 * c + 4 * u);
+    v[4 * c] = f.x;
+    v[4 * c + 1] = f.y;
+    v[4 * c + 2] = f.z;
+    v[4 * c + 3] = f.w;
+  }
+}
+
+__device__ __forceinline__ void q8k_block16_f16(const float (&v)[16], int i16, const Lds &L, int m, int b, int nb) {
+  const int j = i16 >> 1, u = i16 & 1;
+  float amax = 0.0f, vmax = 0.0f;
+  int idx = 0x7fffffff;
+#pragma unroll
+  for (int c = 0; c < 4; c++)
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      const float x = v[4 * c + i];
+      const float av = fabsf(x);
+      const bool gt = av > amax;  // strictly greater: the first maximum wins
+      amax = gt ? av : amax;
+      vmax = gt ? x : vmax;
+      idx = gt ? 32 * j + 8 * c + 4 * u + i : idx;
+    }
+  lexmax_<0xB1>(amax, vmax, idx);   // quad_perm [1,0,3,2]
+  lexmax_<0x4E>(amax, vmax, idx);   // quad_perm [2,3,0,1]
+  lexmax_<0x141>(amax, vmax, idx);  // row_half_mirror
+  lexmax_<0x140>(amax, vmax, idx);  // row_mirror
+  const bool nz = amax != 0.0f;
+  const float inv = __fdiv_rn(-127.0f, vmax);
+  int sum = 0;
+  _Float16 *xb = L.xh + ((size_t)m * nb + b) * 256;
+#pragma unroll
+  for (int i = 0; i < 4; i++) {
+    half2v p0, p1;
+    int qv[4];
+#pragma unroll
+    for (int c = 0; c < 4; c++) {
+      // Rust: (is * x).round().min(127.0) as i8 (saturating)
+      const float r = fmaxf(fminf(roundf(__fmul_rn(inv, v[4 * c + i])), 127.0f), -128.0f);
+      qv[c] = nz ? (int)r : 0;
+      sum += qv[c];
+    }
+    p0 = (half2v){(_Float16)qv[0], (_Float16)qv[1]};
+    p1 = (half2v){(_Float16)qv[2], (_Float16)qv[3]};
+    const int l = 4 * u + i;
+    *reinterpret_cast<uint2 *>(xb + l * 32 + 4 * j) = make_uint2(as_u32(p0), as_u32(p1));
+  }
+  L.bs[((size_t)m * nb + b) * 16 + i16] = (_Float16)sum;  // |sum| <= 2048: exact
+  if (i16 == 0) L.dx[(size_t)m * nb + b] = nz ? __fdiv_rn(1.0f, inv) : 0.0f;
+}
+
+__device__ __forceinline__ f32x4 mfma(half8 a, half8 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+}
+
+__device__ __forceinline__ half8 cat(half2v a, half2v b, half2v c, half2v d) {
+  return (half8){a[0], a[1], b[0], b[1], c[0], c[1], d[0], d[1]};
+}
+
+__device__ __forceinline__ half8 lds_h8(const void *p) {
+  return __builtin_bit_cast(half8, *reinterpret_cast<const uint4 *>(p));
+}
+
+// Raw loads of one (tile, block) segment for lane i.
+// (every field is always set: the double buffer is copied as a whole and
+// must stay in registers)
+struct SegRegs {
+  uint4 hdr;    // Q4_K: row header (d | dmin, 12 scale bytes); Q6_K: 16 scales
+  uint4 c0, c1, c2;
+  uint4 d6;     // .x: Q6_K f16 d of row i%16
+};
+
+__device__ __forceinline__ SegRegs load_seg(const uint8_t *seg, bool q4, int lane) {
+  const int rho = lane & 15;
+  SegRegs r;
+  r.hdr = *reinterpret_cast<const uint4 *>(seg + 16 * rho);
+  r.c2 = make_uint4(0, 0, 0, 0);
+  r.d6 = make_uint4(0, 0, 0, 0);
+  if (q4) {
+    r.c0 = *reinterpret_cast<const uint4 *>(seg + 256 + 16 * lane);
+    r.c1 = *reinterpret_cast<const uint4 *>(seg + 256 + 1024 + 16 * lane);
+  } else {
+    r.d6.x = *reinterpret_cast<const uint16_t *>(seg + 256 + 2 * rho);
+    r.c0 = *reinterpret_cast<const uint4 *>(seg + 288 + 16 * lane);
+    r.c1 = *reinterpret_cast<const uint4 *>(seg + 288 + 1024 + 16 * lane);
+    r.c2 = *reinterpret_cast<const uint4 *>(seg + 288 + 2048 + 16 * lane);
+  }
+  return r;
+}
+
+// A operands of one block: a[g][u] for MFMA (g, u); Q4_K also amin (mins).
+// Also returns this lane's (D layout) row d / dmin via ds_bpermute.
+struct BlockOps {
+  half8 a[2][4];
+  half8 amin;
+  float dw[4], dmw[4];
+};
+
+__device__ __forceinline__ void build_q4k(BlockOps &o, const SegRegs &r, int lane) {
+  const int q = lane >> 4;
+  const uint32_t s0 = r.hdr.y, s1 = r.hdr.z, s2 = r.hdr.w;
+  // scale bytes sc0..3 | sc4..7 and mins mn0..3 | mn4..7 (6-bit, one per byte)
+  const uint32_t sclo = s0 & 0x3F3F3F3Fu;
+  const uint32_t schi = (s2 & 0x0F0F0F0Fu) | ((s0 >> 2) & 0x30303030u);
+  const uint32_t mnlo = s1 & 0x3F3F3F3Fu;
+  const uint32_t mnhi = ((s2 >> 4) & 0x0F0F0F0Fu) | ((s1 >> 2) & 0x30303030u);
+  half2v S[8], N[8];
+#pragma unroll
+  for (int j = 0; j < 8; j++) {
+    S[j] = dup_byte(j < 4 ? sclo : schi, j & 3, 1024.0f);  // (sc_j, sc_j)
+    N[j] = S[j] * (half2v){(_Float16)-1024.0f, (_Float16)-1024.0f};
+  }
+#pragma unroll
+  for (int g = 0; g < 2; g++) {
+    const uint4 ch = g ? r.c1 : r.c0;
+#pragma unroll
+    for (int u = 0; u < 4; u++) {
+      const uint32_t dw = u4at(ch, u);
+      const uint32_t lo = dw & 0x0F0F0F0Fu, hi = (dw >> 4) & 0x0F0F0F0Fu;
+      o.a[g][u] = cat(fma2(magic_pair<kSel01>(lo), S[2 * u], N[2 * u]), fma2(magic_pair<kSel23>(lo), S[2 * u], N[2 * u]),
+                      fma2(magic_pair<kSel01>(hi), S[2 * u + 1], N[2 * u + 1]),
+                      fma2(magic_pair<kSel23>(hi), S[2 * u + 1], N[2 * u + 1]));
+    }
+  }
+  // mins: quarter q < 2 carries k = 8q + e -> (j = 4q + e/2, half e%2)
+  const uint32_t mn = q == 0 ? mnlo : mnhi;
+  half2v M[4];
+#pragma unroll
+  for (int e = 0; e < 4; e++) M[e] = dup_byte(mn, e, 1024.0f);
+  const half8 am = cat(M[0], M[1], M[2], M[3]);
+  o.amin = q < 2 ? am : (half8){0, 0, 0, 0, 0, 0, 0, 0};
+  const int src = ((lane >> 4) * 4) << 2;  // lane of row 4(i/16)+j is that row index
+#pragma unroll
+  for (int j = 0; j < 4; j++) {
+    const uint32_t v = (uint32_t)__builtin_amdgcn_ds_bpermute(src + 4 * j, (int)r.hdr.x);
+    o.dw[j] = h2f_bits(v & 0xFFFFu);
+    o.dmw[j] = h2f_bits(v >> 16);
+  }
+}
+
+__device__ __forceinline__ void build_q6k(BlockOps &o, const SegRegs &r, int lane) {
+  // signed scales: bytes ^ 0x80 are s + 128; (1024 + 128 + s) - 1152 = s
+  const uint4 sb = make_uint4(r.hdr.x ^ 0x80808080u, r.hdr.y ^ 0x80808080u, r.hdr.z ^ 0x80808080u,
+                              r.hdr.w ^ 0x80808080u);
+#pragma unroll
+  for (int u = 0; u < 4; u++) {
+    // groups 4u, 4u+1 (j = 2u; c = 0,1 | c = 2,3) and 4u+2, 4u+3 (j = 2u+1)
+    const uint32_t gs = u4at(sb, u);
+    half2v S[4], N[4];
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+      S[e] = dup_byte(gs, e, 1152.0f);
+      N[e] = S[e] * (half2v){(_Float16)-1056.0f, (_Float16)-1056.0f};  // -(1024 + 32) * sc
+    }
+    const int jj = 2 * (u & 1);
+#pragma unroll
+    for (int g = 0; g < 2; g++) {
+      const uint32_t ql = u4at(g ? r.c1 : r.c0, u);
+      const uint32_t qh = u4at(r.c2, 2 * g + (u >> 1));
+      const uint32_t lo = (ql & 0x0F0F0F0Fu) | (((qh >> (2 * jj)) & 0x03030303u) << 4);
+      const uint32_t hi = ((ql >> 4) & 0x0F0F0F0Fu) | (((qh >> (2 * jj + 2)) & 0x03030303u) << 4);
+      o.a[g][u] = cat(fma2(magic_pair<kSel01>(lo), S[0], N[0]), fma2(magic_pair<kSel23>(lo), S[1], N[1]),
+                      fma2(magic_pair<kSel01>(hi), S[2], N[2]), fma2(magic_pair<kSel23>(hi), S[3], N[3]));
+    }
+  }
+  const int src = ((lane >> 4) * 4) << 2;
+#pragma unroll
+  for (int j = 0; j < 4; j++) {
+    const uint32_t v = (uint32_t)__builtin_amdgcn_ds_bpermute(src + 4 * j, (int)r.d6.x);
+    o.dw[j] = h2f_bits(v & 0xFFFFu);
+    o.dmw[j] = 0.0f;
+  }
+}
+
+struct Chains {
+  float s[2][4];  // class 2s+g chains of rows 4(i/16)+j
+  float f[4];     // Q4_K sumf of rows 4(i/16)+j (valid in lanes n < 4)
+};
+
+template <int NSET, bool Q4>
+__device__ __forceinline__ void block_step(Chains (&ch)[NSET], const BlockOps &o, const Lds &L, int b, int nb,
+                                           int lane) {
+  const int n = lane & 15, q = lane >> 4;
+  const int s = n >> 2;
+#pragma unroll
+  for (int st = 0; st < NSET; st++) {
+    const int m = 4 * st + (n & 3);
+    const _Float16 *xm = L.xh + ((size_t)m * nb + b) * 256;
+    f32x4 acc[2];
+#pragma unroll
+    for (int g = 0; g < 2; g++) {
+      acc[g] = (f32x4){0.0f, 0.0f, 0.0f, 0.0f};
+      const _Float16 *xc = xm + (2 * q + g) * 32;
+#pragma unroll
+      for (int u = 0; u < 4; u++) {
+        const half8 bf = lds_h8(q == s ? (const void *)(xc + 8 * u) : (const void *)L.zero);
+        acc[g] = mfma(o.a[g][u], bf, acc[g]);
+      }
+    }
+    const float dx = L.dx[(size_t)m * nb + b];
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+      const float dd = __fmul_rn(o.dw[j], dx);
+#pragma unroll
+      for (int g = 0; g < 2; g++) ch[st].s[g][j] = __fadd_rn(ch[st].s[g][j], __fmul_rn(dd, acc[g][j]));
+    }
+    if (Q4) {
+      const half8 bm = lds_h8(q < 2 && s == 0 ? (const void *)(L.bs + ((size_t)m * nb + b) * 16 + 8 * q)
+                                              : (const void *)L.zero);
+      const f32x4 am = mfma(o.amin, bm, (f32x4){0.0f, 0.0f, 0.0f, 0.0f});
+#pragma unroll
+      for (int j = 0; j < 4; j++) {
+        const float dm = __fmul_rn(o.dmw[j], dx);
+        ch[st].f[j] = __fsub_rn(ch[st].f[j], __fmul_rn(dm, am[j]));
+      }
+    }
+  }
+}
+
+template <int NSET>
+__device__ __forceinline__ void process_block(Chains (&ch)[NSET], const SegRegs &r, bool q4, const Lds &L, int b,
+                                              int nb, int lane) {
+  BlockOps o;
+  if (q4) {
+    build_q4k(o, r, lane);
+    block_step<NSET, true>(ch, o, L, b, nb, lane);
+  } else {
+    build_q6k(o, r, lane);
+    block_step<NSET, false>(ch, o, L, b, nb, lane);
+  }
+}
+
+// result(row, m) = [sumf +] ((((-0 + s0) + s1) + ...) + s7); chains of class
+// l = 2s + g of (row 4G + j, m) sit in lane 16G + m + 4s, group g, register j.
+template <int NSET>
+__device__ __forceinline__ void finish_tile(const Chains (&ch)[NSET], const Lds &L, int lane, bool q4,
+                                            float *out, int rows, int row0, int out_col0, int cols) {
+  const int n = lane & 15, G = lane >> 4;
+#pragma unroll
+  for (int st = 0; st < NSET; st++) {
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+      L.fin[((4 * G + j) * 16 + n) * 2 + 0] = ch[st].s[0][j];
+      L.fin[((4 * G + j) * 16 + n) * 2 + 1] = ch[st].s[1][j];
+      if (n < 4) L.finf[(4 * G + j) * 4 + n] = ch[st].f[j];
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    const int rho = lane >> 2, m4 = lane & 3;
+    float tot = -0.0f;
+#pragma unroll
+    for (int l = 0; l < 8; l++) tot = __fadd_rn(tot, L.fin[(rho * 16 + m4 + 4 * (l >> 1)) * 2 + (l & 1)]);
+    if (q4) tot = __fadd_rn(L.finf[rho * 4 + m4], tot);
+    const int m = 4 * st + m4;
+    if (row0 + rho < rows && m < cols) out[(size_t)(out_col0 + m) * rows + row0 + rho] = tot;
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  }
+}
+
+template <int NSET>
+__global__ __launch_bounds__(256) void kquant_mfma_kernel(const MfmaArgs a) {
+  extern __shared__ __align__(16) uint8_t smem[];
+  const int nb = a.nb;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const Lds L = lds_layout(smem, 4 * NSET, nb, wave);
+
+  // prologue: Q8_K of the launch's columns (f16 B layout), 16 lanes per
+  // block; columns past `cols` are zero
+  const int grp = wave * 4 + (lane >> 4), i16 = lane & 15;
+  const int nq = 4 * NSET * nb;
+  if (threadIdx.x < 4) reinterpret_cast<uint32_t *>(L.zero)[threadIdx.x] = 0;
+  for (int qb = grp; qb < nq; qb += 16) {
+    const int m = qb / nb, b = qb - m * nb;
+    if (m < a.cols) {
+      float xv[16];
+      load_x16_(xv, a.x + (size_t)m * a.k + (size_t)b * kQK, i16);
+      q8k_block16_f16(xv, i16, L, m, b, nb);
+    } else {
+      _Float16 *xb = L.xh + ((size_t)m * nb + b) * 256;
+      *reinterpret_cast<uint4 *>(xb + 16 * i16) = make_uint4(0, 0, 0, 0);
+      *reinterpret_cast<uint4 *>(xb + 16 * i16 + 8) = make_uint4(0, 0, 0, 0);
+      L.bs[((size_t)m * nb + b) * 16 + i16] = (_Float16)0.0f;
+      if (i16 == 0) L.dx[(size_t)m * nb + b] = 0.0f;
+    }
+  }
+  __syncthreads();
+
+  const int stride = gridDim.x * 4;
+  for (int t = blockIdx.x * 4 + wave; t < a.total_tiles; t += stride) {
+    MfmaWeight W = a.w[0];
+    if (a.count > 1 && t >= a.w[1].tile_begin) W = a.w[1];
+    if (a.count > 2 && t >= a.w[2].tile_begin) W = a.w[2];
+    if (a.count > 3 && t >= a.w[3].tile_begin) W = a.w[3];
+    const bool q4 = W.type == kTypeQ4K;
+    const int segb = q4 ? 2304 : 3360;
+    const int tt = t - W.tile_begin;
+    const uint8_t *seg = W.seg + (size_t)tt * segb;
+    const size_t bstride = (size_t)W.tiles * segb;  // next block of this tile
+    Chains ch[NSET];
+#pragma unroll
+    for (int st = 0; st < NSET; st++)
+#pragma unroll
+      for (int j = 0; j < 4; j++) {
+        ch[st].s[0][j] = 0.0f;
+        ch[st].s[1][j] = 0.0f;
+        ch[st].f[j] = 0.0f;
+      }
+    // ping-pong register buffers: block b + 1 loads while block b computes
+    SegRegs buf0 = load_seg(seg, q4, lane), buf1;
+    for (int b = 0; b < nb; b += 2) {
+      if (b + 1 < nb) buf1 = load_seg(seg + (size_t)(b + 1) * bstride, q4, lane);
+      process_block<NSET>(ch, buf0, q4, L, b, nb, lane);
+      if (b + 1 < nb) {
+        if (b + 2 < nb) buf0 = load_seg(seg + (size_t)(b + 2) * bstride, q4, lane);
+        process_block<NSET>(ch, buf1, q4, L, b + 1, nb, lane);
+      }
+    }
+    finish_tile<NSET>(ch, L, lane, q4, W.out, W.rows, 16 * tt, a.out_col0, a.cols);
+  }
+}
+
+// One thread per (tile, row-in-tile, block): copies / transposes one GGUF
+// block into the segment layout above (zeros for rows past the weight).
+__global__ void repack_mfma_kernel(const uint8_t *__restrict__ raw, int type, int rows, int nb,
+                                   uint8_t *__restrict__ segs) {
+  const long long tid = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+  const int tiles = (rows + 15) / 16;
+  if (tid >= (long long)tiles * 16 * nb) return;
+  const int b = (int)(tid % nb);
+  const int rho = (int)((tid / nb) % 16);
+  const int T = (int)(tid / ((long long)nb * 16));
+  const int r = T * 16 + rho;
+  const bool q4 = type == kTypeQ4K;
+  const int bb = q4 ? 144 : 210, segb = q4 ? 2304 : 3360;
+  uint8_t *seg = segs + ((size_t)b * tiles + T) * segb;
+  const uint8_t *blk = r < rows ? raw + ((size_t)r * nb + b) * bb : nullptr;
+  auto at = [&](int o) -> uint32_t { return blk ? blk[o] : 0u; };
+  if (q4) {
+    for (int o = 0; o < 16; o++) seg[16 * rho + o] = (uint8_t)at(o);
+    // element e = 32j + 8c + l: byte 16 + 32*(j/2) + 8c + l, nibble j%2
+    for (int qq = 0; qq < 4; qq++)
+      for (int c = 0; c < 2; c++) {
+        const int l = 2 * qq + c, i = qq * 16 + rho;
+        for (int u = 0; u < 4; u++)
+          for (int cc = 0; cc < 4; cc++) {
+            // j = 2u and 2u+1 share byte 16 + 32u + 8cc + l (low / high nibble)
+            seg[256 + (c * 64 + i) * 16 + 4 * u + cc] = (uint8_t)at(16 + 32 * u + 8 * cc + l);
+          }
+      }
+  } else {
+    for (int o = 0; o < 16; o++) seg[16 * rho + o] = (uint8_t)at(192 + o);
+    seg[256 + 2 * rho] = (uint8_t)at(208);
+    seg[256 + 2 * rho + 1] = (uint8_t)at(209);
+    // q6(e): e = 128h + 32t + l5 -> low nibble ql[64h + l5 + 32(t&1)] >> 4(t>>1),
+    // high 2 bits qh[32h + l5] >> 2t
+    auto q6 = [&](int e) -> uint32_t {
+      const int h = e >> 7, t5 = (e & 127) >> 5, l5 = e & 31;
+      const uint32_t lo = (at(64 * h + l5 + 32 * (t5 & 1)) >> (4 * (t5 >> 1))) & 15u;
+      const uint32_t hi = (at(128 + 32 * h + l5) >> (2 * t5)) & 3u;
+      return lo | (hi << 4);
+    };
+    for (int qq = 0; qq < 4; qq++) {
+      const int i = qq * 16 + rho;
+      for (int c = 0; c < 2; c++) {
+        const int l = 2 * qq + c;
+        for (int u = 0; u < 4; u++)
+          for (int cc = 0; cc < 4; cc++) {
+            const uint32_t v = (q6(32 * (2 * u) + 8 * cc + l) & 15u) | ((q6(32 * (2 * u + 1) + 8 * cc + l) & 15u) << 4);
+            seg[288 + (c * 64 + i) * 16 + 4 * u + cc] = (uint8_t)v;
+          }
+      }
+      for (int cls = 0; cls < 2; cls++) {
+        const int l = 2 * qq + cls;
+        for (int h = 0; h < 2; h++)
+          for (int cc = 0; cc < 4; cc++) {
+            uint32_t v = 0;
+            for (int jj = 0; jj < 4; jj++) v |= (q6(32 * (4 * h + jj) + 8 * cc + l) >> 4) << (2 * jj);
+            seg[288 + (2 * 64 + i) * 16 + 4 * (2 * cls + h) + cc] = (uint8_t)v;
+          }
+      }
+    }
+  }
+}
+
+}  // namespace
+
+size_t mfma_segment_bytes(int type, int rows, int nb) {
+  return (size_t)((rows + 15) / 16) * nb * (type == kTypeQ4K ? 2304 : 3360);
+}
+
+size_t mfma_lds_bytes(int cols, int nb) {
+  const int m4 = cols <= 4 ? 4 : 8;
+  return (size_t)m4 * nb * (512 + 32 + 4) + 16 + 4 * kFinFloats * 4;
+}
+
+hipError_t launch_repack_mfma(int type, const uint8_t *raw, int rows, int nb, uint8_t *segs, hipStream_t s) {
+  const long long n = (long long)((rows + 15) / 16) * 16 * nb;
+  const int threads = 256;
+  hipLaunchKernelGGL(repack_mfma_kernel, dim3((unsigned)((n + threads - 1) / threads)), dim3(threads), 0, s, raw,
+                     type, rows, nb, segs);
+  return hipGetLastError();
+}
+
+hipError_t launch_matvec_mfma(const MfmaLaunch &l, int num_cus, hipStream_t s) {
+  if (l.cols < 1 || l.cols > 8 || l.count < 1 || l.count > kMaxWeights) return hipErrorInvalidValue;
+  MfmaArgs a{};
+  a.count = l.count;
+  int tiles = 0;
+  for (int i = 0; i < l.count; i++) {
+    a.w[i].seg = l.seg[i];
+    a.w[i].out = l.out[i];
+    a.w[i].type = l.type[i];
+    a.w[i].rows = l.rows[i];
+    a.w[i].tiles = (l.rows[i] + 15) / 16;
+    a.w[i].tile_begin = tiles;
+    tiles += a.w[i].tiles;
+  }
+  a.total_tiles = tiles;
+  a.nb = l.k / kQK;
+  a.x = l.x;
+  a.k = l.k;
+  a.cols = l.cols;
+  a.out_col0 = l.out_col0;
+  int grid = (tiles + 3) / 4;
+  if (grid > num_cus * 8) grid = num_cus * 8;
+  const size_t lds = mfma_lds_bytes(l.cols, a.nb);
+  if (l.cols <= 4)
+    hipLaunchKernelGGL(kquant_mfma_kernel<1>, dim3(grid), dim3(256), lds, s, a);
+  else
+    hipLaunchKernelGGL(kquant_mfma_kernel<2>, dim3(grid), dim3(256), lds, s, a);
+  return hipGetLastError();
+}
+
+}  // namespace hp

@@ -103,8 +103,10 @@ def _declare(L: ctypes.CDLL) -> None:
 
 
 def _declare_optional(L: ctypes.CDLL) -> None:
-    """Top-k and GeGLU entry points."""
+    """Top-k, GeGLU and tuning entry points."""
     i32 = ctypes.c_int32
+    L.hp_hip_set_matvec_kernel.argtypes = [i32]
+    L.hp_hip_set_matvec_kernel.restype = i32
     vp = ctypes.c_void_p
     L.hp_hip_matmul_topk.argtypes = [_u64, vp, _sz, _sz, _sz, _sz, ctypes.c_double, vp, vp, _sz]
     L.hp_hip_topk.argtypes = [vp, _sz, _sz, _sz, ctypes.c_double, vp, vp, _sz]
@@ -355,6 +357,15 @@ def matmul_multi_device(handles: Sequence[int], d_input: int, input_size: int, c
     code = lib().hp_hip_matmul_multi_device(n, hs, d_input, input_size * column_count, input_size, column_count,
                                             optr, olen, stream or None)
     assertHipOk(code, "matmulMultiDevice")
+
+
+MATVEC_AUTO, MATVEC_VALU, MATVEC_MFMA = 0, 1, 2
+
+
+def setMatvecKernel(which: int) -> None:
+    """Select the matvec kernel (0 automatic, 1 vector ALU, 2 matrix cores);
+    both are bit-exact, only speed differs.  No counterpart in the reference."""
+    assertHipOk(lib().hp_hip_set_matvec_kernel(int(which)), "setMatvecKernel")
 
 
 def profile(enable: bool) -> None:

@@ -152,6 +152,13 @@ int32_t hp_hip_dequantize(uint64_t handle, size_t row_start, size_t row_count, f
 int32_t hp_hip_quantize_q8_k(const float *input, size_t input_len, size_t input_size, size_t column_count,
                              int8_t *qs, float *d, int16_t *bsums32);
 
+/* Matvec kernel selection (no counterpart in the reference; a tuning and
+ * test hook): 0 = automatic (vector-ALU kernel for one column, matrix-core
+ * kernel for two or more when its LDS fits), 1 = always the vector-ALU
+ * kernel, 2 = the matrix-core kernel whenever its LDS fits the device.
+ * Both are bit-exact with the reference; only speed differs. */
+int32_t hp_hip_set_matvec_kernel(int32_t which);
+
 /* wasmResidentWeightStats (wasm-kernels.ts:586-591) plus call counters. */
 int32_t hp_hip_stats(hp_hip_stats_t *out);
 /* Wait for all work queued on the library stream. */

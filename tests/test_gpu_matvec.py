@@ -21,6 +21,14 @@ def _weights(type_name, seed, rows, k):
     return S.weight_blocks(type_name, seed, rows, k)
 
 
+@pytest.fixture(params=[1, 2], ids=["valu", "mfma"])
+def kernel(request, hip):
+    """Runs the test with the vector-ALU and with the matrix-core matvec."""
+    hip.setMatvecKernel(request.param)
+    yield request.param
+    hip.setMatvecKernel(0)
+
+
 @pytest.mark.parametrize("type_name", ["Q4_K", "Q6_K"])
 @pytest.mark.parametrize("rows,k", [(1, 256), (7, 2560), (100, 512), (13, 10240), (64, 2048)])
 def test_dequantize_bit_exact(hip, oracle, type_name, rows, k):
@@ -41,8 +49,8 @@ def test_dequantize_bit_exact(hip, oracle, type_name, rows, k):
 @pytest.mark.parametrize("type_name", ["Q4_K", "Q6_K"])
 @pytest.mark.parametrize("rows,k,m", [(1, 256, 1), (7, 2560, 1), (61, 2560, 3), (100, 512, 8), (13, 10240, 2),
                                       (64, 2048, 4), (5, 768, 11), (130, 2560, 5), (3, 4096, 1)])
-def test_matmul_bit_exact(hip, oracle, type_name, rows, k, m):
-    print(f"matmul {type_name} rows={rows} k={k} m={m}", flush=True)
+def test_matmul_bit_exact(hip, oracle, kernel, type_name, rows, k, m):
+    print(f"matmul kernel={kernel} {type_name} rows={rows} k={k} m={m}", flush=True)
     seed = S.derive(S.BASE_SEED, "mm", type_name, rows, k, m)
     w = _weights(type_name, seed, rows, k)
     x = S.activations(seed, m, k)
@@ -55,12 +63,12 @@ def test_matmul_bit_exact(hip, oracle, type_name, rows, k, m):
         hip.releaseHipQuantizedWeightHandle(h)
 
 
-def test_multi_mixed_types_bit_exact(hip, oracle):
+def test_multi_mixed_types_bit_exact(hip, oracle, kernel):
     """Q (Q4_K) + K (Q4_K) + V (Q6_K) in one launch sharing one Q8_K (lib.rs:300-426)."""
     k = 2560
     specs = [("Q4_K", 96), ("Q4_K", 40), ("Q6_K", 40)]
     for m in (1, 4):
-        print(f"multi m={m}", flush=True)
+        print(f"multi kernel={kernel} m={m}", flush=True)
         seed = S.derive(S.BASE_SEED, "multi", m)
         ws = [_weights(t, S.derive(seed, i), r, k) for i, (t, r) in enumerate(specs)]
         x = S.activations(seed, m, k)
@@ -78,7 +86,7 @@ def test_multi_mixed_types_bit_exact(hip, oracle):
                 hip.releaseHipQuantizedWeightHandle(h)
 
 
-def test_special_inputs(hip, oracle):
+def test_special_inputs(hip, oracle, kernel):
     """All-zero columns, first-index |x| ties, a huge spike and denormal-scale inputs."""
     k, rows = 2560, 37
     for type_name in ("Q4_K", "Q6_K"):

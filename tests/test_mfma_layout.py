@@ -1,0 +1,278 @@
+"""CPU model of the matrix-core weight layout and kernel (kquant_mfma.hip).
+
+Emulates, in numpy, the upload repack into 16-row tiles and every index the
+kernel uses: which bytes each lane loads, how it builds its f16 MFMA
+operands (scale x quant, exact integers), the v_mfma_f32_16x16x32_f16 lane
+layout (A: lane i holds row i%16, k = 8*(i//16)..+7; B: lane i holds
+column i%16, the same k; D: lane i holds rows 4*(i//16)+j, column i%16),
+and the f32 tail in block order.  Checks:
+  * the repack writes every byte of a tile segment exactly once and keeps
+    the weight's byte count per 16-row tile;
+  * the emulated MFMA accumulators equal the oracle's exact per-lane-class
+    integers (aux32, sumi: lib.rs:2116-2172, 1923-1968) and stay below 2^24,
+    where f16 x f16 products summed in f32 are exact;
+  * the emulated outputs equal the oracle's matmul bit for bit.
+"""
+import numpy as np
+import pytest
+
+from heliopause_amd import synthetic as S
+
+Q4K, Q6K = 1, 3
+SEG = {Q4K: 2304, Q6K: 3360}
+
+
+def elem(j, c, l):
+    """Element index of (sub-block j, position c, lane class l): 32j + 8c + l."""
+    return 32 * j + 8 * c + l
+
+
+def q4k_fields(blk):
+    s = blk[4:16].astype(np.int64)
+    sc, mn = [], []
+    for j in range(8):
+        if j < 4:
+            sc.append(s[j] & 63)
+            mn.append(s[j + 4] & 63)
+        else:
+            sc.append((s[j + 4] & 15) | ((s[j - 4] >> 6) << 4))
+            mn.append((s[j + 4] >> 4) | ((s[j] >> 6) << 4))
+    e = np.arange(256)
+    q = (blk[16 + 32 * (e // 64) + e % 32] >> (4 * ((e // 32) % 2))) & 15
+    return np.array(sc), np.array(mn), q.astype(np.int64)
+
+
+def q6k_fields(blk):
+    e = np.arange(256)
+    h, t, l = e // 128, (e % 128) // 32, e % 32
+    lo = (blk[64 * h + l + 32 * (t & 1)] >> (4 * (t >> 1))) & 15
+    hi = (blk[128 + 32 * h + l] >> (2 * t)) & 3
+    return (lo | (hi << 4)).astype(np.int64), blk[192:208].view(np.int8).astype(np.int64)
+
+
+def repack_mfma(type_id, raw, rows, k):
+    """Tile segments: (tile T, block b) at (b * tiles + T) * SEG (block-major).
+    Q4_K: [0,256) 16 row headers (GGUF bytes 0..15); [256, 2304) chunk c in
+      {0,1} x lane i (row i%16, quarter q = i//16): 16 bytes = dwords u = 0..3
+      of class l = 2q + c, byte cc of dword u = q(2u, cc, l) | q(2u+1, cc, l) << 4.
+    Q6_K: [0,256) 16 rows x 16 int8 scales; [256,288) 16 f16 d; [288, 3360)
+      chunk c in {0,1,2} x lane i: c < 2 as Q4_K with the low 4 bits of q6;
+      c = 2: dword 2*cls + h holds, in byte cc, the high 2 bits of q6 at
+      (j = 4h + jj, cc, class 2q + cls) in bits 2jj.
+    Rows past the weight in the last tile are zero."""
+    nb = k // 256
+    tiles = (rows + 15) // 16
+    out = np.zeros(tiles * nb * SEG[type_id], dtype=np.uint8)
+    written = np.zeros_like(out, dtype=np.int32)
+    blocks = raw.reshape(rows, nb, -1)
+    for T in range(tiles):
+        for b in range(nb):
+            base = (b * tiles + T) * SEG[type_id]
+            for rho in range(16):
+                r = T * 16 + rho
+                blk = blocks[r, b] if r < rows else None
+                if type_id == Q4K:
+                    hdr = blk[0:16] if blk is not None else np.zeros(16, np.uint8)
+                    out[base + 16 * rho: base + 16 * rho + 16] = hdr
+                    written[base + 16 * rho: base + 16 * rho + 16] += 1
+                    _, _, q = q4k_fields(blk) if blk is not None else (None, None, np.zeros(256, np.int64))
+                    for qq in range(4):
+                        i = qq * 16 + rho
+                        for c in range(2):
+                            l = 2 * qq + c
+                            for u in range(4):
+                                for cc in range(4):
+                                    v = q[elem(2 * u, cc, l)] | (q[elem(2 * u + 1, cc, l)] << 4)
+                                    off = base + 256 + (c * 64 + i) * 16 + 4 * u + cc
+                                    out[off] = v
+                                    written[off] += 1
+                else:
+                    if blk is not None:
+                        q6, sc = q6k_fields(blk)
+                        out[base + 16 * rho: base + 16 * rho + 16] = blk[192:208]
+                        out[base + 256 + 2 * rho: base + 258 + 2 * rho] = blk[208:210]
+                    else:
+                        q6 = np.zeros(256, np.int64)
+                    written[base + 16 * rho: base + 16 * rho + 16] += 1
+                    written[base + 256 + 2 * rho: base + 258 + 2 * rho] += 1
+                    for qq in range(4):
+                        i = qq * 16 + rho
+                        for c in range(2):
+                            l = 2 * qq + c
+                            for u in range(4):
+                                for cc in range(4):
+                                    v = (q6[elem(2 * u, cc, l)] & 15) | ((q6[elem(2 * u + 1, cc, l)] & 15) << 4)
+                                    off = base + 288 + (c * 64 + i) * 16 + 4 * u + cc
+                                    out[off] = v
+                                    written[off] += 1
+                        for cls in range(2):
+                            l = 2 * qq + cls
+                            for h in range(2):
+                                for cc in range(4):
+                                    v = 0
+                                    for jj in range(4):
+                                        v |= (q6[elem(4 * h + jj, cc, l)] >> 4) << (2 * jj)
+                                    off = base + 288 + (2 * 64 + i) * 16 + 4 * (2 * cls + h) + cc
+                                    out[off] = v
+                                    written[off] += 1
+    return out, written
+
+
+def lane_a_fragment(type_id, seg, i, g, u):
+    """f16 values (exact ints) lane i supplies as A of MFMA (group g, u):
+    class 2q+g, elements (j = 2u, c = 0..3) then (j = 2u+1, c = 0..3), each
+    times its group scale."""
+    rho, q = i % 16, i // 16
+    if type_id == Q4K:
+        hdr = seg[16 * rho: 16 * rho + 16]
+        blk = np.concatenate([hdr, np.zeros(128, np.uint8)])
+        sc, _, _ = q4k_fields(blk)
+        dw = seg[256 + (g * 64 + i) * 16 + 4 * u: 256 + (g * 64 + i) * 16 + 4 * u + 4]
+        lo = [int(x) & 15 for x in dw]
+        hi = [int(x) >> 4 for x in dw]
+        return [sc[2 * u] * v for v in lo] + [sc[2 * u + 1] * v for v in hi]
+    sc = seg[16 * rho: 16 * rho + 16].view(np.int8).astype(np.int64)
+    dw = seg[288 + (g * 64 + i) * 16 + 4 * u: 288 + (g * 64 + i) * 16 + 4 * u + 4]
+    h = u // 2
+    qh = seg[288 + (2 * 64 + i) * 16 + 4 * (2 * g + h): 288 + (2 * 64 + i) * 16 + 4 * (2 * g + h) + 4]
+    vals = []
+    for half, j in ((0, 2 * u), (1, 2 * u + 1)):
+        jj = j - 4 * h
+        for cc in range(4):
+            lo = (int(dw[cc]) >> (4 * half)) & 15
+            hi = (int(qh[cc]) >> (2 * jj)) & 3
+            grp = 2 * j + (cc >= 2)
+            vals.append(int(sc[grp]) * ((lo | (hi << 4)) - 32))
+    return vals
+
+
+def q8k(x):
+    from oracle import oracle as O
+    return O.quantize_q8_k(x)
+
+
+def emulate(type_id, seg_bytes, rows, k, x):
+    """Runs the kernel's arithmetic for all tiles; returns [M][rows] f32."""
+    nb = k // 256
+    m_cols = x.shape[0]
+    qs, dx, _ = q8k(x)
+    qs = qs.reshape(m_cols, nb, 256).astype(np.int64)
+    out = np.zeros((m_cols, rows), np.float32)
+    tiles = (rows + 15) // 16
+    nset = (m_cols + 3) // 4
+    for T in range(tiles):
+        sums = np.zeros((nset, 64, 2, 4), np.float32)   # [set][lane][g][j]
+        sumf = np.zeros((nset, 64, 4), np.float32)
+        for b in range(nb):
+            base = (b * tiles + T) * SEG[type_id]
+            seg = seg_bytes[base: base + SEG[type_id]]
+            for st in range(nset):
+                acc = np.zeros((2, 16, 16), np.int64)   # [g][row][n]
+                for g in range(2):
+                    for u in range(4):
+                        A = np.zeros((16, 32), np.int64)
+                        B = np.zeros((32, 16), np.int64)
+                        for i in range(64):
+                            a = lane_a_fragment(type_id, seg, i, g, u)
+                            A[i % 16, 8 * (i // 16): 8 * (i // 16) + 8] = a
+                            n, qq = i % 16, i // 16
+                            m, s = 4 * st + n % 4, n // 4
+                            if m < m_cols and qq == s:
+                                l = 2 * qq + g
+                                xs = [qs[m, b, elem(2 * u + (e >= 4), e % 4, l)] for e in range(8)]
+                                B[8 * qq: 8 * qq + 8, n] = xs
+                        assert np.abs(A).max() <= 2048 and np.abs(B).max() <= 2048  # exact in f16
+                        acc[g] += A @ B
+                        assert np.abs(acc[g]).max() < 2 ** 24
+                if type_id == Q4K:
+                    A = np.zeros((16, 32), np.int64)
+                    B = np.zeros((32, 16), np.int64)
+                    _, _, bs16 = bsums16(qs[:, b])
+                    for i in range(64):
+                        rho, qq = i % 16, i // 16
+                        if qq < 2:
+                            hdr = seg[16 * rho: 16 * rho + 16]
+                            _, mn, _ = q4k_fields(np.concatenate([hdr, np.zeros(128, np.uint8)]))
+                            A[rho, 8 * qq: 8 * qq + 8] = [mn[4 * qq + e // 2] for e in range(8)]
+                            n = i % 16
+                            m = 4 * st + n % 4
+                            if n < 4 and m < m_cols:
+                                B[8 * qq: 8 * qq + 8, n] = bs16[m, 8 * qq: 8 * qq + 8]
+                    accmin = A @ B
+                # tail: lane i holds rows 4*(i//16)+j, column n = i % 16
+                for i in range(64):
+                    n = i % 16
+                    m, s = 4 * st + n % 4, n // 4
+                    if m >= m_cols:
+                        continue
+                    for j in range(4):
+                        rho = 4 * (i // 16) + j
+                        r = T * 16 + rho
+                        if r >= rows:
+                            continue
+                        if type_id == Q4K:
+                            dw = np.frombuffer(seg[16 * rho: 16 * rho + 2].tobytes(), np.float16)[0]
+                            dmw = np.frombuffer(seg[16 * rho + 2: 16 * rho + 4].tobytes(), np.float16)[0]
+                        else:
+                            dw = np.frombuffer(seg[256 + 2 * rho: 258 + 2 * rho].tobytes(), np.float16)[0]
+                        dd = np.float32(np.float32(dw) * dx[m, b])
+                        for g in range(2):
+                            p = np.float32(dd * np.float32(acc[g][rho, n]))
+                            sums[st, i, g, j] = np.float32(sums[st, i, g, j] + p)
+                        if type_id == Q4K and s == 0:
+                            dm = np.float32(np.float32(dmw) * dx[m, b])
+                            sumf[st, i, j] = np.float32(sumf[st, i, j] - np.float32(dm * np.float32(accmin[rho, n])))
+        # final: s_l for class l = 2s + g lives in lane n = m%4 + 4s (row group), group g
+        for st in range(nset):
+            for m4 in range(4):
+                m = 4 * st + m4
+                if m >= m_cols:
+                    continue
+                for rho in range(16):
+                    r = T * 16 + rho
+                    if r >= rows:
+                        continue
+                    grp, j = rho // 4, rho % 4
+                    tot = np.float32(-0.0)
+                    for l in range(8):
+                        s, g = l // 2, l % 2
+                        tot = np.float32(tot + sums[st, 16 * grp + m4 + 4 * s, g, j])
+                    if type_id == Q4K:
+                        tot = np.float32(sumf[st, 16 * grp + m4, j] + tot)
+                    out[m, r] = tot
+    return out
+
+
+def bsums16(qs_b):
+    """Per column, sums of the 16 elements lane 2j+u of the Q8_K prologue
+    owns (32j + 8c + 4u + i, c, i = 0..3): halves of each bsums32."""
+    m_cols = qs_b.shape[0]
+    bs = np.zeros((m_cols, 16), np.int64)
+    for j in range(8):
+        for u in range(2):
+            idx = [32 * j + 8 * c + 4 * u + i for c in range(4) for i in range(4)]
+            bs[:, 2 * j + u] = qs_b[:, idx].sum(axis=1)
+    assert np.abs(bs).max() <= 2048
+    return None, None, bs
+
+
+@pytest.mark.parametrize("type_id", [Q4K, Q6K])
+def test_repack_writes_each_byte_once(type_id):
+    rows, k = 21, 512
+    raw = (S.q4_k_blocks if type_id == Q4K else S.q6_k_blocks)(3, rows, k)
+    out, written = repack_mfma(type_id, raw, rows, k)
+    assert (written == 1).all()
+    assert out.size == ((rows + 15) // 16) * (k // 256) * SEG[type_id]
+    assert SEG[type_id] == 16 * (144 if type_id == Q4K else 210)
+
+
+@pytest.mark.parametrize("type_id,rows,m_cols", [(Q4K, 18, 1), (Q4K, 16, 6), (Q6K, 19, 3), (Q6K, 16, 5)])
+def test_emulated_kernel_matches_oracle(oracle, type_id, rows, m_cols):
+    k = 512
+    raw = (S.q4_k_blocks if type_id == Q4K else S.q6_k_blocks)(rows + m_cols, rows, k)
+    x = S.activations(type_id * 100 + rows, m_cols, k)
+    x[0, 7] = -50.0
+    segs, _ = repack_mfma(type_id, raw, rows, k)
+    got = emulate(type_id, segs, rows, k, x)
+    want = oracle.matmul(type_id, raw, x, rows).reshape(m_cols, rows)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
