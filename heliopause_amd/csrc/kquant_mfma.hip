@@ -97,9 +97,12 @@ struct MfmaArgs {
   int out_col0;
 };
 
-// LDS layout (bytes): xh [M4][nb][8 classes][32] f16; bs16 [M4][nb][16] f16;
-// dx [M4][nb] f32; 16 zero bytes; per wave fin [16 rows][16 n][2] f32 and
-// finf [16 rows][4] f32.
+// LDS layout: xh [nb][M4] regions of kXRegion bytes, each 8 classes of
+// kXClass bytes (32 f16 + 16 bytes of padding); bs16 [nb][M4][16] f16;
+// dx [nb][M4] f32; 16 zero bytes; per wave fin [16 rows][16 n][2] f32 and
+// finf [16 rows][4] f32.  The padding makes the 16 B-operand reads of one
+// MFMA (4 columns x 4 class slots, 16 bytes each) use every 16-byte bank
+// slot exactly twice: slot = (2s + g) * 5 + m (mod 8).
 struct Lds {
   _Float16 *xh, *bs;
   float *dx;
@@ -108,12 +111,14 @@ struct Lds {
 };
 
 constexpr int kFinFloats = 16 * 16 * 2 + 16 * 4;
+constexpr int kXClass = 80;              // bytes per class: 64 + 16 padding
+constexpr int kXRegion = 8 * kXClass + 16;  // bytes per (block, column): 656 = 16 mod 128
 
 __device__ __forceinline__ Lds lds_layout(uint8_t *smem, int m4, int nb, int wave) {
   Lds L;
   L.xh = reinterpret_cast<_Float16 *>(smem);
-  L.bs = L.xh + (size_t)m4 * nb * 256;
-  L.dx = reinterpret_cast<float *>(L.bs + (size_t)m4 * nb * 16);
+  L.bs = reinterpret_cast<_Float16 *>(smem + (size_t)m4 * nb * kXRegion);
+  L.dx = reinterpret_cast<float *>(L.bs + (size_t)m4 * nb * 16);  // bs16: 32 bytes per (b, m)
   L.zero = reinterpret_cast<uint8_t *>(L.dx + (size_t)m4 * nb);
   L.fin = reinterpret_cast<float *>(L.zero + 16) + (size_t)wave * kFinFloats;
   L.finf = L.fin + 16 * 16 * 2;
@@ -142,6 +147,12 @@ __device__ __forceinline__ void lexmax_(float &amax, float &vmax, int &idx) {
   idx = take ? oi : idx;
 }
 
+// f16 x of class l of (block b, column m); element t at +t.
+__device__ __forceinline__ _Float16 *x_class(const Lds &L, int m4, int b, int m, int l) {
+  return reinterpret_cast<_Float16 *>(reinterpret_cast<uint8_t *>(L.xh) + ((size_t)b * m4 + m) * kXRegion +
+                                      l * kXClass);
+}
+
 __device__ __forceinline__ void load_x16_(float (&v)[16], const float *__restrict__ xb, int i16) {
   const int j = i16 >> 1, u = i16 & 1;
 #pragma unroll
@@ -154,7 +165,7 @@ __device__ __forceinline__ void load_x16_(float (&v)[16], const float *__restric
   }
 }
 
-__device__ __forceinline__ void q8k_block16_f16(const float (&v)[16], int i16, const Lds &L, int m, int b, int nb) {
+__device__ __forceinline__ void q8k_block16_f16(const float (&v)[16], int i16, const Lds &L, int m4, int m, int b) {
   const int j = i16 >> 1, u = i16 & 1;
   float amax = 0.0f, vmax = 0.0f;
   int idx = 0x7fffffff;
@@ -176,7 +187,6 @@ __device__ __forceinline__ void q8k_block16_f16(const float (&v)[16], int i16, c
   const bool nz = amax != 0.0f;
   const float inv = __fdiv_rn(-127.0f, vmax);
   int sum = 0;
-  _Float16 *xb = L.xh + ((size_t)m * nb + b) * 256;
 #pragma unroll
   for (int i = 0; i < 4; i++) {
     half2v p0, p1;
@@ -191,10 +201,10 @@ __device__ __forceinline__ void q8k_block16_f16(const float (&v)[16], int i16, c
     p0 = (half2v){(_Float16)qv[0], (_Float16)qv[1]};
     p1 = (half2v){(_Float16)qv[2], (_Float16)qv[3]};
     const int l = 4 * u + i;
-    *reinterpret_cast<uint2 *>(xb + l * 32 + 4 * j) = make_uint2(as_u32(p0), as_u32(p1));
+    *reinterpret_cast<uint2 *>(x_class(L, m4, b, m, l) + 4 * j) = make_uint2(as_u32(p0), as_u32(p1));
   }
-  L.bs[((size_t)m * nb + b) * 16 + i16] = (_Float16)sum;  // |sum| <= 2048: exact
-  if (i16 == 0) L.dx[(size_t)m * nb + b] = nz ? __fdiv_rn(1.0f, inv) : 0.0f;
+  L.bs[((size_t)b * m4 + m) * 16 + i16] = (_Float16)sum;  // |sum| <= 2048: exact
+  if (i16 == 0) L.dx[(size_t)b * m4 + m] = nz ? __fdiv_rn(1.0f, inv) : 0.0f;
 }
 
 __device__ __forceinline__ f32x4 mfma(half8 a, half8 b, f32x4 c) {
@@ -209,26 +219,32 @@ __device__ __forceinline__ half8 lds_h8(const void *p) {
   return __builtin_bit_cast(half8, *reinterpret_cast<const uint4 *>(p));
 }
 
-// Raw loads of one (tile, block) segment for lane i.
-// (every field is always set: the double buffer is copied as a whole and
-// must stay in registers)
-struct SegRegs {
-  uint4 hdr;    // Q4_K: row header (d | dmin, 12 scale bytes); Q6_K: 16 scales
+// Raw loads of one (tile, block) segment for lane i (per weight type, so a
+// Q4_K tile carries only its 12 registers).
+template <bool Q4>
+struct Seg;
+template <>
+struct Seg<true> {
+  uint4 hdr;  // row header: d | dmin, 12 packed scale/min bytes
+  uint4 c0, c1;
+};
+template <>
+struct Seg<false> {
+  uint4 hdr;  // 16 int8 scales of row i%16
   uint4 c0, c1, c2;
-  uint4 d6;     // .x: Q6_K f16 d of row i%16
+  uint32_t d;  // f16 d of row i%16
 };
 
-__device__ __forceinline__ SegRegs load_seg(const uint8_t *seg, bool q4, int lane) {
+template <bool Q4>
+__device__ __forceinline__ Seg<Q4> load_seg(const uint8_t *seg, int lane) {
   const int rho = lane & 15;
-  SegRegs r;
+  Seg<Q4> r;
   r.hdr = *reinterpret_cast<const uint4 *>(seg + 16 * rho);
-  r.c2 = make_uint4(0, 0, 0, 0);
-  r.d6 = make_uint4(0, 0, 0, 0);
-  if (q4) {
+  if constexpr (Q4) {
     r.c0 = *reinterpret_cast<const uint4 *>(seg + 256 + 16 * lane);
     r.c1 = *reinterpret_cast<const uint4 *>(seg + 256 + 1024 + 16 * lane);
   } else {
-    r.d6.x = *reinterpret_cast<const uint16_t *>(seg + 256 + 2 * rho);
+    r.d = *reinterpret_cast<const uint16_t *>(seg + 256 + 2 * rho);
     r.c0 = *reinterpret_cast<const uint4 *>(seg + 288 + 16 * lane);
     r.c1 = *reinterpret_cast<const uint4 *>(seg + 288 + 1024 + 16 * lane);
     r.c2 = *reinterpret_cast<const uint4 *>(seg + 288 + 2048 + 16 * lane);
@@ -236,145 +252,159 @@ __device__ __forceinline__ SegRegs load_seg(const uint8_t *seg, bool q4, int lan
   return r;
 }
 
-// A operands of one block: a[g][u] for MFMA (g, u); Q4_K also amin (mins).
-// Also returns this lane's (D layout) row d / dmin via ds_bpermute.
-struct BlockOps {
-  half8 a[2][4];
-  half8 amin;
-  float dw[4], dmw[4];
-};
-
-__device__ __forceinline__ void build_q4k(BlockOps &o, const SegRegs &r, int lane) {
-  const int q = lane >> 4;
-  const uint32_t s0 = r.hdr.y, s1 = r.hdr.z, s2 = r.hdr.w;
-  // scale bytes sc0..3 | sc4..7 and mins mn0..3 | mn4..7 (6-bit, one per byte)
-  const uint32_t sclo = s0 & 0x3F3F3F3Fu;
-  const uint32_t schi = (s2 & 0x0F0F0F0Fu) | ((s0 >> 2) & 0x30303030u);
-  const uint32_t mnlo = s1 & 0x3F3F3F3Fu;
-  const uint32_t mnhi = ((s2 >> 4) & 0x0F0F0F0Fu) | ((s1 >> 2) & 0x30303030u);
-  half2v S[8], N[8];
-#pragma unroll
-  for (int j = 0; j < 8; j++) {
-    S[j] = dup_byte(j < 4 ? sclo : schi, j & 3, 1024.0f);  // (sc_j, sc_j)
-    N[j] = S[j] * (half2v){(_Float16)-1024.0f, (_Float16)-1024.0f};
-  }
-#pragma unroll
-  for (int g = 0; g < 2; g++) {
-    const uint4 ch = g ? r.c1 : r.c0;
-#pragma unroll
-    for (int u = 0; u < 4; u++) {
-      const uint32_t dw = u4at(ch, u);
-      const uint32_t lo = dw & 0x0F0F0F0Fu, hi = (dw >> 4) & 0x0F0F0F0Fu;
-      o.a[g][u] = cat(fma2(magic_pair<kSel01>(lo), S[2 * u], N[2 * u]), fma2(magic_pair<kSel23>(lo), S[2 * u], N[2 * u]),
-                      fma2(magic_pair<kSel01>(hi), S[2 * u + 1], N[2 * u + 1]),
-                      fma2(magic_pair<kSel23>(hi), S[2 * u + 1], N[2 * u + 1]));
-    }
-  }
-  // mins: quarter q < 2 carries k = 8q + e -> (j = 4q + e/2, half e%2)
-  const uint32_t mn = q == 0 ? mnlo : mnhi;
-  half2v M[4];
-#pragma unroll
-  for (int e = 0; e < 4; e++) M[e] = dup_byte(mn, e, 1024.0f);
-  const half8 am = cat(M[0], M[1], M[2], M[3]);
-  o.amin = q < 2 ? am : (half8){0, 0, 0, 0, 0, 0, 0, 0};
-  const int src = ((lane >> 4) * 4) << 2;  // lane of row 4(i/16)+j is that row index
-#pragma unroll
-  for (int j = 0; j < 4; j++) {
-    const uint32_t v = (uint32_t)__builtin_amdgcn_ds_bpermute(src + 4 * j, (int)r.hdr.x);
-    o.dw[j] = h2f_bits(v & 0xFFFFu);
-    o.dmw[j] = h2f_bits(v >> 16);
-  }
-}
-
-__device__ __forceinline__ void build_q6k(BlockOps &o, const SegRegs &r, int lane) {
-  // signed scales: bytes ^ 0x80 are s + 128; (1024 + 128 + s) - 1152 = s
-  const uint4 sb = make_uint4(r.hdr.x ^ 0x80808080u, r.hdr.y ^ 0x80808080u, r.hdr.z ^ 0x80808080u,
-                              r.hdr.w ^ 0x80808080u);
-#pragma unroll
-  for (int u = 0; u < 4; u++) {
-    // groups 4u, 4u+1 (j = 2u; c = 0,1 | c = 2,3) and 4u+2, 4u+3 (j = 2u+1)
-    const uint32_t gs = u4at(sb, u);
-    half2v S[4], N[4];
-#pragma unroll
-    for (int e = 0; e < 4; e++) {
-      S[e] = dup_byte(gs, e, 1152.0f);
-      N[e] = S[e] * (half2v){(_Float16)-1056.0f, (_Float16)-1056.0f};  // -(1024 + 32) * sc
-    }
-    const int jj = 2 * (u & 1);
-#pragma unroll
-    for (int g = 0; g < 2; g++) {
-      const uint32_t ql = u4at(g ? r.c1 : r.c0, u);
-      const uint32_t qh = u4at(r.c2, 2 * g + (u >> 1));
-      const uint32_t lo = (ql & 0x0F0F0F0Fu) | (((qh >> (2 * jj)) & 0x03030303u) << 4);
-      const uint32_t hi = ((ql >> 4) & 0x0F0F0F0Fu) | (((qh >> (2 * jj + 2)) & 0x03030303u) << 4);
-      o.a[g][u] = cat(fma2(magic_pair<kSel01>(lo), S[0], N[0]), fma2(magic_pair<kSel23>(lo), S[1], N[1]),
-                      fma2(magic_pair<kSel01>(hi), S[2], N[2]), fma2(magic_pair<kSel23>(hi), S[3], N[3]));
-    }
-  }
-  const int src = ((lane >> 4) * 4) << 2;
-#pragma unroll
-  for (int j = 0; j < 4; j++) {
-    const uint32_t v = (uint32_t)__builtin_amdgcn_ds_bpermute(src + 4 * j, (int)r.d6.x);
-    o.dw[j] = h2f_bits(v & 0xFFFFu);
-    o.dmw[j] = 0.0f;
-  }
-}
-
 struct Chains {
   float s[2][4];  // class 2s+g chains of rows 4(i/16)+j
   float f[4];     // Q4_K sumf of rows 4(i/16)+j (valid in lanes n < 4)
 };
 
+// A operand of MFMA (g, u): quarter q's class 2q + g, elements (j = 2u,
+// c = 0..3) then (j = 2u+1, c = 0..3), each sc_j * q as exact f16.
+__device__ __forceinline__ half8 a_q4k(const Seg<true> &r, int g, int u, const half2v (&S)[8],
+                                       const half2v (&N)[8]) {
+  const uint32_t dw = u4at(g ? r.c1 : r.c0, u);
+  const uint32_t lo = dw & 0x0F0F0F0Fu, hi = (dw >> 4) & 0x0F0F0F0Fu;
+  return cat(fma2(magic_pair<kSel01>(lo), S[2 * u], N[2 * u]), fma2(magic_pair<kSel23>(lo), S[2 * u], N[2 * u]),
+             fma2(magic_pair<kSel01>(hi), S[2 * u + 1], N[2 * u + 1]),
+             fma2(magic_pair<kSel23>(hi), S[2 * u + 1], N[2 * u + 1]));
+}
+
+// Q6_K: groups 4u, 4u+1 (j = 2u; c = 0,1 | c = 2,3) and 4u+2, 4u+3 (j = 2u+1);
+// the weights are sc_g * (q6 - 32).
+__device__ __forceinline__ half8 a_q6k(const Seg<false> &r, int g, int u, const half2v (&S)[4],
+                                       const half2v (&N)[4]) {
+  const int jj = 2 * (u & 1);
+  const uint32_t ql = u4at(g ? r.c1 : r.c0, u);
+  const uint32_t qh = u4at(r.c2, 2 * g + (u >> 1));
+  const uint32_t lo = (ql & 0x0F0F0F0Fu) | (((qh >> (2 * jj)) & 0x03030303u) << 4);
+  const uint32_t hi = ((ql >> 4) & 0x0F0F0F0Fu) | (((qh >> (2 * jj + 2)) & 0x03030303u) << 4);
+  return cat(fma2(magic_pair<kSel01>(lo), S[0], N[0]), fma2(magic_pair<kSel23>(lo), S[1], N[1]),
+             fma2(magic_pair<kSel01>(hi), S[2], N[2]), fma2(magic_pair<kSel23>(hi), S[3], N[3]));
+}
+
+// One block of a tile for every column set: A operands are built one at a
+// time right before their MFMAs; then the f32 tail in block order.
 template <int NSET, bool Q4>
-__device__ __forceinline__ void block_step(Chains (&ch)[NSET], const BlockOps &o, const Lds &L, int b, int nb,
-                                           int lane) {
+__device__ __forceinline__ void process_block(Chains (&ch)[NSET], const Seg<Q4> &r, const Lds &L, int b, int nb,
+                                              int lane) {
   const int n = lane & 15, q = lane >> 4;
   const int s = n >> 2;
+  // B operand addresses (x of class 2q + g when q == s, else the zero bytes)
+  const _Float16 *xq[NSET];  // class 2q of (b, column 4st + n%4); class 2q+1 is kXClass further
+#pragma unroll
+  for (int st = 0; st < NSET; st++) xq[st] = x_class(L, 4 * NSET, b, 4 * st + (n & 3), 2 * q);
+  f32x4 acc[NSET][2];
+#pragma unroll
+  for (int st = 0; st < NSET; st++) acc[st][0] = acc[st][1] = (f32x4){0.0f, 0.0f, 0.0f, 0.0f};
+  float dw[4], dmw[4];
+  const int src = ((lane >> 4) * 4) << 2;  // lane index = row of the D layout's row 4(i/16)
+  if constexpr (Q4) {
+    const uint32_t s0 = r.hdr.y, s2 = r.hdr.w;
+    // scale bytes sc0..3 | sc4..7 (6-bit, one per byte)
+    const uint32_t sclo = s0 & 0x3F3F3F3Fu;
+    const uint32_t schi = (s2 & 0x0F0F0F0Fu) | ((s0 >> 2) & 0x30303030u);
+    half2v S[8], N[8];
+#pragma unroll
+    for (int j = 0; j < 8; j++) {
+      S[j] = dup_byte(j < 4 ? sclo : schi, j & 3, 1024.0f);  // (sc_j, sc_j)
+      N[j] = S[j] * (half2v){(_Float16)-1024.0f, (_Float16)-1024.0f};
+    }
+#pragma unroll
+    for (int g = 0; g < 2; g++)
+#pragma unroll
+      for (int u = 0; u < 4; u++) {
+        const half8 a = a_q4k(r, g, u, S, N);
+#pragma unroll
+        for (int st = 0; st < NSET; st++) {
+          const half8 bf = lds_h8(q == s ? (const void *)(xq[st] + g * (kXClass / 2) + 8 * u) : (const void *)L.zero);
+          acc[st][g] = mfma(a, bf, acc[st][g]);
+        }
+      }
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+      const uint32_t v = (uint32_t)__builtin_amdgcn_ds_bpermute(src + 4 * j, (int)r.hdr.x);
+      dw[j] = h2f_bits(v & 0xFFFFu);
+      dmw[j] = h2f_bits(v >> 16);
+    }
+  } else {
+    // signed scales: bytes ^ 0x80 are s + 128; (1024 + 128 + s) - 1152 = s
+#pragma unroll
+    for (int u = 0; u < 4; u++) {
+      const uint32_t gs = u4at(r.hdr, u) ^ 0x80808080u;
+      half2v S[4], N[4];
+#pragma unroll
+      for (int e = 0; e < 4; e++) {
+        S[e] = dup_byte(gs, e, 1152.0f);
+        N[e] = S[e] * (half2v){(_Float16)-1056.0f, (_Float16)-1056.0f};  // -(1024 + 32) * sc
+      }
+#pragma unroll
+      for (int g = 0; g < 2; g++) {
+        const half8 a = a_q6k(r, g, u, S, N);
+#pragma unroll
+        for (int st = 0; st < NSET; st++) {
+          const half8 bf = lds_h8(q == s ? (const void *)(xq[st] + g * (kXClass / 2) + 8 * u) : (const void *)L.zero);
+          acc[st][g] = mfma(a, bf, acc[st][g]);
+        }
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+      const uint32_t v = (uint32_t)__builtin_amdgcn_ds_bpermute(src + 4 * j, (int)r.d);
+      dw[j] = h2f_bits(v & 0xFFFFu);
+      dmw[j] = 0.0f;
+    }
+  }
 #pragma unroll
   for (int st = 0; st < NSET; st++) {
     const int m = 4 * st + (n & 3);
-    const _Float16 *xm = L.xh + ((size_t)m * nb + b) * 256;
-    f32x4 acc[2];
-#pragma unroll
-    for (int g = 0; g < 2; g++) {
-      acc[g] = (f32x4){0.0f, 0.0f, 0.0f, 0.0f};
-      const _Float16 *xc = xm + (2 * q + g) * 32;
-#pragma unroll
-      for (int u = 0; u < 4; u++) {
-        const half8 bf = lds_h8(q == s ? (const void *)(xc + 8 * u) : (const void *)L.zero);
-        acc[g] = mfma(o.a[g][u], bf, acc[g]);
-      }
-    }
-    const float dx = L.dx[(size_t)m * nb + b];
+    const float dx = L.dx[(size_t)b * 4 * NSET + m];
 #pragma unroll
     for (int j = 0; j < 4; j++) {
-      const float dd = __fmul_rn(o.dw[j], dx);
+      const float dd = __fmul_rn(dw[j], dx);
 #pragma unroll
-      for (int g = 0; g < 2; g++) ch[st].s[g][j] = __fadd_rn(ch[st].s[g][j], __fmul_rn(dd, acc[g][j]));
+      for (int g = 0; g < 2; g++) ch[st].s[g][j] = __fadd_rn(ch[st].s[g][j], __fmul_rn(dd, acc[st][g][j]));
     }
-    if (Q4) {
-      const half8 bm = lds_h8(q < 2 && s == 0 ? (const void *)(L.bs + ((size_t)m * nb + b) * 16 + 8 * q)
+  }
+  if constexpr (Q4) {
+    // mins: quarter q < 2 carries k = 8q + e -> (j = 4q + e/2, half e%2)
+    const uint32_t s1 = r.hdr.z, s2 = r.hdr.w;
+    const uint32_t mn = q == 0 ? (s1 & 0x3F3F3F3Fu) : (((s2 >> 4) & 0x0F0F0F0Fu) | ((s1 >> 2) & 0x30303030u));
+    const half8 am = q < 2 ? cat(dup_byte(mn, 0, 1024.0f), dup_byte(mn, 1, 1024.0f), dup_byte(mn, 2, 1024.0f),
+                                 dup_byte(mn, 3, 1024.0f))
+                           : (half8){0, 0, 0, 0, 0, 0, 0, 0};
+#pragma unroll
+    for (int st = 0; st < NSET; st++) {
+      const int m = 4 * st + (n & 3);
+      const half8 bm = lds_h8(q < 2 && s == 0 ? (const void *)(L.bs + ((size_t)b * 4 * NSET + m) * 16 + 8 * q)
                                               : (const void *)L.zero);
-      const f32x4 am = mfma(o.amin, bm, (f32x4){0.0f, 0.0f, 0.0f, 0.0f});
+      const f32x4 sm = mfma(am, bm, (f32x4){0.0f, 0.0f, 0.0f, 0.0f});
+      const float dx = L.dx[(size_t)b * 4 * NSET + m];
 #pragma unroll
       for (int j = 0; j < 4; j++) {
-        const float dm = __fmul_rn(o.dmw[j], dx);
-        ch[st].f[j] = __fsub_rn(ch[st].f[j], __fmul_rn(dm, am[j]));
+        const float dm = __fmul_rn(dmw[j], dx);
+        ch[st].f[j] = __fsub_rn(ch[st].f[j], __fmul_rn(dm, sm[j]));
       }
     }
   }
 }
 
-template <int NSET>
-__device__ __forceinline__ void process_block(Chains (&ch)[NSET], const SegRegs &r, bool q4, const Lds &L, int b,
-                                              int nb, int lane) {
-  BlockOps o;
-  if (q4) {
-    build_q4k(o, r, lane);
-    block_step<NSET, true>(ch, o, L, b, nb, lane);
-  } else {
-    build_q6k(o, r, lane);
-    block_step<NSET, false>(ch, o, L, b, nb, lane);
+// All blocks of one tile, in order; three register buffers keep the loads of
+// the next two blocks in flight while a block computes.
+template <int NSET, bool Q4>
+__device__ __forceinline__ void run_tile(Chains (&ch)[NSET], const uint8_t *seg, size_t bstride, const Lds &L,
+                                         int nb, int lane) {
+  Seg<Q4> r0 = load_seg<Q4>(seg, lane), r1, r2;
+  if (nb > 1) r1 = load_seg<Q4>(seg + bstride, lane);
+  for (int b = 0; b < nb; b += 3) {
+    if (b + 2 < nb) r2 = load_seg<Q4>(seg + (size_t)(b + 2) * bstride, lane);
+    process_block<NSET, Q4>(ch, r0, L, b, nb, lane);
+    if (b + 1 < nb) {
+      if (b + 3 < nb) r0 = load_seg<Q4>(seg + (size_t)(b + 3) * bstride, lane);
+      process_block<NSET, Q4>(ch, r1, L, b + 1, nb, lane);
+    }
+    if (b + 2 < nb) {
+      if (b + 4 < nb) r1 = load_seg<Q4>(seg + (size_t)(b + 4) * bstride, lane);
+      process_block<NSET, Q4>(ch, r2, L, b + 2, nb, lane);
+    }
   }
 }
 
@@ -426,13 +456,14 @@ __global__ __launch_bounds__(256) void kquant_mfma_kernel(const MfmaArgs a) {
     if (m < a.cols) {
       float xv[16];
       load_x16_(xv, a.x + (size_t)m * a.k + (size_t)b * kQK, i16);
-      q8k_block16_f16(xv, i16, L, m, b, nb);
+      q8k_block16_f16(xv, i16, L, 4 * NSET, m, b);
     } else {
-      _Float16 *xb = L.xh + ((size_t)m * nb + b) * 256;
-      *reinterpret_cast<uint4 *>(xb + 16 * i16) = make_uint4(0, 0, 0, 0);
-      *reinterpret_cast<uint4 *>(xb + 16 * i16 + 8) = make_uint4(0, 0, 0, 0);
-      L.bs[((size_t)m * nb + b) * 16 + i16] = (_Float16)0.0f;
-      if (i16 == 0) L.dx[(size_t)m * nb + b] = 0.0f;
+      // 16 lanes clear the region's 8 classes of 64 data bytes
+      _Float16 *xc = x_class(L, 4 * NSET, b, m, i16 >> 1) + 16 * (i16 & 1);
+      *reinterpret_cast<uint4 *>(xc) = make_uint4(0, 0, 0, 0);
+      *reinterpret_cast<uint4 *>(xc + 8) = make_uint4(0, 0, 0, 0);
+      L.bs[((size_t)b * 4 * NSET + m) * 16 + i16] = (_Float16)0.0f;
+      if (i16 == 0) L.dx[(size_t)b * 4 * NSET + m] = 0.0f;
     }
   }
   __syncthreads();
@@ -457,16 +488,10 @@ __global__ __launch_bounds__(256) void kquant_mfma_kernel(const MfmaArgs a) {
         ch[st].s[1][j] = 0.0f;
         ch[st].f[j] = 0.0f;
       }
-    // ping-pong register buffers: block b + 1 loads while block b computes
-    SegRegs buf0 = load_seg(seg, q4, lane), buf1;
-    for (int b = 0; b < nb; b += 2) {
-      if (b + 1 < nb) buf1 = load_seg(seg + (size_t)(b + 1) * bstride, q4, lane);
-      process_block<NSET>(ch, buf0, q4, L, b, nb, lane);
-      if (b + 1 < nb) {
-        if (b + 2 < nb) buf0 = load_seg(seg + (size_t)(b + 2) * bstride, q4, lane);
-        process_block<NSET>(ch, buf1, q4, L, b + 1, nb, lane);
-      }
-    }
+    if (q4)
+      run_tile<NSET, true>(ch, seg, bstride, L, nb, lane);
+    else
+      run_tile<NSET, false>(ch, seg, bstride, L, nb, lane);
     finish_tile<NSET>(ch, L, lane, q4, W.out, W.rows, 16 * tt, a.out_col0, a.cols);
   }
 }
@@ -542,7 +567,7 @@ size_t mfma_segment_bytes(int type, int rows, int nb) {
 
 size_t mfma_lds_bytes(int cols, int nb) {
   const int m4 = cols <= 4 ? 4 : 8;
-  return (size_t)m4 * nb * (512 + 32 + 4) + 16 + 4 * kFinFloats * 4;
+  return (size_t)m4 * nb * (kXRegion + 32 + 4) + 16 + 4 * kFinFloats * 4;
 }
 
 hipError_t launch_repack_mfma(int type, const uint8_t *raw, int rows, int nb, uint8_t *segs, hipStream_t s) {
