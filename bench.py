@@ -78,6 +78,23 @@ def algorithmic_bytes(workload: str, m: int) -> int:
     return b
 
 
+def matvec_kernel_name(choice: str, k: int, m: int, rows: list) -> str:
+    """The matvec kernel the runner picks for one launch (its automatic
+    policy restated: tile counts of the vector-ALU and matrix-core layouts)."""
+    nb = k // 256
+    s = next(d for d in range(min(nb, 64), 0, -1) if nb % d == 0 and ((64 // d) * d >= 48 or d == 1))
+    r6 = 64 // s
+    tiles = sum((r + r6 - 1) // r6 for r in rows)
+    tiles16 = sum((r + 15) // 16 for r in rows)
+    half = s <= 32 and m <= 4 and (choice == "half" or (choice == "auto" and s <= 16 and
+                                                         (tiles <= 2048 if m == 1 else tiles <= 1024)))
+    mfma = choice == "mfma" or (choice == "auto" and not half and k <= 2560 and
+                                (m >= 5 or (m >= 2 and tiles16 >= 1024)))
+    if half:
+        return f"kquant_matvec_half_kernel<{m}>"
+    return "kquant_mfma_kernel" if mfma else f"kquant_matvec_kernel<{min(m, 8)}>"
+
+
 def parse() -> argparse.Namespace:
     p = argparse.ArgumentParser()
     p.add_argument("--gpus", type=int, default=1)
@@ -88,8 +105,8 @@ def parse() -> argparse.Namespace:
     p.add_argument("--rotate-mib", type=int, default=640, help="distinct weight bytes cycled through")
     p.add_argument("--cpu-seconds", type=float, default=12.0)
     p.add_argument("--no-cpu", action="store_true")
-    p.add_argument("--kernel", choices=["auto", "valu", "mfma"], default="auto",
-                   help="matvec kernel: automatic choice, vector ALU, or matrix cores")
+    p.add_argument("--kernel", choices=["auto", "valu", "mfma", "half"], default="auto",
+                   help="matvec kernel: automatic choice, vector ALU, matrix cores, half-split vector ALU")
     p.add_argument("--copy-probe", action="store_true",
                    help="only run a plain 256 MiB device copy (HBM counter calibration) and exit")
     return p.parse_args()
@@ -157,7 +174,8 @@ def main() -> int:
     support = H.checkHipSupport()
     if not support["available"]:
         raise SystemExit(f"HIP runner unavailable: {support}")
-    H.setMatvecKernel({"auto": H.MATVEC_AUTO, "valu": H.MATVEC_VALU, "mfma": H.MATVEC_MFMA}[args.kernel])
+    H.setMatvecKernel({"auto": H.MATVEC_AUTO, "valu": H.MATVEC_VALU, "mfma": H.MATVEC_MFMA,
+                       "half": H.MATVEC_HALF}[args.kernel])
     torch.cuda.init()
     dev = torch.device("cuda:0")
     wl, m = args.workload, args.m
@@ -278,8 +296,7 @@ def main() -> int:
         cpu = cpu_baseline(wl, ws, x_host, args.cpu_seconds)
 
     kernels = {"ffn": "matvec + geglu + matvec", "head": "matvec + top-k"}
-    tiles16 = sum((r + 15) // 16 for _, r in specs)
-    uses_mfma = args.kernel == "mfma" or (args.kernel == "auto" and k <= 2560 and (m >= 5 or (m >= 2 and tiles16 >= 1024)))
+    kernel_name = matvec_kernel_name(args.kernel, k, m, [r for _, r in specs])
     line = {
         "metric": METRIC,
         "value": round(value, 2),
@@ -310,7 +327,7 @@ def main() -> int:
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBPS, 4),
             "traffic": traffic,
-            "kernel": kernels.get(wl, "kquant_mfma_kernel" if uses_mfma else f"kquant_matvec_kernel<{min(m, 8)}>"),
+            "kernel": kernels.get(wl, kernel_name),
             "kernel_avg_us": round(kern_us, 3),
             "kernel_avg_us_mall_hot": round(hot_us, 3),
         },

@@ -202,10 +202,24 @@ bool use_mfma(size_t cols, int nb, int tiles16) {
   const State &s = st();
   const int forced = s.matvec_kernel;
   const size_t lds = mfma_lds_bytes(cols < 8 ? (int)cols : 8, nb);
-  if (forced == 1 || lds > s.max_lds) return false;
+  if (forced == 1 || forced == 3 || lds > s.max_lds) return false;
   if (forced == 2) return true;
   if (cols < 2 || lds > 64 * 1024) return false;
   return cols >= 5 || tiles16 >= 1024;
+}
+
+// Half-split vector-ALU kernel (two lanes per row-block).  It halves each
+// wave's work and doubles the waves, which pays while the launch has few
+// tiles (small projections are latency-bound) and costs throughput on large
+// ones.  Measured on MI355X: faster for one column up to ~2048 tiles (Q/K/V
+// 512, 10240 rows 1707) and for two to four columns up to ~1024 tiles; slower
+// for gate/up (3414 tiles), the head, and 40-block rows (S = 20).
+bool use_half(int cols, const TileGeom &g, int tiles) {
+  const int forced = st().matvec_kernel;
+  if (cols > 4 || g.S > 32) return false;
+  if (forced == 3) return true;
+  if (forced != 0 || g.S > 16) return false;
+  return cols == 1 ? tiles <= 2048 : tiles <= 1024;
 }
 
 // One matvec launch per column chunk covering every weight (multi == one
@@ -231,6 +245,14 @@ int32_t run_matvec(size_t count, Handle *const *hs, const float *d_input, size_t
     tiles += hs[i]->tiles;
   }
   a.total_tiles = tiles;
+  a.Rh = g.S <= 32 ? 32 / g.S : 0;
+  int units = 0;
+  for (size_t i = 0; i < count; i++) {
+    a.w[i].units = a.Rh ? (int)((hs[i]->row_count + a.Rh - 1) / a.Rh) : 0;
+    a.w[i].unit_begin = units;
+    units += a.w[i].units;
+  }
+  a.total_units = units;
   int tiles16 = 0;
   for (size_t i = 0; i < count; i++) tiles16 += (int)((hs[i]->row_count + 15) / 16);
   if (use_mfma(cols, g.nb, tiles16)) {
@@ -264,7 +286,10 @@ int32_t run_matvec(size_t count, Handle *const *hs, const float *d_input, size_t
     a.cols = c;
     a.out_col0 = (int)m0;
     hipEvent_t e1 = prof_begin(stream);
-    HP_HIP_TRY(launch_matvec(a, s.num_cus, stream));
+    if (use_half(c, g, a.total_tiles))
+      HP_HIP_TRY(launch_matvec_half(a, s.num_cus, stream));
+    else
+      HP_HIP_TRY(launch_matvec(a, s.num_cus, stream));
     prof_end(HP_KERNEL_MATVEC, e1, stream);
     s.launches++;
   }
@@ -736,7 +761,7 @@ int32_t hp_hip_quantize_q8_k(const float *input, size_t input_len, size_t input_
 int32_t hp_hip_set_matvec_kernel(int32_t which) {
   State &s = st();
   std::lock_guard<std::recursive_mutex> lock(s.mu);
-  if (which < 0 || which > 2) return fail(HP_ERR_ARG, "kernel selector must be 0, 1 or 2");
+  if (which < 0 || which > 3) return fail(HP_ERR_ARG, "kernel selector must be 0..3");
   s.matvec_kernel = which;
   return HP_OK;
 }

@@ -63,6 +63,8 @@ struct WeightDesc {
   int rows;               // N
   int tiles;              // ceil(N / R)
   int tile_begin;         // first global tile index of this weight
+  int units;              // half-split kernel: ceil(N / Rh)
+  int unit_begin;         // first global unit index of this weight
 };
 
 struct MatvecArgs {
@@ -74,12 +76,17 @@ struct MatvecArgs {
   int k;              // input size (nb * 256)
   int cols;           // columns in this launch (<= kMaxCols)
   int out_col0;       // first output column written by this launch
+  int total_units;    // half-split kernel: units of Rh rows over all weights
+  int Rh;             // half-split kernel: rows per unit (floor(32 / S))
 };
 
 // Launchers (return hipError_t of the launch).
 hipError_t launch_q8k_natural(const float *x, int k, int cols, int8_t *qs, float *d, int16_t *bsums,
                               hipStream_t s);
 hipError_t launch_matvec(const MatvecArgs &a, int num_cus, hipStream_t s);
+// Half-split variant (two lanes per row-block, lane classes 0-3 / 4-7):
+// needs S <= 32 and cols <= 4; a.units/unit_begin/total_units/Rh set.
+hipError_t launch_matvec_half(const MatvecArgs &a, int num_cus, hipStream_t s);
 hipError_t launch_repack(int type, const uint8_t *raw, int rows, const TileGeom &g, uint8_t *tiles,
                          uint16_t *dplane, hipStream_t s);
 // Top-k (k <= kTopkMaxK) of each of `rows` (<= kTopkMaxRows) rows of n

@@ -428,6 +428,259 @@ __global__ __launch_bounds__(256) void kquant_matvec_kernel(const MatvecArgs a) 
   }
 }
 
+// ---------------------------------------------------------------------------
+// Half-split variant: two lanes per (row, block).  Lane (rr, h, s) =
+// lane (2 rr + h) * S + s handles lane classes l = 4h .. 4h+3 of row
+// row0 + rr, block it * S + s: it loads chunk 0 and the nibble (Q4_K) or
+// nibble / high-bit (Q6_K) chunks of its classes only, forms aux32 of its four
+// classes, and chains four sums (h = 0 also sumf) across the S block lanes
+// in block order.  The h = 0 lane then takes its partner's four sums
+// (ds_bpermute) and finishes ((((-0 + s0) + ...) + s7), the reference's
+// order.  Each row-block costs each lane half the integer work and the chain
+// carries 5 values instead of 9; units of Rh = 32 / S rows make twice as
+// many waves as the full kernel, which fills the CUs on small projections.
+// Lanes address the tile layout (hp_common.h) from their own row, so a unit
+// may span two tiles.
+
+struct HalfRegs {
+  uint4 c0;    // bytes 0..15 of the block (Q4_K) / the 16 scales (Q6_K)
+  uint4 d[4];  // Q4_K nibble chunks 1 + 2p + h; Q6_K low-nibble chunks 2p + h
+  uint4 e[2];  // Q6_K high-bit chunks 8 + 2p + h
+  uint32_t d6;
+};
+
+template <int M>
+__device__ __forceinline__ void q4k_ints_half(const HalfRegs &rg, const uint8_t *xq, int nb, int b, int h,
+                                              int (&aux)[M][4], int (&sumi)[M]) {
+  const uint32_t s0 = rg.c0.y, s1 = rg.c0.z, s2 = rg.c0.w;
+  int sc[8], mn[8];
+#pragma unroll
+  for (int j = 0; j < 4; j++) {
+    sc[j] = (s0 >> (8 * j)) & 63;
+    mn[j] = (s1 >> (8 * j)) & 63;
+    sc[j + 4] = ((s2 >> (8 * j)) & 15) | (((s0 >> (8 * j + 6)) & 3) << 4);
+    mn[j + 4] = ((s2 >> (8 * j + 4)) & 15) | (((s1 >> (8 * j + 6)) & 3) << 4);
+  }
+  int dsc[8];  // Abel weights: sum_j sc_j d_j = sum_j T_j (sc_j - sc_{j+1})
+#pragma unroll
+  for (int j = 0; j < 8; j++) dsc[j] = j < 7 ? sc[j] - sc[j + 1] : sc[7];
+  int T[M][4];
+#pragma unroll
+  for (int m = 0; m < M; m++) {
+#pragma unroll
+    for (int l = 0; l < 4; l++) aux[m][l] = T[m][l] = 0;
+    const uint4 bs = *reinterpret_cast<const uint4 *>(xq + ((size_t)m * nb + b) * kQ8BlockBytes + 256);
+    int si = 0;
+#pragma unroll
+    for (int j = 0; j < 8; j++) {
+      const int v = (int)(int16_t)(u4get(bs, j >> 1) >> (16 * (j & 1)));
+      si += __mul24(v, mn[j]);
+    }
+    sumi[m] = si;
+  }
+#pragma unroll
+  for (int j = 0; j < 8; j++) {
+    const uint4 D = rg.d[j >> 1];
+    uint32_t w[4];
+#pragma unroll
+    for (int li = 0; li < 4; li++) {
+      const uint32_t d = u4get(D, li);
+      w[li] = (j & 1) ? ((d >> 4) & 0x0F0F0F0Fu) : (d & 0x0F0F0F0Fu);
+    }
+#pragma unroll
+    for (int m = 0; m < M; m++) {
+      const uint4 xv = reinterpret_cast<const uint4 *>(xq + ((size_t)m * nb + b) * kQ8BlockBytes)[2 * j + h];
+#pragma unroll
+      for (int li = 0; li < 4; li++) {
+        T[m][li] = __builtin_amdgcn_sdot4((int)w[li], (int)u4get(xv, li), T[m][li], false);
+        aux[m][li] = mad24(T[m][li], dsc[j], aux[m][li]);
+      }
+    }
+  }
+}
+
+template <int M>
+__device__ __forceinline__ void q6k_ints_half(const HalfRegs &rg, const uint8_t *xq, int nb, int b, int h,
+                                              int (&aux)[M][4]) {
+  int sc[16];
+#pragma unroll
+  for (int g = 0; g < 16; g++) sc[g] = (int)(int8_t)(u4get(rg.c0, g >> 2) >> (8 * (g & 3)));
+  int dsc[16];
+#pragma unroll
+  for (int g = 0; g < 16; g++) dsc[g] = g < 15 ? sc[g] - sc[g + 1] : sc[15];
+  int T[M][4];
+#pragma unroll
+  for (int m = 0; m < M; m++)
+#pragma unroll
+    for (int l = 0; l < 4; l++) aux[m][l] = T[m][l] = 0;
+#pragma unroll
+  for (int j = 0; j < 8; j++) {
+    const uint4 Dl = rg.d[j >> 1];
+    const uint4 Dh = rg.e[j >> 2];
+    uint32_t wlo[4], whi[4];
+#pragma unroll
+    for (int li = 0; li < 4; li++) {
+      const uint32_t ql = u4get(Dl, li), qh = u4get(Dh, li);
+      const uint32_t nib = (j & 1) ? ((ql >> 2) & 0x3C3C3C3Cu) : ((ql << 2) & 0x3C3C3C3Cu);
+      const int u = j & 3;
+      const uint32_t w = nib | ((qh << (6 - 2 * u)) & 0xC0C0C0C0u);  // bytes = 4 * (q6 - 32)
+      wlo[li] = w & 0x0000FFFFu;
+      whi[li] = w & 0xFFFF0000u;
+    }
+#pragma unroll
+    for (int m = 0; m < M; m++) {
+      const uint4 xv = reinterpret_cast<const uint4 *>(xq + ((size_t)m * nb + b) * kQ8BlockBytes)[2 * j + h];
+#pragma unroll
+      for (int li = 0; li < 4; li++) {
+        T[m][li] = __builtin_amdgcn_sdot4((int)wlo[li], (int)u4get(xv, li), T[m][li], false);
+        aux[m][li] = mad24(T[m][li], dsc[2 * j], aux[m][li]);
+        T[m][li] = __builtin_amdgcn_sdot4((int)whi[li], (int)u4get(xv, li), T[m][li], false);
+        aux[m][li] = mad24(T[m][li], dsc[2 * j + 1], aux[m][li]);
+      }
+    }
+  }
+#pragma unroll
+  for (int m = 0; m < M; m++)
+#pragma unroll
+    for (int l = 0; l < 4; l++) aux[m][l] >>= 2;  // weights carried 4 * (q6 - 32)
+}
+
+template <int M>
+__global__ __launch_bounds__(256) void kquant_matvec_half_kernel(const MatvecArgs a) {
+  extern __shared__ __align__(16) uint8_t smem[];
+  const TileGeom g = a.g;
+  const int nb = g.nb, S = g.S, R = g.R, Rh = a.Rh;
+  uint8_t *xq = smem;
+  float *xd = reinterpret_cast<float *>(smem + (size_t)M * nb * kQ8BlockBytes);
+
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int wpg = blockDim.x >> 6;
+  const int stride = gridDim.x * wpg;
+  const int grp2 = lane / S;  // 2 rr + h
+  const int rr = grp2 >> 1, h = grp2 & 1;
+  const int s = lane - grp2 * S;
+
+  const int grp = wave * 4 + (lane >> 4);
+  const int i16 = lane & 15;
+  const int nq = M * nb;
+  float xv[16];
+  if (grp < nq) load_x16(xv, a.x + (size_t)(grp / nb) * a.k + (size_t)(grp % nb) * kQK, i16);
+  for (int q = grp; q < nq; q += wpg * 4) {
+    const int qn = q + wpg * 4;
+    float xn[16];
+    if (qn < nq) load_x16(xn, a.x + (size_t)(qn / nb) * a.k + (size_t)(qn % nb) * kQK, i16);
+    q8k_block16(xv, i16, xq + (size_t)q * kQ8BlockBytes, xd + q);
+    if (qn < nq) {
+#pragma unroll
+      for (int i = 0; i < 16; i++) xv[i] = xn[i];
+    }
+  }
+  __syncthreads();
+
+  float carry[M][5];
+  for (int u = blockIdx.x * wpg + wave; u < a.total_units; u += stride) {
+    WeightDesc W = a.w[0];
+    if (a.count > 1 && u >= a.w[1].unit_begin) W = a.w[1];
+    if (a.count > 2 && u >= a.w[2].unit_begin) W = a.w[2];
+    if (a.count > 3 && u >= a.w[3].unit_begin) W = a.w[3];
+    const bool q4 = W.type == kTypeQ4K;
+    const int CH = q4 ? 9 : 13;
+    const int row0 = (u - W.unit_begin) * Rh;
+    const int row = row0 + rr;
+    const bool active = rr < Rh && row < W.rows && grp2 < 2 * Rh;
+    // this lane's tile, tile row count and lane index inside the tile
+    const int t = active ? row / R : 0;
+    const int Rt = min(R, W.rows - t * R);
+    const int k = (row - t * R) * S + s;
+    const uint8_t *tile = W.data + (size_t)t * R * nb * CH * 16;
+    for (int it = 0; it < g.iters; it++) {
+      HalfRegs rg;
+      if (active) {
+        const uint4 *ch = reinterpret_cast<const uint4 *>(tile + ((size_t)it * CH * Rt * S + k) * 16);
+        const size_t cs = (size_t)Rt * S;  // uint4 stride between chunks
+        rg.c0 = ch[(q4 ? 0 : 12) * cs];
+        if (q4) {
+#pragma unroll
+          for (int p = 0; p < 4; p++) rg.d[p] = ch[(1 + 2 * p + h) * cs];
+        } else {
+#pragma unroll
+          for (int p = 0; p < 4; p++) rg.d[p] = ch[(2 * p + h) * cs];
+#pragma unroll
+          for (int p = 0; p < 2; p++) rg.e[p] = ch[(8 + 2 * p + h) * cs];
+          rg.d6 = W.dplane[(size_t)t * R * nb + (size_t)it * Rt * S + k];
+        }
+      }
+      const int b = it * S + s;
+      int aux[M][4];
+      int sumi[M];
+      float dw = 0.0f, dminw = 0.0f;
+      if (active) {
+        if (q4) {
+          q4k_ints_half<M>(rg, xq, nb, b, h, aux, sumi);
+          dw = h2f(rg.c0.x & 0xFFFFu);
+          dminw = h2f(rg.c0.x >> 16);
+        } else {
+          q6k_ints_half<M>(rg, xq, nb, b, h, aux);
+          dw = h2f(rg.d6);
+#pragma unroll
+          for (int m = 0; m < M; m++) sumi[m] = 0;
+        }
+      } else {
+#pragma unroll
+        for (int m = 0; m < M; m++) {
+          sumi[m] = 0;
+#pragma unroll
+          for (int l = 0; l < 4; l++) aux[m][l] = 0;
+        }
+      }
+      const bool last = it + 1 == g.iters;
+#pragma unroll
+      for (int m = 0; m < M; m++) {
+        const float dx = xd[m * nb + (b < nb ? b : 0)];
+        const float dd = __fmul_rn(dw, dx);
+        float p[5];
+#pragma unroll
+        for (int l = 0; l < 4; l++) p[l] = __fmul_rn(dd, (float)aux[m][l]);
+        p[4] = __fmul_rn(__fmul_rn(dminw, dx), (float)sumi[m]);
+        float v[5];
+#pragma unroll
+        for (int c = 0; c < 4; c++) v[c] = __fadd_rn(it == 0 ? 0.0f : carry[m][c], p[c]);
+        v[4] = __fsub_rn(it == 0 ? 0.0f : carry[m][4], p[4]);
+        for (int kk = 1; kk < S; kk++) {
+#pragma unroll
+          for (int c = 0; c < 4; c++) v[c] = __fadd_rn(shr1(v[c]), p[c]);
+          v[4] = __fsub_rn(shr1(v[4]), p[4]);
+        }
+        if (!last) {
+          // lane (rr, h, 0) continues from lane (rr, h, S-1)
+          const int src = (grp2 * S + S - 1) << 2;
+#pragma unroll
+          for (int c = 0; c < 5; c++)
+            carry[m][c] = __builtin_bit_cast(float, __builtin_amdgcn_ds_bpermute(src, __builtin_bit_cast(int, v[c])));
+        } else {
+          // lane (rr, 0, S-1) takes classes 4..7 from lane (rr, 1, S-1)
+          const int partner = (lane + S < 64 ? lane + S : lane) << 2;
+          float o[4];
+#pragma unroll
+          for (int c = 0; c < 4; c++)
+            o[c] = __builtin_bit_cast(float, __builtin_amdgcn_ds_bpermute(partner, __builtin_bit_cast(int, v[c])));
+          if (active && h == 0 && s == S - 1) {
+            // result = [sumf +] ((((-0 + s0) + s1) + ...) + s7)
+            float tsum = -0.0f;
+#pragma unroll
+            for (int l = 0; l < 4; l++) tsum = __fadd_rn(tsum, v[l]);
+#pragma unroll
+            for (int l = 0; l < 4; l++) tsum = __fadd_rn(tsum, o[l]);
+            const float res = q4 ? __fadd_rn(v[4], tsum) : tsum;
+            W.out[(size_t)(a.out_col0 + m) * W.rows + row] = res;
+          }
+        }
+      }
+    }
+  }
+}
+
 static size_t matvec_lds_bytes(int cols, const TileGeom &g, int wpg) {
   (void)wpg;
   return (size_t)cols * g.nb * kQ8BlockBytes + (size_t)((cols * g.nb + 3) & ~3) * 4;
@@ -442,6 +695,27 @@ static hipError_t launch_m(const MatvecArgs &a, int num_cus, hipStream_t s) {
   size_t lds = matvec_lds_bytes(M, a.g, wpg);
   hipLaunchKernelGGL((kquant_matvec_kernel<M, (M <= 3)>), dim3(grid), dim3(64 * wpg), lds, s, a);
   return hipGetLastError();
+}
+
+template <int M>
+static hipError_t launch_half_m(const MatvecArgs &a, int num_cus, hipStream_t s) {
+  const int wpg = 4;
+  int grid = (a.total_units + wpg - 1) / wpg;
+  const int cap = num_cus * 8;
+  if (grid > cap) grid = cap;
+  hipLaunchKernelGGL(kquant_matvec_half_kernel<M>, dim3(grid), dim3(64 * wpg), matvec_lds_bytes(M, a.g, wpg), s, a);
+  return hipGetLastError();
+}
+
+hipError_t launch_matvec_half(const MatvecArgs &a, int num_cus, hipStream_t s) {
+  if (a.g.S > 32 || a.Rh < 1 || 2 * a.Rh * a.g.S > 64) return hipErrorInvalidValue;
+  switch (a.cols) {
+    case 1: return launch_half_m<1>(a, num_cus, s);
+    case 2: return launch_half_m<2>(a, num_cus, s);
+    case 3: return launch_half_m<3>(a, num_cus, s);
+    case 4: return launch_half_m<4>(a, num_cus, s);
+    default: return hipErrorInvalidValue;
+  }
 }
 
 hipError_t launch_matvec(const MatvecArgs &a, int num_cus, hipStream_t s) {

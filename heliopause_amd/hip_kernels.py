@@ -359,12 +359,13 @@ def matmul_multi_device(handles: Sequence[int], d_input: int, input_size: int, c
     assertHipOk(code, "matmulMultiDevice")
 
 
-MATVEC_AUTO, MATVEC_VALU, MATVEC_MFMA = 0, 1, 2
+MATVEC_AUTO, MATVEC_VALU, MATVEC_MFMA, MATVEC_HALF = 0, 1, 2, 3
 
 
 def setMatvecKernel(which: int) -> None:
-    """Select the matvec kernel (0 automatic, 1 vector ALU, 2 matrix cores);
-    both are bit-exact, only speed differs.  No counterpart in the reference."""
+    """Select the matvec kernel (0 automatic, 1 vector ALU, 2 matrix cores,
+    3 half-split vector ALU); all are bit-exact, only speed differs.  No
+    counterpart in the reference."""
     assertHipOk(lib().hp_hip_set_matvec_kernel(int(which)), "setMatvecKernel")
 
 

@@ -153,10 +153,12 @@ int32_t hp_hip_quantize_q8_k(const float *input, size_t input_len, size_t input_
                              int8_t *qs, float *d, int16_t *bsums32);
 
 /* Matvec kernel selection (no counterpart in the reference; a tuning and
- * test hook): 0 = automatic (vector-ALU kernel for one column, matrix-core
- * kernel for two or more when its LDS fits), 1 = always the vector-ALU
- * kernel, 2 = the matrix-core kernel whenever its LDS fits the device.
- * Both are bit-exact with the reference; only speed differs. */
+ * test hook): 0 = automatic (by column count and tile count: half-split
+ * vector ALU for small projections, vector ALU for one column, matrix
+ * cores for several columns of large ones), 1 = always the vector-ALU
+ * kernel, 2 = the matrix-core kernel whenever its LDS fits the device,
+ * 3 = the half-split vector-ALU kernel (two lanes per row-block) for up to
+ * four columns.  All are bit-exact with the reference; only speed differs. */
 int32_t hp_hip_set_matvec_kernel(int32_t which);
 
 /* wasmResidentWeightStats (wasm-kernels.ts:586-591) plus call counters. */

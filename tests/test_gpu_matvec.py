@@ -21,9 +21,10 @@ def _weights(type_name, seed, rows, k):
     return S.weight_blocks(type_name, seed, rows, k)
 
 
-@pytest.fixture(params=[1, 2], ids=["valu", "mfma"])
+@pytest.fixture(params=[1, 2, 3], ids=["valu", "mfma", "half"])
 def kernel(request, hip):
-    """Runs the test with the vector-ALU and with the matrix-core matvec."""
+    """Runs the test with the vector-ALU, the matrix-core and the half-split
+    vector-ALU matvec."""
     hip.setMatvecKernel(request.param)
     yield request.param
     hip.setMatvecKernel(0)
