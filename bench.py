@@ -53,6 +53,14 @@ WORKLOADS = {
 FFN_DOWN = ("Q6_K", 2560, 10240)
 TOPK = 40
 
+# The 42-layer synthetic Gemma-like model: per layer (type, rows, input size)
+LAYER = [("Q4_K", 2048, 2560), ("Q4_K", 512, 2560), ("Q6_K", 512, 2560),   # Q, K, V
+         ("Q4_K", 2560, 2048),                                              # O
+         ("Q4_K", 10240, 2560), ("Q4_K", 10240, 2560),                      # gate, up
+         ("Q6_K", 2560, 10240)]                                             # down
+N_LAYERS = 42
+HEAD = ("Q6_K", 262144, 2560)
+
 
 def row_bytes(t: str, k: int) -> int:
     return k // 256 * BLOCK[t]
@@ -101,7 +109,7 @@ def parse() -> argparse.Namespace:
     p.add_argument("--steps", type=int, default=400)
     p.add_argument("--warmup", type=int, default=40)
     p.add_argument("--m", type=int, default=1)
-    p.add_argument("--workload", choices=sorted(WORKLOADS), default="qkv")
+    p.add_argument("--workload", choices=sorted(WORKLOADS) + ["decode42"], default="qkv")
     p.add_argument("--rotate-mib", type=int, default=640, help="distinct weight bytes cycled through")
     p.add_argument("--cpu-seconds", type=float, default=12.0)
     p.add_argument("--no-cpu", action="store_true")
@@ -158,6 +166,94 @@ def cpu_baseline(workload: str, ws, x, seconds: float) -> dict:
     }
 
 
+def decode_chain(args) -> int:
+    """Projection chain of one decode step of the 42-layer model at M = 1:
+    per layer Q/K/V (one launch) -> O (fed Q's 2048 outputs) -> gate/up (one
+    launch) -> GeGLU -> down, then the head and top-40; every layer's weights
+    are distinct device copies (3.02 GB, so nothing is Infinity-Cache hot).
+    Attention, norms, RoPE and residuals are not part of this path and are
+    not run; each layer's Q/K/V and the head read one fixed input, which does
+    not change the launch order (one stream)."""
+    import numpy as np
+    import torch
+
+    from heliopause_amd import hip_kernels as H
+    from heliopause_amd import synthetic as S
+
+    if args.m != 1:
+        raise SystemExit("decode42 runs at M = 1")
+    H.setMatvecKernel({"auto": H.MATVEC_AUTO, "valu": H.MATVEC_VALU, "mfma": H.MATVEC_MFMA,
+                       "half": H.MATVEC_HALF}[args.kernel])
+    torch.cuda.init()
+    dev = torch.device("cuda:0")
+    seed = S.config_seed(5)
+    host = {}
+    for i, (t, r, k) in enumerate(LAYER + [HEAD]):
+        if (t, r, k) not in host:
+            host[(t, r, k)] = S.weight_blocks(t, S.derive(seed, "decode42", i), r, k)
+    layers = []
+    for _ in range(N_LAYERS):
+        layers.append([H.createHipQuantizedWeightHandle(t, host[(t, r, k)], k, r).handle for t, r, k in LAYER])
+    head = H.createHipQuantizedWeightHandle(HEAD[0], host[HEAD], HEAD[2], HEAD[1]).handle
+    x = torch.from_numpy(S.activations(S.derive(seed, "x"), 1, 2560)).to(dev)
+    buf = {n: torch.empty(c, dtype=torch.float32, device=dev)
+           for n, c in (("q", 2048), ("k", 512), ("v", 512), ("o", 2560), ("g", 10240), ("u", 10240),
+                        ("h", 10240), ("y", 2560), ("logits", 262144))}
+    ids = torch.empty(TOPK, dtype=torch.int32, device=dev)
+    vals = torch.empty(TOPK, dtype=torch.float32, device=dev)
+    L = H.lib()
+    p = {n: t.data_ptr() for n, t in buf.items()}
+
+    def step(stream: int) -> None:
+        for hs in layers:
+            H.matmul_multi_device(hs[0:3], x.data_ptr(), 2560, 1, [p["q"], p["k"], p["v"]], [2048, 512, 512], stream)
+            H.matmul_multi_device(hs[3:4], p["q"], 2048, 1, [p["o"]], [2560], stream)
+            H.matmul_multi_device(hs[4:6], p["o"], 2560, 1, [p["g"], p["u"]], [10240, 10240], stream)
+            H.assertHipOk(L.hp_hip_geglu_device(p["g"], p["u"], 10240, p["h"], stream), "geglu")
+            H.matmul_multi_device(hs[6:7], p["h"], 10240, 1, [p["y"]], [2560], stream)
+        H.matmul_multi_device([head], x.data_ptr(), 2560, 1, [p["logits"]], [262144], stream)
+        H.assertHipOk(L.hp_hip_topk_device(p["logits"], 1, 262144, TOPK, 0.0, ids.data_ptr(), vals.data_ptr(),
+                                           stream), "topk")
+
+    side = torch.cuda.Stream()
+    with torch.cuda.stream(side):
+        step(side.cuda_stream)
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=side):
+            step(torch.cuda.current_stream().cuda_stream)
+    for _ in range(max(1, args.warmup // 10)):
+        graph.replay()
+    torch.cuda.synchronize()
+    steps = max(1, args.steps // 10)
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    start.record()
+    for _ in range(steps):
+        graph.replay()
+    end.record()
+    torch.cuda.synchronize()
+    wall_ms = (time.perf_counter() - t0) / steps * 1e3
+    ms = start.elapsed_time(end) / steps
+    wbytes = N_LAYERS * sum(row_bytes(t, k) * r for t, r, k in LAYER) + row_bytes(HEAD[0], HEAD[2]) * HEAD[1]
+    launches = N_LAYERS * 5 + 1 + 3
+    line = {
+        "metric": "decode step projection chain ms at M=1 (1 GPU)",
+        "value": round(ms, 4), "unit": "ms", "n_gpus": 1, "steps": steps, "warmup": args.warmup,
+        "ms_per_step": round(ms, 4), "higher_is_better": False, "scaling": "weak", "vs_baseline": None,
+        "dtype": "int8", "data": "synthetic",
+        "config": {"workload": "42-layer synthetic Gemma-like model, projections + GeGLU + head + top-40 at M=1 "
+                               "(attention, norms, RoPE, residuals not included)",
+                   "weight_bytes": wbytes, "launches_per_step": launches, "wall_ms_per_step": round(wall_ms, 4),
+                   "timing": "one step captured in a HIP graph and replayed"},
+        "roofline": {"bound": "hbm", "achieved": round(wbytes / (ms * 1e-3) / 1e9, 2), "peak": HBM_PEAK_GBPS,
+                     "unit": "GB/s", "frac": round(wbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4),
+                     "weight_bytes_over_peak_ms": round(wbytes / HBM_PEAK_GBPS / 1e6, 4)},
+    }
+    print(json.dumps(line))
+    return 0
+
+
 def main() -> int:
     args = parse()
     if args.copy_probe:
@@ -165,6 +261,8 @@ def main() -> int:
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU only; --gpus must be 1", "n_gpus": args.gpus}))
         return 2
+    if args.workload == "decode42":
+        return decode_chain(args)
     import numpy as np
     import torch
 
