@@ -182,6 +182,9 @@ void prof_collect() {
   }
 }
 
+// sqrt(2/pi) as Math.sqrt(2 / Math.PI) evaluates it (IEEE f64 divide and sqrt).
+double gelu_constant() { return std::sqrt(2.0 / 3.141592653589793); }
+
 // Column chunk such that the matvec launch's LDS fits the device limit.
 int cols_per_launch(const TileGeom &g, size_t max_lds) {
   for (int c = kMaxCols; c >= 1; c--) {
@@ -297,6 +300,74 @@ int32_t run_matvec(size_t count, Handle *const *hs, const float *d_input, size_t
   return HP_OK;
 }
 
+// gate/up projections + GeGLU into d_out ([cols][rows]).  One fused
+// vector-ALU launch when the kernel policy would run the full vector-ALU
+// kernel on this launch (one column of large projections); otherwise the
+// projections (one launch, any kernel) into scratch, then the GeGLU kernel.
+// Both give the same bits.
+int32_t run_matvec_geglu(Handle *hg, Handle *hu, const float *d_input, size_t input_size, size_t cols,
+                         float *d_out, hipStream_t stream) {
+  State &s = st();
+  if (cols == 0) return HP_OK;
+  const size_t rows = hg->row_count;
+  const TileGeom g = hg->g;
+  const int tiles16 = 2 * (int)((rows + 15) / 16);
+  const bool fused = cols <= 4 && s.matvec_kernel <= 1 && !use_mfma(cols, g.nb, tiles16) &&
+                     !use_half((int)cols, g, 2 * hg->tiles) && cols_per_launch(g, s.max_lds) >= (int)cols;
+  if (fused) {
+    MatvecArgs a{};
+    a.count = 2;
+    a.g = g;
+    a.k = (int)input_size;
+    Handle *hs[2] = {hg, hu};
+    for (int i = 0; i < 2; i++) {
+      a.w[i].data = hs[i]->data;
+      a.w[i].dplane = hs[i]->dplane;
+      a.w[i].out = nullptr;
+      a.w[i].type = hs[i]->type;
+      a.w[i].rows = (int)rows;
+      a.w[i].tiles = hs[i]->tiles;
+      a.w[i].tile_begin = i * hs[0]->tiles;
+    }
+    a.total_tiles = 2 * hg->tiles;
+    a.x = d_input;
+    a.cols = (int)cols;
+    a.out_col0 = 0;
+    a.pair_out = d_out;
+    a.gelu_c = gelu_constant();
+    hipEvent_t e1 = prof_begin(stream);
+    HP_HIP_TRY(launch_matvec_pair(a, s.num_cus, stream));
+    prof_end(HP_KERNEL_MATVEC, e1, stream);
+    s.launches++;
+    s.matmul_calls++;
+    return HP_OK;
+  }
+  int32_t rc = grow((void **)&s.io_out[2], &s.io_out_cap[2], cols * rows * sizeof(float));
+  if (rc == HP_OK) rc = grow((void **)&s.io_out[3], &s.io_out_cap[3], cols * rows * sizeof(float));
+  if (rc != HP_OK) return rc;
+  Handle *hs[2] = {hg, hu};
+  float *outs[2] = {s.io_out[2], s.io_out[3]};
+  rc = run_matvec(2, hs, d_input, input_size, cols, outs, stream);
+  if (rc != HP_OK) return rc;
+  hipEvent_t e2 = prof_begin(stream);
+  HP_HIP_TRY(launch_geglu(outs[0], outs[1], cols * rows, gelu_constant(), d_out, s.num_cus, stream));
+  prof_end(HP_KERNEL_GEGLU, e2, stream);
+  s.launches++;
+  return HP_OK;
+}
+
+int32_t geglu_pair_check(uint64_t gate, uint64_t up, size_t input_len, size_t input_size, size_t cols,
+                         size_t output_len, Handle **hg, Handle **hu) {
+  *hg = lookup(gate);
+  *hu = lookup(up);
+  if (!*hg || !*hu) return fail(HP_ERR_HANDLE, "unknown weight handle");
+  if ((*hg)->input_size != input_size || (*hu)->input_size != input_size || input_len != sat_mul(input_size, cols))
+    return fail(HP_ERR_SHAPE, "gate/up input shape mismatch");
+  if ((*hg)->row_count != (*hu)->row_count) return fail(HP_ERR_SHAPE, "gate and up row counts differ");
+  if (output_len != sat_mul((*hg)->row_count, cols)) return fail(HP_ERR_SHAPE, "output length mismatch");
+  return HP_OK;
+}
+
 int32_t upload_common(int32_t type_id, const void *src, bool src_device, size_t weight_len, size_t input_size,
                       size_t row_count, uint64_t *out_handle) {
   State &s = st();
@@ -369,9 +440,6 @@ int32_t upload_common(int32_t type_id, const void *src, bool src_device, size_t 
   *out_handle = ((uint64_t)h.generation << 32) | (uint64_t)(slot + 1);
   return HP_OK;
 }
-
-// sqrt(2/pi) as Math.sqrt(2 / Math.PI) evaluates it (IEEE f64 divide and sqrt).
-double gelu_constant() { return std::sqrt(2.0 / 3.141592653589793); }
 
 int32_t topk_check(size_t rows, size_t n, size_t k) {
   if (k == 0 || k > 64) return fail(HP_ERR_ARG, "k must be in 1..64");
@@ -690,6 +758,45 @@ int32_t hp_hip_matmul_topk(uint64_t handle, const float *input, size_t input_len
   if (rc != HP_OK) return rc;
   HP_HIP_TRY(hipMemcpyAsync(ids, d_ids, column_count * k * 4, hipMemcpyDeviceToHost, s.stream));
   HP_HIP_TRY(hipMemcpyAsync(values, d_vals, column_count * k * 4, hipMemcpyDeviceToHost, s.stream));
+  HP_HIP_TRY(hipStreamSynchronize(s.stream));
+  return HP_OK;
+}
+
+int32_t hp_hip_matmul_geglu_device(uint64_t gate, uint64_t up, const float *d_input, size_t input_len,
+                                   size_t input_size, size_t column_count, float *d_output, size_t output_len,
+                                   void *stream) {
+  State &s = st();
+  std::lock_guard<std::recursive_mutex> lock(s.mu);
+  int32_t rc = ensure_init(s.ready ? s.device : 0);
+  if (rc != HP_OK) return rc;
+  Handle *hg, *hu;
+  rc = geglu_pair_check(gate, up, input_len, input_size, column_count, output_len, &hg, &hu);
+  if (rc != HP_OK) return rc;
+  if (column_count == 0) return HP_OK;
+  if (!d_input || !d_output) return fail(HP_ERR_ARG, "null pointer");
+  if (reinterpret_cast<uintptr_t>(d_input) % 16 != 0) return fail(HP_ERR_ARG, "input must be 16-byte aligned");
+  hipStream_t strm = stream ? static_cast<hipStream_t>(stream) : s.stream;
+  return run_matvec_geglu(hg, hu, d_input, input_size, column_count, d_output, strm);
+}
+
+int32_t hp_hip_matmul_geglu(uint64_t gate, uint64_t up, const float *input, size_t input_len, size_t input_size,
+                            size_t column_count, float *output, size_t output_len) {
+  State &s = st();
+  std::lock_guard<std::recursive_mutex> lock(s.mu);
+  int32_t rc = ensure_init(s.ready ? s.device : 0);
+  if (rc != HP_OK) return rc;
+  Handle *hg, *hu;
+  rc = geglu_pair_check(gate, up, input_len, input_size, column_count, output_len, &hg, &hu);
+  if (rc != HP_OK) return rc;
+  if (column_count == 0) return HP_OK;
+  if (!input || !output) return fail(HP_ERR_ARG, "null pointer");
+  rc = grow((void **)&s.io_in, &s.io_in_cap, input_len * sizeof(float));
+  if (rc == HP_OK) rc = grow((void **)&s.io_out[0], &s.io_out_cap[0], output_len * sizeof(float));
+  if (rc != HP_OK) return rc;
+  HP_HIP_TRY(hipMemcpyAsync(s.io_in, input, input_len * sizeof(float), hipMemcpyHostToDevice, s.stream));
+  rc = run_matvec_geglu(hg, hu, s.io_in, input_size, column_count, s.io_out[0], s.stream);
+  if (rc != HP_OK) return rc;
+  HP_HIP_TRY(hipMemcpyAsync(output, s.io_out[0], output_len * sizeof(float), hipMemcpyDeviceToHost, s.stream));
   HP_HIP_TRY(hipStreamSynchronize(s.stream));
   return HP_OK;
 }

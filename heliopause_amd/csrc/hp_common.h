@@ -78,6 +78,8 @@ struct MatvecArgs {
   int out_col0;       // first output column written by this launch
   int total_units;    // half-split kernel: units of Rh rows over all weights
   int Rh;             // half-split kernel: rows per unit (floor(32 / S))
+  float *pair_out;    // gate/up + GeGLU launch: [cols][rows] output
+  double gelu_c;      // sqrt(2 / pi) as Math.sqrt(2 / Math.PI)
 };
 
 // Launchers (return hipError_t of the launch).
@@ -87,6 +89,9 @@ hipError_t launch_matvec(const MatvecArgs &a, int num_cus, hipStream_t s);
 // Half-split variant (two lanes per row-block, lane classes 0-3 / 4-7):
 // needs S <= 32 and cols <= 4; a.units/unit_begin/total_units/Rh set.
 hipError_t launch_matvec_half(const MatvecArgs &a, int num_cus, hipStream_t s);
+// Gate/up + GeGLU in one vector-ALU launch (count == 2, equal rows, cols <= 4):
+// a.pair_out[m][r] = fround(gelu(gate) * up).
+hipError_t launch_matvec_pair(const MatvecArgs &a, int num_cus, hipStream_t s);
 hipError_t launch_repack(int type, const uint8_t *raw, int rows, const TileGeom &g, uint8_t *tiles,
                          uint16_t *dplane, hipStream_t s);
 // Top-k (k <= kTopkMaxK) of each of `rows` (<= kTopkMaxRows) rows of n

@@ -24,6 +24,7 @@
 // block order.  Each workgroup first quantises the f32 input to Q8_K into
 // LDS (16 lanes per 256-element block), so a projection is one launch.
 #include "hp_common.h"
+#include "hp_gelu.h"
 #include "hp_q8k.h"
 
 namespace hp {
@@ -298,7 +299,11 @@ __device__ __forceinline__ float shr1(float v) {
   return dppf<kDppWaveShr1>(v);
 }
 
-template <int M, bool PREFETCH>
+// PAIR: gate/up + GeGLU (layers.ts:435-456).  Weight 0 is gate, weight 1 up,
+// with equal row counts; a wave takes gate tile p and then up tile p, which
+// cover the same rows, so the lane that finishes row r's gate sum keeps it
+// and, after the up pass, writes fround(gelu(gate) * up) to a.pair_out.
+template <int M, bool PREFETCH, bool PAIR = false>
 __global__ __launch_bounds__(256) void kquant_matvec_kernel(const MatvecArgs a) {
   extern __shared__ __align__(16) uint8_t smem[];
   const TileGeom g = a.g;
@@ -321,10 +326,21 @@ __global__ __launch_bounds__(256) void kquant_matvec_kernel(const MatvecArgs a) 
   float xv[16];
   if (grp < nq) load_x16(xv, a.x + (size_t)(grp / nb) * a.k + (size_t)(grp % nb) * kQK, i16);
 
-  int t = blockIdx.x * wpg + wave;
+  // the i-th tile of this wave (-1: none); with PAIR, gate then up tile
+  const int t0 = blockIdx.x * wpg + wave;
+  auto tile_of = [&](int i) -> int {
+    if (!PAIR) {
+      const int tt = t0 + i * stride;
+      return tt < a.total_tiles ? tt : -1;
+    }
+    const int p = t0 + (i >> 1) * stride;
+    return p < a.w[0].tiles ? p + (i & 1) * a.w[0].tiles : -1;
+  };
+  int ti = 0;
+  int t = tile_of(0);
   TileCtx cx{};
   Regs cur;
-  if (t < a.total_tiles) {
+  if (t >= 0) {
     cx = make_ctx(a, t, nb, R, S);
     load_regs(cur, cx, 0, lane, nb);
   }
@@ -342,18 +358,19 @@ __global__ __launch_bounds__(256) void kquant_matvec_kernel(const MatvecArgs a) 
   __syncthreads();
 
   float carry[M][9];
-  while (t < a.total_tiles) {
+  float gkeep[M];  // PAIR: this lane's gate results
+  while (t >= 0) {
     for (int it = 0; it < g.iters; it++) {
       Regs nxt;
       if (PREFETCH) {
         int nt = t, nit = it + 1;
         TileCtx ncx = cx;
         if (nit == g.iters) {
-          nt = t + stride;
+          nt = tile_of(ti + 1);
           nit = 0;
-          if (nt < a.total_tiles) ncx = make_ctx(a, nt, nb, R, S);
+          if (nt >= 0) ncx = make_ctx(a, nt, nb, R, S);
         }
-        if (nt < a.total_tiles) load_regs(nxt, ncx, nit, lane, nb);
+        if (nt >= 0) load_regs(nxt, ncx, nit, lane, nb);
       }
       const int b = it * S + s;
       const bool active = lane < cx.lanes;
@@ -411,7 +428,12 @@ __global__ __launch_bounds__(256) void kquant_matvec_kernel(const MatvecArgs a) 
 #pragma unroll
           for (int l = 0; l < 8; l++) tsum = __fadd_rn(tsum, v[l]);
           const float res = cx.q4 ? __fadd_rn(v[8], tsum) : tsum;
-          cx.out[(size_t)(a.out_col0 + m) * cx.rows + cx.row0 + r] = res;
+          if (!PAIR)
+            cx.out[(size_t)(a.out_col0 + m) * cx.rows + cx.row0 + r] = res;
+          else if ((ti & 1) == 0)
+            gkeep[m] = res;
+          else
+            a.pair_out[(size_t)(a.out_col0 + m) * cx.rows + cx.row0 + r] = geglu_ts(gkeep[m], res, a.gelu_c);
         }
       }
       if (PREFETCH) {
@@ -420,8 +442,8 @@ __global__ __launch_bounds__(256) void kquant_matvec_kernel(const MatvecArgs a) 
         load_regs(cur, cx, it + 1, lane, nb);
       }
     }
-    t += stride;
-    if (t < a.total_tiles) {
+    t = tile_of(++ti);
+    if (t >= 0) {
       cx = make_ctx(a, t, nb, R, S);
       if (!PREFETCH) load_regs(cur, cx, 0, lane, nb);
     }
@@ -714,6 +736,29 @@ hipError_t launch_matvec_half(const MatvecArgs &a, int num_cus, hipStream_t s) {
     case 2: return launch_half_m<2>(a, num_cus, s);
     case 3: return launch_half_m<3>(a, num_cus, s);
     case 4: return launch_half_m<4>(a, num_cus, s);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+template <int M>
+static hipError_t launch_pair_m(const MatvecArgs &a, int num_cus, hipStream_t s) {
+  const int wpg = 4;
+  int grid = (a.w[0].tiles + wpg - 1) / wpg;
+  const int cap = num_cus * 8;
+  if (grid > cap) grid = cap;
+  hipLaunchKernelGGL((kquant_matvec_kernel<M, (M <= 3), true>), dim3(grid), dim3(64 * wpg),
+                     matvec_lds_bytes(M, a.g, wpg), s, a);
+  return hipGetLastError();
+}
+
+hipError_t launch_matvec_pair(const MatvecArgs &a, int num_cus, hipStream_t s) {
+  if (a.count != 2 || a.w[0].rows != a.w[1].rows || a.w[0].tiles != a.w[1].tiles || !a.pair_out)
+    return hipErrorInvalidValue;
+  switch (a.cols) {
+    case 1: return launch_pair_m<1>(a, num_cus, s);
+    case 2: return launch_pair_m<2>(a, num_cus, s);
+    case 3: return launch_pair_m<3>(a, num_cus, s);
+    case 4: return launch_pair_m<4>(a, num_cus, s);
     default: return hipErrorInvalidValue;
   }
 }

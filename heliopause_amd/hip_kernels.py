@@ -107,6 +107,11 @@ def _declare_optional(L: ctypes.CDLL) -> None:
     i32 = ctypes.c_int32
     L.hp_hip_set_matvec_kernel.argtypes = [i32]
     L.hp_hip_set_matvec_kernel.restype = i32
+    L.hp_hip_matmul_geglu.argtypes = [_u64, _u64, ctypes.c_void_p, _sz, _sz, _sz, ctypes.c_void_p, _sz]
+    L.hp_hip_matmul_geglu.restype = i32
+    L.hp_hip_matmul_geglu_device.argtypes = [_u64, _u64, ctypes.c_void_p, _sz, _sz, _sz, ctypes.c_void_p, _sz,
+                                             ctypes.c_void_p]
+    L.hp_hip_matmul_geglu_device.restype = i32
     vp = ctypes.c_void_p
     L.hp_hip_matmul_topk.argtypes = [_u64, vp, _sz, _sz, _sz, _sz, ctypes.c_double, vp, vp, _sz]
     L.hp_hip_topk.argtypes = [vp, _sz, _sz, _sz, ctypes.c_double, vp, vp, _sz]
@@ -334,6 +339,34 @@ def matMulQuantizedHipResidentTopK(handle: HipQuantizedWeightHandle, input_colum
                                     float(softcap), ids.ctypes.data, vals.ctypes.data, ids.size)
     assertHipOk(code, "matMulQuantizedResidentTopK")
     return _topk_result(ids, vals, handle.rowCount, top_k)
+
+
+def matMulGegluHipResident(gate: HipQuantizedWeightHandle, up: HipQuantizedWeightHandle, input_columns,
+                           input_size: int, column_count: int) -> np.ndarray:
+    """forwardFfn's gate/up batch + GeGLU (layers.ts:432-456) on the GPU:
+    fround(gelu(gate . x) * (up . x)), [column_count][rows]; one launch for a
+    single column of large projections."""
+    for h in (gate, up):
+        if h.released:
+            raise RuntimeError(f"Resident quantized matmul handle {h.handle} is not available")
+    x = _f32(input_columns)
+    if gate.inputSize != input_size or up.inputSize != input_size or x.size != input_size * column_count:
+        raise ValueError(f"Resident quantized matmul input shape mismatch: {x.size}")
+    if gate.rowCount != up.rowCount:
+        raise ValueError("gate and up row counts differ")
+    out = np.empty(gate.rowCount * column_count, dtype=np.float32)
+    code = lib().hp_hip_matmul_geglu(gate.handle, up.handle, x.ctypes.data, x.size, input_size, column_count,
+                                     out.ctypes.data, out.size)
+    assertHipOk(code, "matMulGeglu")
+    return out
+
+
+def matmul_geglu_device(gate: int, up: int, d_input: int, input_size: int, column_count: int, d_output: int,
+                        rows: int, stream: int = 0) -> None:
+    """Device-pointer gate/up + GeGLU (asynchronous on `stream`)."""
+    assertHipOk(lib().hp_hip_matmul_geglu_device(gate, up, d_input, input_size * column_count, input_size,
+                                                 column_count, d_output, rows * column_count, stream or None),
+                "matMulGegluDevice")
 
 
 def gegluHip(gate, up) -> np.ndarray:

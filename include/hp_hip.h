@@ -139,6 +139,20 @@ int32_t hp_hip_topk_device(const float *d_logits, size_t rows, size_t n, size_t 
 int32_t hp_hip_geglu(const float *gate, const float *up, size_t n, float *output);
 int32_t hp_hip_geglu_device(const float *d_gate, const float *d_up, size_t n, float *d_output, void *stream);
 
+/* FFN gate/up + GeGLU: forwardFfn's matMulWeightBatch([gate, up]) followed
+ * by its GeGLU loop (layers.ts:432-456): output[m][r] =
+ * fround(gelu(gate_m . x)[r] * (up_m . x)[r]), bit-exact.  gate and up need
+ * the same input size and row count.  With one column on large projections
+ * it is a single launch: the gate and up sums of a row finish in the same
+ * lane, which applies GeGLU and writes only the product; otherwise the two
+ * projections run as one launch and GeGLU as a second.  output_len =
+ * column_count * rows. */
+int32_t hp_hip_matmul_geglu(uint64_t gate, uint64_t up, const float *input, size_t input_len, size_t input_size,
+                            size_t column_count, float *output, size_t output_len);
+int32_t hp_hip_matmul_geglu_device(uint64_t gate, uint64_t up, const float *d_input, size_t input_len,
+                                   size_t input_size, size_t column_count, float *d_output, size_t output_len,
+                                   void *stream);
+
 /* Dequantise rows [row_start, row_start + row_count) of a handle into f32
  * [row_count][input_size] (lib.rs:1630-1664, 1709-1744; bit-exact).  Test
  * hook proving the resident layout is lossless. */

@@ -113,3 +113,30 @@ def test_geglu_bit_exact(hip, oracle):
     ref = oracle.geglu(gate, up)
     diff = np.flatnonzero(got.view(np.uint32) != ref.view(np.uint32))
     assert diff.size == 0, (diff[:5], gate[diff[:5]], got[diff[:5]], ref[diff[:5]])
+
+
+@pytest.mark.parametrize("kernel", [0, 1, 2, 3], ids=["auto", "valu-fused", "mfma", "half"])
+@pytest.mark.parametrize("rows,k,m", [(600, 2560, 1), (610, 2560, 3), (60, 10240, 1)])
+def test_matmul_geglu_bit_exact(hip, oracle, kernel, rows, k, m):
+    """gate/up + GeGLU (layers.ts:432-456) through hp_hip_matmul_geglu: the
+    fused single launch (vector ALU, up to four columns) and the
+    two-launch path of the other kernels against the oracle."""
+    print(f"matmul_geglu kernel={kernel} rows={rows} k={k} m={m}", flush=True)
+    seed = S.derive(S.BASE_SEED, "ffn-geglu", rows, k, m)
+    wg = S.q4_k_blocks(S.derive(seed, "g"), rows, k)
+    wu = S.q4_k_blocks(S.derive(seed, "u"), rows, k)
+    x = S.activations(seed, m, k)
+    hg = hip.createHipQuantizedWeightHandle("Q4_K", wg, k, rows)
+    hu = hip.createHipQuantizedWeightHandle("Q4_K", wu, k, rows)
+    hip.setMatvecKernel(kernel)
+    try:
+        got = hip.matMulGegluHipResident(hg, hu, x, k, m).reshape(m, rows)
+    finally:
+        hip.setMatvecKernel(0)
+        hip.releaseHipQuantizedWeightHandle(hg)
+        hip.releaseHipQuantizedWeightHandle(hu)
+    g = oracle.matmul(1, wg, x, rows)
+    u = oracle.matmul(1, wu, x, rows)
+    ref = oracle.geglu(g.reshape(-1), u.reshape(-1)).reshape(m, rows)
+    bad = np.flatnonzero(got.view(np.uint32) != ref.view(np.uint32))
+    assert bad.size == 0, (bad[:5], got.reshape(-1)[bad[:5]], ref.reshape(-1)[bad[:5]])
