@@ -17,6 +17,9 @@ PKG = Path(__file__).resolve().parent
 CSRC = PKG / "csrc"
 BUILD = PKG / "_build"
 LIB = PKG / "libhp_hip.so"
+NAPI_SRC = PKG / "napi" / "hp_hip_napi.c"
+NAPI_ADDON = PKG / "napi" / "hp_hip.node"
+NODE_INCLUDE = Path(os.environ.get("NODE_INCLUDE", "/usr/include/node"))
 SOURCES = ["q8k.hip", "kquant_matvec.hip", "kquant_mfma.hip", "repack.hip", "topk.hip", "geglu.hip", "capi.hip"]
 
 HIPCC = os.environ.get("HIPCC", shutil.which("hipcc") or "/opt/rocm/bin/hipcc")
@@ -63,5 +66,30 @@ def build(jobs: int | None = None) -> Path:
     return LIB
 
 
+def build_napi() -> Path | None:
+    """Node N-API addon over libhp_hip.so (heliopause_amd/napi/hp_hip.node).
+
+    Plain C against node_api.h; it links the runner with an rpath of its
+    parent directory, so the two files travel together.  Returns None (and
+    says so) when the Node headers are not installed.
+    """
+    if not (NODE_INCLUDE / "node_api.h").exists():
+        sys.stderr.write(f"node_api.h not found under {NODE_INCLUDE}; N-API addon not built\n")
+        return None
+    cc = os.environ.get("CC", shutil.which("gcc") or "cc")
+    tmp = NAPI_ADDON.with_suffix(".node.tmp")
+    cmd = [cc, "-O2", "-fPIC", "-shared", "-std=c11", "-Wall", "-Wextra", "-Wno-unused-parameter",
+           f"-I{NODE_INCLUDE}", f"-I{PKG.parent / 'include'}", str(NAPI_SRC), "-o", str(tmp),
+           f"-L{PKG}", "-lhp_hip", "-Wl,-rpath,$ORIGIN/.."]
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError(f"N-API addon build failed:\n{r.stdout}\n{r.stderr}")
+    if r.stderr.strip():
+        sys.stderr.write(r.stderr)
+    os.replace(tmp, NAPI_ADDON)
+    return NAPI_ADDON
+
+
 if __name__ == "__main__":
     print(build())
+    print(build_napi())

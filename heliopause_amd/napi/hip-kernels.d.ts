@@ -1,0 +1,73 @@
+// Types of hip-kernels.js: the HIP runner's resident-weight API, shaped like
+// packages/engine/src/runner/wasm/wasm-kernels.ts (WasmQuantizedWeightHandle
+// 387-397, WasmResidentWeightStats 399-402, WasmSupport 404-408).
+
+export type QuantizedType = "Q4_0" | "Q4_K" | "Q5_K" | "Q6_K" | "IQ4_XS" | "Q8_0";
+
+export type HipQuantizedWeightHandle = {
+  handle: bigint;
+  type: QuantizedType;
+  byteLength: number;
+  rowCount: number;
+  inputSize: number;
+  released: boolean;
+};
+
+export type HipResidentWeightStats = {
+  instanceCount: number;
+  residentBytes: number;
+  handleCount: number;
+  scratchBytes: number;
+  matmulCalls: number;
+  kernelLaunches: number;
+  device: number;
+  computeUnits: number;
+};
+
+export type HipSupport = {
+  available: boolean;
+  reason?: "module-missing" | "device-missing";
+  error?: string;
+};
+
+export type TopKCandidate = { id: number; value: number };
+
+export function checkHipSupport(): Promise<HipSupport>;
+export function quantizedTypeId(type: QuantizedType): number | undefined;
+export function assertHipOk(code: number, kernelName: string, detail?: string): void;
+export function createHipQuantizedWeightHandle(
+  type: QuantizedType,
+  weightBytes: Uint8Array,
+  inputSize: number,
+  rowCount: number,
+): Promise<HipQuantizedWeightHandle | undefined>;
+export function releaseHipQuantizedWeightHandle(handle: HipQuantizedWeightHandle): void;
+export function hipResidentWeightStats(): HipResidentWeightStats;
+export function matMulQuantizedHipResident(
+  handle: HipQuantizedWeightHandle,
+  inputColumns: Float32Array,
+  inputSize: number,
+  rowCount: number,
+  columnCount: number,
+): Promise<Float32Array>;
+export function matMulQuantizedHipResidentMulti(
+  handles: readonly HipQuantizedWeightHandle[],
+  inputColumns: Float32Array,
+  inputSize: number,
+  columnCount: number,
+): Promise<Float32Array[] | undefined>;
+export function matMulQuantizedHipResidentTopK(
+  handle: HipQuantizedWeightHandle,
+  inputColumns: Float32Array,
+  inputSize: number,
+  columnCount: number,
+  topK: number,
+  softcap?: number,
+): Promise<TopKCandidate[][]>;
+export function matMulGegluHipResident(
+  gate: HipQuantizedWeightHandle,
+  up: HipQuantizedWeightHandle,
+  inputColumns: Float32Array,
+  inputSize: number,
+  columnCount: number,
+): Promise<Float32Array>;
