@@ -6,12 +6,16 @@
 // activation/output lengths) and the resident wrappers in
 // packages/engine/src/runner/wasm/wasm-kernels.ts (520-749: handle shape must
 // match the call).
+#include "../../include/hp_gguf.h"
 #include "../../include/hp_hip.h"
 #include "hp_common.h"
 
+#include <algorithm>
+#include <atomic>
 #include <cmath>
 #include <mutex>
 #include <string>
+#include <thread>
 #include <vector>
 
 namespace {
@@ -54,6 +58,14 @@ struct State {
   bool profiling = false;
   ProfileSlot prof[HP_KERNEL_COUNT];
   std::vector<hipEvent_t> event_pool;
+  // GGUF loader: pinned staging (two chunks per reader), one copy stream and
+  // two events per reader, and the device staging of a batch of tensors.
+  uint8_t *pinned = nullptr;
+  size_t pinned_cap = 0;
+  std::vector<hipStream_t> copy_streams;
+  std::vector<hipEvent_t> copy_events;
+  uint8_t *load_staging = nullptr;
+  size_t load_staging_cap = 0;
 };
 
 State &st() {
@@ -368,8 +380,11 @@ int32_t geglu_pair_check(uint64_t gate, uint64_t up, size_t input_len, size_t in
   return HP_OK;
 }
 
+// Uploads one weight.  With sync == false (device source only) the repack is
+// left queued on the library stream; the caller synchronises before it
+// reuses or frees the source.
 int32_t upload_common(int32_t type_id, const void *src, bool src_device, size_t weight_len, size_t input_size,
-                      size_t row_count, uint64_t *out_handle) {
+                      size_t row_count, uint64_t *out_handle, bool sync = true) {
   State &s = st();
   if (!out_handle || !src) return fail(HP_ERR_ARG, "null pointer");
   int32_t rc = ensure_init(s.ready ? s.device : 0);
@@ -381,6 +396,8 @@ int32_t upload_common(int32_t type_id, const void *src, bool src_device, size_t 
   if (weight_len != sat_mul(rb, row_count)) return fail(HP_ERR_SHAPE, "weight byte length mismatch");
   if (row_count > (size_t)0x7fffffff / 64 || input_size / kQK > 4096) return fail(HP_ERR_SHAPE, "weight too large");
 
+  if (src_device && reinterpret_cast<uintptr_t>(src) % 16 != 0)
+    return fail(HP_ERR_ARG, "device weight buffer must be 16-byte aligned");
   Handle h;
   h.type = type_id;
   h.input_size = input_size;
@@ -388,11 +405,15 @@ int32_t upload_common(int32_t type_id, const void *src, bool src_device, size_t 
   h.byte_length = weight_len;
   h.g = choose_geometry((int)(input_size / kQK));
   h.tiles = (int)((row_count + h.g.R - 1) / h.g.R);
-  if (hipMalloc((void **)&h.data, weight_len) != hipSuccess) return fail(HP_ERR_OOM, "weight allocation failed");
+  // one allocation holds both layouts: tiles (+ Q6_K d plane), then segments
+  const int nb = (int)(input_size / kQK);
+  const size_t tile_bytes = (weight_len + 255) & ~(size_t)255;
+  h.seg_bytes = mfma_segment_bytes(type_id, (int)row_count, nb);
+  if (hipMalloc((void **)&h.data, tile_bytes + h.seg_bytes) != hipSuccess)
+    return fail(HP_ERR_OOM, "weight allocation failed");
+  h.segs = h.data + tile_bytes;
   if (type_id == kTypeQ6K) h.dplane = reinterpret_cast<uint16_t *>(h.data + row_count * (input_size / kQK) * 208);
 
-  if (src_device && reinterpret_cast<uintptr_t>(src) % 16 != 0)
-    return fail(HP_ERR_ARG, "device weight buffer must be 16-byte aligned");
   const uint8_t *raw = static_cast<const uint8_t *>(src);
   uint8_t *staging = nullptr;
   if (!src_device) {
@@ -408,22 +429,13 @@ int32_t upload_common(int32_t type_id, const void *src, bool src_device, size_t 
     }
     raw = staging;
   }
-  const int nb = (int)(input_size / kQK);
-  h.seg_bytes = mfma_segment_bytes(type_id, (int)row_count, nb);
-  hipError_t e = hipMalloc((void **)&h.segs, h.seg_bytes);
-  if (e != hipSuccess) {
-    h.segs = nullptr;
-    if (staging) (void)hipFree(staging);
-    (void)hipFree(h.data);
-    return fail(HP_ERR_OOM, "weight allocation failed");
-  }
-  e = launch_repack(type_id, raw, (int)row_count, h.g, h.data, h.dplane, s.stream);
+  hipError_t e = launch_repack(type_id, raw, (int)row_count, h.g, h.data, h.dplane, s.stream);
   if (e == hipSuccess) e = launch_repack_mfma(type_id, raw, (int)row_count, nb, h.segs, s.stream);
-  if (e == hipSuccess) e = hipStreamSynchronize(s.stream);
+  if (e == hipSuccess && (sync || !src_device)) e = hipStreamSynchronize(s.stream);
   if (staging) (void)hipFree(staging);
   if (e != hipSuccess) {
+    (void)hipStreamSynchronize(s.stream);
     (void)hipFree(h.data);
-    (void)hipFree(h.segs);
     return hip_fail(e, "repack");
   }
   // reuse a free slot
@@ -439,6 +451,133 @@ int32_t upload_common(int32_t type_id, const void *src, bool src_device, size_t 
   s.handles[slot] = h;
   *out_handle = ((uint64_t)h.generation << 32) | (uint64_t)(slot + 1);
   return HP_OK;
+}
+
+// ---- GGUF -> HBM loader ----------------------------------------------------
+// Tensor bytes go file -> pinned host chunk (pread) -> device staging
+// (hipMemcpyAsync) -> repack into the resident layouts.  Readers work on
+// interleaved chunks (chunk c on reader c % n), each with two pinned chunks
+// and its own stream, so one chunk's DMA overlaps the next chunk's read.
+constexpr size_t kLoadChunk = 8u << 20;
+constexpr int kLoadMaxReaders = 8;
+constexpr size_t kLoadBatch = 1ull << 30;  // device staging per batch of tensors
+
+void release_loader(State &s) {
+  for (hipStream_t q : s.copy_streams) (void)hipStreamDestroy(q);
+  for (hipEvent_t e : s.copy_events) (void)hipEventDestroy(e);
+  s.copy_streams.clear();
+  s.copy_events.clear();
+  if (s.pinned) (void)hipHostFree(s.pinned);
+  s.pinned = nullptr;
+  s.pinned_cap = 0;
+  if (s.load_staging) (void)hipFree(s.load_staging);
+  s.load_staging = nullptr;
+  s.load_staging_cap = 0;
+}
+
+int load_readers() {
+  const unsigned hw = std::thread::hardware_concurrency();
+  const int n = hw == 0 ? 4 : (int)hw;
+  return std::max(1, std::min(kLoadMaxReaders, n));
+}
+
+int32_t ensure_loader(State &s, int readers) {
+  const size_t need = (size_t)readers * 2 * kLoadChunk;
+  if (s.pinned_cap < need) {
+    if (s.pinned) (void)hipHostFree(s.pinned);
+    s.pinned = nullptr;
+    s.pinned_cap = 0;
+    HP_HIP_TRY(hipHostMalloc((void **)&s.pinned, need, hipHostMallocDefault));
+    s.pinned_cap = need;
+  }
+  while ((int)s.copy_streams.size() < readers) {
+    hipStream_t q;
+    HP_HIP_TRY(hipStreamCreateWithFlags(&q, hipStreamNonBlocking));
+    s.copy_streams.push_back(q);
+  }
+  while ((int)s.copy_events.size() < 2 * readers) {
+    hipEvent_t e;
+    HP_HIP_TRY(hipEventCreateWithFlags(&e, hipEventDisableTiming));
+    s.copy_events.push_back(e);
+  }
+  return HP_OK;
+}
+
+struct CopyJob {
+  uint64_t file_offset;
+  size_t length;
+  uint8_t *dst;
+};
+
+// Copies every job's file range into device memory; returns once all copies
+// have landed.  Jobs are cut into kLoadChunk pieces dealt round-robin.
+int32_t stream_ranges(const hp_gguf_t *g, const std::vector<CopyJob> &jobs) {
+  State &s = st();
+  struct Piece {
+    uint64_t off;
+    size_t n;
+    uint8_t *dst;
+  };
+  std::vector<Piece> pieces;
+  for (const CopyJob &j : jobs)
+    for (size_t done = 0; done < j.length; done += kLoadChunk)
+      pieces.push_back({j.file_offset + done, std::min(kLoadChunk, j.length - done), j.dst + done});
+  if (pieces.empty()) return HP_OK;
+  const int readers = (int)std::min<size_t>((size_t)load_readers(), pieces.size());
+  int32_t rc = ensure_loader(s, readers);
+  if (rc != HP_OK) return rc;
+  std::atomic<int32_t> status{HP_OK};
+  std::mutex msg_mu;
+  std::string msg;
+  auto note = [&](int32_t code, const std::string &m) {
+    int32_t ok = HP_OK;
+    if (status.compare_exchange_strong(ok, code)) {
+      std::lock_guard<std::mutex> lk(msg_mu);
+      msg = m;
+    }
+  };
+  auto reader = [&](int t) {
+    hipStream_t q = s.copy_streams[t];
+    bool used[2] = {false, false};
+    for (size_t p = (size_t)t, round = 0; p < pieces.size(); p += (size_t)readers, round++) {
+      if (status.load() != HP_OK) break;
+      const int b = (int)(round & 1);
+      hipEvent_t ev = s.copy_events[2 * t + b];
+      uint8_t *buf = s.pinned + ((size_t)t * 2 + b) * kLoadChunk;
+      if (used[b] && hipEventSynchronize(ev) != hipSuccess) {
+        note(HP_ERR_HIP, "hipEventSynchronize(loader)");
+        break;
+      }
+      if (hp_gguf_read(g, pieces[p].off, buf, pieces[p].n) != 0) {
+        note(HP_ERR_IO, "read of " + std::to_string(pieces[p].n) + " bytes at offset " + std::to_string(pieces[p].off) +
+                            " failed");
+        break;
+      }
+      hipError_t e = hipMemcpyAsync(pieces[p].dst, buf, pieces[p].n, hipMemcpyHostToDevice, q);
+      if (e == hipSuccess) e = hipEventRecord(ev, q);
+      if (e != hipSuccess) {
+        note(HP_ERR_HIP, std::string("hipMemcpyAsync(loader): ") + hipGetErrorString(e));
+        break;
+      }
+      used[b] = true;
+    }
+    if (hipStreamSynchronize(q) != hipSuccess) note(HP_ERR_HIP, "hipStreamSynchronize(loader)");
+  };
+  std::vector<std::thread> pool;
+  for (int t = 1; t < readers; t++) pool.emplace_back(reader, t);
+  reader(0);
+  for (std::thread &th : pool) th.join();
+  if (status.load() != HP_OK) return fail(status.load(), msg);
+  return HP_OK;
+}
+
+// ggml type id -> runner type id (lib.rs:12-17), 0 when the runner has none.
+int32_t runner_type(uint32_t ggml) {
+  switch (ggml) {
+    case HP_GGML_Q4_K: return kTypeQ4K;
+    case HP_GGML_Q6_K: return kTypeQ6K;
+    default: return 0;
+  }
 }
 
 int32_t topk_check(size_t rows, size_t n, size_t k) {
@@ -499,6 +638,8 @@ const char *hp_hip_status_string(int32_t status) {
     case HP_ERR_ARG: return "invalid argument";
     case HP_ERR_NODEV: return "no GPU available";
     case HP_ERR_OOM: return "device out of memory";
+    case HP_ERR_FORMAT: return "malformed GGUF";
+    case HP_ERR_IO: return "file read error";
     default: return "unknown status";
   }
 }
@@ -527,8 +668,7 @@ int32_t hp_hip_shutdown(void) {
   (void)hipStreamSynchronize(s.stream);
   for (auto &h : s.handles)
     if (h.live) {
-      (void)hipFree(h.data);
-      (void)hipFree(h.segs);
+      (void)hipFree(h.data);  // both layouts
       h.live = false;
     }
   if (s.io_in) (void)hipFree(s.io_in);
@@ -546,6 +686,7 @@ int32_t hp_hip_shutdown(void) {
   prof_collect();
   for (hipEvent_t e : s.event_pool) (void)hipEventDestroy(e);
   s.event_pool.clear();
+  release_loader(s);
   (void)hipStreamDestroy(s.stream);
   s.stream = nullptr;
   s.ready = false;
@@ -564,14 +705,94 @@ int32_t hp_hip_weight_upload_device(int32_t type_id, const void *d_weight, size_
   return upload_common(type_id, d_weight, true, weight_len, input_size, row_count, out_handle);
 }
 
+int32_t hp_hip_weight_upload_gguf(const hp_gguf_t *g, size_t count, const uint64_t *tensor_indices,
+                                  uint64_t *handles, int32_t *statuses) {
+  State &s = st();
+  std::lock_guard<std::recursive_mutex> lock(s.mu);
+  if (!g || (count && (!tensor_indices || !handles || !statuses))) return fail(HP_ERR_ARG, "null pointer");
+  int32_t rc = ensure_init(s.ready ? s.device : 0);
+  if (rc != HP_OK) return rc;
+  uint64_t tensor_count = 0, file_size = 0;
+  hp_gguf_header(g, nullptr, &tensor_count, nullptr, nullptr, nullptr, &file_size);
+  // validate everything first: the call uploads all or nothing
+  std::vector<hp_gguf_tensor_t> info(count);
+  for (size_t i = 0; i < count; i++) {
+    handles[i] = 0;
+    statuses[i] = HP_ERR_TYPE;
+    if (tensor_indices[i] >= tensor_count) return fail(HP_ERR_ARG, "tensor index out of range");
+    hp_gguf_tensor_info(g, tensor_indices[i], &info[i]);
+    const hp_gguf_tensor_t &t = info[i];
+    const int32_t type = runner_type(t.type_id);
+    if (type == 0) continue;  // the caller falls back, as for createWasmQuantizedWeightHandle -> undefined
+    const std::string name(t.name, t.name_length);
+    const size_t input_size = t.n_dims >= 1 ? t.dims[0] : 0, rows = t.n_dims >= 2 ? t.dims[1] : 0;
+    const size_t rb = row_bytes_for(type, input_size);
+    if (t.n_dims < 2 || !t.storage_known || rb == 0 || t.byte_length != sat_mul(rb, rows))
+      return fail(HP_ERR_SHAPE, "tensor " + name + " is not a [rows][input] weight of whole blocks");
+    if (t.data_offset > file_size || t.byte_length > file_size - t.data_offset)
+      return fail(HP_ERR_IO, "tensor " + name + " data runs past the end of the file");
+    statuses[i] = HP_OK;
+  }
+  // batches of tensors whose bytes fit the device staging (a larger tensor goes alone)
+  size_t begin = 0;
+  while (begin < count) {
+    size_t end = begin, bytes = 0;
+    while (end < count && (statuses[end] != HP_OK || bytes == 0 || bytes + info[end].byte_length <= kLoadBatch)) {
+      if (statuses[end] == HP_OK) bytes += (bytes % 256 ? 256 - bytes % 256 : 0) + info[end].byte_length;
+      end++;
+    }
+    if (bytes > 0) {
+      rc = grow((void **)&s.load_staging, &s.load_staging_cap, bytes);
+      std::vector<CopyJob> jobs;
+      std::vector<size_t> at(end - begin);
+      size_t off = 0;
+      for (size_t i = begin; i < end && rc == HP_OK; i++) {
+        if (statuses[i] != HP_OK) continue;
+        off = (off + 255) & ~(size_t)255;
+        at[i - begin] = off;
+        jobs.push_back({info[i].data_offset, (size_t)info[i].byte_length, s.load_staging + off});
+        off += info[i].byte_length;
+      }
+      if (rc == HP_OK) rc = stream_ranges(g, jobs);
+      for (size_t i = begin; i < end && rc == HP_OK; i++) {
+        if (statuses[i] != HP_OK) continue;
+        const hp_gguf_tensor_t &t = info[i];
+        rc = upload_common(runner_type(t.type_id), s.load_staging + at[i - begin], true, t.byte_length, t.dims[0],
+                           t.dims[1], &handles[i], false);
+      }
+      // the next batch overwrites the staging the queued repacks read
+      if (rc == HP_OK && hipStreamSynchronize(s.stream) != hipSuccess) rc = fail(HP_ERR_HIP, "repack (GGUF load)");
+    }
+    if (rc != HP_OK) {
+      const std::string why = g_last_error;
+      (void)hipStreamSynchronize(s.stream);
+      for (size_t i = 0; i < count; i++)
+        if (handles[i]) {
+          Handle *h = lookup(handles[i]);
+          if (h) {
+            (void)hipFree(h->data);
+            h->data = h->segs = nullptr;
+            h->dplane = nullptr;
+            h->live = false;
+          }
+          handles[i] = 0;
+        }
+      release_loader(s);
+      return fail(rc, why);
+    }
+    begin = end;
+  }
+  release_loader(s);  // staging is only needed while loading
+  return HP_OK;
+}
+
 int32_t hp_hip_weight_release(uint64_t handle) {
   State &s = st();
   std::lock_guard<std::recursive_mutex> lock(s.mu);
   Handle *h = lookup(handle);
   if (!h) return fail(HP_ERR_HANDLE, "unknown weight handle");
   (void)hipStreamSynchronize(s.stream);
-  (void)hipFree(h->data);
-  (void)hipFree(h->segs);
+  (void)hipFree(h->data);  // both layouts
   h->data = nullptr;
   h->segs = nullptr;
   h->dplane = nullptr;

@@ -496,65 +496,92 @@ __global__ __launch_bounds__(256) void kquant_mfma_kernel(const MfmaArgs a) {
   }
 }
 
-// One thread per (tile, row-in-tile, block): copies / transposes one GGUF
-// block into the segment layout above (zeros for rows past the weight).
+// One thread per (tile, block, row-in-tile), the row fastest: the 16 lanes of
+// one (tile, block) write whole 256-byte runs of its segment.  Each thread
+// loads its GGUF block once with vector loads, then builds every output word
+// from registers (zeros for rows past the weight).
 __global__ void repack_mfma_kernel(const uint8_t *__restrict__ raw, int type, int rows, int nb,
                                    uint8_t *__restrict__ segs) {
   const long long tid = (long long)blockIdx.x * blockDim.x + threadIdx.x;
   const int tiles = (rows + 15) / 16;
   if (tid >= (long long)tiles * 16 * nb) return;
-  const int b = (int)(tid % nb);
-  const int rho = (int)((tid / nb) % 16);
-  const int T = (int)(tid / ((long long)nb * 16));
+  const int rho = (int)(tid & 15);
+  const int b = (int)((tid >> 4) % nb);
+  const int T = (int)((tid >> 4) / nb);
   const int r = T * 16 + rho;
-  const bool q4 = type == kTypeQ4K;
-  const int bb = q4 ? 144 : 210, segb = q4 ? 2304 : 3360;
-  uint8_t *seg = segs + ((size_t)b * tiles + T) * segb;
-  const uint8_t *blk = r < rows ? raw + ((size_t)r * nb + b) * bb : nullptr;
-  auto at = [&](int o) -> uint32_t { return blk ? blk[o] : 0u; };
-  if (q4) {
-    for (int o = 0; o < 16; o++) seg[16 * rho + o] = (uint8_t)at(o);
-    // element e = 32j + 8c + l: byte 16 + 32*(j/2) + 8c + l, nibble j%2
+  const bool live = r < rows;
+  if (type == kTypeQ4K) {
+    uint8_t *seg = segs + ((size_t)b * tiles + T) * 2304;
+    uint32_t w[36];  // the 144-byte block as 36 little-endian words
+    const uint4 *src = reinterpret_cast<const uint4 *>(raw + ((size_t)(live ? r : 0) * nb + b) * 144);
+#pragma unroll
+    for (int i = 0; i < 9; i++) {
+      const uint4 v = live ? src[i] : make_uint4(0, 0, 0, 0);
+      w[4 * i] = v.x;
+      w[4 * i + 1] = v.y;
+      w[4 * i + 2] = v.z;
+      w[4 * i + 3] = v.w;
+    }
+    auto byte = [&](int o) -> uint32_t { return (w[o >> 2] >> (8 * (o & 3))) & 0xFFu; };
+    reinterpret_cast<uint4 *>(seg)[rho] = make_uint4(w[0], w[1], w[2], w[3]);
+    // lane (c, i = 16qq + rho), element class l = 2qq + c: byte 4u + cc =
+    // block byte 16 + 32u + 8cc + l (nibbles of j = 2u, 2u + 1)
+#pragma unroll
     for (int qq = 0; qq < 4; qq++)
-      for (int c = 0; c < 2; c++) {
-        const int l = 2 * qq + c, i = qq * 16 + rho;
-        for (int u = 0; u < 4; u++)
-          for (int cc = 0; cc < 4; cc++) {
-            // j = 2u and 2u+1 share byte 16 + 32u + 8cc + l (low / high nibble)
-            seg[256 + (c * 64 + i) * 16 + 4 * u + cc] = (uint8_t)at(16 + 32 * u + 8 * cc + l);
-          }
-      }
-  } else {
-    for (int o = 0; o < 16; o++) seg[16 * rho + o] = (uint8_t)at(192 + o);
-    seg[256 + 2 * rho] = (uint8_t)at(208);
-    seg[256 + 2 * rho + 1] = (uint8_t)at(209);
-    // q6(e): e = 128h + 32t + l5 -> low nibble ql[64h + l5 + 32(t&1)] >> 4(t>>1),
-    // high 2 bits qh[32h + l5] >> 2t
-    auto q6 = [&](int e) -> uint32_t {
-      const int h = e >> 7, t5 = (e & 127) >> 5, l5 = e & 31;
-      const uint32_t lo = (at(64 * h + l5 + 32 * (t5 & 1)) >> (4 * (t5 >> 1))) & 15u;
-      const uint32_t hi = (at(128 + 32 * h + l5) >> (2 * t5)) & 3u;
-      return lo | (hi << 4);
-    };
-    for (int qq = 0; qq < 4; qq++) {
-      const int i = qq * 16 + rho;
+#pragma unroll
       for (int c = 0; c < 2; c++) {
         const int l = 2 * qq + c;
+        uint32_t o[4];
+#pragma unroll
         for (int u = 0; u < 4; u++)
-          for (int cc = 0; cc < 4; cc++) {
-            const uint32_t v = (q6(32 * (2 * u) + 8 * cc + l) & 15u) | ((q6(32 * (2 * u + 1) + 8 * cc + l) & 15u) << 4);
-            seg[288 + (c * 64 + i) * 16 + 4 * u + cc] = (uint8_t)v;
-          }
+          o[u] = byte(16 + 32 * u + l) | (byte(16 + 32 * u + 8 + l) << 8) | (byte(16 + 32 * u + 16 + l) << 16) |
+                 (byte(16 + 32 * u + 24 + l) << 24);
+        reinterpret_cast<uint4 *>(seg + 256)[c * 64 + qq * 16 + rho] = make_uint4(o[0], o[1], o[2], o[3]);
       }
-      for (int cls = 0; cls < 2; cls++) {
-        const int l = 2 * qq + cls;
-        for (int h = 0; h < 2; h++)
+  } else {
+    uint8_t *seg = segs + ((size_t)b * tiles + T) * 3360;
+    uint32_t h[105];  // the 210-byte block as 105 little-endian half-words (2-byte aligned)
+    const uint16_t *src = reinterpret_cast<const uint16_t *>(raw + ((size_t)(live ? r : 0) * nb + b) * 210);
+#pragma unroll
+    for (int i = 0; i < 105; i++) h[i] = live ? src[i] : 0u;
+    auto byte = [&](int o) -> uint32_t { return (h[o >> 1] >> (8 * (o & 1))) & 0xFFu; };
+    auto word = [&](int o) -> uint32_t { return h[o >> 1] | (h[(o >> 1) + 1] << 16); };  // o even
+    reinterpret_cast<uint4 *>(seg)[rho] = make_uint4(word(192), word(196), word(200), word(204));
+    reinterpret_cast<uint16_t *>(seg + 256)[rho] = (uint16_t)h[104];
+    // q6 of element e = 128h + 32t + l5: low nibble of ql[64h + l5 + 32(t&1)]
+    // (shifted by 4(t>>1)), high 2 bits qh[32h + l5] >> 2t.  For lane class
+    // l: nibble byte 4u + cc pairs j = 2u (low) and 2u + 1 (high nibble); the
+    // high-bit byte 4(2cls + hh) + cc is qh[32hh + 8cc + l] as stored.
+#pragma unroll
+    for (int qq = 0; qq < 4; qq++) {
+#pragma unroll
+      for (int c = 0; c < 2; c++) {
+        const int l = 2 * qq + c;
+        uint32_t o[4];
+#pragma unroll
+        for (int u = 0; u < 4; u++) {
+          const int hh = u >> 1, sh = 4 * (u & 1);
+          uint32_t v = 0;
+#pragma unroll
           for (int cc = 0; cc < 4; cc++) {
-            uint32_t v = 0;
-            for (int jj = 0; jj < 4; jj++) v |= (q6(32 * (4 * h + jj) + 8 * cc + l) >> 4) << (2 * jj);
-            seg[288 + (2 * 64 + i) * 16 + 4 * (2 * cls + h) + cc] = (uint8_t)v;
+            const uint32_t lo = (byte(64 * hh + 8 * cc + l) >> sh) & 15u;
+            const uint32_t hi = (byte(64 * hh + 32 + 8 * cc + l) >> sh) & 15u;
+            v |= (lo | (hi << 4)) << (8 * cc);
           }
+          o[u] = v;
+        }
+        reinterpret_cast<uint4 *>(seg + 288)[c * 64 + qq * 16 + rho] = make_uint4(o[0], o[1], o[2], o[3]);
       }
+      uint32_t q[4];
+#pragma unroll
+      for (int cls = 0; cls < 2; cls++)
+#pragma unroll
+        for (int hh = 0; hh < 2; hh++) {
+          const int l = 2 * qq + cls;
+          q[2 * cls + hh] = byte(128 + 32 * hh + l) | (byte(128 + 32 * hh + 8 + l) << 8) |
+                            (byte(128 + 32 * hh + 16 + l) << 16) | (byte(128 + 32 * hh + 24 + l) << 24);
+        }
+      reinterpret_cast<uint4 *>(seg + 288)[128 + qq * 16 + rho] = make_uint4(q[0], q[1], q[2], q[3]);
     }
   }
 }

@@ -89,6 +89,20 @@ int32_t hp_hip_weight_upload(int32_t type_id, const uint8_t *weight, size_t weig
 /* Same from a device buffer already holding the GGUF bytes. */
 int32_t hp_hip_weight_upload_device(int32_t type_id, const void *d_weight, size_t weight_len, size_t input_size,
                                     size_t row_count, uint64_t *out_handle);
+/* Upload tensors of a parsed GGUF file (hp_gguf.h) straight from the file
+ * into HBM-resident handles: readWasmWeightHandle's readTensorBytes +
+ * createWasmQuantizedWeightHandle (acceleration.ts:164-201), for a batch of
+ * tensors at once.  Shape as matMulKQ8K reads it (wasm/layers.ts:758-759):
+ * input size = dims[0], rows = dims[1].  Bytes stream file -> pinned host
+ * chunks (parallel pread) -> device staging -> repack; no pageable copy.
+ * statuses[i] = HP_OK with handles[i] set, or HP_ERR_TYPE with handles[i] = 0
+ * for a block type this runner does not implement (the caller falls back).
+ * Any other failure (a tensor that is not a [rows][input] weight of whole
+ * blocks, data past the end of the file, a read or HIP error) returns that
+ * code and leaves no handle from this call. */
+struct hp_gguf;
+int32_t hp_hip_weight_upload_gguf(const struct hp_gguf *gguf, size_t count, const uint64_t *tensor_indices,
+                                  uint64_t *handles, int32_t *statuses);
 /* releaseWasmQuantizedWeightHandle (wasm-kernels.ts:576-584). */
 int32_t hp_hip_weight_release(uint64_t handle);
 int32_t hp_hip_weight_info(uint64_t handle, int32_t *type_id, size_t *input_size, size_t *row_count,
