@@ -71,3 +71,47 @@ export function matMulGegluHipResident(
   inputSize: number,
   columnCount: number,
 ): Promise<Float32Array>;
+
+// GGUF files (parseGguf's GgufMetadata shape, gguf.ts:30-37, plus byteLength).
+export type HipGgufArraySummary = { type: string; length: number; sample: HipGgufMetadataValue[]; truncated: boolean };
+export type HipGgufMetadataValue = number | boolean | string | HipGgufArraySummary;
+export type HipGgufTensorInfo = {
+  name: string;
+  dimensions: number[];
+  type: string;
+  typeId: number;
+  offset: bigint;
+  dataOffset: bigint;
+  byteLength?: number;
+};
+export type HipGgufMetadata = {
+  version: number;
+  tensorCount: number;
+  metadataCount: number;
+  metadata: Record<string, HipGgufMetadataValue>;
+  tensors: HipGgufTensorInfo[];
+  dataStart: bigint;
+  alignment: number;
+  fileSize: number;
+};
+
+export class HipGgufFile {
+  constructor(path: string, options?: { maxArraySample?: number; completeArrayKeys?: readonly string[] });
+  readonly metadata: HipGgufMetadata;
+  getTensor(name: string): HipGgufTensorInfo;
+  close(): void;
+}
+export function openHipGgufFile(
+  path: string,
+  options?: { maxArraySample?: number; completeArrayKeys?: readonly string[] },
+): HipGgufFile;
+
+export class HipGgufWeights {
+  constructor(file: HipGgufFile);
+  hits: number;
+  misses: number;
+  bytes: number;
+  upload(names: readonly string[]): Promise<Map<string, HipQuantizedWeightHandle | undefined>>;
+  handle(name: string): Promise<HipQuantizedWeightHandle | undefined>;
+  release(): void;
+}

@@ -17,6 +17,12 @@
  *   quantizedTypeId 1908-1923                  quantizedTypeId
  *   quantizedScaleValueCount 1925-1941         (its shape check, in create)
  *
+ * the GGUF path that feeds them (file -> HBM without a JS copy):
+ *   parseGguf (gguf.ts:150-215), GgufTensorReader.getTensor (tensor-reader.ts:66-72)
+ *                                              openHipGgufFile -> HipGgufFile
+ *   readWasmWeightHandle (acceleration.ts:164-201)
+ *                                              HipGgufWeights.handle / upload
+ *
  * plus the two calls the decode loop makes around the projections:
  *   forwardOutput + topK (layers.ts:381-416, runtime.ts:514-527)
  *                                              matMulQuantizedHipResidentTopK
@@ -232,7 +238,137 @@ async function matMulGegluHipResident(gate, up, inputColumns, inputSize, columnC
   return result.output;
 }
 
+/* A GGUF file parsed by the runner's reader and held open for uploads.
+ * `metadata` has parseGguf's shape (GgufMetadata, gguf.ts:30-37), with each
+ * tensor's byteLength (tensorByteLength) when its storage type is known. */
+class HipGgufFile {
+  constructor(path, options) {
+    const opts = options || {};
+    const result = native().ggufOpen(
+      path,
+      opts.maxArraySample === undefined ? 16 : opts.maxArraySample,
+      opts.completeArrayKeys || [],
+    );
+    if (result.status !== 0) {
+      throw new Error(result.error);
+    }
+    this.file = result.file;
+    this.metadata = native().ggufInfo(this.file);
+    this.tensorsByName = new Map(this.metadata.tensors.map((tensor, index) => [tensor.name, index]));
+  }
+
+  getTensor(name) {
+    const index = this.tensorsByName.get(name);
+    if (index === undefined) {
+      throw new Error(`Unknown tensor: ${name}`);
+    }
+    return this.metadata.tensors[index];
+  }
+
+  close() {
+    if (this.file) {
+      native().ggufClose(this.file);
+      this.file = undefined;
+    }
+  }
+}
+
+function openHipGgufFile(path, options) {
+  return new HipGgufFile(path, options);
+}
+
+/* Session cache of HBM-resident handles keyed by tensor name
+ * (readWasmWeightHandle, acceleration.ts:164-201): a hit returns the cached
+ * handle, a pending upload is shared, a miss uploads.  upload(names) loads
+ * many tensors in one streamed call.  Block types the runner does not
+ * implement resolve to undefined, so the engine falls back. */
+class HipGgufWeights {
+  constructor(file) {
+    this.file = file;
+    this.handles = new Map();
+    this.pending = new Map();
+    this.unsupported = new Set();
+    this.hits = 0;
+    this.misses = 0;
+    this.bytes = 0;
+  }
+
+  async upload(names) {
+    const todo = [];
+    for (const name of new Set(names)) {
+      if (!this.handles.has(name) && !this.pending.has(name) && !this.unsupported.has(name)) {
+        todo.push(name);
+      }
+    }
+    if (todo.length > 0) {
+      const tensors = todo.map((name) => this.file.getTensor(name));
+      const run = native()
+        .ggufUpload(this.file.file, todo.map((name) => this.file.tensorsByName.get(name)))
+        .then((result) => {
+          assertHipOk(result.status, "uploadGgufWeights", result.error);
+          tensors.forEach((tensor, index) => {
+            if (result.statuses[index] !== 0) {
+              this.unsupported.add(tensor.name);
+              return;
+            }
+            this.handles.set(tensor.name, {
+              handle: result.handles[index],
+              type: tensor.type,
+              byteLength: tensor.byteLength,
+              rowCount: tensor.dimensions[1],
+              inputSize: tensor.dimensions[0],
+              released: false,
+            });
+            this.bytes += tensor.byteLength;
+          });
+        });
+      const settled = run.then(() => undefined, () => undefined);
+      for (const name of todo) {
+        this.pending.set(name, settled);
+      }
+      try {
+        await run;
+      } finally {
+        for (const name of todo) {
+          this.pending.delete(name);
+        }
+      }
+    }
+    await Promise.all(names.map((name) => this.pending.get(name)).filter((p) => p !== undefined));
+    const out = new Map();
+    for (const name of names) {
+      out.set(name, this.handles.get(name));
+    }
+    return out;
+  }
+
+  async handle(name) {
+    if (this.handles.has(name) || this.unsupported.has(name)) {
+      this.hits += 1;
+      return this.handles.get(name);
+    }
+    if (this.pending.has(name)) {
+      this.hits += 1;
+      await this.pending.get(name);
+      return this.handles.get(name);
+    }
+    this.misses += 1;
+    return (await this.upload([name])).get(name);
+  }
+
+  release() {
+    for (const handle of this.handles.values()) {
+      releaseHipQuantizedWeightHandle(handle);
+    }
+    this.handles.clear();
+    this.bytes = 0;
+  }
+}
+
 module.exports = {
+  HipGgufFile,
+  HipGgufWeights,
+  openHipGgufFile,
   assertHipOk,
   checkHipSupport,
   createHipQuantizedWeightHandle,

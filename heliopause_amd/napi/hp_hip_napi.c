@@ -19,6 +19,10 @@
  *   matmulGeglu(gate, up, Float32Array, inputSize, columnCount, rowCount) -> Promise<{status, error, output}>
  *   dequantize(handle, rowStart, rowCount, inputSize) -> {status, output}
  *   geglu(Float32Array gate, Float32Array up) -> {status, output}
+ *   ggufOpen(path, maxArraySample, completeArrayKeys[]) -> {status, error, file}
+ *   ggufInfo(file) -> parseGguf's GgufMetadata (gguf.ts:30-37) + byteLength per tensor
+ *   ggufUpload(file, tensorIndices[]) -> Promise<{status, error, handles[], statuses[]}>
+ *   ggufClose(file)
  */
 #define NAPI_VERSION 8
 #include <node_api.h>
@@ -26,6 +30,7 @@
 #include <stdlib.h>
 #include <string.h>
 
+#include "hp_gguf.h"
 #include "hp_hip.h"
 
 #define CHECK(env, call)                                             \
@@ -451,6 +456,290 @@ static napi_value js_geglu(napi_env env, napi_callback_info info) {
   return r;
 }
 
+/* ---- GGUF files ----------------------------------------------------------- */
+
+typedef struct {
+  hp_gguf_t *g;
+  int busy; /* async uploads in flight */
+  int close_requested;
+} GgufBox;
+
+static void gguf_finalize(napi_env env, void *data, void *hint) {
+  (void)env;
+  (void)hint;
+  GgufBox *b = (GgufBox *)data;
+  if (b->g) hp_gguf_close(b->g);
+  free(b);
+}
+
+static GgufBox *get_box(napi_env env, napi_value v) {
+  void *p = NULL;
+  napi_valuetype t;
+  if (napi_typeof(env, v, &t) != napi_ok || t != napi_external) return NULL;
+  if (napi_get_value_external(env, v, &p) != napi_ok) return NULL;
+  return (GgufBox *)p;
+}
+
+static napi_value js_gguf_open(napi_env env, napi_callback_info info) {
+  size_t argc = 3;
+  napi_value argv[3], r, ext;
+  char path[4096];
+  size_t plen = 0;
+  double max_sample = 16;
+  CHECK(env, napi_get_cb_info(env, info, &argc, argv, NULL, NULL));
+  if (argc < 1 || napi_get_value_string_utf8(env, argv[0], path, sizeof path, &plen) != napi_ok ||
+      plen >= sizeof path - 1) {
+    napi_throw_type_error(env, NULL, "ggufOpen(path, maxArraySample?, completeArrayKeys?)");
+    return NULL;
+  }
+  if (argc > 1) napi_get_value_double(env, argv[1], &max_sample);
+  uint32_t nkeys = 0;
+  bool is_arr = false;
+  if (argc > 2 && napi_is_array(env, argv[2], &is_arr) == napi_ok && is_arr) napi_get_array_length(env, argv[2], &nkeys);
+  char **keys = (char **)calloc(nkeys ? nkeys : 1, sizeof(char *));
+  for (uint32_t i = 0; keys && i < nkeys; i++) {
+    napi_value k;
+    size_t len = 0;
+    napi_get_element(env, argv[2], i, &k);
+    if (napi_get_value_string_utf8(env, k, NULL, 0, &len) != napi_ok) continue;
+    keys[i] = (char *)malloc(len + 1);
+    if (keys[i]) napi_get_value_string_utf8(env, k, keys[i], len + 1, &len);
+  }
+  hp_gguf_t *g = NULL;
+  const uint64_t ms = max_sample >= 9007199254740991.0 ? 9007199254740991ull
+                      : max_sample > 0 ? (uint64_t)max_sample : 0;
+  const int32_t rc = hp_gguf_open(path, ms, (const char *const *)keys, nkeys, &g);
+  for (uint32_t i = 0; keys && i < nkeys; i++) free(keys[i]);
+  free(keys);
+  napi_create_object(env, &r);
+  set(env, r, "status", make_i32(env, rc));
+  napi_value err;
+  napi_create_string_utf8(env, rc == 0 ? "" : hp_gguf_last_error(), NAPI_AUTO_LENGTH, &err);
+  set(env, r, "error", err);
+  if (rc == 0) {
+    GgufBox *b = (GgufBox *)calloc(1, sizeof(GgufBox));
+    if (!b) {
+      hp_gguf_close(g);
+      napi_throw_error(env, NULL, "out of host memory");
+      return NULL;
+    }
+    b->g = g;
+    napi_create_external(env, b, gguf_finalize, NULL, &ext);
+    set(env, r, "file", ext);
+  }
+  return r;
+}
+
+static napi_value gguf_value(napi_env env, const hp_gguf_t *g, const hp_gguf_value_t *v) {
+  static const char *names[] = {"uint8", "int8", "uint16", "int16", "uint32", "int32", "float32",
+                                "bool",  "string", "array", "uint64", "int64", "float64"};
+  napi_value r;
+  if (v->type == HP_GGUF_STRING) {
+    napi_create_string_utf8(env, v->string, (size_t)v->string_length, &r);
+  } else if (v->type == HP_GGUF_BOOL) {
+    napi_get_boolean(env, v->number != 0, &r);
+  } else if (v->type != HP_GGUF_ARRAY) {
+    napi_create_double(env, v->number, &r);
+  } else {
+    napi_value sample, t, b;
+    napi_create_object(env, &r);
+    napi_create_string_utf8(env, v->element_type >= 0 && v->element_type <= 12 ? names[v->element_type] : "array",
+                            NAPI_AUTO_LENGTH, &t);
+    set(env, r, "type", t);
+    set(env, r, "length", make_f64(env, (double)v->length));
+    napi_create_array_with_length(env, (size_t)v->sample_count, &sample);
+    for (uint64_t i = 0; i < v->sample_count; i++) {
+      hp_gguf_value_t c;
+      hp_gguf_array_element(g, v->node, i, &c);
+      napi_set_element(env, sample, (uint32_t)i, gguf_value(env, g, &c));
+    }
+    set(env, r, "sample", sample);
+    napi_get_boolean(env, v->truncated != 0, &b);
+    set(env, r, "truncated", b);
+  }
+  return r;
+}
+
+static napi_value make_bigint(napi_env env, uint64_t v) {
+  napi_value r;
+  napi_create_bigint_uint64(env, v, &r);
+  return r;
+}
+
+static napi_value js_gguf_info(napi_env env, napi_callback_info info) {
+  size_t argc = 1;
+  napi_value argv[1], r, md, tensors;
+  CHECK(env, napi_get_cb_info(env, info, &argc, argv, NULL, NULL));
+  GgufBox *b = argc > 0 ? get_box(env, argv[0]) : NULL;
+  if (!b || !b->g) {
+    napi_throw_type_error(env, NULL, "ggufInfo(file): not an open GGUF file");
+    return NULL;
+  }
+  uint32_t version = 0;
+  uint64_t tc = 0, mc = 0, ds = 0, al = 0, fs = 0;
+  hp_gguf_header(b->g, &version, &tc, &mc, &ds, &al, &fs);
+  napi_create_object(env, &r);
+  set(env, r, "version", make_f64(env, version));
+  set(env, r, "tensorCount", make_f64(env, (double)tc));
+  set(env, r, "metadataCount", make_f64(env, (double)mc));
+  set(env, r, "dataStart", make_bigint(env, ds));
+  set(env, r, "alignment", make_f64(env, (double)al));
+  set(env, r, "fileSize", make_f64(env, (double)fs));
+  napi_create_object(env, &md);
+  const uint64_t n = hp_gguf_metadata_count(b->g);
+  for (uint64_t i = 0; i < n; i++) {
+    const char *key;
+    uint64_t klen;
+    hp_gguf_value_t v;
+    napi_value kv;
+    hp_gguf_metadata_entry(b->g, i, &key, &klen, &v);
+    napi_create_string_utf8(env, key, (size_t)klen, &kv);
+    napi_set_property(env, md, kv, gguf_value(env, b->g, &v));
+  }
+  set(env, r, "metadata", md);
+  napi_create_array_with_length(env, (size_t)tc, &tensors);
+  for (uint64_t i = 0; i < tc; i++) {
+    hp_gguf_tensor_t t;
+    napi_value o, name, dims, tn;
+    hp_gguf_tensor_info(b->g, i, &t);
+    napi_create_object(env, &o);
+    napi_create_string_utf8(env, t.name, (size_t)t.name_length, &name);
+    set(env, o, "name", name);
+    napi_create_array_with_length(env, t.n_dims, &dims);
+    for (uint32_t d = 0; d < t.n_dims; d++) napi_set_element(env, dims, d, make_f64(env, (double)t.dims[d]));
+    set(env, o, "dimensions", dims);
+    napi_create_string_utf8(env, hp_gguf_type_name(t.type_id), NAPI_AUTO_LENGTH, &tn);
+    set(env, o, "type", tn);
+    set(env, o, "typeId", make_f64(env, t.type_id));
+    set(env, o, "offset", make_bigint(env, t.offset));
+    set(env, o, "dataOffset", make_bigint(env, t.data_offset));
+    if (t.storage_known) set(env, o, "byteLength", make_f64(env, (double)t.byte_length));
+    napi_set_element(env, tensors, (uint32_t)i, o);
+  }
+  set(env, r, "tensors", tensors);
+  return r;
+}
+
+typedef struct {
+  napi_async_work work;
+  napi_deferred deferred;
+  napi_ref file_ref;
+  GgufBox *box;
+  size_t count;
+  uint64_t *indices, *handles;
+  int32_t *statuses;
+  int32_t status;
+  char error[512];
+} GgufJob;
+
+static void gguf_execute(napi_env env, void *data) {
+  (void)env;
+  GgufJob *j = (GgufJob *)data;
+  j->status = hp_hip_weight_upload_gguf(j->box->g, j->count, j->indices, j->handles, j->statuses);
+  if (j->status != HP_OK) {
+    strncpy(j->error, hp_hip_last_error(), sizeof j->error - 1);
+    j->error[sizeof j->error - 1] = 0;
+  }
+}
+
+static void gguf_complete(napi_env env, napi_status s, void *data) {
+  (void)s;
+  GgufJob *j = (GgufJob *)data;
+  napi_value r, hs, st, err;
+  napi_create_object(env, &r);
+  set(env, r, "status", make_i32(env, j->status));
+  napi_create_string_utf8(env, j->error, NAPI_AUTO_LENGTH, &err);
+  set(env, r, "error", err);
+  napi_create_array_with_length(env, j->count, &hs);
+  napi_create_array_with_length(env, j->count, &st);
+  for (size_t i = 0; i < j->count; i++) {
+    napi_set_element(env, hs, (uint32_t)i, make_bigint(env, j->handles[i]));
+    napi_set_element(env, st, (uint32_t)i, make_i32(env, j->statuses[i]));
+  }
+  set(env, r, "handles", hs);
+  set(env, r, "statuses", st);
+  j->box->busy--;
+  if (j->box->close_requested && j->box->busy == 0 && j->box->g) {
+    hp_gguf_close(j->box->g);
+    j->box->g = NULL;
+  }
+  napi_delete_reference(env, j->file_ref);
+  napi_resolve_deferred(env, j->deferred, r);
+  napi_delete_async_work(env, j->work);
+  free(j->indices);
+  free(j->handles);
+  free(j->statuses);
+  free(j);
+}
+
+static napi_value js_gguf_upload(napi_env env, napi_callback_info info) {
+  size_t argc = 2;
+  napi_value argv[2], promise, name;
+  uint32_t n = 0;
+  bool is_arr = false;
+  CHECK(env, napi_get_cb_info(env, info, &argc, argv, NULL, NULL));
+  GgufBox *b = argc > 0 ? get_box(env, argv[0]) : NULL;
+  if (!b || !b->g || b->close_requested || argc < 2 || napi_is_array(env, argv[1], &is_arr) != napi_ok || !is_arr ||
+      napi_get_array_length(env, argv[1], &n) != napi_ok) {
+    napi_throw_type_error(env, NULL, "ggufUpload(file, tensorIndices[]) on an open GGUF file");
+    return NULL;
+  }
+  GgufJob *j = (GgufJob *)calloc(1, sizeof(GgufJob));
+  if (!j) return NULL;
+  j->box = b;
+  j->count = n;
+  j->indices = (uint64_t *)calloc(n ? n : 1, sizeof(uint64_t));
+  j->handles = (uint64_t *)calloc(n ? n : 1, sizeof(uint64_t));
+  j->statuses = (int32_t *)calloc(n ? n : 1, sizeof(int32_t));
+  if (!j->indices || !j->handles || !j->statuses) {
+    free(j->indices);
+    free(j->handles);
+    free(j->statuses);
+    free(j);
+    napi_throw_error(env, NULL, "out of host memory");
+    return NULL;
+  }
+  for (uint32_t i = 0; i < n; i++) {
+    napi_value v;
+    size_t idx;
+    napi_get_element(env, argv[1], i, &v);
+    if (!get_size(env, v, &idx)) {
+      free(j->indices);
+      free(j->handles);
+      free(j->statuses);
+      free(j);
+      napi_throw_type_error(env, NULL, "ggufUpload: tensor indices must be non-negative integers");
+      return NULL;
+    }
+    j->indices[i] = idx;
+  }
+  b->busy++;
+  napi_create_reference(env, argv[0], 1, &j->file_ref);  /* the file stays open while the worker reads */
+  napi_create_promise(env, &j->deferred, &promise);
+  napi_create_string_utf8(env, "hp_hip_weight_upload_gguf", NAPI_AUTO_LENGTH, &name);
+  napi_create_async_work(env, NULL, name, gguf_execute, gguf_complete, j, &j->work);
+  napi_queue_async_work(env, j->work);
+  return promise;
+}
+
+static napi_value js_gguf_close(napi_env env, napi_callback_info info) {
+  size_t argc = 1;
+  napi_value argv[1];
+  CHECK(env, napi_get_cb_info(env, info, &argc, argv, NULL, NULL));
+  GgufBox *b = argc > 0 ? get_box(env, argv[0]) : NULL;
+  if (!b) {
+    napi_throw_type_error(env, NULL, "ggufClose(file)");
+    return NULL;
+  }
+  if (b->busy > 0) {
+    b->close_requested = 1; /* closed when the last upload completes */
+  } else if (b->g) {
+    hp_gguf_close(b->g);
+    b->g = NULL;
+  }
+  return make_i32(env, 0);
+}
+
 static napi_value init_module(napi_env env, napi_value exports) {
   napi_property_descriptor d[] = {
       {"statusString", NULL, js_status_string, NULL, NULL, NULL, napi_enumerable, NULL},
@@ -466,6 +755,10 @@ static napi_value init_module(napi_env env, napi_value exports) {
       {"matmulGeglu", NULL, js_matmul_geglu, NULL, NULL, NULL, napi_enumerable, NULL},
       {"dequantize", NULL, js_dequantize, NULL, NULL, NULL, napi_enumerable, NULL},
       {"geglu", NULL, js_geglu, NULL, NULL, NULL, napi_enumerable, NULL},
+      {"ggufOpen", NULL, js_gguf_open, NULL, NULL, NULL, napi_enumerable, NULL},
+      {"ggufInfo", NULL, js_gguf_info, NULL, NULL, NULL, napi_enumerable, NULL},
+      {"ggufUpload", NULL, js_gguf_upload, NULL, NULL, NULL, napi_enumerable, NULL},
+      {"ggufClose", NULL, js_gguf_close, NULL, NULL, NULL, napi_enumerable, NULL},
   };
   napi_define_properties(env, exports, sizeof d / sizeof d[0], d);
   return exports;

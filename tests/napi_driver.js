@@ -3,6 +3,11 @@
 //   node napi_driver.js api            -> JSON of the API-level checks that need no GPU
 //   node napi_driver.js run <dir>      -> reads case.json + *.bin from <dir>, runs the
 //                                         projections through the addon, writes out_*.bin
+//   node napi_driver.js gguf <file> <maxArraySample> [completeKey...]
+//                                      -> the parsed file as JSON (bigints as strings,
+//                                         like serializeGgufMetadata, gguf.ts:246-259)
+//   node napi_driver.js ggufrun <dir>  -> loads <dir>/model.gguf through HipGgufWeights,
+//                                         projects <dir>/x.bin with every handle
 const fs = require("fs");
 const path = require("path");
 const hip = require(path.join(__dirname, "..", "heliopause_amd", "napi", "hip-kernels.js"));
@@ -75,8 +80,54 @@ async function run(dir) {
   process.stdout.write(JSON.stringify({ residentBefore: stats.residentBytes, residentAfter: after.residentBytes, handlesAfter: after.handleCount, mismatch }));
 }
 
+function serialize(value) {
+  return JSON.stringify(value, (key, v) => (typeof v === "bigint" ? v.toString() : v));
+}
+
+async function gguf(file, maxArraySample, keys) {
+  const f = hip.openHipGgufFile(file, { maxArraySample: Number(maxArraySample), completeArrayKeys: keys });
+  try {
+    process.stdout.write(serialize(f.metadata));
+  } finally {
+    f.close();
+  }
+}
+
+async function ggufRun(dir) {
+  const spec = JSON.parse(fs.readFileSync(path.join(dir, "case.json"), "utf8"));
+  const x = readF32(path.join(dir, "x.bin"));
+  const f = hip.openHipGgufFile(path.join(dir, "model.gguf"));
+  const weights = new hip.HipGgufWeights(f);
+  const names = f.metadata.tensors.map((t) => t.name);
+  // a single-tensor request and a batch racing it share one upload
+  const [first, all] = await Promise.all([weights.handle(names[0]), weights.upload(names)]);
+  const again = await weights.handle(names[0]);
+  const result = { supported: [], unsupported: [], sameHandle: first === again && first === all.get(names[0]) };
+  for (const name of names) {
+    const h = all.get(name);
+    if (!h) {
+      result.unsupported.push(name);
+      continue;
+    }
+    result.supported.push(name);
+    const out = await hip.matMulQuantizedHipResident(h, x.subarray(0, h.inputSize * spec.columns), h.inputSize, h.rowCount, spec.columns);
+    fs.writeFileSync(path.join(dir, `out_${name}.bin`), Buffer.from(out.buffer, out.byteOffset, out.byteLength));
+  }
+  result.hits = weights.hits;
+  result.misses = weights.misses;
+  result.bytes = weights.bytes;
+  weights.release();
+  result.handlesAfter = hip.hipResidentWeightStats().handleCount;
+  f.close();
+  process.stdout.write(JSON.stringify(result));
+}
+
 const mode = process.argv[2];
-(mode === "api" ? api() : run(process.argv[3])).catch((error) => {
+const job = mode === "api" ? api()
+  : mode === "gguf" ? gguf(process.argv[3], process.argv[4], process.argv.slice(5))
+  : mode === "ggufrun" ? ggufRun(process.argv[3])
+  : run(process.argv[3]);
+job.catch((error) => {
   process.stderr.write(`${error.stack || error}\n`);
   process.exit(1);
 });

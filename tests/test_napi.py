@@ -5,8 +5,11 @@ CPU: the addon loads in Node, exports the runner API of wasm-kernels.ts
 648-749) under its Hip names, and keeps that module's undefined-vs-throw
 behaviour and messages.  GPU: projections, gate/up + GeGLU and head + top-k
 issued from Node (async, on the libuv pool) match the oracle bit for bit.
+GGUF: ggufOpen/ggufInfo from Node against the oracle's parseGguf (CPU), and
+HipGgufWeights loading a file and projecting with it (GPU).
 """
 import json
+import math
 import shutil
 import subprocess
 from pathlib import Path
@@ -36,6 +39,7 @@ def _node(*args, timeout=90):
 def test_addon_api_without_gpu():
     out = _node("api")
     assert out["exports"] == sorted([
+        "HipGgufFile", "HipGgufWeights", "openHipGgufFile",
         "assertHipOk", "checkHipSupport", "createHipQuantizedWeightHandle", "hipResidentWeightStats",
         "matMulGegluHipResident", "matMulQuantizedHipResident", "matMulQuantizedHipResidentMulti",
         "matMulQuantizedHipResidentTopK", "quantizedTypeId", "releaseHipQuantizedWeightHandle"])
@@ -90,3 +94,69 @@ def test_addon_projections_bit_exact(oracle, tmp_path):
         assert np.array_equal(got_vals.view(np.uint32), vals.view(np.uint32))
     assert res["residentBefore"] > 0 and res["residentAfter"] == 0 and res["handlesAfter"] == 0
     assert res["mismatch"] == "Resident quantized matmul handle shape mismatch: 2560x64"
+
+
+def _jsonable(v):
+    """The oracle's parse as the driver serialises it: big integers (offsets,
+    data start) as strings, non-finite floats as JSON null."""
+    if isinstance(v, dict):
+        return {k: _jsonable(x) for k, x in v.items()}
+    if isinstance(v, list):
+        return [_jsonable(x) for x in v]
+    if isinstance(v, float) and not math.isfinite(v):
+        return None
+    return v
+
+
+@needs_node
+@pytest.mark.parametrize("seed", [3, 5, 8, 13, 21])
+def test_addon_gguf_parse_matches_oracle(tmp_path, seed):
+    """ggufOpen / ggufInfo from Node against the oracle's parseGguf."""
+    from oracle import gguf as OG
+    from test_gguf import random_file
+
+    data, *_ = random_file(seed)
+    path = tmp_path / "f.gguf"
+    path.write_bytes(data)
+    for max_sample, keys in ((16, ()), (1, ("key.0", "key.1"))):
+        got = _node("gguf", str(path), str(max_sample), *keys)
+        ref = OG.parse_gguf(data, max_sample, keys)
+        for t, r in zip(got["tensors"], ref["tensors"]):
+            assert t.pop("byteLength", None) == (OG.tensor_byte_length(r) if r["type"] in OG.GGML_TYPE_STORAGE else None)
+            r["offset"], r["dataOffset"] = str(r["offset"]), str(r["dataOffset"])
+        ref["dataStart"] = str(ref["dataStart"])
+        for k in ("alignment", "fileSize"):
+            got.pop(k)
+        assert got == _jsonable(ref)
+
+
+@needs_node
+@pytest.mark.gpu
+def test_addon_gguf_upload_bit_exact(oracle, tmp_path):
+    """A GGUF file loaded from Node (HipGgufWeights over ggufUpload) gives
+    projections bit-exact with the oracle on the file's tensor bytes."""
+    from heliopause_amd import gguf as G
+
+    k, m = 2560, 2
+    specs = [("blk.0.attn_q.weight", "Q4_K", 640), ("blk.0.attn_v.weight", "Q6_K", 512),
+             ("blk.0.attn_norm.weight", "F32", 1), ("output.weight", "Q6_K", 9000)]
+    tensors, ws = [], {}
+    for i, (name, typ, rows) in enumerate(specs):
+        if typ == "F32":
+            data = S.random_bytes(S.derive(S.BASE_SEED, "napi-gguf", i), 4 * k)
+        else:
+            data = S.weight_blocks(typ, S.derive(S.BASE_SEED, "napi-gguf", i), rows, k)
+            ws[name] = (typ, rows, data)
+        tensors.append((name, [k, rows], G.GGML_TYPE_IDS[typ], data))
+    G.write_gguf(tmp_path / "model.gguf", [("general.architecture", G.GGUF_STRING, "gemma4")], tensors)
+    x = S.activations(S.derive(S.BASE_SEED, "napi-gguf-x"), m, k)
+    (tmp_path / "x.bin").write_bytes(x.astype(np.float32).tobytes())
+    (tmp_path / "case.json").write_text(json.dumps({"columns": m}))
+    print("napi gguf upload", flush=True)
+    res = _node("ggufrun", str(tmp_path))
+    assert res["unsupported"] == ["blk.0.attn_norm.weight"] and res["sameHandle"]
+    assert res["handlesAfter"] == 0 and res["bytes"] == sum(w[2].size for w in ws.values())
+    for name, (typ, rows, data) in ws.items():
+        got = np.fromfile(tmp_path / f"out_{name}.bin", dtype=np.float32)
+        ref = oracle.matmul({"Q4_K": 1, "Q6_K": 3}[typ], data, x, rows)
+        assert np.array_equal(got.view(np.uint32), ref.reshape(-1).view(np.uint32)), name
