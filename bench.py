@@ -171,7 +171,8 @@ def cpu_baseline(workload: str, ws, x, seconds: float) -> dict:
 def decode_chain(args) -> int:
     """Projection chain of one decode step of the 42-layer model at M = 1:
     per layer Q/K/V (one launch) -> O (fed Q's 2048 outputs) -> gate/up +
-    GeGLU (one launch) -> down, then the head and top-40; every layer's weights
+    GeGLU (one launch) -> down, then the head, top-40 and the sampled next
+    token (generator state kept in HBM); every layer's weights
     are distinct device copies (3.02 GB, so nothing is Infinity-Cache hot).
     Attention, norms, RoPE and residuals are not part of this path and are
     not run; each layer's Q/K/V and the head read one fixed input, which does
@@ -203,6 +204,13 @@ def decode_chain(args) -> int:
                         ("h", 10240), ("y", 2560), ("logits", 262144))}
     ids = torch.empty(TOPK, dtype=torch.int32, device=dev)
     vals = torch.empty(TOPK, dtype=torch.float32, device=dev)
+    # next-token sampling on the device (top-40 slice, top-p 0.95, T = 1); the
+    # generator state stays in HBM and advances every step
+    sampling = H.resolveGenerationSamplingOptions(topK=TOPK)
+    rng = torch.from_numpy(np.array([sampling["seed"]], np.uint32).view(np.int32)).to(dev)
+    token = torch.zeros(1, dtype=torch.int32, device=dev)
+    kept = torch.zeros(1, dtype=torch.int32, device=dev)
+    probs = torch.zeros(TOPK, dtype=torch.float64, device=dev)
     L = H.lib()
     p = {n: t.data_ptr() for n, t in buf.items()}
 
@@ -215,6 +223,8 @@ def decode_chain(args) -> int:
         H.matmul_multi_device([head], x.data_ptr(), 2560, 1, [p["logits"]], [262144], stream)
         H.assertHipOk(L.hp_hip_topk_device(p["logits"], 1, 262144, TOPK, 0.0, ids.data_ptr(), vals.data_ptr(),
                                            stream), "topk")
+        H.sample_device(ids.data_ptr(), vals.data_ptr(), 1, TOPK, TOPK, sampling, rng.data_ptr(), token.data_ptr(),
+                        probs.data_ptr(), kept.data_ptr(), stream)
 
     side = torch.cuda.Stream()
     with torch.cuda.stream(side):
@@ -237,14 +247,14 @@ def decode_chain(args) -> int:
     wall_ms = (time.perf_counter() - t0) / steps * 1e3
     ms = start.elapsed_time(end) / steps
     wbytes = N_LAYERS * sum(row_bytes(t, k) * r for t, r, k in LAYER) + row_bytes(HEAD[0], HEAD[2]) * HEAD[1]
-    launches = N_LAYERS * 4 + 1 + 3
+    launches = N_LAYERS * 4 + 1 + 3 + 1
     line = {
         "metric": "decode step projection chain ms at M=1 (1 GPU)",
         "value": round(ms, 4), "unit": "ms", "n_gpus": 1, "steps": steps, "warmup": args.warmup,
         "ms_per_step": round(ms, 4), "higher_is_better": False, "scaling": "weak", "vs_baseline": None,
         "dtype": "int8", "data": "synthetic",
-        "config": {"workload": "42-layer synthetic Gemma-like model, projections + GeGLU + head + top-40 at M=1 "
-                               "(attention, norms, RoPE, residuals not included)",
+        "config": {"workload": "42-layer synthetic Gemma-like model, projections + GeGLU + head + top-40 + "
+                               "next-token sampling at M=1 (attention, norms, RoPE, residuals not included)",
                    "weight_bytes": wbytes, "launches_per_step": launches, "wall_ms_per_step": round(wall_ms, 4),
                    "timing": "one step captured in a HIP graph and replayed"},
         "roofline": {"bound": "hbm", "achieved": round(wbytes / (ms * 1e-3) / 1e9, 2), "peak": HBM_PEAK_GBPS,

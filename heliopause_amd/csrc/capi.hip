@@ -66,6 +66,10 @@ struct State {
   std::vector<hipEvent_t> copy_events;
   uint8_t *load_staging = nullptr;
   size_t load_staging_cap = 0;
+  // sampling outputs of the host-pointer entry point: rng state, tokens,
+  // kept counts and probabilities
+  void *sample_out = nullptr;
+  size_t sample_out_cap = 0;
 };
 
 State &st() {
@@ -580,6 +584,28 @@ int32_t runner_type(uint32_t ggml) {
   }
 }
 
+// resolveGenerationSamplingOptions' checks (generation.ts:49-60) on the
+// resolved options the entry points take.
+int32_t sampling_check(const hp_hip_sampling_t *o, size_t k) {
+  if (!o) return fail(HP_ERR_ARG, "null sampling options");
+  if (!std::isfinite(o->temperature) || o->temperature < 0)
+    return fail(HP_ERR_ARG, "temperature must be a finite number greater than or equal to 0.");
+  if (!std::isfinite(o->top_p) || o->top_p <= 0 || o->top_p > 1)
+    return fail(HP_ERR_ARG, "topP must be a finite number in the range (0, 1].");
+  if (o->top_k < 1) return fail(HP_ERR_ARG, "topK must be a positive finite number.");
+  if (k == 0 || k > 64) return fail(HP_ERR_ARG, "k must be in 1..64");
+  return HP_OK;
+}
+
+SampleParams sample_params(const hp_hip_sampling_t *o) {
+  SampleParams p;
+  p.do_sample = o->do_sample ? 1 : 0;
+  p.top_k = o->top_k;
+  p.temperature = o->temperature;
+  p.top_p = o->top_p;
+  return p;
+}
+
 int32_t topk_check(size_t rows, size_t n, size_t k) {
   if (k == 0 || k > 64) return fail(HP_ERR_ARG, "k must be in 1..64");
   if (n == 0 || n > 524288 || rows > 65535) return fail(HP_ERR_SHAPE, "topk supports 1..524288 values per row");
@@ -681,6 +707,9 @@ int32_t hp_hip_shutdown(void) {
   }
   if (s.topk_scratch) (void)hipFree(s.topk_scratch);
   if (s.topk_out) (void)hipFree(s.topk_out);
+  if (s.sample_out) (void)hipFree(s.sample_out);
+  s.sample_out = nullptr;
+  s.sample_out_cap = 0;
   s.topk_scratch = s.topk_out = nullptr;
   s.topk_scratch_cap = s.topk_out_cap = 0;
   prof_collect();
@@ -979,6 +1008,80 @@ int32_t hp_hip_matmul_topk(uint64_t handle, const float *input, size_t input_len
   if (rc != HP_OK) return rc;
   HP_HIP_TRY(hipMemcpyAsync(ids, d_ids, column_count * k * 4, hipMemcpyDeviceToHost, s.stream));
   HP_HIP_TRY(hipMemcpyAsync(values, d_vals, column_count * k * 4, hipMemcpyDeviceToHost, s.stream));
+  HP_HIP_TRY(hipStreamSynchronize(s.stream));
+  return HP_OK;
+}
+
+int32_t hp_hip_sample_device(const uint32_t *d_ids, const float *d_values, size_t column_count, size_t k,
+                             size_t count, const hp_hip_sampling_t *sampling, uint32_t *d_rng_state,
+                             int32_t *d_tokens, double *d_probabilities, int32_t *d_kept, void *stream) {
+  State &s = st();
+  std::lock_guard<std::recursive_mutex> lock(s.mu);
+  int32_t rc = ensure_init(s.ready ? s.device : 0);
+  if (rc != HP_OK) return rc;
+  rc = sampling_check(sampling, k);
+  if (rc != HP_OK) return rc;
+  if (count == 0 || count > k) return fail(HP_ERR_ARG, "count must be in 1..k");
+  if (column_count == 0) return HP_OK;
+  if (column_count > 65535) return fail(HP_ERR_SHAPE, "too many columns");
+  if (!d_ids || !d_values || !d_rng_state || !d_tokens || !d_probabilities || !d_kept)
+    return fail(HP_ERR_ARG, "null pointer");
+  hipStream_t q = stream ? static_cast<hipStream_t>(stream) : s.stream;
+  HP_HIP_TRY(launch_sample(d_ids, d_values, (int)column_count, (int)k, (int)count, sample_params(sampling), d_rng_state,
+                           d_tokens, d_probabilities, d_kept, q));
+  s.launches++;
+  return HP_OK;
+}
+
+int32_t hp_hip_matmul_topk_sample(uint64_t handle, const float *input, size_t input_len, size_t input_size,
+                                  size_t column_count, size_t k, double softcap, const hp_hip_sampling_t *sampling,
+                                  uint32_t *rng_state, int32_t *tokens, uint32_t *ids, float *values,
+                                  double *probabilities, int32_t *kept, size_t out_len) {
+  State &s = st();
+  std::lock_guard<std::recursive_mutex> lock(s.mu);
+  Handle *h = lookup(handle);
+  if (!h) return fail(HP_ERR_HANDLE, "unknown weight handle");
+  if (h->input_size != input_size || input_len != sat_mul(input_size, column_count))
+    return fail(HP_ERR_SHAPE, "matmul shape mismatch");
+  int32_t rc = topk_check(column_count, h->row_count, k);
+  if (rc != HP_OK) return rc;
+  rc = sampling_check(sampling, k);
+  if (rc != HP_OK) return rc;
+  if (out_len != sat_mul(column_count, k)) return fail(HP_ERR_SHAPE, "topk output length mismatch");
+  if (column_count == 0) return HP_OK;
+  if (!input || !rng_state || !tokens || !ids || !values || !probabilities || !kept)
+    return fail(HP_ERR_ARG, "null pointer");
+  rc = grow((void **)&s.io_in, &s.io_in_cap, input_len * sizeof(float));
+  if (rc == HP_OK) rc = grow((void **)&s.io_out[0], &s.io_out_cap[0], column_count * h->row_count * sizeof(float));
+  uint32_t *d_ids = nullptr;
+  float *d_vals = nullptr;
+  if (rc == HP_OK) rc = topk_outputs(column_count, k, &d_ids, &d_vals);
+  // rng state (16 B slot), tokens, kept, probabilities
+  const size_t probs_off = (16 + column_count * 8 + 15) & ~(size_t)15;
+  if (rc == HP_OK) rc = grow(&s.sample_out, &s.sample_out_cap, probs_off + column_count * k * sizeof(double));
+  if (rc != HP_OK) return rc;
+  uint8_t *base = static_cast<uint8_t *>(s.sample_out);
+  uint32_t *d_rng = reinterpret_cast<uint32_t *>(base);
+  int32_t *d_tokens = reinterpret_cast<int32_t *>(base + 16);
+  int32_t *d_kept = d_tokens + column_count;
+  double *d_probs = reinterpret_cast<double *>(base + probs_off);
+  HP_HIP_TRY(hipMemcpyAsync(s.io_in, input, input_len * sizeof(float), hipMemcpyHostToDevice, s.stream));
+  HP_HIP_TRY(hipMemcpyAsync(d_rng, rng_state, 4, hipMemcpyHostToDevice, s.stream));
+  float *logits = s.io_out[0];
+  rc = run_matvec(1, &h, s.io_in, input_size, column_count, &logits, s.stream);
+  if (rc != HP_OK) return rc;
+  rc = run_topk(logits, column_count, h->row_count, k, softcap, d_ids, d_vals, s.stream);
+  if (rc != HP_OK) return rc;
+  const size_t count = h->row_count < k ? h->row_count : k;
+  HP_HIP_TRY(launch_sample(d_ids, d_vals, (int)column_count, (int)k, (int)count, sample_params(sampling), d_rng,
+                           d_tokens, d_probs, d_kept, s.stream));
+  s.launches++;
+  HP_HIP_TRY(hipMemcpyAsync(ids, d_ids, column_count * k * 4, hipMemcpyDeviceToHost, s.stream));
+  HP_HIP_TRY(hipMemcpyAsync(values, d_vals, column_count * k * 4, hipMemcpyDeviceToHost, s.stream));
+  HP_HIP_TRY(hipMemcpyAsync(tokens, d_tokens, column_count * 4, hipMemcpyDeviceToHost, s.stream));
+  HP_HIP_TRY(hipMemcpyAsync(kept, d_kept, column_count * 4, hipMemcpyDeviceToHost, s.stream));
+  HP_HIP_TRY(hipMemcpyAsync(probabilities, d_probs, column_count * k * 8, hipMemcpyDeviceToHost, s.stream));
+  HP_HIP_TRY(hipMemcpyAsync(rng_state, d_rng, 4, hipMemcpyDeviceToHost, s.stream));
   HP_HIP_TRY(hipStreamSynchronize(s.stream));
   return HP_OK;
 }

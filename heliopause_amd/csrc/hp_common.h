@@ -105,6 +105,18 @@ constexpr int kTopkMaxRows = 16;
 hipError_t launch_topk(const float *logits, int rows, int n, int k, double cap, uint8_t *scratch, uint32_t *ids,
                        float *vals, hipStream_t s);
 size_t topk_scratch_bytes(int rows, int n, int k);
+
+// Next-token sampling over [cols][k] sorted candidates (count valid per
+// column): one wave; rng points to the 32-bit generator state, advanced once
+// per sampled column.  tokens [cols], probs [cols][k] (first kept[c] valid).
+struct SampleParams {
+  int do_sample;  // 0: greedy
+  int top_k;      // >= 1
+  double temperature;
+  double top_p;
+};
+hipError_t launch_sample(const uint32_t *ids, const float *vals, int cols, int k, int count, const SampleParams &p,
+                         uint32_t *rng, int32_t *tokens, double *probs, int32_t *kept, hipStream_t s);
 // Matrix-core matvec (kquant_mfma.hip): weights in 16-row tile segments.
 struct MfmaLaunch {
   const uint8_t *seg[kMaxWeights];

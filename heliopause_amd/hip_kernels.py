@@ -102,9 +102,23 @@ def _declare(L: ctypes.CDLL) -> None:
     _declare_optional(L)
 
 
+class HipSampling(ctypes.Structure):
+    """hp_hip_sampling_t: resolved sampling options."""
+    _fields_ = [("do_sample", ctypes.c_int32), ("top_k", ctypes.c_int32), ("temperature", ctypes.c_double),
+                ("top_p", ctypes.c_double)]
+
+
 def _declare_optional(L: ctypes.CDLL) -> None:
-    """Top-k, GeGLU and tuning entry points."""
+    """Top-k, GeGLU, sampling and tuning entry points."""
     i32 = ctypes.c_int32
+    sp = ctypes.POINTER(HipSampling)
+    L.hp_hip_sample_device.argtypes = [ctypes.c_void_p, ctypes.c_void_p, _sz, _sz, _sz, sp, ctypes.c_void_p,
+                                       ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p]
+    L.hp_hip_sample_device.restype = i32
+    L.hp_hip_matmul_topk_sample.argtypes = [_u64, ctypes.c_void_p, _sz, _sz, _sz, _sz, ctypes.c_double, sp,
+                                            ctypes.POINTER(ctypes.c_uint32), ctypes.c_void_p, ctypes.c_void_p,
+                                            ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, _sz]
+    L.hp_hip_matmul_topk_sample.restype = i32
     L.hp_hip_set_matvec_kernel.argtypes = [i32]
     L.hp_hip_set_matvec_kernel.restype = i32
     L.hp_hip_matmul_geglu.argtypes = [_u64, _u64, ctypes.c_void_p, _sz, _sz, _sz, ctypes.c_void_p, _sz]
@@ -419,3 +433,90 @@ def synchronize() -> None:
 
 def shutdown() -> None:
     assertHipOk(lib().hp_hip_shutdown(), "shutdown")
+
+
+# ---- sampling (generation.ts:40-165) -----------------------------------------
+
+DEFAULT_SAMPLING_SEED = 0x48454C49
+DEFAULT_GENERATION_CONFIG = {"doSample": True, "temperature": 1.0, "topP": 0.95, "topK": 64}
+
+
+def resolveGenerationSamplingOptions(doSample=None, temperature=None, topP=None, topK=None, seed=None) -> dict:
+    """resolveGenerationSamplingOptions (generation.ts:40-76): defaults,
+    validation (same messages), floor(topK), seed >>> 0, logitsTopK."""
+    import math
+
+    d = DEFAULT_GENERATION_CONFIG["doSample"] if doSample is None else doSample
+    t = DEFAULT_GENERATION_CONFIG["temperature"] if temperature is None else temperature
+    p = DEFAULT_GENERATION_CONFIG["topP"] if topP is None else topP
+    k = DEFAULT_GENERATION_CONFIG["topK"] if topK is None else topK
+    s = DEFAULT_SAMPLING_SEED if seed is None else seed
+    if not math.isfinite(t) or t < 0:
+        raise ValueError("temperature must be a finite number greater than or equal to 0.")
+    if not math.isfinite(p) or p <= 0 or p > 1:
+        raise ValueError("topP must be a finite number in the range (0, 1].")
+    if not math.isfinite(k) or k < 1:
+        raise ValueError("topK must be a positive finite number.")
+    if not math.isfinite(s):
+        raise ValueError("seed must be a finite number.")
+    k = max(1, math.floor(k))
+    greedy = d is False or t == 0
+    return {"doSample": d, "temperature": float(t), "topP": float(p), "topK": k,
+            "seed": math.floor(s) & 0xFFFFFFFF, "logitsTopK": 1 if greedy else k}
+
+
+class HipSamplingState:
+    """The generator of createDeterministicRng (generation.ts:78-87) as a
+    32-bit state that the GPU advances; seeded like the reference."""
+
+    def __init__(self, seed=DEFAULT_SAMPLING_SEED):
+        import math
+
+        self.state = ctypes.c_uint32(math.floor(seed) & 0xFFFFFFFF)
+
+
+def _sampling_struct(o: dict) -> HipSampling:
+    return HipSampling(0 if o["doSample"] is False else 1, min(int(o["topK"]), 2 ** 31 - 1), float(o["temperature"]),
+                       float(o["topP"]))
+
+
+def matMulQuantizedHipResidentTopKSample(handle: HipQuantizedWeightHandle, input_columns, input_size: int,
+                                         column_count: int, sampling: dict, state: HipSamplingState,
+                                         softcap: float = 0.0, top_k: Optional[int] = None) -> list:
+    """forwardOutput + sampleNextToken per column on the GPU: the head, its
+    top-k (k = sampling["logitsTopK"] unless given) and the sampled token.
+    Returns per column {"token", "distribution": [{id, value, probability}]};
+    ``state`` advances once per sampled column."""
+    if handle.released:
+        raise RuntimeError(f"Resident quantized matmul handle {handle.handle} is not available")
+    x = _f32(input_columns)
+    if handle.inputSize != input_size or x.size != input_size * column_count:
+        raise ValueError(f"Resident quantized matmul input shape mismatch: {x.size}")
+    k = int(sampling["logitsTopK"] if top_k is None else top_k)
+    ids = np.empty((column_count, k), dtype=np.uint32)
+    vals = np.empty((column_count, k), dtype=np.float32)
+    probs = np.empty((column_count, k), dtype=np.float64)
+    tokens = np.empty(column_count, dtype=np.int32)
+    kept = np.empty(column_count, dtype=np.int32)
+    opts = _sampling_struct(sampling)
+    code = lib().hp_hip_matmul_topk_sample(handle.handle, x.ctypes.data, x.size, input_size, column_count, k,
+                                           float(softcap), ctypes.byref(opts), ctypes.byref(state.state),
+                                           tokens.ctypes.data, ids.ctypes.data, vals.ctypes.data, probs.ctypes.data,
+                                           kept.ctypes.data, ids.size)
+    assertHipOk(code, "matMulQuantizedResidentTopKSample")
+    out = []
+    for c in range(column_count):
+        n = int(kept[c])
+        out.append({"token": int(tokens[c]),
+                    "distribution": [{"id": int(ids[c, i]), "value": float(vals[c, i]),
+                                      "probability": float(probs[c, i])} for i in range(n)]})
+    return out
+
+
+def sample_device(d_ids: int, d_values: int, column_count: int, k: int, count: int, sampling: dict, d_rng_state: int,
+                  d_tokens: int, d_probabilities: int, d_kept: int, stream: int = 0) -> None:
+    """hp_hip_sample_device over device pointers (asynchronous on ``stream``)."""
+    opts = _sampling_struct(sampling)
+    code = lib().hp_hip_sample_device(d_ids, d_values, column_count, k, count, ctypes.byref(opts), d_rng_state,
+                                      d_tokens, d_probabilities, d_kept, stream or None)
+    assertHipOk(code, "sample")

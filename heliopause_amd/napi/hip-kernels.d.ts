@@ -115,3 +115,31 @@ export class HipGgufWeights {
   handle(name: string): Promise<HipQuantizedWeightHandle | undefined>;
   release(): void;
 }
+
+// Token sampling on the device (generation.ts:40-165).
+export const DEFAULT_SAMPLING_SEED: number;
+export type ResolvedHipSamplingOptions = {
+  doSample: boolean;
+  temperature: number;
+  topP: number;
+  topK: number;
+  seed: number;
+  logitsTopK: number;
+};
+export function resolveGenerationSamplingOptions(options?: {
+  doSample?: boolean;
+  temperature?: number;
+  topP?: number;
+  topK?: number;
+  seed?: number;
+}): ResolvedHipSamplingOptions;
+export function createHipSamplingState(seed?: number): Uint32Array;
+export function matMulQuantizedHipResidentTopKSample(
+  handle: HipQuantizedWeightHandle,
+  inputColumns: Float32Array,
+  inputSize: number,
+  columnCount: number,
+  sampling: ResolvedHipSamplingOptions,
+  state: Uint32Array,
+  softcap?: number,
+): Promise<{ token: number; distribution: { id: number; value: number; probability: number }[] }[]>;

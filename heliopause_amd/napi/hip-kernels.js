@@ -23,6 +23,11 @@
  *   readWasmWeightHandle (acceleration.ts:164-201)
  *                                              HipGgufWeights.handle / upload
  *
+ * token sampling on the device (generation.ts:40-165):
+ *   resolveGenerationSamplingOptions           resolveGenerationSamplingOptions
+ *   createDeterministicRng                     createHipSamplingState (state in a Uint32Array)
+ *   forwardOutput + topK + sampleNextToken     matMulQuantizedHipResidentTopKSample
+ *
  * plus the two calls the decode loop makes around the projections:
  *   forwardOutput + topK (layers.ts:381-416, runtime.ts:514-527)
  *                                              matMulQuantizedHipResidentTopK
@@ -238,6 +243,73 @@ async function matMulGegluHipResident(gate, up, inputColumns, inputSize, columnC
   return result.output;
 }
 
+const DEFAULT_SAMPLING_SEED = 0x48454c49;
+
+/* resolveGenerationSamplingOptions (generation.ts:40-76). */
+function resolveGenerationSamplingOptions(options) {
+  const o = options || {};
+  const doSample = o.doSample === undefined ? true : o.doSample;
+  const temperature = o.temperature === undefined ? 1.0 : o.temperature;
+  const topP = o.topP === undefined ? 0.95 : o.topP;
+  const topK = o.topK === undefined ? 64 : o.topK;
+  const seed = o.seed === undefined ? DEFAULT_SAMPLING_SEED : o.seed;
+  if (!Number.isFinite(temperature) || temperature < 0) {
+    throw new Error("temperature must be a finite number greater than or equal to 0.");
+  }
+  if (!Number.isFinite(topP) || topP <= 0 || topP > 1) {
+    throw new Error("topP must be a finite number in the range (0, 1].");
+  }
+  if (!Number.isFinite(topK) || topK < 1) {
+    throw new Error("topK must be a positive finite number.");
+  }
+  if (!Number.isFinite(seed)) {
+    throw new Error("seed must be a finite number.");
+  }
+  const normalizedTopK = Math.max(1, Math.floor(topK));
+  const greedy = doSample === false || temperature === 0;
+  return {
+    doSample,
+    temperature,
+    topP,
+    topK: normalizedTopK,
+    seed: Math.floor(seed) >>> 0,
+    logitsTopK: greedy ? 1 : normalizedTopK,
+  };
+}
+
+/* The generator of createDeterministicRng (generation.ts:78-87) as the
+ * 32-bit state the GPU advances, one draw per sampled column. */
+function createHipSamplingState(seed) {
+  return Uint32Array.of(Math.floor(seed === undefined ? DEFAULT_SAMPLING_SEED : seed) >>> 0);
+}
+
+/* forwardOutput + topK + sampleNextToken per column on the GPU; `sampling`
+ * is resolved options, `state` a createHipSamplingState array (advanced).
+ * Returns [{token, distribution: [{id, value, probability}]}] per column. */
+async function matMulQuantizedHipResidentTopKSample(handle, inputColumns, inputSize, columnCount, sampling, state,
+  softcap) {
+  if (handle.released) {
+    throw new Error(`Resident quantized matmul instance ${handle.handle} is not available`);
+  }
+  if (handle.inputSize !== inputSize || inputColumns.length !== inputSize * columnCount) {
+    throw new Error(`Resident quantized matmul input shape mismatch: ${inputColumns.length}`);
+  }
+  const k = sampling.logitsTopK;
+  const result = await native().matmulTopKSample(handle.handle, inputColumns, inputSize, columnCount, k,
+    softcap === undefined ? 0 : softcap, sampling, state);
+  assertHipOk(result.status, "matMulQuantizedResidentTopKSample", result.error);
+  const columns = [];
+  for (let column = 0; column < columnCount; column += 1) {
+    const distribution = [];
+    for (let index = 0; index < result.kept[column]; index += 1) {
+      const at = column * k + index;
+      distribution.push({ id: result.ids[at], value: result.values[at], probability: result.probabilities[at] });
+    }
+    columns.push({ token: result.tokens[column], distribution });
+  }
+  return columns;
+}
+
 /* A GGUF file parsed by the runner's reader and held open for uploads.
  * `metadata` has parseGguf's shape (GgufMetadata, gguf.ts:30-37), with each
  * tensor's byteLength (tensorByteLength) when its storage type is known. */
@@ -366,6 +438,10 @@ class HipGgufWeights {
 }
 
 module.exports = {
+  DEFAULT_SAMPLING_SEED,
+  createHipSamplingState,
+  matMulQuantizedHipResidentTopKSample,
+  resolveGenerationSamplingOptions,
   HipGgufFile,
   HipGgufWeights,
   openHipGgufFile,

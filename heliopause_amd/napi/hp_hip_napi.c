@@ -19,6 +19,9 @@
  *   matmulGeglu(gate, up, Float32Array, inputSize, columnCount, rowCount) -> Promise<{status, error, output}>
  *   dequantize(handle, rowStart, rowCount, inputSize) -> {status, output}
  *   geglu(Float32Array gate, Float32Array up) -> {status, output}
+ *   matmulTopKSample(handle, Float32Array, inputSize, columnCount, k, softcap,
+ *                    {doSample, topK, temperature, topP}, Uint32Array(1) rngState)
+ *       -> Promise<{status, error, tokens, ids, values, probabilities, kept}>
  *   ggufOpen(path, maxArraySample, completeArrayKeys[]) -> {status, error, file}
  *   ggufInfo(file) -> parseGguf's GgufMetadata (gguf.ts:30-37) + byteLength per tensor
  *   ggufUpload(file, tensorIndices[]) -> Promise<{status, error, handles[], statuses[]}>
@@ -215,7 +218,7 @@ static napi_value js_stats(napi_env env, napi_callback_info info) {
 
 /* ---- asynchronous projections ------------------------------------------ */
 
-enum { JOB_MULTI, JOB_TOPK, JOB_GEGLU };
+enum { JOB_MULTI, JOB_TOPK, JOB_GEGLU, JOB_SAMPLE };
 
 typedef struct {
   napi_async_work work;
@@ -232,6 +235,12 @@ typedef struct {
   double softcap;
   uint32_t *ids;
   size_t rows[4];
+  hp_hip_sampling_t sampling;
+  uint32_t rng;           /* generator state in, advanced state out */
+  napi_ref rng_ref;       /* the caller's Uint32Array(1), updated on completion */
+  uint32_t *rng_out;
+  int32_t *tokens, *kept;
+  double *probs;
   int32_t status;
   char error[512]; /* hp_hip_last_error of the worker thread */
 } Job;
@@ -248,6 +257,10 @@ static void job_execute(napi_env env, void *data) {
   } else if (j->kind == JOB_TOPK) {
     j->status = hp_hip_matmul_topk(j->handles[0], j->input, j->input_len, j->input_size, j->columns, j->k,
                                    j->softcap, j->ids, j->outputs[0], j->output_lens[0]);
+  } else if (j->kind == JOB_SAMPLE) {
+    j->status = hp_hip_matmul_topk_sample(j->handles[0], j->input, j->input_len, j->input_size, j->columns, j->k,
+                                          j->softcap, &j->sampling, &j->rng, j->tokens, j->ids, j->outputs[0],
+                                          j->probs, j->kept, j->output_lens[0]);
   } else {
     j->status = hp_hip_matmul_geglu(j->handles[0], j->handles[1], j->input, j->input_len, j->input_size, j->columns,
                                     j->outputs[0], j->output_lens[0]);
@@ -280,6 +293,19 @@ static void job_complete(napi_env env, napi_status s, void *data) {
     set(env, r, "values", adopt(env, j->outputs[0], j->output_lens[0], 4, napi_float32_array));
     j->ids = NULL;
     j->outputs[0] = NULL;
+  } else if (j->kind == JOB_SAMPLE) {
+    set(env, r, "ids", adopt(env, j->ids, j->output_lens[0], 4, napi_uint32_array));
+    set(env, r, "values", adopt(env, j->outputs[0], j->output_lens[0], 4, napi_float32_array));
+    set(env, r, "probabilities", adopt(env, j->probs, j->output_lens[0], 8, napi_float64_array));
+    set(env, r, "tokens", adopt(env, j->tokens, j->columns, 4, napi_int32_array));
+    set(env, r, "kept", adopt(env, j->kept, j->columns, 4, napi_int32_array));
+    j->ids = NULL;
+    j->outputs[0] = NULL;
+    j->probs = NULL;
+    j->tokens = NULL;
+    j->kept = NULL;
+    if (j->status == HP_OK && j->rng_out) *j->rng_out = j->rng;  /* the caller's state advances */
+    napi_delete_reference(env, j->rng_ref);
   } else {
     set(env, r, "output", adopt(env, j->outputs[0], j->output_lens[0], 4, napi_float32_array));
     j->outputs[0] = NULL;
@@ -289,6 +315,9 @@ static void job_complete(napi_env env, napi_status s, void *data) {
   napi_delete_async_work(env, j->work);
   for (size_t i = 0; i < 4; i++) free(j->outputs[i]);
   free(j->ids);
+  free(j->probs);
+  free(j->tokens);
+  free(j->kept);
   free(j);
 }
 
@@ -313,6 +342,9 @@ static int alloc_outputs(Job *j) {
 static void free_job(Job *j) {
   for (size_t i = 0; i < 4; i++) free(j->outputs[i]);
   free(j->ids);
+  free(j->probs);
+  free(j->tokens);
+  free(j->kept);
   free(j);
 }
 
@@ -411,6 +443,69 @@ static napi_value js_matmul_geglu(napi_env env, napi_callback_info info) {
     return NULL;
   }
   return start_job(env, j, argv[2], "hp_hip_matmul_geglu");
+}
+
+static int get_prop_f64(napi_env env, napi_value obj, const char *name, double *out) {
+  napi_value v;
+  bool has = false;
+  if (napi_has_named_property(env, obj, name, &has) != napi_ok || !has) return 0;
+  if (napi_get_named_property(env, obj, name, &v) != napi_ok) return 0;
+  napi_valuetype t;
+  napi_typeof(env, v, &t);
+  if (t == napi_boolean) {
+    bool b;
+    napi_get_value_bool(env, v, &b);
+    *out = b ? 1.0 : 0.0;
+    return 1;
+  }
+  return napi_get_value_double(env, v, out) == napi_ok;
+}
+
+static napi_value js_matmul_topk_sample(napi_env env, napi_callback_info info) {
+  size_t argc = 8;
+  napi_value argv[8];
+  CHECK(env, napi_get_cb_info(env, info, &argc, argv, NULL, NULL));
+  Job *j = (Job *)calloc(1, sizeof(Job));
+  void *in, *rng;
+  size_t rng_len = 0;
+  double do_sample = 1, top_k = 0, temperature = 0, top_p = 0;
+  if (!j) return NULL;
+  j->kind = JOB_SAMPLE;
+  j->count = 1;
+  if (argc < 8 || !get_u64(env, argv[0], &j->handles[0]) ||
+      !get_typed(env, argv[1], napi_float32_array, &in, &j->input_len) || !get_size(env, argv[2], &j->input_size) ||
+      !get_size(env, argv[3], &j->columns) || !get_size(env, argv[4], &j->k) ||
+      napi_get_value_double(env, argv[5], &j->softcap) != napi_ok || !get_prop_f64(env, argv[6], "topK", &top_k) ||
+      !get_prop_f64(env, argv[6], "temperature", &temperature) || !get_prop_f64(env, argv[6], "topP", &top_p) ||
+      !get_typed(env, argv[7], napi_uint32_array, &rng, &rng_len) || rng_len < 1) {
+    free_job(j);
+    napi_throw_type_error(env, NULL,
+                          "matmulTopKSample(handle, Float32Array, inputSize, columnCount, k, softcap, "
+                          "{doSample, topK, temperature, topP}, Uint32Array rngState)");
+    return NULL;
+  }
+  get_prop_f64(env, argv[6], "doSample", &do_sample);
+  j->sampling.do_sample = do_sample != 0;
+  j->sampling.top_k = top_k >= 2147483647.0 ? 2147483647 : (int32_t)top_k;
+  j->sampling.temperature = temperature;
+  j->sampling.top_p = top_p;
+  j->input = (const float *)in;
+  j->rng_out = (uint32_t *)rng;
+  j->rng = j->rng_out[0];
+  j->output_lens[0] = j->columns * j->k;
+  const size_t n = j->output_lens[0] ? j->output_lens[0] : 1, c = j->columns ? j->columns : 1;
+  j->ids = (uint32_t *)malloc(n * 4);
+  j->outputs[0] = (float *)malloc(n * 4);
+  j->probs = (double *)malloc(n * 8);
+  j->tokens = (int32_t *)malloc(c * 4);
+  j->kept = (int32_t *)malloc(c * 4);
+  if (!j->ids || !j->outputs[0] || !j->probs || !j->tokens || !j->kept) {
+    free_job(j);
+    napi_throw_error(env, NULL, "matmulTopKSample: out of host memory");
+    return NULL;
+  }
+  napi_create_reference(env, argv[7], 1, &j->rng_ref);  /* the state array outlives the worker */
+  return start_job(env, j, argv[1], "hp_hip_matmul_topk_sample");
 }
 
 /* ---- synchronous test hooks -------------------------------------------- */
@@ -753,6 +848,7 @@ static napi_value init_module(napi_env env, napi_value exports) {
       {"matmulMulti", NULL, js_matmul_multi, NULL, NULL, NULL, napi_enumerable, NULL},
       {"matmulTopK", NULL, js_matmul_topk, NULL, NULL, NULL, napi_enumerable, NULL},
       {"matmulGeglu", NULL, js_matmul_geglu, NULL, NULL, NULL, napi_enumerable, NULL},
+      {"matmulTopKSample", NULL, js_matmul_topk_sample, NULL, NULL, NULL, napi_enumerable, NULL},
       {"dequantize", NULL, js_dequantize, NULL, NULL, NULL, napi_enumerable, NULL},
       {"geglu", NULL, js_geglu, NULL, NULL, NULL, napi_enumerable, NULL},
       {"ggufOpen", NULL, js_gguf_open, NULL, NULL, NULL, napi_enumerable, NULL},

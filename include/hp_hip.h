@@ -148,6 +148,39 @@ int32_t hp_hip_topk(const float *logits, size_t rows, size_t n, size_t k, double
 int32_t hp_hip_topk_device(const float *d_logits, size_t rows, size_t n, size_t k, double softcap,
                            uint32_t *d_ids, float *d_values, void *stream);
 
+/* Next-token sampling options, resolved as resolveGenerationSamplingOptions
+ * does (generation.ts:40-76): greedy when do_sample == 0 or temperature ==
+ * 0; top_k = floor(topK) >= 1; temperature finite >= 0; top_p in (0, 1]. */
+typedef struct hp_hip_sampling {
+  int32_t do_sample;
+  int32_t top_k;
+  double temperature;
+  double top_p;
+} hp_hip_sampling_t;
+
+/* sampleNextToken / tokenSamplingDistribution (generation.ts:89-165) on the
+ * device, over top-k candidates [column_count][k] in the order the top-k
+ * entry points produce (value descending, ties to the lower id; count <= k
+ * valid per column).  Per column: the top_k slice, top-p nucleus
+ * (applyTopP), softmax of value / temperature in double with the JS engine's
+ * exp, one draw from the generator (createDeterministicRng, state at
+ * *d_rng_state, advanced per sampled column in column order; greedy draws
+ * nothing).  Writes d_tokens [column_count], d_kept [column_count] (the
+ * nucleus size) and d_probabilities [column_count][k] (first kept valid),
+ * bit-exact with the reference.  Asynchronous on stream (NULL = library
+ * stream); a decode loop keeps the generator state in HBM across steps. */
+int32_t hp_hip_sample_device(const uint32_t *d_ids, const float *d_values, size_t column_count, size_t k,
+                             size_t count, const hp_hip_sampling_t *sampling, uint32_t *d_rng_state,
+                             int32_t *d_tokens, double *d_probabilities, int32_t *d_kept, void *stream);
+/* Output head + top-k + sampling in one call (forwardOutput, then
+ * sampleNextToken per column).  *rng_state (host) is read and advanced.
+ * ids / values / probabilities are [column_count][k] (out_len =
+ * column_count * k); tokens and kept are [column_count]. */
+int32_t hp_hip_matmul_topk_sample(uint64_t handle, const float *input, size_t input_len, size_t input_size,
+                                  size_t column_count, size_t k, double softcap, const hp_hip_sampling_t *sampling,
+                                  uint32_t *rng_state, int32_t *tokens, uint32_t *ids, float *values,
+                                  double *probabilities, int32_t *kept, size_t out_len);
+
 /* GeGLU epilogue (layers.ts:450-456 with gelu 1062-1076):
  * out[i] = fround(gelu(gate[i]) * up[i]), bit-exact with the JS engine. */
 int32_t hp_hip_geglu(const float *gate, const float *up, size_t n, float *output);

@@ -543,6 +543,53 @@ static uint32_t hiw(double x) { uint64_t b; memcpy(&b, &x, 8); return (uint32_t)
 static uint32_t low(double x) { uint64_t b; memcpy(&b, &x, 8); return (uint32_t)b; }
 static double words(uint32_t hi, uint32_t lo) { uint64_t b = ((uint64_t)hi << 32) | lo; double d; memcpy(&d, &b, 8); return d; }
 
+/* Math.exp as V8 evaluates it: fdlibm's e_exp.c in FreeBSD msun's form (the
+ * published algorithm V8 ships as ieee754::exp), including V8's exact answer
+ * for exp(1).  Called by the sampling softmax, generation.ts:157-165.
+ * Pinned against Math.exp outputs in tests/golden/v8_exp.json. */
+double hpo_exp(double x) {
+  const double o_threshold = 7.09782712893383973096e+02, u_threshold = -7.45133219101941108420e+02,
+               ln2hi = 6.93147180369123816490e-01, ln2lo = 1.90821492927058770002e-10,
+               invln2 = 1.44269504088896338700e+00, P1 = 1.66666666666666019037e-01,
+               P2 = -2.77777777770155933842e-03, P3 = 6.61375632143793436117e-05,
+               P4 = -1.65339022054652515390e-06, P5 = 4.13813679705723846039e-08,
+               E = 2.718281828459045, huge = 1.0e+300, twom1000 = 9.33263618503218878990e-302,
+               two1023 = 8.988465674311579539e307;
+  uint32_t hx = hiw(x);
+  int xsb = (int)(hx >> 31);
+  double hi = 0, lo = 0, t, c, y, twopk;
+  int k = 0;
+  hx &= 0x7fffffffu;
+  if (hx >= 0x40862E42u) {
+    if (hx >= 0x7ff00000u) return (((hx & 0xfffffu) | low(x)) != 0) ? x + x : (xsb ? 0.0 : x);
+    if (x > o_threshold) return huge * huge;
+    if (x < u_threshold) return twom1000 * twom1000;
+  }
+  if (hx > 0x3FD62E42u) {
+    if (hx < 0x3FF0A2B2u) {
+      if (x == 1.0) return E;
+      hi = xsb ? x + ln2hi : x - ln2hi;
+      lo = xsb ? -ln2lo : ln2lo;
+      k = 1 - 2 * xsb;
+    } else {
+      k = (int)(invln2 * x + (xsb ? -0.5 : 0.5));
+      t = k;
+      hi = x - t * ln2hi;
+      lo = t * ln2lo;
+    }
+    x = hi - lo;
+  } else if (hx < 0x3E300000u) {
+    if (huge + x > 1.0) return 1.0 + x;
+  }
+  t = x * x;
+  twopk = words(0x3FF00000u + ((uint32_t)(k >= -1021 ? k : k + 1000) << 20), 0);
+  c = x - t * (P1 + t * (P2 + t * (P3 + t * (P4 + t * P5))));
+  if (k == 0) return 1.0 - ((x * c) / (c - 2.0) - x);
+  y = 1.0 - ((lo - (x * c) / (2.0 - c)) - hi);
+  if (k >= -1021) return k == 1024 ? y * 2.0 * two1023 : y * twopk;
+  return y * twopk * twom1000;
+}
+
 double hpo_expm1(double x) {
   const double o_threshold = 7.09782712893383973096e+02, ln2_hi = 6.93147180369123816490e-01,
                ln2_lo = 1.90821492927058770002e-10, invln2 = 1.44269504088896338700e+00,

@@ -84,6 +84,7 @@ int32_t hpo_matmul_quantized_multi_threaded(size_t count, const float *input, si
 /* Math.tanh / expm1 as V8 computes them (fdlibm s_tanh.c, s_expm1.c). */
 double hpo_tanh(double x);
 double hpo_expm1(double x);
+double hpo_exp(double x);
 /* gelu: packages/engine/src/runner/wasm/layers.ts:1062-1076 (returns an f32). */
 float hpo_gelu(float v);
 /* GeGLU: layers.ts:450-456: out[i] = fround(gelu(gate[i]) * up[i]). */

@@ -83,6 +83,8 @@ def lib() -> ctypes.CDLL:
     L.hpo_matmul_quantized_multi_threaded.restype = ctypes.c_int32
     L.hpo_gelu.argtypes = [ctypes.c_float]
     L.hpo_gelu.restype = ctypes.c_float
+    L.hpo_exp.argtypes = [ctypes.c_double]
+    L.hpo_exp.restype = ctypes.c_double
     L.hpo_geglu.argtypes = [_f32p, _f32p, _sz, _f32p]
     L.hpo_topk.argtypes = [_f32p, _sz, _sz, _u32p, _f32p]
     L.hpo_topk.restype = _sz
@@ -229,6 +231,11 @@ def matmul_multi(type_ids, weights, x: np.ndarray, row_counts, threads: int = 0)
 
 
 # ---- epilogues ----------------------------------------------------------------
+def exp(x: float) -> float:
+    """Math.exp as the JS engine computes it (fdlibm e_exp.c)."""
+    return lib().hpo_exp(x)
+
+
 def gelu(v: float) -> float:
     return lib().hpo_gelu(v)
 

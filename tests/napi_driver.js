@@ -41,6 +41,12 @@ async function api() {
     ),
     assertShape: await throws(() => hip.assertHipOk(1, "k")),
     assertType: await throws(() => hip.assertHipOk(3, "k")),
+    sampling: hip.resolveGenerationSamplingOptions(),
+    samplingGreedy: hip.resolveGenerationSamplingOptions({ doSample: false, topK: 64 }).logitsTopK,
+    samplingTopK: hip.resolveGenerationSamplingOptions({ topK: 64.9 }).topK,
+    samplingBadTemp: await throws(() => hip.resolveGenerationSamplingOptions({ temperature: -1 })),
+    samplingBadTopP: await throws(() => hip.resolveGenerationSamplingOptions({ topP: 1.1 })),
+    samplingState: Array.from(hip.createHipSamplingState(-1)),
   };
   process.stdout.write(JSON.stringify(out));
 }
@@ -74,6 +80,14 @@ async function run(dir) {
   ]);
   fs.writeFileSync(path.join(dir, "out_geglu.bin"), Buffer.from(geglu.buffer, geglu.byteOffset, geglu.byteLength));
   fs.writeFileSync(path.join(dir, "out_topk.json"), JSON.stringify(top));
+  // head + top-k + sampling with a seeded state, twice (the state advances)
+  const sampling = hip.resolveGenerationSamplingOptions({ temperature: 0.8, topP: 0.9, topK: 40, seed: spec.seed });
+  const state = hip.createHipSamplingState(sampling.seed);
+  const sampled = [];
+  for (let i = 0; i < 2; i += 1) {
+    sampled.push(await hip.matMulQuantizedHipResidentTopKSample(handles[5], x, spec.inputSize, spec.columns, sampling, state, spec.softcap));
+  }
+  fs.writeFileSync(path.join(dir, "out_sample.json"), JSON.stringify({ sampled, state: state[0] }));
   const mismatch = await throws(() => hip.matMulQuantizedHipResident(handles[0], x, spec.inputSize + 256, spec.weights[0].rows, spec.columns));
   handles.forEach((h) => hip.releaseHipQuantizedWeightHandle(h));
   const after = hip.hipResidentWeightStats();

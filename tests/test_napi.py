@@ -39,7 +39,8 @@ def _node(*args, timeout=90):
 def test_addon_api_without_gpu():
     out = _node("api")
     assert out["exports"] == sorted([
-        "HipGgufFile", "HipGgufWeights", "openHipGgufFile",
+        "HipGgufFile", "HipGgufWeights", "openHipGgufFile", "DEFAULT_SAMPLING_SEED", "createHipSamplingState",
+        "matMulQuantizedHipResidentTopKSample", "resolveGenerationSamplingOptions",
         "assertHipOk", "checkHipSupport", "createHipQuantizedWeightHandle", "hipResidentWeightStats",
         "matMulGegluHipResident", "matMulQuantizedHipResident", "matMulQuantizedHipResidentMulti",
         "matMulQuantizedHipResidentTopK", "quantizedTypeId", "releaseHipQuantizedWeightHandle"])
@@ -55,6 +56,11 @@ def test_addon_api_without_gpu():
     assert out["multiShape"] == "Resident quantized multi matmul handle shape mismatch: 512"
     assert out["assertShape"] == "k hip shape mismatch"
     assert out["assertType"] == "k hip unsupported type"
+    assert out["sampling"] == {"doSample": True, "temperature": 1, "topP": 0.95, "topK": 64, "seed": 0x48454C49,
+                               "logitsTopK": 64}                      # generation.test.ts:12-30
+    assert out["samplingGreedy"] == 1 and out["samplingTopK"] == 64
+    assert out["samplingBadTemp"].startswith("temperature") and out["samplingBadTopP"].startswith("topP")
+    assert out["samplingState"] == [0xFFFFFFFF]
 
 
 @needs_node
@@ -68,7 +74,7 @@ def test_addon_projections_bit_exact(oracle, tmp_path):
     for i, w in enumerate(ws):
         (tmp_path / f"w{i}.bin").write_bytes(np.ascontiguousarray(w).tobytes())
     (tmp_path / "x.bin").write_bytes(x.astype(np.float32).tobytes())
-    spec = {"inputSize": k, "columns": m, "topK": top_k, "softcap": softcap,
+    spec = {"inputSize": k, "columns": m, "topK": top_k, "softcap": softcap, "seed": 4242,
             "weights": [{"type": t, "rows": r, "file": f"w{i}.bin"} for i, (t, r) in enumerate(specs)]}
     (tmp_path / "case.json").write_text(json.dumps(spec))
     print(f"napi k={k} m={m}", flush=True)
@@ -94,6 +100,20 @@ def test_addon_projections_bit_exact(oracle, tmp_path):
         assert np.array_equal(got_vals.view(np.uint32), vals.view(np.uint32))
     assert res["residentBefore"] > 0 and res["residentAfter"] == 0 and res["handlesAfter"] == 0
     assert res["mismatch"] == "Resident quantized matmul handle shape mismatch: 2560x64"
+    from oracle import sampling as SM
+
+    sampled = json.loads((tmp_path / "out_sample.json").read_text())
+    opts = SM.resolve_options(temperature=0.8, topP=0.9, topK=40, seed=4242)
+    rng = SM.DeterministicRng(4242)
+    for call in sampled["sampled"]:
+        for col in range(m):
+            capped = np.array([oracle.softcap(float(v), softcap) for v in refs[5].reshape(m, -1)[col]], np.float32)
+            ids, vals = oracle.topk(capped, 40)
+            cands = [{"id": int(i), "value": float(v)} for i, v in zip(ids, vals)]
+            dist = SM.token_sampling_distribution(cands, opts)
+            assert call[col]["token"] == SM.sample_next_token(cands, opts, rng)
+            assert [d["probability"] for d in call[col]["distribution"]] == [d["probability"] for d in dist]
+    assert sampled["state"] == rng.state
 
 
 def _jsonable(v):
