@@ -9,8 +9,10 @@ Other workloads (``--workload``): ``cfg1`` (one Q4_K 10240x2560 matvec),
 ``gate_up`` (two Q4_K 10240x2560 in one launch), ``down`` (Q6_K 2560x10240),
 ``ffn`` (gate/up launch -> GeGLU -> down), ``head`` (Q6_K 262144x2560 output
 head + top-40 per column, candidates only), ``decode42`` (the projection chain
-of one decode step of a 42-layer model, in one graph) and ``gguf-load`` (a
-3.02 GB GGUF file of that model streamed into HBM-resident handles).
+of one decode step of a 42-layer model, in one graph), ``prefill42`` (a
+512-token chunk through that model's projections on the matrix cores) and
+``gguf-load`` (a 3.02 GB GGUF file of that model streamed into HBM-resident
+handles).
 
 Weights are GGUF super-blocks generated from a fixed seed and uploaded once;
 steps rotate over enough distinct weight copies (>= 640 MiB) that every step
@@ -111,7 +113,7 @@ def parse() -> argparse.Namespace:
     p.add_argument("--steps", type=int, default=400)
     p.add_argument("--warmup", type=int, default=40)
     p.add_argument("--m", type=int, default=1)
-    p.add_argument("--workload", choices=sorted(WORKLOADS) + ["decode42", "gguf-load"], default="qkv")
+    p.add_argument("--workload", choices=sorted(WORKLOADS) + ["decode42", "prefill42", "gguf-load"], default="qkv")
     p.add_argument("--rotate-mib", type=int, default=640, help="distinct weight bytes cycled through")
     p.add_argument("--cpu-seconds", type=float, default=12.0)
     p.add_argument("--no-cpu", action="store_true")
@@ -265,6 +267,88 @@ def decode_chain(args) -> int:
     return 0
 
 
+MFMA_F16_PEAK_TFLOPS = 2500.0  # dense f16 matrix-core peak, MI355X
+
+
+def prefill_chain(args) -> int:
+    """Projections of one 512-token prefill chunk through the 42-layer model:
+    per layer Q/K/V (one launch over all 512 columns) -> O (fed Q's outputs)
+    -> gate/up + GeGLU -> down, every layer's weights a distinct device copy;
+    captured in one HIP graph.  FLOPs = 2 * 512 * (projection weights of the
+    42 layers) = 3.946e12.  The head is not part of prefill (only the last
+    token's logits are needed) and attention is not run."""
+    import numpy as np
+    import torch
+
+    from heliopause_amd import hip_kernels as H
+    from heliopause_amd import synthetic as S
+
+    m = args.m if args.m > 1 else 512
+    H.setMatvecKernel({"auto": H.MATVEC_AUTO, "valu": H.MATVEC_VALU, "mfma": H.MATVEC_MFMA,
+                       "half": H.MATVEC_HALF}[args.kernel])
+    torch.cuda.init()
+    dev = torch.device("cuda:0")
+    seed = S.config_seed(5)
+    host = {}
+    for i, (t, r, k) in enumerate(LAYER):
+        if (t, r, k) not in host:
+            host[(t, r, k)] = S.weight_blocks(t, S.derive(seed, "decode42", i), r, k)
+    layers = [[H.createHipQuantizedWeightHandle(t, host[(t, r, k)], k, r).handle for t, r, k in LAYER]
+              for _ in range(N_LAYERS)]
+    x = torch.from_numpy(S.activations(S.derive(seed, "prefill-x"), m, 2560)).to(dev)
+    buf = {n: torch.empty(m * c, dtype=torch.float32, device=dev)
+           for n, c in (("q", 2048), ("k", 512), ("v", 512), ("o", 2560), ("h", 10240), ("y", 2560))}
+    p = {n: t.data_ptr() for n, t in buf.items()}
+
+    def step(stream: int) -> None:
+        for hs in layers:
+            H.matmul_multi_device(hs[0:3], x.data_ptr(), 2560, m, [p["q"], p["k"], p["v"]],
+                                  [2048 * m, 512 * m, 512 * m], stream)
+            H.matmul_multi_device(hs[3:4], p["q"], 2048, m, [p["o"]], [2560 * m], stream)
+            H.matmul_geglu_device(hs[4], hs[5], p["o"], 2560, m, p["h"], 10240, stream)
+            H.matmul_multi_device(hs[6:7], p["h"], 10240, m, [p["y"]], [2560 * m], stream)
+
+    side = torch.cuda.Stream()
+    with torch.cuda.stream(side):
+        step(side.cuda_stream)
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=side):
+            step(torch.cuda.current_stream().cuda_stream)
+    warm = max(1, args.warmup // 40)
+    for _ in range(warm):
+        graph.replay()
+    torch.cuda.synchronize()
+    steps = max(1, args.steps // 80)
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    start.record()
+    for _ in range(steps):
+        graph.replay()
+    end.record()
+    torch.cuda.synchronize()
+    wall_ms = (time.perf_counter() - t0) / steps * 1e3
+    ms = start.elapsed_time(end) / steps
+    weights = N_LAYERS * sum(r * k for _, r, k in LAYER)
+    flops = 2.0 * m * weights
+    tflops = flops / (ms * 1e-3) / 1e12
+    line = {
+        "metric": f"prefill chunk projections ms at M={m} (1 GPU)",
+        "value": round(ms, 4), "unit": "ms", "n_gpus": 1, "steps": steps, "warmup": warm,
+        "ms_per_step": round(ms, 4), "higher_is_better": False, "scaling": "weak", "vs_baseline": None,
+        "dtype": "f16 MFMA (exact integers) + f32 tail", "data": "synthetic",
+        "config": {"workload": f"42-layer synthetic Gemma-like model, projections + GeGLU of a {m}-token prefill "
+                               "chunk (head and attention not included)",
+                   "columns": m, "weight_elements": weights, "flops": flops,
+                   "launches_per_step": N_LAYERS * 9, "wall_ms_per_step": round(wall_ms, 4),
+                   "timing": "one chunk captured in a HIP graph and replayed"},
+        "roofline": {"bound": "mfma", "achieved": round(tflops, 2), "peak": MFMA_F16_PEAK_TFLOPS, "unit": "TFLOP/s",
+                     "frac": round(tflops / MFMA_F16_PEAK_TFLOPS, 4), "traffic": None},
+    }
+    print(json.dumps(line))
+    return 0
+
+
 PCIE_PEAK_GBPS = 64.0  # PCIe 5.0 x16, one direction
 
 
@@ -400,6 +484,8 @@ def main() -> int:
         return decode_chain(args)
     if args.workload == "gguf-load":
         return gguf_load(args)
+    if args.workload == "prefill42":
+        return prefill_chain(args)
     import numpy as np
     import torch
 

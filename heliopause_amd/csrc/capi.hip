@@ -54,7 +54,9 @@ struct State {
   void *topk_scratch = nullptr, *topk_out = nullptr;  // selection scratch; ids + values
   size_t topk_scratch_cap = 0, topk_out_cap = 0;
   uint64_t matmul_calls = 0, launches = 0;
-  int matvec_kernel = 0;  // 0 auto, 1 vector ALU, 2 matrix cores
+  int matvec_kernel = 0;  // 0 auto, 1 vector ALU, 2 matrix cores, 3 half-split, 4 prefill
+  void *prefill_scratch = nullptr;  // Q8_K of the columns of a prefill launch
+  size_t prefill_scratch_cap = 0;
   bool profiling = false;
   ProfileSlot prof[HP_KERNEL_COUNT];
   std::vector<hipEvent_t> event_pool;
@@ -217,6 +219,29 @@ int cols_per_launch(const TileGeom &g, size_t max_lds) {
 // matrix cores win from five columns on, and from two columns on when the
 // launch has >= 1024 tiles (16 rows each); one column stays on the vector
 // ALU.  Both need their LDS (the columns' Q8_K for every block) to fit.
+// Prefill kernels (matrix cores, columns in tiles of 64, weights read once per
+// column tile) for many columns.  From kFastMinCols columns the automatic
+// policy takes the fast one, whose outputs agree with the reference within the
+// 1e-4 relative tolerance of projections (M >= 64 prefill chunks); selector 4
+// forces the bit-exact one, 5 the fast one.  Below kPrefillMinCols the decode
+// kernels, which read the weights once per 8 columns, are as fast.
+constexpr size_t kPrefillMinCols = 32;
+constexpr size_t kFastMinCols = 64;
+
+// 0: not a prefill launch, 1: bit-exact prefill, 2: fast prefill
+int prefill_kind(size_t cols) {
+  const State &s = st();
+  const int forced = s.matvec_kernel;
+  const bool exact_fits = prefill_lds_bytes() <= s.max_lds;
+  const bool fast_fits = prefill_fast_lds_bytes() <= s.max_lds;
+  if (forced == 4) return exact_fits ? 1 : 0;
+  if (forced == 5) return fast_fits ? 2 : 0;
+  if (forced != 0) return 0;
+  if (cols >= kFastMinCols && fast_fits) return 2;
+  if (cols >= kPrefillMinCols && exact_fits) return 1;
+  return 0;
+}
+
 bool use_mfma(size_t cols, int nb, int tiles16) {
   const State &s = st();
   const int forced = s.matvec_kernel;
@@ -272,6 +297,35 @@ int32_t run_matvec(size_t count, Handle *const *hs, const float *d_input, size_t
     units += a.w[i].units;
   }
   a.total_units = units;
+  if (const int kind = prefill_kind(cols)) {
+    if (cols > 65535) return fail(HP_ERR_SHAPE, "too many columns");
+    const size_t need = kind == 2 ? prefill_fast_bytes((int)input_size, (int)cols)
+                                  : prefill_q8k_bytes((int)input_size, (int)cols);
+    int32_t rc = grow(&s.prefill_scratch, &s.prefill_scratch_cap, need);
+    if (rc != HP_OK) return rc;
+    uint8_t *q8 = static_cast<uint8_t *>(s.prefill_scratch);
+    MfmaLaunch l{};
+    l.count = (int)count;
+    l.k = (int)input_size;
+    l.cols = (int)cols;
+    for (size_t i = 0; i < count; i++) {
+      l.seg[i] = hs[i]->segs;
+      l.type[i] = hs[i]->type;
+      l.rows[i] = (int)hs[i]->row_count;
+      l.out[i] = d_outs[i];
+    }
+    hipEvent_t e1 = prof_begin(stream);
+    if (kind == 2) {
+      HP_HIP_TRY(launch_prefill_fast(l, d_input, q8, s.num_cus, stream));
+    } else {
+      HP_HIP_TRY(launch_q8k_prefill(d_input, (int)input_size, (int)cols, q8, stream));
+      HP_HIP_TRY(launch_prefill(l, q8, s.num_cus, stream));
+    }
+    prof_end(HP_KERNEL_MATVEC, e1, stream);
+    s.launches += 2;
+    s.matmul_calls++;
+    return HP_OK;
+  }
   int tiles16 = 0;
   for (size_t i = 0; i < count; i++) tiles16 += (int)((hs[i]->row_count + 15) / 16);
   if (use_mfma(cols, g.nb, tiles16)) {
@@ -708,6 +762,9 @@ int32_t hp_hip_shutdown(void) {
   if (s.topk_scratch) (void)hipFree(s.topk_scratch);
   if (s.topk_out) (void)hipFree(s.topk_out);
   if (s.sample_out) (void)hipFree(s.sample_out);
+  if (s.prefill_scratch) (void)hipFree(s.prefill_scratch);
+  s.prefill_scratch = nullptr;
+  s.prefill_scratch_cap = 0;
   s.sample_out = nullptr;
   s.sample_out_cap = 0;
   s.topk_scratch = s.topk_out = nullptr;
@@ -1192,7 +1249,7 @@ int32_t hp_hip_quantize_q8_k(const float *input, size_t input_len, size_t input_
 int32_t hp_hip_set_matvec_kernel(int32_t which) {
   State &s = st();
   std::lock_guard<std::recursive_mutex> lock(s.mu);
-  if (which < 0 || which > 3) return fail(HP_ERR_ARG, "kernel selector must be 0..3");
+  if (which < 0 || which > 5) return fail(HP_ERR_ARG, "kernel selector must be 0..5");
   s.matvec_kernel = which;
   return HP_OK;
 }

@@ -133,6 +133,24 @@ size_t mfma_segment_bytes(int type, int rows, int nb);
 size_t mfma_lds_bytes(int cols, int nb);
 hipError_t launch_repack_mfma(int type, const uint8_t *raw, int rows, int nb, uint8_t *segs, hipStream_t s);
 hipError_t launch_matvec_mfma(const MfmaLaunch &l, int num_cus, hipStream_t s);
+
+// Prefill (many columns) on the matrix cores: a Q8_K pre-pass writes
+// prefill_q8k_bytes(k, cols) of class-major quants, half-block sums and
+// scales to `scratch`; launch_prefill runs every weight of `l` (l.x unused,
+// l.cols = all columns, l.out_col0 = 0) over them.  Needs prefill_lds_bytes()
+// of LDS per workgroup.
+size_t prefill_q8k_bytes(int k, int cols);
+size_t prefill_lds_bytes();
+hipError_t launch_q8k_prefill(const float *x, int k, int cols, uint8_t *scratch, hipStream_t s);
+hipError_t launch_prefill(const MfmaLaunch &l, const uint8_t *scratch, int num_cus, hipStream_t s);
+// Fast prefill (within the 1e-4 relative tolerance of projections, not
+// bit-exact): its own pre-pass of x into prefill_fast_bytes(k, cols) of
+// scratch, then 128-row x 64-column tiles with the eight classes in one
+// accumulator.
+size_t prefill_fast_bytes(int k, int cols);
+size_t prefill_fast_lds_bytes();
+hipError_t launch_prefill_fast(const MfmaLaunch &l, const float *x, uint8_t *scratch, int num_cus, hipStream_t s);
+
 hipError_t launch_geglu(const float *gate, const float *up, size_t n, double c, float *out, int num_cus,
                         hipStream_t s);
 hipError_t launch_dequantize(int type, const uint8_t *tiles, const uint16_t *dplane, int rows,

@@ -41,44 +41,11 @@
 //     dword 2*cls + h holds in byte cc the high 2 bits of q6 at
 //     (j = 4h + jj, cc, class 2q + cls) in bits 2jj.
 #include "hp_common.h"
+#include "hp_mfma.h"
 
 namespace hp {
 
-typedef _Float16 half8 __attribute__((ext_vector_type(8)));
-typedef _Float16 half2v __attribute__((ext_vector_type(2)));
-typedef float f32x4 __attribute__((ext_vector_type(4)));
-
 namespace {
-
-__device__ __forceinline__ float h2f_bits(uint32_t bits16) {
-  return (float)__builtin_bit_cast(_Float16, (uint16_t)bits16);
-}
-
-__device__ __forceinline__ uint32_t u4at(const uint4 &v, int i) {
-  return i == 0 ? v.x : i == 1 ? v.y : i == 2 ? v.z : v.w;
-}
-
-__device__ __forceinline__ half2v as_h2(uint32_t v) { return __builtin_bit_cast(half2v, v); }
-__device__ __forceinline__ uint32_t as_u32(half2v v) { return __builtin_bit_cast(uint32_t, v); }
-
-// Halves (1024 + byte a, 1024 + byte b) of dword v: the f16 with exponent
-// bits 0x64 and mantissa = the byte is exactly 1024 + byte (byte < 1024).
-template <uint32_t SEL>
-__device__ __forceinline__ half2v magic_pair(uint32_t v) {
-  return as_h2(__builtin_amdgcn_perm(0x64646464u, v, SEL));
-}
-constexpr uint32_t kSel01 = 0x04010400u;  // bytes 0, 1
-constexpr uint32_t kSel23 = 0x04030402u;  // bytes 2, 3
-
-// (s, s) for scale byte `idx` of dword v (unsigned bytes) and the matching
-// addend -off * s, both exact in f16: fma((1024 + q), s, -off * s) = s * (q + 1024 - off).
-__device__ __forceinline__ half2v dup_byte(uint32_t v, int idx, float bias) {
-  const uint32_t sel = (uint32_t)idx | 0x04000400u | ((uint32_t)idx << 16);
-  const half2v h = as_h2(__builtin_amdgcn_perm(0x64646464u, v, sel));
-  return h - (half2v){(_Float16)bias, (_Float16)bias};
-}
-
-__device__ __forceinline__ half2v fma2(half2v a, half2v b, half2v c) { return __builtin_elementwise_fma(a, b, c); }
 
 struct MfmaWeight {
   const uint8_t *seg;  // segments of this weight
@@ -205,14 +172,6 @@ __device__ __forceinline__ void q8k_block16_f16(const float (&v)[16], int i16, c
   }
   L.bs[((size_t)b * m4 + m) * 16 + i16] = (_Float16)sum;  // |sum| <= 2048: exact
   if (i16 == 0) L.dx[(size_t)b * m4 + m] = nz ? __fdiv_rn(1.0f, inv) : 0.0f;
-}
-
-__device__ __forceinline__ f32x4 mfma(half8 a, half8 b, f32x4 c) {
-  return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
-}
-
-__device__ __forceinline__ half8 cat(half2v a, half2v b, half2v c, half2v d) {
-  return (half8){a[0], a[1], b[0], b[1], c[0], c[1], d[0], d[1]};
 }
 
 __device__ __forceinline__ half8 lds_h8(const void *p) {

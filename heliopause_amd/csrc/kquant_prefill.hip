@@ -1,0 +1,690 @@
+// kquant_prefill.hip -- Q4_K / Q6_K x Q8_K projections of many columns
+// (prefill chunks, M >= 32) on the gfx950 matrix cores, bit-exact with the
+// reference's WASM path (packages/engine/wasm-kernels/src/lib.rs:224-426 with
+// the vec-dots 2116-2172 and 1923-1968).
+//
+// Numerics are those of kquant_mfma.hip: per (row, column, block) the eight
+// integers aux32[l] (l = element index mod 8) come out of one
+// v_mfma_f32_16x16x32_f16 each, exactly, with A = sc * q (f16) and B = q8
+// (f16); the f32 tail then runs in block order per class:
+//   sums[l] += (dW_b * dX_b) * f32(aux32[l]);  Q4_K: sumf -= (dminW_b * dX_b) * f32(sumi)
+//   result = [sumf +] ((((-0 + s0) + s1) + ...) + s7)
+// Here the 16 MFMA columns are 16 input columns and the K = 32 dimension is
+// the 32 elements of one class (quarter q of the A/B lanes carries elements
+// j = 2q, 2q + 1, c = 0..3 of e = 32j + 8c + l), so every MFMA does useful
+// work.  Exactness forces nine f32 chains per output, so the 8 classes are
+// split over the 4 waves of a workgroup: wave w keeps classes 2w, 2w+1 of a
+// 32-row x 64-column tile (64 chains per lane) and the Q4_K min chain of
+// column slice w; the chains are added in class order through LDS at the end
+// of the tile.
+//
+// Data flow per block: the two 16-row weight segments of the tile (the
+// matrix-core layout of kquant_mfma.hip, read straight from HBM, each byte
+// once per column tile) and the 64 columns' Q8_K quants (int8, class-major,
+// written by the pre-pass below) are staged in LDS, double-buffered through
+// registers; A fragments (one dword per lane and class) and B fragments
+// (8 bytes per lane) are built from LDS.
+#include "hp_common.h"
+#include "hp_mfma.h"
+#include "hp_q8k.h"
+
+namespace hp {
+
+namespace {
+
+constexpr int kPfRows = 32;                        // rows per workgroup tile (2 segments)
+constexpr int kPfCols = 64;                        // columns per workgroup tile
+constexpr int kPfXStride = 272;                    // LDS bytes per column of one block's quants (256 + 16)
+constexpr int kPfWBytes = 2 * 3360;                // two segments (Q6_K size)
+constexpr int kPfXQ = kPfWBytes;                   // offsets within one stage buffer
+constexpr int kPfXB = kPfXQ + kPfCols * kPfXStride;
+constexpr int kPfXD = kPfXB + kPfCols * 32;
+constexpr int kPfStage = kPfXD + kPfCols * 4;      // 26,432 bytes
+constexpr int kPfFinStride = 68;                   // floats per row of the combine buffer
+constexpr int kPfLds = 2 * kPfStage + kPfRows * kPfFinStride * 4;
+
+// Q8_K pre-pass: one wave per (column, block) (hp_q8k.h, lib.rs:1774-1811).
+// xq[(m * nb + b) * 256 + 32 l + 4 j + c] = q8 of element 32 j + 8 c + l;
+// xb[(m * nb + b) * 16 + h] = f16 sum of the 16 quants 16 h .. 16 h + 15;
+// xd[m * nb + b] = d.
+__global__ __launch_bounds__(64) void q8k_prefill_kernel(const float *__restrict__ x, int k, int nb,
+                                                         int8_t *__restrict__ xq, _Float16 *__restrict__ xb,
+                                                         float *__restrict__ xd) {
+  const int b = blockIdx.x, m = blockIdx.y, lane = threadIdx.x;
+  const Q8KLane r = q8k_block(x + (size_t)m * k + (size_t)b * kQK, lane);
+  int8_t *dst = xq + ((size_t)m * nb + b) * kQK;
+  // lane owns elements e = 4 lane + i: j = lane / 8, c = (lane / 2) % 4, l = 4 (lane % 2) + i
+  const int base = 4 * (lane >> 3) + ((lane >> 1) & 3);
+#pragma unroll
+  for (int i = 0; i < 4; i++) dst[(4 * (lane & 1) + i) * 32 + base] = r.q[i];
+  int s = (int)r.q[0] + (int)r.q[1] + (int)r.q[2] + (int)r.q[3];
+  s += __shfl_xor(s, 1);
+  s += __shfl_xor(s, 2);
+  if ((lane & 3) == 0) xb[((size_t)m * nb + b) * 16 + (lane >> 2)] = (_Float16)s;  // |s| <= 2048: exact
+  if (lane == 0) xd[(size_t)m * nb + b] = r.d;
+}
+
+struct PfWeight {
+  const uint8_t *seg;
+  float *out;
+  int type, rows, tiles, rt_begin;  // tiles: 16-row segments; rt: 32-row workgroup tiles
+};
+
+struct PfArgs {
+  PfWeight w[kMaxWeights];
+  int count, total_rt, col_tiles, nb, cols;
+  const int8_t *xq;
+  const _Float16 *xb;
+  const float *xd;
+};
+
+// Registers holding one block's staging loads of this thread.
+struct Stage {
+  uint4 w[2], x[4], e;
+};
+
+__device__ __forceinline__ void stage_load(Stage &st, const PfWeight &W, int T0, int b, const PfArgs &a, int col0,
+                                           int tid) {
+  const int segb = W.type == kTypeQ4K ? 2304 : 3360;
+  const int nseg = T0 + 1 < W.tiles ? 2 : 1;
+  const uint8_t *src = W.seg + ((size_t)b * W.tiles + T0) * segb;  // segments T0, T0 + 1 are adjacent
+  const int n16 = nseg * segb / 16;
+#pragma unroll
+  for (int r = 0; r < 2; r++) {
+    const int i = tid + 256 * r;
+    st.w[r] = i < n16 ? reinterpret_cast<const uint4 *>(src)[i] : make_uint4(0, 0, 0, 0);
+  }
+#pragma unroll
+  for (int r = 0; r < 4; r++) {
+    const int i = tid + 256 * r, col = i >> 4, part = i & 15;
+    const int m = col0 + col;
+    st.x[r] = m < a.cols ? reinterpret_cast<const uint4 *>(a.xq + ((size_t)m * a.nb + b) * kQK)[part]
+                         : make_uint4(0, 0, 0, 0);
+  }
+  st.e = make_uint4(0, 0, 0, 0);
+  if (tid < 128) {  // bs16: 64 columns x 32 bytes
+    const int col = tid >> 1, m = col0 + col;
+    st.e = m < a.cols ? reinterpret_cast<const uint4 *>(a.xb + ((size_t)m * a.nb + b) * 16)[tid & 1]
+                      : make_uint4(0, 0, 0, 0);
+  } else if (tid < 144) {  // d: 64 columns x 4 bytes
+    const int c4 = tid - 128;
+    float v[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      const int m = col0 + 4 * c4 + i;
+      v[i] = m < a.cols ? a.xd[(size_t)m * a.nb + b] : 0.0f;
+    }
+    st.e = make_uint4(__float_as_uint(v[0]), __float_as_uint(v[1]), __float_as_uint(v[2]), __float_as_uint(v[3]));
+  }
+}
+
+__device__ __forceinline__ void stage_store(const Stage &st, uint8_t *buf, int tid) {
+#pragma unroll
+  for (int r = 0; r < 2; r++) {
+    const int i = tid + 256 * r;
+    if (i < kPfWBytes / 16) reinterpret_cast<uint4 *>(buf)[i] = st.w[r];
+  }
+#pragma unroll
+  for (int r = 0; r < 4; r++) {
+    const int i = tid + 256 * r, col = i >> 4, part = i & 15;
+    *reinterpret_cast<uint4 *>(buf + kPfXQ + col * kPfXStride + 16 * part) = st.x[r];
+  }
+  if (tid < 128)
+    reinterpret_cast<uint4 *>(buf + kPfXB)[tid] = st.e;
+  else if (tid < 144)
+    reinterpret_cast<uint4 *>(buf + kPfXD)[tid - 128] = st.e;
+}
+
+// B fragment: 8 int8 quants of (column n, class l, quarter q) as f16.
+__device__ __forceinline__ half8 b_frag(const uint8_t *xq_col, int l, int q) {
+  const uint2 v = *reinterpret_cast<const uint2 *>(xq_col + 32 * l + 8 * q);
+  // (byte ^ 0x80) is q8 + 128 < 256: 1024 + that as f16, minus 1152, is q8 exactly
+  const uint32_t lo = v.x ^ 0x80808080u, hi = v.y ^ 0x80808080u;
+  const half2v off = (half2v){(_Float16)1152.0f, (_Float16)1152.0f};
+  return cat(magic_pair<kSel01>(lo) - off, magic_pair<kSel23>(lo) - off, magic_pair<kSel01>(hi) - off,
+             magic_pair<kSel23>(hi) - off);
+}
+
+// A fragment of class l for the 16 rows of one segment: lane (row n,
+// quarter q) takes the dword of (chunk l % 2, u = q) that segment lane
+// (n, l / 2) holds, i.e. elements j = 2q, 2q + 1, c = 0..3 of class l.
+template <bool Q4>
+__device__ __forceinline__ half8 a_frag(const uint8_t *seg, int l, int n, int q) {
+  const int g = l & 1, src = n + 16 * (l >> 1);
+  if constexpr (Q4) {
+    const uint4 hdr = *reinterpret_cast<const uint4 *>(seg + 16 * n);
+    const uint32_t sclo = hdr.y & 0x3F3F3F3Fu;
+    const uint32_t schi = (hdr.w & 0x0F0F0F0Fu) | ((hdr.y >> 2) & 0x30303030u);
+    const uint32_t sc = q < 2 ? sclo : schi;  // scales of j = 2q, 2q + 1 are bytes 2(q%2), 2(q%2)+1
+    const half2v S0 = dup_byte(sc, 2 * (q & 1), 1024.0f), S1 = dup_byte(sc, 2 * (q & 1) + 1, 1024.0f);
+    const half2v m1024 = (half2v){(_Float16)-1024.0f, (_Float16)-1024.0f};
+    const half2v N0 = S0 * m1024, N1 = S1 * m1024;
+    const uint32_t dw = *reinterpret_cast<const uint32_t *>(seg + 256 + 1024 * g + 16 * src + 4 * q);
+    const uint32_t lo = dw & 0x0F0F0F0Fu, hi = (dw >> 4) & 0x0F0F0F0Fu;
+    return cat(fma2(magic_pair<kSel01>(lo), S0, N0), fma2(magic_pair<kSel23>(lo), S0, N0),
+               fma2(magic_pair<kSel01>(hi), S1, N1), fma2(magic_pair<kSel23>(hi), S1, N1));
+  } else {
+    // groups 16-element: g(j, c) = 2j + c/2; for u = q: 4q, 4q+1 (j = 2q) and 4q+2, 4q+3 (j = 2q+1)
+    const uint32_t gs = *reinterpret_cast<const uint32_t *>(seg + 16 * n + 4 * q) ^ 0x80808080u;
+    half2v S[4], N[4];
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+      S[e] = dup_byte(gs, e, 1152.0f);
+      N[e] = S[e] * (half2v){(_Float16)-1056.0f, (_Float16)-1056.0f};
+    }
+    const int jj = 2 * (q & 1);
+    const uint32_t ql = *reinterpret_cast<const uint32_t *>(seg + 288 + 1024 * g + 16 * src + 4 * q);
+    const uint32_t qh = *reinterpret_cast<const uint32_t *>(seg + 288 + 2048 + 16 * src + 4 * (2 * g + (q >> 1)));
+    const uint32_t lo = (ql & 0x0F0F0F0Fu) | (((qh >> (2 * jj)) & 0x03030303u) << 4);
+    const uint32_t hi = ((ql >> 4) & 0x0F0F0F0Fu) | (((qh >> (2 * jj + 2)) & 0x03030303u) << 4);
+    return cat(fma2(magic_pair<kSel01>(lo), S[0], N[0]), fma2(magic_pair<kSel23>(lo), S[1], N[1]),
+               fma2(magic_pair<kSel01>(hi), S[2], N[2]), fma2(magic_pair<kSel23>(hi), S[3], N[3]));
+  }
+}
+
+struct PfChains {
+  float s[2][2][4][4];  // [class of the wave][row segment][column slice][row j of the D layout]
+  float f[2][4];        // Q4_K min chain of the wave's column slice: [row segment][j]
+};
+
+// One block of the tile from stage buffer `buf`.
+template <bool Q4>
+__device__ __forceinline__ void pf_block(PfChains &ch, const uint8_t *buf, int wave, int lane) {
+  const int n = lane & 15, q = lane >> 4;
+  const int segb = Q4 ? 2304 : 3360;
+  // dW of rows 16 rs + 4q + j, dX of columns 16 cs + n
+  float dw[2][4], dmw[2][4], dx[4];
+#pragma unroll
+  for (int rs = 0; rs < 2; rs++)
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+      const int row = 4 * q + j;
+      if constexpr (Q4) {
+        const uint32_t v = *reinterpret_cast<const uint32_t *>(buf + rs * segb + 16 * row);
+        dw[rs][j] = h2f_bits(v & 0xFFFFu);
+        dmw[rs][j] = h2f_bits(v >> 16);
+      } else {
+        dw[rs][j] = h2f_bits(*reinterpret_cast<const uint16_t *>(buf + rs * segb + 256 + 2 * row));
+        dmw[rs][j] = 0.0f;
+      }
+    }
+#pragma unroll
+  for (int cs = 0; cs < 4; cs++) dx[cs] = reinterpret_cast<const float *>(buf + kPfXD)[16 * cs + n];
+  float dd[2][4][4];
+#pragma unroll
+  for (int rs = 0; rs < 2; rs++)
+#pragma unroll
+    for (int cs = 0; cs < 4; cs++)
+#pragma unroll
+      for (int j = 0; j < 4; j++) dd[rs][cs][j] = __fmul_rn(dw[rs][j], dx[cs]);
+#pragma unroll
+  for (int li = 0; li < 2; li++) {
+    const int l = 2 * wave + li;
+    const half8 a0 = a_frag<Q4>(buf, l, n, q);
+    const half8 a1 = a_frag<Q4>(buf + segb, l, n, q);
+#pragma unroll
+    for (int cs = 0; cs < 4; cs++) {
+      const half8 bf = b_frag(buf + kPfXQ + (16 * cs + n) * kPfXStride, l, q);
+      const f32x4 z = (f32x4){0.0f, 0.0f, 0.0f, 0.0f};
+      const f32x4 d0 = mfma(a0, bf, z);
+      const f32x4 d1 = mfma(a1, bf, z);
+#pragma unroll
+      for (int j = 0; j < 4; j++) {
+        ch.s[li][0][cs][j] = __fadd_rn(ch.s[li][0][cs][j], __fmul_rn(dd[0][cs][j], d0[j]));
+        ch.s[li][1][cs][j] = __fadd_rn(ch.s[li][1][cs][j], __fmul_rn(dd[1][cs][j], d1[j]));
+      }
+    }
+  }
+  if constexpr (Q4) {
+    // sumi = sum_j mn_j * bsums32_j by one MFMA per segment: quarter q < 2
+    // carries k = 8q + e -> (j = 4q + e/2, half e%2); B = the 16 half sums
+    const int cs = wave;
+    const uint8_t *xcol = buf + kPfXB + (16 * cs + n) * 32;
+    const half8 bm = q < 2 ? __builtin_bit_cast(half8, *reinterpret_cast<const uint4 *>(xcol + 16 * q))
+                           : (half8){0, 0, 0, 0, 0, 0, 0, 0};
+#pragma unroll
+    for (int rs = 0; rs < 2; rs++) {
+      const uint4 hdr = *reinterpret_cast<const uint4 *>(buf + rs * segb + 16 * n);
+      const uint32_t mn = q == 0 ? (hdr.z & 0x3F3F3F3Fu) : (((hdr.w >> 4) & 0x0F0F0F0Fu) | ((hdr.z >> 2) & 0x30303030u));
+      const half8 am = q < 2 ? cat(dup_byte(mn, 0, 1024.0f), dup_byte(mn, 1, 1024.0f), dup_byte(mn, 2, 1024.0f),
+                                   dup_byte(mn, 3, 1024.0f))
+                             : (half8){0, 0, 0, 0, 0, 0, 0, 0};
+      const f32x4 sm = mfma(am, bm, (f32x4){0.0f, 0.0f, 0.0f, 0.0f});
+#pragma unroll
+      for (int j = 0; j < 4; j++) ch.f[rs][j] = __fsub_rn(ch.f[rs][j], __fmul_rn(__fmul_rn(dmw[rs][j], dx[cs]), sm[j]));
+    }
+  }
+}
+
+template <bool Q4>
+__device__ void pf_tile(const PfArgs &a, const PfWeight &W, int T0, int col0, uint8_t *smem, int wave, int lane,
+                        int tid) {
+  PfChains ch;
+#pragma unroll
+  for (int li = 0; li < 2; li++)
+#pragma unroll
+    for (int rs = 0; rs < 2; rs++)
+#pragma unroll
+      for (int cs = 0; cs < 4; cs++)
+#pragma unroll
+        for (int j = 0; j < 4; j++) ch.s[li][rs][cs][j] = 0.0f;
+#pragma unroll
+  for (int rs = 0; rs < 2; rs++)
+#pragma unroll
+    for (int j = 0; j < 4; j++) ch.f[rs][j] = 0.0f;
+
+  Stage st;
+  stage_load(st, W, T0, 0, a, col0, tid);
+  stage_store(st, smem, tid);
+  __syncthreads();
+  for (int b = 0; b < a.nb; b++) {
+    if (b + 1 < a.nb) stage_load(st, W, T0, b + 1, a, col0, tid);
+    pf_block<Q4>(ch, smem + (b & 1) * kPfStage, wave, lane);
+    if (b + 1 < a.nb) stage_store(st, smem + ((b + 1) & 1) * kPfStage, tid);
+    __syncthreads();
+  }
+
+  // class chains in order l = 0..7 through LDS, then [sumf +] and the store
+  float *fin = reinterpret_cast<float *>(smem + 2 * kPfStage);
+  const int n = lane & 15, q = lane >> 4;
+  for (int p = 0; p < 4; p++) {
+    if (wave == p) {
+#pragma unroll
+      for (int rs = 0; rs < 2; rs++)
+#pragma unroll
+        for (int cs = 0; cs < 4; cs++)
+#pragma unroll
+          for (int j = 0; j < 4; j++) {
+            float *slot = fin + (16 * rs + 4 * q + j) * kPfFinStride + 16 * cs + n;
+            const float t = __fadd_rn(p == 0 ? -0.0f : *slot, ch.s[0][rs][cs][j]);
+            *slot = __fadd_rn(t, ch.s[1][rs][cs][j]);
+          }
+    }
+    __syncthreads();
+  }
+  const int cs = wave;
+  const int m = col0 + 16 * cs + n;
+#pragma unroll
+  for (int rs = 0; rs < 2; rs++)
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+      const int row = 16 * (T0 + rs) + 4 * q + j;
+      float v = fin[(16 * rs + 4 * q + j) * kPfFinStride + 16 * cs + n];
+      if (Q4) v = __fadd_rn(ch.f[rs][j], v);
+      if (row < W.rows && m < a.cols) W.out[(size_t)m * W.rows + row] = v;
+    }
+  __syncthreads();  // fin and the stage buffers are reused by the next tile
+}
+
+__global__ __launch_bounds__(256) void kquant_prefill_kernel(const PfArgs a) {
+  extern __shared__ __align__(16) uint8_t smem[];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int items = a.total_rt * a.col_tiles;
+  for (int it = blockIdx.x; it < items; it += gridDim.x) {
+    // column tiles innermost: neighbouring workgroups share a weight tile
+    const int rt = it / a.col_tiles, ct = it - rt * a.col_tiles;
+    PfWeight W = a.w[0];
+    if (a.count > 1 && rt >= a.w[1].rt_begin) W = a.w[1];
+    if (a.count > 2 && rt >= a.w[2].rt_begin) W = a.w[2];
+    if (a.count > 3 && rt >= a.w[3].rt_begin) W = a.w[3];
+    const int T0 = 2 * (rt - W.rt_begin);
+    if (W.type == kTypeQ4K)
+      pf_tile<true>(a, W, T0, ct * kPfCols, smem, wave, lane, tid);
+    else
+      pf_tile<false>(a, W, T0, ct * kPfCols, smem, wave, lane, tid);
+  }
+}
+
+// ---- fast prefill (within the stated tolerance, not bit-exact) -------------
+//
+// Per (row, column, block) the eight class MFMAs accumulate into one f32
+// D = sum_l aux32[l] (exact integer products; partial sums may round above
+// 2^24), then out += (dW_b * dX_b) * D and, for Q4_K, out -= (dminW_b * dX_b) *
+// sumi, with fused multiply-adds.  That reorders the reference's f32 tail, so
+// outputs agree to within a relative 1e-4 (the stated tolerance for
+// projections), and cuts the vector-ALU tail from 18 to at most 4 operations
+// per output and block.
+//
+// Workgroup tile: 128 rows (8 segments; wave w owns segments 2w, 2w + 1) x
+// 64 columns.  Per block, two contiguous regions are copied into LDS with
+// direct global->LDS loads (no register staging), one stage per workgroup
+// and two workgroups per CU, so one computes while the other loads: the 8
+// weight segments and the 64 columns' activation tile written by the
+// pre-pass in the order the B fragments are read (conflict-free):
+//   XH f16 [class l][quarter q][column n (64)][8]   32768 bytes
+//   XB f16 [q < 2][n][8]  (half-block sums 16h..16h+15, h = 8q + e)  2048
+//   XD f32 [n]                                                         256
+constexpr int kF2Cols = 64;
+constexpr int kF2W = 8 * 3360;
+constexpr int kF2XTile = 32768 + 2048 + 256;  // 35,072 bytes per (column tile, block)
+constexpr int kF2Stage = kF2W + kF2XTile;      // 61,952
+constexpr int kF2Lds = kF2Stage;               // one stage per workgroup, two workgroups per CU
+
+__global__ __launch_bounds__(64) void q8k_prefill_tiles_kernel(const float *__restrict__ x, int k, int nb, int cols,
+                                                               uint8_t *__restrict__ xt) {
+  const int b = blockIdx.x, m = blockIdx.y, lane = threadIdx.x;
+  const int ct = m / kF2Cols, n = m % kF2Cols;
+  uint8_t *tile = xt + ((size_t)ct * nb + b) * kF2XTile;
+  _Float16 *xh = reinterpret_cast<_Float16 *>(tile);
+  _Float16 *xb = reinterpret_cast<_Float16 *>(tile + 32768);
+  float *xd = reinterpret_cast<float *>(tile + 32768 + 2048);
+  Q8KLane r;
+  if (m < cols) {
+    r = q8k_block(x + (size_t)m * k + (size_t)b * kQK, lane);
+  } else {
+    r.q[0] = r.q[1] = r.q[2] = r.q[3] = 0;
+    r.d = 0.0f;
+  }
+  // lane owns e = 4 lane + i: j = lane / 8, c = (lane / 2) % 4, l = 4 (lane % 2) + i;
+  // quarter q = j / 2, position in the quarter (j % 2) * 4 + c
+  const int j = lane >> 3, c = (lane >> 1) & 3, qq = j >> 1, pos = 4 * (j & 1) + c;
+#pragma unroll
+  for (int i = 0; i < 4; i++) {
+    const int l = 4 * (lane & 1) + i;
+    xh[((l * 4 + qq) * kF2Cols + n) * 8 + pos] = (_Float16)r.q[i];
+  }
+  int s = (int)r.q[0] + (int)r.q[1] + (int)r.q[2] + (int)r.q[3];
+  s += __shfl_xor(s, 1);
+  s += __shfl_xor(s, 2);
+  if ((lane & 3) == 0) {
+    const int h = lane >> 2;  // 16 elements 16h .. 16h + 15
+    xb[((h >> 3) * kF2Cols + n) * 8 + (h & 7)] = (_Float16)s;
+  }
+  if (lane == 0) xd[n] = r.d;
+}
+
+// Copies `bytes` (a multiple of 16) from global to LDS with the wave's share
+// of 1 KB chunks (chunk c by wave c % 4).
+__device__ __forceinline__ void lds_copy(const uint8_t *src, uint8_t *dst, int bytes, int wave, int lane) {
+  const int full = bytes >> 10;
+  for (int c = wave; c < full; c += 4)
+    __builtin_amdgcn_global_load_lds(reinterpret_cast<const void *>(src + c * 1024 + 16 * lane),
+                                     (__attribute__((address_space(3))) void *)(dst + c * 1024), 16, 0, 0);
+  if ((full & 3) == wave && 16 * lane < bytes - (full << 10))  // the last, partial chunk
+    __builtin_amdgcn_global_load_lds(reinterpret_cast<const void *>(src + full * 1024 + 16 * lane),
+                                     (__attribute__((address_space(3))) void *)(dst + full * 1024), 16, 0, 0);
+}
+
+struct F2Args {
+  PfWeight w[kMaxWeights];  // rt_begin counts 128-row tiles here
+  int count, total_rt, col_tiles, nb, cols;
+  const uint8_t *xt;
+};
+
+// A fragment of class l for rows n of one segment from the raw segment bytes
+// (fast path: scales pre-expanded in S, N).
+template <bool Q4>
+__device__ __forceinline__ half8 f2_a(const uint8_t *seg, int l, int n, int q, const half2v (&S)[4],
+                                      const half2v (&N)[4]) {
+  const int g = l & 1, src = n + 16 * (l >> 1);
+  if constexpr (Q4) {
+    const uint32_t dw = *reinterpret_cast<const uint32_t *>(seg + 256 + 1024 * g + 16 * src + 4 * q);
+    const uint32_t lo = dw & 0x0F0F0F0Fu, hi = (dw >> 4) & 0x0F0F0F0Fu;
+    return cat(fma2(magic_pair<kSel01>(lo), S[0], N[0]), fma2(magic_pair<kSel23>(lo), S[0], N[0]),
+               fma2(magic_pair<kSel01>(hi), S[1], N[1]), fma2(magic_pair<kSel23>(hi), S[1], N[1]));
+  } else {
+    const int jj = 2 * (q & 1);
+    const uint32_t ql = *reinterpret_cast<const uint32_t *>(seg + 288 + 1024 * g + 16 * src + 4 * q);
+    const uint32_t qh = *reinterpret_cast<const uint32_t *>(seg + 288 + 2048 + 16 * src + 4 * (2 * g + (q >> 1)));
+    const uint32_t lo = (ql & 0x0F0F0F0Fu) | (((qh >> (2 * jj)) & 0x03030303u) << 4);
+    const uint32_t hi = ((ql >> 4) & 0x0F0F0F0Fu) | (((qh >> (2 * jj + 2)) & 0x03030303u) << 4);
+    return cat(fma2(magic_pair<kSel01>(lo), S[0], N[0]), fma2(magic_pair<kSel23>(lo), S[1], N[1]),
+               fma2(magic_pair<kSel01>(hi), S[2], N[2]), fma2(magic_pair<kSel23>(hi), S[3], N[3]));
+  }
+}
+
+// One block of the wave's 32 x 64 tile.  Branch-free (a missing second
+// segment computes on stale LDS bytes and is never stored), so the compiler
+// can overlap the LDS reads of a class with the MFMAs of the previous one.
+template <bool Q4>
+__device__ __forceinline__ void f2_block(float (&out)[2][4][4], const uint8_t *wl, const uint8_t *xl, int lane) {
+  const int n = lane & 15, q = lane >> 4;
+  constexpr int segb = Q4 ? 2304 : 3360;
+  const _Float16 *xh = reinterpret_cast<const _Float16 *>(xl);
+  half2v S[2][4], N[2][4];
+#pragma unroll
+  for (int rs = 0; rs < 2; rs++) {
+    const uint8_t *seg = wl + rs * segb;
+    if constexpr (Q4) {
+      const uint4 hdr = *reinterpret_cast<const uint4 *>(seg + 16 * n);
+      const uint32_t sclo = hdr.y & 0x3F3F3F3Fu;
+      const uint32_t schi = (hdr.w & 0x0F0F0F0Fu) | ((hdr.y >> 2) & 0x30303030u);
+      const uint32_t sc = q < 2 ? sclo : schi;
+      S[rs][0] = dup_byte(sc, 2 * (q & 1), 1024.0f);
+      S[rs][1] = dup_byte(sc, 2 * (q & 1) + 1, 1024.0f);
+      S[rs][2] = S[rs][3] = S[rs][0];
+      const half2v m1024 = (half2v){(_Float16)-1024.0f, (_Float16)-1024.0f};
+#pragma unroll
+      for (int e = 0; e < 4; e++) N[rs][e] = S[rs][e] * m1024;
+    } else {
+      const uint32_t gs = *reinterpret_cast<const uint32_t *>(seg + 16 * n + 4 * q) ^ 0x80808080u;
+#pragma unroll
+      for (int e = 0; e < 4; e++) {
+        S[rs][e] = dup_byte(gs, e, 1152.0f);
+        N[rs][e] = S[rs][e] * (half2v){(_Float16)-1056.0f, (_Float16)-1056.0f};
+      }
+    }
+  }
+  f32x4 D[2][4];
+#pragma unroll
+  for (int l = 0; l < 8; l++) {
+    half8 B[4];
+#pragma unroll
+    for (int cs = 0; cs < 4; cs++)
+      B[cs] = __builtin_bit_cast(half8, *reinterpret_cast<const uint4 *>(xh + ((l * 4 + q) * kF2Cols + 16 * cs + n) * 8));
+    const half8 A0 = f2_a<Q4>(wl, l, n, q, S[0], N[0]);
+    const half8 A1 = f2_a<Q4>(wl + segb, l, n, q, S[1], N[1]);
+#pragma unroll
+    for (int cs = 0; cs < 4; cs++) {
+      const f32x4 c0 = l == 0 ? (f32x4){0.0f, 0.0f, 0.0f, 0.0f} : D[0][cs];
+      const f32x4 c1 = l == 0 ? (f32x4){0.0f, 0.0f, 0.0f, 0.0f} : D[1][cs];
+      D[0][cs] = mfma(A0, B[cs], c0);
+      D[1][cs] = mfma(A1, B[cs], c1);
+    }
+  }
+  const float *xd = reinterpret_cast<const float *>(xl + 32768 + 2048);
+  float dx[4], dw[2][4], dmw[2][4];
+#pragma unroll
+  for (int cs = 0; cs < 4; cs++) dx[cs] = xd[16 * cs + n];
+#pragma unroll
+  for (int rs = 0; rs < 2; rs++)
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+      const int row = 4 * q + j;
+      if constexpr (Q4) {
+        const uint32_t v = *reinterpret_cast<const uint32_t *>(wl + rs * segb + 16 * row);
+        dw[rs][j] = h2f_bits(v & 0xFFFFu);
+        dmw[rs][j] = h2f_bits(v >> 16);
+      } else {
+        dw[rs][j] = h2f_bits(*reinterpret_cast<const uint16_t *>(wl + rs * segb + 256 + 2 * row));
+        dmw[rs][j] = 0.0f;
+      }
+    }
+  if constexpr (Q4) {
+    // sumi = sum_j mn_j * bsums32_j: quarter q < 2 carries k = 8q + e ->
+    // (j = 4q + e/2, half e%2) against the 16 half-block sums;
+    // out += dx * (dw * D - dmin * sumi)
+    const _Float16 *xb = reinterpret_cast<const _Float16 *>(xl + 32768);
+    half8 bm[4];
+#pragma unroll
+    for (int cs = 0; cs < 4; cs++)
+      bm[cs] = q < 2 ? __builtin_bit_cast(half8, *reinterpret_cast<const uint4 *>(xb + ((q * kF2Cols) + 16 * cs + n) * 8))
+                     : (half8){0, 0, 0, 0, 0, 0, 0, 0};
+#pragma unroll
+    for (int rs = 0; rs < 2; rs++) {
+      const uint4 hdr = *reinterpret_cast<const uint4 *>(wl + rs * segb + 16 * n);
+      const uint32_t mn = q == 0 ? (hdr.z & 0x3F3F3F3Fu) : (((hdr.w >> 4) & 0x0F0F0F0Fu) | ((hdr.z >> 2) & 0x30303030u));
+      const half8 am = q < 2 ? cat(dup_byte(mn, 0, 1024.0f), dup_byte(mn, 1, 1024.0f), dup_byte(mn, 2, 1024.0f),
+                                   dup_byte(mn, 3, 1024.0f))
+                             : (half8){0, 0, 0, 0, 0, 0, 0, 0};
+#pragma unroll
+      for (int cs = 0; cs < 4; cs++) {
+        const f32x4 sm = mfma(am, bm[cs], (f32x4){0.0f, 0.0f, 0.0f, 0.0f});
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+          const float t = __builtin_fmaf(-dmw[rs][j], sm[j], dw[rs][j] * D[rs][cs][j]);
+          out[rs][cs][j] = __builtin_fmaf(dx[cs], t, out[rs][cs][j]);
+        }
+      }
+    }
+  } else {
+#pragma unroll
+    for (int rs = 0; rs < 2; rs++)
+#pragma unroll
+      for (int cs = 0; cs < 4; cs++)
+#pragma unroll
+        for (int j = 0; j < 4; j++) out[rs][cs][j] = __builtin_fmaf(dx[cs], dw[rs][j] * D[rs][cs][j], out[rs][cs][j]);
+  }
+}
+
+// Two workgroups per CU (LDS), so two waves per SIMD.
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void kquant_prefill_fast_kernel(
+    const F2Args a) {
+  extern __shared__ __align__(16) uint8_t smem[];
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int items = a.total_rt * a.col_tiles;
+  for (int it = blockIdx.x; it < items; it += gridDim.x) {
+    const int rt = it / a.col_tiles, ct = it - rt * a.col_tiles;
+    PfWeight W = a.w[0];
+    if (a.count > 1 && rt >= a.w[1].rt_begin) W = a.w[1];
+    if (a.count > 2 && rt >= a.w[2].rt_begin) W = a.w[2];
+    if (a.count > 3 && rt >= a.w[3].rt_begin) W = a.w[3];
+    const bool q4 = W.type == kTypeQ4K;
+    const int segb = q4 ? 2304 : 3360;
+    const int T0 = 8 * (rt - W.rt_begin);
+    const int nseg_tile = W.tiles - T0 < 8 ? W.tiles - T0 : 8;
+    const int wbytes = nseg_tile * segb;
+    const int my_seg = 2 * wave;
+    const int nseg = nseg_tile - my_seg >= 2 ? 2 : nseg_tile - my_seg;  // this wave's live segments (<= 0: none)
+    float out[2][4][4];
+#pragma unroll
+    for (int rs = 0; rs < 2; rs++)
+#pragma unroll
+      for (int cs = 0; cs < 4; cs++)
+#pragma unroll
+        for (int j = 0; j < 4; j++) out[rs][cs][j] = 0.0f;
+    const uint8_t *xt = a.xt + (size_t)ct * a.nb * kF2XTile;
+    // one LDS stage: load, compute, repeat; the other workgroup on the CU
+    // computes while this one loads
+    for (int b = 0; b < a.nb; b++) {
+      lds_copy(W.seg + ((size_t)b * W.tiles + T0) * segb, smem, wbytes, wave, lane);
+      lds_copy(xt + (size_t)b * kF2XTile, smem + kF2W, kF2XTile, wave, lane);
+      __builtin_amdgcn_s_waitcnt(0);
+      __syncthreads();
+      if (nseg > 0) {
+        if (q4)
+          f2_block<true>(out, smem + my_seg * segb, smem + kF2W, lane);
+        else
+          f2_block<false>(out, smem + my_seg * segb, smem + kF2W, lane);
+      }
+      __syncthreads();
+    }
+    if (nseg > 0) {
+      const int n = lane & 15, q = lane >> 4;
+#pragma unroll
+      for (int rs = 0; rs < 2; rs++)
+#pragma unroll
+        for (int cs = 0; cs < 4; cs++) {
+          const int m = ct * kF2Cols + 16 * cs + n;
+#pragma unroll
+          for (int j = 0; j < 4; j++) {
+            const int row = 16 * (T0 + my_seg + rs) + 4 * q + j;
+            if (rs < nseg && row < W.rows && m < a.cols) W.out[(size_t)m * W.rows + row] = out[rs][cs][j];
+          }
+        }
+    }
+  }
+}
+
+}  // namespace
+
+size_t prefill_q8k_bytes(int k, int cols) {
+  const size_t nb = (size_t)(k / kQK);
+  return (size_t)cols * nb * (kQK + 32 + 4);
+}
+
+hipError_t launch_q8k_prefill(const float *x, int k, int cols, uint8_t *scratch, hipStream_t s) {
+  const int nb = k / kQK;
+  int8_t *xq = reinterpret_cast<int8_t *>(scratch);
+  _Float16 *xb = reinterpret_cast<_Float16 *>(scratch + (size_t)cols * nb * kQK);
+  float *xd = reinterpret_cast<float *>(scratch + (size_t)cols * nb * (kQK + 32));
+  hipLaunchKernelGGL(q8k_prefill_kernel, dim3(nb, cols), dim3(64), 0, s, x, k, nb, xq, xb, xd);
+  return hipGetLastError();
+}
+
+size_t prefill_lds_bytes() { return kPfLds; }
+
+size_t prefill_fast_bytes(int k, int cols) {
+  return (size_t)((cols + kF2Cols - 1) / kF2Cols) * (k / kQK) * kF2XTile;
+}
+
+size_t prefill_fast_lds_bytes() { return kF2Lds; }
+
+hipError_t launch_prefill_fast(const MfmaLaunch &l, const float *x, uint8_t *scratch, int num_cus, hipStream_t s) {
+  if (l.count < 1 || l.count > kMaxWeights || l.cols < 1 || l.k % kQK != 0) return hipErrorInvalidValue;
+  const int nb = l.k / kQK;
+  const int col_tiles = (l.cols + kF2Cols - 1) / kF2Cols;
+  hipLaunchKernelGGL(q8k_prefill_tiles_kernel, dim3(nb, col_tiles * kF2Cols), dim3(64), 0, s, x, l.k, nb, l.cols,
+                     scratch);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  F2Args a{};
+  a.count = l.count;
+  int rt = 0;
+  for (int i = 0; i < l.count; i++) {
+    a.w[i].seg = l.seg[i];
+    a.w[i].out = l.out[i];
+    a.w[i].type = l.type[i];
+    a.w[i].rows = l.rows[i];
+    a.w[i].tiles = (l.rows[i] + 15) / 16;
+    a.w[i].rt_begin = rt;
+    rt += (a.w[i].tiles + 7) / 8;
+  }
+  a.total_rt = rt;
+  a.col_tiles = col_tiles;
+  a.nb = nb;
+  a.cols = l.cols;
+  a.xt = scratch;
+  static bool attr = false;
+  if (!attr) {
+    e = hipFuncSetAttribute(reinterpret_cast<const void *>(kquant_prefill_fast_kernel),
+                            hipFuncAttributeMaxDynamicSharedMemorySize, kF2Lds);
+    if (e != hipSuccess) return e;
+    attr = true;
+  }
+  const long long items = (long long)a.total_rt * a.col_tiles;
+  const int grid = (int)(items < 2LL * num_cus ? items : 2LL * num_cus);
+  hipLaunchKernelGGL(kquant_prefill_fast_kernel, dim3(grid), dim3(256), kF2Lds, s, a);
+  return hipGetLastError();
+}
+
+hipError_t launch_prefill(const MfmaLaunch &l, const uint8_t *scratch, int num_cus, hipStream_t s) {
+  if (l.count < 1 || l.count > kMaxWeights || l.cols < 1 || l.k % kQK != 0) return hipErrorInvalidValue;
+  PfArgs a{};
+  a.count = l.count;
+  int rt = 0;
+  for (int i = 0; i < l.count; i++) {
+    a.w[i].seg = l.seg[i];
+    a.w[i].out = l.out[i];
+    a.w[i].type = l.type[i];
+    a.w[i].rows = l.rows[i];
+    a.w[i].tiles = (l.rows[i] + 15) / 16;
+    a.w[i].rt_begin = rt;
+    rt += (a.w[i].tiles + 1) / 2;
+  }
+  a.total_rt = rt;
+  a.nb = l.k / kQK;
+  a.cols = l.cols;
+  a.col_tiles = (l.cols + kPfCols - 1) / kPfCols;
+  a.xq = reinterpret_cast<const int8_t *>(scratch);
+  a.xb = reinterpret_cast<const _Float16 *>(scratch + (size_t)l.cols * a.nb * kQK);
+  a.xd = reinterpret_cast<const float *>(scratch + (size_t)l.cols * a.nb * (kQK + 32));
+  const long long items = (long long)a.total_rt * a.col_tiles;
+  const int grid = (int)(items < (long long)num_cus * 2 ? items : (long long)num_cus * 2);
+  hipLaunchKernelGGL(kquant_prefill_kernel, dim3(grid), dim3(256), kPfLds, s, a);
+  return hipGetLastError();
+}
+
+}  // namespace hp

@@ -406,13 +406,15 @@ def matmul_multi_device(handles: Sequence[int], d_input: int, input_size: int, c
     assertHipOk(code, "matmulMultiDevice")
 
 
-MATVEC_AUTO, MATVEC_VALU, MATVEC_MFMA, MATVEC_HALF = 0, 1, 2, 3
+MATVEC_AUTO, MATVEC_VALU, MATVEC_MFMA, MATVEC_HALF, MATVEC_PREFILL, MATVEC_PREFILL_FAST = 0, 1, 2, 3, 4, 5
 
 
 def setMatvecKernel(which: int) -> None:
     """Select the matvec kernel (0 automatic, 1 vector ALU, 2 matrix cores,
-    3 half-split vector ALU); all are bit-exact, only speed differs.  No
-    counterpart in the reference."""
+    3 half-split vector ALU, 4 bit-exact prefill, 5 fast prefill).  1-4 are
+    bit-exact; 5 (and the automatic choice from 64 columns) agrees within
+    the 1e-4 relative tolerance of projections.  No counterpart in the
+    reference."""
     assertHipOk(lib().hp_hip_set_matvec_kernel(int(which)), "setMatvecKernel")
 
 

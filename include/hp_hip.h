@@ -216,10 +216,15 @@ int32_t hp_hip_quantize_q8_k(const float *input, size_t input_len, size_t input_
 /* Matvec kernel selection (no counterpart in the reference; a tuning and
  * test hook): 0 = automatic (by column count and tile count: half-split
  * vector ALU for small projections, vector ALU for one column, matrix
- * cores for several columns of large ones), 1 = always the vector-ALU
- * kernel, 2 = the matrix-core kernel whenever its LDS fits the device,
- * 3 = the half-split vector-ALU kernel (two lanes per row-block) for up to
- * four columns.  All are bit-exact with the reference; only speed differs. */
+ * cores for several columns of large ones, the bit-exact prefill kernel
+ * from 32 columns, the fast prefill kernel from 64), 1 = always the
+ * vector-ALU kernel, 2 = the matrix-core kernel whenever its LDS fits the
+ * device, 3 = the half-split vector-ALU kernel (two lanes per row-block) for
+ * up to four columns, 4 = the bit-exact prefill kernel (64-column tiles) for
+ * any column count, 5 = the fast prefill kernel for any column count.
+ * Kernels 1-4 are bit-exact with the reference; the fast prefill kernel adds
+ * each block's eight lane-class sums before scaling, so its outputs agree
+ * within the 1e-4 relative tolerance of projections (M >= 64 prefill). */
 int32_t hp_hip_set_matvec_kernel(int32_t which);
 
 /* wasmResidentWeightStats (wasm-kernels.ts:586-591) plus call counters. */

@@ -21,7 +21,7 @@ def _weights(type_name, seed, rows, k):
     return S.weight_blocks(type_name, seed, rows, k)
 
 
-@pytest.fixture(params=[1, 2, 3], ids=["valu", "mfma", "half"])
+@pytest.fixture(params=[1, 2, 3, 4], ids=["valu", "mfma", "half", "prefill"])
 def kernel(request, hip):
     """Runs the test with the vector-ALU, the matrix-core and the half-split
     vector-ALU matvec."""

@@ -1,0 +1,150 @@
+"""GPU parity: the prefill matrix-core kernels (many columns per launch).
+
+Two kernels:
+- the bit-exact prefill kernel (selector 4; automatic for 32..63 columns):
+  bit-identical to the oracle's restatement of lib.rs:224-426;
+- the fast prefill kernel (selector 5; automatic from 64 columns, the M >= 64
+  prefill chunk): it adds each block's eight lane-class sums before scaling,
+  so it is held to the stated tolerance for projections instead: max
+  relative error <= 1e-4 against the oracle, relative to max(|ref|,
+  0.01 * rms(ref)) so that outputs that cancel to near zero are compared
+  on the scale of their column (TOL, FLOOR below).
+Shapes cover the ways the workgroup tiles can be cut: rows not a multiple of
+16, 32 or 128 (last tiles with one segment), columns not a multiple of 64, a
+single column, mixed Q4_K/Q6_K weights in one launch, both input sizes of
+the model and a 512-column chunk.
+"""
+import numpy as np
+import pytest
+
+from heliopause_amd import synthetic as S
+
+pytestmark = pytest.mark.gpu
+
+TYPES = {"Q4_K": 1, "Q6_K": 3}
+TOL = 1e-4     # max relative error of projections
+FLOOR = 0.01   # denominators at least FLOOR * rms of the reference
+
+
+def _bits(a):
+    return np.ascontiguousarray(a, dtype=np.float32).reshape(-1).view(np.uint32)
+
+
+def _rel_err(got, ref):
+    got = np.asarray(got, np.float64).reshape(-1)
+    ref = np.asarray(ref, np.float64).reshape(-1)
+    rms = np.sqrt(np.mean(ref * ref)) if ref.size else 0.0
+    den = np.maximum(np.abs(ref), FLOOR * rms)
+    den[den == 0] = 1.0
+    return float(np.max(np.abs(got - ref) / den)) if ref.size else 0.0
+
+
+@pytest.fixture
+def selector(request, hip):
+    hip.setMatvecKernel(request.param)
+    yield request.param
+    hip.setMatvecKernel(0)
+
+
+SHAPES = [(64, 2560, 64), (33, 2560, 65), (16, 256, 32), (1, 512, 40), (300, 10240, 37), (100, 2560, 130),
+          (48, 2560, 1), (200, 2560, 200), (2560, 10240, 64)]
+
+
+@pytest.mark.parametrize("selector", [4], ids=["exact"], indirect=True)
+@pytest.mark.parametrize("type_name", ["Q4_K", "Q6_K"])
+@pytest.mark.parametrize("rows,k,m", SHAPES[:7])
+def test_prefill_exact_bit_exact(hip, oracle, selector, type_name, rows, k, m):
+    print(f"prefill exact {type_name} rows={rows} k={k} m={m}", flush=True)
+    seed = S.derive(S.BASE_SEED, "prefill", type_name, rows, k, m)
+    w = S.weight_blocks(type_name, seed, rows, k)
+    x = S.activations(S.derive(seed, "x"), m, k)
+    h = hip.createHipQuantizedWeightHandle(type_name, w, k, rows)
+    try:
+        got = hip.matMulQuantizedHipResident(h, x, k, rows, m)
+    finally:
+        hip.releaseHipQuantizedWeightHandle(h)
+    ref = oracle.matmul(TYPES[type_name], w, x, rows, threads=8)
+    bad = np.flatnonzero(_bits(got) != _bits(ref))
+    assert bad.size == 0, (bad[:5], got.reshape(-1)[bad[:5]], ref.reshape(-1)[bad[:5]])
+
+
+@pytest.mark.parametrize("selector", [0, 5], ids=["auto", "fast"], indirect=True)
+@pytest.mark.parametrize("type_name", ["Q4_K", "Q6_K"])
+@pytest.mark.parametrize("rows,k,m", SHAPES)
+def test_prefill_fast_within_tolerance(hip, oracle, selector, type_name, rows, k, m):
+    print(f"prefill fast {type_name} rows={rows} k={k} m={m} selector={selector}", flush=True)
+    seed = S.derive(S.BASE_SEED, "prefill", type_name, rows, k, m)
+    w = S.weight_blocks(type_name, seed, rows, k)
+    x = S.activations(S.derive(seed, "x"), m, k)
+    h = hip.createHipQuantizedWeightHandle(type_name, w, k, rows)
+    try:
+        got = hip.matMulQuantizedHipResident(h, x, k, rows, m)
+    finally:
+        hip.releaseHipQuantizedWeightHandle(h)
+    ref = oracle.matmul(TYPES[type_name], w, x, rows, threads=8)
+    err = _rel_err(got, ref)
+    assert err <= TOL, err
+    if selector == 0 and m < 64:          # the automatic policy stays bit-exact below 64 columns
+        assert np.array_equal(_bits(got), _bits(ref))
+
+
+@pytest.mark.parametrize("selector", [4, 0], ids=["exact", "auto"], indirect=True)
+def test_prefill_multi_and_large_chunk(hip, oracle, selector):
+    """Q/K/V of one layer (Q4_K 2048 + Q4_K 512 + Q6_K 512 rows) over a
+    512-column chunk in one launch, and special columns (zeros, ties, a huge
+    spike, tiny values) among them."""
+    k, m = 2560, 512
+    specs = [("Q4_K", 2048), ("Q4_K", 512), ("Q6_K", 512)]
+    seed = S.derive(S.BASE_SEED, "prefill-qkv")
+    ws = [S.weight_blocks(t, S.derive(seed, i), r, k) for i, (t, r) in enumerate(specs)]
+    x = S.activations(S.derive(seed, "x"), m, k)
+    x[3] = 0.0
+    x[7, 5], x[7, 9] = 2.0, -2.0
+    x[11, 1000] = 1e30
+    x[13] *= 1e-39
+    hs = [hip.createHipQuantizedWeightHandle(t, w, k, r) for (t, r), w in zip(specs, ws)]
+    print(f"prefill qkv m=512 selector={selector}", flush=True)
+    try:
+        outs = hip.matMulQuantizedHipResidentMulti(hs, x, k, m)
+    finally:
+        for h in hs:
+            hip.releaseHipQuantizedWeightHandle(h)
+    refs = oracle.matmul_multi([TYPES[t] for t, _ in specs], ws, x, [r for _, r in specs], threads=8)
+    for (t, r), got, ref in zip(specs, outs, refs):
+        if selector == 4:
+            assert np.array_equal(_bits(got), _bits(ref))
+        else:
+            g, f = got.reshape(m, r), ref.reshape(m, r)
+            assert np.array_equal(g[3], f[3])                   # a zero column is exactly zero
+            for col in range(m):                                 # tolerance per column (its own scale)
+                assert _rel_err(g[col], f[col]) <= TOL, (t, col)
+
+
+@pytest.mark.parametrize("selector", [4, 0], ids=["exact", "auto"], indirect=True)
+def test_prefill_geglu(hip, oracle, selector):
+    """gate/up + GeGLU over 96 columns: the projections take a prefill
+    kernel, GeGLU follows as its own launch."""
+    rows, k, m = 160, 2560, 96
+    seed = S.derive(S.BASE_SEED, "prefill-geglu")
+    wg = S.q4_k_blocks(S.derive(seed, "g"), rows, k)
+    wu = S.q4_k_blocks(S.derive(seed, "u"), rows, k)
+    x = S.activations(seed, m, k)
+    hg = hip.createHipQuantizedWeightHandle("Q4_K", wg, k, rows)
+    hu = hip.createHipQuantizedWeightHandle("Q4_K", wu, k, rows)
+    try:
+        got = hip.matMulGegluHipResident(hg, hu, x, k, m)
+    finally:
+        hip.releaseHipQuantizedWeightHandle(hg)
+        hip.releaseHipQuantizedWeightHandle(hu)
+    ref = oracle.geglu(oracle.matmul(1, wg, x, rows, threads=8).reshape(-1),
+                       oracle.matmul(1, wu, x, rows, threads=8).reshape(-1))
+    if selector == 4:
+        assert np.array_equal(_bits(got), _bits(ref))
+    else:
+        # gelu rounds its input and its result to f16 (layers.ts:1062-1076):
+        # projections within 1e-4 can land across an f16 rounding boundary,
+        # so an element may move by up to two f16 steps (2 * 2^-10)
+        g, f = np.asarray(got, np.float64), np.asarray(ref, np.float64)
+        rel = np.abs(g - f) / np.maximum(np.abs(f), FLOOR * np.sqrt(np.mean(f * f)))
+        assert rel.max() <= 2 * 2.0 ** -10, rel.max()
+        assert np.median(rel) <= TOL
