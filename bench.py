@@ -8,8 +8,9 @@ in-kernel Q8_K), M = 1 column.  A step is one such projection pass.
 Other workloads (``--workload``): ``cfg1`` (one Q4_K 10240x2560 matvec),
 ``gate_up`` (two Q4_K 10240x2560 in one launch), ``down`` (Q6_K 2560x10240),
 ``ffn`` (gate/up launch -> GeGLU -> down), ``head`` (Q6_K 262144x2560 output
-head + top-40 per column, candidates only), ``decode42`` (the projection chain
-of one decode step of a 42-layer model, in one graph), ``prefill42`` (a
+head + top-40 per column, candidates only), ``decode42`` (a full decode step
+of a 42-layer model with a 4096-token KV cache, in one graph),
+``decode42-proj`` (only that step's projection chain), ``prefill42`` (a
 512-token chunk through that model's projections on the matrix cores) and
 ``gguf-load`` (a 3.02 GB GGUF file of that model streamed into HBM-resident
 handles).
@@ -113,7 +114,7 @@ def parse() -> argparse.Namespace:
     p.add_argument("--steps", type=int, default=400)
     p.add_argument("--warmup", type=int, default=40)
     p.add_argument("--m", type=int, default=1)
-    p.add_argument("--workload", choices=sorted(WORKLOADS) + ["decode42", "prefill42", "gguf-load"], default="qkv")
+    p.add_argument("--workload", choices=sorted(WORKLOADS) + ["decode42", "decode42-proj", "prefill42", "gguf-load"], default="qkv")
     p.add_argument("--rotate-mib", type=int, default=640, help="distinct weight bytes cycled through")
     p.add_argument("--cpu-seconds", type=float, default=12.0)
     p.add_argument("--no-cpu", action="store_true")
@@ -265,6 +266,150 @@ def decode_chain(args) -> int:
     }
     print(json.dumps(line))
     return 0
+
+
+def decode_step(args) -> int:
+    """One decode step of the 42-layer synthetic Gemma-like model at M = 1
+    (hidden 2560, 8 query / 2 KV heads of 256, FFN 10240; Q4_K_M mix) with a
+    4096-token f16 KV cache filled with N(0,1): the token at position 4096
+    attends over the last 4096 positions of every layer.  Per layer: attn_norm
+    -> Q/K/V -> q/k norms + RoPE + v norm + cache append -> GQA attention ->
+    O -> post-attention norm + residual + ffn_norm -> gate/up + GeGLU -> down
+    -> post-FFN norm + residual + layer scale + next attn_norm; then
+    output_norm, the Q6_K 262144x2560 head, top-40 and the sampled next token.
+    Every layer's weights and cache are distinct device copies (3.02 GB of
+    weights + 352 MB of cache).  The step starts by copying the input hidden
+    state into the residual buffer (standing in for the embedding row), so
+    every replay computes the same step.  One step is captured in a HIP graph
+    and replayed."""
+    import numpy as np
+    import torch
+
+    from heliopause_amd import decode as DM
+    from heliopause_amd import hip_kernels as H
+    from heliopause_amd import synthetic as S
+
+    if args.m != 1:
+        raise SystemExit("decode42 runs at M = 1")
+    torch.cuda.init()
+    dev = torch.device("cuda:0")
+    shape = DM.ModelShape()
+    seed = S.config_seed(5)
+    data = DM.layer_host_data(shape, seed, 0)
+    model = DM.HipDecodeModel(shape)
+    for _ in range(N_LAYERS):
+        model.add_layer(data)
+    head_blocks = S.weight_blocks(HEAD[0], S.derive(seed, "head"), HEAD[1], HEAD[2])
+    head = H.createHipQuantizedWeightHandle(HEAD[0], head_blocks, HEAD[2], HEAD[1])
+    model.set_head((1.0 + 0.1 * S.normal(S.derive(seed, "output_norm"), shape.hidden)).astype(np.float32), head)
+    x0 = torch.from_numpy(S.activations(S.derive(seed, "x"), 1, shape.hidden).reshape(-1) * 4).to(dev)
+    hidden = torch.empty_like(x0)
+    normed = torch.empty_like(x0)
+    pos = torch.tensor([shape.capacity], dtype=torch.int32, device=dev)
+    logits = torch.empty(HEAD[1], dtype=torch.float32, device=dev)
+    ids = torch.empty(TOPK, dtype=torch.int32, device=dev)
+    vals = torch.empty(TOPK, dtype=torch.float32, device=dev)
+    sampling = H.resolveGenerationSamplingOptions(topK=TOPK)
+    rng = torch.from_numpy(np.array([sampling["seed"]], np.uint32).view(np.int32)).to(dev)
+    token = torch.zeros(1, dtype=torch.int32, device=dev)
+    kept = torch.zeros(1, dtype=torch.int32, device=dev)
+    probs = torch.zeros(TOPK, dtype=torch.float64, device=dev)
+    L = H.lib()
+
+    def step(stream: int) -> None:
+        hidden.copy_(x0)
+        model.run_layers(hidden.data_ptr(), pos.data_ptr(), normed.data_ptr(), stream)
+        H.matmul_multi_device([head.handle], normed.data_ptr(), shape.hidden, 1, [logits.data_ptr()], [HEAD[1]],
+                              stream)
+        H.assertHipOk(L.hp_hip_topk_device(logits.data_ptr(), 1, HEAD[1], TOPK, 0.0, ids.data_ptr(),
+                                           vals.data_ptr(), stream), "topk")
+        H.sample_device(ids.data_ptr(), vals.data_ptr(), 1, TOPK, TOPK, sampling, rng.data_ptr(), token.data_ptr(),
+                        probs.data_ptr(), kept.data_ptr(), stream)
+
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        step(side.cuda_stream)
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=side):
+            step(torch.cuda.current_stream().cuda_stream)
+    torch.cuda.synchronize()
+    for _ in range(max(1, args.warmup // 10)):
+        graph.replay()
+    torch.cuda.synchronize()
+    steps = max(1, args.steps // 10)
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    start.record()
+    for _ in range(steps):
+        graph.replay()
+    end.record()
+    torch.cuda.synchronize()
+    wall_ms = (time.perf_counter() - t0) / steps * 1e3
+    ms = start.elapsed_time(end) / steps
+    wbytes = N_LAYERS * sum(row_bytes(t, k) * r for t, r, k in LAYER) + row_bytes(HEAD[0], HEAD[2]) * HEAD[1]
+    kv_bytes = N_LAYERS * 2 * shape.head_count_kv * shape.capacity * 256 * 2
+    total = wbytes + kv_bytes
+    cpu = None if args.no_cpu else decode_cpu_baseline(shape, data, head_blocks, args.cpu_seconds)
+    launches = 1 + 1 + N_LAYERS * 9 + 1 + 3 + 1
+    line = {
+        "metric": "decode step ms at M=1 (1 GPU)",
+        "value": round(ms, 4), "unit": "ms", "n_gpus": 1, "steps": steps, "warmup": args.warmup,
+        "ms_per_step": round(ms, 4), "higher_is_better": False, "scaling": "weak", "vs_baseline": None,
+        "dtype": "int8", "data": "synthetic",
+        "config": {"workload": "42-layer synthetic Gemma-like model, full decode step at M=1 with a 4096-token f16 "
+                               "KV cache: norms, Q/K/V, RoPE, cache append, GQA attention, O, GeGLU FFN, residuals, "
+                               "output norm, head, top-40, next-token sampling",
+                   "weight_bytes": wbytes, "kv_cache_bytes_read": kv_bytes, "launches_per_step": launches,
+                   "wall_ms_per_step": round(wall_ms, 4), "position": int(shape.capacity),
+                   "timing": "one step captured in a HIP graph and replayed"},
+        "roofline": {"bound": "hbm", "achieved": round(total / (ms * 1e-3) / 1e9, 2), "peak": HBM_PEAK_GBPS,
+                     "unit": "GB/s", "frac": round(total / (ms * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4),
+                     "traffic": None, "bytes_per_step": total,
+                     "weight_bytes_over_peak_ms": round(wbytes / HBM_PEAK_GBPS / 1e6, 4),
+                     "target_ms": round(1.3 * wbytes / HBM_PEAK_GBPS / 1e6, 4)},
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line))
+    model.release()
+    H.releaseHipQuantizedWeightHandle(head)
+    return 0
+
+
+def decode_cpu_baseline(shape, data, head_blocks, seconds: float) -> dict:
+    """The oracle's restatement of the WASM decode step on the host: layers of
+    the same model (4096-token cache) run until ``seconds`` pass, plus the head
+    once; the step time is extrapolated to 42 layers + head."""
+    import numpy as np
+
+    from oracle import decode_layer as OD
+    from oracle import oracle as O
+
+    tids = {"Q4_K": 1, "Q6_K": 3}
+    w = {n: (tids[t], blocks, rows) for n, (t, blocks, rows, _) in data["weights"].items()}
+    layer = OD.Layer(weights=w, norms=dict(data["norms"]), key_cache=data["key_cache"].copy(),
+                     value_cache=data["value_cache"].copy(), head_count=shape.head_count,
+                     head_count_kv=shape.head_count_kv, epsilon=shape.epsilon,
+                     output_scale=float(data["output_scale"]))
+    x = np.zeros(shape.hidden, np.float32) + 0.5
+    n, t0 = 0, time.perf_counter()
+    while True:
+        x = OD.forward_layer(layer, x, shape.capacity)
+        n += 1
+        el = time.perf_counter() - t0
+        if el >= seconds:
+            break
+    per_layer = el / n
+    th = time.perf_counter()
+    O.matmul(TYPE_IDS[HEAD[0]], head_blocks, x.reshape(1, -1), head_blocks.shape[0], threads=O.default_threads())
+    head_s = time.perf_counter() - th
+    step_ms = (N_LAYERS * per_layer + head_s) * 1e3
+    return {"value": round(step_ms, 2), "unit": "ms", "cores": O.default_threads(), "kind": "port",
+            "sample": f"{n} decoder layers ({per_layer * 1e3:.1f} ms each: projections on {O.default_threads()} "
+                      f"threads, attention over 4096 cached tokens on one) + the head once ({head_s * 1e3:.0f} ms), "
+                      f"extrapolated to 42 layers + head; host {platform.processor() or platform.machine()}, "
+                      f"{os.cpu_count()} logical CPUs"}
 
 
 MFMA_F16_PEAK_TFLOPS = 2500.0  # dense f16 matrix-core peak, MI355X
@@ -481,6 +626,8 @@ def main() -> int:
         print(json.dumps({"error": "this build runs on one GPU only; --gpus must be 1", "n_gpus": args.gpus}))
         return 2
     if args.workload == "decode42":
+        return decode_step(args)
+    if args.workload == "decode42-proj":
         return decode_chain(args)
     if args.workload == "gguf-load":
         return gguf_load(args)

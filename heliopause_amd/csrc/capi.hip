@@ -72,6 +72,9 @@ struct State {
   // kept counts and probabilities
   void *sample_out = nullptr;
   size_t sample_out_cap = 0;
+  // decoder layers: attention partials; activations of a decode step
+  void *attn_scratch = nullptr, *decode_scratch = nullptr;
+  size_t attn_scratch_cap = 0, decode_scratch_cap = 0;
 };
 
 State &st() {
@@ -268,12 +271,36 @@ bool use_half(int cols, const TileGeom &g, int tiles) {
 
 // One matvec launch per column chunk covering every weight (multi == one
 // launch, lib.rs:300-426); each launch quantises its columns in its prologue.
+int32_t run_norm(const float *y, int rows, int n, const float *w_post, const float *x_res, float scale, float *x_out,
+                 const float *w_next, float *next_out, double eps, hipStream_t stream);
+
+// Whether a one-column launch over these weights runs a vector-ALU kernel,
+// which can form its input with the norm prologue.
+bool norm_prologue_ok(size_t count, Handle *const *hs, size_t cols) {
+  if (cols != 1 || hs[0]->g.nb > 16 || prefill_kind(cols) != 0) return false;
+  int tiles16 = 0;
+  for (size_t i = 0; i < count; i++) tiles16 += (int)((hs[i]->row_count + 15) / 16);
+  return !use_mfma(cols, hs[0]->g.nb, tiles16);
+}
+
+// norm != null: the input is formed from a residual stream (NormIn) -- in the
+// launch's prologue when the launch runs a vector-ALU kernel, else by the norm
+// kernel into norm_scratch first.
 int32_t run_matvec(size_t count, Handle *const *hs, const float *d_input, size_t input_size, size_t cols,
-                   float *const *d_outs, hipStream_t stream) {
+                   float *const *d_outs, hipStream_t stream, const NormIn *norm = nullptr,
+                   float *norm_scratch = nullptr) {
   State &s = st();
   if (cols == 0) return HP_OK;
+  if (norm && !norm_prologue_ok(count, hs, cols)) {
+    int32_t rc = run_norm(norm->y, (int)cols, (int)input_size, norm->w_post, norm->mode == 2 ? norm->x_res : nullptr,
+                          norm->scale, norm->x_out, norm->w_next, norm_scratch, norm->eps, stream);
+    if (rc != HP_OK) return rc;
+    d_input = norm_scratch;
+    norm = nullptr;
+  }
   const TileGeom g = hs[0]->g;
   MatvecArgs a{};
+  if (norm) a.norm = *norm;
   a.count = (int)count;
   a.g = g;
   a.k = (int)input_size;
@@ -376,7 +403,8 @@ int32_t run_matvec(size_t count, Handle *const *hs, const float *d_input, size_t
 // projections (one launch, any kernel) into scratch, then the GeGLU kernel.
 // Both give the same bits.
 int32_t run_matvec_geglu(Handle *hg, Handle *hu, const float *d_input, size_t input_size, size_t cols,
-                         float *d_out, hipStream_t stream) {
+                         float *d_out, hipStream_t stream, const NormIn *norm = nullptr,
+                         float *norm_scratch = nullptr) {
   State &s = st();
   if (cols == 0) return HP_OK;
   const size_t rows = hg->row_count;
@@ -384,8 +412,16 @@ int32_t run_matvec_geglu(Handle *hg, Handle *hu, const float *d_input, size_t in
   const int tiles16 = 2 * (int)((rows + 15) / 16);
   const bool fused = cols <= 4 && s.matvec_kernel <= 1 && !use_mfma(cols, g.nb, tiles16) &&
                      !use_half((int)cols, g, 2 * hg->tiles) && cols_per_launch(g, s.max_lds) >= (int)cols;
+  if (norm && !(fused && cols == 1 && g.nb <= 16)) {
+    int32_t rc = run_norm(norm->y, (int)cols, (int)input_size, norm->w_post, norm->mode == 2 ? norm->x_res : nullptr,
+                          norm->scale, norm->x_out, norm->w_next, norm_scratch, norm->eps, stream);
+    if (rc != HP_OK) return rc;
+    d_input = norm_scratch;
+    norm = nullptr;
+  }
   if (fused) {
     MatvecArgs a{};
+    if (norm) a.norm = *norm;
     a.count = 2;
     a.g = g;
     a.k = (int)input_size;
@@ -660,6 +696,120 @@ SampleParams sample_params(const hp_hip_sampling_t *o) {
   return p;
 }
 
+// Grows a library scratch buffer, which a stream capturing a graph must not
+// do (the allocation would not be part of the graph).
+int32_t grow_uncaptured(void **p, size_t *cap, size_t bytes, hipStream_t stream) {
+  if (*p && *cap >= bytes) return HP_OK;
+  hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+  if (hipStreamIsCapturing(stream, &cs) != hipSuccess) cs = hipStreamCaptureStatusNone;
+  if (cs != hipStreamCaptureStatusNone)
+    return fail(HP_ERR_ARG, "scratch must be sized by an uncaptured call of this shape before graph capture");
+  return grow(p, cap, bytes);
+}
+
+constexpr size_t kNormMaxN = 4096;
+
+int32_t attention_check(const hp_hip_attention_config_t *c) {
+  if (!c) return fail(HP_ERR_ARG, "null attention config");
+  if (c->head_dim != kHeadDim) return fail(HP_ERR_SHAPE, "head_dim must be 256");
+  if (c->head_count < 1 || c->head_count_kv < 1 || c->head_count % c->head_count_kv != 0 ||
+      c->head_count / c->head_count_kv > kAttnMaxGroup)
+    return fail(HP_ERR_HEADS, "head_count must be a multiple (at most 8x) of head_count_kv");
+  if (c->rope_dims < 0 || c->rope_dims > kHeadDim || c->rope_dims % 2 != 0)
+    return fail(HP_ERR_ARG, "rope_dims must be even and at most head_dim");
+  if (c->rope_dims > 0 && !(c->rope_freq_base > 0.0 && std::isfinite(c->rope_freq_base)))
+    return fail(HP_ERR_ARG, "rope_freq_base must be positive");
+  if (c->capacity < 1 || c->sliding_window < 0) return fail(HP_ERR_ARG, "bad KV capacity or window");
+  if (!(c->epsilon >= 0.0)) return fail(HP_ERR_ARG, "epsilon must be >= 0");
+  return HP_OK;
+}
+
+QkvPostArgs qkv_post_args(const hp_hip_attention_config_t *c) {
+  QkvPostArgs a{};
+  a.nq = c->head_count;
+  a.nkv = c->head_count_kv;
+  a.capacity = c->capacity;
+  a.rope_dims = c->rope_dims;
+  // thetaScale = Math.pow(freqBase, -2 / nDims) (layers.ts:1013)
+  a.theta_scale = c->rope_dims > 0 ? std::pow(c->rope_freq_base, -2.0 / (double)c->rope_dims) : 1.0;
+  a.freq_factors = c->d_rope_freq_factors;
+  a.eps = c->epsilon;
+  return a;
+}
+
+AttnArgs attn_args(const hp_hip_attention_config_t *c) {
+  const QkvPostArgs p = qkv_post_args(c);
+  AttnArgs a{};
+  a.nq = c->head_count;
+  a.nkv = c->head_count_kv;
+  a.capacity = c->capacity;
+  a.window = c->sliding_window;
+  a.rope_dims = p.rope_dims;
+  a.theta_scale = p.theta_scale;
+  a.freq_factors = p.freq_factors;
+  a.eps = p.eps;
+  return a;
+}
+
+int32_t run_attention(AttnArgs a, float *partials, hipStream_t stream) {
+  HP_HIP_TRY(launch_attention(a, partials, stream));
+  st().launches += 2;
+  return HP_OK;
+}
+
+int32_t run_norm(const float *y, int rows, int n, const float *w_post, const float *x_res, float scale, float *x_out,
+                 const float *w_next, float *next_out, double eps, hipStream_t stream) {
+  NormArgs a{};
+  a.y = y;
+  a.w_post = w_post;
+  a.x_res = x_res;
+  a.scale = scale;
+  a.x_out = x_out;
+  a.w_next = w_next;
+  a.next_out = next_out;
+  a.n = n;
+  a.rows = rows;
+  a.eps = eps;
+  HP_HIP_TRY(launch_norm_residual(a, stream));
+  st().launches++;
+  return HP_OK;
+}
+
+// Weights of one decode layer, looked up and checked against each other.
+struct LayerHandles {
+  Handle *q, *k, *v, *o, *gate, *up, *down;
+};
+
+int32_t decode_layer_check(const hp_hip_decode_layer_t &L, size_t hidden, LayerHandles *out) {
+  int32_t rc = attention_check(&L.attention);
+  if (rc != HP_OK) return rc;
+  LayerHandles h{};
+  h.q = lookup(L.attn_q);
+  h.k = lookup(L.attn_k);
+  h.v = L.attn_v ? lookup(L.attn_v) : nullptr;
+  h.o = lookup(L.attn_output);
+  h.gate = lookup(L.ffn_gate);
+  h.up = lookup(L.ffn_up);
+  h.down = lookup(L.ffn_down);
+  if (!h.q || !h.k || (L.attn_v && !h.v) || !h.o || !h.gate || !h.up || !h.down)
+    return fail(HP_ERR_HANDLE, "unknown weight handle in decode layer");
+  const size_t qd = (size_t)L.attention.head_count * kHeadDim, kd = (size_t)L.attention.head_count_kv * kHeadDim;
+  if (h.q->input_size != hidden || h.k->input_size != hidden || (h.v && h.v->input_size != hidden) ||
+      h.q->row_count != qd || h.k->row_count != kd || (h.v && h.v->row_count != kd))
+    return fail(HP_ERR_SHAPE, "attention projection shapes do not match the attention config");
+  if (h.o->input_size != qd || h.o->row_count != hidden)
+    return fail(HP_ERR_SHAPE, "attn_output shape mismatch");
+  if (h.gate->input_size != hidden || h.up->input_size != hidden || h.gate->row_count != h.up->row_count ||
+      h.down->input_size != h.gate->row_count || h.down->row_count != hidden)
+    return fail(HP_ERR_SHAPE, "FFN shape mismatch");
+  if (!L.d_attn_norm || !L.d_attn_q_norm || !L.d_attn_k_norm || !L.d_post_attention_norm || !L.d_ffn_norm ||
+      !L.d_post_ffw_norm || !L.d_key_cache || !L.d_value_cache)
+    return fail(HP_ERR_ARG, "null norm weight or cache in decode layer");
+  if (L.reserved != 0) return fail(HP_ERR_ARG, "reserved field must be 0");
+  *out = h;
+  return HP_OK;
+}
+
 int32_t topk_check(size_t rows, size_t n, size_t k) {
   if (k == 0 || k > 64) return fail(HP_ERR_ARG, "k must be in 1..64");
   if (n == 0 || n > 524288 || rows > 65535) return fail(HP_ERR_SHAPE, "topk supports 1..524288 values per row");
@@ -767,6 +917,10 @@ int32_t hp_hip_shutdown(void) {
   s.prefill_scratch_cap = 0;
   s.sample_out = nullptr;
   s.sample_out_cap = 0;
+  if (s.attn_scratch) (void)hipFree(s.attn_scratch);
+  if (s.decode_scratch) (void)hipFree(s.decode_scratch);
+  s.attn_scratch = s.decode_scratch = nullptr;
+  s.attn_scratch_cap = s.decode_scratch_cap = 0;
   s.topk_scratch = s.topk_out = nullptr;
   s.topk_scratch_cap = s.topk_out_cap = 0;
   prof_collect();
@@ -1301,6 +1455,206 @@ int32_t hp_hip_profile_read(int32_t kernel, double *total_ms, uint64_t *launches
   prof_collect();
   if (total_ms) *total_ms = s.prof[kernel].total_ms;
   if (launches) *launches = s.prof[kernel].launches;
+  return HP_OK;
+}
+
+int32_t hp_hip_rms_norm_device(const float *d_input, size_t rows, size_t n, const float *d_weight,
+                               double epsilon, float *d_output, void *stream) {
+  State &s = st();
+  std::lock_guard<std::recursive_mutex> lock(s.mu);
+  int32_t rc = ensure_init(s.ready ? s.device : 0);
+  if (rc != HP_OK) return rc;
+  if (n == 0 || n > kNormMaxN) return fail(HP_ERR_SHAPE, "norm width must be 1..4096");
+  if (rows > 65535) return fail(HP_ERR_SHAPE, "too many rows");
+  if (rows == 0) return HP_OK;
+  if (!d_input || !d_output) return fail(HP_ERR_ARG, "null pointer");
+  hipStream_t strm = stream ? static_cast<hipStream_t>(stream) : s.stream;
+  return run_norm(d_input, (int)rows, (int)n, nullptr, nullptr, 1.0f, nullptr, d_weight, d_output, epsilon, strm);
+}
+
+int32_t hp_hip_residual_norm_device(const float *d_branch, size_t rows, size_t n, const float *d_post_weight,
+                                    const float *d_residual, float scale, float *d_residual_out,
+                                    const float *d_next_weight, float *d_next_out, double epsilon,
+                                    void *stream) {
+  State &s = st();
+  std::lock_guard<std::recursive_mutex> lock(s.mu);
+  int32_t rc = ensure_init(s.ready ? s.device : 0);
+  if (rc != HP_OK) return rc;
+  if (n == 0 || n > kNormMaxN) return fail(HP_ERR_SHAPE, "norm width must be 1..4096");
+  if (rows > 65535) return fail(HP_ERR_SHAPE, "too many rows");
+  if (rows == 0) return HP_OK;
+  if (!d_branch || !d_residual || !d_residual_out) return fail(HP_ERR_ARG, "null pointer");
+  hipStream_t strm = stream ? static_cast<hipStream_t>(stream) : s.stream;
+  return run_norm(d_branch, (int)rows, (int)n, d_post_weight, d_residual, scale, d_residual_out, d_next_weight,
+                  d_next_out, epsilon, strm);
+}
+
+int32_t hp_hip_attention_prep_device(const hp_hip_attention_config_t *config, const float *d_q, const float *d_k,
+                                     const float *d_v, const float *d_q_norm, const float *d_k_norm,
+                                     const int32_t *d_position, float *d_q_out, uint16_t *d_key_cache,
+                                     uint16_t *d_value_cache, void *stream) {
+  State &s = st();
+  std::lock_guard<std::recursive_mutex> lock(s.mu);
+  int32_t rc = ensure_init(s.ready ? s.device : 0);
+  if (rc != HP_OK) return rc;
+  rc = attention_check(config);
+  if (rc != HP_OK) return rc;
+  if (!d_q || !d_k || !d_q_norm || !d_k_norm || !d_position || !d_q_out || !d_key_cache || !d_value_cache)
+    return fail(HP_ERR_ARG, "null pointer");
+  hipStream_t strm = stream ? static_cast<hipStream_t>(stream) : s.stream;
+  QkvPostArgs a = qkv_post_args(config);
+  a.q = d_q;
+  a.k = d_k;
+  a.v = d_v ? d_v : d_k;
+  a.wq = d_q_norm;
+  a.wk = d_k_norm;
+  a.position = d_position;
+  a.q_out = d_q_out;
+  a.k_cache = reinterpret_cast<_Float16 *>(d_key_cache);
+  a.v_cache = reinterpret_cast<_Float16 *>(d_value_cache);
+  HP_HIP_TRY(launch_qkv_post(a, strm));
+  s.launches++;
+  return HP_OK;
+}
+
+int32_t hp_hip_gqa_attention_device(const hp_hip_attention_config_t *config, const float *d_q,
+                                    const uint16_t *d_key_cache, const uint16_t *d_value_cache,
+                                    const int32_t *d_position, float *d_output, void *stream) {
+  State &s = st();
+  std::lock_guard<std::recursive_mutex> lock(s.mu);
+  int32_t rc = ensure_init(s.ready ? s.device : 0);
+  if (rc != HP_OK) return rc;
+  rc = attention_check(config);
+  if (rc != HP_OK) return rc;
+  if (!d_q || !d_key_cache || !d_value_cache || !d_position || !d_output) return fail(HP_ERR_ARG, "null pointer");
+  hipStream_t strm = stream ? static_cast<hipStream_t>(stream) : s.stream;
+  rc = grow_uncaptured(&s.attn_scratch, &s.attn_scratch_cap,
+                       attn_partial_floats(config->head_count_kv, config->capacity) * sizeof(float), strm);
+  if (rc != HP_OK) return rc;
+  AttnArgs a = attn_args(config);
+  a.q = d_q;
+  a.k_cache = reinterpret_cast<_Float16 *>(const_cast<uint16_t *>(d_key_cache));  // read only: prep == 0
+  a.v_cache = reinterpret_cast<_Float16 *>(const_cast<uint16_t *>(d_value_cache));
+  a.position = d_position;
+  a.out = d_output;
+  return run_attention(a, static_cast<float *>(s.attn_scratch), strm);
+}
+
+int32_t hp_hip_decode_layers_device(const hp_hip_decode_layer_t *layers, size_t layer_count, float *d_hidden,
+                                    const int32_t *d_position, const float *d_output_norm, float *d_output,
+                                    void *stream) {
+  State &s = st();
+  std::lock_guard<std::recursive_mutex> lock(s.mu);
+  int32_t rc = ensure_init(s.ready ? s.device : 0);
+  if (rc != HP_OK) return rc;
+  if (layer_count == 0 && !d_output_norm) return HP_OK;
+  if (!d_hidden || !d_position || (layer_count && !layers) || (d_output_norm && !d_output))
+    return fail(HP_ERR_ARG, "null pointer");
+  if (reinterpret_cast<uintptr_t>(d_hidden) % 16 != 0) return fail(HP_ERR_ARG, "hidden must be 16-byte aligned");
+  std::vector<LayerHandles> hs(layer_count);
+  size_t hidden = 0, qmax = 0, kvmax = 0, ffmax = 0, partials = 0;
+  for (size_t i = 0; i < layer_count; i++) {
+    if (i == 0) hidden = lookup(layers[0].attn_q) ? lookup(layers[0].attn_q)->input_size : 0;
+    rc = decode_layer_check(layers[i], hidden, &hs[i]);
+    if (rc != HP_OK) return rc;
+    const hp_hip_attention_config_t &c = layers[i].attention;
+    qmax = std::max(qmax, (size_t)c.head_count * kHeadDim);
+    kvmax = std::max(kvmax, (size_t)c.head_count_kv * kHeadDim);
+    ffmax = std::max(ffmax, hs[i].gate->row_count);
+    partials = std::max(partials, attn_partial_floats(c.head_count_kv, c.capacity));
+  }
+  if (layer_count == 0) return fail(HP_ERR_ARG, "the final norm alone: use hp_hip_rms_norm_device");
+  if (hidden == 0 || hidden > kNormMaxN) return fail(HP_ERR_SHAPE, "hidden size must be 1..4096");
+  // scratch: xn, q, k, v, attention, o, x1, h, y, attention partials, RoPE table
+  auto al = [](size_t n) { return (n + 63) & ~(size_t)63; };
+  const size_t sizes[11] = {al(hidden), al(qmax), al(kvmax), al(kvmax), al(qmax),   al(hidden),
+                            al(hidden), al(ffmax), al(hidden), al(partials), al(kHeadDim / 2 * 4)};
+  size_t total = 0;
+  for (size_t z : sizes) total += z;
+  hipStream_t strm = stream ? static_cast<hipStream_t>(stream) : s.stream;
+  rc = grow_uncaptured(&s.decode_scratch, &s.decode_scratch_cap, total * sizeof(float), strm);
+  if (rc != HP_OK) return rc;
+  float *buf[11];
+  float *p = static_cast<float *>(s.decode_scratch);
+  for (int i = 0; i < 11; i++) {
+    buf[i] = p;
+    p += sizes[i];
+  }
+  double2 *rope_table = reinterpret_cast<double2 *>(buf[10]);
+  float *xn = buf[0], *q = buf[1], *k = buf[2], *v = buf[3], *att = buf[4], *o = buf[5], *x1 = buf[6],
+        *h = buf[7], *y = buf[8], *part = buf[9];
+  // The norms ride in the prologues of the launches that consume them: the
+  // Q/K/V launch forms attn_norm(previous residual), the gate/up launch
+  // ffn_norm(residual after attention); xn takes them only when a launch
+  // cannot (a forced matrix-core kernel).
+  NormIn nin{};
+  nin.mode = 1;
+  nin.y = d_hidden;
+  nin.w_next = layers[0].d_attn_norm;
+  nin.scale = 1.0f;
+  nin.eps = layers[0].attention.epsilon;
+  for (size_t i = 0; i < layer_count; i++) {
+    const hp_hip_decode_layer_t &L = layers[i];
+    const LayerHandles &H = hs[i];
+    const double eps = L.attention.epsilon;
+    Handle *qkv[3] = {H.q, H.k, H.v};
+    float *qkv_out[3] = {q, k, v};
+    rc = run_matvec(H.v ? 3 : 2, qkv, nullptr, hidden, 1, qkv_out, strm, &nin, xn);
+    if (rc != HP_OK) return rc;
+    AttnArgs aa = attn_args(&L.attention);
+    aa.prep = 1;
+    aa.q = q;
+    aa.k = k;
+    aa.v = H.v ? v : k;
+    aa.wq = L.d_attn_q_norm;
+    aa.wk = L.d_attn_k_norm;
+    aa.k_cache = reinterpret_cast<_Float16 *>(L.d_key_cache);
+    aa.v_cache = reinterpret_cast<_Float16 *>(L.d_value_cache);
+    aa.position = d_position;
+    aa.out = att;
+    // the RoPE angles depend on the position and the RoPE parameters only:
+    // a layer whose parameters match the previous layer's reads its table
+    aa.rope_table = rope_table;
+    const hp_hip_attention_config_t *pc = i > 0 ? &layers[i - 1].attention : nullptr;
+    aa.rope_table_mode = pc && pc->rope_dims == L.attention.rope_dims &&
+                                 pc->rope_freq_base == L.attention.rope_freq_base &&
+                                 pc->d_rope_freq_factors == L.attention.d_rope_freq_factors
+                             ? 2
+                             : 1;
+    rc = run_attention(aa, part, strm);
+    if (rc != HP_OK) return rc;
+    Handle *oh[1] = {H.o};
+    float *oo[1] = {o};
+    rc = run_matvec(1, oh, att, H.o->input_size, 1, oo, strm);
+    if (rc != HP_OK) return rc;
+    NormIn fin{};
+    fin.mode = 2;
+    fin.y = o;
+    fin.w_post = L.d_post_attention_norm;
+    fin.x_res = d_hidden;
+    fin.scale = 1.0f;
+    fin.x_out = x1;
+    fin.w_next = L.d_ffn_norm;
+    fin.eps = eps;
+    rc = run_matvec_geglu(H.gate, H.up, nullptr, hidden, 1, h, strm, &fin, xn);
+    if (rc != HP_OK) return rc;
+    Handle *dh[1] = {H.down};
+    float *yo[1] = {y};
+    rc = run_matvec(1, dh, h, H.down->input_size, 1, yo, strm);
+    if (rc != HP_OK) return rc;
+    nin.mode = 2;
+    nin.y = y;
+    nin.w_post = L.d_post_ffw_norm;
+    nin.x_res = x1;
+    nin.scale = L.layer_output_scale;
+    nin.x_out = d_hidden;
+    nin.w_next = i + 1 < layer_count ? layers[i + 1].d_attn_norm : nullptr;
+    nin.eps = eps;
+  }
+  // the last layer's post-FFN residual, then output_norm
+  rc = run_norm(y, 1, (int)hidden, nin.w_post, x1, nin.scale, d_hidden, d_output_norm, d_output_norm ? d_output : nullptr,
+                nin.eps, strm);
+  if (rc != HP_OK) return rc;
   return HP_OK;
 }
 

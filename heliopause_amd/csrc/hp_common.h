@@ -67,7 +67,23 @@ struct WeightDesc {
   int unit_begin;         // first global unit index of this weight
 };
 
+// Input of a one-column matvec launch formed in every workgroup's prologue
+// from a residual stream (input size <= 16 * 256), in place of a plain x:
+//   mode 1: x = rmsnorm(y) * w_next
+//   mode 2: x1 = f32(f32(x_res + rmsnorm(y) * w_post) * scale), written to
+//           x_out by workgroup 0 (x_out must not alias y or x_res), and
+//           x = rmsnorm(x1) * w_next
+// with rmsnorm as the norm kernels compute it (f64 sum of squares).
+struct NormIn {
+  const float *y, *w_post, *x_res, *w_next;
+  float *x_out;
+  float scale;
+  int mode;  // 0: plain x
+  double eps;
+};
+
 struct MatvecArgs {
+  NormIn norm;
   WeightDesc w[kMaxWeights];
   int count;
   int total_tiles;
@@ -153,6 +169,56 @@ hipError_t launch_prefill_fast(const MfmaLaunch &l, const float *x, uint8_t *scr
 
 hipError_t launch_geglu(const float *gate, const float *up, size_t n, double c, float *out, int num_cus,
                         hipStream_t s);
+
+// Decoder-layer steps for one decode token (decode_layer.hip).  Heads are
+// kHeadDim wide; `position` points to the token's position in device memory.
+constexpr int kHeadDim = 256;
+constexpr int kAttnChunk = 32;    // cache slots per attention workgroup
+constexpr int kAttnMaxGroup = 8;  // query heads per kv head
+
+// Per row of [rows][n] (n <= 4096): x_res == null: next_out = rmsnorm(y) *
+// w_next.  Otherwise x_out = f32(f32(x_res + rmsnorm(y) * w_post) * scale)
+// and, if next_out != null, next_out = rmsnorm(x_out) * w_next.  A null
+// norm weight means a norm without weight.
+struct NormArgs {
+  const float *y, *w_post, *x_res, *w_next;
+  float *x_out, *next_out;
+  float scale;
+  int n, rows;
+  double eps;
+};
+struct QkvPostArgs {
+  const float *q, *k, *v;  // projections [heads][kHeadDim]
+  const float *wq, *wk;    // head norm weights [kHeadDim]
+  const float *freq_factors;  // [rope_dims / 2] or null
+  const int *position;
+  float *q_out;
+  _Float16 *k_cache, *v_cache;  // [nkv][capacity][kHeadDim]
+  int nq, nkv, capacity, rope_dims;
+  double theta_scale;  // base^(-2 / rope_dims)
+  double eps;
+};
+// prep == 0: q holds the queries after RoPE and the caches already hold the
+// token.  prep == 1: q, k, v are the token's projections ([heads][kHeadDim],
+// v may equal k); the kernel applies the head norms (wq, wk; v without
+// weight) and RoPE and appends the key and value at slot position % capacity.
+struct AttnArgs {
+  const float *q, *k, *v;
+  const float *wq, *wk, *freq_factors;
+  _Float16 *k_cache, *v_cache;
+  const int *position;
+  float *out;      // [nq][kHeadDim], f16-rounded
+  float *part_m, *part_l, *part_o;  // set by launch_attention
+  double2 *rope_table;  // [kHeadDim / 2] cos, sin (rope_table_mode 1: written, 2: read)
+  int nq, nkv, capacity, window, chunks, rope_dims, prep, rope_table_mode;
+  double theta_scale, eps;
+};
+hipError_t launch_norm_residual(const NormArgs &a, hipStream_t s);
+hipError_t launch_qkv_post(const QkvPostArgs &a, hipStream_t s);
+// partials: attn_partial_floats(nkv, capacity) floats of device scratch
+// (a.rope_table, when used, lives elsewhere).
+size_t attn_partial_floats(int nkv, int capacity);
+hipError_t launch_attention(AttnArgs a, float *partials, hipStream_t s);
 hipError_t launch_dequantize(int type, const uint8_t *tiles, const uint16_t *dplane, int rows,
                              const TileGeom &g, int row_start, int row_count, float *out, hipStream_t s);
 

@@ -26,6 +26,7 @@
 #include "hp_common.h"
 #include "hp_gelu.h"
 #include "hp_q8k.h"
+#include "hp_wave.h"
 
 namespace hp {
 
@@ -237,6 +238,65 @@ __device__ __forceinline__ void load_x16(float (&v)[16], const float *__restrict
   }
 }
 
+__device__ __forceinline__ void store_x16(float *__restrict__ xb, const float (&v)[16], int i16) {
+  const int j = i16 >> 1, u = i16 & 1;
+#pragma unroll
+  for (int c = 0; c < 4; c++)
+    *reinterpret_cast<float4 *>(xb + 32 * j + 8 * c + 4 * u) = make_float4(v[4 * c], v[4 * c + 1], v[4 * c + 2],
+                                                                           v[4 * c + 3]);
+}
+
+// Norm prologue of a one-column launch (NormIn, hp_common.h): group grp < nb
+// of 16 lanes holds block grp in load_x16's element order; the sums of
+// squares are f64 sums over the workgroup (256 threads).
+struct NormRegs {
+  float y[16], r[16], wp[16], wn[16];
+};
+
+__device__ __forceinline__ void norm_load(const NormIn &n, NormRegs &nr, int grp, int nb, int i16) {
+#pragma unroll
+  for (int i = 0; i < 16; i++) nr.y[i] = nr.r[i] = nr.wp[i] = nr.wn[i] = 0.0f;
+  if (grp < nb) {
+    const size_t off = (size_t)grp * kQK;
+    load_x16(nr.y, n.y + off, i16);
+    if (n.mode == 2) {
+      load_x16(nr.r, n.x_res + off, i16);
+      load_x16(nr.wp, n.w_post + off, i16);
+    }
+    load_x16(nr.wn, n.w_next + off, i16);
+  }
+}
+
+__device__ __forceinline__ double wg_sum_f64(double v, double *sh) {
+  v = wave_sum_f64(v);
+  __syncthreads();
+  if ((threadIdx.x & 63) == 0) sh[threadIdx.x >> 6] = v;
+  __syncthreads();
+  return (sh[0] + sh[1]) + (sh[2] + sh[3]);
+}
+
+__device__ __forceinline__ void norm_finish(const NormIn &n, NormRegs &nr, float (&xv)[16], int grp, int nb,
+                                            int i16, int k, double *sh) {
+  double ss = 0.0;
+#pragma unroll
+  for (int i = 0; i < 16; i++) ss += (double)nr.y[i] * (double)nr.y[i];
+  double sc = 1.0 / sqrt(wg_sum_f64(ss, sh) / (double)k + n.eps);
+  if (n.mode == 2) {
+    ss = 0.0;
+#pragma unroll
+    for (int i = 0; i < 16; i++) {
+      const float t = (float)(((double)nr.y[i] * sc) * (double)nr.wp[i]);
+      const float x1 = (nr.r[i] + t) * n.scale;
+      nr.y[i] = x1;
+      ss += (double)x1 * (double)x1;
+    }
+    if (blockIdx.x == 0 && grp < nb) store_x16(n.x_out + (size_t)grp * kQK, nr.y, i16);
+    sc = 1.0 / sqrt(wg_sum_f64(ss, sh) / (double)k + n.eps);
+  }
+#pragma unroll
+  for (int i = 0; i < 16; i++) xv[i] = (float)(((double)nr.y[i] * sc) * (double)nr.wn[i]);
+}
+
 // One butterfly step of the (|x| desc, index asc) maximum with the partner
 // lane selected by the DPP control.
 template <int CTRL>
@@ -324,7 +384,13 @@ __global__ __launch_bounds__(256) void kquant_matvec_kernel(const MatvecArgs a) 
   const int i16 = lane & 15;
   const int nq = M * nb;
   float xv[16];
-  if (grp < nq) load_x16(xv, a.x + (size_t)(grp / nb) * a.k + (size_t)(grp % nb) * kQK, i16);
+  __shared__ double norm_sh[4];
+  NormRegs nr;
+  const bool normed = M == 1 && a.norm.mode != 0;
+  if (normed)
+    norm_load(a.norm, nr, grp, nb, i16);
+  else if (grp < nq)
+    load_x16(xv, a.x + (size_t)(grp / nb) * a.k + (size_t)(grp % nb) * kQK, i16);
 
   // the i-th tile of this wave (-1: none); with PAIR, gate then up tile
   const int t0 = blockIdx.x * wpg + wave;
@@ -344,6 +410,7 @@ __global__ __launch_bounds__(256) void kquant_matvec_kernel(const MatvecArgs a) 
     cx = make_ctx(a, t, nb, R, S);
     load_regs(cur, cx, 0, lane, nb);
   }
+  if (normed) norm_finish(a.norm, nr, xv, grp, nb, i16, a.k, norm_sh);
 
   for (int q = grp; q < nq; q += wpg * 4) {
     const int qn = q + wpg * 4;
@@ -587,7 +654,14 @@ __global__ __launch_bounds__(256) void kquant_matvec_half_kernel(const MatvecArg
   const int i16 = lane & 15;
   const int nq = M * nb;
   float xv[16];
-  if (grp < nq) load_x16(xv, a.x + (size_t)(grp / nb) * a.k + (size_t)(grp % nb) * kQK, i16);
+  __shared__ double norm_sh[4];
+  if (M == 1 && a.norm.mode != 0) {
+    NormRegs nr;
+    norm_load(a.norm, nr, grp, nb, i16);
+    norm_finish(a.norm, nr, xv, grp, nb, i16, a.k, norm_sh);
+  } else if (grp < nq) {
+    load_x16(xv, a.x + (size_t)(grp / nb) * a.k + (size_t)(grp % nb) * kQK, i16);
+  }
   for (int q = grp; q < nq; q += wpg * 4) {
     const int qn = q + wpg * 4;
     float xn[16];
@@ -730,6 +804,7 @@ static hipError_t launch_half_m(const MatvecArgs &a, int num_cus, hipStream_t s)
 }
 
 hipError_t launch_matvec_half(const MatvecArgs &a, int num_cus, hipStream_t s) {
+  if (a.norm.mode != 0 && (a.cols != 1 || a.g.nb > 16)) return hipErrorInvalidValue;
   if (a.g.S > 32 || a.Rh < 1 || 2 * a.Rh * a.g.S > 64) return hipErrorInvalidValue;
   switch (a.cols) {
     case 1: return launch_half_m<1>(a, num_cus, s);
@@ -752,6 +827,7 @@ static hipError_t launch_pair_m(const MatvecArgs &a, int num_cus, hipStream_t s)
 }
 
 hipError_t launch_matvec_pair(const MatvecArgs &a, int num_cus, hipStream_t s) {
+  if (a.norm.mode != 0 && (a.cols != 1 || a.g.nb > 16)) return hipErrorInvalidValue;
   if (a.count != 2 || a.w[0].rows != a.w[1].rows || a.w[0].tiles != a.w[1].tiles || !a.pair_out)
     return hipErrorInvalidValue;
   switch (a.cols) {
@@ -764,6 +840,7 @@ hipError_t launch_matvec_pair(const MatvecArgs &a, int num_cus, hipStream_t s) {
 }
 
 hipError_t launch_matvec(const MatvecArgs &a, int num_cus, hipStream_t s) {
+  if (a.norm.mode != 0 && (a.cols != 1 || a.g.nb > 16)) return hipErrorInvalidValue;
   switch (a.cols) {
     case 1: return launch_m<1>(a, num_cus, s);
     case 2: return launch_m<2>(a, num_cus, s);

@@ -108,6 +108,41 @@ class HipSampling(ctypes.Structure):
                 ("top_p", ctypes.c_double)]
 
 
+class HipAttentionConfig(ctypes.Structure):
+    """hp_hip_attention_config_t: attention shape, RoPE and KV ring of a layer."""
+    _fields_ = [("head_count", ctypes.c_int32), ("head_count_kv", ctypes.c_int32), ("head_dim", ctypes.c_int32),
+                ("rope_dims", ctypes.c_int32), ("rope_freq_base", ctypes.c_double),
+                ("d_rope_freq_factors", ctypes.c_void_p), ("capacity", ctypes.c_int32),
+                ("sliding_window", ctypes.c_int32), ("epsilon", ctypes.c_double)]
+
+
+class HipDecodeLayer(ctypes.Structure):
+    """hp_hip_decode_layer_t: one decoder layer's handles, norm weights and caches."""
+    _fields_ = [("attn_q", _u64), ("attn_k", _u64), ("attn_v", _u64), ("attn_output", _u64),
+                ("ffn_gate", _u64), ("ffn_up", _u64), ("ffn_down", _u64),
+                ("d_attn_norm", ctypes.c_void_p), ("d_attn_q_norm", ctypes.c_void_p),
+                ("d_attn_k_norm", ctypes.c_void_p), ("d_post_attention_norm", ctypes.c_void_p),
+                ("d_ffn_norm", ctypes.c_void_p), ("d_post_ffw_norm", ctypes.c_void_p),
+                ("layer_output_scale", ctypes.c_float), ("reserved", ctypes.c_int32),
+                ("d_key_cache", ctypes.c_void_p), ("d_value_cache", ctypes.c_void_p),
+                ("attention", HipAttentionConfig)]
+
+
+def _declare_decode(L: ctypes.CDLL) -> None:
+    """Decoder-layer entry points."""
+    vp, i32 = ctypes.c_void_p, ctypes.c_int32
+    cfg = ctypes.POINTER(HipAttentionConfig)
+    L.hp_hip_rms_norm_device.argtypes = [vp, _sz, _sz, vp, ctypes.c_double, vp, vp]
+    L.hp_hip_residual_norm_device.argtypes = [vp, _sz, _sz, vp, vp, ctypes.c_float, vp, vp, vp, ctypes.c_double,
+                                              vp]
+    L.hp_hip_attention_prep_device.argtypes = [cfg, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp]
+    L.hp_hip_gqa_attention_device.argtypes = [cfg, vp, vp, vp, vp, vp, vp]
+    L.hp_hip_decode_layers_device.argtypes = [ctypes.POINTER(HipDecodeLayer), _sz, vp, vp, vp, vp, vp]
+    for name in ("hp_hip_rms_norm_device", "hp_hip_residual_norm_device", "hp_hip_attention_prep_device",
+                 "hp_hip_gqa_attention_device", "hp_hip_decode_layers_device"):
+        getattr(L, name).restype = i32
+
+
 def _declare_optional(L: ctypes.CDLL) -> None:
     """Top-k, GeGLU, sampling and tuning entry points."""
     i32 = ctypes.c_int32
@@ -135,6 +170,7 @@ def _declare_optional(L: ctypes.CDLL) -> None:
     for name in ("hp_hip_matmul_topk", "hp_hip_topk", "hp_hip_topk_device", "hp_hip_geglu",
                  "hp_hip_geglu_device"):
         getattr(L, name).restype = i32
+    _declare_decode(L)
 
 
 def lib() -> ctypes.CDLL:
@@ -144,6 +180,15 @@ def lib() -> ctypes.CDLL:
         return _lib
     if not LIB_PATH.exists():
         raise HipUnavailable(f"{LIB_PATH} is not built (run __graft_entry__.build())")
+    # One HIP runtime per process.  PyTorch ships its own libamdhip64 under
+    # the same soname; with torch loaded first this library binds to that
+    # runtime, so torch's device pointers, streams and graphs are valid here.
+    # Loaded the other way round, the process would hold two HIP runtimes
+    # and torch's device initialisation fails.
+    try:
+        import torch  # noqa: F401
+    except ImportError:
+        pass
     try:
         L = ctypes.CDLL(str(LIB_PATH))
     except OSError as exc:  # pragma: no cover - depends on the host
@@ -522,3 +567,56 @@ def sample_device(d_ids: int, d_values: int, column_count: int, k: int, count: i
     code = lib().hp_hip_sample_device(d_ids, d_values, column_count, k, count, ctypes.byref(opts), d_rng_state,
                                       d_tokens, d_probabilities, d_kept, stream or None)
     assertHipOk(code, "sample")
+
+
+# ---- decoder layer (device pointers; asynchronous on ``stream``) ----------
+
+def attention_config(head_count: int, head_count_kv: int, capacity: int, *, head_dim: int = 256,
+                     rope_dims: int = 256, rope_freq_base: float = 10000.0, d_rope_freq_factors: int = 0,
+                     sliding_window: int = 0, epsilon: float = 1e-6) -> HipAttentionConfig:
+    """hp_hip_attention_config_t from the manifest's attention fields."""
+    return HipAttentionConfig(head_count, head_count_kv, head_dim, rope_dims, rope_freq_base,
+                              d_rope_freq_factors or None, capacity, sliding_window, epsilon)
+
+
+def rms_norm_device(d_input: int, rows: int, n: int, d_weight: int, epsilon: float, d_output: int,
+                    stream: int = 0) -> None:
+    """rmsNormRows (d_weight 0: rmsNormRowsNoWeight) on device rows."""
+    assertHipOk(lib().hp_hip_rms_norm_device(d_input, rows, n, d_weight or None, epsilon, d_output,
+                                             stream or None), "rms_norm")
+
+
+def residual_norm_device(d_branch: int, rows: int, n: int, d_post_weight: int, d_residual: int, scale: float,
+                         d_residual_out: int, d_next_weight: int, d_next_out: int, epsilon: float,
+                         stream: int = 0) -> None:
+    """Post-norm residual add (times scale), then the next norm (d_next_out 0: none)."""
+    assertHipOk(lib().hp_hip_residual_norm_device(d_branch, rows, n, d_post_weight or None, d_residual, scale,
+                                                  d_residual_out, d_next_weight or None, d_next_out or None,
+                                                  epsilon, stream or None), "residual_norm")
+
+
+def attention_prep_device(config: HipAttentionConfig, d_q: int, d_k: int, d_v: int, d_q_norm: int, d_k_norm: int,
+                          d_position: int, d_q_out: int, d_key_cache: int, d_value_cache: int,
+                          stream: int = 0) -> None:
+    """q/k head norms + RoPE, v norm, and the KV-cache append at *d_position."""
+    assertHipOk(lib().hp_hip_attention_prep_device(ctypes.byref(config), d_q, d_k, d_v or None, d_q_norm, d_k_norm,
+                                                   d_position, d_q_out, d_key_cache, d_value_cache,
+                                                   stream or None), "attention_prep")
+
+
+def gqa_attention_device(config: HipAttentionConfig, d_q: int, d_key_cache: int, d_value_cache: int,
+                         d_position: int, d_output: int, stream: int = 0) -> None:
+    """GQA attention of the token at *d_position over its window, output f16-rounded."""
+    assertHipOk(lib().hp_hip_gqa_attention_device(ctypes.byref(config), d_q, d_key_cache, d_value_cache,
+                                                  d_position, d_output, stream or None), "gqa_attention")
+
+
+def decode_layers_device(layers: Sequence[HipDecodeLayer], d_hidden: int, d_position: int,
+                         d_output_norm: int = 0, d_output: int = 0, stream: int = 0):
+    """forwardAttentionLayer for one token through ``layers`` (hidden in place),
+    then the final norm into d_output when d_output_norm is given.  Returns the
+    ctypes array passed (keep it alive while a captured graph may replay)."""
+    arr = (HipDecodeLayer * len(layers))(*layers)
+    assertHipOk(lib().hp_hip_decode_layers_device(arr, len(layers), d_hidden, d_position, d_output_norm or None,
+                                                  d_output or None, stream or None), "decode_layers")
+    return arr

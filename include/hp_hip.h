@@ -238,6 +238,106 @@ int32_t hp_hip_synchronize(void);
 int32_t hp_hip_profile(int32_t enable);
 int32_t hp_hip_profile_read(int32_t kernel, double *total_ms, uint64_t *launches);
 
+/* ---- Decoder layer for one decode token -------------------------------
+ * The non-projection steps of forwardAttentionLayer / forwardFfn
+ * (packages/engine/src/runner/wasm/layers.ts:161-473) on the device, for
+ * chaining a whole decode step in HBM and capturing it in one HIP graph.
+ * The token position is read from device memory (d_position, one int32) when
+ * the kernels run, so one captured step serves every position.
+ *
+ * Numerics follow the reference's operation order per element; its sums (the
+ * f64 sum of squares of a norm, the f32 dot products and softmax sums of
+ * attention) are tree sums here, so these steps agree with the reference
+ * within a tolerance, not bit for bit.  The KV cache holds f16 keys and
+ * values (as the WebGPU runner's caches, shaders.ts:1134-1202) laid out
+ * [head_count_kv][capacity][head_dim], entries rounded to nearest even; the
+ * WASM runner keeps f32 entries.
+ *
+ * Calls under HIP graph capture must follow an uncaptured call of the same
+ * shape: the library's scratch is sized outside capture, and a call that
+ * would have to grow it while its stream is capturing fails with
+ * HP_ERR_ARG. */
+typedef struct hp_hip_attention_config {
+  int32_t head_count;     /* query heads */
+  int32_t head_count_kv;  /* key/value heads: head_count % head_count_kv == 0,
+                             head_count / head_count_kv <= 8 */
+  int32_t head_dim;       /* 256 (the only width the kernels take) */
+  int32_t rope_dims;      /* ropeDimensionCount: even, <= head_dim (0: no RoPE) */
+  double rope_freq_base;  /* ropeFreqBase */
+  const float *d_rope_freq_factors; /* rope_freqs.weight [rope_dims / 2], or NULL */
+  int32_t capacity;       /* KV ring slots; slot = position % capacity */
+  int32_t sliding_window; /* 0: none; else the window of attentionRange */
+  double epsilon;         /* layer_norm_rms_epsilon */
+} hp_hip_attention_config_t;
+
+/* rmsNormRows (layers.ts:825-832, rmsNormVector 871-885) over [rows][n]
+ * (n <= 4096): out = f32((x * scale) * w), scale = 1 / sqrt(sum(x^2) / n +
+ * eps) in f64.  d_weight NULL: rmsNormRowsNoWeight (834-849). */
+int32_t hp_hip_rms_norm_device(const float *d_input, size_t rows, size_t n, const float *d_weight,
+                               double epsilon, float *d_output, void *stream);
+
+/* Post-norm residual of a block, fused with the next norm:
+ *   d_residual_out = f32(residualAdd(d_residual, rmsNormRows(d_branch,
+ *                    d_post_weight)) * scale)
+ * (layers.ts:350-355 and 466-472: post_attention_norm / post_ffw_norm then
+ * residualAdd 851-860; the layer output scale 360-369 with scale 1 when
+ * absent), then, when d_next_out is not NULL, d_next_out =
+ * rmsNormRows(d_residual_out, d_next_weight) (the next ffn_norm,
+ * attn_norm or output_norm).  d_residual_out may equal d_residual. */
+int32_t hp_hip_residual_norm_device(const float *d_branch, size_t rows, size_t n, const float *d_post_weight,
+                                    const float *d_residual, float scale, float *d_residual_out,
+                                    const float *d_next_weight, float *d_next_out, double epsilon,
+                                    void *stream);
+
+/* Attention prologue of one token (layers.ts:205-268, as the WebGPU runner
+ * fuses it, shaders.ts:1306-1385): q = ropeNeox(normHeads(d_q, d_q_norm)) ->
+ * d_q_out [head_count][256]; k = ropeNeox(normHeads(d_k, d_k_norm)) and v =
+ * rmsNormRowsNoWeight(d_v) appended to the caches at slot position %
+ * capacity (updateFullAttentionCache, layers.ts:887-911).  d_v NULL: the
+ * value shares the key projection (layerValueProjectionModes
+ * "shared-with-key", layers.ts:231-238). */
+int32_t hp_hip_attention_prep_device(const hp_hip_attention_config_t *config, const float *d_q, const float *d_k,
+                                     const float *d_v, const float *d_q_norm, const float *d_k_norm,
+                                     const int32_t *d_position, float *d_q_out, uint16_t *d_key_cache,
+                                     uint16_t *d_value_cache, void *stream);
+
+/* GQA decode attention of one token over its window of the caches
+ * (attentionRange, layers.ts:972-980) as hp_gqa_attention_f32
+ * (packages/engine/wasm-kernels/src/lib.rs:538-654) computes it with scale 1
+ * and an f16-rounded query, followed by castF16Rows (layers.ts:982-988):
+ * d_output [head_count][256]. */
+int32_t hp_hip_gqa_attention_device(const hp_hip_attention_config_t *config, const float *d_q,
+                                    const uint16_t *d_key_cache, const uint16_t *d_value_cache,
+                                    const int32_t *d_position, float *d_output, void *stream);
+
+/* One decoder layer's weights and state.  Handles from hp_hip_weight_upload*;
+ * attn_v 0 means the value shares the key projection.  Norm weights are f32
+ * device arrays: attn_norm, post_attention_norm, ffn_norm, post_ffw_norm
+ * [hidden]; attn_q_norm, attn_k_norm [head_dim]. */
+typedef struct hp_hip_decode_layer {
+  uint64_t attn_q, attn_k, attn_v, attn_output, ffn_gate, ffn_up, ffn_down;
+  const float *d_attn_norm, *d_attn_q_norm, *d_attn_k_norm, *d_post_attention_norm, *d_ffn_norm,
+      *d_post_ffw_norm;
+  float layer_output_scale; /* layer_output_scale.weight[0], or 1 */
+  int32_t reserved;         /* 0 */
+  uint16_t *d_key_cache, *d_value_cache; /* f16 [head_count_kv][capacity][head_dim] */
+  hp_hip_attention_config_t attention;
+} hp_hip_decode_layer_t;
+
+/* forwardAttentionLayer (layers.ts:161-379, with forwardFfn 418-473) for one
+ * token through layers[0 .. layer_count): d_hidden [hidden] is the residual
+ * stream, updated in place.  When d_output_norm is not NULL, d_output =
+ * rmsNormRows(hidden, d_output_norm) (forwardOutput's final norm,
+ * layers.ts:389-396), ready for the output head.  Per layer: Q/K/V in one
+ * matvec launch, the attention prologue, attention (two launches), O, the
+ * post-attention residual fused with ffn_norm, gate/up + GeGLU, down, and the
+ * post-FFN residual with the layer scale fused with the next layer's
+ * attn_norm.  Per-layer input embeddings (applyPerLayerInput) are not part
+ * of this path. */
+int32_t hp_hip_decode_layers_device(const hp_hip_decode_layer_t *layers, size_t layer_count, float *d_hidden,
+                                    const int32_t *d_position, const float *d_output_norm, float *d_output,
+                                    void *stream);
+
 #ifdef __cplusplus
 }
 #endif

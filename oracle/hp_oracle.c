@@ -744,3 +744,131 @@ size_t hpo_topk(const float *values, size_t n, size_t k, uint32_t *ids, float *o
   }
   return len;
 }
+
+/* ---------------------------------------------------------------------- */
+/* Decoder-layer steps (packages/engine/src/runner/wasm/layers.ts).         */
+
+/* rmsNormVector (layers.ts:871-885): sumSquares += value * value in f64, in
+ * index order; scale = 1 / sqrt(sumSquares / n + eps); output[i] =
+ * f32((x[i] * scale) * w[i]) in f64.  w == NULL: rmsNormRowsNoWeight
+ * (layers.ts:834-849), output[i] = f32(x[i] * scale). */
+void hpo_rms_norm_vector(const float *x, size_t n, const float *w, double eps, float *out) {
+  double sum = 0.0;
+  for (size_t i = 0; i < n; i++) sum += (double)x[i] * (double)x[i];
+  const double scale = 1.0 / sqrt(sum / (double)n + eps);
+  for (size_t i = 0; i < n; i++)
+    out[i] = w ? (float)(((double)x[i] * scale) * (double)w[i]) : (float)((double)x[i] * scale);
+}
+
+/* residualAdd (layers.ts:851-860): f32(a + b). */
+void hpo_residual_add(const float *a, const float *b, size_t n, float *out) {
+  for (size_t i = 0; i < n; i++) out[i] = (float)((double)a[i] + (double)b[i]);
+}
+
+/* castF16Rows (layers.ts:982-988): float16ToFloat32(float32ToFloat16(v)). */
+void hpo_cast_f16_rows(const float *in, size_t n, float *out) {
+  for (size_t i = 0; i < n; i++) out[i] = (float)hpo_f16_to_f64_ts(hpo_f64_to_f16_ts((double)in[i]));
+}
+
+/* ropeNeox (layers.ts:990-1033) over [token_count][head_count][head_size].
+ * thetaScale = pow(freqBase, -2 / nDims); per head theta starts at the
+ * token's position and becomes f32(theta * thetaScale) after each pair;
+ * the angle is theta / freq_factors[i] (1 without factors); outputs
+ * f32(f32(x0 cos) - f32(x1 sin)) and f32(f32(x0 sin) + f32(x1 cos)).
+ * Returns HPO_ERR_SHAPE for an odd or too large nDims. */
+int32_t hpo_rope_neox(const float *input, size_t head_size, size_t head_count, size_t token_count,
+                      const int32_t *positions, size_t n_dims, double freq_base, const float *freq_factors,
+                      float *output) {
+  if (n_dims > head_size || n_dims % 2 != 0) return HPO_ERR_SHAPE;
+  const size_t total = head_size * head_count * token_count;
+  memcpy(output, input, total * sizeof(float));
+  const double theta_scale = pow(freq_base, -2.0 / (double)n_dims);
+  const size_t half = n_dims / 2;
+  for (size_t t = 0; t < token_count; t++) {
+    for (size_t h = 0; h < head_count; h++) {
+      const size_t row = (t * head_count + h) * head_size;
+      double theta = (double)positions[t];
+      for (size_t i = 0; i < half; i++) {
+        const double x0 = input[row + i], x1 = input[row + half + i];
+        const double ang = freq_factors ? theta / (double)freq_factors[i] : theta;
+        const double c = cos(ang), s = sin(ang);
+        output[row + i] = (float)((double)(float)(x0 * c) - (double)(float)(x1 * s));
+        output[row + half + i] = (float)((double)(float)(x0 * s) + (double)(float)(x1 * c));
+        theta = (double)(float)(theta * theta_scale);
+      }
+    }
+  }
+  return HPO_OK;
+}
+
+/* hp_gqa_attention_f32 (packages/engine/wasm-kernels/src/lib.rs:538-654):
+ * the same checks and status codes, f32 arithmetic in the same order
+ * (dot = dot + q * k per index; score = (dot * scale) + mask; p =
+ * f32(exp(f64(score - max))); weighted = weighted + (p / sum) * v).  exp is
+ * f64 exp as Rust's std resolves it on wasm32 (compiler-builtins' libm, a
+ * port of FreeBSD msun e_exp.c: hpo_exp).  value_layout 1 =
+ * "dim-head-token" ((index * kv_heads + kv_head) * capacity + token), else
+ * token-major like the key. */
+int32_t hpo_gqa_attention_f32(const float *query, size_t query_len, const float *key, size_t key_len,
+                              const float *value, size_t value_len, const float *mask, size_t mask_len,
+                              size_t head_size, size_t query_head_count, size_t key_value_head_count,
+                              size_t token_count, size_t key_value_token_count, size_t key_value_start,
+                              size_t key_value_capacity, float scale, int32_t value_layout,
+                              int32_t quantize_query_f16, float *output, size_t output_len) {
+  if (query_len != sat_mul(sat_mul(token_count, query_head_count), head_size) ||
+      key_len != sat_mul(sat_mul(key_value_capacity, key_value_head_count), head_size) ||
+      value_len != sat_mul(sat_mul(key_value_capacity, key_value_head_count), head_size) ||
+      output_len != sat_mul(sat_mul(token_count, query_head_count), head_size) ||
+      (mask_len != 0 && mask_len != sat_mul(token_count, key_value_token_count)))
+    return HPO_ERR_SHAPE;
+  if (key_value_head_count == 0 || key_value_capacity == 0 || key_value_token_count > key_value_capacity ||
+      query_head_count % key_value_head_count != 0)
+    return HPO_ERR_HEADS;
+  const size_t group = query_head_count / key_value_head_count;
+  float *scores = malloc((key_value_token_count ? key_value_token_count : 1) * sizeof(float));
+  float *qv = malloc((head_size ? head_size : 1) * sizeof(float));
+  if (!scores || !qv) {
+    free(scores);
+    free(qv);
+    return HPO_ERR_SHAPE;
+  }
+  for (size_t t = 0; t < token_count; t++) {
+    for (size_t qh = 0; qh < query_head_count; qh++) {
+      const size_t kvh = qh / group;
+      const size_t qo = (t * query_head_count + qh) * head_size;
+      for (size_t i = 0; i < head_size; i++)
+        qv[i] = quantize_query_f16 ? hpo_f16_to_f32(hpo_f32_to_f16_rust(query[qo + i])) : query[qo + i];
+      float max_score = -INFINITY;
+      for (size_t kt = 0; kt < key_value_token_count; kt++) {
+        const size_t phys = (key_value_start + kt) % key_value_capacity;
+        const size_t ko = (phys * key_value_head_count + kvh) * head_size;
+        float dot = 0.0f;
+        for (size_t i = 0; i < head_size; i++) dot = dot + qv[i] * key[ko + i];
+        const float mv = mask_len == 0 ? 0.0f : mask[t * key_value_token_count + kt];
+        const float score = mv == -INFINITY ? -INFINITY : (dot * scale) + mv;
+        scores[kt] = score;
+        if (score > max_score) max_score = score;
+      }
+      float sum = 0.0f;
+      for (size_t kt = 0; kt < key_value_token_count; kt++) {
+        const float sc = scores[kt];
+        const float p = sc == -INFINITY ? 0.0f : (float)hpo_exp((double)(sc - max_score));
+        scores[kt] = p;
+        sum += p;
+      }
+      for (size_t i = 0; i < head_size; i++) {
+        float weighted = 0.0f;
+        for (size_t kt = 0; kt < key_value_token_count; kt++) {
+          const size_t phys = (key_value_start + kt) % key_value_capacity;
+          const size_t vo = value_layout == 1 ? (i * key_value_head_count + kvh) * key_value_capacity + phys
+                                              : (phys * key_value_head_count + kvh) * head_size + i;
+          weighted = weighted + (scores[kt] / sum) * value[vo];
+        }
+        output[qo + i] = weighted;
+      }
+    }
+  }
+  free(scores);
+  free(qv);
+  return HPO_OK;
+}

@@ -94,6 +94,25 @@ size_t hpo_topk(const float *values, size_t n, size_t k, uint32_t *ids, float *o
 /* softcap: layers.ts:407-412: fround(tanh(v / c) * c) in f64. */
 float hpo_softcap(float v, double cap);
 
+/* ---- decoder-layer steps ---------------------------------------------- */
+/* rmsNormVector (layers.ts:871-885); w NULL: rmsNormRowsNoWeight (834-849). */
+void hpo_rms_norm_vector(const float *x, size_t n, const float *w, double eps, float *out);
+/* residualAdd (layers.ts:851-860). */
+void hpo_residual_add(const float *a, const float *b, size_t n, float *out);
+/* castF16Rows (layers.ts:982-988). */
+void hpo_cast_f16_rows(const float *in, size_t n, float *out);
+/* ropeNeox (layers.ts:990-1033). */
+int32_t hpo_rope_neox(const float *input, size_t head_size, size_t head_count, size_t token_count,
+                      const int32_t *positions, size_t n_dims, double freq_base, const float *freq_factors,
+                      float *output);
+/* hp_gqa_attention_f32 (lib.rs:538-654). */
+int32_t hpo_gqa_attention_f32(const float *query, size_t query_len, const float *key, size_t key_len,
+                              const float *value, size_t value_len, const float *mask, size_t mask_len,
+                              size_t head_size, size_t query_head_count, size_t key_value_head_count,
+                              size_t token_count, size_t key_value_token_count, size_t key_value_start,
+                              size_t key_value_capacity, float scale, int32_t value_layout,
+                              int32_t quantize_query_f16, float *output, size_t output_len);
+
 #ifdef __cplusplus
 }
 #endif

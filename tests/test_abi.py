@@ -22,11 +22,22 @@ def declared_functions():
 def test_library_exports_every_declared_entry_point():
     from heliopause_amd import hip_kernels as H
 
-    L = ctypes.CDLL(str(H.LIB_PATH))
+    L = H.lib()
     names = declared_functions()
     assert len(names) >= 20
     missing = [n for n in names if not hasattr(L, n)]
     assert not missing, missing
+
+
+def test_one_hip_runtime_in_the_process():
+    """With PyTorch installed, the library binds to torch's HIP runtime (one
+    libamdhip64 mapped), so torch tensors and streams can be passed in."""
+    from heliopause_amd import hip_kernels as H
+
+    H.lib()
+    maps = Path("/proc/self/maps").read_text().splitlines()
+    runtimes = {line.split()[-1] for line in maps if "libamdhip64" in line}
+    assert len(runtimes) == 1, runtimes
 
 
 def test_constants_match_reference():
