@@ -352,7 +352,7 @@ def decode_step(args) -> int:
     kv_bytes = N_LAYERS * 2 * shape.head_count_kv * shape.capacity * 256 * 2
     total = wbytes + kv_bytes
     cpu = None if args.no_cpu else decode_cpu_baseline(shape, data, head_blocks, args.cpu_seconds)
-    launches = 1 + 1 + N_LAYERS * 9 + 1 + 3 + 1
+    launches = 1 + N_LAYERS * 6 + 1 + 1 + 3 + 1  # input copy, 6 per layer, final norm, head, top-k, sample
     line = {
         "metric": "decode step ms at M=1 (1 GPU)",
         "value": round(ms, 4), "unit": "ms", "n_gpus": 1, "steps": steps, "warmup": args.warmup,
