@@ -266,7 +266,7 @@ bool use_half(int cols, const TileGeom &g, int tiles) {
   if (cols > 4 || g.S > 32) return false;
   if (forced == 3) return true;
   if (forced != 0 || g.S > 16) return false;
-  return cols == 1 ? tiles <= 2048 : tiles <= 1024;
+  return tiles <= 1024;
 }
 
 // One matvec launch per column chunk covering every weight (multi == one

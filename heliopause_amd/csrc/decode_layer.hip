@@ -506,40 +506,46 @@ __device__ __forceinline__ float block_sum_f32(float v, float *sh) {
   return (sh[0] + sh[1]) + (sh[2] + sh[3]);
 }
 
-// Merge of the chunks of query head blockIdx.x for dims 64 blockIdx.y .. +
-// 63: thread t sums chunks t / 64, t / 64 + 4, ... of dim t % 64, scaled by
-// exp(m_c - m); then castF16Rows of o / l.
+// Merge of the chunks of query head blockIdx.x for dims 64 blockIdx.y ..
+// + 63: thread t sums chunks t / 64, t / 64 + 4, ... of dim t % 64, scaled by
+// exp(m_c - m); then castF16Rows of o / l.  The chunk outputs are loaded
+// together with the chunk maxima (one memory round trip per 128 chunks).
+constexpr int kMergeTile = 128;  // chunks per round trip: 32 per thread
 __global__ __launch_bounds__(256) void attn_reduce_kernel(const AttnArgs a) {
-  __shared__ float fs[256];
+  __shared__ float fs[kMergeTile];
   __shared__ float sh[4];
   __shared__ float red[4][64];
   const int qh = blockIdx.x, tid = threadIdx.x;
   const int group = a.nq / a.nkv, g = qh / group, h = qh % group;
   const int chunks = a.chunks;
   const size_t row0 = (size_t)g * a.chunks * kAttnMaxGroup + h;  // chunk c at row0 + c * kAttnMaxGroup
+  const int d = blockIdx.y * 64 + (tid & 63), cg = tid >> 6;
   float m = -__builtin_inff();
   for (int c = tid; c < chunks; c += 256) m = fmaxf(m, a.part_m[row0 + (size_t)c * kAttnMaxGroup]);
-  m = block_max_f32(m, sh);
-  const int d = blockIdx.y * 64 + (tid & 63), cg = tid >> 6;
   float l = 0.0f, o = 0.0f;
-  for (int c0 = 0; c0 < chunks; c0 += 256) {
-    const int c = c0 + tid;
-    float f = 0.0f;
-    if (c < chunks) {
-      const size_t base = row0 + (size_t)c * kAttnMaxGroup;
-      const float mc = a.part_m[base];
-      if (mc != -__builtin_inff()) {  // a chunk with no slot in the window adds nothing
-        f = (float)exp((double)(mc - m));
-        l = __builtin_fmaf(f, a.part_l[base], l);
-      }
+  for (int c0 = 0; c0 < chunks; c0 += kMergeTile) {
+    const int n = chunks - c0 < kMergeTile ? chunks - c0 : kMergeTile;
+    float po[kMergeTile / 4];
+#pragma unroll
+    for (int i = 0; i < kMergeTile / 4; i++) {
+      const int cc = cg + 4 * i;
+      po[i] = cc < n ? a.part_o[(row0 + (size_t)(c0 + cc) * kAttnMaxGroup) * kHeadDim + d] : 0.0f;
     }
-    fs[tid] = f;
+    float mc = -__builtin_inff(), lc = 0.0f;
+    if (tid < n) {
+      const size_t base = row0 + (size_t)(c0 + tid) * kAttnMaxGroup;
+      mc = a.part_m[base];
+      lc = a.part_l[base];
+    }
+    if (c0 == 0) m = block_max_f32(m, sh);
+    // a chunk with no slot in the window (m_c = -inf) adds nothing
+    const float f = mc == -__builtin_inff() ? 0.0f : (float)exp((double)(mc - m));
+    l = __builtin_fmaf(f, lc, l);
     __syncthreads();
-    const int n = chunks - c0 < 256 ? chunks - c0 : 256;
-#pragma unroll 4
-    for (int cc = cg; cc < n; cc += 4)
-      o = __builtin_fmaf(fs[cc], a.part_o[(row0 + (size_t)(c0 + cc) * kAttnMaxGroup) * kHeadDim + d], o);
+    if (tid < kMergeTile) fs[tid] = f;
     __syncthreads();
+#pragma unroll
+    for (int i = 0; i < kMergeTile / 4; i++) o = __builtin_fmaf(fs[cg + 4 * i], po[i], o);
   }
   l = block_sum_f32(l, sh);
   red[cg][tid & 63] = o;

@@ -339,15 +339,19 @@ __device__ __forceinline__ void q8k_block16(const float (&v)[16], int i16, uint8
     uint32_t wv = 0;
 #pragma unroll
     for (int c = 0; c < 4; c++) {
-      // Rust: (is * x).round().min(127.0) as i8; min() never yields NaN, so
-      // only the low clamp of the saturating cast can act
-      const float r = fmaxf(fminf(roundf(__fmul_rn(inv, v[4 * c + l4])), 127.0f), -128.0f);
-      const int q = nz ? (int)r : 0;
+      // Rust: (is * x).round().min(127.0) as i8.  |is * x| <= 127 (1 + 2^-23)
+      // for every element, so the saturating cast never acts; NaN -> min()
+      // -> 127.  round() (half away from zero) as trunc(p + copysign(0.5 -
+      // 2^-25, p)): equal for every f32 |p| < 128 (checked exhaustively).
+      const float p = __fmul_rn(inv, v[4 * c + l4]);
+      const float r = fminf(truncf(__fadd_rn(p, copysignf(0.49999997f, p))), 127.0f);
+      const int q = (int)r;
       sum += q;
       wv |= (uint32_t)(q & 0xff) << (8 * c);
     }
-    word[l4] = wv;  // dword l = 4u + l4 of sub-block j
+    word[l4] = nz ? wv : 0u;  // dword l = 4u + l4 of sub-block j
   }
+  sum = nz ? sum : 0;
   sum += dppi<kDppQuadXor1>(sum);
   *reinterpret_cast<uint4 *>(blk + 32 * j + 16 * u) = make_uint4(word[0], word[1], word[2], word[3]);
   if (u == 0) reinterpret_cast<int16_t *>(blk + 256)[j] = (int16_t)sum;
@@ -383,14 +387,20 @@ __global__ __launch_bounds__(256) void kquant_matvec_kernel(const MatvecArgs a) 
   const int grp = wave * 4 + (lane >> 4);
   const int i16 = lane & 15;
   const int nq = M * nb;
-  float xv[16];
+  float xv[16], xv2[16], xv3[16];  // the blocks of this group's first three passes
   __shared__ double norm_sh[4];
   NormRegs nr;
   const bool normed = M == 1 && a.norm.mode != 0;
-  if (normed)
+  auto x_block = [&](int q) { return a.x + (size_t)(q / nb) * a.k + (size_t)(q % nb) * kQK; };
+  if (normed) {
     norm_load(a.norm, nr, grp, nb, i16);
-  else if (grp < nq)
-    load_x16(xv, a.x + (size_t)(grp / nb) * a.k + (size_t)(grp % nb) * kQK, i16);
+  } else {
+    // every pass's input before the weights: vector loads return in order,
+    // so a pass loaded after them would wait for the weights
+    if (grp < nq) load_x16(xv, x_block(grp), i16);
+    if (grp + wpg * 4 < nq) load_x16(xv2, x_block(grp + wpg * 4), i16);
+    if (grp + wpg * 8 < nq) load_x16(xv3, x_block(grp + wpg * 8), i16);
+  }
 
   // the i-th tile of this wave (-1: none); with PAIR, gate then up tile
   const int t0 = blockIdx.x * wpg + wave;
@@ -412,14 +422,16 @@ __global__ __launch_bounds__(256) void kquant_matvec_kernel(const MatvecArgs a) 
   }
   if (normed) norm_finish(a.norm, nr, xv, grp, nb, i16, a.k, norm_sh);
 
-  for (int q = grp; q < nq; q += wpg * 4) {
-    const int qn = q + wpg * 4;
-    float xn[16];
-    if (qn < nq) load_x16(xn, a.x + (size_t)(qn / nb) * a.k + (size_t)(qn % nb) * kQK, i16);
-    q8k_block16(xv, i16, xq + (size_t)q * kQ8BlockBytes, xd + q);
-    if (qn < nq) {
-#pragma unroll
-      for (int i = 0; i < 16; i++) xv[i] = xn[i];
+  {
+    int q = grp;
+    if (q < nq) q8k_block16(xv, i16, xq + (size_t)q * kQ8BlockBytes, xd + q);
+    q += wpg * 4;
+    if (q < nq) q8k_block16(xv2, i16, xq + (size_t)q * kQ8BlockBytes, xd + q);
+    q += wpg * 4;
+    if (q < nq) q8k_block16(xv3, i16, xq + (size_t)q * kQ8BlockBytes, xd + q);
+    for (q += wpg * 4; q < nq; q += wpg * 4) {  // more than three passes (several columns)
+      load_x16(xv, x_block(q), i16);
+      q8k_block16(xv, i16, xq + (size_t)q * kQ8BlockBytes, xd + q);
     }
   }
   __syncthreads();
