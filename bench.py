@@ -288,8 +288,9 @@ def decode_step(args) -> int:
     from heliopause_amd import hip_kernels as H
     from heliopause_amd import synthetic as S
 
-    if args.m != 1:
-        raise SystemExit("decode42 runs at M = 1")
+    m = args.m  # tokens per step: 1 (decode) or a draft of up to 8 being verified
+    if not 1 <= m <= 8:
+        raise SystemExit("decode42 runs 1..8 tokens per step")
     torch.cuda.init()
     dev = torch.device("cuda:0")
     shape = DM.ModelShape()
@@ -301,13 +302,13 @@ def decode_step(args) -> int:
     head_blocks = S.weight_blocks(HEAD[0], S.derive(seed, "head"), HEAD[1], HEAD[2])
     head = H.createHipQuantizedWeightHandle(HEAD[0], head_blocks, HEAD[2], HEAD[1])
     model.set_head((1.0 + 0.1 * S.normal(S.derive(seed, "output_norm"), shape.hidden)).astype(np.float32), head)
-    x0 = torch.from_numpy(S.activations(S.derive(seed, "x"), 1, shape.hidden).reshape(-1) * 4).to(dev)
+    x0 = torch.from_numpy(S.activations(S.derive(seed, "x"), m, shape.hidden).reshape(-1) * 4).to(dev)
     hidden = torch.empty_like(x0)
     normed = torch.empty_like(x0)
-    pos = torch.tensor([shape.capacity], dtype=torch.int32, device=dev)
-    logits = torch.empty(HEAD[1], dtype=torch.float32, device=dev)
-    ids = torch.empty(TOPK, dtype=torch.int32, device=dev)
-    vals = torch.empty(TOPK, dtype=torch.float32, device=dev)
+    pos = torch.tensor([shape.capacity + 1 - m], dtype=torch.int32, device=dev)  # last token at 4096
+    logits = torch.empty(m * HEAD[1], dtype=torch.float32, device=dev)
+    ids = torch.empty(m * TOPK, dtype=torch.int32, device=dev)
+    vals = torch.empty(m * TOPK, dtype=torch.float32, device=dev)
     sampling = H.resolveGenerationSamplingOptions(topK=TOPK)
     rng = torch.from_numpy(np.array([sampling["seed"]], np.uint32).view(np.int32)).to(dev)
     token = torch.zeros(1, dtype=torch.int32, device=dev)
@@ -317,13 +318,14 @@ def decode_step(args) -> int:
 
     def step(stream: int) -> None:
         hidden.copy_(x0)
-        model.run_layers(hidden.data_ptr(), pos.data_ptr(), normed.data_ptr(), stream)
-        H.matmul_multi_device([head.handle], normed.data_ptr(), shape.hidden, 1, [logits.data_ptr()], [HEAD[1]],
-                              stream)
-        H.assertHipOk(L.hp_hip_topk_device(logits.data_ptr(), 1, HEAD[1], TOPK, 0.0, ids.data_ptr(),
+        model.run_layers(hidden.data_ptr(), pos.data_ptr(), normed.data_ptr(), stream, tokens=m)
+        H.matmul_multi_device([head.handle], normed.data_ptr(), shape.hidden, m, [logits.data_ptr()],
+                              [m * HEAD[1]], stream)
+        H.assertHipOk(L.hp_hip_topk_device(logits.data_ptr(), m, HEAD[1], TOPK, 0.0, ids.data_ptr(),
                                            vals.data_ptr(), stream), "topk")
-        H.sample_device(ids.data_ptr(), vals.data_ptr(), 1, TOPK, TOPK, sampling, rng.data_ptr(), token.data_ptr(),
-                        probs.data_ptr(), kept.data_ptr(), stream)
+        if m == 1:  # a draft's positions are compared with the draft on the host (acceptMtpDraft)
+            H.sample_device(ids.data_ptr(), vals.data_ptr(), 1, TOPK, TOPK, sampling, rng.data_ptr(),
+                            token.data_ptr(), probs.data_ptr(), kept.data_ptr(), stream)
 
     side = torch.cuda.Stream()
     side.wait_stream(torch.cuda.current_stream())
@@ -350,18 +352,24 @@ def decode_step(args) -> int:
     wbytes = N_LAYERS * sum(row_bytes(t, k) * r for t, r, k in LAYER) + row_bytes(HEAD[0], HEAD[2]) * HEAD[1]
     kv_bytes = N_LAYERS * 2 * shape.head_count_kv * shape.capacity * 256 * 2
     total = wbytes + kv_bytes
-    cpu = None if args.no_cpu else decode_cpu_baseline(shape, data, head_blocks, args.cpu_seconds)
-    launches = 1 + N_LAYERS * 6 + 1 + 1 + 3 + 1  # input copy, 6 per layer, final norm, head, top-k, sample
+    cpu = None if (args.no_cpu or m != 1) else decode_cpu_baseline(shape, data, head_blocks, args.cpu_seconds)
+    # input copy, per layer (6 for one token; a draft adds the prologue launch and
+    # the norm launches), final norm, head, top-k (3), sample
+    launches = 1 + N_LAYERS * (6 if m == 1 else 9) + 1 + 1 + 3 + (1 if m == 1 else 0)
     line = {
-        "metric": "decode step ms at M=1 (1 GPU)",
+        "metric": "decode step ms at M=1 (1 GPU)" if m == 1 else f"draft verification step ms at M={m} (1 GPU)",
         "value": round(ms, 4), "unit": "ms", "n_gpus": 1, "steps": steps, "warmup": args.warmup,
         "ms_per_step": round(ms, 4), "higher_is_better": False, "scaling": "weak", "vs_baseline": None,
         "dtype": "int8", "data": "synthetic",
         "config": {"workload": "42-layer synthetic Gemma-like model, full decode step at M=1 with a 4096-token f16 "
                                "KV cache: norms, Q/K/V, RoPE, cache append, GQA attention, O, GeGLU FFN, residuals, "
-                               "output norm, head, top-40, next-token sampling",
+                               "output norm, head, top-40, next-token sampling" if m == 1 else
+                               f"42-layer synthetic Gemma-like model, verification of a {m}-token draft (every "
+                               "position through every layer with causal attention over a 4096-token f16 KV cache, "
+                               "output norm, head, top-40 per position)",
                    "weight_bytes": wbytes, "kv_cache_bytes_read": kv_bytes, "launches_per_step": launches,
-                   "wall_ms_per_step": round(wall_ms, 4), "position": int(shape.capacity),
+                   "wall_ms_per_step": round(wall_ms, 4), "tokens": m,
+                   "positions": [int(shape.capacity) + 1 - m, int(shape.capacity)],
                    "timing": "one step captured in a HIP graph and replayed"},
         "roofline": {"bound": "hbm", "achieved": round(total / (ms * 1e-3) / 1e9, 2), "peak": HBM_PEAK_GBPS,
                      "unit": "GB/s", "frac": round(total / (ms * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4),

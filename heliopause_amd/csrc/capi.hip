@@ -734,6 +734,7 @@ QkvPostArgs qkv_post_args(const hp_hip_attention_config_t *c) {
   a.theta_scale = c->rope_dims > 0 ? std::pow(c->rope_freq_base, -2.0 / (double)c->rope_dims) : 1.0;
   a.freq_factors = c->d_rope_freq_factors;
   a.eps = c->epsilon;
+  a.tokens = 1;
   return a;
 }
 
@@ -748,6 +749,7 @@ AttnArgs attn_args(const hp_hip_attention_config_t *c) {
   a.theta_scale = p.theta_scale;
   a.freq_factors = p.freq_factors;
   a.eps = p.eps;
+  a.tokens = 1;
   return a;
 }
 
@@ -1489,16 +1491,17 @@ int32_t hp_hip_residual_norm_device(const float *d_branch, size_t rows, size_t n
                   d_next_out, epsilon, strm);
 }
 
-int32_t hp_hip_attention_prep_device(const hp_hip_attention_config_t *config, const float *d_q, const float *d_k,
-                                     const float *d_v, const float *d_q_norm, const float *d_k_norm,
-                                     const int32_t *d_position, float *d_q_out, uint16_t *d_key_cache,
-                                     uint16_t *d_value_cache, void *stream) {
+int32_t hp_hip_attention_prep_device(const hp_hip_attention_config_t *config, size_t token_count, const float *d_q,
+                                     const float *d_k, const float *d_v, const float *d_q_norm,
+                                     const float *d_k_norm, const int32_t *d_position, float *d_q_out,
+                                     uint16_t *d_key_cache, uint16_t *d_value_cache, void *stream) {
   State &s = st();
   std::lock_guard<std::recursive_mutex> lock(s.mu);
   int32_t rc = ensure_init(s.ready ? s.device : 0);
   if (rc != HP_OK) return rc;
   rc = attention_check(config);
   if (rc != HP_OK) return rc;
+  if (token_count < 1 || token_count > (size_t)kMaxTokens) return fail(HP_ERR_SHAPE, "token_count must be 1..8");
   if (!d_q || !d_k || !d_q_norm || !d_k_norm || !d_position || !d_q_out || !d_key_cache || !d_value_cache)
     return fail(HP_ERR_ARG, "null pointer");
   hipStream_t strm = stream ? static_cast<hipStream_t>(stream) : s.stream;
@@ -1512,12 +1515,13 @@ int32_t hp_hip_attention_prep_device(const hp_hip_attention_config_t *config, co
   a.q_out = d_q_out;
   a.k_cache = reinterpret_cast<_Float16 *>(d_key_cache);
   a.v_cache = reinterpret_cast<_Float16 *>(d_value_cache);
+  a.tokens = (int)token_count;
   HP_HIP_TRY(launch_qkv_post(a, strm));
   s.launches++;
   return HP_OK;
 }
 
-int32_t hp_hip_gqa_attention_device(const hp_hip_attention_config_t *config, const float *d_q,
+int32_t hp_hip_gqa_attention_device(const hp_hip_attention_config_t *config, size_t token_count, const float *d_q,
                                     const uint16_t *d_key_cache, const uint16_t *d_value_cache,
                                     const int32_t *d_position, float *d_output, void *stream) {
   State &s = st();
@@ -1526,10 +1530,13 @@ int32_t hp_hip_gqa_attention_device(const hp_hip_attention_config_t *config, con
   if (rc != HP_OK) return rc;
   rc = attention_check(config);
   if (rc != HP_OK) return rc;
+  if (token_count < 1 || token_count > (size_t)kMaxTokens) return fail(HP_ERR_SHAPE, "token_count must be 1..8");
   if (!d_q || !d_key_cache || !d_value_cache || !d_position || !d_output) return fail(HP_ERR_ARG, "null pointer");
   hipStream_t strm = stream ? static_cast<hipStream_t>(stream) : s.stream;
   rc = grow_uncaptured(&s.attn_scratch, &s.attn_scratch_cap,
-                       attn_partial_floats(config->head_count_kv, config->capacity) * sizeof(float), strm);
+                       attn_partial_floats(config->head_count_kv, config->capacity, (int)token_count) *
+                           sizeof(float),
+                       strm);
   if (rc != HP_OK) return rc;
   AttnArgs a = attn_args(config);
   a.q = d_q;
@@ -1537,56 +1544,59 @@ int32_t hp_hip_gqa_attention_device(const hp_hip_attention_config_t *config, con
   a.v_cache = reinterpret_cast<_Float16 *>(const_cast<uint16_t *>(d_value_cache));
   a.position = d_position;
   a.out = d_output;
+  a.tokens = (int)token_count;
   return run_attention(a, static_cast<float *>(s.attn_scratch), strm);
 }
 
-int32_t hp_hip_decode_layers_device(const hp_hip_decode_layer_t *layers, size_t layer_count, float *d_hidden,
-                                    const int32_t *d_position, const float *d_output_norm, float *d_output,
-                                    void *stream) {
+int32_t hp_hip_decode_layers_device(const hp_hip_decode_layer_t *layers, size_t layer_count, size_t token_count,
+                                    float *d_hidden, const int32_t *d_position, const float *d_output_norm,
+                                    float *d_output, void *stream) {
   State &s = st();
   std::lock_guard<std::recursive_mutex> lock(s.mu);
   int32_t rc = ensure_init(s.ready ? s.device : 0);
   if (rc != HP_OK) return rc;
-  if (layer_count == 0 && !d_output_norm) return HP_OK;
-  if (!d_hidden || !d_position || (layer_count && !layers) || (d_output_norm && !d_output))
-    return fail(HP_ERR_ARG, "null pointer");
+  if (token_count < 1 || token_count > (size_t)kMaxTokens) return fail(HP_ERR_SHAPE, "token_count must be 1..8");
+  if (layer_count == 0) return fail(HP_ERR_ARG, "no layers (the final norm alone: hp_hip_rms_norm_device)");
+  if (!d_hidden || !d_position || !layers || (d_output_norm && !d_output)) return fail(HP_ERR_ARG, "null pointer");
   if (reinterpret_cast<uintptr_t>(d_hidden) % 16 != 0) return fail(HP_ERR_ARG, "hidden must be 16-byte aligned");
+  const size_t M = token_count;
   std::vector<LayerHandles> hs(layer_count);
-  size_t hidden = 0, qmax = 0, kvmax = 0, ffmax = 0, partials = 0;
+  size_t hidden = lookup(layers[0].attn_q) ? lookup(layers[0].attn_q)->input_size : 0;
+  size_t qmax = 0, kvmax = 0, ffmax = 0, partials = 0;
   for (size_t i = 0; i < layer_count; i++) {
-    if (i == 0) hidden = lookup(layers[0].attn_q) ? lookup(layers[0].attn_q)->input_size : 0;
     rc = decode_layer_check(layers[i], hidden, &hs[i]);
     if (rc != HP_OK) return rc;
     const hp_hip_attention_config_t &c = layers[i].attention;
     qmax = std::max(qmax, (size_t)c.head_count * kHeadDim);
     kvmax = std::max(kvmax, (size_t)c.head_count_kv * kHeadDim);
     ffmax = std::max(ffmax, hs[i].gate->row_count);
-    partials = std::max(partials, attn_partial_floats(c.head_count_kv, c.capacity));
+    partials = std::max(partials, attn_partial_floats(c.head_count_kv, c.capacity, (int)M));
   }
-  if (layer_count == 0) return fail(HP_ERR_ARG, "the final norm alone: use hp_hip_rms_norm_device");
   if (hidden == 0 || hidden > kNormMaxN) return fail(HP_ERR_SHAPE, "hidden size must be 1..4096");
-  // scratch: xn, q, k, v, attention, o, x1, h, y, attention partials, RoPE table
+  // scratch ([M] rows each): xn, q, k, v, q after RoPE, attention, o, x1, h, y;
+  // attention partials; RoPE tables [M][128] cos, sin
   auto al = [](size_t n) { return (n + 63) & ~(size_t)63; };
-  const size_t sizes[11] = {al(hidden), al(qmax), al(kvmax), al(kvmax), al(qmax),   al(hidden),
-                            al(hidden), al(ffmax), al(hidden), al(partials), al(kHeadDim / 2 * 4)};
+  const size_t sizes[12] = {al(M * hidden), al(M * qmax),   al(M * kvmax),  al(M * kvmax),
+                            al(M * qmax),   al(M * qmax),   al(M * hidden), al(M * hidden),
+                            al(M * ffmax),  al(M * hidden), al(partials),   al(M * kHeadDim / 2 * 4)};
   size_t total = 0;
   for (size_t z : sizes) total += z;
   hipStream_t strm = stream ? static_cast<hipStream_t>(stream) : s.stream;
   rc = grow_uncaptured(&s.decode_scratch, &s.decode_scratch_cap, total * sizeof(float), strm);
   if (rc != HP_OK) return rc;
-  float *buf[11];
+  float *buf[12];
   float *p = static_cast<float *>(s.decode_scratch);
-  for (int i = 0; i < 11; i++) {
+  for (int i = 0; i < 12; i++) {
     buf[i] = p;
     p += sizes[i];
   }
-  double2 *rope_table = reinterpret_cast<double2 *>(buf[10]);
-  float *xn = buf[0], *q = buf[1], *k = buf[2], *v = buf[3], *att = buf[4], *o = buf[5], *x1 = buf[6],
-        *h = buf[7], *y = buf[8], *part = buf[9];
-  // The norms ride in the prologues of the launches that consume them: the
-  // Q/K/V launch forms attn_norm(previous residual), the gate/up launch
-  // ffn_norm(residual after attention); xn takes them only when a launch
-  // cannot (a forced matrix-core kernel).
+  float *xn = buf[0], *q = buf[1], *k = buf[2], *v = buf[3], *qr = buf[4], *att = buf[5], *o = buf[6],
+        *x1 = buf[7], *h = buf[8], *y = buf[9], *part = buf[10];
+  double2 *rope_table = reinterpret_cast<double2 *>(buf[11]);
+  // The norms ride in the prologues of the launches that consume them (one
+  // token): the Q/K/V launch forms attn_norm(previous residual), the gate/up
+  // launch ffn_norm(residual after attention).  With several tokens, or a
+  // forced matrix-core kernel, they run as norm launches into xn.
   NormIn nin{};
   nin.mode = 1;
   nin.y = d_hidden;
@@ -1599,33 +1609,57 @@ int32_t hp_hip_decode_layers_device(const hp_hip_decode_layer_t *layers, size_t 
     const double eps = L.attention.epsilon;
     Handle *qkv[3] = {H.q, H.k, H.v};
     float *qkv_out[3] = {q, k, v};
-    rc = run_matvec(H.v ? 3 : 2, qkv, nullptr, hidden, 1, qkv_out, strm, &nin, xn);
+    rc = run_matvec(H.v ? 3 : 2, qkv, nullptr, hidden, M, qkv_out, strm, &nin, xn);
     if (rc != HP_OK) return rc;
+    // the RoPE angles depend on the positions and the RoPE parameters only:
+    // a layer whose parameters match the previous layer's reads its table
+    const hp_hip_attention_config_t *pc = i > 0 ? &layers[i - 1].attention : nullptr;
+    const int table_mode = pc && pc->rope_dims == L.attention.rope_dims &&
+                                   pc->rope_freq_base == L.attention.rope_freq_base &&
+                                   pc->d_rope_freq_factors == L.attention.d_rope_freq_factors
+                               ? 2
+                               : 1;
     AttnArgs aa = attn_args(&L.attention);
-    aa.prep = 1;
-    aa.q = q;
-    aa.k = k;
-    aa.v = H.v ? v : k;
-    aa.wq = L.d_attn_q_norm;
-    aa.wk = L.d_attn_k_norm;
     aa.k_cache = reinterpret_cast<_Float16 *>(L.d_key_cache);
     aa.v_cache = reinterpret_cast<_Float16 *>(L.d_value_cache);
     aa.position = d_position;
     aa.out = att;
-    // the RoPE angles depend on the position and the RoPE parameters only:
-    // a layer whose parameters match the previous layer's reads its table
     aa.rope_table = rope_table;
-    const hp_hip_attention_config_t *pc = i > 0 ? &layers[i - 1].attention : nullptr;
-    aa.rope_table_mode = pc && pc->rope_dims == L.attention.rope_dims &&
-                                 pc->rope_freq_base == L.attention.rope_freq_base &&
-                                 pc->d_rope_freq_factors == L.attention.d_rope_freq_factors
-                             ? 2
-                             : 1;
+    aa.rope_table_mode = table_mode;
+    if (M == 1) {
+      // one token: norms, RoPE and the cache append inside the attention launch
+      aa.prep = 1;
+      aa.q = q;
+      aa.k = k;
+      aa.v = H.v ? v : k;
+      aa.wq = L.d_attn_q_norm;
+      aa.wk = L.d_attn_k_norm;
+    } else {
+      // a draft: every token's key and value enter the caches first, then
+      // each token attends causally
+      QkvPostArgs pa = qkv_post_args(&L.attention);
+      pa.q = q;
+      pa.k = k;
+      pa.v = H.v ? v : k;
+      pa.wq = L.d_attn_q_norm;
+      pa.wk = L.d_attn_k_norm;
+      pa.position = d_position;
+      pa.q_out = qr;
+      pa.k_cache = aa.k_cache;
+      pa.v_cache = aa.v_cache;
+      pa.tokens = (int)M;
+      pa.rope_table = rope_table;
+      pa.rope_table_mode = table_mode;
+      HP_HIP_TRY(launch_qkv_post(pa, strm));
+      s.launches++;
+      aa.q = qr;
+      aa.tokens = (int)M;
+    }
     rc = run_attention(aa, part, strm);
     if (rc != HP_OK) return rc;
     Handle *oh[1] = {H.o};
     float *oo[1] = {o};
-    rc = run_matvec(1, oh, att, H.o->input_size, 1, oo, strm);
+    rc = run_matvec(1, oh, att, H.o->input_size, M, oo, strm);
     if (rc != HP_OK) return rc;
     NormIn fin{};
     fin.mode = 2;
@@ -1636,11 +1670,11 @@ int32_t hp_hip_decode_layers_device(const hp_hip_decode_layer_t *layers, size_t 
     fin.x_out = x1;
     fin.w_next = L.d_ffn_norm;
     fin.eps = eps;
-    rc = run_matvec_geglu(H.gate, H.up, nullptr, hidden, 1, h, strm, &fin, xn);
+    rc = run_matvec_geglu(H.gate, H.up, nullptr, hidden, M, h, strm, &fin, xn);
     if (rc != HP_OK) return rc;
     Handle *dh[1] = {H.down};
     float *yo[1] = {y};
-    rc = run_matvec(1, dh, h, H.down->input_size, 1, yo, strm);
+    rc = run_matvec(1, dh, h, H.down->input_size, M, yo, strm);
     if (rc != HP_OK) return rc;
     nin.mode = 2;
     nin.y = y;
@@ -1652,8 +1686,8 @@ int32_t hp_hip_decode_layers_device(const hp_hip_decode_layer_t *layers, size_t 
     nin.eps = eps;
   }
   // the last layer's post-FFN residual, then output_norm
-  rc = run_norm(y, 1, (int)hidden, nin.w_post, x1, nin.scale, d_hidden, d_output_norm, d_output_norm ? d_output : nullptr,
-                nin.eps, strm);
+  rc = run_norm(y, (int)M, (int)hidden, nin.w_post, x1, nin.scale, d_hidden, d_output_norm,
+                d_output_norm ? d_output : nullptr, nin.eps, strm);
   if (rc != HP_OK) return rc;
   return HP_OK;
 }

@@ -165,7 +165,10 @@ __global__ __launch_bounds__(64) void qkv_post_kernel(const QkvPostArgs a) {
     kind = 2;
     head = h - a.nq - a.nkv;
   }
-  const float *src = (kind == 0 ? a.q : kind == 1 ? a.k : a.v) + (size_t)head * kHeadDim;
+  const int t = blockIdx.y;  // token: position *a.position + t
+  const size_t qrow = (size_t)t * a.nq, kvrow = (size_t)t * a.nkv;
+  const float *src = kind == 0 ? a.q + (qrow + head) * kHeadDim
+                               : (kind == 1 ? a.k : a.v) + (kvrow + head) * kHeadDim;
   const float *w = kind == 0 ? a.wq : kind == 1 ? a.wk : nullptr;
   float x[4];
   double s = 0.0;
@@ -181,7 +184,7 @@ __global__ __launch_bounds__(64) void qkv_post_kernel(const QkvPostArgs a) {
     xs[i] = w ? (float)(((double)x[j] * sc) * (double)w[i]) : (float)((double)x[j] * sc);
   }
   __syncthreads();
-  const int pos = *a.position;
+  const int pos = *a.position + t;
   if (kind != 2) {
     const int half = a.rope_dims >> 1;
     float r0[2], r1[2];
@@ -190,10 +193,18 @@ __global__ __launch_bounds__(64) void qkv_post_kernel(const QkvPostArgs a) {
       const int i = lane + 64 * p;
       r0[p] = r1[p] = 0.0f;
       if (i < half) {
-        double theta = (double)pos;
-        for (int it = 0; it < i; it++) theta = (double)(float)(theta * a.theta_scale);
-        const double ang = a.freq_factors ? theta / (double)a.freq_factors[i] : theta;
-        const double c = cos(ang), sn = sin(ang);
+        double c, sn;
+        if (a.rope_table_mode == 2) {
+          const double2 e = a.rope_table[t * (kHeadDim / 2) + i];
+          c = e.x;
+          sn = e.y;
+        } else {
+          double theta = (double)pos;
+          for (int it = 0; it < i; it++) theta = (double)(float)(theta * a.theta_scale);
+          const double ang = a.freq_factors ? theta / (double)a.freq_factors[i] : theta;
+          sincos(ang, &sn, &c);
+          if (a.rope_table_mode == 1 && h == 0) a.rope_table[t * (kHeadDim / 2) + i] = make_double2(c, sn);
+        }
         const double x0 = xs[i], x1 = xs[i + half];
         r0[p] = (float)(x0 * c) - (float)(x1 * sn);
         r1[p] = (float)(x0 * sn) + (float)(x1 * c);
@@ -212,7 +223,7 @@ __global__ __launch_bounds__(64) void qkv_post_kernel(const QkvPostArgs a) {
   }
   if (kind == 0) {
 #pragma unroll
-    for (int j = 0; j < 4; j++) a.q_out[(size_t)head * kHeadDim + lane + 64 * j] = xs[lane + 64 * j];
+    for (int j = 0; j < 4; j++) a.q_out[(qrow + head) * kHeadDim + lane + 64 * j] = xs[lane + 64 * j];
   } else if (pos >= 0) {  // a negative position (invalid) writes no cache entry
     const int slot = pos % a.capacity;
     _Float16 *dst = (kind == 1 ? a.k_cache : a.v_cache) + ((size_t)head * a.capacity + slot) * kHeadDim;
@@ -277,7 +288,12 @@ __global__ __launch_bounds__(256) void attn_partial_kernel(const AttnArgs a) {
         if (lane + 64 * p < half) tab[p] = a.rope_table[lane + 64 * p];
     }
   }
-  const int pos = *a.position;
+  // tokens at *a.position .. + a.tokens - 1 share the window of the last
+  // (attentionRange of the largest position); token blockIdx.z sees the keys
+  // up to its own position (causalMask)
+  const int tok = blockIdx.z;
+  const int pos = *a.position + (a.tokens - 1);
+  const int pos_t = pos - (a.tokens - 1) + tok;
 
   const int kj = tid >> 3, kp = tid & 7;
   const int kslot = c * kAttnChunk + kj;
@@ -297,10 +313,11 @@ __global__ __launch_bounds__(256) void attn_partial_kernel(const AttnArgs a) {
   int start, count;
   window_of(pos, cap, a.window, &start, &count);
   const int s0 = pos < 0 ? 0 : start % cap;
+  const int last_w = pos_t - start;  // window index of the token's own position
   auto in_window = [&](int slot) {
     int w = slot - s0;  // window index of the slot (both in [0, cap))
     w += w < 0 ? cap : 0;
-    return pos >= 0 && slot < cap && w < count;
+    return pos >= 0 && slot < cap && w < count && w <= last_w;
   };
   const int new_slot = pos < 0 ? -1 : pos % cap;
 
@@ -379,7 +396,7 @@ __global__ __launch_bounds__(256) void attn_partial_kernel(const AttnArgs a) {
     }
   } else {
     for (int idx = tid; idx < G * kHeadDim; idx += 256)
-      xs[idx >> 8][idx & 255] = rs_f16_round(a.q[(size_t)g * G * kHeadDim + idx]);
+      xs[idx >> 8][idx & 255] = rs_f16_round(a.q[((size_t)tok * a.nq + g * G) * kHeadDim + idx]);
     __syncthreads();
   }
 
@@ -446,7 +463,7 @@ __global__ __launch_bounds__(256) void attn_partial_kernel(const AttnArgs a) {
       l += __shfl_xor(l, 16);
       sc[h][j] = p;
       if (j == 0) {
-        const size_t base = ((size_t)g * a.chunks + c) * kAttnMaxGroup + h;
+        const size_t base = (((size_t)tok * a.nkv + g) * a.chunks + c) * kAttnMaxGroup + h;
         a.part_m[base] = m;
         a.part_l[base] = l;
       }
@@ -484,7 +501,8 @@ __global__ __launch_bounds__(256) void attn_partial_kernel(const AttnArgs a) {
   for (int idx = tid; idx < G * (kHeadDim / 4); idx += 256) {
     const int h = idx >> 6, d4 = idx & 63;
     const float4 r0 = red[0][h][d4], r1 = red[1][h][d4], r2 = red[2][h][d4], r3 = red[3][h][d4];
-    *reinterpret_cast<float4 *>(&a.part_o[(((size_t)g * a.chunks + c) * kAttnMaxGroup + h) * kHeadDim + 4 * d4]) =
+    *reinterpret_cast<float4 *>(
+        &a.part_o[((((size_t)tok * a.nkv + g) * a.chunks + c) * kAttnMaxGroup + h) * kHeadDim + 4 * d4]) =
         make_float4((r0.x + r1.x) + (r2.x + r3.x), (r0.y + r1.y) + (r2.y + r3.y), (r0.z + r1.z) + (r2.z + r3.z),
                     (r0.w + r1.w) + (r2.w + r3.w));
   }
@@ -518,7 +536,8 @@ __global__ __launch_bounds__(256) void attn_reduce_kernel(const AttnArgs a) {
   const int qh = blockIdx.x, tid = threadIdx.x;
   const int group = a.nq / a.nkv, g = qh / group, h = qh % group;
   const int chunks = a.chunks;
-  const size_t row0 = (size_t)g * a.chunks * kAttnMaxGroup + h;  // chunk c at row0 + c * kAttnMaxGroup
+  const int tok = blockIdx.z;
+  const size_t row0 = ((size_t)tok * a.nkv + g) * a.chunks * kAttnMaxGroup + h;  // chunk c at row0 + c * kAttnMaxGroup
   const int d = blockIdx.y * 64 + (tid & 63), cg = tid >> 6;
   float m = -__builtin_inff();
   for (int c = tid; c < chunks; c += 256) m = fmaxf(m, a.part_m[row0 + (size_t)c * kAttnMaxGroup]);
@@ -552,7 +571,7 @@ __global__ __launch_bounds__(256) void attn_reduce_kernel(const AttnArgs a) {
   __syncthreads();
   if (tid < 64) {
     const float oo = (red[0][tid] + red[1][tid]) + (red[2][tid] + red[3][tid]);
-    a.out[(size_t)qh * kHeadDim + d] = l > 0.0f ? ts_f16_round(oo / l) : 0.0f;  // l == 0: no key (position < 0)
+    a.out[((size_t)tok * a.nq + qh) * kHeadDim + d] = l > 0.0f ? ts_f16_round(oo / l) : 0.0f;  // l == 0: no key
   }
 }
 
@@ -567,26 +586,28 @@ hipError_t launch_norm_residual(const NormArgs &a, hipStream_t s) {
 hipError_t launch_qkv_post(const QkvPostArgs &a, hipStream_t s) {
   if (a.nq < 1 || a.nkv < 1 || a.capacity < 1 || a.rope_dims < 0 || a.rope_dims > kHeadDim || (a.rope_dims & 1))
     return hipErrorInvalidValue;
-  hipLaunchKernelGGL(qkv_post_kernel, dim3(a.nq + 2 * a.nkv), dim3(64), 0, s, a);
+  if (a.tokens < 1 || a.tokens > kMaxTokens) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(qkv_post_kernel, dim3(a.nq + 2 * a.nkv, a.tokens), dim3(64), 0, s, a);
   return hipGetLastError();
 }
 
 int attn_max_chunks(int capacity) { return (capacity + kAttnChunk - 1) / kAttnChunk; }
 
-size_t attn_partial_floats(int nkv, int capacity) {
-  return (size_t)nkv * attn_max_chunks(capacity) * kAttnMaxGroup * (kHeadDim + 2);
+size_t attn_partial_floats(int nkv, int capacity, int tokens) {
+  return (size_t)tokens * nkv * attn_max_chunks(capacity) * kAttnMaxGroup * (kHeadDim + 2);
 }
 
 hipError_t launch_attention(AttnArgs a, float *partials, hipStream_t s) {
   if (a.nkv < 1 || a.nq % a.nkv != 0 || a.nq / a.nkv > kAttnMaxGroup || a.capacity < 1 || a.window < 0 ||
-      a.rope_dims < 0 || a.rope_dims > kHeadDim || (a.rope_dims & 1))
+      a.rope_dims < 0 || a.rope_dims > kHeadDim || (a.rope_dims & 1) || a.tokens < 1 || a.tokens > kMaxTokens ||
+      (a.prep && a.tokens != 1))
     return hipErrorInvalidValue;
   a.chunks = attn_max_chunks(a.capacity);
-  const size_t slots = (size_t)a.nkv * a.chunks * kAttnMaxGroup;
+  const size_t slots = (size_t)a.tokens * a.nkv * a.chunks * kAttnMaxGroup;
   a.part_m = partials;
   a.part_l = partials + slots;
   a.part_o = partials + 2 * slots;
-  const dim3 grid(a.chunks, a.nkv);
+  const dim3 grid(a.chunks, a.nkv, a.tokens);
   switch (a.nq / a.nkv) {
     case 1: hipLaunchKernelGGL(attn_partial_kernel<1>, grid, dim3(256), 0, s, a); break;
     case 2: hipLaunchKernelGGL(attn_partial_kernel<2>, grid, dim3(256), 0, s, a); break;
@@ -599,7 +620,7 @@ hipError_t launch_attention(AttnArgs a, float *partials, hipStream_t s) {
   }
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
-  hipLaunchKernelGGL(attn_reduce_kernel, dim3(a.nq, kHeadDim / 64), dim3(256), 0, s, a);
+  hipLaunchKernelGGL(attn_reduce_kernel, dim3(a.nq, kHeadDim / 64, a.tokens), dim3(256), 0, s, a);
   return hipGetLastError();
 }
 

@@ -175,6 +175,7 @@ hipError_t launch_geglu(const float *gate, const float *up, size_t n, double c, 
 constexpr int kHeadDim = 256;
 constexpr int kAttnChunk = 32;    // cache slots per attention workgroup
 constexpr int kAttnMaxGroup = 8;  // query heads per kv head
+constexpr int kMaxTokens = 8;     // tokens per decode call (a draft to verify)
 
 // Per row of [rows][n] (n <= 4096): x_res == null: next_out = rmsnorm(y) *
 // w_next.  Otherwise x_out = f32(f32(x_res + rmsnorm(y) * w_post) * scale)
@@ -194,7 +195,10 @@ struct QkvPostArgs {
   const int *position;
   float *q_out;
   _Float16 *k_cache, *v_cache;  // [nkv][capacity][kHeadDim]
+  double2 *rope_table;  // [tokens][kHeadDim / 2] cos, sin (rope_table_mode 1: written, 2: read)
+  int rope_table_mode;
   int nq, nkv, capacity, rope_dims;
+  int tokens;          // token t at position *position + t; rows [t][heads][kHeadDim]
   double theta_scale;  // base^(-2 / rope_dims)
   double eps;
 };
@@ -211,13 +215,14 @@ struct AttnArgs {
   float *part_m, *part_l, *part_o;  // set by launch_attention
   double2 *rope_table;  // [kHeadDim / 2] cos, sin (rope_table_mode 1: written, 2: read)
   int nq, nkv, capacity, window, chunks, rope_dims, prep, rope_table_mode;
+  int tokens;  // prep == 0: queries of tokens *position .. + tokens - 1, rows [t][nq][kHeadDim]
   double theta_scale, eps;
 };
 hipError_t launch_norm_residual(const NormArgs &a, hipStream_t s);
 hipError_t launch_qkv_post(const QkvPostArgs &a, hipStream_t s);
 // partials: attn_partial_floats(nkv, capacity) floats of device scratch
 // (a.rope_table, when used, lives elsewhere).
-size_t attn_partial_floats(int nkv, int capacity);
+size_t attn_partial_floats(int nkv, int capacity, int tokens);
 hipError_t launch_attention(AttnArgs a, float *partials, hipStream_t s);
 hipError_t launch_dequantize(int type, const uint8_t *tiles, const uint16_t *dplane, int rows,
                              const TileGeom &g, int row_start, int row_count, float *out, hipStream_t s);

@@ -129,11 +129,13 @@ class HipDecodeModel:
         """The layer structs as one C array (read by the call, not kept)."""
         return (H.HipDecodeLayer * len(self.layers))(*self.layers)
 
-    def run_layers(self, d_hidden: int, d_position: int, d_normed: int = 0, stream: int = 0) -> None:
-        """Every layer on d_hidden (in place); the output norm into d_normed."""
+    def run_layers(self, d_hidden: int, d_position: int, d_normed: int = 0, stream: int = 0,
+                   tokens: int = 1) -> None:
+        """Every layer on d_hidden ([tokens][hidden], in place) for the tokens
+        at *d_position + t; the output norm into d_normed."""
         arr = self.layers_array()
         onorm = self.output_norm.data_ptr() if (d_normed and self.output_norm is not None) else 0
-        H.assertHipOk(H.lib().hp_hip_decode_layers_device(arr, len(self.layers), d_hidden, d_position,
+        H.assertHipOk(H.lib().hp_hip_decode_layers_device(arr, len(self.layers), tokens, d_hidden, d_position,
                                                           onorm or None, d_normed if onorm else None,
                                                           stream or None), "decode_layers")
 

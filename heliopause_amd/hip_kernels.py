@@ -135,9 +135,9 @@ def _declare_decode(L: ctypes.CDLL) -> None:
     L.hp_hip_rms_norm_device.argtypes = [vp, _sz, _sz, vp, ctypes.c_double, vp, vp]
     L.hp_hip_residual_norm_device.argtypes = [vp, _sz, _sz, vp, vp, ctypes.c_float, vp, vp, vp, ctypes.c_double,
                                               vp]
-    L.hp_hip_attention_prep_device.argtypes = [cfg, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp]
-    L.hp_hip_gqa_attention_device.argtypes = [cfg, vp, vp, vp, vp, vp, vp]
-    L.hp_hip_decode_layers_device.argtypes = [ctypes.POINTER(HipDecodeLayer), _sz, vp, vp, vp, vp, vp]
+    L.hp_hip_attention_prep_device.argtypes = [cfg, _sz, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp]
+    L.hp_hip_gqa_attention_device.argtypes = [cfg, _sz, vp, vp, vp, vp, vp, vp]
+    L.hp_hip_decode_layers_device.argtypes = [ctypes.POINTER(HipDecodeLayer), _sz, _sz, vp, vp, vp, vp, vp]
     for name in ("hp_hip_rms_norm_device", "hp_hip_residual_norm_device", "hp_hip_attention_prep_device",
                  "hp_hip_gqa_attention_device", "hp_hip_decode_layers_device"):
         getattr(L, name).restype = i32
@@ -597,26 +597,28 @@ def residual_norm_device(d_branch: int, rows: int, n: int, d_post_weight: int, d
 
 def attention_prep_device(config: HipAttentionConfig, d_q: int, d_k: int, d_v: int, d_q_norm: int, d_k_norm: int,
                           d_position: int, d_q_out: int, d_key_cache: int, d_value_cache: int,
-                          stream: int = 0) -> None:
-    """q/k head norms + RoPE, v norm, and the KV-cache append at *d_position."""
-    assertHipOk(lib().hp_hip_attention_prep_device(ctypes.byref(config), d_q, d_k, d_v or None, d_q_norm, d_k_norm,
-                                                   d_position, d_q_out, d_key_cache, d_value_cache,
+                          stream: int = 0, token_count: int = 1) -> None:
+    """q/k head norms + RoPE, v norm, and the KV-cache append of tokens at
+    *d_position + t."""
+    assertHipOk(lib().hp_hip_attention_prep_device(ctypes.byref(config), token_count, d_q, d_k, d_v or None, d_q_norm,
+                                                   d_k_norm, d_position, d_q_out, d_key_cache, d_value_cache,
                                                    stream or None), "attention_prep")
 
 
 def gqa_attention_device(config: HipAttentionConfig, d_q: int, d_key_cache: int, d_value_cache: int,
-                         d_position: int, d_output: int, stream: int = 0) -> None:
-    """GQA attention of the token at *d_position over its window, output f16-rounded."""
-    assertHipOk(lib().hp_hip_gqa_attention_device(ctypes.byref(config), d_q, d_key_cache, d_value_cache,
-                                                  d_position, d_output, stream or None), "gqa_attention")
+                         d_position: int, d_output: int, stream: int = 0, token_count: int = 1) -> None:
+    """GQA attention of the tokens at *d_position + t (causal), output f16-rounded."""
+    assertHipOk(lib().hp_hip_gqa_attention_device(ctypes.byref(config), token_count, d_q, d_key_cache,
+                                                  d_value_cache, d_position, d_output, stream or None),
+                "gqa_attention")
 
 
 def decode_layers_device(layers: Sequence[HipDecodeLayer], d_hidden: int, d_position: int,
-                         d_output_norm: int = 0, d_output: int = 0, stream: int = 0):
-    """forwardAttentionLayer for one token through ``layers`` (hidden in place),
-    then the final norm into d_output when d_output_norm is given.  Returns the
-    ctypes array passed (keep it alive while a captured graph may replay)."""
+                         d_output_norm: int = 0, d_output: int = 0, stream: int = 0, token_count: int = 1) -> None:
+    """forwardAttentionLayer for the tokens at *d_position + t through
+    ``layers`` (hidden [token][hidden] in place), then the final norm into
+    d_output when d_output_norm is given."""
     arr = (HipDecodeLayer * len(layers))(*layers)
-    assertHipOk(lib().hp_hip_decode_layers_device(arr, len(layers), d_hidden, d_position, d_output_norm or None,
-                                                  d_output or None, stream or None), "decode_layers")
-    return arr
+    assertHipOk(lib().hp_hip_decode_layers_device(arr, len(layers), token_count, d_hidden, d_position,
+                                                  d_output_norm or None, d_output or None, stream or None),
+                "decode_layers")

@@ -289,24 +289,27 @@ int32_t hp_hip_residual_norm_device(const float *d_branch, size_t rows, size_t n
                                     const float *d_next_weight, float *d_next_out, double epsilon,
                                     void *stream);
 
-/* Attention prologue of one token (layers.ts:205-268, as the WebGPU runner
- * fuses it, shaders.ts:1306-1385): q = ropeNeox(normHeads(d_q, d_q_norm)) ->
- * d_q_out [head_count][256]; k = ropeNeox(normHeads(d_k, d_k_norm)) and v =
- * rmsNormRowsNoWeight(d_v) appended to the caches at slot position %
- * capacity (updateFullAttentionCache, layers.ts:887-911).  d_v NULL: the
- * value shares the key projection (layerValueProjectionModes
- * "shared-with-key", layers.ts:231-238). */
-int32_t hp_hip_attention_prep_device(const hp_hip_attention_config_t *config, const float *d_q, const float *d_k,
-                                     const float *d_v, const float *d_q_norm, const float *d_k_norm,
-                                     const int32_t *d_position, float *d_q_out, uint16_t *d_key_cache,
-                                     uint16_t *d_value_cache, void *stream);
+/* Attention prologue (layers.ts:205-268, as the WebGPU runner fuses it,
+ * shaders.ts:1306-1385) of token_count (1..8) tokens at positions
+ * *d_position + t: q = ropeNeox(normHeads(d_q, d_q_norm)) -> d_q_out
+ * [token][head_count][256]; k = ropeNeox(normHeads(d_k, d_k_norm)) and v =
+ * rmsNormRowsNoWeight(d_v) ([token][head_count_kv][256]) appended to the
+ * caches at slot position % capacity (updateFullAttentionCache,
+ * layers.ts:887-911).  d_v NULL: the value shares the key projection
+ * (layerValueProjectionModes "shared-with-key", layers.ts:231-238). */
+int32_t hp_hip_attention_prep_device(const hp_hip_attention_config_t *config, size_t token_count, const float *d_q,
+                                     const float *d_k, const float *d_v, const float *d_q_norm,
+                                     const float *d_k_norm, const int32_t *d_position, float *d_q_out,
+                                     uint16_t *d_key_cache, uint16_t *d_value_cache, void *stream);
 
-/* GQA decode attention of one token over its window of the caches
- * (attentionRange, layers.ts:972-980) as hp_gqa_attention_f32
- * (packages/engine/wasm-kernels/src/lib.rs:538-654) computes it with scale 1
- * and an f16-rounded query, followed by castF16Rows (layers.ts:982-988):
- * d_output [head_count][256]. */
-int32_t hp_hip_gqa_attention_device(const hp_hip_attention_config_t *config, const float *d_q,
+/* GQA attention of token_count (1..8) tokens at positions *d_position + t
+ * over the caches, as forwardAttentionLayer runs it (layers.ts:270-335): the
+ * window is attentionRange of the largest position (972-980), each token
+ * sees the keys up to its own position (causalMask, 913-925), scores and
+ * softmax as hp_gqa_attention_f32 (packages/engine/wasm-kernels/src/
+ * lib.rs:538-654) with scale 1 and an f16-rounded query, then castF16Rows
+ * (layers.ts:982-988).  d_q and d_output are [token][head_count][256]. */
+int32_t hp_hip_gqa_attention_device(const hp_hip_attention_config_t *config, size_t token_count, const float *d_q,
                                     const uint16_t *d_key_cache, const uint16_t *d_value_cache,
                                     const int32_t *d_position, float *d_output, void *stream);
 
@@ -324,19 +327,24 @@ typedef struct hp_hip_decode_layer {
   hp_hip_attention_config_t attention;
 } hp_hip_decode_layer_t;
 
-/* forwardAttentionLayer (layers.ts:161-379, with forwardFfn 418-473) for one
- * token through layers[0 .. layer_count): d_hidden [hidden] is the residual
- * stream, updated in place.  When d_output_norm is not NULL, d_output =
- * rmsNormRows(hidden, d_output_norm) (forwardOutput's final norm,
- * layers.ts:389-396), ready for the output head.  Per layer: Q/K/V in one
- * matvec launch, the attention prologue, attention (two launches), O, the
- * post-attention residual fused with ffn_norm, gate/up + GeGLU, down, and the
- * post-FFN residual with the layer scale fused with the next layer's
- * attn_norm.  Per-layer input embeddings (applyPerLayerInput) are not part
- * of this path. */
-int32_t hp_hip_decode_layers_device(const hp_hip_decode_layer_t *layers, size_t layer_count, float *d_hidden,
-                                    const int32_t *d_position, const float *d_output_norm, float *d_output,
-                                    void *stream);
+/* forwardAttentionLayer (layers.ts:161-379, with forwardFfn 418-473) for
+ * token_count (1..8) tokens at positions *d_position + t through
+ * layers[0 .. layer_count): d_hidden [token][hidden] is the residual stream,
+ * updated in place; every token's row is kept (a draft being verified needs
+ * each position's logits, as the WebGPU MTP target runner reads all hidden
+ * rows, mtp-target-runner.ts:80-130).  When d_output_norm is not NULL,
+ * d_output [token][hidden] = rmsNormRows(hidden, d_output_norm)
+ * (forwardOutput's final norm, layers.ts:389-396), ready for the output head.
+ * Per layer (one token): Q/K/V in one matvec launch whose prologue forms
+ * attn_norm of the residual, attention with the head norms, RoPE and the
+ * cache append inside it plus the merge, O, gate/up + GeGLU whose prologue
+ * forms the post-attention residual and ffn_norm, down.  Several tokens add a
+ * prologue launch (norms, RoPE, every token's cache append) before the
+ * attention, and the norms run as their own launches.  Per-layer input
+ * embeddings (applyPerLayerInput) are not part of this path. */
+int32_t hp_hip_decode_layers_device(const hp_hip_decode_layer_t *layers, size_t layer_count, size_t token_count,
+                                    float *d_hidden, const int32_t *d_position, const float *d_output_norm,
+                                    float *d_output, void *stream);
 
 #ifdef __cplusplus
 }

@@ -1,11 +1,13 @@
-"""CPU restatement of one decoder layer for one decode token.
+"""CPU restatement of one decoder layer for the tokens of one decode call
+(one token, or a draft of up to eight being verified).
 
 TEST INFRASTRUCTURE ONLY: this module is the checker.  Only tests/,
 ``__graft_entry__.smoke()`` and ``bench.py``'s ``cpu_baseline`` leg may
 import it; the HIP product path never does.
 
 Follows forwardAttentionLayer (packages/engine/src/runner/wasm/layers.ts:
-161-379) and forwardFfn (418-473) for tokenCount = 1 with causal attention:
+161-379) and forwardFfn (418-473) with causal attention, keeping every
+token's row:
 the element-wise steps are the C restatements in hp_oracle.c
 (hpo_rms_norm_vector, hpo_rope_neox, hpo_gqa_attention_f32,
 hpo_cast_f16_rows, hpo_residual_add) and the projections the oracle's
@@ -126,22 +128,28 @@ def gqa_attention_f32(query, key, value, *, head_size, query_heads, kv_heads, to
 
 
 def decode_attention(q, key_cache, value_cache, position: int, window: int = 0) -> np.ndarray:
-    """Attention of one token (q [nq][256] after RoPE) over f16 caches
-    [nkv][capacity][256], as forwardAttentionLayer runs it (layers.ts:270-
-    335): window from attentionRange, causal mask, scale 1, f16 query, then
-    castF16Rows.  Returns [nq][256]."""
+    """Attention of tokens at position .. position + T - 1 (q [T][nq][256], or
+    [nq][256] for one token, after RoPE) over f16 caches [nkv][capacity][256]
+    that already hold every token, as forwardAttentionLayer runs it
+    (layers.ts:270-335): one window, attentionRange of the largest position;
+    causalMask per token; scale 1; f16 query; then castF16Rows."""
+    q = _f(q)
+    one = q.ndim == 2
+    qq = q[None] if one else q
+    tokens, nq, _ = qq.shape
     nkv, cap, hd = key_cache.shape
-    nq = q.shape[0]
-    start, count = attention_range(position, cap, window)
+    start, count = attention_range(position + tokens - 1, cap, window)
     key = np.ascontiguousarray(key_cache.astype(np.float32).transpose(1, 0, 2))      # [slot][head][dim]
     value = np.ascontiguousarray(value_cache.astype(np.float32).transpose(2, 0, 1))  # [dim][head][slot]
-    # causalMask (layers.ts:913-925): key position start + j <= position
-    mask = np.where(start + np.arange(count) <= position, 0.0, -np.inf).astype(np.float32)
-    rc, out = gqa_attention_f32(q, key, value, head_size=hd, query_heads=nq, kv_heads=nkv, token_count=1,
+    # causalMask (layers.ts:913-925): key position start + j <= the token's position
+    kpos = start + np.arange(count)
+    mask = np.stack([np.where(kpos <= position + t, 0.0, -np.inf) for t in range(tokens)]).astype(np.float32)
+    rc, out = gqa_attention_f32(qq, key, value, head_size=hd, query_heads=nq, kv_heads=nkv, token_count=tokens,
                                 kv_count=count, kv_start=start, capacity=cap, mask=mask)
     if rc != O.OK:
         raise ValueError(f"attention status {rc}")
-    return cast_f16_rows(out).reshape(nq, hd)
+    out = cast_f16_rows(out).reshape(tokens, nq, hd)
+    return out[0] if one else out
 
 
 @dataclass
@@ -164,17 +172,26 @@ class Layer:
 
 
 def _proj(layer: Layer, names, x) -> list:
+    """Projections of the columns x [T][k]: outputs [T][rows] each."""
     specs = [layer.weights[n] for n in names]
-    return [o.reshape(-1) for o in O.matmul_multi([t for t, _, _ in specs], [w for _, w, _ in specs],
-                                                  _f(x).reshape(1, -1), [r for _, _, r in specs], threads=8)]
+    xx = _f(x)
+    xx = xx.reshape(-1, xx.shape[-1])
+    return O.matmul_multi([t for t, _, _ in specs], [w for _, w, _ in specs], xx, [r for _, _, r in specs],
+                          threads=8)
 
 
 def forward_layer(layer: Layer, hidden, position: int) -> np.ndarray:
-    """forwardAttentionLayer + forwardFfn + layer output scale for one token
-    at ``position``; appends the token's key and value to the caches."""
+    """forwardAttentionLayer + forwardFfn + layer output scale for the tokens
+    at position .. position + T - 1 (hidden [T][n], or [n] for one token);
+    appends every token's key and value to the caches.  Every token's row is
+    returned."""
     eps, hd = layer.epsilon, HEAD_DIM
     nq, nkv = layer.head_count, layer.head_count_kv
-    x = _f(hidden).reshape(-1)
+    x0 = _f(hidden)
+    one = x0.ndim == 1
+    x = x0.reshape(-1, x0.shape[-1])
+    tokens = x.shape[0]
+    positions = np.arange(position, position + tokens, dtype=np.int32)
     t = layer.trace
     t["attn_norm"] = xn = rms_norm_rows(x, layer.norms["attn_norm"], eps)
     shared = "attn_v" not in layer.weights
@@ -182,24 +199,26 @@ def forward_layer(layer: Layer, hidden, position: int) -> np.ndarray:
     q, k = outs[0], outs[1]
     v = k if shared else outs[2]
     t["q"], t["k"], t["v"] = q, k, v
-    qn = rms_norm_rows(q.reshape(nq, hd), layer.norms["attn_q_norm"], eps)
-    qr = rope_neox(qn, [position], layer.rope_dims, layer.rope_freq_base, layer.rope_freq_factors)
-    kn = rms_norm_rows(k.reshape(nkv, hd), layer.norms["attn_k_norm"], eps)
-    vn = rms_norm_rows(v.reshape(nkv, hd), None, eps)
-    kr = rope_neox(kn, [position], layer.rope_dims, layer.rope_freq_base, layer.rope_freq_factors)
-    slot = position % layer.key_cache.shape[1]
-    layer.key_cache[:, slot, :] = kr.astype(np.float16)
-    layer.value_cache[:, slot, :] = vn.astype(np.float16)
+    qn = rms_norm_rows(q.reshape(tokens, nq, hd), layer.norms["attn_q_norm"], eps)
+    qr = rope_neox(qn, positions, layer.rope_dims, layer.rope_freq_base, layer.rope_freq_factors)
+    kn = rms_norm_rows(k.reshape(tokens, nkv, hd), layer.norms["attn_k_norm"], eps)
+    vn = rms_norm_rows(v.reshape(tokens, nkv, hd), None, eps)
+    kr = rope_neox(kn, positions, layer.rope_dims, layer.rope_freq_base, layer.rope_freq_factors)
+    for i, p in enumerate(positions):  # updateFullAttentionCache
+        slot = int(p) % layer.key_cache.shape[1]
+        layer.key_cache[:, slot, :] = kr[i].astype(np.float16)
+        layer.value_cache[:, slot, :] = vn[i].astype(np.float16)
     t["q_rope"] = qr
     t["attention"] = att = decode_attention(qr, layer.key_cache, layer.value_cache, position, layer.sliding_window)
-    t["o"] = o = _proj(layer, ["attn_output"], att.reshape(-1))[0]
+    t["o"] = o = _proj(layer, ["attn_output"], att.reshape(tokens, -1))[0]
     t["x1"] = x1 = residual_add(x, rms_norm_rows(o, layer.norms["post_attention_norm"], eps))
     t["ffn_norm"] = xn2 = rms_norm_rows(x1, layer.norms["ffn_norm"], eps)
     gate, up = _proj(layer, ["ffn_gate", "ffn_up"], xn2)
     t["ffn_hidden"] = h = O.geglu(gate, up)
     t["down"] = y = _proj(layer, ["ffn_down"], h)[0]
     x2 = residual_add(x1, rms_norm_rows(y, layer.norms["post_ffw_norm"], eps))
-    return (x2.astype(np.float64) * np.float64(np.float32(layer.output_scale))).astype(np.float32)
+    out = (x2.astype(np.float64) * np.float64(np.float32(layer.output_scale))).astype(np.float32)
+    return out[0] if one else out
 
 
 def rope_theta_table(position: int, n_dims: int, freq_base: float) -> np.ndarray:

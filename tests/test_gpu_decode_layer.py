@@ -349,3 +349,99 @@ def test_decode_layer_rejects_bad_shapes(hip):
             model.run_layers(dx.data_ptr(), dpos.data_ptr())
     finally:
         model.release()
+
+
+@pytest.mark.parametrize("tokens,cap,pos,window,qscale", [(3, 4096, 4094, 0, 0.25), (4, 64, 70, 0, 1.0),
+                                                          (8, 4096, 100, 0, 0.0625), (2, 4096, 3000, 512, 0.25),
+                                                          (5, 40, 2, 0, 0.25)])
+def test_draft_attention_prep_and_attention(hip, D, tokens, cap, pos, window, qscale):
+    """Several tokens (a draft): every token's key and value appended at its
+    own slot, then each token attends causally within the shared window."""
+    import torch
+
+    nq, nkv = 8, 2
+    rng = np.random.default_rng(tokens * 1000 + cap + pos)
+    q = (rng.standard_normal((tokens, nq, 256)) * 2).astype(np.float32)
+    k = (rng.standard_normal((tokens, nkv, 256)) * 2).astype(np.float32)
+    v = (rng.standard_normal((tokens, nkv, 256)) * 2).astype(np.float32)
+    wq = (qscale * (1 + 0.1 * rng.standard_normal(256))).astype(np.float32)
+    wk = (1 + 0.1 * rng.standard_normal(256)).astype(np.float32)
+    kc = rng.standard_normal((nkv, cap, 256)).astype(np.float16)
+    vc = rng.standard_normal((nkv, cap, 256)).astype(np.float16)
+    dkc, dvc = _dev(kc.view(np.int16)), _dev(vc.view(np.int16))
+    dq, dk, dv, dwq, dwk = _dev(q), _dev(k), _dev(v), _dev(wq), _dev(wk)
+    dpos = _dev(np.array([pos], np.int32))
+    qo = torch.empty(tokens * nq * 256, dtype=torch.float32, device="cuda:0")
+    out = torch.empty(tokens * nq * 256, dtype=torch.float32, device="cuda:0")
+    cfg = H.attention_config(nq, nkv, cap, sliding_window=window)
+    print(f"draft attention tokens={tokens} cap={cap} pos={pos} window={window}", flush=True)
+    H.attention_prep_device(cfg, dq.data_ptr(), dk.data_ptr(), dv.data_ptr(), dwq.data_ptr(), dwk.data_ptr(),
+                            dpos.data_ptr(), qo.data_ptr(), dkc.data_ptr(), dvc.data_ptr(), token_count=tokens)
+    H.gqa_attention_device(cfg, qo.data_ptr(), dkc.data_ptr(), dvc.data_ptr(), dpos.data_ptr(), out.data_ptr(),
+                           token_count=tokens)
+    torch.cuda.synchronize()
+    positions = np.arange(pos, pos + tokens)
+    qr = D.rope_neox(D.rms_norm_rows(q, wq, 1e-6), positions, 256, 10000.0)
+    kr = D.rope_neox(D.rms_norm_rows(k, wk, 1e-6), positions, 256, 10000.0)
+    vn = D.rms_norm_rows(v, None, 1e-6)
+    rk, rv = kc.copy(), vc.copy()
+    for t, p_ in enumerate(positions):
+        rk[:, p_ % cap] = kr[t].astype(np.float16)
+        rv[:, p_ % cap] = vn[t].astype(np.float16)
+    assert _ulps(qo.cpu().numpy().reshape(tokens, nq, 256), qr).max() <= 1
+    gk = dkc.cpu().numpy().view(np.float16)
+    gv = dvc.cpu().numpy().view(np.float16)
+    assert _f16_steps(gk, rk).max() <= 1 and _f16_steps(gv, rv).max() <= 1
+    ref = D.decode_attention(qo.cpu().numpy().reshape(tokens, nq, 256), gk, gv, pos, window)
+    got = out.cpu().numpy().reshape(tokens, nq, 256)
+    errs = [_rel(got[t, h], ref[t, h]) for t in range(tokens) for h in range(nq)]
+    steps = _f16_steps(got, ref)
+    print(f"max rel err {max(errs):.2e}, elements off {np.count_nonzero(steps)}", flush=True)
+    assert max(errs) <= 2.0 ** -8
+    assert np.count_nonzero(steps) <= 0.03 * steps.size
+
+
+@pytest.mark.parametrize("full,tokens,pos", [(True, 4, 4093), (False, 3, 62), (False, 8, 0)],
+                         ids=["model-draft4", "small-wrap-draft3", "small-start-draft8"])
+def test_decode_draft_matches_oracle(hip, D, full, tokens, pos):
+    """A draft of several tokens through one layer (every row kept)."""
+    import torch
+
+    shape = DM.ModelShape() if full else _small_shape()
+    seed = S.derive(S.BASE_SEED, "decode-draft", full, tokens, pos)
+    data = DM.layer_host_data(shape, seed, 0)
+    model = DM.HipDecodeModel(shape)
+    model.add_layer(data)
+    x = S.activations(S.derive(seed, "x"), tokens, shape.hidden) * 4
+    dx = _dev(x)
+    dpos = _dev(np.array([pos], np.int32))
+    print(f"decode draft hidden={shape.hidden} tokens={tokens} pos={pos}", flush=True)
+    try:
+        model.run_layers(dx.data_ptr(), dpos.data_ptr(), tokens=tokens)
+        torch.cuda.synchronize()
+        got = dx.cpu().numpy().reshape(tokens, shape.hidden)
+        gk = model.caches[0][0].cpu().numpy().view(np.float16)
+    finally:
+        model.release()
+    ol = _oracle_layer(D, shape, data)
+    ref = D.forward_layer(ol, x, pos)
+    errs = [_rel(got[t], ref[t]) for t in range(tokens)]
+    print(f"draft max rel err {max(errs):.3e}; identical {np.mean(got == ref):.4f}", flush=True)
+    assert max(errs) <= LAYER_TOL
+    assert _f16_steps(gk, ol.key_cache).max() <= 1
+
+
+def test_draft_rejects_too_many_tokens(hip):
+    import torch
+
+    shape = _small_shape()
+    data = DM.layer_host_data(shape, S.derive(S.BASE_SEED, "decode-bad9"), 0, cache_fill=False)
+    model = DM.HipDecodeModel(shape)
+    model.add_layer(data)
+    dx = torch.zeros(9 * shape.hidden, dtype=torch.float32, device="cuda:0")
+    dpos = torch.zeros(1, dtype=torch.int32, device="cuda:0")
+    try:
+        with pytest.raises(ValueError):
+            model.run_layers(dx.data_ptr(), dpos.data_ptr(), tokens=9)
+    finally:
+        model.release()
