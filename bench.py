@@ -103,8 +103,10 @@ def matvec_kernel_name(choice: str, k: int, m: int, rows: list) -> str:
     mfma = choice == "mfma" or (choice == "auto" and not half and k <= 2560 and
                                 (m >= 5 or (m >= 2 and tiles16 >= 1024)))
     if half:
-        return f"kquant_matvec_half_kernel<{m}>"
-    return "kquant_mfma_kernel" if mfma else f"kquant_matvec_kernel<{min(m, 8)}>"
+        return f"kquant_matvec_half_kernel<{m}, 0>"
+    if mfma:
+        return "kquant_mfma_kernel"
+    return f"kquant_matvec_kernel<{m}, {'true' if m <= 3 else 'false'}, false, 0>"
 
 
 def parse() -> argparse.Namespace:

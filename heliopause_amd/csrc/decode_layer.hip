@@ -117,23 +117,25 @@ __global__ __launch_bounds__(256) void norm_residual_kernel(const NormArgs a) {
   __shared__ double sh[4];
   const int tid = threadIdx.x;
   const size_t row = (size_t)blockIdx.x * a.n;
-  float v[kNormPer];
+  // every input first: one memory round trip
+  float v[kNormPer], r[kNormPer], wp[kNormPer], wn[kNormPer];
 #pragma unroll
   for (int j = 0; j < kNormPer; j++) {
     const int i = tid + 256 * j;
-    v[j] = i < a.n ? a.y[row + i] : 0.0f;
+    const bool in = i < a.n;
+    v[j] = in ? a.y[row + i] : 0.0f;
+    r[j] = in && a.x_res ? a.x_res[row + i] : 0.0f;
+    wp[j] = in && a.w_post ? a.w_post[i] : 1.0f;
+    wn[j] = in && a.w_next ? a.w_next[i] : 1.0f;
   }
   if (a.x_res) {
     const double sc = rms_scale(v, a.n, a.eps, sh);
 #pragma unroll
     for (int j = 0; j < kNormPer; j++) {
       const int i = tid + 256 * j;
-      if (i < a.n) {
-        const float t = (float)(((double)v[j] * sc) * (double)a.w_post[i]);
-        const float x1 = (a.x_res[row + i] + t) * a.scale;
-        v[j] = x1;
-        a.x_out[row + i] = x1;
-      }
+      const float t = a.w_post ? (float)(((double)v[j] * sc) * (double)wp[j]) : (float)((double)v[j] * sc);
+      v[j] = i < a.n ? (r[j] + t) * a.scale : 0.0f;
+      if (i < a.n) a.x_out[row + i] = v[j];
     }
   }
   if (a.next_out) {
@@ -142,8 +144,7 @@ __global__ __launch_bounds__(256) void norm_residual_kernel(const NormArgs a) {
     for (int j = 0; j < kNormPer; j++) {
       const int i = tid + 256 * j;
       if (i < a.n)
-        a.next_out[row + i] =
-            a.w_next ? (float)(((double)v[j] * sc) * (double)a.w_next[i]) : (float)((double)v[j] * sc);
+        a.next_out[row + i] = a.w_next ? (float)(((double)v[j] * sc) * (double)wn[j]) : (float)((double)v[j] * sc);
     }
   }
 }

@@ -93,17 +93,20 @@ __device__ __forceinline__ TileCtx make_ctx(const MatvecArgs &a, int t, int nb, 
   return cx;
 }
 
-__device__ __forceinline__ void load_regs(Regs &rg, const TileCtx &cx, int it, int lane, int nb) {
-  if (lane < cx.lanes) {
-    const uint4 *ch = reinterpret_cast<const uint4 *>(cx.tile + ((size_t)it * cx.CH * cx.lanes + lane) * 16);
+// lane < cx.lanes: no bounds check
+__device__ __forceinline__ void load_regs_from(Regs &rg, const TileCtx &cx, int it, int lane, int nb) {
+  const uint4 *ch = reinterpret_cast<const uint4 *>(cx.tile + ((size_t)it * cx.CH * cx.lanes + lane) * 16);
 #pragma unroll
-    for (int c = 0; c < 9; c++) rg.c[c] = ch[(size_t)c * cx.lanes];
-    if (!cx.q4) {
+  for (int c = 0; c < 9; c++) rg.c[c] = ch[(size_t)c * cx.lanes];
+  if (!cx.q4) {
 #pragma unroll
-      for (int c = 9; c < 13; c++) rg.c[c] = ch[(size_t)c * cx.lanes];
-      rg.d6 = cx.dpl[(size_t)cx.row0 * nb + (size_t)it * cx.lanes + lane];
-    }
+    for (int c = 9; c < 13; c++) rg.c[c] = ch[(size_t)c * cx.lanes];
+    rg.d6 = cx.dpl[(size_t)cx.row0 * nb + (size_t)it * cx.lanes + lane];
   }
+}
+
+__device__ __forceinline__ void load_regs(Regs &rg, const TileCtx &cx, int it, int lane, int nb) {
+  if (lane < cx.lanes) load_regs_from(rg, cx, it, lane, nb);
 }
 
 // Integer part of one Q4_K row-block for M columns (exact aux32, sumi).
@@ -253,18 +256,21 @@ struct NormRegs {
   float y[16], r[16], wp[16], wn[16];
 };
 
+// Every group loads (groups grp >= nb re-read block nb - 1; norm_finish
+// zeroes them): no branch around the loads, so nothing that consumes them can
+// be placed ahead of the weight loads issued next.
+template <int MODE>
 __device__ __forceinline__ void norm_load(const NormIn &n, NormRegs &nr, int grp, int nb, int i16) {
+  const size_t off = (size_t)min(grp, nb - 1) * kQK;
+  load_x16(nr.y, n.y + off, i16);
+  if (MODE == 2) {
+    load_x16(nr.r, n.x_res + off, i16);
+    load_x16(nr.wp, n.w_post + off, i16);
+  } else {
 #pragma unroll
-  for (int i = 0; i < 16; i++) nr.y[i] = nr.r[i] = nr.wp[i] = nr.wn[i] = 0.0f;
-  if (grp < nb) {
-    const size_t off = (size_t)grp * kQK;
-    load_x16(nr.y, n.y + off, i16);
-    if (n.mode == 2) {
-      load_x16(nr.r, n.x_res + off, i16);
-      load_x16(nr.wp, n.w_post + off, i16);
-    }
-    load_x16(nr.wn, n.w_next + off, i16);
+    for (int i = 0; i < 16; i++) nr.r[i] = nr.wp[i] = 0.0f;
   }
+  load_x16(nr.wn, n.w_next + off, i16);
 }
 
 __device__ __forceinline__ double wg_sum_f64(double v, double *sh) {
@@ -275,13 +281,18 @@ __device__ __forceinline__ double wg_sum_f64(double v, double *sh) {
   return (sh[0] + sh[1]) + (sh[2] + sh[3]);
 }
 
+template <int MODE>
 __device__ __forceinline__ void norm_finish(const NormIn &n, NormRegs &nr, float (&xv)[16], int grp, int nb,
                                             int i16, int k, double *sh) {
+  if (grp >= nb) {
+#pragma unroll
+    for (int i = 0; i < 16; i++) nr.y[i] = nr.r[i] = 0.0f;
+  }
   double ss = 0.0;
 #pragma unroll
   for (int i = 0; i < 16; i++) ss += (double)nr.y[i] * (double)nr.y[i];
   double sc = 1.0 / sqrt(wg_sum_f64(ss, sh) / (double)k + n.eps);
-  if (n.mode == 2) {
+  if (MODE == 2) {
     ss = 0.0;
 #pragma unroll
     for (int i = 0; i < 16; i++) {
@@ -367,7 +378,7 @@ __device__ __forceinline__ float shr1(float v) {
 // with equal row counts; a wave takes gate tile p and then up tile p, which
 // cover the same rows, so the lane that finishes row r's gate sum keeps it
 // and, after the up pass, writes fround(gelu(gate) * up) to a.pair_out.
-template <int M, bool PREFETCH, bool PAIR = false>
+template <int M, bool PREFETCH, bool PAIR, int NORM>
 __global__ __launch_bounds__(256) void kquant_matvec_kernel(const MatvecArgs a) {
   extern __shared__ __align__(16) uint8_t smem[];
   const TileGeom g = a.g;
@@ -390,10 +401,9 @@ __global__ __launch_bounds__(256) void kquant_matvec_kernel(const MatvecArgs a) 
   float xv[16], xv2[16], xv3[16];  // the blocks of this group's first three passes
   __shared__ double norm_sh[4];
   NormRegs nr;
-  const bool normed = M == 1 && a.norm.mode != 0;
   auto x_block = [&](int q) { return a.x + (size_t)(q / nb) * a.k + (size_t)(q % nb) * kQK; };
-  if (normed) {
-    norm_load(a.norm, nr, grp, nb, i16);
+  if (NORM) {
+    norm_load<NORM>(a.norm, nr, grp, nb, i16);
   } else {
     // every pass's input before the weights: vector loads return in order,
     // so a pass loaded after them would wait for the weights
@@ -414,13 +424,14 @@ __global__ __launch_bounds__(256) void kquant_matvec_kernel(const MatvecArgs a) 
   };
   int ti = 0;
   int t = tile_of(0);
-  TileCtx cx{};
+  // unconditional first loads (an idle wave reads the last tile, an idle lane
+  // its tile's last lane): a path that skipped them would make the
+  // prologue's first wait on its input a wait on every load
+  TileCtx cx = make_ctx(a, t >= 0 ? t : PAIR ? 2 * a.w[0].tiles - 1 : a.total_tiles - 1, nb, R, S);
   Regs cur;
-  if (t >= 0) {
-    cx = make_ctx(a, t, nb, R, S);
-    load_regs(cur, cx, 0, lane, nb);
-  }
-  if (normed) norm_finish(a.norm, nr, xv, grp, nb, i16, a.k, norm_sh);
+  load_regs_from(cur, cx, 0, min(lane, cx.lanes - 1), nb);
+  __builtin_amdgcn_sched_barrier(0);  // keep the prologue's work after the weight loads
+  if (NORM) norm_finish<NORM>(a.norm, nr, xv, grp, nb, i16, a.k, norm_sh);
 
   {
     int q = grp;
@@ -646,7 +657,7 @@ __device__ __forceinline__ void q6k_ints_half(const HalfRegs &rg, const uint8_t 
     for (int l = 0; l < 4; l++) aux[m][l] >>= 2;  // weights carried 4 * (q6 - 32)
 }
 
-template <int M>
+template <int M, int NORM>
 __global__ __launch_bounds__(256) void kquant_matvec_half_kernel(const MatvecArgs a) {
   extern __shared__ __align__(16) uint8_t smem[];
   const TileGeom g = a.g;
@@ -662,63 +673,101 @@ __global__ __launch_bounds__(256) void kquant_matvec_half_kernel(const MatvecArg
   const int rr = grp2 >> 1, h = grp2 & 1;
   const int s = lane - grp2 * S;
 
+  // weight unit u: its descriptor and this lane's row, tile and chunk index
+  struct Unit {
+    WeightDesc W;
+    bool q4, active;
+    int CH, row, t, Rt, k;
+    const uint8_t *tile;
+  };
+  // SAFE: an idle lane addresses a row of the unit that exists (and the last
+  // unit stands in for u >= total_units), so its loads need no branch
+  auto unit_of = [&](int u, bool safe) {
+    Unit n;
+    const bool real = u < a.total_units;
+    if (safe) u = min(u, a.total_units - 1);
+    n.W = a.w[0];
+    if (a.count > 1 && u >= a.w[1].unit_begin) n.W = a.w[1];
+    if (a.count > 2 && u >= a.w[2].unit_begin) n.W = a.w[2];
+    if (a.count > 3 && u >= a.w[3].unit_begin) n.W = a.w[3];
+    n.q4 = n.W.type == kTypeQ4K;
+    n.CH = n.q4 ? 9 : 13;
+    n.row = (u - n.W.unit_begin) * Rh + rr;
+    n.active = real && rr < Rh && n.row < n.W.rows && grp2 < 2 * Rh;
+    const int arow = n.active ? n.row : safe ? min((u - n.W.unit_begin) * Rh + min(rr, Rh - 1), n.W.rows - 1) : 0;
+    n.t = arow / R;
+    n.Rt = min(R, n.W.rows - n.t * R);
+    n.k = (arow - n.t * R) * S + s;
+    n.tile = n.W.data + (size_t)n.t * R * nb * n.CH * 16;
+    return n;
+  };
+  auto load_unit = [&](HalfRegs &rg, const Unit &n, int it) {
+    const uint4 *ch = reinterpret_cast<const uint4 *>(n.tile + ((size_t)it * n.CH * n.Rt * S + n.k) * 16);
+    const size_t cs = (size_t)n.Rt * S;  // uint4 stride between chunks
+    rg.c0 = ch[(n.q4 ? 0 : 12) * cs];
+    if (n.q4) {
+#pragma unroll
+      for (int p = 0; p < 4; p++) rg.d[p] = ch[(1 + 2 * p + h) * cs];
+    } else {
+#pragma unroll
+      for (int p = 0; p < 4; p++) rg.d[p] = ch[(2 * p + h) * cs];
+#pragma unroll
+      for (int p = 0; p < 2; p++) rg.e[p] = ch[(8 + 2 * p + h) * cs];
+      rg.d6 = n.W.dplane[(size_t)n.t * R * nb + (size_t)it * n.Rt * S + n.k];
+    }
+  };
+
+  // prologue inputs of up to three passes first, then the first unit's first
+  // block (vector loads return in order), so the weights stream in while the
+  // prologue computes
   const int grp = wave * 4 + (lane >> 4);
   const int i16 = lane & 15;
   const int nq = M * nb;
-  float xv[16];
+  float xv[16], xv2[16], xv3[16];
   __shared__ double norm_sh[4];
-  if (M == 1 && a.norm.mode != 0) {
-    NormRegs nr;
-    norm_load(a.norm, nr, grp, nb, i16);
-    norm_finish(a.norm, nr, xv, grp, nb, i16, a.k, norm_sh);
-  } else if (grp < nq) {
-    load_x16(xv, a.x + (size_t)(grp / nb) * a.k + (size_t)(grp % nb) * kQK, i16);
+  NormRegs nr;
+  auto x_block = [&](int q) { return a.x + (size_t)(q / nb) * a.k + (size_t)(q % nb) * kQK; };
+  if (NORM) {
+    norm_load<NORM>(a.norm, nr, grp, nb, i16);
+  } else {
+    if (grp < nq) load_x16(xv, x_block(grp), i16);
+    if (grp + wpg * 4 < nq) load_x16(xv2, x_block(grp + wpg * 4), i16);
+    if (grp + wpg * 8 < nq) load_x16(xv3, x_block(grp + wpg * 8), i16);
   }
-  for (int q = grp; q < nq; q += wpg * 4) {
-    const int qn = q + wpg * 4;
-    float xn[16];
-    if (qn < nq) load_x16(xn, a.x + (size_t)(qn / nb) * a.k + (size_t)(qn % nb) * kQK, i16);
-    q8k_block16(xv, i16, xq + (size_t)q * kQ8BlockBytes, xd + q);
-    if (qn < nq) {
-#pragma unroll
-      for (int i = 0; i < 16; i++) xv[i] = xn[i];
+  // unconditional loads: a path that skipped them would make the prologue's
+  // first wait on its input a wait on every load
+  const int u0 = blockIdx.x * wpg + wave;
+  HalfRegs first;
+  const Unit un0 = unit_of(u0, true);
+  load_unit(first, un0, 0);
+  __builtin_amdgcn_sched_barrier(0);  // keep the prologue's work after the weight loads
+  if (NORM) norm_finish<NORM>(a.norm, nr, xv, grp, nb, i16, a.k, norm_sh);
+  {
+    int q = grp;
+    if (q < nq) q8k_block16(xv, i16, xq + (size_t)q * kQ8BlockBytes, xd + q);
+    q += wpg * 4;
+    if (q < nq) q8k_block16(xv2, i16, xq + (size_t)q * kQ8BlockBytes, xd + q);
+    q += wpg * 4;
+    if (q < nq) q8k_block16(xv3, i16, xq + (size_t)q * kQ8BlockBytes, xd + q);
+    for (q += wpg * 4; q < nq; q += wpg * 4) {  // more than three passes (several columns)
+      load_x16(xv, x_block(q), i16);
+      q8k_block16(xv, i16, xq + (size_t)q * kQ8BlockBytes, xd + q);
     }
   }
   __syncthreads();
 
   float carry[M][5];
-  for (int u = blockIdx.x * wpg + wave; u < a.total_units; u += stride) {
-    WeightDesc W = a.w[0];
-    if (a.count > 1 && u >= a.w[1].unit_begin) W = a.w[1];
-    if (a.count > 2 && u >= a.w[2].unit_begin) W = a.w[2];
-    if (a.count > 3 && u >= a.w[3].unit_begin) W = a.w[3];
-    const bool q4 = W.type == kTypeQ4K;
-    const int CH = q4 ? 9 : 13;
-    const int row0 = (u - W.unit_begin) * Rh;
-    const int row = row0 + rr;
-    const bool active = rr < Rh && row < W.rows && grp2 < 2 * Rh;
-    // this lane's tile, tile row count and lane index inside the tile
-    const int t = active ? row / R : 0;
-    const int Rt = min(R, W.rows - t * R);
-    const int k = (row - t * R) * S + s;
-    const uint8_t *tile = W.data + (size_t)t * R * nb * CH * 16;
+  for (int u = u0; u < a.total_units; u += stride) {
+    const Unit un = u == u0 ? un0 : unit_of(u, false);
+    const WeightDesc &W = un.W;
+    const bool q4 = un.q4, active = un.active;
+    const int row = un.row;
     for (int it = 0; it < g.iters; it++) {
       HalfRegs rg;
-      if (active) {
-        const uint4 *ch = reinterpret_cast<const uint4 *>(tile + ((size_t)it * CH * Rt * S + k) * 16);
-        const size_t cs = (size_t)Rt * S;  // uint4 stride between chunks
-        rg.c0 = ch[(q4 ? 0 : 12) * cs];
-        if (q4) {
-#pragma unroll
-          for (int p = 0; p < 4; p++) rg.d[p] = ch[(1 + 2 * p + h) * cs];
-        } else {
-#pragma unroll
-          for (int p = 0; p < 4; p++) rg.d[p] = ch[(2 * p + h) * cs];
-#pragma unroll
-          for (int p = 0; p < 2; p++) rg.e[p] = ch[(8 + 2 * p + h) * cs];
-          rg.d6 = W.dplane[(size_t)t * R * nb + (size_t)it * Rt * S + k];
-        }
-      }
+      if (u == u0 && it == 0)
+        rg = first;
+      else if (active)
+        load_unit(rg, un, it);
       const int b = it * S + s;
       int aux[M][4];
       int sumi[M];
@@ -801,7 +850,12 @@ static hipError_t launch_m(const MatvecArgs &a, int num_cus, hipStream_t s) {
   const int cap = num_cus * 8;
   if (grid > cap) grid = cap;
   size_t lds = matvec_lds_bytes(M, a.g, wpg);
-  hipLaunchKernelGGL((kquant_matvec_kernel<M, (M <= 3)>), dim3(grid), dim3(64 * wpg), lds, s, a);
+  if (M == 1 && a.norm.mode == 1)
+    hipLaunchKernelGGL((kquant_matvec_kernel<1, true, false, 1>), dim3(grid), dim3(64 * wpg), lds, s, a);
+  else if (M == 1 && a.norm.mode == 2)
+    hipLaunchKernelGGL((kquant_matvec_kernel<1, true, false, 2>), dim3(grid), dim3(64 * wpg), lds, s, a);
+  else
+    hipLaunchKernelGGL((kquant_matvec_kernel<M, (M <= 3), false, 0>), dim3(grid), dim3(64 * wpg), lds, s, a);
   return hipGetLastError();
 }
 
@@ -811,12 +865,19 @@ static hipError_t launch_half_m(const MatvecArgs &a, int num_cus, hipStream_t s)
   int grid = (a.total_units + wpg - 1) / wpg;
   const int cap = num_cus * 8;
   if (grid > cap) grid = cap;
-  hipLaunchKernelGGL(kquant_matvec_half_kernel<M>, dim3(grid), dim3(64 * wpg), matvec_lds_bytes(M, a.g, wpg), s, a);
+  const size_t lds = matvec_lds_bytes(M, a.g, wpg);
+  if (M == 1 && a.norm.mode == 1)
+    hipLaunchKernelGGL((kquant_matvec_half_kernel<1, 1>), dim3(grid), dim3(64 * wpg), lds, s, a);
+  else if (M == 1 && a.norm.mode == 2)
+    hipLaunchKernelGGL((kquant_matvec_half_kernel<1, 2>), dim3(grid), dim3(64 * wpg), lds, s, a);
+  else
+    hipLaunchKernelGGL((kquant_matvec_half_kernel<M, 0>), dim3(grid), dim3(64 * wpg), lds, s, a);
   return hipGetLastError();
 }
 
 hipError_t launch_matvec_half(const MatvecArgs &a, int num_cus, hipStream_t s) {
-  if (a.norm.mode != 0 && (a.cols != 1 || a.g.nb > 16)) return hipErrorInvalidValue;
+  if (a.norm.mode < 0 || a.norm.mode > 2 || (a.norm.mode != 0 && (a.cols != 1 || a.g.nb > 16)))
+    return hipErrorInvalidValue;
   if (a.g.S > 32 || a.Rh < 1 || 2 * a.Rh * a.g.S > 64) return hipErrorInvalidValue;
   switch (a.cols) {
     case 1: return launch_half_m<1>(a, num_cus, s);
@@ -833,13 +894,21 @@ static hipError_t launch_pair_m(const MatvecArgs &a, int num_cus, hipStream_t s)
   int grid = (a.w[0].tiles + wpg - 1) / wpg;
   const int cap = num_cus * 8;
   if (grid > cap) grid = cap;
-  hipLaunchKernelGGL((kquant_matvec_kernel<M, (M <= 3), true>), dim3(grid), dim3(64 * wpg),
+  if (M == 1 && a.norm.mode == 1)
+    hipLaunchKernelGGL((kquant_matvec_kernel<1, true, true, 1>), dim3(grid), dim3(64 * wpg),
+                       matvec_lds_bytes(M, a.g, wpg), s, a);
+  else if (M == 1 && a.norm.mode == 2)
+    hipLaunchKernelGGL((kquant_matvec_kernel<1, true, true, 2>), dim3(grid), dim3(64 * wpg),
+                       matvec_lds_bytes(M, a.g, wpg), s, a);
+  else
+    hipLaunchKernelGGL((kquant_matvec_kernel<M, (M <= 3), true, 0>), dim3(grid), dim3(64 * wpg),
                      matvec_lds_bytes(M, a.g, wpg), s, a);
   return hipGetLastError();
 }
 
 hipError_t launch_matvec_pair(const MatvecArgs &a, int num_cus, hipStream_t s) {
-  if (a.norm.mode != 0 && (a.cols != 1 || a.g.nb > 16)) return hipErrorInvalidValue;
+  if (a.norm.mode < 0 || a.norm.mode > 2 || (a.norm.mode != 0 && (a.cols != 1 || a.g.nb > 16)))
+    return hipErrorInvalidValue;
   if (a.count != 2 || a.w[0].rows != a.w[1].rows || a.w[0].tiles != a.w[1].tiles || !a.pair_out)
     return hipErrorInvalidValue;
   switch (a.cols) {
@@ -852,7 +921,8 @@ hipError_t launch_matvec_pair(const MatvecArgs &a, int num_cus, hipStream_t s) {
 }
 
 hipError_t launch_matvec(const MatvecArgs &a, int num_cus, hipStream_t s) {
-  if (a.norm.mode != 0 && (a.cols != 1 || a.g.nb > 16)) return hipErrorInvalidValue;
+  if (a.norm.mode < 0 || a.norm.mode > 2 || (a.norm.mode != 0 && (a.cols != 1 || a.g.nb > 16)))
+    return hipErrorInvalidValue;
   switch (a.cols) {
     case 1: return launch_m<1>(a, num_cus, s);
     case 2: return launch_m<2>(a, num_cus, s);
