@@ -117,16 +117,29 @@ __global__ __launch_bounds__(256) void norm_residual_kernel(const NormArgs a) {
   __shared__ double sh[4];
   const int tid = threadIdx.x;
   const size_t row = (size_t)blockIdx.x * a.n;
-  // every input first: one memory round trip
+  // every input first, one memory round trip: the loads take no branch
+  // (indexes past n re-read element n - 1, absent operands re-read y), so
+  // none of them waits for another
   float v[kNormPer], r[kNormPer], wp[kNormPer], wn[kNormPer];
+  const float *py = a.y + row;
+  const float *pr = a.x_res ? a.x_res + row : py;
+  const float *pwp = a.w_post ? a.w_post : py;
+  const float *pwn = a.w_next ? a.w_next : py;
 #pragma unroll
   for (int j = 0; j < kNormPer; j++) {
-    const int i = tid + 256 * j;
-    const bool in = i < a.n;
-    v[j] = in ? a.y[row + i] : 0.0f;
-    r[j] = in && a.x_res ? a.x_res[row + i] : 0.0f;
-    wp[j] = in && a.w_post ? a.w_post[i] : 1.0f;
-    wn[j] = in && a.w_next ? a.w_next[i] : 1.0f;
+    const int ic = min(tid + 256 * j, a.n - 1);
+    v[j] = py[ic];
+    r[j] = pr[ic];
+    wp[j] = pwp[ic];
+    wn[j] = pwn[ic];
+  }
+#pragma unroll
+  for (int j = 0; j < kNormPer; j++) {
+    const bool in = tid + 256 * j < a.n;
+    v[j] = in ? v[j] : 0.0f;
+    r[j] = in && a.x_res ? r[j] : 0.0f;
+    wp[j] = in && a.w_post ? wp[j] : 1.0f;
+    wn[j] = in && a.w_next ? wn[j] : 1.0f;
   }
   if (a.x_res) {
     const double sc = rms_scale(v, a.n, a.eps, sh);
@@ -171,23 +184,32 @@ __global__ __launch_bounds__(64) void qkv_post_kernel(const QkvPostArgs a) {
   const float *src = kind == 0 ? a.q + (qrow + head) * kHeadDim
                                : (kind == 1 ? a.k : a.v) + (kvrow + head) * kHeadDim;
   const float *w = kind == 0 ? a.wq : kind == 1 ? a.wk : nullptr;
-  float x[4];
-  double s = 0.0;
+  const int half = a.rope_dims >> 1;
+  // every load first, none in a branch (an absent weight re-reads the row)
+  float x[4], wv[4];
+  const float *pw = w ? w : src;
 #pragma unroll
   for (int j = 0; j < 4; j++) {
     x[j] = src[lane + 64 * j];
-    s += (double)x[j] * (double)x[j];
+    wv[j] = pw[lane + 64 * j];
   }
+  double2 tab[2] = {make_double2(1.0, 0.0), make_double2(1.0, 0.0)};
+  if (a.rope_table_mode == 2 && kind != 2 && half > 0) {
+#pragma unroll
+    for (int p = 0; p < 2; p++) tab[p] = a.rope_table[t * (kHeadDim / 2) + min(lane + 64 * p, half - 1)];
+  }
+  double s = 0.0;
+#pragma unroll
+  for (int j = 0; j < 4; j++) s += (double)x[j] * (double)x[j];
   const double sc = 1.0 / sqrt(wave_sum_f64(s) / (double)kHeadDim + a.eps);
 #pragma unroll
   for (int j = 0; j < 4; j++) {
     const int i = lane + 64 * j;
-    xs[i] = w ? (float)(((double)x[j] * sc) * (double)w[i]) : (float)((double)x[j] * sc);
+    xs[i] = w ? (float)(((double)x[j] * sc) * (double)wv[j]) : (float)((double)x[j] * sc);
   }
   __syncthreads();
   const int pos = *a.position + t;
   if (kind != 2) {
-    const int half = a.rope_dims >> 1;
     float r0[2], r1[2];
 #pragma unroll
     for (int p = 0; p < 2; p++) {
@@ -196,9 +218,8 @@ __global__ __launch_bounds__(64) void qkv_post_kernel(const QkvPostArgs a) {
       if (i < half) {
         double c, sn;
         if (a.rope_table_mode == 2) {
-          const double2 e = a.rope_table[t * (kHeadDim / 2) + i];
-          c = e.x;
-          sn = e.y;
+          c = tab[p].x;
+          sn = tab[p].y;
         } else {
           double theta = (double)pos;
           for (int it = 0; it < i; it++) theta = (double)(float)(theta * a.theta_scale);
@@ -269,24 +290,26 @@ __global__ __launch_bounds__(256) void attn_partial_kernel(const AttnArgs a) {
   constexpr int kRows = (G + 2 + 3) / 4;  // rows per wave: queries, key, value
   float px[kRows][4], pw[kRows][4];
   double2 tab[2] = {make_double2(1.0, 0.0), make_double2(1.0, 0.0)};
+  // Loads take no branch on a lane or wave (rows past the last re-read it,
+  // absent weights re-read the row, slots past the capacity re-read the last
+  // slot; what they bring is masked later): a path that skipped loads would
+  // make the compiler's first wait on an early load a wait on every load.
   if (a.prep) {
 #pragma unroll
     for (int k3 = 0; k3 < kRows; k3++) {
-      const int r = wave + 4 * k3;
-      if (r < G + 2) {
-        const float *src = r < G ? a.q + (size_t)(g * G + r) * kHeadDim : (r == G ? a.k : a.v) + (size_t)g * kHeadDim;
-        const float *w = r < G ? a.wq : (r == G ? a.wk : nullptr);
+      const int r = min(wave + 4 * k3, G + 1);
+      const float *src = r < G ? a.q + (size_t)(g * G + r) * kHeadDim : (r == G ? a.k : a.v) + (size_t)g * kHeadDim;
+      const float *w = r < G ? a.wq : (r == G ? a.wk : nullptr);
+      const float *pwr = w ? w : src;
 #pragma unroll
-        for (int j = 0; j < 4; j++) {
-          px[k3][j] = src[lane + 64 * j];
-          pw[k3][j] = w ? w[lane + 64 * j] : 1.0f;
-        }
+      for (int j = 0; j < 4; j++) {
+        px[k3][j] = src[lane + 64 * j];
+        pw[k3][j] = pwr[lane + 64 * j];
       }
     }
-    if (a.rope_table_mode == 2 && lane_pairs) {
+    if (a.rope_table_mode == 2 && lane_pairs && half > 0) {
 #pragma unroll
-      for (int p = 0; p < 2; p++)
-        if (lane + 64 * p < half) tab[p] = a.rope_table[lane + 64 * p];
+      for (int p = 0; p < 2; p++) tab[p] = a.rope_table[min(lane + 64 * p, half - 1)];
     }
   }
   // tokens at *a.position .. + a.tokens - 1 share the window of the last
@@ -299,8 +322,8 @@ __global__ __launch_bounds__(256) void attn_partial_kernel(const AttnArgs a) {
   const int kj = tid >> 3, kp = tid & 7;
   const int kslot = c * kAttnChunk + kj;
   uint4 kraw[4];
-  if (kslot < cap) {
-    const _Float16 *kr = a.k_cache + head_base + (size_t)kslot * kHeadDim;
+  {
+    const _Float16 *kr = a.k_cache + head_base + (size_t)min(kslot, cap - 1) * kHeadDim;
 #pragma unroll
     for (int i = 0; i < 4; i++) kraw[i] = *reinterpret_cast<const uint4 *>(kr + 8 * (8 * i + kp));
   }
@@ -308,8 +331,9 @@ __global__ __launch_bounds__(256) void attn_partial_kernel(const AttnArgs a) {
   uint2 vraw[8];
 #pragma unroll
   for (int j = 0; j < 8; j++)
-    if (vslot0 + j < cap)
-      vraw[j] = *reinterpret_cast<const uint2 *>(a.v_cache + head_base + (size_t)(vslot0 + j) * kHeadDim + 4 * lane);
+    vraw[j] = *reinterpret_cast<const uint2 *>(a.v_cache + head_base + (size_t)min(vslot0 + j, cap - 1) * kHeadDim +
+                                               4 * lane);
+  __builtin_amdgcn_sched_barrier(0);  // every load issued before the prologue's first use of one
 
   int start, count;
   window_of(pos, cap, a.window, &start, &count);
@@ -350,7 +374,8 @@ __global__ __launch_bounds__(256) void attn_partial_kernel(const AttnArgs a) {
         float x[4];
 #pragma unroll
         for (int j = 0; j < 4; j++)
-          x[j] = r <= G ? (float)(((double)px[k3][j] * scl) * (double)pw[k3][j]) : (float)((double)px[k3][j] * scl);
+          x[j] = r <= G && (r < G ? a.wq : a.wk) ? (float)(((double)px[k3][j] * scl) * (double)pw[k3][j])
+                                                   : (float)((double)px[k3][j] * scl);
         if (r <= G && lane_pairs) {
           const int hj = half >> 6;  // pair (j, j + hj) for j < hj
 #pragma unroll
@@ -540,24 +565,27 @@ __global__ __launch_bounds__(256) void attn_reduce_kernel(const AttnArgs a) {
   const int tok = blockIdx.z;
   const size_t row0 = ((size_t)tok * a.nkv + g) * a.chunks * kAttnMaxGroup + h;  // chunk c at row0 + c * kAttnMaxGroup
   const int d = blockIdx.y * 64 + (tid & 63), cg = tid >> 6;
+  // more chunks than one tile: the maximum over all of them first (with one
+  // tile, the tile's own chunk maxima give it)
   float m = -__builtin_inff();
-  for (int c = tid; c < chunks; c += 256) m = fmaxf(m, a.part_m[row0 + (size_t)c * kAttnMaxGroup]);
+  if (chunks > kMergeTile)
+    for (int c = tid; c < chunks; c += 256) m = fmaxf(m, a.part_m[row0 + (size_t)c * kAttnMaxGroup]);
   float l = 0.0f, o = 0.0f;
   for (int c0 = 0; c0 < chunks; c0 += kMergeTile) {
     const int n = chunks - c0 < kMergeTile ? chunks - c0 : kMergeTile;
+    // the tile's loads take no branch (chunks past n re-read chunk n - 1 and
+    // are masked), so none waits for another
     float po[kMergeTile / 4];
 #pragma unroll
-    for (int i = 0; i < kMergeTile / 4; i++) {
-      const int cc = cg + 4 * i;
-      po[i] = cc < n ? a.part_o[(row0 + (size_t)(c0 + cc) * kAttnMaxGroup) * kHeadDim + d] : 0.0f;
-    }
-    float mc = -__builtin_inff(), lc = 0.0f;
-    if (tid < n) {
-      const size_t base = row0 + (size_t)(c0 + tid) * kAttnMaxGroup;
-      mc = a.part_m[base];
-      lc = a.part_l[base];
-    }
-    if (c0 == 0) m = block_max_f32(m, sh);
+    for (int i = 0; i < kMergeTile / 4; i++)
+      po[i] = a.part_o[(row0 + (size_t)(c0 + min(cg + 4 * i, n - 1)) * kAttnMaxGroup) * kHeadDim + d];
+    const size_t base = row0 + (size_t)(c0 + min(tid, n - 1)) * kAttnMaxGroup;
+    float mc = a.part_m[base], lc = a.part_l[base];
+#pragma unroll
+    for (int i = 0; i < kMergeTile / 4; i++) po[i] = cg + 4 * i < n ? po[i] : 0.0f;
+    mc = tid < n ? mc : -__builtin_inff();
+    lc = tid < n ? lc : 0.0f;
+    if (c0 == 0) m = block_max_f32(fmaxf(m, mc), sh);
     // a chunk with no slot in the window (m_c = -inf) adds nothing
     const float f = mc == -__builtin_inff() ? 0.0f : (float)exp((double)(mc - m));
     l = __builtin_fmaf(f, lc, l);
