@@ -75,13 +75,16 @@ struct TileCtx {
   bool q4;
 };
 
+// TYPE: kTypeQ4K or kTypeQ6K when every weight of the launch has that type
+// (then the type tests fold away), 0 for a mixed launch.
+template <int TYPE>
 __device__ __forceinline__ TileCtx make_ctx(const MatvecArgs &a, int t, int nb, int R, int S) {
   WeightDesc W = a.w[0];
   if (a.count > 1 && t >= a.w[1].tile_begin) W = a.w[1];
   if (a.count > 2 && t >= a.w[2].tile_begin) W = a.w[2];
   if (a.count > 3 && t >= a.w[3].tile_begin) W = a.w[3];
   TileCtx cx;
-  cx.q4 = W.type == kTypeQ4K;
+  cx.q4 = TYPE == kTypeQ4K ? true : TYPE == kTypeQ6K ? false : W.type == kTypeQ4K;
   cx.CH = cx.q4 ? 9 : 13;
   cx.rows = W.rows;
   cx.row0 = (t - W.tile_begin) * R;
@@ -93,7 +96,11 @@ __device__ __forceinline__ TileCtx make_ctx(const MatvecArgs &a, int t, int nb, 
   return cx;
 }
 
-// lane < cx.lanes: no bounds check
+// lane < cx.lanes: no bounds check.  In a mixed launch (TYPE 0) a Q4_K
+// block issues 9 loads and a Q6_K block 14, so a wait for loads issued
+// before these also waits for the first 5 of a Q6_K block's: the price of
+// mixing types in one launch.
+template <int TYPE>
 __device__ __forceinline__ void load_regs_from(Regs &rg, const TileCtx &cx, int it, int lane, int nb) {
   const uint4 *ch = reinterpret_cast<const uint4 *>(cx.tile + ((size_t)it * cx.CH * cx.lanes + lane) * 16);
 #pragma unroll
@@ -105,8 +112,9 @@ __device__ __forceinline__ void load_regs_from(Regs &rg, const TileCtx &cx, int 
   }
 }
 
+template <int TYPE>
 __device__ __forceinline__ void load_regs(Regs &rg, const TileCtx &cx, int it, int lane, int nb) {
-  if (lane < cx.lanes) load_regs_from(rg, cx, it, lane, nb);
+  if (lane < cx.lanes) load_regs_from<TYPE>(rg, cx, it, lane, nb);
 }
 
 // Integer part of one Q4_K row-block for M columns (exact aux32, sumi).
@@ -378,7 +386,7 @@ __device__ __forceinline__ float shr1(float v) {
 // with equal row counts; a wave takes gate tile p and then up tile p, which
 // cover the same rows, so the lane that finishes row r's gate sum keeps it
 // and, after the up pass, writes fround(gelu(gate) * up) to a.pair_out.
-template <int M, bool PREFETCH, bool PAIR, int NORM>
+template <int M, bool PREFETCH, bool PAIR, int NORM, int TYPE>
 __global__ __launch_bounds__(256) void kquant_matvec_kernel(const MatvecArgs a) {
   extern __shared__ __align__(16) uint8_t smem[];
   const TileGeom g = a.g;
@@ -427,9 +435,9 @@ __global__ __launch_bounds__(256) void kquant_matvec_kernel(const MatvecArgs a) 
   // unconditional first loads (an idle wave reads the last tile, an idle lane
   // its tile's last lane): a path that skipped them would make the
   // prologue's first wait on its input a wait on every load
-  TileCtx cx = make_ctx(a, t >= 0 ? t : PAIR ? 2 * a.w[0].tiles - 1 : a.total_tiles - 1, nb, R, S);
+  TileCtx cx = make_ctx<TYPE>(a, t >= 0 ? t : PAIR ? 2 * a.w[0].tiles - 1 : a.total_tiles - 1, nb, R, S);
   Regs cur;
-  load_regs_from(cur, cx, 0, min(lane, cx.lanes - 1), nb);
+  load_regs_from<TYPE>(cur, cx, 0, min(lane, cx.lanes - 1), nb);
   __builtin_amdgcn_sched_barrier(0);  // keep the prologue's work after the weight loads
   if (NORM) norm_finish<NORM>(a.norm, nr, xv, grp, nb, i16, a.k, norm_sh);
 
@@ -458,9 +466,14 @@ __global__ __launch_bounds__(256) void kquant_matvec_kernel(const MatvecArgs a) 
         if (nit == g.iters) {
           nt = tile_of(ti + 1);
           nit = 0;
-          if (nt >= 0) ncx = make_ctx(a, nt, nb, R, S);
+          if (nt >= 0) ncx = make_ctx<TYPE>(a, nt, nb, R, S);
         }
-        if (nt >= 0) load_regs(nxt, ncx, nit, lane, nb);
+        // every iteration loads (the wave's last block re-reads itself): an
+        // iteration without these loads would make the wait below for the
+        // current block a wait for the next one too
+        if (nt < 0) nit = it;
+        load_regs_from<TYPE>(nxt, ncx, nit, min(lane, ncx.lanes - 1), nb);
+        __builtin_amdgcn_sched_barrier(0);  // the current block's work after the next block's loads
       }
       const int b = it * S + s;
       const bool active = lane < cx.lanes;
@@ -529,13 +542,13 @@ __global__ __launch_bounds__(256) void kquant_matvec_kernel(const MatvecArgs a) 
       if (PREFETCH) {
         cur = nxt;
       } else if (!last) {
-        load_regs(cur, cx, it + 1, lane, nb);
+        load_regs<TYPE>(cur, cx, it + 1, lane, nb);
       }
     }
     t = tile_of(++ti);
     if (t >= 0) {
-      cx = make_ctx(a, t, nb, R, S);
-      if (!PREFETCH) load_regs(cur, cx, 0, lane, nb);
+      cx = make_ctx<TYPE>(a, t, nb, R, S);
+      if (!PREFETCH) load_regs<TYPE>(cur, cx, 0, lane, nb);
     }
   }
 }
@@ -843,19 +856,42 @@ static size_t matvec_lds_bytes(int cols, const TileGeom &g, int wpg) {
   return (size_t)cols * g.nb * kQ8BlockBytes + (size_t)((cols * g.nb + 3) & ~3) * 4;
 }
 
+// The weight type shared by every weight of the launch, or 0.
+static int uniform_type(const MatvecArgs &a) {
+  for (int i = 1; i < a.count; i++)
+    if (a.w[i].type != a.w[0].type) return 0;
+  return a.w[0].type == kTypeQ4K || a.w[0].type == kTypeQ6K ? a.w[0].type : 0;
+}
+
+template <int M, bool PAIR, int NORM>
+static void launch_typed(const MatvecArgs &a, dim3 grid, size_t lds, hipStream_t s) {
+  constexpr bool PF = M <= 3;
+  const int t = PF ? uniform_type(a) : 0;
+  if (t == kTypeQ4K)
+    hipLaunchKernelGGL((kquant_matvec_kernel<M, PF, PAIR, NORM, (PF ? kTypeQ4K : 0)>), grid, dim3(256), lds, s, a);
+  else if (t == kTypeQ6K)
+    hipLaunchKernelGGL((kquant_matvec_kernel<M, PF, PAIR, NORM, (PF ? kTypeQ6K : 0)>), grid, dim3(256), lds, s, a);
+  else
+    hipLaunchKernelGGL((kquant_matvec_kernel<M, PF, PAIR, NORM, 0>), grid, dim3(256), lds, s, a);
+}
+
+template <int M, bool PAIR>
+static void launch_full(const MatvecArgs &a, dim3 grid, size_t lds, hipStream_t s) {
+  if (M == 1 && a.norm.mode == 1)
+    launch_typed<1, PAIR, 1>(a, grid, lds, s);
+  else if (M == 1 && a.norm.mode == 2)
+    launch_typed<1, PAIR, 2>(a, grid, lds, s);
+  else
+    launch_typed<M, PAIR, 0>(a, grid, lds, s);
+}
+
 template <int M>
 static hipError_t launch_m(const MatvecArgs &a, int num_cus, hipStream_t s) {
   const int wpg = 4;
   int grid = (a.total_tiles + wpg - 1) / wpg;
   const int cap = num_cus * 8;
   if (grid > cap) grid = cap;
-  size_t lds = matvec_lds_bytes(M, a.g, wpg);
-  if (M == 1 && a.norm.mode == 1)
-    hipLaunchKernelGGL((kquant_matvec_kernel<1, true, false, 1>), dim3(grid), dim3(64 * wpg), lds, s, a);
-  else if (M == 1 && a.norm.mode == 2)
-    hipLaunchKernelGGL((kquant_matvec_kernel<1, true, false, 2>), dim3(grid), dim3(64 * wpg), lds, s, a);
-  else
-    hipLaunchKernelGGL((kquant_matvec_kernel<M, (M <= 3), false, 0>), dim3(grid), dim3(64 * wpg), lds, s, a);
+  launch_full<M, false>(a, dim3(grid), matvec_lds_bytes(M, a.g, wpg), s);
   return hipGetLastError();
 }
 
@@ -894,15 +930,7 @@ static hipError_t launch_pair_m(const MatvecArgs &a, int num_cus, hipStream_t s)
   int grid = (a.w[0].tiles + wpg - 1) / wpg;
   const int cap = num_cus * 8;
   if (grid > cap) grid = cap;
-  if (M == 1 && a.norm.mode == 1)
-    hipLaunchKernelGGL((kquant_matvec_kernel<1, true, true, 1>), dim3(grid), dim3(64 * wpg),
-                       matvec_lds_bytes(M, a.g, wpg), s, a);
-  else if (M == 1 && a.norm.mode == 2)
-    hipLaunchKernelGGL((kquant_matvec_kernel<1, true, true, 2>), dim3(grid), dim3(64 * wpg),
-                       matvec_lds_bytes(M, a.g, wpg), s, a);
-  else
-    hipLaunchKernelGGL((kquant_matvec_kernel<M, (M <= 3), true, 0>), dim3(grid), dim3(64 * wpg),
-                     matvec_lds_bytes(M, a.g, wpg), s, a);
+  launch_full<M, true>(a, dim3(grid), matvec_lds_bytes(M, a.g, wpg), s);
   return hipGetLastError();
 }
 
