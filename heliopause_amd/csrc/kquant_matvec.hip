@@ -355,22 +355,24 @@ __device__ __forceinline__ void q8k_block16(const float (&v)[16], int i16, uint8
   int sum = 0;
 #pragma unroll
   for (int l4 = 0; l4 < 4; l4++) {
-    uint32_t wv = 0;
+    int q[4];
 #pragma unroll
     for (int c = 0; c < 4; c++) {
       // Rust: (is * x).round().min(127.0) as i8.  |is * x| <= 127 (1 + 2^-23)
       // for every element, so the saturating cast never acts; NaN -> min()
       // -> 127.  round() (half away from zero) as trunc(p + copysign(0.5 -
-      // 2^-25, p)): equal for every f32 |p| < 128 (checked exhaustively).
+      // 2^-25, p)): equal for every f32 |p| < 128 (checked exhaustively);
+      // the int conversion truncates, and truncation commutes with min(., 127).
       const float p = __fmul_rn(inv, v[4 * c + l4]);
-      const float r = fminf(truncf(__fadd_rn(p, copysignf(0.49999997f, p))), 127.0f);
-      const int q = (int)r;
-      sum += q;
-      wv |= (uint32_t)(q & 0xff) << (8 * c);
+      q[c] = (int)fminf(__fadd_rn(p, copysignf(0.49999997f, p)), 127.0f);
     }
+    // bytes q0..q3 (low to high): the low bytes of two packed int16 pairs
+    const uint32_t lo = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pk_i16(q[0], q[1]));
+    const uint32_t hi = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pk_i16(q[2], q[3]));
+    const uint32_t wv = __builtin_amdgcn_perm(hi, lo, 0x06040200u);
     word[l4] = nz ? wv : 0u;  // dword l = 4u + l4 of sub-block j
+    sum = __builtin_amdgcn_sdot4((int)word[l4], 0x01010101, sum, false);
   }
-  sum = nz ? sum : 0;
   sum += dppi<kDppQuadXor1>(sum);
   *reinterpret_cast<uint4 *>(blk + 32 * j + 16 * u) = make_uint4(word[0], word[1], word[2], word[3]);
   if (u == 0) reinterpret_cast<int16_t *>(blk + 256)[j] = (int16_t)sum;
