@@ -388,8 +388,11 @@ __global__ __launch_bounds__(256) void attn_partial_kernel(const AttnArgs a) {
             }
           }
         }
+        // queries as the scorer rounds them; the new key and value as the
+        // cache stores them (other RoPE widths: after the pass over LDS)
 #pragma unroll
-        for (int j = 0; j < 4; j++) xs[r][lane + 64 * j] = x[j];
+        for (int j = 0; j < 4; j++)
+          xs[r][lane + 64 * j] = !lane_pairs ? x[j] : r < G ? rs_f16_round(x[j]) : (float)(_Float16)x[j];
       }
     }
     __syncthreads();
@@ -407,14 +410,13 @@ __global__ __launch_bounds__(256) void attn_partial_kernel(const AttnArgs a) {
         xs[r][i + half] = (float)(x0 * sn) + (float)(x1 * cn);
       }
       __syncthreads();
+      for (int idx = tid; idx < (G + 2) * kHeadDim; idx += 256) {
+        const int r = idx >> 8, i = idx & 255;
+        const float v = xs[r][i];
+        xs[r][i] = r < G ? rs_f16_round(v) : (float)(_Float16)v;
+      }
+      __syncthreads();
     }
-    // queries as the scorer rounds them; the new key and value as the cache stores them
-    for (int idx = tid; idx < (G + 2) * kHeadDim; idx += 256) {
-      const int r = idx >> 8, i = idx & 255;
-      const float v = xs[r][i];
-      xs[r][i] = r < G ? rs_f16_round(v) : (float)(_Float16)v;
-    }
-    __syncthreads();
     if (new_slot >= 0 && new_slot / kAttnChunk == c) {
       const size_t o = head_base + (size_t)new_slot * kHeadDim + tid;
       a.k_cache[o] = (_Float16)xs[G][tid];
@@ -565,11 +567,54 @@ __global__ __launch_bounds__(256) void attn_reduce_kernel(const AttnArgs a) {
   const int tok = blockIdx.z;
   const size_t row0 = ((size_t)tok * a.nkv + g) * a.chunks * kAttnMaxGroup + h;  // chunk c at row0 + c * kAttnMaxGroup
   const int d = blockIdx.y * 64 + (tid & 63), cg = tid >> 6;
-  // more chunks than one tile: the maximum over all of them first (with one
-  // tile, the tile's own chunk maxima give it)
+  if (chunks <= kMergeTile) {
+    // One tile: every wave forms m, the factors exp(m_c - m) and l itself
+    // (lane L takes chunks L and L + 64), so the only barrier is the final
+    // sum over the four chunk groups.  Loads take no branch (chunks past the
+    // last re-read it and are masked).
+    __shared__ float fw[4][kMergeTile];
+    const int lane = tid & 63;
+    const int n = chunks;
+    float po[kMergeTile / 4];
+#pragma unroll
+    for (int i = 0; i < kMergeTile / 4; i++)
+      po[i] = a.part_o[(row0 + (size_t)min(cg + 4 * i, n - 1) * kAttnMaxGroup) * kHeadDim + d];
+    float mc[2], lc[2];
+#pragma unroll
+    for (int k = 0; k < 2; k++) {
+      const size_t base = row0 + (size_t)min(lane + 64 * k, n - 1) * kAttnMaxGroup;
+      mc[k] = a.part_m[base];
+      lc[k] = a.part_l[base];
+    }
+#pragma unroll
+    for (int k = 0; k < 2; k++) {
+      mc[k] = lane + 64 * k < n ? mc[k] : -__builtin_inff();
+      lc[k] = lane + 64 * k < n ? lc[k] : 0.0f;
+    }
+    const float m = wave_max_f32(fmaxf(mc[0], mc[1]));
+    float lsum = 0.0f;
+#pragma unroll
+    for (int k = 0; k < 2; k++) {
+      // a chunk with no slot in the window (m_c = -inf) adds nothing
+      const float f = mc[k] == -__builtin_inff() ? 0.0f : (float)exp((double)(mc[k] - m));
+      fw[cg][lane + 64 * k] = f;
+      lsum = __builtin_fmaf(f, lc[k], lsum);
+    }
+    const float l = wave_sum_f32(lsum);
+    float o = 0.0f;  // this wave's own LDS row: no barrier between the writes above and these reads
+#pragma unroll
+    for (int i = 0; i < kMergeTile / 4; i++) o = __builtin_fmaf(fw[cg][cg + 4 * i], cg + 4 * i < n ? po[i] : 0.0f, o);
+    red[cg][lane] = o;
+    __syncthreads();
+    if (tid < 64) {
+      const float oo = (red[0][tid] + red[1][tid]) + (red[2][tid] + red[3][tid]);
+      a.out[((size_t)tok * a.nq + qh) * kHeadDim + d] = l > 0.0f ? ts_f16_round(oo / l) : 0.0f;  // l == 0: no key
+    }
+    return;
+  }
+  // several tiles: the maximum over all chunks first
   float m = -__builtin_inff();
-  if (chunks > kMergeTile)
-    for (int c = tid; c < chunks; c += 256) m = fmaxf(m, a.part_m[row0 + (size_t)c * kAttnMaxGroup]);
+  for (int c = tid; c < chunks; c += 256) m = fmaxf(m, a.part_m[row0 + (size_t)c * kAttnMaxGroup]);
   float l = 0.0f, o = 0.0f;
   for (int c0 = 0; c0 < chunks; c0 += kMergeTile) {
     const int n = chunks - c0 < kMergeTile ? chunks - c0 : kMergeTile;
