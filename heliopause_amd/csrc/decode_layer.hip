@@ -90,11 +90,11 @@ __device__ __forceinline__ void window_of(int pos, int capacity, int window, int
 }
 
 // Sum over the 256 threads of the workgroup (every thread gets the total).
+// Sum over the workgroup's four waves; sh (4 doubles) must not have been
+// used by an earlier call in the kernel (no barrier guards its reuse).
 __device__ __forceinline__ double block_sum_f64(double v, double *sh) {
   v = wave_sum_f64(v);
-  const int wave = threadIdx.x >> 6;
-  __syncthreads();
-  if ((threadIdx.x & 63) == 0) sh[wave] = v;
+  if ((threadIdx.x & 63) == 0) sh[threadIdx.x >> 6] = v;
   __syncthreads();
   return (sh[0] + sh[1]) + (sh[2] + sh[3]);
 }
@@ -114,7 +114,7 @@ __device__ __forceinline__ double rms_scale(const float (&v)[kNormPer], int n, d
 // Workgroup r handles row r of [rows][n].  w_post / w_next null: the norm
 // has no weight (rmsNormRowsNoWeight).
 __global__ __launch_bounds__(256) void norm_residual_kernel(const NormArgs a) {
-  __shared__ double sh[4];
+  __shared__ double sh[8];  // two workgroup sums
   const int tid = threadIdx.x;
   const size_t row = (size_t)blockIdx.x * a.n;
   // every input first, one memory round trip: the loads take no branch
@@ -152,7 +152,7 @@ __global__ __launch_bounds__(256) void norm_residual_kernel(const NormArgs a) {
     }
   }
   if (a.next_out) {
-    const double sc = rms_scale(v, a.n, a.eps, sh);
+    const double sc = rms_scale(v, a.n, a.eps, sh + 4);
 #pragma unroll
     for (int j = 0; j < kNormPer; j++) {
       const int i = tid + 256 * j;

@@ -281,9 +281,10 @@ __device__ __forceinline__ void norm_load(const NormIn &n, NormRegs &nr, int grp
   load_x16(nr.wn, n.w_next + off, i16);
 }
 
+// Sum over the workgroup's four waves; sh (4 doubles) must not have been
+// used by an earlier call in the kernel (no barrier guards its reuse).
 __device__ __forceinline__ double wg_sum_f64(double v, double *sh) {
   v = wave_sum_f64(v);
-  __syncthreads();
   if ((threadIdx.x & 63) == 0) sh[threadIdx.x >> 6] = v;
   __syncthreads();
   return (sh[0] + sh[1]) + (sh[2] + sh[3]);
@@ -310,7 +311,7 @@ __device__ __forceinline__ void norm_finish(const NormIn &n, NormRegs &nr, float
       ss += (double)x1 * (double)x1;
     }
     if (blockIdx.x == 0 && grp < nb) store_x16(n.x_out + (size_t)grp * kQK, nr.y, i16);
-    sc = 1.0 / sqrt(wg_sum_f64(ss, sh) / (double)k + n.eps);
+    sc = 1.0 / sqrt(wg_sum_f64(ss, sh + 4) / (double)k + n.eps);
   }
 #pragma unroll
   for (int i = 0; i < 16; i++) xv[i] = (float)(((double)nr.y[i] * sc) * (double)nr.wn[i]);
@@ -409,7 +410,7 @@ __global__ __launch_bounds__(256) void kquant_matvec_kernel(const MatvecArgs a) 
   const int i16 = lane & 15;
   const int nq = M * nb;
   float xv[16], xv2[16], xv3[16];  // the blocks of this group's first three passes
-  __shared__ double norm_sh[4];
+  __shared__ double norm_sh[8];  // two workgroup sums
   NormRegs nr;
   auto x_block = [&](int q) { return a.x + (size_t)(q / nb) * a.k + (size_t)(q % nb) * kQK; };
   if (NORM) {
@@ -739,7 +740,7 @@ __global__ __launch_bounds__(256) void kquant_matvec_half_kernel(const MatvecArg
   const int i16 = lane & 15;
   const int nq = M * nb;
   float xv[16], xv2[16], xv3[16];
-  __shared__ double norm_sh[4];
+  __shared__ double norm_sh[8];  // two workgroup sums
   NormRegs nr;
   auto x_block = [&](int q) { return a.x + (size_t)(q / nb) * a.k + (size_t)(q % nb) * kQK; };
   if (NORM) {
