@@ -91,9 +91,14 @@ def algorithmic_bytes(workload: str, m: int) -> int:
     return b
 
 
-def matvec_kernel_name(choice: str, k: int, m: int, rows: list) -> str:
-    """The matvec kernel the runner picks for one launch (its automatic
-    policy restated: tile counts of the vector-ALU and matrix-core layouts)."""
+def matvec_kernel_name(choice: str, k: int, m: int, specs: list) -> str:
+    """The matvec kernel the runner picks for one launch of weights specs
+    [(type, rows)] (its automatic policy restated: tile counts of the
+    vector-ALU and matrix-core layouts; the weight-type template argument is
+    the launch's common type id, 0 when the types differ)."""
+    rows = [r for _, r in specs]
+    types = {TYPE_IDS[t] for t, _ in specs}
+    type_id = types.pop() if len(types) == 1 else 0
     nb = k // 256
     s = next(d for d in range(min(nb, 64), 0, -1) if nb % d == 0 and ((64 // d) * d >= 48 or d == 1))
     r6 = 64 // s
@@ -103,10 +108,10 @@ def matvec_kernel_name(choice: str, k: int, m: int, rows: list) -> str:
     mfma = choice == "mfma" or (choice == "auto" and not half and k <= 2560 and
                                 (m >= 5 or (m >= 2 and tiles16 >= 1024)))
     if half:
-        return f"kquant_matvec_half_kernel<{m}, 0>"
+        return f"kquant_matvec_half_kernel<{m}, 0, {type_id}>"
     if mfma:
         return "kquant_mfma_kernel"
-    return f"kquant_matvec_kernel<{m}, {'true' if m <= 3 else 'false'}, false, 0>"
+    return f"kquant_matvec_kernel<{m}, {'true' if m <= 3 else 'false'}, false, 0, {type_id if m <= 3 else 0}>"
 
 
 def parse() -> argparse.Namespace:
@@ -776,7 +781,7 @@ def main() -> int:
         cpu = cpu_baseline(wl, ws, x_host, args.cpu_seconds)
 
     kernels = {"ffn": "gate/up+GeGLU matvec + down matvec", "head": "matvec + top-k"}
-    kernel_name = matvec_kernel_name(args.kernel, k, m, [r for _, r in specs])
+    kernel_name = matvec_kernel_name(args.kernel, k, m, specs)
     line = {
         "metric": METRIC,
         "value": round(value, 2),

@@ -673,7 +673,7 @@ __device__ __forceinline__ void q6k_ints_half(const HalfRegs &rg, const uint8_t 
     for (int l = 0; l < 4; l++) aux[m][l] >>= 2;  // weights carried 4 * (q6 - 32)
 }
 
-template <int M, int NORM>
+template <int M, int NORM, int TYPE>
 __global__ __launch_bounds__(256) void kquant_matvec_half_kernel(const MatvecArgs a) {
   extern __shared__ __align__(16) uint8_t smem[];
   const TileGeom g = a.g;
@@ -706,7 +706,7 @@ __global__ __launch_bounds__(256) void kquant_matvec_half_kernel(const MatvecArg
     if (a.count > 1 && u >= a.w[1].unit_begin) n.W = a.w[1];
     if (a.count > 2 && u >= a.w[2].unit_begin) n.W = a.w[2];
     if (a.count > 3 && u >= a.w[3].unit_begin) n.W = a.w[3];
-    n.q4 = n.W.type == kTypeQ4K;
+    n.q4 = TYPE == kTypeQ4K ? true : TYPE == kTypeQ6K ? false : n.W.type == kTypeQ4K;
     n.CH = n.q4 ? 9 : 13;
     n.row = (u - n.W.unit_begin) * Rh + rr;
     n.active = real && rr < Rh && n.row < n.W.rows && grp2 < 2 * Rh;
@@ -717,20 +717,22 @@ __global__ __launch_bounds__(256) void kquant_matvec_half_kernel(const MatvecArg
     n.tile = n.W.data + (size_t)n.t * R * nb * n.CH * 16;
     return n;
   };
+  // No branch on the type: a Q4_K unit issues 5 loads, a Q6_K unit 8; in a
+  // mixed launch (TYPE 0) a Q4_K unit also issues the 3 Q6_K-only loads at
+  // its chunk 0, so both paths leave the same count in flight and a wait for
+  // an earlier load never waits for these.
   auto load_unit = [&](HalfRegs &rg, const Unit &n, int it) {
     const uint4 *ch = reinterpret_cast<const uint4 *>(n.tile + ((size_t)it * n.CH * n.Rt * S + n.k) * 16);
     const size_t cs = (size_t)n.Rt * S;  // uint4 stride between chunks
     rg.c0 = ch[(n.q4 ? 0 : 12) * cs];
-    if (n.q4) {
 #pragma unroll
-      for (int p = 0; p < 4; p++) rg.d[p] = ch[(1 + 2 * p + h) * cs];
-    } else {
+    for (int p = 0; p < 4; p++) rg.d[p] = ch[(n.q4 ? 1 + 2 * p + h : 2 * p + h) * cs];
+    if (TYPE == kTypeQ4K) return;
 #pragma unroll
-      for (int p = 0; p < 4; p++) rg.d[p] = ch[(2 * p + h) * cs];
-#pragma unroll
-      for (int p = 0; p < 2; p++) rg.e[p] = ch[(8 + 2 * p + h) * cs];
-      rg.d6 = n.W.dplane[(size_t)n.t * R * nb + (size_t)it * n.Rt * S + n.k];
-    }
+    for (int p = 0; p < 2; p++) rg.e[p] = ch[(n.q4 ? 0 : 8 + 2 * p + h) * cs];
+    const uint16_t *dp = n.q4 ? reinterpret_cast<const uint16_t *>(ch)
+                              : n.W.dplane + (size_t)n.t * R * nb + (size_t)it * n.Rt * S + n.k;
+    rg.d6 = *dp;
   };
 
   // prologue inputs of up to three passes first, then the first unit's first
@@ -854,17 +856,29 @@ __global__ __launch_bounds__(256) void kquant_matvec_half_kernel(const MatvecArg
   }
 }
 
-static size_t matvec_lds_bytes(int cols, const TileGeom &g, int wpg) {
-  (void)wpg;
-  return (size_t)cols * g.nb * kQ8BlockBytes + (size_t)((cols * g.nb + 3) & ~3) * 4;
-}
-
 // The weight type shared by every weight of the launch, or 0.
 static int uniform_type(const MatvecArgs &a) {
   for (int i = 1; i < a.count; i++)
     if (a.w[i].type != a.w[0].type) return 0;
   return a.w[0].type == kTypeQ4K || a.w[0].type == kTypeQ6K ? a.w[0].type : 0;
 }
+
+template <int M, int NORM>
+static void launch_half_typed(const MatvecArgs &a, dim3 grid, size_t lds, hipStream_t s) {
+  const int t = uniform_type(a);
+  if (t == kTypeQ4K)
+    hipLaunchKernelGGL((kquant_matvec_half_kernel<M, NORM, kTypeQ4K>), grid, dim3(256), lds, s, a);
+  else if (t == kTypeQ6K)
+    hipLaunchKernelGGL((kquant_matvec_half_kernel<M, NORM, kTypeQ6K>), grid, dim3(256), lds, s, a);
+  else
+    hipLaunchKernelGGL((kquant_matvec_half_kernel<M, NORM, 0>), grid, dim3(256), lds, s, a);
+}
+
+static size_t matvec_lds_bytes(int cols, const TileGeom &g, int wpg) {
+  (void)wpg;
+  return (size_t)cols * g.nb * kQ8BlockBytes + (size_t)((cols * g.nb + 3) & ~3) * 4;
+}
+
 
 template <int M, bool PAIR, int NORM>
 static void launch_typed(const MatvecArgs &a, dim3 grid, size_t lds, hipStream_t s) {
@@ -906,11 +920,11 @@ static hipError_t launch_half_m(const MatvecArgs &a, int num_cus, hipStream_t s)
   if (grid > cap) grid = cap;
   const size_t lds = matvec_lds_bytes(M, a.g, wpg);
   if (M == 1 && a.norm.mode == 1)
-    hipLaunchKernelGGL((kquant_matvec_half_kernel<1, 1>), dim3(grid), dim3(64 * wpg), lds, s, a);
+    launch_half_typed<1, 1>(a, dim3(grid), lds, s);
   else if (M == 1 && a.norm.mode == 2)
-    hipLaunchKernelGGL((kquant_matvec_half_kernel<1, 2>), dim3(grid), dim3(64 * wpg), lds, s, a);
+    launch_half_typed<1, 2>(a, dim3(grid), lds, s);
   else
-    hipLaunchKernelGGL((kquant_matvec_half_kernel<M, 0>), dim3(grid), dim3(64 * wpg), lds, s, a);
+    launch_half_typed<M, 0>(a, dim3(grid), lds, s);
   return hipGetLastError();
 }
 
