@@ -351,19 +351,18 @@ __device__ __forceinline__ void process_block(Chains (&ch)[NSET], const Seg<Q4> 
 template <int NSET, bool Q4>
 __device__ __forceinline__ void run_tile(Chains (&ch)[NSET], const uint8_t *seg, size_t bstride, const Lds &L,
                                          int nb, int lane) {
-  Seg<Q4> r0 = load_seg<Q4>(seg, lane), r1, r2;
-  if (nb > 1) r1 = load_seg<Q4>(seg + bstride, lane);
+  // every load unconditional (a block index past the last re-reads it): a
+  // path that skipped a load would turn the wait for one block into a wait
+  // for the blocks loaded after it
+  auto blk = [&](int b) { return seg + (size_t)min(b, nb - 1) * bstride; };
+  Seg<Q4> r0 = load_seg<Q4>(blk(0), lane), r1 = load_seg<Q4>(blk(1), lane), r2;
   for (int b = 0; b < nb; b += 3) {
-    if (b + 2 < nb) r2 = load_seg<Q4>(seg + (size_t)(b + 2) * bstride, lane);
+    r2 = load_seg<Q4>(blk(b + 2), lane);
     process_block<NSET, Q4>(ch, r0, L, b, nb, lane);
-    if (b + 1 < nb) {
-      if (b + 3 < nb) r0 = load_seg<Q4>(seg + (size_t)(b + 3) * bstride, lane);
-      process_block<NSET, Q4>(ch, r1, L, b + 1, nb, lane);
-    }
-    if (b + 2 < nb) {
-      if (b + 4 < nb) r1 = load_seg<Q4>(seg + (size_t)(b + 4) * bstride, lane);
-      process_block<NSET, Q4>(ch, r2, L, b + 2, nb, lane);
-    }
+    r0 = load_seg<Q4>(blk(b + 3), lane);
+    if (b + 1 < nb) process_block<NSET, Q4>(ch, r1, L, b + 1, nb, lane);
+    r1 = load_seg<Q4>(blk(b + 4), lane);
+    if (b + 2 < nb) process_block<NSET, Q4>(ch, r2, L, b + 2, nb, lane);
   }
 }
 
@@ -410,11 +409,27 @@ __global__ __launch_bounds__(256) void kquant_mfma_kernel(const MfmaArgs a) {
   const int grp = wave * 4 + (lane >> 4), i16 = lane & 15;
   const int nq = 4 * NSET * nb;
   if (threadIdx.x < 4) reinterpret_cast<uint32_t *>(L.zero)[threadIdx.x] = 0;
-  for (int qb = grp; qb < nq; qb += 16) {
+  // the inputs of the first three passes load together, before any pass
+  // (a block past the last, or of a column past `cols`, re-reads a valid one
+  // and is not used)
+  auto x_of = [&](int qb) {
+    const int qc = min(qb, nq - 1), m = qc / nb, b = qc - m * nb;
+    return a.x + (size_t)min(m, a.cols - 1) * a.k + (size_t)b * kQK;
+  };
+  float xp[3][16];
+#pragma unroll
+  for (int p = 0; p < 3; p++) load_x16_(xp[p], x_of(grp + 16 * p), i16);
+  __builtin_amdgcn_sched_barrier(0);
+  for (int qb = grp, p = 0; qb < nq; qb += 16, p++) {
     const int m = qb / nb, b = qb - m * nb;
     if (m < a.cols) {
       float xv[16];
-      load_x16_(xv, a.x + (size_t)m * a.k + (size_t)b * kQK, i16);
+      if (p < 3) {
+#pragma unroll
+        for (int i = 0; i < 16; i++) xv[i] = p == 0 ? xp[0][i] : p == 1 ? xp[1][i] : xp[2][i];
+      } else {
+        load_x16_(xv, a.x + (size_t)m * a.k + (size_t)b * kQK, i16);
+      }
       q8k_block16_f16(xv, i16, L, 4 * NSET, m, b);
     } else {
       // 16 lanes clear the region's 8 classes of 64 data bytes
