@@ -272,7 +272,7 @@ bool use_half(int cols, const TileGeom &g, int tiles) {
 // One matvec launch per column chunk covering every weight (multi == one
 // launch, lib.rs:300-426); each launch quantises its columns in its prologue.
 int32_t run_norm(const float *y, int rows, int n, const float *w_post, const float *x_res, float scale, float *x_out,
-                 const float *w_next, float *next_out, double eps, hipStream_t stream);
+                 const float *w_next, float *next_out, double eps, hipStream_t stream, uint8_t *q8img = nullptr);
 
 // Whether a one-column launch over these weights runs a vector-ALU kernel,
 // which can form its input with the norm prologue.
@@ -283,21 +283,38 @@ bool norm_prologue_ok(size_t count, Handle *const *hs, size_t cols) {
   return !use_mfma(cols, hs[0]->g.nb, tiles16);
 }
 
+// Whether a launch of `cols` columns (4 or more) runs the vector-ALU kernels
+// in one chunk, so it can take its input as a pre-quantised image.
+bool image_input_ok(size_t count, Handle *const *hs, size_t cols) {
+  if (cols < 4 || prefill_kind(cols) != 0) return false;
+  int tiles16 = 0;
+  for (size_t i = 0; i < count; i++) tiles16 += (int)((hs[i]->row_count + 15) / 16);
+  return !use_mfma(cols, hs[0]->g.nb, tiles16) && cols_per_launch(hs[0]->g, st().max_lds) >= (int)cols;
+}
+
 // norm != null: the input is formed from a residual stream (NormIn) -- in the
 // launch's prologue when the launch runs a vector-ALU kernel, else by the norm
 // kernel into norm_scratch first.
+// q8img_in (4 or more columns): the input already quantised, as written by
+// the norm or GeGLU kernels (q8_image_bytes(cols, nb)); used when the launch
+// runs the vector-ALU kernels in one chunk.  img_scratch: where a norm run
+// here writes that image for the launch.
 int32_t run_matvec(size_t count, Handle *const *hs, const float *d_input, size_t input_size, size_t cols,
                    float *const *d_outs, hipStream_t stream, const NormIn *norm = nullptr,
-                   float *norm_scratch = nullptr) {
+                   float *norm_scratch = nullptr, uint8_t *img_scratch = nullptr, const uint8_t *q8img_in = nullptr) {
   State &s = st();
   if (cols == 0) return HP_OK;
+  const bool image_ok = cols >= 4 && image_input_ok(count, hs, cols);
   if (norm && !norm_prologue_ok(count, hs, cols)) {
+    uint8_t *img = image_ok && img_scratch ? img_scratch : nullptr;
     int32_t rc = run_norm(norm->y, (int)cols, (int)input_size, norm->w_post, norm->mode == 2 ? norm->x_res : nullptr,
-                          norm->scale, norm->x_out, norm->w_next, norm_scratch, norm->eps, stream);
+                          norm->scale, norm->x_out, norm->w_next, norm_scratch, norm->eps, stream, img);
     if (rc != HP_OK) return rc;
     d_input = norm_scratch;
     norm = nullptr;
+    q8img_in = img;
   }
+  if (!image_ok) q8img_in = nullptr;
   const TileGeom g = hs[0]->g;
   MatvecArgs a{};
   if (norm) a.norm = *norm;
@@ -380,6 +397,7 @@ int32_t run_matvec(size_t count, Handle *const *hs, const float *d_input, size_t
   }
   const int chunk = cols_per_launch(g, s.max_lds);
   if (chunk <= 0) return fail(HP_ERR_SHAPE, "input_size too large for the matvec LDS budget");
+  a.q8img = q8img_in;  // one chunk (image_input_ok)
   for (size_t m0 = 0; m0 < cols; m0 += (size_t)chunk) {
     const int c = (int)((cols - m0) < (size_t)chunk ? (cols - m0) : (size_t)chunk);
     a.x = d_input + m0 * input_size;
@@ -402,9 +420,13 @@ int32_t run_matvec(size_t count, Handle *const *hs, const float *d_input, size_t
 // kernel on this launch (one column of large projections); otherwise the
 // projections (one launch, any kernel) into scratch, then the GeGLU kernel.
 // Both give the same bits.
+// q8img_out (4 or more columns): when the GeGLU runs as its own launch it also
+// writes d_out as a matvec input image there, and *q8img_written says so.
 int32_t run_matvec_geglu(Handle *hg, Handle *hu, const float *d_input, size_t input_size, size_t cols,
                          float *d_out, hipStream_t stream, const NormIn *norm = nullptr,
-                         float *norm_scratch = nullptr) {
+                         float *norm_scratch = nullptr, uint8_t *q8img_out = nullptr,
+                         bool *q8img_written = nullptr) {
+  if (q8img_written) *q8img_written = false;
   State &s = st();
   if (cols == 0) return HP_OK;
   const size_t rows = hg->row_count;
@@ -456,7 +478,12 @@ int32_t run_matvec_geglu(Handle *hg, Handle *hu, const float *d_input, size_t in
   rc = run_matvec(2, hs, d_input, input_size, cols, outs, stream);
   if (rc != HP_OK) return rc;
   hipEvent_t e2 = prof_begin(stream);
-  HP_HIP_TRY(launch_geglu(outs[0], outs[1], cols * rows, gelu_constant(), d_out, s.num_cus, stream));
+  if (q8img_out && cols >= 4 && rows % kQK == 0) {
+    HP_HIP_TRY(launch_geglu_q8k(outs[0], outs[1], (int)rows, (int)cols, gelu_constant(), d_out, q8img_out, stream));
+    if (q8img_written) *q8img_written = true;
+  } else {
+    HP_HIP_TRY(launch_geglu(outs[0], outs[1], cols * rows, gelu_constant(), d_out, s.num_cus, stream));
+  }
   prof_end(HP_KERNEL_GEGLU, e2, stream);
   s.launches++;
   return HP_OK;
@@ -760,8 +787,9 @@ int32_t run_attention(AttnArgs a, float *partials, hipStream_t stream) {
 }
 
 int32_t run_norm(const float *y, int rows, int n, const float *w_post, const float *x_res, float scale, float *x_out,
-                 const float *w_next, float *next_out, double eps, hipStream_t stream) {
+                 const float *w_next, float *next_out, double eps, hipStream_t stream, uint8_t *q8img) {
   NormArgs a{};
+  a.q8img = q8img;
   a.y = y;
   a.w_post = w_post;
   a.x_res = x_res;
@@ -1575,24 +1603,30 @@ int32_t hp_hip_decode_layers_device(const hp_hip_decode_layer_t *layers, size_t 
   if (hidden == 0 || hidden > kNormMaxN) return fail(HP_ERR_SHAPE, "hidden size must be 1..4096");
   // scratch ([M] rows each): xn, q, k, v, q after RoPE, attention, o, x1, h, y;
   // attention partials; RoPE tables [M][128] cos, sin
+  // (4 or more tokens) the Q/K/V and down inputs as pre-quantised images
   auto al = [](size_t n) { return (n + 63) & ~(size_t)63; };
-  const size_t sizes[12] = {al(M * hidden), al(M * qmax),   al(M * kvmax),  al(M * kvmax),
+  const size_t img_x = M >= 4 ? q8_image_bytes((int)M, (int)(hidden / kQK)) / sizeof(float) : 0;
+  const size_t img_h = M >= 4 ? q8_image_bytes((int)M, (int)(ffmax / kQK)) / sizeof(float) : 0;
+  const size_t sizes[14] = {al(M * hidden), al(M * qmax),   al(M * kvmax),  al(M * kvmax),
                             al(M * qmax),   al(M * qmax),   al(M * hidden), al(M * hidden),
-                            al(M * ffmax),  al(M * hidden), al(partials),   al(M * kHeadDim / 2 * 4)};
+                            al(M * ffmax),  al(M * hidden), al(partials),   al(M * kHeadDim / 2 * 4),
+                            al(img_x),      al(img_h)};
   size_t total = 0;
   for (size_t z : sizes) total += z;
   hipStream_t strm = stream ? static_cast<hipStream_t>(stream) : s.stream;
   rc = grow_uncaptured(&s.decode_scratch, &s.decode_scratch_cap, total * sizeof(float), strm);
   if (rc != HP_OK) return rc;
-  float *buf[12];
+  float *buf[14];
   float *p = static_cast<float *>(s.decode_scratch);
-  for (int i = 0; i < 12; i++) {
+  for (int i = 0; i < 14; i++) {
     buf[i] = p;
     p += sizes[i];
   }
   float *xn = buf[0], *q = buf[1], *k = buf[2], *v = buf[3], *qr = buf[4], *att = buf[5], *o = buf[6],
         *x1 = buf[7], *h = buf[8], *y = buf[9], *part = buf[10];
   double2 *rope_table = reinterpret_cast<double2 *>(buf[11]);
+  uint8_t *imgx = M >= 4 && hidden % kQK == 0 ? reinterpret_cast<uint8_t *>(buf[12]) : nullptr;
+  uint8_t *imgh = M >= 4 && ffmax % kQK == 0 ? reinterpret_cast<uint8_t *>(buf[13]) : nullptr;
   // The norms ride in the prologues of the launches that consume them (one
   // token): the Q/K/V launch forms attn_norm(previous residual), the gate/up
   // launch ffn_norm(residual after attention).  With several tokens, or a
@@ -1609,7 +1643,7 @@ int32_t hp_hip_decode_layers_device(const hp_hip_decode_layer_t *layers, size_t 
     const double eps = L.attention.epsilon;
     Handle *qkv[3] = {H.q, H.k, H.v};
     float *qkv_out[3] = {q, k, v};
-    rc = run_matvec(H.v ? 3 : 2, qkv, nullptr, hidden, M, qkv_out, strm, &nin, xn);
+    rc = run_matvec(H.v ? 3 : 2, qkv, nullptr, hidden, M, qkv_out, strm, &nin, xn, imgx);
     if (rc != HP_OK) return rc;
     // the RoPE angles depend on the positions and the RoPE parameters only:
     // a layer whose parameters match the previous layer's reads its table
@@ -1670,11 +1704,12 @@ int32_t hp_hip_decode_layers_device(const hp_hip_decode_layer_t *layers, size_t 
     fin.x_out = x1;
     fin.w_next = L.d_ffn_norm;
     fin.eps = eps;
-    rc = run_matvec_geglu(H.gate, H.up, nullptr, hidden, M, h, strm, &fin, xn);
+    bool h_img = false;
+    rc = run_matvec_geglu(H.gate, H.up, nullptr, hidden, M, h, strm, &fin, xn, imgh, &h_img);
     if (rc != HP_OK) return rc;
     Handle *dh[1] = {H.down};
     float *yo[1] = {y};
-    rc = run_matvec(1, dh, h, H.down->input_size, M, yo, strm);
+    rc = run_matvec(1, dh, h, H.down->input_size, M, yo, strm, nullptr, nullptr, nullptr, h_img ? imgh : nullptr);
     if (rc != HP_OK) return rc;
     nin.mode = 2;
     nin.y = y;

@@ -35,6 +35,7 @@
 #include "hp_common.h"
 #include "hp_gelu.h"
 #include "hp_wave.h"
+#include "hp_q8k16.h"
 
 namespace hp {
 
@@ -153,11 +154,30 @@ __global__ __launch_bounds__(256) void norm_residual_kernel(const NormArgs a) {
   }
   if (a.next_out) {
     const double sc = rms_scale(v, a.n, a.eps, sh + 4);
+    __shared__ float xs[256 * kNormPer];  // the row, for the image below
 #pragma unroll
     for (int j = 0; j < kNormPer; j++) {
       const int i = tid + 256 * j;
-      if (i < a.n)
-        a.next_out[row + i] = a.w_next ? (float)(((double)v[j] * sc) * (double)wn[j]) : (float)((double)v[j] * sc);
+      const float o = a.w_next ? (float)(((double)v[j] * sc) * (double)wn[j]) : (float)((double)v[j] * sc);
+      if (i < a.n) a.next_out[row + i] = o;
+      if (a.q8img) xs[i] = o;
+    }
+    if (a.q8img) {
+      // the row as Q8_K blocks of a matvec input image (n a multiple of 256):
+      // 16-lane group g quantises block g
+      __syncthreads();
+      const int g = tid >> 4, i16 = tid & 15, nb = a.n / kQK;
+      if (g < nb) {
+        float xv[16];
+        const int jj = i16 >> 1, u = i16 & 1;
+#pragma unroll
+        for (int c = 0; c < 4; c++)
+#pragma unroll
+          for (int i = 0; i < 4; i++) xv[4 * c + i] = xs[g * kQK + 32 * jj + 8 * c + 4 * u + i];
+        const size_t q = (size_t)blockIdx.x * nb + g;
+        q8k_block16(xv, i16, a.q8img + q * kQ8BlockBytes,
+                    reinterpret_cast<float *>(a.q8img + (size_t)a.rows * nb * kQ8BlockBytes) + q);
+      }
     }
   }
 }
@@ -653,6 +673,7 @@ __global__ __launch_bounds__(256) void attn_reduce_kernel(const AttnArgs a) {
 
 hipError_t launch_norm_residual(const NormArgs &a, hipStream_t s) {
   if (a.n < 1 || a.n > 256 * kNormPer || a.rows < 1) return hipErrorInvalidValue;
+  if (a.q8img && (a.n % kQK != 0 || !a.next_out)) return hipErrorInvalidValue;
   hipLaunchKernelGGL(norm_residual_kernel, dim3(a.rows), dim3(256), 0, s, a);
   return hipGetLastError();
 }

@@ -10,6 +10,7 @@
 // as Math.sqrt(2 / Math.PI) is (correctly rounded f64).
 #include "hp_common.h"
 #include "hp_gelu.h"
+#include "hp_q8k16.h"
 
 namespace hp {
 
@@ -17,6 +18,40 @@ __global__ __launch_bounds__(256) void geglu_kernel(const float *__restrict__ ga
                                                     size_t n, double c, float *__restrict__ out) {
   for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x)
     out[i] = geglu_ts(gate[i], up[i], c);
+}
+
+// One workgroup per 256-element block of one column: each thread takes one
+// element's GeGLU (stored to out and to LDS), then one 16-lane group
+// quantises the block from LDS into the image.
+__global__ __launch_bounds__(256) void geglu_q8k_kernel(const float *__restrict__ gate, const float *__restrict__ up,
+                                                        int rows, int blocks, double c, float *__restrict__ out,
+                                                        uint8_t *__restrict__ img) {
+  __shared__ float hs[kQK];
+  const int q = blockIdx.x, t = threadIdx.x;
+  const int nb = rows / kQK, m = q / nb, b = q - m * nb;
+  const size_t off = (size_t)m * rows + (size_t)b * kQK;
+  const float h = geglu_ts(gate[off + t], up[off + t], c);
+  out[off + t] = h;
+  hs[t] = h;
+  __syncthreads();
+  if (t < 16) {
+    float v[16];
+    const int j = t >> 1, u = t & 1;
+#pragma unroll
+    for (int cc = 0; cc < 4; cc++)
+#pragma unroll
+      for (int i = 0; i < 4; i++) v[4 * cc + i] = hs[32 * j + 8 * cc + 4 * u + i];
+    q8k_block16(v, t, img + (size_t)q * kQ8BlockBytes,
+                reinterpret_cast<float *>(img + (size_t)blocks * kQ8BlockBytes) + q);
+  }
+}
+
+hipError_t launch_geglu_q8k(const float *gate, const float *up, int rows, int cols, double c, float *out,
+                            uint8_t *q8img, hipStream_t s) {
+  if (rows <= 0 || rows % kQK != 0 || cols < 1) return hipErrorInvalidValue;
+  const int blocks = cols * (rows / kQK);
+  hipLaunchKernelGGL(geglu_q8k_kernel, dim3((unsigned)blocks), dim3(256), 0, s, gate, up, rows, blocks, c, out, q8img);
+  return hipGetLastError();
 }
 
 hipError_t launch_geglu(const float *gate, const float *up, size_t n, double c, float *out, int num_cus,

@@ -96,7 +96,18 @@ struct MatvecArgs {
   int Rh;             // half-split kernel: rows per unit (floor(32 / S))
   float *pair_out;    // gate/up + GeGLU launch: [cols][rows] output
   double gelu_c;      // sqrt(2 / pi) as Math.sqrt(2 / Math.PI)
+  // non-null (launches of 4 or more columns): the input already quantised,
+  // as the LDS image of this launch's columns (q8_image_bytes(cols, nb)),
+  // copied in place of the Q8_K prologue
+  const uint8_t *q8img;
 };
+
+// The vector-ALU matvec's LDS image of `cols` quantised input columns: the
+// cols * nb Q8_K blocks (kQ8BlockBytes each, column-major) and then their
+// cols * nb f32 scales, padded to 16 bytes.
+__host__ __device__ constexpr size_t q8_image_bytes(int cols, int nb) {
+  return (size_t)cols * nb * kQ8BlockBytes + (size_t)((cols * nb + 3) & ~3) * 4;
+}
 
 // Launchers (return hipError_t of the launch).
 hipError_t launch_q8k_natural(const float *x, int k, int cols, int8_t *qs, float *d, int16_t *bsums,
@@ -167,6 +178,10 @@ size_t prefill_fast_bytes(int k, int cols);
 size_t prefill_fast_lds_bytes();
 hipError_t launch_prefill_fast(const MfmaLaunch &l, const float *x, uint8_t *scratch, int num_cus, hipStream_t s);
 
+// GeGLU of cols columns of `rows` (a multiple of 256) that also writes the
+// result as a matvec input image (q8_image_bytes(cols, rows / 256)).
+hipError_t launch_geglu_q8k(const float *gate, const float *up, int rows, int cols, double c, float *out,
+                            uint8_t *q8img, hipStream_t s);
 hipError_t launch_geglu(const float *gate, const float *up, size_t n, double c, float *out, int num_cus,
                         hipStream_t s);
 
@@ -184,6 +199,7 @@ constexpr int kMaxTokens = 8;     // tokens per decode call (a draft to verify)
 struct NormArgs {
   const float *y, *w_post, *x_res, *w_next;
   float *x_out, *next_out;
+  uint8_t *q8img;  // non-null: next_out also as a matvec input image (q8_image_bytes(rows, n / 256))
   float scale;
   int n, rows;
   double eps;

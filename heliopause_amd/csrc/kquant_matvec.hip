@@ -27,6 +27,7 @@
 #include "hp_gelu.h"
 #include "hp_q8k.h"
 #include "hp_wave.h"
+#include "hp_q8k16.h"
 
 namespace hp {
 
@@ -49,10 +50,6 @@ __device__ __forceinline__ int dppi(int v) {
   return __builtin_amdgcn_update_dpp(0, v, CTRL, 0xf, 0xf, false);
 }
 
-constexpr int kDppQuadXor1 = 0xB1;   // quad_perm [1,0,3,2]
-constexpr int kDppQuadXor2 = 0x4E;   // quad_perm [2,3,0,1]
-constexpr int kDppHalfMirror = 0x141;  // row_half_mirror
-constexpr int kDppMirror = 0x140;      // row_mirror
 constexpr int kDppWaveShr1 = 0x138;    // wave_shr:1
 
 __device__ __forceinline__ uint32_t u4get(const uint4 &v, int i) {
@@ -233,30 +230,6 @@ __device__ __forceinline__ void q6k_ints(const Regs &rg, const uint8_t *xq, int 
     for (int l = 0; l < 8; l++) aux[m][l] >>= 2;  // weights carried 4 * (q6 - 32)
 }
 
-// Q8_K of block (m, b) by one 16-lane DPP row (lib.rs:1774-1811).  Lane
-// i16 = 2j + u owns the 16 elements 32j + 8c + 4u + i (c, i = 0..3), i.e.
-// bytes 32j + 16u .. +15 of the transposed layout, so its quants are one
-// 16-byte LDS store; its elements are scanned in increasing index order.
-__device__ __forceinline__ void load_x16(float (&v)[16], const float *__restrict__ xb, int i16) {
-  const int j = i16 >> 1, u = i16 & 1;
-#pragma unroll
-  for (int c = 0; c < 4; c++) {
-    const float4 f = *reinterpret_cast<const float4 *>(xb + 32 * j + 8 * c + 4 * u);
-    v[4 * c] = f.x;
-    v[4 * c + 1] = f.y;
-    v[4 * c + 2] = f.z;
-    v[4 * c + 3] = f.w;
-  }
-}
-
-__device__ __forceinline__ void store_x16(float *__restrict__ xb, const float (&v)[16], int i16) {
-  const int j = i16 >> 1, u = i16 & 1;
-#pragma unroll
-  for (int c = 0; c < 4; c++)
-    *reinterpret_cast<float4 *>(xb + 32 * j + 8 * c + 4 * u) = make_float4(v[4 * c], v[4 * c + 1], v[4 * c + 2],
-                                                                           v[4 * c + 3]);
-}
-
 // Norm prologue of a one-column launch (NormIn, hp_common.h): group grp < nb
 // of 16 lanes holds block grp in load_x16's element order; the sums of
 // squares are f64 sums over the workgroup (256 threads).
@@ -317,69 +290,6 @@ __device__ __forceinline__ void norm_finish(const NormIn &n, NormRegs &nr, float
   for (int i = 0; i < 16; i++) xv[i] = (float)(((double)nr.y[i] * sc) * (double)nr.wn[i]);
 }
 
-// One butterfly step of the (|x| desc, index asc) maximum with the partner
-// lane selected by the DPP control.
-template <int CTRL>
-__device__ __forceinline__ void lexmax_step(float &amax, float &vmax, int &idx) {
-  const float oa = dppf<CTRL>(amax);
-  const float ov = dppf<CTRL>(vmax);
-  const int oi = dppi<CTRL>(idx);
-  const bool take = oa > amax || (oa == amax && oi < idx);
-  amax = take ? oa : amax;
-  vmax = take ? ov : vmax;
-  idx = take ? oi : idx;
-}
-
-__device__ __forceinline__ void q8k_block16(const float (&v)[16], int i16, uint8_t *blk, float *dptr) {
-  const int j = i16 >> 1, u = i16 & 1;
-  float amax = 0.0f, vmax = 0.0f;
-  int idx = 0x7fffffff;
-#pragma unroll
-  for (int c = 0; c < 4; c++)
-#pragma unroll
-    for (int i = 0; i < 4; i++) {
-      const float x = v[4 * c + i];
-      const float av = fabsf(x);
-      const bool gt = av > amax;  // strictly greater: the first maximum wins
-      amax = gt ? av : amax;
-      vmax = gt ? x : vmax;
-      idx = gt ? 32 * j + 8 * c + 4 * u + i : idx;
-    }
-  // (amax desc, idx asc) across the 16 lanes of the row
-  lexmax_step<kDppQuadXor1>(amax, vmax, idx);
-  lexmax_step<kDppQuadXor2>(amax, vmax, idx);
-  lexmax_step<kDppHalfMirror>(amax, vmax, idx);
-  lexmax_step<kDppMirror>(amax, vmax, idx);
-  const bool nz = amax != 0.0f;
-  const float inv = __fdiv_rn(-127.0f, vmax);
-  uint32_t word[4];
-  int sum = 0;
-#pragma unroll
-  for (int l4 = 0; l4 < 4; l4++) {
-    int q[4];
-#pragma unroll
-    for (int c = 0; c < 4; c++) {
-      // Rust: (is * x).round().min(127.0) as i8.  |is * x| <= 127 (1 + 2^-23)
-      // for every element, so the saturating cast never acts; NaN -> min()
-      // -> 127.  round() (half away from zero) as trunc(p + copysign(0.5 -
-      // 2^-25, p)): equal for every f32 |p| < 128 (checked exhaustively);
-      // the int conversion truncates, and truncation commutes with min(., 127).
-      const float p = __fmul_rn(inv, v[4 * c + l4]);
-      q[c] = (int)fminf(__fadd_rn(p, copysignf(0.49999997f, p)), 127.0f);
-    }
-    // bytes q0..q3 (low to high): the low bytes of two packed int16 pairs
-    const uint32_t lo = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pk_i16(q[0], q[1]));
-    const uint32_t hi = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pk_i16(q[2], q[3]));
-    const uint32_t wv = __builtin_amdgcn_perm(hi, lo, 0x06040200u);
-    word[l4] = nz ? wv : 0u;  // dword l = 4u + l4 of sub-block j
-    sum = __builtin_amdgcn_sdot4((int)word[l4], 0x01010101, sum, false);
-  }
-  sum += dppi<kDppQuadXor1>(sum);
-  *reinterpret_cast<uint4 *>(blk + 32 * j + 16 * u) = make_uint4(word[0], word[1], word[2], word[3]);
-  if (u == 0) reinterpret_cast<int16_t *>(blk + 256)[j] = (int16_t)sum;
-  if (i16 == 0) *dptr = nz ? __fdiv_rn(1.0f, inv) : 0.0f;
-}
-
 // lane L receives lane L-1's value (DPP wave_shr:1).
 __device__ __forceinline__ float shr1(float v) {
   return dppf<kDppWaveShr1>(v);
@@ -413,9 +323,12 @@ __global__ __launch_bounds__(256) void kquant_matvec_kernel(const MatvecArgs a) 
   __shared__ double norm_sh[8];  // two workgroup sums
   NormRegs nr;
   auto x_block = [&](int q) { return a.x + (size_t)(q / nb) * a.k + (size_t)(q % nb) * kQK; };
+  // four or more columns may come already quantised (a.q8img): the image
+  // is copied in place of the Q8_K passes
+  const bool pre = M >= 4 && a.q8img != nullptr;
   if (NORM) {
     norm_load<NORM>(a.norm, nr, grp, nb, i16);
-  } else {
+  } else if (!pre) {
     // every pass's input before the weights: vector loads return in order,
     // so a pass loaded after them would wait for the weights
     if (grp < nq) load_x16(xv, x_block(grp), i16);
@@ -444,7 +357,11 @@ __global__ __launch_bounds__(256) void kquant_matvec_kernel(const MatvecArgs a) 
   __builtin_amdgcn_sched_barrier(0);  // keep the prologue's work after the weight loads
   if (NORM) norm_finish<NORM>(a.norm, nr, xv, grp, nb, i16, a.k, norm_sh);
 
-  {
+  if (pre) {
+    const int n16 = (int)(q8_image_bytes(M, nb) / 16);
+    const uint4 *src = reinterpret_cast<const uint4 *>(a.q8img);
+    for (int i = threadIdx.x; i < n16; i += blockDim.x) reinterpret_cast<uint4 *>(smem)[i] = src[i];
+  } else {
     int q = grp;
     if (q < nq) q8k_block16(xv, i16, xq + (size_t)q * kQ8BlockBytes, xd + q);
     q += wpg * 4;
@@ -745,9 +662,12 @@ __global__ __launch_bounds__(256) void kquant_matvec_half_kernel(const MatvecArg
   __shared__ double norm_sh[8];  // two workgroup sums
   NormRegs nr;
   auto x_block = [&](int q) { return a.x + (size_t)(q / nb) * a.k + (size_t)(q % nb) * kQK; };
+  // four or more columns may come already quantised (a.q8img): the image
+  // is copied in place of the Q8_K passes
+  const bool pre = M >= 4 && a.q8img != nullptr;
   if (NORM) {
     norm_load<NORM>(a.norm, nr, grp, nb, i16);
-  } else {
+  } else if (!pre) {
     if (grp < nq) load_x16(xv, x_block(grp), i16);
     if (grp + wpg * 4 < nq) load_x16(xv2, x_block(grp + wpg * 4), i16);
     if (grp + wpg * 8 < nq) load_x16(xv3, x_block(grp + wpg * 8), i16);
@@ -760,7 +680,11 @@ __global__ __launch_bounds__(256) void kquant_matvec_half_kernel(const MatvecArg
   load_unit(first, un0, 0);
   __builtin_amdgcn_sched_barrier(0);  // keep the prologue's work after the weight loads
   if (NORM) norm_finish<NORM>(a.norm, nr, xv, grp, nb, i16, a.k, norm_sh);
-  {
+  if (pre) {
+    const int n16 = (int)(q8_image_bytes(M, nb) / 16);
+    const uint4 *src = reinterpret_cast<const uint4 *>(a.q8img);
+    for (int i = threadIdx.x; i < n16; i += blockDim.x) reinterpret_cast<uint4 *>(smem)[i] = src[i];
+  } else {
     int q = grp;
     if (q < nq) q8k_block16(xv, i16, xq + (size_t)q * kQ8BlockBytes, xd + q);
     q += wpg * 4;
@@ -929,6 +853,7 @@ static hipError_t launch_half_m(const MatvecArgs &a, int num_cus, hipStream_t s)
 }
 
 hipError_t launch_matvec_half(const MatvecArgs &a, int num_cus, hipStream_t s) {
+  if (a.q8img && (a.cols < 4 || a.norm.mode != 0)) return hipErrorInvalidValue;
   if (a.norm.mode < 0 || a.norm.mode > 2 || (a.norm.mode != 0 && (a.cols != 1 || a.g.nb > 16)))
     return hipErrorInvalidValue;
   if (a.g.S > 32 || a.Rh < 1 || 2 * a.Rh * a.g.S > 64) return hipErrorInvalidValue;
@@ -952,6 +877,7 @@ static hipError_t launch_pair_m(const MatvecArgs &a, int num_cus, hipStream_t s)
 }
 
 hipError_t launch_matvec_pair(const MatvecArgs &a, int num_cus, hipStream_t s) {
+  if (a.q8img) return hipErrorInvalidValue;
   if (a.norm.mode < 0 || a.norm.mode > 2 || (a.norm.mode != 0 && (a.cols != 1 || a.g.nb > 16)))
     return hipErrorInvalidValue;
   if (a.count != 2 || a.w[0].rows != a.w[1].rows || a.w[0].tiles != a.w[1].tiles || !a.pair_out)
@@ -966,6 +892,7 @@ hipError_t launch_matvec_pair(const MatvecArgs &a, int num_cus, hipStream_t s) {
 }
 
 hipError_t launch_matvec(const MatvecArgs &a, int num_cus, hipStream_t s) {
+  if (a.q8img && (a.cols < 4 || a.norm.mode != 0)) return hipErrorInvalidValue;
   if (a.norm.mode < 0 || a.norm.mode > 2 || (a.norm.mode != 0 && (a.cols != 1 || a.g.nb > 16)))
     return hipErrorInvalidValue;
   switch (a.cols) {
