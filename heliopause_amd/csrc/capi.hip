@@ -259,14 +259,15 @@ bool use_mfma(size_t cols, int nb, int tiles16) {
 // wave's work and doubles the waves, which pays while the launch has few
 // tiles (small projections are latency-bound) and costs throughput on large
 // ones.  Measured on MI355X: faster for one column up to ~2048 tiles (Q/K/V
-// 512, 10240 rows 1707) and for two to four columns up to ~1024 tiles; slower
-// for gate/up (3414 tiles), the head, and 40-block rows (S = 20).
+// 512, 10240 rows 1707: 7.39 against 7.75 us) and for two to four columns up
+// to ~1024 tiles; slower for gate/up (3414 tiles), the head, and 40-block
+// rows (S = 20: down 15.6 against 13.2 us).
 bool use_half(int cols, const TileGeom &g, int tiles) {
   const int forced = st().matvec_kernel;
   if (cols > 4 || g.S > 32) return false;
   if (forced == 3) return true;
   if (forced != 0 || g.S > 16) return false;
-  return tiles <= 1024;
+  return tiles <= (cols == 1 ? 2048 : 1024);
 }
 
 // One matvec launch per column chunk covering every weight (multi == one
@@ -334,13 +335,13 @@ int32_t run_matvec(size_t count, Handle *const *hs, const float *d_input, size_t
   }
   a.total_tiles = tiles;
   a.Rh = g.S <= 32 ? 32 / g.S : 0;
-  int units = 0;
+  int rows_all = 0;
   for (size_t i = 0; i < count; i++) {
-    a.w[i].units = a.Rh ? (int)((hs[i]->row_count + a.Rh - 1) / a.Rh) : 0;
-    a.w[i].unit_begin = units;
-    units += a.w[i].units;
+    a.w[i].row_begin = rows_all;
+    rows_all += (int)hs[i]->row_count;
   }
-  a.total_units = units;
+  a.total_rows = rows_all;
+  a.total_units = a.Rh ? (rows_all + a.Rh - 1) / a.Rh : 0;
   if (const int kind = prefill_kind(cols)) {
     if (cols > 65535) return fail(HP_ERR_SHAPE, "too many columns");
     const size_t need = kind == 2 ? prefill_fast_bytes((int)input_size, (int)cols)

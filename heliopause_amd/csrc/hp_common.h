@@ -63,8 +63,8 @@ struct WeightDesc {
   int rows;               // N
   int tiles;              // ceil(N / R)
   int tile_begin;         // first global tile index of this weight
-  int units;              // half-split kernel: ceil(N / Rh)
-  int unit_begin;         // first global unit index of this weight
+  int row_begin;          // half-split kernel: first row of this weight in the
+                          // launch's rows (the weights' rows end to end)
 };
 
 // Input of a one-column matvec launch formed in every workgroup's prologue
@@ -92,7 +92,9 @@ struct MatvecArgs {
   int k;              // input size (nb * 256)
   int cols;           // columns in this launch (<= kMaxCols)
   int out_col0;       // first output column written by this launch
-  int total_units;    // half-split kernel: units of Rh rows over all weights
+  int total_units;    // half-split kernel: ceil(total_rows / Rh) units of Rh
+                      // consecutive launch rows (a unit may span two weights)
+  int total_rows;     // half-split kernel: the weights' rows summed
   int Rh;             // half-split kernel: rows per unit (floor(32 / S))
   float *pair_out;    // gate/up + GeGLU launch: [cols][rows] output
   double gelu_c;      // sqrt(2 / pi) as Math.sqrt(2 / Math.PI)
@@ -114,7 +116,7 @@ hipError_t launch_q8k_natural(const float *x, int k, int cols, int8_t *qs, float
                               hipStream_t s);
 hipError_t launch_matvec(const MatvecArgs &a, int num_cus, hipStream_t s);
 // Half-split variant (two lanes per row-block, lane classes 0-3 / 4-7):
-// needs S <= 32 and cols <= 4; a.units/unit_begin/total_units/Rh set.
+// needs S <= 32 and cols <= 4; a.w[].row_begin, total_rows, total_units, Rh set.
 hipError_t launch_matvec_half(const MatvecArgs &a, int num_cus, hipStream_t s);
 // Gate/up + GeGLU in one vector-ALU launch (count == 2, equal rows, cols <= 4):
 // a.pair_out[m][r] = fround(gelu(gate) * up).

@@ -606,31 +606,33 @@ __global__ __launch_bounds__(256) void kquant_matvec_half_kernel(const MatvecArg
   const int rr = grp2 >> 1, h = grp2 & 1;
   const int s = lane - grp2 * S;
 
-  // weight unit u: its descriptor and this lane's row, tile and chunk index
+  // unit u: rows u * Rh .. u * Rh + Rh - 1 of the launch (the weights' rows
+  // end to end, so a unit may span two weights and the units fill the grid
+  // without a partial unit per weight); this lane's weight, row, tile and
+  // chunk index
   struct Unit {
     WeightDesc W;
     bool q4, active;
     int CH, row, t, Rt, k;
     const uint8_t *tile;
   };
-  // SAFE: an idle lane addresses a row of the unit that exists (and the last
-  // unit stands in for u >= total_units), so its loads need no branch
-  auto unit_of = [&](int u, bool safe) {
+  // An idle lane addresses a launch row that exists (the unit's last, or the
+  // launch's last for u >= total_units), so its loads need no branch
+  auto unit_of = [&](int u) {
     Unit n;
-    const bool real = u < a.total_units;
-    if (safe) u = min(u, a.total_units - 1);
+    const int grow = u * Rh + rr;
+    n.active = u < a.total_units && rr < Rh && grow < a.total_rows;
+    const int arow = n.active ? grow : min(min(u, a.total_units - 1) * Rh + min(rr, Rh - 1), a.total_rows - 1);
     n.W = a.w[0];
-    if (a.count > 1 && u >= a.w[1].unit_begin) n.W = a.w[1];
-    if (a.count > 2 && u >= a.w[2].unit_begin) n.W = a.w[2];
-    if (a.count > 3 && u >= a.w[3].unit_begin) n.W = a.w[3];
+    if (a.count > 1 && arow >= a.w[1].row_begin) n.W = a.w[1];
+    if (a.count > 2 && arow >= a.w[2].row_begin) n.W = a.w[2];
+    if (a.count > 3 && arow >= a.w[3].row_begin) n.W = a.w[3];
     n.q4 = TYPE == kTypeQ4K ? true : TYPE == kTypeQ6K ? false : n.W.type == kTypeQ4K;
     n.CH = n.q4 ? 9 : 13;
-    n.row = (u - n.W.unit_begin) * Rh + rr;
-    n.active = real && rr < Rh && n.row < n.W.rows && grp2 < 2 * Rh;
-    const int arow = n.active ? n.row : safe ? min((u - n.W.unit_begin) * Rh + min(rr, Rh - 1), n.W.rows - 1) : 0;
-    n.t = arow / R;
+    n.row = arow - n.W.row_begin;
+    n.t = n.row / R;
     n.Rt = min(R, n.W.rows - n.t * R);
-    n.k = (arow - n.t * R) * S + s;
+    n.k = (n.row - n.t * R) * S + s;
     n.tile = n.W.data + (size_t)n.t * R * nb * n.CH * 16;
     return n;
   };
@@ -676,7 +678,7 @@ __global__ __launch_bounds__(256) void kquant_matvec_half_kernel(const MatvecArg
   // first wait on its input a wait on every load
   const int u0 = blockIdx.x * wpg + wave;
   HalfRegs first;
-  const Unit un0 = unit_of(u0, true);
+  const Unit un0 = unit_of(u0);
   load_unit(first, un0, 0);
   __builtin_amdgcn_sched_barrier(0);  // keep the prologue's work after the weight loads
   if (NORM) norm_finish<NORM>(a.norm, nr, xv, grp, nb, i16, a.k, norm_sh);
@@ -700,7 +702,7 @@ __global__ __launch_bounds__(256) void kquant_matvec_half_kernel(const MatvecArg
 
   float carry[M][5];
   for (int u = u0; u < a.total_units; u += stride) {
-    const Unit un = u == u0 ? un0 : unit_of(u, false);
+    const Unit un = u == u0 ? un0 : unit_of(u);
     const WeightDesc &W = un.W;
     const bool q4 = un.q4, active = un.active;
     const int row = un.row;

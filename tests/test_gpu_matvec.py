@@ -64,13 +64,17 @@ def test_matmul_bit_exact(hip, oracle, kernel, type_name, rows, k, m):
         hip.releaseHipQuantizedWeightHandle(h)
 
 
-def test_multi_mixed_types_bit_exact(hip, oracle, kernel):
-    """Q (Q4_K) + K (Q4_K) + V (Q6_K) in one launch sharing one Q8_K (lib.rs:300-426)."""
+@pytest.mark.parametrize("specs", [[("Q4_K", 96), ("Q4_K", 40), ("Q6_K", 40)],
+                                   [("Q6_K", 97), ("Q4_K", 41), ("Q4_K", 1), ("Q6_K", 8)]],
+                         ids=["qkv", "ragged4"])
+def test_multi_mixed_types_bit_exact(hip, oracle, kernel, specs):
+    """Q (Q4_K) + K (Q4_K) + V (Q6_K) in one launch sharing one Q8_K (lib.rs:300-426);
+    ragged row counts put rows of two weights (of either type) in one
+    half-split unit."""
     k = 2560
-    specs = [("Q4_K", 96), ("Q4_K", 40), ("Q6_K", 40)]
-    for m in (1, 4):
-        print(f"multi kernel={kernel} m={m}", flush=True)
-        seed = S.derive(S.BASE_SEED, "multi", m)
+    for m in (1, 2, 4):
+        print(f"multi kernel={kernel} m={m} specs={specs}", flush=True)
+        seed = S.derive(S.BASE_SEED, "multi", m, len(specs))
         ws = [_weights(t, S.derive(seed, i), r, k) for i, (t, r) in enumerate(specs)]
         x = S.activations(seed, m, k)
         hs = [hip.createHipQuantizedWeightHandle(t, w, k, r) for (t, r), w in zip(specs, ws)]
