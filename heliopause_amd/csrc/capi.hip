@@ -344,11 +344,6 @@ int32_t run_matvec(size_t count, Handle *const *hs, const float *d_input, size_t
   a.total_units = a.Rh ? (rows_all + a.Rh - 1) / a.Rh : 0;
   if (const int kind = prefill_kind(cols)) {
     if (cols > 65535) return fail(HP_ERR_SHAPE, "too many columns");
-    const size_t need = kind == 2 ? prefill_fast_bytes((int)input_size, (int)cols)
-                                  : prefill_q8k_bytes((int)input_size, (int)cols);
-    int32_t rc = grow(&s.prefill_scratch, &s.prefill_scratch_cap, need);
-    if (rc != HP_OK) return rc;
-    uint8_t *q8 = static_cast<uint8_t *>(s.prefill_scratch);
     MfmaLaunch l{};
     l.count = (int)count;
     l.k = (int)input_size;
@@ -359,6 +354,10 @@ int32_t run_matvec(size_t count, Handle *const *hs, const float *d_input, size_t
       l.rows[i] = (int)hs[i]->row_count;
       l.out[i] = d_outs[i];
     }
+    const size_t need = kind == 2 ? prefill_fast_bytes(l, s.num_cus) : prefill_q8k_bytes((int)input_size, (int)cols);
+    int32_t rc = grow(&s.prefill_scratch, &s.prefill_scratch_cap, need);
+    if (rc != HP_OK) return rc;
+    uint8_t *q8 = static_cast<uint8_t *>(s.prefill_scratch);
     hipEvent_t e1 = prof_begin(stream);
     if (kind == 2) {
       HP_HIP_TRY(launch_prefill_fast(l, d_input, q8, s.num_cus, stream));

@@ -173,10 +173,12 @@ size_t prefill_lds_bytes();
 hipError_t launch_q8k_prefill(const float *x, int k, int cols, uint8_t *scratch, hipStream_t s);
 hipError_t launch_prefill(const MfmaLaunch &l, const uint8_t *scratch, int num_cus, hipStream_t s);
 // Fast prefill (within the 1e-4 relative tolerance of projections, not
-// bit-exact): its own pre-pass of x into prefill_fast_bytes(k, cols) of
-// scratch, then 128-row x 64-column tiles with the eight classes in one
-// accumulator.
-size_t prefill_fast_bytes(int k, int cols);
+// bit-exact): its own pre-pass of x into scratch, then 128-row x 64-column
+// tiles with the eight classes in one accumulator.  A launch with fewer
+// tiles than two per CU splits each tile's blocks into consecutive ranges
+// whose partial sums (in scratch) a reduction adds in range order.
+// prefill_fast_bytes: the scratch of a launch of these weights' rows.
+size_t prefill_fast_bytes(const MfmaLaunch &l, int num_cus);
 size_t prefill_fast_lds_bytes();
 hipError_t launch_prefill_fast(const MfmaLaunch &l, const float *x, uint8_t *scratch, int num_cus, hipStream_t s);
 

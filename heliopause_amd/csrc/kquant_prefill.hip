@@ -410,6 +410,12 @@ struct F2Args {
   PfWeight w[kMaxWeights];  // rt_begin counts 128-row tiles here
   int count, total_rt, col_tiles, nb, cols;
   const uint8_t *xt;
+  // ksplit > 1: block range r of a tile writes its sums to part + r * part_stride
+  // + part_off[weight] + m * rows + row instead of the output
+  int ksplit;
+  float *part;
+  size_t part_stride;
+  size_t part_off[kMaxWeights];
 };
 
 // A fragment of class l for rows n of one segment from the raw segment bytes
@@ -544,13 +550,18 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   extern __shared__ __align__(16) uint8_t smem[];
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int items = a.total_rt * a.col_tiles;
+  const int tiles = a.total_rt * a.col_tiles;
+  const int items = tiles * a.ksplit;
   for (int it = blockIdx.x; it < items; it += gridDim.x) {
-    const int rt = it / a.col_tiles, ct = it - rt * a.col_tiles;
+    const int kr = it / tiles, t2 = it - kr * tiles;
+    const int rt = t2 / a.col_tiles, ct = t2 - rt * a.col_tiles;
+    const int b_begin = (int)((long long)kr * a.nb / a.ksplit), b_end = (int)((long long)(kr + 1) * a.nb / a.ksplit);
     PfWeight W = a.w[0];
-    if (a.count > 1 && rt >= a.w[1].rt_begin) W = a.w[1];
-    if (a.count > 2 && rt >= a.w[2].rt_begin) W = a.w[2];
-    if (a.count > 3 && rt >= a.w[3].rt_begin) W = a.w[3];
+    size_t poff = a.part_off[0];
+    if (a.count > 1 && rt >= a.w[1].rt_begin) W = a.w[1], poff = a.part_off[1];
+    if (a.count > 2 && rt >= a.w[2].rt_begin) W = a.w[2], poff = a.part_off[2];
+    if (a.count > 3 && rt >= a.w[3].rt_begin) W = a.w[3], poff = a.part_off[3];
+    float *dst = a.ksplit > 1 ? a.part + kr * a.part_stride + poff : W.out;
     const bool q4 = W.type == kTypeQ4K;
     const int segb = q4 ? 2304 : 3360;
     const int T0 = 8 * (rt - W.rt_begin);
@@ -568,7 +579,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     const uint8_t *xt = a.xt + (size_t)ct * a.nb * kF2XTile;
     // one LDS stage: load, compute, repeat; the other workgroup on the CU
     // computes while this one loads
-    for (int b = 0; b < a.nb; b++) {
+    for (int b = b_begin; b < b_end; b++) {
       lds_copy(W.seg + ((size_t)b * W.tiles + T0) * segb, smem, wbytes, wave, lane);
       lds_copy(xt + (size_t)b * kF2XTile, smem + kF2W, kF2XTile, wave, lane);
       __builtin_amdgcn_s_waitcnt(0);
@@ -591,11 +602,74 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
 #pragma unroll
           for (int j = 0; j < 4; j++) {
             const int row = 16 * (T0 + my_seg + rs) + 4 * q + j;
-            if (rs < nseg && row < W.rows && m < a.cols) W.out[(size_t)m * W.rows + row] = out[rs][cs][j];
+            if (rs < nseg && row < W.rows && m < a.cols) dst[(size_t)m * W.rows + row] = out[rs][cs][j];
           }
         }
     }
   }
+}
+
+// out = ((part_0 + part_1) + ...) + part_{ks-1} over the launch's outputs
+// (the weights' [cols][rows] outputs end to end), four floats per thread.
+__global__ __launch_bounds__(256) void f2_reduce_kernel(const F2Args a, size_t total) {
+  const size_t i = 4 * ((size_t)blockIdx.x * blockDim.x + threadIdx.x);
+  if (i >= total) return;
+  int w = 0;
+  if (a.count > 1 && i >= a.part_off[1]) w = 1;
+  if (a.count > 2 && i >= a.part_off[2]) w = 2;
+  if (a.count > 3 && i >= a.part_off[3]) w = 3;
+  const size_t end = w + 1 < a.count ? a.part_off[w + 1] : total;
+  float *out = a.w[w].out - a.part_off[w];
+  if (i + 4 <= end && (((uintptr_t)(out + i)) & 15) == 0) {
+    float4 acc = *reinterpret_cast<const float4 *>(a.part + i);
+    for (int r = 1; r < a.ksplit; r++) {
+      const float4 p = *reinterpret_cast<const float4 *>(a.part + r * a.part_stride + i);
+      acc.x += p.x;
+      acc.y += p.y;
+      acc.z += p.z;
+      acc.w += p.w;
+    }
+    *reinterpret_cast<float4 *>(out + i) = acc;
+  } else {
+    for (size_t e = i; e < i + 4 && e < total; e++) {
+      int we = 0;
+      if (a.count > 1 && e >= a.part_off[1]) we = 1;
+      if (a.count > 2 && e >= a.part_off[2]) we = 2;
+      if (a.count > 3 && e >= a.part_off[3]) we = 3;
+      float acc = a.part[e];
+      for (int r = 1; r < a.ksplit; r++) acc += a.part[r * a.part_stride + e];
+      a.w[we].out[e - a.part_off[we]] = acc;
+    }
+  }
+}
+
+// Block ranges per tile: enough to give every CU two tiles' worth of
+// workgroups when the launch has fewer tiles, at least four blocks a range.
+int f2_ksplit(int tiles, int nb, int num_cus) {
+  if (tiles <= 0 || tiles >= 2 * num_cus) return 1;
+  int ks = 2 * num_cus / tiles;
+  if (ks > nb / 4) ks = nb / 4;
+  if (ks > 8) ks = 8;
+  return ks < 1 ? 1 : ks;
+}
+
+struct F2Shape {
+  int nb, col_tiles, total_rt, ks;
+  size_t outs;    // floats of all outputs
+  size_t stride;  // floats between block ranges' partial sums (16-byte multiple)
+};
+
+F2Shape f2_shape(const MfmaLaunch &l, int num_cus) {
+  F2Shape sh{};
+  sh.nb = l.k / kQK;
+  sh.col_tiles = (l.cols + kF2Cols - 1) / kF2Cols;
+  for (int i = 0; i < l.count; i++) {
+    sh.total_rt += ((l.rows[i] + 15) / 16 + 7) / 8;
+    sh.outs += (size_t)l.cols * l.rows[i];
+  }
+  sh.ks = f2_ksplit(sh.total_rt * sh.col_tiles, sh.nb, num_cus);
+  sh.stride = (sh.outs + 3) & ~(size_t)3;
+  return sh;
 }
 
 }  // namespace
@@ -616,16 +690,18 @@ hipError_t launch_q8k_prefill(const float *x, int k, int cols, uint8_t *scratch,
 
 size_t prefill_lds_bytes() { return kPfLds; }
 
-size_t prefill_fast_bytes(int k, int cols) {
-  return (size_t)((cols + kF2Cols - 1) / kF2Cols) * (k / kQK) * kF2XTile;
+size_t prefill_fast_bytes(const MfmaLaunch &l, int num_cus) {
+  const F2Shape sh = f2_shape(l, num_cus);
+  const size_t xt = (size_t)sh.col_tiles * sh.nb * kF2XTile;
+  return xt + (sh.ks > 1 ? (size_t)sh.ks * sh.stride * sizeof(float) : 0);
 }
 
 size_t prefill_fast_lds_bytes() { return kF2Lds; }
 
 hipError_t launch_prefill_fast(const MfmaLaunch &l, const float *x, uint8_t *scratch, int num_cus, hipStream_t s) {
   if (l.count < 1 || l.count > kMaxWeights || l.cols < 1 || l.k % kQK != 0) return hipErrorInvalidValue;
-  const int nb = l.k / kQK;
-  const int col_tiles = (l.cols + kF2Cols - 1) / kF2Cols;
+  const F2Shape sh = f2_shape(l, num_cus);
+  const int nb = sh.nb, col_tiles = sh.col_tiles;
   hipLaunchKernelGGL(q8k_prefill_tiles_kernel, dim3(nb, col_tiles * kF2Cols), dim3(64), 0, s, x, l.k, nb, l.cols,
                      scratch);
   hipError_t e = hipGetLastError();
@@ -633,6 +709,7 @@ hipError_t launch_prefill_fast(const MfmaLaunch &l, const float *x, uint8_t *scr
   F2Args a{};
   a.count = l.count;
   int rt = 0;
+  size_t off = 0;
   for (int i = 0; i < l.count; i++) {
     a.w[i].seg = l.seg[i];
     a.w[i].out = l.out[i];
@@ -641,12 +718,17 @@ hipError_t launch_prefill_fast(const MfmaLaunch &l, const float *x, uint8_t *scr
     a.w[i].tiles = (l.rows[i] + 15) / 16;
     a.w[i].rt_begin = rt;
     rt += (a.w[i].tiles + 7) / 8;
+    a.part_off[i] = off;
+    off += (size_t)l.cols * l.rows[i];
   }
   a.total_rt = rt;
   a.col_tiles = col_tiles;
   a.nb = nb;
   a.cols = l.cols;
   a.xt = scratch;
+  a.ksplit = sh.ks;
+  a.part = reinterpret_cast<float *>(scratch + (size_t)col_tiles * nb * kF2XTile);
+  a.part_stride = sh.stride;
   static bool attr = false;
   if (!attr) {
     e = hipFuncSetAttribute(reinterpret_cast<const void *>(kquant_prefill_fast_kernel),
@@ -654,9 +736,14 @@ hipError_t launch_prefill_fast(const MfmaLaunch &l, const float *x, uint8_t *scr
     if (e != hipSuccess) return e;
     attr = true;
   }
-  const long long items = (long long)a.total_rt * a.col_tiles;
+  const long long items = (long long)a.total_rt * a.col_tiles * a.ksplit;
   const int grid = (int)(items < 2LL * num_cus ? items : 2LL * num_cus);
   hipLaunchKernelGGL(kquant_prefill_fast_kernel, dim3(grid), dim3(256), kF2Lds, s, a);
+  if (a.ksplit == 1) return hipGetLastError();
+  e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  const size_t threads = (sh.outs + 3) / 4;
+  hipLaunchKernelGGL(f2_reduce_kernel, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, s, a, sh.outs);
   return hipGetLastError();
 }
 
