@@ -366,7 +366,7 @@ int32_t run_matvec(size_t count, Handle *const *hs, const float *d_input, size_t
       HP_HIP_TRY(launch_prefill(l, q8, s.num_cus, stream));
     }
     prof_end(HP_KERNEL_MATVEC, e1, stream);
-    s.launches += 2;
+    s.launches += kind == 2 ? prefill_fast_launches(l, s.num_cus) : 2;
     s.matmul_calls++;
     return HP_OK;
   }
@@ -417,7 +417,9 @@ int32_t run_matvec(size_t count, Handle *const *hs, const float *d_input, size_t
 
 // gate/up projections + GeGLU into d_out ([cols][rows]).  One fused
 // vector-ALU launch when the kernel policy would run the full vector-ALU
-// kernel on this launch (one column of large projections); otherwise the
+// kernel on this launch (one column of large projections); the fast prefill
+// kernel with gate and up rows in one tile when the policy takes it (gate and
+// up of one type); otherwise the
 // projections (one launch, any kernel) into scratch, then the GeGLU kernel.
 // Both give the same bits.
 // q8img_out (4 or more columns): when the GeGLU runs as its own launch it also
@@ -467,6 +469,29 @@ int32_t run_matvec_geglu(Handle *hg, Handle *hu, const float *d_input, size_t in
     HP_HIP_TRY(launch_matvec_pair(a, s.num_cus, stream));
     prof_end(HP_KERNEL_MATVEC, e1, stream);
     s.launches++;
+    s.matmul_calls++;
+    return HP_OK;
+  }
+  if (prefill_kind(cols) == 2 && hg->type == hu->type) {
+    // fast prefill: gate and up rows in one tile, GeGLU in its epilogue
+    int32_t rc = grow(&s.prefill_scratch, &s.prefill_scratch_cap,
+                      prefill_fast_geglu_bytes((int)input_size, (int)cols));
+    if (rc != HP_OK) return rc;
+    MfmaLaunch l{};
+    l.count = 2;
+    l.k = (int)input_size;
+    l.cols = (int)cols;
+    Handle *hs[2] = {hg, hu};
+    for (int i = 0; i < 2; i++) {
+      l.seg[i] = hs[i]->segs;
+      l.type[i] = hs[i]->type;
+      l.rows[i] = (int)rows;
+    }
+    hipEvent_t e1 = prof_begin(stream);
+    HP_HIP_TRY(launch_prefill_fast_geglu(l, d_input, static_cast<uint8_t *>(s.prefill_scratch), gelu_constant(), d_out,
+                                         s.num_cus, stream));
+    prof_end(HP_KERNEL_MATVEC, e1, stream);
+    s.launches += 2;
     s.matmul_calls++;
     return HP_OK;
   }

@@ -179,6 +179,13 @@ hipError_t launch_prefill(const MfmaLaunch &l, const uint8_t *scratch, int num_c
 // whose partial sums (in scratch) a reduction adds in range order.
 // prefill_fast_bytes: the scratch of a launch of these weights' rows.
 size_t prefill_fast_bytes(const MfmaLaunch &l, int num_cus);
+int prefill_fast_launches(const MfmaLaunch &l, int num_cus);  // 2, or 3 with the reduction
+// Gate/up (l.w 0 and 1, same type and rows) + GeGLU with the fast prefill
+// kernel: out[m][r] = fround(gelu(gate) * up), gate and up as the fast
+// kernel computes them; prefill_fast_geglu_bytes(k, cols) of scratch.
+size_t prefill_fast_geglu_bytes(int k, int cols);
+hipError_t launch_prefill_fast_geglu(const MfmaLaunch &l, const float *x, uint8_t *scratch, double gelu_c,
+                                     float *out, int num_cus, hipStream_t s);
 size_t prefill_fast_lds_bytes();
 hipError_t launch_prefill_fast(const MfmaLaunch &l, const float *x, uint8_t *scratch, int num_cus, hipStream_t s);
 

@@ -25,6 +25,7 @@
 // registers; A fragments (one dword per lane and class) and B fragments
 // (8 bytes per lane) are built from LDS.
 #include "hp_common.h"
+#include "hp_gelu.h"
 #include "hp_mfma.h"
 #include "hp_q8k.h"
 
@@ -416,6 +417,9 @@ struct F2Args {
   float *part;
   size_t part_stride;
   size_t part_off[kMaxWeights];
+  // gate/up + GeGLU tiles (w[0] gate, w[1] up): pair_out[m][row]
+  float *pair_out;
+  double gelu_c;
 };
 
 // A fragment of class l for rows n of one segment from the raw segment bytes
@@ -545,6 +549,10 @@ __device__ __forceinline__ void f2_block(float (&out)[2][4][4], const uint8_t *w
 }
 
 // Two workgroups per CU (LDS), so two waves per SIMD.
+// PAIR: a tile is 64 rows of gate (waves 0, 1) and the same 64 rows of up
+// (waves 2, 3); up's sums go through LDS to the gate waves, which store
+// fround(gelu(gate) * up).  total_rt then counts 64-row tiles, ksplit is 1.
+template <bool PAIR>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void kquant_prefill_fast_kernel(
     const F2Args a) {
   extern __shared__ __align__(16) uint8_t smem[];
@@ -558,16 +566,19 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     const int b_begin = (int)((long long)kr * a.nb / a.ksplit), b_end = (int)((long long)(kr + 1) * a.nb / a.ksplit);
     PfWeight W = a.w[0];
     size_t poff = a.part_off[0];
-    if (a.count > 1 && rt >= a.w[1].rt_begin) W = a.w[1], poff = a.part_off[1];
-    if (a.count > 2 && rt >= a.w[2].rt_begin) W = a.w[2], poff = a.part_off[2];
-    if (a.count > 3 && rt >= a.w[3].rt_begin) W = a.w[3], poff = a.part_off[3];
+    if (!PAIR) {
+      if (a.count > 1 && rt >= a.w[1].rt_begin) W = a.w[1], poff = a.part_off[1];
+      if (a.count > 2 && rt >= a.w[2].rt_begin) W = a.w[2], poff = a.part_off[2];
+      if (a.count > 3 && rt >= a.w[3].rt_begin) W = a.w[3], poff = a.part_off[3];
+    }
     float *dst = a.ksplit > 1 ? a.part + kr * a.part_stride + poff : W.out;
     const bool q4 = W.type == kTypeQ4K;
     const int segb = q4 ? 2304 : 3360;
-    const int T0 = 8 * (rt - W.rt_begin);
-    const int nseg_tile = W.tiles - T0 < 8 ? W.tiles - T0 : 8;
+    constexpr int kTileSegs = PAIR ? 4 : 8;  // 16-row segments per weight and tile
+    const int T0 = kTileSegs * (rt - W.rt_begin);
+    const int nseg_tile = W.tiles - T0 < kTileSegs ? W.tiles - T0 : kTileSegs;
     const int wbytes = nseg_tile * segb;
-    const int my_seg = 2 * wave;
+    const int my_seg = PAIR ? 2 * (wave & 1) : 2 * wave;  // within this wave's weight
     const int nseg = nseg_tile - my_seg >= 2 ? 2 : nseg_tile - my_seg;  // this wave's live segments (<= 0: none)
     float out[2][4][4];
 #pragma unroll
@@ -581,18 +592,48 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     // computes while this one loads
     for (int b = b_begin; b < b_end; b++) {
       lds_copy(W.seg + ((size_t)b * W.tiles + T0) * segb, smem, wbytes, wave, lane);
+      if (PAIR) lds_copy(a.w[1].seg + ((size_t)b * W.tiles + T0) * segb, smem + 4 * segb, wbytes, wave, lane);
       lds_copy(xt + (size_t)b * kF2XTile, smem + kF2W, kF2XTile, wave, lane);
       __builtin_amdgcn_s_waitcnt(0);
       __syncthreads();
       if (nseg > 0) {
         if (q4)
-          f2_block<true>(out, smem + my_seg * segb, smem + kF2W, lane);
+          f2_block<true>(out, smem + 2 * wave * segb, smem + kF2W, lane);
         else
-          f2_block<false>(out, smem + my_seg * segb, smem + kF2W, lane);
+          f2_block<false>(out, smem + 2 * wave * segb, smem + kF2W, lane);
       }
       __syncthreads();
     }
-    if (nseg > 0) {
+    if (PAIR) {
+      // up waves hand their sums to the gate wave of the same rows
+      float *xch = reinterpret_cast<float *>(smem) + (wave & 1) * 32 * 64 + lane;
+      if (wave >= 2) {
+#pragma unroll
+        for (int rs = 0; rs < 2; rs++)
+#pragma unroll
+          for (int cs = 0; cs < 4; cs++)
+#pragma unroll
+            for (int j = 0; j < 4; j++) xch[((rs * 4 + cs) * 4 + j) * 64] = out[rs][cs][j];
+      }
+      __syncthreads();
+      if (wave < 2 && nseg > 0) {
+        const int n = lane & 15, q = lane >> 4;
+#pragma unroll
+        for (int rs = 0; rs < 2; rs++)
+#pragma unroll
+          for (int cs = 0; cs < 4; cs++) {
+            const int m = ct * kF2Cols + 16 * cs + n;
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+              const int row = 16 * (T0 + my_seg + rs) + 4 * q + j;
+              const float up = xch[((rs * 4 + cs) * 4 + j) * 64];
+              if (rs < nseg && row < W.rows && m < a.cols)
+                a.pair_out[(size_t)m * W.rows + row] = geglu_ts(out[rs][cs][j], up, a.gelu_c);
+            }
+          }
+      }
+      __syncthreads();  // the next tile's copies overwrite the exchange
+    } else if (nseg > 0) {
       const int n = lane & 15, q = lane >> 4;
 #pragma unroll
       for (int rs = 0; rs < 2; rs++)
@@ -690,6 +731,61 @@ hipError_t launch_q8k_prefill(const float *x, int k, int cols, uint8_t *scratch,
 
 size_t prefill_lds_bytes() { return kPfLds; }
 
+// The fast kernels' dynamic LDS above the default limit (once per process).
+static hipError_t f2_set_lds() {
+  static bool done = false;
+  if (done) return hipSuccess;
+  hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(kquant_prefill_fast_kernel<false>),
+                                     hipFuncAttributeMaxDynamicSharedMemorySize, kF2Lds);
+  if (e == hipSuccess)
+    e = hipFuncSetAttribute(reinterpret_cast<const void *>(kquant_prefill_fast_kernel<true>),
+                            hipFuncAttributeMaxDynamicSharedMemorySize, kF2Lds);
+  if (e == hipSuccess) done = true;
+  return e;
+}
+
+size_t prefill_fast_geglu_bytes(int k, int cols) {
+  return (size_t)((cols + kF2Cols - 1) / kF2Cols) * (k / kQK) * kF2XTile;
+}
+
+hipError_t launch_prefill_fast_geglu(const MfmaLaunch &l, const float *x, uint8_t *scratch, double gelu_c,
+                                     float *out, int num_cus, hipStream_t s) {
+  if (l.count != 2 || l.cols < 1 || l.k % kQK != 0 || l.type[0] != l.type[1] || l.rows[0] != l.rows[1])
+    return hipErrorInvalidValue;
+  const int nb = l.k / kQK;
+  const int col_tiles = (l.cols + kF2Cols - 1) / kF2Cols;
+  hipLaunchKernelGGL(q8k_prefill_tiles_kernel, dim3(nb, col_tiles * kF2Cols), dim3(64), 0, s, x, l.k, nb, l.cols,
+                     scratch);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  F2Args a{};
+  a.count = 2;
+  for (int i = 0; i < 2; i++) {
+    a.w[i].seg = l.seg[i];
+    a.w[i].out = nullptr;
+    a.w[i].type = l.type[i];
+    a.w[i].rows = l.rows[i];
+    a.w[i].tiles = (l.rows[i] + 15) / 16;
+    a.w[i].rt_begin = 0;
+  }
+  a.total_rt = (a.w[0].tiles + 3) / 4;
+  a.col_tiles = col_tiles;
+  a.nb = nb;
+  a.cols = l.cols;
+  a.xt = scratch;
+  a.ksplit = 1;
+  a.pair_out = out;
+  a.gelu_c = gelu_c;
+  e = f2_set_lds();
+  if (e != hipSuccess) return e;
+  const long long items = (long long)a.total_rt * a.col_tiles;
+  const int grid = (int)(items < 2LL * num_cus ? items : 2LL * num_cus);
+  hipLaunchKernelGGL(kquant_prefill_fast_kernel<true>, dim3(grid), dim3(256), kF2Lds, s, a);
+  return hipGetLastError();
+}
+
+int prefill_fast_launches(const MfmaLaunch &l, int num_cus) { return f2_shape(l, num_cus).ks > 1 ? 3 : 2; }
+
 size_t prefill_fast_bytes(const MfmaLaunch &l, int num_cus) {
   const F2Shape sh = f2_shape(l, num_cus);
   const size_t xt = (size_t)sh.col_tiles * sh.nb * kF2XTile;
@@ -729,16 +825,11 @@ hipError_t launch_prefill_fast(const MfmaLaunch &l, const float *x, uint8_t *scr
   a.ksplit = sh.ks;
   a.part = reinterpret_cast<float *>(scratch + (size_t)col_tiles * nb * kF2XTile);
   a.part_stride = sh.stride;
-  static bool attr = false;
-  if (!attr) {
-    e = hipFuncSetAttribute(reinterpret_cast<const void *>(kquant_prefill_fast_kernel),
-                            hipFuncAttributeMaxDynamicSharedMemorySize, kF2Lds);
-    if (e != hipSuccess) return e;
-    attr = true;
-  }
+  e = f2_set_lds();
+  if (e != hipSuccess) return e;
   const long long items = (long long)a.total_rt * a.col_tiles * a.ksplit;
   const int grid = (int)(items < 2LL * num_cus ? items : 2LL * num_cus);
-  hipLaunchKernelGGL(kquant_prefill_fast_kernel, dim3(grid), dim3(256), kF2Lds, s, a);
+  hipLaunchKernelGGL(kquant_prefill_fast_kernel<false>, dim3(grid), dim3(256), kF2Lds, s, a);
   if (a.ksplit == 1) return hipGetLastError();
   e = hipGetLastError();
   if (e != hipSuccess) return e;

@@ -12,7 +12,10 @@ Two kernels:
 Shapes cover the ways the workgroup tiles can be cut: rows not a multiple of
 16, 32 or 128 (last tiles with one segment), columns not a multiple of 64, a
 single column, mixed Q4_K/Q6_K weights in one launch, both input sizes of
-the model and a 512-column chunk.
+the model and a 512-column chunk.  Launches of the fast kernel with fewer
+tiles than two per CU split each tile's blocks into ranges added by a
+reduction: 2 ranges for (64, 2560, 64) and the 512-column Q/K/V, 8 for
+(300, 10240, 37) and (2560, 10240, 64).
 """
 import numpy as np
 import pytest
@@ -121,11 +124,16 @@ def test_prefill_multi_and_large_chunk(hip, oracle, selector):
 
 
 @pytest.mark.parametrize("selector", [4, 0], ids=["exact", "auto"], indirect=True)
-def test_prefill_geglu(hip, oracle, selector):
-    """gate/up + GeGLU over 96 columns: the projections take a prefill
-    kernel, GeGLU follows as its own launch."""
-    rows, k, m = 160, 2560, 96
-    seed = S.derive(S.BASE_SEED, "prefill-geglu")
+@pytest.mark.parametrize("rows,m", [(160, 96), (100, 64), (1000, 130)])
+def test_prefill_geglu(hip, oracle, selector, rows, m):
+    """gate/up + GeGLU: with the exact prefill kernel GeGLU follows as its own
+    launch; with the fast one (automatic from 64 columns) each tile holds 64
+    rows of gate and the same rows of up and stores the GeGLU.  Row counts
+    leave partial 64-row tiles (160: 2 of 4 segments; 100: 3 of 4, the last
+    one partial), columns partial 64-column tiles."""
+    k = 2560
+    print(f"prefill geglu rows={rows} m={m} selector={selector}", flush=True)
+    seed = S.derive(S.BASE_SEED, "prefill-geglu", rows, m)
     wg = S.q4_k_blocks(S.derive(seed, "g"), rows, k)
     wu = S.q4_k_blocks(S.derive(seed, "u"), rows, k)
     x = S.activations(seed, m, k)
