@@ -50,7 +50,9 @@ __device__ __forceinline__ void lexmax_step(float &amax, float &vmax, int &idx) 
   idx = take ? oi : idx;
 }
 
-__device__ __forceinline__ void q8k_block16(const float (&v)[16], int i16, uint8_t *blk, float *dptr) {
+// -127 / (the block's first element of largest |x|), the same in all 16
+// lanes of the row; nz: some element is not zero.
+__device__ __forceinline__ float q8k_inv16(const float (&v)[16], int i16, bool &nz) {
   const int j = i16 >> 1, u = i16 & 1;
   float amax = 0.0f, vmax = 0.0f;
   int idx = 0x7fffffff;
@@ -70,23 +72,33 @@ __device__ __forceinline__ void q8k_block16(const float (&v)[16], int i16, uint8
   lexmax_step<kDppXor2>(amax, vmax, idx);
   lexmax_step<kDppRowHalfMirror>(amax, vmax, idx);
   lexmax_step<kDppRowMirror>(amax, vmax, idx);
-  const bool nz = amax != 0.0f;
-  const float inv = __fdiv_rn(-127.0f, vmax);
+  nz = amax != 0.0f;
+  return __fdiv_rn(-127.0f, vmax);
+}
+
+// Rust: (is * x).round().min(127.0) as i8.  For a finite is, |is * x| <= 127
+// (1 + 2^-23); when the block's maximum is below ~3.7e-37 in magnitude, is
+// overflows to -inf or +inf and the saturating cast gives -128 for products
+// of -inf (the max(., -128) here); NaN (0 * inf) -> min() -> 127.  round()
+// (half away from zero) as trunc(p + copysign(0.5 - 2^-25, p)): equal for
+// every f32 |p| < 128 (checked exhaustively); the int conversion truncates,
+// and truncation commutes with the clamp to [-128, 127].
+__device__ __forceinline__ int q8k_round(float inv, float x) {
+  const float p = __fmul_rn(inv, x);
+  return (int)fmaxf(fminf(__fadd_rn(p, copysignf(0.49999997f, p)), 127.0f), -128.0f);
+}
+
+__device__ __forceinline__ void q8k_block16(const float (&v)[16], int i16, uint8_t *blk, float *dptr) {
+  const int j = i16 >> 1, u = i16 & 1;
+  bool nz;
+  const float inv = q8k_inv16(v, i16, nz);
   uint32_t word[4];
   int sum = 0;
 #pragma unroll
   for (int l4 = 0; l4 < 4; l4++) {
     int q[4];
 #pragma unroll
-    for (int c = 0; c < 4; c++) {
-      // Rust: (is * x).round().min(127.0) as i8.  |is * x| <= 127 (1 + 2^-23)
-      // for every element, so the saturating cast never acts; NaN -> min()
-      // -> 127.  round() (half away from zero) as trunc(p + copysign(0.5 -
-      // 2^-25, p)): equal for every f32 |p| < 128 (checked exhaustively);
-      // the int conversion truncates, and truncation commutes with min(., 127).
-      const float p = __fmul_rn(inv, v[4 * c + l4]);
-      q[c] = (int)fminf(__fadd_rn(p, copysignf(0.49999997f, p)), 127.0f);
-    }
+    for (int c = 0; c < 4; c++) q[c] = q8k_round(inv, v[4 * c + l4]);
     // bytes q0..q3 (low to high): the low bytes of two packed int16 pairs
     const uint32_t lo = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pk_i16(q[0], q[1]));
     const uint32_t hi = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pk_i16(q[2], q[3]));

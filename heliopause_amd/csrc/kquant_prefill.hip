@@ -28,6 +28,7 @@
 #include "hp_gelu.h"
 #include "hp_mfma.h"
 #include "hp_q8k.h"
+#include "hp_q8k16.h"
 
 namespace hp {
 
@@ -362,37 +363,52 @@ constexpr int kF2XTile = 32768 + 2048 + 256;  // 35,072 bytes per (column tile, 
 constexpr int kF2Stage = kF2W + kF2XTile;      // 61,952
 constexpr int kF2Lds = kF2Stage;               // one stage per workgroup, two workgroups per CU
 
-__global__ __launch_bounds__(64) void q8k_prefill_tiles_kernel(const float *__restrict__ x, int k, int nb, int cols,
-                                                               uint8_t *__restrict__ xt) {
-  const int b = blockIdx.x, m = blockIdx.y, lane = threadIdx.x;
+// The fast kernel's activation tiles (f16 quants [class][quarter][column][8],
+// f16 16-element sums, f32 d per column) from Q8_K of x, one 16-lane row per
+// (block, column): 16 columns per workgroup, vector loads of the column and 8-byte stores of four quants of
+// one class.  Lane i16 = 2j + u holds elements 32j + 8c + 4u + i (c, i < 4):
+// class l = 4u + i, quarter j / 2, position 4 (j & 1) + c of the quarter's
+// eight; its 16-element sums are halves of groups 2j (c < 2) and 2j + 1.
+__global__ __launch_bounds__(256) void q8k_prefill_tiles16_kernel(const float *__restrict__ x, int k, int nb,
+                                                                  int cols, uint8_t *__restrict__ xt) {
+  const int b = blockIdx.x, i16 = threadIdx.x & 15;
+  const int m = blockIdx.y * 16 + (threadIdx.x >> 4);
   const int ct = m / kF2Cols, n = m % kF2Cols;
   uint8_t *tile = xt + ((size_t)ct * nb + b) * kF2XTile;
   _Float16 *xh = reinterpret_cast<_Float16 *>(tile);
   _Float16 *xb = reinterpret_cast<_Float16 *>(tile + 32768);
   float *xd = reinterpret_cast<float *>(tile + 32768 + 2048);
-  Q8KLane r;
-  if (m < cols) {
-    r = q8k_block(x + (size_t)m * k + (size_t)b * kQK, lane);
-  } else {
-    r.q[0] = r.q[1] = r.q[2] = r.q[3] = 0;
-    r.d = 0.0f;
+  float v[16];
+  load_x16(v, x + (size_t)min(m, cols - 1) * k + (size_t)b * kQK, i16);
+  if (m >= cols) {
+#pragma unroll
+    for (int e = 0; e < 16; e++) v[e] = 0.0f;
   }
-  // lane owns e = 4 lane + i: j = lane / 8, c = (lane / 2) % 4, l = 4 (lane % 2) + i;
-  // quarter q = j / 2, position in the quarter (j % 2) * 4 + c
-  const int j = lane >> 3, c = (lane >> 1) & 3, qq = j >> 1, pos = 4 * (j & 1) + c;
+  bool nz;
+  const float inv = q8k_inv16(v, i16, nz);
+  int q[16];
+#pragma unroll
+  for (int e = 0; e < 16; e++) q[e] = nz ? q8k_round(inv, v[e]) : 0;
+  const int j = i16 >> 1, u = i16 & 1, qq = j >> 1;
 #pragma unroll
   for (int i = 0; i < 4; i++) {
-    const int l = 4 * (lane & 1) + i;
-    xh[((l * 4 + qq) * kF2Cols + n) * 8 + pos] = (_Float16)r.q[i];
+    const int l = 4 * u + i;
+    const half2v lo = (half2v){(_Float16)q[i], (_Float16)q[4 + i]};
+    const half2v hi = (half2v){(_Float16)q[8 + i], (_Float16)q[12 + i]};
+    *reinterpret_cast<uint2 *>(xh + ((l * 4 + qq) * kF2Cols + n) * 8 + 4 * (j & 1)) =
+        make_uint2(__builtin_bit_cast(uint32_t, lo), __builtin_bit_cast(uint32_t, hi));
   }
-  int s = (int)r.q[0] + (int)r.q[1] + (int)r.q[2] + (int)r.q[3];
-  s += __shfl_xor(s, 1);
-  s += __shfl_xor(s, 2);
-  if ((lane & 3) == 0) {
-    const int h = lane >> 2;  // 16 elements 16h .. 16h + 15
-    xb[((h >> 3) * kF2Cols + n) * 8 + (h & 7)] = (_Float16)s;
+  int s0 = 0, s1 = 0;
+#pragma unroll
+  for (int i = 0; i < 8; i++) {
+    s0 += q[i];
+    s1 += q[8 + i];
   }
-  if (lane == 0) xd[n] = r.d;
+  s0 += (int)dpp_u32<kDppXor1>((uint32_t)s0);
+  s1 += (int)dpp_u32<kDppXor1>((uint32_t)s1);
+  const int h = 2 * j + u;  // lane u writes group 2j + u
+  xb[((h >> 3) * kF2Cols + n) * 8 + (h & 7)] = (_Float16)(u ? s1 : s0);
+  if (i16 == 0) xd[n] = nz ? __fdiv_rn(1.0f, inv) : 0.0f;
 }
 
 // Copies `bytes` (a multiple of 16) from global to LDS with the wave's share
@@ -660,8 +676,8 @@ __global__ __launch_bounds__(256) void f2_reduce_kernel(const F2Args a, size_t t
   if (a.count > 2 && i >= a.part_off[2]) w = 2;
   if (a.count > 3 && i >= a.part_off[3]) w = 3;
   const size_t end = w + 1 < a.count ? a.part_off[w + 1] : total;
-  float *out = a.w[w].out - a.part_off[w];
-  if (i + 4 <= end && (((uintptr_t)(out + i)) & 15) == 0) {
+  float *out = a.w[w].out + (i - a.part_off[w]);
+  if (i + 4 <= end && (((uintptr_t)out) & 15) == 0) {
     float4 acc = *reinterpret_cast<const float4 *>(a.part + i);
     for (int r = 1; r < a.ksplit; r++) {
       const float4 p = *reinterpret_cast<const float4 *>(a.part + r * a.part_stride + i);
@@ -670,7 +686,7 @@ __global__ __launch_bounds__(256) void f2_reduce_kernel(const F2Args a, size_t t
       acc.z += p.z;
       acc.w += p.w;
     }
-    *reinterpret_cast<float4 *>(out + i) = acc;
+    *reinterpret_cast<float4 *>(out) = acc;
   } else {
     for (size_t e = i; e < i + 4 && e < total; e++) {
       int we = 0;
@@ -754,8 +770,8 @@ hipError_t launch_prefill_fast_geglu(const MfmaLaunch &l, const float *x, uint8_
     return hipErrorInvalidValue;
   const int nb = l.k / kQK;
   const int col_tiles = (l.cols + kF2Cols - 1) / kF2Cols;
-  hipLaunchKernelGGL(q8k_prefill_tiles_kernel, dim3(nb, col_tiles * kF2Cols), dim3(64), 0, s, x, l.k, nb, l.cols,
-                     scratch);
+  hipLaunchKernelGGL(q8k_prefill_tiles16_kernel, dim3(nb, col_tiles * kF2Cols / 16), dim3(256), 0, s, x, l.k, nb,
+                     l.cols, scratch);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
   F2Args a{};
@@ -798,8 +814,8 @@ hipError_t launch_prefill_fast(const MfmaLaunch &l, const float *x, uint8_t *scr
   if (l.count < 1 || l.count > kMaxWeights || l.cols < 1 || l.k % kQK != 0) return hipErrorInvalidValue;
   const F2Shape sh = f2_shape(l, num_cus);
   const int nb = sh.nb, col_tiles = sh.col_tiles;
-  hipLaunchKernelGGL(q8k_prefill_tiles_kernel, dim3(nb, col_tiles * kF2Cols), dim3(64), 0, s, x, l.k, nb, l.cols,
-                     scratch);
+  hipLaunchKernelGGL(q8k_prefill_tiles16_kernel, dim3(nb, col_tiles * kF2Cols / 16), dim3(256), 0, s, x, l.k, nb,
+                     l.cols, scratch);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
   F2Args a{};
