@@ -701,11 +701,11 @@ __global__ __launch_bounds__(256) void f2_reduce_kernel(const F2Args a, size_t t
 }
 
 // Block ranges per tile: enough to give every CU two tiles' worth of
-// workgroups when the launch has fewer tiles, at least four blocks a range.
+// workgroups when the launch has fewer tiles, at least two blocks a range.
 int f2_ksplit(int tiles, int nb, int num_cus) {
   if (tiles <= 0 || tiles >= 2 * num_cus) return 1;
   int ks = 2 * num_cus / tiles;
-  if (ks > nb / 4) ks = nb / 4;
+  if (ks > nb / 2) ks = nb / 2;
   if (ks > 8) ks = 8;
   return ks < 1 ? 1 : ks;
 }

@@ -14,7 +14,7 @@ Shapes cover the ways the workgroup tiles can be cut: rows not a multiple of
 single column, mixed Q4_K/Q6_K weights in one launch, both input sizes of
 the model and a 512-column chunk.  Launches of the fast kernel with fewer
 tiles than two per CU split each tile's blocks into ranges added by a
-reduction: 2 ranges for (64, 2560, 64) and the 512-column Q/K/V, 8 for
+reduction: 5 ranges for (64, 2560, 64), 2 for the 512-column Q/K/V, 8 for
 (300, 10240, 37) and (2560, 10240, 64).
 """
 import numpy as np
