@@ -104,7 +104,8 @@ def matvec_kernel_name(choice: str, k: int, m: int, specs: list) -> str:
     r6 = 64 // s
     tiles = sum((r + r6 - 1) // r6 for r in rows)
     tiles16 = sum((r + 15) // 16 for r in rows)
-    half = s <= 32 and m <= 4 and (choice == "half" or (choice == "auto" and s <= 16 and tiles <= 1024))
+    half = s <= 32 and m <= 4 and (choice == "half" or
+                                   (choice == "auto" and s <= 16 and tiles <= (2048 if m == 1 else 1024)))
     mfma = choice == "mfma" or (choice == "auto" and not half and k <= 2560 and
                                 (m >= 5 or (m >= 2 and tiles16 >= 1024)))
     if half:
