@@ -284,10 +284,10 @@ bool norm_prologue_ok(size_t count, Handle *const *hs, size_t cols) {
   return !use_mfma(cols, hs[0]->g.nb, tiles16);
 }
 
-// Whether a launch of `cols` columns (4 or more) runs the vector-ALU kernels
+// Whether a launch of `cols` columns (2 or more) runs the vector-ALU kernels
 // in one chunk, so it can take its input as a pre-quantised image.
 bool image_input_ok(size_t count, Handle *const *hs, size_t cols) {
-  if (cols < 4 || prefill_kind(cols) != 0) return false;
+  if (cols < 2 || prefill_kind(cols) != 0) return false;
   int tiles16 = 0;
   for (size_t i = 0; i < count; i++) tiles16 += (int)((hs[i]->row_count + 15) / 16);
   return !use_mfma(cols, hs[0]->g.nb, tiles16) && cols_per_launch(hs[0]->g, st().max_lds) >= (int)cols;
@@ -296,7 +296,7 @@ bool image_input_ok(size_t count, Handle *const *hs, size_t cols) {
 // norm != null: the input is formed from a residual stream (NormIn) -- in the
 // launch's prologue when the launch runs a vector-ALU kernel, else by the norm
 // kernel into norm_scratch first.
-// q8img_in (4 or more columns): the input already quantised, as written by
+// q8img_in (2 or more columns): the input already quantised, as written by
 // the norm or GeGLU kernels (q8_image_bytes(cols, nb)); used when the launch
 // runs the vector-ALU kernels in one chunk.  img_scratch: where a norm run
 // here writes that image for the launch.
@@ -305,7 +305,7 @@ int32_t run_matvec(size_t count, Handle *const *hs, const float *d_input, size_t
                    float *norm_scratch = nullptr, uint8_t *img_scratch = nullptr, const uint8_t *q8img_in = nullptr) {
   State &s = st();
   if (cols == 0) return HP_OK;
-  const bool image_ok = cols >= 4 && image_input_ok(count, hs, cols);
+  const bool image_ok = cols >= 2 && image_input_ok(count, hs, cols);
   if (norm && !norm_prologue_ok(count, hs, cols)) {
     uint8_t *img = image_ok && img_scratch ? img_scratch : nullptr;
     int32_t rc = run_norm(norm->y, (int)cols, (int)input_size, norm->w_post, norm->mode == 2 ? norm->x_res : nullptr,
@@ -422,7 +422,7 @@ int32_t run_matvec(size_t count, Handle *const *hs, const float *d_input, size_t
 // up of one type); otherwise the
 // projections (one launch, any kernel) into scratch, then the GeGLU kernel.
 // Both give the same bits.
-// q8img_out (4 or more columns): when the GeGLU runs as its own launch it also
+// q8img_out (2 or more columns): when the GeGLU runs as its own launch it also
 // writes d_out as a matvec input image there, and *q8img_written says so.
 int32_t run_matvec_geglu(Handle *hg, Handle *hu, const float *d_input, size_t input_size, size_t cols,
                          float *d_out, hipStream_t stream, const NormIn *norm = nullptr,
@@ -503,7 +503,7 @@ int32_t run_matvec_geglu(Handle *hg, Handle *hu, const float *d_input, size_t in
   rc = run_matvec(2, hs, d_input, input_size, cols, outs, stream);
   if (rc != HP_OK) return rc;
   hipEvent_t e2 = prof_begin(stream);
-  if (q8img_out && cols >= 4 && rows % kQK == 0) {
+  if (q8img_out && cols >= 2 && rows % kQK == 0) {
     HP_HIP_TRY(launch_geglu_q8k(outs[0], outs[1], (int)rows, (int)cols, gelu_constant(), d_out, q8img_out, stream));
     if (q8img_written) *q8img_written = true;
   } else {
@@ -1628,10 +1628,10 @@ int32_t hp_hip_decode_layers_device(const hp_hip_decode_layer_t *layers, size_t 
   if (hidden == 0 || hidden > kNormMaxN) return fail(HP_ERR_SHAPE, "hidden size must be 1..4096");
   // scratch ([M] rows each): xn, q, k, v, q after RoPE, attention, o, x1, h, y;
   // attention partials; RoPE tables [M][128] cos, sin
-  // (4 or more tokens) the Q/K/V and down inputs as pre-quantised images
+  // (2 or more tokens) the Q/K/V and down inputs as pre-quantised images
   auto al = [](size_t n) { return (n + 63) & ~(size_t)63; };
-  const size_t img_x = M >= 4 ? q8_image_bytes((int)M, (int)(hidden / kQK)) / sizeof(float) : 0;
-  const size_t img_h = M >= 4 ? q8_image_bytes((int)M, (int)(ffmax / kQK)) / sizeof(float) : 0;
+  const size_t img_x = M >= 2 ? q8_image_bytes((int)M, (int)(hidden / kQK)) / sizeof(float) : 0;
+  const size_t img_h = M >= 2 ? q8_image_bytes((int)M, (int)(ffmax / kQK)) / sizeof(float) : 0;
   const size_t sizes[14] = {al(M * hidden), al(M * qmax),   al(M * kvmax),  al(M * kvmax),
                             al(M * qmax),   al(M * qmax),   al(M * hidden), al(M * hidden),
                             al(M * ffmax),  al(M * hidden), al(partials),   al(M * kHeadDim / 2 * 4),
@@ -1650,8 +1650,8 @@ int32_t hp_hip_decode_layers_device(const hp_hip_decode_layer_t *layers, size_t 
   float *xn = buf[0], *q = buf[1], *k = buf[2], *v = buf[3], *qr = buf[4], *att = buf[5], *o = buf[6],
         *x1 = buf[7], *h = buf[8], *y = buf[9], *part = buf[10];
   double2 *rope_table = reinterpret_cast<double2 *>(buf[11]);
-  uint8_t *imgx = M >= 4 && hidden % kQK == 0 ? reinterpret_cast<uint8_t *>(buf[12]) : nullptr;
-  uint8_t *imgh = M >= 4 && ffmax % kQK == 0 ? reinterpret_cast<uint8_t *>(buf[13]) : nullptr;
+  uint8_t *imgx = M >= 2 && hidden % kQK == 0 ? reinterpret_cast<uint8_t *>(buf[12]) : nullptr;
+  uint8_t *imgh = M >= 2 && ffmax % kQK == 0 ? reinterpret_cast<uint8_t *>(buf[13]) : nullptr;
   // The norms ride in the prologues of the launches that consume them (one
   // token): the Q/K/V launch forms attn_norm(previous residual), the gate/up
   // launch ffn_norm(residual after attention).  With several tokens, or a

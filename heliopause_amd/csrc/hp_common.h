@@ -98,7 +98,7 @@ struct MatvecArgs {
   int Rh;             // half-split kernel: rows per unit (floor(32 / S))
   float *pair_out;    // gate/up + GeGLU launch: [cols][rows] output
   double gelu_c;      // sqrt(2 / pi) as Math.sqrt(2 / Math.PI)
-  // non-null (launches of 4 or more columns): the input already quantised,
+  // non-null (launches of 2 or more columns): the input already quantised,
   // as the LDS image of this launch's columns (q8_image_bytes(cols, nb)),
   // copied in place of the Q8_K prologue
   const uint8_t *q8img;

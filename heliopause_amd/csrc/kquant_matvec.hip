@@ -323,9 +323,9 @@ __global__ __launch_bounds__(256) void kquant_matvec_kernel(const MatvecArgs a) 
   __shared__ double norm_sh[8];  // two workgroup sums
   NormRegs nr;
   auto x_block = [&](int q) { return a.x + (size_t)(q / nb) * a.k + (size_t)(q % nb) * kQK; };
-  // four or more columns may come already quantised (a.q8img): the image
+  // two or more columns may come already quantised (a.q8img): the image
   // is copied in place of the Q8_K passes
-  const bool pre = M >= 4 && a.q8img != nullptr;
+  const bool pre = M >= 2 && a.q8img != nullptr;
   if (NORM) {
     norm_load<NORM>(a.norm, nr, grp, nb, i16);
   } else if (!pre) {
@@ -664,9 +664,9 @@ __global__ __launch_bounds__(256) void kquant_matvec_half_kernel(const MatvecArg
   __shared__ double norm_sh[8];  // two workgroup sums
   NormRegs nr;
   auto x_block = [&](int q) { return a.x + (size_t)(q / nb) * a.k + (size_t)(q % nb) * kQK; };
-  // four or more columns may come already quantised (a.q8img): the image
+  // two or more columns may come already quantised (a.q8img): the image
   // is copied in place of the Q8_K passes
-  const bool pre = M >= 4 && a.q8img != nullptr;
+  const bool pre = M >= 2 && a.q8img != nullptr;
   if (NORM) {
     norm_load<NORM>(a.norm, nr, grp, nb, i16);
   } else if (!pre) {
@@ -855,7 +855,7 @@ static hipError_t launch_half_m(const MatvecArgs &a, int num_cus, hipStream_t s)
 }
 
 hipError_t launch_matvec_half(const MatvecArgs &a, int num_cus, hipStream_t s) {
-  if (a.q8img && (a.cols < 4 || a.norm.mode != 0)) return hipErrorInvalidValue;
+  if (a.q8img && (a.cols < 2 || a.norm.mode != 0)) return hipErrorInvalidValue;
   if (a.norm.mode < 0 || a.norm.mode > 2 || (a.norm.mode != 0 && (a.cols != 1 || a.g.nb > 16)))
     return hipErrorInvalidValue;
   if (a.g.S > 32 || a.Rh < 1 || 2 * a.Rh * a.g.S > 64) return hipErrorInvalidValue;
@@ -894,7 +894,7 @@ hipError_t launch_matvec_pair(const MatvecArgs &a, int num_cus, hipStream_t s) {
 }
 
 hipError_t launch_matvec(const MatvecArgs &a, int num_cus, hipStream_t s) {
-  if (a.q8img && (a.cols < 4 || a.norm.mode != 0)) return hipErrorInvalidValue;
+  if (a.q8img && (a.cols < 2 || a.norm.mode != 0)) return hipErrorInvalidValue;
   if (a.norm.mode < 0 || a.norm.mode > 2 || (a.norm.mode != 0 && (a.cols != 1 || a.g.nb > 16)))
     return hipErrorInvalidValue;
   switch (a.cols) {

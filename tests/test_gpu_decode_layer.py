@@ -401,8 +401,8 @@ def test_draft_attention_prep_and_attention(hip, D, tokens, cap, pos, window, qs
     assert np.count_nonzero(steps) <= 0.03 * steps.size
 
 
-@pytest.mark.parametrize("full,tokens,pos", [(True, 4, 4093), (False, 3, 62), (False, 8, 0)],
-                         ids=["model-draft4", "small-wrap-draft3", "small-start-draft8"])
+@pytest.mark.parametrize("full,tokens,pos", [(True, 4, 4093), (True, 2, 4095), (False, 3, 62), (False, 8, 0)],
+                         ids=["model-draft4", "model-draft2", "small-wrap-draft3", "small-start-draft8"])
 def test_decode_draft_matches_oracle(hip, D, full, tokens, pos):
     """A draft of several tokens through one layer (every row kept)."""
     import torch
