@@ -67,6 +67,23 @@ def build(jobs: int | None = None) -> Path:
     return LIB
 
 
+SYNTH_SRC = CSRC / "hp_synth.c"
+SYNTH_LIB = PKG / "libhp_synth.so"
+
+
+def build_synth() -> Path:
+    """The host-side SplitMix64 stream of the synthetic workloads
+    (heliopause_amd/libhp_synth.so; plain C, no GPU code)."""
+    cc = os.environ.get("CC", shutil.which("gcc") or "cc")
+    tmp = SYNTH_LIB.with_suffix(".so.tmp")
+    cmd = [cc, "-O2", "-fPIC", "-shared", "-std=c11", "-Wall", "-Wextra", "-pthread", str(SYNTH_SRC), "-o", str(tmp)]
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError(f"synthetic-stream build failed:\n{r.stdout}\n{r.stderr}")
+    os.replace(tmp, SYNTH_LIB)
+    return SYNTH_LIB
+
+
 def build_napi() -> Path | None:
     """Node N-API addon over libhp_hip.so (heliopause_amd/napi/hp_hip.node).
 
@@ -93,4 +110,5 @@ def build_napi() -> Path | None:
 
 if __name__ == "__main__":
     print(build())
+    print(build_synth())
     print(build_napi())

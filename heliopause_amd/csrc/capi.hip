@@ -9,6 +9,7 @@
 #include "../../include/hp_gguf.h"
 #include "../../include/hp_hip.h"
 #include "hp_common.h"
+#include "hp_scratch.h"
 
 #include <algorithm>
 #include <atomic>
@@ -41,6 +42,16 @@ struct ProfileSlot {
   uint64_t launches = 0;
 };
 
+// Device memory for the scratch pool (hp_scratch.h).
+struct HipAlloc {
+  bool alloc(void **p, size_t bytes) { return hipMalloc(p, bytes) == hipSuccess; }
+  void free(void *p) { (void)hipFree(p); }
+  bool zero(void *p, size_t bytes, void *stream) {
+    hipStream_t q = static_cast<hipStream_t>(stream);
+    return hipMemsetAsync(p, 0, bytes, q) == hipSuccess && hipStreamSynchronize(q) == hipSuccess;
+  }
+};
+
 struct State {
   std::recursive_mutex mu;
   bool ready = false;
@@ -51,12 +62,16 @@ struct State {
   std::vector<Handle> handles;
   float *io_in = nullptr, *io_out[kMaxWeights] = {nullptr, nullptr, nullptr, nullptr};
   size_t io_in_cap = 0, io_out_cap[kMaxWeights] = {0, 0, 0, 0};
-  void *topk_scratch = nullptr, *topk_out = nullptr;  // selection scratch; ids + values
-  size_t topk_scratch_cap = 0, topk_out_cap = 0;
+  void *topk_out = nullptr;  // ids + values of the host-pointer top-k entry points
+  size_t topk_out_cap = 0;
   uint64_t matmul_calls = 0, launches = 0;
   int matvec_kernel = 0;  // 0 auto, 1 vector ALU, 2 matrix cores, 3 half-split, 4 prefill
-  void *prefill_scratch = nullptr;  // Q8_K of the columns of a prefill launch
-  size_t prefill_scratch_cap = 0;
+  // set while a host-pointer matmul entry point runs: the automatic policy then
+  // keeps to the bit-exact kernels, as the reference's resident calls are
+  bool host_exact = false;
+  // pre-quantised input images between the launches of a draft step (a
+  // test switch: off, every vector-ALU launch quantises its own input)
+  bool images = true;
   bool profiling = false;
   ProfileSlot prof[HP_KERNEL_COUNT];
   std::vector<hipEvent_t> event_pool;
@@ -72,9 +87,8 @@ struct State {
   // kept counts and probabilities
   void *sample_out = nullptr;
   size_t sample_out_cap = 0;
-  // decoder layers: attention partials; activations of a decode step
-  void *attn_scratch = nullptr, *decode_scratch = nullptr;
-  size_t attn_scratch_cap = 0, decode_scratch_cap = 0;
+  // intermediate device memory of the asynchronous entry points, per stream
+  ScratchPool<HipAlloc> pool;
 };
 
 State &st() {
@@ -155,6 +169,22 @@ int32_t grow(void **p, size_t *cap, size_t bytes) {
   }
   *cap = want;
   return HP_OK;
+}
+
+// Scratch of `kind` for work queued on `stream` (hp_scratch.h): per stream,
+// grow-only, and never grown while the stream captures a graph.
+int32_t scratch(hipStream_t stream, int kind, size_t bytes, void **out, bool zero = false) {
+  State &s = st();
+  void *key = stream ? static_cast<void *>(stream) : static_cast<void *>(s.stream);
+  hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+  if (hipStreamIsCapturing(stream, &cs) != hipSuccess) cs = hipStreamCaptureStatusNone;
+  switch (s.pool.get(key, kind, bytes, cs != hipStreamCaptureStatusNone, zero, out)) {
+    case kScratchOk: return HP_OK;
+    case kScratchCapturing:
+      return fail(HP_ERR_ARG, "scratch must be sized by an uncaptured call of this shape before graph capture");
+    case kScratchZeroFailed: return fail(HP_ERR_HIP, "clearing scratch failed");
+    default: return fail(HP_ERR_OOM, "device allocation failed");
+  }
 }
 
 hipEvent_t take_event() {
@@ -240,7 +270,7 @@ int prefill_kind(size_t cols) {
   if (forced == 4) return exact_fits ? 1 : 0;
   if (forced == 5) return fast_fits ? 2 : 0;
   if (forced != 0) return 0;
-  if (cols >= kFastMinCols && fast_fits) return 2;
+  if (cols >= kFastMinCols && fast_fits && !s.host_exact) return 2;
   if (cols >= kPrefillMinCols && exact_fits) return 1;
   return 0;
 }
@@ -305,7 +335,7 @@ int32_t run_matvec(size_t count, Handle *const *hs, const float *d_input, size_t
                    float *norm_scratch = nullptr, uint8_t *img_scratch = nullptr, const uint8_t *q8img_in = nullptr) {
   State &s = st();
   if (cols == 0) return HP_OK;
-  const bool image_ok = cols >= 2 && image_input_ok(count, hs, cols);
+  const bool image_ok = s.images && cols >= 2 && image_input_ok(count, hs, cols);
   if (norm && !norm_prologue_ok(count, hs, cols)) {
     uint8_t *img = image_ok && img_scratch ? img_scratch : nullptr;
     int32_t rc = run_norm(norm->y, (int)cols, (int)input_size, norm->w_post, norm->mode == 2 ? norm->x_res : nullptr,
@@ -355,9 +385,10 @@ int32_t run_matvec(size_t count, Handle *const *hs, const float *d_input, size_t
       l.out[i] = d_outs[i];
     }
     const size_t need = kind == 2 ? prefill_fast_bytes(l, s.num_cus) : prefill_q8k_bytes((int)input_size, (int)cols);
-    int32_t rc = grow(&s.prefill_scratch, &s.prefill_scratch_cap, need);
+    void *pre = nullptr;
+    int32_t rc = scratch(stream, kScratchPrefill, need, &pre);
     if (rc != HP_OK) return rc;
-    uint8_t *q8 = static_cast<uint8_t *>(s.prefill_scratch);
+    uint8_t *q8 = static_cast<uint8_t *>(pre);
     hipEvent_t e1 = prof_begin(stream);
     if (kind == 2) {
       HP_HIP_TRY(launch_prefill_fast(l, d_input, q8, s.num_cus, stream));
@@ -474,8 +505,8 @@ int32_t run_matvec_geglu(Handle *hg, Handle *hu, const float *d_input, size_t in
   }
   if (prefill_kind(cols) == 2 && hg->type == hu->type) {
     // fast prefill: gate and up rows in one tile, GeGLU in its epilogue
-    int32_t rc = grow(&s.prefill_scratch, &s.prefill_scratch_cap,
-                      prefill_fast_geglu_bytes((int)input_size, (int)cols));
+    void *pre = nullptr;
+    int32_t rc = scratch(stream, kScratchPrefill, prefill_fast_geglu_bytes((int)input_size, (int)cols), &pre);
     if (rc != HP_OK) return rc;
     MfmaLaunch l{};
     l.count = 2;
@@ -488,22 +519,22 @@ int32_t run_matvec_geglu(Handle *hg, Handle *hu, const float *d_input, size_t in
       l.rows[i] = (int)rows;
     }
     hipEvent_t e1 = prof_begin(stream);
-    HP_HIP_TRY(launch_prefill_fast_geglu(l, d_input, static_cast<uint8_t *>(s.prefill_scratch), gelu_constant(), d_out,
+    HP_HIP_TRY(launch_prefill_fast_geglu(l, d_input, static_cast<uint8_t *>(pre), gelu_constant(), d_out,
                                          s.num_cus, stream));
     prof_end(HP_KERNEL_MATVEC, e1, stream);
     s.launches += 2;
     s.matmul_calls++;
     return HP_OK;
   }
-  int32_t rc = grow((void **)&s.io_out[2], &s.io_out_cap[2], cols * rows * sizeof(float));
-  if (rc == HP_OK) rc = grow((void **)&s.io_out[3], &s.io_out_cap[3], cols * rows * sizeof(float));
+  void *sums = nullptr;
+  int32_t rc = scratch(stream, kScratchGeglu, 2 * cols * rows * sizeof(float), &sums);
   if (rc != HP_OK) return rc;
   Handle *hs[2] = {hg, hu};
-  float *outs[2] = {s.io_out[2], s.io_out[3]};
+  float *outs[2] = {static_cast<float *>(sums), static_cast<float *>(sums) + cols * rows};
   rc = run_matvec(2, hs, d_input, input_size, cols, outs, stream);
   if (rc != HP_OK) return rc;
   hipEvent_t e2 = prof_begin(stream);
-  if (q8img_out && cols >= 2 && rows % kQK == 0) {
+  if (q8img_out && s.images && cols >= 2 && rows % kQK == 0) {
     HP_HIP_TRY(launch_geglu_q8k(outs[0], outs[1], (int)rows, (int)cols, gelu_constant(), d_out, q8img_out, stream));
     if (q8img_written) *q8img_written = true;
   } else {
@@ -513,6 +544,16 @@ int32_t run_matvec_geglu(Handle *hg, Handle *hu, const float *d_input, size_t in
   s.launches++;
   return HP_OK;
 }
+
+// Scope of a host-pointer matmul entry point (hp_hip_matmul, _multi, _geglu,
+// _topk, _topk_sample): these replace the reference's resident matmul calls,
+// whose results are bit-exact, so the automatic kernel policy does not pick
+// the fast prefill kernel inside them (selector 5 still forces it).
+struct HostExactScope {
+  bool prev;
+  HostExactScope() : prev(st().host_exact) { st().host_exact = true; }
+  ~HostExactScope() { st().host_exact = prev; }
+};
 
 int32_t geglu_pair_check(uint64_t gate, uint64_t up, size_t input_len, size_t input_size, size_t cols,
                          size_t output_len, Handle **hg, Handle **hu) {
@@ -748,17 +789,6 @@ SampleParams sample_params(const hp_hip_sampling_t *o) {
   return p;
 }
 
-// Grows a library scratch buffer, which a stream capturing a graph must not
-// do (the allocation would not be part of the graph).
-int32_t grow_uncaptured(void **p, size_t *cap, size_t bytes, hipStream_t stream) {
-  if (*p && *cap >= bytes) return HP_OK;
-  hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
-  if (hipStreamIsCapturing(stream, &cs) != hipSuccess) cs = hipStreamCaptureStatusNone;
-  if (cs != hipStreamCaptureStatusNone)
-    return fail(HP_ERR_ARG, "scratch must be sized by an uncaptured call of this shape before graph capture");
-  return grow(p, cap, bytes);
-}
-
 constexpr size_t kNormMaxN = 4096;
 
 int32_t attention_check(const hp_hip_attention_config_t *c) {
@@ -880,17 +910,14 @@ int32_t run_topk(const float *d_logits, size_t rows, size_t n, size_t k, double 
   State &s = st();
   const size_t batch = rows < (size_t)kTopkMaxRows ? rows : (size_t)kTopkMaxRows;
   const size_t bytes = topk_scratch_bytes((int)batch, (int)n, (int)k);
-  if (s.topk_scratch_cap < bytes || !s.topk_scratch) {
-    int32_t rc = grow(&s.topk_scratch, &s.topk_scratch_cap, bytes);
-    if (rc != HP_OK) return rc;
-    HP_HIP_TRY(hipMemsetAsync(s.topk_scratch, 0, s.topk_scratch_cap, s.stream));
-    HP_HIP_TRY(hipStreamSynchronize(s.stream));
-  }
+  void *sel = nullptr;
+  int32_t rc = scratch(stream, kScratchTopk, bytes, &sel, true);
+  if (rc != HP_OK) return rc;
   hipEvent_t e = prof_begin(stream);
   for (size_t r0 = 0; r0 < rows; r0 += batch) {
     const size_t nr = rows - r0 < batch ? rows - r0 : batch;
     HP_HIP_TRY(launch_topk(d_logits + r0 * n, (int)nr, (int)n, (int)k, cap,
-                           static_cast<uint8_t *>(s.topk_scratch), d_ids + r0 * k, d_vals + r0 * k, stream));
+                           static_cast<uint8_t *>(sel), d_ids + r0 * k, d_vals + r0 * k, stream));
     s.launches += 3;
   }
   prof_end(HP_KERNEL_TOPK, e, stream);
@@ -964,20 +991,14 @@ int32_t hp_hip_shutdown(void) {
     s.io_out[i] = nullptr;
     s.io_out_cap[i] = 0;
   }
-  if (s.topk_scratch) (void)hipFree(s.topk_scratch);
   if (s.topk_out) (void)hipFree(s.topk_out);
   if (s.sample_out) (void)hipFree(s.sample_out);
-  if (s.prefill_scratch) (void)hipFree(s.prefill_scratch);
-  s.prefill_scratch = nullptr;
-  s.prefill_scratch_cap = 0;
   s.sample_out = nullptr;
   s.sample_out_cap = 0;
-  if (s.attn_scratch) (void)hipFree(s.attn_scratch);
-  if (s.decode_scratch) (void)hipFree(s.decode_scratch);
-  s.attn_scratch = s.decode_scratch = nullptr;
-  s.attn_scratch_cap = s.decode_scratch_cap = 0;
-  s.topk_scratch = s.topk_out = nullptr;
-  s.topk_scratch_cap = s.topk_out_cap = 0;
+  s.topk_out = nullptr;
+  s.topk_out_cap = 0;
+  (void)hipDeviceSynchronize();
+  s.pool.release_all();
   prof_collect();
   for (hipEvent_t e : s.event_pool) (void)hipEventDestroy(e);
   s.event_pool.clear();
@@ -1136,6 +1157,7 @@ int32_t hp_hip_matmul_multi(size_t count, const uint64_t *handles, const float *
                             const size_t *output_lens) {
   State &s = st();
   std::lock_guard<std::recursive_mutex> lock(s.mu);
+  HostExactScope exact;
   int32_t rc = ensure_init(s.ready ? s.device : 0);
   if (rc != HP_OK) return rc;
   if (count == 0 || count > (size_t)kMaxWeights || input_len != sat_mul(input_size, column_count))
@@ -1249,6 +1271,7 @@ int32_t hp_hip_matmul_topk(uint64_t handle, const float *input, size_t input_len
                            size_t out_len) {
   State &s = st();
   std::lock_guard<std::recursive_mutex> lock(s.mu);
+  HostExactScope exact;
   Handle *h = lookup(handle);
   if (!h) return fail(HP_ERR_HANDLE, "unknown weight handle");
   if (h->input_size != input_size || input_len != sat_mul(input_size, column_count))
@@ -1305,6 +1328,7 @@ int32_t hp_hip_matmul_topk_sample(uint64_t handle, const float *input, size_t in
                                   double *probabilities, int32_t *kept, size_t out_len) {
   State &s = st();
   std::lock_guard<std::recursive_mutex> lock(s.mu);
+  HostExactScope exact;
   Handle *h = lookup(handle);
   if (!h) return fail(HP_ERR_HANDLE, "unknown weight handle");
   if (h->input_size != input_size || input_len != sat_mul(input_size, column_count))
@@ -1373,6 +1397,7 @@ int32_t hp_hip_matmul_geglu(uint64_t gate, uint64_t up, const float *input, size
                             size_t column_count, float *output, size_t output_len) {
   State &s = st();
   std::lock_guard<std::recursive_mutex> lock(s.mu);
+  HostExactScope exact;
   int32_t rc = ensure_init(s.ready ? s.device : 0);
   if (rc != HP_OK) return rc;
   Handle *hg, *hu;
@@ -1463,6 +1488,13 @@ int32_t hp_hip_set_matvec_kernel(int32_t which) {
   return HP_OK;
 }
 
+int32_t hp_hip_set_input_images(int32_t enable) {
+  State &s = st();
+  std::lock_guard<std::recursive_mutex> lock(s.mu);
+  s.images = enable != 0;
+  return HP_OK;
+}
+
 int32_t hp_hip_stats(hp_hip_stats_t *out) {
   State &s = st();
   std::lock_guard<std::recursive_mutex> lock(s.mu);
@@ -1473,7 +1505,8 @@ int32_t hp_hip_stats(hp_hip_stats_t *out) {
       r.handle_count++;
       r.resident_bytes += h.byte_length + h.seg_bytes;
     }
-  r.scratch_bytes = s.io_in_cap + s.topk_scratch_cap + s.topk_out_cap;
+  r.scratch_bytes = s.io_in_cap + s.topk_out_cap + s.sample_out_cap + s.pool.stats().live_bytes +
+                    s.pool.stats().retired_bytes;
   for (int i = 0; i < kMaxWeights; i++) r.scratch_bytes += s.io_out_cap[i];
   r.matmul_calls = s.matmul_calls;
   r.kernel_launches = s.launches;
@@ -1586,10 +1619,10 @@ int32_t hp_hip_gqa_attention_device(const hp_hip_attention_config_t *config, siz
   if (token_count < 1 || token_count > (size_t)kMaxTokens) return fail(HP_ERR_SHAPE, "token_count must be 1..8");
   if (!d_q || !d_key_cache || !d_value_cache || !d_position || !d_output) return fail(HP_ERR_ARG, "null pointer");
   hipStream_t strm = stream ? static_cast<hipStream_t>(stream) : s.stream;
-  rc = grow_uncaptured(&s.attn_scratch, &s.attn_scratch_cap,
-                       attn_partial_floats(config->head_count_kv, config->capacity, (int)token_count) *
-                           sizeof(float),
-                       strm);
+  void *partials = nullptr;
+  rc = scratch(strm, kScratchAttn,
+               attn_partial_floats(config->head_count_kv, config->capacity, (int)token_count) * sizeof(float),
+               &partials);
   if (rc != HP_OK) return rc;
   AttnArgs a = attn_args(config);
   a.q = d_q;
@@ -1598,7 +1631,7 @@ int32_t hp_hip_gqa_attention_device(const hp_hip_attention_config_t *config, siz
   a.position = d_position;
   a.out = d_output;
   a.tokens = (int)token_count;
-  return run_attention(a, static_cast<float *>(s.attn_scratch), strm);
+  return run_attention(a, static_cast<float *>(partials), strm);
 }
 
 int32_t hp_hip_decode_layers_device(const hp_hip_decode_layer_t *layers, size_t layer_count, size_t token_count,
@@ -1639,10 +1672,11 @@ int32_t hp_hip_decode_layers_device(const hp_hip_decode_layer_t *layers, size_t 
   size_t total = 0;
   for (size_t z : sizes) total += z;
   hipStream_t strm = stream ? static_cast<hipStream_t>(stream) : s.stream;
-  rc = grow_uncaptured(&s.decode_scratch, &s.decode_scratch_cap, total * sizeof(float), strm);
+  void *dscr = nullptr;
+  rc = scratch(strm, kScratchDecode, total * sizeof(float), &dscr);
   if (rc != HP_OK) return rc;
   float *buf[14];
-  float *p = static_cast<float *>(s.decode_scratch);
+  float *p = static_cast<float *>(dscr);
   for (int i = 0; i < 14; i++) {
     buf[i] = p;
     p += sizes[i];

@@ -1,0 +1,126 @@
+// hp_scratch.h -- device scratch of the *_device entry points: one set per
+// stream, grow-only, never freed while a captured graph may still hold it.
+//
+// The asynchronous entry points (decode layers, attention, top-k, the
+// prefill pre-pass, the gate/up sums of a split GeGLU) keep intermediate
+// results in library-owned device memory.  Two rules make that safe under
+// HIP graph capture and across caller streams:
+//   * Each (stream, kind) pair owns its buffer, so calls queued on different
+//     streams never share intermediate memory.  A captured graph keeps the
+//     buffers of the stream it was captured on.
+//   * A buffer that is too small is replaced by a larger one, and the old one
+//     is retired, not freed: a graph captured earlier may still point at it.
+//     Retired and live buffers are freed only by release_all()
+//     (hp_hip_shutdown).  Growth itself is refused while the stream is
+//     capturing (the allocation would not be part of the graph), so a
+//     captured call must follow an uncaptured call of the same shape.
+// Capacities grow at least 2x, so retired memory stays below the live size.
+//
+// Host-only C++ with the allocator as a template parameter, so the policy
+// can be exercised on the CPU with a recording allocator.
+#ifndef HP_SCRATCH_H
+#define HP_SCRATCH_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#include <map>
+#include <utility>
+#include <vector>
+
+namespace hp {
+
+enum ScratchKind {
+  kScratchDecode = 0,   // activations of a decode step
+  kScratchAttn = 1,     // attention partials
+  kScratchTopk = 2,     // top-k selection state (zeroed when allocated)
+  kScratchPrefill = 3,  // Q8_K / f16 images of a prefill launch
+  kScratchGeglu = 4,    // gate and up sums ahead of a GeGLU launch
+  kScratchKinds = 5
+};
+
+enum ScratchStatus { kScratchOk = 0, kScratchCapturing = 1, kScratchNoMemory = 2, kScratchZeroFailed = 3 };
+
+// Alloc provides:
+//   bool alloc(void **p, size_t bytes);            device allocation
+//   void free(void *p);                            device free
+//   bool zero(void *p, size_t bytes, void *stream) clear, complete on return
+template <class Alloc>
+class ScratchPool {
+ public:
+  struct Stats {
+    uint64_t live_bytes = 0;     // buffers currently handed out
+    uint64_t retired_bytes = 0;  // replaced buffers kept until release_all
+    uint64_t allocations = 0;
+    uint64_t frees = 0;          // buffers freed (only release_all frees)
+  };
+
+  explicit ScratchPool(Alloc a = Alloc()) : alloc_(a) {}
+
+  // A buffer of at least `bytes` for (stream, kind) in *out.
+  int get(void *stream, int kind, size_t bytes, bool capturing, bool zero, void **out) {
+    Buf &b = sets_[stream].buf[kind];
+    if (b.p && b.cap >= bytes) {
+      *out = b.p;
+      return kScratchOk;
+    }
+    if (capturing) return kScratchCapturing;
+    size_t want = bytes < 4096 ? 4096 : bytes;
+    if (b.p && want < 2 * b.cap) want = 2 * b.cap;
+    void *p = nullptr;
+    if (!alloc_.alloc(&p, want) || !p) return kScratchNoMemory;
+    if (zero && !alloc_.zero(p, want, stream)) {
+      alloc_.free(p);
+      return kScratchZeroFailed;
+    }
+    stats_.allocations++;
+    if (b.p) {
+      retired_.push_back(b);
+      stats_.retired_bytes += b.cap;
+      stats_.live_bytes -= b.cap;
+    }
+    b.p = p;
+    b.cap = want;
+    stats_.live_bytes += want;
+    *out = p;
+    return kScratchOk;
+  }
+
+  // Frees every buffer, live and retired.  The caller has synchronised the
+  // device and no graph that holds these buffers is replayed afterwards.
+  void release_all() {
+    for (auto &kv : sets_)
+      for (Buf &b : kv.second.buf)
+        if (b.p) {
+          alloc_.free(b.p);
+          stats_.frees++;
+          b = Buf();
+        }
+    for (Buf &b : retired_) {
+      alloc_.free(b.p);
+      stats_.frees++;
+    }
+    sets_.clear();
+    retired_.clear();
+    stats_.live_bytes = stats_.retired_bytes = 0;
+  }
+
+  const Stats &stats() const { return stats_; }
+
+ private:
+  struct Buf {
+    void *p = nullptr;
+    size_t cap = 0;
+  };
+  struct Set {
+    Buf buf[kScratchKinds];
+  };
+  Alloc alloc_;
+  std::map<void *, Set> sets_;
+  std::vector<Buf> retired_;
+  Stats stats_;
+};
+
+}  // namespace hp
+
+#endif

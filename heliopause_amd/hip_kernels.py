@@ -156,6 +156,8 @@ def _declare_optional(L: ctypes.CDLL) -> None:
     L.hp_hip_matmul_topk_sample.restype = i32
     L.hp_hip_set_matvec_kernel.argtypes = [i32]
     L.hp_hip_set_matvec_kernel.restype = i32
+    L.hp_hip_set_input_images.argtypes = [i32]
+    L.hp_hip_set_input_images.restype = i32
     L.hp_hip_matmul_geglu.argtypes = [_u64, _u64, ctypes.c_void_p, _sz, _sz, _sz, ctypes.c_void_p, _sz]
     L.hp_hip_matmul_geglu.restype = i32
     L.hp_hip_matmul_geglu_device.argtypes = [_u64, _u64, ctypes.c_void_p, _sz, _sz, _sz, ctypes.c_void_p, _sz,
@@ -461,6 +463,11 @@ def setMatvecKernel(which: int) -> None:
     the 1e-4 relative tolerance of projections.  No counterpart in the
     reference."""
     assertHipOk(lib().hp_hip_set_matvec_kernel(int(which)), "setMatvecKernel")
+
+
+def setInputImages(enable: bool) -> None:
+    """Test switch: pre-quantised input images inside draft steps (default on)."""
+    assertHipOk(lib().hp_hip_set_input_images(1 if enable else 0), "setInputImages")
 
 
 def profile(enable: bool) -> None:

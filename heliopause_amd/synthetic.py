@@ -58,8 +58,40 @@ def derive(seed: int, *labels) -> int:
     return s
 
 
+_SYNTH = None
+
+
+def _synth_lib():
+    """The C form of the stream (libhp_synth.so, built beside this file), or
+    None; both give the same words."""
+    global _SYNTH
+    if _SYNTH is None:
+        import ctypes
+        from pathlib import Path
+
+        path = Path(__file__).resolve().parent / "libhp_synth.so"
+        _SYNTH = False
+        if path.exists():
+            try:
+                L = ctypes.CDLL(str(path))
+                L.hp_synth_splitmix64.argtypes = [ctypes.c_uint64, ctypes.c_uint64, ctypes.c_uint64,
+                                                  ctypes.c_void_p, ctypes.c_int]
+                L.hp_synth_splitmix64.restype = ctypes.c_int
+                _SYNTH = L
+            except OSError:
+                _SYNTH = False
+    return _SYNTH or None
+
+
 def splitmix64(seed: int, n: int, start: int = 0) -> np.ndarray:
     """Draws ``start .. start+n-1`` of the SplitMix64 stream ``seed``."""
+    L = _synth_lib() if n >= 4096 else None
+    if L is not None:
+        import os
+
+        out = np.empty(n, dtype=np.uint64)
+        L.hp_synth_splitmix64(seed & MASK64, start, n, out.ctypes.data, min(16, os.cpu_count() or 1))
+        return out
     with np.errstate(over="ignore"):
         i = np.arange(start + 1, start + n + 1, dtype=np.uint64)
         z = np.uint64(seed & MASK64) + i * GOLDEN
@@ -68,7 +100,7 @@ def splitmix64(seed: int, n: int, start: int = 0) -> np.ndarray:
 
 def random_bytes(seed: int, nbytes: int) -> np.ndarray:
     words = splitmix64(seed, (nbytes + 7) // 8)
-    return words.view(np.uint8)[:nbytes].copy()
+    return words.view(np.uint8)[:nbytes]
 
 
 def normal(seed: int, n: int) -> np.ndarray:

@@ -14,6 +14,22 @@
  * *_device entry points take device pointers and are asynchronous on the
  * given stream.  Calls are serialised by an internal lock; results written
  * by concurrent calls on one device must not overlap.
+ *
+ * Intermediate device memory of the *_device entry points (decode
+ * activations, attention partials, top-k selection state, prefill images,
+ * gate/up sums) belongs to the stream a call is queued on: calls on
+ * different streams never share it, and calls queued on one stream run in
+ * order.  It only grows, and replaced buffers are kept until
+ * hp_hip_shutdown, so a HIP graph captured earlier never points at freed
+ * memory.  Growth is refused while the stream captures (HP_ERR_ARG): a
+ * captured call must follow an uncaptured call of the same shape on the
+ * capturing stream.  Replaying a graph concurrently with other calls on its
+ * capture stream races on that stream's scratch.
+ *
+ * The host-pointer matmul entry points (hp_hip_matmul, _multi, _geglu,
+ * _topk, _topk_sample) stay on the bit-exact kernels under the automatic
+ * kernel policy; the fast prefill kernel (1e-4 relative) runs automatically
+ * only on *_device calls of 64 or more columns.
  */
 #ifndef HP_HIP_H
 #define HP_HIP_H
@@ -217,7 +233,7 @@ int32_t hp_hip_quantize_q8_k(const float *input, size_t input_len, size_t input_
  * test hook): 0 = automatic (by column count and tile count: half-split
  * vector ALU for small projections, vector ALU for one column, matrix
  * cores for several columns of large ones, the bit-exact prefill kernel
- * from 32 columns, the fast prefill kernel from 64), 1 = always the
+ * from 32 columns, the fast prefill kernel from 64 on *_device calls), 1 = always the
  * vector-ALU kernel, 2 = the matrix-core kernel whenever its LDS fits the
  * device, 3 = the half-split vector-ALU kernel (two lanes per row-block) for
  * up to four columns, 4 = the bit-exact prefill kernel (64-column tiles) for
@@ -226,6 +242,14 @@ int32_t hp_hip_quantize_q8_k(const float *input, size_t input_len, size_t input_
  * each block's eight lane-class sums before scaling, so its outputs agree
  * within the 1e-4 relative tolerance of projections (M >= 64 prefill). */
 int32_t hp_hip_set_matvec_kernel(int32_t which);
+
+/* Pre-quantised input images inside a draft step (no counterpart in the
+ * reference; a test hook): with enable != 0 (the default) the norm and GeGLU
+ * launches of hp_hip_decode_layers_device at 2..8 tokens also write their
+ * output as the next projection's Q8_K input, which the projection copies
+ * instead of quantising; with 0 every projection quantises its f32 input
+ * itself.  Both give the same bits. */
+int32_t hp_hip_set_input_images(int32_t enable);
 
 /* wasmResidentWeightStats (wasm-kernels.ts:586-591) plus call counters. */
 int32_t hp_hip_stats(hp_hip_stats_t *out);
@@ -254,9 +278,9 @@ int32_t hp_hip_profile_read(int32_t kernel, double *total_ms, uint64_t *launches
  * WASM runner keeps f32 entries.
  *
  * Calls under HIP graph capture must follow an uncaptured call of the same
- * shape: the library's scratch is sized outside capture, and a call that
- * would have to grow it while its stream is capturing fails with
- * HP_ERR_ARG. */
+ * shape on the capturing stream: the stream's scratch is sized outside
+ * capture, and a call that would have to grow it while its stream is
+ * capturing fails with HP_ERR_ARG. */
 typedef struct hp_hip_attention_config {
   int32_t head_count;     /* query heads */
   int32_t head_count_kv;  /* key/value heads: head_count % head_count_kv == 0,

@@ -11,16 +11,18 @@ are tolerances stated per step:
 - attention prologue: q within 1 f32 ulp; cache entries (f16) within one
   f16 step;
 - attention output (f16-rounded by castF16Rows): per head, max relative
-  error 2^-8 (four f16 steps), relative to max(|ref|, 0.01 rms(ref)): with
-  unscaled N(0,1) queries and keys the scores reach |s| ~ 50, their f32 sums
-  differ by ~1e-5 between summation orders, and outputs that cancel to a
-  few percent of the head's scale carry that absolute error; at most 3 % of
-  elements off at all (1.4 % measured with unscaled queries, where each
-  output is dominated by a few keys);
+  error 2^-8 (four f16 steps; 2.7e-3 is the largest measured), relative to
+  max(|ref|, 0.01 rms(ref)): with unscaled N(0,1) queries and keys the
+  scores reach |s| ~ 50, their f32 sums differ by ~1e-5 between summation
+  orders, and outputs that cancel to a few percent of the head's scale carry
+  that absolute error; at most 2 % of elements off at all (1.6 % measured
+  with unscaled queries, where each output is dominated by a few keys);
 - a whole layer: max relative error LAYER_TOL of the new residual stream
-  (relative to max(|ref|, 0.01 rms(ref))).  The f16 steps of the attention
-  output feed the O projection's Q8_K input, which can move by one
-  quantisation step in a block.
+  (relative to max(|ref|, 0.01 rms(ref))).  An f16 step of the attention
+  output feeds the O projection's Q8_K input, which can move by one
+  quantisation step in a block.  Measured on every layer case here: 0 (the
+  residual stream comes out bit-identical), which the printed fraction of
+  identical elements shows.
 Projections inside the layer are the bit-exact matvec kernels.
 """
 import numpy as np
@@ -32,7 +34,7 @@ from heliopause_amd import synthetic as S
 
 pytestmark = pytest.mark.gpu
 
-LAYER_TOL = 2e-3
+LAYER_TOL = 5e-4
 FLOOR = 0.01
 
 
@@ -202,7 +204,7 @@ def test_gqa_attention(hip, D, nq, nkv, cap, pos, window, qscale):
     print(f"max rel err per head {max(errs):.2e}, elements off {np.count_nonzero(steps)}, max steps {steps.max()}",
           flush=True)
     assert max(errs) <= 2.0 ** -8
-    assert np.count_nonzero(steps) <= 0.03 * steps.size, np.count_nonzero(steps)
+    assert np.count_nonzero(steps) <= 0.02 * steps.size, np.count_nonzero(steps)
 
 
 def _small_shape(**kw):
@@ -398,7 +400,7 @@ def test_draft_attention_prep_and_attention(hip, D, tokens, cap, pos, window, qs
     steps = _f16_steps(got, ref)
     print(f"max rel err {max(errs):.2e}, elements off {np.count_nonzero(steps)}", flush=True)
     assert max(errs) <= 2.0 ** -8
-    assert np.count_nonzero(steps) <= 0.03 * steps.size
+    assert np.count_nonzero(steps) <= 0.02 * steps.size
 
 
 @pytest.mark.parametrize("full,tokens,pos", [(True, 4, 4093), (True, 2, 4095), (False, 3, 62), (False, 8, 0)],

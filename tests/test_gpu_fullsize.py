@@ -1,0 +1,274 @@
+"""GPU parity at the benchmark's full sizes, against the oracle.
+
+- The output head, Q6_K 262144 x 2560 (550 MB), at one column (vector ALU)
+  and four columns (matrix cores), with the top-40 of every column: logits
+  bit-identical (lib.rs:1923-1968), top-40 ids and values identical
+  (runtime.ts:514-527).  Both kernels cap their grid at 8 workgroups per CU,
+  so a launch of this size makes every wave walk several tiles.
+- Row counts just past that cap, with a ragged last tile, for each matvec
+  kernel (vector ALU, half-split, matrix cores) and both block types.
+- The FFN of one layer at its real shape (gate/up Q4_K 10240 x 2560, GeGLU,
+  down Q6_K 2560 x 10240) at 1, 2, 4 and 8 columns: bit-identical, through
+  the host-pointer and the device-pointer entry points.
+- A whole decode step of the 42-layer model (4096-token caches, token at
+  position 4096) plus the output norm, head and top-40, and a 4-token draft
+  of it, against the oracle's layers (oracle/decode_layer.py) run over all 42
+  layers: the residual stream within the layer tolerance and the top-40 ids
+  identical.
+- Draft steps with the pre-quantised input images on and off: identical bits.
+"""
+import numpy as np
+import pytest
+
+from heliopause_amd import decode as DM
+from heliopause_amd import synthetic as S
+
+pytestmark = pytest.mark.gpu
+
+TYPES = {"Q4_K": 1, "Q6_K": 3}
+HEAD_ROWS, HIDDEN, FFN = 262144, 2560, 10240
+LAYER_TOL = 5e-4   # the residual stream after a layer, relative to max(|ref|, 0.01 rms(ref))
+FLOOR = 0.01
+
+
+def _bits(a):
+    return np.ascontiguousarray(a, dtype=np.float32).reshape(-1).view(np.uint32)
+
+
+def _dev(a):
+    import torch
+
+    return torch.from_numpy(np.ascontiguousarray(a)).to(torch.device("cuda:0"))
+
+
+def _rel(got, ref):
+    got = np.asarray(got, np.float64).reshape(-1)
+    ref = np.asarray(ref, np.float64).reshape(-1)
+    den = np.maximum(np.abs(ref), FLOOR * np.sqrt(np.mean(ref * ref)))
+    return float(np.max(np.abs(got - ref) / den))
+
+
+def _first_diff(got, ref):
+    bad = np.flatnonzero(_bits(got) != _bits(ref))
+    return bad.size, bad[:4], np.asarray(got).reshape(-1)[bad[:4]], np.asarray(ref).reshape(-1)[bad[:4]]
+
+
+def _topk_ok(got, logits, k, oracle):
+    for r, row in enumerate(np.atleast_2d(logits)):
+        ids, vals = oracle.topk(row, k)
+        g_ids = np.array([c["id"] for c in got[r]], dtype=np.uint32)
+        g_vals = np.array([c["value"] for c in got[r]], dtype=np.float32)
+        assert np.array_equal(g_ids, ids), (r, g_ids[:6], ids[:6])
+        assert np.array_equal(_bits(g_vals), _bits(vals)), r
+
+
+def _cus(hip):
+    hip.assertHipOk(hip.lib().hp_hip_init(0), "init")
+    cus = hip.hipResidentWeightStats()["computeUnits"]
+    assert cus > 0
+    return cus
+
+
+@pytest.fixture(scope="module")
+def head_blocks():
+    return S.q6_k_blocks(S.derive(S.config_seed(4), "head-full"), HEAD_ROWS, HIDDEN)
+
+
+@pytest.fixture
+def selector(request, hip):
+    hip.setMatvecKernel(request.param)
+    yield request.param
+    hip.setMatvecKernel(0)
+
+
+@pytest.mark.parametrize("m", [1, 4])
+def test_head_full_size(hip, oracle, head_blocks, m):
+    """Config 4: the tied head at its real size; one column runs the
+    vector-ALU kernel (43,691 tiles of 6 rows), four the matrix cores
+    (16,384 tiles of 16 rows), both past their grid cap."""
+    x = S.activations(S.derive(S.config_seed(4), "x-full", m), m, HIDDEN)
+    print(f"head full size m={m}", flush=True)
+    h = hip.createHipQuantizedWeightHandle("Q6_K", head_blocks, HIDDEN, HEAD_ROWS)
+    try:
+        cus = _cus(hip)
+        assert HEAD_ROWS // 6 > 32 * cus and HEAD_ROWS // 16 > 32 * cus   # past both grid caps
+        logits = hip.matMulQuantizedHipResident(h, x, HIDDEN, HEAD_ROWS, m)
+        top = hip.matMulQuantizedHipResidentTopK(h, x, HIDDEN, m, 40)
+    finally:
+        hip.releaseHipQuantizedWeightHandle(h)
+    ref = oracle.matmul(3, head_blocks, x, HEAD_ROWS, threads=8)
+    assert np.array_equal(_bits(logits), _bits(ref)), _first_diff(logits, ref)
+    _topk_ok(top, ref, 40, oracle)
+
+
+# (selector, rows per grid unit): vector ALU tiles of R rows, half-split units
+# of Rh rows, matrix-core tiles of 16 rows; K = 2560 has R = 6 and Rh = 3,
+# K = 10240 has R = 3 and Rh = 1
+CAP_CASES = [(1, "Q4_K", 2560, 6, 1), (1, "Q6_K", 2560, 6, 3), (1, "Q6_K", 10240, 3, 2),
+             (3, "Q4_K", 2560, 3, 1), (3, "Q6_K", 2560, 3, 4), (3, "Q4_K", 10240, 1, 1),
+             (2, "Q4_K", 2560, 16, 1), (2, "Q6_K", 2560, 16, 5)]
+
+
+@pytest.mark.parametrize("selector,type_name,k,unit_rows,m", CAP_CASES, indirect=["selector"],
+                         ids=[f"sel{c[0]}-{c[1]}-k{c[2]}-m{c[4]}" for c in CAP_CASES])
+def test_rows_past_grid_cap(hip, oracle, selector, type_name, k, unit_rows, m):
+    """A few grid units more than 8 workgroups x 4 waves per CU, the last one
+    ragged: every wave walks two units, some the ragged one."""
+    cus = _cus(hip)
+    units = 32 * cus + 3
+    rows = units * unit_rows - (unit_rows // 2 if unit_rows > 1 else 0)
+    print(f"grid cap selector={selector} {type_name} k={k} rows={rows} m={m}", flush=True)
+    seed = S.derive(S.BASE_SEED, "gridcap", selector, type_name, k, m)
+    w = S.weight_blocks(type_name, seed, rows, k)
+    x = S.activations(S.derive(seed, "x"), m, k)
+    h = hip.createHipQuantizedWeightHandle(type_name, w, k, rows)
+    try:
+        got = hip.matMulQuantizedHipResident(h, x, k, rows, m)
+    finally:
+        hip.releaseHipQuantizedWeightHandle(h)
+    ref = oracle.matmul(TYPES[type_name], w, x, rows, threads=8)
+    assert np.array_equal(_bits(got), _bits(ref)), _first_diff(got, ref)
+
+
+@pytest.fixture(scope="module")
+def ffn_weights():
+    seed = S.derive(S.config_seed(3), "ffn-full")
+    return (S.q4_k_blocks(S.derive(seed, "gate"), FFN, HIDDEN), S.q4_k_blocks(S.derive(seed, "up"), FFN, HIDDEN),
+            S.q6_k_blocks(S.derive(seed, "down"), HIDDEN, FFN))
+
+
+@pytest.mark.parametrize("m", [1, 2, 4, 8])
+def test_ffn_full_size(hip, oracle, ffn_weights, m):
+    """Config 3: gate/up + GeGLU then down at the model's shapes."""
+    import torch
+
+    wg, wu, wd = ffn_weights
+    x = S.activations(S.derive(S.config_seed(3), "x-full", m), m, HIDDEN)
+    print(f"ffn full size m={m}", flush=True)
+    hg = hip.createHipQuantizedWeightHandle("Q4_K", wg, HIDDEN, FFN)
+    hu = hip.createHipQuantizedWeightHandle("Q4_K", wu, HIDDEN, FFN)
+    hd = hip.createHipQuantizedWeightHandle("Q6_K", wd, FFN, HIDDEN)
+    try:
+        h_host = hip.matMulGegluHipResident(hg, hu, x, HIDDEN, m)
+        y_host = hip.matMulQuantizedHipResident(hd, h_host, FFN, HIDDEN, m)
+        dx = _dev(x.reshape(-1))
+        dh = torch.empty(m * FFN, dtype=torch.float32, device="cuda:0")
+        dy = torch.empty(m * HIDDEN, dtype=torch.float32, device="cuda:0")
+        hip.matmul_geglu_device(hg.handle, hu.handle, dx.data_ptr(), HIDDEN, m, dh.data_ptr(), FFN)
+        hip.matmul_multi_device([hd.handle], dh.data_ptr(), FFN, m, [dy.data_ptr()], [m * HIDDEN])
+        torch.cuda.synchronize()
+        h_dev, y_dev = dh.cpu().numpy(), dy.cpu().numpy()
+    finally:
+        for h in (hg, hu, hd):
+            hip.releaseHipQuantizedWeightHandle(h)
+    gate = oracle.matmul(1, wg, x, FFN, threads=8)
+    up = oracle.matmul(1, wu, x, FFN, threads=8)
+    h_ref = oracle.geglu(gate.reshape(-1), up.reshape(-1)).reshape(m, FFN)
+    y_ref = oracle.matmul(3, wd, h_ref, HIDDEN, threads=8)
+    assert np.array_equal(_bits(h_host), _bits(h_ref)), _first_diff(h_host, h_ref)
+    assert np.array_equal(_bits(y_host), _bits(y_ref)), _first_diff(y_host, y_ref)
+    assert np.array_equal(_bits(h_dev), _bits(h_ref)), _first_diff(h_dev, h_ref)
+    assert np.array_equal(_bits(y_dev), _bits(y_ref)), _first_diff(y_dev, y_ref)
+
+
+def _oracle_layer(D, shape, data):
+    w = {n: (TYPES[t], blocks, rows) for n, (t, blocks, rows, _) in data["weights"].items()}
+    return D.Layer(weights=w, norms=dict(data["norms"]), key_cache=data["key_cache"].copy(),
+                   value_cache=data["value_cache"].copy(), head_count=shape.head_count,
+                   head_count_kv=shape.head_count_kv, rope_dims=shape.rope_dims,
+                   rope_freq_base=shape.rope_freq_base, sliding_window=shape.sliding_window,
+                   epsilon=shape.epsilon, output_scale=float(data["output_scale"]))
+
+
+N_LAYERS = 42
+DISTINCT = 3  # layer i uses the weights of synthetic layer i % 3; every layer has its own cache
+
+
+@pytest.mark.parametrize("tokens", [1, 4], ids=["decode", "draft4"])
+def test_decode_step_42_layers_with_head(hip, oracle, head_blocks, tokens):
+    """Config 5a: every layer, the output norm, the head and the top-40 of each
+    token, against the oracle's 42 layers and head."""
+    import torch
+
+    from oracle import decode_layer as D
+
+    shape = DM.ModelShape()
+    seed = S.derive(S.config_seed(5), "step-full")
+    datas = [DM.layer_host_data(shape, seed, i) for i in range(DISTINCT)]
+    onorm = (1.0 + 0.1 * S.normal(S.derive(seed, "output_norm"), shape.hidden)).astype(np.float32)
+    pos = shape.capacity + 1 - tokens          # the last token at position 4096
+    x = S.activations(S.derive(seed, "x", tokens), tokens, shape.hidden) * 4
+    model = DM.HipDecodeModel(shape)
+    shared = [None] * DISTINCT
+    head = hip.createHipQuantizedWeightHandle("Q6_K", head_blocks, HIDDEN, HEAD_ROWS)
+    print(f"decode step 42 layers tokens={tokens}", flush=True)
+    try:
+        for i in range(N_LAYERS):
+            j = i % DISTINCT
+            model.add_layer(datas[j], shared_weights=shared[j])
+            if shared[j] is None:
+                shared[j] = {n: h for n, h in zip(DM.PROJ_NAMES, model.handles[-len(DM.PROJ_NAMES):])}
+        model.set_head(onorm, head)
+        dx = _dev(x.reshape(-1))
+        dpos = _dev(np.array([pos], np.int32))
+        normed = torch.empty(tokens * shape.hidden, dtype=torch.float32, device="cuda:0")
+        logits = torch.empty(tokens * HEAD_ROWS, dtype=torch.float32, device="cuda:0")
+        model.run_layers(dx.data_ptr(), dpos.data_ptr(), normed.data_ptr(), tokens=tokens)
+        hip.matmul_multi_device([head.handle], normed.data_ptr(), shape.hidden, tokens, [logits.data_ptr()],
+                                [tokens * HEAD_ROWS])
+        torch.cuda.synchronize()
+        got_hidden = dx.cpu().numpy().reshape(tokens, shape.hidden)
+        got_normed = normed.cpu().numpy().reshape(tokens, shape.hidden)
+        got_logits = logits.cpu().numpy().reshape(tokens, HEAD_ROWS)
+        got_top = hip.topKHip(got_logits, 40)
+    finally:
+        model.release()
+        hip.releaseHipQuantizedWeightHandle(head)
+    layers = [_oracle_layer(D, shape, datas[i % DISTINCT]) for i in range(N_LAYERS)]
+    h = x.copy()
+    for L in layers:
+        h = D.forward_layer(L, h, pos)
+    ref_normed = D.rms_norm_rows(h, onorm, shape.epsilon)
+    ref_logits = oracle.matmul(3, head_blocks, ref_normed, HEAD_ROWS, threads=8)
+    ident = float(np.mean(got_hidden == h))
+    print(f"42 layers: hidden max rel err {_rel(got_hidden, h):.3e}, identical {ident:.5f}; normed "
+          f"{_rel(got_normed, ref_normed):.3e}", flush=True)
+    assert _rel(got_hidden, h) <= LAYER_TOL
+    assert _rel(got_normed, ref_normed) <= LAYER_TOL
+    if np.array_equal(_bits(got_normed), _bits(ref_normed)):
+        assert np.array_equal(_bits(got_logits), _bits(ref_logits)), _first_diff(got_logits, ref_logits)
+    for t in range(tokens):
+        ids, vals = oracle.topk(ref_logits[t], 40)
+        g_ids = np.array([c["id"] for c in got_top[t]], dtype=np.uint32)
+        assert np.array_equal(g_ids, ids), (t, g_ids[:6], ids[:6])
+
+
+@pytest.mark.parametrize("tokens", [2, 3, 4, 5, 6, 7, 8])
+def test_draft_input_images_bit_identical(hip, tokens):
+    """The pre-quantised inputs of a draft step (the Q/K/V input written by the
+    norm launch, the down input written by the GeGLU launch) against every
+    projection quantising its own f32 input: the same layer at full size run
+    both ways gives identical residual streams and caches."""
+    import torch
+
+    shape = DM.ModelShape()
+    data = DM.layer_host_data(shape, S.derive(S.BASE_SEED, "images", tokens), 0)
+    x = S.activations(S.derive(S.BASE_SEED, "images-x", tokens), tokens, shape.hidden) * 4
+    results = []
+    print(f"draft images tokens={tokens}", flush=True)
+    for images in (True, False):
+        model = DM.HipDecodeModel(shape)
+        model.add_layer(data)
+        dx = _dev(x.reshape(-1))
+        dpos = _dev(np.array([shape.capacity - tokens], np.int32))
+        try:
+            hip.setInputImages(images)
+            model.run_layers(dx.data_ptr(), dpos.data_ptr(), tokens=tokens)
+            torch.cuda.synchronize()
+            results.append((dx.cpu().numpy(), model.caches[0][0].cpu().numpy(), model.caches[0][1].cpu().numpy()))
+        finally:
+            hip.setInputImages(True)
+            model.release()
+    (h1, k1, v1), (h2, k2, v2) = results
+    assert np.array_equal(_bits(h1), _bits(h2)), _first_diff(h1, h2)
+    assert np.array_equal(k1, k2) and np.array_equal(v1, v2)

@@ -3,8 +3,10 @@
 Two kernels:
 - the bit-exact prefill kernel (selector 4; automatic for 32..63 columns):
   bit-identical to the oracle's restatement of lib.rs:224-426;
-- the fast prefill kernel (selector 5; automatic from 64 columns, the M >= 64
-  prefill chunk): it adds each block's eight lane-class sums before scaling,
+- the fast prefill kernel (selector 5; automatic from 64 columns on the
+  *_device entry points, the M >= 64 prefill chunk; the host-pointer matmul
+  entry points stay bit-exact): it adds each block's eight lane-class sums
+  before scaling,
   so it is held to the stated tolerance for projections instead: max
   relative error <= 1e-4 against the oracle, relative to max(|ref|,
   0.01 * rms(ref)) so that outputs that cancel to near zero are compared
@@ -40,6 +42,24 @@ def _rel_err(got, ref):
     den = np.maximum(np.abs(ref), FLOOR * rms)
     den[den == 0] = 1.0
     return float(np.max(np.abs(got - ref) / den)) if ref.size else 0.0
+
+
+def _dev(a):
+    import torch
+
+    return torch.from_numpy(np.ascontiguousarray(a)).to(torch.device("cuda:0"))
+
+
+def _device_matmul(hip, handles, x, k, m):
+    """hp_hip_matmul_multi_device on device copies of x; host outputs."""
+    import torch
+
+    dx = _dev(np.asarray(x, np.float32).reshape(-1))
+    outs = [torch.empty(h.rowCount * m, dtype=torch.float32, device="cuda:0") for h in handles]
+    hip.matmul_multi_device([h.handle for h in handles], dx.data_ptr(), k, m, [o.data_ptr() for o in outs],
+                            [o.numel() for o in outs])
+    torch.cuda.synchronize()
+    return [o.cpu().numpy() for o in outs]
 
 
 @pytest.fixture
@@ -82,13 +102,20 @@ def test_prefill_fast_within_tolerance(hip, oracle, selector, type_name, rows, k
     h = hip.createHipQuantizedWeightHandle(type_name, w, k, rows)
     try:
         got = hip.matMulQuantizedHipResident(h, x, k, rows, m)
+        got_dev = _device_matmul(hip, [h], x, k, m)[0]
     finally:
         hip.releaseHipQuantizedWeightHandle(h)
     ref = oracle.matmul(TYPES[type_name], w, x, rows, threads=8)
-    err = _rel_err(got, ref)
+    err = _rel_err(got_dev, ref)
     assert err <= TOL, err
-    if selector == 0 and m < 64:          # the automatic policy stays bit-exact below 64 columns
+    if selector == 0:
+        # the host-pointer entry point stays bit-exact under the automatic
+        # policy; the device entry point does below 64 columns
         assert np.array_equal(_bits(got), _bits(ref))
+        if m < 64:
+            assert np.array_equal(_bits(got_dev), _bits(ref))
+    else:
+        assert _rel_err(got, ref) <= TOL
 
 
 @pytest.mark.parametrize("selector", [4, 0], ids=["exact", "auto"], indirect=True)
@@ -108,11 +135,14 @@ def test_prefill_multi_and_large_chunk(hip, oracle, selector):
     hs = [hip.createHipQuantizedWeightHandle(t, w, k, r) for (t, r), w in zip(specs, ws)]
     print(f"prefill qkv m=512 selector={selector}", flush=True)
     try:
-        outs = hip.matMulQuantizedHipResidentMulti(hs, x, k, m)
+        host_outs = hip.matMulQuantizedHipResidentMulti(hs, x, k, m)
+        outs = _device_matmul(hip, hs, x, k, m)
     finally:
         for h in hs:
             hip.releaseHipQuantizedWeightHandle(h)
     refs = oracle.matmul_multi([TYPES[t] for t, _ in specs], ws, x, [r for _, r in specs], threads=8)
+    for got, ref in zip(host_outs, refs):                      # host entry point: bit-exact
+        assert np.array_equal(_bits(got), _bits(ref))
     for (t, r), got, ref in zip(specs, outs, refs):
         if selector == 4:
             assert np.array_equal(_bits(got), _bits(ref))
@@ -137,15 +167,23 @@ def test_prefill_geglu(hip, oracle, selector, rows, m):
     wg = S.q4_k_blocks(S.derive(seed, "g"), rows, k)
     wu = S.q4_k_blocks(S.derive(seed, "u"), rows, k)
     x = S.activations(seed, m, k)
+    import torch
+
     hg = hip.createHipQuantizedWeightHandle("Q4_K", wg, k, rows)
     hu = hip.createHipQuantizedWeightHandle("Q4_K", wu, k, rows)
     try:
-        got = hip.matMulGegluHipResident(hg, hu, x, k, m)
+        host = hip.matMulGegluHipResident(hg, hu, x, k, m)
+        dx = _dev(x.reshape(-1))
+        dout = torch.empty(rows * m, dtype=torch.float32, device="cuda:0")
+        hip.matmul_geglu_device(hg.handle, hu.handle, dx.data_ptr(), k, m, dout.data_ptr(), rows)
+        torch.cuda.synchronize()
+        got = dout.cpu().numpy()
     finally:
         hip.releaseHipQuantizedWeightHandle(hg)
         hip.releaseHipQuantizedWeightHandle(hu)
     ref = oracle.geglu(oracle.matmul(1, wg, x, rows, threads=8).reshape(-1),
                        oracle.matmul(1, wu, x, rows, threads=8).reshape(-1))
+    assert np.array_equal(_bits(host), _bits(ref))             # host entry point: bit-exact
     if selector == 4:
         assert np.array_equal(_bits(got), _bits(ref))
     else:
