@@ -19,6 +19,14 @@
 #include <thread>
 #include <vector>
 
+// Selection state of hp_hip_topk_device_noalloc: one batch of kTopkMaxRows
+// rows at the largest top-k shape (n = 524288, k = 64) needs 8,454,400
+// bytes.  Every device the library runs on holds its own copy for the life
+// of the process; host code reaches it only through the address that
+// hipGetSymbolAddress returns on that device (State::static_scratch).
+constexpr size_t kNoAllocScratchBytes = (8u << 20) + (512u << 10);
+static __device__ __align__(256) uint8_t scratch[kNoAllocScratchBytes];
+
 namespace {
 
 using namespace hp;
@@ -89,6 +97,9 @@ struct State {
   size_t sample_out_cap = 0;
   // intermediate device memory of the asynchronous entry points, per stream
   ScratchPool<HipAlloc> pool;
+  // device address of the file-scope `scratch` array on `device`, looked up
+  // by ensure_init (the allocation-free entry point's only scratch)
+  uint8_t *static_scratch = nullptr;
 };
 
 State &st() {
@@ -138,6 +149,12 @@ int32_t ensure_init(int device) {
   HP_HIP_TRY(hipDeviceGetAttribute(&lds, hipDeviceAttributeMaxSharedMemoryPerBlock, device));
   s.max_lds = (size_t)lds;
   HP_HIP_TRY(hipStreamCreateWithFlags(&s.stream, hipStreamNonBlocking));
+  // this device's copy of the static scratch: the array's name is a host
+  // stand-in, only this address reaches its device memory
+  void *sym = nullptr;
+  HP_HIP_TRY(hipGetSymbolAddress(&sym, HIP_SYMBOL(scratch)));
+  if (!sym) return fail(HP_ERR_HIP, "hipGetSymbolAddress(scratch) returned null");
+  s.static_scratch = static_cast<uint8_t *>(sym);
   s.device = device;
   s.ready = true;
   return HP_OK;
@@ -173,7 +190,7 @@ int32_t grow(void **p, size_t *cap, size_t bytes) {
 
 // Scratch of `kind` for work queued on `stream` (hp_scratch.h): per stream,
 // grow-only, and never grown while the stream captures a graph.
-int32_t scratch(hipStream_t stream, int kind, size_t bytes, void **out, bool zero = false) {
+int32_t stream_scratch(hipStream_t stream, int kind, size_t bytes, void **out, bool zero = false) {
   State &s = st();
   void *key = stream ? static_cast<void *>(stream) : static_cast<void *>(s.stream);
   hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
@@ -386,7 +403,7 @@ int32_t run_matvec(size_t count, Handle *const *hs, const float *d_input, size_t
     }
     const size_t need = kind == 2 ? prefill_fast_bytes(l, s.num_cus) : prefill_q8k_bytes((int)input_size, (int)cols);
     void *pre = nullptr;
-    int32_t rc = scratch(stream, kScratchPrefill, need, &pre);
+    int32_t rc = stream_scratch(stream, kScratchPrefill, need, &pre);
     if (rc != HP_OK) return rc;
     uint8_t *q8 = static_cast<uint8_t *>(pre);
     hipEvent_t e1 = prof_begin(stream);
@@ -506,7 +523,7 @@ int32_t run_matvec_geglu(Handle *hg, Handle *hu, const float *d_input, size_t in
   if (prefill_kind(cols) == 2 && hg->type == hu->type) {
     // fast prefill: gate and up rows in one tile, GeGLU in its epilogue
     void *pre = nullptr;
-    int32_t rc = scratch(stream, kScratchPrefill, prefill_fast_geglu_bytes((int)input_size, (int)cols), &pre);
+    int32_t rc = stream_scratch(stream, kScratchPrefill, prefill_fast_geglu_bytes((int)input_size, (int)cols), &pre);
     if (rc != HP_OK) return rc;
     MfmaLaunch l{};
     l.count = 2;
@@ -527,7 +544,7 @@ int32_t run_matvec_geglu(Handle *hg, Handle *hu, const float *d_input, size_t in
     return HP_OK;
   }
   void *sums = nullptr;
-  int32_t rc = scratch(stream, kScratchGeglu, 2 * cols * rows * sizeof(float), &sums);
+  int32_t rc = stream_scratch(stream, kScratchGeglu, 2 * cols * rows * sizeof(float), &sums);
   if (rc != HP_OK) return rc;
   Handle *hs[2] = {hg, hu};
   float *outs[2] = {static_cast<float *>(sums), static_cast<float *>(sums) + cols * rows};
@@ -911,7 +928,7 @@ int32_t run_topk(const float *d_logits, size_t rows, size_t n, size_t k, double 
   const size_t batch = rows < (size_t)kTopkMaxRows ? rows : (size_t)kTopkMaxRows;
   const size_t bytes = topk_scratch_bytes((int)batch, (int)n, (int)k);
   void *sel = nullptr;
-  int32_t rc = scratch(stream, kScratchTopk, bytes, &sel, true);
+  int32_t rc = stream_scratch(stream, kScratchTopk, bytes, &sel, true);
   if (rc != HP_OK) return rc;
   hipEvent_t e = prof_begin(stream);
   for (size_t r0 = 0; r0 < rows; r0 += batch) {
@@ -1005,6 +1022,7 @@ int32_t hp_hip_shutdown(void) {
   release_loader(s);
   (void)hipStreamDestroy(s.stream);
   s.stream = nullptr;
+  s.static_scratch = nullptr;
   s.ready = false;
   return HP_OK;
 }
@@ -1238,6 +1256,33 @@ int32_t hp_hip_topk_device(const float *d_logits, size_t rows, size_t n, size_t 
   if (!d_logits || !d_ids || !d_values) return fail(HP_ERR_ARG, "null pointer");
   hipStream_t strm = stream ? static_cast<hipStream_t>(stream) : s.stream;
   return run_topk(d_logits, rows, n, k, softcap, d_ids, d_values, strm);
+}
+
+int32_t hp_hip_topk_device_noalloc(const float *d_logits, size_t rows, size_t n, size_t k, double softcap,
+                                   uint32_t *d_ids, float *d_values, void *stream) {
+  State &s = st();
+  std::lock_guard<std::recursive_mutex> lock(s.mu);
+  if (!s.ready || !s.static_scratch)
+    return fail(HP_ERR_ARG, "hp_hip_init must run before hp_hip_topk_device_noalloc");
+  int32_t rc = topk_check(rows, n, k);
+  if (rc != HP_OK) return rc;
+  if (rows == 0) return HP_OK;
+  if (!d_logits || !d_ids || !d_values) return fail(HP_ERR_ARG, "null pointer");
+  const size_t batch = rows < (size_t)kTopkMaxRows ? rows : (size_t)kTopkMaxRows;
+  if (topk_scratch_bytes((int)batch, (int)n, (int)k) > kNoAllocScratchBytes)
+    return fail(HP_ERR_SHAPE, "top-k selection state exceeds the static scratch of " +
+                                  std::to_string(kNoAllocScratchBytes) + " bytes");
+  hipStream_t strm = stream ? static_cast<hipStream_t>(stream) : s.stream;
+  // the array keeps the last call's contents: its counters start at zero here
+  HP_HIP_TRY(launch_topk_clear(s.static_scratch, strm));
+  s.launches++;
+  for (size_t r0 = 0; r0 < rows; r0 += batch) {
+    const size_t nr = rows - r0 < batch ? rows - r0 : batch;
+    HP_HIP_TRY(launch_topk(d_logits + r0 * n, (int)nr, (int)n, (int)k, softcap, s.static_scratch, d_ids + r0 * k,
+                           d_values + r0 * k, strm));
+    s.launches += 3;
+  }
+  return HP_OK;
 }
 
 int32_t hp_hip_topk(const float *logits, size_t rows, size_t n, size_t k, double softcap, uint32_t *ids,
@@ -1620,7 +1665,7 @@ int32_t hp_hip_gqa_attention_device(const hp_hip_attention_config_t *config, siz
   if (!d_q || !d_key_cache || !d_value_cache || !d_position || !d_output) return fail(HP_ERR_ARG, "null pointer");
   hipStream_t strm = stream ? static_cast<hipStream_t>(stream) : s.stream;
   void *partials = nullptr;
-  rc = scratch(strm, kScratchAttn,
+  rc = stream_scratch(strm, kScratchAttn,
                attn_partial_floats(config->head_count_kv, config->capacity, (int)token_count) * sizeof(float),
                &partials);
   if (rc != HP_OK) return rc;
@@ -1673,7 +1718,7 @@ int32_t hp_hip_decode_layers_device(const hp_hip_decode_layer_t *layers, size_t 
   for (size_t z : sizes) total += z;
   hipStream_t strm = stream ? static_cast<hipStream_t>(stream) : s.stream;
   void *dscr = nullptr;
-  rc = scratch(strm, kScratchDecode, total * sizeof(float), &dscr);
+  rc = stream_scratch(strm, kScratchDecode, total * sizeof(float), &dscr);
   if (rc != HP_OK) return rc;
   float *buf[14];
   float *p = static_cast<float *>(dscr);

@@ -134,6 +134,8 @@ constexpr int kTopkMaxRows = 16;
 hipError_t launch_topk(const float *logits, int rows, int n, int k, double cap, uint8_t *scratch, uint32_t *ids,
                        float *vals, hipStream_t s);
 size_t topk_scratch_bytes(int rows, int n, int k);
+// Zeroes the counters a top-k scratch buffer must start with (one small kernel).
+hipError_t launch_topk_clear(uint8_t *scratch, hipStream_t s);
 
 // Next-token sampling over [cols][k] sorted candidates (count valid per
 // column): one wave; rng points to the 32-bit generator state, advanced once

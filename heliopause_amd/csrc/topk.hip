@@ -325,6 +325,17 @@ __global__ __launch_bounds__(kTopkThreads) void topk_final_kernel(const float *_
 
 size_t topk_scratch_bytes(int rows, int n, int k) { return kTopkHeader + (size_t)rows * topk_row_stride(n, k); }
 
+// Zeroes the per-row candidate counters at the head of a scratch buffer (a
+// kernel rather than a memset, so a captured graph replays it faithfully).
+__global__ __launch_bounds__(64) void topk_clear_kernel(uint32_t *header) {
+  for (int i = threadIdx.x; i < (int)(kTopkHeader / 4); i += 64) header[i] = 0u;
+}
+
+hipError_t launch_topk_clear(uint8_t *scratch, hipStream_t s) {
+  hipLaunchKernelGGL(topk_clear_kernel, dim3(1), dim3(64), 0, s, reinterpret_cast<uint32_t *>(scratch));
+  return hipGetLastError();
+}
+
 hipError_t launch_topk(const float *logits, int rows, int n, int k, double cap, uint8_t *scratch, uint32_t *ids,
                        float *vals, hipStream_t s) {
   if (n < 1 || n > kTopkMaxN || k < 1 || k > kTopkMaxK || rows < 1 || rows > kTopkMaxRows)

@@ -167,10 +167,11 @@ def _declare_optional(L: ctypes.CDLL) -> None:
     L.hp_hip_matmul_topk.argtypes = [_u64, vp, _sz, _sz, _sz, _sz, ctypes.c_double, vp, vp, _sz]
     L.hp_hip_topk.argtypes = [vp, _sz, _sz, _sz, ctypes.c_double, vp, vp, _sz]
     L.hp_hip_topk_device.argtypes = [vp, _sz, _sz, _sz, ctypes.c_double, vp, vp, vp]
+    L.hp_hip_topk_device_noalloc.argtypes = [vp, _sz, _sz, _sz, ctypes.c_double, vp, vp, vp]
     L.hp_hip_geglu.argtypes = [vp, vp, _sz, vp]
     L.hp_hip_geglu_device.argtypes = [vp, vp, _sz, vp, vp]
-    for name in ("hp_hip_matmul_topk", "hp_hip_topk", "hp_hip_topk_device", "hp_hip_geglu",
-                 "hp_hip_geglu_device"):
+    for name in ("hp_hip_matmul_topk", "hp_hip_topk", "hp_hip_topk_device", "hp_hip_topk_device_noalloc",
+                 "hp_hip_geglu", "hp_hip_geglu_device"):
         getattr(L, name).restype = i32
     _declare_decode(L)
 

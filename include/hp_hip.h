@@ -163,6 +163,21 @@ int32_t hp_hip_topk(const float *logits, size_t rows, size_t n, size_t k, double
 /* Device-pointer topK; asynchronous on stream (NULL = library stream). */
 int32_t hp_hip_topk_device(const float *d_logits, size_t rows, size_t n, size_t k, double softcap,
                            uint32_t *d_ids, float *d_values, void *stream);
+/* hp_hip_topk_device without any device allocation.  No counterpart in the
+ * reference: it is for callers that cannot allocate (code under HIP graph
+ * capture on a stream no earlier call has sized, tight serving loops,
+ * harnesses that forbid hipMalloc).  Same arguments and results.  Its
+ * selection state lives in a static device array of 8.5 MiB per GPU, held
+ * until the process ends, which fits one batch of 16 rows at every shape
+ * hp_hip_topk_device takes (n <= 524288, k <= 64; larger row counts run in
+ * batches of 16); a shape whose state would not fit fails with HP_ERR_SHAPE.
+ * The library must be initialised first (hp_hip_init, or any earlier call):
+ * HP_ERR_ARG otherwise.  Every call on one GPU shares that array, so calls
+ * that overlap on one GPU (two streams at once) race; calls queued on one
+ * stream are ordered.  Each call starts by clearing the array's counters
+ * with a kernel (no memset), so a captured call replays correctly. */
+int32_t hp_hip_topk_device_noalloc(const float *d_logits, size_t rows, size_t n, size_t k, double softcap,
+                                   uint32_t *d_ids, float *d_values, void *stream);
 
 /* Next-token sampling options, resolved as resolveGenerationSamplingOptions
  * does (generation.ts:40-76): greedy when do_sample == 0 or temperature ==
