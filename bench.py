@@ -18,11 +18,15 @@ handles).
 Weights are GGUF super-blocks generated from a fixed seed and uploaded once;
 steps rotate over enough distinct weight copies (>= 640 MiB) that every step
 streams its weights from HBM rather than from the 256 MB Infinity Cache.
-Inputs and outputs stay in HBM.  The timed steps are captured once in a HIP
-graph and replayed back to back.
+Inputs and outputs stay in HBM.  Exactly ``--steps`` steps are timed: they
+are captured in one HIP graph (step i on copy i % copies) and replayed once,
+after a warm-up graph of the ``--warmup`` steps that also streams every other
+copy.
 
 Prints one JSON line.  ``value`` = algorithmic bytes per step (weights as
 stored + f32 activations read and written) / wall time per step, in GB/s.
+The default line also carries ``decode_step``: the 42-layer model's decode
+step at M = 1 (``--workload decode42``), measured in the same run.
 """
 from __future__ import annotations
 
@@ -118,13 +122,15 @@ def matvec_kernel_name(choice: str, k: int, m: int, specs: list) -> str:
 def parse() -> argparse.Namespace:
     p = argparse.ArgumentParser()
     p.add_argument("--gpus", type=int, default=1)
-    p.add_argument("--steps", type=int, default=400)
-    p.add_argument("--warmup", type=int, default=40)
+    p.add_argument("--steps", type=int, default=200)
+    p.add_argument("--warmup", type=int, default=20)
     p.add_argument("--m", type=int, default=1)
     p.add_argument("--workload", choices=sorted(WORKLOADS) + ["decode42", "decode42-proj", "prefill42", "gguf-load"], default="qkv")
     p.add_argument("--rotate-mib", type=int, default=640, help="distinct weight bytes cycled through")
     p.add_argument("--cpu-seconds", type=float, default=12.0)
     p.add_argument("--no-cpu", action="store_true")
+    p.add_argument("--no-decode", action="store_true",
+                   help="leave the decode-step object out of the default line")
     p.add_argument("--kernel", choices=["auto", "valu", "mfma", "half"], default="auto",
                    help="matvec kernel: automatic choice, vector ALU, matrix cores, half-split vector ALU")
     p.add_argument("--copy-probe", action="store_true",
@@ -147,34 +153,90 @@ def copy_probe() -> int:
     return 0
 
 
+def host_cpu_model() -> str:
+    """The host CPU's model name (/proc/cpuinfo), else what platform reports."""
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return platform.processor() or platform.machine()
+
+
+def host_threads() -> int:
+    """CPUs this process may run on (its affinity set), at most 16: the host
+    share of one GPU on the benchmark machines."""
+    try:
+        n = len(os.sched_getaffinity(0))
+    except (AttributeError, OSError):
+        n = os.cpu_count() or 1
+    return max(1, min(16, n))
+
+
+def time_calls(fn, min_seconds: float) -> tuple[float, int]:
+    """prefill-kernels.bench.ts:90-121's loop: 8 warm-ups, then the iteration
+    count doubles until one run lasts >= min_seconds; returns (seconds per
+    call, calls in that run)."""
+    for _ in range(8):
+        fn()
+    n = 1
+    while True:
+        t0 = time.perf_counter()
+        for _ in range(n):
+            fn()
+        el = time.perf_counter() - t0
+        if el >= min_seconds:
+            return el / n, n
+        n *= 2
+
+
 def cpu_baseline(workload: str, ws, x, seconds: float) -> dict:
-    """The oracle's threaded restatement of the reference's resident WASM path on
-    the same launch (bounded sample); threads = the reference's default pool."""
+    """The oracle's threaded restatement of the reference's resident WASM path
+    (hp_matmul_quantized_prepared_multi_f32 with splitRows sharding) on the
+    same launch, bounded to about ``seconds`` of host time over four legs:
+    the 128-bit SSE4.1 build (the width of wasm simd128) and a build for this
+    host's own ISA (-march=native), each at the reference's default pool size
+    and at every CPU the process may use.  ``value`` is the SSE4.1 leg at the
+    default pool size, the reference's configuration."""
+    import tempfile
+
     from oracle import oracle as O
 
     _, k, specs, _ = WORKLOADS[workload]
-    threads = O.default_threads()
     tids = [TYPE_IDS[t] for t, _ in specs]
     rows = [r for _, r in specs]
-    O.matmul_multi(tids, ws, x, rows, threads=threads)  # warm
-    n, t0 = 0, time.perf_counter()
-    while True:
-        O.matmul_multi(tids, ws, x, rows, threads=threads)
-        n += 1
-        el = time.perf_counter() - t0
-        if el >= seconds:
-            break
     m = x.shape[0]
     launch_bytes = sum(row_bytes(t, k) * r for t, r in specs) + m * k * 4 + m * sum(rows) * 4
+    t_default = O.default_threads()
+    t_all = host_threads()
+    libs = [("sse4.1 (wasm simd128 width)", None)]
+    note = ""
+    try:
+        libs.append(("-march=native", O.native_lib(tempfile.mkdtemp(prefix="hp_oracle_"))))
+    except (OSError, Exception) as exc:  # no compiler on the host: the leg is reported missing
+        note = f"; native leg not built ({type(exc).__name__})"
+    legs = []
+    per_leg = max(0.75, seconds / (2 * len(libs)))
+    for isa, library in libs:
+        for threads in sorted({t_default, t_all}):
+            sec, n = time_calls(lambda: O.matmul_multi(tids, ws, x, rows, threads=threads, library=library), per_leg)
+            legs.append({"isa": isa, "threads": threads, "ms_per_call": round(sec * 1e3, 4),
+                         "GB/s": round(launch_bytes / sec / 1e9, 3), "calls": n})
+    ref_leg = legs[0]
     return {
-        "value": round(launch_bytes * n / el / 1e9, 3),
+        "value": ref_leg["GB/s"],
         "unit": "GB/s",
-        "cores": threads,
+        "cores": t_default,
         "kind": "port",
-        "sample": f"{n} calls of the {workload} projection launch at M={m} in {el:.1f} s "
-                  f"({el / n * 1e3:.3f} ms/call); C restatement of lib.rs resident kernels, "
-                  f"splitRows sharding over {threads} threads; host {platform.processor() or platform.machine()}, "
-                  f"{os.cpu_count()} logical CPUs",
+        "sample": f"the {workload} projection launch at M={m} ({launch_bytes} algorithmic bytes); C restatement of "
+                  f"lib.rs resident kernels with splitRows sharding, timed as prefill-kernels.bench.ts does (8 "
+                  f"warm-ups, doubling to >= {per_leg:.2f} s per leg); value: SSE4.1 build on the reference's "
+                  f"default pool of {t_default} threads; excludes the reference's JS/worker overhead{note}",
+        "cpu_model": host_cpu_model(),
+        "logical_cpus": os.cpu_count(),
+        "usable_cpus": t_all,
+        "legs": legs,
     }
 
 
@@ -275,20 +337,22 @@ def decode_chain(args) -> int:
     return 0
 
 
-def decode_step(args) -> int:
-    """One decode step of the 42-layer synthetic Gemma-like model at M = 1
+def measure_decode_step(m: int, steps: int, warmup: int, cpu_seconds: float | None) -> dict:
+    """One decode step of the 42-layer synthetic Gemma-like model at M = m
     (hidden 2560, 8 query / 2 KV heads of 256, FFN 10240; Q4_K_M mix) with a
-    4096-token f16 KV cache filled with N(0,1): the token at position 4096
-    attends over the last 4096 positions of every layer.  Per layer: attn_norm
-    -> Q/K/V -> q/k norms + RoPE + v norm + cache append -> GQA attention ->
-    O -> post-attention norm + residual + ffn_norm -> gate/up + GeGLU -> down
-    -> post-FFN norm + residual + layer scale + next attn_norm; then
-    output_norm, the Q6_K 262144x2560 head, top-40 and the sampled next token.
-    Every layer's weights and cache are distinct device copies (3.02 GB of
-    weights + 352 MB of cache).  The step starts by copying the input hidden
-    state into the residual buffer (standing in for the embedding row), so
-    every replay computes the same step.  One step is captured in a HIP graph
-    and replayed."""
+    4096-token f16 KV cache filled with N(0,1): the last token at position
+    4096 attends over the last 4096 positions of every layer.  Per layer:
+    attn_norm -> Q/K/V -> q/k norms + RoPE + v norm + cache append -> GQA
+    attention -> O -> post-attention norm + residual + ffn_norm -> gate/up +
+    GeGLU -> down -> post-FFN norm + residual + layer scale + next attn_norm;
+    then output_norm, the Q6_K 262144x2560 head, top-40 and (one token) the
+    sampled next token.  Every layer's weights and cache are distinct device
+    copies (3.02 GB of weights + 352 MB of cache).  The step starts by copying
+    the input hidden state into the residual buffer (standing in for the
+    embedding row), so every replay computes the same step.  One step is
+    captured in a HIP graph; `warmup` replays, then `steps` replays timed.
+    The per-kernel split comes from one eager step with HIP events around
+    every launch (hp_hip_profile)."""
     import numpy as np
     import torch
 
@@ -296,7 +360,6 @@ def decode_step(args) -> int:
     from heliopause_amd import hip_kernels as H
     from heliopause_amd import synthetic as S
 
-    m = args.m  # tokens per step: 1 (decode) or a draft of up to 8 being verified
     if not 1 <= m <= 8:
         raise SystemExit("decode42 runs 1..8 tokens per step")
     torch.cuda.init()
@@ -338,16 +401,27 @@ def decode_step(args) -> int:
     side = torch.cuda.Stream()
     side.wait_stream(torch.cuda.current_stream())
     with torch.cuda.stream(side):
+        launches0 = H.hipResidentWeightStats()["kernelLaunches"]
+        step(side.cuda_stream)
+        launches = H.hipResidentWeightStats()["kernelLaunches"] - launches0 + 1  # + the input copy
+        torch.cuda.synchronize()
+        # per-kernel split: one eager step with events around every launch
+        H.profile(True)
         step(side.cuda_stream)
         torch.cuda.synchronize()
+        split = {}
+        for kid, name in H.KERNEL_NAMES.items():
+            ms, n = H.profile_read(kid)
+            if n:
+                split[name] = {"us": round(ms * 1e3, 1), "launches": n}
+        H.profile(False)
         graph = torch.cuda.CUDAGraph()
         with torch.cuda.graph(graph, stream=side):
             step(torch.cuda.current_stream().cuda_stream)
     torch.cuda.synchronize()
-    for _ in range(max(1, args.warmup // 10)):
+    for _ in range(max(1, warmup)):
         graph.replay()
     torch.cuda.synchronize()
-    steps = max(1, args.steps // 10)
     start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     t0 = time.perf_counter()
     start.record()
@@ -359,36 +433,66 @@ def decode_step(args) -> int:
     ms = start.elapsed_time(end) / steps
     wbytes = N_LAYERS * sum(row_bytes(t, k) * r for t, r, k in LAYER) + row_bytes(HEAD[0], HEAD[2]) * HEAD[1]
     kv_bytes = N_LAYERS * 2 * shape.head_count_kv * shape.capacity * 256 * 2
-    total = wbytes + kv_bytes
-    cpu = None if (args.no_cpu or m != 1) else decode_cpu_baseline(shape, data, head_blocks, args.cpu_seconds)
-    # input copy, per layer (6 for one token; a draft adds the prologue launch and
-    # the norm launches), final norm, head, top-k (3), sample
-    launches = 1 + N_LAYERS * (6 if m == 1 else 9) + 1 + 1 + 3 + (1 if m == 1 else 0)
+    cpu = None if (cpu_seconds is None or m != 1) else decode_cpu_baseline(shape, data, head_blocks, cpu_seconds)
+    model.release()
+    H.releaseHipQuantizedWeightHandle(head)
+    return {"m": m, "ms": ms, "wall_ms": wall_ms, "steps": steps, "launches": launches, "split": split,
+            "weight_bytes": wbytes, "kv_bytes": kv_bytes, "cpu": cpu,
+            "positions": [int(shape.capacity) + 1 - m, int(shape.capacity)]}
+
+
+def decode_summary(r: dict) -> dict:
+    """The decode-step object of the JSON line (one token)."""
+    total = r["weight_bytes"] + r["kv_bytes"]
+    target = 1.3 * r["weight_bytes"] / HBM_PEAK_GBPS / 1e6
+    return {
+        "workload": "42-layer synthetic Gemma-like model, full decode step at M=1 with a 4096-token f16 KV cache "
+                    "(token at position 4096): norms, Q/K/V, RoPE, cache append, GQA attention, O, GeGLU FFN, "
+                    "residuals, output norm, Q6_K 262144x2560 head, top-40, next-token sampling; one HIP graph",
+        "ms_per_step": round(r["ms"], 4),
+        "wall_ms_per_step": round(r["wall_ms"], 4),
+        "steps": r["steps"],
+        "weight_bytes": r["weight_bytes"],
+        "kv_cache_bytes": r["kv_bytes"],
+        "GB/s": round(total / (r["ms"] * 1e-3) / 1e9, 1),
+        "frac_of_peak": round(total / (r["ms"] * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4),
+        "target_ms": round(target, 4),
+        "vs_target": round(r["ms"] / target, 3),
+        "launches_per_step": r["launches"],
+        "kernel_split_us": r["split"],
+        "kernel_split_note": "one eager step with HIP events around each launch (includes per-launch gaps)",
+    }
+
+
+def decode_step(args) -> int:
+    """``--workload decode42``: the decode step (or a draft of --m tokens) as
+    its own JSON line."""
+    m = args.m
+    r = measure_decode_step(m, max(1, args.steps // 10), max(1, args.warmup // 10),
+                            None if args.no_cpu else args.cpu_seconds)
+    ms = r["ms"]
+    total = r["weight_bytes"] + r["kv_bytes"]
     line = {
         "metric": "decode step ms at M=1 (1 GPU)" if m == 1 else f"draft verification step ms at M={m} (1 GPU)",
-        "value": round(ms, 4), "unit": "ms", "n_gpus": 1, "steps": steps, "warmup": args.warmup,
+        "value": round(ms, 4), "unit": "ms", "n_gpus": 1, "steps": r["steps"], "warmup": max(1, args.warmup // 10),
         "ms_per_step": round(ms, 4), "higher_is_better": False, "scaling": "weak", "vs_baseline": None,
         "dtype": "int8", "data": "synthetic",
-        "config": {"workload": "42-layer synthetic Gemma-like model, full decode step at M=1 with a 4096-token f16 "
-                               "KV cache: norms, Q/K/V, RoPE, cache append, GQA attention, O, GeGLU FFN, residuals, "
-                               "output norm, head, top-40, next-token sampling" if m == 1 else
+        "config": {"workload": decode_summary(r)["workload"] if m == 1 else
                                f"42-layer synthetic Gemma-like model, verification of a {m}-token draft (every "
                                "position through every layer with causal attention over a 4096-token f16 KV cache, "
                                "output norm, head, top-40 per position)",
-                   "weight_bytes": wbytes, "kv_cache_bytes_read": kv_bytes, "launches_per_step": launches,
-                   "wall_ms_per_step": round(wall_ms, 4), "tokens": m,
-                   "positions": [int(shape.capacity) + 1 - m, int(shape.capacity)],
+                   "weight_bytes": r["weight_bytes"], "kv_cache_bytes_read": r["kv_bytes"],
+                   "launches_per_step": r["launches"], "wall_ms_per_step": round(r["wall_ms"], 4), "tokens": m,
+                   "positions": r["positions"], "kernel_split_us": r["split"],
                    "timing": "one step captured in a HIP graph and replayed"},
         "roofline": {"bound": "hbm", "achieved": round(total / (ms * 1e-3) / 1e9, 2), "peak": HBM_PEAK_GBPS,
                      "unit": "GB/s", "frac": round(total / (ms * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4),
                      "traffic": None, "bytes_per_step": total,
-                     "weight_bytes_over_peak_ms": round(wbytes / HBM_PEAK_GBPS / 1e6, 4),
-                     "target_ms": round(1.3 * wbytes / HBM_PEAK_GBPS / 1e6, 4)},
-        "cpu_baseline": cpu,
+                     "weight_bytes_over_peak_ms": round(r["weight_bytes"] / HBM_PEAK_GBPS / 1e6, 4),
+                     "target_ms": round(1.3 * r["weight_bytes"] / HBM_PEAK_GBPS / 1e6, 4)},
+        "cpu_baseline": r["cpu"],
     }
     print(json.dumps(line))
-    model.release()
-    H.releaseHipQuantizedWeightHandle(head)
     return 0
 
 
@@ -423,8 +527,7 @@ def decode_cpu_baseline(shape, data, head_blocks, seconds: float) -> dict:
     return {"value": round(step_ms, 2), "unit": "ms", "cores": O.default_threads(), "kind": "port",
             "sample": f"{n} decoder layers ({per_layer * 1e3:.1f} ms each: projections on {O.default_threads()} "
                       f"threads, attention over 4096 cached tokens on one) + the head once ({head_s * 1e3:.0f} ms), "
-                      f"extrapolated to 42 layers + head; host {platform.processor() or platform.machine()}, "
-                      f"{os.cpu_count()} logical CPUs"}
+                      f"extrapolated to 42 layers + head; host {host_cpu_model()}, {os.cpu_count()} logical CPUs"}
 
 
 MFMA_F16_PEAK_TFLOPS = 2500.0  # dense f16 matrix-core peak, MI355X
@@ -670,7 +773,13 @@ def main() -> int:
     w_down = S.weight_blocks(FFN_DOWN[0], S.derive(seed, wl, "down"), FFN_DOWN[1], FFN_DOWN[2]) if wl == "ffn" else None
     x_host = S.activations(S.derive(seed, wl), m, k)
 
-    copies = max(1, math.ceil(args.rotate_mib * 2**20 / weight_bytes(wl)))
+    # distinct copies: >= rotate_mib in all, and enough that the steps just
+    # before the timed ones (the warm-up graph) cover >= 320 MiB of other
+    # copies, more than the 256 MB Infinity Cache holds
+    wb = weight_bytes(wl)
+    copies = max(1, math.ceil(args.rotate_mib * 2**20 / wb))
+    if args.rotate_mib >= 320:
+        copies = max(copies, min(args.steps, 4096) + math.ceil(320 * 2**20 / wb))
     handles, down_handles = [], []
     for _ in range(copies):
         handles.append([H.createHipQuantizedWeightHandle(t, w, k, r).handle for (t, r), w in zip(specs, ws)])
@@ -712,42 +821,55 @@ def main() -> int:
                 raise SystemExit("device-pointer path disagrees with the host path")
 
     step_bytes = algorithmic_bytes(wl, m)
+    K, W = max(1, args.steps), max(0, args.warmup)
     # eager: host-submitted launches (bounded by the host submission rate)
-    for i in range(args.warmup):
-        step(i)
+    for i in range(min(W, 8)):
+        step(K + i)
     torch.cuda.synchronize()
+    n_eager = min(K, 100)
     t0 = time.perf_counter()
-    for i in range(args.steps):
-        step(i)
+    for i in range(n_eager):
+        step(K + i)
     torch.cuda.synchronize()
-    eager_ms = (time.perf_counter() - t0) / args.steps * 1e3
+    eager_ms = (time.perf_counter() - t0) / n_eager * 1e3
 
-    # timed: one pass over every weight copy captured in a HIP graph, replayed
+    # Graphs on one side stream (warmed by an uncaptured step first): the
+    # timed graph holds exactly K steps, step i on copy i % copies; the
+    # warm-up graph holds the W warm-up steps and at least every copy the
+    # timed graph does not touch first, so the timed steps start with cold
+    # weights.
     side = torch.cuda.Stream()
-    per_graph = copies if copies >= 8 else 8 * copies
-    graph = torch.cuda.CUDAGraph()
+    side.wait_stream(torch.cuda.current_stream())
+
+    def capture(first: int, count: int, same_copy: bool = False):
+        nonlocal stream
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.stream(side):
+            with torch.cuda.graph(g, stream=side):
+                stream = torch.cuda.current_stream().cuda_stream
+                for i in range(count):
+                    step(0 if same_copy else first + i)
+        return g
+
     with torch.cuda.stream(side):
         stream = side.cuda_stream
         step(0)
-        torch.cuda.synchronize()
-        with torch.cuda.graph(graph, stream=side):
-            stream = torch.cuda.current_stream().cuda_stream
-            for i in range(per_graph):
-                step(i)
-    replays = max(1, math.ceil(args.steps / per_graph))
-    steps = replays * per_graph
+    torch.cuda.synchronize()
+    warm_count = max(W, copies - K if K < copies else 0, 1)
+    g_warm = capture(K, warm_count)
+    g_timed = capture(0, K)
     start = torch.cuda.Event(enable_timing=True)
     end = torch.cuda.Event(enable_timing=True)
-    for _ in range(max(1, math.ceil(args.warmup / per_graph))):
-        graph.replay()
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    start.record()
-    for _ in range(replays):
-        graph.replay()
-    end.record()
-    torch.cuda.synchronize()
-    wall = time.perf_counter() - t0
+    with torch.cuda.stream(side):
+        g_warm.replay()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        start.record()
+        g_timed.replay()
+        end.record()
+        torch.cuda.synchronize()
+        wall = time.perf_counter() - t0
+    steps = K
     ms_per_step = wall / steps * 1e3
     value = step_bytes / (ms_per_step * 1e-3) / 1e9
     # HIP events bracketing the timed region on the launch stream: average
@@ -755,21 +877,24 @@ def main() -> int:
     kern_us = start.elapsed_time(end) / steps * 1e3
     achieved = step_bytes / (kern_us * 1e-6) / 1e9
 
-    # Infinity-Cache-hot reference: the same step on one resident copy
-    hot = torch.cuda.CUDAGraph()
+    # Infinity-Cache-hot reference: K steps on one resident copy
+    hot = capture(0, K, same_copy=True)
     with torch.cuda.stream(side):
-        with torch.cuda.graph(hot, stream=side):
-            stream = torch.cuda.current_stream().cuda_stream
-            for i in range(per_graph):
-                step(0)
-    hot.replay()
-    torch.cuda.synchronize()
-    start.record()
-    for _ in range(replays):
         hot.replay()
-    end.record()
-    torch.cuda.synchronize()
-    hot_us = start.elapsed_time(end) / steps * 1e3
+        torch.cuda.synchronize()
+        start.record()
+        hot.replay()
+        end.record()
+        torch.cuda.synchronize()
+    hot_us = start.elapsed_time(end) / K * 1e3
+
+    decode = None
+    if wl == "qkv" and m == 1 and not args.no_decode:
+        for hs in handles:
+            for h in hs:
+                H.lib().hp_hip_weight_release(h)
+        handles.clear()
+        decode = decode_summary(measure_decode_step(1, 20, 3, None))
 
     traffic = None
     tfile = ROOT / "profiles" / f"{wl}_m{m}_traffic.json"
@@ -805,7 +930,8 @@ def main() -> int:
             "algorithmic_bytes_per_step": step_bytes,
             "weight_copies_rotated": copies,
             "parallelism": "single GPU",
-            "timing": "steps captured in a HIP graph and replayed back to back",
+            "timing": f"exactly {K} steps (step i on weight copy i % {copies}) captured in one HIP graph and "
+                      f"replayed once, after a warm-up graph of {warm_count} steps over the other copies",
             "eager_host_launch_ms_per_step": round(eager_ms, 5),
         },
         "roofline": {
@@ -821,6 +947,8 @@ def main() -> int:
         },
         "cpu_baseline": cpu,
     }
+    if decode is not None:
+        line["decode_step"] = decode
     print(json.dumps(line))
     return 0
 

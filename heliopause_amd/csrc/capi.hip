@@ -853,7 +853,9 @@ AttnArgs attn_args(const hp_hip_attention_config_t *c) {
 }
 
 int32_t run_attention(AttnArgs a, float *partials, hipStream_t stream) {
+  hipEvent_t e = prof_begin(stream);
   HP_HIP_TRY(launch_attention(a, partials, stream));
+  prof_end(HP_KERNEL_ATTENTION, e, stream);
   st().launches += 2;
   return HP_OK;
 }
@@ -872,7 +874,9 @@ int32_t run_norm(const float *y, int rows, int n, const float *w_post, const flo
   a.n = n;
   a.rows = rows;
   a.eps = eps;
+  hipEvent_t e = prof_begin(stream);
   HP_HIP_TRY(launch_norm_residual(a, stream));
+  prof_end(HP_KERNEL_NORM, e, stream);
   st().launches++;
   return HP_OK;
 }
@@ -1361,8 +1365,10 @@ int32_t hp_hip_sample_device(const uint32_t *d_ids, const float *d_values, size_
   if (!d_ids || !d_values || !d_rng_state || !d_tokens || !d_probabilities || !d_kept)
     return fail(HP_ERR_ARG, "null pointer");
   hipStream_t q = stream ? static_cast<hipStream_t>(stream) : s.stream;
+  hipEvent_t e = prof_begin(q);
   HP_HIP_TRY(launch_sample(d_ids, d_values, (int)column_count, (int)k, (int)count, sample_params(sampling), d_rng_state,
                            d_tokens, d_probabilities, d_kept, q));
+  prof_end(HP_KERNEL_SAMPLE, e, q);
   s.launches++;
   return HP_OK;
 }
@@ -1788,7 +1794,9 @@ int32_t hp_hip_decode_layers_device(const hp_hip_decode_layer_t *layers, size_t 
       pa.tokens = (int)M;
       pa.rope_table = rope_table;
       pa.rope_table_mode = table_mode;
+      hipEvent_t e = prof_begin(strm);
       HP_HIP_TRY(launch_qkv_post(pa, strm));
+      prof_end(HP_KERNEL_ATTENTION, e, strm);
       s.launches++;
       aa.q = qr;
       aa.tokens = (int)M;

@@ -36,6 +36,9 @@ LIB_PATH = PKG / "libhp_hip.so"
 HP_OK, HP_ERR_SHAPE, HP_ERR_HEADS, HP_ERR_TYPE = 0, 1, 2, 3
 HP_ERR_HIP, HP_ERR_HANDLE, HP_ERR_ARG, HP_ERR_NODEV, HP_ERR_OOM = 16, 17, 18, 19, 20
 HP_KERNEL_Q8K, HP_KERNEL_MATVEC, HP_KERNEL_TOPK, HP_KERNEL_GEGLU = 0, 1, 2, 3
+HP_KERNEL_ATTENTION, HP_KERNEL_NORM, HP_KERNEL_SAMPLE = 4, 5, 6
+KERNEL_NAMES = {HP_KERNEL_Q8K: "q8k", HP_KERNEL_MATVEC: "matvec", HP_KERNEL_TOPK: "topk", HP_KERNEL_GEGLU: "geglu",
+                HP_KERNEL_ATTENTION: "attention", HP_KERNEL_NORM: "norm", HP_KERNEL_SAMPLE: "sample"}
 GELU_C = float(np.sqrt(2.0 / np.pi))
 
 TYPE_IDS = {"Q4_K": 1, "Q5_K": 2, "Q6_K": 3, "IQ4_XS": 4, "Q8_0": 5, "Q4_0": 6}

@@ -69,7 +69,10 @@ extern "C" {
 #define HP_KERNEL_MATVEC 1
 #define HP_KERNEL_TOPK 2
 #define HP_KERNEL_GEGLU 3
-#define HP_KERNEL_COUNT 4
+#define HP_KERNEL_ATTENTION 4 /* attention prologue, partials and merge */
+#define HP_KERNEL_NORM 5      /* norm / residual launches of the decoder layer */
+#define HP_KERNEL_SAMPLE 6
+#define HP_KERNEL_COUNT 7
 
 typedef struct hp_hip_stats {
   uint64_t handle_count;   /* live weight handles */

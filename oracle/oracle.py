@@ -47,7 +47,23 @@ def lib() -> ctypes.CDLL:
         return _lib
     if not LIB_PATH.exists():
         build()
-    L = ctypes.CDLL(str(LIB_PATH))
+    _lib = _declare(ctypes.CDLL(str(LIB_PATH)))
+    return _lib
+
+
+def native_lib(build_dir) -> ctypes.CDLL:
+    """The oracle compiled for the running host's own ISA (-march=native, with
+    the same -ffp-contract=off / -fno-fast-math numerics) into build_dir: the
+    CPU baseline's native leg.  Built where it runs, since its code is only
+    valid on this host's CPU."""
+    out = Path(build_dir) / "libhp_oracle_native.so"
+    subprocess.run([os.environ.get("CC", "gcc"), "-std=gnu11", "-O3", "-march=native", "-ffp-contract=off",
+                    "-fno-fast-math", "-fPIC", "-pthread", "-shared", "-o", str(out), str(HERE / "hp_oracle.c"),
+                    "-lm"], check=True, capture_output=True)
+    return _declare(ctypes.CDLL(str(out)))
+
+
+def _declare(L: ctypes.CDLL) -> ctypes.CDLL:
     L.hpo_f16_to_f32.argtypes = [ctypes.c_uint16]
     L.hpo_f16_to_f32.restype = ctypes.c_float
     L.hpo_f16_to_f32_bits.argtypes = [ctypes.c_uint16]
@@ -90,7 +106,6 @@ def lib() -> ctypes.CDLL:
     L.hpo_topk.restype = _sz
     L.hpo_softcap.argtypes = [ctypes.c_float, ctypes.c_double]
     L.hpo_softcap.restype = ctypes.c_float
-    _lib = L
     return L
 
 
@@ -207,7 +222,8 @@ def matmul(type_id: int, weight: np.ndarray, x: np.ndarray, row_count: int, thre
     return out.reshape(m, row_count)
 
 
-def matmul_multi(type_ids, weights, x: np.ndarray, row_counts, threads: int = 0) -> list[np.ndarray]:
+def matmul_multi(type_ids, weights, x: np.ndarray, row_counts, threads: int = 0,
+                 library: ctypes.CDLL | None = None) -> list[np.ndarray]:
     x = _c(np.atleast_2d(x), np.float32)
     m, k = x.shape
     count = len(type_ids)
@@ -219,12 +235,12 @@ def matmul_multi(type_ids, weights, x: np.ndarray, row_counts, threads: int = 0)
     rc = (_sz * count)(*row_counts)
     optr = (_f32p * count)(*[_p(o, _f32p) for o in outs])
     olen = (_sz * count)(*[r * m for r in row_counts])
+    L = library if library is not None else lib()
     if threads:
-        st = lib().hpo_matmul_quantized_multi_threaded(count, _p(x, _f32p), x.size, k, m, tids, wptr, wlen, rc,
-                                                       optr, olen, threads)
+        st = L.hpo_matmul_quantized_multi_threaded(count, _p(x, _f32p), x.size, k, m, tids, wptr, wlen, rc,
+                                                   optr, olen, threads)
     else:
-        st = lib().hpo_matmul_quantized_multi(count, _p(x, _f32p), x.size, k, m, tids, wptr, wlen, rc, optr,
-                                              olen)
+        st = L.hpo_matmul_quantized_multi(count, _p(x, _f32p), x.size, k, m, tids, wptr, wlen, rc, optr, olen)
     if st != OK:
         raise RuntimeError(f"oracle multi matmul failed with status {st}")
     return [o[: r * m].reshape(m, r) for o, r in zip(outs, row_counts)]
