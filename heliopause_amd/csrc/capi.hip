@@ -1638,7 +1638,8 @@ int32_t hp_hip_attention_prep_device(const hp_hip_attention_config_t *config, si
   if (rc != HP_OK) return rc;
   rc = attention_check(config);
   if (rc != HP_OK) return rc;
-  if (token_count < 1 || token_count > (size_t)kMaxTokens) return fail(HP_ERR_SHAPE, "token_count must be 1..8");
+  if (token_count < 1 || token_count > (size_t)kMaxChunkTokens || token_count > (size_t)config->capacity)
+    return fail(HP_ERR_SHAPE, "token_count must be 1..min(4096, capacity)");
   if (!d_q || !d_k || !d_q_norm || !d_k_norm || !d_position || !d_q_out || !d_key_cache || !d_value_cache)
     return fail(HP_ERR_ARG, "null pointer");
   hipStream_t strm = stream ? static_cast<hipStream_t>(stream) : s.stream;
@@ -1667,13 +1668,20 @@ int32_t hp_hip_gqa_attention_device(const hp_hip_attention_config_t *config, siz
   if (rc != HP_OK) return rc;
   rc = attention_check(config);
   if (rc != HP_OK) return rc;
-  if (token_count < 1 || token_count > (size_t)kMaxTokens) return fail(HP_ERR_SHAPE, "token_count must be 1..8");
+  if (token_count < 1 || token_count > (size_t)kMaxChunkTokens || token_count > (size_t)config->capacity)
+    return fail(HP_ERR_SHAPE, "token_count must be 1..min(4096, capacity)");
   if (!d_q || !d_key_cache || !d_value_cache || !d_position || !d_output) return fail(HP_ERR_ARG, "null pointer");
   hipStream_t strm = stream ? static_cast<hipStream_t>(stream) : s.stream;
+  const bool prefill = token_count > (size_t)kMaxTokens;
+  const int ranges = prefill ? attn_prefill_ranges((int)token_count, config->head_count, config->head_count_kv,
+                                                   config->capacity, s.num_cus)
+                             : 0;
   void *partials = nullptr;
   rc = stream_scratch(strm, kScratchAttn,
-               attn_partial_floats(config->head_count_kv, config->capacity, (int)token_count) * sizeof(float),
-               &partials);
+                      (prefill ? attn_prefill_partial_floats(config->head_count_kv, (int)token_count, ranges)
+                               : attn_partial_floats(config->head_count_kv, config->capacity, (int)token_count)) *
+                          sizeof(float),
+                      &partials);
   if (rc != HP_OK) return rc;
   AttnArgs a = attn_args(config);
   a.q = d_q;
@@ -1682,7 +1690,12 @@ int32_t hp_hip_gqa_attention_device(const hp_hip_attention_config_t *config, siz
   a.position = d_position;
   a.out = d_output;
   a.tokens = (int)token_count;
-  return run_attention(a, static_cast<float *>(partials), strm);
+  if (!prefill) return run_attention(a, static_cast<float *>(partials), strm);
+  hipEvent_t e = prof_begin(strm);
+  HP_HIP_TRY(launch_attention_prefill(a, static_cast<float *>(partials), ranges, strm));
+  prof_end(HP_KERNEL_ATTENTION, e, strm);
+  s.launches += 2;
+  return HP_OK;
 }
 
 int32_t hp_hip_decode_layers_device(const hp_hip_decode_layer_t *layers, size_t layer_count, size_t token_count,
@@ -1692,14 +1705,15 @@ int32_t hp_hip_decode_layers_device(const hp_hip_decode_layer_t *layers, size_t 
   std::lock_guard<std::recursive_mutex> lock(s.mu);
   int32_t rc = ensure_init(s.ready ? s.device : 0);
   if (rc != HP_OK) return rc;
-  if (token_count < 1 || token_count > (size_t)kMaxTokens) return fail(HP_ERR_SHAPE, "token_count must be 1..8");
+  if (token_count < 1 || token_count > (size_t)kMaxLayerTokens)
+    return fail(HP_ERR_SHAPE, "token_count must be 1.." + std::to_string(kMaxLayerTokens));
   if (layer_count == 0) return fail(HP_ERR_ARG, "no layers (the final norm alone: hp_hip_rms_norm_device)");
   if (!d_hidden || !d_position || !layers || (d_output_norm && !d_output)) return fail(HP_ERR_ARG, "null pointer");
   if (reinterpret_cast<uintptr_t>(d_hidden) % 16 != 0) return fail(HP_ERR_ARG, "hidden must be 16-byte aligned");
-  const size_t M = token_count;
   std::vector<LayerHandles> hs(layer_count);
   size_t hidden = lookup(layers[0].attn_q) ? lookup(layers[0].attn_q)->input_size : 0;
-  size_t qmax = 0, kvmax = 0, ffmax = 0, partials = 0;
+  size_t qmax = 0, kvmax = 0, ffmax = 0;
+  int min_cap = INT32_MAX;
   for (size_t i = 0; i < layer_count; i++) {
     rc = decode_layer_check(layers[i], hidden, &hs[i]);
     if (rc != HP_OK) return rc;
@@ -1707,15 +1721,36 @@ int32_t hp_hip_decode_layers_device(const hp_hip_decode_layer_t *layers, size_t 
     qmax = std::max(qmax, (size_t)c.head_count * kHeadDim);
     kvmax = std::max(kvmax, (size_t)c.head_count_kv * kHeadDim);
     ffmax = std::max(ffmax, hs[i].gate->row_count);
-    partials = std::max(partials, attn_partial_floats(c.head_count_kv, c.capacity, (int)M));
+    min_cap = std::min(min_cap, c.capacity);
   }
   if (hidden == 0 || hidden > kNormMaxN) return fail(HP_ERR_SHAPE, "hidden size must be 1..4096");
+  // Chunks of tokens go through every layer in turn, each chunk spanning
+  // fewer positions than the smallest KV ring holds, so a chunk's appends
+  // never overwrite keys that its own tokens still attend to
+  // (slidingRingChunkTokenCount, wasm/segment-runner.ts:181-207).
+  const size_t chunk = std::min<size_t>({token_count, (size_t)min_cap, (size_t)kMaxChunkTokens});
+  const size_t last = token_count - (token_count - 1) / chunk * chunk;  // tokens of the last chunk
+  size_t partials = 0;
+  for (size_t i = 0; i < layer_count; i++) {
+    const hp_hip_attention_config_t &c = layers[i].attention;
+    for (size_t mc : {chunk, last}) {
+      const size_t need =
+          mc <= (size_t)kMaxTokens
+              ? attn_partial_floats(c.head_count_kv, c.capacity, (int)mc)
+              : attn_prefill_partial_floats(
+                    c.head_count_kv, (int)mc,
+                    attn_prefill_ranges((int)mc, c.head_count, c.head_count_kv, c.capacity, s.num_cus));
+      partials = std::max(partials, need);
+    }
+  }
+  const size_t M = chunk;  // rows of every scratch buffer
   // scratch ([M] rows each): xn, q, k, v, q after RoPE, attention, o, x1, h, y;
   // attention partials; RoPE tables [M][128] cos, sin
-  // (2 or more tokens) the Q/K/V and down inputs as pre-quantised images
+  // (2..8 tokens) the Q/K/V and down inputs as pre-quantised images
   auto al = [](size_t n) { return (n + 63) & ~(size_t)63; };
-  const size_t img_x = M >= 2 ? q8_image_bytes((int)M, (int)(hidden / kQK)) / sizeof(float) : 0;
-  const size_t img_h = M >= 2 ? q8_image_bytes((int)M, (int)(ffmax / kQK)) / sizeof(float) : 0;
+  const bool images = M >= 2 && M <= (size_t)kMaxTokens;
+  const size_t img_x = images ? q8_image_bytes((int)M, (int)(hidden / kQK)) / sizeof(float) : 0;
+  const size_t img_h = images ? q8_image_bytes((int)M, (int)(ffmax / kQK)) / sizeof(float) : 0;
   const size_t sizes[14] = {al(M * hidden), al(M * qmax),   al(M * kvmax),  al(M * kvmax),
                             al(M * qmax),   al(M * qmax),   al(M * hidden), al(M * hidden),
                             al(M * ffmax),  al(M * hidden), al(partials),   al(M * kHeadDim / 2 * 4),
@@ -1735,107 +1770,125 @@ int32_t hp_hip_decode_layers_device(const hp_hip_decode_layer_t *layers, size_t 
   float *xn = buf[0], *q = buf[1], *k = buf[2], *v = buf[3], *qr = buf[4], *att = buf[5], *o = buf[6],
         *x1 = buf[7], *h = buf[8], *y = buf[9], *part = buf[10];
   double2 *rope_table = reinterpret_cast<double2 *>(buf[11]);
-  uint8_t *imgx = M >= 2 && hidden % kQK == 0 ? reinterpret_cast<uint8_t *>(buf[12]) : nullptr;
-  uint8_t *imgh = M >= 2 && ffmax % kQK == 0 ? reinterpret_cast<uint8_t *>(buf[13]) : nullptr;
-  // The norms ride in the prologues of the launches that consume them (one
-  // token): the Q/K/V launch forms attn_norm(previous residual), the gate/up
-  // launch ffn_norm(residual after attention).  With several tokens, or a
-  // forced matrix-core kernel, they run as norm launches into xn.
-  NormIn nin{};
-  nin.mode = 1;
-  nin.y = d_hidden;
-  nin.w_next = layers[0].d_attn_norm;
-  nin.scale = 1.0f;
-  nin.eps = layers[0].attention.epsilon;
-  for (size_t i = 0; i < layer_count; i++) {
-    const hp_hip_decode_layer_t &L = layers[i];
-    const LayerHandles &H = hs[i];
-    const double eps = L.attention.epsilon;
-    Handle *qkv[3] = {H.q, H.k, H.v};
-    float *qkv_out[3] = {q, k, v};
-    rc = run_matvec(H.v ? 3 : 2, qkv, nullptr, hidden, M, qkv_out, strm, &nin, xn, imgx);
-    if (rc != HP_OK) return rc;
-    // the RoPE angles depend on the positions and the RoPE parameters only:
-    // a layer whose parameters match the previous layer's reads its table
-    const hp_hip_attention_config_t *pc = i > 0 ? &layers[i - 1].attention : nullptr;
-    const int table_mode = pc && pc->rope_dims == L.attention.rope_dims &&
-                                   pc->rope_freq_base == L.attention.rope_freq_base &&
-                                   pc->d_rope_freq_factors == L.attention.d_rope_freq_factors
-                               ? 2
-                               : 1;
-    AttnArgs aa = attn_args(&L.attention);
-    aa.k_cache = reinterpret_cast<_Float16 *>(L.d_key_cache);
-    aa.v_cache = reinterpret_cast<_Float16 *>(L.d_value_cache);
-    aa.position = d_position;
-    aa.out = att;
-    aa.rope_table = rope_table;
-    aa.rope_table_mode = table_mode;
-    if (M == 1) {
-      // one token: norms, RoPE and the cache append inside the attention launch
-      aa.prep = 1;
-      aa.q = q;
-      aa.k = k;
-      aa.v = H.v ? v : k;
-      aa.wq = L.d_attn_q_norm;
-      aa.wk = L.d_attn_k_norm;
-    } else {
-      // a draft: every token's key and value enter the caches first, then
-      // each token attends causally
-      QkvPostArgs pa = qkv_post_args(&L.attention);
-      pa.q = q;
-      pa.k = k;
-      pa.v = H.v ? v : k;
-      pa.wq = L.d_attn_q_norm;
-      pa.wk = L.d_attn_k_norm;
-      pa.position = d_position;
-      pa.q_out = qr;
-      pa.k_cache = aa.k_cache;
-      pa.v_cache = aa.v_cache;
-      pa.tokens = (int)M;
-      pa.rope_table = rope_table;
-      pa.rope_table_mode = table_mode;
-      hipEvent_t e = prof_begin(strm);
-      HP_HIP_TRY(launch_qkv_post(pa, strm));
-      prof_end(HP_KERNEL_ATTENTION, e, strm);
-      s.launches++;
-      aa.q = qr;
-      aa.tokens = (int)M;
+  uint8_t *imgx_buf = images && hidden % kQK == 0 ? reinterpret_cast<uint8_t *>(buf[12]) : nullptr;
+  uint8_t *imgh_buf = images && ffmax % kQK == 0 ? reinterpret_cast<uint8_t *>(buf[13]) : nullptr;
+
+  for (size_t c0 = 0; c0 < token_count; c0 += chunk) {
+    const size_t Mc = std::min(chunk, token_count - c0);
+    float *hid = d_hidden + c0 * hidden;
+    uint8_t *imgx = Mc >= 2 && Mc <= (size_t)kMaxTokens ? imgx_buf : nullptr;
+    uint8_t *imgh = Mc >= 2 && Mc <= (size_t)kMaxTokens ? imgh_buf : nullptr;
+    // The norms ride in the prologues of the launches that consume them (one
+    // token): the Q/K/V launch forms attn_norm(previous residual), the gate/up
+    // launch ffn_norm(residual after attention).  With several tokens, or a
+    // forced matrix-core kernel, they run as norm launches into xn.
+    NormIn nin{};
+    nin.mode = 1;
+    nin.y = hid;
+    nin.w_next = layers[0].d_attn_norm;
+    nin.scale = 1.0f;
+    nin.eps = layers[0].attention.epsilon;
+    for (size_t i = 0; i < layer_count; i++) {
+      const hp_hip_decode_layer_t &L = layers[i];
+      const LayerHandles &H = hs[i];
+      const double eps = L.attention.epsilon;
+      Handle *qkv[3] = {H.q, H.k, H.v};
+      float *qkv_out[3] = {q, k, v};
+      rc = run_matvec(H.v ? 3 : 2, qkv, nullptr, hidden, Mc, qkv_out, strm, &nin, xn, imgx);
+      if (rc != HP_OK) return rc;
+      // the RoPE angles depend on the positions and the RoPE parameters only:
+      // a layer whose parameters match the previous layer's reads its table
+      const hp_hip_attention_config_t *pc = i > 0 ? &layers[i - 1].attention : nullptr;
+      const int table_mode = pc && pc->rope_dims == L.attention.rope_dims &&
+                                     pc->rope_freq_base == L.attention.rope_freq_base &&
+                                     pc->d_rope_freq_factors == L.attention.d_rope_freq_factors
+                                 ? 2
+                                 : 1;
+      AttnArgs aa = attn_args(&L.attention);
+      aa.k_cache = reinterpret_cast<_Float16 *>(L.d_key_cache);
+      aa.v_cache = reinterpret_cast<_Float16 *>(L.d_value_cache);
+      aa.position = d_position;
+      aa.pos_offset = (int)c0;
+      aa.out = att;
+      aa.rope_table = rope_table;
+      aa.rope_table_mode = table_mode;
+      if (Mc == 1) {
+        // one token: norms, RoPE and the cache append inside the attention launch
+        aa.prep = 1;
+        aa.q = q;
+        aa.k = k;
+        aa.v = H.v ? v : k;
+        aa.wq = L.d_attn_q_norm;
+        aa.wk = L.d_attn_k_norm;
+      } else {
+        // a draft or a prefill chunk: every token's key and value enter the
+        // caches first, then each token attends causally
+        QkvPostArgs pa = qkv_post_args(&L.attention);
+        pa.q = q;
+        pa.k = k;
+        pa.v = H.v ? v : k;
+        pa.wq = L.d_attn_q_norm;
+        pa.wk = L.d_attn_k_norm;
+        pa.position = d_position;
+        pa.pos_offset = (int)c0;
+        pa.q_out = qr;
+        pa.k_cache = aa.k_cache;
+        pa.v_cache = aa.v_cache;
+        pa.tokens = (int)Mc;
+        pa.rope_table = rope_table;
+        pa.rope_table_mode = table_mode;
+        hipEvent_t e = prof_begin(strm);
+        HP_HIP_TRY(launch_qkv_post(pa, strm));
+        prof_end(HP_KERNEL_ATTENTION, e, strm);
+        s.launches++;
+        aa.q = qr;
+        aa.tokens = (int)Mc;
+      }
+      if (Mc <= (size_t)kMaxTokens) {
+        rc = run_attention(aa, part, strm);
+      } else {
+        const int ranges = attn_prefill_ranges((int)Mc, L.attention.head_count, L.attention.head_count_kv,
+                                               L.attention.capacity, s.num_cus);
+        hipEvent_t e = prof_begin(strm);
+        HP_HIP_TRY(launch_attention_prefill(aa, part, ranges, strm));
+        prof_end(HP_KERNEL_ATTENTION, e, strm);
+        s.launches += 2;
+      }
+      if (rc != HP_OK) return rc;
+      Handle *oh[1] = {H.o};
+      float *oo[1] = {o};
+      rc = run_matvec(1, oh, att, H.o->input_size, Mc, oo, strm);
+      if (rc != HP_OK) return rc;
+      NormIn fin{};
+      fin.mode = 2;
+      fin.y = o;
+      fin.w_post = L.d_post_attention_norm;
+      fin.x_res = hid;
+      fin.scale = 1.0f;
+      fin.x_out = x1;
+      fin.w_next = L.d_ffn_norm;
+      fin.eps = eps;
+      bool h_img = false;
+      rc = run_matvec_geglu(H.gate, H.up, nullptr, hidden, Mc, h, strm, &fin, xn, imgh, &h_img);
+      if (rc != HP_OK) return rc;
+      Handle *dh[1] = {H.down};
+      float *yo[1] = {y};
+      rc = run_matvec(1, dh, h, H.down->input_size, Mc, yo, strm, nullptr, nullptr, nullptr, h_img ? imgh : nullptr);
+      if (rc != HP_OK) return rc;
+      nin.mode = 2;
+      nin.y = y;
+      nin.w_post = L.d_post_ffw_norm;
+      nin.x_res = x1;
+      nin.scale = L.layer_output_scale;
+      nin.x_out = hid;
+      nin.w_next = i + 1 < layer_count ? layers[i + 1].d_attn_norm : nullptr;
+      nin.eps = eps;
     }
-    rc = run_attention(aa, part, strm);
+    // the last layer's post-FFN residual, then output_norm
+    rc = run_norm(y, (int)Mc, (int)hidden, nin.w_post, x1, nin.scale, hid, d_output_norm,
+                  d_output_norm ? d_output + c0 * hidden : nullptr, nin.eps, strm);
     if (rc != HP_OK) return rc;
-    Handle *oh[1] = {H.o};
-    float *oo[1] = {o};
-    rc = run_matvec(1, oh, att, H.o->input_size, M, oo, strm);
-    if (rc != HP_OK) return rc;
-    NormIn fin{};
-    fin.mode = 2;
-    fin.y = o;
-    fin.w_post = L.d_post_attention_norm;
-    fin.x_res = d_hidden;
-    fin.scale = 1.0f;
-    fin.x_out = x1;
-    fin.w_next = L.d_ffn_norm;
-    fin.eps = eps;
-    bool h_img = false;
-    rc = run_matvec_geglu(H.gate, H.up, nullptr, hidden, M, h, strm, &fin, xn, imgh, &h_img);
-    if (rc != HP_OK) return rc;
-    Handle *dh[1] = {H.down};
-    float *yo[1] = {y};
-    rc = run_matvec(1, dh, h, H.down->input_size, M, yo, strm, nullptr, nullptr, nullptr, h_img ? imgh : nullptr);
-    if (rc != HP_OK) return rc;
-    nin.mode = 2;
-    nin.y = y;
-    nin.w_post = L.d_post_ffw_norm;
-    nin.x_res = x1;
-    nin.scale = L.layer_output_scale;
-    nin.x_out = d_hidden;
-    nin.w_next = i + 1 < layer_count ? layers[i + 1].d_attn_norm : nullptr;
-    nin.eps = eps;
   }
-  // the last layer's post-FFN residual, then output_norm
-  rc = run_norm(y, (int)M, (int)hidden, nin.w_post, x1, nin.scale, d_hidden, d_output_norm,
-                d_output_norm ? d_output : nullptr, nin.eps, strm);
-  if (rc != HP_OK) return rc;
   return HP_OK;
 }
 

@@ -36,59 +36,13 @@
 #include "hp_gelu.h"
 #include "hp_wave.h"
 #include "hp_q8k16.h"
+#include "hp_attn.h"
 
 namespace hp {
 
 namespace {
 
 constexpr int kNormPer = 16;  // elements per thread of the 256-thread norm: n <= 4096
-
-// float32_to_float16 then float16_to_float32 of lib.rs:2507-2568.
-__device__ __forceinline__ float rs_f16_round(float v) {
-  const uint32_t bits = __builtin_bit_cast(uint32_t, v);
-  const uint32_t sign = (bits >> 16) & 0x8000u;
-  const int e = (int)((bits >> 23) & 0xffu);
-  const uint32_t man = bits & 0x7fffffu;
-  uint32_t h;
-  if (e == 0xff) {
-    h = man == 0 ? (sign | 0x7c00u) : 0x7e00u;
-  } else {
-    const int he = e - 112;
-    if (he >= 31) {
-      h = sign | 0x7bffu;
-    } else if (he <= 0) {
-      if (he < -10) {
-        h = sign;
-      } else {
-        const uint32_t mh = man | 0x800000u;
-        const int sh = 14 - he;
-        h = sign | ((mh + (1u << (sh - 1))) >> sh);
-      }
-    } else {
-      const uint32_t rm = man + 0x1000u;
-      if (rm & 0x800000u)
-        h = he + 1 >= 31 ? (sign | 0x7bffu) : (sign | ((uint32_t)(he + 1) << 10));
-      else
-        h = sign | ((uint32_t)he << 10) | (rm >> 13);
-    }
-  }
-  return (float)__builtin_bit_cast(_Float16, (uint16_t)h);
-}
-
-// Two f32 values as packed f16 (round to nearest even).
-__device__ __forceinline__ uint32_t pack2_f16(float lo, float hi) {
-  return (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)lo) |
-         ((uint32_t)__builtin_bit_cast(uint16_t, (_Float16)hi) << 16);
-}
-
-// Attention window of the token at `pos`: [start, start + count).
-__device__ __forceinline__ void window_of(int pos, int capacity, int window, int *start, int *count) {
-  int c = pos + 1;
-  if (c > capacity) c = capacity;
-  if (window > 0 && c > window) c = window;
-  *count = c;
-  *start = pos + 1 - c;
-}
 
 // Sum over the 256 threads of the workgroup (every thread gets the total).
 // Sum over the workgroup's four waves; sh (4 doubles) must not have been
@@ -199,7 +153,7 @@ __global__ __launch_bounds__(64) void qkv_post_kernel(const QkvPostArgs a) {
     kind = 2;
     head = h - a.nq - a.nkv;
   }
-  const int t = blockIdx.y;  // token: position *a.position + t
+  const int t = blockIdx.y;  // token: position *a.position + a.pos_offset + t
   const size_t qrow = (size_t)t * a.nq, kvrow = (size_t)t * a.nkv;
   const float *src = kind == 0 ? a.q + (qrow + head) * kHeadDim
                                : (kind == 1 ? a.k : a.v) + (kvrow + head) * kHeadDim;
@@ -228,7 +182,7 @@ __global__ __launch_bounds__(64) void qkv_post_kernel(const QkvPostArgs a) {
     xs[i] = w ? (float)(((double)x[j] * sc) * (double)wv[j]) : (float)((double)x[j] * sc);
   }
   __syncthreads();
-  const int pos = *a.position + t;
+  const int pos = *a.position + a.pos_offset + t;
   if (kind != 2) {
     float r0[2], r1[2];
 #pragma unroll
@@ -336,7 +290,7 @@ __global__ __launch_bounds__(256) void attn_partial_kernel(const AttnArgs a) {
   // (attentionRange of the largest position); token blockIdx.z sees the keys
   // up to its own position (causalMask)
   const int tok = blockIdx.z;
-  const int pos = *a.position + (a.tokens - 1);
+  const int pos = *a.position + a.pos_offset + (a.tokens - 1);
   const int pos_t = pos - (a.tokens - 1) + tok;
 
   const int kj = tid >> 3, kp = tid & 7;
@@ -681,7 +635,7 @@ hipError_t launch_norm_residual(const NormArgs &a, hipStream_t s) {
 hipError_t launch_qkv_post(const QkvPostArgs &a, hipStream_t s) {
   if (a.nq < 1 || a.nkv < 1 || a.capacity < 1 || a.rope_dims < 0 || a.rope_dims > kHeadDim || (a.rope_dims & 1))
     return hipErrorInvalidValue;
-  if (a.tokens < 1 || a.tokens > kMaxTokens) return hipErrorInvalidValue;
+  if (a.tokens < 1 || a.tokens > kMaxChunkTokens) return hipErrorInvalidValue;
   hipLaunchKernelGGL(qkv_post_kernel, dim3(a.nq + 2 * a.nkv, a.tokens), dim3(64), 0, s, a);
   return hipGetLastError();
 }
@@ -715,6 +669,10 @@ hipError_t launch_attention(AttnArgs a, float *partials, hipStream_t s) {
   }
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
+  return launch_attention_merge(a, s);
+}
+
+hipError_t launch_attention_merge(const AttnArgs &a, hipStream_t s) {
   hipLaunchKernelGGL(attn_reduce_kernel, dim3(a.nq, kHeadDim / 64, a.tokens), dim3(256), 0, s, a);
   return hipGetLastError();
 }

@@ -203,7 +203,9 @@ hipError_t launch_geglu(const float *gate, const float *up, size_t n, double c, 
 constexpr int kHeadDim = 256;
 constexpr int kAttnChunk = 32;    // cache slots per attention workgroup
 constexpr int kAttnMaxGroup = 8;  // query heads per kv head
-constexpr int kMaxTokens = 8;     // tokens per decode call (a draft to verify)
+constexpr int kMaxTokens = 8;     // tokens of a decode call (a draft to verify) on the decode attention
+constexpr int kMaxChunkTokens = 4096;  // tokens of one prefill chunk (the prefill attention beyond 8)
+constexpr int kMaxLayerTokens = 65536; // tokens of one decoder-layers call (in chunks of <= kMaxChunkTokens)
 
 // Per row of [rows][n] (n <= 4096): x_res == null: next_out = rmsnorm(y) *
 // w_next.  Otherwise x_out = f32(f32(x_res + rmsnorm(y) * w_post) * scale)
@@ -227,7 +229,8 @@ struct QkvPostArgs {
   double2 *rope_table;  // [tokens][kHeadDim / 2] cos, sin (rope_table_mode 1: written, 2: read)
   int rope_table_mode;
   int nq, nkv, capacity, rope_dims;
-  int tokens;          // token t at position *position + t; rows [t][heads][kHeadDim]
+  int tokens;          // token t at position *position + pos_offset + t; rows [t][heads][kHeadDim]
+  int pos_offset;
   double theta_scale;  // base^(-2 / rope_dims)
   double eps;
 };
@@ -244,7 +247,8 @@ struct AttnArgs {
   float *part_m, *part_l, *part_o;  // set by launch_attention
   double2 *rope_table;  // [kHeadDim / 2] cos, sin (rope_table_mode 1: written, 2: read)
   int nq, nkv, capacity, window, chunks, rope_dims, prep, rope_table_mode;
-  int tokens;  // prep == 0: queries of tokens *position .. + tokens - 1, rows [t][nq][kHeadDim]
+  int tokens;  // prep == 0: queries of tokens *position + pos_offset .. + tokens - 1, rows [t][nq][kHeadDim]
+  int pos_offset;
   double theta_scale, eps;
 };
 hipError_t launch_norm_residual(const NormArgs &a, hipStream_t s);
@@ -253,6 +257,16 @@ hipError_t launch_qkv_post(const QkvPostArgs &a, hipStream_t s);
 // (a.rope_table, when used, lives elsewhere).
 size_t attn_partial_floats(int nkv, int capacity, int tokens);
 hipError_t launch_attention(AttnArgs a, float *partials, hipStream_t s);
+// The merge of attention partials (a.part_m/l/o, a.chunks slices per row)
+// into a.out: exp-weighted sum, division by l, castF16Rows.
+hipError_t launch_attention_merge(const AttnArgs &a, hipStream_t s);
+// Prefill attention (attn_prefill.hip): a chunk of a.tokens (<= capacity,
+// <= kMaxChunkTokens) queries after RoPE, causal over the caches, in
+// `ranges` window slices merged by launch_attention_merge.
+constexpr int kAttnPrefillMaxRanges = 16;
+int attn_prefill_ranges(int tokens, int nq, int nkv, int capacity, int num_cus);
+size_t attn_prefill_partial_floats(int nkv, int tokens, int ranges);
+hipError_t launch_attention_prefill(AttnArgs a, float *partials, int ranges, hipStream_t s);
 hipError_t launch_dequantize(int type, const uint8_t *tiles, const uint16_t *dplane, int rows,
                              const TileGeom &g, int row_start, int row_count, float *out, hipStream_t s);
 

@@ -451,7 +451,9 @@ def test_decode_draft_matches_oracle(hip, D, full, tokens, pos):
     assert _f16_steps(gk, ol.key_cache).max() <= 1
 
 
-def test_draft_rejects_too_many_tokens(hip):
+def test_layers_reject_token_counts(hip):
+    """0 tokens and more than one call takes (65536, in chunks) fail before
+    any memory is touched."""
     import torch
 
     shape = _small_shape()
@@ -461,7 +463,8 @@ def test_draft_rejects_too_many_tokens(hip):
     dx = torch.zeros(9 * shape.hidden, dtype=torch.float32, device="cuda:0")
     dpos = torch.zeros(1, dtype=torch.int32, device="cuda:0")
     try:
-        with pytest.raises(ValueError):
-            model.run_layers(dx.data_ptr(), dpos.data_ptr(), tokens=9)
+        for bad in (0, 65537):
+            with pytest.raises(ValueError):
+                model.run_layers(dx.data_ptr(), dpos.data_ptr(), tokens=bad)
     finally:
         model.release()
