@@ -125,7 +125,8 @@ def parse() -> argparse.Namespace:
     p.add_argument("--steps", type=int, default=200)
     p.add_argument("--warmup", type=int, default=20)
     p.add_argument("--m", type=int, default=1)
-    p.add_argument("--workload", choices=sorted(WORKLOADS) + ["decode42", "decode42-proj", "prefill42", "gguf-load"], default="qkv")
+    p.add_argument("--workload", choices=sorted(WORKLOADS) + ["decode42", "decode42-proj", "prefill42", "prefill42-layers",
+                                                            "gguf-load"], default="qkv")
     p.add_argument("--rotate-mib", type=int, default=640, help="distinct weight bytes cycled through")
     p.add_argument("--cpu-seconds", type=float, default=12.0)
     p.add_argument("--no-cpu", action="store_true")
@@ -614,6 +615,103 @@ def prefill_chain(args) -> int:
     return 0
 
 
+def prefill_layers(args) -> int:
+    """A 512-token prefill chunk through the whole 42-layer model on the
+    device: per layer attn_norm -> Q/K/V -> q/k norms + RoPE + v norm + the
+    chunk's cache append -> causal GQA attention over the ring (prefill
+    attention on the matrix cores + merge) -> O -> residual + ffn_norm ->
+    gate/up + GeGLU -> down -> residual + layer scale; then output_norm.  The
+    chunk sits at positions 3584..4095 of a 4096-slot f16 cache filled with
+    N(0,1), so the last token attends over all 4096 positions.  One chunk is
+    captured in a HIP graph and replayed (every replay rewrites the same
+    cache slots with the same values)."""
+    import numpy as np
+    import torch
+
+    from heliopause_amd import decode as DM
+    from heliopause_amd import hip_kernels as H
+    from heliopause_amd import synthetic as S
+
+    m = args.m if args.m > 1 else 512
+    torch.cuda.init()
+    dev = torch.device("cuda:0")
+    shape = DM.ModelShape()
+    seed = S.config_seed(5)
+    data = DM.layer_host_data(shape, seed, 0)
+    model = DM.HipDecodeModel(shape)
+    for _ in range(N_LAYERS):
+        model.add_layer(data)
+    model.output_norm = torch.from_numpy(
+        (1.0 + 0.1 * S.normal(S.derive(seed, "output_norm"), shape.hidden)).astype(np.float32)).to(dev)
+    x0 = torch.from_numpy(S.activations(S.derive(seed, "prefill-x"), m, shape.hidden).reshape(-1) * 4).to(dev)
+    hidden, normed = torch.empty_like(x0), torch.empty_like(x0)
+    p0 = shape.capacity - m
+    pos = torch.tensor([p0], dtype=torch.int32, device=dev)
+
+    def step(stream: int) -> None:
+        hidden.copy_(x0)
+        model.run_layers(hidden.data_ptr(), pos.data_ptr(), normed.data_ptr(), stream, tokens=m)
+
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        launches0 = H.hipResidentWeightStats()["kernelLaunches"]
+        step(side.cuda_stream)
+        launches = H.hipResidentWeightStats()["kernelLaunches"] - launches0 + 1
+        torch.cuda.synchronize()
+        H.profile(True)
+        step(side.cuda_stream)
+        torch.cuda.synchronize()
+        split = {}
+        for kid, name in H.KERNEL_NAMES.items():
+            t_ms, n = H.profile_read(kid)
+            if n:
+                split[name] = {"us": round(t_ms * 1e3, 1), "launches": n}
+        H.profile(False)
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=side):
+            step(torch.cuda.current_stream().cuda_stream)
+    torch.cuda.synchronize()
+    warm = max(1, args.warmup // 40)
+    for _ in range(warm):
+        graph.replay()
+    torch.cuda.synchronize()
+    steps = max(1, args.steps // 80)
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    start.record()
+    for _ in range(steps):
+        graph.replay()
+    end.record()
+    torch.cuda.synchronize()
+    wall_ms = (time.perf_counter() - t0) / steps * 1e3
+    ms = start.elapsed_time(end) / steps
+    weights = N_LAYERS * sum(r * k for _, r, k in LAYER)
+    proj_flops = 2.0 * m * weights
+    # attention: token t sees p0 + t + 1 keys; q.k and p.v, 256 dims, every query head
+    visits = sum(min(p0 + t + 1, shape.capacity) for t in range(m))
+    attn_flops = N_LAYERS * shape.head_count * visits * 256 * 2 * 2
+    flops = proj_flops + attn_flops
+    tflops = flops / (ms * 1e-3) / 1e12
+    model.release()
+    line = {
+        "metric": f"prefill chunk ms at M={m}, all layers (1 GPU)",
+        "value": round(ms, 4), "unit": "ms", "n_gpus": 1, "steps": steps, "warmup": warm,
+        "ms_per_step": round(ms, 4), "higher_is_better": False, "scaling": "weak", "vs_baseline": None,
+        "dtype": "f16 MFMA (exact integers) + f32 tail; f16 attention MFMA", "data": "synthetic",
+        "config": {"workload": f"42-layer synthetic Gemma-like model, a {m}-token prefill chunk at positions "
+                               f"{p0}..{p0 + m - 1} of a 4096-slot f16 KV ring through every layer (norms, Q/K/V, "
+                               "RoPE, cache append, causal attention, O, GeGLU FFN, residuals) and the output norm",
+                   "columns": m, "projection_flops": proj_flops, "attention_flops": attn_flops,
+                   "launches_per_step": launches, "wall_ms_per_step": round(wall_ms, 4), "kernel_split_us": split,
+                   "timing": "one chunk captured in a HIP graph and replayed"},
+        "roofline": {"bound": "mfma", "achieved": round(tflops, 2), "peak": MFMA_F16_PEAK_TFLOPS, "unit": "TFLOP/s",
+                     "frac": round(tflops / MFMA_F16_PEAK_TFLOPS, 4), "traffic": None},
+    }
+    print(json.dumps(line))
+    return 0
+
+
 PCIE_PEAK_GBPS = 64.0  # PCIe 5.0 x16, one direction
 
 
@@ -753,6 +851,8 @@ def main() -> int:
         return gguf_load(args)
     if args.workload == "prefill42":
         return prefill_chain(args)
+    if args.workload == "prefill42-layers":
+        return prefill_layers(args)
     import numpy as np
     import torch
 

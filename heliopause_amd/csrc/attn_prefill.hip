@@ -16,7 +16,7 @@
 //           keys multiply exactly, so only the order of the f32 sums differs
 //           from the reference;
 //   softmax online: a running maximum m and sum l per row, p = exp(s - m)
-//           in f32, earlier sums rescaled by exp(m_old - m);
+//           in f32 (hardware exp2), earlier sums rescaled by exp(m_old - m);
 //   values  O^T += V^T P^T on the matrix cores with p split into two f16
 //           parts (hi + lo carries 22 bits of p), so p * v is formed from
 //           exact products.
@@ -28,8 +28,14 @@
 // LDS per tile: the 32 keys as rows (K), the 32 values transposed (V^T, dim
 // rows of 32 keys), and per wave its P tile.  Row strides are padded so the
 // 16 lanes of an MFMA operand read hit distinct 16-byte slots.
+//
+// Every token block of one (KV head, slice) reads the same keys and values.
+// Workgroup i runs on XCD i % 8, so the work items are dealt out such that
+// the blocks of one (KV head, slice) share an XCD and its L2: the keys and
+// values then cross from HBM once per slice instead of once per block.
 #include "hp_attn.h"
 #include "hp_common.h"
+#include "hp_gelu.h"
 #include "hp_mfma.h"
 #include "hp_wave.h"
 
@@ -51,19 +57,19 @@ struct PfShared {
   float alpha[4][16];
 };
 
-// Halves c of the eight dwords d[r] (r = 0..7) as four dwords (rows 0..7 of
-// column c): byte select 0x05040100 takes the low halves of (y, x), 0x07060302
+// Halves c of the four dwords v[r].c/2 (keys r = 0..3 of dim c) as two
+// dwords: byte select 0x05040100 takes the low halves of (y, x), 0x07060302
 // the high halves.
-__device__ __forceinline__ uint4 column8(const uint4 (&v)[8], int c) {
+__device__ __forceinline__ uint2 column4(const uint4 (&v)[4], int c) {
   const uint32_t sel = (c & 1) ? 0x07060302u : 0x05040100u;
-  uint32_t w[4];
-#pragma unroll
-  for (int r = 0; r < 4; r++) {
-    const uint32_t lo = u4at(v[2 * r], c >> 1), hi = u4at(v[2 * r + 1], c >> 1);
-    w[r] = __builtin_amdgcn_perm(hi, lo, sel);
-  }
-  return make_uint4(w[0], w[1], w[2], w[3]);
+  const uint32_t w0 = __builtin_amdgcn_perm(u4at(v[1], c >> 1), u4at(v[0], c >> 1), sel);
+  const uint32_t w1 = __builtin_amdgcn_perm(u4at(v[3], c >> 1), u4at(v[2], c >> 1), sel);
+  return make_uint2(w0, w1);
 }
+
+// e^x for x <= 0 as 2^(x log2 e) on the hardware exp2 (about 1 ulp, plus the
+// rounding of the product: a relative error near 1e-6 at x = -20).
+__device__ __forceinline__ float exp_of(float x) { return __builtin_amdgcn_exp2f(x * 1.44269504088896341f); }
 
 __device__ __forceinline__ float row16_max(float v) {
   v = fmaxf(v, dpp_f32<kDppXor1>(v));
@@ -79,13 +85,21 @@ __device__ __forceinline__ float row16_sum(float v) {
   return v + dpp_f32<kDppRowMirror>(v);
 }
 
-__global__ __launch_bounds__(256) void attn_prefill_kernel(const AttnArgs a) {
+constexpr int kXcds = 8;
+
+__global__ __launch_bounds__(256, 1) void attn_prefill_kernel(const AttnArgs a, int blocks, int items) {
   __shared__ __align__(16) PfShared sh;
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int q4 = lane >> 4, c16 = lane & 15;
   const int G = a.nq / a.nkv, Tq = kPfRows / G;
-  const int t0 = blockIdx.x * Tq, g = blockIdx.y, range = blockIdx.z;
+  // work item (slice-major: item = (g * ranges + range) * blocks + block):
+  // XCD x takes the contiguous items [x * per_xcd, (x + 1) * per_xcd)
+  const int per_xcd = (items + kXcds - 1) / kXcds;
+  const int item = (int)(blockIdx.x % kXcds) * per_xcd + (int)(blockIdx.x / kXcds);
+  if (item >= items) return;
+  const int pair = item / blocks;
+  const int t0 = (item - pair * blocks) * Tq, g = pair / a.chunks, range = pair - g * a.chunks;
   const int M = a.tokens, cap = a.capacity;
   const size_t head_base = (size_t)g * cap * kHeadDim;
 
@@ -142,44 +156,54 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(const AttnArgs a) {
     l_run[j] = 0.0f;
   }
 
-  // staging: threads 0..127 load an 8-key x 8-dim block of values and
-  // transpose it; threads 128..255 load one key's 64 dims
-  const bool vstage = tid < 128;
-  const int b = tid & 127;
-  const int v_ko = b & 3, v_do = b >> 2;   // keys 8 v_ko.., dims 8 v_do..
-  const int k_j = b >> 2, k_u = b & 3;     // key k_j, dims 64 k_u..
-  uint4 stg[8];
-  auto slot_of = [&](int w) { return (s0 + min(w, w_stop - 1)) % cap; };
-  auto load_tile = [&](int w0) {
-    if (vstage) {
-#pragma unroll
-      for (int r = 0; r < 8; r++)
-        stg[r] = *reinterpret_cast<const uint4 *>(a.v_cache + head_base + (size_t)slot_of(w0 + 8 * v_ko + r) * kHeadDim +
-                                                  8 * v_do);
-    } else {
-      const _Float16 *krow = a.k_cache + head_base + (size_t)slot_of(w0 + k_j) * kHeadDim + 64 * k_u;
-#pragma unroll
-      for (int r = 0; r < 8; r++) stg[r] = *reinterpret_cast<const uint4 *>(krow + 8 * r);
-    }
+  // staging, the same for every thread (no branch, so no load waits on
+  // another path's): 32 bytes of values -- keys 4 v_kq .. + 3 at dims
+  // 8 v_dq .. + 7, stored transposed -- and a quarter row of one key
+  const int v_kq = tid & 7, v_dq = tid >> 3;  // keys 4 v_kq.., dims 8 v_dq..
+  const int k_j = tid >> 3, k_e = tid & 7;    // key k_j, dims 32 k_e..
+  uint4 v0, v1, v2, v3, k0, k1, k2, k3;
+  auto slot_of = [&](int w) {  // s0 < cap and w < count <= cap
+    const int slot = s0 + min(w, w_stop - 1);
+    return slot >= cap ? slot - cap : slot;
   };
-  auto store_tile = [&]() {
-    if (vstage) {
-#pragma unroll
-      for (int c = 0; c < 8; c++) *reinterpret_cast<uint4 *>(&sh.vt[8 * v_do + c][8 * v_ko]) = column8(stg, c);
-    } else {
-#pragma unroll
-      for (int r = 0; r < 8; r++) *reinterpret_cast<uint4 *>(&sh.k[k_j][64 * k_u + 8 * r]) = stg[r];
-    }
+  auto vrow = [&](int w) {
+    return reinterpret_cast<const uint4 *>(a.v_cache + head_base + (size_t)slot_of(w) * kHeadDim + 8 * v_dq);
   };
+  auto krow = [&](int w) {
+    return reinterpret_cast<const uint4 *>(a.k_cache + head_base + (size_t)slot_of(w) * kHeadDim + 32 * k_e);
+  };
+#define HP_PF_LOAD(w0)                                                                      \
+  do {                                                                                      \
+    v0 = *vrow((w0) + 4 * v_kq);                                                            \
+    v1 = *vrow((w0) + 4 * v_kq + 1);                                                        \
+    v2 = *vrow((w0) + 4 * v_kq + 2);                                                        \
+    v3 = *vrow((w0) + 4 * v_kq + 3);                                                        \
+    const uint4 *kr = krow((w0) + k_j);                                                     \
+    k0 = kr[0];                                                                             \
+    k1 = kr[1];                                                                             \
+    k2 = kr[2];                                                                             \
+    k3 = kr[3];                                                                             \
+  } while (0)
+#define HP_PF_STORE()                                                                       \
+  do {                                                                                      \
+    const uint4 vv[4] = {v0, v1, v2, v3};                                                   \
+    _Pragma("unroll") for (int c = 0; c < 8; c++)                                           \
+        *reinterpret_cast<uint2 *>(&sh.vt[8 * v_dq + c][4 * v_kq]) = column4(vv, c);        \
+    uint4 *kd = reinterpret_cast<uint4 *>(&sh.k[k_j][32 * k_e]);                            \
+    kd[0] = k0;                                                                             \
+    kd[1] = k1;                                                                             \
+    kd[2] = k2;                                                                             \
+    kd[3] = k3;                                                                             \
+  } while (0)
 
   if (w_begin < w_stop) {
-    load_tile(w_begin);
-    store_tile();
+    HP_PF_LOAD(w_begin);
+    HP_PF_STORE();
   }
   __syncthreads();
   for (int w0 = w_begin; w0 < w_stop; w0 += kPfKeys) {
     const bool more = w0 + kPfKeys < w_stop;
-    if (more) load_tile(w0 + kPfKeys);  // the next tile streams in while this one computes
+    if (more) HP_PF_LOAD(w0 + kPfKeys);  // the next tile streams in while this one computes
 
     // scores of the wave's 16 rows x 32 keys (two 16-key halves)
     f32x4 s[2];
@@ -203,11 +227,11 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(const AttnArgs a) {
         v[hf] = svalid[j] && w < w_stop && w <= last_w[j] ? s[hf][j] : -__builtin_inff();
       }
       const float m_new = fmaxf(m_run[j], row16_max(fmaxf(v[0], v[1])));
-      const float alpha = m_new == -__builtin_inff() ? 1.0f : expf(m_run[j] - m_new);
+      const float alpha = m_new == -__builtin_inff() ? 1.0f : exp_of(m_run[j] - m_new);
       float psum = 0.0f;
 #pragma unroll
       for (int hf = 0; hf < 2; hf++) {
-        p[hf][j] = v[hf] == -__builtin_inff() ? 0.0f : expf(v[hf] - m_new);
+        p[hf][j] = v[hf] == -__builtin_inff() ? 0.0f : exp_of(v[hf] - m_new);
         psum += p[hf][j];
       }
       l_run[j] = l_run[j] * alpha + row16_sum(psum);
@@ -233,10 +257,12 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(const AttnArgs a) {
       acc[d] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va, pl, acc[d], 0, 0, 0);
     }
     __syncthreads();
-    if (more) store_tile();
+    if (more) HP_PF_STORE();
     __syncthreads();
   }
 
+#undef HP_PF_LOAD
+#undef HP_PF_STORE
   // partials in attn_reduce_kernel's layout: chunk = this slice
   auto part_row = [&](int t, int h) {
     return (((size_t)t * a.nkv + g) * a.chunks + range) * kAttnMaxGroup + h;
@@ -257,6 +283,26 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(const AttnArgs a) {
     for (int d = 0; d < 16; d++)
       *reinterpret_cast<float4 *>(orow + 16 * d + 4 * q4) = make_float4(acc[d][0], acc[d][1], acc[d][2], acc[d][3]);
   }
+}
+
+// The slices of one (token, query head): thread d merges dim d,
+// o = sum_c exp(m_c - m) o_c / sum_c exp(m_c - m) l_c with m the largest m_c,
+// then castF16Rows (a row with no key in its window is 0).
+__global__ __launch_bounds__(kHeadDim) void attn_merge_slices_kernel(const AttnArgs a) {
+  const int qh = blockIdx.x, tok = blockIdx.y, d = threadIdx.x;
+  const int G = a.nq / a.nkv, g = qh / G, h = qh - g * G;
+  const size_t row0 = ((size_t)tok * a.nkv + g) * a.chunks * kAttnMaxGroup + h;  // slice c at row0 + c * 8
+  float m = -__builtin_inff();
+  for (int c = 0; c < a.chunks; c++) m = fmaxf(m, a.part_m[row0 + (size_t)c * kAttnMaxGroup]);
+  float l = 0.0f, o = 0.0f;
+  for (int c = 0; c < a.chunks; c++) {
+    const size_t r = row0 + (size_t)c * kAttnMaxGroup;
+    const float mc = a.part_m[r];
+    const float f = mc == -__builtin_inff() ? 0.0f : expf(mc - m);
+    l = __builtin_fmaf(f, a.part_l[r], l);
+    o = __builtin_fmaf(f, a.part_o[r * kHeadDim + d], o);
+  }
+  a.out[((size_t)tok * a.nq + qh) * kHeadDim + d] = l > 0.0f ? ts_f16_round(o / l) : 0.0f;
 }
 
 }  // namespace
@@ -286,11 +332,14 @@ hipError_t launch_attention_prefill(AttnArgs a, float *partials, int ranges, hip
   a.part_l = partials + slots;
   a.part_o = partials + 2 * slots;
   const int Tq = kPfRows / (a.nq / a.nkv);
-  const dim3 grid((a.tokens + Tq - 1) / Tq, a.nkv, ranges);
-  hipLaunchKernelGGL(attn_prefill_kernel, grid, dim3(256), 0, s, a);
+  const int blocks = (a.tokens + Tq - 1) / Tq;
+  const int items = blocks * a.nkv * ranges;
+  const int per_xcd = (items + kXcds - 1) / kXcds;
+  hipLaunchKernelGGL(attn_prefill_kernel, dim3(per_xcd * kXcds), dim3(256), 0, s, a, blocks, items);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
-  return launch_attention_merge(a, s);
+  hipLaunchKernelGGL(attn_merge_slices_kernel, dim3(a.nq, a.tokens), dim3(kHeadDim), 0, s, a);
+  return hipGetLastError();
 }
 
 }  // namespace hp
