@@ -108,6 +108,9 @@ def matvec_kernel_name(choice: str, k: int, m: int, specs: list) -> str:
     r6 = 64 // s
     tiles = sum((r + r6 - 1) // r6 for r in rows)
     tiles16 = sum((r + 15) // 16 for r in rows)
+    wide = m <= 4 and type_id in (1, 3) and (choice == "wide" or (choice == "auto" and m == 1 and nb >= 40))
+    if wide:
+        return f"kquant_wide_kernel<{m}, {type_id}>"
     half = s <= 32 and m <= 4 and (choice == "half" or
                                    (choice == "auto" and s <= 16 and tiles <= (2048 if m == 1 else 1024)))
     mfma = choice == "mfma" or (choice == "auto" and not half and k <= 2560 and
@@ -132,8 +135,9 @@ def parse() -> argparse.Namespace:
     p.add_argument("--no-cpu", action="store_true")
     p.add_argument("--no-decode", action="store_true",
                    help="leave the decode-step object out of the default line")
-    p.add_argument("--kernel", choices=["auto", "valu", "mfma", "half"], default="auto",
-                   help="matvec kernel: automatic choice, vector ALU, matrix cores, half-split vector ALU")
+    p.add_argument("--kernel", choices=["auto", "valu", "mfma", "half", "wide"], default="auto",
+                   help="matvec kernel: automatic choice, vector ALU, matrix cores, half-split vector ALU, "
+                        "wide (one workgroup per block of rows)")
     p.add_argument("--copy-probe", action="store_true",
                    help="only run a plain 256 MiB device copy (HBM counter calibration) and exit")
     return p.parse_args()
@@ -259,7 +263,7 @@ def decode_chain(args) -> int:
     if args.m != 1:
         raise SystemExit("decode42 runs at M = 1")
     H.setMatvecKernel({"auto": H.MATVEC_AUTO, "valu": H.MATVEC_VALU, "mfma": H.MATVEC_MFMA,
-                       "half": H.MATVEC_HALF}[args.kernel])
+                       "half": H.MATVEC_HALF, "wide": H.MATVEC_WIDE}[args.kernel])
     torch.cuda.init()
     dev = torch.device("cuda:0")
     seed = S.config_seed(5)
@@ -549,7 +553,7 @@ def prefill_chain(args) -> int:
 
     m = args.m if args.m > 1 else 512
     H.setMatvecKernel({"auto": H.MATVEC_AUTO, "valu": H.MATVEC_VALU, "mfma": H.MATVEC_MFMA,
-                       "half": H.MATVEC_HALF}[args.kernel])
+                       "half": H.MATVEC_HALF, "wide": H.MATVEC_WIDE}[args.kernel])
     torch.cuda.init()
     dev = torch.device("cuda:0")
     seed = S.config_seed(5)
@@ -863,7 +867,7 @@ def main() -> int:
     if not support["available"]:
         raise SystemExit(f"HIP runner unavailable: {support}")
     H.setMatvecKernel({"auto": H.MATVEC_AUTO, "valu": H.MATVEC_VALU, "mfma": H.MATVEC_MFMA,
-                       "half": H.MATVEC_HALF}[args.kernel])
+                       "half": H.MATVEC_HALF, "wide": H.MATVEC_WIDE}[args.kernel])
     torch.cuda.init()
     dev = torch.device("cuda:0")
     wl, m = args.workload, args.m

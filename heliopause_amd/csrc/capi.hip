@@ -317,6 +317,38 @@ bool use_half(int cols, const TileGeom &g, int tiles) {
   return tiles <= (cols == 1 ? 2048 : 1024);
 }
 
+// Wide kernel (kquant_wide.hip): one workgroup per block of rows, every
+// block of each row, products chained in LDS.  Needs one weight type (Q4_K or
+// Q6_K) across the launch, at most four columns, no norm prologue and its LDS
+// within the device limit.  Automatic for one column of long rows (40 blocks
+// and more: the FFN down projection), where the one-wave-per-tile kernel
+// leaves most SIMDs idle; selector 6 forces it wherever it applies.
+int wide_rows_for(int rows, int nb, int cols, int type) {
+  const State &s = st();
+  int r = (rows + s.num_cus - 1) / s.num_cus;
+  while (r > 1 && wide_lds_bytes(cols, nb, type, r) > s.max_lds) r = (r + 1) / 2;
+  return r;
+}
+
+bool use_wide(size_t count, Handle *const *hs, size_t cols) {
+  const State &s = st();
+  const int forced = s.matvec_kernel;
+  if (cols < 1 || cols > 4 || (forced != 0 && forced != 6)) return false;
+  const int type = hs[0]->type;
+  if (type != kTypeQ4K && type != kTypeQ6K) return false;
+  size_t rows = 0;
+  for (size_t i = 0; i < count; i++) {
+    if (hs[i]->type != type) return false;
+    rows += hs[i]->row_count;
+  }
+  const int nb = hs[0]->g.nb;
+  if (nb > 256 || rows >= (1u << 20)) return false;  // div_magic's exact range
+  if (wide_lds_bytes((int)cols, nb, type, wide_rows_for((int)rows, nb, (int)cols, type)) > s.max_lds)
+    return false;
+  if (forced == 6) return true;
+  return cols == 1 && nb >= 40;
+}
+
 // One matvec launch per column chunk covering every weight (multi == one
 // launch, lib.rs:300-426); each launch quantises its columns in its prologue.
 int32_t run_norm(const float *y, int rows, int n, const float *w_post, const float *x_res, float scale, float *x_out,
@@ -353,7 +385,8 @@ int32_t run_matvec(size_t count, Handle *const *hs, const float *d_input, size_t
   State &s = st();
   if (cols == 0) return HP_OK;
   const bool image_ok = s.images && cols >= 2 && image_input_ok(count, hs, cols);
-  if (norm && !norm_prologue_ok(count, hs, cols)) {
+  const bool wide = prefill_kind(cols) == 0 && use_wide(count, hs, cols);
+  if (norm && (wide || !norm_prologue_ok(count, hs, cols))) {
     uint8_t *img = image_ok && img_scratch ? img_scratch : nullptr;
     int32_t rc = run_norm(norm->y, (int)cols, (int)input_size, norm->w_post, norm->mode == 2 ? norm->x_res : nullptr,
                           norm->scale, norm->x_out, norm->w_next, norm_scratch, norm->eps, stream, img);
@@ -415,6 +448,22 @@ int32_t run_matvec(size_t count, Handle *const *hs, const float *d_input, size_t
     }
     prof_end(HP_KERNEL_MATVEC, e1, stream);
     s.launches += kind == 2 ? prefill_fast_launches(l, s.num_cus) : 2;
+    s.matmul_calls++;
+    return HP_OK;
+  }
+  if (wide) {
+    a.wide_rows = wide_rows_for(rows_all, g.nb, (int)cols, hs[0]->type);
+    a.mg_nb = div_magic(g.nb);
+    a.mg_S = div_magic(g.S);
+    a.mg_R = div_magic(g.R);
+    a.x = d_input;
+    a.cols = (int)cols;
+    a.out_col0 = 0;
+    a.q8img = q8img_in;
+    hipEvent_t e1 = prof_begin(stream);
+    HP_HIP_TRY(launch_matvec_wide(a, stream));
+    prof_end(HP_KERNEL_MATVEC, e1, stream);
+    s.launches++;
     s.matmul_calls++;
     return HP_OK;
   }
@@ -1534,7 +1583,7 @@ int32_t hp_hip_quantize_q8_k(const float *input, size_t input_len, size_t input_
 int32_t hp_hip_set_matvec_kernel(int32_t which) {
   State &s = st();
   std::lock_guard<std::recursive_mutex> lock(s.mu);
-  if (which < 0 || which > 5) return fail(HP_ERR_ARG, "kernel selector must be 0..5");
+  if (which < 0 || which > 6) return fail(HP_ERR_ARG, "kernel selector must be 0..6");
   s.matvec_kernel = which;
   return HP_OK;
 }

@@ -102,7 +102,14 @@ struct MatvecArgs {
   // as the LDS image of this launch's columns (q8_image_bytes(cols, nb)),
   // copied in place of the Q8_K prologue
   const uint8_t *q8img;
+  int wide_rows;      // wide kernel: launch rows per workgroup
+  // wide kernel: div_magic of nb, g.S and g.R (x / d as one high multiply)
+  uint32_t mg_nb, mg_S, mg_R;
 };
+
+// x / d for 0 <= x < 2^20 as __umulhi(x, div_magic(d)) (0 for d = 1: x);
+// exact for 1 <= d <= 256 (checked exhaustively).
+__host__ __device__ constexpr uint32_t div_magic(int d) { return d <= 1 ? 0u : 0xFFFFFFFFu / (uint32_t)d + 1u; }
 
 // The vector-ALU matvec's LDS image of `cols` quantised input columns: the
 // cols * nb Q8_K blocks (kQ8BlockBytes each, column-major) and then their
@@ -121,6 +128,12 @@ hipError_t launch_matvec_half(const MatvecArgs &a, int num_cus, hipStream_t s);
 // Gate/up + GeGLU in one vector-ALU launch (count == 2, equal rows, cols <= 4):
 // a.pair_out[m][r] = fround(gelu(gate) * up).
 hipError_t launch_matvec_pair(const MatvecArgs &a, int num_cus, hipStream_t s);
+// Wide kernel: one workgroup per a.wide_rows launch rows (every block of
+// each row), products in LDS, block-order chains per (row, lane class).
+// Uniform Q4_K or Q6_K weights, 1..4 columns, no norm prologue.
+size_t wide_lds_bytes(int cols, int nb, int type, int rows_per_wg);
+int wide_threads(int cols, int nb, int rows_per_wg);
+hipError_t launch_matvec_wide(const MatvecArgs &a, hipStream_t s);
 hipError_t launch_repack(int type, const uint8_t *raw, int rows, const TileGeom &g, uint8_t *tiles,
                          uint16_t *dplane, hipStream_t s);
 // Top-k (k <= kTopkMaxK) of each of `rows` (<= kTopkMaxRows) rows of n

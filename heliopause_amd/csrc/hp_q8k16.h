@@ -88,28 +88,63 @@ __device__ __forceinline__ int q8k_round(float inv, float x) {
   return (int)fmaxf(fminf(__fadd_rn(p, copysignf(0.49999997f, p)), 127.0f), -128.0f);
 }
 
-__device__ __forceinline__ void q8k_block16(const float (&v)[16], int i16, uint8_t *blk, float *dptr) {
-  const int j = i16 >> 1, u = i16 & 1;
-  bool nz;
-  const float inv = q8k_inv16(v, i16, nz);
+// The quantised block as one 16-lane row holds it: lane i16 = 2j + u owns
+// dwords 8j + 4u .. 8j + 4u + 3 of the transposed layout (word[l4]: element
+// 32j + 8c + 4u + l4 in byte c), sum: the sum of sub-block j's 32 quants
+// (the image's bsums), in both lanes of the pair; inv: -127 / (the block's first
+// element of largest |x|); nz: some element is not zero (else every quant
+// is 0).
+struct Q8Words {
   uint32_t word[4];
+  int sum;
+  float inv;
+  bool nz;
+};
+
+__device__ __forceinline__ Q8Words q8k_words16(const float (&v)[16], int i16) {
+  Q8Words r;
+  r.inv = q8k_inv16(v, i16, r.nz);
   int sum = 0;
 #pragma unroll
   for (int l4 = 0; l4 < 4; l4++) {
     int q[4];
 #pragma unroll
-    for (int c = 0; c < 4; c++) q[c] = q8k_round(inv, v[4 * c + l4]);
+    for (int c = 0; c < 4; c++) q[c] = q8k_round(r.inv, v[4 * c + l4]);
     // bytes q0..q3 (low to high): the low bytes of two packed int16 pairs
     const uint32_t lo = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pk_i16(q[0], q[1]));
     const uint32_t hi = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pk_i16(q[2], q[3]));
     const uint32_t wv = __builtin_amdgcn_perm(hi, lo, 0x06040200u);
-    word[l4] = nz ? wv : 0u;  // dword l = 4u + l4 of sub-block j
-    sum = __builtin_amdgcn_sdot4((int)word[l4], 0x01010101, sum, false);
+    r.word[l4] = r.nz ? wv : 0u;  // dword l = 4u + l4 of sub-block j
+    sum = __builtin_amdgcn_sdot4((int)r.word[l4], 0x01010101, sum, false);
   }
-  sum += (int)dpp_u32<kDppXor1>((uint32_t)sum);
-  *reinterpret_cast<uint4 *>(blk + 32 * j + 16 * u) = make_uint4(word[0], word[1], word[2], word[3]);
-  if (u == 0) reinterpret_cast<int16_t *>(blk + 256)[j] = (int16_t)sum;
-  if (i16 == 0) *dptr = nz ? __fdiv_rn(1.0f, inv) : 0.0f;
+  r.sum = sum + (int)dpp_u32<kDppXor1>((uint32_t)sum);
+  return r;
+}
+
+// The 272-byte block (256 quants, 8 sub-block sums) and its f32 scale.
+__device__ __forceinline__ void q8k_store16(const Q8Words &q, int i16, uint8_t *blk, float *dptr) {
+  const int j = i16 >> 1, u = i16 & 1;
+  *reinterpret_cast<uint4 *>(blk + 32 * j + 16 * u) = make_uint4(q.word[0], q.word[1], q.word[2], q.word[3]);
+  if (u == 0) reinterpret_cast<int16_t *>(blk + 256)[j] = (int16_t)q.sum;
+  if (i16 == 0) *dptr = q.nz ? __fdiv_rn(1.0f, q.inv) : 0.0f;
+}
+
+__device__ __forceinline__ void q8k_block16(const float (&v)[16], int i16, uint8_t *blk, float *dptr) {
+  q8k_store16(q8k_words16(v, i16), i16, blk, dptr);
+}
+
+// The block's quants as two masked 256-byte copies in the same order: lo
+// keeps bytes 0, 1 of every dword (c = 0, 1: the first 16-element group of
+// the dword's 32), hi bytes 2, 3 (the second group); and its f32 scale.  The
+// Q6_K kernels' input (q6k_ints_split).
+__device__ __forceinline__ void q8k_store16_split(const Q8Words &q, int i16, uint8_t *lo, uint8_t *hi,
+                                                  float *dptr) {
+  const int j = i16 >> 1, u = i16 & 1;
+  *reinterpret_cast<uint4 *>(lo + 32 * j + 16 * u) =
+      make_uint4(q.word[0] & 0xFFFFu, q.word[1] & 0xFFFFu, q.word[2] & 0xFFFFu, q.word[3] & 0xFFFFu);
+  *reinterpret_cast<uint4 *>(hi + 32 * j + 16 * u) = make_uint4(
+      q.word[0] & 0xFFFF0000u, q.word[1] & 0xFFFF0000u, q.word[2] & 0xFFFF0000u, q.word[3] & 0xFFFF0000u);
+  if (i16 == 0) *dptr = q.nz ? __fdiv_rn(1.0f, q.inv) : 0.0f;
 }
 
 }  // namespace hp

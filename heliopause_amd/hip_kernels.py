@@ -457,7 +457,8 @@ def matmul_multi_device(handles: Sequence[int], d_input: int, input_size: int, c
     assertHipOk(code, "matmulMultiDevice")
 
 
-MATVEC_AUTO, MATVEC_VALU, MATVEC_MFMA, MATVEC_HALF, MATVEC_PREFILL, MATVEC_PREFILL_FAST = 0, 1, 2, 3, 4, 5
+MATVEC_AUTO, MATVEC_VALU, MATVEC_MFMA, MATVEC_HALF, MATVEC_PREFILL, MATVEC_PREFILL_FAST, MATVEC_WIDE = \
+    0, 1, 2, 3, 4, 5, 6
 
 
 def setMatvecKernel(which: int) -> None:

@@ -21,10 +21,12 @@ def _weights(type_name, seed, rows, k):
     return S.weight_blocks(type_name, seed, rows, k)
 
 
-@pytest.fixture(params=[1, 2, 3, 4], ids=["valu", "mfma", "half", "prefill"])
+@pytest.fixture(params=[1, 2, 3, 4, 6], ids=["valu", "mfma", "half", "prefill", "wide"])
 def kernel(request, hip):
-    """Runs the test with the vector-ALU, the matrix-core and the half-split
-    vector-ALU matvec."""
+    """Runs the test with the vector-ALU, the matrix-core, the half-split
+    vector-ALU, the bit-exact prefill and the wide (one workgroup per block of
+    rows) matvec; a launch a forced kernel does not take (the wide kernel:
+    more than four columns, mixed types) runs the automatic choice."""
     hip.setMatvecKernel(request.param)
     yield request.param
     hip.setMatvecKernel(0)
@@ -65,8 +67,10 @@ def test_matmul_bit_exact(hip, oracle, kernel, type_name, rows, k, m):
 
 
 @pytest.mark.parametrize("specs", [[("Q4_K", 96), ("Q4_K", 40), ("Q6_K", 40)],
-                                   [("Q6_K", 97), ("Q4_K", 41), ("Q4_K", 1), ("Q6_K", 8)]],
-                         ids=["qkv", "ragged4"])
+                                   [("Q6_K", 97), ("Q4_K", 41), ("Q4_K", 1), ("Q6_K", 8)],
+                                   [("Q4_K", 301), ("Q4_K", 3), ("Q4_K", 77)],
+                                   [("Q6_K", 5), ("Q6_K", 260), ("Q6_K", 31), ("Q6_K", 2)]],
+                         ids=["qkv", "ragged4", "q4x3", "q6x4"])
 def test_multi_mixed_types_bit_exact(hip, oracle, kernel, specs):
     """Q (Q4_K) + K (Q4_K) + V (Q6_K) in one launch sharing one Q8_K (lib.rs:300-426);
     ragged row counts put rows of two weights (of either type) in one
@@ -110,6 +114,33 @@ def test_special_inputs(hip, oracle, kernel):
             assert np.array_equal(_bits(got), _bits(ref)), type_name
         finally:
             hip.releaseHipQuantizedWeightHandle(h)
+
+
+@pytest.mark.parametrize("type_name", ["Q4_K", "Q6_K"])
+@pytest.mark.parametrize("rows,k", [(2560, 10240), (37, 10240), (700, 2560), (1, 256), (300, 4096)])
+def test_wide_kernel_columns(hip, oracle, type_name, rows, k):
+    """The wide kernel at one to four columns, with the special inputs of
+    test_special_inputs (an all-zero column, first-index |x| ties, a huge
+    spike, denormal scales): one launch per column count, every column
+    compared with the oracle bit for bit."""
+    seed = S.derive(S.BASE_SEED, "wide", type_name, rows, k)
+    w = _weights(type_name, seed, rows, k)
+    x = S.activations(seed, 4, k)
+    x[1, :] = 0.0
+    x[1, 5], x[1, 9], x[1, 300 % k], x[1, 301 % k] = 2.0, -2.0, -3.5, 3.5
+    x[2, k // 3] = 1e30
+    x[3] *= 1e-39
+    h = hip.createHipQuantizedWeightHandle(type_name, w, k, rows)
+    hip.setMatvecKernel(6)
+    try:
+        ref = oracle.matmul(TYPES[type_name], w, x, rows, threads=8)
+        for m in (1, 2, 3, 4):
+            print(f"wide {type_name} rows={rows} k={k} m={m}", flush=True)
+            got = hip.matMulQuantizedHipResident(h, x[:m], k, rows, m).reshape(m, rows)
+            assert np.array_equal(_bits(got), _bits(ref[:m])), m
+    finally:
+        hip.setMatvecKernel(0)
+        hip.releaseHipQuantizedWeightHandle(h)
 
 
 def test_shape_errors(hip):
