@@ -330,6 +330,8 @@ int wide_rows_for(int rows, int nb, int cols, int type) {
   return r;
 }
 
+int g_nb_of(Handle *const *hs) { return hs[0]->g.nb; }
+
 bool use_wide(size_t count, Handle *const *hs, size_t cols) {
   const State &s = st();
   const int forced = s.matvec_kernel;
@@ -347,6 +349,23 @@ bool use_wide(size_t count, Handle *const *hs, size_t cols) {
     return false;
   if (forced == 6) return true;
   return cols == 1 && nb >= 40;
+}
+
+// The wide kernel for gate/up + GeGLU (equal rows, one type): selector 6
+// forces it (one to four columns); automatic for one column.
+bool use_wide_pair(Handle *const *hs, size_t cols) {
+  const State &s = st();
+  const int forced = s.matvec_kernel;
+  if (cols < 1 || cols > 4 || (forced != 0 && forced != 6)) return false;
+  const int type = hs[0]->type;
+  if ((type != kTypeQ4K && type != kTypeQ6K) || hs[1]->type != type || hs[0]->row_count != hs[1]->row_count)
+    return false;
+  const int nb = hs[0]->g.nb;
+  const size_t rows = hs[0]->row_count;
+  if (nb > 256 || 2 * rows >= (1u << 20)) return false;
+  const int r = wide_rows_for((int)(2 * rows), nb, (int)cols, type) / 2;
+  if (r < 1 || wide_lds_bytes((int)cols, nb, type, 2 * r) > s.max_lds) return false;
+  return forced == 6 || cols == 1;
 }
 
 // One matvec launch per column chunk covering every weight (multi == one
@@ -386,7 +405,8 @@ int32_t run_matvec(size_t count, Handle *const *hs, const float *d_input, size_t
   if (cols == 0) return HP_OK;
   const bool image_ok = s.images && cols >= 2 && image_input_ok(count, hs, cols);
   const bool wide = prefill_kind(cols) == 0 && use_wide(count, hs, cols);
-  if (norm && (wide || !norm_prologue_ok(count, hs, cols))) {
+  const bool wide_norm = wide && cols == 1 && g_nb_of(hs) <= 16;  // the wide kernel's norm prologue
+  if (norm && (wide ? !wide_norm : !norm_prologue_ok(count, hs, cols))) {
     uint8_t *img = image_ok && img_scratch ? img_scratch : nullptr;
     int32_t rc = run_norm(norm->y, (int)cols, (int)input_size, norm->w_post, norm->mode == 2 ? norm->x_res : nullptr,
                           norm->scale, norm->x_out, norm->w_next, norm_scratch, norm->eps, stream, img);
@@ -531,14 +551,49 @@ int32_t run_matvec_geglu(Handle *hg, Handle *hu, const float *d_input, size_t in
   const size_t rows = hg->row_count;
   const TileGeom g = hg->g;
   const int tiles16 = 2 * (int)((rows + 15) / 16);
-  const bool fused = cols <= 4 && s.matvec_kernel <= 1 && !use_mfma(cols, g.nb, tiles16) &&
+  Handle *pair[2] = {hg, hu};
+  const bool wide = prefill_kind(cols) == 0 && hg->type == hu->type && use_wide_pair(pair, cols);
+  const bool fused = !wide && cols <= 4 && s.matvec_kernel <= 1 && !use_mfma(cols, g.nb, tiles16) &&
                      !use_half((int)cols, g, 2 * hg->tiles) && cols_per_launch(g, s.max_lds) >= (int)cols;
-  if (norm && !(fused && cols == 1 && g.nb <= 16)) {
+  if (norm && !((fused || wide) && cols == 1 && g.nb <= 16)) {
     int32_t rc = run_norm(norm->y, (int)cols, (int)input_size, norm->w_post, norm->mode == 2 ? norm->x_res : nullptr,
                           norm->scale, norm->x_out, norm->w_next, norm_scratch, norm->eps, stream);
     if (rc != HP_OK) return rc;
     d_input = norm_scratch;
     norm = nullptr;
+  }
+  if (wide) {
+    MatvecArgs a{};
+    if (norm) a.norm = *norm;
+    a.count = 2;
+    a.g = g;
+    a.k = (int)input_size;
+    for (int i = 0; i < 2; i++) {
+      a.w[i].data = pair[i]->data;
+      a.w[i].dplane = pair[i]->dplane;
+      a.w[i].out = nullptr;
+      a.w[i].type = pair[i]->type;
+      a.w[i].rows = (int)rows;
+      a.w[i].tiles = pair[i]->tiles;
+      a.w[i].row_begin = i * (int)rows;
+    }
+    a.total_rows = (int)rows;
+    a.wide_rows = wide_rows_for((int)(2 * rows), g.nb, (int)cols, hg->type) / 2;
+    if (a.wide_rows < 1) a.wide_rows = 1;
+    a.mg_nb = div_magic(g.nb);
+    a.mg_S = div_magic(g.S);
+    a.mg_R = div_magic(g.R);
+    a.x = d_input;
+    a.cols = (int)cols;
+    a.out_col0 = 0;
+    a.pair_out = d_out;
+    a.gelu_c = gelu_constant();
+    hipEvent_t e1 = prof_begin(stream);
+    HP_HIP_TRY(launch_matvec_wide(a, stream));
+    prof_end(HP_KERNEL_MATVEC, e1, stream);
+    s.launches++;
+    s.matmul_calls++;
+    return HP_OK;
   }
   if (fused) {
     MatvecArgs a{};

@@ -102,7 +102,8 @@ struct MatvecArgs {
   // as the LDS image of this launch's columns (q8_image_bytes(cols, nb)),
   // copied in place of the Q8_K prologue
   const uint8_t *q8img;
-  int wide_rows;      // wide kernel: launch rows per workgroup
+  int wide_rows;      // wide kernel: launch rows per workgroup (with pair_out:
+                      // rows of each of gate and up)
   // wide kernel: div_magic of nb, g.S and g.R (x / d as one high multiply)
   uint32_t mg_nb, mg_S, mg_R;
 };
@@ -130,7 +131,8 @@ hipError_t launch_matvec_half(const MatvecArgs &a, int num_cus, hipStream_t s);
 hipError_t launch_matvec_pair(const MatvecArgs &a, int num_cus, hipStream_t s);
 // Wide kernel: one workgroup per a.wide_rows launch rows (every block of
 // each row), products in LDS, block-order chains per (row, lane class).
-// Uniform Q4_K or Q6_K weights, 1..4 columns, no norm prologue.
+// Uniform Q4_K or Q6_K weights, 1..4 columns; the norm prologue (one column,
+// nb <= 16); with a.pair_out, gate/up + GeGLU (a.wide_rows rows of each).
 size_t wide_lds_bytes(int cols, int nb, int type, int rows_per_wg);
 int wide_threads(int cols, int nb, int rows_per_wg);
 hipError_t launch_matvec_wide(const MatvecArgs &a, hipStream_t s);

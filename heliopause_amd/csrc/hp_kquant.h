@@ -239,11 +239,14 @@ __device__ __forceinline__ void norm_load(const NormIn &n, NormRegs &nr, int grp
   load_x16(nr.wn, n.w_next + off, i16);
 }
 
-// Sum over the workgroup's four waves; sh (4 doubles) must not have been
-// used by an earlier call in the kernel (no barrier guards its reuse).
+// Sum over the workgroup's first four waves (the 16 groups a norm prologue
+// uses; waves past them, in workgroups of more than four, hold none), the
+// same order at any workgroup size; sh (4 doubles) must not have been used by
+// an earlier call in the kernel (no barrier guards its reuse).  Every thread
+// of the workgroup must call it.
 __device__ __forceinline__ double wg_sum_f64(double v, double *sh) {
   v = wave_sum_f64(v);
-  if ((threadIdx.x & 63) == 0) sh[threadIdx.x >> 6] = v;
+  if ((threadIdx.x & 63) == 0 && threadIdx.x < 256) sh[threadIdx.x >> 6] = v;
   __syncthreads();
   return (sh[0] + sh[1]) + (sh[2] + sh[3]);
 }

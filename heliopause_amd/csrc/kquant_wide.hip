@@ -29,6 +29,7 @@
 // (q8k_store16_split, q6k_ints_split), which saves masking the weights.  From
 // two columns the input may come already quantised (a.q8img).
 #include "hp_common.h"
+#include "hp_gelu.h"
 #include "hp_kquant.h"
 #include "hp_q8k16.h"
 #include "hp_wave.h"
@@ -76,7 +77,14 @@ __host__ __device__ inline WideLayout wide_layout(int cols, int nb, int type, in
   return L;
 }
 
-__device__ __forceinline__ int mdiv(int x, uint32_t m) { return m ? (int)__umulhi((uint32_t)x, m) : x; }
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+
+// No branch (a divisor of 1 adds x back): a branch between loads would split
+// the loaded registers' live ranges and make the compiler wait for them.
+__device__ __forceinline__ int mdiv(int x, uint32_t m) {
+  const uint32_t keep = 0u - (uint32_t)(m == 0u);
+  return (int)(__umulhi((uint32_t)x, m) + ((uint32_t)x & keep));
+}
 
 // One (row, block) task's addresses in the tile layout.
 struct WideTask {
@@ -85,17 +93,22 @@ struct WideTask {
   const uint16_t *d6;  // Q6_K: f16 d of this row-block
 };
 
-template <int TYPE>
-__device__ __forceinline__ WideTask wide_task(const MatvecArgs &a, int lrow, int b) {
-  constexpr int CH = TYPE == kTypeQ4K ? 9 : 13;
-  const int nb = a.g.nb, S = a.g.S, RG = a.g.R;
+// Launch row lrow of the launch's weights end to end, or with PAIR virtual
+// row vr of the workgroup (gate rows, then the same rows of up).
+__device__ __forceinline__ WeightDesc weight_of(const MatvecArgs &a, int lrow) {
   WeightDesc W = a.w[0];
   if (a.count > 1) {  // wave-uniform: single-weight launches skip the selects
     if (lrow >= a.w[1].row_begin) W = a.w[1];
     if (a.count > 2 && lrow >= a.w[2].row_begin) W = a.w[2];
     if (a.count > 3 && lrow >= a.w[3].row_begin) W = a.w[3];
   }
-  const int row = lrow - W.row_begin;
+  return W;
+}
+
+template <int TYPE>
+__device__ __forceinline__ WideTask wide_task(const MatvecArgs &a, const WeightDesc &W, int row, int b) {
+  constexpr int CH = TYPE == kTypeQ4K ? 9 : 13;
+  const int nb = a.g.nb, S = a.g.S, RG = a.g.R;
   const int tile = mdiv(row, a.mg_R);
   const int r = row - tile * RG;
   const int Rt = min(RG, W.rows - tile * RG);
@@ -110,6 +123,18 @@ __device__ __forceinline__ WideTask wide_task(const MatvecArgs &a, int lrow, int
   return t;
 }
 
+// Task (vr, b) of the workgroup whose first row is row0 (VRh: its rows of
+// each weight with PAIR).
+template <int TYPE, bool PAIR>
+__device__ __forceinline__ WideTask task_at(const MatvecArgs &a, int row0, int VRh, int vr, int b) {
+  if (PAIR) {
+    const bool up = vr >= VRh;
+    return wide_task<TYPE>(a, up ? a.w[1] : a.w[0], row0 + vr - (up ? VRh : 0), b);
+  }
+  const WeightDesc W = weight_of(a, row0 + vr);
+  return wide_task<TYPE>(a, W, row0 + vr - W.row_begin, b);
+}
+
 template <int TYPE>
 __device__ __forceinline__ void wide_load(Regs &rg, const WideTask &t) {
   constexpr int CH = TYPE == kTypeQ4K ? 9 : 13;
@@ -118,9 +143,65 @@ __device__ __forceinline__ void wide_load(Regs &rg, const WideTask &t) {
   if (TYPE == kTypeQ6K) rg.d6 = *t.d6;
 }
 
+// The norm prologue's finish (hp_kquant.h norm_finish: the same arithmetic
+// in the same order, so the same bits) where only the waves that hold one of
+// the input's blocks do the math: with eight waves and a 10-block input,
+// five would otherwise repeat it on zeros.  `active`: this wave holds a
+// group below nb (wave-uniform).  Of the first four waves an inactive one
+// contributes +0.0 to the two sums, as its zeroed lanes would.  Every thread
+// of the workgroup calls it (two barriers).
+template <int MODE>
+__device__ __forceinline__ void wide_norm_finish(const NormIn &n, NormRegs &nr, float (&xv)[16], int grp, int nb,
+                                                 int i16, int k, double *sh, bool active) {
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  double part = 0.0;
+  if (active) {
+    if (grp >= nb) {
+#pragma unroll
+      for (int i = 0; i < 16; i++) nr.y[i] = nr.r[i] = 0.0f;
+    }
+    double ss = 0.0;
+#pragma unroll
+    for (int i = 0; i < 16; i++) ss += (double)nr.y[i] * (double)nr.y[i];
+    part = wave_sum_f64(ss);
+  }
+  if (lane == 0 && wave < 4) sh[wave] = part;
+  __syncthreads();
+  double sc = 1.0 / sqrt(((sh[0] + sh[1]) + (sh[2] + sh[3])) / (double)k + n.eps);
+  if (MODE == 2) {
+    part = 0.0;
+    if (active) {
+      double ss = 0.0;
+#pragma unroll
+      for (int i = 0; i < 16; i++) {
+        const float t = (float)(((double)nr.y[i] * sc) * (double)nr.wp[i]);
+        const float x1 = (nr.r[i] + t) * n.scale;
+        nr.y[i] = x1;
+        ss += (double)x1 * (double)x1;
+      }
+      if (blockIdx.x == 0 && grp < nb) store_x16(n.x_out + (size_t)grp * kQK, nr.y, i16);
+      part = wave_sum_f64(ss);
+    }
+    if (lane == 0 && wave < 4) sh[4 + wave] = part;
+    __syncthreads();
+    sc = 1.0 / sqrt(((sh[4] + sh[5]) + (sh[6] + sh[7])) / (double)k + n.eps);
+  }
+  if (active) {
+#pragma unroll
+    for (int i = 0; i < 16; i++) xv[i] = (float)(((double)nr.y[i] * sc) * (double)nr.wn[i]);
+  }
+}
+
 }  // namespace
 
-template <int M, int TYPE>
+// NORM (1, 2; one column, nb <= 16): the input formed from a residual stream
+// in the prologue (NormIn), by the first four waves.  PAIR: weights 0 and 1
+// are gate and up with equal rows; the workgroup takes the same rows of both
+// and writes fround(gelu(gate) * up) to a.pair_out (layers.ts:435-456).
+// TPL (1, 2): tasks per thread whose loads are issued before the prologue
+// (the launch's tasks per workgroup fit TPL * blockDim.x; more run after,
+// their loads waited for one at a time).
+template <int M, int TYPE, int NORM, bool PAIR, int TPL>
 __global__ __launch_bounds__(kWideMaxThreads) void kquant_wide_kernel(const MatvecArgs a) {
   extern __shared__ __align__(16) uint8_t smem[];
   constexpr bool Q4 = TYPE == kTypeQ4K;
@@ -128,8 +209,9 @@ __global__ __launch_bounds__(kWideMaxThreads) void kquant_wide_kernel(const Matv
   const int nb = a.g.nb;
   const int R = a.wide_rows;
   const int row0 = blockIdx.x * R;
-  const int VR = min(R, a.total_rows - row0);
-  const WideLayout L = wide_layout(M, nb, TYPE, R);
+  const int VRh = min(R, (PAIR ? a.w[0].rows : a.total_rows) - row0);  // rows of each weight (PAIR)
+  const int VR = PAIR ? 2 * VRh : VRh;
+  const WideLayout L = wide_layout(M, nb, TYPE, PAIR ? 2 * R : R);
   uint8_t *xq = smem;  // Q4_K: the image; Q6_K: the lower-half copies
   uint8_t *xhi = smem + L.xhi;
   float *xd = reinterpret_cast<float *>(smem + L.xd);
@@ -150,7 +232,15 @@ __global__ __launch_bounds__(kWideMaxThreads) void kquant_wide_kernel(const Matv
   // group past the end re-reads the last block): with no branch around these
   // loads the waits for them count exactly and never wait for the weights
   float xv[16], xv2[16];
-  if (!pre) {
+  __shared__ double norm_sh[8];  // two workgroup sums
+  NormRegs nr;
+  if (NORM) {
+    // the norm's 16 groups (nb <= 16) are in the first four waves; every
+    // wave loads (groups past nb re-read block nb - 1 and wide_norm_finish zeroes
+    // them): a branch around these loads lets the compiler wait for them
+    // before the weight loads are issued
+    norm_load<NORM>(a.norm, nr, grp, nb, i16);
+  } else if (!pre) {
     load_x16(xv, x_block(min(grp, nq - 1)), i16);
     load_x16(xv2, x_block(min(grp + ngrp, nq - 1)), i16);
   }
@@ -164,15 +254,28 @@ __global__ __launch_bounds__(kWideMaxThreads) void kquant_wide_kernel(const Matv
     for (int i = 0; i < kImgRegs; i++) iv[i] = img[min(tid + i * nthr, n16 - 1)];
   }
 
-  // an idle thread loads the workgroup's last task: no branch around the loads
-  int t = tid;
-  Regs cur;
-  {
-    const int te = min(t, ntask - 1);
+  // the first TPL tasks' weights; a thread past the end loads the
+  // workgroup's last task: no branch around the loads
+  // (every address first: no branch between the loads)
+  WideTask tk[TPL];
+#pragma unroll
+  for (int i = 0; i < TPL; i++) {
+    const int te = min(tid + i * nthr, ntask - 1);
     const int vr = mdiv(te, a.mg_nb);
-    wide_load<TYPE>(cur, wide_task<TYPE>(a, row0 + vr, te - vr * nb));
+    tk[i] = task_at<TYPE, PAIR>(a, row0, VRh, vr, te - vr * nb);
   }
+  Regs rg[TPL];
+#pragma unroll
+  for (int i = 0; i < TPL; i++) wide_load<TYPE>(rg[i], tk[i]);
+  // keep the loads here: without a memory barrier the compiler may sink them
+  // past the prologue to their first use (a machine scheduling barrier does
+  // not stop that); the barrier reads none of the loaded registers, so it
+  // waits for nothing
+  asm volatile("" ::: "memory");
   __builtin_amdgcn_sched_barrier(0);
+  if (NORM)
+    wide_norm_finish<NORM>(a.norm, nr, xv, grp, nb, i16, a.k, norm_sh,
+                           4 * __builtin_amdgcn_readfirstlane(tid >> 6) < nb);
 
   if (pre) {
     // the image into LDS: Q4_K as it is (the same layout), Q6_K as the two
@@ -205,7 +308,7 @@ __global__ __launch_bounds__(kWideMaxThreads) void kquant_wide_kernel(const Matv
         q8k_store16_split(w, i16, xq + (size_t)q * kSplitStride, xhi + (size_t)q * kSplitStride, xd + q);
     };
     auto quant = [&](const float (&v)[16], int q) { put_words(q8k_words16(v, i16), q); };
-    if (grp + ngrp < nq) {
+    if (!NORM && grp + ngrp < nq) {
       // two blocks: their two dependency chains interleave
       const Q8Words q0 = q8k_words16(xv, i16), q1 = q8k_words16(xv2, i16);
       put_words(q0, grp);
@@ -213,7 +316,7 @@ __global__ __launch_bounds__(kWideMaxThreads) void kquant_wide_kernel(const Matv
     } else if (grp < nq) {
       put_words(q8k_words16(xv, i16), grp);
     }
-    for (int q = grp + 2 * ngrp; q < nq; q += ngrp) {  // more than two passes (several columns)
+    for (int q = grp + 2 * ngrp; !NORM && q < nq; q += ngrp) {  // more than two passes (several columns)
       load_x16(xv, x_block(q), i16);
       quant(xv, q);
     }
@@ -221,17 +324,14 @@ __global__ __launch_bounds__(kWideMaxThreads) void kquant_wide_kernel(const Matv
   __syncthreads();
 
   // phase 1: products
-  for (; t < ntask; t += nthr) {
+  // a thread past the end computes the clamped task's products and stores
+  // none (no branch around the work: branches split the loaded registers'
+  // live ranges, and the copies that follow wait for the loads)
+  auto products = [&](const Regs &cur, int t_in) {
+    const bool live = t_in < ntask;
+    const int t = min(t_in, ntask - 1);
     const int vr = mdiv(t, a.mg_nb);
     const int b = t - vr * nb;
-    Regs nxt;
-    const int tn = t + nthr;
-    const bool more = tn < ntask;
-    if (more) {
-      const int vn = mdiv(tn, a.mg_nb);
-      wide_load<TYPE>(nxt, wide_task<TYPE>(a, row0 + vn, tn - vn * nb));
-    }
-    __builtin_amdgcn_sched_barrier(0);
     int aux[M][8];
     int sumi[M];
     float dw, dminw = 0.0f;
@@ -248,12 +348,37 @@ __global__ __launch_bounds__(kWideMaxThreads) void kquant_wide_kernel(const Matv
       const float dx = xd[m * nb + b];
       const float dd = __fmul_rn(dw, dx);
       float *pr = prod + ((size_t)(vr * M + m) * NC) * L.nbp + b;
+      float p[9];
 #pragma unroll
-      for (int l = 0; l < 8; l++) pr[l * L.nbp] = __fmul_rn(dd, (float)aux[m][l]);
+      for (int l = 0; l < 8; l++) p[l] = __fmul_rn(dd, (float)aux[m][l]);
       // class 8 (Q4_K sumf -= ...) stored negated: s - p == s + (-p) in IEEE
-      if (Q4) pr[8 * L.nbp] = -__fmul_rn(__fmul_rn(dminw, dx), (float)sumi[m]);
+      p[8] = Q4 ? -__fmul_rn(__fmul_rn(dminw, dx), (float)sumi[m]) : 0.0f;
+      if (live) {
+#pragma unroll
+        for (int l = 0; l < NC; l++) pr[l * L.nbp] = p[l];
+      }
     }
-    if (more) cur = nxt;
+  };
+  // each task's chunks used whole here (no instruction): the register
+  // allocator then keeps every loaded tuple intact up to this point instead
+  // of copying parts of one right after its load, a copy that would wait for
+  // the load during the prologue
+#pragma unroll
+  for (int i = 0; i < TPL; i++) {
+#pragma unroll
+    for (int c = 0; c < (Q4 ? 9 : 13); c++) {
+      u32x4 v = __builtin_bit_cast(u32x4, rg[i].c[c]);
+      asm volatile("" : "+v"(v));
+      rg[i].c[c] = __builtin_bit_cast(uint4, v);
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < TPL; i++) products(rg[i], tid + i * nthr);
+  for (int t = tid + TPL * nthr; t < ntask; t += nthr) {
+    const int vr = mdiv(t, a.mg_nb);
+    Regs more;
+    wide_load<TYPE>(more, task_at<TYPE, PAIR>(a, row0, VRh, vr, t - vr * nb));
+    products(more, t);
   }
   __syncthreads();
 
@@ -275,21 +400,22 @@ __global__ __launch_bounds__(kWideMaxThreads) void kquant_wide_kernel(const Matv
   __syncthreads();
 
   // phase 3: result = [sumf +] ((((-0 + s0) + s1) + ...) + s7)
-  for (int u = tid; u < VR * M; u += nthr) {
-    const int vr = u / M, m = u - vr * M;
-    const float *f = fin + (size_t)u * NC;
+  auto tail = [&](int vr, int m) {
+    const float *f = fin + (size_t)(vr * M + m) * NC;
     float tsum = -0.0f;
 #pragma unroll
     for (int l = 0; l < 8; l++) tsum = __fadd_rn(tsum, f[l]);
-    const float res = Q4 ? __fadd_rn(f[8], tsum) : tsum;
-    const int lrow = row0 + vr;
-    WeightDesc W = a.w[0];
-    if (a.count > 1) {
-      if (lrow >= a.w[1].row_begin) W = a.w[1];
-      if (a.count > 2 && lrow >= a.w[2].row_begin) W = a.w[2];
-      if (a.count > 3 && lrow >= a.w[3].row_begin) W = a.w[3];
+    return Q4 ? __fadd_rn(f[8], tsum) : tsum;
+  };
+  for (int u = tid; u < VRh * M; u += nthr) {
+    const int vr = u / M, m = u - vr * M;
+    if (PAIR) {
+      a.pair_out[(size_t)(a.out_col0 + m) * a.w[0].rows + row0 + vr] =
+          geglu_ts(tail(vr, m), tail(VRh + vr, m), a.gelu_c);
+    } else {
+      const WeightDesc W = weight_of(a, row0 + vr);
+      W.out[(size_t)(a.out_col0 + m) * W.rows + (row0 + vr - W.row_begin)] = tail(vr, m);
     }
-    W.out[(size_t)(a.out_col0 + m) * W.rows + (lrow - W.row_begin)] = res;
   }
 }
 
@@ -308,33 +434,65 @@ int wide_threads(int cols, int nb, int rows_per_wg) {
   return n < kWideMaxThreads ? n : kWideMaxThreads;
 }
 
-template <int M>
+template <int M, int NORM, bool PAIR>
+static void launch_wide_t(const MatvecArgs &a, int type, dim3 grid, dim3 block, size_t lds, hipStream_t s) {
+  const int vrows = PAIR ? 2 * a.wide_rows : a.wide_rows;
+  const bool two = vrows * a.g.nb > (int)block.x;
+  if (type == kTypeQ4K) {
+    if (two)
+      hipLaunchKernelGGL((kquant_wide_kernel<M, kTypeQ4K, NORM, PAIR, 2>), grid, block, lds, s, a);
+    else
+      hipLaunchKernelGGL((kquant_wide_kernel<M, kTypeQ4K, NORM, PAIR, 1>), grid, block, lds, s, a);
+  } else {
+    if (two)
+      hipLaunchKernelGGL((kquant_wide_kernel<M, kTypeQ6K, NORM, PAIR, 2>), grid, block, lds, s, a);
+    else
+      hipLaunchKernelGGL((kquant_wide_kernel<M, kTypeQ6K, NORM, PAIR, 1>), grid, block, lds, s, a);
+  }
+}
+
+template <int M, bool PAIR>
 static void launch_wide_m(const MatvecArgs &a, int type, dim3 grid, dim3 block, size_t lds, hipStream_t s) {
-  if (type == kTypeQ4K)
-    hipLaunchKernelGGL((kquant_wide_kernel<M, kTypeQ4K>), grid, block, lds, s, a);
+  if (M == 1 && a.norm.mode == 1)
+    launch_wide_t<1, 1, PAIR>(a, type, grid, block, lds, s);
+  else if (M == 1 && a.norm.mode == 2)
+    launch_wide_t<1, 2, PAIR>(a, type, grid, block, lds, s);
   else
-    hipLaunchKernelGGL((kquant_wide_kernel<M, kTypeQ6K>), grid, block, lds, s, a);
+    launch_wide_t<M, 0, PAIR>(a, type, grid, block, lds, s);
+}
+
+template <bool PAIR>
+static hipError_t launch_wide_pair(const MatvecArgs &a, int type, dim3 grid, dim3 block, size_t lds, hipStream_t s) {
+  switch (a.cols) {
+    case 1: launch_wide_m<1, PAIR>(a, type, grid, block, lds, s); break;
+    case 2: launch_wide_m<2, PAIR>(a, type, grid, block, lds, s); break;
+    case 3: launch_wide_m<3, PAIR>(a, type, grid, block, lds, s); break;
+    case 4: launch_wide_m<4, PAIR>(a, type, grid, block, lds, s); break;
+    default: return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
 }
 
 hipError_t launch_matvec_wide(const MatvecArgs &a, hipStream_t s) {
-  if (a.count < 1 || a.count > kMaxWeights || a.wide_rows < 1 || a.total_rows < 1 || a.norm.mode != 0)
+  const bool pair = a.pair_out != nullptr;
+  if (a.count < 1 || a.count > kMaxWeights || a.wide_rows < 1 || a.total_rows < 1) return hipErrorInvalidValue;
+  if (a.norm.mode < 0 || a.norm.mode > 2 || (a.norm.mode != 0 && (a.cols != 1 || a.g.nb > 16)))
     return hipErrorInvalidValue;
-  if (a.q8img && a.cols < 2) return hipErrorInvalidValue;
+  if (a.q8img && (a.cols < 2 || a.norm.mode != 0)) return hipErrorInvalidValue;
+  if (pair && (a.count != 2 || a.w[0].rows != a.w[1].rows)) return hipErrorInvalidValue;
   const int type = a.w[0].type;
   if (type != kTypeQ4K && type != kTypeQ6K) return hipErrorInvalidValue;
   for (int i = 1; i < a.count; i++)
     if (a.w[i].type != type) return hipErrorInvalidValue;
-  const int grid = (a.total_rows + a.wide_rows - 1) / a.wide_rows;
-  const dim3 block(wide_threads(a.cols, a.g.nb, a.wide_rows));
-  const size_t lds = wide_lds_bytes(a.cols, a.g.nb, type, a.wide_rows);
-  switch (a.cols) {
-    case 1: launch_wide_m<1>(a, type, dim3(grid), block, lds, s); break;
-    case 2: launch_wide_m<2>(a, type, dim3(grid), block, lds, s); break;
-    case 3: launch_wide_m<3>(a, type, dim3(grid), block, lds, s); break;
-    case 4: launch_wide_m<4>(a, type, dim3(grid), block, lds, s); break;
-    default: return hipErrorInvalidValue;
-  }
-  return hipGetLastError();
+  const int rows = pair ? a.w[0].rows : a.total_rows;
+  const int grid = (rows + a.wide_rows - 1) / a.wide_rows;
+  const int vrows = pair ? 2 * a.wide_rows : a.wide_rows;
+  // a norm prologue sums over four waves (wg_sum_f64): at least 256 threads
+  const int threads = wide_threads(a.cols, a.g.nb, vrows);
+  const dim3 block(a.norm.mode != 0 && threads < 256 ? 256 : threads);
+  const size_t lds = wide_lds_bytes(a.cols, a.g.nb, type, vrows);
+  return pair ? launch_wide_pair<true>(a, type, dim3(grid), block, lds, s)
+              : launch_wide_pair<false>(a, type, dim3(grid), block, lds, s);
 }
 
 }  // namespace hp

@@ -268,6 +268,40 @@ def test_decode_layer_matches_oracle(hip, D, full, pos, kernel):
     assert _f16_steps(gv[:, slot], ol.value_cache[:, slot]).max() <= 1
 
 
+@pytest.mark.parametrize("full", [True, False], ids=["model", "small"])
+def test_decode_layer_kernels_bit_identical(hip, full):
+    """One decode layer of the 42-layer model (hidden 2560, FFN 10240) and of
+    a small model (hidden 512, FFN 1024) with the automatic kernel choice (the wide gate/up + GeGLU launch with its
+    residual-norm prologue, the wide down projection), the vector-ALU
+    kernels and the half-split kernels: every projection is the oracle's
+    bits and every norm prologue sums in one order, so the layer's output and
+    cache entries agree bit for bit."""
+    import torch
+
+    shape = DM.ModelShape() if full else _small_shape()
+    seed = S.derive(S.BASE_SEED, "decode-layer-kernels", full)
+    data = DM.layer_host_data(shape, seed, 0)
+    x = S.activations(S.derive(seed, "x"), 1, shape.hidden).reshape(-1) * 4
+    outs = {}
+    for kernel in (0, 1, 3, 6):
+        hip.setMatvecKernel(kernel)
+        model = DM.HipDecodeModel(shape)
+        model.add_layer(data)
+        dx = _dev(x)
+        dpos = _dev(np.array([1000 if full else 40], np.int32))
+        print(f"decode layer kernel={kernel}", flush=True)
+        try:
+            model.run_layers(dx.data_ptr(), dpos.data_ptr())
+            torch.cuda.synchronize()
+            outs[kernel] = (dx.cpu().numpy(), model.caches[0][0].cpu().numpy(), model.caches[0][1].cpu().numpy())
+        finally:
+            model.release()
+            hip.setMatvecKernel(0)
+    for kernel in (1, 3, 6):
+        for got, ref in zip(outs[kernel], outs[0]):
+            assert np.array_equal(got.view(np.uint8), ref.view(np.uint8)), kernel
+
+
 def test_decode_layers_chain_output_norm_and_graph(hip, D):
     """Three small layers + output norm: eager vs the oracle, then the same
     step captured in a HIP graph and replayed at three positions (the

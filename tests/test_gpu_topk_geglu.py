@@ -115,8 +115,9 @@ def test_geglu_bit_exact(hip, oracle):
     assert diff.size == 0, (diff[:5], gate[diff[:5]], got[diff[:5]], ref[diff[:5]])
 
 
-@pytest.mark.parametrize("kernel", [0, 1, 2, 3], ids=["auto", "valu-fused", "mfma", "half"])
-@pytest.mark.parametrize("rows,k,m", [(600, 2560, 1), (610, 2560, 3), (60, 10240, 1)])
+@pytest.mark.parametrize("kernel", [0, 1, 2, 3, 6], ids=["auto", "valu-fused", "mfma", "half", "wide"])
+@pytest.mark.parametrize("rows,k,m", [(600, 2560, 1), (610, 2560, 3), (60, 10240, 1), (10240, 2560, 1),
+                                      (777, 2560, 4), (1, 2560, 2)])
 def test_matmul_geglu_bit_exact(hip, oracle, kernel, rows, k, m):
     """gate/up + GeGLU (layers.ts:432-456) through hp_hip_matmul_geglu: the
     fused single launch (vector ALU, up to four columns) and the
