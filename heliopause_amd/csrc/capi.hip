@@ -319,10 +319,12 @@ bool use_half(int cols, const TileGeom &g, int tiles) {
 
 // Wide kernel (kquant_wide.hip): one workgroup per block of rows, every
 // block of each row, products chained in LDS.  Needs one weight type (Q4_K or
-// Q6_K) across the launch, at most four columns, no norm prologue and its LDS
-// within the device limit.  Automatic for one column of long rows (40 blocks
-// and more: the FFN down projection), where the one-wave-per-tile kernel
-// leaves most SIMDs idle; selector 6 forces it wherever it applies.
+// Q6_K) across the launch, at most four columns and its LDS within the device
+// limit.  Automatic for long rows (40 blocks and more: the FFN down
+// projection) at one to four columns, where the one-wave-per-tile kernel
+// leaves most SIMDs idle (down, measured: 13.2 -> 10.6 us at one column,
+// 19.5 -> 14.6 at two, 30.9 -> 23.1 at four); selector 6 forces it wherever it
+// applies.
 int wide_rows_for(int rows, int nb, int cols, int type) {
   const State &s = st();
   int r = (rows + s.num_cus - 1) / s.num_cus;
@@ -348,11 +350,13 @@ bool use_wide(size_t count, Handle *const *hs, size_t cols) {
   if (wide_lds_bytes((int)cols, nb, type, wide_rows_for((int)rows, nb, (int)cols, type)) > s.max_lds)
     return false;
   if (forced == 6) return true;
-  return cols == 1 && nb >= 40;
+  return nb >= 40;  // 1..4 columns (checked above)
 }
 
-// The wide kernel for gate/up + GeGLU (equal rows, one type): selector 6
-// forces it (one to four columns); automatic for one column.
+// The wide kernel for gate/up + GeGLU (equal rows, one type) at one to four
+// columns (the FFN gate/up + GeGLU + down, measured: 42.3 -> 31.4 us at two
+// columns, 56.0 -> 45.5 at four against the matrix-core gate/up and its GeGLU
+// launch).
 bool use_wide_pair(Handle *const *hs, size_t cols) {
   const State &s = st();
   const int forced = s.matvec_kernel;
@@ -365,7 +369,7 @@ bool use_wide_pair(Handle *const *hs, size_t cols) {
   if (nb > 256 || 2 * rows >= (1u << 20)) return false;
   const int r = wide_rows_for((int)(2 * rows), nb, (int)cols, type) / 2;
   if (r < 1 || wide_lds_bytes((int)cols, nb, type, 2 * r) > s.max_lds) return false;
-  return forced == 6 || cols == 1;
+  return true;  // 1..4 columns (checked above)
 }
 
 // One matvec launch per column chunk covering every weight (multi == one
