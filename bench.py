@@ -108,7 +108,7 @@ def matvec_kernel_name(choice: str, k: int, m: int, specs: list) -> str:
     r6 = 64 // s
     tiles = sum((r + r6 - 1) // r6 for r in rows)
     tiles16 = sum((r + 15) // 16 for r in rows)
-    wide = m <= 4 and type_id in (1, 3) and (choice == "wide" or (choice == "auto" and m == 1 and nb >= 40))
+    wide = m <= 4 and type_id in (1, 3) and (choice == "wide" or (choice == "auto" and nb >= 40))
     if wide:
         return f"kquant_wide_kernel<{m}, {type_id}>"
     half = s <= 32 and m <= 4 and (choice == "half" or
