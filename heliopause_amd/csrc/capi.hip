@@ -40,6 +40,11 @@ struct Handle {
   uint16_t *dplane = nullptr;  // Q6_K only
   uint8_t *segs = nullptr;     // matrix-core layout (16-row tile segments)
   size_t seg_bytes = 0;
+  uint32_t *f16_flag = nullptr;  // set by the Q6_K repack (launch_repack)
+  // The matrix-core kernels' f16 weight operands sc * q are exact for every
+  // block (always for Q4_K; for Q6_K unless the repack set f16_flag).  When
+  // false the launches that would use matrix cores run the vector-ALU kernels.
+  bool f16_exact = true;
   uint32_t generation = 0;
   bool live = false;
 };
@@ -279,9 +284,12 @@ constexpr size_t kPrefillMinCols = 32;
 constexpr size_t kFastMinCols = 64;
 
 // 0: not a prefill launch, 1: bit-exact prefill, 2: fast prefill
-int prefill_kind(size_t cols) {
+// f16ok: every weight of the launch has exact f16 operands (Handle::f16_exact);
+// otherwise no prefill kernel applies, forced or not.
+int prefill_kind(size_t cols, bool f16ok) {
   const State &s = st();
   const int forced = s.matvec_kernel;
+  if (!f16ok) return 0;
   const bool exact_fits = prefill_lds_bytes() <= s.max_lds;
   const bool fast_fits = prefill_fast_lds_bytes() <= s.max_lds;
   if (forced == 4) return exact_fits ? 1 : 0;
@@ -292,11 +300,11 @@ int prefill_kind(size_t cols) {
   return 0;
 }
 
-bool use_mfma(size_t cols, int nb, int tiles16) {
+bool use_mfma(size_t cols, int nb, int tiles16, bool f16ok) {
   const State &s = st();
   const int forced = s.matvec_kernel;
   const size_t lds = mfma_lds_bytes(cols < 8 ? (int)cols : 8, nb);
-  if (forced == 1 || forced == 3 || lds > s.max_lds) return false;
+  if (!f16ok || forced == 1 || forced == 3 || lds > s.max_lds) return false;
   if (forced == 2) return true;
   if (cols < 2 || lds > 64 * 1024) return false;
   return cols >= 5 || tiles16 >= 1024;
@@ -333,6 +341,12 @@ int wide_rows_for(int rows, int nb, int cols, int type) {
 }
 
 int g_nb_of(Handle *const *hs) { return hs[0]->g.nb; }
+
+bool f16_ok(size_t count, Handle *const *hs) {
+  for (size_t i = 0; i < count; i++)
+    if (!hs[i]->f16_exact) return false;
+  return true;
+}
 
 bool use_wide(size_t count, Handle *const *hs, size_t cols) {
   const State &s = st();
@@ -380,19 +394,21 @@ int32_t run_norm(const float *y, int rows, int n, const float *w_post, const flo
 // Whether a one-column launch over these weights runs a vector-ALU kernel,
 // which can form its input with the norm prologue.
 bool norm_prologue_ok(size_t count, Handle *const *hs, size_t cols) {
-  if (cols != 1 || hs[0]->g.nb > 16 || prefill_kind(cols) != 0) return false;
+  const bool f16 = f16_ok(count, hs);
+  if (cols != 1 || hs[0]->g.nb > 16 || prefill_kind(cols, f16) != 0) return false;
   int tiles16 = 0;
   for (size_t i = 0; i < count; i++) tiles16 += (int)((hs[i]->row_count + 15) / 16);
-  return !use_mfma(cols, hs[0]->g.nb, tiles16);
+  return !use_mfma(cols, hs[0]->g.nb, tiles16, f16);
 }
 
 // Whether a launch of `cols` columns (2 or more) runs the vector-ALU kernels
 // in one chunk, so it can take its input as a pre-quantised image.
 bool image_input_ok(size_t count, Handle *const *hs, size_t cols) {
-  if (cols < 2 || prefill_kind(cols) != 0) return false;
+  const bool f16 = f16_ok(count, hs);
+  if (cols < 2 || prefill_kind(cols, f16) != 0) return false;
   int tiles16 = 0;
   for (size_t i = 0; i < count; i++) tiles16 += (int)((hs[i]->row_count + 15) / 16);
-  return !use_mfma(cols, hs[0]->g.nb, tiles16) && cols_per_launch(hs[0]->g, st().max_lds) >= (int)cols;
+  return !use_mfma(cols, hs[0]->g.nb, tiles16, f16) && cols_per_launch(hs[0]->g, st().max_lds) >= (int)cols;
 }
 
 // norm != null: the input is formed from a residual stream (NormIn) -- in the
@@ -408,7 +424,8 @@ int32_t run_matvec(size_t count, Handle *const *hs, const float *d_input, size_t
   State &s = st();
   if (cols == 0) return HP_OK;
   const bool image_ok = s.images && cols >= 2 && image_input_ok(count, hs, cols);
-  const bool wide = prefill_kind(cols) == 0 && use_wide(count, hs, cols);
+  const bool f16 = f16_ok(count, hs);
+  const bool wide = prefill_kind(cols, f16) == 0 && use_wide(count, hs, cols);
   const bool wide_norm = wide && cols == 1 && g_nb_of(hs) <= 16;  // the wide kernel's norm prologue
   if (norm && (wide ? !wide_norm : !norm_prologue_ok(count, hs, cols))) {
     uint8_t *img = image_ok && img_scratch ? img_scratch : nullptr;
@@ -446,7 +463,7 @@ int32_t run_matvec(size_t count, Handle *const *hs, const float *d_input, size_t
   }
   a.total_rows = rows_all;
   a.total_units = a.Rh ? (rows_all + a.Rh - 1) / a.Rh : 0;
-  if (const int kind = prefill_kind(cols)) {
+  if (const int kind = prefill_kind(cols, f16)) {
     if (cols > 65535) return fail(HP_ERR_SHAPE, "too many columns");
     MfmaLaunch l{};
     l.count = (int)count;
@@ -493,7 +510,7 @@ int32_t run_matvec(size_t count, Handle *const *hs, const float *d_input, size_t
   }
   int tiles16 = 0;
   for (size_t i = 0; i < count; i++) tiles16 += (int)((hs[i]->row_count + 15) / 16);
-  if (use_mfma(cols, g.nb, tiles16)) {
+  if (use_mfma(cols, g.nb, tiles16, f16)) {
     MfmaLaunch l{};
     l.count = (int)count;
     l.k = (int)input_size;
@@ -556,8 +573,9 @@ int32_t run_matvec_geglu(Handle *hg, Handle *hu, const float *d_input, size_t in
   const TileGeom g = hg->g;
   const int tiles16 = 2 * (int)((rows + 15) / 16);
   Handle *pair[2] = {hg, hu};
-  const bool wide = prefill_kind(cols) == 0 && hg->type == hu->type && use_wide_pair(pair, cols);
-  const bool fused = !wide && cols <= 4 && s.matvec_kernel <= 1 && !use_mfma(cols, g.nb, tiles16) &&
+  const bool f16 = f16_ok(2, pair);
+  const bool wide = prefill_kind(cols, f16) == 0 && hg->type == hu->type && use_wide_pair(pair, cols);
+  const bool fused = !wide && cols <= 4 && s.matvec_kernel <= 1 && !use_mfma(cols, g.nb, tiles16, f16) &&
                      !use_half((int)cols, g, 2 * hg->tiles) && cols_per_launch(g, s.max_lds) >= (int)cols;
   if (norm && !((fused || wide) && cols == 1 && g.nb <= 16)) {
     int32_t rc = run_norm(norm->y, (int)cols, (int)input_size, norm->w_post, norm->mode == 2 ? norm->x_res : nullptr,
@@ -628,7 +646,7 @@ int32_t run_matvec_geglu(Handle *hg, Handle *hu, const float *d_input, size_t in
     s.matmul_calls++;
     return HP_OK;
   }
-  if (prefill_kind(cols) == 2 && hg->type == hu->type) {
+  if (prefill_kind(cols, f16) == 2 && hg->type == hu->type) {
     // fast prefill: gate and up rows in one tile, GeGLU in its epilogue
     void *pre = nullptr;
     int32_t rc = stream_scratch(stream, kScratchPrefill, prefill_fast_geglu_bytes((int)input_size, (int)cols), &pre);
@@ -692,9 +710,18 @@ int32_t geglu_pair_check(uint64_t gate, uint64_t up, size_t input_len, size_t in
   return HP_OK;
 }
 
+// Handle::f16_exact from the Q6_K repack's flag, once the repack has finished.
+hipError_t read_f16_flag(Handle &h) {
+  if (h.type != kTypeQ6K) return hipSuccess;
+  uint32_t v = 1;
+  const hipError_t e = hipMemcpy(&v, h.f16_flag, sizeof v, hipMemcpyDeviceToHost);
+  h.f16_exact = e == hipSuccess && v == 0;
+  return e;
+}
+
 // Uploads one weight.  With sync == false (device source only) the repack is
 // left queued on the library stream; the caller synchronises before it
-// reuses or frees the source.
+// reuses or frees the source, then calls read_f16_flag.
 int32_t upload_common(int32_t type_id, const void *src, bool src_device, size_t weight_len, size_t input_size,
                       size_t row_count, uint64_t *out_handle, bool sync = true) {
   State &s = st();
@@ -717,13 +744,16 @@ int32_t upload_common(int32_t type_id, const void *src, bool src_device, size_t 
   h.byte_length = weight_len;
   h.g = choose_geometry((int)(input_size / kQK));
   h.tiles = (int)((row_count + h.g.R - 1) / h.g.R);
-  // one allocation holds both layouts: tiles (+ Q6_K d plane), then segments
+  // one allocation holds both layouts: tiles (+ Q6_K d plane), then
+  // segments, then the repack's f16 flag
   const int nb = (int)(input_size / kQK);
   const size_t tile_bytes = (weight_len + 255) & ~(size_t)255;
   h.seg_bytes = mfma_segment_bytes(type_id, (int)row_count, nb);
-  if (hipMalloc((void **)&h.data, tile_bytes + h.seg_bytes) != hipSuccess)
+  if (hipMalloc((void **)&h.data, tile_bytes + h.seg_bytes + 256) != hipSuccess)
     return fail(HP_ERR_OOM, "weight allocation failed");
   h.segs = h.data + tile_bytes;
+  h.f16_flag = reinterpret_cast<uint32_t *>(h.segs + h.seg_bytes);
+  h.f16_exact = type_id != kTypeQ6K;  // Q6_K: read_f16_flag after the repack
   if (type_id == kTypeQ6K) h.dplane = reinterpret_cast<uint16_t *>(h.data + row_count * (input_size / kQK) * 208);
 
   const uint8_t *raw = static_cast<const uint8_t *>(src);
@@ -741,10 +771,12 @@ int32_t upload_common(int32_t type_id, const void *src, bool src_device, size_t 
     }
     raw = staging;
   }
-  hipError_t e = launch_repack(type_id, raw, (int)row_count, h.g, h.data, h.dplane, s.stream);
+  hipError_t e = hipMemsetAsync(h.f16_flag, 0, sizeof(uint32_t), s.stream);
+  if (e == hipSuccess) e = launch_repack(type_id, raw, (int)row_count, h.g, h.data, h.dplane, h.f16_flag, s.stream);
   if (e == hipSuccess) e = launch_repack_mfma(type_id, raw, (int)row_count, nb, h.segs, s.stream);
   if (e == hipSuccess && (sync || !src_device)) e = hipStreamSynchronize(s.stream);
   if (staging) (void)hipFree(staging);
+  if (e == hipSuccess && (sync || !src_device)) e = read_f16_flag(h);
   if (e != hipSuccess) {
     (void)hipStreamSynchronize(s.stream);
     (void)hipFree(h.data);
@@ -1208,6 +1240,10 @@ int32_t hp_hip_weight_upload_gguf(const hp_gguf_t *g, size_t count, const uint64
       }
       // the next batch overwrites the staging the queued repacks read
       if (rc == HP_OK && hipStreamSynchronize(s.stream) != hipSuccess) rc = fail(HP_ERR_HIP, "repack (GGUF load)");
+      for (size_t i = begin; i < end && rc == HP_OK; i++) {
+        Handle *h = handles[i] ? lookup(handles[i]) : nullptr;
+        if (h && read_f16_flag(*h) != hipSuccess) rc = fail(HP_ERR_HIP, "repack flag (GGUF load)");
+      }
     }
     if (rc != HP_OK) {
       const std::string why = g_last_error;
@@ -1219,6 +1255,7 @@ int32_t hp_hip_weight_upload_gguf(const hp_gguf_t *g, size_t count, const uint64
             (void)hipFree(h->data);
             h->data = h->segs = nullptr;
             h->dplane = nullptr;
+            h->f16_flag = nullptr;
             h->live = false;
           }
           handles[i] = 0;
@@ -1242,6 +1279,7 @@ int32_t hp_hip_weight_release(uint64_t handle) {
   h->data = nullptr;
   h->segs = nullptr;
   h->dplane = nullptr;
+  h->f16_flag = nullptr;
   h->live = false;
   return HP_OK;
 }

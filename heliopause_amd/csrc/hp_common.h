@@ -136,8 +136,10 @@ hipError_t launch_matvec_pair(const MatvecArgs &a, int num_cus, hipStream_t s);
 size_t wide_lds_bytes(int cols, int nb, int type, int rows_per_wg);
 int wide_threads(int cols, int nb, int rows_per_wg);
 hipError_t launch_matvec_wide(const MatvecArgs &a, hipStream_t s);
+// Q6_K also sets *f16_flag (zeroed by the caller) to 1 when some scale makes
+// sc * (q - 32) inexact in f16, which the matrix-core kernels need exact.
 hipError_t launch_repack(int type, const uint8_t *raw, int rows, const TileGeom &g, uint8_t *tiles,
-                         uint16_t *dplane, hipStream_t s);
+                         uint16_t *dplane, uint32_t *f16_flag, hipStream_t s);
 // Top-k (k <= kTopkMaxK) of each of `rows` (<= kTopkMaxRows) rows of n
 // (<= kTopkMaxN) logits, optional softcap (cap > 0).  scratch holds
 // topk_scratch_bytes(rows, n, k) bytes, zero when first used; the kernels

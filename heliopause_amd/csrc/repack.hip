@@ -58,8 +58,13 @@ __global__ void repack_q4k_kernel(const uint8_t *__restrict__ raw, int rows, Til
   }
 }
 
+// f16_flag: set to 1 when some sub-block scale s is odd with |s| >= 67.  The
+// matrix-core kernels take sc * (q - 32) as an f16 operand; with |q - 32| <=
+// 32 that product is odd and above 2048 in magnitude (so not exact in f16)
+// only for such scales (67 * 31 = 2077; 65 * 31 = 2015; even scales give even
+// products of at most 4096).
 __global__ void repack_q6k_kernel(const uint8_t *__restrict__ raw, int rows, TileGeom g, uint8_t *__restrict__ out,
-                                  uint16_t *__restrict__ dplane) {
+                                  uint16_t *__restrict__ dplane, uint32_t *__restrict__ f16_flag) {
   const size_t gidx = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (gidx >= (size_t)rows * g.nb) return;
   const TilePos p = tile_pos(gidx, rows, g, 13);
@@ -115,6 +120,13 @@ __global__ void repack_q6k_kernel(const uint8_t *__restrict__ raw, int rows, Til
            ((uint32_t)sc[4 * e + 3] << 24);
   dst[(size_t)12 * p.lanes] = make_uint4(s[0], s[1], s[2], s[3]);
   dplane[gidx] = (uint16_t)(b[208] | (b[209] << 8));
+  bool wide_product = false;
+#pragma unroll
+  for (int i = 0; i < 16; i++) {
+    const int v = (int)(int8_t)sc[i];
+    wide_product |= (v & 1) && (v >= 67 || v <= -67);
+  }
+  if (wide_product) *f16_flag = 1u;
 }
 
 __device__ __forceinline__ float h2f_r(uint32_t bits16) {
@@ -186,14 +198,14 @@ __global__ void dequant_kernel(int type, const uint8_t *__restrict__ tiles, cons
 }
 
 hipError_t launch_repack(int type, const uint8_t *raw, int rows, const TileGeom &g, uint8_t *tiles, uint16_t *dplane,
-                         hipStream_t s) {
+                         uint32_t *f16_flag, hipStream_t s) {
   const size_t n = (size_t)rows * g.nb;
   const int tpb = 128;
   const int blocks = (int)((n + tpb - 1) / tpb);
   if (type == kTypeQ4K)
     hipLaunchKernelGGL(repack_q4k_kernel, dim3(blocks), dim3(tpb), 0, s, raw, rows, g, tiles);
   else
-    hipLaunchKernelGGL(repack_q6k_kernel, dim3(blocks), dim3(tpb), 0, s, raw, rows, g, tiles, dplane);
+    hipLaunchKernelGGL(repack_q6k_kernel, dim3(blocks), dim3(tpb), 0, s, raw, rows, g, tiles, dplane, f16_flag);
   return hipGetLastError();
 }
 

@@ -143,6 +143,46 @@ def test_wide_kernel_columns(hip, oracle, type_name, rows, k):
         hip.releaseHipQuantizedWeightHandle(h)
 
 
+def _q6k_full_range_scales(seed, rows, k):
+    """Q6_K blocks whose 16 int8 sub-block scales span -128..127 (as in
+    quantised model files, where a block's largest sub-block takes -128),
+    with +-127 and -67 planted in the first block."""
+    w = S.q6_k_blocks(seed, rows, k).reshape(-1, 210).copy()
+    w[:, 192:208] = S.random_bytes(S.derive(seed, "q6k.fullscales"), 16 * w.shape[0]).reshape(-1, 16)
+    w[0, 192:195] = np.array([127, -127, -67], dtype=np.int8).view(np.uint8)
+    return w.reshape(rows, -1)
+
+
+@pytest.mark.parametrize("kernel_id", [0, 1, 2, 3, 4, 5, 6], ids=["auto", "valu", "mfma", "half", "prefill",
+                                                                  "fast", "wide"])
+def test_q6k_full_range_scales(hip, oracle, kernel_id):
+    """Q6_K scales beyond +-66 make sc * (q - 32) inexact as an f16 matrix-core
+    operand; such weights run the vector-ALU kernels under every selector, so
+    the results stay bit-exact (alone and in a launch with Q4_K weights) at
+    decode and prefill column counts."""
+    k = 2560
+    seed = S.derive(S.BASE_SEED, "q6kfull", kernel_id)
+    w6 = _q6k_full_range_scales(seed, 300, k)
+    w4 = _weights("Q4_K", S.derive(seed, 1), 64, k)
+    h6 = hip.createHipQuantizedWeightHandle("Q6_K", w6, k, 300)
+    h4 = hip.createHipQuantizedWeightHandle("Q4_K", w4, k, 64)
+    hip.setMatvecKernel(kernel_id)
+    try:
+        for m in (1, 4, 8, 64):
+            print(f"q6k full-range kernel={kernel_id} m={m}", flush=True)
+            x = S.activations(S.derive(seed, m), m, k)
+            ref6 = oracle.matmul(3, w6, x, 300, threads=8)
+            got = hip.matMulQuantizedHipResident(h6, x, k, 300, m).reshape(m, 300)
+            assert np.array_equal(_bits(got), _bits(ref6)), (m, np.abs(got - ref6).max())
+            outs = hip.matMulQuantizedHipResidentMulti([h4, h6], x, k, m)
+            assert np.array_equal(_bits(outs[1].reshape(m, 300)), _bits(ref6)), m
+            assert np.array_equal(_bits(outs[0].reshape(m, 64)), _bits(oracle.matmul(1, w4, x, 64))), m
+    finally:
+        hip.setMatvecKernel(0)
+        hip.releaseHipQuantizedWeightHandle(h6)
+        hip.releaseHipQuantizedWeightHandle(h4)
+
+
 def test_shape_errors(hip):
     k, rows = 512, 8
     w = _weights("Q4_K", 1, rows, k)

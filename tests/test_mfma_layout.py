@@ -276,3 +276,19 @@ def test_emulated_kernel_matches_oracle(oracle, type_id, rows, m_cols):
     got = emulate(type_id, segs, rows, k, x)
     want = oracle.matmul(type_id, raw, x, rows).reshape(m_cols, rows)
     assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
+def test_q6k_f16_operand_exactness_criterion():
+    """The matrix-core kernels take sc * (q - 32) as an f16 operand.  The set of
+    int8 scales for which some 6-bit quant makes that product inexact in f16
+    is exactly the odd scales with |sc| >= 67 -- the condition the Q6_K repack
+    flags (those weights then run the vector-ALU kernels).  Checked over every
+    (scale, quant) pair."""
+    sc = np.arange(-128, 128, dtype=np.int64)[:, None]
+    qq = np.arange(-32, 32, dtype=np.int64)[None, :]
+    prod = sc * qq
+    inexact = (prod.astype(np.float16).astype(np.int64) != prod).any(axis=1)
+    flagged = (sc[:, 0] % 2 != 0) & (np.abs(sc[:, 0]) >= 67)
+    assert np.array_equal(inexact, flagged)
+    # the synthetic distribution (scales -32..31) never reaches it
+    assert not inexact[(sc[:, 0] >= -32) & (sc[:, 0] <= 31)].any()
