@@ -233,7 +233,7 @@ __device__ __forceinline__ half8 a_q6k(const Seg<false> &r, int g, int u, const 
                                        const half2v (&N)[4]) {
   const int jj = 2 * (u & 1);
   const uint32_t ql = u4at(g ? r.c1 : r.c0, u);
-  const uint32_t qh = u4at(r.c2, 2 * g + (u >> 1));
+  const uint32_t qh = u4at(r.c2, 2 * (u >> 1) + g);
   const uint32_t lo = (ql & 0x0F0F0F0Fu) | (((qh >> (2 * jj)) & 0x03030303u) << 4);
   const uint32_t hi = ((ql >> 4) & 0x0F0F0F0Fu) | (((qh >> (2 * jj + 2)) & 0x03030303u) << 4);
   return cat(fma2(magic_pair<kSel01>(lo), S[0], N[0]), fma2(magic_pair<kSel23>(lo), S[1], N[1]),
@@ -525,7 +525,8 @@ __global__ void repack_mfma_kernel(const uint8_t *__restrict__ raw, int type, in
     // q6 of element e = 128h + 32t + l5: low nibble of ql[64h + l5 + 32(t&1)]
     // (shifted by 4(t>>1)), high 2 bits qh[32h + l5] >> 2t.  For lane class
     // l: nibble byte 4u + cc pairs j = 2u (low) and 2u + 1 (high nibble); the
-    // high-bit byte 4(2cls + hh) + cc is qh[32hh + 8cc + l] as stored.
+    // high-bit byte 4(2hh + cls) + cc is qh[32hh + 8cc + l] as stored (hh
+    // major, so a quarter's two classes are one aligned 8-byte pair).
 #pragma unroll
     for (int qq = 0; qq < 4; qq++) {
 #pragma unroll
@@ -552,7 +553,7 @@ __global__ void repack_mfma_kernel(const uint8_t *__restrict__ raw, int type, in
 #pragma unroll
         for (int hh = 0; hh < 2; hh++) {
           const int l = 2 * qq + cls;
-          q[2 * cls + hh] = byte(128 + 32 * hh + l) | (byte(128 + 32 * hh + 8 + l) << 8) |
+          q[2 * hh + cls] = byte(128 + 32 * hh + l) | (byte(128 + 32 * hh + 8 + l) << 8) |
                             (byte(128 + 32 * hh + 16 + l) << 16) | (byte(128 + 32 * hh + 24 + l) << 24);
         }
       reinterpret_cast<uint4 *>(seg + 288)[128 + qq * 16 + rho] = make_uint4(q[0], q[1], q[2], q[3]);

@@ -176,7 +176,7 @@ __device__ __forceinline__ half8 a_frag(const uint8_t *seg, int l, int n, int q)
     }
     const int jj = 2 * (q & 1);
     const uint32_t ql = *reinterpret_cast<const uint32_t *>(seg + 288 + 1024 * g + 16 * src + 4 * q);
-    const uint32_t qh = *reinterpret_cast<const uint32_t *>(seg + 288 + 2048 + 16 * src + 4 * (2 * g + (q >> 1)));
+    const uint32_t qh = *reinterpret_cast<const uint32_t *>(seg + 288 + 2048 + 16 * src + 4 * (2 * (q >> 1) + g));
     const uint32_t lo = (ql & 0x0F0F0F0Fu) | (((qh >> (2 * jj)) & 0x03030303u) << 4);
     const uint32_t hi = ((ql >> 4) & 0x0F0F0F0Fu) | (((qh >> (2 * jj + 2)) & 0x03030303u) << 4);
     return cat(fma2(magic_pair<kSel01>(lo), S[0], N[0]), fma2(magic_pair<kSel23>(lo), S[1], N[1]),
@@ -348,20 +348,33 @@ __global__ __launch_bounds__(256) void kquant_prefill_kernel(const PfArgs a) {
 // projections), and cuts the vector-ALU tail from 18 to at most 4 operations
 // per output and block.
 //
-// Workgroup tile: 128 rows (8 segments; wave w owns segments 2w, 2w + 1) x
-// 64 columns.  Per block, two contiguous regions are copied into LDS with
-// direct global->LDS loads (no register staging), one stage per workgroup
-// and two workgroups per CU, so one computes while the other loads: the 8
-// weight segments and the 64 columns' activation tile written by the
-// pre-pass in the order the B fragments are read (conflict-free):
+// Workgroup tile: 8 waves; a wave owns 32 rows (two 16-row segments) x 64
+// columns.  256 rows x 64 columns (PAIR: 128 rows of gate, waves 0-3, and
+// the same 128 rows of up, waves 4-7).
+//
+// Weights go straight from global memory to registers: each wave's rows are
+// its own, so staging them in LDS would buy no reuse.  The 64 columns'
+// activation tile (written by the pre-pass in the order the fragments are
+// read) is shared by the 8 waves through two LDS stages:
 //   XH f16 [class l][quarter q][column n (64)][8]   32768 bytes
 //   XB f16 [q < 2][n][8]  (half-block sums 16h..16h+15, h = 8q + e)  2048
 //   XD f32 [n]                                                         256
+// Per block b the loads of block b + 1 (its weights into the other register
+// set, its activation tile into staging registers) are issued first and land
+// while block b computes; the staged tile is then written to the other LDS
+// stage, and one barrier per block separates the stages' readers and writers.
+//
+// Operand order: the activation tile is the MFMA's first operand and the
+// weights the second, so lane (n, q)'s accumulator holds weight row n of the
+// segment and columns 4q .. 4q + 3 of the column set: the row's d and dmin
+// come with the lane's own header load.
 constexpr int kF2Cols = 64;
-constexpr int kF2W = 8 * 3360;
 constexpr int kF2XTile = 32768 + 2048 + 256;  // 35,072 bytes per (column tile, block)
-constexpr int kF2Stage = kF2W + kF2XTile;      // 61,952
-constexpr int kF2Lds = kF2Stage;               // one stage per workgroup, two workgroups per CU
+constexpr int kF3Waves = 8;
+constexpr int kF3Threads = 64 * kF3Waves;
+constexpr int kF3Segs = 2 * kF3Waves;                                // segments per workgroup tile
+constexpr int kF3Full = kF2XTile / 1024;                             // whole 1 KB chunks per activation tile
+constexpr int kF3Part = kF2XTile % 1024;                             // bytes of the last, partial chunk
 
 // The fast kernel's activation tiles (f16 quants [class][quarter][column][8],
 // f16 16-element sums, f32 d per column) from Q8_K of x, one 16-lane row per
@@ -411,20 +424,8 @@ __global__ __launch_bounds__(256) void q8k_prefill_tiles16_kernel(const float *_
   if (i16 == 0) xd[n] = nz ? __fdiv_rn(1.0f, inv) : 0.0f;
 }
 
-// Copies `bytes` (a multiple of 16) from global to LDS with the wave's share
-// of 1 KB chunks (chunk c by wave c % 4).
-__device__ __forceinline__ void lds_copy(const uint8_t *src, uint8_t *dst, int bytes, int wave, int lane) {
-  const int full = bytes >> 10;
-  for (int c = wave; c < full; c += 4)
-    __builtin_amdgcn_global_load_lds(reinterpret_cast<const void *>(src + c * 1024 + 16 * lane),
-                                     (__attribute__((address_space(3))) void *)(dst + c * 1024), 16, 0, 0);
-  if ((full & 3) == wave && 16 * lane < bytes - (full << 10))  // the last, partial chunk
-    __builtin_amdgcn_global_load_lds(reinterpret_cast<const void *>(src + full * 1024 + 16 * lane),
-                                     (__attribute__((address_space(3))) void *)(dst + full * 1024), 16, 0, 0);
-}
-
 struct F2Args {
-  PfWeight w[kMaxWeights];  // rt_begin counts 128-row tiles here
+  PfWeight w[kMaxWeights];  // rt_begin counts 256-row workgroup tiles here
   int count, total_rt, col_tiles, nb, cols;
   const uint8_t *xt;
   // ksplit > 1: block range r of a tile writes its sums to part + r * part_stride
@@ -438,21 +439,80 @@ struct F2Args {
   double gelu_c;
 };
 
-// A fragment of class l for rows n of one segment from the raw segment bytes
-// (fast path: scales pre-expanded in S, N).
+// One segment's weights in a lane's registers, loaded with 16- and 8-byte
+// loads (few memory instructions).  The quant chunks come in the matrix-core
+// layout -- lane (n, r) holds unit n + 16r of chunk g, dwords u = 0..3 -- and
+// f3_transpose turns them into what the A fragments take: lane (n, q) holds
+// dword q of units n + 16t, t = 0..3 (class l = 2t + g).
+// Q4_K: row n's header (d | dmin, then the 12 bytes of 6-bit scales and mins).
+struct W4 {
+  uint4 hdr;
+  uint4 qa[2];  // [g]
+};
+// Q6_K: low-bit chunks as Q4_K's; high bits: per t the two dwords (classes g =
+// 0, 1) of unit n + 16t for quarter pair q >> 1 (hh-major units); row n's
+// scales 4q .. 4q + 3 and its d (f16 bits).
+struct W6 {
+  uint4 qa[2];  // [g]
+  uint2 qh[4];  // [t]
+  uint32_t gs, d16;
+};
 template <bool Q4>
-__device__ __forceinline__ half8 f2_a(const uint8_t *seg, int l, int n, int q, const half2v (&S)[4],
-                                      const half2v (&N)[4]) {
-  const int g = l & 1, src = n + 16 * (l >> 1);
+struct WSel {
+  using T = W6;
+};
+template <>
+struct WSel<true> {
+  using T = W4;
+};
+
+// Segment layouts of the matrix-core repack (kquant_mfma.hip): Q4_K [16 rows
+// x 16-byte header][2 chunks x 64 units x 16 bytes of quants]; Q6_K [16 rows x
+// 16 scales][16 x f16 d][2 chunks x 1024 low bits][1024 high bits].
+template <bool Q4>
+__device__ __forceinline__ void f3_wload(typename WSel<Q4>::T &w, const uint8_t *seg, int lane) {
+  const int n = lane & 15, q = lane >> 4;
   if constexpr (Q4) {
-    const uint32_t dw = *reinterpret_cast<const uint32_t *>(seg + 256 + 1024 * g + 16 * src + 4 * q);
+    w.hdr = *reinterpret_cast<const uint4 *>(seg + 16 * n);
+#pragma unroll
+    for (int g = 0; g < 2; g++) w.qa[g] = *reinterpret_cast<const uint4 *>(seg + 256 + 1024 * g + 16 * lane);
+  } else {
+    w.gs = *reinterpret_cast<const uint32_t *>(seg + 16 * n + 4 * q);
+    w.d16 = *reinterpret_cast<const uint16_t *>(seg + 256 + 2 * n);
+#pragma unroll
+    for (int g = 0; g < 2; g++) w.qa[g] = *reinterpret_cast<const uint4 *>(seg + 288 + 1024 * g + 16 * lane);
+#pragma unroll
+    for (int t = 0; t < 4; t++) w.qh[t] = *reinterpret_cast<const uint2 *>(seg + 2336 + 256 * t + 16 * n + 8 * (q >> 1));
+  }
+}
+
+// 4 x 4 transpose across the wave's four 16-lane rows: in, lane (n, r) holds
+// v[u] = element (r, u); out, lane (n, q) holds v[t] = element (t, q).
+__device__ __forceinline__ void f3_transpose(uint32_t (&v)[4]) {
+  const auto a = __builtin_amdgcn_permlane32_swap(v[0], v[2], false, false);
+  const auto b = __builtin_amdgcn_permlane32_swap(v[1], v[3], false, false);
+  const auto c = __builtin_amdgcn_permlane16_swap(a[0], b[0], false, false);
+  const auto d = __builtin_amdgcn_permlane16_swap(a[1], b[1], false, false);
+  v[0] = c[0];
+  v[1] = c[1];
+  v[2] = d[0];
+  v[3] = d[1];
+}
+
+// Weight fragment of class l = 2t + g (sc * q as exact f16); qd[g][t] are the
+// transposed quant dwords.
+template <bool Q4>
+__device__ __forceinline__ half8 f3_a(const typename WSel<Q4>::T &w, const uint32_t (&qd)[2][4], int l, int q,
+                                      const half2v (&S)[4], const half2v (&N)[4]) {
+  const int g = l & 1, t = l >> 1;
+  if constexpr (Q4) {
+    const uint32_t dw = qd[g][t];
     const uint32_t lo = dw & 0x0F0F0F0Fu, hi = (dw >> 4) & 0x0F0F0F0Fu;
     return cat(fma2(magic_pair<kSel01>(lo), S[0], N[0]), fma2(magic_pair<kSel23>(lo), S[0], N[0]),
                fma2(magic_pair<kSel01>(hi), S[1], N[1]), fma2(magic_pair<kSel23>(hi), S[1], N[1]));
   } else {
     const int jj = 2 * (q & 1);
-    const uint32_t ql = *reinterpret_cast<const uint32_t *>(seg + 288 + 1024 * g + 16 * src + 4 * q);
-    const uint32_t qh = *reinterpret_cast<const uint32_t *>(seg + 288 + 2048 + 16 * src + 4 * (2 * g + (q >> 1)));
+    const uint32_t ql = qd[g][t], qh = g ? w.qh[t].y : w.qh[t].x;
     const uint32_t lo = (ql & 0x0F0F0F0Fu) | (((qh >> (2 * jj)) & 0x03030303u) << 4);
     const uint32_t hi = ((ql >> 4) & 0x0F0F0F0Fu) | (((qh >> (2 * jj + 2)) & 0x03030303u) << 4);
     return cat(fma2(magic_pair<kSel01>(lo), S[0], N[0]), fma2(magic_pair<kSel23>(lo), S[1], N[1]),
@@ -460,20 +520,19 @@ __device__ __forceinline__ half8 f2_a(const uint8_t *seg, int l, int n, int q, c
   }
 }
 
-// One block of the wave's 32 x 64 tile.  Branch-free (a missing second
-// segment computes on stale LDS bytes and is never stored), so the compiler
-// can overlap the LDS reads of a class with the MFMAs of the previous one.
+// One block of the wave's 32 x 64 tile: weights w (two segments) against the
+// activation tile at xl.  A wave whose second segment lies past the weight's
+// end computes on a repeat of its first and never stores it.
 template <bool Q4>
-__device__ __forceinline__ void f2_block(float (&out)[2][4][4], const uint8_t *wl, const uint8_t *xl, int lane) {
+__device__ __forceinline__ void f3_block(float (&out)[2][4][4], const typename WSel<Q4>::T (&w)[2],
+                                         const uint8_t *xl, int lane) {
   const int n = lane & 15, q = lane >> 4;
-  constexpr int segb = Q4 ? 2304 : 3360;
   const _Float16 *xh = reinterpret_cast<const _Float16 *>(xl);
   half2v S[2][4], N[2][4];
 #pragma unroll
   for (int rs = 0; rs < 2; rs++) {
-    const uint8_t *seg = wl + rs * segb;
     if constexpr (Q4) {
-      const uint4 hdr = *reinterpret_cast<const uint4 *>(seg + 16 * n);
+      const uint4 hdr = w[rs].hdr;
       const uint32_t sclo = hdr.y & 0x3F3F3F3Fu;
       const uint32_t schi = (hdr.w & 0x0F0F0F0Fu) | ((hdr.y >> 2) & 0x30303030u);
       const uint32_t sc = q < 2 ? sclo : schi;
@@ -484,49 +543,57 @@ __device__ __forceinline__ void f2_block(float (&out)[2][4][4], const uint8_t *w
 #pragma unroll
       for (int e = 0; e < 4; e++) N[rs][e] = S[rs][e] * m1024;
     } else {
-      const uint32_t gs = *reinterpret_cast<const uint32_t *>(seg + 16 * n + 4 * q) ^ 0x80808080u;
+      // signed scales: bytes ^ 0x80 are s + 128; (1024 + 128 + s) - 1152 = s
+      const uint32_t gs = w[rs].gs ^ 0x80808080u;
 #pragma unroll
       for (int e = 0; e < 4; e++) {
         S[rs][e] = dup_byte(gs, e, 1152.0f);
-        N[rs][e] = S[rs][e] * (half2v){(_Float16)-1056.0f, (_Float16)-1056.0f};
+        N[rs][e] = S[rs][e] * (half2v){(_Float16)-1056.0f, (_Float16)-1056.0f};  // -(1024 + 32) * sc
       }
     }
   }
+  uint32_t qd[2][2][4];  // [rs][g][t]
+#pragma unroll
+  for (int rs = 0; rs < 2; rs++)
+#pragma unroll
+    for (int g = 0; g < 2; g++) {
+      const uint4 v = w[rs].qa[g];
+      qd[rs][g][0] = v.x;
+      qd[rs][g][1] = v.y;
+      qd[rs][g][2] = v.z;
+      qd[rs][g][3] = v.w;
+      f3_transpose(qd[rs][g]);
+    }
   f32x4 D[2][4];
+  // B fragments one class ahead: class l + 1's LDS reads are in flight while
+  // class l's weights unpack and its MFMAs run
+  half8 B[2][4];
+#pragma unroll
+  for (int cs = 0; cs < 4; cs++)
+    B[0][cs] = __builtin_bit_cast(half8, *reinterpret_cast<const uint4 *>(xh + (q * kF2Cols + 16 * cs + n) * 8));
 #pragma unroll
   for (int l = 0; l < 8; l++) {
-    half8 B[4];
+    if (l < 7) {
 #pragma unroll
-    for (int cs = 0; cs < 4; cs++)
-      B[cs] = __builtin_bit_cast(half8, *reinterpret_cast<const uint4 *>(xh + ((l * 4 + q) * kF2Cols + 16 * cs + n) * 8));
-    const half8 A0 = f2_a<Q4>(wl, l, n, q, S[0], N[0]);
-    const half8 A1 = f2_a<Q4>(wl + segb, l, n, q, S[1], N[1]);
+      for (int cs = 0; cs < 4; cs++)
+        B[(l + 1) & 1][cs] = __builtin_bit_cast(
+            half8, *reinterpret_cast<const uint4 *>(xh + (((l + 1) * 4 + q) * kF2Cols + 16 * cs + n) * 8));
+    }
+    __builtin_amdgcn_sched_barrier(0);  // keeps the reads ahead of this class's work
+    const half8 A0 = f3_a<Q4>(w[0], qd[0], l, q, S[0], N[0]);
+    const half8 A1 = f3_a<Q4>(w[1], qd[1], l, q, S[1], N[1]);
 #pragma unroll
     for (int cs = 0; cs < 4; cs++) {
       const f32x4 c0 = l == 0 ? (f32x4){0.0f, 0.0f, 0.0f, 0.0f} : D[0][cs];
       const f32x4 c1 = l == 0 ? (f32x4){0.0f, 0.0f, 0.0f, 0.0f} : D[1][cs];
-      D[0][cs] = mfma(A0, B[cs], c0);
-      D[1][cs] = mfma(A1, B[cs], c1);
+      D[0][cs] = mfma(B[l & 1][cs], A0, c0);
+      D[1][cs] = mfma(B[l & 1][cs], A1, c1);
     }
   }
   const float *xd = reinterpret_cast<const float *>(xl + 32768 + 2048);
-  float dx[4], dw[2][4], dmw[2][4];
+  f32x4 dx[4];
 #pragma unroll
-  for (int cs = 0; cs < 4; cs++) dx[cs] = xd[16 * cs + n];
-#pragma unroll
-  for (int rs = 0; rs < 2; rs++)
-#pragma unroll
-    for (int j = 0; j < 4; j++) {
-      const int row = 4 * q + j;
-      if constexpr (Q4) {
-        const uint32_t v = *reinterpret_cast<const uint32_t *>(wl + rs * segb + 16 * row);
-        dw[rs][j] = h2f_bits(v & 0xFFFFu);
-        dmw[rs][j] = h2f_bits(v >> 16);
-      } else {
-        dw[rs][j] = h2f_bits(*reinterpret_cast<const uint16_t *>(wl + rs * segb + 256 + 2 * row));
-        dmw[rs][j] = 0.0f;
-      }
-    }
+  for (int cs = 0; cs < 4; cs++) dx[cs] = *reinterpret_cast<const f32x4 *>(xd + 16 * cs + 4 * q);
   if constexpr (Q4) {
     // sumi = sum_j mn_j * bsums32_j: quarter q < 2 carries k = 8q + e ->
     // (j = 4q + e/2, half e%2) against the 16 half-block sums;
@@ -539,45 +606,125 @@ __device__ __forceinline__ void f2_block(float (&out)[2][4][4], const uint8_t *w
                      : (half8){0, 0, 0, 0, 0, 0, 0, 0};
 #pragma unroll
     for (int rs = 0; rs < 2; rs++) {
-      const uint4 hdr = *reinterpret_cast<const uint4 *>(wl + rs * segb + 16 * n);
+      const uint4 hdr = w[rs].hdr;
+      const float dw = h2f_bits(hdr.x & 0xFFFFu), dmw = h2f_bits(hdr.x >> 16);
       const uint32_t mn = q == 0 ? (hdr.z & 0x3F3F3F3Fu) : (((hdr.w >> 4) & 0x0F0F0F0Fu) | ((hdr.z >> 2) & 0x30303030u));
       const half8 am = q < 2 ? cat(dup_byte(mn, 0, 1024.0f), dup_byte(mn, 1, 1024.0f), dup_byte(mn, 2, 1024.0f),
                                    dup_byte(mn, 3, 1024.0f))
                              : (half8){0, 0, 0, 0, 0, 0, 0, 0};
 #pragma unroll
       for (int cs = 0; cs < 4; cs++) {
-        const f32x4 sm = mfma(am, bm[cs], (f32x4){0.0f, 0.0f, 0.0f, 0.0f});
+        const f32x4 sm = mfma(bm[cs], am, (f32x4){0.0f, 0.0f, 0.0f, 0.0f});
 #pragma unroll
         for (int j = 0; j < 4; j++) {
-          const float t = __builtin_fmaf(-dmw[rs][j], sm[j], dw[rs][j] * D[rs][cs][j]);
-          out[rs][cs][j] = __builtin_fmaf(dx[cs], t, out[rs][cs][j]);
+          const float t = __builtin_fmaf(-dmw, sm[j], dw * D[rs][cs][j]);
+          out[rs][cs][j] = __builtin_fmaf(dx[cs][j], t, out[rs][cs][j]);
         }
       }
     }
   } else {
 #pragma unroll
-    for (int rs = 0; rs < 2; rs++)
+    for (int rs = 0; rs < 2; rs++) {
+      const float dw = h2f_bits(w[rs].d16);
 #pragma unroll
       for (int cs = 0; cs < 4; cs++)
 #pragma unroll
-        for (int j = 0; j < 4; j++) out[rs][cs][j] = __builtin_fmaf(dx[cs], dw[rs][j] * D[rs][cs][j], out[rs][cs][j]);
+        for (int j = 0; j < 4; j++) out[rs][cs][j] = __builtin_fmaf(dx[cs][j], dw * D[rs][cs][j], out[rs][cs][j]);
+    }
   }
 }
 
-// Two workgroups per CU (LDS), so two waves per SIMD.
-// PAIR: a tile is 64 rows of gate (waves 0, 1) and the same 64 rows of up
-// (waves 2, 3); up's sums go through LDS to the gate waves, which store
-// fround(gelu(gate) * up).  total_rt then counts 64-row tiles, ksplit is 1.
+// Blocks [b0, b1) of one tile for this wave's segments s0, s1 (clamped into
+// the weight) of weight `wseg` (`wtiles` segments per block); xt is the
+// column tile's activation tiles.  Loads are unconditional (the block index
+// is clamped), so they never sit behind a branch.
+template <bool Q4>
+__device__ __forceinline__ void f3_wload2(typename WSel<Q4>::T (&w)[2], const uint8_t *wseg, int wtiles, int s0,
+                                          int s1, int b, int lane) {
+  constexpr int segb = Q4 ? 2304 : 3360;
+  const uint8_t *base = wseg + (size_t)b * wtiles * segb;
+  f3_wload<Q4>(w[0], base + (size_t)s0 * segb, lane);
+  f3_wload<Q4>(w[1], base + (size_t)s1 * segb, lane);
+}
+
+// The two activation-tile stages.  Two distinct arrays, so the compiler sees
+// that a direct global->LDS copy into one does not touch reads of the other
+// and issues no wait for it.
+__shared__ __align__(16) uint8_t f3_st0[kF2XTile];
+__shared__ __align__(16) uint8_t f3_st1[kF2XTile];
+
+// Copies activation tile b into a stage with direct global->LDS loads (1 KB
+// per wave and load; chunk c by wave c % 8).  Branch-free: chunk indices past
+// the end repeat the last whole chunk (the same bytes to the same place).
+__device__ __forceinline__ void f3_xcopy(const uint8_t *xt, int b, uint8_t *stage, int wave, int lane) {
+  const uint8_t *src = xt + (size_t)b * kF2XTile;
+#pragma unroll
+  for (int i = 0; i < (kF3Full + kF3Waves - 1) / kF3Waves; i++) {
+    const int c = min(wave + i * kF3Waves, kF3Full - 1);
+    __builtin_amdgcn_global_load_lds(reinterpret_cast<const void *>(src + c * 1024 + 16 * lane),
+                                     (__attribute__((address_space(3))) void *)(stage + c * 1024), 16, 0, 0);
+  }
+  if (wave == kF3Full % kF3Waves && 16 * lane < kF3Part)
+    __builtin_amdgcn_global_load_lds(reinterpret_cast<const void *>(src + kF3Full * 1024 + 16 * lane),
+                                     (__attribute__((address_space(3))) void *)(stage + kF3Full * 1024), 16, 0, 0);
+}
+
+// Blocks [b0, b1) of one tile for this wave's segments s0, s1 (clamped into
+// the weight) of weight `wseg` (`wtiles` segments per block); xt is the
+// column tile's activation tiles.  Loads are unconditional (the block index
+// is clamped), so they never sit behind a branch; every copy has landed
+// (vmcnt(0)) before the barrier that ends its block.
+template <bool Q4>
+__device__ __forceinline__ void f3_tile(float (&out)[2][4][4], const uint8_t *wseg, int wtiles, int s0, int s1,
+                                        const uint8_t *xt, int b0, int b1) {
+  if (b1 <= b0) return;  // (block ranges hold at least two blocks)
+  const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  typename WSel<Q4>::T wa[2], wb[2];
+  f3_xcopy(xt, b0, f3_st0, wave, lane);
+  f3_wload2<Q4>(wa, wseg, wtiles, s0, s1, b0, lane);
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  for (int b = b0;; b += 2) {
+    const int bn = min(b + 1, b1 - 1);
+    f3_xcopy(xt, bn, f3_st1, wave, lane);
+    f3_wload2<Q4>(wb, wseg, wtiles, s0, s1, bn, lane);
+    __builtin_amdgcn_sched_barrier(0);  // the loads stay ahead of the block's compute
+    f3_block<Q4>(out, wa, f3_st0, lane);
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    if (b + 1 >= b1) break;
+    const int bn2 = min(b + 2, b1 - 1);
+    f3_xcopy(xt, bn2, f3_st0, wave, lane);
+    f3_wload2<Q4>(wa, wseg, wtiles, s0, s1, bn2, lane);
+    __builtin_amdgcn_sched_barrier(0);
+    f3_block<Q4>(out, wb, f3_st1, lane);
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    if (b + 2 >= b1) break;
+  }
+}
+
+// One workgroup per CU (8 waves, two per SIMD).
+// PAIR: a tile is 128 rows of gate (waves 0-3) and the same 128 rows of up
+// (waves 4-7); up's sums go through LDS to the gate wave of the same rows,
+// which stores fround(gelu(gate) * up).  total_rt then counts 128-row tiles,
+// ksplit is 1.
 template <bool PAIR>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void kquant_prefill_fast_kernel(
+__global__ __launch_bounds__(kF3Threads) __attribute__((amdgpu_waves_per_eu(2, 2))) void kquant_prefill_fast_kernel(
     const F2Args a) {
-  extern __shared__ __align__(16) uint8_t smem[];
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int tiles = a.total_rt * a.col_tiles;
   const int items = tiles * a.ksplit;
+  // XCD-aware order: workgroup i runs on XCD i % 8 and the grid is a
+  // multiple of 8, so item `it` runs on XCD it % 8; each XCD takes a
+  // contiguous run of the (block range, row tile, column tile) order, so the
+  // column tiles of one row tile share its weights in that XCD's L2.
+  const int per = items / 8, rem = items % 8;
   for (int it = blockIdx.x; it < items; it += gridDim.x) {
-    const int kr = it / tiles, t2 = it - kr * tiles;
+    const int x = it & 7, j = it >> 3;
+    const int nat = x < rem ? x * (per + 1) + j : rem * (per + 1) + (x - rem) * per + j;
+    const int kr = nat / tiles, t2 = nat - kr * tiles;
     const int rt = t2 / a.col_tiles, ct = t2 - rt * a.col_tiles;
     const int b_begin = (int)((long long)kr * a.nb / a.ksplit), b_end = (int)((long long)(kr + 1) * a.nb / a.ksplit);
     PfWeight W = a.w[0];
@@ -588,14 +735,13 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
       if (a.count > 3 && rt >= a.w[3].rt_begin) W = a.w[3], poff = a.part_off[3];
     }
     float *dst = a.ksplit > 1 ? a.part + kr * a.part_stride + poff : W.out;
-    const bool q4 = W.type == kTypeQ4K;
-    const int segb = q4 ? 2304 : 3360;
-    constexpr int kTileSegs = PAIR ? 4 : 8;  // 16-row segments per weight and tile
+    constexpr int kTileSegs = PAIR ? kF3Segs / 2 : kF3Segs;  // 16-row segments per weight and tile
     const int T0 = kTileSegs * (rt - W.rt_begin);
     const int nseg_tile = W.tiles - T0 < kTileSegs ? W.tiles - T0 : kTileSegs;
-    const int wbytes = nseg_tile * segb;
-    const int my_seg = PAIR ? 2 * (wave & 1) : 2 * wave;  // within this wave's weight
+    const int my_seg = PAIR ? 2 * (wave & 3) : 2 * wave;                 // within this wave's weight
     const int nseg = nseg_tile - my_seg >= 2 ? 2 : nseg_tile - my_seg;  // this wave's live segments (<= 0: none)
+    const int s0 = min(T0 + my_seg, W.tiles - 1), s1 = min(T0 + my_seg + 1, W.tiles - 1);
+    const uint8_t *wseg = PAIR && wave >= 4 ? a.w[1].seg : W.seg;
     float out[2][4][4];
 #pragma unroll
     for (int rs = 0; rs < 2; rs++)
@@ -604,26 +750,16 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
 #pragma unroll
         for (int j = 0; j < 4; j++) out[rs][cs][j] = 0.0f;
     const uint8_t *xt = a.xt + (size_t)ct * a.nb * kF2XTile;
-    // one LDS stage: load, compute, repeat; the other workgroup on the CU
-    // computes while this one loads
-    for (int b = b_begin; b < b_end; b++) {
-      lds_copy(W.seg + ((size_t)b * W.tiles + T0) * segb, smem, wbytes, wave, lane);
-      if (PAIR) lds_copy(a.w[1].seg + ((size_t)b * W.tiles + T0) * segb, smem + 4 * segb, wbytes, wave, lane);
-      lds_copy(xt + (size_t)b * kF2XTile, smem + kF2W, kF2XTile, wave, lane);
-      __builtin_amdgcn_s_waitcnt(0);
-      __syncthreads();
-      if (nseg > 0) {
-        if (q4)
-          f2_block<true>(out, smem + 2 * wave * segb, smem + kF2W, lane);
-        else
-          f2_block<false>(out, smem + 2 * wave * segb, smem + kF2W, lane);
-      }
-      __syncthreads();
-    }
+    if (W.type == kTypeQ4K)
+      f3_tile<true>(out, wseg, W.tiles, s0, s1, xt, b_begin, b_end);
+    else
+      f3_tile<false>(out, wseg, W.tiles, s0, s1, xt, b_begin, b_end);
+    const int n = lane & 15, q = lane >> 4;
     if (PAIR) {
-      // up waves hand their sums to the gate wave of the same rows
-      float *xch = reinterpret_cast<float *>(smem) + (wave & 1) * 32 * 64 + lane;
-      if (wave >= 2) {
+      // up waves hand their sums to the gate wave of the same rows (the
+      // stages are free: the tile's last barrier has passed)
+      float *xch = reinterpret_cast<float *>(f3_st0) + (wave & 3) * 32 * 64 + lane;
+      if (wave >= 4) {
 #pragma unroll
         for (int rs = 0; rs < 2; rs++)
 #pragma unroll
@@ -632,36 +768,34 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
             for (int j = 0; j < 4; j++) xch[((rs * 4 + cs) * 4 + j) * 64] = out[rs][cs][j];
       }
       __syncthreads();
-      if (wave < 2 && nseg > 0) {
-        const int n = lane & 15, q = lane >> 4;
+      if (wave < 4 && nseg > 0) {
 #pragma unroll
-        for (int rs = 0; rs < 2; rs++)
+        for (int rs = 0; rs < 2; rs++) {
+          const int row = 16 * (T0 + my_seg + rs) + n;
 #pragma unroll
-          for (int cs = 0; cs < 4; cs++) {
-            const int m = ct * kF2Cols + 16 * cs + n;
+          for (int cs = 0; cs < 4; cs++)
 #pragma unroll
             for (int j = 0; j < 4; j++) {
-              const int row = 16 * (T0 + my_seg + rs) + 4 * q + j;
+              const int m = ct * kF2Cols + 16 * cs + 4 * q + j;
               const float up = xch[((rs * 4 + cs) * 4 + j) * 64];
               if (rs < nseg && row < W.rows && m < a.cols)
                 a.pair_out[(size_t)m * W.rows + row] = geglu_ts(out[rs][cs][j], up, a.gelu_c);
             }
-          }
+        }
       }
-      __syncthreads();  // the next tile's copies overwrite the exchange
+      __syncthreads();  // the next tile's first stage overwrites the exchange
     } else if (nseg > 0) {
-      const int n = lane & 15, q = lane >> 4;
 #pragma unroll
-      for (int rs = 0; rs < 2; rs++)
+      for (int rs = 0; rs < 2; rs++) {
+        const int row = 16 * (T0 + my_seg + rs) + n;
 #pragma unroll
-        for (int cs = 0; cs < 4; cs++) {
-          const int m = ct * kF2Cols + 16 * cs + n;
+        for (int cs = 0; cs < 4; cs++)
 #pragma unroll
           for (int j = 0; j < 4; j++) {
-            const int row = 16 * (T0 + my_seg + rs) + 4 * q + j;
+            const int m = ct * kF2Cols + 16 * cs + 4 * q + j;
             if (rs < nseg && row < W.rows && m < a.cols) dst[(size_t)m * W.rows + row] = out[rs][cs][j];
           }
-        }
+      }
     }
   }
 }
@@ -721,7 +855,7 @@ F2Shape f2_shape(const MfmaLaunch &l, int num_cus) {
   sh.nb = l.k / kQK;
   sh.col_tiles = (l.cols + kF2Cols - 1) / kF2Cols;
   for (int i = 0; i < l.count; i++) {
-    sh.total_rt += ((l.rows[i] + 15) / 16 + 7) / 8;
+    sh.total_rt += ((l.rows[i] + 15) / 16 + kF3Segs - 1) / kF3Segs;
     sh.outs += (size_t)l.cols * l.rows[i];
   }
   sh.ks = f2_ksplit(sh.total_rt * sh.col_tiles, sh.nb, num_cus);
@@ -747,19 +881,6 @@ hipError_t launch_q8k_prefill(const float *x, int k, int cols, uint8_t *scratch,
 
 size_t prefill_lds_bytes() { return kPfLds; }
 
-// The fast kernels' dynamic LDS above the default limit (once per process).
-static hipError_t f2_set_lds() {
-  static bool done = false;
-  if (done) return hipSuccess;
-  hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(kquant_prefill_fast_kernel<false>),
-                                     hipFuncAttributeMaxDynamicSharedMemorySize, kF2Lds);
-  if (e == hipSuccess)
-    e = hipFuncSetAttribute(reinterpret_cast<const void *>(kquant_prefill_fast_kernel<true>),
-                            hipFuncAttributeMaxDynamicSharedMemorySize, kF2Lds);
-  if (e == hipSuccess) done = true;
-  return e;
-}
-
 size_t prefill_fast_geglu_bytes(int k, int cols) {
   return (size_t)((cols + kF2Cols - 1) / kF2Cols) * (k / kQK) * kF2XTile;
 }
@@ -784,7 +905,7 @@ hipError_t launch_prefill_fast_geglu(const MfmaLaunch &l, const float *x, uint8_
     a.w[i].tiles = (l.rows[i] + 15) / 16;
     a.w[i].rt_begin = 0;
   }
-  a.total_rt = (a.w[0].tiles + 3) / 4;
+  a.total_rt = (a.w[0].tiles + kF3Segs / 2 - 1) / (kF3Segs / 2);
   a.col_tiles = col_tiles;
   a.nb = nb;
   a.cols = l.cols;
@@ -792,11 +913,9 @@ hipError_t launch_prefill_fast_geglu(const MfmaLaunch &l, const float *x, uint8_
   a.ksplit = 1;
   a.pair_out = out;
   a.gelu_c = gelu_c;
-  e = f2_set_lds();
-  if (e != hipSuccess) return e;
   const long long items = (long long)a.total_rt * a.col_tiles;
-  const int grid = (int)(items < 2LL * num_cus ? items : 2LL * num_cus);
-  hipLaunchKernelGGL(kquant_prefill_fast_kernel<true>, dim3(grid), dim3(256), kF2Lds, s, a);
+  const int grid = (int)(items < num_cus ? items : num_cus);
+  hipLaunchKernelGGL(kquant_prefill_fast_kernel<true>, dim3(grid), dim3(kF3Threads), 0, s, a);
   return hipGetLastError();
 }
 
@@ -808,7 +927,7 @@ size_t prefill_fast_bytes(const MfmaLaunch &l, int num_cus) {
   return xt + (sh.ks > 1 ? (size_t)sh.ks * sh.stride * sizeof(float) : 0);
 }
 
-size_t prefill_fast_lds_bytes() { return kF2Lds; }
+size_t prefill_fast_lds_bytes() { return 2 * (size_t)kF2XTile; }  // the two static stages
 
 hipError_t launch_prefill_fast(const MfmaLaunch &l, const float *x, uint8_t *scratch, int num_cus, hipStream_t s) {
   if (l.count < 1 || l.count > kMaxWeights || l.cols < 1 || l.k % kQK != 0) return hipErrorInvalidValue;
@@ -829,7 +948,7 @@ hipError_t launch_prefill_fast(const MfmaLaunch &l, const float *x, uint8_t *scr
     a.w[i].rows = l.rows[i];
     a.w[i].tiles = (l.rows[i] + 15) / 16;
     a.w[i].rt_begin = rt;
-    rt += (a.w[i].tiles + 7) / 8;
+    rt += (a.w[i].tiles + kF3Segs - 1) / kF3Segs;
     a.part_off[i] = off;
     off += (size_t)l.cols * l.rows[i];
   }
@@ -841,11 +960,9 @@ hipError_t launch_prefill_fast(const MfmaLaunch &l, const float *x, uint8_t *scr
   a.ksplit = sh.ks;
   a.part = reinterpret_cast<float *>(scratch + (size_t)col_tiles * nb * kF2XTile);
   a.part_stride = sh.stride;
-  e = f2_set_lds();
-  if (e != hipSuccess) return e;
   const long long items = (long long)a.total_rt * a.col_tiles * a.ksplit;
-  const int grid = (int)(items < 2LL * num_cus ? items : 2LL * num_cus);
-  hipLaunchKernelGGL(kquant_prefill_fast_kernel<false>, dim3(grid), dim3(256), kF2Lds, s, a);
+  const int grid = (int)(items < num_cus ? items : num_cus);
+  hipLaunchKernelGGL(kquant_prefill_fast_kernel<false>, dim3(grid), dim3(kF3Threads), 0, s, a);
   if (a.ksplit == 1) return hipGetLastError();
   e = hipGetLastError();
   if (e != hipSuccess) return e;

@@ -112,7 +112,7 @@ def repack_mfma(type_id, raw, rows, k):
                                     v = 0
                                     for jj in range(4):
                                         v |= (q6[elem(4 * h + jj, cc, l)] >> 4) << (2 * jj)
-                                    off = base + 288 + (2 * 64 + i) * 16 + 4 * (2 * cls + h) + cc
+                                    off = base + 288 + (2 * 64 + i) * 16 + 4 * (2 * h + cls) + cc
                                     out[off] = v
                                     written[off] += 1
     return out, written
@@ -134,7 +134,7 @@ def lane_a_fragment(type_id, seg, i, g, u):
     sc = seg[16 * rho: 16 * rho + 16].view(np.int8).astype(np.int64)
     dw = seg[288 + (g * 64 + i) * 16 + 4 * u: 288 + (g * 64 + i) * 16 + 4 * u + 4]
     h = u // 2
-    qh = seg[288 + (2 * 64 + i) * 16 + 4 * (2 * g + h): 288 + (2 * 64 + i) * 16 + 4 * (2 * g + h) + 4]
+    qh = seg[288 + (2 * 64 + i) * 16 + 4 * (2 * h + g): 288 + (2 * 64 + i) * 16 + 4 * (2 * h + g) + 4]
     vals = []
     for half, j in ((0, 2 * u), (1, 2 * u + 1)):
         jj = j - 4 * h
