@@ -370,9 +370,10 @@ __global__ __launch_bounds__(256) void kquant_prefill_kernel(const PfArgs a) {
 // come with the lane's own header load.
 constexpr int kF2Cols = 64;
 constexpr int kF2XTile = 32768 + 2048 + 256;  // 35,072 bytes per (column tile, block)
-constexpr int kF3Waves = 8;
+constexpr int kF3Waves = 8;                                          // two per SIMD
+constexpr int kF3RS = 2;                                             // 16-row segments per wave
 constexpr int kF3Threads = 64 * kF3Waves;
-constexpr int kF3Segs = 2 * kF3Waves;                                // segments per workgroup tile
+constexpr int kF3Segs = kF3RS * kF3Waves;                            // segments per workgroup tile
 constexpr int kF3Full = kF2XTile / 1024;                             // whole 1 KB chunks per activation tile
 constexpr int kF3Part = kF2XTile % 1024;                             // bytes of the last, partial chunk
 
@@ -520,17 +521,17 @@ __device__ __forceinline__ half8 f3_a(const typename WSel<Q4>::T &w, const uint3
   }
 }
 
-// One block of the wave's 32 x 64 tile: weights w (two segments) against the
-// activation tile at xl.  A wave whose second segment lies past the weight's
-// end computes on a repeat of its first and never stores it.
+// One block of the wave's tile (kF3RS segments x 64 columns): weights w
+// against the activation tile at xl.  Segments past the weight's end repeat
+// the last one and are never stored.
 template <bool Q4>
-__device__ __forceinline__ void f3_block(float (&out)[2][4][4], const typename WSel<Q4>::T (&w)[2],
+__device__ __forceinline__ void f3_block(float (&out)[kF3RS][4][4], const typename WSel<Q4>::T (&w)[kF3RS],
                                          const uint8_t *xl, int lane) {
   const int n = lane & 15, q = lane >> 4;
   const _Float16 *xh = reinterpret_cast<const _Float16 *>(xl);
-  half2v S[2][4], N[2][4];
+  half2v S[kF3RS][4], N[kF3RS][4];
 #pragma unroll
-  for (int rs = 0; rs < 2; rs++) {
+  for (int rs = 0; rs < kF3RS; rs++) {
     if constexpr (Q4) {
       const uint4 hdr = w[rs].hdr;
       const uint32_t sclo = hdr.y & 0x3F3F3F3Fu;
@@ -552,9 +553,9 @@ __device__ __forceinline__ void f3_block(float (&out)[2][4][4], const typename W
       }
     }
   }
-  uint32_t qd[2][2][4];  // [rs][g][t]
+  uint32_t qd[kF3RS][2][4];  // [rs][g][t]
 #pragma unroll
-  for (int rs = 0; rs < 2; rs++)
+  for (int rs = 0; rs < kF3RS; rs++)
 #pragma unroll
     for (int g = 0; g < 2; g++) {
       const uint4 v = w[rs].qa[g];
@@ -564,31 +565,44 @@ __device__ __forceinline__ void f3_block(float (&out)[2][4][4], const typename W
       qd[rs][g][3] = v.w;
       f3_transpose(qd[rs][g]);
     }
-  f32x4 D[2][4];
-  // B fragments one class ahead: class l + 1's LDS reads are in flight while
-  // class l's weights unpack and its MFMAs run
+  f32x4 D[kF3RS][4];
+  // Software pipeline over the classes: while class l's MFMAs run, class
+  // l + 1's B fragments are read from LDS and its weight fragments unpacked
+  // (interleaved: one MFMA, then a few vector-ALU instructions).
   half8 B[2][4];
 #pragma unroll
   for (int cs = 0; cs < 4; cs++)
     B[0][cs] = __builtin_bit_cast(half8, *reinterpret_cast<const uint4 *>(xh + (q * kF2Cols + 16 * cs + n) * 8));
+  half8 An[kF3RS];
+#pragma unroll
+  for (int rs = 0; rs < kF3RS; rs++) An[rs] = f3_a<Q4>(w[rs], qd[rs], 0, q, S[rs], N[rs]);
 #pragma unroll
   for (int l = 0; l < 8; l++) {
+    half8 A[kF3RS];
+#pragma unroll
+    for (int rs = 0; rs < kF3RS; rs++) A[rs] = An[rs];
     if (l < 7) {
 #pragma unroll
       for (int cs = 0; cs < 4; cs++)
         B[(l + 1) & 1][cs] = __builtin_bit_cast(
             half8, *reinterpret_cast<const uint4 *>(xh + (((l + 1) * 4 + q) * kF2Cols + 16 * cs + n) * 8));
-    }
-    __builtin_amdgcn_sched_barrier(0);  // keeps the reads ahead of this class's work
-    const half8 A0 = f3_a<Q4>(w[0], qd[0], l, q, S[0], N[0]);
-    const half8 A1 = f3_a<Q4>(w[1], qd[1], l, q, S[1], N[1]);
 #pragma unroll
-    for (int cs = 0; cs < 4; cs++) {
-      const f32x4 c0 = l == 0 ? (f32x4){0.0f, 0.0f, 0.0f, 0.0f} : D[0][cs];
-      const f32x4 c1 = l == 0 ? (f32x4){0.0f, 0.0f, 0.0f, 0.0f} : D[1][cs];
-      D[0][cs] = mfma(B[l & 1][cs], A0, c0);
-      D[1][cs] = mfma(B[l & 1][cs], A1, c1);
+      for (int rs = 0; rs < kF3RS; rs++) An[rs] = f3_a<Q4>(w[rs], qd[rs], l + 1, q, S[rs], N[rs]);
     }
+#pragma unroll
+    for (int cs = 0; cs < 4; cs++)
+#pragma unroll
+      for (int rs = 0; rs < kF3RS; rs++)
+        D[rs][cs] = mfma(B[l & 1][cs], A[rs], l == 0 ? (f32x4){0.0f, 0.0f, 0.0f, 0.0f} : D[rs][cs]);
+    if (l < 7) {
+      __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);  // the 4 B reads first
+#pragma unroll
+      for (int k = 0; k < 4 * kF3RS; k++) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
+        __builtin_amdgcn_sched_group_barrier(0x002, 3, 0);  // up to 3 vector-ALU
+      }
+    }
+    __builtin_amdgcn_sched_barrier(0);
   }
   const float *xd = reinterpret_cast<const float *>(xl + 32768 + 2048);
   f32x4 dx[4];
@@ -596,22 +610,24 @@ __device__ __forceinline__ void f3_block(float (&out)[2][4][4], const typename W
   for (int cs = 0; cs < 4; cs++) dx[cs] = *reinterpret_cast<const f32x4 *>(xd + 16 * cs + 4 * q);
   if constexpr (Q4) {
     // sumi = sum_j mn_j * bsums32_j: quarter q < 2 carries k = 8q + e ->
-    // (j = 4q + e/2, half e%2) against the 16 half-block sums;
-    // out += dx * (dw * D - dmin * sumi)
+    // (j = 4q + e/2, half e%2) against the 16 half-block sums (zero operands
+    // in quarters 2, 3); out += dx * (dw * D - dmin * sumi)
     const _Float16 *xb = reinterpret_cast<const _Float16 *>(xl + 32768);
+    const bool lo = q < 2;
     half8 bm[4];
 #pragma unroll
-    for (int cs = 0; cs < 4; cs++)
-      bm[cs] = q < 2 ? __builtin_bit_cast(half8, *reinterpret_cast<const uint4 *>(xb + ((q * kF2Cols) + 16 * cs + n) * 8))
-                     : (half8){0, 0, 0, 0, 0, 0, 0, 0};
+    for (int cs = 0; cs < 4; cs++) {
+      const uint4 v = *reinterpret_cast<const uint4 *>(xb + (((q & 1) * kF2Cols) + 16 * cs + n) * 8);
+      bm[cs] = __builtin_bit_cast(half8, lo ? v : make_uint4(0, 0, 0, 0));
+    }
 #pragma unroll
-    for (int rs = 0; rs < 2; rs++) {
+    for (int rs = 0; rs < kF3RS; rs++) {
       const uint4 hdr = w[rs].hdr;
       const float dw = h2f_bits(hdr.x & 0xFFFFu), dmw = h2f_bits(hdr.x >> 16);
-      const uint32_t mn = q == 0 ? (hdr.z & 0x3F3F3F3Fu) : (((hdr.w >> 4) & 0x0F0F0F0Fu) | ((hdr.z >> 2) & 0x30303030u));
-      const half8 am = q < 2 ? cat(dup_byte(mn, 0, 1024.0f), dup_byte(mn, 1, 1024.0f), dup_byte(mn, 2, 1024.0f),
-                                   dup_byte(mn, 3, 1024.0f))
-                             : (half8){0, 0, 0, 0, 0, 0, 0, 0};
+      const uint32_t mn0 = hdr.z & 0x3F3F3F3Fu, mn1 = ((hdr.w >> 4) & 0x0F0F0F0Fu) | ((hdr.z >> 2) & 0x30303030u);
+      const uint32_t mn = q == 0 ? mn0 : mn1;
+      half8 am = cat(dup_byte(mn, 0, 1024.0f), dup_byte(mn, 1, 1024.0f), dup_byte(mn, 2, 1024.0f),
+                     dup_byte(mn, 3, 1024.0f));
 #pragma unroll
       for (int cs = 0; cs < 4; cs++) {
         const f32x4 sm = mfma(bm[cs], am, (f32x4){0.0f, 0.0f, 0.0f, 0.0f});
@@ -624,7 +640,7 @@ __device__ __forceinline__ void f3_block(float (&out)[2][4][4], const typename W
     }
   } else {
 #pragma unroll
-    for (int rs = 0; rs < 2; rs++) {
+    for (int rs = 0; rs < kF3RS; rs++) {
       const float dw = h2f_bits(w[rs].d16);
 #pragma unroll
       for (int cs = 0; cs < 4; cs++)
@@ -634,17 +650,15 @@ __device__ __forceinline__ void f3_block(float (&out)[2][4][4], const typename W
   }
 }
 
-// Blocks [b0, b1) of one tile for this wave's segments s0, s1 (clamped into
-// the weight) of weight `wseg` (`wtiles` segments per block); xt is the
-// column tile's activation tiles.  Loads are unconditional (the block index
-// is clamped), so they never sit behind a branch.
+// The wave's segments s0 .. s0 + kF3RS - 1 (each clamped to the weight's last)
+// of block b.
 template <bool Q4>
-__device__ __forceinline__ void f3_wload2(typename WSel<Q4>::T (&w)[2], const uint8_t *wseg, int wtiles, int s0,
-                                          int s1, int b, int lane) {
+__device__ __forceinline__ void f3_wloads(typename WSel<Q4>::T (&w)[kF3RS], const uint8_t *wseg, int wtiles, int s0,
+                                          int b, int lane) {
   constexpr int segb = Q4 ? 2304 : 3360;
   const uint8_t *base = wseg + (size_t)b * wtiles * segb;
-  f3_wload<Q4>(w[0], base + (size_t)s0 * segb, lane);
-  f3_wload<Q4>(w[1], base + (size_t)s1 * segb, lane);
+#pragma unroll
+  for (int rs = 0; rs < kF3RS; rs++) f3_wload<Q4>(w[rs], base + (size_t)min(s0 + rs, wtiles - 1) * segb, lane);
 }
 
 // The two activation-tile stages.  Two distinct arrays, so the compiler sees
@@ -654,8 +668,9 @@ __shared__ __align__(16) uint8_t f3_st0[kF2XTile];
 __shared__ __align__(16) uint8_t f3_st1[kF2XTile];
 
 // Copies activation tile b into a stage with direct global->LDS loads (1 KB
-// per wave and load; chunk c by wave c % 8).  Branch-free: chunk indices past
-// the end repeat the last whole chunk (the same bytes to the same place).
+// per wave and load; chunk c by wave c % kF3Waves).  Branch-free: chunk
+// indices past the end repeat the last whole chunk (the same bytes to the
+// same place).
 __device__ __forceinline__ void f3_xcopy(const uint8_t *xt, int b, uint8_t *stage, int wave, int lane) {
   const uint8_t *src = xt + (size_t)b * kF2XTile;
 #pragma unroll
@@ -669,25 +684,25 @@ __device__ __forceinline__ void f3_xcopy(const uint8_t *xt, int b, uint8_t *stag
                                      (__attribute__((address_space(3))) void *)(stage + kF3Full * 1024), 16, 0, 0);
 }
 
-// Blocks [b0, b1) of one tile for this wave's segments s0, s1 (clamped into
-// the weight) of weight `wseg` (`wtiles` segments per block); xt is the
-// column tile's activation tiles.  Loads are unconditional (the block index
-// is clamped), so they never sit behind a branch; every copy has landed
-// (vmcnt(0)) before the barrier that ends its block.
+// Blocks [b0, b1) of one tile for this wave's segments from s0 of weight
+// `wseg` (`wtiles` segments per block); xt is the column tile's activation
+// tiles.  Loads are unconditional (the block index is clamped), so they
+// never sit behind a branch; every copy has landed (vmcnt(0)) before the
+// barrier that ends its block.
 template <bool Q4>
-__device__ __forceinline__ void f3_tile(float (&out)[2][4][4], const uint8_t *wseg, int wtiles, int s0, int s1,
+__device__ __forceinline__ void f3_tile(float (&out)[kF3RS][4][4], const uint8_t *wseg, int wtiles, int s0,
                                         const uint8_t *xt, int b0, int b1) {
   if (b1 <= b0) return;  // (block ranges hold at least two blocks)
   const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  typename WSel<Q4>::T wa[2], wb[2];
+  typename WSel<Q4>::T wa[kF3RS], wb[kF3RS];
   f3_xcopy(xt, b0, f3_st0, wave, lane);
-  f3_wload2<Q4>(wa, wseg, wtiles, s0, s1, b0, lane);
+  f3_wloads<Q4>(wa, wseg, wtiles, s0, b0, lane);
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
   for (int b = b0;; b += 2) {
     const int bn = min(b + 1, b1 - 1);
     f3_xcopy(xt, bn, f3_st1, wave, lane);
-    f3_wload2<Q4>(wb, wseg, wtiles, s0, s1, bn, lane);
+    f3_wloads<Q4>(wb, wseg, wtiles, s0, bn, lane);
     __builtin_amdgcn_sched_barrier(0);  // the loads stay ahead of the block's compute
     f3_block<Q4>(out, wa, f3_st0, lane);
     __builtin_amdgcn_s_waitcnt(0);
@@ -695,7 +710,7 @@ __device__ __forceinline__ void f3_tile(float (&out)[2][4][4], const uint8_t *ws
     if (b + 1 >= b1) break;
     const int bn2 = min(b + 2, b1 - 1);
     f3_xcopy(xt, bn2, f3_st0, wave, lane);
-    f3_wload2<Q4>(wa, wseg, wtiles, s0, s1, bn2, lane);
+    f3_wloads<Q4>(wa, wseg, wtiles, s0, bn2, lane);
     __builtin_amdgcn_sched_barrier(0);
     f3_block<Q4>(out, wb, f3_st1, lane);
     __builtin_amdgcn_s_waitcnt(0);
@@ -704,23 +719,25 @@ __device__ __forceinline__ void f3_tile(float (&out)[2][4][4], const uint8_t *ws
   }
 }
 
-// One workgroup per CU (8 waves, two per SIMD).
-// PAIR: a tile is 128 rows of gate (waves 0-3) and the same 128 rows of up
-// (waves 4-7); up's sums go through LDS to the gate wave of the same rows,
-// which stores fround(gelu(gate) * up).  total_rt then counts 128-row tiles,
-// ksplit is 1.
+// One workgroup per CU (kF3Waves waves, kF3Waves / 4 per SIMD).  PAIR: a tile is kF3Segs / 2 segments of gate (the first
+// half of the waves) and the same rows of up (the second half); up's sums go
+// through LDS to the gate wave of the same rows, which stores
+// fround(gelu(gate) * up).  total_rt then counts those tiles, ksplit is 1.
 template <bool PAIR>
-__global__ __launch_bounds__(kF3Threads) __attribute__((amdgpu_waves_per_eu(2, 2))) void kquant_prefill_fast_kernel(
+__global__ __launch_bounds__(kF3Threads) __attribute__((amdgpu_waves_per_eu(kF3Waves / 4, kF3Waves / 4))) void
+kquant_prefill_fast_kernel(
     const F2Args a) {
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int tiles = a.total_rt * a.col_tiles;
   const int items = tiles * a.ksplit;
   // XCD-aware order: workgroup i runs on XCD i % 8 and the grid is a
-  // multiple of 8, so item `it` runs on XCD it % 8; each XCD takes a
-  // contiguous run of the (block range, row tile, column tile) order, so the
-  // column tiles of one row tile share its weights in that XCD's L2.
+  // multiple of 8 (or one item per workgroup), so item `it` runs on XCD it %
+  // 8; each XCD takes a contiguous run of the (block range, row tile, column
+  // tile) order, so the column tiles of one row tile share its weights in
+  // that XCD's L2.
   const int per = items / 8, rem = items % 8;
+  constexpr int kHalf = kF3Waves / 2;
   for (int it = blockIdx.x; it < items; it += gridDim.x) {
     const int x = it & 7, j = it >> 3;
     const int nat = x < rem ? x * (per + 1) + j : rem * (per + 1) + (x - rem) * per + j;
@@ -738,39 +755,38 @@ __global__ __launch_bounds__(kF3Threads) __attribute__((amdgpu_waves_per_eu(2, 2
     constexpr int kTileSegs = PAIR ? kF3Segs / 2 : kF3Segs;  // 16-row segments per weight and tile
     const int T0 = kTileSegs * (rt - W.rt_begin);
     const int nseg_tile = W.tiles - T0 < kTileSegs ? W.tiles - T0 : kTileSegs;
-    const int my_seg = PAIR ? 2 * (wave & 3) : 2 * wave;                 // within this wave's weight
-    const int nseg = nseg_tile - my_seg >= 2 ? 2 : nseg_tile - my_seg;  // this wave's live segments (<= 0: none)
-    const int s0 = min(T0 + my_seg, W.tiles - 1), s1 = min(T0 + my_seg + 1, W.tiles - 1);
-    const uint8_t *wseg = PAIR && wave >= 4 ? a.w[1].seg : W.seg;
-    float out[2][4][4];
+    const int my_seg = kF3RS * (PAIR ? wave % kHalf : wave);  // within this wave's weight
+    const int nseg = nseg_tile - my_seg;                       // this wave's live segments (<= 0: none)
+    const uint8_t *wseg = PAIR && wave >= kHalf ? a.w[1].seg : W.seg;
+    float out[kF3RS][4][4];
 #pragma unroll
-    for (int rs = 0; rs < 2; rs++)
+    for (int rs = 0; rs < kF3RS; rs++)
 #pragma unroll
       for (int cs = 0; cs < 4; cs++)
 #pragma unroll
         for (int j = 0; j < 4; j++) out[rs][cs][j] = 0.0f;
     const uint8_t *xt = a.xt + (size_t)ct * a.nb * kF2XTile;
     if (W.type == kTypeQ4K)
-      f3_tile<true>(out, wseg, W.tiles, s0, s1, xt, b_begin, b_end);
+      f3_tile<true>(out, wseg, W.tiles, T0 + my_seg, xt, b_begin, b_end);
     else
-      f3_tile<false>(out, wseg, W.tiles, s0, s1, xt, b_begin, b_end);
+      f3_tile<false>(out, wseg, W.tiles, T0 + my_seg, xt, b_begin, b_end);
     const int n = lane & 15, q = lane >> 4;
     if (PAIR) {
       // up waves hand their sums to the gate wave of the same rows (the
       // stages are free: the tile's last barrier has passed)
-      float *xch = reinterpret_cast<float *>(f3_st0) + (wave & 3) * 32 * 64 + lane;
-      if (wave >= 4) {
+      float *xch = reinterpret_cast<float *>(f3_st0) + (wave % kHalf) * (kF3RS * 16) * 64 + lane;
+      if (wave >= kHalf) {
 #pragma unroll
-        for (int rs = 0; rs < 2; rs++)
+        for (int rs = 0; rs < kF3RS; rs++)
 #pragma unroll
           for (int cs = 0; cs < 4; cs++)
 #pragma unroll
             for (int j = 0; j < 4; j++) xch[((rs * 4 + cs) * 4 + j) * 64] = out[rs][cs][j];
       }
       __syncthreads();
-      if (wave < 4 && nseg > 0) {
+      if (wave < kHalf && nseg > 0) {
 #pragma unroll
-        for (int rs = 0; rs < 2; rs++) {
+        for (int rs = 0; rs < kF3RS; rs++) {
           const int row = 16 * (T0 + my_seg + rs) + n;
 #pragma unroll
           for (int cs = 0; cs < 4; cs++)
@@ -786,7 +802,7 @@ __global__ __launch_bounds__(kF3Threads) __attribute__((amdgpu_waves_per_eu(2, 2
       __syncthreads();  // the next tile's first stage overwrites the exchange
     } else if (nseg > 0) {
 #pragma unroll
-      for (int rs = 0; rs < 2; rs++) {
+      for (int rs = 0; rs < kF3RS; rs++) {
         const int row = 16 * (T0 + my_seg + rs) + n;
 #pragma unroll
         for (int cs = 0; cs < 4; cs++)
