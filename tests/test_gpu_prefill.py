@@ -12,7 +12,7 @@ Two kernels:
   0.01 * rms(ref)) so that outputs that cancel to near zero are compared
   on the scale of their column (TOL, FLOOR below).
 Shapes cover the ways the workgroup tiles can be cut: rows not a multiple of
-16, 32 or 128 (last tiles with one segment), columns not a multiple of 64, a
+16, 32 or 256 (last tiles with one segment), columns not a multiple of 64, a
 single column, mixed Q4_K/Q6_K weights in one launch, both input sizes of
 the model and a 512-column chunk.  Launches of the fast kernel with fewer
 tiles than two per CU split each tile's blocks into ranges added by a
@@ -157,10 +157,10 @@ def test_prefill_multi_and_large_chunk(hip, oracle, selector):
 @pytest.mark.parametrize("rows,m", [(160, 96), (100, 64), (1000, 130)])
 def test_prefill_geglu(hip, oracle, selector, rows, m):
     """gate/up + GeGLU: with the exact prefill kernel GeGLU follows as its own
-    launch; with the fast one (automatic from 64 columns) each tile holds 64
+    launch; with the fast one (automatic from 64 columns) each tile holds 128
     rows of gate and the same rows of up and stores the GeGLU.  Row counts
-    leave partial 64-row tiles (160: 2 of 4 segments; 100: 3 of 4, the last
-    one partial), columns partial 64-column tiles."""
+    leave partial 128-row tiles (160: 2 of 8 segments; 100: 7 of 8, the last
+    one partial; 1000: 7 of 8), columns partial 64-column tiles."""
     k = 2560
     print(f"prefill geglu rows={rows} m={m} selector={selector}", flush=True)
     seed = S.derive(S.BASE_SEED, "prefill-geglu", rows, m)
