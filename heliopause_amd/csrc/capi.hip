@@ -648,9 +648,6 @@ int32_t run_matvec_geglu(Handle *hg, Handle *hu, const float *d_input, size_t in
   }
   if (prefill_kind(cols, f16) == 2 && hg->type == hu->type) {
     // fast prefill: gate and up rows in one tile, GeGLU in its epilogue
-    void *pre = nullptr;
-    int32_t rc = stream_scratch(stream, kScratchPrefill, prefill_fast_geglu_bytes((int)input_size, (int)cols), &pre);
-    if (rc != HP_OK) return rc;
     MfmaLaunch l{};
     l.count = 2;
     l.k = (int)input_size;
@@ -661,11 +658,14 @@ int32_t run_matvec_geglu(Handle *hg, Handle *hu, const float *d_input, size_t in
       l.type[i] = hs[i]->type;
       l.rows[i] = (int)rows;
     }
+    void *pre = nullptr;
+    int32_t rc = stream_scratch(stream, kScratchPrefill, prefill_fast_geglu_bytes(l, s.num_cus), &pre);
+    if (rc != HP_OK) return rc;
     hipEvent_t e1 = prof_begin(stream);
     HP_HIP_TRY(launch_prefill_fast_geglu(l, d_input, static_cast<uint8_t *>(pre), gelu_constant(), d_out,
                                          s.num_cus, stream));
     prof_end(HP_KERNEL_MATVEC, e1, stream);
-    s.launches += 2;
+    s.launches += prefill_fast_geglu_launches(l, s.num_cus);
     s.matmul_calls++;
     return HP_OK;
   }

@@ -201,8 +201,12 @@ size_t prefill_fast_bytes(const MfmaLaunch &l, int num_cus);
 int prefill_fast_launches(const MfmaLaunch &l, int num_cus);  // 2, or 3 with the reduction
 // Gate/up (l.w 0 and 1, same type and rows) + GeGLU with the fast prefill
 // kernel: out[m][r] = fround(gelu(gate) * up), gate and up as the fast
-// kernel computes them; prefill_fast_geglu_bytes(k, cols) of scratch.
-size_t prefill_fast_geglu_bytes(int k, int cols);
+// kernel computes them; prefill_fast_geglu_bytes(l, num_cus) of scratch.
+// When fewer than half a round of tiles trail the last full round, those
+// tiles run as two block ranges whose sums a second kernel adds before the
+// GeGLU (prefill_fast_geglu_launches: 2, or 3 with it).
+size_t prefill_fast_geglu_bytes(const MfmaLaunch &l, int num_cus);
+int prefill_fast_geglu_launches(const MfmaLaunch &l, int num_cus);
 hipError_t launch_prefill_fast_geglu(const MfmaLaunch &l, const float *x, uint8_t *scratch, double gelu_c,
                                      float *out, int num_cus, hipStream_t s);
 size_t prefill_fast_lds_bytes();

@@ -438,6 +438,11 @@ struct F2Args {
   // gate/up + GeGLU tiles (w[0] gate, w[1] up): pair_out[m][row]
   float *pair_out;
   double gelu_c;
+  // tail_full > 0 (gate/up): the items from tail_full on, fewer than half a
+  // round, run as two block ranges each; the ranges write their sums to
+  // tail_part (f2_geglu_tail_kernel adds them and applies the GeGLU)
+  int tail_full;
+  float *tail_part;
 };
 
 // One segment's weights in a lane's registers, loaded with 16- and 8-byte
@@ -719,6 +724,19 @@ __device__ __forceinline__ void f3_tile(float (&out)[kF3RS][4][4], const uint8_t
   }
 }
 
+// Work index `it` of `total` -> its place in the (block range, row tile,
+// column tile) order.  Workgroup i runs on XCD i % 8 and index it on
+// workgroup it % gridDim.x, so within each round of gridDim.x indices every
+// XCD takes a contiguous share of the order: the column tiles of one row tile
+// share its weights in that XCD's L2.
+__device__ __forceinline__ int f3_order(int it, int total) {
+  const int G = gridDim.x, base = it - it % G, size = min(G, total - base), p = it - base;
+  const int per = size / 8, rem = size % 8, x = p & 7, j = p >> 3;
+  return base + (x < rem ? x * (per + 1) + j : rem * (per + 1) + (x - rem) * per + j);
+}
+
+constexpr int kF3WaveFloats = kF3RS * 16 * 64;  // a wave's sums (out) of one tile
+
 // One workgroup per CU (kF3Waves waves, kF3Waves / 4 per SIMD).  PAIR: a tile is kF3Segs / 2 segments of gate (the first
 // half of the waves) and the same rows of up (the second half); up's sums go
 // through LDS to the gate wave of the same rows, which stores
@@ -731,19 +749,21 @@ kquant_prefill_fast_kernel(
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int tiles = a.total_rt * a.col_tiles;
   const int items = tiles * a.ksplit;
-  // XCD-aware order: workgroup i runs on XCD i % 8 and the grid is a
-  // multiple of 8 (or one item per workgroup), so item `it` runs on XCD it %
-  // 8; each XCD takes a contiguous run of the (block range, row tile, column
-  // tile) order, so the column tiles of one row tile share its weights in
-  // that XCD's L2.
-  const int per = items / 8, rem = items % 8;
+  const int full = PAIR && a.tail_full > 0 ? a.tail_full : items;
+  const int work = full + 2 * (items - full);  // trailing items as two block ranges each
   constexpr int kHalf = kF3Waves / 2;
-  for (int it = blockIdx.x; it < items; it += gridDim.x) {
-    const int x = it & 7, j = it >> 3;
-    const int nat = x < rem ? x * (per + 1) + j : rem * (per + 1) + (x - rem) * per + j;
+  for (int it = blockIdx.x; it < work; it += gridDim.x) {
+    const int nat0 = f3_order(it, work);
+    const bool split = PAIR && nat0 >= full;
+    const int hidx = nat0 - full;  // split: range hidx & 1 of item full + hidx / 2
+    const int nat = split ? full + (hidx >> 1) : nat0;
     const int kr = nat / tiles, t2 = nat - kr * tiles;
     const int rt = t2 / a.col_tiles, ct = t2 - rt * a.col_tiles;
-    const int b_begin = (int)((long long)kr * a.nb / a.ksplit), b_end = (int)((long long)(kr + 1) * a.nb / a.ksplit);
+    int b_begin = (int)((long long)kr * a.nb / a.ksplit), b_end = (int)((long long)(kr + 1) * a.nb / a.ksplit);
+    if (split) {
+      b_begin = (hidx & 1) ? a.nb / 2 : 0;
+      b_end = (hidx & 1) ? a.nb : a.nb / 2;
+    }
     PfWeight W = a.w[0];
     size_t poff = a.part_off[0];
     if (!PAIR) {
@@ -771,7 +791,15 @@ kquant_prefill_fast_kernel(
     else
       f3_tile<false>(out, wseg, W.tiles, T0 + my_seg, xt, b_begin, b_end);
     const int n = lane & 15, q = lane >> 4;
-    if (PAIR) {
+    if (PAIR && split) {
+      float *part = a.tail_part + ((size_t)hidx * kF3Waves + wave) * kF3WaveFloats + lane;
+#pragma unroll
+      for (int rs = 0; rs < kF3RS; rs++)
+#pragma unroll
+        for (int cs = 0; cs < 4; cs++)
+#pragma unroll
+          for (int j = 0; j < 4; j++) part[((rs * 4 + cs) * 4 + j) * 64] = out[rs][cs][j];
+    } else if (PAIR) {
       // up waves hand their sums to the gate wave of the same rows (the
       // stages are free: the tile's last barrier has passed)
       float *xch = reinterpret_cast<float *>(f3_st0) + (wave % kHalf) * (kF3RS * 16) * 64 + lane;
@@ -814,6 +842,30 @@ kquant_prefill_fast_kernel(
       }
     }
   }
+}
+
+// The gate/up items run as two block ranges (a.tail_full on): gate = range 0
+// + range 1, up likewise, then fround(gelu(gate) * up).  One thread per
+// output: (item, gate wave, sum index, lane), lane fastest.
+__global__ __launch_bounds__(256) void f2_geglu_tail_kernel(const F2Args a, int rem) {
+  constexpr int kHalf = kF3Waves / 2;
+  const int t = blockIdx.x * blockDim.x + threadIdx.x;
+  const int lane = t & 63, k = (t >> 6) % (kF3RS * 16), w = (t >> 6) / (kF3RS * 16) % kHalf;
+  const int i = (t >> 6) / (kF3RS * 16) / kHalf;
+  if (i >= rem) return;
+  const int rs = k >> 4, cs = (k >> 2) & 3, j = k & 3;  // k = (rs * 4 + cs) * 4 + j
+  const int nat = a.tail_full + i, rt = nat / a.col_tiles, ct = nat - rt * a.col_tiles;
+  const PfWeight &W = a.w[0];
+  constexpr int kTileSegs = kF3Segs / 2;
+  const int T0 = kTileSegs * rt, my_seg = kF3RS * w;
+  const int nseg = (W.tiles - T0 < kTileSegs ? W.tiles - T0 : kTileSegs) - my_seg;
+  const int n = lane & 15, q = lane >> 4;
+  const int row = 16 * (T0 + my_seg + rs) + n, m = ct * kF2Cols + 16 * cs + 4 * q + j;
+  if (rs >= nseg || row >= W.rows || m >= a.cols) return;
+  const float *p0 = a.tail_part + (size_t)(2 * i) * kF3Waves * kF3WaveFloats + k * 64 + lane;
+  const float *p1 = p0 + (size_t)kF3Waves * kF3WaveFloats;
+  const size_t gi = (size_t)w * kF3WaveFloats, ui = gi + (size_t)kHalf * kF3WaveFloats;
+  a.pair_out[(size_t)m * W.rows + row] = geglu_ts(p0[gi] + p1[gi], p0[ui] + p1[ui], a.gelu_c);
 }
 
 // out = ((part_0 + part_1) + ...) + part_{ks-1} over the launch's outputs
@@ -900,16 +952,40 @@ hipError_t launch_q8k_prefill(const float *x, int k, int cols, uint8_t *scratch,
 
 size_t prefill_lds_bytes() { return kPfLds; }
 
-size_t prefill_fast_geglu_bytes(int k, int cols) {
-  return (size_t)((cols + kF2Cols - 1) / kF2Cols) * (k / kQK) * kF2XTile;
+// gate/up launch shape: the workgroup tiles (128 rows of each weight x 64
+// columns), the grid, and where the trailing items start when fewer than
+// half a round of them remain (0: none split).
+struct F2Pair {
+  int nb, col_tiles, total_rt, items, grid, tail_full;
+};
+
+F2Pair f2_pair(const MfmaLaunch &l, int num_cus) {
+  F2Pair p{};
+  p.nb = l.k / kQK;
+  p.col_tiles = (l.cols + kF2Cols - 1) / kF2Cols;
+  p.total_rt = ((l.rows[0] + 15) / 16 + kF3Segs / 2 - 1) / (kF3Segs / 2);
+  p.items = p.total_rt * p.col_tiles;
+  p.grid = p.items < num_cus ? p.items : num_cus;
+  const int full = p.items / p.grid * p.grid, rem = p.items - full;
+  p.tail_full = rem > 0 && 2 * rem <= p.grid && p.nb >= 2 ? full : 0;
+  return p;
+}
+
+int prefill_fast_geglu_launches(const MfmaLaunch &l, int num_cus) { return f2_pair(l, num_cus).tail_full ? 3 : 2; }
+
+size_t prefill_fast_geglu_bytes(const MfmaLaunch &l, int num_cus) {
+  const F2Pair p = f2_pair(l, num_cus);
+  const size_t xt = (size_t)p.col_tiles * p.nb * kF2XTile;
+  const size_t tail = p.tail_full ? (size_t)2 * (p.items - p.tail_full) * kF3Waves * kF3WaveFloats * sizeof(float) : 0;
+  return xt + tail;
 }
 
 hipError_t launch_prefill_fast_geglu(const MfmaLaunch &l, const float *x, uint8_t *scratch, double gelu_c,
                                      float *out, int num_cus, hipStream_t s) {
   if (l.count != 2 || l.cols < 1 || l.k % kQK != 0 || l.type[0] != l.type[1] || l.rows[0] != l.rows[1])
     return hipErrorInvalidValue;
-  const int nb = l.k / kQK;
-  const int col_tiles = (l.cols + kF2Cols - 1) / kF2Cols;
+  const F2Pair p = f2_pair(l, num_cus);
+  const int nb = p.nb, col_tiles = p.col_tiles;
   hipLaunchKernelGGL(q8k_prefill_tiles16_kernel, dim3(nb, col_tiles * kF2Cols / 16), dim3(256), 0, s, x, l.k, nb,
                      l.cols, scratch);
   hipError_t e = hipGetLastError();
@@ -924,7 +1000,7 @@ hipError_t launch_prefill_fast_geglu(const MfmaLaunch &l, const float *x, uint8_
     a.w[i].tiles = (l.rows[i] + 15) / 16;
     a.w[i].rt_begin = 0;
   }
-  a.total_rt = (a.w[0].tiles + kF3Segs / 2 - 1) / (kF3Segs / 2);
+  a.total_rt = p.total_rt;
   a.col_tiles = col_tiles;
   a.nb = nb;
   a.cols = l.cols;
@@ -932,9 +1008,14 @@ hipError_t launch_prefill_fast_geglu(const MfmaLaunch &l, const float *x, uint8_
   a.ksplit = 1;
   a.pair_out = out;
   a.gelu_c = gelu_c;
-  const long long items = (long long)a.total_rt * a.col_tiles;
-  const int grid = (int)(items < num_cus ? items : num_cus);
-  hipLaunchKernelGGL(kquant_prefill_fast_kernel<true>, dim3(grid), dim3(kF3Threads), 0, s, a);
+  a.tail_full = p.tail_full;
+  a.tail_part = reinterpret_cast<float *>(scratch + (size_t)col_tiles * nb * kF2XTile);
+  hipLaunchKernelGGL(kquant_prefill_fast_kernel<true>, dim3(p.grid), dim3(kF3Threads), 0, s, a);
+  if (!p.tail_full) return hipGetLastError();
+  e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  const int rem = p.items - p.tail_full, threads = rem * (kF3Waves / 2) * kF3WaveFloats;
+  hipLaunchKernelGGL(f2_geglu_tail_kernel, dim3((threads + 255) / 256), dim3(256), 0, s, a, rem);
   return hipGetLastError();
 }
 

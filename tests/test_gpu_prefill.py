@@ -154,13 +154,15 @@ def test_prefill_multi_and_large_chunk(hip, oracle, selector):
 
 
 @pytest.mark.parametrize("selector", [4, 0], ids=["exact", "auto"], indirect=True)
-@pytest.mark.parametrize("rows,m", [(160, 96), (100, 64), (1000, 130)])
+@pytest.mark.parametrize("rows,m", [(160, 96), (100, 64), (1000, 130), (5120, 448)])
 def test_prefill_geglu(hip, oracle, selector, rows, m):
     """gate/up + GeGLU: with the exact prefill kernel GeGLU follows as its own
     launch; with the fast one (automatic from 64 columns) each tile holds 128
     rows of gate and the same rows of up and stores the GeGLU.  Row counts
     leave partial 128-row tiles (160: 2 of 8 segments; 100: 7 of 8, the last
-    one partial; 1000: 7 of 8), columns partial 64-column tiles."""
+    one partial; 1000: 7 of 8), columns partial 64-column tiles; 5120 x 448
+    makes 280 tiles, so the 24 after the first round of 256 run as two block
+    ranges added by the tail kernel."""
     k = 2560
     print(f"prefill geglu rows={rows} m={m} selector={selector}", flush=True)
     seed = S.derive(S.BASE_SEED, "prefill-geglu", rows, m)
