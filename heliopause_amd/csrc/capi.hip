@@ -105,6 +105,7 @@ struct State {
   // device address of the file-scope `scratch` array on `device`, looked up
   // by ensure_init (the allocation-free entry point's only scratch)
   uint8_t *static_scratch = nullptr;
+  uint16_t *gelu_lut = nullptr;  // the GeGLU launches' gelu table (ensure_init)
 };
 
 State &st() {
@@ -142,6 +143,8 @@ size_t row_bytes_for(int type, size_t input_size) {
   return 0;
 }
 
+double gelu_constant();
+
 int32_t ensure_init(int device) {
   State &s = st();
   if (s.ready) return HP_OK;
@@ -160,6 +163,13 @@ int32_t ensure_init(int device) {
   HP_HIP_TRY(hipGetSymbolAddress(&sym, HIP_SYMBOL(scratch)));
   if (!sym) return fail(HP_ERR_HIP, "hipGetSymbolAddress(scratch) returned null");
   s.static_scratch = static_cast<uint8_t *>(sym);
+  // the gelu table of the GeGLU launches (hp_gelu.h gelu_lut), built once
+  if (hipMalloc((void **)&s.gelu_lut, 65536 * sizeof(uint16_t)) != hipSuccess) {
+    s.gelu_lut = nullptr;
+    return fail(HP_ERR_OOM, "gelu table allocation failed");
+  }
+  HP_HIP_TRY(launch_gelu_lut(gelu_constant(), s.gelu_lut, s.stream));
+  HP_HIP_TRY(hipStreamSynchronize(s.stream));
   s.device = device;
   s.ready = true;
   return HP_OK;
@@ -662,7 +672,7 @@ int32_t run_matvec_geglu(Handle *hg, Handle *hu, const float *d_input, size_t in
     int32_t rc = stream_scratch(stream, kScratchPrefill, prefill_fast_geglu_bytes(l, s.num_cus), &pre);
     if (rc != HP_OK) return rc;
     hipEvent_t e1 = prof_begin(stream);
-    HP_HIP_TRY(launch_prefill_fast_geglu(l, d_input, static_cast<uint8_t *>(pre), gelu_constant(), d_out,
+    HP_HIP_TRY(launch_prefill_fast_geglu(l, d_input, static_cast<uint8_t *>(pre), s.gelu_lut, d_out,
                                          s.num_cus, stream));
     prof_end(HP_KERNEL_MATVEC, e1, stream);
     s.launches += prefill_fast_geglu_launches(l, s.num_cus);
@@ -678,10 +688,10 @@ int32_t run_matvec_geglu(Handle *hg, Handle *hu, const float *d_input, size_t in
   if (rc != HP_OK) return rc;
   hipEvent_t e2 = prof_begin(stream);
   if (q8img_out && s.images && cols >= 2 && rows % kQK == 0) {
-    HP_HIP_TRY(launch_geglu_q8k(outs[0], outs[1], (int)rows, (int)cols, gelu_constant(), d_out, q8img_out, stream));
+    HP_HIP_TRY(launch_geglu_q8k(outs[0], outs[1], (int)rows, (int)cols, s.gelu_lut, d_out, q8img_out, stream));
     if (q8img_written) *q8img_written = true;
   } else {
-    HP_HIP_TRY(launch_geglu(outs[0], outs[1], cols * rows, gelu_constant(), d_out, s.num_cus, stream));
+    HP_HIP_TRY(launch_geglu(outs[0], outs[1], cols * rows, s.gelu_lut, d_out, s.num_cus, stream));
   }
   prof_end(HP_KERNEL_GEGLU, e2, stream);
   s.launches++;
@@ -1153,6 +1163,8 @@ int32_t hp_hip_shutdown(void) {
     s.io_out_cap[i] = 0;
   }
   if (s.topk_out) (void)hipFree(s.topk_out);
+  if (s.gelu_lut) (void)hipFree(s.gelu_lut);
+  s.gelu_lut = nullptr;
   if (s.sample_out) (void)hipFree(s.sample_out);
   s.sample_out = nullptr;
   s.sample_out_cap = 0;
@@ -1622,7 +1634,7 @@ int32_t hp_hip_geglu_device(const float *d_gate, const float *d_up, size_t n, fl
   if (!d_gate || !d_up || !d_output) return fail(HP_ERR_ARG, "null pointer");
   hipStream_t strm = stream ? static_cast<hipStream_t>(stream) : s.stream;
   hipEvent_t e = prof_begin(strm);
-  HP_HIP_TRY(launch_geglu(d_gate, d_up, n, gelu_constant(), d_output, s.num_cus, strm));
+  HP_HIP_TRY(launch_geglu(d_gate, d_up, n, s.gelu_lut, d_output, s.num_cus, strm));
   prof_end(HP_KERNEL_GEGLU, e, strm);
   s.launches++;
   return HP_OK;
@@ -1641,7 +1653,7 @@ int32_t hp_hip_geglu(const float *gate, const float *up, size_t n, float *output
   if (rc != HP_OK) return rc;
   HP_HIP_TRY(hipMemcpyAsync(s.io_in, gate, n * 4, hipMemcpyHostToDevice, s.stream));
   HP_HIP_TRY(hipMemcpyAsync(s.io_in + n, up, n * 4, hipMemcpyHostToDevice, s.stream));
-  HP_HIP_TRY(launch_geglu(s.io_in, s.io_in + n, n, gelu_constant(), s.io_out[0], s.num_cus, s.stream));
+  HP_HIP_TRY(launch_geglu(s.io_in, s.io_in + n, n, s.gelu_lut, s.io_out[0], s.num_cus, s.stream));
   s.launches++;
   HP_HIP_TRY(hipMemcpyAsync(output, s.io_out[0], n * 4, hipMemcpyDeviceToHost, s.stream));
   HP_HIP_TRY(hipStreamSynchronize(s.stream));

@@ -14,23 +14,37 @@
 
 namespace hp {
 
+// lut[bits] = gelu of the f16 value with those bits (hp_gelu.h gelu_lut).
+__global__ __launch_bounds__(256) void gelu_lut_kernel(double c, uint16_t *__restrict__ lut) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= 65536) return;
+  const double x = (float)__builtin_bit_cast(_Float16, (uint16_t)i);
+  lut[i] = __builtin_bit_cast(uint16_t, (_Float16)gelu_of_x(x, c));
+}
+
+hipError_t launch_gelu_lut(double c, uint16_t *lut, hipStream_t s) {
+  hipLaunchKernelGGL(gelu_lut_kernel, dim3(256), dim3(256), 0, s, c, lut);
+  return hipGetLastError();
+}
+
 __global__ __launch_bounds__(256) void geglu_kernel(const float *__restrict__ gate, const float *__restrict__ up,
-                                                    size_t n, double c, float *__restrict__ out) {
+                                                    size_t n, const uint16_t *__restrict__ lut,
+                                                    float *__restrict__ out) {
   for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x)
-    out[i] = geglu_ts(gate[i], up[i], c);
+    out[i] = geglu_lut(gate[i], up[i], lut);
 }
 
 // One workgroup per 256-element block of one column: each thread takes one
 // element's GeGLU (stored to out and to LDS), then one 16-lane group
 // quantises the block from LDS into the image.
 __global__ __launch_bounds__(256) void geglu_q8k_kernel(const float *__restrict__ gate, const float *__restrict__ up,
-                                                        int rows, int blocks, double c, float *__restrict__ out,
-                                                        uint8_t *__restrict__ img) {
+                                                        int rows, int blocks, const uint16_t *__restrict__ lut,
+                                                        float *__restrict__ out, uint8_t *__restrict__ img) {
   __shared__ float hs[kQK];
   const int q = blockIdx.x, t = threadIdx.x;
   const int nb = rows / kQK, m = q / nb, b = q - m * nb;
   const size_t off = (size_t)m * rows + (size_t)b * kQK;
-  const float h = geglu_ts(gate[off + t], up[off + t], c);
+  const float h = geglu_lut(gate[off + t], up[off + t], lut);
   out[off + t] = h;
   hs[t] = h;
   __syncthreads();
@@ -46,21 +60,22 @@ __global__ __launch_bounds__(256) void geglu_q8k_kernel(const float *__restrict_
   }
 }
 
-hipError_t launch_geglu_q8k(const float *gate, const float *up, int rows, int cols, double c, float *out,
+hipError_t launch_geglu_q8k(const float *gate, const float *up, int rows, int cols, const uint16_t *lut, float *out,
                             uint8_t *q8img, hipStream_t s) {
   if (rows <= 0 || rows % kQK != 0 || cols < 1) return hipErrorInvalidValue;
   const int blocks = cols * (rows / kQK);
-  hipLaunchKernelGGL(geglu_q8k_kernel, dim3((unsigned)blocks), dim3(256), 0, s, gate, up, rows, blocks, c, out, q8img);
+  hipLaunchKernelGGL(geglu_q8k_kernel, dim3((unsigned)blocks), dim3(256), 0, s, gate, up, rows, blocks, lut, out,
+                     q8img);
   return hipGetLastError();
 }
 
-hipError_t launch_geglu(const float *gate, const float *up, size_t n, double c, float *out, int num_cus,
+hipError_t launch_geglu(const float *gate, const float *up, size_t n, const uint16_t *lut, float *out, int num_cus,
                         hipStream_t s) {
   if (n == 0) return hipSuccess;
   size_t blocks = (n + 255) / 256;
   const size_t cap = (size_t)num_cus * 8;
   if (blocks > cap) blocks = cap;
-  hipLaunchKernelGGL(geglu_kernel, dim3((unsigned)blocks), dim3(256), 0, s, gate, up, n, c, out);
+  hipLaunchKernelGGL(geglu_kernel, dim3((unsigned)blocks), dim3(256), 0, s, gate, up, n, lut, out);
   return hipGetLastError();
 }
 

@@ -207,16 +207,18 @@ int prefill_fast_launches(const MfmaLaunch &l, int num_cus);  // 2, or 3 with th
 // GeGLU (prefill_fast_geglu_launches: 2, or 3 with it).
 size_t prefill_fast_geglu_bytes(const MfmaLaunch &l, int num_cus);
 int prefill_fast_geglu_launches(const MfmaLaunch &l, int num_cus);
-hipError_t launch_prefill_fast_geglu(const MfmaLaunch &l, const float *x, uint8_t *scratch, double gelu_c,
+hipError_t launch_prefill_fast_geglu(const MfmaLaunch &l, const float *x, uint8_t *scratch, const uint16_t *gelu_lut,
                                      float *out, int num_cus, hipStream_t s);
 size_t prefill_fast_lds_bytes();
 hipError_t launch_prefill_fast(const MfmaLaunch &l, const float *x, uint8_t *scratch, int num_cus, hipStream_t s);
 
+// The gelu table (65536 f16 entries, hp_gelu.h gelu_lut) for the constant c.
+hipError_t launch_gelu_lut(double c, uint16_t *lut, hipStream_t s);
 // GeGLU of cols columns of `rows` (a multiple of 256) that also writes the
 // result as a matvec input image (q8_image_bytes(cols, rows / 256)).
-hipError_t launch_geglu_q8k(const float *gate, const float *up, int rows, int cols, double c, float *out,
+hipError_t launch_geglu_q8k(const float *gate, const float *up, int rows, int cols, const uint16_t *lut, float *out,
                             uint8_t *q8img, hipStream_t s);
-hipError_t launch_geglu(const float *gate, const float *up, size_t n, double c, float *out, int num_cus,
+hipError_t launch_geglu(const float *gate, const float *up, size_t n, const uint16_t *lut, float *out, int num_cus,
                         hipStream_t s);
 
 // Decoder-layer steps for one decode token (decode_layer.hip).  Heads are

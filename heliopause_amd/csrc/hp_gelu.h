@@ -23,11 +23,9 @@ __device__ __forceinline__ float ts_f16_round(float v) {
   return (float)(_Float16)v;  // round to nearest even
 }
 
-__device__ __forceinline__ float gelu_ts(float vf, double c) {
-  const double value = vf;
-  if (value <= -10.0) return 0.0f;
-  if (value >= 10.0) return vf;
-  const double x = ts_f16_round(vf);
+// gelu past its range checks, as a function of x = the f16 round trip of its
+// input.
+__device__ __forceinline__ float gelu_of_x(double x, double c) {
   const double t1 = (float)(c * x);
   const double x2 = (float)(x * x);
   const double t2 = (float)(0.044715 * x2);
@@ -39,9 +37,32 @@ __device__ __forceinline__ float gelu_ts(float vf, double c) {
   return ts_f16_round((float)act);
 }
 
+__device__ __forceinline__ float gelu_ts(float vf, double c) {
+  const double value = vf;
+  if (value <= -10.0) return 0.0f;
+  if (value >= 10.0) return vf;
+  return gelu_of_x(ts_f16_round(vf), c);
+}
+
+// The same gelu from a table: inside (-10, 10) the result depends only on the
+// 16 bits of x = ts_f16_round(vf), so lut[bits] = gelu_of_x(x, c) for every
+// f16 pattern (built by launch_gelu_lut; each entry is an f16 value, NaN as
+// 0x7e00) gives gelu_ts exactly, in one gather instead of f64 tanh.
+__device__ __forceinline__ float gelu_lut(float vf, const uint16_t *__restrict__ lut) {
+  const double value = vf;
+  if (value <= -10.0) return 0.0f;
+  if (value >= 10.0) return vf;
+  const uint16_t x = __builtin_bit_cast(uint16_t, (_Float16)ts_f16_round(vf));
+  return (float)__builtin_bit_cast(_Float16, lut[x]);
+}
+
 // GeGLU of one element (layers.ts:450-456): fround(gelu(gate) * up).
 __device__ __forceinline__ float geglu_ts(float gate, float up, double c) {
   return (float)((double)gelu_ts(gate, c) * (double)up);
+}
+
+__device__ __forceinline__ float geglu_lut(float gate, float up, const uint16_t *__restrict__ lut) {
+  return (float)((double)gelu_lut(gate, lut) * (double)up);
 }
 
 }  // namespace hp

@@ -437,7 +437,7 @@ struct F2Args {
   size_t part_off[kMaxWeights];
   // gate/up + GeGLU tiles (w[0] gate, w[1] up): pair_out[m][row]
   float *pair_out;
-  double gelu_c;
+  const uint16_t *gelu_lut;
   // tail_full > 0 (gate/up): the items from tail_full on, fewer than half a
   // round, run as two block ranges each; the ranges write their sums to
   // tail_part (f2_geglu_tail_kernel adds them and applies the GeGLU)
@@ -823,7 +823,7 @@ kquant_prefill_fast_kernel(
               const int m = ct * kF2Cols + 16 * cs + 4 * q + j;
               const float up = xch[((rs * 4 + cs) * 4 + j) * 64];
               if (rs < nseg && row < W.rows && m < a.cols)
-                a.pair_out[(size_t)m * W.rows + row] = geglu_ts(out[rs][cs][j], up, a.gelu_c);
+                a.pair_out[(size_t)m * W.rows + row] = geglu_lut(out[rs][cs][j], up, a.gelu_lut);
             }
         }
       }
@@ -865,7 +865,7 @@ __global__ __launch_bounds__(256) void f2_geglu_tail_kernel(const F2Args a, int 
   const float *p0 = a.tail_part + (size_t)(2 * i) * kF3Waves * kF3WaveFloats + k * 64 + lane;
   const float *p1 = p0 + (size_t)kF3Waves * kF3WaveFloats;
   const size_t gi = (size_t)w * kF3WaveFloats, ui = gi + (size_t)kHalf * kF3WaveFloats;
-  a.pair_out[(size_t)m * W.rows + row] = geglu_ts(p0[gi] + p1[gi], p0[ui] + p1[ui], a.gelu_c);
+  a.pair_out[(size_t)m * W.rows + row] = geglu_lut(p0[gi] + p1[gi], p0[ui] + p1[ui], a.gelu_lut);
 }
 
 // out = ((part_0 + part_1) + ...) + part_{ks-1} over the launch's outputs
@@ -980,7 +980,7 @@ size_t prefill_fast_geglu_bytes(const MfmaLaunch &l, int num_cus) {
   return xt + tail;
 }
 
-hipError_t launch_prefill_fast_geglu(const MfmaLaunch &l, const float *x, uint8_t *scratch, double gelu_c,
+hipError_t launch_prefill_fast_geglu(const MfmaLaunch &l, const float *x, uint8_t *scratch, const uint16_t *gelu_lut,
                                      float *out, int num_cus, hipStream_t s) {
   if (l.count != 2 || l.cols < 1 || l.k % kQK != 0 || l.type[0] != l.type[1] || l.rows[0] != l.rows[1])
     return hipErrorInvalidValue;
@@ -1007,7 +1007,7 @@ hipError_t launch_prefill_fast_geglu(const MfmaLaunch &l, const float *x, uint8_
   a.xt = scratch;
   a.ksplit = 1;
   a.pair_out = out;
-  a.gelu_c = gelu_c;
+  a.gelu_lut = gelu_lut;
   a.tail_full = p.tail_full;
   a.tail_part = reinterpret_cast<float *>(scratch + (size_t)col_tiles * nb * kF2XTile);
   hipLaunchKernelGGL(kquant_prefill_fast_kernel<true>, dim3(p.grid), dim3(kF3Threads), 0, s, a);

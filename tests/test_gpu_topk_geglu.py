@@ -115,6 +115,26 @@ def test_geglu_bit_exact(hip, oracle):
     assert diff.size == 0, (diff[:5], gate[diff[:5]], got[diff[:5]], ref[diff[:5]])
 
 
+def test_geglu_every_f16_input(hip, oracle):
+    """The GeGLU launches read gelu from a table of its value at each f16
+    pattern (gelu rounds its input to f16 first).  Every one of the 65536
+    patterns as gate, each beside up = 1 (the table entry itself), a NaN
+    payload and neighbours just inside and outside +-10 (the range checks
+    run on the unrounded input), against the oracle bit for bit."""
+    pats = np.arange(65536, dtype=np.uint32).astype(np.uint16).view(np.float16).astype(np.float32)
+    nudge = np.array([np.nextafter(np.float32(10.0), np.float32(0.0)), np.nextafter(np.float32(-10.0), np.float32(0.0)),
+                      np.float32(9.9951171875), np.float32(-9.9951171875), np.float32(9.998), np.float32(-9.998)],
+                     dtype=np.float32)
+    nan = np.array([0x7FC00001, 0xFFC12345], dtype=np.uint32).view(np.float32)
+    gate = np.concatenate([pats, pats, nudge, nan]).astype(np.float32)
+    up = np.concatenate([np.ones(65536, np.float32), np.full(65536, -1.75, np.float32),
+                         np.full(nudge.size + nan.size, 0.625, np.float32)])
+    got = hip.gegluHip(gate, up)
+    ref = oracle.geglu(gate, up)
+    diff = np.flatnonzero(got.view(np.uint32) != ref.view(np.uint32))
+    assert diff.size == 0, (diff[:5], gate[diff[:5]], got[diff[:5]], ref[diff[:5]])
+
+
 @pytest.mark.parametrize("kernel", [0, 1, 2, 3, 6], ids=["auto", "valu-fused", "mfma", "half", "wide"])
 @pytest.mark.parametrize("rows,k,m", [(600, 2560, 1), (610, 2560, 3), (60, 10240, 1), (10240, 2560, 1),
                                       (777, 2560, 4), (1, 2560, 2)])
