@@ -619,7 +619,7 @@ int32_t run_matvec_geglu(Handle *hg, Handle *hu, const float *d_input, size_t in
     a.cols = (int)cols;
     a.out_col0 = 0;
     a.pair_out = d_out;
-    a.gelu_c = gelu_constant();
+    a.gelu_lut = s.gelu_lut;
     hipEvent_t e1 = prof_begin(stream);
     HP_HIP_TRY(launch_matvec_wide(a, stream));
     prof_end(HP_KERNEL_MATVEC, e1, stream);
@@ -648,7 +648,7 @@ int32_t run_matvec_geglu(Handle *hg, Handle *hu, const float *d_input, size_t in
     a.cols = (int)cols;
     a.out_col0 = 0;
     a.pair_out = d_out;
-    a.gelu_c = gelu_constant();
+    a.gelu_lut = s.gelu_lut;
     hipEvent_t e1 = prof_begin(stream);
     HP_HIP_TRY(launch_matvec_pair(a, s.num_cus, stream));
     prof_end(HP_KERNEL_MATVEC, e1, stream);

@@ -97,7 +97,7 @@ struct MatvecArgs {
   int total_rows;     // half-split kernel: the weights' rows summed
   int Rh;             // half-split kernel: rows per unit (floor(32 / S))
   float *pair_out;    // gate/up + GeGLU launch: [cols][rows] output
-  double gelu_c;      // sqrt(2 / pi) as Math.sqrt(2 / Math.PI)
+  const uint16_t *gelu_lut;  // the gelu table (hp_gelu.h gelu_lut)
   // non-null (launches of 2 or more columns): the input already quantised,
   // as the LDS image of this launch's columns (q8_image_bytes(cols, nb)),
   // copied in place of the Q8_K prologue

@@ -263,7 +263,7 @@ __global__ __launch_bounds__(256) void kquant_matvec_kernel(const MatvecArgs a) 
           else if ((ti & 1) == 0)
             gkeep[m] = res;
           else
-            a.pair_out[(size_t)(a.out_col0 + m) * cx.rows + cx.row0 + r] = geglu_ts(gkeep[m], res, a.gelu_c);
+            a.pair_out[(size_t)(a.out_col0 + m) * cx.rows + cx.row0 + r] = geglu_lut(gkeep[m], res, a.gelu_lut);
         }
       }
       if (PREFETCH) {

@@ -411,7 +411,7 @@ __global__ __launch_bounds__(kWideMaxThreads) void kquant_wide_kernel(const Matv
     const int vr = u / M, m = u - vr * M;
     if (PAIR) {
       a.pair_out[(size_t)(a.out_col0 + m) * a.w[0].rows + row0 + vr] =
-          geglu_ts(tail(vr, m), tail(VRh + vr, m), a.gelu_c);
+          geglu_lut(tail(vr, m), tail(VRh + vr, m), a.gelu_lut);
     } else {
       const WeightDesc W = weight_of(a, row0 + vr);
       W.out[(size_t)(a.out_col0 + m) * W.rows + (row0 + vr - W.row_begin)] = tail(vr, m);
