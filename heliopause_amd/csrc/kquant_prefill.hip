@@ -625,6 +625,8 @@ __device__ __forceinline__ void f3_block(float (&out)[kF3RS][4][4], const typena
       const uint4 v = *reinterpret_cast<const uint4 *>(xb + (((q & 1) * kF2Cols) + 16 * cs + n) * 8);
       bm[cs] = __builtin_bit_cast(half8, lo ? v : make_uint4(0, 0, 0, 0));
     }
+    // each stage over all 16 sums of a segment before the next, so the
+    // sums' independent chains interleave instead of waiting on each other
 #pragma unroll
     for (int rs = 0; rs < kF3RS; rs++) {
       const uint4 hdr = w[rs].hdr;
@@ -633,24 +635,36 @@ __device__ __forceinline__ void f3_block(float (&out)[kF3RS][4][4], const typena
       const uint32_t mn = q == 0 ? mn0 : mn1;
       half8 am = cat(dup_byte(mn, 0, 1024.0f), dup_byte(mn, 1, 1024.0f), dup_byte(mn, 2, 1024.0f),
                      dup_byte(mn, 3, 1024.0f));
+      f32x4 sm[4];
 #pragma unroll
-      for (int cs = 0; cs < 4; cs++) {
-        const f32x4 sm = mfma(bm[cs], am, (f32x4){0.0f, 0.0f, 0.0f, 0.0f});
+      for (int cs = 0; cs < 4; cs++) sm[cs] = mfma(bm[cs], am, (f32x4){0.0f, 0.0f, 0.0f, 0.0f});
+      float t[4][4];
 #pragma unroll
-        for (int j = 0; j < 4; j++) {
-          const float t = __builtin_fmaf(-dmw, sm[j], dw * D[rs][cs][j]);
-          out[rs][cs][j] = __builtin_fmaf(dx[cs][j], t, out[rs][cs][j]);
-        }
-      }
+      for (int cs = 0; cs < 4; cs++)
+#pragma unroll
+        for (int j = 0; j < 4; j++) t[cs][j] = dw * D[rs][cs][j];
+#pragma unroll
+      for (int cs = 0; cs < 4; cs++)
+#pragma unroll
+        for (int j = 0; j < 4; j++) t[cs][j] = __builtin_fmaf(-dmw, sm[cs][j], t[cs][j]);
+#pragma unroll
+      for (int cs = 0; cs < 4; cs++)
+#pragma unroll
+        for (int j = 0; j < 4; j++) out[rs][cs][j] = __builtin_fmaf(dx[cs][j], t[cs][j], out[rs][cs][j]);
     }
   } else {
 #pragma unroll
     for (int rs = 0; rs < kF3RS; rs++) {
       const float dw = h2f_bits(w[rs].d16);
+      float t[4][4];
 #pragma unroll
       for (int cs = 0; cs < 4; cs++)
 #pragma unroll
-        for (int j = 0; j < 4; j++) out[rs][cs][j] = __builtin_fmaf(dx[cs][j], dw * D[rs][cs][j], out[rs][cs][j]);
+        for (int j = 0; j < 4; j++) t[cs][j] = dw * D[rs][cs][j];
+#pragma unroll
+      for (int cs = 0; cs < 4; cs++)
+#pragma unroll
+        for (int j = 0; j < 4; j++) out[rs][cs][j] = __builtin_fmaf(dx[cs][j], t[cs][j], out[rs][cs][j]);
     }
   }
 }
