@@ -370,7 +370,8 @@ __global__ __launch_bounds__(256) void kquant_prefill_kernel(const PfArgs a) {
 // come with the lane's own header load.
 constexpr int kF2Cols = 64;
 constexpr int kF2XTile = 32768 + 2048 + 256;  // 35,072 bytes per (column tile, block)
-constexpr int kF3Waves = 8;                                          // two per SIMD
+constexpr int kF3Waves = 8;                                          // per workgroup
+constexpr int kF3PerCU = 8 / kF3Waves;                               // workgroups per CU: two waves per SIMD
 constexpr int kF3RS = 2;                                             // 16-row segments per wave
 constexpr int kF3Threads = 64 * kF3Waves;
 constexpr int kF3Segs = kF3RS * kF3Waves;                            // segments per workgroup tile
@@ -751,12 +752,12 @@ __device__ __forceinline__ int f3_order(int it, int total) {
 
 constexpr int kF3WaveFloats = kF3RS * 16 * 64;  // a wave's sums (out) of one tile
 
-// One workgroup per CU (kF3Waves waves, kF3Waves / 4 per SIMD).  PAIR: a tile is kF3Segs / 2 segments of gate (the first
+// kF3PerCU workgroups per CU, two waves per SIMD in all.  PAIR: a tile is kF3Segs / 2 segments of gate (the first
 // half of the waves) and the same rows of up (the second half); up's sums go
 // through LDS to the gate wave of the same rows, which stores
 // fround(gelu(gate) * up).  total_rt then counts those tiles, ksplit is 1.
 template <bool PAIR>
-__global__ __launch_bounds__(kF3Threads) __attribute__((amdgpu_waves_per_eu(kF3Waves / 4, kF3Waves / 4))) void
+__global__ __launch_bounds__(kF3Threads) __attribute__((amdgpu_waves_per_eu(2, 2))) void
 kquant_prefill_fast_kernel(
     const F2Args a) {
   const int lane = threadIdx.x & 63;
@@ -916,14 +917,14 @@ __global__ __launch_bounds__(256) void f2_reduce_kernel(const F2Args a, size_t t
   }
 }
 
-// Block ranges per tile: enough to give every CU (one workgroup each) a
-// tile's worth of work when the launch has fewer tiles, at least two blocks a
-// range.  One round rather than two: each range's partial sums cost a write
-// and a read in the reduction (measured on the 42-layer chunk: O 20.8 -> 16.7
-// us, down 54.3 -> 50.8 us, against two workgroups' worth per CU).
-int f2_ksplit(int tiles, int nb, int num_cus) {
-  if (tiles <= 0 || tiles >= num_cus) return 1;
-  int ks = num_cus / tiles;
+// Block ranges per tile: enough to give every workgroup slot a tile's worth
+// of work when the launch has fewer tiles, at least two blocks a range.  One
+// round rather than two: each range's partial sums cost a write and a read in
+// the reduction (measured on the 42-layer chunk: O 20.8 -> 16.7 us, down
+// 54.3 -> 50.8 us, against two rounds' worth).
+int f2_ksplit(int tiles, int nb, int slots) {
+  if (tiles <= 0 || tiles >= slots) return 1;
+  int ks = slots / tiles;
   if (ks > nb / 2) ks = nb / 2;
   if (ks > 8) ks = 8;
   return ks < 1 ? 1 : ks;
@@ -943,7 +944,7 @@ F2Shape f2_shape(const MfmaLaunch &l, int num_cus) {
     sh.total_rt += ((l.rows[i] + 15) / 16 + kF3Segs - 1) / kF3Segs;
     sh.outs += (size_t)l.cols * l.rows[i];
   }
-  sh.ks = f2_ksplit(sh.total_rt * sh.col_tiles, sh.nb, num_cus);
+  sh.ks = f2_ksplit(sh.total_rt * sh.col_tiles, sh.nb, kF3PerCU * num_cus);
   sh.stride = (sh.outs + 3) & ~(size_t)3;
   return sh;
 }
@@ -979,7 +980,7 @@ F2Pair f2_pair(const MfmaLaunch &l, int num_cus) {
   p.col_tiles = (l.cols + kF2Cols - 1) / kF2Cols;
   p.total_rt = ((l.rows[0] + 15) / 16 + kF3Segs / 2 - 1) / (kF3Segs / 2);
   p.items = p.total_rt * p.col_tiles;
-  p.grid = p.items < num_cus ? p.items : num_cus;
+  p.grid = p.items < kF3PerCU * num_cus ? p.items : kF3PerCU * num_cus;
   const int full = p.items / p.grid * p.grid, rem = p.items - full;
   p.tail_full = rem > 0 && 2 * rem <= p.grid && p.nb >= 2 ? full : 0;
   return p;
@@ -1075,7 +1076,7 @@ hipError_t launch_prefill_fast(const MfmaLaunch &l, const float *x, uint8_t *scr
   a.part = reinterpret_cast<float *>(scratch + (size_t)col_tiles * nb * kF2XTile);
   a.part_stride = sh.stride;
   const long long items = (long long)a.total_rt * a.col_tiles * a.ksplit;
-  const int grid = (int)(items < num_cus ? items : num_cus);
+  const int grid = (int)(items < kF3PerCU * num_cus ? items : kF3PerCU * num_cus);
   hipLaunchKernelGGL(kquant_prefill_fast_kernel<false>, dim3(grid), dim3(kF3Threads), 0, s, a);
   if (a.ksplit == 1) return hipGetLastError();
   e = hipGetLastError();
