@@ -108,7 +108,7 @@ def matvec_kernel_name(choice: str, k: int, m: int, specs: list) -> str:
     r6 = 64 // s
     tiles = sum((r + r6 - 1) // r6 for r in rows)
     tiles16 = sum((r + 15) // 16 for r in rows)
-    wide = m <= 4 and type_id in (1, 3) and (choice == "wide" or (choice == "auto" and nb >= 40))
+    wide = m <= 4 and type_id in (1, 3) and (choice.startswith("wide") or (choice == "auto" and nb >= 40))
     if wide:
         return f"kquant_wide_kernel<{m}, {type_id}>"
     half = s <= 32 and m <= 4 and (choice == "half" or
@@ -135,9 +135,11 @@ def parse() -> argparse.Namespace:
     p.add_argument("--no-cpu", action="store_true")
     p.add_argument("--no-decode", action="store_true",
                    help="leave the decode-step object out of the default line")
-    p.add_argument("--kernel", choices=["auto", "valu", "mfma", "half", "wide"], default="auto",
+    p.add_argument("--kernel", choices=["auto", "valu", "mfma", "half", "wide", "wide-whole", "wide-half"],
+                   default="auto",
                    help="matvec kernel: automatic choice, vector ALU, matrix cores, half-split vector ALU, "
-                        "wide (one workgroup per block of rows)")
+                        "wide (one workgroup per block of rows), the wide kernel with whole or half "
+                        "row-blocks per thread")
     p.add_argument("--copy-probe", action="store_true",
                    help="only run a plain 256 MiB device copy (HBM counter calibration) and exit")
     return p.parse_args()
@@ -263,7 +265,8 @@ def decode_chain(args) -> int:
     if args.m != 1:
         raise SystemExit("decode42 runs at M = 1")
     H.setMatvecKernel({"auto": H.MATVEC_AUTO, "valu": H.MATVEC_VALU, "mfma": H.MATVEC_MFMA,
-                       "half": H.MATVEC_HALF, "wide": H.MATVEC_WIDE}[args.kernel])
+                       "half": H.MATVEC_HALF, "wide": H.MATVEC_WIDE,
+                       "wide-whole": H.MATVEC_WIDE_WHOLE, "wide-half": H.MATVEC_WIDE_HALF}[args.kernel])
     torch.cuda.init()
     dev = torch.device("cuda:0")
     seed = S.config_seed(5)
@@ -472,7 +475,12 @@ def decode_summary(r: dict) -> dict:
 def decode_step(args) -> int:
     """``--workload decode42``: the decode step (or a draft of --m tokens) as
     its own JSON line."""
+    from heliopause_amd import hip_kernels as H
+
     m = args.m
+    H.setMatvecKernel({"auto": H.MATVEC_AUTO, "valu": H.MATVEC_VALU, "mfma": H.MATVEC_MFMA,
+                       "half": H.MATVEC_HALF, "wide": H.MATVEC_WIDE,
+                       "wide-whole": H.MATVEC_WIDE_WHOLE, "wide-half": H.MATVEC_WIDE_HALF}[args.kernel])
     r = measure_decode_step(m, max(1, args.steps // 10), max(1, args.warmup // 10),
                             None if args.no_cpu else args.cpu_seconds)
     ms = r["ms"]
@@ -553,7 +561,8 @@ def prefill_chain(args) -> int:
 
     m = args.m if args.m > 1 else 512
     H.setMatvecKernel({"auto": H.MATVEC_AUTO, "valu": H.MATVEC_VALU, "mfma": H.MATVEC_MFMA,
-                       "half": H.MATVEC_HALF, "wide": H.MATVEC_WIDE}[args.kernel])
+                       "half": H.MATVEC_HALF, "wide": H.MATVEC_WIDE,
+                       "wide-whole": H.MATVEC_WIDE_WHOLE, "wide-half": H.MATVEC_WIDE_HALF}[args.kernel])
     torch.cuda.init()
     dev = torch.device("cuda:0")
     seed = S.config_seed(5)
@@ -867,7 +876,8 @@ def main() -> int:
     if not support["available"]:
         raise SystemExit(f"HIP runner unavailable: {support}")
     H.setMatvecKernel({"auto": H.MATVEC_AUTO, "valu": H.MATVEC_VALU, "mfma": H.MATVEC_MFMA,
-                       "half": H.MATVEC_HALF, "wide": H.MATVEC_WIDE}[args.kernel])
+                       "half": H.MATVEC_HALF, "wide": H.MATVEC_WIDE,
+                       "wide-whole": H.MATVEC_WIDE_WHOLE, "wide-half": H.MATVEC_WIDE_HALF}[args.kernel])
     torch.cuda.init()
     dev = torch.device("cuda:0")
     wl, m = args.workload, args.m

@@ -78,7 +78,8 @@ struct State {
   void *topk_out = nullptr;  // ids + values of the host-pointer top-k entry points
   size_t topk_out_cap = 0;
   uint64_t matmul_calls = 0, launches = 0;
-  int matvec_kernel = 0;  // 0 auto, 1 vector ALU, 2 matrix cores, 3 half-split, 4 prefill
+  int matvec_kernel = 0;  // 0 auto, 1 vector ALU, 2 matrix cores, 3 half-split, 4 prefill,
+                          // 5 fast prefill, 6 wide, 7 wide (whole tasks), 8 wide (half tasks)
   // set while a host-pointer matmul entry point runs: the automatic policy then
   // keeps to the bit-exact kernels, as the reference's resident calls are
   bool host_exact = false;
@@ -361,7 +362,7 @@ bool f16_ok(size_t count, Handle *const *hs) {
 bool use_wide(size_t count, Handle *const *hs, size_t cols) {
   const State &s = st();
   const int forced = s.matvec_kernel;
-  if (cols < 1 || cols > 4 || (forced != 0 && forced != 6)) return false;
+  if (cols < 1 || cols > 4 || (forced != 0 && forced < 6)) return false;
   const int type = hs[0]->type;
   if (type != kTypeQ4K && type != kTypeQ6K) return false;
   size_t rows = 0;
@@ -373,8 +374,20 @@ bool use_wide(size_t count, Handle *const *hs, size_t cols) {
   if (nb > 256 || rows >= (1u << 20)) return false;  // div_magic's exact range
   if (wide_lds_bytes((int)cols, nb, type, wide_rows_for((int)rows, nb, (int)cols, type)) > s.max_lds)
     return false;
-  if (forced == 6) return true;
+  if (forced >= 6) return true;
   return nb >= 40;  // 1..4 columns (checked above)
+}
+
+// Tasks of the wide kernel: whole row-blocks (up to 512 threads) or half
+// row-blocks (lane classes 4h .. 4h+3, up to 1024 threads).  Selector 7
+// forces whole, 8 half; both give the same bits.
+// Half tasks exist for launches without the norm prologue or GeGLU at one or
+// two columns.
+int wide_half_for(bool norm, bool pair, int cols) {
+  const int forced = st().matvec_kernel;
+  if (norm || pair || cols > 2 || forced == 7) return 0;
+  if (forced == 8) return 1;
+  return cols == 1 ? 1 : 0;
 }
 
 // The wide kernel for gate/up + GeGLU (equal rows, one type) at one to four
@@ -384,7 +397,7 @@ bool use_wide(size_t count, Handle *const *hs, size_t cols) {
 bool use_wide_pair(Handle *const *hs, size_t cols) {
   const State &s = st();
   const int forced = s.matvec_kernel;
-  if (cols < 1 || cols > 4 || (forced != 0 && forced != 6)) return false;
+  if (cols < 1 || cols > 4 || (forced != 0 && forced < 6)) return false;
   const int type = hs[0]->type;
   if ((type != kTypeQ4K && type != kTypeQ6K) || hs[1]->type != type || hs[0]->row_count != hs[1]->row_count)
     return false;
@@ -504,6 +517,7 @@ int32_t run_matvec(size_t count, Handle *const *hs, const float *d_input, size_t
   }
   if (wide) {
     a.wide_rows = wide_rows_for(rows_all, g.nb, (int)cols, hs[0]->type);
+    a.wide_half = wide_half_for(norm != nullptr, false, (int)cols);
     a.mg_nb = div_magic(g.nb);
     a.mg_S = div_magic(g.S);
     a.mg_R = div_magic(g.R);
@@ -612,6 +626,7 @@ int32_t run_matvec_geglu(Handle *hg, Handle *hu, const float *d_input, size_t in
     a.total_rows = (int)rows;
     a.wide_rows = wide_rows_for((int)(2 * rows), g.nb, (int)cols, hg->type) / 2;
     if (a.wide_rows < 1) a.wide_rows = 1;
+    a.wide_half = wide_half_for(norm != nullptr, true, (int)cols);
     a.mg_nb = div_magic(g.nb);
     a.mg_S = div_magic(g.S);
     a.mg_R = div_magic(g.R);
@@ -1692,7 +1707,7 @@ int32_t hp_hip_quantize_q8_k(const float *input, size_t input_len, size_t input_
 int32_t hp_hip_set_matvec_kernel(int32_t which) {
   State &s = st();
   std::lock_guard<std::recursive_mutex> lock(s.mu);
-  if (which < 0 || which > 6) return fail(HP_ERR_ARG, "kernel selector must be 0..6");
+  if (which < 0 || which > 8) return fail(HP_ERR_ARG, "kernel selector must be 0..8");
   s.matvec_kernel = which;
   return HP_OK;
 }

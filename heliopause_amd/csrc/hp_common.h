@@ -106,6 +106,8 @@ struct MatvecArgs {
                       // rows of each of gate and up)
   // wide kernel: div_magic of nb, g.S and g.R (x / d as one high multiply)
   uint32_t mg_nb, mg_S, mg_R;
+  int wide_half;      // wide kernel: 1 = tasks are half row-blocks (lane
+                      // classes 4h .. 4h+3), up to 1024 threads
 };
 
 // x / d for 0 <= x < 2^20 as __umulhi(x, div_magic(d)) (0 for d = 1: x);
@@ -134,7 +136,7 @@ hipError_t launch_matvec_pair(const MatvecArgs &a, int num_cus, hipStream_t s);
 // Uniform Q4_K or Q6_K weights, 1..4 columns; the norm prologue (one column,
 // nb <= 16); with a.pair_out, gate/up + GeGLU (a.wide_rows rows of each).
 size_t wide_lds_bytes(int cols, int nb, int type, int rows_per_wg);
-int wide_threads(int cols, int nb, int rows_per_wg);
+int wide_threads(int cols, int nb, int rows_per_wg, bool half);
 hipError_t launch_matvec_wide(const MatvecArgs &a, hipStream_t s);
 // Q6_K also sets *f16_flag (zeroed by the caller) to 1 when some scale makes
 // sc * (q - 32) inexact in f16, which the matrix-core kernels need exact.

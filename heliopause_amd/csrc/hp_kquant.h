@@ -215,6 +215,160 @@ __device__ __forceinline__ void q6k_ints_split(const Regs &rg, const uint8_t *xl
     for (int l = 0; l < 8; l++) aux[m][l] >>= 2;  // weights carried 4 * (q6 - 32)
 }
 
+// Half row-blocks: lane classes l = 4h .. 4h+3 of one (row, block) only
+// (the half-split and wide kernels).  A half loads chunk 0 (Q4_K) or the
+// scales (Q6_K) and the nibble (and high-bit) chunks of its classes.
+struct HalfRegs {
+  uint4 c0;    // bytes 0..15 of the block (Q4_K) / the 16 scales (Q6_K)
+  uint4 d[4];  // Q4_K nibble chunks 1 + 2p + h; Q6_K low-nibble chunks 2p + h
+  uint4 e[2];  // Q6_K high-bit chunks 8 + 2p + h
+  uint32_t d6;
+};
+
+template <int M>
+__device__ __forceinline__ void q4k_ints_half(const HalfRegs &rg, const uint8_t *xq, int nb, int b, int h,
+                                              int (&aux)[M][4], int (&sumi)[M]) {
+  const uint32_t s0 = rg.c0.y, s1 = rg.c0.z, s2 = rg.c0.w;
+  int sc[8], mn[8];
+#pragma unroll
+  for (int j = 0; j < 4; j++) {
+    sc[j] = (s0 >> (8 * j)) & 63;
+    mn[j] = (s1 >> (8 * j)) & 63;
+    sc[j + 4] = ((s2 >> (8 * j)) & 15) | (((s0 >> (8 * j + 6)) & 3) << 4);
+    mn[j + 4] = ((s2 >> (8 * j + 4)) & 15) | (((s1 >> (8 * j + 6)) & 3) << 4);
+  }
+  int dsc[8];  // Abel weights: sum_j sc_j d_j = sum_j T_j (sc_j - sc_{j+1})
+#pragma unroll
+  for (int j = 0; j < 8; j++) dsc[j] = j < 7 ? sc[j] - sc[j + 1] : sc[7];
+  int T[M][4];
+#pragma unroll
+  for (int m = 0; m < M; m++) {
+#pragma unroll
+    for (int l = 0; l < 4; l++) aux[m][l] = T[m][l] = 0;
+    const uint4 bs = *reinterpret_cast<const uint4 *>(xq + ((size_t)m * nb + b) * kQ8BlockBytes + 256);
+    int si = 0;
+#pragma unroll
+    for (int j = 0; j < 8; j++) {
+      const int v = (int)(int16_t)(u4get(bs, j >> 1) >> (16 * (j & 1)));
+      si += __mul24(v, mn[j]);
+    }
+    sumi[m] = si;
+  }
+#pragma unroll
+  for (int j = 0; j < 8; j++) {
+    const uint4 D = rg.d[j >> 1];
+    uint32_t w[4];
+#pragma unroll
+    for (int li = 0; li < 4; li++) {
+      const uint32_t d = u4get(D, li);
+      w[li] = (j & 1) ? ((d >> 4) & 0x0F0F0F0Fu) : (d & 0x0F0F0F0Fu);
+    }
+#pragma unroll
+    for (int m = 0; m < M; m++) {
+      const uint4 xv = reinterpret_cast<const uint4 *>(xq + ((size_t)m * nb + b) * kQ8BlockBytes)[2 * j + h];
+#pragma unroll
+      for (int li = 0; li < 4; li++) {
+        T[m][li] = __builtin_amdgcn_sdot4((int)w[li], (int)u4get(xv, li), T[m][li], false);
+        aux[m][li] = mad24(T[m][li], dsc[j], aux[m][li]);
+      }
+    }
+  }
+}
+
+template <int M>
+__device__ __forceinline__ void q6k_ints_half(const HalfRegs &rg, const uint8_t *xq, int nb, int b, int h,
+                                              int (&aux)[M][4]) {
+  int sc[16];
+#pragma unroll
+  for (int g = 0; g < 16; g++) sc[g] = (int)(int8_t)(u4get(rg.c0, g >> 2) >> (8 * (g & 3)));
+  int dsc[16];
+#pragma unroll
+  for (int g = 0; g < 16; g++) dsc[g] = g < 15 ? sc[g] - sc[g + 1] : sc[15];
+  int T[M][4];
+#pragma unroll
+  for (int m = 0; m < M; m++)
+#pragma unroll
+    for (int l = 0; l < 4; l++) aux[m][l] = T[m][l] = 0;
+#pragma unroll
+  for (int j = 0; j < 8; j++) {
+    const uint4 Dl = rg.d[j >> 1];
+    const uint4 Dh = rg.e[j >> 2];
+    uint32_t wlo[4], whi[4];
+#pragma unroll
+    for (int li = 0; li < 4; li++) {
+      const uint32_t ql = u4get(Dl, li), qh = u4get(Dh, li);
+      const uint32_t nib = (j & 1) ? ((ql >> 2) & 0x3C3C3C3Cu) : ((ql << 2) & 0x3C3C3C3Cu);
+      const int u = j & 3;
+      const uint32_t w = nib | ((qh << (6 - 2 * u)) & 0xC0C0C0C0u);  // bytes = 4 * (q6 - 32)
+      wlo[li] = w & 0x0000FFFFu;
+      whi[li] = w & 0xFFFF0000u;
+    }
+#pragma unroll
+    for (int m = 0; m < M; m++) {
+      const uint4 xv = reinterpret_cast<const uint4 *>(xq + ((size_t)m * nb + b) * kQ8BlockBytes)[2 * j + h];
+#pragma unroll
+      for (int li = 0; li < 4; li++) {
+        T[m][li] = __builtin_amdgcn_sdot4((int)wlo[li], (int)u4get(xv, li), T[m][li], false);
+        aux[m][li] = mad24(T[m][li], dsc[2 * j], aux[m][li]);
+        T[m][li] = __builtin_amdgcn_sdot4((int)whi[li], (int)u4get(xv, li), T[m][li], false);
+        aux[m][li] = mad24(T[m][li], dsc[2 * j + 1], aux[m][li]);
+      }
+    }
+  }
+#pragma unroll
+  for (int m = 0; m < M; m++)
+#pragma unroll
+    for (int l = 0; l < 4; l++) aux[m][l] >>= 2;  // weights carried 4 * (q6 - 32)
+}
+
+// q6k_ints_half with the input as the two masked copies of q6k_ints_split:
+// the same integers for lane classes 4h .. 4h+3.
+template <int M, int STRIDE>
+__device__ __forceinline__ void q6k_ints_half_split(const HalfRegs &rg, const uint8_t *xlo, const uint8_t *xhi, int nb,
+                                                    int b, int h, int (&aux)[M][4]) {
+  int sc[16];
+#pragma unroll
+  for (int g = 0; g < 16; g++) sc[g] = (int)(int8_t)(u4get(rg.c0, g >> 2) >> (8 * (g & 3)));
+  int dsc[16];
+#pragma unroll
+  for (int g = 0; g < 16; g++) dsc[g] = g < 15 ? sc[g] - sc[g + 1] : sc[15];
+  int T[M][4];
+#pragma unroll
+  for (int m = 0; m < M; m++)
+#pragma unroll
+    for (int l = 0; l < 4; l++) aux[m][l] = T[m][l] = 0;
+#pragma unroll
+  for (int j = 0; j < 8; j++) {
+    const uint4 Dl = rg.d[j >> 1];
+    const uint4 Dh = rg.e[j >> 2];
+    uint32_t w[4];
+#pragma unroll
+    for (int li = 0; li < 4; li++) {
+      const uint32_t ql = u4get(Dl, li), qh = u4get(Dh, li);
+      const uint32_t nib = (j & 1) ? ((ql >> 2) & 0x3C3C3C3Cu) : ((ql << 2) & 0x3C3C3C3Cu);
+      const int u = j & 3;
+      w[li] = nib | ((qh << (6 - 2 * u)) & 0xC0C0C0C0u);  // bytes = 4 * (q6 - 32)
+    }
+#pragma unroll
+    for (int m = 0; m < M; m++) {
+      const size_t off = ((size_t)m * nb + b) * STRIDE;
+      const uint4 xl = reinterpret_cast<const uint4 *>(xlo + off)[2 * j + h];
+      const uint4 xh = reinterpret_cast<const uint4 *>(xhi + off)[2 * j + h];
+#pragma unroll
+      for (int li = 0; li < 4; li++) {
+        T[m][li] = __builtin_amdgcn_sdot4((int)w[li], (int)u4get(xl, li), T[m][li], false);
+        aux[m][li] = mad24(T[m][li], dsc[2 * j], aux[m][li]);
+        T[m][li] = __builtin_amdgcn_sdot4((int)w[li], (int)u4get(xh, li), T[m][li], false);
+        aux[m][li] = mad24(T[m][li], dsc[2 * j + 1], aux[m][li]);
+      }
+    }
+  }
+#pragma unroll
+  for (int m = 0; m < M; m++)
+#pragma unroll
+    for (int l = 0; l < 4; l++) aux[m][l] >>= 2;  // weights carried 4 * (q6 - 32)
+}
+
 // Norm prologue of a one-column launch (NormIn, hp_common.h): group grp < nb
 // of 16 lanes holds block grp in load_x16's element order; the sums of
 // squares are f64 sums over the workgroup (256 threads).

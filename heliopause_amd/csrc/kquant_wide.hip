@@ -34,6 +34,8 @@
 #include "hp_q8k16.h"
 #include "hp_wave.h"
 
+#include <type_traits>
+
 namespace hp {
 
 namespace {
@@ -42,6 +44,12 @@ namespace {
 // 256 registers, room for a task's raw chunks twice: the next task's loads
 // are issued before the current one's work).
 constexpr int kWideMaxThreads = 512;
+// With half tasks (HALF: a thread forms lane classes 4h .. 4h+3 of a
+// row-block, half the integer work and half the chunks) up to sixteen waves:
+// four per SIMD hide the latency of the products' LDS reads and dot chains
+// that two leave exposed, and a Q8_K prologue of up to 64 blocks runs as one
+// pass.  128 registers per wave.
+constexpr int kWideHalfThreads = 1024;
 
 // LDS carve-up of one workgroup (byte offsets).  The input: Q4_K reads the
 // Q8_K image (cols * nb blocks of kQ8BlockBytes), Q6_K two masked copies of
@@ -52,8 +60,9 @@ constexpr int kWideMaxThreads = 512;
 constexpr int kSplitStride = kQ8BlockBytes;
 
 // 16-byte pieces of an input image each thread loads ahead of the weights:
-// four columns of 40 blocks over 512 threads need six.
-constexpr int kImgRegs = 6;
+// four columns of 40 blocks over 512 threads need six (three over 1024).
+template <bool HALF>
+constexpr int kImgRegs = HALF ? 3 : 6;
 
 struct WideLayout {
   int nbp;        // products per (row, col, class) row: nb rounded up to 4, == 4 (mod 8)
@@ -143,6 +152,22 @@ __device__ __forceinline__ void wide_load(Regs &rg, const WideTask &t) {
   if (TYPE == kTypeQ6K) rg.d6 = *t.d6;
 }
 
+// The chunks of half h of a task: Q4_K chunk 0 and nibble chunks 1 + 2p + h;
+// Q6_K the scales (chunk 12), low-nibble chunks 2p + h and high-bit chunks
+// 8 + 2p + h, and d.
+template <int TYPE>
+__device__ __forceinline__ void wide_load(HalfRegs &rg, const WideTask &t, int h) {
+  constexpr bool Q4 = TYPE == kTypeQ4K;
+  rg.c0 = t.ch[(size_t)(Q4 ? 0 : 12) * t.cs];
+#pragma unroll
+  for (int p = 0; p < 4; p++) rg.d[p] = t.ch[(size_t)(Q4 ? 1 + 2 * p + h : 2 * p + h) * t.cs];
+  if (!Q4) {
+#pragma unroll
+    for (int p = 0; p < 2; p++) rg.e[p] = t.ch[(size_t)(8 + 2 * p + h) * t.cs];
+    rg.d6 = *t.d6;
+  }
+}
+
 // The norm prologue's finish (hp_kquant.h norm_finish: the same arithmetic
 // in the same order, so the same bits) where only the waves that hold one of
 // the input's blocks do the math: with eight waves and a 10-block input,
@@ -200,9 +225,11 @@ __device__ __forceinline__ void wide_norm_finish(const NormIn &n, NormRegs &nr, 
 // and writes fround(gelu(gate) * up) to a.pair_out (layers.ts:435-456).
 // TPL (1, 2): tasks per thread whose loads are issued before the prologue
 // (the launch's tasks per workgroup fit TPL * blockDim.x; more run after,
-// their loads waited for one at a time).
-template <int M, int TYPE, int NORM, bool PAIR, int TPL>
-__global__ __launch_bounds__(kWideMaxThreads) void kquant_wide_kernel(const MatvecArgs a) {
+// their loads waited for one at a time).  HALF: tasks are half row-blocks,
+// task te = h * (rows * nb) + row * nb + b (h the slowest index, so a wave's
+// halves agree but for one wave at the boundary).
+template <int M, int TYPE, int NORM, bool PAIR, int TPL, bool HALF>
+__global__ __launch_bounds__(HALF ? kWideHalfThreads : kWideMaxThreads) void kquant_wide_kernel(const MatvecArgs a) {
   extern __shared__ __align__(16) uint8_t smem[];
   constexpr bool Q4 = TYPE == kTypeQ4K;
   constexpr int NC = Q4 ? 9 : 8;
@@ -220,7 +247,11 @@ __global__ __launch_bounds__(kWideMaxThreads) void kquant_wide_kernel(const Matv
 
   const int tid = threadIdx.x;
   const int nthr = blockDim.x;
-  const int ntask = VR * nb;
+  const int nfull = VR * nb;  // (row, block) tasks
+  const int ntask = HALF ? 2 * nfull : nfull;
+  using TaskRegs = typename std::conditional<HALF, HalfRegs, Regs>::type;
+  // task te's half (0 without HALF) and its (row, block) index
+  auto half_of = [&](int te) { return HALF ? (int)(te >= nfull) : 0; };
 
   // prologue input first (vector loads return in order), then the first
   // task's weights, so the weights stream in while the prologue computes
@@ -242,31 +273,40 @@ __global__ __launch_bounds__(kWideMaxThreads) void kquant_wide_kernel(const Matv
     norm_load<NORM>(a.norm, nr, grp, nb, i16);
   } else if (!pre) {
     load_x16(xv, x_block(min(grp, nq - 1)), i16);
-    load_x16(xv2, x_block(min(grp + ngrp, nq - 1)), i16);
+    if (!HALF) load_x16(xv2, x_block(min(grp + ngrp, nq - 1)), i16);
   }
   // or the first kImgRegs 16-byte pieces per thread of the input image (a
   // thread past the end re-reads the last piece), likewise before the weights
   const int n16 = (int)(q8_image_bytes(M, nb) / 16);
   const uint4 *img = reinterpret_cast<const uint4 *>(a.q8img);
-  uint4 iv[kImgRegs];
+  constexpr int NIMG = kImgRegs<HALF>;
+  uint4 iv[NIMG];
   if (pre) {
 #pragma unroll
-    for (int i = 0; i < kImgRegs; i++) iv[i] = img[min(tid + i * nthr, n16 - 1)];
+    for (int i = 0; i < NIMG; i++) iv[i] = img[min(tid + i * nthr, n16 - 1)];
   }
 
   // the first TPL tasks' weights; a thread past the end loads the
   // workgroup's last task: no branch around the loads
   // (every address first: no branch between the loads)
   WideTask tk[TPL];
+  int th[TPL];
 #pragma unroll
   for (int i = 0; i < TPL; i++) {
     const int te = min(tid + i * nthr, ntask - 1);
-    const int vr = mdiv(te, a.mg_nb);
-    tk[i] = task_at<TYPE, PAIR>(a, row0, VRh, vr, te - vr * nb);
+    th[i] = half_of(te);
+    const int tf = te - th[i] * nfull;
+    const int vr = mdiv(tf, a.mg_nb);
+    tk[i] = task_at<TYPE, PAIR>(a, row0, VRh, vr, tf - vr * nb);
   }
-  Regs rg[TPL];
+  TaskRegs rg[TPL];
 #pragma unroll
-  for (int i = 0; i < TPL; i++) wide_load<TYPE>(rg[i], tk[i]);
+  for (int i = 0; i < TPL; i++) {
+    if constexpr (HALF)
+      wide_load<TYPE>(rg[i], tk[i], th[i]);
+    else
+      wide_load<TYPE>(rg[i], tk[i]);
+  }
   // keep the loads here: without a memory barrier the compiler may sink them
   // past the prologue to their first use (a machine scheduling barrier does
   // not stop that); the barrier reads none of the loaded registers, so it
@@ -297,9 +337,9 @@ __global__ __launch_bounds__(kWideMaxThreads) void kquant_wide_kernel(const Matv
       }
     };
 #pragma unroll
-    for (int i = 0; i < kImgRegs; i++)
+    for (int i = 0; i < NIMG; i++)
       if (tid + i * nthr < n16) put(tid + i * nthr, iv[i]);
-    for (int u = tid + kImgRegs * nthr; u < n16; u += nthr) put(u, img[u]);
+    for (int u = tid + NIMG * nthr; u < n16; u += nthr) put(u, img[u]);
   } else {
     auto put_words = [&](const Q8Words &w, int q) {
       if (Q4)
@@ -308,7 +348,7 @@ __global__ __launch_bounds__(kWideMaxThreads) void kquant_wide_kernel(const Matv
         q8k_store16_split(w, i16, xq + (size_t)q * kSplitStride, xhi + (size_t)q * kSplitStride, xd + q);
     };
     auto quant = [&](const float (&v)[16], int q) { put_words(q8k_words16(v, i16), q); };
-    if (!NORM && grp + ngrp < nq) {
+    if (!HALF && !NORM && grp + ngrp < nq) {
       // two blocks: their two dependency chains interleave
       const Q8Words q0 = q8k_words16(xv, i16), q1 = q8k_words16(xv2, i16);
       put_words(q0, grp);
@@ -316,7 +356,8 @@ __global__ __launch_bounds__(kWideMaxThreads) void kquant_wide_kernel(const Matv
     } else if (grp < nq) {
       put_words(q8k_words16(xv, i16), grp);
     }
-    for (int q = grp + 2 * ngrp; !NORM && q < nq; q += ngrp) {  // more than two passes (several columns)
+    // more passes (several columns; with HALF from the second)
+    for (int q = grp + (HALF ? 1 : 2) * ngrp; !NORM && q < nq; q += ngrp) {
       load_x16(xv, x_block(q), i16);
       quant(xv, q);
     }
@@ -327,35 +368,51 @@ __global__ __launch_bounds__(kWideMaxThreads) void kquant_wide_kernel(const Matv
   // a thread past the end computes the clamped task's products and stores
   // none (no branch around the work: branches split the loaded registers'
   // live ranges, and the copies that follow wait for the loads)
-  auto products = [&](const Regs &cur, int t_in) {
+  auto products = [&](const TaskRegs &cur, int t_in) {
     const bool live = t_in < ntask;
-    const int t = min(t_in, ntask - 1);
+    const int te = min(t_in, ntask - 1);
+    const int h = half_of(te);
+    const int t = te - h * nfull;
     const int vr = mdiv(t, a.mg_nb);
     const int b = t - vr * nb;
-    int aux[M][8];
+    constexpr int NL = HALF ? 4 : 8;  // lane classes of a task: 4h + li
+    int aux[M][NL];
     int sumi[M];
     float dw, dminw = 0.0f;
-    if (Q4) {
-      q4k_ints<M>(cur, xq, nb, b, aux, sumi);
-      dw = h2f(cur.c[0].x & 0xFFFFu);
-      dminw = h2f(cur.c[0].x >> 16);
+    if constexpr (HALF) {
+      if (Q4) {
+        q4k_ints_half<M>(cur, xq, nb, b, h, aux, sumi);
+        dw = h2f(cur.c0.x & 0xFFFFu);
+        dminw = h2f(cur.c0.x >> 16);
+      } else {
+        q6k_ints_half_split<M, kSplitStride>(cur, xq, xhi, nb, b, h, aux);
+        dw = h2f(cur.d6);
+      }
     } else {
-      q6k_ints_split<M, kSplitStride>(cur, xq, xhi, nb, b, aux);
-      dw = h2f(cur.d6);
+      if (Q4) {
+        q4k_ints<M>(cur, xq, nb, b, aux, sumi);
+        dw = h2f(cur.c[0].x & 0xFFFFu);
+        dminw = h2f(cur.c[0].x >> 16);
+      } else {
+        q6k_ints_split<M, kSplitStride>(cur, xq, xhi, nb, b, aux);
+        dw = h2f(cur.d6);
+      }
     }
 #pragma unroll
     for (int m = 0; m < M; m++) {
       const float dx = xd[m * nb + b];
       const float dd = __fmul_rn(dw, dx);
-      float *pr = prod + ((size_t)(vr * M + m) * NC) * L.nbp + b;
-      float p[9];
+      float *pr = prod + ((size_t)(vr * M + m) * NC + NL * h) * L.nbp + b;
+      float p[NL];
 #pragma unroll
-      for (int l = 0; l < 8; l++) p[l] = __fmul_rn(dd, (float)aux[m][l]);
-      // class 8 (Q4_K sumf -= ...) stored negated: s - p == s + (-p) in IEEE
-      p[8] = Q4 ? -__fmul_rn(__fmul_rn(dminw, dx), (float)sumi[m]) : 0.0f;
+      for (int l = 0; l < NL; l++) p[l] = __fmul_rn(dd, (float)aux[m][l]);
+      // class 8 (Q4_K sumf -= ...) stored negated: s - p == s + (-p) in IEEE;
+      // with HALF by the h = 0 half
+      const float p8 = Q4 ? -__fmul_rn(__fmul_rn(dminw, dx), (float)sumi[m]) : 0.0f;
       if (live) {
 #pragma unroll
-        for (int l = 0; l < NC; l++) pr[l * L.nbp] = p[l];
+        for (int l = 0; l < NL; l++) pr[l * L.nbp] = p[l];
+        if (Q4 && h == 0) pr[(8 - NL * h) * L.nbp] = p8;
       }
     }
   };
@@ -363,21 +420,37 @@ __global__ __launch_bounds__(kWideMaxThreads) void kquant_wide_kernel(const Matv
   // allocator then keeps every loaded tuple intact up to this point instead
   // of copying parts of one right after its load, a copy that would wait for
   // the load during the prologue
+  auto keep = [](uint4 &c) {
+    u32x4 v = __builtin_bit_cast(u32x4, c);
+    asm volatile("" : "+v"(v));
+    c = __builtin_bit_cast(uint4, v);
+  };
 #pragma unroll
   for (int i = 0; i < TPL; i++) {
+    if constexpr (HALF) {
+      keep(rg[i].c0);
 #pragma unroll
-    for (int c = 0; c < (Q4 ? 9 : 13); c++) {
-      u32x4 v = __builtin_bit_cast(u32x4, rg[i].c[c]);
-      asm volatile("" : "+v"(v));
-      rg[i].c[c] = __builtin_bit_cast(uint4, v);
+      for (int p = 0; p < 4; p++) keep(rg[i].d[p]);
+      if (!Q4) {
+#pragma unroll
+        for (int p = 0; p < 2; p++) keep(rg[i].e[p]);
+      }
+    } else {
+#pragma unroll
+      for (int c = 0; c < (Q4 ? 9 : 13); c++) keep(rg[i].c[c]);
     }
   }
 #pragma unroll
   for (int i = 0; i < TPL; i++) products(rg[i], tid + i * nthr);
   for (int t = tid + TPL * nthr; t < ntask; t += nthr) {
-    const int vr = mdiv(t, a.mg_nb);
-    Regs more;
-    wide_load<TYPE>(more, task_at<TYPE, PAIR>(a, row0, VRh, vr, t - vr * nb));
+    const int h = half_of(t);
+    const int tf = t - h * nfull;
+    const int vr = mdiv(tf, a.mg_nb);
+    TaskRegs more;
+    if constexpr (HALF)
+      wide_load<TYPE>(more, task_at<TYPE, PAIR>(a, row0, VRh, vr, tf - vr * nb), h);
+    else
+      wide_load<TYPE>(more, task_at<TYPE, PAIR>(a, row0, VRh, vr, tf - vr * nb));
     products(more, t);
   }
   __syncthreads();
@@ -425,30 +498,47 @@ size_t wide_lds_bytes(int cols, int nb, int type, int rows_per_wg) {
 
 // Threads per workgroup: enough for one task per thread and for one pass of
 // the Q8_K prologue (16 per block), in whole waves, at most
-// kWideMaxThreads.
-int wide_threads(int cols, int nb, int rows_per_wg) {
-  int n = rows_per_wg * nb;
+// kWideMaxThreads (kWideHalfThreads with half tasks).
+int wide_threads(int cols, int nb, int rows_per_wg, bool half) {
+  int n = rows_per_wg * nb * (half ? 2 : 1);
   const int q = 16 * cols * nb;
   if (q > n) n = q;
   n = (n + 63) & ~63;
-  return n < kWideMaxThreads ? n : kWideMaxThreads;
+  const int cap = half ? kWideHalfThreads : kWideMaxThreads;
+  return n < cap ? n : cap;
 }
+
+template <int M, int NORM, bool PAIR, bool HALF>
+static void launch_wide_h(const MatvecArgs &a, int type, dim3 grid, dim3 block, size_t lds, hipStream_t s) {
+  const int vrows = PAIR ? 2 * a.wide_rows : a.wide_rows;
+  const bool two = vrows * a.g.nb * (HALF ? 2 : 1) > (int)block.x;
+  if (type == kTypeQ4K) {
+    if (two)
+      hipLaunchKernelGGL((kquant_wide_kernel<M, kTypeQ4K, NORM, PAIR, 2, HALF>), grid, block, lds, s, a);
+    else
+      hipLaunchKernelGGL((kquant_wide_kernel<M, kTypeQ4K, NORM, PAIR, 1, HALF>), grid, block, lds, s, a);
+  } else {
+    if (two)
+      hipLaunchKernelGGL((kquant_wide_kernel<M, kTypeQ6K, NORM, PAIR, 2, HALF>), grid, block, lds, s, a);
+    else
+      hipLaunchKernelGGL((kquant_wide_kernel<M, kTypeQ6K, NORM, PAIR, 1, HALF>), grid, block, lds, s, a);
+  }
+}
+
+// Half tasks are built for launches without a norm prologue or GeGLU at one
+// or two columns (128 registers hold them; more columns spill).
+template <int M, int NORM, bool PAIR>
+constexpr bool kWideHalfBuilt = NORM == 0 && !PAIR && M <= 2;
 
 template <int M, int NORM, bool PAIR>
 static void launch_wide_t(const MatvecArgs &a, int type, dim3 grid, dim3 block, size_t lds, hipStream_t s) {
-  const int vrows = PAIR ? 2 * a.wide_rows : a.wide_rows;
-  const bool two = vrows * a.g.nb > (int)block.x;
-  if (type == kTypeQ4K) {
-    if (two)
-      hipLaunchKernelGGL((kquant_wide_kernel<M, kTypeQ4K, NORM, PAIR, 2>), grid, block, lds, s, a);
-    else
-      hipLaunchKernelGGL((kquant_wide_kernel<M, kTypeQ4K, NORM, PAIR, 1>), grid, block, lds, s, a);
-  } else {
-    if (two)
-      hipLaunchKernelGGL((kquant_wide_kernel<M, kTypeQ6K, NORM, PAIR, 2>), grid, block, lds, s, a);
-    else
-      hipLaunchKernelGGL((kquant_wide_kernel<M, kTypeQ6K, NORM, PAIR, 1>), grid, block, lds, s, a);
+  if constexpr (kWideHalfBuilt<M, NORM, PAIR>) {
+    if (a.wide_half) {
+      launch_wide_h<M, NORM, PAIR, true>(a, type, grid, block, lds, s);
+      return;
+    }
   }
+  launch_wide_h<M, NORM, PAIR, false>(a, type, grid, block, lds, s);
 }
 
 template <int M, bool PAIR>
@@ -484,11 +574,12 @@ hipError_t launch_matvec_wide(const MatvecArgs &a, hipStream_t s) {
   if (type != kTypeQ4K && type != kTypeQ6K) return hipErrorInvalidValue;
   for (int i = 1; i < a.count; i++)
     if (a.w[i].type != type) return hipErrorInvalidValue;
+  if (a.wide_half && (a.norm.mode != 0 || pair || a.cols > 2)) return hipErrorInvalidValue;
   const int rows = pair ? a.w[0].rows : a.total_rows;
   const int grid = (rows + a.wide_rows - 1) / a.wide_rows;
   const int vrows = pair ? 2 * a.wide_rows : a.wide_rows;
   // a norm prologue sums over four waves (wg_sum_f64): at least 256 threads
-  const int threads = wide_threads(a.cols, a.g.nb, vrows);
+  const int threads = wide_threads(a.cols, a.g.nb, vrows, a.wide_half != 0);
   const dim3 block(a.norm.mode != 0 && threads < 256 ? 256 : threads);
   const size_t lds = wide_lds_bytes(a.cols, a.g.nb, type, vrows);
   return pair ? launch_wide_pair<true>(a, type, dim3(grid), block, lds, s)

@@ -459,11 +459,13 @@ def matmul_multi_device(handles: Sequence[int], d_input: int, input_size: int, c
 
 MATVEC_AUTO, MATVEC_VALU, MATVEC_MFMA, MATVEC_HALF, MATVEC_PREFILL, MATVEC_PREFILL_FAST, MATVEC_WIDE = \
     0, 1, 2, 3, 4, 5, 6
+MATVEC_WIDE_WHOLE, MATVEC_WIDE_HALF = 7, 8
 
 
 def setMatvecKernel(which: int) -> None:
     """Select the matvec kernel (0 automatic, 1 vector ALU, 2 matrix cores,
-    3 half-split vector ALU, 4 bit-exact prefill, 5 fast prefill).  1-4 are
+    3 half-split vector ALU, 4 bit-exact prefill, 5 fast prefill, 6 wide,
+    7 / 8 wide with whole / half row-blocks per thread).  1-4 and 6-8 are
     bit-exact; 5 (and the automatic choice from 64 columns) agrees within
     the 1e-4 relative tolerance of projections.  No counterpart in the
     reference."""

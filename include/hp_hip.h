@@ -255,8 +255,12 @@ int32_t hp_hip_quantize_q8_k(const float *input, size_t input_len, size_t input_
  * vector-ALU kernel, 2 = the matrix-core kernel whenever its LDS fits the
  * device, 3 = the half-split vector-ALU kernel (two lanes per row-block) for
  * up to four columns, 4 = the bit-exact prefill kernel (64-column tiles) for
- * any column count, 5 = the fast prefill kernel for any column count.
- * Kernels 1-4 are bit-exact with the reference; the fast prefill kernel adds
+ * any column count, 5 = the fast prefill kernel for any column count,
+ * 6 = the wide kernel (one workgroup per block of rows) wherever it applies
+ * (one weight type, one to four columns), 7 and 8 = the wide kernel with
+ * whole or with half row-blocks (lane classes 0-3 / 4-7) per thread (half
+ * row-blocks at one or two columns without the norm prologue or GeGLU).
+ * Kernels 1-4 and 6-8 are bit-exact with the reference; the fast prefill kernel adds
  * each block's eight lane-class sums before scaling, so its outputs agree
  * within the 1e-4 relative tolerance of projections (M >= 64 prefill). */
 int32_t hp_hip_set_matvec_kernel(int32_t which);

@@ -283,7 +283,7 @@ def test_decode_layer_kernels_bit_identical(hip, full):
     data = DM.layer_host_data(shape, seed, 0)
     x = S.activations(S.derive(seed, "x"), 1, shape.hidden).reshape(-1) * 4
     outs = {}
-    for kernel in (0, 1, 3, 6):
+    for kernel in (0, 1, 3, 6, 7, 8):
         hip.setMatvecKernel(kernel)
         model = DM.HipDecodeModel(shape)
         model.add_layer(data)
@@ -297,7 +297,7 @@ def test_decode_layer_kernels_bit_identical(hip, full):
         finally:
             model.release()
             hip.setMatvecKernel(0)
-    for kernel in (1, 3, 6):
+    for kernel in (1, 3, 6, 7, 8):
         for got, ref in zip(outs[kernel], outs[0]):
             assert np.array_equal(got.view(np.uint8), ref.view(np.uint8)), kernel
 

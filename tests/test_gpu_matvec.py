@@ -21,12 +21,15 @@ def _weights(type_name, seed, rows, k):
     return S.weight_blocks(type_name, seed, rows, k)
 
 
-@pytest.fixture(params=[1, 2, 3, 4, 6], ids=["valu", "mfma", "half", "prefill", "wide"])
+@pytest.fixture(params=[1, 2, 3, 4, 6, 7, 8], ids=["valu", "mfma", "half", "prefill", "wide", "wide-whole",
+                                                   "wide-half"])
 def kernel(request, hip):
     """Runs the test with the vector-ALU, the matrix-core, the half-split
     vector-ALU, the bit-exact prefill and the wide (one workgroup per block of
-    rows) matvec; a launch a forced kernel does not take (the wide kernel:
-    more than four columns, mixed types) runs the automatic choice."""
+    rows) matvec, the last with whole and with half row-blocks per thread; a
+    launch a forced kernel does not take (the wide kernel: more than four
+    columns, mixed types; half row-blocks: more than two columns) runs the
+    automatic choice."""
     hip.setMatvecKernel(request.param)
     yield request.param
     hip.setMatvecKernel(0)
@@ -131,13 +134,14 @@ def test_wide_kernel_columns(hip, oracle, type_name, rows, k):
     x[2, k // 3] = 1e30
     x[3] *= 1e-39
     h = hip.createHipQuantizedWeightHandle(type_name, w, k, rows)
-    hip.setMatvecKernel(6)
     try:
         ref = oracle.matmul(TYPES[type_name], w, x, rows, threads=8)
-        for m in (1, 2, 3, 4):
-            print(f"wide {type_name} rows={rows} k={k} m={m}", flush=True)
-            got = hip.matMulQuantizedHipResident(h, x[:m], k, rows, m).reshape(m, rows)
-            assert np.array_equal(_bits(got), _bits(ref[:m])), m
+        for sel in (6, 7, 8):  # automatic split, whole and half row-blocks per thread
+            hip.setMatvecKernel(sel)
+            for m in (1, 2, 3, 4):
+                print(f"wide sel={sel} {type_name} rows={rows} k={k} m={m}", flush=True)
+                got = hip.matMulQuantizedHipResident(h, x[:m], k, rows, m).reshape(m, rows)
+                assert np.array_equal(_bits(got), _bits(ref[:m])), (sel, m)
     finally:
         hip.setMatvecKernel(0)
         hip.releaseHipQuantizedWeightHandle(h)
@@ -153,8 +157,8 @@ def _q6k_full_range_scales(seed, rows, k):
     return w.reshape(rows, -1)
 
 
-@pytest.mark.parametrize("kernel_id", [0, 1, 2, 3, 4, 5, 6], ids=["auto", "valu", "mfma", "half", "prefill",
-                                                                  "fast", "wide"])
+@pytest.mark.parametrize("kernel_id", [0, 1, 2, 3, 4, 5, 6, 7, 8],
+                         ids=["auto", "valu", "mfma", "half", "prefill", "fast", "wide", "wide-whole", "wide-half"])
 def test_q6k_full_range_scales(hip, oracle, kernel_id):
     """Q6_K scales beyond +-66 make sc * (q - 32) inexact as an f16 matrix-core
     operand; such weights run the vector-ALU kernels under every selector, so
