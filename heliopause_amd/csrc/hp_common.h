@@ -121,6 +121,184 @@ __host__ __device__ constexpr size_t q8_image_bytes(int cols, int nb) {
   return (size_t)cols * nb * kQ8BlockBytes + (size_t)((cols * nb + 3) & ~3) * 4;
 }
 
+// Kernel entry: one dword of every 64-byte line of the kernel's argument
+// segment (an argument struct of sizeof(T) bytes at its start), read as one
+// batch of scalar loads followed by one wait, in one asm statement (the
+// compiler splits such loads into dependent batches otherwise, each a round
+// trip to memory).  The scalar loads of the arguments that follow then hit
+// the scalar cache.  The loads complete inside the statement, so no load is
+// in flight when its registers are reused.
+template <int N>
+__device__ __forceinline__ void kernarg_lines(const void *p);
+template <>
+__device__ __forceinline__ void kernarg_lines<1>(const void *p) {
+  uint32_t d[1];
+  asm volatile("s_load_dword %0, %1, 0x0\n"
+               "s_waitcnt lgkmcnt(0)"
+               : "=&s"(d[0])
+               : "s"(p));
+}
+template <>
+__device__ __forceinline__ void kernarg_lines<2>(const void *p) {
+  uint32_t d[2];
+  asm volatile("s_load_dword %0, %2, 0x0\n"
+               "s_load_dword %1, %2, 0x40\n"
+               "s_waitcnt lgkmcnt(0)"
+               : "=&s"(d[0]), "=&s"(d[1])
+               : "s"(p));
+}
+template <>
+__device__ __forceinline__ void kernarg_lines<3>(const void *p) {
+  uint32_t d[3];
+  asm volatile("s_load_dword %0, %3, 0x0\n"
+               "s_load_dword %1, %3, 0x40\n"
+               "s_load_dword %2, %3, 0x80\n"
+               "s_waitcnt lgkmcnt(0)"
+               : "=&s"(d[0]), "=&s"(d[1]), "=&s"(d[2])
+               : "s"(p));
+}
+template <>
+__device__ __forceinline__ void kernarg_lines<4>(const void *p) {
+  uint32_t d[4];
+  asm volatile("s_load_dword %0, %4, 0x0\n"
+               "s_load_dword %1, %4, 0x40\n"
+               "s_load_dword %2, %4, 0x80\n"
+               "s_load_dword %3, %4, 0xc0\n"
+               "s_waitcnt lgkmcnt(0)"
+               : "=&s"(d[0]), "=&s"(d[1]), "=&s"(d[2]), "=&s"(d[3])
+               : "s"(p));
+}
+template <>
+__device__ __forceinline__ void kernarg_lines<5>(const void *p) {
+  uint32_t d[5];
+  asm volatile("s_load_dword %0, %5, 0x0\n"
+               "s_load_dword %1, %5, 0x40\n"
+               "s_load_dword %2, %5, 0x80\n"
+               "s_load_dword %3, %5, 0xc0\n"
+               "s_load_dword %4, %5, 0x100\n"
+               "s_waitcnt lgkmcnt(0)"
+               : "=&s"(d[0]), "=&s"(d[1]), "=&s"(d[2]), "=&s"(d[3]), "=&s"(d[4])
+               : "s"(p));
+}
+template <>
+__device__ __forceinline__ void kernarg_lines<6>(const void *p) {
+  uint32_t d[6];
+  asm volatile("s_load_dword %0, %6, 0x0\n"
+               "s_load_dword %1, %6, 0x40\n"
+               "s_load_dword %2, %6, 0x80\n"
+               "s_load_dword %3, %6, 0xc0\n"
+               "s_load_dword %4, %6, 0x100\n"
+               "s_load_dword %5, %6, 0x140\n"
+               "s_waitcnt lgkmcnt(0)"
+               : "=&s"(d[0]), "=&s"(d[1]), "=&s"(d[2]), "=&s"(d[3]), "=&s"(d[4]), "=&s"(d[5])
+               : "s"(p));
+}
+template <>
+__device__ __forceinline__ void kernarg_lines<7>(const void *p) {
+  uint32_t d[7];
+  asm volatile("s_load_dword %0, %7, 0x0\n"
+               "s_load_dword %1, %7, 0x40\n"
+               "s_load_dword %2, %7, 0x80\n"
+               "s_load_dword %3, %7, 0xc0\n"
+               "s_load_dword %4, %7, 0x100\n"
+               "s_load_dword %5, %7, 0x140\n"
+               "s_load_dword %6, %7, 0x180\n"
+               "s_waitcnt lgkmcnt(0)"
+               : "=&s"(d[0]), "=&s"(d[1]), "=&s"(d[2]), "=&s"(d[3]), "=&s"(d[4]), "=&s"(d[5]), "=&s"(d[6])
+               : "s"(p));
+}
+template <>
+__device__ __forceinline__ void kernarg_lines<8>(const void *p) {
+  uint32_t d[8];
+  asm volatile("s_load_dword %0, %8, 0x0\n"
+               "s_load_dword %1, %8, 0x40\n"
+               "s_load_dword %2, %8, 0x80\n"
+               "s_load_dword %3, %8, 0xc0\n"
+               "s_load_dword %4, %8, 0x100\n"
+               "s_load_dword %5, %8, 0x140\n"
+               "s_load_dword %6, %8, 0x180\n"
+               "s_load_dword %7, %8, 0x1c0\n"
+               "s_waitcnt lgkmcnt(0)"
+               : "=&s"(d[0]), "=&s"(d[1]), "=&s"(d[2]), "=&s"(d[3]), "=&s"(d[4]), "=&s"(d[5]), "=&s"(d[6]), "=&s"(d[7])
+               : "s"(p));
+}
+template <>
+__device__ __forceinline__ void kernarg_lines<9>(const void *p) {
+  uint32_t d[9];
+  asm volatile("s_load_dword %0, %9, 0x0\n"
+               "s_load_dword %1, %9, 0x40\n"
+               "s_load_dword %2, %9, 0x80\n"
+               "s_load_dword %3, %9, 0xc0\n"
+               "s_load_dword %4, %9, 0x100\n"
+               "s_load_dword %5, %9, 0x140\n"
+               "s_load_dword %6, %9, 0x180\n"
+               "s_load_dword %7, %9, 0x1c0\n"
+               "s_load_dword %8, %9, 0x200\n"
+               "s_waitcnt lgkmcnt(0)"
+               : "=&s"(d[0]), "=&s"(d[1]), "=&s"(d[2]), "=&s"(d[3]), "=&s"(d[4]), "=&s"(d[5]), "=&s"(d[6]), "=&s"(d[7]), "=&s"(d[8])
+               : "s"(p));
+}
+template <>
+__device__ __forceinline__ void kernarg_lines<10>(const void *p) {
+  uint32_t d[10];
+  asm volatile("s_load_dword %0, %10, 0x0\n"
+               "s_load_dword %1, %10, 0x40\n"
+               "s_load_dword %2, %10, 0x80\n"
+               "s_load_dword %3, %10, 0xc0\n"
+               "s_load_dword %4, %10, 0x100\n"
+               "s_load_dword %5, %10, 0x140\n"
+               "s_load_dword %6, %10, 0x180\n"
+               "s_load_dword %7, %10, 0x1c0\n"
+               "s_load_dword %8, %10, 0x200\n"
+               "s_load_dword %9, %10, 0x240\n"
+               "s_waitcnt lgkmcnt(0)"
+               : "=&s"(d[0]), "=&s"(d[1]), "=&s"(d[2]), "=&s"(d[3]), "=&s"(d[4]), "=&s"(d[5]), "=&s"(d[6]), "=&s"(d[7]), "=&s"(d[8]), "=&s"(d[9])
+               : "s"(p));
+}
+template <>
+__device__ __forceinline__ void kernarg_lines<11>(const void *p) {
+  uint32_t d[11];
+  asm volatile("s_load_dword %0, %11, 0x0\n"
+               "s_load_dword %1, %11, 0x40\n"
+               "s_load_dword %2, %11, 0x80\n"
+               "s_load_dword %3, %11, 0xc0\n"
+               "s_load_dword %4, %11, 0x100\n"
+               "s_load_dword %5, %11, 0x140\n"
+               "s_load_dword %6, %11, 0x180\n"
+               "s_load_dword %7, %11, 0x1c0\n"
+               "s_load_dword %8, %11, 0x200\n"
+               "s_load_dword %9, %11, 0x240\n"
+               "s_load_dword %10, %11, 0x280\n"
+               "s_waitcnt lgkmcnt(0)"
+               : "=&s"(d[0]), "=&s"(d[1]), "=&s"(d[2]), "=&s"(d[3]), "=&s"(d[4]), "=&s"(d[5]), "=&s"(d[6]), "=&s"(d[7]), "=&s"(d[8]), "=&s"(d[9]), "=&s"(d[10])
+               : "s"(p));
+}
+template <>
+__device__ __forceinline__ void kernarg_lines<12>(const void *p) {
+  uint32_t d[12];
+  asm volatile("s_load_dword %0, %12, 0x0\n"
+               "s_load_dword %1, %12, 0x40\n"
+               "s_load_dword %2, %12, 0x80\n"
+               "s_load_dword %3, %12, 0xc0\n"
+               "s_load_dword %4, %12, 0x100\n"
+               "s_load_dword %5, %12, 0x140\n"
+               "s_load_dword %6, %12, 0x180\n"
+               "s_load_dword %7, %12, 0x1c0\n"
+               "s_load_dword %8, %12, 0x200\n"
+               "s_load_dword %9, %12, 0x240\n"
+               "s_load_dword %10, %12, 0x280\n"
+               "s_load_dword %11, %12, 0x2c0\n"
+               "s_waitcnt lgkmcnt(0)"
+               : "=&s"(d[0]), "=&s"(d[1]), "=&s"(d[2]), "=&s"(d[3]), "=&s"(d[4]), "=&s"(d[5]), "=&s"(d[6]), "=&s"(d[7]), "=&s"(d[8]), "=&s"(d[9]), "=&s"(d[10]), "=&s"(d[11])
+               : "s"(p));
+}
+template <class T>
+__device__ __forceinline__ void kernarg_warm() {
+  constexpr int kLines = (int)((sizeof(T) + 63) / 64);
+  static_assert(kLines >= 1 && kLines <= 12, "argument struct of at most 768 bytes");
+  kernarg_lines<kLines>((const void *)__builtin_amdgcn_kernarg_segment_ptr());
+}
+
 // Launchers (return hipError_t of the launch).
 hipError_t launch_q8k_natural(const float *x, int k, int cols, int8_t *qs, float *d, int16_t *bsums,
                               hipStream_t s);

@@ -297,6 +297,8 @@ __global__ __launch_bounds__(256) void kquant_matvec_kernel(const MatvecArgs a) 
 template <int M, int NORM, int TYPE>
 __global__ __launch_bounds__(256) void kquant_matvec_half_kernel(const MatvecArgs a) {
   extern __shared__ __align__(16) uint8_t smem[];
+  // the argument lines in one round trip (measured: Q/K/V 5.89 -> 5.37 us)
+  kernarg_warm<MatvecArgs>();
   const TileGeom g = a.g;
   const int nb = g.nb, S = g.S, R = g.R, Rh = a.Rh;
   uint8_t *xq = smem;

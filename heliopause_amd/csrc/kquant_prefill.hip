@@ -319,6 +319,7 @@ __device__ void pf_tile(const PfArgs &a, const PfWeight &W, int T0, int col0, ui
 }
 
 __global__ __launch_bounds__(256) void kquant_prefill_kernel(const PfArgs a) {
+  kernarg_warm<PfArgs>();
   extern __shared__ __align__(16) uint8_t smem[];
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -760,6 +761,7 @@ template <bool PAIR>
 __global__ __launch_bounds__(kF3Threads) __attribute__((amdgpu_waves_per_eu(2, 2))) void
 kquant_prefill_fast_kernel(
     const F2Args a) {
+  kernarg_warm<F2Args>();
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int tiles = a.total_rt * a.col_tiles;
@@ -863,6 +865,7 @@ kquant_prefill_fast_kernel(
 // + range 1, up likewise, then fround(gelu(gate) * up).  One thread per
 // output: (item, gate wave, sum index, lane), lane fastest.
 __global__ __launch_bounds__(256) void f2_geglu_tail_kernel(const F2Args a, int rem) {
+  kernarg_warm<F2Args>();
   constexpr int kHalf = kF3Waves / 2;
   const int t = blockIdx.x * blockDim.x + threadIdx.x;
   const int lane = t & 63, k = (t >> 6) % (kF3RS * 16), w = (t >> 6) / (kF3RS * 16) % kHalf;
@@ -886,6 +889,7 @@ __global__ __launch_bounds__(256) void f2_geglu_tail_kernel(const F2Args a, int 
 // out = ((part_0 + part_1) + ...) + part_{ks-1} over the launch's outputs
 // (the weights' [cols][rows] outputs end to end), four floats per thread.
 __global__ __launch_bounds__(256) void f2_reduce_kernel(const F2Args a, size_t total) {
+  kernarg_warm<F2Args>();
   const size_t i = 4 * ((size_t)blockIdx.x * blockDim.x + threadIdx.x);
   if (i >= total) return;
   int w = 0;

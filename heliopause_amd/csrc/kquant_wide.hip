@@ -230,6 +230,12 @@ __device__ __forceinline__ void wide_norm_finish(const NormIn &n, NormRegs &nr, 
 // halves agree but for one wave at the boundary).
 template <int M, int TYPE, int NORM, bool PAIR, int TPL, bool HALF>
 __global__ __launch_bounds__(HALF ? kWideHalfThreads : kWideMaxThreads) void kquant_wide_kernel(const MatvecArgs a) {
+  // the argument lines in one round trip where the first loads need most of
+  // them: the norm prologue's inputs, the two weights of gate/up (measured:
+  // gate/up + GeGLU 11.1 -> 10.7 us); a plain launch's input loads go out
+  // after the first few lines and the rest arrive under them (down 9.2 us,
+  // 9.8 with the warm-up)
+  if constexpr (NORM != 0 || PAIR) kernarg_warm<MatvecArgs>();
   extern __shared__ __align__(16) uint8_t smem[];
   constexpr bool Q4 = TYPE == kTypeQ4K;
   constexpr int NC = Q4 ? 9 : 8;
