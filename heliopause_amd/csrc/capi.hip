@@ -328,9 +328,9 @@ bool use_mfma(size_t cols, int nb, int tiles16, bool f16ok) {
 // 512, 10240 rows 1707: 7.39 against 7.75 us) and for two to four columns up
 // to ~1024 tiles; slower for gate/up (3414 tiles), the head, and 40-block
 // rows (S = 20: down 15.6 against 13.2 us).
-bool use_half(int cols, const TileGeom &g, int tiles) {
+bool use_half(int cols, const TileGeom &g, int tiles, int rows) {
   const int forced = st().matvec_kernel;
-  if (cols > 4 || g.S > 32) return false;
+  if (cols > 4 || g.S > 32 || rows >= (1 << 20)) return false;  // (rows: the kernel's index range)
   if (forced == 3) return true;
   if (forced != 0 || g.S > 16) return false;
   return tiles <= (cols == 1 ? 2048 : 1024);
@@ -566,7 +566,7 @@ int32_t run_matvec(size_t count, Handle *const *hs, const float *d_input, size_t
     a.cols = c;
     a.out_col0 = (int)m0;
     hipEvent_t e1 = prof_begin(stream);
-    if (use_half(c, g, a.total_tiles))
+    if (use_half(c, g, a.total_tiles, a.total_rows))
       HP_HIP_TRY(launch_matvec_half(a, s.num_cus, stream));
     else
       HP_HIP_TRY(launch_matvec(a, s.num_cus, stream));
@@ -600,7 +600,7 @@ int32_t run_matvec_geglu(Handle *hg, Handle *hu, const float *d_input, size_t in
   const bool f16 = f16_ok(2, pair);
   const bool wide = prefill_kind(cols, f16) == 0 && hg->type == hu->type && use_wide_pair(pair, cols);
   const bool fused = !wide && cols <= 4 && s.matvec_kernel <= 1 && !use_mfma(cols, g.nb, tiles16, f16) &&
-                     !use_half((int)cols, g, 2 * hg->tiles) && cols_per_launch(g, s.max_lds) >= (int)cols;
+                     !use_half((int)cols, g, 2 * hg->tiles, (int)(2 * rows)) && cols_per_launch(g, s.max_lds) >= (int)cols;
   if (norm && !((fused || wide) && cols == 1 && g.nb <= 16)) {
     int32_t rc = run_norm(norm->y, (int)cols, (int)input_size, norm->w_post, norm->mode == 2 ? norm->x_res : nullptr,
                           norm->scale, norm->x_out, norm->w_next, norm_scratch, norm->eps, stream);

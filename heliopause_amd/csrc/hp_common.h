@@ -114,6 +114,14 @@ struct MatvecArgs {
 // exact for 1 <= d <= 256 (checked exhaustively).
 __host__ __device__ constexpr uint32_t div_magic(int d) { return d <= 1 ? 0u : 0xFFFFFFFFu / (uint32_t)d + 1u; }
 
+// x / d with m = div_magic(d) (0 <= x < 2^20, 1 <= d <= 256).  No branch (a
+// divisor of 1 adds x back): a branch between loads would split the loaded
+// registers' live ranges and make the compiler wait for them.
+__device__ __forceinline__ int mdiv(int x, uint32_t m) {
+  const uint32_t keep = 0u - (uint32_t)(m == 0u);
+  return (int)(__umulhi((uint32_t)x, m) + ((uint32_t)x & keep));
+}
+
 // The vector-ALU matvec's LDS image of `cols` quantised input columns: the
 // cols * nb Q8_K blocks (kQ8BlockBytes each, column-major) and then their
 // cols * nb f32 scales, padded to 16 bytes.

@@ -88,12 +88,6 @@ __host__ __device__ inline WideLayout wide_layout(int cols, int nb, int type, in
 
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 
-// No branch (a divisor of 1 adds x back): a branch between loads would split
-// the loaded registers' live ranges and make the compiler wait for them.
-__device__ __forceinline__ int mdiv(int x, uint32_t m) {
-  const uint32_t keep = 0u - (uint32_t)(m == 0u);
-  return (int)(__umulhi((uint32_t)x, m) + ((uint32_t)x & keep));
-}
 
 // One (row, block) task's addresses in the tile layout.
 struct WideTask {
