@@ -286,13 +286,6 @@ __global__ __launch_bounds__(256) void attn_partial_kernel(const AttnArgs a) {
       for (int p = 0; p < 2; p++) tab[p] = a.rope_table[min(lane + 64 * p, half - 1)];
     }
   }
-  // tokens at *a.position .. + a.tokens - 1 share the window of the last
-  // (attentionRange of the largest position); token blockIdx.z sees the keys
-  // up to its own position (causalMask)
-  const int tok = blockIdx.z;
-  const int pos = *a.position + a.pos_offset + (a.tokens - 1);
-  const int pos_t = pos - (a.tokens - 1) + tok;
-
   const int kj = tid >> 3, kp = tid & 7;
   const int kslot = c * kAttnChunk + kj;
   uint4 kraw[4];
@@ -308,6 +301,15 @@ __global__ __launch_bounds__(256) void attn_partial_kernel(const AttnArgs a) {
     vraw[j] = *reinterpret_cast<const uint2 *>(a.v_cache + head_base + (size_t)min(vslot0 + j, cap - 1) * kHeadDim +
                                                4 * lane);
   __builtin_amdgcn_sched_barrier(0);  // every load issued before the prologue's first use of one
+
+  // tokens at *a.position .. + a.tokens - 1 share the window of the last
+  // (attentionRange of the largest position); token blockIdx.z sees the keys
+  // up to its own position (causalMask).  Read after the cache loads are
+  // issued (they take slots, not positions): a scalar read of device memory
+  // placed before them made them wait for its round trip.
+  const int tok = blockIdx.z;
+  const int pos = *a.position + a.pos_offset + (a.tokens - 1);
+  const int pos_t = pos - (a.tokens - 1) + tok;
 
   int start, count;
   window_of(pos, cap, a.window, &start, &count);
