@@ -412,7 +412,8 @@ bool use_wide_pair(Handle *const *hs, size_t cols) {
 // One matvec launch per column chunk covering every weight (multi == one
 // launch, lib.rs:300-426); each launch quantises its columns in its prologue.
 int32_t run_norm(const float *y, int rows, int n, const float *w_post, const float *x_res, float scale, float *x_out,
-                 const float *w_next, float *next_out, double eps, hipStream_t stream, uint8_t *q8img = nullptr);
+                 const float *w_next, float *next_out, double eps, hipStream_t stream, uint8_t *q8img = nullptr,
+                 uint8_t *xt = nullptr);
 
 // Whether a one-column launch over these weights runs a vector-ALU kernel,
 // which can form its input with the norm prologue.
@@ -450,10 +451,33 @@ int32_t run_matvec(size_t count, Handle *const *hs, const float *d_input, size_t
   const bool f16 = f16_ok(count, hs);
   const bool wide = prefill_kind(cols, f16) == 0 && use_wide(count, hs, cols);
   const bool wide_norm = wide && cols == 1 && g_nb_of(hs) <= 16;  // the wide kernel's norm prologue
+  const int kind = prefill_kind(cols, f16);
+  if (kind && cols > 65535) return fail(HP_ERR_SHAPE, "too many columns");
+  MfmaLaunch l{};
+  l.count = (int)count;
+  l.k = (int)input_size;
+  l.cols = (int)cols;
+  for (size_t i = 0; i < count; i++) {
+    l.seg[i] = hs[i]->segs;
+    l.type[i] = hs[i]->type;
+    l.rows[i] = (int)hs[i]->row_count;
+    l.out[i] = d_outs[i];
+  }
+  uint8_t *pre = nullptr;  // the prefill kernels' scratch
+  if (kind) {
+    const size_t need = kind == 2 ? prefill_fast_bytes(l, s.num_cus) : prefill_q8k_bytes((int)input_size, (int)cols);
+    void *p = nullptr;
+    int32_t rc = stream_scratch(stream, kScratchPrefill, need, &p);
+    if (rc != HP_OK) return rc;
+    pre = static_cast<uint8_t *>(p);
+  }
+  bool tiles_ready = false;  // the norm kernel wrote the fast prefill's tiles
   if (norm && (wide ? !wide_norm : !norm_prologue_ok(count, hs, cols))) {
     uint8_t *img = image_ok && img_scratch ? img_scratch : nullptr;
+    tiles_ready = kind == 2 && input_size % kQK == 0;
     int32_t rc = run_norm(norm->y, (int)cols, (int)input_size, norm->w_post, norm->mode == 2 ? norm->x_res : nullptr,
-                          norm->scale, norm->x_out, norm->w_next, norm_scratch, norm->eps, stream, img);
+                          norm->scale, norm->x_out, norm->w_next, norm_scratch, norm->eps, stream, img,
+                          tiles_ready ? pre : nullptr);
     if (rc != HP_OK) return rc;
     d_input = norm_scratch;
     norm = nullptr;
@@ -486,32 +510,16 @@ int32_t run_matvec(size_t count, Handle *const *hs, const float *d_input, size_t
   }
   a.total_rows = rows_all;
   a.total_units = a.Rh ? (rows_all + a.Rh - 1) / a.Rh : 0;
-  if (const int kind = prefill_kind(cols, f16)) {
-    if (cols > 65535) return fail(HP_ERR_SHAPE, "too many columns");
-    MfmaLaunch l{};
-    l.count = (int)count;
-    l.k = (int)input_size;
-    l.cols = (int)cols;
-    for (size_t i = 0; i < count; i++) {
-      l.seg[i] = hs[i]->segs;
-      l.type[i] = hs[i]->type;
-      l.rows[i] = (int)hs[i]->row_count;
-      l.out[i] = d_outs[i];
-    }
-    const size_t need = kind == 2 ? prefill_fast_bytes(l, s.num_cus) : prefill_q8k_bytes((int)input_size, (int)cols);
-    void *pre = nullptr;
-    int32_t rc = stream_scratch(stream, kScratchPrefill, need, &pre);
-    if (rc != HP_OK) return rc;
-    uint8_t *q8 = static_cast<uint8_t *>(pre);
+  if (kind) {
     hipEvent_t e1 = prof_begin(stream);
     if (kind == 2) {
-      HP_HIP_TRY(launch_prefill_fast(l, d_input, q8, s.num_cus, stream));
+      HP_HIP_TRY(launch_prefill_fast(l, d_input, pre, s.num_cus, stream, tiles_ready));
     } else {
-      HP_HIP_TRY(launch_q8k_prefill(d_input, (int)input_size, (int)cols, q8, stream));
-      HP_HIP_TRY(launch_prefill(l, q8, s.num_cus, stream));
+      HP_HIP_TRY(launch_q8k_prefill(d_input, (int)input_size, (int)cols, pre, stream));
+      HP_HIP_TRY(launch_prefill(l, pre, s.num_cus, stream));
     }
     prof_end(HP_KERNEL_MATVEC, e1, stream);
-    s.launches += kind == 2 ? prefill_fast_launches(l, s.num_cus) : 2;
+    s.launches += kind == 2 ? prefill_fast_launches(l, s.num_cus) - (tiles_ready ? 1 : 0) : 2;
     s.matmul_calls++;
     return HP_OK;
   }
@@ -601,9 +609,30 @@ int32_t run_matvec_geglu(Handle *hg, Handle *hu, const float *d_input, size_t in
   const bool wide = prefill_kind(cols, f16) == 0 && hg->type == hu->type && use_wide_pair(pair, cols);
   const bool fused = !wide && cols <= 4 && s.matvec_kernel <= 1 && !use_mfma(cols, g.nb, tiles16, f16) &&
                      !use_half((int)cols, g, 2 * hg->tiles, (int)(2 * rows)) && cols_per_launch(g, s.max_lds) >= (int)cols;
+  // fast prefill: gate and up rows in one tile, GeGLU in its epilogue
+  const bool fast = prefill_kind(cols, f16) == 2 && hg->type == hu->type;
+  MfmaLaunch l{};
+  uint8_t *pre = nullptr;  // its scratch, tiles first
+  if (fast) {
+    l.count = 2;
+    l.k = (int)input_size;
+    l.cols = (int)cols;
+    for (int i = 0; i < 2; i++) {
+      l.seg[i] = pair[i]->segs;
+      l.type[i] = pair[i]->type;
+      l.rows[i] = (int)rows;
+    }
+    void *p = nullptr;
+    int32_t rc = stream_scratch(stream, kScratchPrefill, prefill_fast_geglu_bytes(l, s.num_cus), &p);
+    if (rc != HP_OK) return rc;
+    pre = static_cast<uint8_t *>(p);
+  }
+  bool tiles_ready = false;  // the norm kernel wrote the fast prefill's tiles
   if (norm && !((fused || wide) && cols == 1 && g.nb <= 16)) {
+    tiles_ready = fast && input_size % kQK == 0;
     int32_t rc = run_norm(norm->y, (int)cols, (int)input_size, norm->w_post, norm->mode == 2 ? norm->x_res : nullptr,
-                          norm->scale, norm->x_out, norm->w_next, norm_scratch, norm->eps, stream);
+                          norm->scale, norm->x_out, norm->w_next, norm_scratch, norm->eps, stream, nullptr,
+                          tiles_ready ? pre : nullptr);
     if (rc != HP_OK) return rc;
     d_input = norm_scratch;
     norm = nullptr;
@@ -671,26 +700,11 @@ int32_t run_matvec_geglu(Handle *hg, Handle *hu, const float *d_input, size_t in
     s.matmul_calls++;
     return HP_OK;
   }
-  if (prefill_kind(cols, f16) == 2 && hg->type == hu->type) {
-    // fast prefill: gate and up rows in one tile, GeGLU in its epilogue
-    MfmaLaunch l{};
-    l.count = 2;
-    l.k = (int)input_size;
-    l.cols = (int)cols;
-    Handle *hs[2] = {hg, hu};
-    for (int i = 0; i < 2; i++) {
-      l.seg[i] = hs[i]->segs;
-      l.type[i] = hs[i]->type;
-      l.rows[i] = (int)rows;
-    }
-    void *pre = nullptr;
-    int32_t rc = stream_scratch(stream, kScratchPrefill, prefill_fast_geglu_bytes(l, s.num_cus), &pre);
-    if (rc != HP_OK) return rc;
+  if (fast) {
     hipEvent_t e1 = prof_begin(stream);
-    HP_HIP_TRY(launch_prefill_fast_geglu(l, d_input, static_cast<uint8_t *>(pre), s.gelu_lut, d_out,
-                                         s.num_cus, stream));
+    HP_HIP_TRY(launch_prefill_fast_geglu(l, d_input, pre, s.gelu_lut, d_out, s.num_cus, stream, tiles_ready));
     prof_end(HP_KERNEL_MATVEC, e1, stream);
-    s.launches += prefill_fast_geglu_launches(l, s.num_cus);
+    s.launches += prefill_fast_geglu_launches(l, s.num_cus) - (tiles_ready ? 1 : 0);
     s.matmul_calls++;
     return HP_OK;
   }
@@ -1026,9 +1040,11 @@ int32_t run_attention(AttnArgs a, float *partials, hipStream_t stream) {
 }
 
 int32_t run_norm(const float *y, int rows, int n, const float *w_post, const float *x_res, float scale, float *x_out,
-                 const float *w_next, float *next_out, double eps, hipStream_t stream, uint8_t *q8img) {
+                 const float *w_next, float *next_out, double eps, hipStream_t stream, uint8_t *q8img,
+                 uint8_t *xt) {
   NormArgs a{};
   a.q8img = q8img;
+  a.xt = xt;
   a.y = y;
   a.w_post = w_post;
   a.x_res = x_res;

@@ -37,6 +37,7 @@
 #include "hp_wave.h"
 #include "hp_q8k16.h"
 #include "hp_attn.h"
+#include "hp_f2tile.h"
 
 namespace hp {
 
@@ -71,6 +72,17 @@ __device__ __forceinline__ double rms_scale(const float (&v)[kNormPer], int n, d
 __global__ __launch_bounds__(256) void norm_residual_kernel(const NormArgs a) {
   __shared__ double sh[8];  // two workgroup sums
   const int tid = threadIdx.x;
+  if (a.xt && (int)blockIdx.x >= a.rows) {
+    // a padding column of the last activation tile: zero blocks, as the
+    // prefill pre-pass writes them
+    const int g = tid >> 4, i16 = tid & 15, nb = a.n / kQK;
+    float z[16];
+#pragma unroll
+    for (int e = 0; e < 16; e++) z[e] = 0.0f;
+    for (int b = g; b < nb; b += 16)
+      f2_tile_store16(z, i16, a.xt + ((size_t)(blockIdx.x / kF2Cols) * nb + b) * kF2XTile, blockIdx.x % kF2Cols);
+    return;
+  }
   const size_t row = (size_t)blockIdx.x * a.n;
   // every input first, one memory round trip: the loads take no branch
   // (indexes past n re-read element n - 1, absent operands re-read y), so
@@ -114,23 +126,29 @@ __global__ __launch_bounds__(256) void norm_residual_kernel(const NormArgs a) {
       const int i = tid + 256 * j;
       const float o = a.w_next ? (float)(((double)v[j] * sc) * (double)wn[j]) : (float)((double)v[j] * sc);
       if (i < a.n) a.next_out[row + i] = o;
-      if (a.q8img) xs[i] = o;
+      if (a.q8img || a.xt) xs[i] = o;
     }
-    if (a.q8img) {
-      // the row as Q8_K blocks of a matvec input image (n a multiple of 256):
-      // 16-lane group g quantises block g
+    if (a.q8img || a.xt) {
+      // the row as Q8_K blocks (n a multiple of 256) of a matvec input
+      // image, or of the fast prefill's activation tiles (column blockIdx.x):
+      // 16-lane group g quantises blocks g, g + 16, ...
       __syncthreads();
       const int g = tid >> 4, i16 = tid & 15, nb = a.n / kQK;
-      if (g < nb) {
+      for (int b = g; b < nb; b += 16) {
         float xv[16];
         const int jj = i16 >> 1, u = i16 & 1;
 #pragma unroll
         for (int c = 0; c < 4; c++)
 #pragma unroll
-          for (int i = 0; i < 4; i++) xv[4 * c + i] = xs[g * kQK + 32 * jj + 8 * c + 4 * u + i];
-        const size_t q = (size_t)blockIdx.x * nb + g;
-        q8k_block16(xv, i16, a.q8img + q * kQ8BlockBytes,
-                    reinterpret_cast<float *>(a.q8img + (size_t)a.rows * nb * kQ8BlockBytes) + q);
+          for (int i = 0; i < 4; i++) xv[4 * c + i] = xs[b * kQK + 32 * jj + 8 * c + 4 * u + i];
+        if (a.q8img) {
+          const size_t q = (size_t)blockIdx.x * nb + b;
+          q8k_block16(xv, i16, a.q8img + q * kQ8BlockBytes,
+                      reinterpret_cast<float *>(a.q8img + (size_t)a.rows * nb * kQ8BlockBytes) + q);
+        }
+        if (a.xt)
+          f2_tile_store16(xv, i16, a.xt + ((size_t)(blockIdx.x / kF2Cols) * nb + b) * kF2XTile,
+                          blockIdx.x % kF2Cols);
       }
     }
   }
@@ -629,8 +647,9 @@ __global__ __launch_bounds__(256) void attn_reduce_kernel(const AttnArgs a) {
 
 hipError_t launch_norm_residual(const NormArgs &a, hipStream_t s) {
   if (a.n < 1 || a.n > 256 * kNormPer || a.rows < 1) return hipErrorInvalidValue;
-  if (a.q8img && (a.n % kQK != 0 || !a.next_out)) return hipErrorInvalidValue;
-  hipLaunchKernelGGL(norm_residual_kernel, dim3(a.rows), dim3(256), 0, s, a);
+  if ((a.q8img || a.xt) && (a.n % kQK != 0 || !a.next_out)) return hipErrorInvalidValue;
+  const int grid = a.xt ? (a.rows + kF2Cols - 1) / kF2Cols * kF2Cols : a.rows;
+  hipLaunchKernelGGL(norm_residual_kernel, dim3(grid), dim3(256), 0, s, a);
   return hipGetLastError();
 }
 

@@ -380,7 +380,9 @@ size_t prefill_lds_bytes();
 hipError_t launch_q8k_prefill(const float *x, int k, int cols, uint8_t *scratch, hipStream_t s);
 hipError_t launch_prefill(const MfmaLaunch &l, const uint8_t *scratch, int num_cus, hipStream_t s);
 // Fast prefill (within the 1e-4 relative tolerance of projections, not
-// bit-exact): its own pre-pass of x into scratch, then 128-row x 64-column
+// bit-exact): its own pre-pass of x into scratch (skipped with tiles_ready:
+// the norm kernel already wrote the tiles, NormArgs::xt, at the scratch's
+// start), then 128-row x 64-column
 // tiles with the eight classes in one accumulator.  A launch with fewer
 // tiles than two per CU splits each tile's blocks into consecutive ranges
 // whose partial sums (in scratch) a reduction adds in range order.
@@ -396,9 +398,10 @@ int prefill_fast_launches(const MfmaLaunch &l, int num_cus);  // 2, or 3 with th
 size_t prefill_fast_geglu_bytes(const MfmaLaunch &l, int num_cus);
 int prefill_fast_geglu_launches(const MfmaLaunch &l, int num_cus);
 hipError_t launch_prefill_fast_geglu(const MfmaLaunch &l, const float *x, uint8_t *scratch, const uint16_t *gelu_lut,
-                                     float *out, int num_cus, hipStream_t s);
+                                     float *out, int num_cus, hipStream_t s, bool tiles_ready = false);
 size_t prefill_fast_lds_bytes();
-hipError_t launch_prefill_fast(const MfmaLaunch &l, const float *x, uint8_t *scratch, int num_cus, hipStream_t s);
+hipError_t launch_prefill_fast(const MfmaLaunch &l, const float *x, uint8_t *scratch, int num_cus, hipStream_t s,
+                               bool tiles_ready = false);
 
 // The gelu table (65536 f16 entries, hp_gelu.h gelu_lut) for the constant c.
 hipError_t launch_gelu_lut(double c, uint16_t *lut, hipStream_t s);
@@ -426,6 +429,10 @@ struct NormArgs {
   const float *y, *w_post, *x_res, *w_next;
   float *x_out, *next_out;
   uint8_t *q8img;  // non-null: next_out also as a matvec input image (q8_image_bytes(rows, n / 256))
+  // non-null: next_out also as the fast prefill kernel's activation tiles
+  // (hp_f2tile.h; row r is column r; the grid covers whole 64-column tiles,
+  // workgroups past `rows` write their padding columns as zeros)
+  uint8_t *xt;
   float scale;
   int n, rows;
   double eps;

@@ -25,6 +25,7 @@
 // registers; A fragments (one dword per lane and class) and B fragments
 // (8 bytes per lane) are built from LDS.
 #include "hp_common.h"
+#include "hp_f2tile.h"
 #include "hp_gelu.h"
 #include "hp_mfma.h"
 #include "hp_q8k.h"
@@ -369,8 +370,6 @@ __global__ __launch_bounds__(256) void kquant_prefill_kernel(const PfArgs a) {
 // weights the second, so lane (n, q)'s accumulator holds weight row n of the
 // segment and columns 4q .. 4q + 3 of the column set: the row's d and dmin
 // come with the lane's own header load.
-constexpr int kF2Cols = 64;
-constexpr int kF2XTile = 32768 + 2048 + 256;  // 35,072 bytes per (column tile, block)
 constexpr int kF3Waves = 8;                                          // per workgroup
 constexpr int kF3PerCU = 8 / kF3Waves;                               // workgroups per CU: two waves per SIMD
 constexpr int kF3RS = 2;                                             // 16-row segments per wave
@@ -391,40 +390,13 @@ __global__ __launch_bounds__(256) void q8k_prefill_tiles16_kernel(const float *_
   const int m = blockIdx.y * 16 + (threadIdx.x >> 4);
   const int ct = m / kF2Cols, n = m % kF2Cols;
   uint8_t *tile = xt + ((size_t)ct * nb + b) * kF2XTile;
-  _Float16 *xh = reinterpret_cast<_Float16 *>(tile);
-  _Float16 *xb = reinterpret_cast<_Float16 *>(tile + 32768);
-  float *xd = reinterpret_cast<float *>(tile + 32768 + 2048);
   float v[16];
   load_x16(v, x + (size_t)min(m, cols - 1) * k + (size_t)b * kQK, i16);
   if (m >= cols) {
 #pragma unroll
     for (int e = 0; e < 16; e++) v[e] = 0.0f;
   }
-  bool nz;
-  const float inv = q8k_inv16(v, i16, nz);
-  int q[16];
-#pragma unroll
-  for (int e = 0; e < 16; e++) q[e] = nz ? q8k_round(inv, v[e]) : 0;
-  const int j = i16 >> 1, u = i16 & 1, qq = j >> 1;
-#pragma unroll
-  for (int i = 0; i < 4; i++) {
-    const int l = 4 * u + i;
-    const half2v lo = (half2v){(_Float16)q[i], (_Float16)q[4 + i]};
-    const half2v hi = (half2v){(_Float16)q[8 + i], (_Float16)q[12 + i]};
-    *reinterpret_cast<uint2 *>(xh + ((l * 4 + qq) * kF2Cols + n) * 8 + 4 * (j & 1)) =
-        make_uint2(__builtin_bit_cast(uint32_t, lo), __builtin_bit_cast(uint32_t, hi));
-  }
-  int s0 = 0, s1 = 0;
-#pragma unroll
-  for (int i = 0; i < 8; i++) {
-    s0 += q[i];
-    s1 += q[8 + i];
-  }
-  s0 += (int)dpp_u32<kDppXor1>((uint32_t)s0);
-  s1 += (int)dpp_u32<kDppXor1>((uint32_t)s1);
-  const int h = 2 * j + u;  // lane u writes group 2j + u
-  xb[((h >> 3) * kF2Cols + n) * 8 + (h & 7)] = (_Float16)(u ? s1 : s0);
-  if (i16 == 0) xd[n] = nz ? __fdiv_rn(1.0f, inv) : 0.0f;
+  f2_tile_store16(v, i16, tile, n);
 }
 
 struct F2Args {
@@ -1000,15 +972,18 @@ size_t prefill_fast_geglu_bytes(const MfmaLaunch &l, int num_cus) {
 }
 
 hipError_t launch_prefill_fast_geglu(const MfmaLaunch &l, const float *x, uint8_t *scratch, const uint16_t *gelu_lut,
-                                     float *out, int num_cus, hipStream_t s) {
+                                     float *out, int num_cus, hipStream_t s, bool tiles_ready) {
   if (l.count != 2 || l.cols < 1 || l.k % kQK != 0 || l.type[0] != l.type[1] || l.rows[0] != l.rows[1])
     return hipErrorInvalidValue;
   const F2Pair p = f2_pair(l, num_cus);
   const int nb = p.nb, col_tiles = p.col_tiles;
-  hipLaunchKernelGGL(q8k_prefill_tiles16_kernel, dim3(nb, col_tiles * kF2Cols / 16), dim3(256), 0, s, x, l.k, nb,
-                     l.cols, scratch);
-  hipError_t e = hipGetLastError();
-  if (e != hipSuccess) return e;
+  hipError_t e;
+  if (!tiles_ready) {
+    hipLaunchKernelGGL(q8k_prefill_tiles16_kernel, dim3(nb, col_tiles * kF2Cols / 16), dim3(256), 0, s, x, l.k, nb,
+                       l.cols, scratch);
+    e = hipGetLastError();
+    if (e != hipSuccess) return e;
+  }
   F2Args a{};
   a.count = 2;
   for (int i = 0; i < 2; i++) {
@@ -1048,14 +1023,18 @@ size_t prefill_fast_bytes(const MfmaLaunch &l, int num_cus) {
 
 size_t prefill_fast_lds_bytes() { return 2 * (size_t)kF2XTile; }  // the two static stages
 
-hipError_t launch_prefill_fast(const MfmaLaunch &l, const float *x, uint8_t *scratch, int num_cus, hipStream_t s) {
+hipError_t launch_prefill_fast(const MfmaLaunch &l, const float *x, uint8_t *scratch, int num_cus, hipStream_t s,
+                               bool tiles_ready) {
   if (l.count < 1 || l.count > kMaxWeights || l.cols < 1 || l.k % kQK != 0) return hipErrorInvalidValue;
   const F2Shape sh = f2_shape(l, num_cus);
   const int nb = sh.nb, col_tiles = sh.col_tiles;
-  hipLaunchKernelGGL(q8k_prefill_tiles16_kernel, dim3(nb, col_tiles * kF2Cols / 16), dim3(256), 0, s, x, l.k, nb,
-                     l.cols, scratch);
-  hipError_t e = hipGetLastError();
-  if (e != hipSuccess) return e;
+  hipError_t e;
+  if (!tiles_ready) {
+    hipLaunchKernelGGL(q8k_prefill_tiles16_kernel, dim3(nb, col_tiles * kF2Cols / 16), dim3(256), 0, s, x, l.k, nb,
+                       l.cols, scratch);
+    e = hipGetLastError();
+    if (e != hipSuccess) return e;
+  }
   F2Args a{};
   a.count = l.count;
   int rt = 0;

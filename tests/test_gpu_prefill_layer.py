@@ -179,12 +179,13 @@ def _oracle_layer(D, shape, data):
                    epsilon=shape.epsilon, output_scale=float(data["output_scale"]))
 
 
-@pytest.mark.parametrize("tokens,kernel", [(128, 4), (128, 0), (512, 0)],
-                         ids=["chunk128-exact", "chunk128-auto", "chunk512-auto"])
+@pytest.mark.parametrize("tokens,kernel", [(128, 4), (128, 0), (100, 0), (512, 0)],
+                         ids=["chunk128-exact", "chunk128-auto", "chunk100-auto", "chunk512-auto"])
 def test_prefill_layer_matches_oracle(hip, D, tokens, kernel):
     """One layer of the model over a chunk ending at position 4095 (kernel 4:
     the bit-exact prefill projections; 0: the automatic policy, the fast
-    prefill kernel from 64 tokens)."""
+    prefill kernel from 64 tokens, whose activation tiles the norm kernel
+    writes; 100 tokens leave 28 padding columns in the last tile)."""
     import torch
 
     hip.setMatvecKernel(kernel)
