@@ -413,7 +413,7 @@ bool use_wide_pair(Handle *const *hs, size_t cols) {
 // launch, lib.rs:300-426); each launch quantises its columns in its prologue.
 int32_t run_norm(const float *y, int rows, int n, const float *w_post, const float *x_res, float scale, float *x_out,
                  const float *w_next, float *next_out, double eps, hipStream_t stream, uint8_t *q8img = nullptr,
-                 uint8_t *xt = nullptr);
+                 uint8_t *xt = nullptr, const PrefillParts *y_parts = nullptr);
 
 // Whether a one-column launch over these weights runs a vector-ALU kernel,
 // which can form its input with the norm prologue.
@@ -444,7 +444,9 @@ bool image_input_ok(size_t count, Handle *const *hs, size_t cols) {
 // here writes that image for the launch.
 int32_t run_matvec(size_t count, Handle *const *hs, const float *d_input, size_t input_size, size_t cols,
                    float *const *d_outs, hipStream_t stream, const NormIn *norm = nullptr,
-                   float *norm_scratch = nullptr, uint8_t *img_scratch = nullptr, const uint8_t *q8img_in = nullptr) {
+                   float *norm_scratch = nullptr, uint8_t *img_scratch = nullptr, const uint8_t *q8img_in = nullptr,
+                   const PrefillParts *norm_parts = nullptr, PrefillParts *defer = nullptr) {
+  if (defer) defer->ks = 1;
   State &s = st();
   if (cols == 0) return HP_OK;
   const bool image_ok = s.images && cols >= 2 && image_input_ok(count, hs, cols);
@@ -472,12 +474,13 @@ int32_t run_matvec(size_t count, Handle *const *hs, const float *d_input, size_t
     pre = static_cast<uint8_t *>(p);
   }
   bool tiles_ready = false;  // the norm kernel wrote the fast prefill's tiles
-  if (norm && (wide ? !wide_norm : !norm_prologue_ok(count, hs, cols))) {
+  const bool y_split = norm_parts && norm_parts->ks > 1;  // the norm's y as partial sums
+  if (norm && (y_split || (wide ? !wide_norm : !norm_prologue_ok(count, hs, cols)))) {
     uint8_t *img = image_ok && img_scratch ? img_scratch : nullptr;
     tiles_ready = kind == 2 && input_size % kQK == 0;
     int32_t rc = run_norm(norm->y, (int)cols, (int)input_size, norm->w_post, norm->mode == 2 ? norm->x_res : nullptr,
                           norm->scale, norm->x_out, norm->w_next, norm_scratch, norm->eps, stream, img,
-                          tiles_ready ? pre : nullptr);
+                          tiles_ready ? pre : nullptr, norm_parts);
     if (rc != HP_OK) return rc;
     d_input = norm_scratch;
     norm = nullptr;
@@ -513,7 +516,15 @@ int32_t run_matvec(size_t count, Handle *const *hs, const float *d_input, size_t
   if (kind) {
     hipEvent_t e1 = prof_begin(stream);
     if (kind == 2) {
-      HP_HIP_TRY(launch_prefill_fast(l, d_input, pre, s.num_cus, stream, tiles_ready));
+      const size_t part_bytes = defer ? prefill_fast_part_bytes(l, s.num_cus) : 0;
+      if (part_bytes) {
+        void *p = nullptr;
+        int32_t rc = stream_scratch(stream, kScratchParts, part_bytes, &p);
+        if (rc != HP_OK) return rc;
+        defer->part = static_cast<float *>(p);
+      }
+      HP_HIP_TRY(launch_prefill_fast(l, d_input, pre, s.num_cus, stream, tiles_ready, part_bytes ? defer : nullptr));
+      if (part_bytes) s.launches--;  // no reduction launch
     } else {
       HP_HIP_TRY(launch_q8k_prefill(d_input, (int)input_size, (int)cols, pre, stream));
       HP_HIP_TRY(launch_prefill(l, pre, s.num_cus, stream));
@@ -597,7 +608,7 @@ int32_t run_matvec(size_t count, Handle *const *hs, const float *d_input, size_t
 int32_t run_matvec_geglu(Handle *hg, Handle *hu, const float *d_input, size_t input_size, size_t cols,
                          float *d_out, hipStream_t stream, const NormIn *norm = nullptr,
                          float *norm_scratch = nullptr, uint8_t *q8img_out = nullptr,
-                         bool *q8img_written = nullptr) {
+                         bool *q8img_written = nullptr, const PrefillParts *norm_parts = nullptr) {
   if (q8img_written) *q8img_written = false;
   State &s = st();
   if (cols == 0) return HP_OK;
@@ -628,11 +639,12 @@ int32_t run_matvec_geglu(Handle *hg, Handle *hu, const float *d_input, size_t in
     pre = static_cast<uint8_t *>(p);
   }
   bool tiles_ready = false;  // the norm kernel wrote the fast prefill's tiles
-  if (norm && !((fused || wide) && cols == 1 && g.nb <= 16)) {
+  const bool y_split = norm_parts && norm_parts->ks > 1;  // the norm's y as partial sums
+  if (norm && (y_split || !((fused || wide) && cols == 1 && g.nb <= 16))) {
     tiles_ready = fast && input_size % kQK == 0;
     int32_t rc = run_norm(norm->y, (int)cols, (int)input_size, norm->w_post, norm->mode == 2 ? norm->x_res : nullptr,
                           norm->scale, norm->x_out, norm->w_next, norm_scratch, norm->eps, stream, nullptr,
-                          tiles_ready ? pre : nullptr);
+                          tiles_ready ? pre : nullptr, norm_parts);
     if (rc != HP_OK) return rc;
     d_input = norm_scratch;
     norm = nullptr;
@@ -1041,10 +1053,15 @@ int32_t run_attention(AttnArgs a, float *partials, hipStream_t stream) {
 
 int32_t run_norm(const float *y, int rows, int n, const float *w_post, const float *x_res, float scale, float *x_out,
                  const float *w_next, float *next_out, double eps, hipStream_t stream, uint8_t *q8img,
-                 uint8_t *xt) {
+                 uint8_t *xt, const PrefillParts *y_parts) {
   NormArgs a{};
   a.q8img = q8img;
   a.xt = xt;
+  if (y_parts && y_parts->ks > 1) {
+    // y is the projection's block-range partial sums
+    a.y_ks = y_parts->ks;
+    a.y_stride = y_parts->stride;
+  }
   a.y = y;
   a.w_post = w_post;
   a.x_res = x_res;
@@ -1972,6 +1989,9 @@ int32_t hp_hip_decode_layers_device(const hp_hip_decode_layer_t *layers, size_t 
     // launch ffn_norm(residual after attention).  With several tokens, or a
     // forced matrix-core kernel, they run as norm launches into xn.
     NormIn nin{};
+    // a fast prefill O or down launch leaves its block-range sums (ks > 1)
+    // in a scratch buffer for the norm launch after it to add
+    PrefillParts op{}, dp{};
     nin.mode = 1;
     nin.y = hid;
     nin.w_next = layers[0].d_attn_norm;
@@ -1983,7 +2003,7 @@ int32_t hp_hip_decode_layers_device(const hp_hip_decode_layer_t *layers, size_t 
       const double eps = L.attention.epsilon;
       Handle *qkv[3] = {H.q, H.k, H.v};
       float *qkv_out[3] = {q, k, v};
-      rc = run_matvec(H.v ? 3 : 2, qkv, nullptr, hidden, Mc, qkv_out, strm, &nin, xn, imgx);
+      rc = run_matvec(H.v ? 3 : 2, qkv, nullptr, hidden, Mc, qkv_out, strm, &nin, xn, imgx, nullptr, &dp);
       if (rc != HP_OK) return rc;
       // the RoPE angles depend on the positions and the RoPE parameters only:
       // a layer whose parameters match the previous layer's reads its table
@@ -2046,11 +2066,14 @@ int32_t hp_hip_decode_layers_device(const hp_hip_decode_layer_t *layers, size_t 
       if (rc != HP_OK) return rc;
       Handle *oh[1] = {H.o};
       float *oo[1] = {o};
-      rc = run_matvec(1, oh, att, H.o->input_size, Mc, oo, strm);
+      const bool defer = H.o->row_count == hidden;
+      rc = run_matvec(1, oh, att, H.o->input_size, Mc, oo, strm, nullptr, nullptr, nullptr, nullptr, nullptr,
+                      defer ? &op : nullptr);
       if (rc != HP_OK) return rc;
+      if (!defer) op.ks = 1;
       NormIn fin{};
       fin.mode = 2;
-      fin.y = o;
+      fin.y = op.ks > 1 ? op.part : o;
       fin.w_post = L.d_post_attention_norm;
       fin.x_res = hid;
       fin.scale = 1.0f;
@@ -2058,14 +2081,16 @@ int32_t hp_hip_decode_layers_device(const hp_hip_decode_layer_t *layers, size_t 
       fin.w_next = L.d_ffn_norm;
       fin.eps = eps;
       bool h_img = false;
-      rc = run_matvec_geglu(H.gate, H.up, nullptr, hidden, Mc, h, strm, &fin, xn, imgh, &h_img);
+      rc = run_matvec_geglu(H.gate, H.up, nullptr, hidden, Mc, h, strm, &fin, xn, imgh, &h_img, &op);
       if (rc != HP_OK) return rc;
       Handle *dh[1] = {H.down};
       float *yo[1] = {y};
-      rc = run_matvec(1, dh, h, H.down->input_size, Mc, yo, strm, nullptr, nullptr, nullptr, h_img ? imgh : nullptr);
+      rc = run_matvec(1, dh, h, H.down->input_size, Mc, yo, strm, nullptr, nullptr, nullptr, h_img ? imgh : nullptr,
+                      nullptr, H.down->row_count == hidden ? &dp : nullptr);
       if (rc != HP_OK) return rc;
+      if (H.down->row_count != hidden) dp.ks = 1;
       nin.mode = 2;
-      nin.y = y;
+      nin.y = dp.ks > 1 ? dp.part : y;
       nin.w_post = L.d_post_ffw_norm;
       nin.x_res = x1;
       nin.scale = L.layer_output_scale;
@@ -2074,8 +2099,8 @@ int32_t hp_hip_decode_layers_device(const hp_hip_decode_layer_t *layers, size_t 
       nin.eps = eps;
     }
     // the last layer's post-FFN residual, then output_norm
-    rc = run_norm(y, (int)Mc, (int)hidden, nin.w_post, x1, nin.scale, hid, d_output_norm,
-                  d_output_norm ? d_output + c0 * hidden : nullptr, nin.eps, strm);
+    rc = run_norm(nin.y, (int)Mc, (int)hidden, nin.w_post, x1, nin.scale, hid, d_output_norm,
+                  d_output_norm ? d_output + c0 * hidden : nullptr, nin.eps, strm, nullptr, nullptr, &dp);
     if (rc != HP_OK) return rc;
   }
   return HP_OK;

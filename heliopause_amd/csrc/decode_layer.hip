@@ -100,6 +100,23 @@ __global__ __launch_bounds__(256) void norm_residual_kernel(const NormArgs a) {
     wp[j] = pwp[ic];
     wn[j] = pwn[ic];
   }
+  if (a.y_ks > 1) {
+    // y as block-range partial sums: every range's loads first, then the
+    // sums in range order
+    float pv[kNormParts - 1][kNormPer];
+#pragma unroll
+    for (int r = 1; r < kNormParts; r++)
+#pragma unroll
+      for (int j = 0; j < kNormPer; j++) {
+        const int ic = min(tid + 256 * j, a.n - 1);
+        pv[r - 1][j] = r < a.y_ks ? py[r * a.y_stride + ic] : 0.0f;
+      }
+#pragma unroll
+    for (int r = 1; r < kNormParts; r++)
+#pragma unroll
+      for (int j = 0; j < kNormPer; j++)
+        if (r < a.y_ks) v[j] += pv[r - 1][j];
+  }
 #pragma unroll
   for (int j = 0; j < kNormPer; j++) {
     const bool in = tid + 256 * j < a.n;
@@ -648,6 +665,7 @@ __global__ __launch_bounds__(256) void attn_reduce_kernel(const AttnArgs a) {
 hipError_t launch_norm_residual(const NormArgs &a, hipStream_t s) {
   if (a.n < 1 || a.n > 256 * kNormPer || a.rows < 1) return hipErrorInvalidValue;
   if ((a.q8img || a.xt) && (a.n % kQK != 0 || !a.next_out)) return hipErrorInvalidValue;
+  if (a.y_ks > kNormParts || (a.y_ks > 1 && a.y_stride < (size_t)a.rows * a.n)) return hipErrorInvalidValue;
   const int grid = a.xt ? (a.rows + kF2Cols - 1) / kF2Cols * kF2Cols : a.rows;
   hipLaunchKernelGGL(norm_residual_kernel, dim3(grid), dim3(256), 0, s, a);
   return hipGetLastError();

@@ -400,8 +400,21 @@ int prefill_fast_geglu_launches(const MfmaLaunch &l, int num_cus);
 hipError_t launch_prefill_fast_geglu(const MfmaLaunch &l, const float *x, uint8_t *scratch, const uint16_t *gelu_lut,
                                      float *out, int num_cus, hipStream_t s, bool tiles_ready = false);
 size_t prefill_fast_lds_bytes();
+// A fast prefill launch of one weight may leave its block-range partial sums
+// for the consumer to add (a norm launch, NormArgs::y_ks): the caller sets
+// part to a buffer of prefill_fast_part_bytes(l, num_cus) and passes it to
+// launch_prefill_fast, which then launches no reduction and sets ks (> 1:
+// range r of output element e at part[r * stride + e]; 1: the output was
+// written as usual).
+constexpr int kNormParts = 4;
+struct PrefillParts {
+  float *part;
+  size_t stride;
+  int ks;
+};
+size_t prefill_fast_part_bytes(const MfmaLaunch &l, int num_cus);
 hipError_t launch_prefill_fast(const MfmaLaunch &l, const float *x, uint8_t *scratch, int num_cus, hipStream_t s,
-                               bool tiles_ready = false);
+                               bool tiles_ready = false, PrefillParts *defer = nullptr);
 
 // The gelu table (65536 f16 entries, hp_gelu.h gelu_lut) for the constant c.
 hipError_t launch_gelu_lut(double c, uint16_t *lut, hipStream_t s);
@@ -433,6 +446,11 @@ struct NormArgs {
   // (hp_f2tile.h; row r is column r; the grid covers whole 64-column tiles,
   // workgroups past `rows` write their padding columns as zeros)
   uint8_t *xt;
+  // y_ks > 1: y holds y_ks block-range partial sums of the projection, range
+  // r of element e at y[r * y_stride + e], added in range order (as
+  // f2_reduce_kernel adds them); at most kNormParts
+  int y_ks;
+  size_t y_stride;
   float scale;
   int n, rows;
   double eps;

@@ -36,7 +36,8 @@ enum ScratchKind {
   kScratchTopk = 2,     // top-k selection state (zeroed when allocated)
   kScratchPrefill = 3,  // Q8_K / f16 images of a prefill launch
   kScratchGeglu = 4,    // gate and up sums ahead of a GeGLU launch
-  kScratchKinds = 5
+  kScratchParts = 5,    // block-range sums of a prefill launch that a norm launch adds
+  kScratchKinds = 6
 };
 
 enum ScratchStatus { kScratchOk = 0, kScratchCapturing = 1, kScratchNoMemory = 2, kScratchZeroFailed = 3 };

@@ -1023,8 +1023,13 @@ size_t prefill_fast_bytes(const MfmaLaunch &l, int num_cus) {
 
 size_t prefill_fast_lds_bytes() { return 2 * (size_t)kF2XTile; }  // the two static stages
 
+size_t prefill_fast_part_bytes(const MfmaLaunch &l, int num_cus) {
+  const F2Shape sh = f2_shape(l, num_cus);
+  return l.count == 1 && sh.ks > 1 && sh.ks <= kNormParts ? (size_t)sh.ks * sh.stride * sizeof(float) : 0;
+}
+
 hipError_t launch_prefill_fast(const MfmaLaunch &l, const float *x, uint8_t *scratch, int num_cus, hipStream_t s,
-                               bool tiles_ready) {
+                               bool tiles_ready, PrefillParts *defer) {
   if (l.count < 1 || l.count > kMaxWeights || l.cols < 1 || l.k % kQK != 0) return hipErrorInvalidValue;
   const F2Shape sh = f2_shape(l, num_cus);
   const int nb = sh.nb, col_tiles = sh.col_tiles;
@@ -1058,10 +1063,16 @@ hipError_t launch_prefill_fast(const MfmaLaunch &l, const float *x, uint8_t *scr
   a.ksplit = sh.ks;
   a.part = reinterpret_cast<float *>(scratch + (size_t)col_tiles * nb * kF2XTile);
   a.part_stride = sh.stride;
+  const bool deferred = defer && prefill_fast_part_bytes(l, num_cus) > 0;
+  if (defer) {
+    defer->ks = deferred ? sh.ks : 1;
+    defer->stride = sh.stride;
+    if (deferred) a.part = defer->part;
+  }
   const long long items = (long long)a.total_rt * a.col_tiles * a.ksplit;
   const int grid = (int)(items < kF3PerCU * num_cus ? items : kF3PerCU * num_cus);
   hipLaunchKernelGGL(kquant_prefill_fast_kernel<false>, dim3(grid), dim3(kF3Threads), 0, s, a);
-  if (a.ksplit == 1) return hipGetLastError();
+  if (a.ksplit == 1 || deferred) return hipGetLastError();
   e = hipGetLastError();
   if (e != hipSuccess) return e;
   const size_t threads = (sh.outs + 3) / 4;
