@@ -1991,7 +1991,7 @@ int32_t hp_hip_decode_layers_device(const hp_hip_decode_layer_t *layers, size_t 
     NormIn nin{};
     // a fast prefill O or down launch leaves its block-range sums (ks > 1)
     // in a scratch buffer for the norm launch after it to add
-    PrefillParts op{}, dp{};
+    PrefillParts qp{}, op{}, dp{};
     nin.mode = 1;
     nin.y = hid;
     nin.w_next = layers[0].d_attn_norm;
@@ -2003,7 +2003,9 @@ int32_t hp_hip_decode_layers_device(const hp_hip_decode_layer_t *layers, size_t 
       const double eps = L.attention.epsilon;
       Handle *qkv[3] = {H.q, H.k, H.v};
       float *qkv_out[3] = {q, k, v};
-      rc = run_matvec(H.v ? 3 : 2, qkv, nullptr, hidden, Mc, qkv_out, strm, &nin, xn, imgx, nullptr, &dp);
+      rc = run_matvec(H.v ? 3 : 2, qkv, nullptr, hidden, Mc, qkv_out, strm, &nin, xn, imgx, nullptr, &dp,
+                      Mc > 1 ? &qp : nullptr);
+      if (Mc == 1) qp.ks = 1;
       if (rc != HP_OK) return rc;
       // the RoPE angles depend on the positions and the RoPE parameters only:
       // a layer whose parameters match the previous layer's reads its table
@@ -2036,6 +2038,14 @@ int32_t hp_hip_decode_layers_device(const hp_hip_decode_layer_t *layers, size_t 
         pa.q = q;
         pa.k = k;
         pa.v = H.v ? v : k;
+        if (qp.ks > 1) {
+          // the Q/K/V launch left its block-range sums for this launch to add
+          pa.q = qp.part + qp.off[0];
+          pa.k = qp.part + qp.off[1];
+          pa.v = H.v ? qp.part + qp.off[2] : pa.k;
+          pa.src_ks = qp.ks;
+          pa.src_stride = qp.stride;
+        }
         pa.wq = L.d_attn_q_norm;
         pa.wk = L.d_attn_k_norm;
         pa.position = d_position;

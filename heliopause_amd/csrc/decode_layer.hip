@@ -202,6 +202,20 @@ __global__ __launch_bounds__(64) void qkv_post_kernel(const QkvPostArgs a) {
     x[j] = src[lane + 64 * j];
     wv[j] = pw[lane + 64 * j];
   }
+  if (a.src_ks > 1) {
+    // the projection as block-range partial sums: every range's loads, then
+    // the sums in range order
+    float pv[kNormParts - 1][4];
+#pragma unroll
+    for (int r = 1; r < kNormParts; r++)
+#pragma unroll
+      for (int j = 0; j < 4; j++) pv[r - 1][j] = r < a.src_ks ? src[r * a.src_stride + lane + 64 * j] : 0.0f;
+#pragma unroll
+    for (int r = 1; r < kNormParts; r++)
+#pragma unroll
+      for (int j = 0; j < 4; j++)
+        if (r < a.src_ks) x[j] += pv[r - 1][j];
+  }
   double2 tab[2] = {make_double2(1.0, 0.0), make_double2(1.0, 0.0)};
   if (a.rope_table_mode == 2 && kind != 2 && half > 0) {
 #pragma unroll
@@ -674,7 +688,7 @@ hipError_t launch_norm_residual(const NormArgs &a, hipStream_t s) {
 hipError_t launch_qkv_post(const QkvPostArgs &a, hipStream_t s) {
   if (a.nq < 1 || a.nkv < 1 || a.capacity < 1 || a.rope_dims < 0 || a.rope_dims > kHeadDim || (a.rope_dims & 1))
     return hipErrorInvalidValue;
-  if (a.tokens < 1 || a.tokens > kMaxChunkTokens) return hipErrorInvalidValue;
+  if (a.tokens < 1 || a.tokens > kMaxChunkTokens || a.src_ks > kNormParts) return hipErrorInvalidValue;
   hipLaunchKernelGGL(qkv_post_kernel, dim3(a.nq + 2 * a.nkv, a.tokens), dim3(64), 0, s, a);
   return hipGetLastError();
 }

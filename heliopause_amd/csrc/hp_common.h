@@ -400,16 +400,18 @@ int prefill_fast_geglu_launches(const MfmaLaunch &l, int num_cus);
 hipError_t launch_prefill_fast_geglu(const MfmaLaunch &l, const float *x, uint8_t *scratch, const uint16_t *gelu_lut,
                                      float *out, int num_cus, hipStream_t s, bool tiles_ready = false);
 size_t prefill_fast_lds_bytes();
-// A fast prefill launch of one weight may leave its block-range partial sums
-// for the consumer to add (a norm launch, NormArgs::y_ks): the caller sets
-// part to a buffer of prefill_fast_part_bytes(l, num_cus) and passes it to
-// launch_prefill_fast, which then launches no reduction and sets ks (> 1:
-// range r of output element e at part[r * stride + e]; 1: the output was
-// written as usual).
+// A fast prefill launch may leave its block-range partial sums for the
+// consumer to add (a norm launch, NormArgs::y_ks; the attention prologue,
+// QkvPostArgs::src_ks): the caller sets part to a buffer of
+// prefill_fast_part_bytes(l, num_cus) and passes it to launch_prefill_fast,
+// which then launches no reduction and sets ks (> 1: range r of element e of
+// weight w's [cols][rows] output at part[r * stride + off[w] + e]; 1: the
+// outputs were written as usual).
 constexpr int kNormParts = 4;
 struct PrefillParts {
   float *part;
   size_t stride;
+  size_t off[kMaxWeights];
   int ks;
 };
 size_t prefill_fast_part_bytes(const MfmaLaunch &l, int num_cus);
@@ -467,6 +469,10 @@ struct QkvPostArgs {
   int nq, nkv, capacity, rope_dims;
   int tokens;          // token t at position *position + pos_offset + t; rows [t][heads][kHeadDim]
   int pos_offset;
+  // src_ks > 1: q, k, v hold src_ks block-range partial sums, range r of
+  // element e at [r * src_stride + e], added in range order (at most kNormParts)
+  int src_ks;
+  size_t src_stride;
   double theta_scale;  // base^(-2 / rope_dims)
   double eps;
 };

@@ -1025,7 +1025,7 @@ size_t prefill_fast_lds_bytes() { return 2 * (size_t)kF2XTile; }  // the two sta
 
 size_t prefill_fast_part_bytes(const MfmaLaunch &l, int num_cus) {
   const F2Shape sh = f2_shape(l, num_cus);
-  return l.count == 1 && sh.ks > 1 && sh.ks <= kNormParts ? (size_t)sh.ks * sh.stride * sizeof(float) : 0;
+  return sh.ks > 1 && sh.ks <= kNormParts ? (size_t)sh.ks * sh.stride * sizeof(float) : 0;
 }
 
 hipError_t launch_prefill_fast(const MfmaLaunch &l, const float *x, uint8_t *scratch, int num_cus, hipStream_t s,
@@ -1067,6 +1067,7 @@ hipError_t launch_prefill_fast(const MfmaLaunch &l, const float *x, uint8_t *scr
   if (defer) {
     defer->ks = deferred ? sh.ks : 1;
     defer->stride = sh.stride;
+    for (int i = 0; i < l.count; i++) defer->off[i] = a.part_off[i];
     if (deferred) a.part = defer->part;
   }
   const long long items = (long long)a.total_rt * a.col_tiles * a.ksplit;
