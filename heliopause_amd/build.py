@@ -21,7 +21,8 @@ NAPI_SRC = PKG / "napi" / "hp_hip_napi.c"
 NAPI_ADDON = PKG / "napi" / "hp_hip.node"
 NODE_INCLUDE = Path(os.environ.get("NODE_INCLUDE", "/usr/include/node"))
 SOURCES = ["q8k.hip", "kquant_matvec.hip", "kquant_wide.hip", "kquant_mfma.hip", "kquant_prefill.hip", "repack.hip", "topk.hip",
-           "geglu.hip", "gguf.hip", "sample.hip", "decode_layer.hip", "attn_prefill.hip", "capi.hip"]
+           "geglu.hip", "gguf.hip", "sample.hip", "decode_layer.hip", "attn_prefill.hip", "decode_fused.hip",
+           "capi.hip"]
 
 HIPCC = os.environ.get("HIPCC", shutil.which("hipcc") or "/opt/rocm/bin/hipcc")
 ARCH = "gfx950"

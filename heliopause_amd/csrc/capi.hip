@@ -9,11 +9,15 @@
 #include "../../include/hp_gguf.h"
 #include "../../include/hp_hip.h"
 #include "hp_common.h"
+#include "hp_fused.h"
 #include "hp_scratch.h"
 
 #include <algorithm>
 #include <atomic>
+#include <climits>
+#include <cstring>
 #include <cmath>
+#include <map>
 #include <mutex>
 #include <string>
 #include <thread>
@@ -107,6 +111,16 @@ struct State {
   // by ensure_init (the allocation-free entry point's only scratch)
   uint8_t *static_scratch = nullptr;
   uint16_t *gelu_lut = nullptr;  // the GeGLU launches' gelu table (ensure_init)
+  // persistent decode step (decode_fused.hip): 1 runs it for one-token calls
+  // that it covers, 0 keeps the launch sequence; the bound of one of its
+  // waits in s_memrealtime ticks (100 MHz); device copies of its layer
+  // tables by content, kept until hp_hip_shutdown (a captured graph may
+  // still point at one)
+  int fused_mode = 0;  // the persistent one-token step is opt-in (hp_hip_set_decode_fused)
+  uint64_t fused_spin = 100000000ull;
+  uint64_t *fused_trace = nullptr;  // stage timeline buffer (hp_hip_set_fused_trace), or null
+  size_t fused_trace_len = 0;
+  std::map<std::vector<uint8_t>, void *> fused_tables;
 };
 
 State &st() {
@@ -1154,6 +1168,244 @@ int32_t topk_outputs(size_t rows, size_t k, uint32_t **ids, float **vals) {
   return HP_OK;
 }
 
+// ---- persistent decode step (decode_fused.hip) ------------------------
+
+// The weights hs[0 .. count) (one input size) of a stage, their rows split
+// over workgroups [wg0, wg0 + wgs): one segment per weight (gate/up: one,
+// both weights' rows), workgroup counts in proportion to weight bytes.
+// false: a workgroup's share would not fit the stage's per-thread task slots.
+bool fused_proj(FusedProj &P, Handle *const *hs, int count, bool pair, int wg0, int wgs) {
+  P = FusedProj{};
+  const TileGeom g = hs[0]->g;
+  P.count = count;
+  P.pair = pair ? 1 : 0;
+  P.nb = g.nb;
+  P.S = g.S;
+  P.R = g.R;
+  P.mg_nb = div_magic(g.nb);
+  P.mg_S = div_magic(g.S);
+  P.mg_R = div_magic(g.R);
+  int row = 0;
+  for (int i = 0; i < 3; i++) {
+    const Handle *h = hs[i < count ? i : 0];  // unused entries repeat weight 0 (offset 0)
+    P.w[i].data = h->data;
+    P.w[i].dplane = h->dplane;
+    P.w[i].type = h->type;
+    P.w[i].rows = (int)h->row_count;
+    P.w[i].row_begin = i < count ? (pair ? 0 : row) : INT_MAX;
+    if (i < count && !pair) row += (int)h->row_count;
+  }
+  P.out_rows = pair ? (int)hs[0]->row_count : row;
+  auto slots_ok = [&](int type, int rpw) {
+    const int tasks = (pair ? 2 : 1) * rpw * g.nb;
+    return (tasks + kFusedThreads - 1) / kFusedThreads <= (type == kTypeQ4K ? kFusedSlotsQ4 : kFusedSlotsQ6);
+  };
+  if (pair) {
+    const int rows = (int)hs[0]->row_count;
+    const int rpw = (rows + wgs - 1) / wgs;
+    P.nseg = 1;
+    P.seg[0] = {0, rows, wg0, (rows + rpw - 1) / rpw, rpw, hs[0]->type};
+    return slots_ok(hs[0]->type, rpw);
+  }
+  double total = 0;
+  double bytes[3] = {0, 0, 0};
+  for (int i = 0; i < count; i++) {
+    bytes[i] = (double)hs[i]->row_count * (double)row_bytes_for(hs[i]->type, hs[i]->input_size);
+    total += bytes[i];
+  }
+  int n[3] = {0, 0, 0}, sum = 0;
+  for (int i = 0; i < count; i++) {
+    n[i] = std::max(1, (int)((double)wgs * bytes[i] / total));
+    sum += n[i];
+  }
+  while (sum > wgs) {  // trim the largest share
+    int j = 0;
+    for (int i = 1; i < count; i++)
+      if (n[i] > n[j]) j = i;
+    if (n[j] <= 1) return false;
+    n[j]--;
+    sum--;
+  }
+  P.nseg = count;
+  int wg = wg0, rb = 0;
+  for (int i = 0; i < count; i++) {
+    const int rows = (int)hs[i]->row_count;
+    const int rpw = (rows + n[i] - 1) / n[i];
+    const int cnt = (rows + rpw - 1) / rpw;
+    P.seg[i] = {rb, rows, wg, cnt, rpw, hs[i]->type};
+    if (!slots_ok(hs[i]->type, rpw)) return false;
+    wg += cnt;
+    rb += rows;
+  }
+  return wg <= wg0 + wgs;
+}
+
+// The persistent step's layer table, exchange layout, LDS and kernel choice
+// for these layers, or false when some layer is outside what it covers (the
+// caller then runs the launch sequence).
+struct FusedPlan {
+  std::vector<FusedLayer> layers;
+  FusedXchg x{};
+  size_t lds = 0;
+  int G = 0;
+};
+
+bool fused_plan(const hp_hip_decode_layer_t *layers, const std::vector<LayerHandles> &hs, size_t hidden,
+                FusedPlan *out) {
+  State &s = st();
+  const int W = s.num_cus;
+  if (W < 8 || hidden % kQK != 0 || hidden > 16 * (size_t)kQK || hs.size() > (size_t)kFusedMaxLayers) return false;
+  FusedPlan p;
+  p.layers.resize(hs.size());
+  size_t qkv_max = 0, att_max = 0, ffn_max = 0, slots_max = 0;
+  for (size_t i = 0; i < hs.size(); i++) {
+    const hp_hip_decode_layer_t &Ls = layers[i];
+    const LayerHandles &H = hs[i];
+    const hp_hip_attention_config_t &c = Ls.attention;
+    const int G = c.head_count / c.head_count_kv;
+    if (i == 0) p.G = G;
+    if (G != p.G || !fused_group_supported(G)) return false;
+    if (c.rope_dims != 0 && c.rope_dims != 128 && c.rope_dims != kHeadDim) return false;  // RoPE pairs within a lane
+    const int chunks = (c.capacity + kAttnChunk - 1) / kAttnChunk;
+    if (chunks > 128 || c.head_count * 4 > 65535) return false;
+    if (H.gate->type != H.up->type) return false;
+    FusedLayer &D = p.layers[i];
+    D = FusedLayer{};
+    Handle *qkv[3] = {H.q, H.k, H.v};
+    if (!fused_proj(D.qkv, qkv, H.v ? 3 : 2, false, 0, W)) return false;
+    // O skips the workgroups that merge attention (they finish that stage last)
+    const int merge_wgs = c.head_count * 4;
+    const int o0 = W - merge_wgs >= W / 2 ? merge_wgs : 0;
+    Handle *o[1] = {H.o};
+    if (!fused_proj(D.o, o, 1, false, o0, W - o0)) return false;
+    Handle *gu[2] = {H.gate, H.up};
+    if (!fused_proj(D.gu, gu, 2, true, 0, W)) return false;
+    Handle *dn[1] = {H.down};
+    if (!fused_proj(D.down, dn, 1, false, 0, W)) return false;
+    D.attn_norm = Ls.d_attn_norm;
+    D.q_norm = Ls.d_attn_q_norm;
+    D.k_norm = Ls.d_attn_k_norm;
+    D.post_attn_norm = Ls.d_post_attention_norm;
+    D.ffn_norm = Ls.d_ffn_norm;
+    D.post_ffw_norm = Ls.d_post_ffw_norm;
+    const AttnArgs aa = attn_args(&c);
+    D.freq_factors = aa.freq_factors;
+    D.k_cache = reinterpret_cast<_Float16 *>(Ls.d_key_cache);
+    D.v_cache = reinterpret_cast<_Float16 *>(Ls.d_value_cache);
+    D.theta_scale = aa.theta_scale;
+    D.eps = aa.eps;
+    D.out_scale = Ls.layer_output_scale;
+    D.nq = c.head_count;
+    D.nkv = c.head_count_kv;
+    D.capacity = c.capacity;
+    D.window = c.sliding_window;
+    D.rope_dims = c.rope_dims;
+    D.chunks = chunks;
+    D.k_off = (int)H.q->row_count;
+    D.v_off = H.v ? (int)(H.q->row_count + H.k->row_count) : D.k_off;
+    // layers with the same RoPE parameters share a key (the first such layer's index)
+    D.rope_key = (int)i;
+    for (size_t j = 0; j < i; j++) {
+      const hp_hip_attention_config_t &cj = layers[j].attention;
+      if (cj.rope_dims == c.rope_dims && cj.rope_freq_base == c.rope_freq_base &&
+          cj.d_rope_freq_factors == c.d_rope_freq_factors) {
+        D.rope_key = (int)j;
+        break;
+      }
+    }
+    qkv_max = std::max(qkv_max, (size_t)D.qkv.out_rows);
+    att_max = std::max(att_max, (size_t)c.head_count * kHeadDim);
+    ffn_max = std::max(ffn_max, H.gate->row_count);
+    slots_max = std::max(slots_max, (size_t)c.head_count_kv * chunks * kAttnMaxGroup);
+  }
+  p.lds = fused_lds_bytes(p.layers.data(), (int)p.layers.size(), (int)hidden);
+  if (p.lds == 0 || p.lds + fused_static_lds(p.G) > s.max_lds) return false;
+  if (fused_blocks_per_cu(p.G, p.lds) < 1) return false;
+  // the exchange arena (8 bytes per value; o right after hid, y right after x1)
+  auto al = [](size_t b) { return (b + 255) & ~(size_t)255; };
+  size_t off = 0;
+  auto take = [&](size_t values) {
+    const size_t o = off;
+    off += al(values * 8);
+    return (uint32_t)o;
+  };
+  p.x.hid = take(hidden);
+  p.x.o = take(hidden);
+  p.x.x1 = take(hidden);
+  p.x.y = take(hidden);
+  p.x.qkv = take(qkv_max);
+  p.x.att = take(att_max);
+  p.x.h = take(ffn_max);
+  p.x.part_slots = (uint32_t)slots_max;
+  p.x.part = take(slots_max * (kHeadDim + 2));
+  p.x.total = (uint32_t)off;
+  if (p.x.o != p.x.hid + hidden * 8 || p.x.y != p.x.x1 + hidden * 8 || off >= (1u << 31)) return false;
+  *out = std::move(p);
+  return true;
+}
+
+// The device copy of a layer table (uploaded once per distinct content).
+int32_t fused_table(const std::vector<FusedLayer> &layers, hipStream_t stream, const FusedLayer **out) {
+  State &s = st();
+  constexpr size_t kDesc = 1024;
+  std::vector<uint8_t> bytes(layers.size() * kDesc, 0);
+  for (size_t i = 0; i < layers.size(); i++) std::memcpy(bytes.data() + i * kDesc, &layers[i], sizeof(FusedLayer));
+  auto it = s.fused_tables.find(bytes);
+  if (it != s.fused_tables.end()) {
+    *out = static_cast<const FusedLayer *>(it->second);
+    return HP_OK;
+  }
+  hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+  if (hipStreamIsCapturing(stream, &cs) != hipSuccess) cs = hipStreamCaptureStatusNone;
+  if (cs != hipStreamCaptureStatusNone)
+    return fail(HP_ERR_ARG, "decode layers: a captured call must follow an uncaptured call with the same layers");
+  void *d = nullptr;
+  if (hipMalloc(&d, bytes.size()) != hipSuccess) return fail(HP_ERR_OOM, "device allocation failed");
+  if (hipMemcpyAsync(d, bytes.data(), bytes.size(), hipMemcpyHostToDevice, stream) != hipSuccess ||
+      hipStreamSynchronize(stream) != hipSuccess) {
+    (void)hipFree(d);
+    return fail(HP_ERR_HIP, "uploading the decode layer table failed");
+  }
+  s.fused_tables.emplace(std::move(bytes), d);
+  *out = static_cast<const FusedLayer *>(d);
+  return HP_OK;
+}
+
+// Enqueue the persistent step for one token through every layer.
+int32_t run_fused(const FusedPlan &p, size_t hidden, float *d_hidden, const int32_t *d_position,
+                  const float *d_output_norm, float *d_output, hipStream_t strm) {
+  State &s = st();
+  const FusedLayer *table = nullptr;
+  int32_t rc = fused_table(p.layers, strm, &table);
+  if (rc != HP_OK) return rc;
+  void *arena = nullptr;
+  rc = stream_scratch(strm, kScratchFused, sizeof(FusedCtl) + p.x.total, &arena, true);
+  if (rc != HP_OK) return rc;
+  FusedArgs a{};
+  a.layers = table;
+  a.n_layers = (int)p.layers.size();
+  a.hidden_n = (int)hidden;
+  a.hidden = d_hidden;
+  a.out_norm = d_output_norm;
+  a.out = d_output;
+  a.position = d_position;
+  a.ctl = static_cast<FusedCtl *>(arena);
+  a.xchg = static_cast<uint8_t *>(arena) + sizeof(FusedCtl);
+  a.xchg_bytes = p.x.total;
+  a.gelu_lut = s.gelu_lut;
+  a.spin_ticks = s.fused_spin;
+  a.x = p.x;
+  a.G = p.G;
+  a.lds_bytes = (int)p.lds;
+  const size_t stamps = (size_t)s.num_cus * p.layers.size() * 6 * 8;
+  a.trace = s.fused_trace && s.fused_trace_len >= stamps ? s.fused_trace : nullptr;
+  hipEvent_t e = prof_begin(strm);
+  HP_HIP_TRY(launch_decode_fused(a, s.num_cus, strm));
+  prof_end(HP_KERNEL_MATVEC, e, strm);
+  s.launches++;
+  return HP_OK;
+}
+
 }  // namespace
 
 extern "C" {
@@ -1220,6 +1472,8 @@ int32_t hp_hip_shutdown(void) {
   s.topk_out_cap = 0;
   (void)hipDeviceSynchronize();
   s.pool.release_all();
+  for (auto &kv : s.fused_tables) (void)hipFree(kv.second);
+  s.fused_tables.clear();
   prof_collect();
   for (hipEvent_t e : s.event_pool) (void)hipEventDestroy(e);
   s.event_pool.clear();
@@ -1930,6 +2184,13 @@ int32_t hp_hip_decode_layers_device(const hp_hip_decode_layer_t *layers, size_t 
     min_cap = std::min(min_cap, c.capacity);
   }
   if (hidden == 0 || hidden > kNormMaxN) return fail(HP_ERR_SHAPE, "hidden size must be 1..4096");
+  if (token_count == 1 && s.fused_mode != 0 && s.matvec_kernel == 0) {
+    // one token: the persistent step, when these layers are within what it covers
+    FusedPlan plan;
+    if (fused_plan(layers, hs, hidden, &plan))
+      return run_fused(plan, hidden, d_hidden, d_position, d_output_norm, d_output,
+                       stream ? static_cast<hipStream_t>(stream) : s.stream);
+  }
   // Chunks of tokens go through every layer in turn, each chunk spanning
   // fewer positions than the smallest KV ring holds, so a chunk's appends
   // never overwrite keys that its own tokens still attend to
@@ -2114,6 +2375,51 @@ int32_t hp_hip_decode_layers_device(const hp_hip_decode_layer_t *layers, size_t 
     if (rc != HP_OK) return rc;
   }
   return HP_OK;
+}
+
+int32_t hp_hip_set_decode_fused(int32_t mode) {
+  if (mode != 0 && mode != 1) return fail(HP_ERR_ARG, "mode must be 0 or 1");
+  State &s = st();
+  std::lock_guard<std::recursive_mutex> lock(s.mu);
+  s.fused_mode = mode;
+  return HP_OK;
+}
+
+int32_t hp_hip_set_fused_wait_limit(uint64_t ticks) {
+  State &s = st();
+  std::lock_guard<std::recursive_mutex> lock(s.mu);
+  s.fused_spin = ticks == 0 ? 100000000ull : ticks;
+  return HP_OK;
+}
+
+int32_t hp_hip_set_fused_trace(uint64_t *d_stamps, size_t len) {
+  State &s = st();
+  std::lock_guard<std::recursive_mutex> lock(s.mu);
+  s.fused_trace = d_stamps;
+  s.fused_trace_len = d_stamps ? len : 0;
+  return HP_OK;
+}
+
+int32_t hp_hip_decode_fused_status(void *stream) {
+  State &s = st();
+  std::lock_guard<std::recursive_mutex> lock(s.mu);
+  if (!s.ready) return HP_OK;
+  hipStream_t strm = stream ? static_cast<hipStream_t>(stream) : s.stream;
+  void *arena = nullptr;
+  // an existing arena only (a zero-byte request never allocates one anew)
+  hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+  if (hipStreamIsCapturing(strm, &cs) == hipSuccess && cs != hipStreamCaptureStatusNone)
+    return fail(HP_ERR_ARG, "hp_hip_decode_fused_status cannot run under graph capture");
+  if (s.pool.peek(static_cast<void *>(strm), kScratchFused, &arena) != kScratchOk || !arena) return HP_OK;
+  HP_HIP_TRY(hipStreamSynchronize(strm));
+  uint32_t status = 0;
+  FusedCtl *ctl = static_cast<FusedCtl *>(arena);
+  HP_HIP_TRY(hipMemcpy(&status, &ctl->status, sizeof(status), hipMemcpyDeviceToHost));
+  if (status == 0) return HP_OK;
+  const uint32_t zero = 0;
+  HP_HIP_TRY(hipMemcpy(&ctl->status, &zero, sizeof(zero), hipMemcpyHostToDevice));
+  return fail(HP_ERR_HIP, "persistent decode step: a stage waited past its time limit (status " +
+                              std::to_string(status) + "); outputs of the failed steps are invalid");
 }
 
 }  // extern "C"

@@ -37,7 +37,8 @@ enum ScratchKind {
   kScratchPrefill = 3,  // Q8_K / f16 images of a prefill launch
   kScratchGeglu = 4,    // gate and up sums ahead of a GeGLU launch
   kScratchParts = 5,    // block-range sums of a prefill launch that a norm launch adds
-  kScratchKinds = 6
+  kScratchFused = 6,    // exchange arena and control words of the persistent decode step (zeroed when allocated)
+  kScratchKinds = 7
 };
 
 enum ScratchStatus { kScratchOk = 0, kScratchCapturing = 1, kScratchNoMemory = 2, kScratchZeroFailed = 3 };
@@ -84,6 +85,14 @@ class ScratchPool {
     b.cap = want;
     stats_.live_bytes += want;
     *out = p;
+    return kScratchOk;
+  }
+
+  // The live buffer of (stream, kind) in *out, if there is one (never allocates).
+  int peek(void *stream, int kind, void **out) const {
+    auto it = sets_.find(stream);
+    if (it == sets_.end() || !it->second.buf[kind].p) return kScratchNoMemory;
+    *out = it->second.buf[kind].p;
     return kScratchOk;
   }
 

@@ -33,6 +33,7 @@
 #include "hp_kquant.h"
 #include "hp_q8k16.h"
 #include "hp_wave.h"
+#include "hp_wide.h"
 
 #include <type_traits>
 
@@ -51,40 +52,10 @@ constexpr int kWideMaxThreads = 512;
 // pass.  128 registers per wave.
 constexpr int kWideHalfThreads = 1024;
 
-// LDS carve-up of one workgroup (byte offsets).  The input: Q4_K reads the
-// Q8_K image (cols * nb blocks of kQ8BlockBytes), Q6_K two masked copies of
-// its quants (q8k_store16_split, 256 bytes per block each, at a stride of
-// kSplitStride bytes).  Lanes of a wave read the same 16 bytes of
-// consecutive blocks; a stride of 68 dwords (4 mod 32 banks) spreads eight
-// such lanes over all banks, where 256 bytes would put them in one.
-constexpr int kSplitStride = kQ8BlockBytes;
-
 // 16-byte pieces of an input image each thread loads ahead of the weights:
 // four columns of 40 blocks over 512 threads need six (three over 1024).
 template <bool HALF>
 constexpr int kImgRegs = HALF ? 3 : 6;
-
-struct WideLayout {
-  int nbp;        // products per (row, col, class) row: nb rounded up to 4, == 4 (mod 8)
-  size_t xhi;     // Q6_K: [cols][nb] upper-half copies (the lower ones at 0)
-  size_t xd;      // [cols * nb] f32 Q8_K scales (padded to 4 entries)
-  size_t prod;    // [rows][cols][NC][nbp] f32 products
-  size_t fin;     // [rows][cols][NC] f32 chain results
-  size_t total;
-};
-
-__host__ __device__ inline WideLayout wide_layout(int cols, int nb, int type, int rows) {
-  WideLayout L;
-  const int nc = type == kTypeQ4K ? 9 : 8;
-  const size_t nq = (size_t)cols * nb;
-  L.nbp = ((nb + 3) & ~3) | 4;
-  L.xhi = type == kTypeQ6K ? nq * kSplitStride : 0;
-  L.xd = type == kTypeQ6K ? 2 * nq * kSplitStride : nq * kQ8BlockBytes;
-  L.prod = L.xd + (size_t)((nq + 3) & ~3) * 4;
-  L.fin = L.prod + (size_t)rows * cols * nc * L.nbp * 4;
-  L.total = L.fin + (size_t)rows * cols * nc * 4;
-  return L;
-}
 
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 
@@ -159,55 +130,6 @@ __device__ __forceinline__ void wide_load(HalfRegs &rg, const WideTask &t, int h
 #pragma unroll
     for (int p = 0; p < 2; p++) rg.e[p] = t.ch[(size_t)(8 + 2 * p + h) * t.cs];
     rg.d6 = *t.d6;
-  }
-}
-
-// The norm prologue's finish (hp_kquant.h norm_finish: the same arithmetic
-// in the same order, so the same bits) where only the waves that hold one of
-// the input's blocks do the math: with eight waves and a 10-block input,
-// five would otherwise repeat it on zeros.  `active`: this wave holds a
-// group below nb (wave-uniform).  Of the first four waves an inactive one
-// contributes +0.0 to the two sums, as its zeroed lanes would.  Every thread
-// of the workgroup calls it (two barriers).
-template <int MODE>
-__device__ __forceinline__ void wide_norm_finish(const NormIn &n, NormRegs &nr, float (&xv)[16], int grp, int nb,
-                                                 int i16, int k, double *sh, bool active) {
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  double part = 0.0;
-  if (active) {
-    if (grp >= nb) {
-#pragma unroll
-      for (int i = 0; i < 16; i++) nr.y[i] = nr.r[i] = 0.0f;
-    }
-    double ss = 0.0;
-#pragma unroll
-    for (int i = 0; i < 16; i++) ss += (double)nr.y[i] * (double)nr.y[i];
-    part = wave_sum_f64(ss);
-  }
-  if (lane == 0 && wave < 4) sh[wave] = part;
-  __syncthreads();
-  double sc = 1.0 / sqrt(((sh[0] + sh[1]) + (sh[2] + sh[3])) / (double)k + n.eps);
-  if (MODE == 2) {
-    part = 0.0;
-    if (active) {
-      double ss = 0.0;
-#pragma unroll
-      for (int i = 0; i < 16; i++) {
-        const float t = (float)(((double)nr.y[i] * sc) * (double)nr.wp[i]);
-        const float x1 = (nr.r[i] + t) * n.scale;
-        nr.y[i] = x1;
-        ss += (double)x1 * (double)x1;
-      }
-      if (blockIdx.x == 0 && grp < nb) store_x16(n.x_out + (size_t)grp * kQK, nr.y, i16);
-      part = wave_sum_f64(ss);
-    }
-    if (lane == 0 && wave < 4) sh[4 + wave] = part;
-    __syncthreads();
-    sc = 1.0 / sqrt(((sh[4] + sh[5]) + (sh[6] + sh[7])) / (double)k + n.eps);
-  }
-  if (active) {
-#pragma unroll
-    for (int i = 0; i < 16; i++) xv[i] = (float)(((double)nr.y[i] * sc) * (double)nr.wn[i]);
   }
 }
 

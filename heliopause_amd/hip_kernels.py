@@ -141,8 +141,14 @@ def _declare_decode(L: ctypes.CDLL) -> None:
     L.hp_hip_attention_prep_device.argtypes = [cfg, _sz, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp]
     L.hp_hip_gqa_attention_device.argtypes = [cfg, _sz, vp, vp, vp, vp, vp, vp]
     L.hp_hip_decode_layers_device.argtypes = [ctypes.POINTER(HipDecodeLayer), _sz, _sz, vp, vp, vp, vp, vp]
+    L.hp_hip_set_decode_fused.argtypes = [i32]
+    L.hp_hip_set_fused_wait_limit.argtypes = [_u64]
+    L.hp_hip_decode_fused_status.argtypes = [vp]
+    L.hp_hip_set_fused_trace.argtypes = [vp, _sz]
+    L.hp_hip_set_fused_trace.restype = i32
     for name in ("hp_hip_rms_norm_device", "hp_hip_residual_norm_device", "hp_hip_attention_prep_device",
-                 "hp_hip_gqa_attention_device", "hp_hip_decode_layers_device"):
+                 "hp_hip_gqa_attention_device", "hp_hip_decode_layers_device", "hp_hip_set_decode_fused",
+                 "hp_hip_set_fused_wait_limit", "hp_hip_decode_fused_status"):
         getattr(L, name).restype = i32
 
 
@@ -475,6 +481,33 @@ def setMatvecKernel(which: int) -> None:
 def setInputImages(enable: bool) -> None:
     """Test switch: pre-quantised input images inside draft steps (default on)."""
     assertHipOk(lib().hp_hip_set_input_images(1 if enable else 0), "setInputImages")
+
+
+def setDecodeFused(enable: bool) -> None:
+    """One-token decode steps as the persistent launch where it applies, or
+    always as the launch sequence (the default, and the faster of the two).
+    No counterpart in the reference; both give identical bits."""
+    assertHipOk(lib().hp_hip_set_decode_fused(1 if enable else 0), "setDecodeFused")
+
+
+def setFusedWaitLimit(ticks: int) -> None:
+    """Bound of one stage wait of the persistent decode step, in 10 ns ticks
+    (0: the default, one second).  A test hook: a tiny bound makes a step
+    stop at its first wait and report it through decodeFusedStatus."""
+    assertHipOk(lib().hp_hip_set_fused_wait_limit(int(ticks)), "setFusedWaitLimit")
+
+
+def decodeFusedStatus(stream: int = 0) -> int:
+    """Waits for `stream` and returns the status of the persistent decode
+    steps queued on it (0, or HP_ERR_HIP when one stopped at a wait; the
+    status is cleared by reading it)."""
+    return int(lib().hp_hip_decode_fused_status(stream or None))
+
+
+def setFusedTrace(d_stamps: int, length: int) -> None:
+    """Stage timeline of the persistent decode step into a device buffer of
+    uint64 stamps (0 turns it off); layout in include/hp_hip.h."""
+    assertHipOk(lib().hp_hip_set_fused_trace(d_stamps or None, int(length)), "setFusedTrace")
 
 
 def profile(enable: bool) -> None:

@@ -392,6 +392,39 @@ int32_t hp_hip_decode_layers_device(const hp_hip_decode_layer_t *layers, size_t 
                                     float *d_hidden, const int32_t *d_position, const float *d_output_norm,
                                     float *d_output, void *stream);
 
+/* On request, the one-token step of hp_hip_decode_layers_device runs as one
+ * persistent launch (one workgroup per CU, every layer's stages inside it,
+ * values handed between stages as round-tagged words) when the layers are
+ * within what it covers: hidden size a multiple of 256 up to 4096, at most 511
+ * layers, RoPE over 0, 128 or 256 dims, caches of at most 4096 slots, gate
+ * and up of one type, and each stage's share of rows within the
+ * workgroup's task slots; otherwise, and at 2..65536 tokens, the launch
+ * sequence runs.  Both give identical bits.  No counterpart in the
+ * reference; these are a switch and test hooks for it:
+ *   hp_hip_set_decode_fused: 1 uses the persistent step where it applies,
+ *     0 (the default) always the launch sequence, which is the faster of
+ *     the two on gfx950;
+ *   hp_hip_set_fused_wait_limit: the bound of one stage wait in 10 ns ticks
+ *     (0: the default, one second).  A wait past it ends the launch early,
+ *     leaves invalid outputs and a status that the next call below reports;
+ *     every launch reached after that skips its work until the status is
+ *     read;
+ *   hp_hip_decode_fused_status: waits for `stream` (NULL = library stream)
+ *     and returns HP_ERR_HIP (clearing the status) when a persistent step
+ *     queued on it stopped at a wait, else HP_OK. */
+int32_t hp_hip_set_decode_fused(int32_t mode);
+int32_t hp_hip_set_fused_wait_limit(uint64_t ticks);
+int32_t hp_hip_decode_fused_status(void *stream);
+/* Stage timeline of later persistent steps (a profiling hook): with a
+ * device buffer of at least compute_units * layers * 48 uint64 entries,
+ * workgroup w stamps the 100 MHz s_memrealtime clock at eight points of
+ * stage s (0..5: Q/K/V, attention, merge, O, gate/up, down) of layer l at
+ * d_stamps[((w * layers + l) * 6 + s) * 8 + k]: k = 0 stage start, 1 loads
+ * issued, 2 input arrived, 3 prologue done, 4 weights in registers, 5
+ * products done, 6 chains done, 7 end (points a stage lacks stay 0).
+ * NULL turns it off; a shorter buffer is not written. */
+int32_t hp_hip_set_fused_trace(uint64_t *d_stamps, size_t len);
+
 #ifdef __cplusplus
 }
 #endif
