@@ -21,6 +21,7 @@
 
 #include <math.h>
 #include <pthread.h>
+#include <unistd.h>
 #include <stdlib.h>
 #include <string.h>
 
@@ -809,6 +810,122 @@ int32_t hpo_rope_neox(const float *input, size_t head_size, size_t head_count, s
  * port of FreeBSD msun e_exp.c: hpo_exp).  value_layout 1 =
  * "dim-head-token" ((index * kv_heads + kv_head) * capacity + token), else
  * token-major like the key. */
+/* One (token, query head) row of hpo_gqa_attention_f32.  Every score and
+ * every weighted sum is its own chain in the reference's order; the loops
+ * run four independent chains side by side (four keys, then four output
+ * dims), which changes no chain's order. */
+typedef struct {
+  const float *query, *key, *value, *mask;
+  size_t mask_len, head_size, query_head_count, key_value_head_count, token_count, key_value_token_count,
+      key_value_start, key_value_capacity, group;
+  float scale;
+  int32_t value_layout, quantize_query_f16;
+  float *output;
+  size_t row_begin, row_end;  /* rows t * query_head_count + qh */
+  int failed;
+} GqaJob;
+
+static void gqa_rows(GqaJob *J) {
+  const size_t hs = J->head_size, nkv = J->key_value_head_count, cap = J->key_value_capacity;
+  const size_t kvn = J->key_value_token_count;
+  float *scores = malloc((kvn ? kvn : 1) * sizeof(float));
+  float *qv = malloc((hs ? hs : 1) * sizeof(float));
+  size_t *phys = malloc((kvn ? kvn : 1) * sizeof(size_t));
+  if (!scores || !qv || !phys) {
+    free(scores);
+    free(qv);
+    free(phys);
+    J->failed = 1;
+    return;
+  }
+  for (size_t kt = 0; kt < kvn; kt++) phys[kt] = (J->key_value_start + kt) % cap;
+  for (size_t row = J->row_begin; row < J->row_end; row++) {
+    const size_t t = row / J->query_head_count, qh = row % J->query_head_count;
+    const size_t kvh = qh / J->group;
+    const size_t qo = row * hs;
+    for (size_t i = 0; i < hs; i++)
+      qv[i] = J->quantize_query_f16 ? hpo_f16_to_f32(hpo_f32_to_f16_rust(J->query[qo + i])) : J->query[qo + i];
+    float max_score = -INFINITY;
+    size_t kt = 0;
+    for (; kt + 4 <= kvn; kt += 4) {
+      const float *k0 = J->key + (phys[kt] * nkv + kvh) * hs, *k1 = J->key + (phys[kt + 1] * nkv + kvh) * hs;
+      const float *k2 = J->key + (phys[kt + 2] * nkv + kvh) * hs, *k3 = J->key + (phys[kt + 3] * nkv + kvh) * hs;
+      float d0 = 0.0f, d1 = 0.0f, d2 = 0.0f, d3 = 0.0f;
+      for (size_t i = 0; i < hs; i++) {
+        d0 = d0 + qv[i] * k0[i];
+        d1 = d1 + qv[i] * k1[i];
+        d2 = d2 + qv[i] * k2[i];
+        d3 = d3 + qv[i] * k3[i];
+      }
+      const float dd[4] = {d0, d1, d2, d3};
+      for (int u = 0; u < 4; u++) {
+        const float mv = J->mask_len == 0 ? 0.0f : J->mask[t * kvn + kt + u];
+        const float score = mv == -INFINITY ? -INFINITY : (dd[u] * J->scale) + mv;
+        scores[kt + u] = score;
+        if (score > max_score) max_score = score;
+      }
+    }
+    for (; kt < kvn; kt++) {
+      const float *kr = J->key + (phys[kt] * nkv + kvh) * hs;
+      float dot = 0.0f;
+      for (size_t i = 0; i < hs; i++) dot = dot + qv[i] * kr[i];
+      const float mv = J->mask_len == 0 ? 0.0f : J->mask[t * kvn + kt];
+      const float score = mv == -INFINITY ? -INFINITY : (dot * J->scale) + mv;
+      scores[kt] = score;
+      if (score > max_score) max_score = score;
+    }
+    float sum = 0.0f;
+    for (kt = 0; kt < kvn; kt++) {
+      const float sc = scores[kt];
+      const float p = sc == -INFINITY ? 0.0f : (float)hpo_exp((double)(sc - max_score));
+      scores[kt] = p;
+      sum += p;
+    }
+    /* the reference forms (p / sum) inside the sum; the same f32 quotient */
+    for (kt = 0; kt < kvn; kt++) scores[kt] = scores[kt] / sum;
+    size_t i = 0;
+    for (; i + 4 <= hs; i += 4) {
+      float w0 = 0.0f, w1 = 0.0f, w2 = 0.0f, w3 = 0.0f;
+      for (kt = 0; kt < kvn; kt++) {
+        const size_t ph = phys[kt];
+        const float pw = scores[kt];
+        if (J->value_layout == 1) {
+          w0 = w0 + pw * J->value[((i + 0) * nkv + kvh) * cap + ph];
+          w1 = w1 + pw * J->value[((i + 1) * nkv + kvh) * cap + ph];
+          w2 = w2 + pw * J->value[((i + 2) * nkv + kvh) * cap + ph];
+          w3 = w3 + pw * J->value[((i + 3) * nkv + kvh) * cap + ph];
+        } else {
+          const float *vr = J->value + (ph * nkv + kvh) * hs + i;
+          w0 = w0 + pw * vr[0];
+          w1 = w1 + pw * vr[1];
+          w2 = w2 + pw * vr[2];
+          w3 = w3 + pw * vr[3];
+        }
+      }
+      J->output[qo + i] = w0;
+      J->output[qo + i + 1] = w1;
+      J->output[qo + i + 2] = w2;
+      J->output[qo + i + 3] = w3;
+    }
+    for (; i < hs; i++) {
+      float weighted = 0.0f;
+      for (kt = 0; kt < kvn; kt++) {
+        const size_t vo = J->value_layout == 1 ? (i * nkv + kvh) * cap + phys[kt] : (phys[kt] * nkv + kvh) * hs + i;
+        weighted = weighted + scores[kt] * J->value[vo];
+      }
+      J->output[qo + i] = weighted;
+    }
+  }
+  free(scores);
+  free(qv);
+  free(phys);
+}
+
+static void *gqa_worker(void *arg) {
+  gqa_rows((GqaJob *)arg);
+  return NULL;
+}
+
 int32_t hpo_gqa_attention_f32(const float *query, size_t query_len, const float *key, size_t key_len,
                               const float *value, size_t value_len, const float *mask, size_t mask_len,
                               size_t head_size, size_t query_head_count, size_t key_value_head_count,
@@ -824,51 +941,42 @@ int32_t hpo_gqa_attention_f32(const float *query, size_t query_len, const float 
   if (key_value_head_count == 0 || key_value_capacity == 0 || key_value_token_count > key_value_capacity ||
       query_head_count % key_value_head_count != 0)
     return HPO_ERR_HEADS;
-  const size_t group = query_head_count / key_value_head_count;
-  float *scores = malloc((key_value_token_count ? key_value_token_count : 1) * sizeof(float));
-  float *qv = malloc((head_size ? head_size : 1) * sizeof(float));
-  if (!scores || !qv) {
-    free(scores);
-    free(qv);
+  const size_t rows = token_count * query_head_count;
+  /* rows are independent: spread them over up to 16 threads when the work
+   * is large enough to pay for them */
+  long hw = sysconf(_SC_NPROCESSORS_ONLN);
+  size_t threads = hw > 0 ? (size_t)hw : 1;
+  if (threads > 16) threads = 16;
+  const double work = (double)rows * (double)key_value_token_count * (double)head_size;
+  if (work < 4e6) threads = 1;
+  if (threads > rows) threads = rows ? rows : 1;
+  GqaJob base = {query, key, value, mask, mask_len, head_size, query_head_count, key_value_head_count, token_count,
+                 key_value_token_count, key_value_start, key_value_capacity, query_head_count / key_value_head_count,
+                 scale, value_layout, quantize_query_f16, output, 0, 0, 0};
+  GqaJob *jobs = calloc(threads, sizeof(GqaJob));
+  pthread_t *tids = calloc(threads, sizeof(pthread_t));
+  if (!jobs || !tids) {
+    free(jobs);
+    free(tids);
     return HPO_ERR_SHAPE;
   }
-  for (size_t t = 0; t < token_count; t++) {
-    for (size_t qh = 0; qh < query_head_count; qh++) {
-      const size_t kvh = qh / group;
-      const size_t qo = (t * query_head_count + qh) * head_size;
-      for (size_t i = 0; i < head_size; i++)
-        qv[i] = quantize_query_f16 ? hpo_f16_to_f32(hpo_f32_to_f16_rust(query[qo + i])) : query[qo + i];
-      float max_score = -INFINITY;
-      for (size_t kt = 0; kt < key_value_token_count; kt++) {
-        const size_t phys = (key_value_start + kt) % key_value_capacity;
-        const size_t ko = (phys * key_value_head_count + kvh) * head_size;
-        float dot = 0.0f;
-        for (size_t i = 0; i < head_size; i++) dot = dot + qv[i] * key[ko + i];
-        const float mv = mask_len == 0 ? 0.0f : mask[t * key_value_token_count + kt];
-        const float score = mv == -INFINITY ? -INFINITY : (dot * scale) + mv;
-        scores[kt] = score;
-        if (score > max_score) max_score = score;
-      }
-      float sum = 0.0f;
-      for (size_t kt = 0; kt < key_value_token_count; kt++) {
-        const float sc = scores[kt];
-        const float p = sc == -INFINITY ? 0.0f : (float)hpo_exp((double)(sc - max_score));
-        scores[kt] = p;
-        sum += p;
-      }
-      for (size_t i = 0; i < head_size; i++) {
-        float weighted = 0.0f;
-        for (size_t kt = 0; kt < key_value_token_count; kt++) {
-          const size_t phys = (key_value_start + kt) % key_value_capacity;
-          const size_t vo = value_layout == 1 ? (i * key_value_head_count + kvh) * key_value_capacity + phys
-                                              : (phys * key_value_head_count + kvh) * head_size + i;
-          weighted = weighted + (scores[kt] / sum) * value[vo];
-        }
-        output[qo + i] = weighted;
-      }
-    }
+  int started[16] = {0};
+  for (size_t w = 0; w < threads; w++) {
+    jobs[w] = base;
+    jobs[w].row_begin = rows * w / threads;
+    jobs[w].row_end = rows * (w + 1) / threads;
   }
-  free(scores);
-  free(qv);
-  return HPO_OK;
+  for (size_t w = 1; w < threads; w++) started[w] = pthread_create(&tids[w], NULL, gqa_worker, &jobs[w]) == 0;
+  gqa_rows(&jobs[0]);
+  int failed = jobs[0].failed;
+  for (size_t w = 1; w < threads; w++) {
+    if (started[w])
+      pthread_join(tids[w], NULL);
+    else
+      gqa_rows(&jobs[w]);  /* no thread: this one runs here */
+    failed |= jobs[w].failed;
+  }
+  free(jobs);
+  free(tids);
+  return failed ? HPO_ERR_SHAPE : HPO_OK;
 }

@@ -21,9 +21,9 @@ are tolerances stated per step:
   the new residual stream.  An f16 step of the attention output feeds the O
   projection's Q8_K input, where it can move a block's rounding and shift O
   by ~1 %, which the post-attention norm carries into the residual (3.0e-3
-  of the row rms the largest measured, over 42 layers of a 4-token draft;
-  every layer case here comes out bit-identical, as the printed fraction
-  shows).
+  of the row rms the largest measured, over 42 layers of a 4-token draft).
+  The one-token layer cases here come out bit-identical to the oracle, and
+  the tests assert it.
 Projections inside the layer are the bit-exact matvec kernels.
 """
 import numpy as np
@@ -35,7 +35,7 @@ from heliopause_amd import synthetic as S
 
 pytestmark = pytest.mark.gpu
 
-LAYER_TOL = 5e-3
+LAYER_TOL = 3.5e-3
 FLOOR = 0.01
 
 
@@ -263,6 +263,7 @@ def test_decode_layer_matches_oracle(hip, D, full, pos, kernel):
     err = _row_err(got, ref)
     print(f"layer err {err:.3e} of the row rms; identical {np.mean(got == ref):.4f}", flush=True)
     assert err <= LAYER_TOL
+    assert np.array_equal(np.asarray(got, np.float32).view(np.uint32), np.asarray(ref, np.float32).view(np.uint32))
     slot = pos % shape.capacity
     assert _f16_steps(gk[:, slot], ol.key_cache[:, slot]).max() <= 1
     assert _f16_steps(gv[:, slot], ol.value_cache[:, slot]).max() <= 1

@@ -34,7 +34,8 @@ HEAD_ROWS, HIDDEN, FFN = 262144, 2560, 10240
 # block's rounding and shift O by ~1 %, which the post-attention norm
 # carries into the residual (measured over 42 layers of a 4-token draft:
 # 3.0e-3 of the row rms at most, 39 of the 42 layers bit-identical).
-LAYER_TOL = 5e-3
+LAYER_TOL = 3.5e-3
+DRAFT_IDENTICAL_LAYERS = 39  # of 42, measured on this seed
 FLOOR = 0.01
 
 
@@ -75,6 +76,23 @@ def _topk_ok(got, logits, k, oracle):
         g_vals = np.array([c["value"] for c in got[r]], dtype=np.float32)
         assert np.array_equal(g_ids, ids), (r, g_ids[:6], ids[:6])
         assert np.array_equal(_bits(g_vals), _bits(vals)), r
+
+
+def _topk_near_ties(g_ids, g_logits, ref_logits, k, what):
+    """Top-k ids of logits that carry an end-to-end perturbation: with D the
+    largest |g - ref| over the row, an id can sit in one top-k and not the
+    other only if its reference logit is within 2D of the reference's k-th
+    largest (a larger margin keeps it on the same side in both)."""
+    ids = np.argsort(-ref_logits, kind="stable")[:k]
+    kth = float(ref_logits[ids[-1]])
+    d = float(np.max(np.abs(np.asarray(g_logits, np.float64) - ref_logits)))
+    moved = set(int(i) for i in g_ids) ^ set(int(i) for i in ids)
+    shared = len(set(int(i) for i in g_ids) & set(int(i) for i in ids))
+    print(f"{what}: top-{k} shared {shared}, logits max diff {d:.3e}, k-th logit {kth:.4f}, "
+          f"moved ids {sorted(moved)[:8]}", flush=True)
+    for i in moved:
+        assert abs(float(ref_logits[i]) - kth) <= 2 * d, (what, i, float(ref_logits[i]), kth, d)
+    return shared
 
 
 def _cus(hip):
@@ -196,7 +214,7 @@ def _oracle_layer(D, shape, data):
 
 
 N_LAYERS = 42
-DISTINCT = 3  # layer i uses the weights of synthetic layer i % 3; every layer has its own cache
+DISTINCT = 42  # every layer its own weights and its own cache
 
 
 def _model_42(hip, shape, datas):
@@ -217,13 +235,22 @@ def test_decode_step_42_layers_with_head(hip, oracle, head_blocks, tokens):
     then the head and the top-40 of each token.
 
     - One token: against the oracle's 42 layers and head end to end; the
-      residual stream within the layer tolerance and the top-40 ids identical.
+      residual stream and the output norm bit-identical, the top-40 ids
+      identical.
     - A 4-token draft: the same step layer by layer, each layer's output
       against the oracle's layer on that layer's GPU input (the layer
-      tolerance), and the one-call step bit-identical to the layer-by-layer
-      run.  End to end, 42 random layers carry an early O difference (see
-      LAYER_TOL) through every later norm, so the end-to-end error is
-      printed, not bounded.
+      tolerance, and at least DRAFT_IDENTICAL_LAYERS of the 42 layers
+      bit-identical), and the one-call step bit-identical to the
+      layer-by-layer run.  End to end, 42 random layers carry an early O
+      difference (see LAYER_TOL) through every later norm, so the end-to-end
+      residual error is printed; what the step produces, the top-40 ids of
+      every draft row through the output norm and head, agrees with the
+      oracle's end to end up to near-ties of that row's measured logit
+      difference (_topk_near_ties).  Measured on this seed: row 0 identical
+      logits and ids; rows 1 and 2 logits within 6.3 (top-40 boundary near
+      380), 39 and 40 ids shared; row 3 diverged (logits 648 apart, 3 ids
+      shared), the three non-identical layers amplified by the 40 after
+      them, so its check constrains nothing.
     - The head on the step's normed output: logits bit-identical to the
       oracle's head on the same input, top-40 ids and values identical."""
     import torch
@@ -284,8 +311,8 @@ def test_decode_step_42_layers_with_head(hip, oracle, head_blocks, tokens):
         ref_normed = D.rms_norm_rows(h, onorm, shape.epsilon)
         print(f"42 layers: hidden err {_row_err(got_hidden, h):.3e} of the row rms, identical "
               f"{float(np.mean(got_hidden == h)):.5f}", flush=True)
-        assert _row_err(got_hidden, h) <= LAYER_TOL
-        assert _row_err(got_normed, ref_normed) <= LAYER_TOL
+        assert np.array_equal(_bits(got_hidden), _bits(h))
+        assert np.array_equal(_bits(got_normed), _bits(ref_normed))
         end_logits = oracle.matmul(3, head_blocks, ref_normed, HEAD_ROWS, threads=8)
         ids, _ = oracle.topk(end_logits[0], 40)
         assert np.array_equal(np.array([c["id"] for c in got_top[0]], np.uint32), ids)
@@ -299,9 +326,16 @@ def test_decode_step_42_layers_with_head(hip, oracle, head_blocks, tokens):
         h = x.copy()
         for L in [_oracle_layer(D, shape, datas[i % DISTINCT]) for i in range(N_LAYERS)]:
             h = D.forward_layer(L, h, pos)
+        n_ident = sum(v == 1.0 for v in ident)
         print(f"42 layers by layer: max err {max(errs):.3e} of the row rms, layers identical "
-              f"{sum(v == 1.0 for v in ident)} of {N_LAYERS}; end to end {_row_err(got_hidden, h):.3e}", flush=True)
+              f"{n_ident} of {N_LAYERS}; end to end {_row_err(got_hidden, h):.3e}", flush=True)
         assert max(errs) <= LAYER_TOL, errs
+        assert n_ident >= DRAFT_IDENTICAL_LAYERS, ident
+        ref_normed = D.rms_norm_rows(h, onorm, shape.epsilon)
+        end_logits = oracle.matmul(3, head_blocks, ref_normed, HEAD_ROWS, threads=8)
+        for r in range(tokens):
+            g_ids = np.array([c["id"] for c in got_top[r]], np.uint32)
+            _topk_near_ties(g_ids, got_logits[r], end_logits[r].astype(np.float64), 40, f"draft row {r}")
 
 
 @pytest.mark.parametrize("tokens", [2, 3, 4, 5, 6, 7, 8])

@@ -25,6 +25,12 @@ forwardFfn (layers.ts:161-473) over the same tokens.
   row rms (2.4e-2 the largest measured).  So the bars are: every row within
   LAYER_TOL, the median row within ROW_TYPICAL, and at least ROWS_CLOSE of
   the rows within 1e-3 (measured values printed).
+- Three layers of the model over a 512-token chunk on the automatic policy
+  (fast prefill kernel, activation tiles written by the norm kernel,
+  block-range sums handed from each layer's down launch to the next
+  layer's norm) against the oracle's forward_layer chain, to the same row
+  bars, then the last token through the output norm and the Q6_K
+  262144 x 2560 head: its top-40 ids equal the oracle's end to end.
 """
 import numpy as np
 import pytest
@@ -34,9 +40,21 @@ from heliopause_amd import synthetic as S
 
 pytestmark = pytest.mark.gpu
 
-LAYER_TOL = 5e-2    # every row
+LAYER_TOL = 3e-2    # every row
 ROW_TYPICAL = 1e-4  # the median row
 ROWS_CLOSE = 0.75   # the fraction of rows within 1e-3
+TILE_OFF = 0.5      # the largest fraction of a 64-row tile beyond 1e-3
+CHAIN_TOL = 6e-2    # every row after two layers on the fast prefill kernel
+# Every row of a 512-token layer on a seed where one attention output lands
+# an f16 step away at the largest element of one of O's Q8_K input blocks:
+# the block re-rounds and that token's residual moves by up to 0.199 of its
+# rms (0.174 with the bit-exact projections, so the projections are not the
+# cause; test_prefill_stages_512_auto pins them stage by stage).
+ATTN_STEP_TOL = 0.25
+STAGE_TOL = 1e-4    # projections on the automatic policy, relative (FLOOR)
+DOWN_TOL = 2e-4     # down on the GeGLU output: outputs near the floor carry the
+                    # fast kernel's f32 accumulation order (1.29e-4 measured)
+SWAP_TOL = 1e-2     # any row, one GPU stage output swapped into the oracle chain
 FLOOR = 0.01
 
 
@@ -84,14 +102,21 @@ def _row_errs(got, ref):
     return np.array([np.max(np.abs(gr - rr)) / np.sqrt(np.mean(rr * rr)) for gr, rr in zip(g, r)])
 
 
-def _check_rows(got, ref, what):
+def _check_rows(got, ref, what, tol=None):
+    """The row bars, and that the rows beyond 1e-3 are spread over the
+    chunk: no 64-token tile (the projections' column tile) has more than
+    TILE_OFF of its rows beyond 1e-3, which a fault confined to one tile
+    would break."""
     e = _row_errs(got, ref)
     worst, median, close = float(e.max()), float(np.median(e)), float(np.mean(e <= 1e-3))
+    tiles = [np.mean(e[t:t + 64] > 1e-3) for t in range(0, len(e) - 15, 64)]
+    tile_off = float(max(tiles)) if tiles else 0.0
     print(f"{what}: max row err {worst:.3e}, median {median:.3e}, rows within 1e-3 {close:.3f}, identical rows "
-          f"{np.mean(e == 0):.3f}", flush=True)
-    assert worst <= LAYER_TOL
+          f"{np.mean(e == 0):.3f}, worst tile off {tile_off:.3f}", flush=True)
+    assert worst <= (LAYER_TOL if tol is None else tol)
     assert median <= ROW_TYPICAL
     assert close >= ROWS_CLOSE
+    assert tile_off <= TILE_OFF
 
 
 ATTN_CASES = [  # tokens, nq, nkv, capacity, first position, window, query scale
@@ -219,13 +244,16 @@ def test_prefill_layer_matches_oracle(hip, D, tokens, kernel):
         assert cache_err <= 4e-3
 
 
-def test_prefill_chunks_through_layers(hip, D):
+@pytest.mark.parametrize("kernel", [4, 0], ids=["exact", "auto"])
+def test_prefill_chunks_through_layers(hip, D, kernel):
     """150 tokens through two small layers with a 64-slot ring: the call
     runs chunks of 64, 64 and 22 tokens, each through both layers in turn, as
-    the WASM runner's chunked path does; then the output norm."""
+    the WASM runner's chunked path does; then the output norm.  Kernel 4:
+    the bit-exact prefill projections; 0: the automatic policy (the
+    64-token chunks on the fast prefill kernel)."""
     import torch
 
-    hip.setMatvecKernel(4)
+    hip.setMatvecKernel(kernel)
     shape = DM.ModelShape(hidden=512, head_count=2, head_count_kv=1, ffn=1024, capacity=64, sliding_window=48)
     seed = S.derive(S.BASE_SEED, "prefill-chunks")
     datas = [DM.layer_host_data(shape, seed, i) for i in range(2)]
@@ -239,7 +267,7 @@ def test_prefill_chunks_through_layers(hip, D):
     dx = _dev(x.reshape(-1))
     dpos = _dev(np.array([pos], np.int32))
     out = torch.empty(tokens * shape.hidden, dtype=torch.float32, device="cuda:0")
-    print("prefill chunks 150 tokens, ring 64", flush=True)
+    print(f"prefill chunks 150 tokens, ring 64, kernel {kernel}", flush=True)
     try:
         model.run_layers(dx.data_ptr(), dpos.data_ptr(), out.data_ptr(), tokens=tokens)
         torch.cuda.synchronize()
@@ -256,5 +284,190 @@ def test_prefill_chunks_through_layers(hip, D):
             h = D.forward_layer(ol, h, pos + c0)
         ref[c0:c0 + len(h)] = h
     ref_out = D.rms_norm_rows(ref, onorm, shape.epsilon)
-    _check_rows(got, ref, "chunked hidden")
-    _check_rows(got_out, ref_out, "chunked output norm")
+    # the automatic policy's 1e-4 projections re-round Q8_K blocks in both
+    # layers: the second layer carries the first one's moved rows (5.6e-2 of
+    # the row rms the largest measured)
+    tol = None if kernel == 4 else CHAIN_TOL
+    _check_rows(got, ref, "chunked hidden", tol)
+    _check_rows(got_out, ref_out, "chunked output norm", tol)
+
+
+def _topk_near_ties(g_ids, g_logits, ref_logits, k, what):
+    """Top-k ids of logits that carry an end-to-end perturbation: with D the
+    largest |g - ref| over the row, an id can sit in one top-k and not the
+    other only if its reference logit is within 2D of the reference's k-th
+    largest (a larger margin keeps it on the same side in both)."""
+    ids = np.argsort(-ref_logits, kind="stable")[:k]
+    kth = float(ref_logits[ids[-1]])
+    d = float(np.max(np.abs(np.asarray(g_logits, np.float64) - ref_logits)))
+    moved = set(int(i) for i in g_ids) ^ set(int(i) for i in ids)
+    shared = len(set(int(i) for i in g_ids) & set(int(i) for i in ids))
+    print(f"{what}: top-{k} shared {shared}, logits max diff {d:.3e}, k-th logit {kth:.4f}, "
+          f"moved ids {sorted(moved)[:8]}", flush=True)
+    for i in moved:
+        assert abs(float(ref_logits[i]) - kth) <= 2 * d, (what, i, float(ref_logits[i]), kth, d)
+    return shared
+
+
+def test_prefill_three_layers_512_auto_with_head(hip, D, oracle):
+    """Three layers of the 42-layer model over one 512-token chunk ending at
+    position 4095, on the automatic policy.
+
+    - The three layers in one call (block-range sums of each down launch
+      added by the next layer's norm launch) bit-identical to three calls
+      of one layer each (whose sums are reduced at the call's end).
+    - Each layer against the oracle's forward_layer on that layer's own
+      input, to the single-layer row bars except the every-row bar, which is
+      ATTN_STEP_TOL on this seed.
+    - The output norm of the last token through the Q6_K 262144 x 2560 head:
+      the oracle's head on the GPU's normed row gives the same logits and
+      top-40; end to end (the oracle's own three layers, whose moved Q8_K
+      blocks the next layers amplify), the top-40 ids agree up to near-ties
+      of the measured logit difference."""
+    import torch
+
+    shape = DM.ModelShape()
+    tokens, n_layers, head_rows = 512, 3, 262144
+    seed = S.derive(S.BASE_SEED, "prefill-3-layers")
+    datas = [DM.layer_host_data(shape, seed, i) for i in range(n_layers)]
+    onorm = (1 + 0.1 * S.normal(S.derive(seed, "onorm"), shape.hidden)).astype(np.float32)
+    head_blocks = S.q6_k_blocks(S.derive(seed, "head"), head_rows, shape.hidden)
+    models = [DM.HipDecodeModel(shape), DM.HipDecodeModel(shape)]
+    for m in models:
+        for d in datas:
+            m.add_layer(d)
+        m.output_norm = _dev(onorm)
+    head = hip.createHipQuantizedWeightHandle("Q6_K", head_blocks, shape.hidden, head_rows)
+    pos = shape.capacity - tokens
+    x = S.activations(S.derive(seed, "x"), tokens, shape.hidden) * 4
+    dpos = _dev(np.array([pos], np.int32))
+    print("prefill 3 layers 512 tokens, automatic policy", flush=True)
+    try:
+        hip.setMatvecKernel(0)
+        dx = _dev(x.reshape(-1))
+        out = torch.empty(tokens * shape.hidden, dtype=torch.float32, device="cuda:0")
+        models[0].run_layers(dx.data_ptr(), dpos.data_ptr(), out.data_ptr(), tokens=tokens)
+        # the same layers one call each, on the second copy of the caches
+        lx = _dev(x.reshape(-1))
+        lout = torch.empty_like(out)
+        inputs = [x.copy()]
+        twin = models[1]
+        for i in range(n_layers):
+            one = (type(twin.layers[0]) * 1)(twin.layers[i])
+            last = i == n_layers - 1
+            hip.assertHipOk(hip.lib().hp_hip_decode_layers_device(
+                one, 1, tokens, lx.data_ptr(), dpos.data_ptr(), twin.output_norm.data_ptr() if last else None,
+                lout.data_ptr() if last else None, None), "decode_layers")
+            torch.cuda.synchronize()
+            inputs.append(lx.cpu().numpy().reshape(tokens, shape.hidden))
+        logits = torch.empty(head_rows, dtype=torch.float32, device="cuda:0")
+        hip.matmul_multi_device([head.handle], out[(tokens - 1) * shape.hidden:].data_ptr(), shape.hidden, 1,
+                                [logits.data_ptr()], [head_rows])
+        torch.cuda.synchronize()
+        got = dx.cpu().numpy().reshape(tokens, shape.hidden)
+        got_out = out.cpu().numpy().reshape(tokens, shape.hidden)
+        got_lout = lout.cpu().numpy().reshape(tokens, shape.hidden)
+        got_logits = logits.cpu().numpy()
+        got_top = hip.topKHip(got_logits.reshape(1, head_rows), 40)
+    finally:
+        for m in models:
+            m.release()
+        hip.releaseHipQuantizedWeightHandle(head)
+        hip.setMatvecKernel(0)
+    assert np.array_equal(got.view(np.uint32), inputs[-1].view(np.uint32)), "one call != one layer per call"
+    assert np.array_equal(got_out.view(np.uint32), got_lout.view(np.uint32)), "output norm differs"
+    for i, d in enumerate(datas):
+        ref = D.forward_layer(_oracle_layer(D, shape, d), inputs[i], pos)
+        _check_rows(inputs[i + 1], ref, f"layer {i} on its own input", ATTN_STEP_TOL)
+    # the head and top-40 on the GPU's normed last row
+    ref_logits = oracle.matmul(3, head_blocks, got_out[-1:], head_rows, threads=8)[0]
+    assert np.array_equal(got_logits.view(np.uint32), ref_logits.view(np.uint32))
+    ids, _ = oracle.topk(ref_logits, 40)
+    g_ids = np.array([c["id"] for c in got_top[0]], np.uint32)
+    assert np.array_equal(g_ids, ids)
+    # end to end
+    h = x.copy()
+    for d in datas:
+        h = D.forward_layer(_oracle_layer(D, shape, d), h, pos)
+    ref_out = D.rms_norm_rows(h, onorm, shape.epsilon)
+    e2e = oracle.matmul(3, head_blocks, ref_out[-1:], head_rows, threads=8)[0].astype(np.float64)
+    shared = _topk_near_ties(g_ids, got_logits, e2e, 40, "last token end to end")
+    assert shared >= 36
+
+
+def _rel(got, ref, floor=FLOOR):
+    got = np.asarray(got, np.float64).reshape(-1)
+    ref = np.asarray(ref, np.float64).reshape(-1)
+    den = np.maximum(np.abs(ref), floor * np.sqrt(np.mean(ref * ref)))
+    return float(np.max(np.abs(got - ref) / den))
+
+
+def test_prefill_stages_512_auto(hip, D, oracle):
+    """The projections of one 512-token layer on the automatic policy (the
+    fast prefill kernel), each on the oracle's own input to that stage:
+    Q/K/V on attn_norm, O on the attention output, gate/up on ffn_norm, down
+    on the GeGLU output, each within its relative bar.  Then each stage's
+    GPU output swapped into the oracle's chain in place of the oracle's: no
+    row of the layer output moves by more than SWAP_TOL of its rms, so the
+    projections stay well inside the whole-layer bars."""
+    import torch
+
+    shape = DM.ModelShape()
+    tokens = 512
+    seed = S.derive(S.BASE_SEED, "prefill-3-layers")
+    data = DM.layer_host_data(shape, seed, 0)
+    pos = shape.capacity - tokens
+    x = S.activations(S.derive(seed, "x"), tokens, shape.hidden) * 4
+    L = _oracle_layer(D, shape, data)
+    ref = D.forward_layer(L, x, pos)
+    tr = L.trace
+    w = {n: data["weights"][n] for n in DM.PROJ_NAMES}
+    tid = {"Q4_K": 1, "Q6_K": 3}
+    hs = {n: hip.createHipQuantizedWeightHandle(t, b, k, r) for n, (t, b, r, k) in w.items()}
+
+    def gpu(names, inp):
+        inp = np.ascontiguousarray(inp, np.float32).reshape(tokens, -1)
+        di = _dev(inp.reshape(-1))
+        outs = [torch.empty(tokens * w[n][2], dtype=torch.float32, device="cuda:0") for n in names]
+        hip.matmul_multi_device([hs[n].handle for n in names], di.data_ptr(), inp.shape[1], tokens,
+                                [o.data_ptr() for o in outs], [o.numel() for o in outs])
+        torch.cuda.synchronize()
+        return [o.cpu().numpy().reshape(tokens, -1) for o in outs]
+
+    print("prefill stages 512 tokens, automatic policy", flush=True)
+    try:
+        hip.setMatvecKernel(0)
+        gq, gk, gv = gpu(["attn_q", "attn_k", "attn_v"], tr["attn_norm"])
+        go, = gpu(["attn_output"], tr["attention"])
+        gg, gu = gpu(["ffn_gate", "ffn_up"], tr["ffn_norm"])
+        gd, = gpu(["ffn_down"], tr["ffn_hidden"])
+    finally:
+        for h in hs.values():
+            hip.releaseHipQuantizedWeightHandle(h)
+    og, ou = oracle.matmul_multi([tid[w["ffn_gate"][0]], tid[w["ffn_up"][0]]], [w["ffn_gate"][1], w["ffn_up"][1]],
+                                 tr["ffn_norm"], [w["ffn_gate"][2], w["ffn_up"][2]], threads=8)
+    errs = {"q": _rel(gq, tr["q"]), "k": _rel(gk, tr["k"]), "v": _rel(gv, tr["v"]), "o": _rel(go, tr["o"]),
+            "gate": _rel(gg, og), "up": _rel(gu, ou), "down": _rel(gd, tr["down"])}
+    print("stage rel err " + ", ".join(f"{k} {v:.2e}" for k, v in errs.items()), flush=True)
+    for k, v in errs.items():
+        assert v <= (DOWN_TOL if k == "down" else STAGE_TOL), (k, v)
+
+    eps = shape.epsilon
+    nrm = data["norms"]
+
+    def chain(o=None, gate=None, up=None, down=None):
+        o = tr["o"] if o is None else o
+        x1 = D.residual_add(x, D.rms_norm_rows(o, nrm["post_attention_norm"], eps))
+        xn2 = D.rms_norm_rows(x1, nrm["ffn_norm"], eps)
+        g0, u0 = oracle.matmul_multi([1, 1], [w["ffn_gate"][1], w["ffn_up"][1]], xn2,
+                                     [w["ffn_gate"][2], w["ffn_up"][2]], threads=8)
+        h = oracle.geglu(g0 if gate is None else gate, u0 if up is None else up)
+        y = oracle.matmul_multi([3], [w["ffn_down"][1]], h, [w["ffn_down"][2]], threads=8)[0] if down is None else down
+        x2 = D.residual_add(x1, D.rms_norm_rows(y, nrm["post_ffw_norm"], eps))
+        return (x2.astype(np.float64) * np.float64(np.float32(data["output_scale"]))).astype(np.float32)
+
+    assert np.array_equal(chain(), ref)   # the replayed chain is forward_layer's
+    for what, out in (("o", chain(o=go)), ("gate/up", chain(gate=gg, up=gu)), ("down", chain(down=gd))):
+        e = float(_row_errs(out, ref).max())
+        print(f"{what} swapped in: max row err {e:.3e}", flush=True)
+        assert e <= SWAP_TOL, (what, e)
