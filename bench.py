@@ -264,9 +264,7 @@ def decode_chain(args) -> int:
 
     if args.m != 1:
         raise SystemExit("decode42 runs at M = 1")
-    H.setMatvecKernel({"auto": H.MATVEC_AUTO, "valu": H.MATVEC_VALU, "mfma": H.MATVEC_MFMA,
-                       "half": H.MATVEC_HALF, "wide": H.MATVEC_WIDE,
-                       "wide-whole": H.MATVEC_WIDE_WHOLE, "wide-half": H.MATVEC_WIDE_HALF}[args.kernel])
+    H.setMatvecKernel(KERNEL_CHOICES[args.kernel](H))
     torch.cuda.init()
     dev = torch.device("cuda:0")
     seed = S.config_seed(5)
@@ -478,9 +476,7 @@ def decode_step(args) -> int:
     from heliopause_amd import hip_kernels as H
 
     m = args.m
-    H.setMatvecKernel({"auto": H.MATVEC_AUTO, "valu": H.MATVEC_VALU, "mfma": H.MATVEC_MFMA,
-                       "half": H.MATVEC_HALF, "wide": H.MATVEC_WIDE,
-                       "wide-whole": H.MATVEC_WIDE_WHOLE, "wide-half": H.MATVEC_WIDE_HALF}[args.kernel])
+    H.setMatvecKernel(KERNEL_CHOICES[args.kernel](H))
     r = measure_decode_step(m, max(1, args.steps // 10), max(1, args.warmup // 10),
                             None if args.no_cpu else args.cpu_seconds)
     ms = r["ms"]
@@ -560,9 +556,7 @@ def prefill_chain(args) -> int:
     from heliopause_amd import synthetic as S
 
     m = args.m if args.m > 1 else 512
-    H.setMatvecKernel({"auto": H.MATVEC_AUTO, "valu": H.MATVEC_VALU, "mfma": H.MATVEC_MFMA,
-                       "half": H.MATVEC_HALF, "wide": H.MATVEC_WIDE,
-                       "wide-whole": H.MATVEC_WIDE_WHOLE, "wide-half": H.MATVEC_WIDE_HALF}[args.kernel])
+    H.setMatvecKernel(KERNEL_CHOICES[args.kernel](H))
     torch.cuda.init()
     dev = torch.device("cuda:0")
     seed = S.config_seed(5)
@@ -866,21 +860,106 @@ def main() -> int:
         return prefill_chain(args)
     if args.workload == "prefill42-layers":
         return prefill_layers(args)
+    from heliopause_amd import hip_kernels as H
+
+    support = H.checkHipSupport()
+    if not support["available"]:
+        raise SystemExit(f"HIP runner unavailable: {support}")
+    H.setMatvecKernel(KERNEL_CHOICES[args.kernel](H))
+    wl, m = args.workload, args.m
+    r = measure_matvec(wl, m, args.kernel, max(1, args.steps), max(0, args.warmup), args.rotate_mib)
+
+    extra = {}
+    if wl == "qkv" and m == 1 and not args.no_decode:
+        # the other matvec configurations with a budget of their own, timed
+        # the same way in the same run: config 1 and the head with top-40
+        for name in ("cfg1", "head"):
+            e = measure_matvec(name, 1, args.kernel, 20 if name == "cfg1" else 10, 5, args.rotate_mib)
+            extra[name] = matvec_summary(e)
+        extra["decode_step"] = decode_summary(measure_decode_step(1, 20, 3, None))
+
+    traffic = None
+    tfile = ROOT / "profiles" / f"{wl}_m{m}_traffic.json"
+    if tfile.exists():
+        try:
+            traffic = json.loads(tfile.read_text()).get("hbm_bytes_per_launch")
+        except (ValueError, OSError):
+            traffic = None
+
+    cpu = None
+    if not args.no_cpu:
+        cpu = cpu_baseline(wl, r["ws"], r["x_host"], args.cpu_seconds)
+
+    K = r["steps"]
+    line = {
+        "metric": METRIC,
+        "value": round(r["value"], 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": K,
+        "warmup": args.warmup,
+        "ms_per_step": round(r["ms_per_step"], 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int8",
+        "data": "synthetic",
+        "config": {
+            "workload": r["desc"],
+            "M": m,
+            "weight_bytes": weight_bytes(wl),
+            "algorithmic_bytes_per_step": r["step_bytes"],
+            "weight_copies_rotated": r["copies"],
+            "parallelism": "single GPU",
+            "timing": f"exactly {K} steps (step i on weight copy i % {r['copies']}) captured in one HIP graph and "
+                      f"replayed once, after a warm-up graph of {r['warm_count']} steps over the other copies",
+            "eager_host_launch_ms_per_step": round(r["eager_ms"], 5),
+            "graph_launch": graph_launch_summary(r),
+        },
+        "roofline": {
+            "bound": "hbm",
+            "achieved": round(r["achieved"], 2),
+            "peak": HBM_PEAK_GBPS,
+            "unit": "GB/s",
+            "frac": round(r["achieved"] / HBM_PEAK_GBPS, 4),
+            "traffic": traffic,
+            "traffic_source": (f"profiles/{tfile.name}: rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE of this launch "
+                               "in an earlier run, scaled by a plain copy kernel's counters; not measured by "
+                               "this run") if traffic is not None else None,
+            "kernel": r["kernel"],
+            "kernel_avg_us": round(r["kern_us"], 3),
+            "kernel_avg_us_mall_hot": round(r["hot_us"], 3),
+        },
+        "cpu_baseline": cpu,
+    }
+    line.update(extra)
+    print(json.dumps(line))
+    return 0
+
+
+KERNEL_CHOICES = {"auto": lambda H: H.MATVEC_AUTO, "valu": lambda H: H.MATVEC_VALU, "mfma": lambda H: H.MATVEC_MFMA,
+                  "half": lambda H: H.MATVEC_HALF, "wide": lambda H: H.MATVEC_WIDE,
+                  "wide-whole": lambda H: H.MATVEC_WIDE_WHOLE, "wide-half": lambda H: H.MATVEC_WIDE_HALF}
+
+# per-call budgets at 8 TB/s (weights plus activations)
+BUDGET_US = {"cfg1": 2.642}
+
+
+def measure_matvec(wl: str, m: int, kernel: str, K: int, W: int, rotate_mib: int) -> dict:
+    """K steps of workload wl at M = m, each on its own weight copy, in one
+    HIP graph after a warm-up graph over the other copies (so the timed
+    steps start with cold weights); HIP events on the launch stream bracket
+    the timed replay.  Also: eager host-submitted launches, the same K steps
+    on one copy (Infinity-Cache hot), and an empty graph of as many kernel
+    nodes as the timed one (what the graph launch itself costs)."""
     import numpy as np
     import torch
 
     from heliopause_amd import hip_kernels as H
     from heliopause_amd import synthetic as S
 
-    support = H.checkHipSupport()
-    if not support["available"]:
-        raise SystemExit(f"HIP runner unavailable: {support}")
-    H.setMatvecKernel({"auto": H.MATVEC_AUTO, "valu": H.MATVEC_VALU, "mfma": H.MATVEC_MFMA,
-                       "half": H.MATVEC_HALF, "wide": H.MATVEC_WIDE,
-                       "wide-whole": H.MATVEC_WIDE_WHOLE, "wide-half": H.MATVEC_WIDE_HALF}[args.kernel])
     torch.cuda.init()
     dev = torch.device("cuda:0")
-    wl, m = args.workload, args.m
     cfg, k, specs, desc = WORKLOADS[wl]
     seed = S.config_seed(cfg)
     ws = [S.weight_blocks(t, S.derive(seed, wl, i), r, k) for i, (t, r) in enumerate(specs)]
@@ -891,9 +970,9 @@ def main() -> int:
     # before the timed ones (the warm-up graph) cover >= 320 MiB of other
     # copies, more than the 256 MB Infinity Cache holds
     wb = weight_bytes(wl)
-    copies = max(1, math.ceil(args.rotate_mib * 2**20 / wb))
-    if args.rotate_mib >= 320:
-        copies = max(copies, min(args.steps, 4096) + math.ceil(320 * 2**20 / wb))
+    copies = max(1, math.ceil(rotate_mib * 2**20 / wb))
+    if rotate_mib >= 320:
+        copies = max(copies, min(K, 4096) + math.ceil(320 * 2**20 / wb))
     handles, down_handles = [], []
     for _ in range(copies):
         handles.append([H.createHipQuantizedWeightHandle(t, w, k, r).handle for (t, r), w in zip(specs, ws)])
@@ -924,147 +1003,134 @@ def main() -> int:
             H.assertHipOk(L.hp_hip_topk_device(out_ptrs[0], m, 262144, TOPK, 0.0, ids.data_ptr(), vals.data_ptr(),
                                                stream), "topk")
 
-    # correctness guard on the benchmarked path (first copy vs the host API)
-    if wl != "ffn":
-        step(0)
+    try:
+        # correctness guard on the benchmarked path (first copy vs the host API)
+        if wl != "ffn":
+            step(0)
+            torch.cuda.synchronize()
+            host = [H.matMulQuantizedHipResident(H.HipQuantizedWeightHandle(h, t, 0, r, k), x_host, k, r, m)
+                    for h, (t, r) in zip(handles[0], specs)]
+            for a, b in zip(outs, host):
+                if not np.array_equal(a.cpu().numpy().view(np.uint32), b.view(np.uint32)):
+                    raise SystemExit("device-pointer path disagrees with the host path")
+
+        step_bytes = algorithmic_bytes(wl, m)
+        # eager: host-submitted launches (bounded by the host submission rate)
+        for i in range(min(W, 8)):
+            step(K + i)
         torch.cuda.synchronize()
-        host = [H.matMulQuantizedHipResident(H.HipQuantizedWeightHandle(h, t, 0, r, k), x_host, k, r, m)
-                for h, (t, r) in zip(handles[0], specs)]
-        for a, b in zip(outs, host):
-            if not np.array_equal(a.cpu().numpy().view(np.uint32), b.view(np.uint32)):
-                raise SystemExit("device-pointer path disagrees with the host path")
-
-    step_bytes = algorithmic_bytes(wl, m)
-    K, W = max(1, args.steps), max(0, args.warmup)
-    # eager: host-submitted launches (bounded by the host submission rate)
-    for i in range(min(W, 8)):
-        step(K + i)
-    torch.cuda.synchronize()
-    n_eager = min(K, 100)
-    t0 = time.perf_counter()
-    for i in range(n_eager):
-        step(K + i)
-    torch.cuda.synchronize()
-    eager_ms = (time.perf_counter() - t0) / n_eager * 1e3
-
-    # Graphs on one side stream (warmed by an uncaptured step first): the
-    # timed graph holds exactly K steps, step i on copy i % copies; the
-    # warm-up graph holds the W warm-up steps and at least every copy the
-    # timed graph does not touch first, so the timed steps start with cold
-    # weights.
-    side = torch.cuda.Stream()
-    side.wait_stream(torch.cuda.current_stream())
-
-    def capture(first: int, count: int, same_copy: bool = False):
-        nonlocal stream
-        g = torch.cuda.CUDAGraph()
-        with torch.cuda.stream(side):
-            with torch.cuda.graph(g, stream=side):
-                stream = torch.cuda.current_stream().cuda_stream
-                for i in range(count):
-                    step(0 if same_copy else first + i)
-        return g
-
-    with torch.cuda.stream(side):
-        stream = side.cuda_stream
-        step(0)
-    torch.cuda.synchronize()
-    warm_count = max(W, copies - K if K < copies else 0, 1)
-    g_warm = capture(K, warm_count)
-    g_timed = capture(0, K)
-    start = torch.cuda.Event(enable_timing=True)
-    end = torch.cuda.Event(enable_timing=True)
-    with torch.cuda.stream(side):
-        g_warm.replay()
-        torch.cuda.synchronize()
+        n_eager = min(K, 100)
+        launches0 = H.hipResidentWeightStats()["kernelLaunches"]
         t0 = time.perf_counter()
-        start.record()
-        g_timed.replay()
-        end.record()
+        for i in range(n_eager):
+            step(K + i)
         torch.cuda.synchronize()
-        wall = time.perf_counter() - t0
-    steps = K
-    ms_per_step = wall / steps * 1e3
-    value = step_bytes / (ms_per_step * 1e-3) / 1e9
-    # HIP events bracketing the timed region on the launch stream: average
-    # device time per step (for one-kernel steps, the launch duration)
-    kern_us = start.elapsed_time(end) / steps * 1e3
-    achieved = step_bytes / (kern_us * 1e-6) / 1e9
+        eager_ms = (time.perf_counter() - t0) / n_eager * 1e3
+        nodes_per_step = (H.hipResidentWeightStats()["kernelLaunches"] - launches0) / n_eager
 
-    # Infinity-Cache-hot reference: K steps on one resident copy
-    hot = capture(0, K, same_copy=True)
-    with torch.cuda.stream(side):
-        hot.replay()
-        torch.cuda.synchronize()
-        start.record()
-        hot.replay()
-        end.record()
-        torch.cuda.synchronize()
-    hot_us = start.elapsed_time(end) / K * 1e3
+        # Graphs on one side stream (warmed by an uncaptured step first): the
+        # timed graph holds exactly K steps, step i on copy i % copies; the
+        # warm-up graph holds the W warm-up steps and at least every copy the
+        # timed graph does not touch first, so the timed steps start with cold
+        # weights.
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
 
-    decode = None
-    if wl == "qkv" and m == 1 and not args.no_decode:
+        def capture(first: int, count: int, same_copy: bool = False):
+            nonlocal stream
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.stream(side):
+                with torch.cuda.graph(g, stream=side):
+                    stream = torch.cuda.current_stream().cuda_stream
+                    for i in range(count):
+                        step(0 if same_copy else first + i)
+            return g
+
+        with torch.cuda.stream(side):
+            stream = side.cuda_stream
+            step(0)
+        torch.cuda.synchronize()
+        warm_count = max(W, copies - K if K < copies else 0, 1)
+        g_warm = capture(K, warm_count)
+        g_timed = capture(0, K)
+        start = torch.cuda.Event(enable_timing=True)
+        end = torch.cuda.Event(enable_timing=True)
+        with torch.cuda.stream(side):
+            g_warm.replay()
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            start.record()
+            g_timed.replay()
+            end.record()
+            torch.cuda.synchronize()
+            wall = time.perf_counter() - t0
+        ms_per_step = wall / K * 1e3
+        # HIP events bracketing the timed region on the launch stream: average
+        # device time per step (for one-kernel steps, the launch duration)
+        kern_us = start.elapsed_time(end) / K * 1e3
+
+        # Infinity-Cache-hot reference: K steps on one resident copy
+        hot = capture(0, K, same_copy=True)
+        with torch.cuda.stream(side):
+            hot.replay()
+            torch.cuda.synchronize()
+            start.record()
+            hot.replay()
+            end.record()
+            torch.cuda.synchronize()
+        hot_us = start.elapsed_time(end) / K * 1e3
+
+        # an empty graph of as many kernel nodes, bracketed the same way
+        nodes = max(1, round(nodes_per_step * K))
+        g_empty = torch.cuda.CUDAGraph()
+        with torch.cuda.stream(side):
+            with torch.cuda.graph(g_empty, stream=side):
+                H.emptyLaunches(nodes, torch.cuda.current_stream().cuda_stream)
+            g_empty.replay()
+            torch.cuda.synchronize()
+            start.record()
+            g_empty.replay()
+            end.record()
+            torch.cuda.synchronize()
+        empty_us = start.elapsed_time(end) * 1e3
+    finally:
         for hs in handles:
             for h in hs:
-                H.lib().hp_hip_weight_release(h)
+                L.hp_hip_weight_release(h)
+        for h in down_handles:
+            L.hp_hip_weight_release(h)
         handles.clear()
-        decode = decode_summary(measure_decode_step(1, 20, 3, None))
-
-    traffic = None
-    tfile = ROOT / "profiles" / f"{wl}_m{m}_traffic.json"
-    if tfile.exists():
-        try:
-            traffic = json.loads(tfile.read_text()).get("hbm_bytes_per_launch")
-        except (ValueError, OSError):
-            traffic = None
-
-    cpu = None
-    if not args.no_cpu:
-        cpu = cpu_baseline(wl, ws, x_host, args.cpu_seconds)
-
+        down_handles.clear()
     kernels = {"ffn": "gate/up+GeGLU matvec + down matvec", "head": "matvec + top-k"}
-    kernel_name = matvec_kernel_name(args.kernel, k, m, specs)
-    line = {
-        "metric": METRIC,
-        "value": round(value, 2),
-        "unit": "GB/s",
-        "n_gpus": 1,
-        "steps": steps,
-        "warmup": args.warmup,
-        "ms_per_step": round(ms_per_step, 5),
-        "higher_is_better": True,
-        "scaling": "weak",
-        "vs_baseline": None,
-        "dtype": "int8",
-        "data": "synthetic",
-        "config": {
-            "workload": desc,
-            "M": m,
-            "weight_bytes": weight_bytes(wl),
-            "algorithmic_bytes_per_step": step_bytes,
-            "weight_copies_rotated": copies,
-            "parallelism": "single GPU",
-            "timing": f"exactly {K} steps (step i on weight copy i % {copies}) captured in one HIP graph and "
-                      f"replayed once, after a warm-up graph of {warm_count} steps over the other copies",
-            "eager_host_launch_ms_per_step": round(eager_ms, 5),
-        },
-        "roofline": {
-            "bound": "hbm",
-            "achieved": round(achieved, 2),
-            "peak": HBM_PEAK_GBPS,
-            "unit": "GB/s",
-            "frac": round(achieved / HBM_PEAK_GBPS, 4),
-            "traffic": traffic,
-            "kernel": kernels.get(wl, kernel_name),
-            "kernel_avg_us": round(kern_us, 3),
-            "kernel_avg_us_mall_hot": round(hot_us, 3),
-        },
-        "cpu_baseline": cpu,
-    }
-    if decode is not None:
-        line["decode_step"] = decode
-    print(json.dumps(line))
-    return 0
+    return {"wl": wl, "m": m, "desc": desc, "ws": ws, "x_host": x_host, "copies": copies, "warm_count": warm_count,
+            "steps": K, "step_bytes": step_bytes, "ms_per_step": ms_per_step,
+            "value": step_bytes / (ms_per_step * 1e-3) / 1e9, "kern_us": kern_us,
+            "achieved": step_bytes / (kern_us * 1e-6) / 1e9, "hot_us": hot_us, "eager_ms": eager_ms,
+            "kernel": kernels.get(wl, matvec_kernel_name(kernel, k, m, specs)),
+            "nodes_per_step": nodes_per_step, "empty_graph_us": empty_us}
+
+
+def graph_launch_summary(r: dict) -> dict:
+    """What launching the graph costs inside the timed bracket: an empty graph
+    of as many kernel nodes, timed with the same events."""
+    timed_us = r["kern_us"] * r["steps"]
+    return {"kernel_nodes": round(r["nodes_per_step"] * r["steps"]),
+            "empty_graph_us": round(r["empty_graph_us"], 2),
+            "timed_bracket_us": round(timed_us, 2),
+            "share": round(r["empty_graph_us"] / timed_us, 4)}
+
+
+def matvec_summary(r: dict) -> dict:
+    """A matvec configuration's object of the JSON line (HIP-event timing)."""
+    o = {"workload": r["desc"], "M": r["m"], "steps": r["steps"], "weight_copies_rotated": r["copies"],
+         "algorithmic_bytes_per_step": r["step_bytes"], "kernel": r["kernel"],
+         "us_per_step": round(r["kern_us"], 3), "us_per_step_wall": round(r["ms_per_step"] * 1e3, 3),
+         "us_per_step_mall_hot": round(r["hot_us"], 3),
+         "GB/s": round(r["achieved"], 2), "frac": round(r["achieved"] / HBM_PEAK_GBPS, 4),
+         "graph_launch": graph_launch_summary(r)}
+    if r["wl"] in BUDGET_US:
+        o["budget_us"] = BUDGET_US[r["wl"]]
+    return o
 
 
 if __name__ == "__main__":

@@ -2047,6 +2047,24 @@ int32_t hp_hip_profile(int32_t enable) {
   return HP_OK;
 }
 
+namespace {
+__global__ void empty_kernel() {}
+}  // namespace
+
+int32_t hp_hip_empty_launches(size_t count, void *stream) {
+  State &s = st();
+  std::lock_guard<std::recursive_mutex> lock(s.mu);
+  int32_t rc = ensure_init(s.ready ? s.device : 0);
+  if (rc != HP_OK) return rc;
+  if (count < 1 || count > 65536) return fail(HP_ERR_ARG, "count must be 1..65536");
+  hipStream_t strm = stream ? static_cast<hipStream_t>(stream) : s.stream;
+  for (size_t i = 0; i < count; i++) {
+    hipLaunchKernelGGL(empty_kernel, dim3(1), dim3(64), 0, strm);
+    HP_HIP_TRY(hipGetLastError());
+  }
+  return HP_OK;
+}
+
 int32_t hp_hip_profile_read(int32_t kernel, double *total_ms, uint64_t *launches) {
   State &s = st();
   std::lock_guard<std::recursive_mutex> lock(s.mu);

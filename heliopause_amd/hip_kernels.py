@@ -146,6 +146,8 @@ def _declare_decode(L: ctypes.CDLL) -> None:
     L.hp_hip_decode_fused_status.argtypes = [vp]
     L.hp_hip_set_fused_trace.argtypes = [vp, _sz]
     L.hp_hip_set_fused_trace.restype = i32
+    L.hp_hip_empty_launches.argtypes = [_sz, vp]
+    L.hp_hip_empty_launches.restype = i32
     for name in ("hp_hip_rms_norm_device", "hp_hip_residual_norm_device", "hp_hip_attention_prep_device",
                  "hp_hip_gqa_attention_device", "hp_hip_decode_layers_device", "hp_hip_set_decode_fused",
                  "hp_hip_set_fused_wait_limit", "hp_hip_decode_fused_status"):
@@ -508,6 +510,12 @@ def setFusedTrace(d_stamps: int, length: int) -> None:
     """Stage timeline of the persistent decode step into a device buffer of
     uint64 stamps (0 turns it off); layout in include/hp_hip.h."""
     assertHipOk(lib().hp_hip_set_fused_trace(d_stamps or None, int(length)), "setFusedTrace")
+
+
+def emptyLaunches(count: int, stream: int = 0) -> None:
+    """count launches of an empty kernel on stream: the floor of a launch or
+    graph node (a measurement hook; no counterpart in the reference)."""
+    assertHipOk(lib().hp_hip_empty_launches(int(count), stream or None), "emptyLaunches")
 
 
 def profile(enable: bool) -> None:

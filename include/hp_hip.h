@@ -283,6 +283,10 @@ int32_t hp_hip_synchronize(void);
  * device milliseconds and launch count of one kernel id since enabling. */
 int32_t hp_hip_profile(int32_t enable);
 int32_t hp_hip_profile_read(int32_t kernel, double *total_ms, uint64_t *launches);
+/* `count` launches of an empty kernel (one workgroup of 64 lanes) on
+ * `stream` (NULL = library stream), 1..65536: the floor of a launch or a
+ * graph node, for measurements.  No counterpart in the reference. */
+int32_t hp_hip_empty_launches(size_t count, void *stream);
 
 /* ---- Decoder layer for one decode token -------------------------------
  * The non-projection steps of forwardAttentionLayer / forwardFfn
