@@ -83,19 +83,28 @@ def _synth_lib():
     return _SYNTH or None
 
 
-def splitmix64(seed: int, n: int, start: int = 0) -> np.ndarray:
-    """Draws ``start .. start+n-1`` of the SplitMix64 stream ``seed``."""
+def splitmix64_numpy(seed: int, n: int, start: int = 0) -> np.ndarray:
+    """The stream's definition: draw i (counted from ``start``) is
+    mix(seed + ((start + i + 1) mod 2^64) * GOLDEN), all mod 2^64."""
+    with np.errstate(over="ignore"):
+        i = np.arange(n, dtype=np.uint64) + np.uint64((start + 1) & MASK64)
+        z = np.uint64(seed & MASK64) + i * GOLDEN
+        return _mix(z)
+
+
+def splitmix64(seed: int, n: int, start: int = 0, threads: int | None = None) -> np.ndarray:
+    """Draws ``start .. start+n-1`` of the SplitMix64 stream ``seed`` (the C
+    form for large draws when libhp_synth.so is built; the numpy form when
+    it is not, or when the C call reports an error)."""
     L = _synth_lib() if n >= 4096 else None
     if L is not None:
         import os
 
         out = np.empty(n, dtype=np.uint64)
-        L.hp_synth_splitmix64(seed & MASK64, start, n, out.ctypes.data, min(16, os.cpu_count() or 1))
-        return out
-    with np.errstate(over="ignore"):
-        i = np.arange(start + 1, start + n + 1, dtype=np.uint64)
-        z = np.uint64(seed & MASK64) + i * GOLDEN
-        return _mix(z)
+        t = threads if threads is not None else min(16, os.cpu_count() or 1)
+        if L.hp_synth_splitmix64(seed & MASK64, start & MASK64, n, out.ctypes.data, t) == 0:
+            return out
+    return splitmix64_numpy(seed, n, start)
 
 
 def random_bytes(seed: int, nbytes: int) -> np.ndarray:
