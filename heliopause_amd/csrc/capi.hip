@@ -121,6 +121,9 @@ struct State {
   uint64_t *fused_trace = nullptr;  // stage timeline buffer (hp_hip_set_fused_trace), or null
   size_t fused_trace_len = 0;
   std::map<std::vector<uint8_t>, void *> fused_tables;
+  // device buffers of hp_hip_device_alloc: base address -> bytes (copies are
+  // checked against them), freed by hp_hip_device_free or hp_hip_shutdown
+  std::map<uintptr_t, size_t> dev_bufs;
 };
 
 State &st() {
@@ -1474,6 +1477,8 @@ int32_t hp_hip_shutdown(void) {
   s.pool.release_all();
   for (auto &kv : s.fused_tables) (void)hipFree(kv.second);
   s.fused_tables.clear();
+  for (auto &kv : s.dev_bufs) (void)hipFree(reinterpret_cast<void *>(kv.first));
+  s.dev_bufs.clear();
   prof_collect();
   for (hipEvent_t e : s.event_pool) (void)hipEventDestroy(e);
   s.event_pool.clear();
@@ -1833,6 +1838,62 @@ int32_t hp_hip_sample_device(const uint32_t *d_ids, const float *d_values, size_
   return HP_OK;
 }
 
+namespace {
+// The head over a device input already ordered on s.stream, top-k of each
+// column and, with `sampling`, the sampled token: candidates, tokens,
+// probabilities and the advanced generator state copied back; returns once
+// they are on the host.
+int32_t head_candidates(Handle *h, const float *d_input, size_t input_size, size_t column_count, size_t k,
+                        double softcap, const hp_hip_sampling_t *sampling, uint32_t *rng_state, int32_t *tokens,
+                        uint32_t *ids, float *values, double *probabilities, int32_t *kept) {
+  State &s = st();
+  int32_t rc = grow((void **)&s.io_out[0], &s.io_out_cap[0], column_count * h->row_count * sizeof(float));
+  uint32_t *d_ids = nullptr;
+  float *d_vals = nullptr;
+  if (rc == HP_OK) rc = topk_outputs(column_count, k, &d_ids, &d_vals);
+  // rng state (16 B slot), tokens, kept, probabilities
+  const size_t probs_off = (16 + column_count * 8 + 15) & ~(size_t)15;
+  if (rc == HP_OK && sampling) rc = grow(&s.sample_out, &s.sample_out_cap, probs_off + column_count * k * sizeof(double));
+  if (rc != HP_OK) return rc;
+  float *logits = s.io_out[0];
+  rc = run_matvec(1, &h, d_input, input_size, column_count, &logits, s.stream);
+  if (rc != HP_OK) return rc;
+  rc = run_topk(logits, column_count, h->row_count, k, softcap, d_ids, d_vals, s.stream);
+  if (rc != HP_OK) return rc;
+  if (sampling) {
+    uint8_t *base = static_cast<uint8_t *>(s.sample_out);
+    uint32_t *d_rng = reinterpret_cast<uint32_t *>(base);
+    int32_t *d_tokens = reinterpret_cast<int32_t *>(base + 16);
+    int32_t *d_kept = d_tokens + column_count;
+    double *d_probs = reinterpret_cast<double *>(base + probs_off);
+    HP_HIP_TRY(hipMemcpyAsync(d_rng, rng_state, 4, hipMemcpyHostToDevice, s.stream));
+    const size_t count = h->row_count < k ? h->row_count : k;
+    HP_HIP_TRY(launch_sample(d_ids, d_vals, (int)column_count, (int)k, (int)count, sample_params(sampling), d_rng,
+                             d_tokens, d_probs, d_kept, s.stream));
+    s.launches++;
+    HP_HIP_TRY(hipMemcpyAsync(tokens, d_tokens, column_count * 4, hipMemcpyDeviceToHost, s.stream));
+    HP_HIP_TRY(hipMemcpyAsync(kept, d_kept, column_count * 4, hipMemcpyDeviceToHost, s.stream));
+    HP_HIP_TRY(hipMemcpyAsync(probabilities, d_probs, column_count * k * 8, hipMemcpyDeviceToHost, s.stream));
+    HP_HIP_TRY(hipMemcpyAsync(rng_state, d_rng, 4, hipMemcpyDeviceToHost, s.stream));
+  }
+  HP_HIP_TRY(hipMemcpyAsync(ids, d_ids, column_count * k * 4, hipMemcpyDeviceToHost, s.stream));
+  HP_HIP_TRY(hipMemcpyAsync(values, d_vals, column_count * k * 4, hipMemcpyDeviceToHost, s.stream));
+  HP_HIP_TRY(hipStreamSynchronize(s.stream));
+  return HP_OK;
+}
+
+// The allocation [base, base + bytes) of hp_hip_device_alloc that holds
+// [p, p + n), or false.
+bool in_device_buffer(const void *p, size_t n) {
+  const State &s = st();
+  const uintptr_t a = reinterpret_cast<uintptr_t>(p);
+  auto it = s.dev_bufs.upper_bound(a);
+  if (it == s.dev_bufs.begin()) return false;
+  --it;
+  return a >= it->first && n <= it->second && a - it->first <= it->second - n;
+}
+}  // namespace
+
 int32_t hp_hip_matmul_topk_sample(uint64_t handle, const float *input, size_t input_len, size_t input_size,
                                   size_t column_count, size_t k, double softcap, const hp_hip_sampling_t *sampling,
                                   uint32_t *rng_state, int32_t *tokens, uint32_t *ids, float *values,
@@ -1853,37 +1914,98 @@ int32_t hp_hip_matmul_topk_sample(uint64_t handle, const float *input, size_t in
   if (!input || !rng_state || !tokens || !ids || !values || !probabilities || !kept)
     return fail(HP_ERR_ARG, "null pointer");
   rc = grow((void **)&s.io_in, &s.io_in_cap, input_len * sizeof(float));
-  if (rc == HP_OK) rc = grow((void **)&s.io_out[0], &s.io_out_cap[0], column_count * h->row_count * sizeof(float));
-  uint32_t *d_ids = nullptr;
-  float *d_vals = nullptr;
-  if (rc == HP_OK) rc = topk_outputs(column_count, k, &d_ids, &d_vals);
-  // rng state (16 B slot), tokens, kept, probabilities
-  const size_t probs_off = (16 + column_count * 8 + 15) & ~(size_t)15;
-  if (rc == HP_OK) rc = grow(&s.sample_out, &s.sample_out_cap, probs_off + column_count * k * sizeof(double));
   if (rc != HP_OK) return rc;
-  uint8_t *base = static_cast<uint8_t *>(s.sample_out);
-  uint32_t *d_rng = reinterpret_cast<uint32_t *>(base);
-  int32_t *d_tokens = reinterpret_cast<int32_t *>(base + 16);
-  int32_t *d_kept = d_tokens + column_count;
-  double *d_probs = reinterpret_cast<double *>(base + probs_off);
   HP_HIP_TRY(hipMemcpyAsync(s.io_in, input, input_len * sizeof(float), hipMemcpyHostToDevice, s.stream));
-  HP_HIP_TRY(hipMemcpyAsync(d_rng, rng_state, 4, hipMemcpyHostToDevice, s.stream));
-  float *logits = s.io_out[0];
-  rc = run_matvec(1, &h, s.io_in, input_size, column_count, &logits, s.stream);
+  return head_candidates(h, s.io_in, input_size, column_count, k, softcap, sampling, rng_state, tokens, ids, values,
+                         probabilities, kept);
+}
+
+int32_t hp_hip_matmul_topk_sample_device(uint64_t handle, const float *d_input, size_t input_len, size_t input_size,
+                                         size_t column_count, size_t k, double softcap,
+                                         const hp_hip_sampling_t *sampling, uint32_t *rng_state, int32_t *tokens,
+                                         uint32_t *ids, float *values, double *probabilities, int32_t *kept,
+                                         size_t out_len) {
+  State &s = st();
+  std::lock_guard<std::recursive_mutex> lock(s.mu);
+  int32_t rc = ensure_init(s.ready ? s.device : 0);
   if (rc != HP_OK) return rc;
-  rc = run_topk(logits, column_count, h->row_count, k, softcap, d_ids, d_vals, s.stream);
+  Handle *h = lookup(handle);
+  if (!h) return fail(HP_ERR_HANDLE, "unknown weight handle");
+  if (h->input_size != input_size || input_len != sat_mul(input_size, column_count))
+    return fail(HP_ERR_SHAPE, "matmul shape mismatch");
+  rc = topk_check(column_count, h->row_count, k);
   if (rc != HP_OK) return rc;
-  const size_t count = h->row_count < k ? h->row_count : k;
-  HP_HIP_TRY(launch_sample(d_ids, d_vals, (int)column_count, (int)k, (int)count, sample_params(sampling), d_rng,
-                           d_tokens, d_probs, d_kept, s.stream));
-  s.launches++;
-  HP_HIP_TRY(hipMemcpyAsync(ids, d_ids, column_count * k * 4, hipMemcpyDeviceToHost, s.stream));
-  HP_HIP_TRY(hipMemcpyAsync(values, d_vals, column_count * k * 4, hipMemcpyDeviceToHost, s.stream));
-  HP_HIP_TRY(hipMemcpyAsync(tokens, d_tokens, column_count * 4, hipMemcpyDeviceToHost, s.stream));
-  HP_HIP_TRY(hipMemcpyAsync(kept, d_kept, column_count * 4, hipMemcpyDeviceToHost, s.stream));
-  HP_HIP_TRY(hipMemcpyAsync(probabilities, d_probs, column_count * k * 8, hipMemcpyDeviceToHost, s.stream));
-  HP_HIP_TRY(hipMemcpyAsync(rng_state, d_rng, 4, hipMemcpyDeviceToHost, s.stream));
-  HP_HIP_TRY(hipStreamSynchronize(s.stream));
+  if (sampling) {
+    rc = sampling_check(sampling, k);
+    if (rc != HP_OK) return rc;
+  }
+  if (out_len != sat_mul(column_count, k)) return fail(HP_ERR_SHAPE, "topk output length mismatch");
+  if (column_count == 0) return HP_OK;
+  if (!d_input || !ids || !values) return fail(HP_ERR_ARG, "null pointer");
+  if (sampling && (!rng_state || !tokens || !probabilities || !kept)) return fail(HP_ERR_ARG, "null pointer");
+  if (reinterpret_cast<uintptr_t>(d_input) % 16 != 0) return fail(HP_ERR_ARG, "input must be 16-byte aligned");
+  return head_candidates(h, d_input, input_size, column_count, k, softcap, sampling, rng_state, tokens, ids, values,
+                         probabilities, kept);
+}
+
+int32_t hp_hip_device_alloc(size_t bytes, void **d_out) {
+  State &s = st();
+  std::lock_guard<std::recursive_mutex> lock(s.mu);
+  if (!d_out) return fail(HP_ERR_ARG, "null pointer");
+  *d_out = nullptr;
+  int32_t rc = ensure_init(s.ready ? s.device : 0);
+  if (rc != HP_OK) return rc;
+  if (bytes == 0) return fail(HP_ERR_ARG, "zero-byte buffer");
+  hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+  HP_HIP_TRY(hipStreamIsCapturing(s.stream, &cs));
+  if (cs != hipStreamCaptureStatusNone) return fail(HP_ERR_ARG, "no allocation while the library stream captures");
+  void *p = nullptr;
+  if (hipMalloc(&p, bytes) != hipSuccess) {
+    (void)hipGetLastError();
+    return fail(HP_ERR_OOM, "device allocation failed");
+  }
+  if (hipMemsetAsync(p, 0, bytes, s.stream) != hipSuccess || hipStreamSynchronize(s.stream) != hipSuccess) {
+    (void)hipFree(p);
+    return fail(HP_ERR_HIP, "device allocation could not be cleared");
+  }
+  s.dev_bufs[reinterpret_cast<uintptr_t>(p)] = bytes;
+  *d_out = p;
+  return HP_OK;
+}
+
+int32_t hp_hip_device_free(void *d) {
+  State &s = st();
+  std::lock_guard<std::recursive_mutex> lock(s.mu);
+  if (!d) return HP_OK;
+  auto it = s.dev_bufs.find(reinterpret_cast<uintptr_t>(d));
+  if (it == s.dev_bufs.end()) return fail(HP_ERR_ARG, "not a buffer of hp_hip_device_alloc");
+  HP_HIP_TRY(hipStreamSynchronize(s.stream));  // work queued on the buffer has finished
+  HP_HIP_TRY(hipFree(d));
+  s.dev_bufs.erase(it);
+  return HP_OK;
+}
+
+int32_t hp_hip_copy_to_device(void *d_dst, const void *src, size_t bytes, void *stream) {
+  State &s = st();
+  std::lock_guard<std::recursive_mutex> lock(s.mu);
+  if (bytes == 0) return HP_OK;
+  if (!d_dst || !src) return fail(HP_ERR_ARG, "null pointer");
+  if (!in_device_buffer(d_dst, bytes)) return fail(HP_ERR_ARG, "destination outside the buffers of hp_hip_device_alloc");
+  hipStream_t strm = stream ? static_cast<hipStream_t>(stream) : s.stream;
+  HP_HIP_TRY(hipMemcpyAsync(d_dst, src, bytes, hipMemcpyHostToDevice, strm));
+  HP_HIP_TRY(hipStreamSynchronize(strm));
+  return HP_OK;
+}
+
+int32_t hp_hip_copy_to_host(void *dst, const void *d_src, size_t bytes, void *stream) {
+  State &s = st();
+  std::lock_guard<std::recursive_mutex> lock(s.mu);
+  if (bytes == 0) return HP_OK;
+  if (!dst || !d_src) return fail(HP_ERR_ARG, "null pointer");
+  if (!in_device_buffer(d_src, bytes)) return fail(HP_ERR_ARG, "source outside the buffers of hp_hip_device_alloc");
+  hipStream_t strm = stream ? static_cast<hipStream_t>(stream) : s.stream;
+  HP_HIP_TRY(hipMemcpyAsync(dst, d_src, bytes, hipMemcpyDeviceToHost, strm));
+  HP_HIP_TRY(hipStreamSynchronize(strm));
   return HP_OK;
 }
 

@@ -310,6 +310,76 @@ async function matMulQuantizedHipResidentTopKSample(handle, inputColumns, inputS
   return columns;
 }
 
+/* Device buffers and the device-resident decode calls behind the segment
+ * runner (hip/segment-runner.js): BigInt device addresses of
+ * hp_hip_device_alloc, copies that return once the bytes have arrived, and
+ * the layer / head calls on device rows (hp_hip.h). */
+function deviceAlloc(bytes) {
+  const result = native().deviceAlloc(bytes);
+  assertHipOk(result.status, "deviceAlloc");
+  return result.ptr;
+}
+
+function deviceFree(ptr) {
+  if (addon && ptr) {
+    assertHipOk(addon.deviceFree(ptr), "deviceFree");
+  }
+}
+
+function copyToDevice(ptr, array, byteOffset) {
+  assertHipOk(native().copyToDevice(ptr, array, byteOffset || 0), "copyToDevice");
+}
+
+function copyToHost(ptr, array, byteOffset) {
+  assertHipOk(native().copyToHost(ptr, array, byteOffset || 0), "copyToHost");
+}
+
+/* hp_hip_decode_layers_device over `layers` (runLayers objects) for
+ * tokenCount tokens at `position` ..: `input` rows (or null: already in
+ * buffers.hidden), then rows [rowStart, rowStart + rowCount) of the residual
+ * stream (readOutput false) or of the output norm read back. */
+async function runDecodeLayers(layers, tokenCount, hiddenSize, buffers, input, position, readOutput, rowStart,
+  rowCount) {
+  const result = await native().runLayers(layers, tokenCount, hiddenSize, buffers, input, position, readOutput,
+    rowStart, rowCount);
+  assertHipOk(result.status, "decodeLayers", result.error);
+  return result.output;
+}
+
+/* forwardOutput's head + topK (+ sampleNextToken with `sampling` and a
+ * createHipSamplingState `state`) on device rows: [{id, value}] per column,
+ * or with sampling [{token, distribution}] as matMulQuantizedHipResidentTopKSample. */
+async function headTopKDevice(handle, dInput, inputSize, columnCount, topK, softcap, sampling, state) {
+  if (handle.released) {
+    throw new Error(`Resident quantized matmul instance ${handle.handle} is not available`);
+  }
+  if (handle.inputSize !== inputSize) {
+    throw new Error(`Resident quantized matmul input shape mismatch: ${inputSize}`);
+  }
+  const k = sampling ? sampling.logitsTopK : topK;
+  const result = await native().headTopK(handle.handle, dInput, inputSize, columnCount, k,
+    softcap === undefined ? 0 : softcap, sampling || null, sampling ? state : null);
+  assertHipOk(result.status, "headTopK", result.error);
+  const columns = [];
+  for (let column = 0; column < columnCount; column += 1) {
+    if (sampling) {
+      const distribution = [];
+      for (let index = 0; index < result.kept[column]; index += 1) {
+        const at = column * k + index;
+        distribution.push({ id: result.ids[at], value: result.values[at], probability: result.probabilities[at] });
+      }
+      columns.push({ token: result.tokens[column], distribution });
+    } else {
+      const candidates = [];
+      for (let index = 0; index < Math.min(handle.rowCount, k); index += 1) {
+        candidates.push({ id: result.ids[column * k + index], value: result.values[column * k + index] });
+      }
+      columns.push(candidates);
+    }
+  }
+  return columns;
+}
+
 /* A GGUF file parsed by the runner's reader and held open for uploads.
  * `metadata` has parseGguf's shape (GgufMetadata, gguf.ts:30-37), with each
  * tensor's byteLength (tensorByteLength) when its storage type is known. */
@@ -439,6 +509,12 @@ class HipGgufWeights {
 
 module.exports = {
   DEFAULT_SAMPLING_SEED,
+  copyToDevice,
+  copyToHost,
+  deviceAlloc,
+  deviceFree,
+  headTopKDevice,
+  runDecodeLayers,
   createHipSamplingState,
   matMulQuantizedHipResidentTopKSample,
   resolveGenerationSamplingOptions,

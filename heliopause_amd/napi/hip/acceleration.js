@@ -65,7 +65,7 @@ function hipProjectionBatchingEnabled(session) {
 function ensureHipWeightCache(session) {
   let cache = hipWeightCaches.get(session);
   if (!cache) {
-    cache = { handles: new Map(), pending: new Map(), declined: new Set(), bytes: 0, hits: 0, misses: 0 };
+    cache = { handles: new Map(), pending: new Map(), declined: new Set(), bytes: 0, hits: 0, misses: 0, generation: 0 };
     hipWeightCaches.set(session, cache);
   }
   return cache;
@@ -90,6 +90,7 @@ function hipExecutionProviderStats(session) {
 function shutdownHipExecutionProvider(session) {
   const cache = hipWeightCaches.get(session);
   if (cache) {
+    cache.generation += 1; // uploads still in flight release their handle on arrival
     for (const handle of cache.handles.values()) {
       kernels.releaseHipQuantizedWeightHandle(handle);
     }
@@ -123,13 +124,23 @@ async function readHipWeightHandle(session, name, type, inputSize, rowCount) {
     return pending;
   }
   cache.misses += 1;
+  const generation = cache.generation;
   const pendingRead = (async () => {
     if (!kernels.quantizedTypeId(type) || !(await hipSupport()).available) {
-      cache.declined.add(name);
+      if (cache.generation === generation) {
+        cache.declined.add(name);
+      }
       return undefined;
     }
     const bytes = await session.tensorReader.readTensorBytes(name);
     const handle = await kernels.createHipQuantizedWeightHandle(type, bytes, inputSize, rowCount);
+    if (cache.generation !== generation) {
+      // shutdownHipExecutionProvider ran while this upload was pending
+      if (handle) {
+        kernels.releaseHipQuantizedWeightHandle(handle);
+      }
+      return undefined;
+    }
     if (!handle) {
       cache.declined.add(name);
       return undefined;
@@ -142,7 +153,9 @@ async function readHipWeightHandle(session, name, type, inputSize, rowCount) {
   try {
     return await pendingRead;
   } finally {
-    cache.pending.delete(name);
+    if (cache.pending.get(name) === pendingRead) {
+      cache.pending.delete(name);
+    }
   }
 }
 

@@ -20,6 +20,7 @@
 
 const acceleration = require("./acceleration.js");
 const layers = require("./layers.js");
+const segmentRunner = require("./segment-runner.js");
 
 /* HBM of one MI355X: the whole model fits, so placement is full-model. */
 const DEFAULT_HBM_BYTES = 288 * 1024 * 1024 * 1024;
@@ -31,13 +32,20 @@ function requireEngine(engine, member) {
   return engine[member];
 }
 
-/* The engine's model runner with provider "hip": its segment runners are the
- * engine's, relabelled, and their projections go to hip/layers.js. */
+/* The engine's model runner with provider "hip".  A segment whose layers the
+ * device path covers runs on HipSegmentRunner (hip/segment-runner.js: the
+ * whole segment in HBM, one call per run); any other segment runs on the
+ * engine's WASM segment runner, relabelled, whose projections go to
+ * hip/layers.js. */
 function createHipModelRunner(engine) {
   const base = requireEngine(engine, "createWasmModelRunner")();
   return Object.assign({}, base, {
     provider: "hip",
     segmentRunner: async (options) => {
+      const device = await segmentRunner.createHipSegmentRunner(options);
+      if (device) {
+        return device;
+      }
       const runner = await base.segmentRunner(options);
       return {
         provider: "hip",
@@ -74,4 +82,5 @@ function createHipProvider(options, engine) {
   };
 }
 
-module.exports = Object.assign({ DEFAULT_HBM_BYTES, createHipModelRunner, createHipProvider }, acceleration, layers);
+module.exports = Object.assign({ DEFAULT_HBM_BYTES, createHipModelRunner, createHipProvider }, acceleration, layers,
+  segmentRunner);

@@ -26,6 +26,13 @@
  *   ggufInfo(file) -> parseGguf's GgufMetadata (gguf.ts:30-37) + byteLength per tensor
  *   ggufUpload(file, tensorIndices[]) -> Promise<{status, error, handles[], statuses[]}>
  *   ggufClose(file)
+ * device-resident decode (napi/hip/segment-runner.js):
+ *   deviceAlloc(bytes) -> {status, ptr}, deviceFree(ptr) -> status
+ *   copyToDevice(ptr, typedArray, byteOffset) / copyToHost(ptr, typedArray, byteOffset) -> status
+ *   runLayers(layers[], tokenCount, hiddenSize, {hidden, position, outputNorm, output}, Float32Array | null,
+ *             position, readOutput, rowStart, rowCount) -> Promise<{status, error, output}>
+ *   headTopK(handle, dInput, inputSize, columnCount, k, softcap, sampling | null, Uint32Array | null)
+ *       -> Promise<{status, error, ids, values[, tokens, probabilities, kept]}>
  */
 #define NAPI_VERSION 8
 #include <node_api.h>
@@ -835,6 +842,376 @@ static napi_value js_gguf_close(napi_env env, napi_callback_info info) {
   return make_i32(env, 0);
 }
 
+/* ---- device-resident decode (the segment runner) ------------------------
+ * Buffers cross into JS as BigInt device addresses of hp_hip_device_alloc. */
+
+static napi_value js_device_alloc(napi_env env, napi_callback_info info) {
+  size_t argc = 1;
+  napi_value argv[1];
+  CHECK(env, napi_get_cb_info(env, info, &argc, argv, NULL, NULL));
+  size_t bytes;
+  if (argc < 1 || !get_size(env, argv[0], &bytes)) {
+    napi_throw_type_error(env, NULL, "deviceAlloc(bytes)");
+    return NULL;
+  }
+  void *d = NULL;
+  const int32_t rc = hp_hip_device_alloc(bytes, &d);
+  napi_value r, ptr;
+  napi_create_object(env, &r);
+  set(env, r, "status", make_i32(env, rc));
+  napi_create_bigint_uint64(env, (uint64_t)(uintptr_t)d, &ptr);
+  set(env, r, "ptr", ptr);
+  return r;
+}
+
+static napi_value js_device_free(napi_env env, napi_callback_info info) {
+  size_t argc = 1;
+  napi_value argv[1];
+  CHECK(env, napi_get_cb_info(env, info, &argc, argv, NULL, NULL));
+  uint64_t p;
+  if (argc < 1 || !get_u64(env, argv[0], &p)) {
+    napi_throw_type_error(env, NULL, "deviceFree(ptr)");
+    return NULL;
+  }
+  return make_i32(env, hp_hip_device_free((void *)(uintptr_t)p));
+}
+
+/* any typed array: its bytes */
+static int get_bytes(napi_env env, napi_value v, void **data, size_t *bytes) {
+  bool is = false;
+  if (napi_is_typedarray(env, v, &is) != napi_ok || !is) return 0;
+  napi_typedarray_type t;
+  napi_value ab;
+  size_t off, len;
+  if (napi_get_typedarray_info(env, v, &t, &len, data, &ab, &off) != napi_ok) return 0;
+  static const size_t elem[] = {1, 1, 1, 2, 2, 4, 4, 4, 8, 8, 8};
+  if ((size_t)t >= sizeof elem / sizeof elem[0]) return 0;
+  *bytes = len * elem[t];
+  return 1;
+}
+
+/* copyToDevice(ptr, typedArray, byteOffset = 0) / copyToHost(ptr, typedArray, byteOffset = 0) */
+static napi_value device_copy(napi_env env, napi_callback_info info, int to_device) {
+  size_t argc = 3;
+  napi_value argv[3];
+  CHECK(env, napi_get_cb_info(env, info, &argc, argv, NULL, NULL));
+  uint64_t p;
+  void *data;
+  size_t bytes, off = 0;
+  if (argc < 2 || !get_u64(env, argv[0], &p) || !get_bytes(env, argv[1], &data, &bytes) ||
+      (argc > 2 && !get_size(env, argv[2], &off))) {
+    napi_throw_type_error(env, NULL, to_device ? "copyToDevice(ptr, typedArray, byteOffset)"
+                                               : "copyToHost(ptr, typedArray, byteOffset)");
+    return NULL;
+  }
+  void *d = (void *)(uintptr_t)(p + off);
+  return make_i32(env, to_device ? hp_hip_copy_to_device(d, data, bytes, NULL) : hp_hip_copy_to_host(data, d, bytes, NULL));
+}
+
+static napi_value js_copy_to_device(napi_env env, napi_callback_info info) { return device_copy(env, info, 1); }
+static napi_value js_copy_to_host(napi_env env, napi_callback_info info) { return device_copy(env, info, 0); }
+
+static int get_prop(napi_env env, napi_value obj, const char *name, napi_value *out) {
+  bool has = false;
+  if (napi_has_named_property(env, obj, name, &has) != napi_ok || !has) return 0;
+  return napi_get_named_property(env, obj, name, out) == napi_ok;
+}
+
+static int get_prop_u64(napi_env env, napi_value obj, const char *name, uint64_t *out) {
+  napi_value v;
+  if (!get_prop(env, obj, name, &v)) return 0;
+  return get_u64(env, v, out);
+}
+
+static int get_prop_ptr(napi_env env, napi_value obj, const char *name, void **out) {
+  uint64_t u = 0;
+  if (!get_prop_u64(env, obj, name, &u)) return 0;
+  *out = (void *)(uintptr_t)u;
+  return 1;
+}
+
+/* one layer object of runLayers -> hp_hip_decode_layer_t */
+static int get_layer(napi_env env, napi_value o, hp_hip_decode_layer_t *L) {
+  memset(L, 0, sizeof *L);
+  napi_value a;
+  double d;
+  void *p;
+  if (!get_prop_u64(env, o, "attnQ", &L->attn_q) || !get_prop_u64(env, o, "attnK", &L->attn_k) ||
+      !get_prop_u64(env, o, "attnV", &L->attn_v) || !get_prop_u64(env, o, "attnOutput", &L->attn_output) ||
+      !get_prop_u64(env, o, "ffnGate", &L->ffn_gate) || !get_prop_u64(env, o, "ffnUp", &L->ffn_up) ||
+      !get_prop_u64(env, o, "ffnDown", &L->ffn_down))
+    return 0;
+  if (!get_prop_ptr(env, o, "attnNorm", &p)) return 0;
+  L->d_attn_norm = (const float *)p;
+  if (!get_prop_ptr(env, o, "attnQNorm", &p)) return 0;
+  L->d_attn_q_norm = (const float *)p;
+  if (!get_prop_ptr(env, o, "attnKNorm", &p)) return 0;
+  L->d_attn_k_norm = (const float *)p;
+  if (!get_prop_ptr(env, o, "postAttentionNorm", &p)) return 0;
+  L->d_post_attention_norm = (const float *)p;
+  if (!get_prop_ptr(env, o, "ffnNorm", &p)) return 0;
+  L->d_ffn_norm = (const float *)p;
+  if (!get_prop_ptr(env, o, "postFfwNorm", &p)) return 0;
+  L->d_post_ffw_norm = (const float *)p;
+  if (!get_prop_ptr(env, o, "keyCache", &p)) return 0;
+  L->d_key_cache = (uint16_t *)p;
+  if (!get_prop_ptr(env, o, "valueCache", &p)) return 0;
+  L->d_value_cache = (uint16_t *)p;
+  if (!get_prop_f64(env, o, "layerOutputScale", &d)) return 0;
+  L->layer_output_scale = (float)d;
+  if (!get_prop(env, o, "attention", &a)) return 0;
+  hp_hip_attention_config_t *c = &L->attention;
+  if (!get_prop_f64(env, a, "headCount", &d)) return 0;
+  c->head_count = (int32_t)d;
+  if (!get_prop_f64(env, a, "headCountKv", &d)) return 0;
+  c->head_count_kv = (int32_t)d;
+  if (!get_prop_f64(env, a, "headDim", &d)) return 0;
+  c->head_dim = (int32_t)d;
+  if (!get_prop_f64(env, a, "ropeDims", &d)) return 0;
+  c->rope_dims = (int32_t)d;
+  if (!get_prop_f64(env, a, "ropeFreqBase", &c->rope_freq_base)) return 0;
+  if (!get_prop_ptr(env, a, "ropeFreqFactors", &p)) return 0;
+  c->d_rope_freq_factors = (const float *)p;
+  if (!get_prop_f64(env, a, "capacity", &d)) return 0;
+  c->capacity = (int32_t)d;
+  if (!get_prop_f64(env, a, "slidingWindow", &d)) return 0;
+  c->sliding_window = (int32_t)d;
+  if (!get_prop_f64(env, a, "epsilon", &c->epsilon)) return 0;
+  return 1;
+}
+
+enum { DJOB_LAYERS, DJOB_HEAD };
+
+typedef struct {
+  napi_async_work work;
+  napi_deferred deferred;
+  napi_ref input_ref, rng_ref;
+  int kind;
+  /* layers */
+  hp_hip_decode_layer_t *layers;
+  size_t n_layers, tokens, hidden_n;
+  void *d_hidden, *d_position, *d_output_norm, *d_output, *d_read;
+  const float *input; /* NULL: the rows are already in d_hidden */
+  size_t input_len;
+  int32_t position;
+  size_t row_start, row_count;
+  float *out;
+  /* head */
+  uint64_t handle;
+  size_t input_size, columns, k;
+  double softcap;
+  int sample;
+  hp_hip_sampling_t sampling;
+  uint32_t rng, *rng_out;
+  uint32_t *ids;
+  float *values;
+  double *probs;
+  int32_t *tokens_out, *kept;
+  int32_t status;
+  char error[512];
+} DevJob;
+
+static void free_devjob(DevJob *j) {
+  free(j->layers);
+  free(j->out);
+  free(j->ids);
+  free(j->values);
+  free(j->probs);
+  free(j->tokens_out);
+  free(j->kept);
+  free(j);
+}
+
+static void devjob_execute(napi_env env, void *data) {
+  (void)env;
+  DevJob *j = (DevJob *)data;
+  int32_t rc = HP_OK;
+  if (j->kind == DJOB_LAYERS) {
+    if (j->input) rc = hp_hip_copy_to_device(j->d_hidden, j->input, j->input_len * sizeof(float), NULL);
+    if (rc == HP_OK) rc = hp_hip_copy_to_device(j->d_position, &j->position, sizeof(int32_t), NULL);
+    if (rc == HP_OK)
+      rc = hp_hip_decode_layers_device(j->layers, j->n_layers, j->tokens, (float *)j->d_hidden,
+                                       (const int32_t *)j->d_position, (const float *)j->d_output_norm,
+                                       (float *)j->d_output, NULL);
+    if (rc == HP_OK && j->row_count)
+      rc = hp_hip_copy_to_host(j->out, (const char *)j->d_read + j->row_start * j->hidden_n * sizeof(float),
+                               j->row_count * j->hidden_n * sizeof(float), NULL);
+  } else {
+    rc = hp_hip_matmul_topk_sample_device(j->handle, (const float *)j->d_hidden, j->input_size * j->columns,
+                                          j->input_size, j->columns, j->k, j->softcap,
+                                          j->sample ? &j->sampling : NULL, j->sample ? &j->rng : NULL,
+                                          j->tokens_out, j->ids, j->values, j->probs, j->kept, j->columns * j->k);
+  }
+  j->status = rc;
+  if (rc != HP_OK) {
+    strncpy(j->error, hp_hip_last_error(), sizeof j->error - 1);
+    j->error[sizeof j->error - 1] = 0;
+  }
+}
+
+static void devjob_complete(napi_env env, napi_status s, void *data) {
+  (void)s;
+  DevJob *j = (DevJob *)data;
+  napi_value r, err;
+  napi_create_object(env, &r);
+  set(env, r, "status", make_i32(env, j->status));
+  napi_create_string_utf8(env, j->error, NAPI_AUTO_LENGTH, &err);
+  set(env, r, "error", err);
+  if (j->kind == DJOB_LAYERS) {
+    set(env, r, "output", adopt(env, j->out, j->row_count * j->hidden_n, 4, napi_float32_array));
+    j->out = NULL;
+    if (j->input_ref) napi_delete_reference(env, j->input_ref);
+  } else {
+    const size_t n = j->columns * j->k;
+    set(env, r, "ids", adopt(env, j->ids, n, 4, napi_uint32_array));
+    set(env, r, "values", adopt(env, j->values, n, 4, napi_float32_array));
+    j->ids = NULL;
+    j->values = NULL;
+    if (j->sample) {
+      set(env, r, "probabilities", adopt(env, j->probs, n, 8, napi_float64_array));
+      set(env, r, "tokens", adopt(env, j->tokens_out, j->columns, 4, napi_int32_array));
+      set(env, r, "kept", adopt(env, j->kept, j->columns, 4, napi_int32_array));
+      j->probs = NULL;
+      j->tokens_out = NULL;
+      j->kept = NULL;
+      if (j->status == HP_OK && j->rng_out) *j->rng_out = j->rng;
+      napi_delete_reference(env, j->rng_ref);
+    }
+  }
+  napi_resolve_deferred(env, j->deferred, r);
+  napi_delete_async_work(env, j->work);
+  free_devjob(j);
+}
+
+static napi_value start_devjob(napi_env env, DevJob *j, const char *name) {
+  napi_value promise, wname;
+  napi_create_promise(env, &j->deferred, &promise);
+  napi_create_string_utf8(env, name, NAPI_AUTO_LENGTH, &wname);
+  napi_create_async_work(env, NULL, wname, devjob_execute, devjob_complete, j, &j->work);
+  napi_queue_async_work(env, j->work);
+  return promise;
+}
+
+/* runLayers(layers[], tokenCount, hiddenSize, {hidden, position, outputNorm, output}, input Float32Array | null,
+ *           position, readOutput, rowStart, rowCount) -> Promise<{status, error, output}>
+ * input rows -> hidden (unless null), *position, hp_hip_decode_layers_device over the layers, then rows
+ * [rowStart, rowStart + rowCount) of hidden (readOutput false) or of the output norm back. */
+static napi_value js_run_layers(napi_env env, napi_callback_info info) {
+  size_t argc = 9;
+  napi_value argv[9];
+  CHECK(env, napi_get_cb_info(env, info, &argc, argv, NULL, NULL));
+  DevJob *j = (DevJob *)calloc(1, sizeof(DevJob));
+  if (!j) return NULL;
+  j->kind = DJOB_LAYERS;
+  uint32_t n = 0;
+  bool is_array = false, read_output = false;
+  double pos = 0;
+  int ok = argc >= 9 && napi_is_array(env, argv[0], &is_array) == napi_ok && is_array &&
+           napi_get_array_length(env, argv[0], &n) == napi_ok && n > 0 && get_size(env, argv[1], &j->tokens) &&
+           get_size(env, argv[2], &j->hidden_n) && get_prop_ptr(env, argv[3], "hidden", &j->d_hidden) &&
+           get_prop_ptr(env, argv[3], "position", &j->d_position) &&
+           napi_get_value_double(env, argv[5], &pos) == napi_ok &&
+           napi_get_value_bool(env, argv[6], &read_output) == napi_ok && get_size(env, argv[7], &j->row_start) &&
+           get_size(env, argv[8], &j->row_count);
+  if (ok) {
+    get_prop_ptr(env, argv[3], "outputNorm", &j->d_output_norm);
+    get_prop_ptr(env, argv[3], "output", &j->d_output);
+    j->layers = (hp_hip_decode_layer_t *)calloc(n, sizeof(hp_hip_decode_layer_t));
+    ok = j->layers != NULL;
+    for (uint32_t i = 0; ok && i < n; i++) {
+      napi_value o;
+      ok = napi_get_element(env, argv[0], i, &o) == napi_ok && get_layer(env, o, &j->layers[i]);
+    }
+    j->n_layers = n;
+  }
+  if (ok) {
+    napi_valuetype t;
+    napi_typeof(env, argv[4], &t);
+    if (t != napi_null && t != napi_undefined) {
+      void *in;
+      ok = get_typed(env, argv[4], napi_float32_array, &in, &j->input_len) &&
+           j->input_len == j->tokens * j->hidden_n;
+      j->input = (const float *)in;
+    }
+  }
+  if (ok) ok = j->row_start + j->row_count <= j->tokens && (!read_output || j->d_output);
+  if (!ok) {
+    free_devjob(j);
+    napi_throw_type_error(env, NULL,
+                          "runLayers(layers[], tokenCount, hiddenSize, {hidden, position, outputNorm, output}, "
+                          "Float32Array | null, position, readOutput, rowStart, rowCount)");
+    return NULL;
+  }
+  j->position = (int32_t)pos;
+  j->d_read = read_output ? j->d_output : j->d_hidden;
+  j->out = (float *)malloc(j->row_count * j->hidden_n * sizeof(float) + 4);
+  if (!j->out) {
+    free_devjob(j);
+    napi_throw_error(env, NULL, "runLayers: out of host memory");
+    return NULL;
+  }
+  if (j->input) napi_create_reference(env, argv[4], 1, &j->input_ref);
+  return start_devjob(env, j, "hp_hip_decode_layers_device");
+}
+
+/* headTopK(handle, dInputPtr, inputSize, columnCount, k, softcap, sampling | null, Uint32Array rngState | null)
+ *   -> Promise<{status, error, ids, values[, tokens, probabilities, kept]}> */
+static napi_value js_head_topk(napi_env env, napi_callback_info info) {
+  size_t argc = 8;
+  napi_value argv[8];
+  CHECK(env, napi_get_cb_info(env, info, &argc, argv, NULL, NULL));
+  DevJob *j = (DevJob *)calloc(1, sizeof(DevJob));
+  if (!j) return NULL;
+  j->kind = DJOB_HEAD;
+  uint64_t din = 0;
+  int ok = argc >= 8 && get_u64(env, argv[0], &j->handle) && get_u64(env, argv[1], &din) &&
+           get_size(env, argv[2], &j->input_size) && get_size(env, argv[3], &j->columns) &&
+           get_size(env, argv[4], &j->k) && napi_get_value_double(env, argv[5], &j->softcap) == napi_ok;
+  j->d_hidden = (void *)(uintptr_t)din;
+  napi_valuetype t = napi_null;
+  if (ok) napi_typeof(env, argv[6], &t);
+  if (ok && t != napi_null && t != napi_undefined) {
+    double do_sample = 1, top_k = 0, temperature = 0, top_p = 0;
+    void *rng;
+    size_t rng_len = 0;
+    ok = get_prop_f64(env, argv[6], "topK", &top_k) && get_prop_f64(env, argv[6], "temperature", &temperature) &&
+         get_prop_f64(env, argv[6], "topP", &top_p) &&
+         get_typed(env, argv[7], napi_uint32_array, &rng, &rng_len) && rng_len >= 1;
+    if (ok) {
+      get_prop_f64(env, argv[6], "doSample", &do_sample);
+      j->sample = 1;
+      j->sampling.do_sample = do_sample != 0;
+      j->sampling.top_k = top_k >= 2147483647.0 ? 2147483647 : (int32_t)top_k;
+      j->sampling.temperature = temperature;
+      j->sampling.top_p = top_p;
+      j->rng_out = (uint32_t *)rng;
+      j->rng = j->rng_out[0];
+    }
+  }
+  if (!ok) {
+    free_devjob(j);
+    napi_throw_type_error(env, NULL,
+                          "headTopK(handle, dInput, inputSize, columnCount, k, softcap, sampling | null, "
+                          "Uint32Array | null)");
+    return NULL;
+  }
+  const size_t n = (j->columns * j->k) != 0 ? j->columns * j->k : 1, c = j->columns ? j->columns : 1;
+  j->ids = (uint32_t *)malloc(n * 4);
+  j->values = (float *)malloc(n * 4);
+  if (j->sample) {
+    j->probs = (double *)malloc(n * 8);
+    j->tokens_out = (int32_t *)malloc(c * 4);
+    j->kept = (int32_t *)malloc(c * 4);
+  }
+  if (!j->ids || !j->values || (j->sample && (!j->probs || !j->tokens_out || !j->kept))) {
+    free_devjob(j);
+    napi_throw_error(env, NULL, "headTopK: out of host memory");
+    return NULL;
+  }
+  if (j->sample) napi_create_reference(env, argv[7], 1, &j->rng_ref);
+  return start_devjob(env, j, "hp_hip_matmul_topk_sample_device");
+}
+
 static napi_value init_module(napi_env env, napi_value exports) {
   napi_property_descriptor d[] = {
       {"statusString", NULL, js_status_string, NULL, NULL, NULL, napi_enumerable, NULL},
@@ -855,6 +1232,12 @@ static napi_value init_module(napi_env env, napi_value exports) {
       {"ggufInfo", NULL, js_gguf_info, NULL, NULL, NULL, napi_enumerable, NULL},
       {"ggufUpload", NULL, js_gguf_upload, NULL, NULL, NULL, napi_enumerable, NULL},
       {"ggufClose", NULL, js_gguf_close, NULL, NULL, NULL, napi_enumerable, NULL},
+      {"deviceAlloc", NULL, js_device_alloc, NULL, NULL, NULL, napi_enumerable, NULL},
+      {"deviceFree", NULL, js_device_free, NULL, NULL, NULL, napi_enumerable, NULL},
+      {"copyToDevice", NULL, js_copy_to_device, NULL, NULL, NULL, napi_enumerable, NULL},
+      {"copyToHost", NULL, js_copy_to_host, NULL, NULL, NULL, napi_enumerable, NULL},
+      {"runLayers", NULL, js_run_layers, NULL, NULL, NULL, napi_enumerable, NULL},
+      {"headTopK", NULL, js_head_topk, NULL, NULL, NULL, napi_enumerable, NULL},
   };
   napi_define_properties(env, exports, sizeof d / sizeof d[0], d);
   return exports;

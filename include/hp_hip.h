@@ -288,6 +288,35 @@ int32_t hp_hip_profile_read(int32_t kernel, double *total_ms, uint64_t *launches
  * graph node, for measurements.  No counterpart in the reference. */
 int32_t hp_hip_empty_launches(size_t count, void *stream);
 
+/* ---- Device buffers for host runtimes without a HIP binding ------------
+ * What the WebGPU runner does with its arena (device.createBuffer,
+ * queue.writeBuffer, copyBufferToBuffer + mapAsync readback;
+ * webgpu/segment-runner.ts:1135-1180, 942-960) for the Node runner, whose
+ * hidden rows, positions, norm weights and KV rings stay in HBM between
+ * calls.  hp_hip_device_alloc returns a zero-filled buffer (refused while
+ * the library stream captures); hp_hip_device_free waits for the library
+ * stream, then frees (NULL: no-op; any other pointer not from
+ * hp_hip_device_alloc: HP_ERR_ARG).  The copies are ordered on `stream`
+ * (NULL = library stream) after the work queued there and return once the
+ * bytes have arrived; the device range must lie inside one buffer of
+ * hp_hip_device_alloc (else HP_ERR_ARG).  hp_hip_shutdown frees what is left. */
+int32_t hp_hip_device_alloc(size_t bytes, void **d_out);
+int32_t hp_hip_device_free(void *d);
+int32_t hp_hip_copy_to_device(void *d_dst, const void *src, size_t bytes, void *stream);
+int32_t hp_hip_copy_to_host(void *dst, const void *d_src, size_t bytes, void *stream);
+
+/* hp_hip_matmul_topk_sample on a device input ([column_count][input_size]
+ * f32, 16-byte aligned, ordered on the library stream): forwardOutput's head,
+ * topK and, when `sampling` is not NULL, sampleNextToken per column
+ * (layers.ts:381-416, runtime.ts:514-527, generation.ts:40-165), only the
+ * candidates (and tokens) read back.  sampling NULL: rng_state, tokens,
+ * probabilities and kept are not used (may be NULL). */
+int32_t hp_hip_matmul_topk_sample_device(uint64_t handle, const float *d_input, size_t input_len, size_t input_size,
+                                         size_t column_count, size_t k, double softcap,
+                                         const hp_hip_sampling_t *sampling, uint32_t *rng_state, int32_t *tokens,
+                                         uint32_t *ids, float *values, double *probabilities, int32_t *kept,
+                                         size_t out_len);
+
 /* ---- Decoder layer for one decode token -------------------------------
  * The non-projection steps of forwardAttentionLayer / forwardFfn
  * (packages/engine/src/runner/wasm/layers.ts:161-473) on the device, for
