@@ -43,7 +43,8 @@ def test_addon_api_without_gpu():
         "matMulQuantizedHipResidentTopKSample", "resolveGenerationSamplingOptions",
         "assertHipOk", "checkHipSupport", "createHipQuantizedWeightHandle", "hipResidentWeightStats",
         "matMulGegluHipResident", "matMulQuantizedHipResident", "matMulQuantizedHipResidentMulti",
-        "matMulQuantizedHipResidentTopK", "quantizedTypeId", "releaseHipQuantizedWeightHandle"])
+        "matMulQuantizedHipResidentTopK", "quantizedTypeId", "releaseHipQuantizedWeightHandle",
+        "copyToDevice", "copyToHost", "deviceAlloc", "deviceFree", "headTopKDevice", "runDecodeLayers"])
     assert set(out["support"]) >= {"available"}
     assert out["typeIds"] == [1, 2, 3, 4, 5, 6, 0]                  # wasm-kernels.ts:1908-1923
     assert out["unknownType"] == "undefined"
