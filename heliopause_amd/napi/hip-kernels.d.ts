@@ -143,3 +143,43 @@ export function matMulQuantizedHipResidentTopKSample(
   state: Uint32Array,
   softcap?: number,
 ): Promise<{ token: number; distribution: { id: number; value: number; probability: number }[] }[]>;
+
+// Device buffers and the device-resident decode calls (hip/segment-runner.js).
+export type HipDevicePointer = bigint;
+export function deviceAlloc(bytes: number): HipDevicePointer;
+export function deviceFree(ptr: HipDevicePointer): void;
+export function copyToDevice(ptr: HipDevicePointer, array: ArrayBufferView, byteOffset?: number): void;
+export function copyToHost(ptr: HipDevicePointer, array: ArrayBufferView, byteOffset?: number): void;
+/* hp_hip_decode_layer_t as an object (include/hp_hip.h). */
+export type HipDecodeLayerDescriptor = {
+  attnQ: bigint; attnK: bigint; attnV: bigint; attnOutput: bigint; ffnGate: bigint; ffnUp: bigint; ffnDown: bigint;
+  attnNorm: HipDevicePointer; attnQNorm: HipDevicePointer; attnKNorm: HipDevicePointer;
+  postAttentionNorm: HipDevicePointer; ffnNorm: HipDevicePointer; postFfwNorm: HipDevicePointer;
+  layerOutputScale: number;
+  keyCache: HipDevicePointer; valueCache: HipDevicePointer;
+  attention: {
+    headCount: number; headCountKv: number; headDim: number; ropeDims: number; ropeFreqBase: number;
+    ropeFreqFactors: HipDevicePointer; capacity: number; slidingWindow: number; epsilon: number;
+  };
+};
+export function runDecodeLayers(
+  layers: HipDecodeLayerDescriptor[],
+  tokenCount: number,
+  hiddenSize: number,
+  buffers: { hidden: HipDevicePointer; position: HipDevicePointer; outputNorm: HipDevicePointer; output: HipDevicePointer },
+  input: Float32Array | null,
+  position: number,
+  readOutput: boolean,
+  rowStart: number,
+  rowCount: number,
+): Promise<Float32Array>;
+export function headTopKDevice(
+  handle: HipQuantizedWeightHandle,
+  dInput: HipDevicePointer,
+  inputSize: number,
+  columnCount: number,
+  topK: number,
+  softcap?: number,
+  sampling?: ResolvedHipSamplingOptions,
+  state?: Uint32Array,
+): Promise<unknown[]>;

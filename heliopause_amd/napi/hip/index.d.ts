@@ -5,6 +5,7 @@ import type { HipProviderOptions, HipSession } from "./acceleration";
 
 export * from "./acceleration";
 export * from "./layers";
+export * from "./segment-runner";
 
 /* SegmentRunnerProvider (runner/segment-runner.ts:6) with the HIP member. */
 export type SegmentRunnerProvider = "reference" | "wasm" | "webgpu" | "hip";
