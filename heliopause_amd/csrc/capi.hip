@@ -1099,6 +1099,7 @@ int32_t run_norm(const float *y, int rows, int n, const float *w_post, const flo
 // Weights of one decode layer, looked up and checked against each other.
 struct LayerHandles {
   Handle *q, *k, *v, *o, *gate, *up, *down;
+  Handle *inp_gate, *proj;  // the per-layer input step, or null
 };
 
 int32_t decode_layer_check(const hp_hip_decode_layer_t &L, size_t hidden, LayerHandles *out) {
@@ -1127,6 +1128,15 @@ int32_t decode_layer_check(const hp_hip_decode_layer_t &L, size_t hidden, LayerH
       !L.d_post_ffw_norm || !L.d_key_cache || !L.d_value_cache)
     return fail(HP_ERR_ARG, "null norm weight or cache in decode layer");
   if (L.reserved != 0) return fail(HP_ERR_ARG, "reserved field must be 0");
+  if (L.inp_gate || L.proj) {
+    h.inp_gate = lookup(L.inp_gate);
+    h.proj = lookup(L.proj);
+    if (!h.inp_gate || !h.proj) return fail(HP_ERR_HANDLE, "unknown per-layer input handle in decode layer");
+    if (h.inp_gate->input_size != hidden || h.proj->row_count != hidden ||
+        h.proj->input_size != h.inp_gate->row_count)
+      return fail(HP_ERR_SHAPE, "per-layer input shape mismatch");
+    if (!L.d_post_norm || !L.d_per_layer_input) return fail(HP_ERR_ARG, "null per-layer input or post_norm");
+  }
   *out = h;
   return HP_OK;
 }
@@ -1272,6 +1282,7 @@ bool fused_plan(const hp_hip_decode_layer_t *layers, const std::vector<LayerHand
     const int chunks = (c.capacity + kAttnChunk - 1) / kAttnChunk;
     if (chunks > 128 || c.head_count * 4 > 65535) return false;
     if (H.gate->type != H.up->type) return false;
+    if (H.inp_gate) return false;  // the per-layer input step runs in the launch sequence
     FusedLayer &D = p.layers[i];
     D = FusedLayer{};
     Handle *qkv[3] = {H.q, H.k, H.v};
@@ -2312,7 +2323,7 @@ int32_t hp_hip_decode_layers_device(const hp_hip_decode_layer_t *layers, size_t 
   if (reinterpret_cast<uintptr_t>(d_hidden) % 16 != 0) return fail(HP_ERR_ARG, "hidden must be 16-byte aligned");
   std::vector<LayerHandles> hs(layer_count);
   size_t hidden = lookup(layers[0].attn_q) ? lookup(layers[0].attn_q)->input_size : 0;
-  size_t qmax = 0, kvmax = 0, ffmax = 0;
+  size_t qmax = 0, kvmax = 0, ffmax = 0, pmax = 0;
   int min_cap = INT32_MAX;
   for (size_t i = 0; i < layer_count; i++) {
     rc = decode_layer_check(layers[i], hidden, &hs[i]);
@@ -2321,6 +2332,7 @@ int32_t hp_hip_decode_layers_device(const hp_hip_decode_layer_t *layers, size_t 
     qmax = std::max(qmax, (size_t)c.head_count * kHeadDim);
     kvmax = std::max(kvmax, (size_t)c.head_count_kv * kHeadDim);
     ffmax = std::max(ffmax, hs[i].gate->row_count);
+    if (hs[i].inp_gate) pmax = std::max(pmax, hs[i].inp_gate->row_count);
     min_cap = std::min(min_cap, c.capacity);
   }
   if (hidden == 0 || hidden > kNormMaxN) return fail(HP_ERR_SHAPE, "hidden size must be 1..4096");
@@ -2358,19 +2370,20 @@ int32_t hp_hip_decode_layers_device(const hp_hip_decode_layer_t *layers, size_t 
   const bool images = M >= 2 && M <= (size_t)kMaxTokens;
   const size_t img_x = images ? q8_image_bytes((int)M, (int)(hidden / kQK)) / sizeof(float) : 0;
   const size_t img_h = images ? q8_image_bytes((int)M, (int)(ffmax / kQK)) / sizeof(float) : 0;
-  const size_t sizes[14] = {al(M * hidden), al(M * qmax),   al(M * kvmax),  al(M * kvmax),
+  // (per-layer input step) the FFN residual x2, the gate and the gelu product
+  const size_t sizes[16] = {al(M * hidden), al(M * qmax),   al(M * kvmax),  al(M * kvmax),
                             al(M * qmax),   al(M * qmax),   al(M * hidden), al(M * hidden),
                             al(M * ffmax),  al(M * hidden), al(partials),   al(M * kHeadDim / 2 * 4),
-                            al(img_x),      al(img_h)};
+                            al(img_x),      al(img_h),      al(pmax ? M * hidden : 0), al(M * 2 * pmax)};
   size_t total = 0;
   for (size_t z : sizes) total += z;
   hipStream_t strm = stream ? static_cast<hipStream_t>(stream) : s.stream;
   void *dscr = nullptr;
   rc = stream_scratch(strm, kScratchDecode, total * sizeof(float), &dscr);
   if (rc != HP_OK) return rc;
-  float *buf[14];
+  float *buf[16];
   float *p = static_cast<float *>(dscr);
-  for (int i = 0; i < 14; i++) {
+  for (int i = 0; i < 16; i++) {
     buf[i] = p;
     p += sizes[i];
   }
@@ -2379,6 +2392,7 @@ int32_t hp_hip_decode_layers_device(const hp_hip_decode_layer_t *layers, size_t 
   double2 *rope_table = reinterpret_cast<double2 *>(buf[11]);
   uint8_t *imgx_buf = images && hidden % kQK == 0 ? reinterpret_cast<uint8_t *>(buf[12]) : nullptr;
   uint8_t *imgh_buf = images && ffmax % kQK == 0 ? reinterpret_cast<uint8_t *>(buf[13]) : nullptr;
+  float *x2 = buf[14], *pg = buf[15];
 
   for (size_t c0 = 0; c0 < token_count; c0 += chunk) {
     const size_t Mc = std::min(chunk, token_count - c0);
@@ -2508,9 +2522,34 @@ int32_t hp_hip_decode_layers_device(const hp_hip_decode_layer_t *layers, size_t 
       nin.x_out = hid;
       nin.w_next = i + 1 < layer_count ? layers[i + 1].d_attn_norm : nullptr;
       nin.eps = eps;
+      if (H.inp_gate) {
+        // applyPerLayerInput: the FFN residual x2 (no scale yet), gate =
+        // inp_gate . x2, mixed = f32(gelu(gate) * input) (the GeGLU product
+        // with the per-layer input as `up`), y = proj . mixed; the next norm
+        // forms f32((x2 + post_norm(y)) * scale)
+        rc = run_norm(nin.y, (int)Mc, (int)hidden, L.d_post_ffw_norm, x1, 1.0f, x2, nullptr, nullptr, eps, strm,
+                      nullptr, nullptr, &dp);
+        if (rc != HP_OK) return rc;
+        dp.ks = 1;
+        const size_t P = H.inp_gate->row_count;
+        Handle *gh[1] = {H.inp_gate};
+        float *go[1] = {pg};
+        rc = run_matvec(1, gh, x2, hidden, Mc, go, strm);
+        if (rc != HP_OK) return rc;
+        float *mixed = pg + Mc * P;
+        HP_HIP_TRY(launch_geglu(pg, L.d_per_layer_input + c0 * P, Mc * P, s.gelu_lut, mixed, s.num_cus, strm));
+        s.launches++;
+        Handle *ph[1] = {H.proj};
+        float *po[1] = {y};
+        rc = run_matvec(1, ph, mixed, P, Mc, po, strm);
+        if (rc != HP_OK) return rc;
+        nin.y = y;
+        nin.w_post = L.d_post_norm;
+        nin.x_res = x2;
+      }
     }
-    // the last layer's post-FFN residual, then output_norm
-    rc = run_norm(nin.y, (int)Mc, (int)hidden, nin.w_post, x1, nin.scale, hid, d_output_norm,
+    // the last layer's post-FFN residual (or per-layer input residual), then output_norm
+    rc = run_norm(nin.y, (int)Mc, (int)hidden, nin.w_post, nin.x_res, nin.scale, hid, d_output_norm,
                   d_output_norm ? d_output + c0 * hidden : nullptr, nin.eps, strm, nullptr, nullptr, &dp);
     if (rc != HP_OK) return rc;
   }

@@ -53,8 +53,11 @@ class ModelShape:
                 ("ffn_down", "Q6_K", self.hidden, self.ffn)]
 
 
-def layer_host_data(shape: ModelShape, seed: int, layer: int, *, cache_fill: bool = True) -> dict:
-    """Deterministic synthetic data of one layer (host arrays)."""
+def layer_host_data(shape: ModelShape, seed: int, layer: int, *, cache_fill: bool = True,
+                    per_layer_length: int = 0) -> dict:
+    """Deterministic synthetic data of one layer (host arrays); with
+    per_layer_length > 0 also the per-layer input step's weights (inp_gate
+    Q4_K [P][hidden], proj Q4_K [hidden][P], post_norm)."""
     ls = S.derive(seed, "layer", layer)
     data = {"weights": {}, "norms": {}}
     for name, t, rows, k in shape.projections():
@@ -63,6 +66,21 @@ def layer_host_data(shape: ModelShape, seed: int, layer: int, *, cache_fill: boo
         n = 256 if name in ("attn_q_norm", "attn_k_norm") else shape.hidden
         data["norms"][name] = (1.0 + 0.1 * S.normal(S.derive(ls, name), n)).astype(np.float32)
     data["output_scale"] = np.float32(1.0 + 0.05 * S.normal(S.derive(ls, "scale"), 1)[0])
+    if per_layer_length:
+        P = per_layer_length
+        # inp_gate as Q6_K (symmetric scales: zero-mean weights, so the
+        # residual stream's offset does not push every gate below gelu's -10
+        # cut) with d scaled by 2^-6 (exact in f16): gate values of a few
+        # units, inside gelu's active range
+        gate = S.weight_blocks("Q6_K", S.derive(ls, "inp_gate"), P, shape.hidden)
+        g = gate.reshape(-1, 210)
+        d = g[:, 208:210].copy().view(np.float16) * np.float16(2.0 ** -6)
+        g[:, 208:210] = d.view(np.uint8).reshape(-1, 2)
+        data["per_layer"] = {
+            "inp_gate": ("Q6_K", gate, P, shape.hidden),
+            "proj": ("Q4_K", S.weight_blocks("Q4_K", S.derive(ls, "proj"), shape.hidden, P), shape.hidden, P),
+            "post_norm": (1.0 + 0.1 * S.normal(S.derive(ls, "post_norm"), shape.hidden)).astype(np.float32),
+        }
     cshape = (shape.head_count_kv, shape.capacity, 256)
     n = int(np.prod(cshape))
     if cache_fill:
@@ -117,7 +135,24 @@ class HipDecodeModel:
         L.reserved = 0
         L.d_key_cache, L.d_value_cache = kc.data_ptr(), vc.data_ptr()
         L.attention = cfg
+        if "per_layer" in data:
+            # applyPerLayerInput: inp_gate / proj handles and post_norm; the
+            # layer's per-layer input rows are set per call (set_per_layer_input)
+            ple = data["per_layer"]
+            for name in ("inp_gate", "proj"):
+                t, blocks, rows, k = ple[name]
+                h = H.createHipQuantizedWeightHandle(t, blocks, k, rows)
+                self.handles.append(h)
+                setattr(L, name, h.handle)
+            pn = torch.from_numpy(ple["post_norm"]).to(dev)
+            self.tensors.append(pn)
+            L.d_post_norm = pn.data_ptr()
         self.layers.append(L)
+
+    def set_per_layer_input(self, index: int, d_rows: int) -> None:
+        """Layer `index`'s rows of the per-layer inputs ([tokens][P] f32 on
+        the device) for the next run_layers call."""
+        self.layers[index].d_per_layer_input = d_rows
 
     def set_head(self, output_norm: np.ndarray, head: H.HipQuantizedWeightHandle) -> None:
         import torch

@@ -128,7 +128,9 @@ class HipDecodeLayer(ctypes.Structure):
                 ("d_ffn_norm", ctypes.c_void_p), ("d_post_ffw_norm", ctypes.c_void_p),
                 ("layer_output_scale", ctypes.c_float), ("reserved", ctypes.c_int32),
                 ("d_key_cache", ctypes.c_void_p), ("d_value_cache", ctypes.c_void_p),
-                ("attention", HipAttentionConfig)]
+                ("attention", HipAttentionConfig),
+                ("inp_gate", _u64), ("proj", _u64), ("d_post_norm", ctypes.c_void_p),
+                ("d_per_layer_input", ctypes.c_void_p)]
 
 
 def _declare_decode(L: ctypes.CDLL) -> None:

@@ -27,8 +27,11 @@
  * runner) when the GPU or the addon is missing or a layer is outside what
  * the device path covers: every layer with its own KV, key and value width
  * 256, query heads a multiple of the KV heads (at most 8 per KV head),
- * Q4_K/Q6_K projections, F32 norms, hidden size a multiple of 256 up to
- * 4096, no per-layer input embeddings (applyPerLayerInput, layers.ts:475-521).
+ * Q4_K/Q6_K projections (inp_gate and proj of the per-layer input step
+ * included, applyPerLayerInput layers.ts:475-521), F32 norms, hidden size a
+ * multiple of 256 up to 4096.  A run given options.perLayerInputs (the
+ * [layer][token][P] array of preparePerLayerInputs) runs that step in every
+ * layer; a run without it skips it, as forwardAttentionLayer does.
  */
 
 const acceleration = require("./acceleration.js");
@@ -68,8 +71,9 @@ function hipSegmentSupport(session, manifest, start, end) {
   if (hidden % 256 !== 0 || hidden > MAX_HIDDEN) {
     return { supported: false, reason: `hidden size ${hidden}` };
   }
-  if (manifest.perLayerEmbeddingLength > 0) {
-    return { supported: false, reason: "per-layer input embeddings" };
+  const ple = manifest.perLayerEmbeddingLength > 0;
+  if (ple && manifest.perLayerEmbeddingLength % 256 !== 0) {
+    return { supported: false, reason: `per-layer input length ${manifest.perLayerEmbeddingLength}` };
   }
   for (let layer = start; layer < end; layer += 1) {
     if (manifest.layerHasKv[layer] !== true) {
@@ -87,6 +91,13 @@ function hipSegmentSupport(session, manifest, start, end) {
     const projections = ["attn_q", "attn_k", "attn_output", "ffn_gate", "ffn_up", "ffn_down"];
     if (!valueShared(manifest, layer)) {
       projections.push("attn_v");
+    }
+    if (ple) {
+      projections.push("inp_gate", "proj");
+      const post = tensorInfo(session, `blk.${layer}.post_norm.weight`);
+      if (!post || post.type !== "F32") {
+        return { supported: false, reason: `blk.${layer}.post_norm.weight` };
+      }
     }
     for (const name of projections) {
       const tensor = tensorInfo(session, `blk.${layer}.${name}.weight`);
@@ -241,12 +252,42 @@ class HipSegmentRunner {
     return s;
   }
 
-  descriptors(s) {
-    return this.layers.map((layer, index) => Object.assign({}, layer.descriptor, {
-      keyCache: s.caches[index].key,
-      valueCache: s.caches[index].value,
-      attention: Object.assign({}, layer.descriptor.attention, { capacity: s.caches[index].capacity }),
-    }));
+  /* The layer objects of one call: the state's rings, and with the
+   * per-layer inputs ([layer][token][P], every layer of the model) this
+   * segment's rows of them in a device buffer, one block per layer. */
+  descriptors(s, perLayerInputs, tokenCount) {
+    const P = this.manifest.perLayerEmbeddingLength;
+    let pli;
+    if (perLayerInputs && P > 0) {
+      const start = this.segmentStartLayer;
+      const count = this.segmentEndLayerExclusive - start;
+      if (perLayerInputs.length !== this.manifest.blockCount * tokenCount * P) {
+        throw new Error(`Per-layer input shape mismatch: ${perLayerInputs.length}`);
+      }
+      const bytes = count * tokenCount * P * 4;
+      if (!s.pli || s.pliBytes < bytes) {
+        if (s.pli) {
+          this.kernels.deviceFree(s.pli);
+          this.stateBuffers.splice(this.stateBuffers.indexOf(s.pli), 1);
+        }
+        s.pli = this.kernels.deviceAlloc(bytes);
+        s.pliBytes = bytes;
+        this.stateBuffers.push(s.pli);
+      }
+      this.kernels.copyToDevice(s.pli, perLayerInputs.subarray(start * tokenCount * P, (start + count) * tokenCount * P));
+      pli = s.pli;
+    }
+    return this.layers.map((layer, index) => {
+      const d = Object.assign({}, layer.descriptor, {
+        keyCache: s.caches[index].key,
+        valueCache: s.caches[index].value,
+        attention: Object.assign({}, layer.descriptor.attention, { capacity: s.caches[index].capacity }),
+      });
+      if (pli !== undefined && layer.ple) {
+        Object.assign(d, layer.ple, { perLayerInput: pli + BigInt(index * tokenCount * P * 4) });
+      }
+      return d;
+    });
   }
 
   /* Calls on one runner run one at a time: they share its row buffers. */
@@ -264,9 +305,6 @@ class HipSegmentRunner {
     if (opts.attentionCausal === false) {
       throw new Error("The HIP segment runner runs causal attention only.");
     }
-    if (opts.perLayerInputs && this.manifest.perLayerEmbeddingLength > 0) {
-      throw new Error("The HIP segment runner has no per-layer input step.");
-    }
     const hiddenSize = this.manifest.embeddingLength;
     const tokenCount = inputHidden.length / hiddenSize;
     if (!Number.isInteger(tokenCount) || tokenCount < 1) {
@@ -281,7 +319,8 @@ class HipSegmentRunner {
     const lastOnly = this.segmentEndLayerExclusive === this.manifest.blockCount && tokenCount > 1;
     return this.serial(async () => {
       const s = this.stateFor(state, tokenCount);
-      const hidden = await this.kernels.runDecodeLayers(this.descriptors(s), tokenCount, hiddenSize,
+      const hidden = await this.kernels.runDecodeLayers(this.descriptors(s, opts.perLayerInputs, tokenCount),
+        tokenCount, hiddenSize,
         { hidden: s.hidden, position: s.position, outputNorm: 0n, output: 0n }, inputHidden, position, false,
         lastOnly ? tokenCount - 1 : 0, lastOnly ? 1 : tokenCount);
       return { hidden };
@@ -336,7 +375,7 @@ class HipSegmentRunner {
     const parts = await this.outputParts();
     return this.serial(async () => {
       const s = this.stateFor(state, 1);
-      await this.kernels.runDecodeLayers(this.descriptors(s), 1, hiddenSize,
+      await this.kernels.runDecodeLayers(this.descriptors(s, opts.perLayerInputs, 1), 1, hiddenSize,
         { hidden: s.hidden, position: s.position, outputNorm: parts.norm, output: s.output }, inputHidden, position,
         true, 0, 0);
       const softcap = this.manifest.finalLogitSoftcap;
@@ -448,7 +487,15 @@ async function createHipSegmentRunner(options) {
         slidingWindow: kind === "sliding-attention" ? manifest.slidingWindow : 0,
         epsilon,
       };
-      layers.push({ layer, headCountKv: descriptor.attention.headCountKv, descriptor });
+      let ple;
+      if (manifest.perLayerEmbeddingLength > 0) {
+        ple = {
+          inpGate: await handle("inp_gate"),
+          proj: await handle("proj"),
+          postNorm: upload(await session.readF32Tensor(`blk.${layer}.post_norm.weight`)),
+        };
+      }
+      layers.push({ layer, headCountKv: descriptor.attention.headCountKv, descriptor, ple });
     }
     return new HipSegmentRunner({ session, manifest, epsilon, segmentStartLayer: start, segmentEndLayerExclusive: end },
       layers, owned, kernels);

@@ -977,6 +977,11 @@ static int get_layer(napi_env env, napi_value o, hp_hip_decode_layer_t *L) {
   if (!get_prop_f64(env, a, "slidingWindow", &d)) return 0;
   c->sliding_window = (int32_t)d;
   if (!get_prop_f64(env, a, "epsilon", &c->epsilon)) return 0;
+  /* the per-layer input step (absent: none) */
+  get_prop_u64(env, o, "inpGate", &L->inp_gate);
+  get_prop_u64(env, o, "proj", &L->proj);
+  if (get_prop_ptr(env, o, "postNorm", &p)) L->d_post_norm = (const float *)p;
+  if (get_prop_ptr(env, o, "perLayerInput", &p)) L->d_per_layer_input = (const float *)p;
   return 1;
 }
 

@@ -404,6 +404,17 @@ typedef struct hp_hip_decode_layer {
   int32_t reserved;         /* 0 */
   uint16_t *d_key_cache, *d_value_cache; /* f16 [head_count_kv][capacity][head_dim] */
   hp_hip_attention_config_t attention;
+  /* The per-layer input step (applyPerLayerInput, layers.ts:475-521), after
+   * the FFN's residual and before the layer output scale:
+   *   x = x + rmsNormRows(proj . f32(gelu(inp_gate . x) * input), post_norm).
+   * inp_gate [per_layer_length][hidden] and proj [hidden][per_layer_length]
+   * handles (both 0: the layer has no such step), post_norm [hidden] f32, and
+   * this layer's rows of the prepared per-layer inputs, [token_count]
+   * [per_layer_length] f32 (the caller points each layer at its own block
+   * of preparePerLayerInputs' [layer][token][per_layer_length] array). */
+  uint64_t inp_gate, proj;
+  const float *d_post_norm;
+  const float *d_per_layer_input;
 } hp_hip_decode_layer_t;
 
 /* forwardAttentionLayer (layers.ts:161-379, with forwardFfn 418-473) for
@@ -419,8 +430,9 @@ typedef struct hp_hip_decode_layer {
  * cache append inside it plus the merge, O, gate/up + GeGLU whose prologue
  * forms the post-attention residual and ffn_norm, down.  Several tokens add a
  * prologue launch (norms, RoPE, every token's cache append) before the
- * attention, and the norms run as their own launches.  Per-layer input
- * embeddings (applyPerLayerInput) are not part of this path. */
+ * attention, and the norms run as their own launches.  A layer with the
+ * per-layer input step adds a norm launch (the FFN residual), the inp_gate
+ * matvec, the gelu product and the proj matvec. */
 int32_t hp_hip_decode_layers_device(const hp_hip_decode_layer_t *layers, size_t layer_count, size_t token_count,
                                     float *d_hidden, const int32_t *d_position, const float *d_output_norm,
                                     float *d_output, void *stream);

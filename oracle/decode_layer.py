@@ -180,11 +180,27 @@ def _proj(layer: Layer, names, x) -> list:
                           threads=8)
 
 
-def forward_layer(layer: Layer, hidden, position: int) -> np.ndarray:
-    """forwardAttentionLayer + forwardFfn + layer output scale for the tokens
-    at position .. position + T - 1 (hidden [T][n], or [n] for one token);
-    appends every token's key and value to the caches.  Every token's row is
-    returned."""
+def apply_per_layer_input(layer: Layer, x: np.ndarray, per_layer_input: np.ndarray) -> np.ndarray:
+    """applyPerLayerInput (layers.ts:475-521) on rows x [T][n] with this
+    layer's per-layer input rows [T][P]: gate = gelu(inp_gate . x) (gelu
+    1062-1076), mixed = f32(gate * input) (503-510), projected = proj .
+    mixed, x + rmsNormRows(projected, post_norm).  f32(gelu(g) * u) is the
+    GeGLU product (450-456), so hpo_geglu forms `mixed`."""
+    eps = layer.epsilon
+    t = layer.trace
+    t["ple_gate"] = gate = _proj(layer, ["inp_gate"], x)[0]
+    pli = _f(per_layer_input).reshape(gate.shape)
+    t["ple_mixed"] = mixed = O.geglu(gate, pli)
+    t["ple_proj"] = projected = _proj(layer, ["proj"], mixed)[0]
+    return residual_add(x, rms_norm_rows(projected, layer.norms["post_norm"], eps))
+
+
+def forward_layer(layer: Layer, hidden, position: int, per_layer_input=None) -> np.ndarray:
+    """forwardAttentionLayer + forwardFfn (+ applyPerLayerInput when the
+    layer has inp_gate / proj and per_layer_input [T][P] is given) + layer
+    output scale for the tokens at position .. position + T - 1 (hidden
+    [T][n], or [n] for one token); appends every token's key and value to the
+    caches.  Every token's row is returned."""
     eps, hd = layer.epsilon, HEAD_DIM
     nq, nkv = layer.head_count, layer.head_count_kv
     x0 = _f(hidden)
@@ -217,6 +233,9 @@ def forward_layer(layer: Layer, hidden, position: int) -> np.ndarray:
     t["ffn_hidden"] = h = O.geglu(gate, up)
     t["down"] = y = _proj(layer, ["ffn_down"], h)[0]
     x2 = residual_add(x1, rms_norm_rows(y, layer.norms["post_ffw_norm"], eps))
+    if per_layer_input is not None and "inp_gate" in layer.weights:
+        t["ffn_residual"] = x2
+        x2 = apply_per_layer_input(layer, x2, per_layer_input)
     out = (x2.astype(np.float64) * np.float64(np.float32(layer.output_scale))).astype(np.float32)
     return out[0] if one else out
 

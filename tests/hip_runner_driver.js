@@ -401,6 +401,7 @@ async function segment() {
   // what the device path covers
   out.support = seg.hipSegmentSupport(session, manifest, 0, 2);
   out.supportPle = seg.hipSegmentSupport(session, manifestOf(2, { perLayerEmbeddingLength: 256 }), 0, 2).reason;
+  out.supportPleLength = seg.hipSegmentSupport(session, manifestOf(2, { perLayerEmbeddingLength: 100 }), 0, 2).reason;
   out.supportKvShared = seg.hipSegmentSupport(session, manifestOf(2, { layerHasKv: [true, false] }), 0, 2).reason;
   out.supportWidth = seg.hipSegmentSupport(session, manifestOf(2, { layerKeyLengths: [256, 512] }), 0, 2).reason;
   out.supportType = seg.hipSegmentSupport(modelSession(modelTensors(2, { "blk.1.ffn_up.weight": { type: "Q8_0",
@@ -414,7 +415,7 @@ async function segment() {
   out.invalidSegment = await throws(() => seg.createHipSegmentRunner({ session, manifest, segmentStartLayer: 1,
     segmentEndLayerExclusive: 3 }));
   const fallback = await hip.createHipModelRunner(engine).segmentRunner({ session: modelSession(tensors,
-    manifestOf(2, { perLayerEmbeddingLength: 64 })), manifest: manifestOf(2, { perLayerEmbeddingLength: 64 }),
+    manifestOf(2, { perLayerEmbeddingLength: 256 })), manifest: manifestOf(2, { perLayerEmbeddingLength: 256 }),
   segmentStartLayer: 0, segmentEndLayerExclusive: 2 });
   out.fallbackProvider = [fallback.provider, fallback instanceof seg.HipSegmentRunner];
   // a state that already holds positions: its host caches go to the device rings
@@ -464,6 +465,29 @@ async function segment() {
   out.frees = log.filter((l) => l === "free").length;
   out.leftBuffers = dev.buffers.size;
   out.afterRelease = await throws(() => runner.runTokensHidden(new Float32Array(512), Int32Array.of(1), state));
+  // the per-layer input step: layer 1 of a 3-layer model, 2 tokens, P = 256
+  const pleTensors = modelTensors(3);
+  for (let l = 0; l < 3; l += 1) {
+    pleTensors[`blk.${l}.inp_gate.weight`] = { type: "Q6_K", dimensions: [512, 256] };
+    pleTensors[`blk.${l}.proj.weight`] = { type: "Q4_K", dimensions: [256, 512] };
+    pleTensors[`blk.${l}.post_norm.weight`] = { type: "F32", dimensions: [512] };
+  }
+  const pleManifest = manifestOf(3, { perLayerEmbeddingLength: 256 });
+  const pleSession = modelSession(pleTensors, pleManifest);
+  const pleRunner = await seg.createHipSegmentRunner({ session: pleSession, manifest: pleManifest,
+    segmentStartLayer: 1, segmentEndLayerExclusive: 2 });
+  const pleState = stateOf(pleManifest, [64, 8192, 64], 0);
+  const pli = Float32Array.from({ length: 3 * 2 * 256 }, (_, i) => i);
+  await pleRunner.runTokensHidden(new Float32Array(2 * 512), Int32Array.of(4, 5), pleState, { perLayerInputs: pli });
+  const pc = dev.calls[dev.calls.length - 1];
+  const rows = new Float32Array(dev.buffers.get(pc.layers[0].perLayerInput).buffer);
+  out.ple = { hasGate: pc.layers[0].inpGate !== undefined && pc.layers[0].proj !== undefined,
+    postNorm: pc.layers[0].postNorm !== undefined, first: rows[0], last: rows[2 * 256 - 1] };
+  await pleRunner.runTokensHidden(new Float32Array(512), Int32Array.of(6), pleState);
+  out.pleSkipped = dev.calls[dev.calls.length - 1].layers[0].perLayerInput === undefined;
+  out.pleShape = await throws(() => pleRunner.runTokensHidden(new Float32Array(512), Int32Array.of(7), pleState,
+    { perLayerInputs: new Float32Array(10) }));
+  pleRunner.release();
   process.stdout.write(JSON.stringify(out, (key, v) => (typeof v === "bigint" ? String(v) : v)));
 }
 

@@ -503,3 +503,63 @@ def test_layers_reject_token_counts(hip):
                 model.run_layers(dx.data_ptr(), dpos.data_ptr(), tokens=bad)
     finally:
         model.release()
+
+
+def _oracle_layer_ple(D, shape, data):
+    """_oracle_layer plus the per-layer input step's weights and post_norm."""
+    ol = _oracle_layer(D, shape, data)
+    tids = {"Q4_K": 1, "Q6_K": 3}
+    for name in ("inp_gate", "proj"):
+        t, blocks, rows, _ = data["per_layer"][name]
+        ol.weights[name] = (tids[t], blocks, rows)
+    ol.norms["post_norm"] = data["per_layer"]["post_norm"]
+    return ol
+
+
+@pytest.mark.parametrize("full,tokens,pos", [(False, 1, 70), (False, 4, 61), (True, 1, 4096), (True, 4, 4093),
+                                             (True, 128, 3968)],
+                         ids=["small-decode", "small-draft4", "model-decode", "model-draft4", "model-prefill128"])
+def test_decode_layer_with_per_layer_input(hip, D, full, tokens, pos):
+    """A layer with the per-layer input step (applyPerLayerInput,
+    layers.ts:475-521; P = 256): inp_gate, the gelu product with the
+    layer's input rows, proj and post_norm between the FFN residual and the
+    layer scale, against the oracle's layer on the same rows.  Decode and
+    draft rows within LAYER_TOL; the 128-token chunk on the bit-exact
+    prefill projections (selector 4) to the prefill bars (every row 3e-2,
+    median 1e-4)."""
+    import torch
+
+    hip.setMatvecKernel(4 if tokens > 8 else 0)
+
+    shape = DM.ModelShape() if full else _small_shape()
+    P = 256
+    seed = S.derive(S.BASE_SEED, "decode-ple", full, tokens)
+    data = DM.layer_host_data(shape, seed, 0, per_layer_length=P)
+    model = DM.HipDecodeModel(shape)
+    model.add_layer(data)
+    x = S.activations(S.derive(seed, "x"), tokens, shape.hidden) * 4
+    pli = S.activations(S.derive(seed, "pli"), tokens, P)
+    dx = _dev(x.reshape(-1))
+    dp = _dev(pli.reshape(-1))
+    dpos = _dev(np.array([pos], np.int32))
+    print(f"decode layer with per-layer input hidden={shape.hidden} tokens={tokens} pos={pos}", flush=True)
+    try:
+        model.set_per_layer_input(0, dp.data_ptr())
+        model.run_layers(dx.data_ptr(), dpos.data_ptr(), tokens=tokens)
+        torch.cuda.synchronize()
+        got = dx.cpu().numpy().reshape(tokens, shape.hidden)
+    finally:
+        model.release()
+        hip.setMatvecKernel(0)
+    ol = _oracle_layer_ple(D, shape, data)
+    ref = D.forward_layer(ol, x, pos, pli)
+    plain = D.forward_layer(_oracle_layer(D, shape, data), x, pos)
+    errs = np.array([_row_err(got[t], ref[t]) for t in range(tokens)])
+    moved = min(_row_err(ref[t], plain[t]) for t in range(tokens))
+    print(f"per-layer input: max row err {errs.max():.3e}, median {np.median(errs):.2e}, identical "
+          f"{np.mean(got == ref):.4f}; the step moves every row by at least {moved:.2e} of its rms", flush=True)
+    assert moved > 1e-2                        # the step is not a no-op on these rows
+    if tokens <= 8:
+        assert errs.max() <= LAYER_TOL
+    else:
+        assert errs.max() <= 3e-2 and np.median(errs) <= 1e-4

@@ -168,14 +168,15 @@ def test_layer_projections_by_name_bit_exact(oracle, tmp_path):
 def test_segment_runner_on_a_stand_in_device():
     out = _node("segment")
     assert out["support"] == {"supported": True}
-    assert out["supportPle"] == "per-layer input embeddings"
+    assert out["supportPle"] == "blk.0.post_norm.weight"   # per-layer inputs need their step's tensors
+    assert out["supportPleLength"] == "per-layer input length 100"
     assert out["supportKvShared"] == "layer 1 reads another layer's KV"
     assert out["supportWidth"] == "layer 1 head width 512/256"
     assert out["supportType"] == "blk.1.ffn_up.weight type Q8_0"
     assert out["supportHidden"] == "hidden size 4352"
     assert out["runnerProvider"] == ["hip", 0, 2]
     assert out["invalidSegment"] == "Invalid HIP layer segment: 1..3"
-    assert out["fallbackProvider"] == ["hip", False]        # the relabelled WASM runner
+    assert out["fallbackProvider"] == ["hip", False]        # no inp_gate tensors: the relabelled WASM runner
     # the model's last layer: only the last token's row comes back
     assert out["lastOnly"] == [512, 2, 1, 300, 3, 1536]
     L0 = out["layer0"]
@@ -203,6 +204,12 @@ def test_segment_runner_on_a_stand_in_device():
     assert out["middleRunToken"] == "runToken needs a segment that ends at the model's last layer."
     assert out["allocs"] == out["frees"] and out["leftBuffers"] == 0
     assert out["afterRelease"] == "The HIP segment runner was released."
+    # per-layer inputs: the segment's layer (1) gets its own block of rows
+    # ([layer][token][P]: layer 1 of 2 tokens starts at 512); a run without
+    # them skips the step; a wrong length throws
+    assert out["ple"] == {"hasGate": True, "postNorm": True, "first": 512.0, "last": 1023.0}
+    assert out["pleSkipped"]
+    assert out["pleShape"] == "Per-layer input shape mismatch: 10"
 
 
 @needs_node

@@ -209,3 +209,79 @@ def test_forward_layer_residual_path(D, oracle):
     assert np.array_equal(kc[:, 11 % cap], D.rope_neox(kn, [11], 256, 10000.0).astype(np.float16))
     assert np.array_equal(vc[:, 11 % cap], D.rms_norm_rows(layer.trace["v"].reshape(nkv, 256), None, 1e-6)
                           .astype(np.float16))
+
+
+def _ple_layer(D, oracle, eps=1e-6, P=256):
+    """A small layer with the per-layer input step (hidden 512, P = 256)."""
+    hidden, nq, nkv, ffn, cap = 512, 2, 1, 256, 8
+    seed = S.derive(S.BASE_SEED, "oracle-ple")
+    rng = np.random.default_rng(13)
+    w = {
+        "attn_q": (1, S.q4_k_blocks(S.derive(seed, "q"), nq * 256, hidden), nq * 256),
+        "attn_k": (1, S.q4_k_blocks(S.derive(seed, "k"), nkv * 256, hidden), nkv * 256),
+        "attn_v": (3, S.q6_k_blocks(S.derive(seed, "v"), nkv * 256, hidden), nkv * 256),
+        "attn_output": (1, S.q4_k_blocks(S.derive(seed, "o"), hidden, nq * 256), hidden),
+        "ffn_gate": (1, S.q4_k_blocks(S.derive(seed, "g"), ffn, hidden), ffn),
+        "ffn_up": (1, S.q4_k_blocks(S.derive(seed, "u"), ffn, hidden), ffn),
+        "ffn_down": (3, S.q6_k_blocks(S.derive(seed, "d"), hidden, ffn), hidden),
+        "inp_gate": (1, S.q4_k_blocks(S.derive(seed, "ig"), P, hidden), P),
+        "proj": (1, S.q4_k_blocks(S.derive(seed, "pr"), hidden, P), hidden),
+    }
+    norms = {n: (1.0 + 0.1 * rng.standard_normal(256 if n in ("attn_q_norm", "attn_k_norm") else hidden))
+             .astype(np.float32) for n in ("attn_norm", "attn_q_norm", "attn_k_norm", "post_attention_norm",
+                                           "ffn_norm", "post_ffw_norm", "post_norm")}
+    kc = rng.standard_normal((nkv, cap, 256)).astype(np.float16)
+    vc = rng.standard_normal((nkv, cap, 256)).astype(np.float16)
+
+    def make():
+        return D.Layer(weights=dict(w), norms=dict(norms), key_cache=kc.copy(), value_cache=vc.copy(),
+                       head_count=nq, head_count_kv=nkv, epsilon=eps, output_scale=0.875)
+    x = (rng.standard_normal((3, hidden)) * 4).astype(np.float32)
+    pli = rng.standard_normal((3, P)).astype(np.float32)
+    return make, x, pli, w, norms
+
+
+def test_per_layer_input_zero_input_is_the_plain_layer(D, oracle):
+    """A zero per-layer input makes mixed = 0, proj . 0 = 0 and its norm 0:
+    the layer's output equals the layer without the step, bit for bit; a
+    layer given no per-layer input skips the step."""
+    make, x, pli, _, _ = _ple_layer(D, oracle)
+    plain = D.forward_layer(make(), x, 5)
+    assert np.array_equal(D.forward_layer(make(), x, 5, np.zeros_like(pli)), plain)
+    with_input = D.forward_layer(make(), x, 5, pli)
+    assert not np.array_equal(with_input, plain)
+
+
+def test_per_layer_input_scale_invariance(D, oracle):
+    """With epsilon 0, scaling the per-layer input by a power of two scales
+    mixed, its Q8_K scales and proj's output exactly, and post_norm's rms
+    normalisation cancels it: the same bits."""
+    make, x, pli, _, _ = _ple_layer(D, oracle, eps=0.0)
+    a = D.forward_layer(make(), x, 5, pli)
+    b = D.forward_layer(make(), x, 5, pli * np.float32(4.0))
+    c = D.forward_layer(make(), x, 5, pli * np.float32(0.25))
+    assert np.array_equal(a, b) and np.array_equal(a, c)
+
+
+def test_per_layer_input_against_f64_formula(D, oracle):
+    """The step against its formula in f64 over the dequantized weights:
+    x + rmsnorm(W_proj (gelu(W_gate x) * u)) * post_norm, with gelu the
+    tanh approximation (the f16 roundings and Q8_K inputs of the reference
+    are inside the bar).  A missing gelu, a transposed weight or the input
+    applied to the wrong factor moves it by O(1)."""
+    make, x, pli, w, norms = _ple_layer(D, oracle)
+    L = make()
+    out = D.forward_layer(L, x, 5, pli)
+    x2 = L.trace["ffn_residual"].astype(np.float64)
+    Wg = oracle.dequantize(1, w["inp_gate"][1], 256 * 512).reshape(256, 512).astype(np.float64)
+    Wp = oracle.dequantize(1, w["proj"][1], 512 * 256).reshape(512, 256).astype(np.float64)
+    g = x2 @ Wg.T
+    gelu = 0.5 * g * (1 + np.tanh(np.sqrt(2 / np.pi) * (g + 0.044715 * g ** 3)))
+    p = (gelu * pli.astype(np.float64)) @ Wp.T
+    pn = p / np.sqrt(np.mean(p * p, axis=1, keepdims=True) + 1e-6) * norms["post_norm"]
+    ref = (x2 + pn) * np.float64(np.float32(0.875))
+    err = np.max(np.abs(out - ref)) / np.sqrt(np.mean(ref * ref))
+    assert err < 2e-2, err
+    # and the step's share is not negligible: without it the bar fails
+    nople = x2 * np.float64(np.float32(0.875))
+    assert np.max(np.abs(out - nople)) / np.sqrt(np.mean(ref * ref)) > 0.1
