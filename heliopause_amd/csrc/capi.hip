@@ -2579,6 +2579,20 @@ int32_t hp_hip_set_fused_trace(uint64_t *d_stamps, size_t len) {
   return HP_OK;
 }
 
+int32_t hp_hip_release_stream_scratch(void *stream) {
+  State &s = st();
+  std::lock_guard<std::recursive_mutex> lock(s.mu);
+  if (!s.ready) return HP_OK;
+  if (!stream) return fail(HP_ERR_ARG, "the library stream's scratch lives until hp_hip_shutdown");
+  hipStream_t strm = static_cast<hipStream_t>(stream);
+  hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+  HP_HIP_TRY(hipStreamIsCapturing(strm, &cs));
+  if (cs != hipStreamCaptureStatusNone) return fail(HP_ERR_ARG, "the stream is capturing");
+  HP_HIP_TRY(hipStreamSynchronize(strm));
+  s.pool.release_stream(stream);
+  return HP_OK;
+}
+
 int32_t hp_hip_decode_fused_status(void *stream) {
   State &s = st();
   std::lock_guard<std::recursive_mutex> lock(s.mu);

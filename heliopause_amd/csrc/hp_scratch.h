@@ -10,8 +10,10 @@
 //     buffers of the stream it was captured on.
 //   * A buffer that is too small is replaced by a larger one, and the old one
 //     is retired, not freed: a graph captured earlier may still point at it.
-//     Retired and live buffers are freed only by release_all()
-//     (hp_hip_shutdown).  Growth itself is refused while the stream is
+//     Retired and live buffers are freed by release_stream(stream)
+//     (hp_hip_release_stream_scratch: the caller is done with the stream and
+//     with every graph captured on it) or by release_all() (hp_hip_shutdown),
+//     never otherwise.  Growth itself is refused while the stream is
 //     capturing (the allocation would not be part of the graph), so a
 //     captured call must follow an uncaptured call of the same shape.
 // Capacities grow at least 2x, so retired memory stays below the live size.
@@ -77,7 +79,7 @@ class ScratchPool {
     }
     stats_.allocations++;
     if (b.p) {
-      retired_.push_back(b);
+      retired_.push_back(Retired{b, stream});
       stats_.retired_bytes += b.cap;
       stats_.live_bytes -= b.cap;
     }
@@ -96,6 +98,40 @@ class ScratchPool {
     return kScratchOk;
   }
 
+  // Frees the live and retired buffers of one stream.  The caller has
+  // synchronised the stream and no graph captured on it is replayed
+  // afterwards.  Returns the bytes freed.
+  uint64_t release_stream(void *stream) {
+    uint64_t freed = 0;
+    auto it = sets_.find(stream);
+    if (it != sets_.end()) {
+      for (Buf &b : it->second.buf)
+        if (b.p) {
+          alloc_.free(b.p);
+          stats_.frees++;
+          stats_.live_bytes -= b.cap;
+          freed += b.cap;
+        }
+      sets_.erase(it);
+    }
+    std::vector<Retired> keep;
+    for (Retired &r : retired_) {
+      if (r.stream == stream) {
+        alloc_.free(r.buf.p);
+        stats_.frees++;
+        stats_.retired_bytes -= r.buf.cap;
+        freed += r.buf.cap;
+      } else {
+        keep.push_back(r);
+      }
+    }
+    retired_.swap(keep);
+    return freed;
+  }
+
+  // Streams that hold buffers.
+  size_t stream_count() const { return sets_.size(); }
+
   // Frees every buffer, live and retired.  The caller has synchronised the
   // device and no graph that holds these buffers is replayed afterwards.
   void release_all() {
@@ -106,8 +142,8 @@ class ScratchPool {
           stats_.frees++;
           b = Buf();
         }
-    for (Buf &b : retired_) {
-      alloc_.free(b.p);
+    for (Retired &r : retired_) {
+      alloc_.free(r.buf.p);
       stats_.frees++;
     }
     sets_.clear();
@@ -125,9 +161,13 @@ class ScratchPool {
   struct Set {
     Buf buf[kScratchKinds];
   };
+  struct Retired {
+    Buf buf;
+    void *stream;
+  };
   Alloc alloc_;
   std::map<void *, Set> sets_;
-  std::vector<Buf> retired_;
+  std::vector<Retired> retired_;
   Stats stats_;
 };
 

@@ -148,6 +148,8 @@ def _declare_decode(L: ctypes.CDLL) -> None:
     L.hp_hip_decode_fused_status.argtypes = [vp]
     L.hp_hip_set_fused_trace.argtypes = [vp, _sz]
     L.hp_hip_set_fused_trace.restype = i32
+    L.hp_hip_release_stream_scratch.argtypes = [vp]
+    L.hp_hip_release_stream_scratch.restype = i32
     L.hp_hip_empty_launches.argtypes = [_sz, vp]
     L.hp_hip_empty_launches.restype = i32
     for name in ("hp_hip_rms_norm_device", "hp_hip_residual_norm_device", "hp_hip_attention_prep_device",
@@ -512,6 +514,12 @@ def setFusedTrace(d_stamps: int, length: int) -> None:
     """Stage timeline of the persistent decode step into a device buffer of
     uint64 stamps (0 turns it off); layout in include/hp_hip.h."""
     assertHipOk(lib().hp_hip_set_fused_trace(d_stamps or None, int(length)), "setFusedTrace")
+
+
+def releaseStreamScratch(stream: int) -> None:
+    """Frees the device scratch kept for `stream` (its work done, no graph
+    captured on it replayed later); no counterpart in the reference."""
+    assertHipOk(lib().hp_hip_release_stream_scratch(stream or None), "releaseStreamScratch")
 
 
 def emptyLaunches(count: int, stream: int = 0) -> None:

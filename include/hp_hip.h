@@ -304,6 +304,14 @@ int32_t hp_hip_device_alloc(size_t bytes, void **d_out);
 int32_t hp_hip_device_free(void *d);
 int32_t hp_hip_copy_to_device(void *d_dst, const void *src, size_t bytes, void *stream);
 int32_t hp_hip_copy_to_host(void *dst, const void *d_src, size_t bytes, void *stream);
+/* Frees the device scratch the asynchronous entry points keep for `stream`
+ * (decode activations, attention partials, top-k state, prefill images;
+ * one set per stream, grown and never freed while a graph captured on the
+ * stream may still use it).  Call once the stream's work is done and no
+ * graph captured on it will be replayed; the next call on the stream
+ * allocates anew.  Waits for the stream.  NULL (the library stream) or a
+ * capturing stream: HP_ERR_ARG.  No counterpart in the reference. */
+int32_t hp_hip_release_stream_scratch(void *stream);
 
 /* hp_hip_matmul_topk_sample on a device input ([column_count][input_size]
  * f32, 16-byte aligned, ordered on the library stream): forwardOutput's head,

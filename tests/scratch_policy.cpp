@@ -1,7 +1,7 @@
 // CPU check of the scratch policy in heliopause_amd/csrc/hp_scratch.h with a
 // recording allocator: a buffer handed out (as a captured graph would hold
-// it) stays allocated until release_all, growth is refused while capturing,
-// streams never share a buffer, and only release_all frees.
+// it) stays allocated until release_all or its stream's release_stream,
+// growth is refused while capturing, streams never share a buffer.
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
@@ -98,10 +98,30 @@ int main() {
   check(pool.get(s2, hp::kScratchDecode, 1 << 20, false, false, &f) == hp::kScratchNoMemory, "allocation failure");
   check(pool.get(s2, hp::kScratchDecode, 100, false, false, &f) == hp::kScratchOk && f == d, "old buffer kept");
   check(rec.frees == 0, "still no free before release_all");
+  // releasing one stream frees its live and retired buffers only
+  void *s3 = reinterpret_cast<void *>(0x3000), *g1 = nullptr, *g2 = nullptr;
+  check(pool.get(s3, hp::kScratchDecode, 5000, false, false, &g1) == hp::kScratchOk, "third stream");
+  check(pool.get(s3, hp::kScratchDecode, 20000, false, false, &g2) == hp::kScratchOk && g2 != g1, "third grows");
+  void *g3 = nullptr;
+  check(pool.get(s3, hp::kScratchAttn, 100, false, false, &g3) == hp::kScratchOk, "third stream, second kind");
+  const size_t streams = pool.stream_count();
+  const size_t before = rec.live.size();
+  const uint64_t freed = pool.release_stream(s3);
+  check(rec.live.size() == before - 3 && !rec.live.count(g1) && !rec.live.count(g2) && !rec.live.count(g3),
+        "release_stream frees that stream's live and retired buffers");
+  check(freed >= 5000 + 20000 + 100 && pool.stream_count() == streams - 1, "release_stream bytes and streams");
+  check(rec.live.count(a) == 1 && rec.live.count(c) == 1 && rec.live.count(d) == 1, "other streams untouched");
+  void *g4 = nullptr;
+  check(pool.get(s3, hp::kScratchDecode, 100, false, false, &g4) == hp::kScratchOk, "a released stream starts anew");
+  check(pool.release_stream(reinterpret_cast<void *>(0x9999)) == 0, "an unknown stream frees nothing");
   const size_t held = rec.live.size();
+  const int frees_before = rec.frees;
+  const uint64_t stat_frees_before = pool.stats().frees;
   pool.release_all();
-  check(rec.live.empty() && rec.frees == (int)held, "release_all frees live and retired buffers");
-  check(pool.stats().frees == (uint64_t)held && pool.stats().live_bytes == 0, "stats after release");
+  check(rec.live.empty() && rec.frees == frees_before + (int)held, "release_all frees live and retired buffers");
+  check(pool.stats().frees == stat_frees_before + held && pool.stats().live_bytes == 0 &&
+            pool.stats().retired_bytes == 0,
+        "stats after release");
   if (failures) return 1;
   std::printf("scratch policy ok\n");
   return 0;

@@ -563,3 +563,43 @@ def test_decode_layer_with_per_layer_input(hip, D, full, tokens, pos):
         assert errs.max() <= LAYER_TOL
     else:
         assert errs.max() <= 3e-2 and np.median(errs) <= 1e-4
+
+
+def test_stream_scratch_release(hip):
+    """A decode step on a side stream allocates that stream's scratch; after
+    hp_hip_release_stream_scratch the library holds what it held before, a
+    later step on the stream allocates anew and gives the same bits, and the
+    library stream's own scratch cannot be released this way."""
+    import torch
+
+    shape = _small_shape()
+    seed = S.derive(S.BASE_SEED, "stream-scratch")
+    data = DM.layer_host_data(shape, seed, 0)
+    model = DM.HipDecodeModel(shape)
+    model.add_layer(data)
+    x = S.activations(S.derive(seed, "x"), 1, shape.hidden).reshape(-1) * 4
+    dpos = _dev(np.array([5], np.int32))
+    side = torch.cuda.Stream()
+    try:
+        # a pooled stream may carry an earlier test's scratch: start from none
+        torch.cuda.synchronize()
+        hip.releaseStreamScratch(side.cuda_stream)
+        base = hip.hipResidentWeightStats()["scratchBytes"]
+        outs = []
+        for _ in range(2):
+            dx = _dev(x)
+            k0 = model.caches[0][0].clone()
+            with torch.cuda.stream(side):
+                model.run_layers(dx.data_ptr(), dpos.data_ptr(), 0, side.cuda_stream)
+            side.synchronize()
+            held = hip.hipResidentWeightStats()["scratchBytes"]
+            outs.append(dx.cpu().numpy())
+            model.caches[0][0].copy_(k0)
+            hip.releaseStreamScratch(side.cuda_stream)
+            after = hip.hipResidentWeightStats()["scratchBytes"]
+            print(f"scratch bytes: before {base}, after the step {held}, after release {after}", flush=True)
+            assert held > base and after == base
+        assert np.array_equal(outs[0].view(np.uint32), outs[1].view(np.uint32))
+        assert hip.lib().hp_hip_release_stream_scratch(None) == hip.HP_ERR_ARG
+    finally:
+        model.release()
