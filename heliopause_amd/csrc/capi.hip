@@ -2465,7 +2465,11 @@ int32_t hp_hip_decode_layers_device(const hp_hip_decode_layer_t *layers, size_t 
         pa.wk = L.d_attn_k_norm;
         pa.position = d_position;
         pa.pos_offset = (int)c0;
-        pa.q_out = qr;
+        // a prefill chunk's queries leave rounded to f16 (the attention's
+        // first step), once per query instead of once per window slice
+        const bool half_q = Mc > (size_t)kMaxTokens;
+        pa.q_out = half_q ? nullptr : qr;
+        pa.q_half = half_q ? reinterpret_cast<uint16_t *>(qr) : nullptr;
         pa.k_cache = aa.k_cache;
         pa.v_cache = aa.v_cache;
         pa.tokens = (int)Mc;
@@ -2475,7 +2479,8 @@ int32_t hp_hip_decode_layers_device(const hp_hip_decode_layer_t *layers, size_t 
         HP_HIP_TRY(launch_qkv_post(pa, strm));
         prof_end(HP_KERNEL_ATTENTION, e, strm);
         s.launches++;
-        aa.q = qr;
+        aa.q = half_q ? nullptr : qr;
+        aa.q_half = pa.q_half;
         aa.tokens = (int)Mc;
       }
       if (Mc <= (size_t)kMaxTokens) {

@@ -171,7 +171,8 @@ __global__ __launch_bounds__(256) void norm_residual_kernel(const NormArgs a) {
   }
 }
 
-// One wave per head: query heads (norm with wq, RoPE, f32 out), key heads
+// One wave per head: query heads (norm with wq, RoPE, f32 out or its f16
+// rounding for the prefill attention), key heads
 // (norm with wk, RoPE, f16 into the key cache) and value heads (norm without
 // weight, f16 into the value cache).
 __global__ __launch_bounds__(64) void qkv_post_kernel(const QkvPostArgs a) {
@@ -267,8 +268,15 @@ __global__ __launch_bounds__(64) void qkv_post_kernel(const QkvPostArgs a) {
     __syncthreads();
   }
   if (kind == 0) {
+    if (a.q_half) {
 #pragma unroll
-    for (int j = 0; j < 4; j++) a.q_out[(qrow + head) * kHeadDim + lane + 64 * j] = xs[lane + 64 * j];
+      for (int j = 0; j < 4; j++)
+        a.q_half[(qrow + head) * kHeadDim + lane + 64 * j] =
+            (uint16_t)rs_f16_bits(__builtin_bit_cast(uint32_t, xs[lane + 64 * j]));
+    } else {
+#pragma unroll
+      for (int j = 0; j < 4; j++) a.q_out[(qrow + head) * kHeadDim + lane + 64 * j] = xs[lane + 64 * j];
+    }
   } else if (pos >= 0) {  // a negative position (invalid) writes no cache entry
     const int slot = pos % a.capacity;
     _Float16 *dst = (kind == 1 ? a.k_cache : a.v_cache) + ((size_t)head * a.capacity + slot) * kHeadDim;
@@ -688,7 +696,8 @@ hipError_t launch_norm_residual(const NormArgs &a, hipStream_t s) {
 hipError_t launch_qkv_post(const QkvPostArgs &a, hipStream_t s) {
   if (a.nq < 1 || a.nkv < 1 || a.capacity < 1 || a.rope_dims < 0 || a.rope_dims > kHeadDim || (a.rope_dims & 1))
     return hipErrorInvalidValue;
-  if (a.tokens < 1 || a.tokens > kMaxChunkTokens || a.src_ks > kNormParts) return hipErrorInvalidValue;
+  if (a.tokens < 1 || a.tokens > kMaxChunkTokens || a.src_ks > kNormParts || (!a.q_out && !a.q_half))
+    return hipErrorInvalidValue;
   hipLaunchKernelGGL(qkv_post_kernel, dim3(a.nq + 2 * a.nkv, a.tokens), dim3(64), 0, s, a);
   return hipGetLastError();
 }

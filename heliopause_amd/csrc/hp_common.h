@@ -463,6 +463,9 @@ struct QkvPostArgs {
   const float *freq_factors;  // [rope_dims / 2] or null
   const int *position;
   float *q_out;
+  // non-null: the queries leave as the f16 bits of float32_to_float16, the
+  // rounding the attention applies, in place of q_out (rows as q_out's)
+  uint16_t *q_half;
   _Float16 *k_cache, *v_cache;  // [nkv][capacity][kHeadDim]
   double2 *rope_table;  // [tokens][kHeadDim / 2] cos, sin (rope_table_mode 1: written, 2: read)
   int rope_table_mode;
@@ -482,6 +485,9 @@ struct QkvPostArgs {
 // weight) and RoPE and appends the key and value at slot position % capacity.
 struct AttnArgs {
   const float *q, *k, *v;
+  // prefill attention only: non-null, the queries already rounded to f16
+  // (float32_to_float16 bits, rows as q's), read in place of q
+  const uint16_t *q_half;
   const float *wq, *wk, *freq_factors;
   _Float16 *k_cache, *v_cache;
   const int *position;
