@@ -370,9 +370,17 @@ __global__ __launch_bounds__(256) void kquant_prefill_kernel(const PfArgs a) {
 // weights the second, so lane (n, q)'s accumulator holds weight row n of the
 // segment and columns 4q .. 4q + 3 of the column set: the row's d and dmin
 // come with the lane's own header load.
+// Two waves per SIMD: measured against one wave per SIMD with 128-column
+// tiles (kF3Waves 4, kF3CS 8: 4.3 instead of 6.5 vector-ALU instructions per
+// MFMA, 374 registers), which took gate/up from 79 to 98 us on the 512-column
+// chunk: a lone wave per SIMD stalls on each block's loads and barrier.
 constexpr int kF3Waves = 8;                                          // per workgroup
-constexpr int kF3PerCU = 8 / kF3Waves;                               // workgroups per CU: two waves per SIMD
+constexpr int kF3PerSIMD = kF3Waves / 4;                             // waves per SIMD (one workgroup per CU)
+constexpr int kF3PerCU = 1;                                          // workgroups per CU
 constexpr int kF3RS = 2;                                             // 16-row segments per wave
+constexpr int kF3CS = 4;                                             // 16-column sets per wave
+constexpr int kF3Tiles = kF3CS / 4;                                  // 64-column activation tiles per work tile
+constexpr int kF3Cols = 16 * kF3CS;                                  // columns per work tile
 constexpr int kF3Threads = 64 * kF3Waves;
 constexpr int kF3Segs = kF3RS * kF3Waves;                            // segments per workgroup tile
 constexpr int kF3Full = kF2XTile / 1024;                             // whole 1 KB chunks per activation tile
@@ -504,10 +512,11 @@ __device__ __forceinline__ half8 f3_a(const typename WSel<Q4>::T &w, const uint3
 // against the activation tile at xl.  Segments past the weight's end repeat
 // the last one and are never stored.
 template <bool Q4>
-__device__ __forceinline__ void f3_block(float (&out)[kF3RS][4][4], const typename WSel<Q4>::T (&w)[kF3RS],
+__device__ __forceinline__ void f3_block(float (&out)[kF3RS][kF3CS][4], const typename WSel<Q4>::T (&w)[kF3RS],
                                          const uint8_t *xl, int lane) {
   const int n = lane & 15, q = lane >> 4;
-  const _Float16 *xh = reinterpret_cast<const _Float16 *>(xl);
+  // column set cs: 16-column slice cs % 4 of activation tile cs / 4
+  auto xh = [&](int cs) { return reinterpret_cast<const _Float16 *>(xl + (cs >> 2) * kF2XTile); };
   half2v S[kF3RS][4], N[kF3RS][4];
 #pragma unroll
   for (int rs = 0; rs < kF3RS; rs++) {
@@ -544,14 +553,15 @@ __device__ __forceinline__ void f3_block(float (&out)[kF3RS][4][4], const typena
       qd[rs][g][3] = v.w;
       f3_transpose(qd[rs][g]);
     }
-  f32x4 D[kF3RS][4];
+  f32x4 D[kF3RS][kF3CS];
   // Software pipeline over the classes: while class l's MFMAs run, class
   // l + 1's B fragments are read from LDS and its weight fragments unpacked
   // (interleaved: one MFMA, then a few vector-ALU instructions).
-  half8 B[2][4];
+  half8 B[2][kF3CS];
 #pragma unroll
-  for (int cs = 0; cs < 4; cs++)
-    B[0][cs] = __builtin_bit_cast(half8, *reinterpret_cast<const uint4 *>(xh + (q * kF2Cols + 16 * cs + n) * 8));
+  for (int cs = 0; cs < kF3CS; cs++)
+    B[0][cs] = __builtin_bit_cast(half8,
+                                  *reinterpret_cast<const uint4 *>(xh(cs) + (q * kF2Cols + 16 * (cs & 3) + n) * 8));
   half8 An[kF3RS];
 #pragma unroll
   for (int rs = 0; rs < kF3RS; rs++) An[rs] = f3_a<Q4>(w[rs], qd[rs], 0, q, S[rs], N[rs]);
@@ -562,41 +572,41 @@ __device__ __forceinline__ void f3_block(float (&out)[kF3RS][4][4], const typena
     for (int rs = 0; rs < kF3RS; rs++) A[rs] = An[rs];
     if (l < 7) {
 #pragma unroll
-      for (int cs = 0; cs < 4; cs++)
+      for (int cs = 0; cs < kF3CS; cs++)
         B[(l + 1) & 1][cs] = __builtin_bit_cast(
-            half8, *reinterpret_cast<const uint4 *>(xh + (((l + 1) * 4 + q) * kF2Cols + 16 * cs + n) * 8));
+            half8, *reinterpret_cast<const uint4 *>(xh(cs) + (((l + 1) * 4 + q) * kF2Cols + 16 * (cs & 3) + n) * 8));
 #pragma unroll
       for (int rs = 0; rs < kF3RS; rs++) An[rs] = f3_a<Q4>(w[rs], qd[rs], l + 1, q, S[rs], N[rs]);
     }
 #pragma unroll
-    for (int cs = 0; cs < 4; cs++)
+    for (int cs = 0; cs < kF3CS; cs++)
 #pragma unroll
       for (int rs = 0; rs < kF3RS; rs++)
         D[rs][cs] = mfma(B[l & 1][cs], A[rs], l == 0 ? (f32x4){0.0f, 0.0f, 0.0f, 0.0f} : D[rs][cs]);
     if (l < 7) {
-      __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);  // the 4 B reads first
+      __builtin_amdgcn_sched_group_barrier(0x100, kF3CS, 0);  // the B reads first
 #pragma unroll
-      for (int k = 0; k < 4 * kF3RS; k++) {
+      for (int k = 0; k < kF3CS * kF3RS; k++) {
         __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
         __builtin_amdgcn_sched_group_barrier(0x002, 3, 0);  // up to 3 vector-ALU
       }
     }
     __builtin_amdgcn_sched_barrier(0);
   }
-  const float *xd = reinterpret_cast<const float *>(xl + 32768 + 2048);
-  f32x4 dx[4];
+  f32x4 dx[kF3CS];
 #pragma unroll
-  for (int cs = 0; cs < 4; cs++) dx[cs] = *reinterpret_cast<const f32x4 *>(xd + 16 * cs + 4 * q);
+  for (int cs = 0; cs < kF3CS; cs++)
+    dx[cs] = *reinterpret_cast<const f32x4 *>(xl + (cs >> 2) * kF2XTile + 32768 + 2048 + 4 * (16 * (cs & 3) + 4 * q));
   if constexpr (Q4) {
     // sumi = sum_j mn_j * bsums32_j: quarter q < 2 carries k = 8q + e ->
     // (j = 4q + e/2, half e%2) against the 16 half-block sums (zero operands
     // in quarters 2, 3); out += dx * (dw * D - dmin * sumi)
-    const _Float16 *xb = reinterpret_cast<const _Float16 *>(xl + 32768);
     const bool lo = q < 2;
-    half8 bm[4];
+    half8 bm[kF3CS];
 #pragma unroll
-    for (int cs = 0; cs < 4; cs++) {
-      const uint4 v = *reinterpret_cast<const uint4 *>(xb + (((q & 1) * kF2Cols) + 16 * cs + n) * 8);
+    for (int cs = 0; cs < kF3CS; cs++) {
+      const _Float16 *xb = reinterpret_cast<const _Float16 *>(xl + (cs >> 2) * kF2XTile + 32768);
+      const uint4 v = *reinterpret_cast<const uint4 *>(xb + (((q & 1) * kF2Cols) + 16 * (cs & 3) + n) * 8);
       bm[cs] = __builtin_bit_cast(half8, lo ? v : make_uint4(0, 0, 0, 0));
     }
     // each stage over all 16 sums of a segment before the next, so the
@@ -609,20 +619,20 @@ __device__ __forceinline__ void f3_block(float (&out)[kF3RS][4][4], const typena
       const uint32_t mn = q == 0 ? mn0 : mn1;
       half8 am = cat(dup_byte(mn, 0, 1024.0f), dup_byte(mn, 1, 1024.0f), dup_byte(mn, 2, 1024.0f),
                      dup_byte(mn, 3, 1024.0f));
-      f32x4 sm[4];
+      f32x4 sm[kF3CS];
 #pragma unroll
-      for (int cs = 0; cs < 4; cs++) sm[cs] = mfma(bm[cs], am, (f32x4){0.0f, 0.0f, 0.0f, 0.0f});
-      float t[4][4];
+      for (int cs = 0; cs < kF3CS; cs++) sm[cs] = mfma(bm[cs], am, (f32x4){0.0f, 0.0f, 0.0f, 0.0f});
+      float t[kF3CS][4];
 #pragma unroll
-      for (int cs = 0; cs < 4; cs++)
+      for (int cs = 0; cs < kF3CS; cs++)
 #pragma unroll
         for (int j = 0; j < 4; j++) t[cs][j] = dw * D[rs][cs][j];
 #pragma unroll
-      for (int cs = 0; cs < 4; cs++)
+      for (int cs = 0; cs < kF3CS; cs++)
 #pragma unroll
         for (int j = 0; j < 4; j++) t[cs][j] = __builtin_fmaf(-dmw, sm[cs][j], t[cs][j]);
 #pragma unroll
-      for (int cs = 0; cs < 4; cs++)
+      for (int cs = 0; cs < kF3CS; cs++)
 #pragma unroll
         for (int j = 0; j < 4; j++) out[rs][cs][j] = __builtin_fmaf(dx[cs][j], t[cs][j], out[rs][cs][j]);
     }
@@ -630,13 +640,13 @@ __device__ __forceinline__ void f3_block(float (&out)[kF3RS][4][4], const typena
 #pragma unroll
     for (int rs = 0; rs < kF3RS; rs++) {
       const float dw = h2f_bits(w[rs].d16);
-      float t[4][4];
+      float t[kF3CS][4];
 #pragma unroll
-      for (int cs = 0; cs < 4; cs++)
+      for (int cs = 0; cs < kF3CS; cs++)
 #pragma unroll
         for (int j = 0; j < 4; j++) t[cs][j] = dw * D[rs][cs][j];
 #pragma unroll
-      for (int cs = 0; cs < 4; cs++)
+      for (int cs = 0; cs < kF3CS; cs++)
 #pragma unroll
         for (int j = 0; j < 4; j++) out[rs][cs][j] = __builtin_fmaf(dx[cs][j], t[cs][j], out[rs][cs][j]);
     }
@@ -657,24 +667,29 @@ __device__ __forceinline__ void f3_wloads(typename WSel<Q4>::T (&w)[kF3RS], cons
 // The two activation-tile stages.  Two distinct arrays, so the compiler sees
 // that a direct global->LDS copy into one does not touch reads of the other
 // and issues no wait for it.
-__shared__ __align__(16) uint8_t f3_st0[kF2XTile];
-__shared__ __align__(16) uint8_t f3_st1[kF2XTile];
+__shared__ __align__(16) uint8_t f3_st0[kF3Tiles * kF2XTile];
+__shared__ __align__(16) uint8_t f3_st1[kF3Tiles * kF2XTile];
 
-// Copies activation tile b into a stage with direct global->LDS loads (1 KB
-// per wave and load; chunk c by wave c % kF3Waves).  Branch-free: chunk
-// indices past the end repeat the last whole chunk (the same bytes to the
-// same place).
-__device__ __forceinline__ void f3_xcopy(const uint8_t *xt, int b, uint8_t *stage, int wave, int lane) {
-  const uint8_t *src = xt + (size_t)b * kF2XTile;
+// Copies block b of the work tile's activation tiles (xt[i], i < kF3Tiles)
+// into a stage with direct global->LDS loads (1 KB per wave and load;
+// chunk c of a tile by wave c % kF3Waves).  Branch-free: chunk indices past
+// the end repeat the last whole chunk (the same bytes to the same place).
+__device__ __forceinline__ void f3_xcopy(const uint8_t *const (&xt)[kF3Tiles], int b, uint8_t *stage, int wave,
+                                         int lane) {
 #pragma unroll
-  for (int i = 0; i < (kF3Full + kF3Waves - 1) / kF3Waves; i++) {
-    const int c = min(wave + i * kF3Waves, kF3Full - 1);
-    __builtin_amdgcn_global_load_lds(reinterpret_cast<const void *>(src + c * 1024 + 16 * lane),
-                                     (__attribute__((address_space(3))) void *)(stage + c * 1024), 16, 0, 0);
+  for (int t = 0; t < kF3Tiles; t++) {
+    const uint8_t *src = xt[t] + (size_t)b * kF2XTile;
+    uint8_t *dst = stage + t * kF2XTile;
+#pragma unroll
+    for (int i = 0; i < (kF3Full + kF3Waves - 1) / kF3Waves; i++) {
+      const int c = min(wave + i * kF3Waves, kF3Full - 1);
+      __builtin_amdgcn_global_load_lds(reinterpret_cast<const void *>(src + c * 1024 + 16 * lane),
+                                       (__attribute__((address_space(3))) void *)(dst + c * 1024), 16, 0, 0);
+    }
+    if (wave == kF3Full % kF3Waves && 16 * lane < kF3Part)
+      __builtin_amdgcn_global_load_lds(reinterpret_cast<const void *>(src + kF3Full * 1024 + 16 * lane),
+                                       (__attribute__((address_space(3))) void *)(dst + kF3Full * 1024), 16, 0, 0);
   }
-  if (wave == kF3Full % kF3Waves && 16 * lane < kF3Part)
-    __builtin_amdgcn_global_load_lds(reinterpret_cast<const void *>(src + kF3Full * 1024 + 16 * lane),
-                                     (__attribute__((address_space(3))) void *)(stage + kF3Full * 1024), 16, 0, 0);
 }
 
 // Blocks [b0, b1) of one tile for this wave's segments from s0 of weight
@@ -683,8 +698,8 @@ __device__ __forceinline__ void f3_xcopy(const uint8_t *xt, int b, uint8_t *stag
 // never sit behind a branch; every copy has landed (vmcnt(0)) before the
 // barrier that ends its block.
 template <bool Q4>
-__device__ __forceinline__ void f3_tile(float (&out)[kF3RS][4][4], const uint8_t *wseg, int wtiles, int s0,
-                                        const uint8_t *xt, int b0, int b1) {
+__device__ __forceinline__ void f3_tile(float (&out)[kF3RS][kF3CS][4], const uint8_t *wseg, int wtiles, int s0,
+                                        const uint8_t *const (&xt)[kF3Tiles], int b0, int b1) {
   if (b1 <= b0) return;  // (block ranges hold at least two blocks)
   const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   typename WSel<Q4>::T wa[kF3RS], wb[kF3RS];
@@ -723,14 +738,14 @@ __device__ __forceinline__ int f3_order(int it, int total) {
   return base + (x < rem ? x * (per + 1) + j : rem * (per + 1) + (x - rem) * per + j);
 }
 
-constexpr int kF3WaveFloats = kF3RS * 16 * 64;  // a wave's sums (out) of one tile
+constexpr int kF3WaveFloats = kF3RS * kF3CS * 4 * 64;  // a wave's sums (out) of one tile
 
-// kF3PerCU workgroups per CU, two waves per SIMD in all.  PAIR: a tile is kF3Segs / 2 segments of gate (the first
+// kF3PerCU workgroups per CU, kF3PerSIMD waves per SIMD in all.  PAIR: a tile is kF3Segs / 2 segments of gate (the first
 // half of the waves) and the same rows of up (the second half); up's sums go
 // through LDS to the gate wave of the same rows, which stores
 // fround(gelu(gate) * up).  total_rt then counts those tiles, ksplit is 1.
 template <bool PAIR>
-__global__ __launch_bounds__(kF3Threads) __attribute__((amdgpu_waves_per_eu(2, 2))) void
+__global__ __launch_bounds__(kF3Threads) __attribute__((amdgpu_waves_per_eu(kF3PerSIMD, kF3PerSIMD))) void
 kquant_prefill_fast_kernel(
     const F2Args a) {
   kernarg_warm<F2Args>();
@@ -767,14 +782,19 @@ kquant_prefill_fast_kernel(
     const int my_seg = kF3RS * (PAIR ? wave % kHalf : wave);  // within this wave's weight
     const int nseg = nseg_tile - my_seg;                       // this wave's live segments (<= 0: none)
     const uint8_t *wseg = PAIR && wave >= kHalf ? a.w[1].seg : W.seg;
-    float out[kF3RS][4][4];
+    float out[kF3RS][kF3CS][4];
 #pragma unroll
     for (int rs = 0; rs < kF3RS; rs++)
 #pragma unroll
-      for (int cs = 0; cs < 4; cs++)
+      for (int cs = 0; cs < kF3CS; cs++)
 #pragma unroll
         for (int j = 0; j < 4; j++) out[rs][cs][j] = 0.0f;
-    const uint8_t *xt = a.xt + (size_t)ct * a.nb * kF2XTile;
+    // the work tile's 64-column activation tiles; one past the input's last
+    // re-reads the last (its columns are never stored)
+    const int xtiles = (a.cols + kF2Cols - 1) / kF2Cols;
+    const uint8_t *xt[kF3Tiles];
+#pragma unroll
+    for (int t = 0; t < kF3Tiles; t++) xt[t] = a.xt + (size_t)min(ct * kF3Tiles + t, xtiles - 1) * a.nb * kF2XTile;
     if (W.type == kTypeQ4K)
       f3_tile<true>(out, wseg, W.tiles, T0 + my_seg, xt, b_begin, b_end);
     else
@@ -785,20 +805,20 @@ kquant_prefill_fast_kernel(
 #pragma unroll
       for (int rs = 0; rs < kF3RS; rs++)
 #pragma unroll
-        for (int cs = 0; cs < 4; cs++)
+        for (int cs = 0; cs < kF3CS; cs++)
 #pragma unroll
-          for (int j = 0; j < 4; j++) part[((rs * 4 + cs) * 4 + j) * 64] = out[rs][cs][j];
+          for (int j = 0; j < 4; j++) part[((rs * kF3CS + cs) * 4 + j) * 64] = out[rs][cs][j];
     } else if (PAIR) {
       // up waves hand their sums to the gate wave of the same rows (the
       // stages are free: the tile's last barrier has passed)
-      float *xch = reinterpret_cast<float *>(f3_st0) + (wave % kHalf) * (kF3RS * 16) * 64 + lane;
+      float *xch = reinterpret_cast<float *>(f3_st0) + (wave % kHalf) * kF3WaveFloats + lane;
       if (wave >= kHalf) {
 #pragma unroll
         for (int rs = 0; rs < kF3RS; rs++)
 #pragma unroll
-          for (int cs = 0; cs < 4; cs++)
+          for (int cs = 0; cs < kF3CS; cs++)
 #pragma unroll
-            for (int j = 0; j < 4; j++) xch[((rs * 4 + cs) * 4 + j) * 64] = out[rs][cs][j];
+            for (int j = 0; j < 4; j++) xch[((rs * kF3CS + cs) * 4 + j) * 64] = out[rs][cs][j];
       }
       __syncthreads();
       if (wave < kHalf && nseg > 0) {
@@ -806,11 +826,11 @@ kquant_prefill_fast_kernel(
         for (int rs = 0; rs < kF3RS; rs++) {
           const int row = 16 * (T0 + my_seg + rs) + n;
 #pragma unroll
-          for (int cs = 0; cs < 4; cs++)
+          for (int cs = 0; cs < kF3CS; cs++)
 #pragma unroll
             for (int j = 0; j < 4; j++) {
-              const int m = ct * kF2Cols + 16 * cs + 4 * q + j;
-              const float up = xch[((rs * 4 + cs) * 4 + j) * 64];
+              const int m = ct * kF3Cols + 16 * cs + 4 * q + j;
+              const float up = xch[((rs * kF3CS + cs) * 4 + j) * 64];
               if (rs < nseg && row < W.rows && m < a.cols)
                 a.pair_out[(size_t)m * W.rows + row] = geglu_lut(out[rs][cs][j], up, a.gelu_lut);
             }
@@ -822,10 +842,10 @@ kquant_prefill_fast_kernel(
       for (int rs = 0; rs < kF3RS; rs++) {
         const int row = 16 * (T0 + my_seg + rs) + n;
 #pragma unroll
-        for (int cs = 0; cs < 4; cs++)
+        for (int cs = 0; cs < kF3CS; cs++)
 #pragma unroll
           for (int j = 0; j < 4; j++) {
-            const int m = ct * kF2Cols + 16 * cs + 4 * q + j;
+            const int m = ct * kF3Cols + 16 * cs + 4 * q + j;
             if (rs < nseg && row < W.rows && m < a.cols) dst[(size_t)m * W.rows + row] = out[rs][cs][j];
           }
       }
@@ -840,17 +860,18 @@ __global__ __launch_bounds__(256) void f2_geglu_tail_kernel(const F2Args a, int 
   kernarg_warm<F2Args>();
   constexpr int kHalf = kF3Waves / 2;
   const int t = blockIdx.x * blockDim.x + threadIdx.x;
-  const int lane = t & 63, k = (t >> 6) % (kF3RS * 16), w = (t >> 6) / (kF3RS * 16) % kHalf;
-  const int i = (t >> 6) / (kF3RS * 16) / kHalf;
+  constexpr int kSums = kF3RS * kF3CS * 4;  // a lane's sums
+  const int lane = t & 63, k = (t >> 6) % kSums, w = (t >> 6) / kSums % kHalf;
+  const int i = (t >> 6) / kSums / kHalf;
   if (i >= rem) return;
-  const int rs = k >> 4, cs = (k >> 2) & 3, j = k & 3;  // k = (rs * 4 + cs) * 4 + j
+  const int rs = k / (kF3CS * 4), cs = (k >> 2) % kF3CS, j = k & 3;  // k = (rs * kF3CS + cs) * 4 + j
   const int nat = a.tail_full + i, rt = nat / a.col_tiles, ct = nat - rt * a.col_tiles;
   const PfWeight &W = a.w[0];
   constexpr int kTileSegs = kF3Segs / 2;
   const int T0 = kTileSegs * rt, my_seg = kF3RS * w;
   const int nseg = (W.tiles - T0 < kTileSegs ? W.tiles - T0 : kTileSegs) - my_seg;
   const int n = lane & 15, q = lane >> 4;
-  const int row = 16 * (T0 + my_seg + rs) + n, m = ct * kF2Cols + 16 * cs + 4 * q + j;
+  const int row = 16 * (T0 + my_seg + rs) + n, m = ct * kF3Cols + 16 * cs + 4 * q + j;
   if (rs >= nseg || row >= W.rows || m >= a.cols) return;
   const float *p0 = a.tail_part + (size_t)(2 * i) * kF3Waves * kF3WaveFloats + k * 64 + lane;
   const float *p1 = p0 + (size_t)kF3Waves * kF3WaveFloats;
@@ -907,7 +928,7 @@ int f2_ksplit(int tiles, int nb, int slots) {
 }
 
 struct F2Shape {
-  int nb, col_tiles, total_rt, ks;
+  int nb, col_tiles, xtiles, total_rt, ks;  // col_tiles of kF3Cols, xtiles of kF2Cols
   size_t outs;    // floats of all outputs
   size_t stride;  // floats between block ranges' partial sums (16-byte multiple)
 };
@@ -915,7 +936,8 @@ struct F2Shape {
 F2Shape f2_shape(const MfmaLaunch &l, int num_cus) {
   F2Shape sh{};
   sh.nb = l.k / kQK;
-  sh.col_tiles = (l.cols + kF2Cols - 1) / kF2Cols;
+  sh.col_tiles = (l.cols + kF3Cols - 1) / kF3Cols;
+  sh.xtiles = (l.cols + kF2Cols - 1) / kF2Cols;
   for (int i = 0; i < l.count; i++) {
     sh.total_rt += ((l.rows[i] + 15) / 16 + kF3Segs - 1) / kF3Segs;
     sh.outs += (size_t)l.cols * l.rows[i];
@@ -947,13 +969,14 @@ size_t prefill_lds_bytes() { return kPfLds; }
 // columns), the grid, and where the trailing items start when fewer than
 // half a round of them remain (0: none split).
 struct F2Pair {
-  int nb, col_tiles, total_rt, items, grid, tail_full;
+  int nb, col_tiles, xtiles, total_rt, items, grid, tail_full;  // col_tiles of kF3Cols, xtiles of kF2Cols
 };
 
 F2Pair f2_pair(const MfmaLaunch &l, int num_cus) {
   F2Pair p{};
   p.nb = l.k / kQK;
-  p.col_tiles = (l.cols + kF2Cols - 1) / kF2Cols;
+  p.col_tiles = (l.cols + kF3Cols - 1) / kF3Cols;
+  p.xtiles = (l.cols + kF2Cols - 1) / kF2Cols;
   p.total_rt = ((l.rows[0] + 15) / 16 + kF3Segs / 2 - 1) / (kF3Segs / 2);
   p.items = p.total_rt * p.col_tiles;
   p.grid = p.items < kF3PerCU * num_cus ? p.items : kF3PerCU * num_cus;
@@ -966,7 +989,7 @@ int prefill_fast_geglu_launches(const MfmaLaunch &l, int num_cus) { return f2_pa
 
 size_t prefill_fast_geglu_bytes(const MfmaLaunch &l, int num_cus) {
   const F2Pair p = f2_pair(l, num_cus);
-  const size_t xt = (size_t)p.col_tiles * p.nb * kF2XTile;
+  const size_t xt = (size_t)p.xtiles * p.nb * kF2XTile;
   const size_t tail = p.tail_full ? (size_t)2 * (p.items - p.tail_full) * kF3Waves * kF3WaveFloats * sizeof(float) : 0;
   return xt + tail;
 }
@@ -979,7 +1002,7 @@ hipError_t launch_prefill_fast_geglu(const MfmaLaunch &l, const float *x, uint8_
   const int nb = p.nb, col_tiles = p.col_tiles;
   hipError_t e;
   if (!tiles_ready) {
-    hipLaunchKernelGGL(q8k_prefill_tiles16_kernel, dim3(nb, col_tiles * kF2Cols / 16), dim3(256), 0, s, x, l.k, nb,
+    hipLaunchKernelGGL(q8k_prefill_tiles16_kernel, dim3(nb, p.xtiles * kF2Cols / 16), dim3(256), 0, s, x, l.k, nb,
                        l.cols, scratch);
     e = hipGetLastError();
     if (e != hipSuccess) return e;
@@ -1003,7 +1026,7 @@ hipError_t launch_prefill_fast_geglu(const MfmaLaunch &l, const float *x, uint8_
   a.pair_out = out;
   a.gelu_lut = gelu_lut;
   a.tail_full = p.tail_full;
-  a.tail_part = reinterpret_cast<float *>(scratch + (size_t)col_tiles * nb * kF2XTile);
+  a.tail_part = reinterpret_cast<float *>(scratch + (size_t)p.xtiles * nb * kF2XTile);
   hipLaunchKernelGGL(kquant_prefill_fast_kernel<true>, dim3(p.grid), dim3(kF3Threads), 0, s, a);
   if (!p.tail_full) return hipGetLastError();
   e = hipGetLastError();
@@ -1017,11 +1040,11 @@ int prefill_fast_launches(const MfmaLaunch &l, int num_cus) { return f2_shape(l,
 
 size_t prefill_fast_bytes(const MfmaLaunch &l, int num_cus) {
   const F2Shape sh = f2_shape(l, num_cus);
-  const size_t xt = (size_t)sh.col_tiles * sh.nb * kF2XTile;
+  const size_t xt = (size_t)sh.xtiles * sh.nb * kF2XTile;
   return xt + (sh.ks > 1 ? (size_t)sh.ks * sh.stride * sizeof(float) : 0);
 }
 
-size_t prefill_fast_lds_bytes() { return 2 * (size_t)kF2XTile; }  // the two static stages
+size_t prefill_fast_lds_bytes() { return 2 * (size_t)kF3Tiles * kF2XTile; }  // the two static stages
 
 size_t prefill_fast_part_bytes(const MfmaLaunch &l, int num_cus) {
   const F2Shape sh = f2_shape(l, num_cus);
@@ -1035,7 +1058,7 @@ hipError_t launch_prefill_fast(const MfmaLaunch &l, const float *x, uint8_t *scr
   const int nb = sh.nb, col_tiles = sh.col_tiles;
   hipError_t e;
   if (!tiles_ready) {
-    hipLaunchKernelGGL(q8k_prefill_tiles16_kernel, dim3(nb, col_tiles * kF2Cols / 16), dim3(256), 0, s, x, l.k, nb,
+    hipLaunchKernelGGL(q8k_prefill_tiles16_kernel, dim3(nb, sh.xtiles * kF2Cols / 16), dim3(256), 0, s, x, l.k, nb,
                        l.cols, scratch);
     e = hipGetLastError();
     if (e != hipSuccess) return e;
@@ -1061,7 +1084,7 @@ hipError_t launch_prefill_fast(const MfmaLaunch &l, const float *x, uint8_t *scr
   a.cols = l.cols;
   a.xt = scratch;
   a.ksplit = sh.ks;
-  a.part = reinterpret_cast<float *>(scratch + (size_t)col_tiles * nb * kF2XTile);
+  a.part = reinterpret_cast<float *>(scratch + (size_t)sh.xtiles * nb * kF2XTile);
   a.part_stride = sh.stride;
   const bool deferred = defer && prefill_fast_part_bytes(l, num_cus) > 0;
   if (defer) {
