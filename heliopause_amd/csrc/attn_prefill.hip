@@ -48,6 +48,7 @@
 // values then cross from HBM once per slice instead of once per block.
 #include "hp_attn.h"
 #include "hp_common.h"
+#include "hp_f2tile.h"
 #include "hp_gelu.h"
 #include "hp_mfma.h"
 #include "hp_wave.h"
@@ -334,47 +335,76 @@ __global__ __launch_bounds__(256, 2) void attn_prefill_kernel(const AttnArgs a, 
   }
 }
 
-// The slices of one (token, query head): lane i merges dims 4 i .. 4 i + 3,
+// The slices of one (token, query head) per wave, four heads of a token per
+// workgroup: lane i merges dims 4 i .. 4 i + 3,
 // o = sum_c exp(m_c - m) o_c / sum_c exp(m_c - m) l_c with m the largest m_c,
 // then castF16Rows (a row with no key in its window is 0).  Every slice's
 // loads are issued before the first sum (one memory round trip per row).
-__global__ __launch_bounds__(64) void attn_merge_slices_kernel(const AttnArgs a) {
-  const int qh = blockIdx.x, tok = blockIdx.y, lane = threadIdx.x;
-  const int G = a.nq / a.nkv, g = qh / G, h = qh - g * G;
-  const size_t row0 = ((size_t)tok * a.nkv + g) * a.chunks * kAttnMaxGroup + h;  // slice c at row0 + c * 8
-  float mc[kAttnPrefillMaxRanges], lc[kAttnPrefillMaxRanges];
-  float4 oc[kAttnPrefillMaxRanges];
+// With a.o_tiles the four rows also leave as Q8_K activation tiles of the
+// next projection: wave 0's 16-lane row r quantises head 4 blockIdx.x + r
+// as q8k_prefill_tiles16_kernel would from the stored rows (the same f32
+// values, the same element order), and workgroups past the last token
+// write the padding columns as zeros.
+__global__ __launch_bounds__(256) void attn_merge_slices_kernel(const AttnArgs a) {
+  __shared__ float4 rows[4][kHeadDim / 4];
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int qh = 4 * blockIdx.x + wave, tok = blockIdx.y;
+  float4 res = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+  if (qh < a.nq && tok < a.tokens) {
+    const int G = a.nq / a.nkv, g = qh / G, h = qh - g * G;
+    const size_t row0 = ((size_t)tok * a.nkv + g) * a.chunks * kAttnMaxGroup + h;  // slice c at row0 + c * 8
+    float mc[kAttnPrefillMaxRanges], lc[kAttnPrefillMaxRanges];
+    float4 oc[kAttnPrefillMaxRanges];
 #pragma unroll
-  for (int c = 0; c < kAttnPrefillMaxRanges; c++) {
-    if (c < a.chunks) {
-      const size_t r = row0 + (size_t)c * kAttnMaxGroup;
-      mc[c] = a.part_m[r];
-      lc[c] = a.part_l[r];
-      oc[c] = *reinterpret_cast<const float4 *>(a.part_o + r * kHeadDim + 4 * lane);
+    for (int c = 0; c < kAttnPrefillMaxRanges; c++) {
+      if (c < a.chunks) {
+        const size_t r = row0 + (size_t)c * kAttnMaxGroup;
+        mc[c] = a.part_m[r];
+        lc[c] = a.part_l[r];
+        oc[c] = *reinterpret_cast<const float4 *>(a.part_o + r * kHeadDim + 4 * lane);
+      }
+    }
+    float m = -__builtin_inff();
+#pragma unroll
+    for (int c = 0; c < kAttnPrefillMaxRanges; c++)
+      if (c < a.chunks) m = fmaxf(m, mc[c]);
+    float l = 0.0f, o[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int c = 0; c < kAttnPrefillMaxRanges; c++) {
+      if (c < a.chunks) {
+        const float f = mc[c] == -__builtin_inff() ? 0.0f : expf(mc[c] - m);
+        l = __builtin_fmaf(f, lc[c], l);
+        o[0] = __builtin_fmaf(f, oc[c].x, o[0]);
+        o[1] = __builtin_fmaf(f, oc[c].y, o[1]);
+        o[2] = __builtin_fmaf(f, oc[c].z, o[2]);
+        o[3] = __builtin_fmaf(f, oc[c].w, o[3]);
+      }
+    }
+    res.x = l > 0.0f ? ts_f16_round(o[0] / l) : 0.0f;
+    res.y = l > 0.0f ? ts_f16_round(o[1] / l) : 0.0f;
+    res.z = l > 0.0f ? ts_f16_round(o[2] / l) : 0.0f;
+    res.w = l > 0.0f ? ts_f16_round(o[3] / l) : 0.0f;
+    *reinterpret_cast<float4 *>(a.out + ((size_t)tok * a.nq + qh) * kHeadDim + 4 * lane) = res;
+  }
+  if (!a.o_tiles) return;  // the same for the whole workgroup
+  rows[wave][lane] = res;
+  __syncthreads();
+  if (wave == 0) {
+    // row r, lane i16 = 2j + u: elements 32 j + 8 c + 4 u .. + 3 (load_x16's order)
+    const int r = lane >> 4, i16 = lane & 15, j = i16 >> 1, u = i16 & 1, hb = 4 * blockIdx.x + r;
+    if (hb < a.nq) {
+      float v[16];
+#pragma unroll
+      for (int c = 0; c < 4; c++) {
+        const float4 f = rows[r][8 * j + 2 * c + u];
+        v[4 * c] = f.x;
+        v[4 * c + 1] = f.y;
+        v[4 * c + 2] = f.z;
+        v[4 * c + 3] = f.w;
+      }
+      f2_tile_store16(v, i16, a.o_tiles + ((size_t)(tok / kF2Cols) * a.nq + hb) * kF2XTile, tok % kF2Cols);
     }
   }
-  float m = -__builtin_inff();
-#pragma unroll
-  for (int c = 0; c < kAttnPrefillMaxRanges; c++)
-    if (c < a.chunks) m = fmaxf(m, mc[c]);
-  float l = 0.0f, o[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-  for (int c = 0; c < kAttnPrefillMaxRanges; c++) {
-    if (c < a.chunks) {
-      const float f = mc[c] == -__builtin_inff() ? 0.0f : expf(mc[c] - m);
-      l = __builtin_fmaf(f, lc[c], l);
-      o[0] = __builtin_fmaf(f, oc[c].x, o[0]);
-      o[1] = __builtin_fmaf(f, oc[c].y, o[1]);
-      o[2] = __builtin_fmaf(f, oc[c].z, o[2]);
-      o[3] = __builtin_fmaf(f, oc[c].w, o[3]);
-    }
-  }
-  float4 res;
-  res.x = l > 0.0f ? ts_f16_round(o[0] / l) : 0.0f;
-  res.y = l > 0.0f ? ts_f16_round(o[1] / l) : 0.0f;
-  res.z = l > 0.0f ? ts_f16_round(o[2] / l) : 0.0f;
-  res.w = l > 0.0f ? ts_f16_round(o[3] / l) : 0.0f;
-  *reinterpret_cast<float4 *>(a.out + ((size_t)tok * a.nq + qh) * kHeadDim + 4 * lane) = res;
 }
 
 }  // namespace
@@ -410,7 +440,8 @@ hipError_t launch_attention_prefill(AttnArgs a, float *partials, int ranges, hip
   hipLaunchKernelGGL(attn_prefill_kernel, dim3(per_xcd * kXcds), dim3(256), 0, s, a, blocks, items);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
-  hipLaunchKernelGGL(attn_merge_slices_kernel, dim3(a.nq, a.tokens), dim3(kHeadDim / 4), 0, s, a);
+  const int merge_cols = a.o_tiles ? (a.tokens + kF2Cols - 1) / kF2Cols * kF2Cols : a.tokens;
+  hipLaunchKernelGGL(attn_merge_slices_kernel, dim3((a.nq + 3) / 4, merge_cols), dim3(256), 0, s, a);
   return hipGetLastError();
 }
 

@@ -462,7 +462,8 @@ bool image_input_ok(size_t count, Handle *const *hs, size_t cols) {
 int32_t run_matvec(size_t count, Handle *const *hs, const float *d_input, size_t input_size, size_t cols,
                    float *const *d_outs, hipStream_t stream, const NormIn *norm = nullptr,
                    float *norm_scratch = nullptr, uint8_t *img_scratch = nullptr, const uint8_t *q8img_in = nullptr,
-                   const PrefillParts *norm_parts = nullptr, PrefillParts *defer = nullptr) {
+                   const PrefillParts *norm_parts = nullptr, PrefillParts *defer = nullptr,
+                   bool tiles_in = false) {
   if (defer) defer->ks = 1;
   State &s = st();
   if (cols == 0) return HP_OK;
@@ -490,7 +491,9 @@ int32_t run_matvec(size_t count, Handle *const *hs, const float *d_input, size_t
     if (rc != HP_OK) return rc;
     pre = static_cast<uint8_t *>(p);
   }
-  bool tiles_ready = false;  // the norm kernel wrote the fast prefill's tiles
+  // the norm kernel below, or the producer of d_input (tiles_in: the prefill
+  // attention's slice merge), wrote the fast prefill's tiles
+  bool tiles_ready = tiles_in && kind == 2 && input_size % kQK == 0;
   const bool y_split = norm_parts && norm_parts->ks > 1;  // the norm's y as partial sums
   if (norm && (y_split || (wide ? !wide_norm : !norm_prologue_ok(count, hs, cols)))) {
     uint8_t *img = image_ok && img_scratch ? img_scratch : nullptr;
@@ -2483,11 +2486,28 @@ int32_t hp_hip_decode_layers_device(const hp_hip_decode_layer_t *layers, size_t 
         aa.q_half = pa.q_half;
         aa.tokens = (int)Mc;
       }
+      bool o_tiles = false;  // the attention left O's activation tiles
       if (Mc <= (size_t)kMaxTokens) {
         rc = run_attention(aa, part, strm);
       } else {
         const int ranges = attn_prefill_ranges((int)Mc, L.attention.head_count, L.attention.head_count_kv,
                                                L.attention.capacity, s.num_cus);
+        // O on the fast prefill kernel: the slice merge writes its
+        // activation tiles into O's prefill scratch (the pre-pass launch
+        // they replace would write the same bytes there)
+        if (prefill_kind(Mc, f16_ok(1, &H.o)) == 2 && H.o->input_size % kQK == 0 &&
+            H.o->input_size == (size_t)L.attention.head_count * kHeadDim) {
+          MfmaLaunch lo{};
+          lo.count = 1;
+          lo.k = (int)H.o->input_size;
+          lo.cols = (int)Mc;
+          lo.rows[0] = (int)H.o->row_count;
+          void *pre = nullptr;
+          rc = stream_scratch(strm, kScratchPrefill, prefill_fast_bytes(lo, s.num_cus), &pre);
+          if (rc != HP_OK) return rc;
+          aa.o_tiles = static_cast<uint8_t *>(pre);
+          o_tiles = true;
+        }
         hipEvent_t e = prof_begin(strm);
         HP_HIP_TRY(launch_attention_prefill(aa, part, ranges, strm));
         prof_end(HP_KERNEL_ATTENTION, e, strm);
@@ -2498,7 +2518,7 @@ int32_t hp_hip_decode_layers_device(const hp_hip_decode_layer_t *layers, size_t 
       float *oo[1] = {o};
       const bool defer = H.o->row_count == hidden;
       rc = run_matvec(1, oh, att, H.o->input_size, Mc, oo, strm, nullptr, nullptr, nullptr, nullptr, nullptr,
-                      defer ? &op : nullptr);
+                      defer ? &op : nullptr, o_tiles);
       if (rc != HP_OK) return rc;
       if (!defer) op.ks = 1;
       NormIn fin{};

@@ -488,6 +488,11 @@ struct AttnArgs {
   // prefill attention only: non-null, the queries already rounded to f16
   // (float32_to_float16 bits, rows as q's), read in place of q
   const uint16_t *q_half;
+  // prefill attention only: non-null, the slice merge also writes out as
+  // the fast prefill kernel's activation tiles (hp_f2tile.h; K = nq * 256,
+  // whole 64-column tiles, padding columns as zeros), the next projection's
+  // input
+  uint8_t *o_tiles;
   const float *wq, *wk, *freq_factors;
   _Float16 *k_cache, *v_cache;
   const int *position;
