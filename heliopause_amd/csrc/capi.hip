@@ -90,6 +90,7 @@ struct State {
   // pre-quantised input images between the launches of a draft step (a
   // test switch: off, every vector-ALU launch quantises its own input)
   bool images = true;
+  bool prefill_folds = true;  // hp_hip_set_prefill_folds
   bool profiling = false;
   ProfileSlot prof[HP_KERNEL_COUNT];
   std::vector<hipEvent_t> event_pool;
@@ -493,11 +494,11 @@ int32_t run_matvec(size_t count, Handle *const *hs, const float *d_input, size_t
   }
   // the norm kernel below, or the producer of d_input (tiles_in: the prefill
   // attention's slice merge), wrote the fast prefill's tiles
-  bool tiles_ready = tiles_in && kind == 2 && input_size % kQK == 0;
+  bool tiles_ready = s.prefill_folds && tiles_in && kind == 2 && input_size % kQK == 0;
   const bool y_split = norm_parts && norm_parts->ks > 1;  // the norm's y as partial sums
   if (norm && (y_split || (wide ? !wide_norm : !norm_prologue_ok(count, hs, cols)))) {
     uint8_t *img = image_ok && img_scratch ? img_scratch : nullptr;
-    tiles_ready = kind == 2 && input_size % kQK == 0;
+    tiles_ready = s.prefill_folds && kind == 2 && input_size % kQK == 0;
     int32_t rc = run_norm(norm->y, (int)cols, (int)input_size, norm->w_post, norm->mode == 2 ? norm->x_res : nullptr,
                           norm->scale, norm->x_out, norm->w_next, norm_scratch, norm->eps, stream, img,
                           tiles_ready ? pre : nullptr, norm_parts);
@@ -661,7 +662,7 @@ int32_t run_matvec_geglu(Handle *hg, Handle *hu, const float *d_input, size_t in
   bool tiles_ready = false;  // the norm kernel wrote the fast prefill's tiles
   const bool y_split = norm_parts && norm_parts->ks > 1;  // the norm's y as partial sums
   if (norm && (y_split || !((fused || wide) && cols == 1 && g.nb <= 16))) {
-    tiles_ready = fast && input_size % kQK == 0;
+    tiles_ready = s.prefill_folds && fast && input_size % kQK == 0;
     int32_t rc = run_norm(norm->y, (int)cols, (int)input_size, norm->w_post, norm->mode == 2 ? norm->x_res : nullptr,
                           norm->scale, norm->x_out, norm->w_next, norm_scratch, norm->eps, stream, nullptr,
                           tiles_ready ? pre : nullptr, norm_parts);
@@ -2142,6 +2143,13 @@ int32_t hp_hip_set_input_images(int32_t enable) {
   return HP_OK;
 }
 
+int32_t hp_hip_set_prefill_folds(int32_t enable) {
+  State &s = st();
+  std::lock_guard<std::recursive_mutex> lock(s.mu);
+  s.prefill_folds = enable != 0;
+  return HP_OK;
+}
+
 int32_t hp_hip_stats(hp_hip_stats_t *out) {
   State &s = st();
   std::lock_guard<std::recursive_mutex> lock(s.mu);
@@ -2422,7 +2430,7 @@ int32_t hp_hip_decode_layers_device(const hp_hip_decode_layer_t *layers, size_t 
       Handle *qkv[3] = {H.q, H.k, H.v};
       float *qkv_out[3] = {q, k, v};
       rc = run_matvec(H.v ? 3 : 2, qkv, nullptr, hidden, Mc, qkv_out, strm, &nin, xn, imgx, nullptr, &dp,
-                      Mc > 1 ? &qp : nullptr);
+                      Mc > 1 && s.prefill_folds ? &qp : nullptr);
       if (Mc == 1) qp.ks = 1;
       if (rc != HP_OK) return rc;
       // the RoPE angles depend on the positions and the RoPE parameters only:
@@ -2470,7 +2478,7 @@ int32_t hp_hip_decode_layers_device(const hp_hip_decode_layer_t *layers, size_t 
         pa.pos_offset = (int)c0;
         // a prefill chunk's queries leave rounded to f16 (the attention's
         // first step), once per query instead of once per window slice
-        const bool half_q = Mc > (size_t)kMaxTokens;
+        const bool half_q = s.prefill_folds && Mc > (size_t)kMaxTokens;
         pa.q_out = half_q ? nullptr : qr;
         pa.q_half = half_q ? reinterpret_cast<uint16_t *>(qr) : nullptr;
         pa.k_cache = aa.k_cache;
@@ -2495,7 +2503,7 @@ int32_t hp_hip_decode_layers_device(const hp_hip_decode_layer_t *layers, size_t 
         // O on the fast prefill kernel: the slice merge writes its
         // activation tiles into O's prefill scratch (the pre-pass launch
         // they replace would write the same bytes there)
-        if (prefill_kind(Mc, f16_ok(1, &H.o)) == 2 && H.o->input_size % kQK == 0 &&
+        if (s.prefill_folds && prefill_kind(Mc, f16_ok(1, &H.o)) == 2 && H.o->input_size % kQK == 0 &&
             H.o->input_size == (size_t)L.attention.head_count * kHeadDim) {
           MfmaLaunch lo{};
           lo.count = 1;
@@ -2516,7 +2524,7 @@ int32_t hp_hip_decode_layers_device(const hp_hip_decode_layer_t *layers, size_t 
       if (rc != HP_OK) return rc;
       Handle *oh[1] = {H.o};
       float *oo[1] = {o};
-      const bool defer = H.o->row_count == hidden;
+      const bool defer = s.prefill_folds && H.o->row_count == hidden;
       rc = run_matvec(1, oh, att, H.o->input_size, Mc, oo, strm, nullptr, nullptr, nullptr, nullptr, nullptr,
                       defer ? &op : nullptr, o_tiles);
       if (rc != HP_OK) return rc;
@@ -2536,7 +2544,7 @@ int32_t hp_hip_decode_layers_device(const hp_hip_decode_layer_t *layers, size_t 
       Handle *dh[1] = {H.down};
       float *yo[1] = {y};
       rc = run_matvec(1, dh, h, H.down->input_size, Mc, yo, strm, nullptr, nullptr, nullptr, h_img ? imgh : nullptr,
-                      nullptr, H.down->row_count == hidden ? &dp : nullptr);
+                      nullptr, s.prefill_folds && H.down->row_count == hidden ? &dp : nullptr);
       if (rc != HP_OK) return rc;
       if (H.down->row_count != hidden) dp.ks = 1;
       nin.mode = 2;

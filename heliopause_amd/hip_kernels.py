@@ -173,6 +173,8 @@ def _declare_optional(L: ctypes.CDLL) -> None:
     L.hp_hip_set_matvec_kernel.restype = i32
     L.hp_hip_set_input_images.argtypes = [i32]
     L.hp_hip_set_input_images.restype = i32
+    L.hp_hip_set_prefill_folds.argtypes = [i32]
+    L.hp_hip_set_prefill_folds.restype = i32
     L.hp_hip_matmul_geglu.argtypes = [_u64, _u64, ctypes.c_void_p, _sz, _sz, _sz, ctypes.c_void_p, _sz]
     L.hp_hip_matmul_geglu.restype = i32
     L.hp_hip_matmul_geglu_device.argtypes = [_u64, _u64, ctypes.c_void_p, _sz, _sz, _sz, ctypes.c_void_p, _sz,
@@ -487,6 +489,13 @@ def setMatvecKernel(which: int) -> None:
 def setInputImages(enable: bool) -> None:
     """Test switch: pre-quantised input images inside draft steps (default on)."""
     assertHipOk(lib().hp_hip_set_input_images(1 if enable else 0), "setInputImages")
+
+
+def setPrefillFolds(enable: bool) -> None:
+    """Test switch: a prefill chunk's launch folds (tiles written by their
+    producers, block-range sums added by their consumers, f16 queries);
+    default on."""
+    assertHipOk(lib().hp_hip_set_prefill_folds(1 if enable else 0), "setPrefillFolds")
 
 
 def setDecodeFused(enable: bool) -> None:

@@ -273,6 +273,16 @@ int32_t hp_hip_set_matvec_kernel(int32_t which);
  * itself.  Both give the same bits. */
 int32_t hp_hip_set_input_images(int32_t enable);
 
+/* Launch folds of a prefill chunk in hp_hip_decode_layers_device (no
+ * counterpart in the reference; a test hook): with enable != 0 (the default)
+ * the norm launches write the next projection's activation tiles, the Q/K/V,
+ * O and down launches leave their block-range sums for the next launch to
+ * add, the attention prologue hands the queries over rounded to f16 and the
+ * attention's slice merge writes O's tiles; with 0 every projection quantises
+ * its own input and reduces its own ranges, and the queries stay f32.  Both
+ * give the same bits. */
+int32_t hp_hip_set_prefill_folds(int32_t enable);
+
 /* wasmResidentWeightStats (wasm-kernels.ts:586-591) plus call counters. */
 int32_t hp_hip_stats(hp_hip_stats_t *out);
 /* Wait for all work queued on the library stream. */

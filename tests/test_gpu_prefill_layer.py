@@ -292,6 +292,51 @@ def test_prefill_chunks_through_layers(hip, D, kernel):
     _check_rows(got_out, ref_out, "chunked output norm", tol)
 
 
+@pytest.mark.parametrize("tokens", [512, 100])
+def test_prefill_folds_bit_identical(hip, tokens):
+    """The launch folds of a prefill chunk (activation tiles written by the
+    norm launches and by the attention's slice merge, block-range sums added
+    by the next launch, f16 queries from the attention prologue) against the
+    plain launches (hp_hip_set_prefill_folds(0)): two layers of the model's
+    shape at 512 and 100 tokens (the last 64-column tile padded), hidden
+    states, output norm and both layers' caches bit-identical."""
+    import torch
+
+    shape = DM.ModelShape()
+    seed = S.derive(S.BASE_SEED, "prefill-folds", tokens)
+    datas = [DM.layer_host_data(shape, seed, i) for i in range(2)]
+    onorm = (1 + 0.1 * S.normal(S.derive(seed, "onorm"), shape.hidden)).astype(np.float32)
+    x = S.activations(S.derive(seed, "x"), tokens, shape.hidden) * 4
+    pos = shape.capacity - tokens
+    results = []
+    for folds in (True, False):
+        hip.setPrefillFolds(folds)
+        model = DM.HipDecodeModel(shape)
+        try:
+            for d in datas:
+                model.add_layer(d)
+            model.output_norm = _dev(onorm)
+            dx = _dev(x.reshape(-1))
+            dpos = _dev(np.array([pos], np.int32))
+            out = torch.empty(tokens * shape.hidden, dtype=torch.float32, device="cuda:0")
+            launches0 = hip.hipResidentWeightStats()["kernelLaunches"]
+            print(f"prefill folds {folds}, {tokens} tokens", flush=True)
+            model.run_layers(dx.data_ptr(), dpos.data_ptr(), out.data_ptr(), tokens=tokens)
+            torch.cuda.synchronize()
+            launches = hip.hipResidentWeightStats()["kernelLaunches"] - launches0
+            caches = [c.cpu().numpy().copy() for layer in model.caches for c in layer]
+            results.append((dx.cpu().numpy(), out.cpu().numpy(), caches, launches))
+        finally:
+            model.release()
+            hip.setPrefillFolds(True)
+    (h1, o1, c1, n1), (h0, o0, c0, n0) = results
+    print(f"launches with folds {n1}, without {n0}", flush=True)
+    assert n1 < n0
+    assert np.array_equal(h1, h0)
+    assert np.array_equal(o1, o0)
+    assert len(c1) == len(c0) and all(np.array_equal(a, b) for a, b in zip(c1, c0))
+
+
 def _topk_near_ties(g_ids, g_logits, ref_logits, k, what):
     """Top-k ids of logits that carry an end-to-end perturbation: with D the
     largest |g - ref| over the row, an id can sit in one top-k and not the
