@@ -55,20 +55,25 @@ __device__ __forceinline__ double block_sum_f64(double v, double *sh) {
   return (sh[0] + sh[1]) + (sh[2] + sh[3]);
 }
 
-__device__ __forceinline__ double rms_scale(const float (&v)[kNormPer], int n, double eps, double *sh) {
+template <int NPER>
+__device__ __forceinline__ double rms_scale(const float (&v)[NPER], int n, double eps, double *sh) {
   double s = 0.0;
 #pragma unroll
-  for (int j = 0; j < kNormPer; j++) s += (double)v[j] * (double)v[j];  // exact squares; padding is 0
+  for (int j = 0; j < NPER; j++) s += (double)v[j] * (double)v[j];  // exact squares; padding is 0
   const double total = block_sum_f64(s, sh);
   return 1.0 / sqrt(total / (double)n + eps);
 }
 
-// 256 threads per row (element i of thread t: i = t + 256 j).
+// 256 threads per row (element i of thread t: i = t + 256 j, j < NPER; the
+// launch takes the smallest instance with 256 NPER >= n, which keeps the
+// clamped re-reads of the row's last element few; a larger NPER only adds
+// zeros at the end of each thread's sum and gives the same bits).
 //   x_res == null:  next_out = rmsnorm(y) * w_next
 //   otherwise:      x1 = f32(f32(x_res + rmsnorm(y) * w_post) * scale) -> x_out
 //                   and, if next_out, next_out = rmsnorm(x1) * w_next.
 // Workgroup r handles row r of [rows][n].  w_post / w_next null: the norm
 // has no weight (rmsNormRowsNoWeight).
+template <int NPER>
 __global__ __launch_bounds__(256) void norm_residual_kernel(const NormArgs a) {
   __shared__ double sh[8];  // two workgroup sums
   const int tid = threadIdx.x;
@@ -87,13 +92,13 @@ __global__ __launch_bounds__(256) void norm_residual_kernel(const NormArgs a) {
   // every input first, one memory round trip: the loads take no branch
   // (indexes past n re-read element n - 1, absent operands re-read y), so
   // none of them waits for another
-  float v[kNormPer], r[kNormPer], wp[kNormPer], wn[kNormPer];
+  float v[NPER], r[NPER], wp[NPER], wn[NPER];
   const float *py = a.y + row;
   const float *pr = a.x_res ? a.x_res + row : py;
   const float *pwp = a.w_post ? a.w_post : py;
   const float *pwn = a.w_next ? a.w_next : py;
 #pragma unroll
-  for (int j = 0; j < kNormPer; j++) {
+  for (int j = 0; j < NPER; j++) {
     const int ic = min(tid + 256 * j, a.n - 1);
     v[j] = py[ic];
     r[j] = pr[ic];
@@ -103,22 +108,22 @@ __global__ __launch_bounds__(256) void norm_residual_kernel(const NormArgs a) {
   if (a.y_ks > 1) {
     // y as block-range partial sums: every range's loads first, then the
     // sums in range order
-    float pv[kNormParts - 1][kNormPer];
+    float pv[kNormParts - 1][NPER];
 #pragma unroll
     for (int r = 1; r < kNormParts; r++)
 #pragma unroll
-      for (int j = 0; j < kNormPer; j++) {
+      for (int j = 0; j < NPER; j++) {
         const int ic = min(tid + 256 * j, a.n - 1);
         pv[r - 1][j] = r < a.y_ks ? py[r * a.y_stride + ic] : 0.0f;
       }
 #pragma unroll
     for (int r = 1; r < kNormParts; r++)
 #pragma unroll
-      for (int j = 0; j < kNormPer; j++)
+      for (int j = 0; j < NPER; j++)
         if (r < a.y_ks) v[j] += pv[r - 1][j];
   }
 #pragma unroll
-  for (int j = 0; j < kNormPer; j++) {
+  for (int j = 0; j < NPER; j++) {
     const bool in = tid + 256 * j < a.n;
     v[j] = in ? v[j] : 0.0f;
     r[j] = in && a.x_res ? r[j] : 0.0f;
@@ -128,7 +133,7 @@ __global__ __launch_bounds__(256) void norm_residual_kernel(const NormArgs a) {
   if (a.x_res) {
     const double sc = rms_scale(v, a.n, a.eps, sh);
 #pragma unroll
-    for (int j = 0; j < kNormPer; j++) {
+    for (int j = 0; j < NPER; j++) {
       const int i = tid + 256 * j;
       const float t = a.w_post ? (float)(((double)v[j] * sc) * (double)wp[j]) : (float)((double)v[j] * sc);
       v[j] = i < a.n ? (r[j] + t) * a.scale : 0.0f;
@@ -137,9 +142,9 @@ __global__ __launch_bounds__(256) void norm_residual_kernel(const NormArgs a) {
   }
   if (a.next_out) {
     const double sc = rms_scale(v, a.n, a.eps, sh + 4);
-    __shared__ float xs[256 * kNormPer];  // the row, for the image below
+    __shared__ float xs[256 * NPER];  // the row, for the image below
 #pragma unroll
-    for (int j = 0; j < kNormPer; j++) {
+    for (int j = 0; j < NPER; j++) {
       const int i = tid + 256 * j;
       const float o = a.w_next ? (float)(((double)v[j] * sc) * (double)wn[j]) : (float)((double)v[j] * sc);
       if (i < a.n) a.next_out[row + i] = o;
@@ -689,7 +694,15 @@ hipError_t launch_norm_residual(const NormArgs &a, hipStream_t s) {
   if ((a.q8img || a.xt) && (a.n % kQK != 0 || !a.next_out)) return hipErrorInvalidValue;
   if (a.y_ks > kNormParts || (a.y_ks > 1 && a.y_stride < (size_t)a.rows * a.n)) return hipErrorInvalidValue;
   const int grid = a.xt ? (a.rows + kF2Cols - 1) / kF2Cols * kF2Cols : a.rows;
-  hipLaunchKernelGGL(norm_residual_kernel, dim3(grid), dim3(256), 0, s, a);
+  const int per = (a.n + 255) / 256;
+  if (per <= 4)
+    hipLaunchKernelGGL(norm_residual_kernel<4>, dim3(grid), dim3(256), 0, s, a);
+  else if (per <= 8)
+    hipLaunchKernelGGL(norm_residual_kernel<8>, dim3(grid), dim3(256), 0, s, a);
+  else if (per <= 10)
+    hipLaunchKernelGGL(norm_residual_kernel<10>, dim3(grid), dim3(256), 0, s, a);
+  else
+    hipLaunchKernelGGL(norm_residual_kernel<kNormPer>, dim3(grid), dim3(256), 0, s, a);
   return hipGetLastError();
 }
 
