@@ -6,6 +6,9 @@
 //
 // Tile (column tile ct, block b) at xt + (ct * nb + b) * kF2XTile, 64 columns:
 //   f16 quants [class l][quarter][column][8]        32768 bytes
+//     (the 8: the quarter's two 4-element runs r = 0, 1, each stored as
+//     elements 0, 2, 1, 3 -- the order in which the kernel's Q4_K weight
+//     fragments come out of a quant dword without a byte permute)
 //   f16 16-element sums [group / 8][column][8]       2048 bytes
 //   f32 d per column                                   256 bytes
 #pragma once
@@ -37,8 +40,8 @@ __device__ __forceinline__ void f2_tile_store16(const float (&v)[16], int i16, u
 #pragma unroll
   for (int i = 0; i < 4; i++) {
     const int l = 4 * u + i;
-    const half2v lo = (half2v){(_Float16)q[i], (_Float16)q[4 + i]};
-    const half2v hi = (half2v){(_Float16)q[8 + i], (_Float16)q[12 + i]};
+    const half2v lo = (half2v){(_Float16)q[i], (_Float16)q[8 + i]};
+    const half2v hi = (half2v){(_Float16)q[4 + i], (_Float16)q[12 + i]};
     *reinterpret_cast<uint2 *>(xh + ((l * 4 + qq) * kF2Cols + n) * 8 + 4 * (j & 1)) =
         make_uint2(__builtin_bit_cast(uint32_t, lo), __builtin_bit_cast(uint32_t, hi));
   }

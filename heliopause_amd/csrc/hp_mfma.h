@@ -36,6 +36,25 @@ __device__ __forceinline__ half2v magic_pair(uint32_t v) {
 }
 constexpr uint32_t kSel01 = 0x04010400u;  // bytes 0, 1
 constexpr uint32_t kSel23 = 0x04030402u;  // bytes 2, 3
+constexpr uint32_t kSel02 = 0x04020400u;  // bytes 0, 2
+constexpr uint32_t kSel13 = 0x04030401u;  // bytes 1, 3
+
+// Halves of dword v under the exponent bits 0x64, with no byte permute:
+// MASK 0x000F000F gives (1024 + v[3:0], 1024 + v[19:16]), MASK 0x00F000F0
+// gives (1024 + 16 v[7:4], 1024 + 16 v[23:20]) (mantissas below 1024, exact).
+// `exp` is 0x64006400 in a vector register (magic_nib_exp), so the mask can
+// be the one scalar operand of a single v_and_or_b32.
+template <uint32_t MASK>
+__device__ __forceinline__ half2v magic_nib(uint32_t v, uint32_t exp) {
+  return as_h2((v & MASK) | exp);
+}
+__device__ __forceinline__ uint32_t magic_nib_exp() {
+  uint32_t e;
+  asm("v_mov_b32 %0, 0x64006400" : "=v"(e));  // opaque: not folded back into a literal
+  return e;
+}
+constexpr uint32_t kNibLo = 0x000F000Fu;
+constexpr uint32_t kNibHi = 0x00F000F0u;
 
 // (s, s) for scale byte `idx` of dword v (unsigned bytes) and the matching
 // addend -off * s, both exact in f16: fma((1024 + q), s, -off * s) = s * (q + 1024 - off).
@@ -43,6 +62,15 @@ __device__ __forceinline__ half2v dup_byte(uint32_t v, int idx, float bias) {
   const uint32_t sel = (uint32_t)idx | 0x04000400u | ((uint32_t)idx << 16);
   const half2v h = as_h2(__builtin_amdgcn_perm(0x64646464u, v, sel));
   return h - (half2v){(_Float16)bias, (_Float16)bias};
+}
+
+// (s / 16, s / 16) for scale byte `idx` of dword v and, with it, a scale for
+// magic_nib<kNibHi>'s halves: the f16 with exponent bits 0x54 and mantissa =
+// the byte is 64 + byte / 16 exactly.
+__device__ __forceinline__ half2v dup_byte_16th(uint32_t v, int idx) {
+  const uint32_t sel = (uint32_t)idx | 0x04000400u | ((uint32_t)idx << 16);
+  const half2v h = as_h2(__builtin_amdgcn_perm(0x54545454u, v, sel));
+  return h - (half2v){(_Float16)64.0f, (_Float16)64.0f};
 }
 
 __device__ __forceinline__ half2v fma2(half2v a, half2v b, half2v c) { return __builtin_elementwise_fma(a, b, c); }

@@ -488,23 +488,26 @@ __device__ __forceinline__ void f3_transpose(uint32_t (&v)[4]) {
 }
 
 // Weight fragment of class l = 2t + g (sc * q as exact f16); qd[g][t] are the
-// transposed quant dwords.
+// transposed quant dwords.  Element order: bytes 0, 2, 1, 3 of the dword's
+// low nibbles (or low 6-bit values), then the same of its high ones -- the
+// activation tiles store their runs the same way.  Q4_K: (S[0], N[0]) scale
+// the low nibbles, (S[1], N[1]) the high ones as 16 q (their scale / 16).
+// Q6_K: S[0] = (s0, s1) for the low values, S[1] = (s2, s3) for the high.
 template <bool Q4>
 __device__ __forceinline__ half8 f3_a(const typename WSel<Q4>::T &w, const uint32_t (&qd)[2][4], int l, int q,
-                                      const half2v (&S)[4], const half2v (&N)[4]) {
+                                      const half2v (&S)[2], const half2v (&N)[2], uint32_t exp) {
   const int g = l & 1, t = l >> 1;
   if constexpr (Q4) {
-    const uint32_t dw = qd[g][t];
-    const uint32_t lo = dw & 0x0F0F0F0Fu, hi = (dw >> 4) & 0x0F0F0F0Fu;
-    return cat(fma2(magic_pair<kSel01>(lo), S[0], N[0]), fma2(magic_pair<kSel23>(lo), S[0], N[0]),
-               fma2(magic_pair<kSel01>(hi), S[1], N[1]), fma2(magic_pair<kSel23>(hi), S[1], N[1]));
+    const uint32_t dw = qd[g][t], d8 = dw >> 8;
+    return cat(fma2(magic_nib<kNibLo>(dw, exp), S[0], N[0]), fma2(magic_nib<kNibLo>(d8, exp), S[0], N[0]),
+               fma2(magic_nib<kNibHi>(dw, exp), S[1], N[1]), fma2(magic_nib<kNibHi>(d8, exp), S[1], N[1]));
   } else {
     const int jj = 2 * (q & 1);
     const uint32_t ql = qd[g][t], qh = g ? w.qh[t].y : w.qh[t].x;
     const uint32_t lo = (ql & 0x0F0F0F0Fu) | (((qh >> (2 * jj)) & 0x03030303u) << 4);
     const uint32_t hi = ((ql >> 4) & 0x0F0F0F0Fu) | (((qh >> (2 * jj + 2)) & 0x03030303u) << 4);
-    return cat(fma2(magic_pair<kSel01>(lo), S[0], N[0]), fma2(magic_pair<kSel23>(lo), S[1], N[1]),
-               fma2(magic_pair<kSel01>(hi), S[2], N[2]), fma2(magic_pair<kSel23>(hi), S[3], N[3]));
+    return cat(fma2(magic_pair<kSel02>(lo), S[0], N[0]), fma2(magic_pair<kSel13>(lo), S[0], N[0]),
+               fma2(magic_pair<kSel02>(hi), S[1], N[1]), fma2(magic_pair<kSel13>(hi), S[1], N[1]));
   }
 }
 
@@ -513,11 +516,11 @@ __device__ __forceinline__ half8 f3_a(const typename WSel<Q4>::T &w, const uint3
 // the last one and are never stored.
 template <bool Q4>
 __device__ __forceinline__ void f3_block(float (&out)[kF3RS][kF3CS][4], const typename WSel<Q4>::T (&w)[kF3RS],
-                                         const uint8_t *xl, int lane) {
+                                         const uint8_t *xl, int lane, uint32_t exp) {
   const int n = lane & 15, q = lane >> 4;
   // column set cs: 16-column slice cs % 4 of activation tile cs / 4
   auto xh = [&](int cs) { return reinterpret_cast<const _Float16 *>(xl + (cs >> 2) * kF2XTile); };
-  half2v S[kF3RS][4], N[kF3RS][4];
+  half2v S[kF3RS][2], N[kF3RS][2];
 #pragma unroll
   for (int rs = 0; rs < kF3RS; rs++) {
     if constexpr (Q4) {
@@ -526,19 +529,19 @@ __device__ __forceinline__ void f3_block(float (&out)[kF3RS][kF3CS][4], const ty
       const uint32_t schi = (hdr.w & 0x0F0F0F0Fu) | ((hdr.y >> 2) & 0x30303030u);
       const uint32_t sc = q < 2 ? sclo : schi;
       S[rs][0] = dup_byte(sc, 2 * (q & 1), 1024.0f);
-      S[rs][1] = dup_byte(sc, 2 * (q & 1) + 1, 1024.0f);
-      S[rs][2] = S[rs][3] = S[rs][0];
+      S[rs][1] = dup_byte_16th(sc, 2 * (q & 1) + 1);
       const half2v m1024 = (half2v){(_Float16)-1024.0f, (_Float16)-1024.0f};
 #pragma unroll
-      for (int e = 0; e < 4; e++) N[rs][e] = S[rs][e] * m1024;
+      for (int e = 0; e < 2; e++) N[rs][e] = S[rs][e] * m1024;
     } else {
       // signed scales: bytes ^ 0x80 are s + 128; (1024 + 128 + s) - 1152 = s
       const uint32_t gs = w[rs].gs ^ 0x80808080u;
+      const half2v b1152 = (half2v){(_Float16)1152.0f, (_Float16)1152.0f};
+      S[rs][0] = magic_pair<kSel01>(gs) - b1152;  // (s0, s1)
+      S[rs][1] = magic_pair<kSel23>(gs) - b1152;  // (s2, s3)
 #pragma unroll
-      for (int e = 0; e < 4; e++) {
-        S[rs][e] = dup_byte(gs, e, 1152.0f);
+      for (int e = 0; e < 2; e++)
         N[rs][e] = S[rs][e] * (half2v){(_Float16)-1056.0f, (_Float16)-1056.0f};  // -(1024 + 32) * sc
-      }
     }
   }
   uint32_t qd[kF3RS][2][4];  // [rs][g][t]
@@ -564,7 +567,7 @@ __device__ __forceinline__ void f3_block(float (&out)[kF3RS][kF3CS][4], const ty
                                   *reinterpret_cast<const uint4 *>(xh(cs) + (q * kF2Cols + 16 * (cs & 3) + n) * 8));
   half8 An[kF3RS];
 #pragma unroll
-  for (int rs = 0; rs < kF3RS; rs++) An[rs] = f3_a<Q4>(w[rs], qd[rs], 0, q, S[rs], N[rs]);
+  for (int rs = 0; rs < kF3RS; rs++) An[rs] = f3_a<Q4>(w[rs], qd[rs], 0, q, S[rs], N[rs], exp);
 #pragma unroll
   for (int l = 0; l < 8; l++) {
     half8 A[kF3RS];
@@ -576,7 +579,7 @@ __device__ __forceinline__ void f3_block(float (&out)[kF3RS][kF3CS][4], const ty
         B[(l + 1) & 1][cs] = __builtin_bit_cast(
             half8, *reinterpret_cast<const uint4 *>(xh(cs) + (((l + 1) * 4 + q) * kF2Cols + 16 * (cs & 3) + n) * 8));
 #pragma unroll
-      for (int rs = 0; rs < kF3RS; rs++) An[rs] = f3_a<Q4>(w[rs], qd[rs], l + 1, q, S[rs], N[rs]);
+      for (int rs = 0; rs < kF3RS; rs++) An[rs] = f3_a<Q4>(w[rs], qd[rs], l + 1, q, S[rs], N[rs], exp);
     }
 #pragma unroll
     for (int cs = 0; cs < kF3CS; cs++)
@@ -599,15 +602,14 @@ __device__ __forceinline__ void f3_block(float (&out)[kF3RS][kF3CS][4], const ty
     dx[cs] = *reinterpret_cast<const f32x4 *>(xl + (cs >> 2) * kF2XTile + 32768 + 2048 + 4 * (16 * (cs & 3) + 4 * q));
   if constexpr (Q4) {
     // sumi = sum_j mn_j * bsums32_j: quarter q < 2 carries k = 8q + e ->
-    // (j = 4q + e/2, half e%2) against the 16 half-block sums (zero operands
-    // in quarters 2, 3); out += dx * (dw * D - dmin * sumi)
-    const bool lo = q < 2;
+    // (j = 4q + e/2, half e%2) against the 16 half-block sums (quarters 2, 3
+    // read the same sums against zero mins); out += dx * (dw * D - dmin * sumi)
     half8 bm[kF3CS];
 #pragma unroll
     for (int cs = 0; cs < kF3CS; cs++) {
       const _Float16 *xb = reinterpret_cast<const _Float16 *>(xl + (cs >> 2) * kF2XTile + 32768);
-      const uint4 v = *reinterpret_cast<const uint4 *>(xb + (((q & 1) * kF2Cols) + 16 * (cs & 3) + n) * 8);
-      bm[cs] = __builtin_bit_cast(half8, lo ? v : make_uint4(0, 0, 0, 0));
+      bm[cs] = __builtin_bit_cast(
+          half8, *reinterpret_cast<const uint4 *>(xb + (((q & 1) * kF2Cols) + 16 * (cs & 3) + n) * 8));
     }
     // each stage over all 16 sums of a segment before the next, so the
     // sums' independent chains interleave instead of waiting on each other
@@ -616,7 +618,7 @@ __device__ __forceinline__ void f3_block(float (&out)[kF3RS][kF3CS][4], const ty
       const uint4 hdr = w[rs].hdr;
       const float dw = h2f_bits(hdr.x & 0xFFFFu), dmw = h2f_bits(hdr.x >> 16);
       const uint32_t mn0 = hdr.z & 0x3F3F3F3Fu, mn1 = ((hdr.w >> 4) & 0x0F0F0F0Fu) | ((hdr.z >> 2) & 0x30303030u);
-      const uint32_t mn = q == 0 ? mn0 : mn1;
+      const uint32_t mn = q == 0 ? mn0 : q == 1 ? mn1 : 0u;
       half8 am = cat(dup_byte(mn, 0, 1024.0f), dup_byte(mn, 1, 1024.0f), dup_byte(mn, 2, 1024.0f),
                      dup_byte(mn, 3, 1024.0f));
       f32x4 sm[kF3CS];
@@ -703,6 +705,7 @@ __device__ __forceinline__ void f3_tile(float (&out)[kF3RS][kF3CS][4], const uin
   if (b1 <= b0) return;  // (block ranges hold at least two blocks)
   const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   typename WSel<Q4>::T wa[kF3RS], wb[kF3RS];
+  const uint32_t exp = magic_nib_exp();
   f3_xcopy(xt, b0, f3_st0, wave, lane);
   f3_wloads<Q4>(wa, wseg, wtiles, s0, b0, lane);
   __builtin_amdgcn_s_waitcnt(0);
@@ -712,7 +715,7 @@ __device__ __forceinline__ void f3_tile(float (&out)[kF3RS][kF3CS][4], const uin
     f3_xcopy(xt, bn, f3_st1, wave, lane);
     f3_wloads<Q4>(wb, wseg, wtiles, s0, bn, lane);
     __builtin_amdgcn_sched_barrier(0);  // the loads stay ahead of the block's compute
-    f3_block<Q4>(out, wa, f3_st0, lane);
+    f3_block<Q4>(out, wa, f3_st0, lane, exp);
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
     if (b + 1 >= b1) break;
@@ -720,7 +723,7 @@ __device__ __forceinline__ void f3_tile(float (&out)[kF3RS][kF3CS][4], const uin
     f3_xcopy(xt, bn2, f3_st0, wave, lane);
     f3_wloads<Q4>(wa, wseg, wtiles, s0, bn2, lane);
     __builtin_amdgcn_sched_barrier(0);
-    f3_block<Q4>(out, wb, f3_st1, lane);
+    f3_block<Q4>(out, wb, f3_st1, lane, exp);
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
     if (b + 2 >= b1) break;
