@@ -140,6 +140,9 @@ def parse() -> argparse.Namespace:
                    help="matvec kernel: automatic choice, vector ALU, matrix cores, half-split vector ALU, "
                         "wide (one workgroup per block of rows), the wide kernel with whole or half "
                         "row-blocks per thread")
+    p.add_argument("--weight-layouts", choices=["both", "one"], default="both",
+                   help="resident weight layouts: both (vector-ALU tiles + matrix-core segments, the default) "
+                        "or one (tiles only; the matrix-core kernels read them)")
     p.add_argument("--copy-probe", action="store_true",
                    help="only run a plain 256 MiB device copy (HBM counter calibration) and exit")
     return p.parse_args()
@@ -339,7 +342,7 @@ def decode_chain(args) -> int:
                      "unit": "GB/s", "frac": round(wbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4),
                      "weight_bytes_over_peak_ms": round(wbytes / HBM_PEAK_GBPS / 1e6, 4)},
     }
-    print(json.dumps(line))
+    print(json.dumps(_label(line)))
     return 0
 
 
@@ -440,10 +443,11 @@ def measure_decode_step(m: int, steps: int, warmup: int, cpu_seconds: float | No
     wbytes = N_LAYERS * sum(row_bytes(t, k) * r for t, r, k in LAYER) + row_bytes(HEAD[0], HEAD[2]) * HEAD[1]
     kv_bytes = N_LAYERS * 2 * shape.head_count_kv * shape.capacity * 256 * 2
     cpu = None if (cpu_seconds is None or m != 1) else decode_cpu_baseline(shape, data, head_blocks, cpu_seconds)
+    resident = H.hipResidentWeightStats()["residentBytes"]  # the model's handles (both layouts by default)
     model.release()
     H.releaseHipQuantizedWeightHandle(head)
     return {"m": m, "ms": ms, "wall_ms": wall_ms, "steps": steps, "launches": launches, "split": split,
-            "weight_bytes": wbytes, "kv_bytes": kv_bytes, "cpu": cpu,
+            "weight_bytes": wbytes, "kv_bytes": kv_bytes, "cpu": cpu, "resident_bytes": resident,
             "positions": [int(shape.capacity) + 1 - m, int(shape.capacity)]}
 
 
@@ -490,7 +494,8 @@ def decode_step(args) -> int:
                                f"42-layer synthetic Gemma-like model, verification of a {m}-token draft (every "
                                "position through every layer with causal attention over a 4096-token f16 KV cache, "
                                "output norm, head, top-40 per position)",
-                   "weight_bytes": r["weight_bytes"], "kv_cache_bytes_read": r["kv_bytes"],
+                   "weight_bytes": r["weight_bytes"], "resident_weight_bytes": r["resident_bytes"],
+                   "kv_cache_bytes_read": r["kv_bytes"],
                    "launches_per_step": r["launches"], "wall_ms_per_step": round(r["wall_ms"], 4), "tokens": m,
                    "positions": r["positions"], "kernel_split_us": r["split"],
                    "timing": "one step captured in a HIP graph and replayed"},
@@ -501,7 +506,7 @@ def decode_step(args) -> int:
                      "target_ms": round(1.3 * r["weight_bytes"] / HBM_PEAK_GBPS / 1e6, 4)},
         "cpu_baseline": r["cpu"],
     }
-    print(json.dumps(line))
+    print(json.dumps(_label(line)))
     return 0
 
 
@@ -618,7 +623,7 @@ def prefill_chain(args) -> int:
         "roofline": {"bound": "mfma", "achieved": round(tflops, 2), "peak": MFMA_F16_PEAK_TFLOPS, "unit": "TFLOP/s",
                      "frac": round(tflops / MFMA_F16_PEAK_TFLOPS, 4), "traffic": None},
     }
-    print(json.dumps(line))
+    print(json.dumps(_label(line)))
     return 0
 
 
@@ -715,7 +720,7 @@ def prefill_layers(args) -> int:
         "roofline": {"bound": "mfma", "achieved": round(tflops, 2), "peak": MFMA_F16_PEAK_TFLOPS, "unit": "TFLOP/s",
                      "frac": round(tflops / MFMA_F16_PEAK_TFLOPS, 4), "traffic": None},
     }
-    print(json.dumps(line))
+    print(json.dumps(_label(line)))
     return 0
 
 
@@ -811,7 +816,7 @@ def gguf_load(args) -> int:
     }
     if cpu:
         line["cpu_baseline"] = cpu
-    print(json.dumps(line))
+    print(json.dumps(_label(line)))
     return 0
 
 
@@ -843,13 +848,29 @@ def gguf_cpu_baseline(path: str, seconds: float) -> dict:
                       "(the engine's path up to the WASM upload; no scale preparation)"}
 
 
+WEIGHT_LAYOUTS = "both"
+
+
+def _label(line: dict) -> dict:
+    """Names the resident-layout mode in a line measured with one layout."""
+    if WEIGHT_LAYOUTS != "both" and isinstance(line.get("config"), dict):
+        line["config"]["weight_layouts"] = WEIGHT_LAYOUTS
+    return line
+
+
 def main() -> int:
+    global WEIGHT_LAYOUTS
     args = parse()
+    WEIGHT_LAYOUTS = args.weight_layouts
     if args.copy_probe:
         return copy_probe()
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU only; --gpus must be 1", "n_gpus": args.gpus}))
         return 2
+    if args.weight_layouts == "one":
+        from heliopause_amd import hip_kernels as H
+
+        H.setWeightLayouts(False)
     if args.workload == "decode42":
         return decode_step(args)
     if args.workload == "decode42-proj":
@@ -933,7 +954,7 @@ def main() -> int:
         "cpu_baseline": cpu,
     }
     line.update(extra)
-    print(json.dumps(line))
+    print(json.dumps(_label(line)))
     return 0
 
 

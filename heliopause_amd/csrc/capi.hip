@@ -42,7 +42,9 @@ struct Handle {
   int tiles = 0;
   uint8_t *data = nullptr;     // tiles (+ Q6_K d plane at the end)
   uint16_t *dplane = nullptr;  // Q6_K only
-  uint8_t *segs = nullptr;     // matrix-core layout (16-row tile segments)
+  // matrix-core layout (16-row tile segments), or null for a weight kept in
+  // one layout (the matrix-core kernels then read its tiles)
+  uint8_t *segs = nullptr;
   size_t seg_bytes = 0;
   uint32_t *f16_flag = nullptr;  // set by the Q6_K repack (launch_repack)
   // The matrix-core kernels' f16 weight operands sc * q are exact for every
@@ -91,6 +93,7 @@ struct State {
   // test switch: off, every vector-ALU launch quantises its own input)
   bool images = true;
   bool prefill_folds = true;  // hp_hip_set_prefill_folds
+  bool both_layouts = true;   // hp_hip_set_weight_layouts: uploads keep the segment copy
   bool profiling = false;
   ProfileSlot prof[HP_KERNEL_COUNT];
   std::vector<hipEvent_t> event_pool;
@@ -371,9 +374,12 @@ int wide_rows_for(int rows, int nb, int cols, int type) {
 
 int g_nb_of(Handle *const *hs) { return hs[0]->g.nb; }
 
-bool f16_ok(size_t count, Handle *const *hs) {
+// The matrix-core kernels can take these weights: their f16 operands are
+// exact, and a weight read from its tiles fits the kernels' 32-bit tile
+// offsets (under 4 GiB).
+bool mfma_ok(size_t count, Handle *const *hs) {
   for (size_t i = 0; i < count; i++)
-    if (!hs[i]->f16_exact) return false;
+    if (!hs[i]->f16_exact || (!hs[i]->segs && hs[i]->byte_length >= ((size_t)1 << 32))) return false;
   return true;
 }
 
@@ -436,7 +442,7 @@ int32_t run_norm(const float *y, int rows, int n, const float *w_post, const flo
 // Whether a one-column launch over these weights runs a vector-ALU kernel,
 // which can form its input with the norm prologue.
 bool norm_prologue_ok(size_t count, Handle *const *hs, size_t cols) {
-  const bool f16 = f16_ok(count, hs);
+  const bool f16 = mfma_ok(count, hs);
   if (cols != 1 || hs[0]->g.nb > 16 || prefill_kind(cols, f16) != 0) return false;
   int tiles16 = 0;
   for (size_t i = 0; i < count; i++) tiles16 += (int)((hs[i]->row_count + 15) / 16);
@@ -446,7 +452,7 @@ bool norm_prologue_ok(size_t count, Handle *const *hs, size_t cols) {
 // Whether a launch of `cols` columns (2 or more) runs the vector-ALU kernels
 // in one chunk, so it can take its input as a pre-quantised image.
 bool image_input_ok(size_t count, Handle *const *hs, size_t cols) {
-  const bool f16 = f16_ok(count, hs);
+  const bool f16 = mfma_ok(count, hs);
   if (cols < 2 || prefill_kind(cols, f16) != 0) return false;
   int tiles16 = 0;
   for (size_t i = 0; i < count; i++) tiles16 += (int)((hs[i]->row_count + 15) / 16);
@@ -469,7 +475,7 @@ int32_t run_matvec(size_t count, Handle *const *hs, const float *d_input, size_t
   State &s = st();
   if (cols == 0) return HP_OK;
   const bool image_ok = s.images && cols >= 2 && image_input_ok(count, hs, cols);
-  const bool f16 = f16_ok(count, hs);
+  const bool f16 = mfma_ok(count, hs);
   const bool wide = prefill_kind(cols, f16) == 0 && use_wide(count, hs, cols);
   const bool wide_norm = wide && cols == 1 && g_nb_of(hs) <= 16;  // the wide kernel's norm prologue
   const int kind = prefill_kind(cols, f16);
@@ -478,8 +484,12 @@ int32_t run_matvec(size_t count, Handle *const *hs, const float *d_input, size_t
   l.count = (int)count;
   l.k = (int)input_size;
   l.cols = (int)cols;
+  l.S = hs[0]->g.S;
+  l.R = hs[0]->g.R;
   for (size_t i = 0; i < count; i++) {
     l.seg[i] = hs[i]->segs;
+    l.wt[i] = hs[i]->data;
+    l.dplane[i] = hs[i]->dplane;
     l.type[i] = hs[i]->type;
     l.rows[i] = (int)hs[i]->row_count;
     l.out[i] = d_outs[i];
@@ -578,8 +588,13 @@ int32_t run_matvec(size_t count, Handle *const *hs, const float *d_input, size_t
     MfmaLaunch l{};
     l.count = (int)count;
     l.k = (int)input_size;
+    l.S = g.S;
+    l.R = g.R;
     for (size_t i = 0; i < count; i++) {
       l.seg[i] = hs[i]->segs;
+      l.seg[i] = hs[i]->segs;
+    l.wt[i] = hs[i]->data;
+      l.dplane[i] = hs[i]->dplane;
       l.type[i] = hs[i]->type;
       l.rows[i] = (int)hs[i]->row_count;
     }
@@ -637,7 +652,7 @@ int32_t run_matvec_geglu(Handle *hg, Handle *hu, const float *d_input, size_t in
   const TileGeom g = hg->g;
   const int tiles16 = 2 * (int)((rows + 15) / 16);
   Handle *pair[2] = {hg, hu};
-  const bool f16 = f16_ok(2, pair);
+  const bool f16 = mfma_ok(2, pair);
   const bool wide = prefill_kind(cols, f16) == 0 && hg->type == hu->type && use_wide_pair(pair, cols);
   const bool fused = !wide && cols <= 4 && s.matvec_kernel <= 1 && !use_mfma(cols, g.nb, tiles16, f16) &&
                      !use_half((int)cols, g, 2 * hg->tiles, (int)(2 * rows)) && cols_per_launch(g, s.max_lds) >= (int)cols;
@@ -648,9 +663,13 @@ int32_t run_matvec_geglu(Handle *hg, Handle *hu, const float *d_input, size_t in
   if (fast) {
     l.count = 2;
     l.k = (int)input_size;
+    l.S = g.S;
+    l.R = g.R;
     l.cols = (int)cols;
     for (int i = 0; i < 2; i++) {
       l.seg[i] = pair[i]->segs;
+      l.wt[i] = pair[i]->data;
+      l.dplane[i] = pair[i]->dplane;
       l.type[i] = pair[i]->type;
       l.rows[i] = (int)rows;
     }
@@ -816,15 +835,15 @@ int32_t upload_common(int32_t type_id, const void *src, bool src_device, size_t 
   h.byte_length = weight_len;
   h.g = choose_geometry((int)(input_size / kQK));
   h.tiles = (int)((row_count + h.g.R - 1) / h.g.R);
-  // one allocation holds both layouts: tiles (+ Q6_K d plane), then
-  // segments, then the repack's f16 flag
+  // one allocation: the tiles (+ Q6_K d plane), the segments unless the
+  // weight is kept in one layout, then the repack's f16 flag
   const int nb = (int)(input_size / kQK);
   const size_t tile_bytes = (weight_len + 255) & ~(size_t)255;
-  h.seg_bytes = mfma_segment_bytes(type_id, (int)row_count, nb);
+  h.seg_bytes = s.both_layouts ? mfma_segment_bytes(type_id, (int)row_count, nb) : 0;
   if (hipMalloc((void **)&h.data, tile_bytes + h.seg_bytes + 256) != hipSuccess)
     return fail(HP_ERR_OOM, "weight allocation failed");
-  h.segs = h.data + tile_bytes;
-  h.f16_flag = reinterpret_cast<uint32_t *>(h.segs + h.seg_bytes);
+  if (s.both_layouts) h.segs = h.data + tile_bytes;
+  h.f16_flag = reinterpret_cast<uint32_t *>(h.data + tile_bytes + h.seg_bytes);
   h.f16_exact = type_id != kTypeQ6K;  // Q6_K: read_f16_flag after the repack
   if (type_id == kTypeQ6K) h.dplane = reinterpret_cast<uint16_t *>(h.data + row_count * (input_size / kQK) * 208);
 
@@ -845,7 +864,7 @@ int32_t upload_common(int32_t type_id, const void *src, bool src_device, size_t 
   }
   hipError_t e = hipMemsetAsync(h.f16_flag, 0, sizeof(uint32_t), s.stream);
   if (e == hipSuccess) e = launch_repack(type_id, raw, (int)row_count, h.g, h.data, h.dplane, h.f16_flag, s.stream);
-  if (e == hipSuccess) e = launch_repack_mfma(type_id, raw, (int)row_count, nb, h.segs, s.stream);
+  if (e == hipSuccess && h.segs) e = launch_repack_mfma(type_id, raw, (int)row_count, nb, h.segs, s.stream);
   if (e == hipSuccess && (sync || !src_device)) e = hipStreamSynchronize(s.stream);
   if (staging) (void)hipFree(staging);
   if (e == hipSuccess && (sync || !src_device)) e = read_f16_flag(h);
@@ -1609,7 +1628,7 @@ int32_t hp_hip_weight_release(uint64_t handle) {
   Handle *h = lookup(handle);
   if (!h) return fail(HP_ERR_HANDLE, "unknown weight handle");
   (void)hipStreamSynchronize(s.stream);
-  (void)hipFree(h->data);  // both layouts
+  (void)hipFree(h->data);  // every layout of the weight
   h->data = nullptr;
   h->segs = nullptr;
   h->dplane = nullptr;
@@ -2150,6 +2169,13 @@ int32_t hp_hip_set_prefill_folds(int32_t enable) {
   return HP_OK;
 }
 
+int32_t hp_hip_set_weight_layouts(int32_t both) {
+  State &s = st();
+  std::lock_guard<std::recursive_mutex> lock(s.mu);
+  s.both_layouts = both != 0;
+  return HP_OK;
+}
+
 int32_t hp_hip_stats(hp_hip_stats_t *out) {
   State &s = st();
   std::lock_guard<std::recursive_mutex> lock(s.mu);
@@ -2503,7 +2529,7 @@ int32_t hp_hip_decode_layers_device(const hp_hip_decode_layer_t *layers, size_t 
         // O on the fast prefill kernel: the slice merge writes its
         // activation tiles into O's prefill scratch (the pre-pass launch
         // they replace would write the same bytes there)
-        if (s.prefill_folds && prefill_kind(Mc, f16_ok(1, &H.o)) == 2 && H.o->input_size % kQK == 0 &&
+        if (s.prefill_folds && prefill_kind(Mc, mfma_ok(1, &H.o)) == 2 && H.o->input_size % kQK == 0 &&
             H.o->input_size == (size_t)L.attention.head_count * kHeadDim) {
           MfmaLaunch lo{};
           lo.count = 1;

@@ -55,6 +55,38 @@ struct TileGeom {
 
 TileGeom choose_geometry(int nb);
 
+// One row's place in the tile layout, for the matrix-core kernels, which
+// read a row at a time: chunk c of (row, block b = i * S + s) sits at byte
+//     base + i * iter + c * chunk + s * 16
+// of the weight's tiles, and the Q6_K d of (row, b) at
+//     dplane[dbase + i * diter + s].
+// 32-bit offsets: the launches that use it take weights under 4 GiB.
+struct TileRow {
+  uint32_t base, chunk, iter, dbase, diter;
+};
+__host__ __device__ inline TileRow tile_row(int row, int rows, int nb, int S, int R, int CH) {
+  const int t = row / R, r = row - t * R, row0 = t * R;
+  const int rt = rows - row0 < R ? rows - row0 : R;
+  TileRow p;
+  p.base = (uint32_t)(((size_t)row0 * nb * CH + (size_t)r * S) * 16);
+  p.chunk = (uint32_t)(rt * S * 16);
+  p.iter = (uint32_t)CH * p.chunk;
+  p.dbase = (uint32_t)((size_t)row0 * nb + (size_t)r * S);
+  p.diter = (uint32_t)(rt * S);
+  return p;
+}
+
+// b = i * S + s for a block index the whole wave shares (nb / S steps at
+// most, none for one-iteration geometries).
+__device__ __forceinline__ void block_split(int b, int S, int &i, int &s) {
+  i = 0;
+  s = b;
+  while (s >= S) {
+    s -= S;
+    i++;
+  }
+}
+
 struct WeightDesc {
   const uint8_t *data;    // tiles
   const uint16_t *dplane; // Q6_K: f16 d per row-block in tile order; else null
@@ -353,9 +385,14 @@ struct SampleParams {
 };
 hipError_t launch_sample(const uint32_t *ids, const float *vals, int cols, int k, int count, const SampleParams &p,
                          uint32_t *rng, int32_t *tokens, double *probs, int32_t *kept, hipStream_t s);
-// Matrix-core matvec (kquant_mfma.hip): weights in 16-row tile segments.
+// Matrix-core matvec (kquant_mfma.hip).  Each weight is read from its
+// 16-row tile segments, or, where seg is null (one resident layout), from its
+// tiles (geometry S, R of choose_geometry(k / 256)).
 struct MfmaLaunch {
   const uint8_t *seg[kMaxWeights];
+  const uint8_t *wt[kMaxWeights];
+  const uint16_t *dplane[kMaxWeights];
+  int S, R;
   float *out[kMaxWeights];
   int type[kMaxWeights];
   int rows[kMaxWeights];
@@ -368,6 +405,18 @@ struct MfmaLaunch {
 size_t mfma_segment_bytes(int type, int rows, int nb);
 size_t mfma_lds_bytes(int cols, int nb);
 hipError_t launch_repack_mfma(int type, const uint8_t *raw, int rows, int nb, uint8_t *segs, hipStream_t s);
+// Some weight of the launch is kept in one layout: the launch reads every
+// weight's tiles.
+inline bool launch_reads_tiles(const MfmaLaunch &l) {
+  for (int i = 0; i < l.count; i++)
+    if (!l.seg[i]) return true;
+  return false;
+}
+// The launch's tile geometry is the one choose_geometry gives its weights.
+inline bool mfma_geometry_ok(const MfmaLaunch &l) {
+  const int nb = l.k / kQK;
+  return l.S >= 1 && l.R >= 1 && l.S * l.R <= 64 && nb >= 1 && nb % l.S == 0;
+}
 hipError_t launch_matvec_mfma(const MfmaLaunch &l, int num_cus, hipStream_t s);
 
 // Prefill (many columns) on the matrix cores: a Q8_K pre-pass writes

@@ -29,7 +29,8 @@
 //         mins x half-block sums of q8)
 //   result = [sumf +] ((((-0 + s0) + s1) + ...) + s7)
 //
-// Weight layout (repacked at upload, same byte count per 16-row tile; rows
+// Weights come from one of two places per weight.  The matrix-core segments
+// (a second copy, repacked at upload, same byte count per 16-row tile; rows
 // past the weight in the last tile are zero): segment (tile T, block b) at
 // (b * tiles + T) * SEG, block-major, so the waves that stream block b of
 // neighbouring tiles at the same time read one contiguous range.
@@ -40,6 +41,18 @@
 //     [288,3360) chunks 0,1 as Q4_K with the low 4 bits of q6; chunk 2
 //     dword 2*cls + h holds in byte cc the high 2 bits of q6 at
 //     (j = 4h + jj, cc, class 2q + cls) in bits 2jj.
+// Or, for a weight uploaded with one layout only (hp_hip_set_weight_layouts),
+// the vector-ALU tile layout (hp_common.h), read a row at a time (tile_row).
+// Lane i = (row rho = i%16 of the 16-row segment, quarter q) needs the
+// dwords D[u][l] (u = 0..3) of classes l = 2q and 2q + 1: they are the
+// 8-byte pair at byte 8(q%2) of quant chunk 2u + q/2 of its row-block, four
+// 8-byte loads.  Q4_K: chunk 0 (header), quant chunks 1..8.  Q6_K: low-bit
+// chunks 0..7 the same way; high-bit dwords Dqh[h][l] (h = 0, 1) the pair at
+// byte 8(q%2) of chunk 8 + 2h + q/2, stored ^ 0xAA per byte; the 16 scales
+// are chunk 12; d from the d plane.  Rows past the weight in the last
+// segment re-read its last row (their sums are never stored).  These loads
+// touch a cache line per lane (a row's blocks are interleaved in the tile
+// layout), against one line per 8 lanes in the segments.
 #include "hp_common.h"
 #include "hp_mfma.h"
 
@@ -48,16 +61,18 @@ namespace hp {
 namespace {
 
 struct MfmaWeight {
-  const uint8_t *seg;  // segments of this weight
+  const uint8_t *seg;       // segments of this weight (null: kept in one layout)
+  const uint8_t *wt;        // tiles of this weight
+  const uint16_t *dplane;   // Q6_K d plane
   float *out;
-  int type, rows, tiles, tile_begin;
+  int type, rows, tiles, tile_begin;  // tiles: 16-row segments
 };
 
 struct MfmaArgs {
   MfmaWeight w[kMaxWeights];
   int count;
   int total_tiles;
-  int nb;
+  int nb, S, R;     // tile geometry of the launch's weights
   const float *x;  // f32 input of the launch's first column, [cols][k]
   int k;
   int cols;        // columns of this launch (<= 8)
@@ -178,8 +193,9 @@ __device__ __forceinline__ half8 lds_h8(const void *p) {
   return __builtin_bit_cast(half8, *reinterpret_cast<const uint4 *>(p));
 }
 
-// Raw loads of one (tile, block) segment for lane i (per weight type, so a
-// Q4_K tile carries only its 12 registers).
+// Raw loads of one (segment, block) for lane i (per weight type, so a Q4_K
+// segment carries only its 12 registers).  c0 / c1: dwords D[u][2q] /
+// D[u][2q + 1], u = 0..3.
 template <bool Q4>
 struct Seg;
 template <>
@@ -190,10 +206,25 @@ struct Seg<true> {
 template <>
 struct Seg<false> {
   uint4 hdr;  // 16 int8 scales of row i%16
-  uint4 c0, c1, c2;
+  uint4 c0, c1, c2;  // c2: high-bit dwords Dqh[h][2q + cls] at 2h + cls (tiles: ^ 0xAA per byte)
   uint32_t d;  // f16 d of row i%16
 };
 
+// Lane offsets of one row for load_tiles: the row's place, and the byte of its
+// first 8-byte quant pair within a row-block.
+struct RowLoads {
+  TileRow tr;
+  uint32_t oq;  // Q4_K: chunk 1 + q/2, Q6_K: chunk q/2; + 8 (q%2)
+};
+
+__device__ __forceinline__ RowLoads row_loads(int row, int rows, int nb, int S, int R, bool q4, int q) {
+  RowLoads r;
+  r.tr = tile_row(row, rows, nb, S, R, q4 ? 9 : 13);
+  r.oq = (uint32_t)((q4 ? 1 : 0) + (q >> 1)) * r.tr.chunk + 8u * (uint32_t)(q & 1);
+  return r;
+}
+
+// One (tile, block) segment for lane i.
 template <bool Q4>
 __device__ __forceinline__ Seg<Q4> load_seg(const uint8_t *seg, int lane) {
   const int rho = lane & 15;
@@ -207,6 +238,32 @@ __device__ __forceinline__ Seg<Q4> load_seg(const uint8_t *seg, int lane) {
     r.c0 = *reinterpret_cast<const uint4 *>(seg + 288 + 16 * lane);
     r.c1 = *reinterpret_cast<const uint4 *>(seg + 288 + 1024 + 16 * lane);
     r.c2 = *reinterpret_cast<const uint4 *>(seg + 288 + 2048 + 16 * lane);
+  }
+  return r;
+}
+
+// The same registers from the weight's tiles (c2 as the tiles store it).
+template <bool Q4>
+__device__ __forceinline__ Seg<Q4> load_tiles(const uint8_t *wt, const uint16_t *dplane, const RowLoads &rl, int b,
+                                              int S) {
+  int i, s;
+  block_split(b, S, i, s);
+  const uint32_t off = rl.tr.base + (uint32_t)i * rl.tr.iter + 16u * (uint32_t)s;
+  const uint32_t ch = rl.tr.chunk;
+  auto ld8 = [&](uint32_t o) { return *reinterpret_cast<const uint2 *>(wt + o); };
+  Seg<Q4> r;
+  uint2 p[4];
+#pragma unroll
+  for (int u = 0; u < 4; u++) p[u] = ld8(off + rl.oq + 2u * (uint32_t)u * ch);
+  r.c0 = make_uint4(p[0].x, p[1].x, p[2].x, p[3].x);
+  r.c1 = make_uint4(p[0].y, p[1].y, p[2].y, p[3].y);
+  if constexpr (Q4) {
+    r.hdr = *reinterpret_cast<const uint4 *>(wt + off);
+  } else {
+    r.hdr = *reinterpret_cast<const uint4 *>(wt + off + 12u * ch);
+    r.d = dplane[rl.tr.dbase + (uint32_t)i * rl.tr.diter + (uint32_t)s];
+    const uint2 h0 = ld8(off + rl.oq + 8u * ch), h1 = ld8(off + rl.oq + 10u * ch);
+    r.c2 = make_uint4(h0.x, h0.y, h1.x, h1.y);
   }
   return r;
 }
@@ -229,11 +286,13 @@ __device__ __forceinline__ half8 a_q4k(const Seg<true> &r, int g, int u, const h
 
 // Q6_K: groups 4u, 4u+1 (j = 2u; c = 0,1 | c = 2,3) and 4u+2, 4u+3 (j = 2u+1);
 // the weights are sc_g * (q6 - 32).
+template <bool TILE>
 __device__ __forceinline__ half8 a_q6k(const Seg<false> &r, int g, int u, const half2v (&S)[4],
                                        const half2v (&N)[4]) {
   const int jj = 2 * (u & 1);
   const uint32_t ql = u4at(g ? r.c1 : r.c0, u);
-  const uint32_t qh = u4at(r.c2, 2 * (u >> 1) + g);
+  // the tiles store the fields as hi ^ 2
+  const uint32_t qh = u4at(r.c2, 2 * (u >> 1) + g) ^ (TILE ? 0xAAAAAAAAu : 0u);
   const uint32_t lo = (ql & 0x0F0F0F0Fu) | (((qh >> (2 * jj)) & 0x03030303u) << 4);
   const uint32_t hi = ((ql >> 4) & 0x0F0F0F0Fu) | (((qh >> (2 * jj + 2)) & 0x03030303u) << 4);
   return cat(fma2(magic_pair<kSel01>(lo), S[0], N[0]), fma2(magic_pair<kSel23>(lo), S[1], N[1]),
@@ -242,7 +301,7 @@ __device__ __forceinline__ half8 a_q6k(const Seg<false> &r, int g, int u, const 
 
 // One block of a tile for every column set: A operands are built one at a
 // time right before their MFMAs; then the f32 tail in block order.
-template <int NSET, bool Q4>
+template <int NSET, bool Q4, bool TILE>
 __device__ __forceinline__ void process_block(Chains (&ch)[NSET], const Seg<Q4> &r, const Lds &L, int b, int nb,
                                               int lane) {
   const int n = lane & 15, q = lane >> 4;
@@ -297,7 +356,7 @@ __device__ __forceinline__ void process_block(Chains (&ch)[NSET], const Seg<Q4> 
       }
 #pragma unroll
       for (int g = 0; g < 2; g++) {
-        const half8 a = a_q6k(r, g, u, S, N);
+        const half8 a = a_q6k<TILE>(r, g, u, S, N);
 #pragma unroll
         for (int st = 0; st < NSET; st++) {
           const half8 bf = lds_h8(q == s ? (const void *)(xq[st] + g * (kXClass / 2) + 8 * u) : (const void *)L.zero);
@@ -348,21 +407,27 @@ __device__ __forceinline__ void process_block(Chains (&ch)[NSET], const Seg<Q4> 
 
 // All blocks of one tile, in order; three register buffers keep the loads of
 // the next two blocks in flight while a block computes.
-template <int NSET, bool Q4>
-__device__ __forceinline__ void run_tile(Chains (&ch)[NSET], const uint8_t *seg, size_t bstride, const Lds &L,
-                                         int nb, int lane) {
+template <int NSET, bool Q4, bool TILE>
+__device__ __forceinline__ void run_tile(Chains (&ch)[NSET], const MfmaWeight &W, int tt, const RowLoads &rl, int S,
+                                         const Lds &L, int nb, int lane) {
   // every load unconditional (a block index past the last re-reads it): a
   // path that skipped a load would turn the wait for one block into a wait
   // for the blocks loaded after it
-  auto blk = [&](int b) { return seg + (size_t)min(b, nb - 1) * bstride; };
-  Seg<Q4> r0 = load_seg<Q4>(blk(0), lane), r1 = load_seg<Q4>(blk(1), lane), r2;
+  const int segb = Q4 ? 2304 : 3360;
+  auto ld = [&](int b) {
+    if constexpr (TILE)
+      return load_tiles<Q4>(W.wt, W.dplane, rl, min(b, nb - 1), S);
+    else
+      return load_seg<Q4>(W.seg + ((size_t)min(b, nb - 1) * W.tiles + tt) * segb, lane);
+  };
+  Seg<Q4> r0 = ld(0), r1 = ld(1), r2;
   for (int b = 0; b < nb; b += 3) {
-    r2 = load_seg<Q4>(blk(b + 2), lane);
-    process_block<NSET, Q4>(ch, r0, L, b, nb, lane);
-    r0 = load_seg<Q4>(blk(b + 3), lane);
-    if (b + 1 < nb) process_block<NSET, Q4>(ch, r1, L, b + 1, nb, lane);
-    r1 = load_seg<Q4>(blk(b + 4), lane);
-    if (b + 2 < nb) process_block<NSET, Q4>(ch, r2, L, b + 2, nb, lane);
+    r2 = ld(b + 2);
+    process_block<NSET, Q4, TILE>(ch, r0, L, b, nb, lane);
+    r0 = ld(b + 3);
+    if (b + 1 < nb) process_block<NSET, Q4, TILE>(ch, r1, L, b + 1, nb, lane);
+    r1 = ld(b + 4);
+    if (b + 2 < nb) process_block<NSET, Q4, TILE>(ch, r2, L, b + 2, nb, lane);
   }
 }
 
@@ -396,7 +461,9 @@ __device__ __forceinline__ void finish_tile(const Chains (&ch)[NSET], const Lds 
   }
 }
 
-template <int NSET>
+// TILE: every weight is read from its tiles (a launch with a weight kept in
+// one layout); else from its segments.
+template <int NSET, bool TILE>
 __global__ __launch_bounds__(256) void kquant_mfma_kernel(const MfmaArgs a) {
   extern __shared__ __align__(16) uint8_t smem[];
   const int nb = a.nb;
@@ -449,10 +516,9 @@ __global__ __launch_bounds__(256) void kquant_mfma_kernel(const MfmaArgs a) {
     if (a.count > 2 && t >= a.w[2].tile_begin) W = a.w[2];
     if (a.count > 3 && t >= a.w[3].tile_begin) W = a.w[3];
     const bool q4 = W.type == kTypeQ4K;
-    const int segb = q4 ? 2304 : 3360;
     const int tt = t - W.tile_begin;
-    const uint8_t *seg = W.seg + (size_t)tt * segb;
-    const size_t bstride = (size_t)W.tiles * segb;  // next block of this tile
+    const RowLoads rl =
+        TILE ? row_loads(min(16 * tt + (lane & 15), W.rows - 1), W.rows, nb, a.S, a.R, q4, lane >> 4) : RowLoads{};
     Chains ch[NSET];
 #pragma unroll
     for (int st = 0; st < NSET; st++)
@@ -463,9 +529,9 @@ __global__ __launch_bounds__(256) void kquant_mfma_kernel(const MfmaArgs a) {
         ch[st].f[j] = 0.0f;
       }
     if (q4)
-      run_tile<NSET, true>(ch, seg, bstride, L, nb, lane);
+      run_tile<NSET, true, TILE>(ch, W, tt, rl, a.S, L, nb, lane);
     else
-      run_tile<NSET, false>(ch, seg, bstride, L, nb, lane);
+      run_tile<NSET, false, TILE>(ch, W, tt, rl, a.S, L, nb, lane);
     finish_tile<NSET>(ch, L, lane, q4, W.out, W.rows, 16 * tt, a.out_col0, a.cols);
   }
 }
@@ -581,12 +647,15 @@ hipError_t launch_repack_mfma(int type, const uint8_t *raw, int rows, int nb, ui
 }
 
 hipError_t launch_matvec_mfma(const MfmaLaunch &l, int num_cus, hipStream_t s) {
-  if (l.cols < 1 || l.cols > 8 || l.count < 1 || l.count > kMaxWeights) return hipErrorInvalidValue;
+  if (l.cols < 1 || l.cols > 8 || l.count < 1 || l.count > kMaxWeights || !mfma_geometry_ok(l))
+    return hipErrorInvalidValue;
   MfmaArgs a{};
   a.count = l.count;
   int tiles = 0;
   for (int i = 0; i < l.count; i++) {
     a.w[i].seg = l.seg[i];
+    a.w[i].wt = l.wt[i];
+    a.w[i].dplane = l.dplane[i];
     a.w[i].out = l.out[i];
     a.w[i].type = l.type[i];
     a.w[i].rows = l.rows[i];
@@ -596,6 +665,8 @@ hipError_t launch_matvec_mfma(const MfmaLaunch &l, int num_cus, hipStream_t s) {
   }
   a.total_tiles = tiles;
   a.nb = l.k / kQK;
+  a.S = l.S;
+  a.R = l.R;
   a.x = l.x;
   a.k = l.k;
   a.cols = l.cols;
@@ -603,10 +674,16 @@ hipError_t launch_matvec_mfma(const MfmaLaunch &l, int num_cus, hipStream_t s) {
   int grid = (tiles + 3) / 4;
   if (grid > num_cus * 8) grid = num_cus * 8;
   const size_t lds = mfma_lds_bytes(l.cols, a.nb);
-  if (l.cols <= 4)
-    hipLaunchKernelGGL(kquant_mfma_kernel<1>, dim3(grid), dim3(256), lds, s, a);
-  else
-    hipLaunchKernelGGL(kquant_mfma_kernel<2>, dim3(grid), dim3(256), lds, s, a);
+  if (launch_reads_tiles(l)) {
+    if (l.cols <= 4)
+      hipLaunchKernelGGL((kquant_mfma_kernel<1, true>), dim3(grid), dim3(256), lds, s, a);
+    else
+      hipLaunchKernelGGL((kquant_mfma_kernel<2, true>), dim3(grid), dim3(256), lds, s, a);
+  } else if (l.cols <= 4) {
+    hipLaunchKernelGGL((kquant_mfma_kernel<1, false>), dim3(grid), dim3(256), lds, s, a);
+  } else {
+    hipLaunchKernelGGL((kquant_mfma_kernel<2, false>), dim3(grid), dim3(256), lds, s, a);
+  }
   return hipGetLastError();
 }
 

@@ -18,12 +18,13 @@
 // column slice w; the chains are added in class order through LDS at the end
 // of the tile.
 //
-// Data flow per block: the two 16-row weight segments of the tile (the
-// matrix-core layout of kquant_mfma.hip, read straight from HBM, each byte
-// once per column tile) and the 64 columns' Q8_K quants (int8, class-major,
-// written by the pre-pass below) are staged in LDS, double-buffered through
-// registers; A fragments (one dword per lane and class) and B fragments
-// (8 bytes per lane) are built from LDS.
+// Data flow per block: the tile's two 16-row weight segments (the
+// matrix-core layout of kquant_mfma.hip, or, for a weight kept in one
+// layout, gathered from its tiles into the same LDS image: see stage_store;
+// each byte read once per column tile) and the 64 columns' Q8_K quants
+// (int8, class-major, written by the pre-pass below) are staged in LDS,
+// double-buffered through registers; A fragments (one dword per lane and
+// class) and B fragments (8 bytes per lane) are built from LDS.
 #include "hp_common.h"
 #include "hp_f2tile.h"
 #include "hp_gelu.h"
@@ -68,7 +69,9 @@ __global__ __launch_bounds__(64) void q8k_prefill_kernel(const float *__restrict
 }
 
 struct PfWeight {
-  const uint8_t *seg;
+  const uint8_t *seg;      // segments of this weight (null: kept in one layout)
+  const uint8_t *wt;       // tiles of this weight
+  const uint16_t *dplane;  // Q6_K d plane
   float *out;
   int type, rows, tiles, rt_begin;  // tiles: 16-row segments; rt: 32-row workgroup tiles
 };
@@ -76,26 +79,54 @@ struct PfWeight {
 struct PfArgs {
   PfWeight w[kMaxWeights];
   int count, total_rt, col_tiles, nb, cols;
+  int S, R;  // tile geometry of the weights
   const int8_t *xq;
   const _Float16 *xb;
   const float *xd;
 };
 
-// Registers holding one block's staging loads of this thread.
+// Registers holding one block's staging loads of this thread: 16-byte weight
+// units u = tid + 256 r of the two segments (TILE: tile-layout chunk c = u /
+// 32 of tile row u % 32, and the Q6_K d of tile row tid < 32), the columns'
+// quants and sums.
 struct Stage {
   uint4 w[2], x[4], e;
+  uint32_t d;
 };
 
-__device__ __forceinline__ void stage_load(Stage &st, const PfWeight &W, int T0, int b, const PfArgs &a, int col0,
-                                           int tid) {
-  const int segb = W.type == kTypeQ4K ? 2304 : 3360;
-  const int nseg = T0 + 1 < W.tiles ? 2 : 1;
-  const uint8_t *src = W.seg + ((size_t)b * W.tiles + T0) * segb;  // segments T0, T0 + 1 are adjacent
-  const int n16 = nseg * segb / 16;
+// Tile-layout place of this thread's weight row, tile row tid % 32 (both its
+// chunks and its d; a row past the weight re-reads the weight's last row,
+// whose sums are never stored).
+__device__ __forceinline__ TileRow stage_row(const PfWeight &W, int T0, const PfArgs &a, int tid, int CH) {
+  return tile_row(min(16 * T0 + (tid & 31), W.rows - 1), W.rows, a.nb, a.S, a.R, CH);
+}
+
+template <bool Q4, bool TILE>
+__device__ __forceinline__ void stage_load(Stage &st, const PfWeight &W, int T0, const TileRow &tr, int b,
+                                           const PfArgs &a, int col0, int tid) {
+  st.d = 0;
+  if constexpr (TILE) {
+    constexpr int CH = Q4 ? 9 : 13;
+    int bi, bs;
+    block_split(b, a.S, bi, bs);
 #pragma unroll
-  for (int r = 0; r < 2; r++) {
-    const int i = tid + 256 * r;
-    st.w[r] = i < n16 ? reinterpret_cast<const uint4 *>(src)[i] : make_uint4(0, 0, 0, 0);
+    for (int r = 0; r < 2; r++) {
+      const int u = tid + 256 * r;
+      st.w[r] = u < 32 * CH ? *reinterpret_cast<const uint4 *>(W.wt + tr.base + (uint32_t)bi * tr.iter +
+                                                               (uint32_t)(u >> 5) * tr.chunk + 16u * (uint32_t)bs)
+                            : make_uint4(0, 0, 0, 0);
+    }
+    if (!Q4 && tid < 32) st.d = W.dplane[tr.dbase + (uint32_t)bi * tr.diter + (uint32_t)bs];
+  } else {
+    constexpr int segb = Q4 ? 2304 : 3360;
+    const int nseg = T0 + 1 < W.tiles ? 2 : 1;
+    const uint8_t *src = W.seg + ((size_t)b * W.tiles + T0) * segb;  // segments T0, T0 + 1 are adjacent
+    const int n16 = nseg * segb / 16;
+#pragma unroll
+    for (int r = 0; r < 2; r++) {
+      const int i = tid + 256 * r;
+      st.w[r] = i < n16 ? reinterpret_cast<const uint4 *>(src)[i] : make_uint4(0, 0, 0, 0);
+    }
   }
 #pragma unroll
   for (int r = 0; r < 4; r++) {
@@ -121,12 +152,51 @@ __device__ __forceinline__ void stage_load(Stage &st, const PfWeight &W, int T0,
   }
 }
 
+// The weights go to LDS as two 16-row segments, in the order the A
+// fragments read them.  Segment units are copied as they are; tile chunks
+// are scattered (dword D[p][l] of row rho -> unit (class l, row rho) of the
+// segment, dword p):
+//   Q4_K, 2304 bytes: [0,256) the 16 row headers; [256,2304) unit (l, rho)
+//     at 256 + 1024 (l % 2) + 16 (16 (l / 2) + rho), dword p = D[p][l].
+//   Q6_K, 3360 bytes: [0,256) the 16 rows' scales; [256,288) their f16 d;
+//     [288,2336) low-bit units as Q4_K's; [2336,3360) high-bit unit (l / 2,
+//     rho) dword 2h + l % 2 = Dqh[h][l] ^ 0xAA.. (the fields as GGUF stores them).
+template <bool Q4, bool TILE>
 __device__ __forceinline__ void stage_store(const Stage &st, uint8_t *buf, int tid) {
+  constexpr int CH = Q4 ? 9 : 13, segb = Q4 ? 2304 : 3360;
 #pragma unroll
   for (int r = 0; r < 2; r++) {
-    const int i = tid + 256 * r;
-    if (i < kPfWBytes / 16) reinterpret_cast<uint4 *>(buf)[i] = st.w[r];
+    const int u = tid + 256 * r;
+    if (!TILE) {
+      if (u < kPfWBytes / 16) reinterpret_cast<uint4 *>(buf)[u] = st.w[r];
+      continue;
+    }
+    if (u >= 32 * CH) continue;
+    const int c = u >> 5, rl = u & 31, rho = rl & 15;
+    uint8_t *seg = buf + (rl >> 4) * segb;
+    const uint32_t wv[4] = {st.w[r].x, st.w[r].y, st.w[r].z, st.w[r].w};
+    if (c == (Q4 ? 0 : 12)) {
+      *reinterpret_cast<uint4 *>(seg + 16 * rho) = st.w[r];
+    } else if (Q4 || c < 8) {
+      const int ck = Q4 ? c - 1 : c;  // dwords 4 ck + e = D[ck / 2][4 (ck % 2) + e]
+#pragma unroll
+      for (int e = 0; e < 4; e++) {
+        const int l = 4 * (ck & 1) + e;
+        *reinterpret_cast<uint32_t *>(seg + (Q4 ? 256 : 288) + 1024 * (l & 1) + 16 * (16 * (l >> 1) + rho) +
+                                      4 * (ck >> 1)) = wv[e];
+      }
+    } else {
+      const int ck = c - 8;  // dwords 4 ck + e = Dqh[ck / 2][4 (ck % 2) + e]
+#pragma unroll
+      for (int e = 0; e < 4; e++) {
+        const int l = 4 * (ck & 1) + e;
+        *reinterpret_cast<uint32_t *>(seg + 2336 + 16 * (16 * (l >> 1) + rho) + 4 * (2 * (ck >> 1) + (l & 1))) =
+            wv[e] ^ 0xAAAAAAAAu;
+      }
+    }
   }
+  if (TILE && !Q4 && tid < 32)
+    *reinterpret_cast<uint16_t *>(buf + (tid >> 4) * segb + 256 + 2 * (tid & 15)) = (uint16_t)st.d;
 #pragma unroll
   for (int r = 0; r < 4; r++) {
     const int i = tid + 256 * r, col = i >> 4, part = i & 15;
@@ -259,7 +329,7 @@ __device__ __forceinline__ void pf_block(PfChains &ch, const uint8_t *buf, int w
   }
 }
 
-template <bool Q4>
+template <bool Q4, bool TILE>
 __device__ void pf_tile(const PfArgs &a, const PfWeight &W, int T0, int col0, uint8_t *smem, int wave, int lane,
                         int tid) {
   PfChains ch;
@@ -277,13 +347,14 @@ __device__ void pf_tile(const PfArgs &a, const PfWeight &W, int T0, int col0, ui
     for (int j = 0; j < 4; j++) ch.f[rs][j] = 0.0f;
 
   Stage st;
-  stage_load(st, W, T0, 0, a, col0, tid);
-  stage_store(st, smem, tid);
+  const TileRow tr = TILE ? stage_row(W, T0, a, tid, Q4 ? 9 : 13) : TileRow{};
+  stage_load<Q4, TILE>(st, W, T0, tr, 0, a, col0, tid);
+  stage_store<Q4, TILE>(st, smem, tid);
   __syncthreads();
   for (int b = 0; b < a.nb; b++) {
-    if (b + 1 < a.nb) stage_load(st, W, T0, b + 1, a, col0, tid);
+    if (b + 1 < a.nb) stage_load<Q4, TILE>(st, W, T0, tr, b + 1, a, col0, tid);
     pf_block<Q4>(ch, smem + (b & 1) * kPfStage, wave, lane);
-    if (b + 1 < a.nb) stage_store(st, smem + ((b + 1) & 1) * kPfStage, tid);
+    if (b + 1 < a.nb) stage_store<Q4, TILE>(st, smem + ((b + 1) & 1) * kPfStage, tid);
     __syncthreads();
   }
 
@@ -319,6 +390,9 @@ __device__ void pf_tile(const PfArgs &a, const PfWeight &W, int T0, int col0, ui
   __syncthreads();  // fin and the stage buffers are reused by the next tile
 }
 
+// TILE: every weight is read from its tiles (a launch with a weight kept in
+// one layout); else from its segments.
+template <bool TILE>
 __global__ __launch_bounds__(256) void kquant_prefill_kernel(const PfArgs a) {
   kernarg_warm<PfArgs>();
   extern __shared__ __align__(16) uint8_t smem[];
@@ -334,9 +408,9 @@ __global__ __launch_bounds__(256) void kquant_prefill_kernel(const PfArgs a) {
     if (a.count > 3 && rt >= a.w[3].rt_begin) W = a.w[3];
     const int T0 = 2 * (rt - W.rt_begin);
     if (W.type == kTypeQ4K)
-      pf_tile<true>(a, W, T0, ct * kPfCols, smem, wave, lane, tid);
+      pf_tile<true, TILE>(a, W, T0, ct * kPfCols, smem, wave, lane, tid);
     else
-      pf_tile<false>(a, W, T0, ct * kPfCols, smem, wave, lane, tid);
+      pf_tile<false, TILE>(a, W, T0, ct * kPfCols, smem, wave, lane, tid);
   }
 }
 
@@ -410,6 +484,7 @@ __global__ __launch_bounds__(256) void q8k_prefill_tiles16_kernel(const float *_
 struct F2Args {
   PfWeight w[kMaxWeights];  // rt_begin counts 256-row workgroup tiles here
   int count, total_rt, col_tiles, nb, cols;
+  int S, R;  // tile geometry of the weights
   const uint8_t *xt;
   // ksplit > 1: block range r of a tile writes its sums to part + r * part_stride
   // + part_off[weight] + m * rows + row instead of the output
@@ -428,21 +503,28 @@ struct F2Args {
 };
 
 // One segment's weights in a lane's registers, loaded with 16- and 8-byte
-// loads (few memory instructions).  The quant chunks come in the matrix-core
-// layout -- lane (n, r) holds unit n + 16r of chunk g, dwords u = 0..3 -- and
-// f3_transpose turns them into what the A fragments take: lane (n, q) holds
-// dword q of units n + 16t, t = 0..3 (class l = 2t + g).
-// Q4_K: row n's header (d | dmin, then the 12 bytes of 6-bit scales and mins).
+// loads (few memory instructions), from one of two places:
+//   segments (matrix-core layout): lane (n, r) holds unit n + 16r of chunk g,
+//     dwords u = 0..3, and f3_transpose turns them into what the A fragments
+//     take: lane (n, q) holds dword q of units n + 16t, t = 0..3 (class
+//     l = 2t + g);
+//   tiles (a weight kept in one layout, hp_common.h): lane (row n, quarter
+//     q) takes the two quant chunks holding dwords D[q][l], l = 0..3 and
+//     4..7, which are what its A fragments need (class l = 2t + g: dword
+//     l % 4 of chunk l / 4), no transpose.
+// Q4_K: row n's header (d | dmin, then the 12 bytes of 6-bit scales and
+// mins) and the quants (qa[g] / qa[l / 4]).
 struct W4 {
   uint4 hdr;
-  uint4 qa[2];  // [g]
+  uint4 qa[2];
 };
-// Q6_K: low-bit chunks as Q4_K's; high bits: per t the two dwords (classes g =
-// 0, 1) of unit n + 16t for quarter pair q >> 1 (hh-major units); row n's
-// scales 4q .. 4q + 3 and its d (f16 bits).
+// Q6_K: low-bit units or chunks as Q4_K's; high bits: for class l = 2t + g
+// dword 2 (t % 2) + g of qh[t / 2] (segments: the two dwords of unit n + 16t
+// for quarter pair q / 2; tiles: chunks 8 + 2h, 9 + 2h, h = q / 2, fields
+// stored ^ 2); row n's scales 4q .. 4q + 3 and its d (f16 bits).
 struct W6 {
-  uint4 qa[2];  // [g]
-  uint2 qh[4];  // [t]
+  uint4 qa[2];
+  uint4 qh[2];
   uint32_t gs, d16;
 };
 template <bool Q4>
@@ -454,11 +536,27 @@ struct WSel<true> {
   using T = W4;
 };
 
+// A lane's offsets into one of its rows' row-blocks (tile_row) and the
+// chunks it loads: oq = its first quant chunk, oh = its first high-bit chunk.
+struct F3Row {
+  TileRow tr;
+  uint32_t oq, oh;
+};
+
+template <bool Q4>
+__device__ __forceinline__ F3Row f3_row(int row, int rows, int nb, int S, int R, int q) {
+  F3Row f;
+  f.tr = tile_row(row, rows, nb, S, R, Q4 ? 9 : 13);
+  f.oq = (uint32_t)(Q4 ? 1 + 2 * q : 2 * q) * f.tr.chunk;
+  f.oh = (uint32_t)(8 + 2 * (q >> 1)) * f.tr.chunk;
+  return f;
+}
+
 // Segment layouts of the matrix-core repack (kquant_mfma.hip): Q4_K [16 rows
 // x 16-byte header][2 chunks x 64 units x 16 bytes of quants]; Q6_K [16 rows x
 // 16 scales][16 x f16 d][2 chunks x 1024 low bits][1024 high bits].
 template <bool Q4>
-__device__ __forceinline__ void f3_wload(typename WSel<Q4>::T &w, const uint8_t *seg, int lane) {
+__device__ __forceinline__ void f3_wload_seg(typename WSel<Q4>::T &w, const uint8_t *seg, int lane) {
   const int n = lane & 15, q = lane >> 4;
   if constexpr (Q4) {
     w.hdr = *reinterpret_cast<const uint4 *>(seg + 16 * n);
@@ -469,8 +567,11 @@ __device__ __forceinline__ void f3_wload(typename WSel<Q4>::T &w, const uint8_t 
     w.d16 = *reinterpret_cast<const uint16_t *>(seg + 256 + 2 * n);
 #pragma unroll
     for (int g = 0; g < 2; g++) w.qa[g] = *reinterpret_cast<const uint4 *>(seg + 288 + 1024 * g + 16 * lane);
+    uint2 h[4];
 #pragma unroll
-    for (int t = 0; t < 4; t++) w.qh[t] = *reinterpret_cast<const uint2 *>(seg + 2336 + 256 * t + 16 * n + 8 * (q >> 1));
+    for (int t = 0; t < 4; t++) h[t] = *reinterpret_cast<const uint2 *>(seg + 2336 + 256 * t + 16 * n + 8 * (q >> 1));
+    w.qh[0] = make_uint4(h[0].x, h[0].y, h[1].x, h[1].y);
+    w.qh[1] = make_uint4(h[2].x, h[2].y, h[3].x, h[3].y);
   }
 }
 
@@ -487,13 +588,31 @@ __device__ __forceinline__ void f3_transpose(uint32_t (&v)[4]) {
   v[3] = d[1];
 }
 
+// Block (bi, bs) = bi * S + bs of row f into w, from the tiles.
+template <bool Q4>
+__device__ __forceinline__ void f3_wload_tile(typename WSel<Q4>::T &w, const uint8_t *wt, const uint16_t *dplane,
+                                              const F3Row &f, int bi, int bs, int q) {
+  const uint32_t off = f.tr.base + (uint32_t)bi * f.tr.iter + 16u * (uint32_t)bs;
+  auto ld16 = [&](uint32_t o) { return *reinterpret_cast<const uint4 *>(wt + o); };
+  w.qa[0] = ld16(off + f.oq);
+  w.qa[1] = ld16(off + f.oq + f.tr.chunk);
+  if constexpr (Q4) {
+    w.hdr = ld16(off);
+  } else {
+    w.qh[0] = ld16(off + f.oh);
+    w.qh[1] = ld16(off + f.oh + f.tr.chunk);
+    w.gs = *reinterpret_cast<const uint32_t *>(wt + off + 12u * f.tr.chunk + 4u * (uint32_t)q);
+    w.d16 = dplane[f.tr.dbase + (uint32_t)bi * f.tr.diter + (uint32_t)bs];
+  }
+}
+
 // Weight fragment of class l = 2t + g (sc * q as exact f16); qd[g][t] are the
-// transposed quant dwords.  Element order: bytes 0, 2, 1, 3 of the dword's
+// quant dwords D[q][l].  Element order: bytes 0, 2, 1, 3 of the dword's
 // low nibbles (or low 6-bit values), then the same of its high ones -- the
 // activation tiles store their runs the same way.  Q4_K: (S[0], N[0]) scale
 // the low nibbles, (S[1], N[1]) the high ones as 16 q (their scale / 16).
 // Q6_K: S[0] = (s0, s1) for the low values, S[1] = (s2, s3) for the high.
-template <bool Q4>
+template <bool Q4, bool TILE>
 __device__ __forceinline__ half8 f3_a(const typename WSel<Q4>::T &w, const uint32_t (&qd)[2][4], int l, int q,
                                       const half2v (&S)[2], const half2v (&N)[2], uint32_t exp) {
   const int g = l & 1, t = l >> 1;
@@ -503,7 +622,8 @@ __device__ __forceinline__ half8 f3_a(const typename WSel<Q4>::T &w, const uint3
                fma2(magic_nib<kNibHi>(dw, exp), S[1], N[1]), fma2(magic_nib<kNibHi>(d8, exp), S[1], N[1]));
   } else {
     const int jj = 2 * (q & 1);
-    const uint32_t ql = qd[g][t], qh = g ? w.qh[t].y : w.qh[t].x;
+    // the tiles store the fields as hi ^ 2
+    const uint32_t ql = qd[g][t], qh = u4at(w.qh[t >> 1], 2 * (t & 1) + g) ^ (TILE ? 0xAAAAAAAAu : 0u);
     const uint32_t lo = (ql & 0x0F0F0F0Fu) | (((qh >> (2 * jj)) & 0x03030303u) << 4);
     const uint32_t hi = ((ql >> 4) & 0x0F0F0F0Fu) | (((qh >> (2 * jj + 2)) & 0x03030303u) << 4);
     return cat(fma2(magic_pair<kSel02>(lo), S[0], N[0]), fma2(magic_pair<kSel13>(lo), S[0], N[0]),
@@ -514,7 +634,7 @@ __device__ __forceinline__ half8 f3_a(const typename WSel<Q4>::T &w, const uint3
 // One block of the wave's tile (kF3RS segments x 64 columns): weights w
 // against the activation tile at xl.  Segments past the weight's end repeat
 // the last one and are never stored.
-template <bool Q4>
+template <bool Q4, bool TILE>
 __device__ __forceinline__ void f3_block(float (&out)[kF3RS][kF3CS][4], const typename WSel<Q4>::T (&w)[kF3RS],
                                          const uint8_t *xl, int lane, uint32_t exp) {
   const int n = lane & 15, q = lane >> 4;
@@ -544,17 +664,22 @@ __device__ __forceinline__ void f3_block(float (&out)[kF3RS][kF3CS][4], const ty
         N[rs][e] = S[rs][e] * (half2v){(_Float16)-1056.0f, (_Float16)-1056.0f};  // -(1024 + 32) * sc
     }
   }
-  uint32_t qd[kF3RS][2][4];  // [rs][g][t]
+  uint32_t qd[kF3RS][2][4];  // [rs][g][t]: dword D[q][2t + g]
 #pragma unroll
   for (int rs = 0; rs < kF3RS; rs++)
 #pragma unroll
     for (int g = 0; g < 2; g++) {
-      const uint4 v = w[rs].qa[g];
-      qd[rs][g][0] = v.x;
-      qd[rs][g][1] = v.y;
-      qd[rs][g][2] = v.z;
-      qd[rs][g][3] = v.w;
-      f3_transpose(qd[rs][g]);
+      if constexpr (TILE) {
+#pragma unroll
+        for (int t = 0; t < 4; t++) qd[rs][g][t] = u4at(w[rs].qa[t >> 1], 2 * (t & 1) + g);
+      } else {
+        const uint4 v = w[rs].qa[g];
+        qd[rs][g][0] = v.x;
+        qd[rs][g][1] = v.y;
+        qd[rs][g][2] = v.z;
+        qd[rs][g][3] = v.w;
+        f3_transpose(qd[rs][g]);
+      }
     }
   f32x4 D[kF3RS][kF3CS];
   // Software pipeline over the classes: while class l's MFMAs run, class
@@ -567,7 +692,7 @@ __device__ __forceinline__ void f3_block(float (&out)[kF3RS][kF3CS][4], const ty
                                   *reinterpret_cast<const uint4 *>(xh(cs) + (q * kF2Cols + 16 * (cs & 3) + n) * 8));
   half8 An[kF3RS];
 #pragma unroll
-  for (int rs = 0; rs < kF3RS; rs++) An[rs] = f3_a<Q4>(w[rs], qd[rs], 0, q, S[rs], N[rs], exp);
+  for (int rs = 0; rs < kF3RS; rs++) An[rs] = f3_a<Q4, TILE>(w[rs], qd[rs], 0, q, S[rs], N[rs], exp);
 #pragma unroll
   for (int l = 0; l < 8; l++) {
     half8 A[kF3RS];
@@ -579,7 +704,7 @@ __device__ __forceinline__ void f3_block(float (&out)[kF3RS][kF3CS][4], const ty
         B[(l + 1) & 1][cs] = __builtin_bit_cast(
             half8, *reinterpret_cast<const uint4 *>(xh(cs) + (((l + 1) * 4 + q) * kF2Cols + 16 * (cs & 3) + n) * 8));
 #pragma unroll
-      for (int rs = 0; rs < kF3RS; rs++) An[rs] = f3_a<Q4>(w[rs], qd[rs], l + 1, q, S[rs], N[rs], exp);
+      for (int rs = 0; rs < kF3RS; rs++) An[rs] = f3_a<Q4, TILE>(w[rs], qd[rs], l + 1, q, S[rs], N[rs], exp);
     }
 #pragma unroll
     for (int cs = 0; cs < kF3CS; cs++)
@@ -655,15 +780,22 @@ __device__ __forceinline__ void f3_block(float (&out)[kF3RS][kF3CS][4], const ty
   }
 }
 
-// The wave's segments s0 .. s0 + kF3RS - 1 (each clamped to the weight's last)
-// of block b.
-template <bool Q4>
-__device__ __forceinline__ void f3_wloads(typename WSel<Q4>::T (&w)[kF3RS], const uint8_t *wseg, int wtiles, int s0,
-                                          int b, int lane) {
-  constexpr int segb = Q4 ? 2304 : 3360;
-  const uint8_t *base = wseg + (size_t)b * wtiles * segb;
+// Block b of the wave's segments s0 .. s0 + kF3RS - 1 (each clamped to the
+// weight's last), from its segments or (TILE) its tiles at rows f[rs].
+template <bool Q4, bool TILE>
+__device__ __forceinline__ void f3_wloads(typename WSel<Q4>::T (&w)[kF3RS], const PfWeight &W, const F3Row (&f)[kF3RS],
+                                          int s0, int b, int S, int lane) {
+  if constexpr (TILE) {
+    int bi, bs;
+    block_split(b, S, bi, bs);
 #pragma unroll
-  for (int rs = 0; rs < kF3RS; rs++) f3_wload<Q4>(w[rs], base + (size_t)min(s0 + rs, wtiles - 1) * segb, lane);
+    for (int rs = 0; rs < kF3RS; rs++) f3_wload_tile<Q4>(w[rs], W.wt, W.dplane, f[rs], bi, bs, lane >> 4);
+  } else {
+    constexpr int segb = Q4 ? 2304 : 3360;
+    const uint8_t *base = W.seg + (size_t)b * W.tiles * segb;
+#pragma unroll
+    for (int rs = 0; rs < kF3RS; rs++) f3_wload_seg<Q4>(w[rs], base + (size_t)min(s0 + rs, W.tiles - 1) * segb, lane);
+  }
 }
 
 // The two activation-tile stages.  Two distinct arrays, so the compiler sees
@@ -694,36 +826,44 @@ __device__ __forceinline__ void f3_xcopy(const uint8_t *const (&xt)[kF3Tiles], i
   }
 }
 
-// Blocks [b0, b1) of one tile for this wave's segments from s0 of weight
-// `wseg` (`wtiles` segments per block); xt is the column tile's activation
-// tiles.  Loads are unconditional (the block index is clamped), so they
-// never sit behind a branch; every copy has landed (vmcnt(0)) before the
-// barrier that ends its block.
-template <bool Q4>
-__device__ __forceinline__ void f3_tile(float (&out)[kF3RS][kF3CS][4], const uint8_t *wseg, int wtiles, int s0,
-                                        const uint8_t *const (&xt)[kF3Tiles], int b0, int b1) {
+// Blocks [b0, b1) of one tile for this wave's segments s0 .. s0 + kF3RS - 1
+// of weight W (each clamped to the weight's last segment, and rows to its
+// last row; their sums are never stored); xt is the column tile's activation
+// tiles.  Loads are unconditional (the block index is clamped), so they never
+// sit behind a branch; every copy has landed (vmcnt(0)) before the barrier
+// that ends its block.
+template <bool Q4, bool TILE>
+__device__ __forceinline__ void f3_tile(float (&out)[kF3RS][kF3CS][4], const PfWeight &W, int nb, int S, int R,
+                                        int s0, const uint8_t *const (&xt)[kF3Tiles], int b0, int b1) {
   if (b1 <= b0) return;  // (block ranges hold at least two blocks)
   const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int q = lane >> 4;
+  F3Row f[kF3RS] = {};
+  if constexpr (TILE) {
+#pragma unroll
+    for (int rs = 0; rs < kF3RS; rs++)
+      f[rs] = f3_row<Q4>(min(16 * min(s0 + rs, W.tiles - 1) + (lane & 15), W.rows - 1), W.rows, nb, S, R, q);
+  }
   typename WSel<Q4>::T wa[kF3RS], wb[kF3RS];
   const uint32_t exp = magic_nib_exp();
   f3_xcopy(xt, b0, f3_st0, wave, lane);
-  f3_wloads<Q4>(wa, wseg, wtiles, s0, b0, lane);
+  f3_wloads<Q4, TILE>(wa, W, f, s0, b0, S, lane);
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
   for (int b = b0;; b += 2) {
     const int bn = min(b + 1, b1 - 1);
     f3_xcopy(xt, bn, f3_st1, wave, lane);
-    f3_wloads<Q4>(wb, wseg, wtiles, s0, bn, lane);
+    f3_wloads<Q4, TILE>(wb, W, f, s0, bn, S, lane);
     __builtin_amdgcn_sched_barrier(0);  // the loads stay ahead of the block's compute
-    f3_block<Q4>(out, wa, f3_st0, lane, exp);
+    f3_block<Q4, TILE>(out, wa, f3_st0, lane, exp);
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
     if (b + 1 >= b1) break;
     const int bn2 = min(b + 2, b1 - 1);
     f3_xcopy(xt, bn2, f3_st0, wave, lane);
-    f3_wloads<Q4>(wa, wseg, wtiles, s0, bn2, lane);
+    f3_wloads<Q4, TILE>(wa, W, f, s0, bn2, S, lane);
     __builtin_amdgcn_sched_barrier(0);
-    f3_block<Q4>(out, wb, f3_st1, lane, exp);
+    f3_block<Q4, TILE>(out, wb, f3_st1, lane, exp);
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
     if (b + 2 >= b1) break;
@@ -747,7 +887,9 @@ constexpr int kF3WaveFloats = kF3RS * kF3CS * 4 * 64;  // a wave's sums (out) of
 // half of the waves) and the same rows of up (the second half); up's sums go
 // through LDS to the gate wave of the same rows, which stores
 // fround(gelu(gate) * up).  total_rt then counts those tiles, ksplit is 1.
-template <bool PAIR>
+// TILE: every weight is read from its tiles (a launch with a weight kept in
+// one layout); else from its segments.
+template <bool PAIR, bool TILE>
 __global__ __launch_bounds__(kF3Threads) __attribute__((amdgpu_waves_per_eu(kF3PerSIMD, kF3PerSIMD))) void
 kquant_prefill_fast_kernel(
     const F2Args a) {
@@ -784,7 +926,7 @@ kquant_prefill_fast_kernel(
     const int nseg_tile = W.tiles - T0 < kTileSegs ? W.tiles - T0 : kTileSegs;
     const int my_seg = kF3RS * (PAIR ? wave % kHalf : wave);  // within this wave's weight
     const int nseg = nseg_tile - my_seg;                       // this wave's live segments (<= 0: none)
-    const uint8_t *wseg = PAIR && wave >= kHalf ? a.w[1].seg : W.seg;
+    const PfWeight &WW = PAIR && wave >= kHalf ? a.w[1] : W;  // the weight of this wave's rows
     float out[kF3RS][kF3CS][4];
 #pragma unroll
     for (int rs = 0; rs < kF3RS; rs++)
@@ -799,9 +941,9 @@ kquant_prefill_fast_kernel(
 #pragma unroll
     for (int t = 0; t < kF3Tiles; t++) xt[t] = a.xt + (size_t)min(ct * kF3Tiles + t, xtiles - 1) * a.nb * kF2XTile;
     if (W.type == kTypeQ4K)
-      f3_tile<true>(out, wseg, W.tiles, T0 + my_seg, xt, b_begin, b_end);
+      f3_tile<true, TILE>(out, WW, a.nb, a.S, a.R, T0 + my_seg, xt, b_begin, b_end);
     else
-      f3_tile<false>(out, wseg, W.tiles, T0 + my_seg, xt, b_begin, b_end);
+      f3_tile<false, TILE>(out, WW, a.nb, a.S, a.R, T0 + my_seg, xt, b_begin, b_end);
     const int n = lane & 15, q = lane >> 4;
     if (PAIR && split) {
       float *part = a.tail_part + ((size_t)hidx * kF3Waves + wave) * kF3WaveFloats + lane;
@@ -999,7 +1141,8 @@ size_t prefill_fast_geglu_bytes(const MfmaLaunch &l, int num_cus) {
 
 hipError_t launch_prefill_fast_geglu(const MfmaLaunch &l, const float *x, uint8_t *scratch, const uint16_t *gelu_lut,
                                      float *out, int num_cus, hipStream_t s, bool tiles_ready) {
-  if (l.count != 2 || l.cols < 1 || l.k % kQK != 0 || l.type[0] != l.type[1] || l.rows[0] != l.rows[1])
+  if (l.count != 2 || l.cols < 1 || l.k % kQK != 0 || l.type[0] != l.type[1] || l.rows[0] != l.rows[1] ||
+      !mfma_geometry_ok(l))
     return hipErrorInvalidValue;
   const F2Pair p = f2_pair(l, num_cus);
   const int nb = p.nb, col_tiles = p.col_tiles;
@@ -1014,6 +1157,8 @@ hipError_t launch_prefill_fast_geglu(const MfmaLaunch &l, const float *x, uint8_
   a.count = 2;
   for (int i = 0; i < 2; i++) {
     a.w[i].seg = l.seg[i];
+    a.w[i].wt = l.wt[i];
+    a.w[i].dplane = l.dplane[i];
     a.w[i].out = nullptr;
     a.w[i].type = l.type[i];
     a.w[i].rows = l.rows[i];
@@ -1023,6 +1168,8 @@ hipError_t launch_prefill_fast_geglu(const MfmaLaunch &l, const float *x, uint8_
   a.total_rt = p.total_rt;
   a.col_tiles = col_tiles;
   a.nb = nb;
+  a.S = l.S;
+  a.R = l.R;
   a.cols = l.cols;
   a.xt = scratch;
   a.ksplit = 1;
@@ -1030,7 +1177,10 @@ hipError_t launch_prefill_fast_geglu(const MfmaLaunch &l, const float *x, uint8_
   a.gelu_lut = gelu_lut;
   a.tail_full = p.tail_full;
   a.tail_part = reinterpret_cast<float *>(scratch + (size_t)p.xtiles * nb * kF2XTile);
-  hipLaunchKernelGGL(kquant_prefill_fast_kernel<true>, dim3(p.grid), dim3(kF3Threads), 0, s, a);
+  if (launch_reads_tiles(l))
+    hipLaunchKernelGGL((kquant_prefill_fast_kernel<true, true>), dim3(p.grid), dim3(kF3Threads), 0, s, a);
+  else
+    hipLaunchKernelGGL((kquant_prefill_fast_kernel<true, false>), dim3(p.grid), dim3(kF3Threads), 0, s, a);
   if (!p.tail_full) return hipGetLastError();
   e = hipGetLastError();
   if (e != hipSuccess) return e;
@@ -1056,7 +1206,8 @@ size_t prefill_fast_part_bytes(const MfmaLaunch &l, int num_cus) {
 
 hipError_t launch_prefill_fast(const MfmaLaunch &l, const float *x, uint8_t *scratch, int num_cus, hipStream_t s,
                                bool tiles_ready, PrefillParts *defer) {
-  if (l.count < 1 || l.count > kMaxWeights || l.cols < 1 || l.k % kQK != 0) return hipErrorInvalidValue;
+  if (l.count < 1 || l.count > kMaxWeights || l.cols < 1 || l.k % kQK != 0 || !mfma_geometry_ok(l))
+    return hipErrorInvalidValue;
   const F2Shape sh = f2_shape(l, num_cus);
   const int nb = sh.nb, col_tiles = sh.col_tiles;
   hipError_t e;
@@ -1072,6 +1223,8 @@ hipError_t launch_prefill_fast(const MfmaLaunch &l, const float *x, uint8_t *scr
   size_t off = 0;
   for (int i = 0; i < l.count; i++) {
     a.w[i].seg = l.seg[i];
+    a.w[i].wt = l.wt[i];
+    a.w[i].dplane = l.dplane[i];
     a.w[i].out = l.out[i];
     a.w[i].type = l.type[i];
     a.w[i].rows = l.rows[i];
@@ -1084,6 +1237,8 @@ hipError_t launch_prefill_fast(const MfmaLaunch &l, const float *x, uint8_t *scr
   a.total_rt = rt;
   a.col_tiles = col_tiles;
   a.nb = nb;
+  a.S = l.S;
+  a.R = l.R;
   a.cols = l.cols;
   a.xt = scratch;
   a.ksplit = sh.ks;
@@ -1098,7 +1253,10 @@ hipError_t launch_prefill_fast(const MfmaLaunch &l, const float *x, uint8_t *scr
   }
   const long long items = (long long)a.total_rt * a.col_tiles * a.ksplit;
   const int grid = (int)(items < kF3PerCU * num_cus ? items : kF3PerCU * num_cus);
-  hipLaunchKernelGGL(kquant_prefill_fast_kernel<false>, dim3(grid), dim3(kF3Threads), 0, s, a);
+  if (launch_reads_tiles(l))
+    hipLaunchKernelGGL((kquant_prefill_fast_kernel<false, true>), dim3(grid), dim3(kF3Threads), 0, s, a);
+  else
+    hipLaunchKernelGGL((kquant_prefill_fast_kernel<false, false>), dim3(grid), dim3(kF3Threads), 0, s, a);
   if (a.ksplit == 1 || deferred) return hipGetLastError();
   e = hipGetLastError();
   if (e != hipSuccess) return e;
@@ -1108,12 +1266,15 @@ hipError_t launch_prefill_fast(const MfmaLaunch &l, const float *x, uint8_t *scr
 }
 
 hipError_t launch_prefill(const MfmaLaunch &l, const uint8_t *scratch, int num_cus, hipStream_t s) {
-  if (l.count < 1 || l.count > kMaxWeights || l.cols < 1 || l.k % kQK != 0) return hipErrorInvalidValue;
+  if (l.count < 1 || l.count > kMaxWeights || l.cols < 1 || l.k % kQK != 0 || !mfma_geometry_ok(l))
+    return hipErrorInvalidValue;
   PfArgs a{};
   a.count = l.count;
   int rt = 0;
   for (int i = 0; i < l.count; i++) {
     a.w[i].seg = l.seg[i];
+    a.w[i].wt = l.wt[i];
+    a.w[i].dplane = l.dplane[i];
     a.w[i].out = l.out[i];
     a.w[i].type = l.type[i];
     a.w[i].rows = l.rows[i];
@@ -1123,6 +1284,8 @@ hipError_t launch_prefill(const MfmaLaunch &l, const uint8_t *scratch, int num_c
   }
   a.total_rt = rt;
   a.nb = l.k / kQK;
+  a.S = l.S;
+  a.R = l.R;
   a.cols = l.cols;
   a.col_tiles = (l.cols + kPfCols - 1) / kPfCols;
   a.xq = reinterpret_cast<const int8_t *>(scratch);
@@ -1130,7 +1293,10 @@ hipError_t launch_prefill(const MfmaLaunch &l, const uint8_t *scratch, int num_c
   a.xd = reinterpret_cast<const float *>(scratch + (size_t)l.cols * a.nb * (kQK + 32));
   const long long items = (long long)a.total_rt * a.col_tiles;
   const int grid = (int)(items < (long long)num_cus * 2 ? items : (long long)num_cus * 2);
-  hipLaunchKernelGGL(kquant_prefill_kernel, dim3(grid), dim3(256), kPfLds, s, a);
+  if (launch_reads_tiles(l))
+    hipLaunchKernelGGL(kquant_prefill_kernel<true>, dim3(grid), dim3(256), kPfLds, s, a);
+  else
+    hipLaunchKernelGGL(kquant_prefill_kernel<false>, dim3(grid), dim3(256), kPfLds, s, a);
   return hipGetLastError();
 }
 

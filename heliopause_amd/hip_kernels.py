@@ -175,6 +175,8 @@ def _declare_optional(L: ctypes.CDLL) -> None:
     L.hp_hip_set_input_images.restype = i32
     L.hp_hip_set_prefill_folds.argtypes = [i32]
     L.hp_hip_set_prefill_folds.restype = i32
+    L.hp_hip_set_weight_layouts.argtypes = [i32]
+    L.hp_hip_set_weight_layouts.restype = i32
     L.hp_hip_matmul_geglu.argtypes = [_u64, _u64, ctypes.c_void_p, _sz, _sz, _sz, ctypes.c_void_p, _sz]
     L.hp_hip_matmul_geglu.restype = i32
     L.hp_hip_matmul_geglu_device.argtypes = [_u64, _u64, ctypes.c_void_p, _sz, _sz, _sz, ctypes.c_void_p, _sz,
@@ -496,6 +498,13 @@ def setPrefillFolds(enable: bool) -> None:
     producers, block-range sums added by their consumers, f16 queries);
     default on."""
     assertHipOk(lib().hp_hip_set_prefill_folds(1 if enable else 0), "setPrefillFolds")
+
+
+def setWeightLayouts(both: bool) -> None:
+    """Resident layouts of weights uploaded from now on: both (default) keeps
+    the vector-ALU tiles and the matrix-core segments; one layout keeps the
+    tiles only (the GGUF byte count), and the matrix-core kernels read them."""
+    assertHipOk(lib().hp_hip_set_weight_layouts(1 if both else 0), "setWeightLayouts")
 
 
 def setDecodeFused(enable: bool) -> None:

@@ -283,6 +283,17 @@ int32_t hp_hip_set_input_images(int32_t enable);
  * give the same bits. */
 int32_t hp_hip_set_prefill_folds(int32_t enable);
 
+/* Resident layouts of the weights uploaded from now on (no counterpart in
+ * the reference, whose WASM arena keeps one copy of each tensor).  both != 0
+ * (the default): every weight is kept twice, in the vector-ALU tile layout
+ * and in the matrix-core segments, so each kernel family streams its own
+ * layout at full rate.  both == 0: the tiles only, exactly the tensor's GGUF
+ * byte count (hp_hip_stats.resident_bytes); the matrix-core kernels (prefill
+ * chunks, drafts of several tokens) then gather their operands from the
+ * tiles, slower (a 512-token prefill chunk ~30 %).  Results are the same
+ * bits either way. */
+int32_t hp_hip_set_weight_layouts(int32_t both);
+
 /* wasmResidentWeightStats (wasm-kernels.ts:586-591) plus call counters. */
 int32_t hp_hip_stats(hp_hip_stats_t *out);
 /* Wait for all work queued on the library stream. */

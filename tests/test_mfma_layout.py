@@ -1,17 +1,27 @@
-"""CPU model of the matrix-core weight layout and kernel (kquant_mfma.hip).
+"""CPU model of the matrix-core kernels' weight operands (kquant_mfma.hip,
+kquant_prefill.hip).
 
-Emulates, in numpy, the upload repack into 16-row tiles and every index the
-kernel uses: which bytes each lane loads, how it builds its f16 MFMA
-operands (scale x quant, exact integers), the v_mfma_f32_16x16x32_f16 lane
-layout (A: lane i holds row i%16, k = 8*(i//16)..+7; B: lane i holds
-column i%16, the same k; D: lane i holds rows 4*(i//16)+j, column i%16),
-and the f32 tail in block order.  Checks:
-  * the repack writes every byte of a tile segment exactly once and keeps
-    the weight's byte count per 16-row tile;
+The kernels' A fragments are defined on a 16-row "segment" image of each
+(16 rows, block): `repack_mfma` below writes it from the GGUF blocks, and
+`emulate` runs the decode kernel's arithmetic on it (lane layout of
+v_mfma_f32_16x16x32_f16: A lane i holds row i%16, k = 8*(i//16)..+7; B lane
+i holds column i%16, the same k; D lane i holds rows 4*(i//16)+j, column
+i%16; the f32 tail in block order).  By default the segment image is also
+the second resident copy the kernels read; a weight kept in one layout
+(hp_hip_set_weight_layouts(0)) stays resident only in the vector-ALU tile
+layout (test_tile_layout.repack), and each kernel gathers its lanes' dwords
+from there with tile_row's offsets.  Checks:
+  * the segment image holds every byte once, the weight's byte count per
+    16-row tile;
   * the emulated MFMA accumulators equal the oracle's exact per-lane-class
     integers (aux32, sumi: lib.rs:2116-2172, 1923-1968) and stay below 2^24,
-    where f16 x f16 products summed in f32 are exact;
-  * the emulated outputs equal the oracle's matmul bit for bit.
+    where f16 x f16 products summed in f32 are exact, and the outputs equal
+    the oracle's matmul bit for bit;
+  * what each kernel's loads take from the tile layout -- the decode
+    kernel's lane registers, the bit-exact prefill kernel's LDS image, the
+    fast prefill kernel's fragment dwords -- equals the segment image, and
+    every load stays inside the weight's tiles, for one- and two-iteration
+    geometries and ragged row counts.
 """
 import numpy as np
 import pytest
@@ -292,3 +302,187 @@ def test_q6k_f16_operand_exactness_criterion():
     assert np.array_equal(inexact, flagged)
     # the synthetic distribution (scales -32..31) never reaches it
     assert not inexact[(sc[:, 0] >= -32) & (sc[:, 0] <= 31)].any()
+
+
+# ---- gathers from the tile layout -----------------------------------------
+
+from test_tile_layout import repack as tile_repack  # noqa: E402
+
+
+def tile_row(row, rows, g, ch):
+    """hp_common.h tile_row: (base, chunk, iter, dbase, diter)."""
+    nb, s_, r_ = g["nb"], g["S"], g["R"]
+    t = row // r_
+    r, row0 = row - t * r_, t * r_
+    rt = min(r_, rows - row0)
+    chunk = rt * s_ * 16
+    return dict(base=(row0 * nb * ch + r * s_) * 16, chunk=chunk, iter=ch * chunk,
+                dbase=row0 * nb + r * s_, diter=rt * s_)
+
+
+def tile_off(tr, b, g, c):
+    i, s = divmod(b, g["S"])
+    return tr["base"] + i * tr["iter"] + c * tr["chunk"] + 16 * s
+
+
+def _take(buf, off, n):
+    assert 0 <= off and off + n <= buf.size, (off, n, buf.size)
+    return buf[off:off + n]
+
+
+def _dwords(b):
+    return [int(x) for x in np.frombuffer(b.tobytes(), np.uint32)]
+
+
+def _seg(segs, type_id, rows, nb, T, b):
+    tiles = (rows + 15) // 16
+    base = (b * tiles + T) * SEG[type_id]
+    return segs[base: base + SEG[type_id]]
+
+
+SHAPES = [(Q4K, 21, 512), (Q4K, 37, 10240), (Q6K, 19, 512), (Q6K, 40, 10240), (Q4K, 16, 2560),
+          (Q6K, 7, 2560)]
+
+
+def _weights(type_id, rows, k):
+    raw = (S.q4_k_blocks if type_id == Q4K else S.q6_k_blocks)(rows + 7, rows, k)
+    tiles_b, dplane, g = tile_repack(type_id, raw, rows, k)
+    segs, _ = repack_mfma(type_id, raw, rows, k)
+    return tiles_b, dplane, g, segs
+
+
+@pytest.mark.parametrize("type_id,rows,k", SHAPES)
+def test_decode_kernel_tile_loads(type_id, rows, k):
+    """kquant_mfma.hip load_seg: lane i = (rho, q) of segment T, block b."""
+    tiles_b, dplane, g, segs = _weights(type_id, rows, k)
+    nb, ch = k // 256, (9 if type_id == Q4K else 13)
+    for T in range((rows + 15) // 16):
+        for i in range(64):
+            rho, q = i % 16, i // 16
+            row = min(16 * T + rho, rows - 1)
+            tr = tile_row(row, rows, g, ch)
+            oq = ((1 if type_id == Q4K else 0) + (q >> 1)) * tr["chunk"] + 8 * (q & 1)
+            for b in range(nb):
+                off = tile_off(tr, b, g, 0)
+                p = [_dwords(_take(tiles_b, off + oq + 2 * u * tr["chunk"], 8)) for u in range(4)]
+                c0 = [p[u][0] for u in range(4)]
+                c1 = [p[u][1] for u in range(4)]
+                seg = _seg(segs, type_id, rows, nb, T, b)
+                if 16 * T + rho >= rows:
+                    continue  # a re-read of the last row; its sums are never stored
+                base = 256 if type_id == Q4K else 288
+                assert c0 == _dwords(seg[base + 16 * i: base + 16 * i + 16])
+                assert c1 == _dwords(seg[base + 1024 + 16 * i: base + 1024 + 16 * i + 16])
+                if type_id == Q4K:
+                    assert np.array_equal(_take(tiles_b, off, 16), seg[16 * rho: 16 * rho + 16])
+                else:
+                    assert np.array_equal(_take(tiles_b, off + 12 * tr["chunk"], 16), seg[16 * rho: 16 * rho + 16])
+                    ib, sb = divmod(b, g["S"])
+                    di = tr["dbase"] + ib * tr["diter"] + sb
+                    assert 0 <= di < dplane.size
+                    assert int(dplane[di]) == int(np.frombuffer(seg[256 + 2 * rho: 258 + 2 * rho].tobytes(), np.uint16)[0])
+                    h0 = _dwords(_take(tiles_b, off + oq + 8 * tr["chunk"], 8))
+                    h1 = _dwords(_take(tiles_b, off + oq + 10 * tr["chunk"], 8))
+                    c2 = [v ^ 0xAAAAAAAA for v in h0 + h1]
+                    assert c2 == _dwords(seg[2336 + 16 * i: 2336 + 16 * i + 16])
+
+
+@pytest.mark.parametrize("type_id,rows,k", SHAPES)
+def test_bit_exact_prefill_stage(type_id, rows, k):
+    """kquant_prefill.hip stage_load + stage_store: the 32-row tile's LDS
+    image equals its two segments (live rows)."""
+    tiles_b, dplane, g, segs = _weights(type_id, rows, k)
+    nb, ch = k // 256, (9 if type_id == Q4K else 13)
+    segb = SEG[type_id]
+    nseg = (rows + 15) // 16
+    for T0 in range(0, nseg, 2):
+        for b in range(nb):
+            img = np.zeros(2 * segb, np.uint8)
+            for tid in range(256):
+                tr = tile_row(min(16 * T0 + (tid & 31), rows - 1), rows, g, ch)
+                for r in range(2):
+                    u = tid + 256 * r
+                    if u >= 32 * ch:
+                        continue
+                    c, rl = u >> 5, u & 31
+                    rho = rl & 15
+                    w = _dwords(_take(tiles_b, tile_off(tr, b, g, c), 16))
+                    sb = (rl >> 4) * segb
+                    if c == (0 if type_id == Q4K else 12):
+                        img[sb + 16 * rho: sb + 16 * rho + 16] = np.array(w, np.uint32).view(np.uint8)
+                    elif type_id == Q4K or c < 8:
+                        ck = c - 1 if type_id == Q4K else c
+                        for e in range(4):
+                            l = 4 * (ck & 1) + e
+                            o = sb + (256 if type_id == Q4K else 288) + 1024 * (l & 1) + 16 * (16 * (l >> 1) + rho) + 4 * (ck >> 1)
+                            img[o: o + 4] = np.array([w[e]], np.uint32).view(np.uint8)
+                    else:
+                        ck = c - 8
+                        for e in range(4):
+                            l = 4 * (ck & 1) + e
+                            o = sb + 2336 + 16 * (16 * (l >> 1) + rho) + 4 * (2 * (ck >> 1) + (l & 1))
+                            img[o: o + 4] = np.array([w[e] ^ 0xAAAAAAAA], np.uint32).view(np.uint8)
+                if type_id == Q6K and tid < 32:
+                    ib, s_ = divmod(b, g["S"])
+                    di = tr["dbase"] + ib * tr["diter"] + s_
+                    o = (tid >> 4) * segb + 256 + 2 * (tid & 15)
+                    img[o: o + 2] = np.array([dplane[di]], np.uint16).view(np.uint8)
+            for rs in range(2):
+                if T0 + rs >= nseg:
+                    continue
+                seg = _seg(segs, type_id, rows, nb, T0 + rs, b)
+                got = img[rs * segb: (rs + 1) * segb]
+                for rho in range(16):
+                    if 16 * (T0 + rs) + rho >= rows:
+                        continue
+                    # every byte of row rho: header/scales, d, and its units
+                    idx = list(range(16 * rho, 16 * rho + 16))
+                    if type_id == Q6K:
+                        idx += [256 + 2 * rho, 257 + 2 * rho]
+                    base = 256 if type_id == Q4K else 288
+                    nun = 2 if type_id == Q4K else 3
+                    for cidx in range(nun):
+                        for qq in range(4):
+                            o = base + 1024 * cidx + 16 * (16 * qq + rho)
+                            idx += list(range(o, o + 16))
+                    assert np.array_equal(got[idx], seg[idx])
+
+
+@pytest.mark.parametrize("type_id,rows,k", SHAPES)
+def test_fast_prefill_fragment_dwords(type_id, rows, k):
+    """kquant_prefill.hip f3_wload: lane (n, q)'s dwords of class l = 2t + g
+    (dword l % 4 of its chunk l / 4) are dword q of segment unit (l / 2, n) of
+    chunk l % 2; Q6_K high bits likewise; scales and d of row n."""
+    tiles_b, dplane, g, segs = _weights(type_id, rows, k)
+    nb, ch = k // 256, (9 if type_id == Q4K else 13)
+    for T in range((rows + 15) // 16):
+        for n in range(16):
+            if 16 * T + n >= rows:
+                continue
+            for q in range(4):
+                tr = tile_row(min(16 * T + n, rows - 1), rows, g, ch)
+                oq = (1 + 2 * q if type_id == Q4K else 2 * q) * tr["chunk"]
+                oh = (8 + 2 * (q >> 1)) * tr["chunk"]
+                for b in range(nb):
+                    off = tile_off(tr, b, g, 0)
+                    qa = [_dwords(_take(tiles_b, off + oq + x * tr["chunk"], 16)) for x in range(2)]
+                    seg = _seg(segs, type_id, rows, nb, T, b)
+                    base = 256 if type_id == Q4K else 288
+                    for l in range(8):
+                        t, gg = l >> 1, l & 1
+                        unit = base + 1024 * gg + 16 * (16 * t + n)
+                        assert qa[l >> 2][l & 3] == _dwords(seg[unit: unit + 16])[q]
+                    if type_id == Q4K:
+                        assert np.array_equal(_take(tiles_b, off, 16), seg[16 * n: 16 * n + 16])
+                    else:
+                        qh = [_dwords(_take(tiles_b, off + oh + x * tr["chunk"], 16)) for x in range(2)]
+                        for t in range(4):
+                            unit = _dwords(seg[2336 + 16 * (16 * t + n): 2336 + 16 * (16 * t + n) + 16])
+                            for gg in range(2):
+                                got = qh[t >> 1][2 * (t & 1) + gg] ^ 0xAAAAAAAA
+                                assert got == unit[2 * (q >> 1) + gg]
+                        gs = _dwords(_take(tiles_b, off + 12 * tr["chunk"] + 4 * q, 4))[0]
+                        assert gs == _dwords(seg[16 * n + 4 * q: 16 * n + 4 * q + 4])[0]
+                        ib, s_ = divmod(b, g["S"])
+                        di = tr["dbase"] + ib * tr["diter"] + s_
+                        assert int(dplane[di]) == int(np.frombuffer(seg[256 + 2 * n: 258 + 2 * n].tobytes(), np.uint16)[0])
