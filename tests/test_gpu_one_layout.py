@@ -10,11 +10,15 @@ gate/up + GeGLU tiles) against the same launch on weights kept in both
 layouts.  Shapes: one- and two-iteration tile geometries (K = 2560: 6-row
 tiles of 10 blocks; K = 10240: 3-row tiles, two iterations of 20 blocks),
 ragged rows (partial last tile and last 16-row segment), Q4_K and Q6_K, and
-a mixed-type Q/K/V launch.
+a mixed-type Q/K/V launch.  Through whole layers too: two layers of the
+model's shape over a 100-token prefill chunk (fast kernel), a 40-token chunk
+(bit-exact kernel) and a 4-token draft (matrix-core decode kernel), hidden
+states, output norm and caches bit-identical either way.
 """
 import numpy as np
 import pytest
 
+from heliopause_amd import decode as DM
 from heliopause_amd import synthetic as S
 
 pytestmark = pytest.mark.gpu
@@ -148,3 +152,39 @@ def test_geglu_tiles_same_bits(hip, rows, m):
             hip.releaseHipQuantizedWeightHandle(hg)
             hip.releaseHipQuantizedWeightHandle(hu)
     assert np.array_equal(_bits(outs[0]), _bits(outs[1]))
+
+
+@pytest.mark.parametrize("tokens", [100, 40, 4])
+def test_layers_same_bits(hip, tokens):
+    import torch
+
+    shape = DM.ModelShape()
+    seed = S.derive(S.BASE_SEED, "one-layout-layers", tokens)
+    datas = [DM.layer_host_data(shape, seed, i) for i in range(2)]
+    onorm = (1 + 0.1 * S.normal(S.derive(seed, "onorm"), shape.hidden)).astype(np.float32)
+    x = S.activations(S.derive(seed, "x"), tokens, shape.hidden) * 4
+    pos = shape.capacity - tokens
+    results = []
+    for both in (False, True):
+        hip.setWeightLayouts(both)
+        model = DM.HipDecodeModel(shape)
+        try:
+            for d in datas:
+                model.add_layer(d)
+            hip.setWeightLayouts(True)
+            model.output_norm = _dev(onorm)
+            dx = _dev(x.reshape(-1))
+            dpos = _dev(np.array([pos], np.int32))
+            out = torch.empty(tokens * shape.hidden, dtype=torch.float32, device="cuda:0")
+            print(f"one layout layers both={both}, {tokens} tokens", flush=True)
+            model.run_layers(dx.data_ptr(), dpos.data_ptr(), out.data_ptr(), tokens=tokens)
+            torch.cuda.synchronize()
+            caches = [c.cpu().numpy().copy() for layer in model.caches for c in layer]
+            results.append((dx.cpu().numpy(), out.cpu().numpy(), caches))
+        finally:
+            model.release()
+            hip.setWeightLayouts(True)
+    (h1, o1, c1), (h2, o2, c2) = results
+    assert np.array_equal(h1, h2)
+    assert np.array_equal(o1, o2)
+    assert len(c1) == len(c2) and all(np.array_equal(a, b) for a, b in zip(c1, c2))
