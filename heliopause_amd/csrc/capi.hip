@@ -316,8 +316,9 @@ constexpr size_t kPrefillMinCols = 32;
 constexpr size_t kFastMinCols = 64;
 
 // 0: not a prefill launch, 1: bit-exact prefill, 2: fast prefill
-// f16ok: every weight of the launch has exact f16 operands (Handle::f16_exact);
-// otherwise no prefill kernel applies, forced or not.
+// f16ok: the matrix-core kernels can take every weight of the launch
+// (mfma_ok: exact f16 operands, tiles they can address); otherwise no prefill
+// kernel applies, forced or not.
 int prefill_kind(size_t cols, bool f16ok) {
   const State &s = st();
   const int forced = s.matvec_kernel;
