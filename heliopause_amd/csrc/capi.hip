@@ -438,7 +438,7 @@ bool use_wide_pair(Handle *const *hs, size_t cols) {
 // launch, lib.rs:300-426); each launch quantises its columns in its prologue.
 int32_t run_norm(const float *y, int rows, int n, const float *w_post, const float *x_res, float scale, float *x_out,
                  const float *w_next, float *next_out, double eps, hipStream_t stream, uint8_t *q8img = nullptr,
-                 uint8_t *xt = nullptr, const PrefillParts *y_parts = nullptr);
+                 uint8_t *xt = nullptr, const PrefillParts *y_parts = nullptr, bool next_image_only = false);
 
 // Whether a one-column launch over these weights runs a vector-ALU kernel,
 // which can form its input with the norm prologue.
@@ -510,9 +510,11 @@ int32_t run_matvec(size_t count, Handle *const *hs, const float *d_input, size_t
   if (norm && (y_split || (wide ? !wide_norm : !norm_prologue_ok(count, hs, cols)))) {
     uint8_t *img = image_ok && img_scratch ? img_scratch : nullptr;
     tiles_ready = s.prefill_folds && kind == 2 && input_size % kQK == 0;
+    // with its tiles written, the fast prefill kernel does not read the f32
+    // input (kept for an image: storing it measured faster for the drafts)
     int32_t rc = run_norm(norm->y, (int)cols, (int)input_size, norm->w_post, norm->mode == 2 ? norm->x_res : nullptr,
                           norm->scale, norm->x_out, norm->w_next, norm_scratch, norm->eps, stream, img,
-                          tiles_ready ? pre : nullptr, norm_parts);
+                          tiles_ready ? pre : nullptr, norm_parts, tiles_ready);
     if (rc != HP_OK) return rc;
     d_input = norm_scratch;
     norm = nullptr;
@@ -685,7 +687,7 @@ int32_t run_matvec_geglu(Handle *hg, Handle *hu, const float *d_input, size_t in
     tiles_ready = s.prefill_folds && fast && input_size % kQK == 0;
     int32_t rc = run_norm(norm->y, (int)cols, (int)input_size, norm->w_post, norm->mode == 2 ? norm->x_res : nullptr,
                           norm->scale, norm->x_out, norm->w_next, norm_scratch, norm->eps, stream, nullptr,
-                          tiles_ready ? pre : nullptr, norm_parts);
+                          tiles_ready ? pre : nullptr, norm_parts, tiles_ready);
     if (rc != HP_OK) return rc;
     d_input = norm_scratch;
     norm = nullptr;
@@ -1094,10 +1096,11 @@ int32_t run_attention(AttnArgs a, float *partials, hipStream_t stream) {
 
 int32_t run_norm(const float *y, int rows, int n, const float *w_post, const float *x_res, float scale, float *x_out,
                  const float *w_next, float *next_out, double eps, hipStream_t stream, uint8_t *q8img,
-                 uint8_t *xt, const PrefillParts *y_parts) {
+                 uint8_t *xt, const PrefillParts *y_parts, bool next_image_only) {
   NormArgs a{};
   a.q8img = q8img;
   a.xt = xt;
+  a.next_image_only = next_image_only && (q8img || xt) ? 1 : 0;
   if (y_parts && y_parts->ks > 1) {
     // y is the projection's block-range partial sums
     a.y_ks = y_parts->ks;

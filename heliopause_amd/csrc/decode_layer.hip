@@ -147,7 +147,7 @@ __global__ __launch_bounds__(256) void norm_residual_kernel(const NormArgs a) {
     for (int j = 0; j < NPER; j++) {
       const int i = tid + 256 * j;
       const float o = a.w_next ? (float)(((double)v[j] * sc) * (double)wn[j]) : (float)((double)v[j] * sc);
-      if (i < a.n) a.next_out[row + i] = o;
+      if (i < a.n && !a.next_image_only) a.next_out[row + i] = o;
       if (a.q8img || a.xt) xs[i] = o;
     }
     if (a.q8img || a.xt) {
@@ -692,6 +692,7 @@ __global__ __launch_bounds__(256) void attn_reduce_kernel(const AttnArgs a) {
 hipError_t launch_norm_residual(const NormArgs &a, hipStream_t s) {
   if (a.n < 1 || a.n > 256 * kNormPer || a.rows < 1) return hipErrorInvalidValue;
   if ((a.q8img || a.xt) && (a.n % kQK != 0 || !a.next_out)) return hipErrorInvalidValue;
+  if (a.next_image_only && !a.q8img && !a.xt) return hipErrorInvalidValue;
   if (a.y_ks > kNormParts || (a.y_ks > 1 && a.y_stride < (size_t)a.rows * a.n)) return hipErrorInvalidValue;
   const int grid = a.xt ? (a.rows + kF2Cols - 1) / kF2Cols * kF2Cols : a.rows;
   const int per = (a.n + 255) / 256;
