@@ -471,16 +471,19 @@ int32_t run_matvec(size_t count, Handle *const *hs, const float *d_input, size_t
                    float *const *d_outs, hipStream_t stream, const NormIn *norm = nullptr,
                    float *norm_scratch = nullptr, uint8_t *img_scratch = nullptr, const uint8_t *q8img_in = nullptr,
                    const PrefillParts *norm_parts = nullptr, PrefillParts *defer = nullptr,
-                   bool tiles_in = false) {
+                   bool tiles_in = false, const GegluTail *tail_in = nullptr) {
   if (defer) defer->ks = 1;
   State &s = st();
   if (cols == 0) return HP_OK;
+  if (tail_in && !tail_in->part) tail_in = nullptr;
   const bool image_ok = s.images && cols >= 2 && image_input_ok(count, hs, cols);
   const bool f16 = mfma_ok(count, hs);
   const bool wide = prefill_kind(cols, f16) == 0 && use_wide(count, hs, cols);
   const bool wide_norm = wide && cols == 1 && g_nb_of(hs) <= 16;  // the wide kernel's norm prologue
   const int kind = prefill_kind(cols, f16);
   if (kind && cols > 65535) return fail(HP_ERR_SHAPE, "too many columns");
+  // a deferred GeGLU tail is completed by the fast prefill kernel's pre-pass
+  if (tail_in && (kind != 2 || norm || tiles_in)) return fail(HP_ERR_ARG, "deferred GeGLU tail needs the fast prefill");
   MfmaLaunch l{};
   l.count = (int)count;
   l.k = (int)input_size;
@@ -557,7 +560,8 @@ int32_t run_matvec(size_t count, Handle *const *hs, const float *d_input, size_t
         if (rc != HP_OK) return rc;
         defer->part = static_cast<float *>(p);
       }
-      HP_HIP_TRY(launch_prefill_fast(l, d_input, pre, s.num_cus, stream, tiles_ready, part_bytes ? defer : nullptr));
+      HP_HIP_TRY(launch_prefill_fast(l, d_input, pre, s.num_cus, stream, tiles_ready, part_bytes ? defer : nullptr,
+                                     tail_in));
       if (part_bytes) s.launches--;  // no reduction launch
     } else {
       HP_HIP_TRY(launch_q8k_prefill(d_input, (int)input_size, (int)cols, pre, stream));
@@ -647,8 +651,10 @@ int32_t run_matvec(size_t count, Handle *const *hs, const float *d_input, size_t
 int32_t run_matvec_geglu(Handle *hg, Handle *hu, const float *d_input, size_t input_size, size_t cols,
                          float *d_out, hipStream_t stream, const NormIn *norm = nullptr,
                          float *norm_scratch = nullptr, uint8_t *q8img_out = nullptr,
-                         bool *q8img_written = nullptr, const PrefillParts *norm_parts = nullptr) {
+                         bool *q8img_written = nullptr, const PrefillParts *norm_parts = nullptr,
+                         GegluTail *tail_out = nullptr) {
   if (q8img_written) *q8img_written = false;
+  if (tail_out) *tail_out = GegluTail{};
   State &s = st();
   if (cols == 0) return HP_OK;
   const size_t rows = hg->row_count;
@@ -756,10 +762,21 @@ int32_t run_matvec_geglu(Handle *hg, Handle *hu, const float *d_input, size_t in
     return HP_OK;
   }
   if (fast) {
+    // tail_out: the trailing tiles' range sums go to their own scratch for
+    // the consumer's pre-pass, in place of the tail launch
+    float *tail_part = nullptr;
+    const size_t tail_bytes = tail_out ? prefill_fast_geglu_tail_bytes(l, s.num_cus) : 0;
+    if (tail_bytes) {
+      void *p = nullptr;
+      int32_t rc = stream_scratch(stream, kScratchGeglu, tail_bytes, &p);
+      if (rc != HP_OK) return rc;
+      tail_part = static_cast<float *>(p);
+    }
     hipEvent_t e1 = prof_begin(stream);
-    HP_HIP_TRY(launch_prefill_fast_geglu(l, d_input, pre, s.gelu_lut, d_out, s.num_cus, stream, tiles_ready));
+    HP_HIP_TRY(launch_prefill_fast_geglu(l, d_input, pre, s.gelu_lut, d_out, s.num_cus, stream, tiles_ready,
+                                         tail_part ? tail_out : nullptr, tail_part));
     prof_end(HP_KERNEL_MATVEC, e1, stream);
-    s.launches += prefill_fast_geglu_launches(l, s.num_cus) - (tiles_ready ? 1 : 0);
+    s.launches += prefill_fast_geglu_launches(l, s.num_cus) - (tiles_ready ? 1 : 0) - (tail_part ? 1 : 0);
     s.matmul_calls++;
     return HP_OK;
   }
@@ -2569,12 +2586,17 @@ int32_t hp_hip_decode_layers_device(const hp_hip_decode_layer_t *layers, size_t 
       fin.w_next = L.d_ffn_norm;
       fin.eps = eps;
       bool h_img = false;
-      rc = run_matvec_geglu(H.gate, H.up, nullptr, hidden, Mc, h, strm, &fin, xn, imgh, &h_img, &op);
-      if (rc != HP_OK) return rc;
+      // down on the fast prefill kernel: its pre-pass completes the gate/up
+      // launch's trailing tiles (no tail launch)
       Handle *dh[1] = {H.down};
+      const bool down_fast = s.prefill_folds && prefill_kind(Mc, mfma_ok(1, dh)) == 2 && H.down->input_size % kQK == 0;
+      GegluTail gtail{};
+      rc = run_matvec_geglu(H.gate, H.up, nullptr, hidden, Mc, h, strm, &fin, xn, imgh, &h_img, &op,
+                            down_fast ? &gtail : nullptr);
+      if (rc != HP_OK) return rc;
       float *yo[1] = {y};
       rc = run_matvec(1, dh, h, H.down->input_size, Mc, yo, strm, nullptr, nullptr, nullptr, h_img ? imgh : nullptr,
-                      nullptr, s.prefill_folds && H.down->row_count == hidden ? &dp : nullptr);
+                      nullptr, s.prefill_folds && H.down->row_count == hidden ? &dp : nullptr, false, &gtail);
       if (rc != HP_OK) return rc;
       if (H.down->row_count != hidden) dp.ks = 1;
       nin.mode = 2;

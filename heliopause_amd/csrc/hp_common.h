@@ -446,8 +446,22 @@ int prefill_fast_launches(const MfmaLaunch &l, int num_cus);  // 2, or 3 with th
 // GeGLU (prefill_fast_geglu_launches: 2, or 3 with it).
 size_t prefill_fast_geglu_bytes(const MfmaLaunch &l, int num_cus);
 int prefill_fast_geglu_launches(const MfmaLaunch &l, int num_cus);
+// Those trailing tiles' range sums may instead be left for the pre-pass of
+// the next fast prefill launch, whose input is `out` (the down projection):
+// with defer non-null and tail_part a buffer of
+// prefill_fast_geglu_tail_bytes(l, num_cus) bytes, no tail kernel runs, the
+// trailing tiles' outputs are not written, and *defer describes them (part
+// null: none trail); the pre-pass forms those inputs from the sums with the
+// same GeGLU, so its tiles are the same bits.
+struct GegluTail {
+  const float *part;
+  const uint16_t *gelu_lut;
+  int tail_full, col_tiles;
+};
+size_t prefill_fast_geglu_tail_bytes(const MfmaLaunch &l, int num_cus);
 hipError_t launch_prefill_fast_geglu(const MfmaLaunch &l, const float *x, uint8_t *scratch, const uint16_t *gelu_lut,
-                                     float *out, int num_cus, hipStream_t s, bool tiles_ready = false);
+                                     float *out, int num_cus, hipStream_t s, bool tiles_ready = false,
+                                     GegluTail *defer = nullptr, float *tail_part = nullptr);
 size_t prefill_fast_lds_bytes();
 // A fast prefill launch may leave its block-range partial sums for the
 // consumer to add (a norm launch, NormArgs::y_ks; the attention prologue,
@@ -464,8 +478,11 @@ struct PrefillParts {
   int ks;
 };
 size_t prefill_fast_part_bytes(const MfmaLaunch &l, int num_cus);
+// tail (non-null part): x is a deferred GeGLU output (GegluTail above); the
+// pre-pass (not tiles_ready) completes its trailing tiles' inputs.
 hipError_t launch_prefill_fast(const MfmaLaunch &l, const float *x, uint8_t *scratch, int num_cus, hipStream_t s,
-                               bool tiles_ready = false, PrefillParts *defer = nullptr);
+                               bool tiles_ready = false, PrefillParts *defer = nullptr,
+                               const GegluTail *tail = nullptr);
 
 // The gelu table (65536 f16 entries, hp_gelu.h gelu_lut) for the constant c.
 hipError_t launch_gelu_lut(double c, uint16_t *lut, hipStream_t s);

@@ -1031,6 +1031,54 @@ __global__ __launch_bounds__(256) void f2_geglu_tail_kernel(const F2Args a, int 
   a.pair_out[(size_t)m * W.rows + row] = geglu_lut(p0[gi] + p1[gi], p0[ui] + p1[ui], a.gelu_lut);
 }
 
+// The pre-pass (q8k_prefill_tiles16_kernel) of a launch whose input x is a
+// gate/up + GeGLU output with its trailing tiles left as two block ranges'
+// sums (GegluTail): lane i16 = 2j + u of a (block b, column m) row holds
+// rows 256 b + 32 j + 8 c + 4 u + i (c, i < 4), all in gate/up row tile
+// 2 b + j / 4; where that tile and column's item is a trailing one, the
+// lane forms its 16 inputs as f2_geglu_tail_kernel does -- fround(gelu(g0 +
+// g1) * (u0 + u1)) from the two ranges' gate and up sums -- else it loads
+// them from x.  Same bits as the tail kernel followed by the plain pre-pass.
+__global__ __launch_bounds__(256) void q8k_prefill_tiles16_tail_kernel(const float *__restrict__ x, int k, int nb,
+                                                                       int cols, uint8_t *__restrict__ xt,
+                                                                       const GegluTail t) {
+  const int b = blockIdx.x, i16 = threadIdx.x & 15;
+  const int m = blockIdx.y * 16 + (threadIdx.x >> 4);
+  const int ct = m / kF2Cols, n = m % kF2Cols;
+  uint8_t *tile = xt + ((size_t)ct * nb + b) * kF2XTile;
+  const int j = i16 >> 1, u = i16 & 1;
+  const int nat = (2 * b + (j >> 2)) * t.col_tiles + m / kF3Cols;  // the gate/up item of these rows
+  float v[16];
+  if (m < cols && nat >= t.tail_full) {
+    constexpr int kHalf = kF3Waves / 2;
+    const int w = j & 3;  // gate wave of the rows; their segment rs = c / 2, row n = 8 (c % 2) + 4 u + i
+    const int mm = m % kF3Cols, cs = mm >> 4, q = (mm & 15) >> 2, jj = mm & 3;
+    const float *p0 = t.part + (size_t)(2 * (nat - t.tail_full)) * kF3Waves * kF3WaveFloats;
+    const float *p1 = p0 + (size_t)kF3Waves * kF3WaveFloats;
+    const size_t gi = (size_t)w * kF3WaveFloats, ui = gi + (size_t)kHalf * kF3WaveFloats;
+#pragma unroll
+    for (int c = 0; c < 4; c++) {
+      const int kk = ((c >> 1) * kF3CS + cs) * 4 + jj;          // the sum's index in its lane
+      const size_t o = (size_t)kk * 64 + 8 * (c & 1) + 4 * u + 16 * q;  // lane n + 16 q, n = 8 (c % 2) + 4 u
+      const float4 g0 = *reinterpret_cast<const float4 *>(p0 + gi + o);
+      const float4 g1 = *reinterpret_cast<const float4 *>(p1 + gi + o);
+      const float4 u0 = *reinterpret_cast<const float4 *>(p0 + ui + o);
+      const float4 u1 = *reinterpret_cast<const float4 *>(p1 + ui + o);
+      v[4 * c] = geglu_lut(g0.x + g1.x, u0.x + u1.x, t.gelu_lut);
+      v[4 * c + 1] = geglu_lut(g0.y + g1.y, u0.y + u1.y, t.gelu_lut);
+      v[4 * c + 2] = geglu_lut(g0.z + g1.z, u0.z + u1.z, t.gelu_lut);
+      v[4 * c + 3] = geglu_lut(g0.w + g1.w, u0.w + u1.w, t.gelu_lut);
+    }
+  } else {
+    load_x16(v, x + (size_t)min(m, cols - 1) * k + (size_t)b * kQK, i16);
+    if (m >= cols) {
+#pragma unroll
+      for (int e = 0; e < 16; e++) v[e] = 0.0f;
+    }
+  }
+  f2_tile_store16(v, i16, tile, n);
+}
+
 // out = ((part_0 + part_1) + ...) + part_{ks-1} over the launch's outputs
 // (the weights' [cols][rows] outputs end to end), four floats per thread.
 __global__ __launch_bounds__(256) void f2_reduce_kernel(const F2Args a, size_t total) {
@@ -1139,6 +1187,11 @@ F2Pair f2_pair(const MfmaLaunch &l, int num_cus) {
 
 int prefill_fast_geglu_launches(const MfmaLaunch &l, int num_cus) { return f2_pair(l, num_cus).tail_full ? 3 : 2; }
 
+size_t prefill_fast_geglu_tail_bytes(const MfmaLaunch &l, int num_cus) {
+  const F2Pair p = f2_pair(l, num_cus);
+  return p.tail_full ? (size_t)2 * (p.items - p.tail_full) * kF3Waves * kF3WaveFloats * sizeof(float) : 0;
+}
+
 size_t prefill_fast_geglu_bytes(const MfmaLaunch &l, int num_cus) {
   const F2Pair p = f2_pair(l, num_cus);
   const size_t xt = (size_t)p.xtiles * p.nb * kF2XTile;
@@ -1147,7 +1200,8 @@ size_t prefill_fast_geglu_bytes(const MfmaLaunch &l, int num_cus) {
 }
 
 hipError_t launch_prefill_fast_geglu(const MfmaLaunch &l, const float *x, uint8_t *scratch, const uint16_t *gelu_lut,
-                                     float *out, int num_cus, hipStream_t s, bool tiles_ready) {
+                                     float *out, int num_cus, hipStream_t s, bool tiles_ready, GegluTail *defer,
+                                     float *tail_part) {
   if (l.count != 2 || l.cols < 1 || l.k % kQK != 0 || l.type[0] != l.type[1] || l.rows[0] != l.rows[1] ||
       !mfma_geometry_ok(l))
     return hipErrorInvalidValue;
@@ -1183,7 +1237,8 @@ hipError_t launch_prefill_fast_geglu(const MfmaLaunch &l, const float *x, uint8_
   a.pair_out = out;
   a.gelu_lut = gelu_lut;
   a.tail_full = p.tail_full;
-  a.tail_part = reinterpret_cast<float *>(scratch + (size_t)p.xtiles * nb * kF2XTile);
+  a.tail_part = defer && tail_part ? tail_part : reinterpret_cast<float *>(scratch + (size_t)p.xtiles * nb * kF2XTile);
+  if (defer) *defer = GegluTail{};
   if (launch_reads_tiles(l))
     hipLaunchKernelGGL((kquant_prefill_fast_kernel<true, true>), dim3(p.grid), dim3(kF3Threads), 0, s, a);
   else
@@ -1191,6 +1246,11 @@ hipError_t launch_prefill_fast_geglu(const MfmaLaunch &l, const float *x, uint8_
   if (!p.tail_full) return hipGetLastError();
   e = hipGetLastError();
   if (e != hipSuccess) return e;
+  if (defer && tail_part) {
+    // the next launch's pre-pass adds the trailing tiles' ranges
+    *defer = GegluTail{tail_part, gelu_lut, p.tail_full, col_tiles};
+    return hipSuccess;
+  }
   const int rem = p.items - p.tail_full, threads = rem * (kF3Waves / 2) * kF3WaveFloats;
   hipLaunchKernelGGL(f2_geglu_tail_kernel, dim3((threads + 255) / 256), dim3(256), 0, s, a, rem);
   return hipGetLastError();
@@ -1212,13 +1272,21 @@ size_t prefill_fast_part_bytes(const MfmaLaunch &l, int num_cus) {
 }
 
 hipError_t launch_prefill_fast(const MfmaLaunch &l, const float *x, uint8_t *scratch, int num_cus, hipStream_t s,
-                               bool tiles_ready, PrefillParts *defer) {
+                               bool tiles_ready, PrefillParts *defer, const GegluTail *tail) {
   if (l.count < 1 || l.count > kMaxWeights || l.cols < 1 || l.k % kQK != 0 || !mfma_geometry_ok(l))
+    return hipErrorInvalidValue;
+  const bool tail_in = tail && tail->part;
+  if (tail_in && (tiles_ready || tail->col_tiles != (l.cols + kF3Cols - 1) / kF3Cols || !tail->gelu_lut))
     return hipErrorInvalidValue;
   const F2Shape sh = f2_shape(l, num_cus);
   const int nb = sh.nb, col_tiles = sh.col_tiles;
   hipError_t e;
-  if (!tiles_ready) {
+  if (tail_in) {
+    hipLaunchKernelGGL(q8k_prefill_tiles16_tail_kernel, dim3(nb, sh.xtiles * kF2Cols / 16), dim3(256), 0, s, x, l.k,
+                       nb, l.cols, scratch, *tail);
+    e = hipGetLastError();
+    if (e != hipSuccess) return e;
+  } else if (!tiles_ready) {
     hipLaunchKernelGGL(q8k_prefill_tiles16_kernel, dim3(nb, sh.xtiles * kF2Cols / 16), dim3(256), 0, s, x, l.k, nb,
                        l.cols, scratch);
     e = hipGetLastError();
