@@ -438,7 +438,8 @@ bool use_wide_pair(Handle *const *hs, size_t cols) {
 // launch, lib.rs:300-426); each launch quantises its columns in its prologue.
 int32_t run_norm(const float *y, int rows, int n, const float *w_post, const float *x_res, float scale, float *x_out,
                  const float *w_next, float *next_out, double eps, hipStream_t stream, uint8_t *q8img = nullptr,
-                 uint8_t *xt = nullptr, const PrefillParts *y_parts = nullptr, bool next_image_only = false);
+                 uint8_t *xt = nullptr, const PrefillParts *y_parts = nullptr, bool next_image_only = false,
+                 bool x16 = false);
 
 // Whether a one-column launch over these weights runs a vector-ALU kernel,
 // which can form its input with the norm prologue.
@@ -517,7 +518,7 @@ int32_t run_matvec(size_t count, Handle *const *hs, const float *d_input, size_t
     // input (kept for an image: storing it measured faster for the drafts)
     int32_t rc = run_norm(norm->y, (int)cols, (int)input_size, norm->w_post, norm->mode == 2 ? norm->x_res : nullptr,
                           norm->scale, norm->x_out, norm->w_next, norm_scratch, norm->eps, stream, img,
-                          tiles_ready ? pre : nullptr, norm_parts, tiles_ready);
+                          tiles_ready ? pre : nullptr, norm_parts, tiles_ready, true);
     if (rc != HP_OK) return rc;
     d_input = norm_scratch;
     norm = nullptr;
@@ -693,7 +694,7 @@ int32_t run_matvec_geglu(Handle *hg, Handle *hu, const float *d_input, size_t in
     tiles_ready = s.prefill_folds && fast && input_size % kQK == 0;
     int32_t rc = run_norm(norm->y, (int)cols, (int)input_size, norm->w_post, norm->mode == 2 ? norm->x_res : nullptr,
                           norm->scale, norm->x_out, norm->w_next, norm_scratch, norm->eps, stream, nullptr,
-                          tiles_ready ? pre : nullptr, norm_parts, tiles_ready);
+                          tiles_ready ? pre : nullptr, norm_parts, tiles_ready, true);
     if (rc != HP_OK) return rc;
     d_input = norm_scratch;
     norm = nullptr;
@@ -1113,8 +1114,9 @@ int32_t run_attention(AttnArgs a, float *partials, hipStream_t stream) {
 
 int32_t run_norm(const float *y, int rows, int n, const float *w_post, const float *x_res, float scale, float *x_out,
                  const float *w_next, float *next_out, double eps, hipStream_t stream, uint8_t *q8img,
-                 uint8_t *xt, const PrefillParts *y_parts, bool next_image_only) {
+                 uint8_t *xt, const PrefillParts *y_parts, bool next_image_only, bool x16) {
   NormArgs a{};
+  a.x16 = x16 ? 1 : 0;
   a.q8img = q8img;
   a.xt = xt;
   a.next_image_only = next_image_only && (q8img || xt) ? 1 : 0;

@@ -176,6 +176,80 @@ __global__ __launch_bounds__(256) void norm_residual_kernel(const NormArgs a) {
   }
 }
 
+// The same norm for the rows that feed a projection (NormArgs::x16; n a
+// multiple of 256, at most 16 blocks), which may leave as Q8_K blocks (a
+// matvec input image or the fast prefill's activation tiles): 16-lane group
+// g holds block g in load_x16's element order from the loads on, so each
+// block is quantised from registers (no pass through LDS) and every operand
+// moves in 16-byte loads and stores.  Per element the arithmetic is
+// norm_residual_kernel's; the f64 sums of squares add in this layout's
+// order (a lane's 16, then the wave's DPP tree, then the four waves), the
+// same with or without the image or tiles.
+__global__ __launch_bounds__(256) void norm_residual_x16_kernel(const NormArgs a) {
+  __shared__ double sh[8];  // two workgroup sums
+  const int tid = threadIdx.x, g = tid >> 4, i16 = tid & 15, nb = a.n / kQK;
+  if (a.xt && (int)blockIdx.x >= a.rows) {
+    // a padding column of the last activation tile: zero blocks, as the
+    // prefill pre-pass writes them
+    float z[16];
+#pragma unroll
+    for (int e = 0; e < 16; e++) z[e] = 0.0f;
+    if (g < nb)
+      f2_tile_store16(z, i16, a.xt + ((size_t)(blockIdx.x / kF2Cols) * nb + g) * kF2XTile, blockIdx.x % kF2Cols);
+    return;
+  }
+  const bool live = g < nb;
+  // every input first, one memory round trip; groups past the row's blocks
+  // re-read its last block (zeroed below), absent operands re-read y
+  const size_t row = (size_t)blockIdx.x * a.n, boff = (size_t)min(g, nb - 1) * kQK;
+  const float *py = a.y + row + boff;
+  float v[16], r[16], wp[16], wn[16];
+  load_x16(v, py, i16);
+  load_x16(r, a.x_res ? a.x_res + row + boff : py, i16);
+  load_x16(wp, a.w_post ? a.w_post + boff : py, i16);
+  load_x16(wn, a.w_next ? a.w_next + boff : py, i16);
+  if (a.y_ks > 1) {
+    float pv[kNormParts - 1][16];
+#pragma unroll
+    for (int k = 1; k < kNormParts; k++) load_x16(pv[k - 1], k < a.y_ks ? py + k * a.y_stride : py, i16);
+#pragma unroll
+    for (int k = 1; k < kNormParts; k++)
+#pragma unroll
+      for (int e = 0; e < 16; e++)
+        if (k < a.y_ks) v[e] += pv[k - 1][e];
+  }
+#pragma unroll
+  for (int e = 0; e < 16; e++) {
+    v[e] = live ? v[e] : 0.0f;
+    r[e] = live && a.x_res ? r[e] : 0.0f;
+    wp[e] = a.w_post ? wp[e] : 1.0f;
+    wn[e] = a.w_next ? wn[e] : 1.0f;
+  }
+  if (a.x_res) {
+    const double sc = rms_scale<16>(v, a.n, a.eps, sh);
+#pragma unroll
+    for (int e = 0; e < 16; e++) {
+      const float t = a.w_post ? (float)(((double)v[e] * sc) * (double)wp[e]) : (float)((double)v[e] * sc);
+      v[e] = live ? (r[e] + t) * a.scale : 0.0f;
+    }
+    if (live) store_x16(a.x_out + row + (size_t)g * kQK, v, i16);
+  }
+  const double sc = rms_scale<16>(v, a.n, a.eps, sh + 4);
+  float o[16];
+#pragma unroll
+  for (int e = 0; e < 16; e++)
+    o[e] = a.w_next ? (float)(((double)v[e] * sc) * (double)wn[e]) : (float)((double)v[e] * sc);
+  if (!live) return;
+  if (!a.next_image_only) store_x16(a.next_out + row + (size_t)g * kQK, o, i16);
+  if (a.q8img) {
+    const size_t q = (size_t)blockIdx.x * nb + g;
+    q8k_block16(o, i16, a.q8img + q * kQ8BlockBytes,
+                reinterpret_cast<float *>(a.q8img + (size_t)a.rows * nb * kQ8BlockBytes) + q);
+  }
+  if (a.xt)
+    f2_tile_store16(o, i16, a.xt + ((size_t)(blockIdx.x / kF2Cols) * nb + g) * kF2XTile, blockIdx.x % kF2Cols);
+}
+
 // One wave per head: query heads (norm with wq, RoPE, f32 out or its f16
 // rounding for the prefill attention), key heads
 // (norm with wk, RoPE, f16 into the key cache) and value heads (norm without
@@ -695,6 +769,11 @@ hipError_t launch_norm_residual(const NormArgs &a, hipStream_t s) {
   if (a.next_image_only && !a.q8img && !a.xt) return hipErrorInvalidValue;
   if (a.y_ks > kNormParts || (a.y_ks > 1 && a.y_stride < (size_t)a.rows * a.n)) return hipErrorInvalidValue;
   const int grid = a.xt ? (a.rows + kF2Cols - 1) / kF2Cols * kF2Cols : a.rows;
+  if (a.x16 && a.next_out && a.n % kQK == 0 && a.n <= 16 * kQK) {
+    // rows that feed a projection: the block-per-group form
+    hipLaunchKernelGGL(norm_residual_x16_kernel, dim3(grid), dim3(256), 0, s, a);
+    return hipGetLastError();
+  }
   const int per = (a.n + 255) / 256;
   if (per <= 4)
     hipLaunchKernelGGL(norm_residual_kernel<4>, dim3(grid), dim3(256), 0, s, a);

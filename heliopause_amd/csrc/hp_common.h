@@ -514,6 +514,9 @@ struct NormArgs {
   // (hp_f2tile.h; row r is column r; the grid covers whole 64-column tiles,
   // workgroups past `rows` write their padding columns as zeros)
   uint8_t *xt;
+  // x16: 16-lane groups hold whole 256-element blocks (norm_residual_x16_kernel;
+  // n a multiple of 256, at most 4096): the norms that feed a projection
+  int x16;
   // next_image_only: the launch that follows reads only q8img or xt, so the
   // f32 values of next_out are formed for them but not stored (prefill
   // chunks through all layers 10.86 -> 10.82 ms)
