@@ -376,11 +376,14 @@ int wide_rows_for(int rows, int nb, int cols, int type) {
 int g_nb_of(Handle *const *hs) { return hs[0]->g.nb; }
 
 // The matrix-core kernels can take these weights: their f16 operands are
-// exact, and a weight read from its tiles fits the kernels' 32-bit tile
-// offsets (under 4 GiB).
+// exact, and when the launch reads its weights from their tiles (one of them
+// kept without segments makes every weight of the launch read that way),
+// each fits the kernels' 32-bit tile offsets (under 4 GiB).
 bool mfma_ok(size_t count, Handle *const *hs) {
+  bool tiles = false;
+  for (size_t i = 0; i < count; i++) tiles = tiles || !hs[i]->segs;
   for (size_t i = 0; i < count; i++)
-    if (!hs[i]->f16_exact || (!hs[i]->segs && hs[i]->byte_length >= ((size_t)1 << 32))) return false;
+    if (!hs[i]->f16_exact || (tiles && hs[i]->byte_length >= ((size_t)1 << 32))) return false;
   return true;
 }
 
@@ -600,8 +603,7 @@ int32_t run_matvec(size_t count, Handle *const *hs, const float *d_input, size_t
     l.R = g.R;
     for (size_t i = 0; i < count; i++) {
       l.seg[i] = hs[i]->segs;
-      l.seg[i] = hs[i]->segs;
-    l.wt[i] = hs[i]->data;
+      l.wt[i] = hs[i]->data;
       l.dplane[i] = hs[i]->dplane;
       l.type[i] = hs[i]->type;
       l.rows[i] = (int)hs[i]->row_count;

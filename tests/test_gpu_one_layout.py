@@ -127,6 +127,28 @@ def test_mixed_qkv_launch_same_bits(hip, oracle, selector):
             assert np.array_equal(_bits(a), _bits(ref))
 
 
+@pytest.mark.parametrize("selector,m", [(2, 3), (4, 40), (5, 70)], indirect=["selector"])
+def test_mixed_layouts_in_one_launch(hip, selector, m):
+    """Q kept in both layouts, K and V in one: the launch reads every weight
+    from its tiles and gives the bits of the all-both launch."""
+    k = 2560
+    specs = [("Q4_K", 2048), ("Q4_K", 512), ("Q6_K", 512)]
+    seed = S.derive(S.BASE_SEED, "mixed-layouts")
+    ws = [S.weight_blocks(t, S.derive(seed, i), r, k) for i, (t, r) in enumerate(specs)]
+    x = S.activations(S.derive(seed, "x", m), m, k)
+    print(f"mixed layouts selector={selector} m={m}", flush=True)
+    mixed = _upload(hip, True, specs[:1], ws[:1], k) + _upload(hip, False, specs[1:], ws[1:], k)
+    both = _upload(hip, True, specs, ws, k)
+    try:
+        a = _device_matmul(hip, mixed, x, k, m)
+        b = _device_matmul(hip, both, x, k, m)
+    finally:
+        for h in mixed + both:
+            hip.releaseHipQuantizedWeightHandle(h)
+    for u, v in zip(a, b):
+        assert np.array_equal(_bits(u), _bits(v))
+
+
 @pytest.mark.parametrize("rows,m", [(160, 96), (1000, 130)])
 def test_geglu_tiles_same_bits(hip, rows, m):
     """gate/up + GeGLU on the fast prefill kernel's paired tiles (automatic
