@@ -364,10 +364,13 @@ __global__ __launch_bounds__(64) void qkv_post_kernel(const QkvPostArgs a) {
   }
 }
 
-// Attention partials: workgroup (chunk c, kv head g) takes the cache slots
-// [32 c, 32 c + 32) -- those inside the token's window -- for the group's G
-// query heads (softmax and the weighted sum do not depend on the order of
-// the keys, so the chunks follow slots and the loads need no position).
+// Attention partials: workgroup (chunk c, kv head g, part hs) takes the cache
+// slots [32 c, 32 c + 32) -- those inside the token's window -- for G of the
+// group's query heads, G (nq / nkv) / a.qsplit of them from head hs G on (the
+// parts of one chunk share its keys through the L2 and each keeps a shorter
+// chain; every head's arithmetic is the same either way).  Softmax and the
+// weighted sum do not depend on the order of the keys, so the chunks follow
+// slots and the loads need no position.
 // With a.prep it first computes, from the projections, the group's queries
 // (norm, RoPE) and the token's own key (norm, RoPE) and value (norm); the
 // workgroup whose slots hold position % capacity appends them to the caches,
@@ -390,7 +393,8 @@ __global__ __launch_bounds__(256) void attn_partial_kernel(const AttnArgs a) {
   __shared__ float xs[G + 2][kHeadDim];       // queries, then the new key and value
   __shared__ float sc[G][kAttnChunk];         // scores, then exp(score - m)
   __shared__ float4 red[4][G][kHeadDim / 4];  // per-wave value sums
-  const int c = blockIdx.x, g = blockIdx.y, tid = threadIdx.x;
+  const int c = blockIdx.x, g = blockIdx.y / a.qsplit, hs = blockIdx.y - g * a.qsplit, tid = threadIdx.x;
+  const int qh0 = (g * a.qsplit + hs) * G;  // the first query head of this workgroup
   const int wave = tid >> 6, lane = tid & 63;
   const int cap = a.capacity;
   const size_t head_base = (size_t)g * cap * kHeadDim;
@@ -408,7 +412,7 @@ __global__ __launch_bounds__(256) void attn_partial_kernel(const AttnArgs a) {
 #pragma unroll
     for (int k3 = 0; k3 < kRows; k3++) {
       const int r = min(wave + 4 * k3, G + 1);
-      const float *src = r < G ? a.q + (size_t)(g * G + r) * kHeadDim : (r == G ? a.k : a.v) + (size_t)g * kHeadDim;
+      const float *src = r < G ? a.q + (size_t)(qh0 + r) * kHeadDim : (r == G ? a.k : a.v) + (size_t)g * kHeadDim;
       const float *w = r < G ? a.wq : (r == G ? a.wk : nullptr);
       const float *pwr = w ? w : src;
 #pragma unroll
@@ -471,7 +475,7 @@ __global__ __launch_bounds__(256) void attn_partial_kernel(const AttnArgs a) {
           double sn, cn;
           sincos(ang, &sn, &cn);
           tab[p] = make_double2(cn, sn);
-          if (a.rope_table_mode == 1 && c == 0 && g == 0 && wave == 0) a.rope_table[i] = tab[p];
+          if (a.rope_table_mode == 1 && c == 0 && blockIdx.y == 0 && wave == 0) a.rope_table[i] = tab[p];
         }
       }
     }
@@ -529,14 +533,14 @@ __global__ __launch_bounds__(256) void attn_partial_kernel(const AttnArgs a) {
       }
       __syncthreads();
     }
-    if (new_slot >= 0 && new_slot / kAttnChunk == c) {
+    if (new_slot >= 0 && new_slot / kAttnChunk == c && hs == 0) {
       const size_t o = head_base + (size_t)new_slot * kHeadDim + tid;
       a.k_cache[o] = (_Float16)xs[G][tid];
       a.v_cache[o] = (_Float16)xs[G + 1][tid];
     }
   } else {
     for (int idx = tid; idx < G * kHeadDim; idx += 256)
-      xs[idx >> 8][idx & 255] = rs_f16_round(a.q[((size_t)tok * a.nq + g * G) * kHeadDim + idx]);
+      xs[idx >> 8][idx & 255] = rs_f16_round(a.q[((size_t)tok * a.nq + qh0) * kHeadDim + idx]);
     __syncthreads();
   }
 
@@ -603,7 +607,7 @@ __global__ __launch_bounds__(256) void attn_partial_kernel(const AttnArgs a) {
       l += __shfl_xor(l, 16);
       sc[h][j] = p;
       if (j == 0) {
-        const size_t base = (((size_t)tok * a.nkv + g) * a.chunks + c) * kAttnMaxGroup + h;
+        const size_t base = (((size_t)tok * a.nkv + g) * a.chunks + c) * kAttnMaxGroup + hs * G + h;
         a.part_m[base] = m;
         a.part_l[base] = l;
       }
@@ -642,7 +646,7 @@ __global__ __launch_bounds__(256) void attn_partial_kernel(const AttnArgs a) {
     const int h = idx >> 6, d4 = idx & 63;
     const float4 r0 = red[0][h][d4], r1 = red[1][h][d4], r2 = red[2][h][d4], r3 = red[3][h][d4];
     *reinterpret_cast<float4 *>(
-        &a.part_o[((((size_t)tok * a.nkv + g) * a.chunks + c) * kAttnMaxGroup + h) * kHeadDim + 4 * d4]) =
+        &a.part_o[((((size_t)tok * a.nkv + g) * a.chunks + c) * kAttnMaxGroup + hs * G + h) * kHeadDim + 4 * d4]) =
         make_float4((r0.x + r1.x) + (r2.x + r3.x), (r0.y + r1.y) + (r2.y + r3.y), (r0.z + r1.z) + (r2.z + r3.z),
                     (r0.w + r1.w) + (r2.w + r3.w));
   }
@@ -811,8 +815,13 @@ hipError_t launch_attention(AttnArgs a, float *partials, hipStream_t s) {
   a.part_m = partials;
   a.part_l = partials + slots;
   a.part_o = partials + 2 * slots;
-  const dim3 grid(a.chunks, a.nkv, a.tokens);
-  switch (a.nq / a.nkv) {
+  // one token: two workgroups per (chunk, kv head) when the group splits
+  // evenly (a 42-layer decode step 2.00 -> 1.98 ms); drafts keep one, their
+  // grid already fills the CUs (4 tokens: 3.73 ms against 3.80 split)
+  const int group = a.nq / a.nkv;
+  a.qsplit = a.tokens == 1 && group % 2 == 0 ? 2 : 1;
+  const dim3 grid(a.chunks, a.nkv * a.qsplit, a.tokens);
+  switch (group / a.qsplit) {
     case 1: hipLaunchKernelGGL(attn_partial_kernel<1>, grid, dim3(256), 0, s, a); break;
     case 2: hipLaunchKernelGGL(attn_partial_kernel<2>, grid, dim3(256), 0, s, a); break;
     case 3: hipLaunchKernelGGL(attn_partial_kernel<3>, grid, dim3(256), 0, s, a); break;

@@ -575,6 +575,7 @@ struct AttnArgs {
   int nq, nkv, capacity, window, chunks, rope_dims, prep, rope_table_mode;
   int tokens;  // prep == 0: queries of tokens *position + pos_offset .. + tokens - 1, rows [t][nq][kHeadDim]
   int pos_offset;
+  int qsplit;  // set by launch_attention: workgroups per (chunk, kv head), each taking nq / nkv / qsplit query heads
   double theta_scale, eps;
 };
 hipError_t launch_norm_residual(const NormArgs &a, hipStream_t s);
