@@ -815,11 +815,12 @@ hipError_t launch_attention(AttnArgs a, float *partials, hipStream_t s) {
   a.part_m = partials;
   a.part_l = partials + slots;
   a.part_o = partials + 2 * slots;
-  // one token: two workgroups per (chunk, kv head) when the group splits
-  // evenly (a 42-layer decode step 2.00 -> 1.98 ms); drafts keep one, their
-  // grid already fills the CUs (4 tokens: 3.73 ms against 3.80 split)
+  // one or two tokens: two workgroups per (chunk, kv head) when the group
+  // splits evenly (a 42-layer decode step 2.00 -> 1.97 ms, a 2-token draft
+  // 2.82 -> 2.81 ms); longer drafts keep one, their grid already fills the
+  // CUs (4 tokens: 3.73 ms against 3.80 split)
   const int group = a.nq / a.nkv;
-  a.qsplit = a.tokens == 1 && group % 2 == 0 ? 2 : 1;
+  a.qsplit = a.tokens <= 2 && group % 2 == 0 ? 2 : 1;
   const dim3 grid(a.chunks, a.nkv * a.qsplit, a.tokens);
   switch (group / a.qsplit) {
     case 1: hipLaunchKernelGGL(attn_partial_kernel<1>, grid, dim3(256), 0, s, a); break;
