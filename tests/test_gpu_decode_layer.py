@@ -406,6 +406,35 @@ def test_decode_layer_rejects_bad_shapes(hip):
         model.release()
 
 
+@pytest.mark.parametrize("nq,nkv,cap,pos,window", [(8, 2, 4096, 4000, 0), (8, 1, 300, 1000, 0),
+                                                   (6, 2, 4096, 3000, 512)])
+def test_one_token_attention_matches_draft_row(hip, nq, nkv, cap, pos, window):
+    """A one-token call splits each KV head's query heads over two workgroups
+    per chunk (when the group is even); a three-token call does not.  The
+    third token's row of the three-token call attends over the same window
+    and keys as a one-token call at its position: the rows must be
+    bit-identical."""
+    import torch
+
+    rng = np.random.default_rng(nq * 100 + nkv * 10 + cap + pos)
+    q = (rng.standard_normal((3, nq, 256)) * 0.25).astype(np.float32)
+    kc = rng.standard_normal((nkv, cap, 256)).astype(np.float16)
+    vc = rng.standard_normal((nkv, cap, 256)).astype(np.float16)
+    dkc, dvc = _dev(kc.view(np.int16)), _dev(vc.view(np.int16))
+    cfg = H.attention_config(nq, nkv, cap, sliding_window=window)
+    print(f"one-token vs draft row nq={nq} nkv={nkv} cap={cap} pos={pos} window={window}", flush=True)
+    out3 = torch.empty(3 * nq * 256, dtype=torch.float32, device="cuda:0")
+    dq3, dpos3 = _dev(q), _dev(np.array([pos], np.int32))
+    H.gqa_attention_device(cfg, dq3.data_ptr(), dkc.data_ptr(), dvc.data_ptr(), dpos3.data_ptr(), out3.data_ptr(),
+                           token_count=3)
+    out1 = torch.empty(nq * 256, dtype=torch.float32, device="cuda:0")
+    dq1, dpos1 = _dev(np.ascontiguousarray(q[2])), _dev(np.array([pos + 2], np.int32))
+    H.gqa_attention_device(cfg, dq1.data_ptr(), dkc.data_ptr(), dvc.data_ptr(), dpos1.data_ptr(), out1.data_ptr())
+    torch.cuda.synchronize()
+    row = out3.cpu().numpy().reshape(3, nq * 256)[2]
+    assert np.array_equal(out1.cpu().numpy().view(np.uint32), row.view(np.uint32))
+
+
 @pytest.mark.parametrize("tokens,cap,pos,window,qscale", [(3, 4096, 4094, 0, 0.25), (4, 64, 70, 0, 1.0),
                                                           (8, 4096, 100, 0, 0.0625), (2, 4096, 3000, 512, 0.25),
                                                           (5, 40, 2, 0, 0.25)])
